@@ -1,0 +1,247 @@
+/*
+ * tgx.h - C ABI of libtgx_hip.so, the MI355X (gfx950) execution provider for
+ * Tiga's CSR message-passing hot path.
+ *
+ * Conventions (kept from the reference runtime ABI, include/tiga/Runtime/
+ * CAPI.h:21-35 and python/tiga/runtime/__init__.py:279-285):
+ *   - every entry point returns an int status, TGX_OK == 0; a non-zero status
+ *     leaves a message readable through tgx_last_error();
+ *   - pointers named *_dev or documented "device" are HIP device pointers;
+ *     everything else is host memory;
+ *   - `stream` is a hipStream_t (pass torch.cuda.current_stream().cuda_stream);
+ *     all work is enqueued on it in order and no entry point synchronises the
+ *     host unless its comment says so (planning calls copy counts back);
+ *   - the library never allocates device memory: outputs, gradients and
+ *     workspaces are owned by the caller (the reference allocates outputs
+ *     through Torch, python/tiga/interop/torch/provider.py:170-198);
+ *   - index arrays supplied by the caller (row_ptr, col_idx) are int32 or
+ *     int64, selected by idx_bits (32 or 64); arrays produced by this library
+ *     (transposed CSR, permutations, plans) are int32.
+ *   - CSR is destination-row: row i lists the sources of destination i
+ *     (reference Graph.from_csr, python/tiga/interop/torch/graph.py:153-190).
+ */
+#ifndef TGX_H_
+#define TGX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; same meaning as GFRTStatus (CAPI.h:21-27). */
+enum {
+  TGX_OK = 0,
+  TGX_INVALID_ARGUMENT = 1,
+  TGX_UNSUPPORTED = 2,
+  TGX_OUT_OF_MEMORY = 3,
+  TGX_INTERNAL = 4
+};
+
+/* Human-readable name of a status code. */
+const char* tgx_status_string(int status);
+/* Message recorded by the last failing call on this thread ("" if none). */
+const char* tgx_last_error(void);
+/* ABI version of this header (bumped on any signature change). */
+int tgx_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Graph indexing                                                            */
+/* ------------------------------------------------------------------------ */
+
+/* Per-edge destination row id: out[e] = i for row_ptr[i] <= e < row_ptr[i+1].
+ * Replaces Graph.destination_index (interop/torch/graph.py:1212-1222,
+ * repeat_interleave(arange(num_dst), degree)).  out_bits selects int32/int64
+ * output. */
+int tgx_destination_index(const void* row_ptr_dev, int idx_bits, int64_t n_rows,
+                          int64_t n_edges, void* out_dev, int out_bits,
+                          void* stream);
+
+/* Workspace bytes needed by tgx_csr_transpose. */
+int tgx_csr_transpose_workspace(int64_t n_dst, int64_t n_src, int64_t n_edges,
+                                size_t* bytes);
+
+/* Stable transpose of a destination-row CSR into a source-row CSR.
+ * Replaces Graph.transpose -> from_coo (interop/torch/graph.py:675-685 and
+ * 193-231: argsort(col_idx, stable=True), bincount, cumsum).
+ *   row_ptr_t_dev [n_src+1]  int32: exclusive prefix of source out-degrees
+ *   col_t_dev     [n_edges]  int32: destination id of each transposed edge
+ *   perm_dev      [n_edges]  int32: original edge id of each transposed edge
+ *                                   (= argsort(col_idx, stable=True))
+ * Deterministic: output is bit-identical across runs. */
+int tgx_csr_transpose(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                      int64_t n_dst, int64_t n_src, int64_t n_edges,
+                      int32_t* row_ptr_t_dev, int32_t* col_t_dev,
+                      int32_t* perm_dev, void* workspace_dev,
+                      size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Row partition / load balancing                                            */
+/* ------------------------------------------------------------------------ */
+
+/* Workspace bytes needed by tgx_plan_degree_bins. */
+int tgx_plan_degree_bins_workspace(int64_t n_rows, int n_bins, size_t* bytes);
+
+/* Degree-binned row worklist (reference gf_degree_reset/histogram/prefix/
+ * scatter, lib/Target/Triton/Translate.cpp:4043-4187, ABI
+ * include/tiga/Dialect/Task/TaskOps.td:63-82), made deterministic.
+ * Bin b holds rows with upper_bounds[b-1] < degree <= upper_bounds[b]
+ * (upper_bounds[-1] = -1); upper_bounds is a host array, strictly ascending,
+ * and its last entry must be >= the maximum degree.
+ *   rows_out_dev [n_rows] int32: row ids grouped by bin, ascending inside
+ *                                 each bin (a stable partition);
+ *   bin_offsets_host [n_bins+1]: start of each bin in rows_out (host).
+ * Synchronises `stream` to return bin_offsets_host. */
+int tgx_plan_degree_bins(const void* row_ptr_dev, int idx_bits, int64_t n_rows,
+                         const int64_t* upper_bounds, int n_bins,
+                         int32_t* rows_out_dev, int64_t* bin_offsets_host,
+                         void* workspace_dev, size_t workspace_bytes,
+                         void* stream);
+
+/* Chunk prefix for split (hub) rows: chunk_offsets_dev[k] = sum over split
+ * rows r < k of ceil(degree(rows[k]) / chunk_edges), k = 0..n_split.
+ * Restates the reference row-split plan (lib/Transforms/PlanSplitRows.cpp:
+ * 136-147, 64-edge partials) with a caller-chosen chunk size.
+ * Synchronises `stream` to return *n_chunks_host. */
+int tgx_plan_split_chunks(const void* row_ptr_dev, int idx_bits,
+                          const int32_t* split_rows_dev, int64_t n_split,
+                          int32_t chunk_edges, int32_t* chunk_offsets_dev,
+                          int64_t* n_chunks_host, void* stream);
+
+/* Row partition consumed by the sparse kernels: rows_dev lists the empty
+ * rows, then the rows done whole by one wavefront (1..wave_max edges), then
+ * the split rows (> wave_max edges) whose chunks are listed by
+ * chunk_offsets_dev.  Built from tgx_plan_degree_bins with upper bounds
+ * {0, wave_max, INT64_MAX} and tgx_plan_split_chunks. */
+typedef struct tgx_row_plan {
+  int64_t n_rows;
+  int64_t n_empty;
+  int64_t n_wave;
+  int64_t n_split;
+  int64_t n_chunks;
+  int32_t wave_max;
+  int32_t chunk_edges;
+  const int32_t* rows_dev;
+  const int32_t* chunk_offsets_dev;
+} tgx_row_plan;
+
+/* Reference planner decisions, host only (restates lib/Transforms/
+ * SelectKernelSchedule.cpp:136-163 annotateLoadBalance, PlanDegreeBuckets.cpp:
+ * 32-143 and PlanSplitRows.cpp:84-147).
+ *   histogram: host [max_degree+1] row counts per degree, or NULL.
+ *   has_node_epilogue: 1 when the kernel has a node() region.
+ * Outputs (host):
+ *   *plan_code: 0 row-neighbor-tile, 1 degree-bucketing (worklist),
+ *               2 high-degree-tail-split, 3 provider-deferred-high-degree,
+ *               4 bounded-row-preferred, 5 high-degree-tail-chunked,
+ *               6 tail-split with row-split partial/finalize;
+ *   *utilization_milli: padding utilization (-1 when not computed);
+ *   bounds_out[*n_bounds] (capacity 64): inclusive bucket upper bounds;
+ *   mapping_out[*n_bounds]: 0 worklist, 1 direct-filter, 2 worklist-chunked;
+ *   rows_in_bucket_out[*n_bounds];
+ *   *partials_per_row, *active_rows: row-split sizing (0 when unused). */
+int tgx_plan_reference_buckets(int64_t n_rows, int64_t max_degree,
+                               int64_t degree_sum, const int64_t* histogram,
+                               int has_node_epilogue, int* plan_code,
+                               int64_t* utilization_milli, int64_t* bounds_out,
+                               int* mapping_out, int64_t* rows_in_bucket_out,
+                               int* n_bounds, int64_t* partials_per_row,
+                               int64_t* active_rows);
+
+/* ------------------------------------------------------------------------ */
+/* Sum reducer: out[i, :] = sum_e w[e] * x[col[e], :]                        */
+/* ------------------------------------------------------------------------ */
+
+/* Forward of the weighted-sum message (reference WeightedSumPattern,
+ * python/tiga/compiler/capture.py:123-145, executed by _execute_weighted_sum,
+ * interop/torch/message_passing.py:2903-3345; fp32).
+ *   x_dev [n_src, F] fp32, w_dev [n_edges] fp32 or NULL (weight 1),
+ *   out_dev [n_dst, F] fp32, fully written.
+ * F may be any positive width; widths that are multiples of 4 with
+ * F*4 <= 1024 bytes take the vectorised path. */
+int tgx_csr_sum_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                    const tgx_row_plan* plan, const float* x_dev,
+                    const float* w_dev, float* out_dev, int64_t n_dst,
+                    int64_t n_src, int64_t F, float* partial_dev,
+                    void* stream);
+
+/* Bytes of partial_dev scratch the sum/attention kernels need for a plan. */
+int tgx_partial_bytes(const tgx_row_plan* plan, int64_t state_floats,
+                      size_t* bytes);
+
+/* Backward of the weighted sum, no float atomics:
+ *   dx[j, :] = sum over transposed edges e' of j: w[perm[e']] * dout[col_t[e'], :]
+ *   dw[e]    = <dout[row(e), :], x[col[e], :]>   (written at perm[e'])
+ * Replaces the reference's Torch replay (message_passing.py:378-409).
+ * plan_t partitions the transposed CSR.  dx_dev / dw_dev may be NULL to skip. */
+int tgx_csr_sum_bwd(const int32_t* row_ptr_t_dev, const int32_t* col_t_dev,
+                    const int32_t* perm_dev, const tgx_row_plan* plan_t,
+                    const float* x_dev, const float* w_dev,
+                    const float* dout_dev, float* dx_dev, float* dw_dev,
+                    int64_t n_dst, int64_t n_src, int64_t F,
+                    float* partial_dev, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* GAT additive edge attention (fp32)                                        */
+/*   z_e = a_src . h[j] + a_dst . h[i]   per head,  s_e = LeakyReLU(z_e)     */
+/*   out[i] = sum_e softmax_i(s)_e * h[j]                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Forward.  h [N, H, D] fp32 (src and dst node sets coincide), a_src/a_dst
+ * [H, D], out [N, H, D].  node_state [N, H, 4] fp32 receives per (node,head):
+ * [0] logsumexp of the row's scores (-inf for an empty row), [1] reserved for
+ * the backward (delta = <dout, out>), [2] a_dst.h[i], [3] a_src.h[i].
+ * partial_dev: tgx_partial_bytes(plan, H*D + 2*H) bytes (NULL if no split rows).
+ * Supported shapes: D % 4 == 0 and H*D in {64, 128, 256}; others return
+ * TGX_UNSUPPORTED.
+ * The reference evaluates this edge function with its eager oracle
+ * (interop/torch/message_passing.py:2848-2894 -> reducer_oracle.py:60-137). */
+int tgx_gat_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                const tgx_row_plan* plan, const float* h_dev,
+                const float* a_src_dev, const float* a_dst_dev,
+                float negative_slope, float* out_dev, float* node_state_dev,
+                int64_t n_nodes, int H, int D, float* partial_dev,
+                void* stream);
+
+/* Workspace bytes for tgx_gat_bwd with these plans. */
+int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
+                          int64_t n_edges, int H, int D, size_t* bytes);
+
+/* Fused backward from the saved logsumexp (no per-edge alpha is stored by
+ * the forward and no float atomics are used):
+ *   dh, da_src, da_dst for loss gradient dout [N, H, D].
+ * Uses the transposed CSR (row_ptr_t, col_t, perm) and its plan. */
+int tgx_gat_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                const tgx_row_plan* plan, const int32_t* row_ptr_t_dev,
+                const int32_t* col_t_dev, const int32_t* perm_dev,
+                const tgx_row_plan* plan_t, const float* h_dev,
+                const float* a_src_dev, const float* a_dst_dev,
+                float negative_slope, const float* out_dev,
+                float* node_state_dev, const float* dout_dev, float* dh_dev,
+                float* da_src_dev, float* da_dst_dev, int64_t n_nodes,
+                int64_t n_edges, int H, int D, void* workspace_dev,
+                size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Per-kernel timing (no reference counterpart; used by the benchmark)       */
+/* ------------------------------------------------------------------------ */
+
+/* Start recording a HIP event pair around every kernel this library
+ * launches (clears previous totals). */
+int tgx_profile_begin(void);
+/* Stop recording; synchronises the recorded events and accumulates the
+ * elapsed time per kernel name. */
+int tgx_profile_end(void);
+/* Number of distinct kernel names with accumulated time. */
+int tgx_profile_count(void);
+/* Entry `index`: kernel name (NUL-terminated, truncated to name_capacity),
+ * number of launches and total milliseconds. */
+int tgx_profile_entry(int index, char* name, int name_capacity, int64_t* launches,
+                      double* total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TGX_H_ */

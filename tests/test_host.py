@@ -1,0 +1,231 @@
+"""CPU tests of the product's host side: the C-ABI library loads and exports
+every declared entry point, the native planner matches the reference lit
+vectors, Graph validation/constructors, and edge-function recognition."""
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import tiga as tg
+from tiga import _native, capture as cap
+from oracle import ref, planner
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLD = json.loads((ROOT / "tests" / "golden" / "reference_vectors.json").read_text())
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "tgx.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tgx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_native.exported_symbols())
+    assert lib.tgx_abi_version() == 1
+    assert lib.tgx_status_string(1) == b"invalid argument"
+
+
+def _native_plan(case):
+    lib = _native.lib()
+    hist = case["histogram"]
+    harr = (ctypes.c_int64 * len(hist))(*hist) if hist is not None else None
+    code = ctypes.c_int()
+    util = ctypes.c_int64()
+    bounds = (ctypes.c_int64 * 64)()
+    mapping = (ctypes.c_int * 64)()
+    rows_in = (ctypes.c_int64 * 64)()
+    nb = ctypes.c_int()
+    ppr = ctypes.c_int64()
+    active = ctypes.c_int64()
+    st = lib.tgx_plan_reference_buckets(case["rows"], case["max"], case["sum"], harr,
+                                        int(case["has_node"]), ctypes.byref(code),
+                                        ctypes.byref(util), bounds, mapping, rows_in,
+                                        ctypes.byref(nb), ctypes.byref(ppr),
+                                        ctypes.byref(active))
+    assert st == 0
+    n = nb.value
+    return {"plan": planner.PLAN_NAMES[code.value], "utilization_milli": util.value,
+            "bounds": list(bounds[:n]), "mapping": [planner.MAPPING_NAMES[m] for m in mapping[:n]],
+            "rows_in_bucket": list(rows_in[:n]), "partials_per_row": ppr.value,
+            "active_rows": active.value}
+
+
+@pytest.mark.parametrize("case", GOLD["planner"], ids=lambda c: c["cite"].split(":")[0].split("/")[-1])
+def test_native_planner_matches_lit_vectors(case):
+    res = _native_plan(case)
+    for key, value in case["expect"].items():
+        if key in res:
+            assert res[key] == value, (key, res[key], value)
+    # and the native planner agrees with the oracle planner on every field
+    o = planner.plan(case["rows"], case["max"], case["sum"], case["histogram"], case["has_node"])
+    for key in res:
+        assert res[key] == o[key], key
+
+
+def test_native_planner_random_histograms_agree_with_oracle():
+    rng = np.random.default_rng(7)
+    for _ in range(200):
+        max_deg = int(rng.integers(1, 300))
+        rows = int(rng.integers(1, 600))
+        hist = np.zeros(max_deg + 1, dtype=np.int64)
+        degs = rng.integers(0, max_deg + 1, size=rows)
+        degs[0] = max_deg
+        np.add.at(hist, degs, 1)
+        case = {"rows": rows, "max": max_deg, "sum": int(degs.sum()),
+                "histogram": hist.tolist() if rng.random() < 0.8 else None,
+                "has_node": bool(rng.random() < 0.5)}
+        res = _native_plan(case)
+        o = planner.plan(case["rows"], case["max"], case["sum"], case["histogram"],
+                         case["has_node"])
+        for key in res:
+            assert res[key] == o[key], (case, key)
+
+
+def test_graph_from_csr_validation_messages():
+    rp = torch.tensor([0, 2, 3, 5])
+    col = torch.tensor([0, 2, 1, 0, 1])
+    g = tg.Graph.from_csr(rp, col, validate="full")
+    assert g.schema.num_src == 3 and g.schema.num_dst == 3
+    bad = [
+        (torch.tensor([1, 2, 3, 5]), col, "row_ptr\\[0\\] must be zero"),
+        (torch.tensor([0, 2, 3, 4]), col, "row_ptr\\[-1\\] must equal"),
+        (torch.tensor([0, 3, 2, 5]), col, "monotonic"),
+        (rp, torch.tensor([0, 2, 1, 0, 7]), "out-of-range"),
+    ]
+    for r, c, msg in bad:
+        with pytest.raises(ValueError, match=msg):
+            tg.Graph.from_csr(r, c, num_src=3, validate="full")
+        # the oracle restatement raises the same message
+        with pytest.raises(ValueError, match=msg):
+            ref.validate_csr(r.numpy(), c.numpy(), 3)
+    with pytest.raises(TypeError):
+        tg.Graph.from_csr(rp.float(), col)
+    with pytest.raises(ValueError):
+        tg.Graph.from_csr(rp.reshape(2, 2), col)
+
+
+def test_graph_constructors_match_oracle():
+    rng = np.random.default_rng(8)
+    src = rng.integers(0, 9, size=40)
+    dst = rng.integers(0, 7, size=40)
+    g = tg.Graph.from_coo(torch.tensor(src), torch.tensor(dst), num_src=9, num_dst=7)
+    rp, col, _ = ref.from_coo(src, dst, 9, 7)
+    r2, c2 = g.resolve_csr()
+    assert r2.tolist() == rp.tolist() and c2.tolist() == col.tolist()
+    t = g.transpose()
+    rpt, colt, _ = ref.transpose(rp, col, 9)
+    r3, c3 = t.resolve_csr()
+    assert r3.tolist() == rpt.tolist() and c3.tolist() == colt.tolist()
+    cu = torch.tensor([0, 3, 4, 9])
+    gv = tg.Graph.cu_seqlens(cu)
+    rp4, col4 = ref.cu_seqlens_csr(cu.numpy())
+    r4, c4 = gv.resolve_csr()
+    assert r4.tolist() == rp4.tolist() and c4.tolist() == col4.tolist()
+    assert gv.num_edges == int(rp4[-1])
+    gc = tg.Graph.cat([tg.Graph.regular(3, 2), tg.Graph.regular(2, 1)])
+    r5, c5 = gc.resolve_csr()
+    assert r5.tolist() == [0, 2, 4, 6, 7, 8] and c5.tolist() == [0, 1, 2, 0, 1, 2, 3, 4]
+
+
+class WeightedSum(tg.MessagePassing):
+    reducer = tg.sum()
+
+    def edge(self, src, dst, edge):
+        return edge.weight * src.x
+
+
+class WithBias(tg.MessagePassing):
+    reducer = tg.sum()
+
+    def edge(self, src, dst, edge):
+        return edge.conductivity * src.temperature
+
+    def node(self, dst, incoming):
+        return incoming + dst.bias
+
+
+class GAT(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def __init__(self, a_s, a_d, slope=0.2):
+        super().__init__()
+        self.a_s, self.a_d, self.slope = a_s, a_d, slope
+
+    def edge(self, src, dst, edge):
+        s = F.leaky_relu((src.h * self.a_s).sum(-1) + (dst.h * self.a_d).sum(-1), self.slope)
+        return self.reducer(s, src.h)
+
+
+class Dot(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge, scale):
+        return self.reducer((src.k * dst.q).sum(dim=-1) * scale + edge.bias, src.v)
+
+
+class Generic(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge):
+        return self.reducer(src.score.exp(), src.value)
+
+
+def test_recognizer_patterns():
+    assert cap.recognize_weighted_sum(WeightedSum()._captured({})) == cap.WeightedSum("x", "weight")
+    a = torch.zeros(2, 4)
+    g = cap.recognize_gat(GAT(a, a)._captured({}))
+    assert g is not None and g.h_field == "h" and g.slope == 0.2
+    d = cap.recognize_dot(Dot()._captured({"scale": 0.125}))
+    assert d == cap.DotProduct("q", "k", "v", 0.125, "bias")
+    assert Generic()._captured({}) is None
+
+
+def test_readme_and_quickstart_on_cpu_eager():
+    g = GOLD["readme_weighted_sum"]
+    graph = tg.Graph.from_csr(torch.tensor(g["row_ptr"]), torch.tensor(g["col_idx"]), num_src=3)
+    x = torch.tensor(g["x"], requires_grad=True)
+    w = torch.tensor(g["weight"], requires_grad=True)
+    k = WeightedSum()
+    out = k(graph=graph, src={"x": x}, dst={}, edge={"weight": w})
+    dx, dw = torch.autograd.grad(out.sum(), (x, w))
+    assert out.tolist() == g["out"] and dx.tolist() == g["dx"] and dw.tolist() == g["dw"]
+    assert k.last_variant.backend == "torch-eager"
+    q = GOLD["quickstart_node_bias"]
+    bias = torch.tensor(q["bias"], requires_grad=True)
+    out = WithBias()(graph=graph, src={"temperature": x}, dst={"bias": bias},
+                     edge={"conductivity": w})
+    np.testing.assert_allclose(out.detach().numpy(), q["out"], rtol=1e-6)
+
+
+def test_strict_mode_refuses_eager():
+    graph = tg.Graph.from_csr(torch.tensor([0, 1]), torch.tensor([0]), num_src=1)
+    tg.config.strict = True
+    try:
+        with pytest.raises(RuntimeError, match="strict"):
+            Generic()(graph=graph, src={"score": torch.ones(1), "value": torch.ones(1)}, dst={})
+    finally:
+        tg.config.strict = False
+
+
+def test_block_prune_threshold_rejected_on_csr():
+    class Pruned(tg.MessagePassing):
+        reducer = tg.online_softmax(block_prune_threshold=0.5)
+
+        def edge(self, src, dst, edge):
+            return self.reducer(src.s, src.v)
+
+    graph = tg.Graph.from_csr(torch.tensor([0, 1]), torch.tensor([0]), num_src=1)
+    with pytest.raises(NotImplementedError):
+        Pruned()(graph=graph, src={"s": torch.ones(1), "v": torch.ones(1)}, dst={})

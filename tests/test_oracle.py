@@ -1,0 +1,241 @@
+"""CPU checks that pin the oracle (oracle/ref.py, oracle/planner.py).
+
+Each oracle function is checked against something other than its own
+formula: the reference's golden vectors (tests/golden/reference_vectors.json),
+brute-force loops, closed forms, round trips and central finite differences.
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import planner, ref
+
+GOLD = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+
+
+def random_csr(rng, n_dst, n_src, max_deg, empty_frac=0.2):
+    deg = rng.integers(0, max_deg + 1, size=n_dst)
+    deg[rng.random(n_dst) < empty_frac] = 0
+    row_ptr = np.zeros(n_dst + 1, dtype=np.int64)
+    np.cumsum(deg, out=row_ptr[1:])
+    col = np.concatenate([np.sort(rng.integers(0, n_src, size=d)) for d in deg]) \
+        if deg.sum() else np.zeros(0, np.int64)
+    return row_ptr, col.astype(np.int64)
+
+
+# ---- graph indexing ---------------------------------------------------------
+
+def test_destination_index_brute_force():
+    rng = np.random.default_rng(0)
+    rp, col = random_csr(rng, 50, 40, 7)
+    expect = [i for i in range(50) for _ in range(rp[i], rp[i + 1])]
+    assert ref.destination_index(rp).tolist() == expect
+
+
+def test_transpose_brute_force_and_round_trip():
+    rng = np.random.default_rng(1)
+    rp, col = random_csr(rng, 60, 45, 9)
+    rpt, colt, perm = ref.transpose(rp, col, 45)
+    # brute force: for each source, scan edges in original order
+    dst = ref.destination_index(rp)
+    exp_rpt, exp_col, exp_perm = [0], [], []
+    for j in range(45):
+        for e in range(col.size):
+            if col[e] == j:
+                exp_col.append(dst[e])
+                exp_perm.append(e)
+        exp_rpt.append(len(exp_col))
+    assert rpt.tolist() == exp_rpt
+    assert colt.tolist() == exp_col
+    assert perm.tolist() == exp_perm
+    rp2, col2, _ = ref.transpose(rpt, colt, 60)
+    assert rp2.tolist() == rp.tolist() and col2.tolist() == col.tolist()
+
+
+def test_cu_seqlens_matches_cat_of_triangles():
+    # Reference property: cat([triangular(L)]) == cu_seqlens(cumsum(L))
+    # (tests/python/test_graph_constructors.py:56-110).
+    lengths = [3, 1, 0, 5]
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    rp, col = ref.cu_seqlens_csr(cu, causal=True)
+    blocks = []
+    for L in lengths:
+        brp = np.zeros(L + 1, np.int64)
+        np.cumsum(np.arange(1, L + 1), out=brp[1:])
+        bcol = np.concatenate([np.arange(i + 1) for i in range(L)]) if L else np.zeros(0, np.int64)
+        blocks.append((brp, bcol, L))
+    crp, ccol, ns = ref.cat_csr(blocks)
+    assert rp.tolist() == crp.tolist() and col.tolist() == ccol.tolist() and ns == sum(lengths)
+    rp_full, col_full = ref.cu_seqlens_csr(cu, causal=False)
+    assert rp_full[-1] == sum(L * L for L in lengths)
+
+
+def test_degree_bins_membership_brute_force():
+    rng = np.random.default_rng(2)
+    rp, _ = random_csr(rng, 300, 100, 40, empty_frac=0.3)
+    ub = [0, 4, 16, 1 << 40]
+    rows, off = ref.degree_bins(rp, ub)
+    deg = np.diff(rp)
+    lower = -1
+    for b, u in enumerate(ub):
+        members = rows[off[b]:off[b + 1]]
+        assert members.tolist() == sorted(members.tolist())       # ascending
+        expect = [i for i in range(300) if lower < deg[i] <= u]
+        assert members.tolist() == expect
+        lower = u
+
+
+# ---- sum reducer -------------------------------------------------------------
+
+def test_sum_readme_known_answer():
+    g = GOLD["readme_weighted_sum"]
+    out = ref.sum_fwd(g["row_ptr"], g["col_idx"], g["x"], g["weight"])
+    dx, dw = ref.sum_bwd(g["row_ptr"], g["col_idx"], g["x"], g["weight"], np.ones(3))
+    assert out.tolist() == g["out"]
+    assert dx.tolist() == g["dx"]
+    assert dw.tolist() == g["dw"]
+
+
+def test_sum_brute_force_and_finite_differences():
+    rng = np.random.default_rng(3)
+    rp, col = random_csr(rng, 20, 15, 6)
+    x = rng.standard_normal((15, 3))
+    w = rng.random(col.size)
+    out = ref.sum_fwd(rp, col, x, w)
+    for i in range(20):
+        s = np.zeros(3)
+        for e in range(rp[i], rp[i + 1]):
+            s += w[e] * x[col[e]]
+        np.testing.assert_allclose(out[i], s, rtol=1e-14, atol=1e-14)
+    dout = rng.standard_normal(out.shape)
+    dx, dw = ref.sum_bwd(rp, col, x, w, dout)
+    eps = 1e-6
+    for (arr, grad) in ((x, dx), (w, dw)):
+        flat = arr.reshape(-1)
+        for idx in rng.choice(flat.size, size=min(8, flat.size), replace=False):
+            old = flat[idx]
+            flat[idx] = old + eps
+            fp = (ref.sum_fwd(rp, col, x, w) * dout).sum()
+            flat[idx] = old - eps
+            fm = (ref.sum_fwd(rp, col, x, w) * dout).sum()
+            flat[idx] = old
+            assert abs((fp - fm) / (2 * eps) - grad.reshape(-1)[idx]) < 1e-6
+
+
+# ---- online softmax ---------------------------------------------------------
+
+def test_online_softmax_reference_known_answer():
+    g = GOLD["online_softmax_large_scores"]
+    score = np.asarray(g["score"])[np.asarray(g["col_idx"])]
+    value = np.asarray(g["value"])[np.asarray(g["col_idx"])]
+    out, lse = ref.segment_softmax(g["row_ptr"], score, value)
+    np.testing.assert_allclose(out, g["out"], atol=10 ** -g["places"])
+    dscore_e, dvalue_e = ref.segment_softmax_bwd(g["row_ptr"], score, value,
+                                                 np.ones_like(out))
+    # gradients w.r.t. the per-source fields: scatter edge grads by col
+    col = np.asarray(g["col_idx"])
+    dscore = np.zeros(3)
+    np.add.at(dscore, col, dscore_e)
+    dvalue = np.zeros((3, 2))
+    np.add.at(dvalue, col, dvalue_e)
+    np.testing.assert_allclose(dscore, g["dscore"], atol=10 ** -g["places"])
+    np.testing.assert_allclose(dvalue, g["dvalue"], atol=10 ** -g["places"])
+    assert np.all(np.isfinite(lse))
+
+
+def test_online_softmax_empty_row_and_heads():
+    g = GOLD["online_softmax_empty_row_heads"]
+    rp, col = np.asarray(g["row_ptr"]), np.asarray(g["col_idx"])
+    H, W = g["heads"], g["width"]
+    value_src = np.arange(4 * H * W, dtype=np.float64).reshape(4, H, W)
+    score = np.asarray(g["score"])
+    out, lse = ref.segment_softmax(rp, score, value_src[col])
+    assert np.all(out[1] == 0) and np.all(np.isneginf(lse[1]))
+    for row in (0, 2):
+        b, e = rp[row], rp[row + 1]
+        s = score[b:e]
+        p = np.exp(s - s.max(0)) / np.exp(s - s.max(0)).sum(0)
+        np.testing.assert_allclose(out[row], (p[..., None] * value_src[col[b:e]]).sum(0),
+                                   rtol=1e-12)
+
+
+def test_single_edge_closed_form():
+    rp = np.array([0, 1]); col = np.array([0])
+    out, lse = ref.segment_softmax(rp, np.array([[3.5]]), np.array([[[2.0, -1.0]]]))
+    assert out.tolist() == [[[2.0, -1.0]]] and lse.tolist() == [[3.5]]
+
+
+def _fd_check(f, arrays, grads, rng, eps=1e-6, tol=1e-6, picks=6):
+    for arr, grad in zip(arrays, grads):
+        flat = arr.reshape(-1)
+        for idx in rng.choice(flat.size, size=min(picks, flat.size), replace=False):
+            old = flat[idx]
+            flat[idx] = old + eps
+            fp = f()
+            flat[idx] = old - eps
+            fm = f()
+            flat[idx] = old
+            num = (fp - fm) / (2 * eps)
+            assert abs(num - grad.reshape(-1)[idx]) < tol * max(1.0, abs(num)), (num, grad.reshape(-1)[idx])
+
+
+def test_gat_finite_differences_and_uniform_closed_form():
+    rng = np.random.default_rng(4)
+    rp, col = random_csr(rng, 12, 12, 5)
+    H, D = 2, 3
+    h = rng.standard_normal((12, H, D))
+    a_s = rng.standard_normal((H, D)) * 0.5
+    a_d = rng.standard_normal((H, D)) * 0.5
+    dout = rng.standard_normal((12, H, D))
+    dh, das, dad = ref.gat_bwd(rp, col, h, a_s, a_d, 0.2, dout)
+    f = lambda: (ref.gat_fwd(rp, col, h, a_s, a_d, 0.2)[0] * dout).sum()
+    _fd_check(f, [h, a_s, a_d], [dh, das, dad], rng)
+    # a = 0 -> every score is 0 -> out is the neighbour mean
+    out, _ = ref.gat_fwd(rp, col, h, np.zeros((H, D)), np.zeros((H, D)), 0.2)
+    for i in range(12):
+        if rp[i + 1] > rp[i]:
+            np.testing.assert_allclose(out[i], h[col[rp[i]:rp[i + 1]]].mean(0), rtol=1e-12)
+        else:
+            assert np.all(out[i] == 0)
+
+
+def test_dot_finite_differences():
+    rng = np.random.default_rng(5)
+    rp, col = random_csr(rng, 10, 9, 6)
+    H, D = 2, 4
+    q = rng.standard_normal((10, H, D)); k = rng.standard_normal((9, H, D))
+    v = rng.standard_normal((9, H, D)); bias = rng.standard_normal((col.size, H))
+    dout = rng.standard_normal((10, H, D))
+    dq, dk, dv, db = ref.dot_bwd(rp, col, q, k, v, 0.5, bias, dout)
+    f = lambda: (ref.dot_fwd(rp, col, q, k, v, 0.5, bias)[0] * dout).sum()
+    _fd_check(f, [q, k, v, bias], [dq, dk, dv, db], rng)
+
+
+def test_varlen_matches_dot_on_materialized_csr():
+    rng = np.random.default_rng(6)
+    lengths = [5, 1, 7]
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    T, H, D = sum(lengths), 2, 4
+    q, k, v = (rng.standard_normal((T, H, D)) for _ in range(3))
+    rp, col = ref.cu_seqlens_csr(cu)
+    o1, l1 = ref.varlen_causal_fwd(cu, q, k, v, 0.3)
+    o2, l2 = ref.dot_fwd(rp, col, q, k, v, 0.3)
+    np.testing.assert_allclose(o1, o2, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(l1, l2, rtol=1e-12)
+    dout = rng.standard_normal((T, H, D))
+    g1 = ref.varlen_causal_bwd(cu, q, k, v, 0.3, dout)
+    g2 = ref.dot_bwd(rp, col, q, k, v, 0.3, None, dout)[:3]
+    for a, b in zip(g1, g2):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
+
+
+# ---- planner ---------------------------------------------------------------
+
+@pytest.mark.parametrize("case", GOLD["planner"], ids=lambda c: c["cite"].split(":")[0].split("/")[-1])
+def test_planner_lit_vectors(case):
+    res = planner.plan(case["rows"], case["max"], case["sum"], case["histogram"], case["has_node"])
+    for key, value in case["expect"].items():
+        assert res[key] == value, (key, res[key], value)

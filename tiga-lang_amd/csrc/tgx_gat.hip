@@ -1,0 +1,649 @@
+// GAT additive edge attention, fp32, over a destination-row CSR.
+//
+//   z_e = a_src[hd] . h[j, hd] + a_dst[hd] . h[i, hd]      (j = col[e], i = row)
+//   s_e = LeakyReLU(z_e, slope)
+//   out[i, hd] = sum_e softmax_i(s)_e * h[j, hd]
+//
+// Reference semantics: an edge() returning
+//   reducer(leaky_relu((src.h*a_src).sum(-1) + (dst.h*a_dst).sum(-1)), src.h)
+// evaluated by the eager oracle (python/tiga/interop/torch/message_passing.py:
+// 2848-2894, reducer_oracle.py:60-137): per-(row, head) max shift, exp, sum,
+// weighted sum, empty row -> 0.
+//
+// Layout: h is [N, H, D] fp32; one node row is 4*G floats spread over G lanes
+// (float4 per lane), so head hd occupies HL = D/4 consecutive lanes and its
+// dot products reduce with DPP inside the lane group.  node_state is
+// [N, H, 4] fp32 = {logsumexp, delta, a_dst.h[i], a_src.h[i]} so one 16-byte
+// load per lane brings every per-(node, head) scalar the backward needs.
+//
+// Backward (no float atomics, nothing per-edge saved by the forward):
+//   B1 node pass   delta[i] = <dout[i], out[i]> per head
+//   B2 source pass over the transposed CSR (row j = source): recompute
+//      alpha_e = exp(s_e - lse[i]) and dz_e = alpha_e (<dout[i], h[j]> - delta[i])
+//      * LeakyReLU'(z_e); dh[j] = sum alpha_e dout[i] + (sum dz_e) a_src;
+//      dz_e stored at its original edge id; da_src += (sum dz_e) h[j].
+//   B3 destination pass over the CSR: dh[i] += (sum_e dz_e) a_dst and
+//      da_dst += (sum_e dz_e) h[i] from the coalesced dz rows.
+//   da_* partials are fp64 per wave (static task striding), reduced in a
+//   fixed order, so every output is deterministic.
+#include <hip/hip_runtime.h>
+
+#include "tgx_device.h"
+#include "tgx_host.h"
+#include "tgx_profile.h"
+#include "tgx_softmax.h"
+#include "tgx_tasks.h"
+
+namespace tgx {
+namespace {
+
+constexpr int kPersistBlocks = 2048;  // persistent backward grid (8 waves / CU)
+
+__device__ __forceinline__ f32x4 ld4(const float* p) {
+  return *reinterpret_cast<const f32x4*>(p);
+}
+__device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+__device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
+  return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+}
+
+template <typename I>
+struct GatFwdArgs {
+  const I* row_ptr;
+  const I* col;
+  PlanView plan;
+  const float* h;
+  const float* a_src;
+  const float* a_dst;
+  float slope;
+  float* out;
+  float* ns;
+  float* partial;  // per chunk: acc[4G] | m[H] | l[H]
+};
+
+// Index of lane `src` in a wave, read by every lane (edge groups differ).
+template <int EPW>
+__device__ __forceinline__ int fetch_lane(int v, int src) {
+  if constexpr (EPW == 1) return __builtin_amdgcn_readlane(v, src);
+  return __shfl(v, src, 64);
+}
+
+template <typename I, int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
+  constexpr int EPW = kWave / G;
+  constexpr int HD = 4 * G;
+  constexpr int H = G / HL;
+  const Task t = decode_task(a.plan, a.row_ptr, global_wave());
+  if (t.kind == kTaskNone) return;
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int c = lane % G;
+  const int hd = c / HL;
+  const bool head_lead = (c % HL) == 0;
+  const f32x4 as4 = ld4(a.a_src + 4 * c);
+  const f32x4 ad4 = ld4(a.a_dst + 4 * c);
+
+  if (t.kind == kTaskEmpty) {
+    for (int k = 0; k < t.n_empty; ++k) {
+      const int64_t i = uniform(a.plan.rows[t.empty0 + k]);
+      const f32x4 hi = ld4(a.h + i * HD + 4 * c);
+      const float sdst = group_sum<HL>(dot4(ad4, hi));
+      const float ssrc = group_sum<HL>(dot4(as4, hi));
+      if (g == 0) {
+        st4(a.out + i * HD + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+        if (head_lead) st4(a.ns + (i * H + hd) * 4, f32x4{kNegInf, 0.f, sdst, ssrc});
+      }
+    }
+    return;
+  }
+
+  const int64_t row = t.row;
+  const f32x4 hi = ld4(a.h + row * HD + 4 * c);
+  const float sdst = group_sum<HL>(dot4(ad4, hi));
+
+  SoftState<4> st;
+  st.init();
+  for (int64_t base = t.e0; base < t.e1; base += kWave) {
+    const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
+    const int my_col = lane < n ? static_cast<int>(a.col[base + lane]) : 0;
+    for (int k = 0; k < n; k += EPW * U) {
+      f32x4 x[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
+        x[u] = ld4(a.h + static_cast<int64_t>(j) * HD + 4 * c);
+      }
+      float s[U];
+      float mc = kNegInf;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const float z = group_sum<HL>(dot4(as4, x[u])) + sdst;
+        s[u] = slot < n ? leaky_relu(z, a.slope) : kNegInf;
+        mc = fmaxf(mc, s[u]);
+      }
+      if (mc > st.m) st.rescale(mc);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float p = s[u] == kNegInf ? 0.f : fast_exp(s[u] - st.m);
+        st.l += p;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) st.acc[q] += p * x[u][q];
+      }
+    }
+  }
+#pragma unroll
+  for (int mask = G; mask < kWave; mask <<= 1) st.merge_xor(mask);
+  if (g != 0) return;
+  if (t.kind == kTaskChunk) {
+    float* p = a.partial + static_cast<int64_t>(t.slot) * (HD + 2 * H);
+    st4(p + 4 * c, f32x4{st.acc[0], st.acc[1], st.acc[2], st.acc[3]});
+    if (head_lead) {
+      p[HD + hd] = st.m;
+      p[HD + H + hd] = st.l;
+    }
+    return;
+  }
+  const float inv = 1.f / st.l;
+  st4(a.out + row * HD + 4 * c,
+      f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
+  const float ssrc_i = group_sum<HL>(dot4(as4, hi));
+  if (head_lead) st4(a.ns + (row * H + hd) * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc_i});
+}
+
+template <int G, int HL>
+__global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
+    PlanView plan, const float* __restrict__ partial, const float* __restrict__ h,
+    const float* __restrict__ a_src, const float* __restrict__ a_dst,
+    float* __restrict__ out, float* __restrict__ ns) {
+  constexpr int HD = 4 * G;
+  constexpr int H = G / HL;
+  const int64_t k = global_wave();
+  if (k >= plan.n_split) return;
+  const int lane = lane_id();
+  if (lane >= G) return;
+  const int c = lane, hd = c / HL;
+  const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
+  const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
+  SoftState<4> st;
+  st.init();
+  for (int q = c0; q < c1; ++q) {
+    const float* p = partial + static_cast<int64_t>(q) * (HD + 2 * H);
+    const f32x4 acc = ld4(p + 4 * c);
+    const float accs[4] = {acc[0], acc[1], acc[2], acc[3]};
+    st.merge(p[HD + hd], p[HD + H + hd], accs);
+  }
+  const float inv = 1.f / st.l;
+  st4(out + row * HD + 4 * c,
+      f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
+  const f32x4 hi = ld4(h + row * HD + 4 * c);
+  const float sdst = group_sum<HL>(dot4(ld4(a_dst + 4 * c), hi));
+  const float ssrc = group_sum<HL>(dot4(ld4(a_src + 4 * c), hi));
+  if (c % HL == 0) st4(ns + (row * H + hd) * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc});
+}
+
+// ---------------------------------------------------------------------------
+// Backward.
+
+template <int G, int HL>
+__global__ __launch_bounds__(kTaskBlock) void gat_delta_kernel(
+    const float* __restrict__ dout, const float* __restrict__ out, float* __restrict__ ns,
+    int64_t n_nodes) {
+  constexpr int EPW = kWave / G;
+  constexpr int HD = 4 * G;
+  constexpr int H = G / HL;
+  const int lane = lane_id();
+  const int c = lane % G, hd = c / HL;
+  const int64_t node = global_wave() * EPW + lane / G;
+  if (node >= n_nodes) return;
+  const float d = group_sum<HL>(dot4(ld4(dout + node * HD + 4 * c), ld4(out + node * HD + 4 * c)));
+  if (c % HL == 0) ns[(node * H + hd) * 4 + 1] = d;
+}
+
+struct GatSrcArgs {
+  const int32_t* row_ptr_t;
+  const int32_t* col_t;
+  const int32_t* perm;
+  PlanView plan;
+  const float* h;
+  const float* a_src;
+  float slope;
+  const float* ns;
+  const float* dout;
+  float* dh;
+  float* partial;   // per chunk: [4G] dh contribution
+  float* dz;        // [E, H] at original edge ids
+  double* dapart;   // [waves, 4G]
+  int64_t n_tasks;
+};
+
+template <int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
+  constexpr int EPW = kWave / G;
+  constexpr int HD = 4 * G;
+  constexpr int H = G / HL;
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int c = lane % G;
+  const int hd = c / HL;
+  const bool head_lead = (c % HL) == 0;
+  const f32x4 as4 = ld4(a.a_src + 4 * c);
+  f64x4 dap = {0.0, 0.0, 0.0, 0.0};
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t w = global_wave(); w < a.n_tasks; w += stride) {
+    const Task t = decode_task(a.plan, a.row_ptr_t, w);
+    if (t.kind == kTaskEmpty) {
+      for (int k = 0; k < t.n_empty; ++k) {
+        const int64_t j = uniform(a.plan.rows[t.empty0 + k]);
+        if (g == 0) st4(a.dh + j * HD + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+      }
+      continue;
+    }
+    if (t.kind == kTaskNone) continue;
+    const int64_t j = t.row;
+    const f32x4 hj = ld4(a.h + j * HD + 4 * c);
+    const float ssrc = a.ns[(j * H + hd) * 4 + 3];
+    f32x4 dha = {0.f, 0.f, 0.f, 0.f};
+    float sdz = 0.f;
+    for (int64_t base = t.e0; base < t.e1; base += kWave) {
+      const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
+      int my_i = 0, my_e = 0;
+      if (lane < n) {
+        my_i = a.col_t[base + lane];
+        my_e = a.perm[base + lane];
+      }
+      for (int k = 0; k < n; k += EPW * U) {
+        f32x4 d[U], nst[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int slot = k + u * EPW + g;
+          const int64_t i = fetch_lane<EPW>(my_i, slot < n ? slot : 0);
+          d[u] = ld4(a.dout + i * HD + 4 * c);
+          nst[u] = ld4(a.ns + (i * H + hd) * 4);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int slot = k + u * EPW + g;
+          const bool valid = slot < n;
+          const float z = ssrc + nst[u][2];
+          const float s = leaky_relu(z, a.slope);
+          const float alpha = valid ? fast_exp(s - nst[u][0]) : 0.f;
+          const float dalpha = group_sum<HL>(dot4(d[u], hj));
+          const float ds = alpha * (dalpha - nst[u][1]);
+          const float dzv = z > 0.f ? ds : ds * a.slope;
+          dha += alpha * d[u];
+          sdz += dzv;
+          const int e = fetch_lane<EPW>(my_e, valid ? slot : 0);
+          if (valid && head_lead) a.dz[static_cast<int64_t>(e) * H + hd] = dzv;
+        }
+      }
+    }
+#pragma unroll
+    for (int mask = G; mask < kWave; mask <<= 1) {
+      dha[0] += __shfl_xor(dha[0], mask, 64);
+      dha[1] += __shfl_xor(dha[1], mask, 64);
+      dha[2] += __shfl_xor(dha[2], mask, 64);
+      dha[3] += __shfl_xor(dha[3], mask, 64);
+      sdz += __shfl_xor(sdz, mask, 64);
+    }
+    const f32x4 contrib = dha + sdz * as4;
+    if (g == 0) {
+      const double sd = static_cast<double>(sdz);
+      dap[0] += sd * hj[0];
+      dap[1] += sd * hj[1];
+      dap[2] += sd * hj[2];
+      dap[3] += sd * hj[3];
+      if (t.kind == kTaskChunk)
+        st4(a.partial + static_cast<int64_t>(t.slot) * HD + 4 * c, contrib);
+      else
+        st4(a.dh + j * HD + 4 * c, contrib);
+    }
+  }
+  if (g == 0) {
+    double* p = a.dapart + global_wave() * HD + 4 * c;
+    p[0] = dap[0];
+    p[1] = dap[1];
+    p[2] = dap[2];
+    p[3] = dap[3];
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
+    PlanView plan, const float* __restrict__ partial, float* __restrict__ dh) {
+  constexpr int HD = 4 * G;
+  const int64_t k = global_wave();
+  if (k >= plan.n_split) return;
+  const int c = lane_id();
+  if (c >= G) return;
+  const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
+  const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int q = c0; q < c1; ++q) s += ld4(partial + static_cast<int64_t>(q) * HD + 4 * c);
+  st4(dh + row * HD + 4 * c, s);
+}
+
+template <typename I>
+struct GatDstArgs {
+  const I* row_ptr;
+  PlanView plan;
+  const float* h;
+  const float* a_dst;
+  const float* dz;   // [E, H]
+  float* dh;
+  float* partial;    // per chunk: [H]
+  double* dapart;    // [waves, 4G]
+  int64_t n_tasks;
+};
+
+template <typename I, int G, int HL>
+__global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a) {
+  constexpr int HD = 4 * G;
+  constexpr int H = G / HL;
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int c = lane % G;
+  const int hd = c / HL;
+  const f32x4 ad4 = ld4(a.a_dst + 4 * c);
+  f64x4 dap = {0.0, 0.0, 0.0, 0.0};
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t w = global_wave(); w < a.n_tasks; w += stride) {
+    const Task t = decode_task(a.plan, a.row_ptr, w);
+    if (t.kind == kTaskEmpty || t.kind == kTaskNone) continue;
+    const int64_t i = t.row;
+    // Sum dz over the row's edges: dz[e0*H .. e1*H) is contiguous and lane l
+    // always sees head l % H.
+    float s = 0.f;
+    const int64_t p0 = t.e0 * H, p1 = t.e1 * H;
+    for (int64_t p = p0 + lane; p < p1; p += kWave) s += a.dz[p];
+#pragma unroll
+    for (int mask = H; mask < kWave; mask <<= 1) s += __shfl_xor(s, mask, 64);
+    const float sdz = __shfl(s, hd, 64);
+    if (t.kind == kTaskChunk) {
+      if (lane < H) a.partial[static_cast<int64_t>(t.slot) * H + lane] = s;
+    }
+    if (g == 0) {
+      const f32x4 hi = ld4(a.h + i * HD + 4 * c);
+      const double sd = static_cast<double>(sdz);
+      dap[0] += sd * hi[0];
+      dap[1] += sd * hi[1];
+      dap[2] += sd * hi[2];
+      dap[3] += sd * hi[3];
+      if (t.kind == kTaskRow) {
+        float* q = a.dh + i * HD + 4 * c;
+        st4(q, ld4(q) + sdz * ad4);
+      }
+    }
+  }
+  if (g == 0) {
+    double* p = a.dapart + global_wave() * HD + 4 * c;
+    p[0] = dap[0];
+    p[1] = dap[1];
+    p[2] = dap[2];
+    p[3] = dap[3];
+  }
+}
+
+template <int G, int HL>
+__global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_merge_kernel(
+    PlanView plan, const float* __restrict__ partial, const float* __restrict__ a_dst,
+    float* __restrict__ dh) {
+  constexpr int HD = 4 * G;
+  constexpr int H = G / HL;
+  const int64_t k = global_wave();
+  if (k >= plan.n_split) return;
+  const int c = lane_id();
+  if (c >= G) return;
+  const int hd = c / HL;
+  const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
+  const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
+  float s = 0.f;
+  for (int q = c0; q < c1; ++q) s += partial[static_cast<int64_t>(q) * H + hd];
+  float* p = dh + row * HD + 4 * c;
+  st4(p, ld4(p) + s * ld4(a_dst + 4 * c));
+}
+
+// da[x] = sum over waves of dapart[w][x], fixed order, fp64.
+__global__ __launch_bounds__(256) void da_reduce_kernel(const double* __restrict__ part_src,
+                                                        const double* __restrict__ part_dst,
+                                                        int64_t src_waves, int64_t dst_waves,
+                                                        int HD,
+                                                        float* __restrict__ da_src,
+                                                        float* __restrict__ da_dst) {
+  const int x = blockIdx.x * 256 + threadIdx.x;
+  if (x >= 2 * HD) return;
+  const bool dst = x >= HD;
+  const int e = dst ? x - HD : x;
+  const double* p = dst ? part_dst : part_src;
+  const int64_t waves = dst ? dst_waves : src_waves;
+  double s = 0.0;
+  for (int64_t w = 0; w < waves; ++w) s += p[w * HD + e];
+  (dst ? da_dst : da_src)[e] = static_cast<float>(s);
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+
+struct GatShape {
+  int G, HL;
+};
+
+bool gat_shape(int H, int D, GatShape* s) {
+  if (H <= 0 || D <= 0 || D % 4 != 0) return false;
+  const int HD = H * D;
+  if (HD != 64 && HD != 128 && HD != 256) return false;
+  s->G = HD / 4;
+  s->HL = D / 4;
+  return s->HL >= 1 && s->HL <= 16 && s->G % s->HL == 0;
+}
+
+int64_t persist_blocks(int64_t tasks) {
+  int64_t b = ceil_div(tasks, kWavesPerBlock);
+  if (b > kPersistBlocks) b = kPersistBlocks;
+  return b > 0 ? b : 1;
+}
+
+#define TGX_GAT_SHAPES(X) \
+  X(64, 16) X(64, 8) X(64, 4) X(64, 2) X(64, 1) \
+  X(32, 16) X(32, 8) X(32, 4) X(32, 2) X(32, 1) \
+  X(16, 16) X(16, 8) X(16, 4) X(16, 2) X(16, 1)
+
+template <typename I, int G, int HL>
+int gat_fwd_launch(const GatFwdArgs<I>& a, hipStream_t s) {
+  constexpr int EPW = kWave / G;
+  constexpr int U = EPW >= 8 ? 1 : 8 / EPW;
+  const int64_t waves = plan_waves(a.plan);
+  if (waves > 0) {
+    TGX_PROFILE("gat_fwd_kernel", s);
+    gat_fwd_kernel<I, G, HL, U><<<ceil_div(waves, kWavesPerBlock), kTaskBlock, 0, s>>>(a);
+    TGX_LAUNCHED("gat_fwd_kernel");
+  }
+  if (a.plan.n_split > 0) {
+    TGX_PROFILE("gat_fwd_merge_kernel", s);
+    gat_fwd_merge_kernel<G, HL><<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        a.plan, a.partial, a.h, a.a_src, a.a_dst, a.out, a.ns);
+    TGX_LAUNCHED("gat_fwd_merge_kernel");
+  }
+  return TGX_OK;
+}
+
+struct GatBwdLayout {
+  size_t dz_off, src_part_off, dst_part_off, dap_src_off, dap_dst_off, bytes;
+  int64_t src_waves, dst_waves;
+};
+
+GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t,
+                            int64_t n_edges, int H, int D) {
+  GatBwdLayout L;
+  const int64_t HD = static_cast<int64_t>(H) * D;
+  const PlanView pv = plan_view(plan), pt = plan_view(plan_t);
+  L.src_waves = persist_blocks(plan_waves(pt)) * kWavesPerBlock;
+  L.dst_waves = persist_blocks(plan_waves(pv)) * kWavesPerBlock;
+  Carve c{nullptr, 0};
+  L.dz_off = reinterpret_cast<size_t>(c.take<float>(n_edges * H));
+  L.src_part_off = reinterpret_cast<size_t>(c.take<float>(plan_t.n_chunks * HD));
+  L.dst_part_off = reinterpret_cast<size_t>(c.take<float>(plan.n_chunks * H));
+  L.dap_src_off = reinterpret_cast<size_t>(c.take<double>(L.src_waves * HD));
+  L.dap_dst_off = reinterpret_cast<size_t>(c.take<double>(L.dst_waves * HD));
+  L.bytes = align_up(c.used);
+  return L;
+}
+
+template <typename I, int G, int HL>
+int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* row_ptr_t,
+                   const int32_t* col_t, const int32_t* perm, const tgx_row_plan& plan_t,
+                   const float* h, const float* a_src, const float* a_dst, float slope,
+                   const float* out, float* ns, const float* dout, float* dh, float* da_src,
+                   float* da_dst, int64_t n_nodes, int64_t n_edges, char* ws,
+                   const GatBwdLayout& L, hipStream_t s) {
+  constexpr int EPW = kWave / G;
+  constexpr int U = EPW >= 8 ? 1 : 8 / EPW;
+  constexpr int HD = 4 * G;
+  (void)n_edges;
+  float* dz = reinterpret_cast<float*>(ws + L.dz_off);
+  float* src_part = reinterpret_cast<float*>(ws + L.src_part_off);
+  float* dst_part = reinterpret_cast<float*>(ws + L.dst_part_off);
+  double* dap_src = reinterpret_cast<double*>(ws + L.dap_src_off);
+  double* dap_dst = reinterpret_cast<double*>(ws + L.dap_dst_off);
+  const PlanView pv = plan_view(plan), pt = plan_view(plan_t);
+
+  {
+  TGX_PROFILE("gat_delta_kernel", s);
+  gat_delta_kernel<G, HL><<<ceil_div(ceil_div(n_nodes, EPW), kWavesPerBlock), kTaskBlock, 0, s>>>(
+      dout, out, ns, n_nodes);
+  TGX_LAUNCHED("gat_delta_kernel");
+  }
+
+  GatSrcArgs sa{row_ptr_t, col_t, perm, pt, h, a_src, slope, ns, dout, dh, src_part, dz,
+                dap_src, plan_waves(pt)};
+  {
+  TGX_PROFILE("gat_bwd_src_kernel", s);
+  gat_bwd_src_kernel<G, HL, U><<<L.src_waves / kWavesPerBlock, kTaskBlock, 0, s>>>(sa);
+  TGX_LAUNCHED("gat_bwd_src_kernel");
+  }
+  if (pt.n_split > 0) {
+    TGX_PROFILE("gat_bwd_src_merge_kernel", s);
+    gat_bwd_src_merge_kernel<G><<<ceil_div(pt.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        pt, src_part, dh);
+    TGX_LAUNCHED("gat_bwd_src_merge_kernel");
+  }
+  GatDstArgs<I> da{row_ptr, pv, h, a_dst, dz, dh, dst_part, dap_dst, plan_waves(pv)};
+  {
+  TGX_PROFILE("gat_bwd_dst_kernel", s);
+  gat_bwd_dst_kernel<I, G, HL><<<L.dst_waves / kWavesPerBlock, kTaskBlock, 0, s>>>(da);
+  TGX_LAUNCHED("gat_bwd_dst_kernel");
+  }
+  if (pv.n_split > 0) {
+    TGX_PROFILE("gat_bwd_dst_merge_kernel", s);
+    gat_bwd_dst_merge_kernel<G, HL><<<ceil_div(pv.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        pv, dst_part, a_dst, dh);
+    TGX_LAUNCHED("gat_bwd_dst_merge_kernel");
+  }
+  if (da_src || da_dst) {
+    // Both outputs are required by the kernel; callers pass both.
+    TGX_PROFILE("da_reduce_kernel", s);
+    da_reduce_kernel<<<ceil_div(2 * HD, 256), 256, 0, s>>>(dap_src, dap_dst, L.src_waves,
+                                                          L.dst_waves, HD, da_src, da_dst);
+    TGX_LAUNCHED("da_reduce_kernel");
+  }
+  return TGX_OK;
+}
+
+}  // namespace
+}  // namespace tgx
+
+using namespace tgx;
+
+extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
+                           const tgx_row_plan* plan, const float* h, const float* a_src,
+                           const float* a_dst, float slope, float* out, float* ns,
+                           int64_t n_nodes, int H, int D, float* partial, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  GatShape shp;
+  if (!gat_shape(H, D, &shp)) {
+    set_error("GAT kernel supports H*D in {64,128,256} with D %% 4 == 0 (got H=%d D=%d)", H, D);
+    return TGX_UNSUPPORTED;
+  }
+  int st = check_plan(plan, n_nodes);
+  if (st != TGX_OK) return st;
+  if (n_nodes == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && col && h && a_src && a_dst && out && ns, "null pointer");
+  TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
+  hipStream_t s = as_stream(stream);
+#define TGX_GAT_FWD(GG, HH)                                                              \
+  if (shp.G == GG && shp.HL == HH) {                                                     \
+    if (idx_bits == 32)                                                                  \
+      return gat_fwd_launch<int32_t, GG, HH>(                                            \
+          GatFwdArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                      \
+                              static_cast<const int32_t*>(col), plan_view(*plan), h,     \
+                              a_src, a_dst, slope, out, ns, partial},                    \
+          s);                                                                            \
+    return gat_fwd_launch<int64_t, GG, HH>(                                              \
+        GatFwdArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                        \
+                            static_cast<const int64_t*>(col), plan_view(*plan), h, a_src, \
+                            a_dst, slope, out, ns, partial},                             \
+        s);                                                                              \
+  }
+  TGX_GAT_SHAPES(TGX_GAT_FWD)
+#undef TGX_GAT_FWD
+  set_error("unsupported GAT shape");
+  return TGX_UNSUPPORTED;
+}
+
+extern "C" int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
+                                     int64_t n_edges, int H, int D, size_t* bytes) {
+  TGX_REQUIRE(plan && plan_t && bytes, "null pointer");
+  GatShape shp;
+  if (!gat_shape(H, D, &shp)) {
+    set_error("unsupported GAT shape H=%d D=%d", H, D);
+    return TGX_UNSUPPORTED;
+  }
+  *bytes = gat_bwd_layout(*plan, *plan_t, n_edges, H, D).bytes;
+  return TGX_OK;
+}
+
+extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
+                           const tgx_row_plan* plan, const int32_t* row_ptr_t,
+                           const int32_t* col_t, const int32_t* perm,
+                           const tgx_row_plan* plan_t, const float* h, const float* a_src,
+                           const float* a_dst, float slope, const float* out, float* ns,
+                           const float* dout, float* dh, float* da_src, float* da_dst,
+                           int64_t n_nodes, int64_t n_edges, int H, int D, void* ws,
+                           size_t ws_bytes, void* stream) {
+  (void)col;
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  GatShape shp;
+  if (!gat_shape(H, D, &shp)) {
+    set_error("unsupported GAT shape H=%d D=%d", H, D);
+    return TGX_UNSUPPORTED;
+  }
+  int st = check_plan(plan, n_nodes);
+  if (st != TGX_OK) return st;
+  st = check_plan(plan_t, n_nodes);
+  if (st != TGX_OK) return st;
+  if (n_nodes == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns && dout && dh && da_src && da_dst,
+              "null pointer");
+  TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && perm), "null transposed CSR");
+  const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, H, D);
+  TGX_REQUIRE(ws && ws_bytes >= L.bytes, "workspace too small: need %zu bytes", L.bytes);
+  hipStream_t s = as_stream(stream);
+  char* w = static_cast<char*>(ws);
+#define TGX_GAT_BWD(GG, HH)                                                                \
+  if (shp.G == GG && shp.HL == HH) {                                                       \
+    if (idx_bits == 32)                                                                    \
+      return gat_bwd_launch<int32_t, GG, HH>(static_cast<const int32_t*>(row_ptr), *plan,  \
+                                             row_ptr_t, col_t, perm, *plan_t, h, a_src,    \
+                                             a_dst, slope, out, ns, dout, dh, da_src,      \
+                                             da_dst, n_nodes, n_edges, w, L, s);           \
+    return gat_bwd_launch<int64_t, GG, HH>(static_cast<const int64_t*>(row_ptr), *plan,    \
+                                           row_ptr_t, col_t, perm, *plan_t, h, a_src,      \
+                                           a_dst, slope, out, ns, dout, dh, da_src, da_dst, \
+                                           n_nodes, n_edges, w, L, s);                     \
+  }
+  TGX_GAT_SHAPES(TGX_GAT_BWD)
+#undef TGX_GAT_BWD
+  set_error("unsupported GAT shape");
+  return TGX_UNSUPPORTED;
+}

@@ -1,0 +1,287 @@
+// Sum reducer over a destination-row CSR:  out[i, :] = sum_e w[e] * x[col[e], :]
+//
+// Layout: a gathered row of F fp32 features is split into feature tiles of
+// G*VEC floats; G lanes hold one tile of one edge, VEC floats per lane
+// (16-byte loads when VEC == 4), so one wave keeps 64/G edges in flight per
+// vector load and U such loads per lane before consuming them.  The edge
+// groups are folded at the end of the row with cross-lane adds.
+//
+// The same kernel is the backward's dx pass: run over the transposed CSR with
+// x := dout and the weight fetched through the transpose permutation, it
+// computes dx[j] = sum_{e'} w[perm[e']] * dout[col_t[e']] with no atomics.  With
+// `self_x` set it also produces dw[perm[e']] = <dout[col_t[e']], x[j]> from the
+// row it already holds.
+#include <hip/hip_runtime.h>
+
+#include "tgx_device.h"
+#include "tgx_host.h"
+#include "tgx_profile.h"
+#include "tgx_tasks.h"
+
+namespace tgx {
+namespace {
+
+template <typename I>
+struct SumArgs {
+  const I* row_ptr;
+  const I* col;
+  PlanView plan;
+  const float* x;          // gathered table [*, F]
+  const float* w;          // per-edge weight or null (=1)
+  const int32_t* wperm;    // weight index = wperm[e] when non-null
+  float* out;              // [rows, F]
+  float* partial;          // [n_chunks, F]
+  const float* self_x;     // dw: row's own features [rows, F] (null = no dw)
+  float* dw;               // dw output, written at wperm ? wperm[e] : e
+  int64_t F;
+};
+
+template <int VEC>
+struct Vec;
+template <>
+struct Vec<4> {
+  typedef f32x4 T;
+  static __device__ __forceinline__ T load(const float* p) {
+    return *reinterpret_cast<const f32x4*>(p);
+  }
+  static __device__ __forceinline__ void store(float* p, T v) {
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+  static __device__ __forceinline__ T zero() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  static __device__ __forceinline__ float dot(T a, T b) {
+    return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+  }
+  static __device__ __forceinline__ T shfl_xor(T v, int m) {
+    return f32x4{__shfl_xor(v[0], m, 64), __shfl_xor(v[1], m, 64),
+                 __shfl_xor(v[2], m, 64), __shfl_xor(v[3], m, 64)};
+  }
+};
+template <>
+struct Vec<1> {
+  typedef float T;
+  static __device__ __forceinline__ T load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, T v) { *p = v; }
+  static __device__ __forceinline__ T zero() { return 0.f; }
+  static __device__ __forceinline__ float dot(T a, T b) { return a * b; }
+  static __device__ __forceinline__ T shfl_xor(T v, int m) { return __shfl_xor(v, m, 64); }
+};
+
+template <int G>
+__device__ __forceinline__ float group_reduce_sum(float v) {
+  // Sum over the G lanes of one edge group (aligned, contiguous).
+  return group_sum<G>(v);
+}
+
+template <typename I, int VEC, int G, int U>
+__global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I> a) {
+  typedef Vec<VEC> V;
+  typedef typename V::T T;
+  constexpr int EPW = kWave / G;  // edges per wave-wide load
+  const Task t = decode_task(a.plan, a.row_ptr, global_wave());
+  if (t.kind == kTaskNone) return;
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int c = lane % G;
+  const int64_t F = a.F;
+  const int64_t fo = static_cast<int64_t>(blockIdx.y) * (G * VEC) + c * VEC;
+  const bool active = fo < F;
+
+  if (t.kind == kTaskEmpty) {
+    for (int k = 0; k < t.n_empty; ++k) {
+      const int row = uniform(a.plan.rows[t.empty0 + k]);
+      if (g == 0 && active) V::store(a.out + static_cast<int64_t>(row) * F + fo, V::zero());
+    }
+    return;
+  }
+
+  T self = V::zero();
+  const bool want_dw = a.self_x != nullptr;
+  if (want_dw && active) self = V::load(a.self_x + static_cast<int64_t>(t.row) * F + fo);
+
+  T acc = V::zero();
+  for (int64_t base = t.e0; base < t.e1; base += kWave) {
+    const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
+    int my_col = 0;
+    float my_w = 0.f;
+    int my_widx = 0;
+    if (lane < n) {
+      my_col = static_cast<int>(a.col[base + lane]);
+      my_widx = a.wperm ? a.wperm[base + lane] : static_cast<int>(base + lane);
+      my_w = a.w ? a.w[my_widx] : 1.f;
+    }
+    for (int k = 0; k < n; k += EPW * U) {
+      T v[U];
+      float wt[U];
+      int slot[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        slot[u] = k + u * EPW + g;
+        const int src = slot[u] < n ? slot[u] : 0;
+        const int j = __shfl(my_col, src, 64);
+        wt[u] = __shfl(my_w, src, 64);
+        v[u] = (slot[u] < n && active) ? V::load(a.x + static_cast<int64_t>(j) * F + fo)
+                                       : V::zero();
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (slot[u] < n) acc += wt[u] * v[u];
+      }
+      if (want_dw) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float d = group_reduce_sum<G>(V::dot(v[u], self));
+          const int src = slot[u] < n ? slot[u] : 0;
+          const int widx = __shfl(my_widx, src, 64);
+          if (c == 0 && slot[u] < n) a.dw[widx] = d;
+        }
+      }
+    }
+  }
+  // Fold the EPW edge groups (lanes with equal c).
+#pragma unroll
+  for (int m = G; m < kWave; m <<= 1) acc += V::shfl_xor(acc, m);
+  if (g != 0 || !active) return;
+  if (t.kind == kTaskChunk)
+    V::store(a.partial + static_cast<int64_t>(t.slot) * F + fo, acc);
+  else
+    V::store(a.out + static_cast<int64_t>(t.row) * F + fo, acc);
+}
+
+// Combine split-row chunk partials in chunk order (deterministic).
+__global__ __launch_bounds__(kTaskBlock) void sum_merge_kernel(PlanView plan,
+                                                               const float* __restrict__ partial,
+                                                               float* __restrict__ out, int64_t F) {
+  const int64_t k = global_wave();
+  if (k >= plan.n_split) return;
+  const int row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
+  const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
+  for (int64_t f = lane_id(); f < F; f += kWave) {
+    float s = 0.f;
+    for (int c = c0; c < c1; ++c) s += partial[static_cast<int64_t>(c) * F + f];
+    out[static_cast<int64_t>(row) * F + f] = s;
+  }
+}
+
+template <typename I, int VEC, int G>
+void launch_sum(const SumArgs<I>& a, int64_t ftiles, hipStream_t s) {
+  const int64_t waves = plan_waves(a.plan);
+  dim3 grid(static_cast<unsigned>(ceil_div(waves, kWavesPerBlock)), static_cast<unsigned>(ftiles));
+  constexpr int U = (kWave / G) >= 16 ? 1 : (16 / (kWave / G) < 8 ? 16 / (kWave / G) : 8);
+  sum_rows_kernel<I, VEC, G, U><<<grid, kTaskBlock, 0, s>>>(a);
+}
+
+template <typename I>
+int sum_dispatch(const SumArgs<I>& a, hipStream_t s) {
+  const int64_t F = a.F;
+  if (F % 4 == 0) {
+    const int64_t lanes = F / 4;
+    if (lanes <= 1) launch_sum<I, 4, 1>(a, 1, s);
+    else if (lanes <= 2) launch_sum<I, 4, 2>(a, 1, s);
+    else if (lanes <= 4) launch_sum<I, 4, 4>(a, 1, s);
+    else if (lanes <= 8) launch_sum<I, 4, 8>(a, 1, s);
+    else if (lanes <= 16) launch_sum<I, 4, 16>(a, 1, s);
+    else if (lanes <= 32) launch_sum<I, 4, 32>(a, 1, s);
+    else launch_sum<I, 4, 64>(a, ceil_div(lanes, 64), s);
+  } else {
+    if (F <= 1) launch_sum<I, 1, 1>(a, 1, s);
+    else if (F <= 2) launch_sum<I, 1, 2>(a, 1, s);
+    else if (F <= 4) launch_sum<I, 1, 4>(a, 1, s);
+    else if (F <= 8) launch_sum<I, 1, 8>(a, 1, s);
+    else if (F <= 16) launch_sum<I, 1, 16>(a, 1, s);
+    else if (F <= 32) launch_sum<I, 1, 32>(a, 1, s);
+    else launch_sum<I, 1, 64>(a, ceil_div(F, 64), s);
+  }
+  TGX_LAUNCHED("sum_rows_kernel");
+  if (a.plan.n_split > 0) {
+    sum_merge_kernel<<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        a.plan, a.partial, a.out, F);
+    TGX_LAUNCHED("sum_merge_kernel");
+  }
+  return TGX_OK;
+}
+
+// dw for feature widths that span several tiles: one wave per edge group of
+// the transposed CSR row, full-width dot product.
+template <typename I>
+__global__ __launch_bounds__(kTaskBlock) void sum_dw_wide_kernel(
+    const int32_t* __restrict__ row_ptr_t, const int32_t* __restrict__ col_t,
+    const int32_t* __restrict__ perm, const float* __restrict__ x,
+    const float* __restrict__ dout, float* __restrict__ dw, int64_t n_src, int64_t F) {
+  const int64_t j = global_wave();
+  if (j >= n_src) return;
+  const int64_t b = row_ptr_t[j], e = row_ptr_t[j + 1];
+  for (int64_t k = b; k < e; ++k) {
+    const int64_t i = col_t[k];
+    float s = 0.f;
+    for (int64_t f = lane_id(); f < F; f += kWave) s += dout[i * F + f] * x[j * F + f];
+    s = group_sum<64>(s);
+    if (lane_id() == 0) dw[perm[k]] = s;
+  }
+}
+
+}  // namespace
+
+}  // namespace tgx
+
+using namespace tgx;
+
+extern "C" int tgx_partial_bytes(const tgx_row_plan* plan, int64_t state_floats,
+                                 size_t* bytes) {
+  TGX_REQUIRE(plan && bytes, "null pointer");
+  TGX_REQUIRE(state_floats >= 0, "negative state size");
+  *bytes = static_cast<size_t>(plan->n_chunks) * state_floats * sizeof(float);
+  return TGX_OK;
+}
+
+extern "C" int tgx_csr_sum_fwd(const void* row_ptr, const void* col, int idx_bits,
+                               const tgx_row_plan* plan, const float* x, const float* w,
+                               float* out, int64_t n_dst, int64_t n_src, int64_t F,
+                               float* partial, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(F > 0 && n_dst >= 0 && n_src >= 0, "bad sizes");
+  int st = check_plan(plan, n_dst);
+  if (st != TGX_OK) return st;
+  if (n_dst == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && col && out && (x || n_src == 0), "null pointer");
+  TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
+  hipStream_t s = as_stream(stream);
+  TGX_PROFILE("csr_sum_fwd", s);
+  if (idx_bits == 32) {
+    SumArgs<int32_t> a{static_cast<const int32_t*>(row_ptr), static_cast<const int32_t*>(col),
+                       plan_view(*plan), x, w, nullptr, out, partial, nullptr, nullptr, F};
+    return sum_dispatch(a, s);
+  }
+  SumArgs<int64_t> a{static_cast<const int64_t*>(row_ptr), static_cast<const int64_t*>(col),
+                     plan_view(*plan), x, w, nullptr, out, partial, nullptr, nullptr, F};
+  return sum_dispatch(a, s);
+}
+
+extern "C" int tgx_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_t,
+                               const int32_t* perm, const tgx_row_plan* plan_t,
+                               const float* x, const float* w, const float* dout,
+                               float* dx, float* dw, int64_t n_dst, int64_t n_src,
+                               int64_t F, float* partial, void* stream) {
+  TGX_REQUIRE(F > 0 && n_dst >= 0 && n_src >= 0, "bad sizes");
+  int st = check_plan(plan_t, n_src);
+  if (st != TGX_OK) return st;
+  if (n_src == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr_t && col_t && perm && dout, "null pointer");
+  TGX_REQUIRE(!dw || x, "dw needs x");
+  TGX_REQUIRE(plan_t->n_chunks == 0 || partial || !dx, "split rows need a partial buffer");
+  hipStream_t s = as_stream(stream);
+  const bool single_tile = (F % 4 == 0) ? (F / 4 <= 64) : (F <= 64);
+  TGX_PROFILE("csr_sum_bwd", s);
+  if (dx) {
+    SumArgs<int32_t> a{row_ptr_t, col_t, plan_view(*plan_t), dout, w, perm, dx, partial,
+                       (dw && single_tile) ? x : nullptr, (dw && single_tile) ? dw : nullptr,
+                       F};
+    st = sum_dispatch(a, s);
+    if (st != TGX_OK) return st;
+  }
+  if (dw && (!dx || !single_tile)) {
+    sum_dw_wide_kernel<int32_t><<<ceil_div(n_src, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        row_ptr_t, col_t, perm, x, dout, dw, n_src, F);
+    TGX_LAUNCHED("sum_dw_wide_kernel");
+  }
+  return TGX_OK;
+}

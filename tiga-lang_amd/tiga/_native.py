@@ -1,0 +1,165 @@
+"""ctypes binding of libtgx_hip.so (the C ABI declared in include/tgx.h).
+
+Every call passes raw device pointers from Torch tensors and Torch's current
+HIP stream; a non-zero status raises ``RuntimeError`` with the library's
+message, as the reference runtime binding does
+(python/tiga/runtime/__init__.py:279-285).  The library is loaded from the
+package's own ``_lib`` directory only; nothing here falls back to another
+implementation when it is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtgx_hip.so"
+_lib = None
+
+c_int = ctypes.c_int
+c_i64 = ctypes.c_int64
+c_f32 = ctypes.c_float
+c_size = ctypes.c_size_t
+c_vp = ctypes.c_void_p
+P = ctypes.POINTER
+
+
+class RowPlan(ctypes.Structure):
+    """Mirror of ``tgx_row_plan``."""
+
+    _fields_ = [
+        ("n_rows", c_i64),
+        ("n_empty", c_i64),
+        ("n_wave", c_i64),
+        ("n_split", c_i64),
+        ("n_chunks", c_i64),
+        ("wave_max", ctypes.c_int32),
+        ("chunk_edges", ctypes.c_int32),
+        ("rows_dev", c_vp),
+        ("chunk_offsets_dev", c_vp),
+    ]
+
+
+# name -> argtypes (all return int status except where noted)
+_SIGNATURES: dict[str, list] = {
+    "tgx_abi_version": [],
+    "tgx_destination_index": [c_vp, c_int, c_i64, c_i64, c_vp, c_int, c_vp],
+    "tgx_csr_transpose_workspace": [c_i64, c_i64, c_i64, P(c_size)],
+    "tgx_csr_transpose": [c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
+                          c_vp, c_size, c_vp],
+    "tgx_plan_degree_bins_workspace": [c_i64, c_int, P(c_size)],
+    "tgx_plan_degree_bins": [c_vp, c_int, c_i64, P(c_i64), c_int, c_vp, P(c_i64), c_vp,
+                             c_size, c_vp],
+    "tgx_plan_split_chunks": [c_vp, c_int, c_vp, c_i64, ctypes.c_int32, c_vp, P(c_i64),
+                              c_vp],
+    "tgx_plan_reference_buckets": [c_i64, c_i64, c_i64, P(c_i64), c_int, P(c_int),
+                                   P(c_i64), P(c_i64), P(c_int), P(c_i64), P(c_int),
+                                   P(c_i64), P(c_i64)],
+    "tgx_partial_bytes": [P(RowPlan), c_i64, P(c_size)],
+    "tgx_csr_sum_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64,
+                        c_i64, c_vp, c_vp],
+    "tgx_csr_sum_bwd": [c_vp, c_vp, c_vp, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_vp,
+                        c_i64, c_i64, c_i64, c_vp, c_vp],
+    "tgx_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
+                    c_i64, c_int, c_int, c_vp, c_vp],
+    "tgx_gat_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, P(c_size)],
+    "tgx_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, P(RowPlan), c_vp,
+                    c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
+                    c_int, c_int, c_vp, c_size, c_vp],
+    "tgx_profile_begin": [],
+    "tgx_profile_end": [],
+    "tgx_profile_count": [],
+    "tgx_profile_entry": [c_int, ctypes.c_char_p, c_int, P(c_i64), P(ctypes.c_double)],
+}
+
+_OPTIONAL: dict[str, list] = {}
+
+
+def library_path() -> Path:
+    return Path(os.environ.get("TGX_LIBRARY", _LIB_PATH))
+
+
+def available() -> bool:
+    return library_path().exists()
+
+
+def lib():
+    """Load (once) and return the native library; raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"libtgx_hip.so not found at {path}; build it with "
+            "`python tiga-lang_amd/build_native.py` (or __graft_entry__.build())")
+    handle = ctypes.CDLL(str(path))
+    handle.tgx_status_string.restype = ctypes.c_char_p
+    handle.tgx_status_string.argtypes = [c_int]
+    handle.tgx_last_error.restype = ctypes.c_char_p
+    handle.tgx_last_error.argtypes = []
+    for name, argtypes in {**_SIGNATURES, **_OPTIONAL}.items():
+        fn = getattr(handle, name, None)
+        if fn is None:
+            if name in _OPTIONAL:
+                continue
+            raise RuntimeError(f"{path} does not export {name}")
+        fn.restype = c_int
+        fn.argtypes = argtypes
+    _lib = handle
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    handle = lib()
+    status = getattr(handle, name)(*args)
+    if status != 0:
+        message = handle.tgx_last_error().decode(errors="replace")
+        kind = handle.tgx_status_string(status).decode()
+        error = NotImplementedError if status == 2 else RuntimeError
+        raise error(f"{name}: {kind}: {message}")
+
+
+def exported_symbols() -> list[str]:
+    return sorted(_SIGNATURES) + ["tgx_last_error", "tgx_status_string"]
+
+
+def ptr(tensor) -> int | None:
+    """Device pointer of a tensor (None for a missing optional operand)."""
+    if tensor is None:
+        return None
+    return tensor.data_ptr()
+
+
+def stream_of(tensor) -> int:
+    import torch
+
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def idx_bits(tensor) -> int:
+    import torch
+
+    return 64 if tensor.dtype == torch.int64 else 32
+
+
+class KernelTimer:
+    """Context manager over tgx_profile_begin/end: per-kernel launch counts
+    and total milliseconds of every kernel the library launched inside it."""
+
+    def __enter__(self):
+        call("tgx_profile_begin")
+        self.totals = {}
+        return self
+
+    def __exit__(self, *exc):
+        call("tgx_profile_end")
+        handle = lib()
+        buf = ctypes.create_string_buffer(128)
+        n_launch = c_i64()
+        ms = ctypes.c_double()
+        for i in range(handle.tgx_profile_count()):
+            call("tgx_profile_entry", i, buf, 128, ctypes.byref(n_launch), ctypes.byref(ms))
+            self.totals[buf.value.decode()] = (n_launch.value, ms.value)
+        return False

@@ -1,0 +1,393 @@
+"""Destination-row CSR relation on Torch tensors.
+
+Public constructors and queries mirror the reference Torch graph
+(python/tiga/interop/torch/graph.py): ``from_csr`` 153-190 (validation
+595-617), ``from_coo`` 193-231, ``regular`` 233-257, ``cu_seqlens`` 260-294,
+``cat`` 297-340, ``transpose`` 675-685, ``destination_index`` 1212-1222,
+``degree_bounds`` 1224-1245.
+
+On top of that, a graph caches the device-side structures the HIP kernels
+need, built once per graph by the native planner (one host sync each):
+the degree-binned row plan of the CSR, and the stable transpose
+(row_ptr_t, col_t, perm) with its own row plan.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Literal
+
+import torch
+
+from . import _native
+
+_INDEX_DTYPES = (torch.int32, torch.int64)
+
+# Rows with at most WAVE_MAX edges run whole on one wavefront; longer rows are
+# split into CHUNK_EDGES-edge chunks whose partial states are merged.
+WAVE_MAX = 512
+CHUNK_EDGES = 512
+
+
+@dataclass(frozen=True)
+class GraphSchema:
+    num_src: int
+    num_dst: int
+    origin: str
+    realization: str
+    index_dtype: torch.dtype
+    sorted_by_dst: bool = True
+
+
+class RowPlanHandle:
+    """A ``tgx_row_plan`` plus the device tensors it points into."""
+
+    def __init__(self, plan: _native.RowPlan, rows: torch.Tensor, chunk_offsets: torch.Tensor):
+        self.plan = plan
+        self.rows = rows
+        self.chunk_offsets = chunk_offsets
+
+    @property
+    def ref(self):
+        return ctypes.byref(self.plan)
+
+    def counts(self) -> dict[str, int]:
+        p = self.plan
+        return {"empty": p.n_empty, "wave": p.n_wave, "split": p.n_split,
+                "chunks": p.n_chunks, "wave_max": p.wave_max,
+                "chunk_edges": p.chunk_edges}
+
+
+class Transposed:
+    """Source-row CSR of a graph: row_ptr_t [num_src+1], col_t [E], perm [E]."""
+
+    def __init__(self, row_ptr_t, col_t, perm, plan):
+        self.row_ptr_t = row_ptr_t
+        self.col_t = col_t
+        self.perm = perm
+        self.plan = plan
+
+
+def build_row_plan(row_ptr: torch.Tensor, n_rows: int, *, wave_max: int = WAVE_MAX,
+                   chunk_edges: int = CHUNK_EDGES) -> RowPlanHandle:
+    """Run the native degree-bin partition (empty | wave | split) on row_ptr."""
+    device = row_ptr.device
+    bits = _native.idx_bits(row_ptr)
+    stream = _native.stream_of(row_ptr)
+    rows = torch.empty(max(n_rows, 1), dtype=torch.int32, device=device)
+    ws_bytes = ctypes.c_size_t()
+    _native.call("tgx_plan_degree_bins_workspace", n_rows, 3, ctypes.byref(ws_bytes))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=device)
+    bounds = (ctypes.c_int64 * 3)(0, wave_max, 1 << 62)
+    offsets = (ctypes.c_int64 * 4)()
+    _native.call("tgx_plan_degree_bins", _native.ptr(row_ptr), bits, n_rows, bounds, 3,
+                 rows.data_ptr(), offsets, ws.data_ptr(), ws_bytes.value, stream)
+    n_empty = offsets[1] - offsets[0]
+    n_wave = offsets[2] - offsets[1]
+    n_split = offsets[3] - offsets[2]
+    chunk_offsets = torch.zeros(n_split + 1, dtype=torch.int32, device=device)
+    n_chunks = ctypes.c_int64(0)
+    if n_split:
+        _native.call("tgx_plan_split_chunks", _native.ptr(row_ptr), bits,
+                     rows.data_ptr() + 4 * offsets[2], n_split, chunk_edges,
+                     chunk_offsets.data_ptr(), ctypes.byref(n_chunks), stream)
+    plan = _native.RowPlan(n_rows, n_empty, n_wave, n_split, n_chunks.value, wave_max,
+                           chunk_edges, rows.data_ptr(), chunk_offsets.data_ptr())
+    return RowPlanHandle(plan, rows, chunk_offsets)
+
+
+def build_transpose(row_ptr: torch.Tensor, col_idx: torch.Tensor, num_dst: int,
+                    num_src: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    device = row_ptr.device
+    E = col_idx.numel()
+    row_ptr_t = torch.empty(num_src + 1, dtype=torch.int32, device=device)
+    col_t = torch.empty(max(E, 1), dtype=torch.int32, device=device)
+    perm = torch.empty(max(E, 1), dtype=torch.int32, device=device)
+    ws_bytes = ctypes.c_size_t()
+    _native.call("tgx_csr_transpose_workspace", num_dst, num_src, E, ctypes.byref(ws_bytes))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=device)
+    _native.call("tgx_csr_transpose", row_ptr.data_ptr(), col_idx.data_ptr(),
+                 _native.idx_bits(row_ptr), num_dst, num_src, E, row_ptr_t.data_ptr(),
+                 col_t.data_ptr(), perm.data_ptr(), ws.data_ptr(), ws_bytes.value,
+                 _native.stream_of(row_ptr))
+    return row_ptr_t, col_t[:E], perm[:E]
+
+
+class Graph:
+    """Torch realization of a Tiga relation (destination-row CSR)."""
+
+    _tiga_graph = True
+
+    def __init__(self, schema: GraphSchema, *, row_ptr=None, col_idx=None,
+                 cu_seqlens=None, causal=True, device=None):
+        self._schema = schema
+        self._row_ptr = row_ptr
+        self._col_idx = col_idx
+        self._cu_seqlens = cu_seqlens
+        self._causal = causal
+        self._device = torch.device(device) if device is not None else None
+        self._destination_index_cache = None
+        self._degree_bounds_cache = None
+        self._native_cache: dict[object, object] = {}
+
+    # ---- constructors ----------------------------------------------------
+    @staticmethod
+    def _validate_index_tensor(name: str, value: torch.Tensor) -> None:
+        if not isinstance(value, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if value.ndim != 1:
+            raise ValueError(f"{name} must be one-dimensional")
+        if value.dtype not in _INDEX_DTYPES:
+            raise TypeError(f"{name} must have int32 or int64 dtype")
+
+    @staticmethod
+    def _validate_csr_values(row_ptr, col_idx, num_src: int) -> None:
+        if int(row_ptr[0].item()) != 0:
+            raise ValueError("row_ptr[0] must be zero")
+        if int(row_ptr[-1].item()) != col_idx.numel():
+            raise ValueError("row_ptr[-1] must equal the number of edges")
+        if bool(torch.any(row_ptr[1:] < row_ptr[:-1]).item()):
+            raise ValueError("row_ptr must be monotonic")
+        if col_idx.numel():
+            lo = int(col_idx.min().item())
+            hi = int(col_idx.max().item())
+            if lo < 0 or hi >= num_src:
+                raise ValueError("col_idx contains an out-of-range source index")
+
+    @classmethod
+    def from_csr(cls, row_ptr: torch.Tensor, col_idx: torch.Tensor, *,
+                 num_src: int | None = None, sorted_by_dst: bool = True,
+                 validate: Literal["basic", "full"] = "basic") -> "Graph":
+        cls._validate_index_tensor("row_ptr", row_ptr)
+        cls._validate_index_tensor("col_idx", col_idx)
+        if row_ptr.device != col_idx.device:
+            raise ValueError("row_ptr and col_idx must be on the same device")
+        if row_ptr.numel() == 0:
+            raise ValueError("row_ptr must contain at least the initial zero")
+        num_dst = row_ptr.numel() - 1
+        if num_src is None:
+            num_src = num_dst if col_idx.numel() == 0 else int(col_idx.max().item()) + 1
+        if num_src < 0:
+            raise ValueError("num_src must be non-negative")
+        if validate == "full":
+            cls._validate_csr_values(row_ptr, col_idx, num_src)
+        elif validate != "basic":
+            raise ValueError("validate must be 'basic' or 'full'")
+        schema = GraphSchema(num_src=num_src, num_dst=num_dst, origin="explicit",
+                             realization="materialized_csr", index_dtype=col_idx.dtype,
+                             sorted_by_dst=sorted_by_dst)
+        return cls(schema, row_ptr=row_ptr, col_idx=col_idx)
+
+    @classmethod
+    def from_coo(cls, src: torch.Tensor, dst: torch.Tensor, *, num_src: int | None = None,
+                 num_dst: int | None = None) -> "Graph":
+        cls._validate_index_tensor("src", src)
+        cls._validate_index_tensor("dst", dst)
+        if src.shape != dst.shape:
+            raise ValueError("src and dst must have identical shapes")
+        if src.device != dst.device:
+            raise ValueError("src and dst must be on the same device")
+        if num_src is None:
+            num_src = int(src.max().item()) + 1 if src.numel() else 0
+        if num_dst is None:
+            num_dst = int(dst.max().item()) + 1 if dst.numel() else 0
+        if not isinstance(num_src, int) or num_src < 0:
+            raise ValueError("num_src must be a non-negative integer")
+        if not isinstance(num_dst, int) or num_dst < 0:
+            raise ValueError("num_dst must be a non-negative integer")
+        if src.numel():
+            if int(src.min().item()) < 0 or int(src.max().item()) >= num_src:
+                raise ValueError("src contains an out-of-range source index")
+            if int(dst.min().item()) < 0 or int(dst.max().item()) >= num_dst:
+                raise ValueError("dst contains an out-of-range destination index")
+        order = torch.argsort(dst, stable=True)
+        col_idx = src[order]
+        counts = torch.bincount(dst.to(torch.int64), minlength=num_dst)
+        row_ptr = torch.empty(num_dst + 1, device=dst.device, dtype=dst.dtype)
+        row_ptr[0] = 0
+        torch.cumsum(counts, dim=0, out=row_ptr[1:])
+        return cls.from_csr(row_ptr, col_idx, num_src=num_src, validate="basic")
+
+    @classmethod
+    def regular(cls, num_nodes: int, degree: int, *, device="cpu") -> "Graph":
+        if not isinstance(num_nodes, int) or num_nodes < 1:
+            raise ValueError("num_nodes must be a positive integer")
+        if not isinstance(degree, int) or degree < 0:
+            raise ValueError("degree must be a non-negative integer")
+        row_ptr = torch.arange(num_nodes + 1, device=device, dtype=torch.int64) * degree
+        col_idx = torch.arange(num_nodes * degree, device=device, dtype=torch.int64) % num_nodes
+        return cls.from_csr(row_ptr, col_idx, num_src=num_nodes)
+
+    @classmethod
+    def cu_seqlens(cls, cu_seqlens: torch.Tensor, *, causal: bool = True) -> "Graph":
+        """Block-diagonal packed varlen relation; kept implicit until needed.
+
+        Row i of sequence k relates to sources [s_k, i] (causal) or
+        [s_k, s_{k+1}) — the reference materializes this CSR at construction;
+        here it is materialized only if an edge function needs the CSR.
+        """
+        cls._validate_index_tensor("cu_seqlens", cu_seqlens)
+        if not isinstance(causal, bool):
+            raise TypeError("causal must be bool")
+        if cu_seqlens.numel() == 0 or int(cu_seqlens[0].item()) != 0:
+            raise ValueError("cu_seqlens must start at zero")
+        if bool(torch.any(cu_seqlens[1:] < cu_seqlens[:-1]).item()):
+            raise ValueError("cu_seqlens must be monotonic")
+        total = int(cu_seqlens[-1].item())
+        schema = GraphSchema(num_src=total, num_dst=total, origin="cu_seqlens",
+                             realization="implicit_varlen", index_dtype=cu_seqlens.dtype)
+        return cls(schema, cu_seqlens=cu_seqlens, causal=causal, device=cu_seqlens.device)
+
+    @classmethod
+    def cat(cls, graphs) -> "Graph":
+        blocks = list(graphs)
+        if not blocks:
+            raise ValueError("graphs must be a non-empty sequence")
+        for block in blocks:
+            if not isinstance(block, Graph):
+                raise TypeError("graphs must contain only Graph instances")
+        device = blocks[0].device
+        if any(str(block.device) != str(device) for block in blocks):
+            raise ValueError("all blocks must share a device")
+        dtype = (torch.int64 if any(b.schema.index_dtype == torch.int64 for b in blocks)
+                 else torch.int32)
+        row_parts = [torch.zeros(1, device=device, dtype=dtype)]
+        col_parts = []
+        edge_offset = 0
+        src_offset = 0
+        for block in blocks:
+            block_rows, block_cols = block.resolve_csr()
+            block_rows = block_rows.to(dtype)
+            col_parts.append(block_cols.to(dtype) + src_offset)
+            row_parts.append(block_rows[1:] + edge_offset)
+            edge_offset += int(block_rows[-1].item())
+            src_offset += block.schema.num_src
+        row_ptr = torch.cat(row_parts)
+        col_idx = (torch.cat(col_parts) if any(p.numel() for p in col_parts)
+                   else torch.empty(0, device=device, dtype=dtype))
+        return cls.from_csr(row_ptr, col_idx, num_src=src_offset)
+
+    # ---- queries ---------------------------------------------------------
+    @property
+    def schema(self) -> GraphSchema:
+        return self._schema
+
+    @property
+    def device(self) -> torch.device:
+        if self._col_idx is not None:
+            return self._col_idx.device
+        if self._cu_seqlens is not None:
+            return self._cu_seqlens.device
+        return self._device or torch.device("cpu")
+
+    @property
+    def is_varlen(self) -> bool:
+        return self._schema.realization == "implicit_varlen"
+
+    @property
+    def num_edges(self) -> int:
+        if self.is_varlen and self._row_ptr is None:
+            lengths = (self._cu_seqlens[1:] - self._cu_seqlens[:-1]).to(torch.int64)
+            if self._causal:
+                return int((lengths * (lengths + 1) // 2).sum().item())
+            return int((lengths * lengths).sum().item())
+        return self._col_idx.numel()
+
+    def resolve_csr(self) -> tuple[torch.Tensor, torch.Tensor]:
+        if self._row_ptr is None and self.is_varlen:
+            self._row_ptr, self._col_idx = _varlen_csr(self._cu_seqlens, self._causal)
+        return self._row_ptr, self._col_idx
+
+    def transpose(self) -> "Graph":
+        row_ptr, col_idx = self.resolve_csr()
+        destination = self.destination_index(row_ptr)
+        return type(self).from_coo(destination.to(col_idx.dtype), col_idx,
+                                   num_src=self._schema.num_dst, num_dst=self._schema.num_src)
+
+    def destination_index(self, row_ptr: torch.Tensor | None = None) -> torch.Tensor:
+        if row_ptr is None and self._destination_index_cache is not None:
+            return self._destination_index_cache
+        if row_ptr is None:
+            row_ptr, _ = self.resolve_csr()
+        degree = row_ptr[1:] - row_ptr[:-1]
+        dst = torch.repeat_interleave(
+            torch.arange(self._schema.num_dst, device=row_ptr.device), degree)
+        if self._row_ptr is row_ptr:
+            self._destination_index_cache = dst
+        return dst
+
+    def degree_bounds(self) -> tuple[int, int]:
+        if self._degree_bounds_cache is not None:
+            return self._degree_bounds_cache
+        row_ptr, _ = self.resolve_csr()
+        if self._schema.num_dst == 0:
+            bounds = (0, 0)
+        else:
+            degrees = row_ptr[1:] - row_ptr[:-1]
+            extrema = torch.stack((degrees.min(), degrees.max())).cpu()
+            bounds = int(extrema[0]), int(extrema[1])
+        self._degree_bounds_cache = bounds
+        return bounds
+
+    def degree_histogram(self) -> torch.Tensor:
+        row_ptr, _ = self.resolve_csr()
+        degrees = (row_ptr[1:] - row_ptr[:-1]).to(torch.int64)
+        return torch.bincount(degrees).cpu()
+
+    def planning_key(self) -> tuple[object, ...]:
+        return (self._schema.realization, self._schema.num_src, self._schema.num_dst,
+                str(self._schema.index_dtype), str(self.device))
+
+    def explain(self) -> str:
+        lines = [f"relation: {self._schema.realization}",
+                 f"num_src: {self._schema.num_src}", f"num_dst: {self._schema.num_dst}"]
+        plan = self._native_cache.get(("plan", WAVE_MAX, CHUNK_EDGES))
+        if plan is not None:
+            lines.append(f"row plan: {plan.counts()}")
+        return "\n".join(lines)
+
+    # ---- native device structures (built once per graph) -----------------
+    def _row_plan(self, wave_max: int = WAVE_MAX, chunk_edges: int = CHUNK_EDGES) -> RowPlanHandle:
+        key = ("plan", wave_max, chunk_edges)
+        handle = self._native_cache.get(key)
+        if handle is None:
+            row_ptr, _ = self.resolve_csr()
+            handle = build_row_plan(row_ptr, self._schema.num_dst, wave_max=wave_max,
+                                    chunk_edges=chunk_edges)
+            self._native_cache[key] = handle
+        return handle
+
+    def _transposed(self, wave_max: int = WAVE_MAX, chunk_edges: int = CHUNK_EDGES) -> Transposed:
+        key = ("transpose", wave_max, chunk_edges)
+        t = self._native_cache.get(key)
+        if t is None:
+            row_ptr, col_idx = self.resolve_csr()
+            row_ptr_t, col_t, perm = build_transpose(
+                row_ptr, col_idx, self._schema.num_dst, self._schema.num_src)
+            plan = build_row_plan(row_ptr_t, self._schema.num_src, wave_max=wave_max,
+                                  chunk_edges=chunk_edges)
+            t = Transposed(row_ptr_t, col_t, perm, plan)
+            self._native_cache[key] = t
+        return t
+
+
+def _varlen_csr(cu_seqlens: torch.Tensor, causal: bool):
+    """Materialize the block-diagonal varlen CSR (reference graph.py:260-294)."""
+    device, dtype = cu_seqlens.device, cu_seqlens.dtype
+    lengths = cu_seqlens.diff()
+    total = int(cu_seqlens[-1].item())
+    positions = torch.arange(total, device=device, dtype=dtype)
+    sequence = torch.repeat_interleave(
+        torch.arange(lengths.numel(), device=device, dtype=dtype), lengths.to(torch.int64))
+    start = cu_seqlens[:-1][sequence]
+    degree = positions - start + 1 if causal else lengths[sequence]
+    row_ptr = torch.cat([cu_seqlens.new_zeros(1), degree.cumsum(0, dtype=dtype)])
+    repeats = degree.to(torch.int64)
+    offset = torch.arange(int(row_ptr[-1].item()), device=device, dtype=dtype)
+    col_idx = start.repeat_interleave(repeats) + (
+        offset - row_ptr[:-1].repeat_interleave(repeats))
+    return row_ptr, col_idx
+
+
+__all__ = ["Graph", "GraphSchema", "build_row_plan", "build_transpose"]

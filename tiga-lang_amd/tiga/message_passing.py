@@ -1,0 +1,189 @@
+"""``tiga.MessagePassing``: the Torch-facing facade of the HIP provider.
+
+Call form and validation follow the reference adapter
+(python/tiga/interop/torch/message_passing.py:1490-1651, 3565-3586):
+``K()(graph=G, src={...}, dst={...}, edge={...}, **params) -> torch.Tensor``,
+``edge(self, src, dst, edge, **params)`` and ``node(self, dst, aggregate,
+**params)``.
+
+Dispatch: the edge function is captured once per parameter structure and
+matched against the patterns that have gfx950 kernels (``capture.py``).  A
+recognized pattern on ROCm tensors of a supported dtype/shape runs through
+``torch.autograd.Function`` bridges over libtgx_hip.so and nothing else: if
+the library is missing it raises.  Edge functions no kernel covers (and CPU
+tensors) run on the eager Torch evaluator, which restates the reference's own
+fallback (``_evaluate_reference`` 2848-2894); ``explain()`` reports which path
+ran.  Setting ``tiga.config.strict = True`` turns that fallback into an error.
+"""
+
+from __future__ import annotations
+
+import inspect
+from collections.abc import Mapping
+from types import SimpleNamespace
+from typing import Any
+
+import torch
+
+from . import _eager, _native
+from . import capture as cap
+from .graph import Graph
+from .kernel import CompiledVariant, Kernel
+from .reducer import OnlineSoftmaxReducer, SumReducer
+
+
+class _Config:
+    strict = False
+
+
+config = _Config()
+
+
+def _call_region(method, positional: tuple, params: Mapping[str, Any]):
+    signature = inspect.signature(method)
+    accepts_rest = any(p.kind is inspect.Parameter.VAR_KEYWORD
+                       for p in signature.parameters.values())
+    selected = params if accepts_rest else {
+        name: value for name, value in params.items() if name in signature.parameters}
+    return method(*positional, **selected)
+
+
+class MessagePassing(Kernel):
+    reducer = SumReducer()
+
+    def __init__(self) -> None:
+        super().__init__()
+
+    def edge(self, src, dst, edge, **params):
+        raise NotImplementedError
+
+    def node(self, dst, aggregate, **params):
+        return aggregate
+
+    # ------------------------------------------------------------------
+    @staticmethod
+    def _validate_fields(role: str, fields, entity_count: int, device) -> None:
+        if not isinstance(fields, Mapping):
+            raise TypeError(f"{role} fields must be a mapping")
+        for name, value in fields.items():
+            if not isinstance(value, torch.Tensor):
+                raise TypeError(f"{role}.{name} must be a torch.Tensor")
+            if value.ndim == 0 or value.shape[0] != entity_count:
+                raise ValueError(
+                    f"{role}.{name} leading dimension must be {entity_count}, "
+                    f"got shape {tuple(value.shape)}")
+            if value.device != device:
+                raise ValueError(f"{role}.{name} is on {value.device}, but graph is on {device}")
+
+    def _captured(self, params):
+        # Captured afresh on every call: the tree holds the module's current
+        # tensors (e.g. attention vectors), which a cache could leave stale.
+        return cap.capture(lambda s, d, e, p: _call_region(self.edge, (s, d, e), p), params)
+
+    def __call__(self, *, graph: Graph, src: Mapping[str, torch.Tensor],
+                 dst: Mapping[str, torch.Tensor], edge: Mapping[str, torch.Tensor] | None = None,
+                 **params: Any):
+        if not getattr(graph, "_tiga_graph", False):
+            raise TypeError("graph must be a tiga.Graph")
+        edge = {} if edge is None else edge
+        device = graph.device
+        self._validate_fields("src", src, graph.schema.num_src, device)
+        self._validate_fields("dst", dst, graph.schema.num_dst, device)
+        if isinstance(self.reducer, OnlineSoftmaxReducer) and \
+                self.reducer.block_prune_threshold is not None:
+            raise NotImplementedError(
+                "block_prune_threshold is defined for dense streaming relations only; "
+                "refusing to run exact softmax on a CSR relation")
+        captured = self._captured(params)
+        result = None
+        if device.type == "cuda" and captured is not None:
+            result = self._execute_native(captured, graph, src, dst, edge, params)
+        if result is None:
+            if config.strict:
+                raise RuntimeError(
+                    f"{type(self).__qualname__}: no HIP kernel covers this edge function / "
+                    "dtype / shape and tiga.config.strict is set")
+            if not graph.is_varlen:
+                self._validate_fields("edge", edge, graph.num_edges, device)
+            self._record_variant(CompiledVariant(
+                key=(type(self).__qualname__, "eager", graph.planning_key()),
+                backend="torch-eager", provider="torch", pattern="generic",
+                lowering="gather -> edge() -> scatter reduce (Torch ops)",
+                remarks=("edge function not covered by a HIP kernel",)))
+            aggregate = _eager.evaluate(self, graph, src, dst, edge, params)
+        else:
+            aggregate = result
+        if type(self).node is MessagePassing.node:
+            return aggregate
+        return _call_region(self.node, (SimpleNamespace(**dst), aggregate), params)
+
+    # ------------------------------------------------------------------
+    def _record_native(self, graph, pattern: str, entry_points, lowering, remarks=()):
+        plan = graph._native_cache.get(("plan", 512, 512))
+        extra = () if plan is None else (f"row plan: {plan.counts()}",)
+        self._record_variant(CompiledVariant(
+            key=(type(self).__qualname__, pattern, graph.planning_key()),
+            backend="hip", provider="libtgx_hip.so (gfx950)", pattern=pattern,
+            lowering=lowering, entry_points=tuple(entry_points),
+            remarks=tuple(remarks) + extra))
+
+    def _execute_native(self, captured, graph, src, dst, edge, params):
+        from . import _ops
+
+        if isinstance(self.reducer, SumReducer):
+            if self.reducer.identity_value != 0 or graph.is_varlen:
+                return None
+            pat = cap.recognize_weighted_sum(captured)
+            if pat is None or pat.src_field not in src:
+                return None
+            x = src[pat.src_field]
+            w = None
+            if pat.edge_field is not None:
+                if pat.edge_field not in edge:
+                    return None
+                w = edge[pat.edge_field]
+                E = graph.num_edges
+                if tuple(w.shape) not in ((E,), (E, 1)) or w.dtype != torch.float32:
+                    return None
+                if x.ndim == 1 and w.ndim == 2:
+                    return None
+            if x.dtype != torch.float32:
+                return None
+            _native.lib()
+            out = _ops.CsrSumFunction.apply(x, w, graph)
+            self._record_native(graph, "weighted-sum", ("tgx_csr_sum_fwd", "tgx_csr_sum_bwd"),
+                                "degree-binned rows -> wave gather-FMA (fp32)")
+            return out
+
+        if not isinstance(self.reducer, OnlineSoftmaxReducer):
+            return None
+        gat = cap.recognize_gat(captured)
+        if gat is not None and not graph.is_varlen:
+            h = src.get(gat.h_field)
+            hd = dst.get(gat.dst_field)
+            if h is None or hd is None or hd is not h:
+                return None
+            if graph.schema.num_src != graph.schema.num_dst or h.ndim != 3:
+                return None
+            N, H, D = h.shape
+            if h.dtype != torch.float32 or tuple(gat.a_src.shape) not in ((H, D), (1, H, D)) \
+                    or tuple(gat.a_dst.shape) not in ((H, D), (1, H, D)):
+                return None
+            if gat.a_src.dtype != torch.float32 or gat.a_dst.dtype != torch.float32:
+                return None
+            if gat.a_src.device != h.device or gat.a_dst.device != h.device:
+                return None
+            if H * D not in (64, 128, 256) or D % 4:
+                return None
+            if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
+                return None
+            _native.lib()
+            out = _ops.GatFunction.apply(h, gat.a_src, gat.a_dst, gat.slope, graph)
+            self._record_native(graph, "gat-additive", ("tgx_gat_fwd", "tgx_gat_bwd"),
+                                "online softmax per (row, head), logsumexp saved; "
+                                "backward recomputes alpha over the transposed CSR")
+            return out
+        return None
+
+
+__all__ = ["MessagePassing", "config"]
