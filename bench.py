@@ -38,7 +38,24 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=None)
     ap.add_argument("--seed", type=int, default=20260821)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a 1 GiB device copy (PMC byte-counter calibration)")
     return ap.parse_args()
+
+
+def calibrate_copy():
+    """A plain copy of known size: reads and writes exactly 1 GiB.  Run under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, it gives the factor between the
+    counters and real bytes."""
+    import torch
+
+    n = (1 << 30) // 4
+    x = torch.randn(n, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n}))
 
 
 # ---------------------------------------------------------------------------
@@ -274,6 +291,9 @@ def run_c1(args):
 
 def main():
     args = parse()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(collectives and sharding are out of scope); run with --gpus 1.",

@@ -404,22 +404,46 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_merge_kernel(
   st4(p, ld4(p) + s * ld4(a_dst + 4 * c));
 }
 
-// da[x] = sum over waves of dapart[w][x], fixed order, fp64.
-__global__ __launch_bounds__(256) void da_reduce_kernel(const double* __restrict__ part_src,
-                                                        const double* __restrict__ part_dst,
-                                                        int64_t src_waves, int64_t dst_waves,
-                                                        int HD,
-                                                        float* __restrict__ da_src,
-                                                        float* __restrict__ da_dst) {
+// da[x] = sum over waves of dapart[w][x] in a fixed order, fp64, two levels:
+// block (tensor, slice) sums a contiguous range of wave rows with coalesced
+// 2 KB row reads, then one wave per element adds the kDaSlices slice sums.
+constexpr int kDaSlices = 64;
+
+__global__ __launch_bounds__(256) void da_slice_kernel(const double* __restrict__ part_src,
+                                                       const double* __restrict__ part_dst,
+                                                       int64_t src_waves, int64_t dst_waves,
+                                                       int HD, double* __restrict__ slices) {
+  const int tensor = blockIdx.y;
+  const int slice = blockIdx.x;
+  const int e = threadIdx.x;
+  if (e >= HD) return;
+  const double* p = tensor ? part_dst : part_src;
+  const int64_t waves = tensor ? dst_waves : src_waves;
+  const int64_t per = (waves + kDaSlices - 1) / kDaSlices;
+  const int64_t w0 = slice * per;
+  const int64_t w1 = w0 + per < waves ? w0 + per : waves;
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  int64_t w = w0;
+  for (; w + 4 <= w1; w += 4) {
+    s0 += p[(w + 0) * HD + e];
+    s1 += p[(w + 1) * HD + e];
+    s2 += p[(w + 2) * HD + e];
+    s3 += p[(w + 3) * HD + e];
+  }
+  for (; w < w1; ++w) s0 += p[w * HD + e];
+  slices[(static_cast<int64_t>(tensor) * kDaSlices + slice) * HD + e] = (s0 + s1) + (s2 + s3);
+}
+
+__global__ __launch_bounds__(256) void da_final_kernel(const double* __restrict__ slices, int HD,
+                                                       float* __restrict__ da_src,
+                                                       float* __restrict__ da_dst) {
   const int x = blockIdx.x * 256 + threadIdx.x;
   if (x >= 2 * HD) return;
-  const bool dst = x >= HD;
-  const int e = dst ? x - HD : x;
-  const double* p = dst ? part_dst : part_src;
-  const int64_t waves = dst ? dst_waves : src_waves;
+  const int tensor = x >= HD;
+  const int e = tensor ? x - HD : x;
   double s = 0.0;
-  for (int64_t w = 0; w < waves; ++w) s += p[w * HD + e];
-  (dst ? da_dst : da_src)[e] = static_cast<float>(s);
+  for (int k = 0; k < kDaSlices; ++k) s += slices[(static_cast<int64_t>(tensor) * kDaSlices + k) * HD + e];
+  (tensor ? da_dst : da_src)[e] = static_cast<float>(s);
 }
 
 // ---------------------------------------------------------------------------
@@ -469,7 +493,7 @@ int gat_fwd_launch(const GatFwdArgs<I>& a, hipStream_t s) {
 }
 
 struct GatBwdLayout {
-  size_t dz_off, src_part_off, dst_part_off, dap_src_off, dap_dst_off, bytes;
+  size_t dz_off, src_part_off, dst_part_off, dap_src_off, dap_dst_off, slices_off, bytes;
   int64_t src_waves, dst_waves;
 };
 
@@ -486,6 +510,7 @@ GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t
   L.dst_part_off = reinterpret_cast<size_t>(c.take<float>(plan.n_chunks * H));
   L.dap_src_off = reinterpret_cast<size_t>(c.take<double>(L.src_waves * HD));
   L.dap_dst_off = reinterpret_cast<size_t>(c.take<double>(L.dst_waves * HD));
+  L.slices_off = reinterpret_cast<size_t>(c.take<double>(2 * kDaSlices * HD));
   L.bytes = align_up(c.used);
   return L;
 }
@@ -543,9 +568,12 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
   if (da_src || da_dst) {
     // Both outputs are required by the kernel; callers pass both.
     TGX_PROFILE("da_reduce_kernel", s);
-    da_reduce_kernel<<<ceil_div(2 * HD, 256), 256, 0, s>>>(dap_src, dap_dst, L.src_waves,
-                                                          L.dst_waves, HD, da_src, da_dst);
-    TGX_LAUNCHED("da_reduce_kernel");
+    double* slices = reinterpret_cast<double*>(ws + L.slices_off);
+    da_slice_kernel<<<dim3(kDaSlices, 2), 256, 0, s>>>(dap_src, dap_dst, L.src_waves,
+                                                        L.dst_waves, HD, slices);
+    TGX_LAUNCHED("da_slice_kernel");
+    da_final_kernel<<<ceil_div(2 * HD, 256), 256, 0, s>>>(slices, HD, da_src, da_dst);
+    TGX_LAUNCHED("da_final_kernel");
   }
   return TGX_OK;
 }
@@ -568,7 +596,7 @@ extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
   int st = check_plan(plan, n_nodes);
   if (st != TGX_OK) return st;
   if (n_nodes == 0) return TGX_OK;
-  TGX_REQUIRE(row_ptr && col && h && a_src && a_dst && out && ns, "null pointer");
+  TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns, "null pointer");
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
   hipStream_t s = as_stream(stream);
 #define TGX_GAT_FWD(GG, HH)                                                              \

@@ -242,7 +242,8 @@ extern "C" int tgx_csr_sum_fwd(const void* row_ptr, const void* col, int idx_bit
   int st = check_plan(plan, n_dst);
   if (st != TGX_OK) return st;
   if (n_dst == 0) return TGX_OK;
-  TGX_REQUIRE(row_ptr && col && out && (x || n_src == 0), "null pointer");
+  TGX_REQUIRE(row_ptr && out && (x || n_src == 0), "null pointer");
+  // col may be null for a graph without edges (no task reads it then).
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("csr_sum_fwd", s);
@@ -265,7 +266,8 @@ extern "C" int tgx_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_t,
   int st = check_plan(plan_t, n_src);
   if (st != TGX_OK) return st;
   if (n_src == 0) return TGX_OK;
-  TGX_REQUIRE(row_ptr_t && col_t && perm && dout, "null pointer");
+  TGX_REQUIRE(row_ptr_t && dout, "null pointer");
+  // col_t / perm may be null for a graph without edges.
   TGX_REQUIRE(!dw || x, "dw needs x");
   TGX_REQUIRE(plan_t->n_chunks == 0 || partial || !dx, "split rows need a partial buffer");
   hipStream_t s = as_stream(stream);
