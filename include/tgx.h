@@ -69,12 +69,14 @@ int tgx_csr_transpose_workspace(int64_t n_dst, int64_t n_src, int64_t n_edges,
  *   col_t_dev     [n_edges]  int32: destination id of each transposed edge
  *   perm_dev      [n_edges]  int32: original edge id of each transposed edge
  *                                   (= argsort(col_idx, stable=True))
+ *   inv_perm_dev  [n_edges]  int32: transposed position of each original edge
+ *                                   (inv_perm[perm[k]] = k); may be NULL
  * Deterministic: output is bit-identical across runs. */
 int tgx_csr_transpose(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                       int64_t n_dst, int64_t n_src, int64_t n_edges,
                       int32_t* row_ptr_t_dev, int32_t* col_t_dev,
-                      int32_t* perm_dev, void* workspace_dev,
-                      size_t workspace_bytes, void* stream);
+                      int32_t* perm_dev, int32_t* inv_perm_dev,
+                      void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Row partition / load balancing                                            */
@@ -211,11 +213,12 @@ int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
 /* Fused backward from the saved logsumexp (no per-edge alpha is stored by
  * the forward and no float atomics are used):
  *   dh, da_src, da_dst for loss gradient dout [N, H, D].
- * Uses the transposed CSR (row_ptr_t, col_t, perm) and its plan. */
+ * Uses the transposed CSR (row_ptr_t, col_t, perm, inv_perm) and its plan.
+ * node_state slot 1 (delta) is overwritten. */
 int tgx_gat_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                 const tgx_row_plan* plan, const int32_t* row_ptr_t_dev,
                 const int32_t* col_t_dev, const int32_t* perm_dev,
-                const tgx_row_plan* plan_t, const float* h_dev,
+                const int32_t* inv_perm_dev, const tgx_row_plan* plan_t, const float* h_dev,
                 const float* a_src_dev, const float* a_dst_dev,
                 float negative_slope, const float* out_dev,
                 float* node_state_dev, const float* dout_dev, float* dh_dev,

@@ -59,14 +59,17 @@ def test_transpose_bit_exact(idx, case):
     print(f"transpose {case} {idx}", flush=True)
     rp, col = skewed_csr(**case)
     n_dst, n_src = case["n_dst"], case["n_src"]
-    rpt, colt, perm = build_transpose(to_dev(rp, idx), to_dev(col, idx), n_dst, n_src)
+    rpt, colt, perm, inv = build_transpose(to_dev(rp, idx), to_dev(col, idx), n_dst, n_src)
     e_rpt, e_colt, e_perm = ref.transpose(rp, col, n_src)
     assert rpt.cpu().numpy().tolist() == e_rpt.tolist()
     assert colt.cpu().numpy().tolist() == e_colt.tolist()
     assert perm.cpu().numpy().tolist() == e_perm.tolist()
+    e_inv = np.empty_like(e_perm)
+    e_inv[e_perm] = np.arange(e_perm.size)
+    assert inv.cpu().numpy().tolist() == e_inv.tolist()
     # determinism: a second run is bit-identical
-    rpt2, colt2, perm2 = build_transpose(to_dev(rp, idx), to_dev(col, idx), n_dst, n_src)
-    assert torch.equal(colt, colt2) and torch.equal(perm, perm2)
+    rpt2, colt2, perm2, inv2 = build_transpose(to_dev(rp, idx), to_dev(col, idx), n_dst, n_src)
+    assert torch.equal(colt, colt2) and torch.equal(perm, perm2) and torch.equal(inv, inv2)
 
 
 @pytest.mark.parametrize("idx", [torch.int32, torch.int64])

@@ -56,8 +56,9 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
         objects.append(obj)
         cmd = [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
         if src.suffix == ".cpp":
-            cmd = [hipcc, "-O2", "-fPIC", "-std=c++17", f"-I{INCLUDE}", f"-I{CSRC}",
-                   "-c", str(src), "-o", str(obj)]
+            cmd = [hipcc, f"--offload-arch={ARCH}", "-O2", "-fPIC", "-std=c++17",
+                   "-Wno-unused-result", f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o",
+                   str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))

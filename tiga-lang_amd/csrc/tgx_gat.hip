@@ -43,6 +43,10 @@ __device__ __forceinline__ f32x4 ld4(const float* p) {
   return *reinterpret_cast<const f32x4*>(p);
 }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+typedef float f32x3 __attribute__((ext_vector_type(3)));
+__device__ __forceinline__ f32x3 ld3(const float* p) {
+  return *reinterpret_cast<const f32x3*>(p);
+}
 __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
   return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
 }
@@ -212,116 +216,111 @@ struct GatSrcArgs {
   const float* ns;
   const float* dout;
   float* dh;
-  float* partial;   // per chunk: [4G] dh contribution
-  float* dz;        // [E, H] at original edge ids
-  double* dapart;   // [waves, 4G]
-  int64_t n_tasks;
+  float* partial;   // per chunk: [4G] dh contribution | [H] sum of dz
+  float* dz;        // [E, H] in transposed edge order (coalesced)
+  float* sdz_src;   // [N, H] sum of dz over each source's out-edges
 };
 
+// One wave per task of the transposed-CSR plan (source rows).
 template <int G, int HL, int U>
 __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
   constexpr int EPW = kWave / G;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
+  const Task t = decode_task(a.plan, a.row_ptr_t, global_wave());
+  if (t.kind == kTaskNone) return;
   const int lane = lane_id();
   const int g = lane / G;
   const int c = lane % G;
   const int hd = c / HL;
   const bool head_lead = (c % HL) == 0;
+  if (t.kind == kTaskEmpty) {
+    for (int k = 0; k < t.n_empty; ++k) {
+      const int64_t j = uniform(a.plan.rows[t.empty0 + k]);
+      if (g == 0) {
+        st4(a.dh + j * HD + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+        if (head_lead) a.sdz_src[j * H + hd] = 0.f;
+      }
+    }
+    return;
+  }
   const f32x4 as4 = ld4(a.a_src + 4 * c);
-  f64x4 dap = {0.0, 0.0, 0.0, 0.0};
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
-  for (int64_t w = global_wave(); w < a.n_tasks; w += stride) {
-    const Task t = decode_task(a.plan, a.row_ptr_t, w);
-    if (t.kind == kTaskEmpty) {
-      for (int k = 0; k < t.n_empty; ++k) {
-        const int64_t j = uniform(a.plan.rows[t.empty0 + k]);
-        if (g == 0) st4(a.dh + j * HD + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
-      }
-      continue;
-    }
-    if (t.kind == kTaskNone) continue;
-    const int64_t j = t.row;
-    const f32x4 hj = ld4(a.h + j * HD + 4 * c);
-    const float ssrc = a.ns[(j * H + hd) * 4 + 3];
-    f32x4 dha = {0.f, 0.f, 0.f, 0.f};
-    float sdz = 0.f;
-    for (int64_t base = t.e0; base < t.e1; base += kWave) {
-      const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
-      int my_i = 0, my_e = 0;
-      if (lane < n) {
-        my_i = a.col_t[base + lane];
-        my_e = a.perm[base + lane];
-      }
-      for (int k = 0; k < n; k += EPW * U) {
-        f32x4 d[U], nst[U];
+  const int64_t j = t.row;
+  const f32x4 hj = ld4(a.h + j * HD + 4 * c);
+  const float ssrc = a.ns[(j * H + hd) * 4 + 3];
+  f32x4 dha = {0.f, 0.f, 0.f, 0.f};
+  float sdz = 0.f;
+  for (int64_t base = t.e0; base < t.e1; base += kWave) {
+    const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
+    const int my_i = lane < n ? a.col_t[base + lane] : 0;
+    for (int k = 0; k < n; k += EPW * U) {
+      f32x4 d[U];
+      f32x3 nst[U];  // {lse, delta, a_dst.h[i]} of the destination
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int slot = k + u * EPW + g;
-          const int64_t i = fetch_lane<EPW>(my_i, slot < n ? slot : 0);
-          d[u] = ld4(a.dout + i * HD + 4 * c);
-          nst[u] = ld4(a.ns + (i * H + hd) * 4);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int slot = k + u * EPW + g;
-          const bool valid = slot < n;
-          const float z = ssrc + nst[u][2];
-          const float s = leaky_relu(z, a.slope);
-          const float alpha = valid ? fast_exp(s - nst[u][0]) : 0.f;
-          const float dalpha = group_sum<HL>(dot4(d[u], hj));
-          const float ds = alpha * (dalpha - nst[u][1]);
-          const float dzv = z > 0.f ? ds : ds * a.slope;
-          dha += alpha * d[u];
-          sdz += dzv;
-          const int e = fetch_lane<EPW>(my_e, valid ? slot : 0);
-          if (valid && head_lead) a.dz[static_cast<int64_t>(e) * H + hd] = dzv;
-        }
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const int64_t i = fetch_lane<EPW>(my_i, slot < n ? slot : 0);
+        d[u] = ld4(a.dout + i * HD + 4 * c);
+        nst[u] = ld3(a.ns + (i * H + hd) * 4);
       }
-    }
 #pragma unroll
-    for (int mask = G; mask < kWave; mask <<= 1) {
-      dha[0] += __shfl_xor(dha[0], mask, 64);
-      dha[1] += __shfl_xor(dha[1], mask, 64);
-      dha[2] += __shfl_xor(dha[2], mask, 64);
-      dha[3] += __shfl_xor(dha[3], mask, 64);
-      sdz += __shfl_xor(sdz, mask, 64);
-    }
-    const f32x4 contrib = dha + sdz * as4;
-    if (g == 0) {
-      const double sd = static_cast<double>(sdz);
-      dap[0] += sd * hj[0];
-      dap[1] += sd * hj[1];
-      dap[2] += sd * hj[2];
-      dap[3] += sd * hj[3];
-      if (t.kind == kTaskChunk)
-        st4(a.partial + static_cast<int64_t>(t.slot) * HD + 4 * c, contrib);
-      else
-        st4(a.dh + j * HD + 4 * c, contrib);
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const bool valid = slot < n;
+        const float z = ssrc + nst[u][2];
+        const float s = leaky_relu(z, a.slope);
+        const float alpha = valid ? fast_exp(s - nst[u][0]) : 0.f;
+        const float dalpha = group_sum<HL>(dot4(d[u], hj));
+        const float ds = alpha * (dalpha - nst[u][1]);
+        const float dzv = z > 0.f ? ds : ds * a.slope;
+        dha += alpha * d[u];
+        sdz += dzv;
+        if (valid && head_lead) a.dz[(base + slot) * H + hd] = dzv;
+      }
     }
   }
-  if (g == 0) {
-    double* p = a.dapart + global_wave() * HD + 4 * c;
-    p[0] = dap[0];
-    p[1] = dap[1];
-    p[2] = dap[2];
-    p[3] = dap[3];
+#pragma unroll
+  for (int mask = G; mask < kWave; mask <<= 1) {
+    dha[0] += __shfl_xor(dha[0], mask, 64);
+    dha[1] += __shfl_xor(dha[1], mask, 64);
+    dha[2] += __shfl_xor(dha[2], mask, 64);
+    dha[3] += __shfl_xor(dha[3], mask, 64);
+    sdz += __shfl_xor(sdz, mask, 64);
+  }
+  if (g != 0) return;
+  const f32x4 contrib = dha + sdz * as4;
+  if (t.kind == kTaskChunk) {
+    float* p = a.partial + static_cast<int64_t>(t.slot) * (HD + H);
+    st4(p + 4 * c, contrib);
+    if (head_lead) p[HD + hd] = sdz;
+  } else {
+    st4(a.dh + j * HD + 4 * c, contrib);
+    if (head_lead) a.sdz_src[j * H + hd] = sdz;
   }
 }
 
-template <int G>
+template <int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
-    PlanView plan, const float* __restrict__ partial, float* __restrict__ dh) {
+    PlanView plan, const float* __restrict__ partial, float* __restrict__ dh,
+    float* __restrict__ sdz_src) {
   constexpr int HD = 4 * G;
+  constexpr int H = G / HL;
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
   const int c = lane_id();
   if (c >= G) return;
+  const int hd = c / HL;
   const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  for (int q = c0; q < c1; ++q) s += ld4(partial + static_cast<int64_t>(q) * HD + 4 * c);
+  float z = 0.f;
+  for (int q = c0; q < c1; ++q) {
+    const float* p = partial + static_cast<int64_t>(q) * (HD + H);
+    s += ld4(p + 4 * c);
+    z += p[HD + hd];
+  }
   st4(dh + row * HD + 4 * c, s);
+  if (c % HL == 0) sdz_src[row * H + hd] = z;
 }
 
 template <typename I>
@@ -330,13 +329,27 @@ struct GatDstArgs {
   PlanView plan;
   const float* h;
   const float* a_dst;
-  const float* dz;   // [E, H]
+  const float* dz;       // [E, H] in transposed edge order
+  const int32_t* inv_perm;  // [E] transposed position of each edge
+  const float* sdz_src;  // [N, H]
   float* dh;
-  float* partial;    // per chunk: [H]
-  double* dapart;    // [waves, 4G]
+  float* partial;        // per chunk: [H]
+  double* dap_src;       // [waves, 4G]
+  double* dap_dst;       // [waves, 4G]
   int64_t n_tasks;
 };
 
+__device__ __forceinline__ void acc_f64(f64x4& acc, float scale, f32x4 v) {
+  const double sd = static_cast<double>(scale);
+  acc[0] += sd * v[0];
+  acc[1] += sd * v[1];
+  acc[2] += sd * v[2];
+  acc[3] += sd * v[3];
+}
+
+// Persistent over the CSR plan (static task striding keeps the fp64
+// partials deterministic).  Every node's h row is read exactly once here:
+// da_dst += (sum over its in-edges of dz) h[i], da_src += sdz_src[i] h[i].
 template <typename I, int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a) {
   constexpr int HD = 4 * G;
@@ -346,30 +359,38 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a
   const int c = lane % G;
   const int hd = c / HL;
   const f32x4 ad4 = ld4(a.a_dst + 4 * c);
-  f64x4 dap = {0.0, 0.0, 0.0, 0.0};
+  f64x4 ds = {0.0, 0.0, 0.0, 0.0};
+  f64x4 dd = {0.0, 0.0, 0.0, 0.0};
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
   for (int64_t w = global_wave(); w < a.n_tasks; w += stride) {
     const Task t = decode_task(a.plan, a.row_ptr, w);
-    if (t.kind == kTaskEmpty || t.kind == kTaskNone) continue;
+    if (t.kind == kTaskNone) continue;
+    if (t.kind == kTaskEmpty) {
+      for (int k = 0; k < t.n_empty; ++k) {
+        const int64_t i = uniform(a.plan.rows[t.empty0 + k]);
+        if (g == 0) acc_f64(ds, a.sdz_src[i * H + hd], ld4(a.h + i * HD + 4 * c));
+      }
+      continue;
+    }
     const int64_t i = t.row;
-    // Sum dz over the row's edges: dz[e0*H .. e1*H) is contiguous and lane l
-    // always sees head l % H.
+    // Sum dz over the edge range, fetching each edge's H values from its
+    // transposed position; lane l always handles head l % H.
     float s = 0.f;
     const int64_t p0 = t.e0 * H, p1 = t.e1 * H;
-    for (int64_t p = p0 + lane; p < p1; p += kWave) s += a.dz[p];
+    for (int64_t p = p0 + lane; p < p1; p += kWave) {
+      const int64_t e = p / H;
+      s += a.dz[static_cast<int64_t>(a.inv_perm[e]) * H + (p - e * H)];
+    }
 #pragma unroll
     for (int mask = H; mask < kWave; mask <<= 1) s += __shfl_xor(s, mask, 64);
     const float sdz = __shfl(s, hd, 64);
-    if (t.kind == kTaskChunk) {
-      if (lane < H) a.partial[static_cast<int64_t>(t.slot) * H + lane] = s;
-    }
+    if (t.kind == kTaskChunk && lane < H)
+      a.partial[static_cast<int64_t>(t.slot) * H + lane] = s;
     if (g == 0) {
       const f32x4 hi = ld4(a.h + i * HD + 4 * c);
-      const double sd = static_cast<double>(sdz);
-      dap[0] += sd * hi[0];
-      dap[1] += sd * hi[1];
-      dap[2] += sd * hi[2];
-      dap[3] += sd * hi[3];
+      acc_f64(dd, sdz, hi);
+      const bool first = t.kind == kTaskRow || t.e0 == static_cast<int64_t>(a.row_ptr[i]);
+      if (first) acc_f64(ds, a.sdz_src[i * H + hd], hi);
       if (t.kind == kTaskRow) {
         float* q = a.dh + i * HD + 4 * c;
         st4(q, ld4(q) + sdz * ad4);
@@ -377,11 +398,10 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a
     }
   }
   if (g == 0) {
-    double* p = a.dapart + global_wave() * HD + 4 * c;
-    p[0] = dap[0];
-    p[1] = dap[1];
-    p[2] = dap[2];
-    p[3] = dap[3];
+    double* p = a.dap_src + global_wave() * HD + 4 * c;
+    double* q = a.dap_dst + global_wave() * HD + 4 * c;
+    p[0] = ds[0]; p[1] = ds[1]; p[2] = ds[2]; p[3] = ds[3];
+    q[0] = dd[0]; q[1] = dd[1]; q[2] = dd[2]; q[3] = dd[3];
   }
 }
 
@@ -462,8 +482,11 @@ bool gat_shape(int H, int D, GatShape* s) {
   return s->HL >= 1 && s->HL <= 16 && s->G % s->HL == 0;
 }
 
-int64_t persist_blocks(int64_t tasks) {
+// Persistent grid: enough workgroups for the tasks, at most what stays
+// resident at once, at most kPersistBlocks (the partial buffers' capacity).
+int64_t persist_blocks(int64_t tasks, int64_t resident) {
   int64_t b = ceil_div(tasks, kWavesPerBlock);
+  if (b > resident) b = resident;
   if (b > kPersistBlocks) b = kPersistBlocks;
   return b > 0 ? b : 1;
 }
@@ -493,7 +516,8 @@ int gat_fwd_launch(const GatFwdArgs<I>& a, hipStream_t s) {
 }
 
 struct GatBwdLayout {
-  size_t dz_off, src_part_off, dst_part_off, dap_src_off, dap_dst_off, slices_off, bytes;
+  size_t dz_off, sdz_off, src_part_off, dst_part_off, dap_src_off, dap_dst_off, slices_off,
+      bytes;
   int64_t src_waves, dst_waves;
 };
 
@@ -501,12 +525,14 @@ GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t
                             int64_t n_edges, int H, int D) {
   GatBwdLayout L;
   const int64_t HD = static_cast<int64_t>(H) * D;
-  const PlanView pv = plan_view(plan), pt = plan_view(plan_t);
-  L.src_waves = persist_blocks(plan_waves(pt)) * kWavesPerBlock;
-  L.dst_waves = persist_blocks(plan_waves(pv)) * kWavesPerBlock;
+  const PlanView pv = plan_view(plan);
+  // Partial buffers are sized for the largest grid; launches may use fewer.
+  L.dst_waves = persist_blocks(plan_waves(pv), kPersistBlocks) * kWavesPerBlock;
+  L.src_waves = L.dst_waves;
   Carve c{nullptr, 0};
   L.dz_off = reinterpret_cast<size_t>(c.take<float>(n_edges * H));
-  L.src_part_off = reinterpret_cast<size_t>(c.take<float>(plan_t.n_chunks * HD));
+  L.sdz_off = reinterpret_cast<size_t>(c.take<float>(plan.n_rows * H));
+  L.src_part_off = reinterpret_cast<size_t>(c.take<float>(plan_t.n_chunks * (HD + H)));
   L.dst_part_off = reinterpret_cast<size_t>(c.take<float>(plan.n_chunks * H));
   L.dap_src_off = reinterpret_cast<size_t>(c.take<double>(L.src_waves * HD));
   L.dap_dst_off = reinterpret_cast<size_t>(c.take<double>(L.dst_waves * HD));
@@ -517,7 +543,8 @@ GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t
 
 template <typename I, int G, int HL>
 int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* row_ptr_t,
-                   const int32_t* col_t, const int32_t* perm, const tgx_row_plan& plan_t,
+                   const int32_t* col_t, const int32_t* perm, const int32_t* inv_perm,
+                   const tgx_row_plan& plan_t,
                    const float* h, const float* a_src, const float* a_dst, float slope,
                    const float* out, float* ns, const float* dout, float* dh, float* da_src,
                    float* da_dst, int64_t n_nodes, int64_t n_edges, char* ws,
@@ -527,6 +554,7 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
   constexpr int HD = 4 * G;
   (void)n_edges;
   float* dz = reinterpret_cast<float*>(ws + L.dz_off);
+  float* sdz_src = reinterpret_cast<float*>(ws + L.sdz_off);
   float* src_part = reinterpret_cast<float*>(ws + L.src_part_off);
   float* dst_part = reinterpret_cast<float*>(ws + L.dst_part_off);
   double* dap_src = reinterpret_cast<double*>(ws + L.dap_src_off);
@@ -541,22 +569,26 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
   }
 
   GatSrcArgs sa{row_ptr_t, col_t, perm, pt, h, a_src, slope, ns, dout, dh, src_part, dz,
-                dap_src, plan_waves(pt)};
+                sdz_src};
+  GatDstArgs<I> da{row_ptr, pv, h, a_dst, dz, inv_perm, sdz_src, dh, dst_part, dap_src,
+                   dap_dst, plan_waves(pv)};
+  const int64_t dst_blocks =
+      persist_blocks(plan_waves(pv), resident_blocks(gat_bwd_dst_kernel<I, G, HL>, kTaskBlock));
   {
   TGX_PROFILE("gat_bwd_src_kernel", s);
-  gat_bwd_src_kernel<G, HL, U><<<L.src_waves / kWavesPerBlock, kTaskBlock, 0, s>>>(sa);
+  if (plan_waves(pt) > 0)
+    gat_bwd_src_kernel<G, HL, U><<<ceil_div(plan_waves(pt), kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
   TGX_LAUNCHED("gat_bwd_src_kernel");
   }
   if (pt.n_split > 0) {
     TGX_PROFILE("gat_bwd_src_merge_kernel", s);
-    gat_bwd_src_merge_kernel<G><<<ceil_div(pt.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        pt, src_part, dh);
+    gat_bwd_src_merge_kernel<G, HL><<<ceil_div(pt.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        pt, src_part, dh, sdz_src);
     TGX_LAUNCHED("gat_bwd_src_merge_kernel");
   }
-  GatDstArgs<I> da{row_ptr, pv, h, a_dst, dz, dh, dst_part, dap_dst, plan_waves(pv)};
   {
   TGX_PROFILE("gat_bwd_dst_kernel", s);
-  gat_bwd_dst_kernel<I, G, HL><<<L.dst_waves / kWavesPerBlock, kTaskBlock, 0, s>>>(da);
+  gat_bwd_dst_kernel<I, G, HL><<<dst_blocks, kTaskBlock, 0, s>>>(da);
   TGX_LAUNCHED("gat_bwd_dst_kernel");
   }
   if (pv.n_split > 0) {
@@ -569,8 +601,9 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
     // Both outputs are required by the kernel; callers pass both.
     TGX_PROFILE("da_reduce_kernel", s);
     double* slices = reinterpret_cast<double*>(ws + L.slices_off);
-    da_slice_kernel<<<dim3(kDaSlices, 2), 256, 0, s>>>(dap_src, dap_dst, L.src_waves,
-                                                        L.dst_waves, HD, slices);
+    da_slice_kernel<<<dim3(kDaSlices, 2), 256, 0, s>>>(dap_src, dap_dst,
+                                                        dst_blocks * kWavesPerBlock,
+                                                        dst_blocks * kWavesPerBlock, HD, slices);
     TGX_LAUNCHED("da_slice_kernel");
     da_final_kernel<<<ceil_div(2 * HD, 256), 256, 0, s>>>(slices, HD, da_src, da_dst);
     TGX_LAUNCHED("da_final_kernel");
@@ -633,7 +666,7 @@ extern "C" int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_pla
 
 extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
                            const tgx_row_plan* plan, const int32_t* row_ptr_t,
-                           const int32_t* col_t, const int32_t* perm,
+                           const int32_t* col_t, const int32_t* perm, const int32_t* inv_perm,
                            const tgx_row_plan* plan_t, const float* h, const float* a_src,
                            const float* a_dst, float slope, const float* out, float* ns,
                            const float* dout, float* dh, float* da_src, float* da_dst,
@@ -653,7 +686,7 @@ extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
   if (n_nodes == 0) return TGX_OK;
   TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns && dout && dh && da_src && da_dst,
               "null pointer");
-  TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && perm), "null transposed CSR");
+  TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && inv_perm), "null transposed CSR");
   const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, H, D);
   TGX_REQUIRE(ws && ws_bytes >= L.bytes, "workspace too small: need %zu bytes", L.bytes);
   hipStream_t s = as_stream(stream);
@@ -662,11 +695,13 @@ extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
   if (shp.G == GG && shp.HL == HH) {                                                       \
     if (idx_bits == 32)                                                                    \
       return gat_bwd_launch<int32_t, GG, HH>(static_cast<const int32_t*>(row_ptr), *plan,  \
-                                             row_ptr_t, col_t, perm, *plan_t, h, a_src,    \
+                                             row_ptr_t, col_t, perm, inv_perm, *plan_t, h, \
+                                             a_src,                                        \
                                              a_dst, slope, out, ns, dout, dh, da_src,      \
                                              da_dst, n_nodes, n_edges, w, L, s);           \
     return gat_bwd_launch<int64_t, GG, HH>(static_cast<const int64_t*>(row_ptr), *plan,    \
-                                           row_ptr_t, col_t, perm, *plan_t, h, a_src,      \
+                                           row_ptr_t, col_t, perm, inv_perm, *plan_t, h,   \
+                                           a_src,                                          \
                                            a_dst, slope, out, ns, dout, dh, da_src, da_dst, \
                                            n_nodes, n_edges, w, L, s);                     \
   }

@@ -245,9 +245,12 @@ __global__ __launch_bounds__(kBlock) void run_end_fill_kernel(
 
 __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
     const int32_t* __restrict__ perm, const int32_t* __restrict__ erow, int64_t n,
-    int32_t* __restrict__ col_t) {
+    int32_t* __restrict__ col_t, int32_t* __restrict__ inv_perm) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (i < n) col_t[i] = erow[perm[i]];
+  if (i >= n) return;
+  const int32_t e = perm[i];
+  col_t[i] = erow[e];
+  if (inv_perm) inv_perm[e] = static_cast<int32_t>(i);
 }
 
 // ---------------------------------------------------------------------------
@@ -394,7 +397,8 @@ extern "C" int tgx_csr_transpose_workspace(int64_t n_dst, int64_t n_src,
 template <typename I>
 static int transpose_impl(const I* row_ptr, const I* col, int64_t n_dst, int64_t n_src,
                           int64_t E, int32_t* row_ptr_t, int32_t* col_t,
-                          int32_t* perm, void* ws, size_t ws_bytes, hipStream_t s) {
+                          int32_t* perm, int32_t* inv_perm, void* ws, size_t ws_bytes,
+                          hipStream_t s) {
   TransposeLayout L = transpose_layout(n_dst, n_src, E);
   TGX_REQUIRE(ws_bytes >= L.bytes, "workspace too small: need %zu bytes", L.bytes);
   Carve c{static_cast<char*>(ws), ws_bytes};
@@ -442,7 +446,7 @@ static int transpose_impl(const I* row_ptr, const I* col, int64_t n_dst, int64_t
   destination_index_kernel<<<ceil_div(n_dst, kBlock / kWave), kBlock, 0, s>>>(
       row_ptr, n_dst, erow);
   TGX_LAUNCHED("destination_index_kernel");
-  gather_rows_kernel<<<ceil_div(E, kBlock), kBlock, 0, s>>>(perm, erow, E, col_t);
+  gather_rows_kernel<<<ceil_div(E, kBlock), kBlock, 0, s>>>(perm, erow, E, col_t, inv_perm);
   TGX_LAUNCHED("gather_rows_kernel");
   return TGX_OK;
 }
@@ -450,7 +454,8 @@ static int transpose_impl(const I* row_ptr, const I* col, int64_t n_dst, int64_t
 extern "C" int tgx_csr_transpose(const void* row_ptr, const void* col, int idx_bits,
                                  int64_t n_dst, int64_t n_src, int64_t n_edges,
                                  int32_t* row_ptr_t, int32_t* col_t, int32_t* perm,
-                                 void* ws, size_t ws_bytes, void* stream) {
+                                 int32_t* inv_perm, void* ws, size_t ws_bytes,
+                                 void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_dst >= 0 && n_src >= 0 && n_edges >= 0, "negative size");
   TGX_REQUIRE(n_edges <= INT32_MAX && n_dst <= INT32_MAX && n_src < INT32_MAX,
@@ -465,10 +470,10 @@ extern "C" int tgx_csr_transpose(const void* row_ptr, const void* col, int idx_b
   if (idx_bits == 32)
     return transpose_impl(static_cast<const int32_t*>(row_ptr),
                           static_cast<const int32_t*>(col), n_dst, n_src, n_edges,
-                          row_ptr_t, col_t, perm, ws, ws_bytes, s);
+                          row_ptr_t, col_t, perm, inv_perm, ws, ws_bytes, s);
   return transpose_impl(static_cast<const int64_t*>(row_ptr),
                         static_cast<const int64_t*>(col), n_dst, n_src, n_edges,
-                        row_ptr_t, col_t, perm, ws, ws_bytes, s);
+                        row_ptr_t, col_t, perm, inv_perm, ws, ws_bytes, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -69,6 +69,21 @@ size_t scan_scratch_ints(int64_t n);
 int scan_exclusive_i32(const int32_t* in, int32_t* out, int64_t n,
                        int32_t* total_dev, int32_t* scratch, hipStream_t stream);
 
+// Workgroups of `block` threads that a kernel can keep resident on the whole
+// device at once (occupancy x compute units); persistent grids use this so no
+// workgroup waits for a second round.
+template <typename Kernel>
+inline int64_t resident_blocks(Kernel kernel, int block) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess)
+    return 1;
+  const int64_t n = static_cast<int64_t>(cus) * (per_cu > 0 ? per_cu : 1);
+  return n > 0 ? n : 1;
+}
+
 // Validate a row plan against the number of rows it must cover.
 inline int check_plan(const tgx_row_plan* p, int64_t rows) {
   TGX_REQUIRE(p != nullptr, "null plan");

@@ -47,7 +47,7 @@ _SIGNATURES: dict[str, list] = {
     "tgx_destination_index": [c_vp, c_int, c_i64, c_i64, c_vp, c_int, c_vp],
     "tgx_csr_transpose_workspace": [c_i64, c_i64, c_i64, P(c_size)],
     "tgx_csr_transpose": [c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
-                          c_vp, c_size, c_vp],
+                          c_vp, c_vp, c_size, c_vp],
     "tgx_plan_degree_bins_workspace": [c_i64, c_int, P(c_size)],
     "tgx_plan_degree_bins": [c_vp, c_int, c_i64, P(c_i64), c_int, c_vp, P(c_i64), c_vp,
                              c_size, c_vp],
@@ -64,7 +64,7 @@ _SIGNATURES: dict[str, list] = {
     "tgx_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
                     c_i64, c_int, c_int, c_vp, c_vp],
     "tgx_gat_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, P(c_size)],
-    "tgx_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, P(RowPlan), c_vp,
+    "tgx_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, P(RowPlan), c_vp,
                     c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                     c_int, c_int, c_vp, c_size, c_vp],
     "tgx_profile_begin": [],

@@ -125,7 +125,8 @@ class GatFunction(torch.autograd.Function):
         # rewritten by every backward before it is read.
         _native.call("tgx_gat_bwd", row_ptr.data_ptr(), col_idx.data_ptr(),
                      _native.idx_bits(row_ptr), plan.ref, t.row_ptr_t.data_ptr(),
-                     t.col_t.data_ptr(), t.perm.data_ptr(), t.plan.ref, hc.data_ptr(),
+                     t.col_t.data_ptr(), t.perm.data_ptr(), t.inv_perm.data_ptr(),
+                     t.plan.ref, hc.data_ptr(),
                      asc.data_ptr(), adc.data_ptr(), ctx.slope, out.data_ptr(),
                      ns.data_ptr(), dout.data_ptr(), dh.data_ptr(), da_src.data_ptr(),
                      da_dst.data_ptr(), N, E, H, D, ws.data_ptr(), ws_bytes.value,

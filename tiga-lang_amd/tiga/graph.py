@@ -60,12 +60,14 @@ class RowPlanHandle:
 
 
 class Transposed:
-    """Source-row CSR of a graph: row_ptr_t [num_src+1], col_t [E], perm [E]."""
+    """Source-row CSR of a graph: row_ptr_t [num_src+1], col_t [E], perm [E]
+    (original edge of each transposed edge) and inv_perm [E] (its inverse)."""
 
-    def __init__(self, row_ptr_t, col_t, perm, plan):
+    def __init__(self, row_ptr_t, col_t, perm, inv_perm, plan):
         self.row_ptr_t = row_ptr_t
         self.col_t = col_t
         self.perm = perm
+        self.inv_perm = inv_perm
         self.plan = plan
 
 
@@ -98,20 +100,22 @@ def build_row_plan(row_ptr: torch.Tensor, n_rows: int, *, wave_max: int = WAVE_M
 
 
 def build_transpose(row_ptr: torch.Tensor, col_idx: torch.Tensor, num_dst: int,
-                    num_src: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                    num_src: int):
+    """Stable transpose on the device: (row_ptr_t, col_t, perm, inv_perm)."""
     device = row_ptr.device
     E = col_idx.numel()
     row_ptr_t = torch.empty(num_src + 1, dtype=torch.int32, device=device)
     col_t = torch.empty(max(E, 1), dtype=torch.int32, device=device)
     perm = torch.empty(max(E, 1), dtype=torch.int32, device=device)
+    inv_perm = torch.empty(max(E, 1), dtype=torch.int32, device=device)
     ws_bytes = ctypes.c_size_t()
     _native.call("tgx_csr_transpose_workspace", num_dst, num_src, E, ctypes.byref(ws_bytes))
     ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=device)
     _native.call("tgx_csr_transpose", row_ptr.data_ptr(), col_idx.data_ptr(),
                  _native.idx_bits(row_ptr), num_dst, num_src, E, row_ptr_t.data_ptr(),
-                 col_t.data_ptr(), perm.data_ptr(), ws.data_ptr(), ws_bytes.value,
-                 _native.stream_of(row_ptr))
-    return row_ptr_t, col_t[:E], perm[:E]
+                 col_t.data_ptr(), perm.data_ptr(), inv_perm.data_ptr(), ws.data_ptr(),
+                 ws_bytes.value, _native.stream_of(row_ptr))
+    return row_ptr_t, col_t[:E], perm[:E], inv_perm[:E]
 
 
 class Graph:
@@ -363,11 +367,11 @@ class Graph:
         t = self._native_cache.get(key)
         if t is None:
             row_ptr, col_idx = self.resolve_csr()
-            row_ptr_t, col_t, perm = build_transpose(
+            row_ptr_t, col_t, perm, inv_perm = build_transpose(
                 row_ptr, col_idx, self._schema.num_dst, self._schema.num_src)
             plan = build_row_plan(row_ptr_t, self._schema.num_src, wave_max=wave_max,
                                   chunk_edges=chunk_edges)
-            t = Transposed(row_ptr_t, col_t, perm, plan)
+            t = Transposed(row_ptr_t, col_t, perm, inv_perm, plan)
             self._native_cache[key] = t
         return t
 
