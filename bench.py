@@ -33,7 +33,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=None)
@@ -91,6 +91,31 @@ def fixed_degree_csr(n_dst, n_src, degree, seed, device):
     return row_ptr, col.reshape(-1)
 
 
+def rmat_csr(scale, edge_factor, probs, seed, device):
+    """R-MAT (Chakrabarti et al. 2004) on the GPU: edge_factor * 2**scale tuples,
+    one quadrant draw per level, duplicates removed, first coordinate = the
+    destination row; returns an int64 dst-row CSR with sorted columns."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    n = 1 << scale
+    m = edge_factor * n
+    a, b, c, _ = probs
+    row = torch.zeros(m, dtype=torch.int64, device=device)
+    col = torch.zeros(m, dtype=torch.int64, device=device)
+    for level in range(scale):
+        r = torch.rand(m, device=device, generator=g)
+        down = r >= a + b
+        right = ((r >= a) & (r < a + b)) | (r >= a + b + c)
+        row |= down.to(torch.int64) << level
+        col |= right.to(torch.int64) << level
+    keys = torch.unique(row * n + col)
+    row, col = keys // n, keys % n
+    row_ptr = torch.zeros(n + 1, dtype=torch.int64, device=device)
+    row_ptr[1:] = torch.cumsum(torch.bincount(row, minlength=n), 0)
+    return row_ptr, col
+
+
 # ---------------------------------------------------------------------------
 # Algorithmic bytes per launch (no-reuse model: every edge reads its index
 # (4 B) and its gathered rows once; every per-node array is read or written
@@ -104,6 +129,16 @@ def gat_kernel_bytes(N, E, H, D):
         "gat_delta_kernel": N * (2 * row + H * 4),
         "gat_bwd_src_kernel": E * (4 + 4 + row + ns + H * 4) + N * (4 + row + ns + row),
         "gat_bwd_dst_kernel": E * (H * 4) + N * (4 + row + 2 * row),
+    }
+
+
+def dot_kernel_bytes(N, E, H, D):
+    row = H * D * 2
+    return {
+        "dot_fwd_kernel": E * (4 + 2 * row + H * 4) + N * (4 + 2 * row + H * 8),
+        "dot_delta_kernel": N * (2 * row + H * 4),
+        "dot_bwd_dst_kernel": E * (4 + 2 * row + 2 * H * 4) + N * (4 + 3 * row + H * 8),
+        "dot_bwd_src_kernel": E * (4 + 4 + 2 * row + H * 4 + H * 8) + N * (4 + 4 * row),
     }
 
 
@@ -289,6 +324,91 @@ def run_c1(args):
     }
 
 
+def run_c3c4(args):
+    """C3: dot-product attention forward, bf16, on R-MAT scale 21; C4: its
+    fused backward (transposed CSR built once, untimed)."""
+    import torch
+
+    import tiga as tg
+    from tiga import _native
+
+    dev = torch.device("cuda")
+    scale_log2 = 21 if args.nodes is None else max(4, int(args.nodes).bit_length() - 1)
+    row_ptr, col = rmat_csr(scale_log2, 16, (0.57, 0.19, 0.19, 0.05), args.seed, dev)
+    N = row_ptr.numel() - 1
+    E = col.numel()
+    H, D = 4, 64
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    q = torch.randn(N, H, D, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+    k = torch.randn(N, H, D, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+    v = torch.randn(N, H, D, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+    bias = torch.randn(E, H, device=dev, generator=g).requires_grad_(True)
+    dout = torch.randn(N, H, D, device=dev, generator=g).to(torch.bfloat16)
+    graph = tg.Graph.from_csr(row_ptr, col, num_src=N)
+    tg.config.strict = True
+
+    class DotAttention(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge, scale):
+            return self.reducer((src.k * dst.q).sum(dim=-1) * scale + edge.bias, src.v)
+
+    kernel = DotAttention()
+
+    def fwd():
+        return kernel(graph=graph, src={"k": k, "v": v}, dst={"q": q}, edge={"bias": bias},
+                      scale=1.0 / 8.0)
+
+    out = fwd()
+    out.backward(dout, retain_graph=True)
+    graph._transposed()
+    deg = (row_ptr[1:] - row_ptr[:-1])
+    stats = {"max_in_degree": int(deg.max()), "empty_rows": int((deg == 0).sum())}
+    for _ in range(args.warmup):
+        if args.config == "c3":
+            with torch.no_grad():
+                fwd()
+        else:
+            out.backward(dout, retain_graph=True)
+    torch.cuda.synchronize()
+    with _native.KernelTimer() as timer:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            if args.config == "c3":
+                with torch.no_grad():
+                    fwd()
+            else:
+                q.grad = k.grad = v.grad = bias.grad = None
+                out.backward(dout, retain_graph=True)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    bytes_per = dot_kernel_bytes(N, E, H, D)
+    names = ["dot_fwd_kernel"] if args.config == "c3" else [
+        "dot_delta_kernel", "dot_bwd_dst_kernel", "dot_bwd_src_kernel"]
+    step_bytes = sum(bytes_per[n] for n in names)
+    dominant = max((n for n in names if n in timer.totals), key=lambda n: timer.totals[n][1])
+    n_launch, total_ms = timer.totals[dominant]
+    achieved = bytes_per[dominant] / (total_ms / n_launch * 1e-3) / 1e9
+    ms = elapsed * 1e3 / args.steps
+    what = "forward" if args.config == "c3" else "fused backward"
+    return {
+        "metric": f"dot-product edge attention {what} edges/s, R-MAT scale 21, bf16, 1xMI355X",
+        "value": E * args.steps / elapsed, "unit": "edges/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded R-MAT a=.57 b=.19 c=.19 d=.05, dedup; q,k,v,bias ~N(0,1))",
+        "config": {"workload": f"{args.config}-dot-attention-{'fwd' if args.config == 'c3' else 'bwd'}",
+                   "nodes": N, "edges": E, "heads": H, "head_dim": D, **stats},
+        "hbm_frac_step": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None, "algorithmic_bytes": bytes_per[dominant]},
+        "kernels": {kk: {"launches": n, "avg_ms": t / n,
+                         "gbs": (bytes_per[kk] / (t / n * 1e-3) / 1e9) if kk in bytes_per else None}
+                    for kk, (n, t) in sorted(timer.totals.items())},
+    }
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
@@ -299,7 +419,8 @@ def main():
               "(collectives and sharding are out of scope); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-    result = run_c2(args) if args.config == "c2" else run_c1(args)
+    runners = {"c1": run_c1, "c2": run_c2, "c3": run_c3c4, "c4": run_c3c4}
+    result = runners[args.config](args)
     print(json.dumps(result), flush=True)
 
 

@@ -227,6 +227,43 @@ int tgx_gat_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                 size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Dot-product edge attention (bf16 in, fp32 accumulate)                     */
+/*   s_e = scale * (k[j] . q[i]) + bias[e]   per head,                       */
+/*   out[i] = sum_e softmax_i(s)_e * v[j]                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Forward.  q [n_dst, H, D], k/v [n_src, H, D], out [n_dst, H, D]: bf16 (raw
+ * 16-bit storage); bias [E, H] fp32 or NULL.  ml [n_dst, H, 2] fp32 receives
+ * {logsumexp (-inf for an empty row), 0}.  partial_dev:
+ * tgx_partial_bytes(plan, H*D + 2*H) bytes (NULL without split rows).
+ * Supported: D % 8 == 0, H*D in {128, 256, 512}.
+ * Replaces the eager evaluation of (src.k*dst.q).sum(-1)*scale + edge.bias
+ * (interop/torch/message_passing.py:2848-2894, reducer_oracle.py:60-137). */
+int tgx_dot_attn_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                     const tgx_row_plan* plan, const void* q_dev, const void* k_dev,
+                     const void* v_dev, const float* bias_dev, float scale,
+                     void* out_dev, float* ml_dev, int64_t n_dst, int64_t n_src, int H,
+                     int D, float* partial_dev, void* stream);
+
+/* Workspace bytes for tgx_dot_attn_bwd with these plans. */
+int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
+                               int H, int D, size_t* bytes);
+
+/* Fused backward from the saved logsumexp, no float atomics: dq (bf16) and
+ * dbias (fp32 [E, H], may be NULL) on the destination-row CSR, dk/dv (bf16)
+ * on the transposed CSR (row_ptr_t, col_t, perm) and its plan.  ml slot 1
+ * (delta = <dout, out>) is overwritten. */
+int tgx_dot_attn_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                     const tgx_row_plan* plan, const int32_t* row_ptr_t_dev,
+                     const int32_t* col_t_dev, const int32_t* perm_dev,
+                     const tgx_row_plan* plan_t, const void* q_dev, const void* k_dev,
+                     const void* v_dev, const float* bias_dev, float scale,
+                     const void* out_dev, float* ml_dev, const void* dout_dev, void* dq_dev,
+                     void* dk_dev, void* dv_dev, float* dbias_dev, int64_t n_dst,
+                     int64_t n_src, int H, int D, void* workspace_dev,
+                     size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Per-kernel timing (no reference counterpart; used by the benchmark)       */
 /* ------------------------------------------------------------------------ */
 

@@ -232,3 +232,84 @@ def test_gat_large_scores_and_determinism():
         assert torch.equal(a, b)          # bit-identical reruns (no float atomics)
     e_out, _ = ref.gat_fwd(rp, col, h, a_s, a_d, 0.2)
     assert rel_err(grads[0][0].cpu(), e_out) <= RTOL32
+
+
+# ---- dot-product attention (bf16, fp32 accumulate) ---------------------------
+
+RTOL_BF16 = 2e-2
+
+
+class DotBias(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge, scale):
+        return self.reducer((src.k * dst.q).sum(dim=-1) * scale + edge.bias, src.v)
+
+
+class DotPlain(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge, scale):
+        return self.reducer((src.k * dst.q).sum(dim=-1) * scale, src.v)
+
+
+def _bf16(a):
+    return torch.as_tensor(a, device=DEV).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("H,D", [(4, 64), (2, 64), (8, 64), (16, 16)])
+@pytest.mark.parametrize("idx", [torch.int32, torch.int64])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_dot_fwd_bwd_parity_rmat(H, D, idx, with_bias):
+    from graphs import rmat_csr
+
+    print(f"dot H={H} D={D} {idx} bias={with_bias}", flush=True)
+    rp, col = rmat_csr(5, 12)                      # 4096 nodes, hubs > 512 edges
+    N = rp.size - 1
+    E = col.size
+    rng = np.random.default_rng(H + D)
+    q = _bf16(rng.standard_normal((N, H, D)))
+    k = _bf16(rng.standard_normal((N, H, D)))
+    v = _bf16(rng.standard_normal((N, H, D)))
+    bias = to_dev(rng.standard_normal((E, H)), torch.float32)
+    dout = _bf16(rng.standard_normal((N, H, D)))
+    scale = 1.0 / np.sqrt(D)
+    graph = tg.Graph.from_csr(to_dev(rp, idx), to_dev(col, idx), num_src=N)
+    qt, kt, vt, bt = (t.clone().requires_grad_(True) for t in (q, k, v, bias))
+    kernel = DotBias() if with_bias else DotPlain()
+    edge = {"bias": bt} if with_bias else {}
+    out = kernel(graph=graph, src={"k": kt, "v": vt}, dst={"q": qt}, edge=edge, scale=scale)
+    assert kernel.last_variant.backend == "hip"
+    assert out.dtype == torch.bfloat16
+    out.backward(dout)
+    f = lambda t: t.detach().float().cpu().numpy()
+    b64 = f(bias) if with_bias else None
+    e_out, _ = ref.dot_fwd(rp, col, f(q), f(k), f(v), scale, b64)
+    e_dq, e_dk, e_dv, e_db = ref.dot_bwd(rp, col, f(q), f(k), f(v), scale, b64, f(dout))
+    assert rel_err(f(out), e_out) <= RTOL_BF16
+    assert rel_err(f(qt.grad), e_dq) <= RTOL_BF16
+    assert rel_err(f(kt.grad), e_dk) <= RTOL_BF16
+    assert rel_err(f(vt.grad), e_dv) <= RTOL_BF16
+    if with_bias:
+        assert rel_err(f(bt.grad), e_db) <= RTOL_BF16
+    # empty destination rows produce exact zeros
+    empty = np.flatnonzero(np.diff(rp) == 0)
+    assert empty.size > 0
+    assert torch.count_nonzero(out[torch.as_tensor(empty, device=DEV)]).item() == 0
+
+
+def test_dot_hub_row_split_matches_unsplit():
+    # One destination with 20000 in-edges (40 chunks) and bipartite shapes.
+    rng = np.random.default_rng(3)
+    n_dst, n_src, H, D = 7, 30000, 4, 64
+    deg = np.array([20000, 0, 1, 511, 512, 513, 3000])
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+    col = np.concatenate([np.sort(rng.integers(0, n_src, d)) for d in deg]).astype(np.int64)
+    q = _bf16(rng.standard_normal((n_dst, H, D)))
+    k = _bf16(rng.standard_normal((n_src, H, D)) * 2)
+    v = _bf16(rng.standard_normal((n_src, H, D)))
+    graph = tg.Graph.from_csr(to_dev(rp, torch.int64), to_dev(col, torch.int64), num_src=n_src)
+    out = DotPlain()(graph=graph, src={"k": k, "v": v}, dst={"q": q}, scale=0.125)
+    f = lambda t: t.detach().float().cpu().numpy()
+    e_out, _ = ref.dot_fwd(rp, col, f(q), f(k), f(v), 0.125)
+    assert rel_err(f(out), e_out) <= RTOL_BF16

@@ -1,0 +1,682 @@
+// Dot-product edge attention over a destination-row CSR, bf16 in / fp32
+// accumulate:
+//
+//   s_e = scale * (k[j, hd] . q[i, hd]) + bias[e, hd]     (j = col[e], i = row)
+//   out[i, hd] = sum_e softmax_i(s)_e * v[j, hd]          (bf16 output)
+//
+// Reference semantics: edge() returning
+//   reducer((src.k * dst.q).sum(-1) * scale + edge.bias, src.v)
+// on the eager oracle (python/tiga/interop/torch/message_passing.py:2848-2894,
+// reducer_oracle.py:60-137, fp32 accumulation for bf16 inputs, result cast
+// back to bf16).
+//
+// Layout: q, k, v, dout are [N, H, D] bf16; one node row is 8*G values over G
+// lanes (16 bytes = 8 bf16 per lane), head hd on HL = D/8 lanes.  bias/dbias
+// are [E, H] fp32 in edge order.  ml [N, H, 2] fp32 = {logsumexp, delta}.
+//
+// Backward (no float atomics; alpha recomputed from the saved logsumexp):
+//   B1 node pass     delta[i] = <dout[i], out[i]> per head
+//   B2 destination pass over the CSR: ds_e = alpha_e (<dout[i], v[j]> - delta[i]),
+//                    dbias[e] = ds_e, dq[i] = scale * sum ds_e k[j]
+//   B3 source pass over the transposed CSR: dk[j] = scale * sum ds_e q[i],
+//                    dv[j] = sum alpha_e dout[i]
+//   Hub rows of either CSR are split into chunks whose fp32 partials are
+//   summed in chunk order.
+#include <hip/hip_runtime.h>
+
+#include "tgx_device.h"
+#include "tgx_host.h"
+#include "tgx_profile.h"
+#include "tgx_softmax.h"
+#include "tgx_tasks.h"
+
+namespace tgx {
+namespace {
+
+__device__ __forceinline__ u32x4 ldv(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void stv(uint16_t* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+__device__ __forceinline__ float dot8(const float (&a)[8], u32x4 b) {
+  float f[8];
+  unpack8(b, f);
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) s += a[q] * f[q];
+  return s;
+}
+__device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+  v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+}
+
+template <int EPW>
+__device__ __forceinline__ int fetch_lane(int v, int src) {
+  if constexpr (EPW == 1) return __builtin_amdgcn_readlane(v, src);
+  return __shfl(v, src, 64);
+}
+
+template <int G>
+__device__ __forceinline__ void fold_groups(float (&v)[8]) {
+#pragma unroll
+  for (int mask = G; mask < kWave; mask <<= 1)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] += __shfl_xor(v[q], mask, 64);
+}
+
+// ---------------------------------------------------------------------------
+// Forward
+
+template <typename I>
+struct DotFwdArgs {
+  const I* row_ptr;
+  const I* col;
+  PlanView plan;
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const float* bias;  // [E, H] or null
+  float scale;
+  uint16_t* out;
+  float* ml;          // [N, H, 2]
+  float* partial;     // per chunk: acc[8G] | m[H] | l[H]
+};
+
+template <typename I, int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
+  constexpr int EPW = kWave / G;
+  constexpr int HD = 8 * G;
+  constexpr int H = G / HL;
+  const Task t = decode_task(a.plan, a.row_ptr, global_wave());
+  if (t.kind == kTaskNone) return;
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int c = lane % G;
+  const int hd = c / HL;
+  const bool head_lead = (c % HL) == 0;
+  if (t.kind == kTaskEmpty) {
+    for (int r = 0; r < t.n_empty; ++r) {
+      const int64_t i = uniform(a.plan.rows[t.empty0 + r]);
+      if (g == 0) {
+        stv(a.out + i * HD + 8 * c, u32x4{0u, 0u, 0u, 0u});
+        if (head_lead) {
+          a.ml[(i * H + hd) * 2] = kNegInf;
+          a.ml[(i * H + hd) * 2 + 1] = 0.f;
+        }
+      }
+    }
+    return;
+  }
+  const int64_t row = t.row;
+  float qf[8];
+  unpack8(ldv(a.q + row * HD + 8 * c), qf);
+  SoftState<8> st;
+  st.init();
+  for (int64_t base = t.e0; base < t.e1; base += kWave) {
+    const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
+    const int my_col = lane < n ? static_cast<int>(a.col[base + lane]) : 0;
+    for (int k = 0; k < n; k += EPW * U) {
+      u32x4 kk[U], vv[U];
+      float bb[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
+        kk[u] = ldv(a.k + static_cast<int64_t>(j) * HD + 8 * c);
+        vv[u] = ldv(a.v + static_cast<int64_t>(j) * HD + 8 * c);
+        bb[u] = (a.bias && slot < n) ? a.bias[(base + slot) * H + hd] : 0.f;
+      }
+      float s[U];
+      float mc = kNegInf;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const float sc = group_sum<HL>(dot8(qf, kk[u])) * a.scale + bb[u];
+        s[u] = slot < n ? sc : kNegInf;
+        mc = fmaxf(mc, s[u]);
+      }
+      if (mc > st.m) st.rescale(mc);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float p = s[u] == kNegInf ? 0.f : fast_exp(s[u] - st.m);
+        st.l += p;
+        float vf[8];
+        unpack8(vv[u], vf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st.acc[q] += p * vf[q];
+      }
+    }
+  }
+#pragma unroll
+  for (int mask = G; mask < kWave; mask <<= 1) st.merge_xor(mask);
+  if (g != 0) return;
+  if (t.kind == kTaskChunk) {
+    float* p = a.partial + static_cast<int64_t>(t.slot) * (HD + 2 * H);
+    store8(p + 8 * c, st.acc);
+    if (head_lead) {
+      p[HD + hd] = st.m;
+      p[HD + H + hd] = st.l;
+    }
+    return;
+  }
+  const float inv = 1.f / st.l;
+  float o[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o[q] = st.acc[q] * inv;
+  stv(a.out + row * HD + 8 * c, pack8(o));
+  if (head_lead) {
+    a.ml[(row * H + hd) * 2] = st.m + __logf(st.l);
+    a.ml[(row * H + hd) * 2 + 1] = 0.f;
+  }
+}
+
+template <int G, int HL>
+__global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
+    PlanView plan, const float* __restrict__ partial, uint16_t* __restrict__ out,
+    float* __restrict__ ml) {
+  constexpr int HD = 8 * G;
+  constexpr int H = G / HL;
+  const int64_t k = global_wave();
+  if (k >= plan.n_split) return;
+  const int c = lane_id();
+  if (c >= G) return;
+  const int hd = c / HL;
+  const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
+  const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
+  SoftState<8> st;
+  st.init();
+  for (int q = c0; q < c1; ++q) {
+    const float* p = partial + static_cast<int64_t>(q) * (HD + 2 * H);
+    float acc[8];
+    load8(p + 8 * c, acc);
+    st.merge(p[HD + hd], p[HD + H + hd], acc);
+  }
+  const float inv = 1.f / st.l;
+  float o[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o[q] = st.acc[q] * inv;
+  stv(out + row * HD + 8 * c, pack8(o));
+  if (c % HL == 0) {
+    ml[(row * H + hd) * 2] = st.m + __logf(st.l);
+    ml[(row * H + hd) * 2 + 1] = 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward
+
+template <int G, int HL>
+__global__ __launch_bounds__(kTaskBlock) void dot_delta_kernel(
+    const uint16_t* __restrict__ dout, const uint16_t* __restrict__ out,
+    float* __restrict__ ml, int64_t n_nodes) {
+  constexpr int EPW = kWave / G;
+  constexpr int HD = 8 * G;
+  constexpr int H = G / HL;
+  const int lane = lane_id();
+  const int c = lane % G, hd = c / HL;
+  const int64_t node = global_wave() * EPW + lane / G;
+  if (node >= n_nodes) return;
+  float d[8];
+  unpack8(ldv(dout + node * HD + 8 * c), d);
+  const float delta = group_sum<HL>(dot8(d, ldv(out + node * HD + 8 * c)));
+  if (c % HL == 0) ml[(node * H + hd) * 2 + 1] = delta;
+}
+
+template <typename I>
+struct DotDstArgs {
+  const I* row_ptr;
+  const I* col;
+  PlanView plan;
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const float* bias;
+  float scale;
+  const float* ml;
+  const uint16_t* dout;
+  uint16_t* dq;
+  float* dbias;     // [E, H] or null
+  float* partial;   // per chunk: [8G] unscaled dq
+};
+
+template <typename I, int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a) {
+  constexpr int EPW = kWave / G;
+  constexpr int HD = 8 * G;
+  constexpr int H = G / HL;
+  const Task t = decode_task(a.plan, a.row_ptr, global_wave());
+  if (t.kind == kTaskNone) return;
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int c = lane % G;
+  const int hd = c / HL;
+  const bool head_lead = (c % HL) == 0;
+  if (t.kind == kTaskEmpty) {
+    for (int r = 0; r < t.n_empty; ++r) {
+      const int64_t i = uniform(a.plan.rows[t.empty0 + r]);
+      if (g == 0) stv(a.dq + i * HD + 8 * c, u32x4{0u, 0u, 0u, 0u});
+    }
+    return;
+  }
+  const int64_t row = t.row;
+  float qf[8], df[8];
+  unpack8(ldv(a.q + row * HD + 8 * c), qf);
+  unpack8(ldv(a.dout + row * HD + 8 * c), df);
+  const float lse = a.ml[(row * H + hd) * 2];
+  const float delta = a.ml[(row * H + hd) * 2 + 1];
+  float dq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t base = t.e0; base < t.e1; base += kWave) {
+    const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
+    const int my_col = lane < n ? static_cast<int>(a.col[base + lane]) : 0;
+    for (int k = 0; k < n; k += EPW * U) {
+      u32x4 kk[U], vv[U];
+      float bb[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
+        kk[u] = ldv(a.k + static_cast<int64_t>(j) * HD + 8 * c);
+        vv[u] = ldv(a.v + static_cast<int64_t>(j) * HD + 8 * c);
+        bb[u] = (a.bias && slot < n) ? a.bias[(base + slot) * H + hd] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const bool valid = slot < n;
+        const float s = group_sum<HL>(dot8(qf, kk[u])) * a.scale + bb[u];
+        const float alpha = valid ? fast_exp(s - lse) : 0.f;
+        const float dalpha = group_sum<HL>(dot8(df, vv[u]));
+        const float ds = alpha * (dalpha - delta);
+        if (a.dbias && valid && head_lead) a.dbias[(base + slot) * H + hd] = ds;
+        float kf[8];
+        unpack8(kk[u], kf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dq[q] += ds * kf[q];
+      }
+    }
+  }
+  fold_groups<G>(dq);
+  if (g != 0) return;
+  if (t.kind == kTaskChunk) {
+    store8(a.partial + static_cast<int64_t>(t.slot) * HD + 8 * c, dq);
+    return;
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) dq[q] *= a.scale;
+  stv(a.dq + row * HD + 8 * c, pack8(dq));
+}
+
+template <int G>
+__global__ __launch_bounds__(kTaskBlock) void dot_dq_merge_kernel(
+    PlanView plan, const float* __restrict__ partial, float scale, uint16_t* __restrict__ dq) {
+  constexpr int HD = 8 * G;
+  const int64_t k = global_wave();
+  if (k >= plan.n_split) return;
+  const int c = lane_id();
+  if (c >= G) return;
+  const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
+  const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int q = c0; q < c1; ++q) {
+    float p[8];
+    load8(partial + static_cast<int64_t>(q) * HD + 8 * c, p);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) s[r] += p[r];
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) s[r] *= scale;
+  stv(dq + row * HD + 8 * c, pack8(s));
+}
+
+struct DotSrcArgs {
+  const int32_t* row_ptr_t;
+  const int32_t* col_t;
+  const int32_t* perm;
+  PlanView plan;
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const float* bias;
+  float scale;
+  const float* ml;
+  const uint16_t* dout;
+  uint16_t* dk;
+  uint16_t* dv;
+  float* partial;   // per chunk: [8G] unscaled dk | [8G] dv
+};
+
+template <int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
+  constexpr int EPW = kWave / G;
+  constexpr int HD = 8 * G;
+  constexpr int H = G / HL;
+  const Task t = decode_task(a.plan, a.row_ptr_t, global_wave());
+  if (t.kind == kTaskNone) return;
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int c = lane % G;
+  const int hd = c / HL;
+  if (t.kind == kTaskEmpty) {
+    for (int r = 0; r < t.n_empty; ++r) {
+      const int64_t j = uniform(a.plan.rows[t.empty0 + r]);
+      if (g == 0) {
+        stv(a.dk + j * HD + 8 * c, u32x4{0u, 0u, 0u, 0u});
+        stv(a.dv + j * HD + 8 * c, u32x4{0u, 0u, 0u, 0u});
+      }
+    }
+    return;
+  }
+  const int64_t j = t.row;
+  float kf[8], vf[8];
+  unpack8(ldv(a.k + j * HD + 8 * c), kf);
+  unpack8(ldv(a.v + j * HD + 8 * c), vf);
+  float dk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float dv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t base = t.e0; base < t.e1; base += kWave) {
+    const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
+    int my_i = 0, my_e = 0;
+    if (lane < n) {
+      my_i = a.col_t[base + lane];
+      my_e = a.perm[base + lane];
+    }
+    for (int k = 0; k < n; k += EPW * U) {
+      u32x4 qq[U], dd[U];
+      float bb[U], lse[U], dl[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const int src = slot < n ? slot : 0;
+        const int64_t i = fetch_lane<EPW>(my_i, src);
+        const int64_t e = fetch_lane<EPW>(my_e, src);
+        qq[u] = ldv(a.q + i * HD + 8 * c);
+        dd[u] = ldv(a.dout + i * HD + 8 * c);
+        lse[u] = a.ml[(i * H + hd) * 2];
+        dl[u] = a.ml[(i * H + hd) * 2 + 1];
+        bb[u] = a.bias ? a.bias[e * H + hd] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int slot = k + u * EPW + g;
+        const bool valid = slot < n;
+        float qf[8], df[8];
+        unpack8(qq[u], qf);
+        unpack8(dd[u], df);
+        float sp = 0.f, dp = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          sp += qf[q] * kf[q];
+          dp += df[q] * vf[q];
+        }
+        const float s = group_sum<HL>(sp) * a.scale + bb[u];
+        const float alpha = valid ? fast_exp(s - lse[u]) : 0.f;
+        const float ds = alpha * (group_sum<HL>(dp) - dl[u]);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          dk[q] += ds * qf[q];
+          dv[q] += alpha * df[q];
+        }
+      }
+    }
+  }
+  fold_groups<G>(dk);
+  fold_groups<G>(dv);
+  if (g != 0) return;
+  if (t.kind == kTaskChunk) {
+    float* p = a.partial + static_cast<int64_t>(t.slot) * (2 * HD);
+    store8(p + 8 * c, dk);
+    store8(p + HD + 8 * c, dv);
+    return;
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) dk[q] *= a.scale;
+  stv(a.dk + j * HD + 8 * c, pack8(dk));
+  stv(a.dv + j * HD + 8 * c, pack8(dv));
+}
+
+template <int G>
+__global__ __launch_bounds__(kTaskBlock) void dot_kv_merge_kernel(
+    PlanView plan, const float* __restrict__ partial, float scale, uint16_t* __restrict__ dk,
+    uint16_t* __restrict__ dv) {
+  constexpr int HD = 8 * G;
+  const int64_t k = global_wave();
+  if (k >= plan.n_split) return;
+  const int c = lane_id();
+  if (c >= G) return;
+  const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
+  const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
+  float sk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int q = c0; q < c1; ++q) {
+    float pk[8], pv[8];
+    load8(partial + static_cast<int64_t>(q) * (2 * HD) + 8 * c, pk);
+    load8(partial + static_cast<int64_t>(q) * (2 * HD) + HD + 8 * c, pv);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      sk[r] += pk[r];
+      sv[r] += pv[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) sk[r] *= scale;
+  stv(dk + row * HD + 8 * c, pack8(sk));
+  stv(dv + row * HD + 8 * c, pack8(sv));
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+
+struct DotShape {
+  int G, HL;
+};
+
+bool dot_shape(int H, int D, DotShape* s) {
+  if (H <= 0 || D <= 0 || D % 8 != 0) return false;
+  const int HD = H * D;
+  if (HD != 128 && HD != 256 && HD != 512) return false;
+  s->G = HD / 8;
+  s->HL = D / 8;
+  return s->HL >= 1 && s->HL <= 16 && s->G % s->HL == 0;
+}
+
+#define TGX_DOT_SHAPES(X) \
+  X(64, 16) X(64, 8) X(64, 4) X(64, 2) X(64, 1) \
+  X(32, 16) X(32, 8) X(32, 4) X(32, 2) X(32, 1) \
+  X(16, 16) X(16, 8) X(16, 4) X(16, 2) X(16, 1)
+
+template <int G>
+constexpr int dot_unroll() {
+  return (kWave / G) >= 4 ? 2 : 4;
+}
+
+template <typename I, int G, int HL>
+int dot_fwd_launch(const DotFwdArgs<I>& a, hipStream_t s) {
+  constexpr int U = dot_unroll<G>();
+  const int64_t waves = plan_waves(a.plan);
+  if (waves > 0) {
+    TGX_PROFILE("dot_fwd_kernel", s);
+    dot_fwd_kernel<I, G, HL, U><<<ceil_div(waves, kWavesPerBlock), kTaskBlock, 0, s>>>(a);
+    TGX_LAUNCHED("dot_fwd_kernel");
+  }
+  if (a.plan.n_split > 0) {
+    TGX_PROFILE("dot_fwd_merge_kernel", s);
+    dot_fwd_merge_kernel<G, HL><<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        a.plan, a.partial, a.out, a.ml);
+    TGX_LAUNCHED("dot_fwd_merge_kernel");
+  }
+  return TGX_OK;
+}
+
+struct DotBwdLayout {
+  size_t dst_part_off, src_part_off, bytes;
+};
+
+DotBwdLayout dot_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t, int H, int D) {
+  DotBwdLayout L;
+  const int64_t HD = static_cast<int64_t>(H) * D;
+  Carve c{nullptr, 0};
+  L.dst_part_off = reinterpret_cast<size_t>(c.take<float>(plan.n_chunks * HD));
+  L.src_part_off = reinterpret_cast<size_t>(c.take<float>(plan_t.n_chunks * 2 * HD));
+  L.bytes = align_up(c.used) + 256;
+  return L;
+}
+
+template <typename I, int G, int HL>
+int dot_bwd_launch(const DotDstArgs<I>& da, DotSrcArgs sa, const uint16_t* out,
+                   float* ml, int64_t n_nodes, hipStream_t s) {
+  constexpr int U = dot_unroll<G>();
+  constexpr int EPW = kWave / G;
+  {
+    TGX_PROFILE("dot_delta_kernel", s);
+    dot_delta_kernel<G, HL><<<ceil_div(ceil_div(n_nodes, EPW), kWavesPerBlock), kTaskBlock, 0,
+                              s>>>(da.dout, out, ml, n_nodes);
+    TGX_LAUNCHED("dot_delta_kernel");
+  }
+  const int64_t dst_waves = plan_waves(da.plan);
+  if (dst_waves > 0) {
+    TGX_PROFILE("dot_bwd_dst_kernel", s);
+    dot_bwd_dst_kernel<I, G, HL, U><<<ceil_div(dst_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(da);
+    TGX_LAUNCHED("dot_bwd_dst_kernel");
+  }
+  if (da.plan.n_split > 0) {
+    TGX_PROFILE("dot_dq_merge_kernel", s);
+    dot_dq_merge_kernel<G><<<ceil_div(da.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        da.plan, da.partial, da.scale, da.dq);
+    TGX_LAUNCHED("dot_dq_merge_kernel");
+  }
+  const int64_t src_waves = plan_waves(sa.plan);
+  if (src_waves > 0) {
+    TGX_PROFILE("dot_bwd_src_kernel", s);
+    dot_bwd_src_kernel<G, HL, U><<<ceil_div(src_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
+    TGX_LAUNCHED("dot_bwd_src_kernel");
+  }
+  if (sa.plan.n_split > 0) {
+    TGX_PROFILE("dot_kv_merge_kernel", s);
+    dot_kv_merge_kernel<G><<<ceil_div(sa.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        sa.plan, sa.partial, sa.scale, sa.dk, sa.dv);
+    TGX_LAUNCHED("dot_kv_merge_kernel");
+  }
+  return TGX_OK;
+}
+
+}  // namespace
+}  // namespace tgx
+
+using namespace tgx;
+
+extern "C" int tgx_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bits,
+                                const tgx_row_plan* plan, const void* q, const void* k,
+                                const void* v, const float* bias, float scale, void* out,
+                                float* ml, int64_t n_dst, int64_t n_src, int H, int D,
+                                float* partial, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  DotShape shp;
+  if (!dot_shape(H, D, &shp)) {
+    set_error("dot attention supports D %% 8 == 0 and H*D in {128,256,512} (got H=%d D=%d)",
+              H, D);
+    return TGX_UNSUPPORTED;
+  }
+  int st = check_plan(plan, n_dst);
+  if (st != TGX_OK) return st;
+  if (n_dst == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && q && out && ml && ((k && v) || n_src == 0), "null pointer");
+  TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
+  hipStream_t s = as_stream(stream);
+  const auto* qq = static_cast<const uint16_t*>(q);
+  const auto* kk = static_cast<const uint16_t*>(k);
+  const auto* vv = static_cast<const uint16_t*>(v);
+  auto* oo = static_cast<uint16_t*>(out);
+#define TGX_DOT_FWD(GG, HH)                                                                 \
+  if (shp.G == GG && shp.HL == HH) {                                                        \
+    if (idx_bits == 32)                                                                     \
+      return dot_fwd_launch<int32_t, GG, HH>(                                               \
+          DotFwdArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                         \
+                              static_cast<const int32_t*>(col), plan_view(*plan), qq, kk,   \
+                              vv, bias, scale, oo, ml, partial},                            \
+          s);                                                                               \
+    return dot_fwd_launch<int64_t, GG, HH>(                                                 \
+        DotFwdArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                           \
+                            static_cast<const int64_t*>(col), plan_view(*plan), qq, kk, vv, \
+                            bias, scale, oo, ml, partial},                                  \
+        s);                                                                                 \
+  }
+  TGX_DOT_SHAPES(TGX_DOT_FWD)
+#undef TGX_DOT_FWD
+  set_error("unsupported dot attention shape");
+  return TGX_UNSUPPORTED;
+}
+
+extern "C" int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
+                                          int H, int D, size_t* bytes) {
+  TGX_REQUIRE(plan && plan_t && bytes, "null pointer");
+  DotShape shp;
+  if (!dot_shape(H, D, &shp)) {
+    set_error("unsupported dot attention shape H=%d D=%d", H, D);
+    return TGX_UNSUPPORTED;
+  }
+  *bytes = dot_bwd_layout(*plan, *plan_t, H, D).bytes;
+  return TGX_OK;
+}
+
+extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bits,
+                                const tgx_row_plan* plan, const int32_t* row_ptr_t,
+                                const int32_t* col_t, const int32_t* perm,
+                                const tgx_row_plan* plan_t, const void* q, const void* k,
+                                const void* v, const float* bias, float scale, const void* out,
+                                float* ml, const void* dout, void* dq, void* dk, void* dv,
+                                float* dbias, int64_t n_dst, int64_t n_src, int H, int D,
+                                void* ws, size_t ws_bytes, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  DotShape shp;
+  if (!dot_shape(H, D, &shp)) {
+    set_error("unsupported dot attention shape H=%d D=%d", H, D);
+    return TGX_UNSUPPORTED;
+  }
+  int st = check_plan(plan, n_dst);
+  if (st != TGX_OK) return st;
+  st = check_plan(plan_t, n_src);
+  if (st != TGX_OK) return st;
+  TGX_REQUIRE(row_ptr && row_ptr_t && q && out && ml && dout && dq &&
+                  ((k && v && dk && dv) || n_src == 0),
+              "null pointer");
+  const DotBwdLayout L = dot_bwd_layout(*plan, *plan_t, H, D);
+  TGX_REQUIRE(ws && ws_bytes >= L.bytes, "workspace too small: need %zu bytes", L.bytes);
+  hipStream_t s = as_stream(stream);
+  char* w = static_cast<char*>(ws);
+  float* dst_part = reinterpret_cast<float*>(w + L.dst_part_off);
+  float* src_part = reinterpret_cast<float*>(w + L.src_part_off);
+  const auto* qq = static_cast<const uint16_t*>(q);
+  const auto* kk = static_cast<const uint16_t*>(k);
+  const auto* vv = static_cast<const uint16_t*>(v);
+  const auto* oo = static_cast<const uint16_t*>(out);
+  const auto* gg = static_cast<const uint16_t*>(dout);
+  DotSrcArgs sa{row_ptr_t, col_t, perm, plan_view(*plan_t), qq, kk, vv, bias, scale, ml, gg,
+                static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv), src_part};
+#define TGX_DOT_BWD(GG, HH)                                                                  \
+  if (shp.G == GG && shp.HL == HH) {                                                         \
+    if (idx_bits == 32)                                                                      \
+      return dot_bwd_launch<int32_t, GG, HH>(                                                \
+          DotDstArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                          \
+                              static_cast<const int32_t*>(col), plan_view(*plan), qq, kk,    \
+                              vv, bias, scale, ml, gg, static_cast<uint16_t*>(dq), dbias,    \
+                              dst_part},                                                     \
+          sa, oo, ml, n_dst, s);                                                             \
+    return dot_bwd_launch<int64_t, GG, HH>(                                                  \
+        DotDstArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                            \
+                            static_cast<const int64_t*>(col), plan_view(*plan), qq, kk, vv,  \
+                            bias, scale, ml, gg, static_cast<uint16_t*>(dq), dbias,          \
+                            dst_part},                                                       \
+        sa, oo, ml, n_dst, s);                                                               \
+  }
+  TGX_DOT_SHAPES(TGX_DOT_BWD)
+#undef TGX_DOT_BWD
+  set_error("unsupported dot attention shape");
+  return TGX_UNSUPPORTED;
+}

@@ -133,3 +133,60 @@ class GatFunction(torch.autograd.Function):
                      _native.stream_of(hc))
         return (dh, da_src.reshape(ctx.a_shapes[0]), da_dst.reshape(ctx.a_shapes[1]),
                 None, None)
+
+
+class DotAttnFunction(torch.autograd.Function):
+    """Dot-product attention, bf16 q [Nd,H,D], k/v [Ns,H,D], bias [E,H] fp32."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, scale: float, graph: Graph):
+        row_ptr, col_idx = graph.resolve_csr()
+        n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
+        _, H, D = q.shape
+        qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+        bc = None if bias is None else bias.contiguous()
+        out = torch.empty_like(qc)
+        ml = torch.empty((n_dst, H, 2), dtype=torch.float32, device=q.device)
+        plan = graph._row_plan()
+        partial = _partial(plan, H * D + 2 * H, q.device)
+        _native.call("tgx_dot_attn_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
+                     _native.idx_bits(row_ptr), plan.ref, qc.data_ptr(), kc.data_ptr(),
+                     vc.data_ptr(), _p(bc), float(scale), out.data_ptr(), ml.data_ptr(),
+                     n_dst, n_src, H, D, _p(partial), _native.stream_of(q))
+        ctx.graph = graph
+        ctx.scale = float(scale)
+        ctx.has_bias = bias is not None
+        ctx.save_for_backward(qc, kc, vc, bc, out, ml)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        qc, kc, vc, bc, out, ml = ctx.saved_tensors
+        graph: Graph = ctx.graph
+        row_ptr, col_idx = graph.resolve_csr()
+        n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
+        _, H, D = qc.shape
+        E = graph.num_edges
+        dout = dout.contiguous()
+        if dout.dtype != qc.dtype:
+            dout = dout.to(qc.dtype)
+        dq = torch.empty_like(qc)
+        dk = torch.empty_like(kc)
+        dv = torch.empty_like(vc)
+        need_db = ctx.has_bias and ctx.needs_input_grad[3]
+        dbias = torch.empty((E, H), dtype=torch.float32, device=qc.device) if need_db else None
+        plan = graph._row_plan()
+        t = graph._transposed()
+        ws_bytes = ctypes.c_size_t()
+        _native.call("tgx_dot_attn_bwd_workspace", plan.ref, t.plan.ref, H, D,
+                     ctypes.byref(ws_bytes))
+        ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=qc.device)
+        # Slot 1 of the saved ml is backward scratch (delta), rewritten each time.
+        _native.call("tgx_dot_attn_bwd", row_ptr.data_ptr(), col_idx.data_ptr(),
+                     _native.idx_bits(row_ptr), plan.ref, t.row_ptr_t.data_ptr(),
+                     t.col_t.data_ptr(), t.perm.data_ptr(), t.plan.ref, qc.data_ptr(),
+                     kc.data_ptr(), vc.data_ptr(), _p(bc), ctx.scale, out.data_ptr(),
+                     ml.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                     dv.data_ptr(), _p(dbias), n_dst, n_src, H, D, ws.data_ptr(),
+                     ws_bytes.value, _native.stream_of(qc))
+        return dq, dk, dv, dbias, None, None

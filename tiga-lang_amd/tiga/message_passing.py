@@ -183,7 +183,45 @@ class MessagePassing(Kernel):
                                 "online softmax per (row, head), logsumexp saved; "
                                 "backward recomputes alpha over the transposed CSR")
             return out
+        dot = cap.recognize_dot(captured)
+        if dot is not None:
+            return self._execute_dot(dot, graph, src, dst, edge)
         return None
+
+    def _execute_dot(self, dot, graph, src, dst, edge):
+        from . import _ops
+
+        q, k, v = dst.get(dot.q_field), src.get(dot.k_field), src.get(dot.v_field)
+        if q is None or k is None or v is None:
+            return None
+        if q.ndim != 3 or k.shape[1:] != q.shape[1:] or v.shape[1:] != q.shape[1:]:
+            return None
+        if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+            return None
+        _, H, D = q.shape
+        if D % 8 or H * D not in (128, 256, 512):
+            return None
+        if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
+            return None
+        bias = None
+        if dot.bias_field is not None:
+            bias = edge.get(dot.bias_field)
+            if bias is None or bias.dtype != torch.float32:
+                return None
+            if graph.is_varlen:
+                return None
+            if tuple(bias.shape) not in ((graph.num_edges, H), (graph.num_edges, H, 1)):
+                return None
+            bias = bias.reshape(graph.num_edges, H)
+        if graph.is_varlen:
+            return None
+        _native.lib()
+        out = _ops.DotAttnFunction.apply(q, k, v, bias, dot.scale, graph)
+        self._record_native(graph, "dot-product", ("tgx_dot_attn_fwd", "tgx_dot_attn_bwd"),
+                            "bf16 gathers, fp32 online softmax per (row, head); hub rows "
+                            "split and merged; backward over CSR (dq, dbias) and transposed "
+                            "CSR (dk, dv)")
+        return out
 
 
 __all__ = ["MessagePassing", "config"]
