@@ -28,6 +28,18 @@ for p in (str(ROOT / "tiga-lang_amd"), str(ROOT)):
 HBM_PEAK_GBS = 8000.0
 
 
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` measured by rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE (scaled by the copy calibration) and recorded in
+    profiles/traffic.json; None when no measurement is recorded."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        rec = json.loads(path.read_text())[config][kernel]
+    except (OSError, KeyError, ValueError):
+        return None, None
+    return rec["fetch_bytes"] + rec["write_bytes"], rec["source"]
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -256,7 +268,8 @@ def run_c2(args):
         "hbm_frac_step": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "avg_ms": avg_ms,
+                     "traffic": measured_traffic("c2", dominant)[0],
+                     "traffic_source": measured_traffic("c2", dominant)[1], "avg_ms": avg_ms,
                      "algorithmic_bytes": bytes_per[dominant]},
         "kernels": {k: {"launches": n, "avg_ms": ms / n,
                         "gbs": (bytes_per[k] / (ms / n * 1e-3) / 1e9) if k in bytes_per else None}
@@ -402,7 +415,9 @@ def run_c3c4(args):
         "hbm_frac_step": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "algorithmic_bytes": bytes_per[dominant]},
+                     "traffic": measured_traffic(args.config, dominant)[0],
+                     "traffic_source": measured_traffic(args.config, dominant)[1],
+                     "algorithmic_bytes": bytes_per[dominant]},
         "kernels": {kk: {"launches": n, "avg_ms": t / n,
                          "gbs": (bytes_per[kk] / (t / n * 1e-3) / 1e9) if kk in bytes_per else None}
                     for kk, (n, t) in sorted(timer.totals.items())},
