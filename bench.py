@@ -26,6 +26,7 @@ for p in (str(ROOT / "tiga-lang_amd"), str(ROOT)):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 
 
 def measured_traffic(config, kernel):
@@ -45,7 +46,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=None)
@@ -424,6 +425,82 @@ def run_c3c4(args):
     }
 
 
+def run_c5(args):
+    """C5: varlen causal attention, 32 sequences of U[512, 4096] tokens,
+    H=16, D=128, bf16, forward + backward on MFMA."""
+    import numpy as np
+    import torch
+
+    import tiga as tg
+    from tiga import _native
+
+    dev = torch.device("cuda")
+    rng = np.random.default_rng(args.seed)
+    lengths = rng.integers(512, 4097, size=32)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int64, device=dev)
+    T, H, D = int(lengths.sum()), 16, 128
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    mk = lambda: torch.randn(T, H, D, device=dev, generator=g).to(torch.bfloat16)
+    q, k, v = (mk().requires_grad_(True) for _ in range(3))
+    dout = mk()
+    graph = tg.Graph.cu_seqlens(cu, causal=True)
+    tg.config.strict = True
+
+    class VarlenAttention(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge, scale):
+            return self.reducer((src.key * dst.query).sum(dim=-1) * scale, src.value)
+
+    kernel = VarlenAttention()
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = kernel(graph=graph, src={"key": k, "value": v}, dst={"query": q}, scale=D ** -0.5)
+        out.backward(dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    assert kernel.last_variant.backend == "hip"
+    with _native.KernelTimer() as timer:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    pairs = int((lengths * (lengths + 1) // 2).sum())
+    fwd_flops = 4.0 * H * D * pairs
+    step_flops = 3.5 * fwd_flops              # FA2 convention: bwd = 2.5 x fwd
+    ms = elapsed * 1e3 / args.steps
+    tflops = step_flops / (ms * 1e-3) / 1e12
+    kflops = {"varlen_fwd_kernel": fwd_flops, "varlen_dkdv_kernel": 2.0 * fwd_flops,
+              "varlen_dq_kernel": 0.5 * fwd_flops}
+    per = {kk: (n, t) for kk, (n, t) in timer.totals.items()}
+    dominant = max((kk for kk in per if kk in kflops), key=lambda kk: per[kk][1])
+    n_launch, total_ms = per[dominant]
+    achieved = kflops[dominant] / (total_ms / n_launch * 1e-3) / 1e12
+    return {
+        "metric": "varlen causal attention fwd+bwd TFLOP/s, 32 seqs U[512,4096], H=16 D=128, "
+                  "bf16, 1xMI355X",
+        "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded lengths, q,k,v,dout ~N(0,1))",
+        "config": {"workload": "c5-varlen-causal-fwd-bwd", "tokens": T, "sequences": 32,
+                   "heads": H, "head_dim": D, "causal_pairs": pairs,
+                   "flop_convention": "fwd 4*H*D*pairs, bwd 2.5x fwd (useful FLOPs; the dQ "
+                                      "pass recomputes S and dP, not counted)"},
+        "mfma_utilization": tflops / BF16_PEAK_TFLOPS,
+        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved,
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None},
+        "kernels": {kk: {"launches": n, "avg_ms": t / n,
+                         "tflops": (kflops[kk] / (t / n * 1e-3) / 1e12) if kk in kflops else None}
+                    for kk, (n, t) in sorted(per.items())},
+    }
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
@@ -434,7 +511,7 @@ def main():
               "(collectives and sharding are out of scope); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-    runners = {"c1": run_c1, "c2": run_c2, "c3": run_c3c4, "c4": run_c3c4}
+    runners = {"c1": run_c1, "c2": run_c2, "c3": run_c3c4, "c4": run_c3c4, "c5": run_c5}
     result = runners[args.config](args)
     print(json.dumps(result), flush=True)
 

@@ -1,0 +1,123 @@
+"""GPU parity of the MFMA varlen causal attention against the fp64 oracle
+(bf16 inputs; tolerance 2e-2 relative, max-norm, as the north star states)."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import tiga as tg
+from tiga import _native
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def rel_err(actual, expected):
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
+
+
+def tiles_for(cu, block=128, kind=0):
+    n = ctypes.c_int64()
+    cu_h = np.ascontiguousarray(cu, dtype=np.int32)
+    _native.call("tgx_varlen_causal_tiles", cu_h.ctypes.data, cu_h.size - 1, block, kind,
+                 None, ctypes.byref(n))
+    tiles = np.zeros(2 * max(n.value, 1), dtype=np.int32)
+    _native.call("tgx_varlen_causal_tiles", cu_h.ctypes.data, cu_h.size - 1, block, kind,
+                 tiles.ctypes.data, ctypes.byref(n))
+    return torch.as_tensor(tiles, device=DEV), n.value
+
+
+def varlen_fwd_capi(cu, q, k, v, scale):
+    T, H, D = q.shape
+    tiles, n = tiles_for(cu)
+    cu_d = torch.as_tensor(np.asarray(cu, dtype=np.int32), device=DEV)
+    out = torch.empty_like(q)
+    lse = torch.empty(T, H, dtype=torch.float32, device=DEV)
+    _native.call("tgx_varlen_causal_fwd", cu_d.data_ptr(), tiles.data_ptr(), n, q.data_ptr(),
+                 k.data_ptr(), v.data_ptr(), scale, out.data_ptr(), lse.data_ptr(), T, H, D,
+                 _native.stream_of(q))
+    torch.cuda.synchronize()
+    return out, lse
+
+
+@pytest.mark.parametrize("lengths,H", [
+    ([1, 5, 17, 64, 65, 128, 129, 300, 1000, 2], 2),
+    ([512, 700], 16),
+])
+def test_varlen_fwd_parity(lengths, H):
+    print(f"varlen fwd lengths={lengths} H={H}", flush=True)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    T, D = int(cu[-1]), 128
+    rng = np.random.default_rng(len(lengths) + H)
+    q, k, v = (torch.as_tensor(rng.standard_normal((T, H, D)), device=DEV).to(torch.bfloat16)
+               for _ in range(3))
+    scale = 1.0 / np.sqrt(D)
+    out, lse = varlen_fwd_capi(cu, q, k, v, scale)
+    f = lambda t: t.float().cpu().numpy()
+    e_out, e_lse = ref.varlen_causal_fwd(cu, f(q), f(k), f(v), scale)
+    assert rel_err(f(out), e_out) <= 2e-2
+    assert rel_err(lse.cpu().numpy(), e_lse) <= 1e-3
+
+
+def test_varlen_tiles_order():
+    cu = np.array([0, 3, 300, 301], dtype=np.int32)
+    tiles, n = tiles_for(cu)
+    t = tiles.cpu().numpy()[: 2 * n].reshape(n, 2)
+    # every query covered once; heaviest (longest causal prefix) first
+    assert sorted(map(tuple, t.tolist())) == [(0, 0), (1, 3), (1, 131), (1, 259), (2, 300)]
+    work = [min(q0 + 128, cu[s + 1]) - cu[s] for s, q0 in t]
+    assert work == sorted(work, reverse=True)
+    tiles, n = tiles_for(cu, block=64, kind=1)
+    t = tiles.cpu().numpy()[: 2 * n].reshape(n, 2)
+    work = [cu[s + 1] - k0 for s, k0 in t]
+    assert work == sorted(work, reverse=True) and len(t) == 1 + 5 + 1
+
+
+class VarlenAttention(tg.MessagePassing):
+    """The reference example's kernel (examples/varlen_causal_attention.py:35-41)."""
+
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge, scale):
+        score = (src.key * dst.query).sum(dim=-1) * scale
+        return self.reducer(score, src.value)
+
+
+@pytest.mark.parametrize("lengths,H", [
+    ([1, 5, 17, 64, 65, 128, 129, 300, 2], 2),
+    ([384, 1, 96, 640, 57], 4),
+    ([700, 129], 16),
+])
+def test_varlen_fwd_bwd_through_api(lengths, H):
+    print(f"varlen api lengths={lengths} H={H}", flush=True)
+    tg.config.strict = True
+    try:
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+        T, D = int(cu[-1]), 128
+        rng = np.random.default_rng(sum(lengths))
+        mk = lambda: torch.as_tensor(rng.standard_normal((T, H, D)), device=DEV).to(
+            torch.bfloat16).requires_grad_(True)
+        q, k, v = mk(), mk(), mk()
+        dout = torch.as_tensor(rng.standard_normal((T, H, D)), device=DEV).to(torch.bfloat16)
+        graph = tg.Graph.cat([tg.Graph.triangular(L, device=DEV) for L in lengths])
+        assert graph.is_varlen
+        kernel = VarlenAttention()
+        scale = D ** -0.5
+        out = kernel(graph=graph, src={"key": k, "value": v}, dst={"query": q}, scale=scale)
+        assert kernel.last_variant.backend == "hip"
+        assert kernel.last_variant.pattern == "varlen-causal"
+        out.backward(dout)
+        f = lambda t: t.detach().float().cpu().numpy()
+        e_out, _ = ref.varlen_causal_fwd(cu, f(q), f(k), f(v), scale)
+        e_dq, e_dk, e_dv = ref.varlen_causal_bwd(cu, f(q), f(k), f(v), scale, f(dout))
+        assert rel_err(f(out), e_out) <= 2e-2
+        assert rel_err(f(q.grad), e_dq) <= 2e-2
+        assert rel_err(f(k.grad), e_dk) <= 2e-2
+        assert rel_err(f(v.grad), e_dv) <= 2e-2
+    finally:
+        tg.config.strict = False

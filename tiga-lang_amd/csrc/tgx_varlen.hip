@@ -1,0 +1,701 @@
+// Varlen causal attention on MFMA (gfx950, bf16 in, fp32 accumulate).
+//
+// The relation is Graph.cu_seqlens(causal=True) (reference
+// python/tiga/interop/torch/graph.py:260-294): token i of sequence k attends
+// to keys [s_k, i].  The edge function is the dot-product score
+// scale * q[i].k[j] with value v[j]; the reference evaluates it on its eager
+// oracle (examples/varlen_causal_attention.py:46-48) and its only compiled
+// streaming tile is dense/triangular fp16 forward (lib/Target/Triton/
+// Translate.cpp:1603-1912).  Here it stays implicit (no materialized CSR).
+//
+// Layout: q, k, v, out, dout are [T, H, 128] bf16 (token-major); lse and
+// delta are [T, H] fp32.
+//
+// MFMA: v_mfma_f32_16x16x32_bf16 with lane l, g = l / 16:
+//   A[i = l % 16][k = 8g + j], B[k = 8g + j][n = l % 16], C[4g + r][n = l % 16].
+// The forward computes S^T = K Q^T, so each lane's accumulators hold 4 keys of
+// one query; two 16-key tiles together are exactly the B operand of
+// O^T = V^T P^T under the key order {4g..4g+3, 16+4g..16+4g+3}, so P never
+// leaves registers.  V^T is staged in LDS (transposed while staging) in that
+// same key order, K is staged row-major; both double-buffered with the next
+// tile's global loads in flight during the current tile's MFMAs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "tgx_device.h"
+#include "tgx_host.h"
+#include "tgx_profile.h"
+
+namespace tgx {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+constexpr int VD = 128;    // head dim
+constexpr int VBM = 128;   // queries per workgroup (4 waves x 32)
+constexpr int VBN = 64;    // keys per iteration
+constexpr int KPAD = 136;  // K row stride in LDS (bf16): 272 B, conflict-free 16 B reads
+constexpr int VPAD = 72;   // V^T row stride in LDS (bf16): 144 B, 16 B aligned rows
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x4v mfma(bf16x8 a, bf16x8 b, f32x4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 ld_bf16x8(const __bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+struct VarlenFwdArgs {
+  const int32_t* cu;      // [n_seq + 1]
+  const int32_t* tiles;   // [n_tiles, 2] = (sequence, first query), heaviest first
+  int n_tiles;
+  int H;
+  const __bf16* q;
+  const __bf16* k;
+  const __bf16* v;
+  __bf16* out;
+  float* lse;             // [T, H]
+  float scale_log2;       // softmax scale * log2(e)
+};
+
+// Stage one 64-key tile: thread t holds 4 rows x 16 B of K and of V.
+struct KvStage {
+  bf16x8 k[4], v[4];
+};
+
+__device__ __forceinline__ void load_kv(KvStage& st, const __bf16* kb, const __bf16* vb,
+                                        int64_t row_stride, int kbase, int s1) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = threadIdx.x + 256 * it;
+    const int key = idx >> 4;
+    const int dc = idx & 15;
+    if (kbase + key < s1) {
+      const int64_t off = static_cast<int64_t>(kbase + key) * row_stride + dc * 8;
+      st.k[it] = ld_bf16x8(kb + off);
+      st.v[it] = ld_bf16x8(vb + off);
+    } else {
+      st.k[it] = bf16x8{};
+      st.v[it] = bf16x8{};
+    }
+  }
+}
+
+// V^T key order inside a 32-key block: position p = 8g + j holds key
+// (j < 4 ? 4g + j : 16 + 4g + j - 4).  Inverse: key kk -> position.
+__device__ __forceinline__ int vt_pos(int key) {
+  const int blk = key & ~31;
+  const int kk = key & 31;
+  const int hi = kk >> 4;        // 0: keys 0..15, 1: keys 16..31
+  const int g = (kk & 15) >> 2;  // 0..3
+  const int j = (kk & 3) + 4 * hi;
+  return blk + 8 * g + j;
+}
+
+__device__ __forceinline__ void store_kv(const KvStage& st, __bf16 (*ks)[KPAD],
+                                         __bf16 (*vt)[VPAD]) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = threadIdx.x + 256 * it;
+    const int key = idx >> 4;
+    const int dc = idx & 15;
+    *reinterpret_cast<bf16x8*>(&ks[key][dc * 8]) = st.k[it];
+    const int pos = vt_pos(key);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) vt[dc * 8 + j][pos] = st.v[it][j];
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
+  __shared__ __bf16 ks[2][VBN][KPAD];
+  __shared__ __bf16 vt[2][VD][VPAD];
+  const int task = blockIdx.x;
+  const int tile = task / a.H;
+  const int h = task - tile * a.H;
+  const int seq = a.tiles[2 * tile];
+  const int q0 = a.tiles[2 * tile + 1];
+  const int s0 = a.cu[seq], s1 = a.cu[seq + 1];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, lr = lane & 15;
+  const int64_t row_stride = static_cast<int64_t>(a.H) * VD;
+  const __bf16* qh = a.q + h * VD;
+  const __bf16* kh = a.k + h * VD;
+  const __bf16* vh = a.v + h * VD;
+  const int qb = q0 + wave * 32;
+
+  // Q^T fragments (B operand): lane holds Q[q = qb + 16 qt + lr][32 ks + 8g .. +8].
+  bf16x8 qf[2][4];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qq = qb + 16 * qt + lr;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+      qf[qt][kc] = qq < s1 ? ld_bf16x8(qh + qq * row_stride + 32 * kc + 8 * g) : bf16x8{};
+  }
+
+  const int kv_end = (q0 + VBM < s1) ? q0 + VBM : s1;
+  const int n_kv = (kv_end - s0 + VBN - 1) / VBN;
+  float m[2] = {kNegInf, kNegInf};
+  float lp[2] = {0.f, 0.f};
+  f32x4v o[8][2];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) o[dt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+  KvStage stage;
+  load_kv(stage, kh, vh, row_stride, s0, s1);
+  store_kv(stage, ks[0], vt[0]);
+  for (int it = 0; it < n_kv; ++it) {
+    __syncthreads();
+    const int buf = it & 1;
+    const int kbase = s0 + it * VBN;
+    const bool more = it + 1 < n_kv;
+    if (more) load_kv(stage, kh, vh, row_stride, kbase + VBN, s1);
+
+    // A wave whose 32 queries all precede this key tile has nothing to add.
+    if (kbase <= qb + 31) {
+    // S^T = K Q^T over D = 128 (4 k-steps of 32).
+    f32x4v c[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) c[kt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const bf16x8 kf = ld_bf16x8(&ks[buf][16 * kt + lr][32 * kc + 8 * g]);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) c[kt][qt] = mfma(kf, qf[qt][kc], c[kt][qt]);
+      }
+    }
+
+    // Causal/sequence mask and online softmax (base-2 exponent).
+    const bool edge_tile = kbase + VBN > qb || kbase + VBN > s1;
+    bf16x8 pf[2][2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int qq = qb + 16 * qt + lr;
+      float sv[4][4];
+      float mt = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float s = c[kt][qt][r] * a.scale_log2;
+          if (edge_tile) {
+            const int key = kbase + 16 * kt + 4 * g + r;
+            if (key > qq || key >= s1) s = kNegInf;
+          }
+          sv[kt][r] = s;
+          mt = fmaxf(mt, s);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float mn = fmaxf(m[qt], mt);
+      const float alpha = (m[qt] == kNegInf) ? 0.f : exp2f(m[qt] - mn);
+      float rs = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = (sv[kt][r] == kNegInf) ? 0.f : exp2f(sv[kt][r] - mn);
+          sv[kt][r] = p;
+          rs += p;
+        }
+      lp[qt] = lp[qt] * alpha + rs;
+      m[qt] = mn;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          pf[qt][k2][j] = static_cast<__bf16>(sv[2 * k2][j]);
+          pf[qt][k2][4 + j] = static_cast<__bf16>(sv[2 * k2 + 1][j]);
+        }
+    }
+
+    // O^T += V^T P^T over the 64 keys (2 k-steps of 32).
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const bf16x8 vf = ld_bf16x8(&vt[buf][16 * dt + lr][32 * k2 + 8 * g]);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) o[dt][qt] = mfma(vf, pf[qt][k2], o[dt][qt]);
+      }
+    }
+    }
+    if (more) store_kv(stage, ks[buf ^ 1], vt[buf ^ 1]);
+  }
+
+  // Finalize: l summed over the 4 lane groups, O = O^T / l, natural-log lse.
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float l = lp[qt];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int qq = qb + 16 * qt + lr;
+    if (qq >= s1) continue;
+    const float inv = 1.f / l;
+    __bf16* orow = a.out + qq * row_stride + h * VD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      bf16x4 w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = static_cast<__bf16>(o[dt][qt][r] * inv);
+      *reinterpret_cast<bf16x4*>(orow + 16 * dt + 4 * g) = w;
+    }
+    if (g == 0) a.lse[static_cast<int64_t>(qq) * a.H + h] = (m[qt] + __log2f(l)) * kLn2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward.  Three launches, no atomics:
+//   delta[t, h] = <dout, out>;
+//   dK/dV: one workgroup per 64-key tile (4 waves x 16 keys), looping over
+//          64-query blocks q >= key; S = Q K^T and dP = dO V^T give P and dS
+//          in C layout [q][key], which (two q-tiles, permuted) is directly the
+//          B operand of dV^T = dO^T P and dK^T = Q^T dS;
+//   dQ:    one workgroup per 128-query tile like the forward; S^T = K Q^T and
+//          dP^T = V dO^T give dS^T, the B operand of dQ^T = K^T dS^T.
+// dO^T, Q^T and K^T operands are staged transposed in LDS in the same
+// permuted order as V^T in the forward.
+
+struct VarlenBwdArgs {
+  const int32_t* cu;
+  const int32_t* tiles;   // dK/dV: (sequence, first key) per 64-key tile; dQ: query tiles
+  int n_tiles;
+  int H;
+  const __bf16* q;
+  const __bf16* k;
+  const __bf16* v;
+  const __bf16* dout;
+  const float* lse;       // [T, H]
+  const float* delta;     // [T, H]
+  __bf16* dq;
+  __bf16* dk;
+  __bf16* dv;
+  float scale;            // softmax scale
+  float scale_log2;       // scale * log2(e)
+};
+
+__global__ __launch_bounds__(256) void varlen_delta_kernel(const __bf16* __restrict__ dout,
+                                                           const __bf16* __restrict__ out,
+                                                           float* __restrict__ delta,
+                                                           int64_t T, int H) {
+  // One wave per (token, group of 4 heads): lane l covers 8 elements of head
+  // 4 * blockpart + l / 16.
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int groups = (H + 3) / 4;
+  const int64_t t = wid / groups;
+  const int hg = static_cast<int>(wid - t * groups);
+  if (t >= T) return;
+  const int lane = threadIdx.x & 63;
+  const int h = 4 * hg + (lane >> 4);
+  float s = 0.f;
+  if (h < H) {
+    const int64_t off = (t * H + h) * VD + (lane & 15) * 8;
+    const bf16x8 a = ld_bf16x8(dout + off);
+    const bf16x8 b = ld_bf16x8(out + off);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += static_cast<float>(a[j]) * static_cast<float>(b[j]);
+  }
+  s = group_sum<16>(s);
+  if (h < H && (lane & 15) == 0) delta[t * H + h] = s;
+}
+
+// Staging of one 64-row block of two [T, H, 128] tensors: thread t holds 4
+// rows x 16 B of each (rows beyond `end` are zero).
+struct Stage2 {
+  bf16x8 a[4], b[4];
+};
+
+__device__ __forceinline__ void load2(Stage2& st, const __bf16* xa, const __bf16* xb,
+                                      int64_t row_stride, int base, int end) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = threadIdx.x + 256 * it;
+    const int row = idx >> 4;
+    const int dc = idx & 15;
+    if (base + row < end) {
+      const int64_t off = static_cast<int64_t>(base + row) * row_stride + dc * 8;
+      st.a[it] = ld_bf16x8(xa + off);
+      st.b[it] = ld_bf16x8(xb + off);
+    } else {
+      st.a[it] = bf16x8{};
+      st.b[it] = bf16x8{};
+    }
+  }
+}
+
+// Row-major copy of `a` into ra, and transposed (permuted row order) copies
+// of a and b into ta and tb (any may be null).
+__device__ __forceinline__ void store2(const Stage2& st, __bf16 (*ra)[KPAD], __bf16 (*rb)[KPAD],
+                                       __bf16 (*ta)[VPAD], __bf16 (*tb)[VPAD]) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = threadIdx.x + 256 * it;
+    const int row = idx >> 4;
+    const int dc = idx & 15;
+    if (ra) *reinterpret_cast<bf16x8*>(&ra[row][dc * 8]) = st.a[it];
+    if (rb) *reinterpret_cast<bf16x8*>(&rb[row][dc * 8]) = st.b[it];
+    const int pos = vt_pos(row);
+    if (ta) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ta[dc * 8 + j][pos] = st.a[it][j];
+    }
+    if (tb) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tb[dc * 8 + j][pos] = st.b[it][j];
+    }
+  }
+}
+
+// dK/dV: workgroup = (64-key tile, head); wave w owns keys k0 + 16w .. +16.
+__global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
+  __shared__ __bf16 qs[VBN][KPAD];    // Q rows of the query block
+  __shared__ __bf16 dos[VBN][KPAD];   // dO rows
+  __shared__ __bf16 qt_s[VD][VPAD];   // Q^T (permuted query order)
+  __shared__ __bf16 dot_s[VD][VPAD];  // dO^T
+  __shared__ float lse_s[VBN], del_s[VBN];
+  const int task = blockIdx.x;
+  const int tile = task / a.H;
+  const int h = task - tile * a.H;
+  const int seq = a.tiles[2 * tile];
+  const int k0 = a.tiles[2 * tile + 1];
+  const int s1 = a.cu[seq + 1];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, lr = lane & 15;
+  const int64_t row_stride = static_cast<int64_t>(a.H) * VD;
+  const int key = k0 + 16 * wave + lr;   // this lane's key (B operand column)
+
+  // K^T and V^T fragments (B operands): K[key][32 kc + 8g .. +8].
+  bf16x8 kf[4], vf[4];
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc) {
+    if (key < s1) {
+      kf[kc] = ld_bf16x8(a.k + key * row_stride + h * VD + 32 * kc + 8 * g);
+      vf[kc] = ld_bf16x8(a.v + key * row_stride + h * VD + 32 * kc + 8 * g);
+    } else {
+      kf[kc] = bf16x8{};
+      vf[kc] = bf16x8{};
+    }
+  }
+  f32x4v dkt[8], dvt[8];   // dK^T / dV^T tiles [d = 16 dt + 4g + r][key]
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    dkt[dt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    dvt[dt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  }
+  const __bf16* qh = a.q + h * VD;
+  const __bf16* doh = a.dout + h * VD;
+  const int n_qb = (s1 - k0 + VBN - 1) / VBN;
+  Stage2 st;
+  load2(st, qh, doh, row_stride, k0, s1);
+  for (int ib = 0; ib < n_qb; ++ib) {
+    const int qbase = k0 + ib * VBN;
+    __syncthreads();   // previous block's LDS reads are done
+    store2(st, qs, dos, qt_s, dot_s);
+    if (threadIdx.x < VBN) {
+      const int qq = qbase + threadIdx.x;
+      lse_s[threadIdx.x] = qq < s1 ? a.lse[static_cast<int64_t>(qq) * a.H + h] * kLog2e
+                                   : __builtin_huge_valf();
+      del_s[threadIdx.x] = qq < s1 ? a.delta[static_cast<int64_t>(qq) * a.H + h] : 0.f;
+    }
+    __syncthreads();
+    if (ib + 1 < n_qb) load2(st, qh, doh, row_stride, qbase + VBN, s1);
+    // Keys of this wave that precede every query of the block all count;
+    // a wave whose keys all exceed the block's last query skips it.
+    if (k0 + 16 * wave > qbase + VBN - 1) continue;
+
+    // S = Q K^T, dP = dO V^T: C tiles [q = 16 qt + 4g + r][key].
+    f32x4v sc[4], dp[4];
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      sc[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+      dp[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+#pragma unroll
+      for (int qt = 0; qt < 4; ++qt) {
+        const bf16x8 qa = ld_bf16x8(&qs[16 * qt + lr][32 * kc + 8 * g]);
+        const bf16x8 da = ld_bf16x8(&dos[16 * qt + lr][32 * kc + 8 * g]);
+        sc[qt] = mfma(qa, kf[kc], sc[qt]);
+        dp[qt] = mfma(da, vf[kc], dp[qt]);
+      }
+    }
+    // P = exp(S*scale - lse), dS = P (dP - delta); packed per 32-query step.
+    bf16x8 pb[2], sb[2];
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qi = 16 * qt + 4 * g + r;
+        const int qq = qbase + qi;
+        float p = exp2f(sc[qt][r] * a.scale_log2 - lse_s[qi]);
+        if (qq < key) p = 0.f;
+        const float ds = p * (dp[qt][r] - del_s[qi]);
+        pb[qt >> 1][4 * (qt & 1) + r] = static_cast<__bf16>(p);
+        sb[qt >> 1][4 * (qt & 1) + r] = static_cast<__bf16>(ds);
+      }
+    }
+    // dV^T += dO^T P, dK^T += Q^T dS over the block's 64 queries.
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const bf16x8 ot = ld_bf16x8(&dot_s[16 * dt + lr][32 * k2 + 8 * g]);
+        const bf16x8 qtv = ld_bf16x8(&qt_s[16 * dt + lr][32 * k2 + 8 * g]);
+        dvt[dt] = mfma(ot, pb[k2], dvt[dt]);
+        dkt[dt] = mfma(qtv, sb[k2], dkt[dt]);
+      }
+    }
+  }
+  if (key >= s1) return;
+  __bf16* dkrow = a.dk + key * row_stride + h * VD;
+  __bf16* dvrow = a.dv + key * row_stride + h * VD;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    bf16x4 wk, wv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      wk[r] = static_cast<__bf16>(dkt[dt][r] * a.scale);
+      wv[r] = static_cast<__bf16>(dvt[dt][r]);
+    }
+    *reinterpret_cast<bf16x4*>(dkrow + 16 * dt + 4 * g) = wk;
+    *reinterpret_cast<bf16x4*>(dvrow + 16 * dt + 4 * g) = wv;
+  }
+}
+
+// dQ: workgroup = (128-query tile, head), wave w owns queries q0 + 32w .. +32.
+__global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
+  __shared__ __bf16 ks[VBN][KPAD];     // K rows of the key tile
+  __shared__ __bf16 vs[VBN][KPAD];     // V rows
+  __shared__ __bf16 kt_s[VD][VPAD];    // K^T (permuted key order)
+  const int task = blockIdx.x;
+  const int tile = task / a.H;
+  const int h = task - tile * a.H;
+  const int seq = a.tiles[2 * tile];
+  const int q0 = a.tiles[2 * tile + 1];
+  const int s0 = a.cu[seq], s1 = a.cu[seq + 1];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, lr = lane & 15;
+  const int64_t row_stride = static_cast<int64_t>(a.H) * VD;
+  const int qb = q0 + wave * 32;
+  bf16x8 qf[2][4], df[2][4];
+  float lse2[2], del[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qq = qb + 16 * qt + lr;
+    const bool ok = qq < s1;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      qf[qt][kc] = ok ? ld_bf16x8(a.q + qq * row_stride + h * VD + 32 * kc + 8 * g) : bf16x8{};
+      df[qt][kc] = ok ? ld_bf16x8(a.dout + qq * row_stride + h * VD + 32 * kc + 8 * g)
+                      : bf16x8{};
+    }
+    lse2[qt] = ok ? a.lse[static_cast<int64_t>(qq) * a.H + h] * kLog2e : __builtin_huge_valf();
+    del[qt] = ok ? a.delta[static_cast<int64_t>(qq) * a.H + h] : 0.f;
+  }
+  f32x4v dqt[8][2];   // dQ^T [d = 16 dt + 4g + r][q]
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) dqt[dt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  const __bf16* kh = a.k + h * VD;
+  const __bf16* vh = a.v + h * VD;
+  const int kv_end = (q0 + VBM < s1) ? q0 + VBM : s1;
+  const int n_kv = (kv_end - s0 + VBN - 1) / VBN;
+  Stage2 st;
+  load2(st, kh, vh, row_stride, s0, s1);
+  for (int it = 0; it < n_kv; ++it) {
+    const int kbase = s0 + it * VBN;
+    __syncthreads();
+    store2(st, ks, vs, kt_s, nullptr);
+    __syncthreads();
+    if (it + 1 < n_kv) load2(st, kh, vh, row_stride, kbase + VBN, s1);
+    if (kbase > qb + 31) continue;
+    // S^T = K Q^T and dP^T = V dO^T: C tiles [key = 16 kt + 4g + r][q].
+    f32x4v sc[4][2], dp[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        sc[kt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        dp[kt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const bf16x8 ka = ld_bf16x8(&ks[16 * kt + lr][32 * kc + 8 * g]);
+        const bf16x8 va = ld_bf16x8(&vs[16 * kt + lr][32 * kc + 8 * g]);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          sc[kt][qt] = mfma(ka, qf[qt][kc], sc[kt][qt]);
+          dp[kt][qt] = mfma(va, df[qt][kc], dp[kt][qt]);
+        }
+      }
+    }
+    bf16x8 sb[2][2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int qq = qb + 16 * qt + lr;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kk = kbase + 16 * kt + 4 * g + r;
+          float p = exp2f(sc[kt][qt][r] * a.scale_log2 - lse2[qt]);
+          if (kk > qq || kk >= s1) p = 0.f;
+          const float ds = p * (dp[kt][qt][r] - del[qt]);
+          sb[qt][kt >> 1][4 * (kt & 1) + r] = static_cast<__bf16>(ds);
+        }
+    }
+    // dQ^T += K^T dS^T.
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const bf16x8 kta = ld_bf16x8(&kt_s[16 * dt + lr][32 * k2 + 8 * g]);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) dqt[dt][qt] = mfma(kta, sb[qt][k2], dqt[dt][qt]);
+      }
+    }
+  }
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qq = qb + 16 * qt + lr;
+    if (qq >= s1) continue;
+    __bf16* row = a.dq + qq * row_stride + h * VD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      bf16x4 w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = static_cast<__bf16>(dqt[dt][qt][r] * a.scale);
+      *reinterpret_cast<bf16x4*>(row + 16 * dt + 4 * g) = w;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace tgx
+
+using namespace tgx;
+
+extern "C" int tgx_varlen_causal_tiles(const int32_t* cu_seqlens_host, int n_seq, int block,
+                                       int kind, int32_t* tiles_host, int64_t* n_tiles) {
+  TGX_REQUIRE(cu_seqlens_host && n_tiles && n_seq >= 0 && block > 0, "bad arguments");
+  TGX_REQUIRE(kind == 0 || kind == 1, "kind must be 0 (query tiles) or 1 (key tiles)");
+  const int block_q = block;
+  struct T {
+    int seq, q0;
+    int64_t work;
+  };
+  std::vector<T> list;
+  for (int b = 0; b < n_seq; ++b) {
+    const int s0 = cu_seqlens_host[b], s1 = cu_seqlens_host[b + 1];
+    TGX_REQUIRE(s1 >= s0 && s0 >= 0, "cu_seqlens must be non-decreasing from 0");
+    for (int q0 = s0; q0 < s1; q0 += block_q) {
+      const int end = q0 + block_q < s1 ? q0 + block_q : s1;
+      // Causal work of a query tile grows with its end; of a key tile, with
+      // the number of queries after it.
+      list.push_back(T{b, q0, static_cast<int64_t>(kind == 0 ? end - s0 : s1 - q0)});
+    }
+  }
+  // Heaviest tiles first, ties by position: a deterministic
+  // longest-processing-time order.
+  std::stable_sort(list.begin(), list.end(),
+                   [](const T& x, const T& y) { return x.work > y.work; });
+  if (tiles_host) {
+    for (size_t i = 0; i < list.size(); ++i) {
+      tiles_host[2 * i] = list[i].seq;
+      tiles_host[2 * i + 1] = list[i].q0;
+    }
+  }
+  *n_tiles = static_cast<int64_t>(list.size());
+  return TGX_OK;
+}
+
+extern "C" int tgx_varlen_causal_fwd(const int32_t* cu_seqlens_dev, const int32_t* tiles_dev,
+                                     int64_t n_tiles, const void* q, const void* k,
+                                     const void* v, float scale, void* out, float* lse,
+                                     int64_t total_tokens, int H, int D, void* stream) {
+  if (D != VD) {
+    set_error("varlen causal attention supports head_dim 128 (got %d)", D);
+    return TGX_UNSUPPORTED;
+  }
+  TGX_REQUIRE(H > 0 && n_tiles >= 0 && total_tokens >= 0, "bad sizes");
+  TGX_REQUIRE(total_tokens * H * VD < (int64_t{1} << 31), "tensor too large for 32-bit offsets");
+  if (n_tiles == 0) return TGX_OK;
+  TGX_REQUIRE(cu_seqlens_dev && tiles_dev && q && k && v && out && lse, "null pointer");
+  TGX_REQUIRE(n_tiles * H < (int64_t{1} << 31), "too many tiles");
+  hipStream_t s = as_stream(stream);
+  VarlenFwdArgs a{cu_seqlens_dev, tiles_dev, static_cast<int>(n_tiles), H,
+                  static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
+                  static_cast<const __bf16*>(v), static_cast<__bf16*>(out), lse,
+                  scale * kLog2e};
+  TGX_PROFILE("varlen_fwd_kernel", s);
+  varlen_fwd_kernel<<<static_cast<unsigned>(n_tiles * H), 256, 0, s>>>(a);
+  TGX_LAUNCHED("varlen_fwd_kernel");
+  return TGX_OK;
+}
+
+extern "C" int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_t* q_tiles_dev,
+                                     int64_t n_q_tiles, const int32_t* k_tiles_dev,
+                                     int64_t n_k_tiles, const void* q, const void* k,
+                                     const void* v, const void* out, const float* lse,
+                                     const void* dout, float scale, void* dq, void* dk, void* dv,
+                                     float* delta, int64_t total_tokens, int H, int D,
+                                     void* stream) {
+  if (D != VD) {
+    set_error("varlen causal attention supports head_dim 128 (got %d)", D);
+    return TGX_UNSUPPORTED;
+  }
+  TGX_REQUIRE(H > 0 && n_q_tiles >= 0 && n_k_tiles >= 0 && total_tokens >= 0, "bad sizes");
+  TGX_REQUIRE(total_tokens * H * VD < (int64_t{1} << 31), "tensor too large for 32-bit offsets");
+  if (total_tokens == 0) return TGX_OK;
+  TGX_REQUIRE(cu_seqlens_dev && q_tiles_dev && k_tiles_dev && q && k && v && out && lse &&
+                  dout && dq && dk && dv && delta,
+              "null pointer");
+  hipStream_t s = as_stream(stream);
+  {
+    TGX_PROFILE("varlen_delta_kernel", s);
+    const int64_t waves = total_tokens * ((H + 3) / 4);
+    varlen_delta_kernel<<<ceil_div(waves, 4), 256, 0, s>>>(
+        static_cast<const __bf16*>(dout), static_cast<const __bf16*>(out), delta, total_tokens,
+        H);
+    TGX_LAUNCHED("varlen_delta_kernel");
+  }
+  VarlenBwdArgs a{cu_seqlens_dev, k_tiles_dev, static_cast<int>(n_k_tiles), H,
+                  static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
+                  static_cast<const __bf16*>(v), static_cast<const __bf16*>(dout), lse, delta,
+                  static_cast<__bf16*>(dq), static_cast<__bf16*>(dk), static_cast<__bf16*>(dv),
+                  scale, scale * kLog2e};
+  if (n_k_tiles > 0) {
+    TGX_PROFILE("varlen_dkdv_kernel", s);
+    varlen_dkdv_kernel<<<static_cast<unsigned>(n_k_tiles * H), 256, 0, s>>>(a);
+    TGX_LAUNCHED("varlen_dkdv_kernel");
+  }
+  a.tiles = q_tiles_dev;
+  a.n_tiles = static_cast<int>(n_q_tiles);
+  if (n_q_tiles > 0) {
+    TGX_PROFILE("varlen_dq_kernel", s);
+    varlen_dq_kernel<<<static_cast<unsigned>(n_q_tiles * H), 256, 0, s>>>(a);
+    TGX_LAUNCHED("varlen_dq_kernel");
+  }
+  return TGX_OK;
+}

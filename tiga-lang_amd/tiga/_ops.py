@@ -190,3 +190,41 @@ class DotAttnFunction(torch.autograd.Function):
                      dv.data_ptr(), _p(dbias), n_dst, n_src, H, D, ws.data_ptr(),
                      ws_bytes.value, _native.stream_of(qc))
         return dq, dk, dv, dbias, None, None
+
+
+class VarlenCausalFunction(torch.autograd.Function):
+    """Causal attention on a Graph.cu_seqlens relation: q/k/v [T, H, 128] bf16."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale: float, graph: Graph):
+        T, H, D = q.shape
+        qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+        cu, tiles, n = graph._varlen_tiles(0, 128)
+        out = torch.empty_like(qc)
+        lse = torch.empty((T, H), dtype=torch.float32, device=q.device)
+        _native.call("tgx_varlen_causal_fwd", cu.data_ptr(), tiles.data_ptr(), n,
+                     qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), float(scale), out.data_ptr(),
+                     lse.data_ptr(), T, H, D, _native.stream_of(q))
+        ctx.graph = graph
+        ctx.scale = float(scale)
+        ctx.save_for_backward(qc, kc, vc, out, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        qc, kc, vc, out, lse = ctx.saved_tensors
+        graph: Graph = ctx.graph
+        T, H, D = qc.shape
+        dout = dout.contiguous()
+        if dout.dtype != qc.dtype:
+            dout = dout.to(qc.dtype)
+        cu, qtiles, nq = graph._varlen_tiles(0, 128)
+        _, ktiles, nk = graph._varlen_tiles(1, 64)
+        dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+        delta = torch.empty((T, H), dtype=torch.float32, device=qc.device)
+        _native.call("tgx_varlen_causal_bwd", cu.data_ptr(), qtiles.data_ptr(), nq,
+                     ktiles.data_ptr(), nk, qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                     out.data_ptr(), lse.data_ptr(), dout.data_ptr(), ctx.scale, dq.data_ptr(),
+                     dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), T, H, D,
+                     _native.stream_of(qc))
+        return dq, dk, dv, None, None

@@ -244,6 +244,15 @@ class Graph:
         return cls(schema, cu_seqlens=cu_seqlens, causal=causal, device=cu_seqlens.device)
 
     @classmethod
+    def triangular(cls, n: int, *, device="cpu") -> "Graph":
+        """Lower-triangular (causal) relation on n positions: row i relates to
+        sources 0..i.  Kept implicit, as one causal cu_seqlens sequence."""
+        if not isinstance(n, int) or n < 0:
+            raise ValueError("n must be a non-negative integer")
+        return cls.cu_seqlens(torch.tensor([0, n], dtype=torch.int64, device=device),
+                              causal=True)
+
+    @classmethod
     def cat(cls, graphs) -> "Graph":
         blocks = list(graphs)
         if not blocks:
@@ -254,6 +263,15 @@ class Graph:
         device = blocks[0].device
         if any(str(block.device) != str(device) for block in blocks):
             raise ValueError("all blocks must share a device")
+        # Causal varlen blocks stay implicit: their cat is one cu_seqlens.
+        if all(b.is_varlen and b._causal and b._row_ptr is None for b in blocks):
+            parts = [torch.zeros(1, dtype=torch.int64, device=device)]
+            offset = 0
+            for b in blocks:
+                cu = b._cu_seqlens.to(torch.int64)
+                parts.append(cu[1:] + offset)
+                offset += int(cu[-1].item())
+            return cls.cu_seqlens(torch.cat(parts), causal=True)
         dtype = (torch.int64 if any(b.schema.index_dtype == torch.int64 for b in blocks)
                  else torch.int32)
         row_parts = [torch.zeros(1, device=device, dtype=dtype)]
@@ -352,6 +370,27 @@ class Graph:
         return "\n".join(lines)
 
     # ---- native device structures (built once per graph) -----------------
+    def _varlen_tiles(self, kind: int, block: int):
+        """(cu_seqlens int32 on device, tiles [n, 2] int32 on device, n) for the
+        varlen kernels; kind 0 = query tiles, 1 = key tiles."""
+        key = ("varlen", kind, block)
+        got = self._native_cache.get(key)
+        if got is None:
+            import numpy as np
+
+            cu_h = np.ascontiguousarray(self._cu_seqlens.cpu().numpy(), dtype=np.int32)
+            n = ctypes.c_int64()
+            _native.call("tgx_varlen_causal_tiles", cu_h.ctypes.data, cu_h.size - 1, block,
+                         kind, None, ctypes.byref(n))
+            tiles = np.zeros(2 * max(n.value, 1), dtype=np.int32)
+            _native.call("tgx_varlen_causal_tiles", cu_h.ctypes.data, cu_h.size - 1, block,
+                         kind, tiles.ctypes.data, ctypes.byref(n))
+            cu_d = torch.as_tensor(cu_h, device=self.device)
+            got = (cu_d, torch.as_tensor(tiles, device=self.device), n.value)
+            self._native_cache[key] = got
+        return got
+
+
     def _row_plan(self, wave_max: int = WAVE_MAX, chunk_edges: int = CHUNK_EDGES) -> RowPlanHandle:
         key = ("plan", wave_max, chunk_edges)
         handle = self._native_cache.get(key)

@@ -199,9 +199,21 @@ class MessagePassing(Kernel):
         if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
             return None
         _, H, D = q.shape
-        if D % 8 or H * D not in (128, 256, 512):
-            return None
         if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
+            return None
+        if graph.is_varlen:
+            if dot.bias_field is not None or not graph._causal or D != 128:
+                return None
+            if not (q.shape[0] == k.shape[0] == v.shape[0] == graph.schema.num_dst):
+                return None
+            _native.lib()
+            out = _ops.VarlenCausalFunction.apply(q, k, v, dot.scale, graph)
+            self._record_native(graph, "varlen-causal", ("tgx_varlen_causal_fwd",
+                                                         "tgx_varlen_causal_bwd"),
+                                "MFMA 16x16x32 bf16 flash tiles over cu_seqlens (implicit "
+                                "causal relation); atomic-free dK/dV and dQ passes")
+            return out
+        if D % 8 or H * D not in (128, 256, 512):
             return None
         bias = None
         if dot.bias_field is not None:
