@@ -16,9 +16,14 @@
 // The forward computes S^T = K Q^T, so each lane's accumulators hold 4 keys of
 // one query; two 16-key tiles together are exactly the B operand of
 // O^T = V^T P^T under the key order {4g..4g+3, 16+4g..16+4g+3}, so P never
-// leaves registers.  V^T is staged in LDS (transposed while staging) in that
-// same key order, K is staged row-major; both double-buffered with the next
-// tile's global loads in flight during the current tile's MFMAs.
+// leaves registers.  Operands needed "down a column" (V^T here, Q^T/dO^T/K^T
+// in the backward) are read from row-major LDS tiles with ds_read_b64_tr_b16:
+// inside each 16-lane group it returns lane i, element j = F[4j + i/4][i % 4]
+// of the 4 x 16-bit values F[lane][0..3] the group's lanes address, so lane i'
+// addressing X[r0 + i'/4][c0 + 4 (i' % 4)] receives X[r0 + j][c0 + i]; two such
+// reads build the permuted 8-key A fragment.  Tiles are staged row-major with
+// 16-byte writes, double-buffered, with the next tile's global loads in
+// flight during the current tile's MFMAs.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -34,12 +39,15 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int VD = 128;    // head dim
 constexpr int VBM = 128;   // queries per workgroup (4 waves x 32)
 constexpr int VBN = 64;    // keys per iteration
-constexpr int KPAD = 136;  // K row stride in LDS (bf16): 272 B, conflict-free 16 B reads
-constexpr int VPAD = 72;   // V^T row stride in LDS (bf16): 144 B, 16 B aligned rows
+constexpr int KPAD = 136;  // row stride for 16 B row-fragment reads (bf16): 272 B
+constexpr int TPAD = 144;  // row stride for transposing reads (bf16): 288 B
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -87,34 +95,36 @@ __device__ __forceinline__ void load_kv(KvStage& st, const __bf16* kb, const __b
   }
 }
 
-// V^T key order inside a 32-key block: position p = 8g + j holds key
-// (j < 4 ? 4g + j : 16 + 4g + j - 4).  Inverse: key kk -> position.
-__device__ __forceinline__ int vt_pos(int key) {
-  const int blk = key & ~31;
-  const int kk = key & 31;
-  const int hi = kk >> 4;        // 0: keys 0..15, 1: keys 16..31
-  const int g = (kk & 15) >> 2;  // 0..3
-  const int j = (kk & 3) + 4 * hi;
-  return blk + 8 * g + j;
-}
-
 __device__ __forceinline__ void store_kv(const KvStage& st, __bf16 (*ks)[KPAD],
-                                         __bf16 (*vt)[VPAD]) {
+                                         __bf16 (*vs)[TPAD]) {
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int idx = threadIdx.x + 256 * it;
     const int key = idx >> 4;
     const int dc = idx & 15;
     *reinterpret_cast<bf16x8*>(&ks[key][dc * 8]) = st.k[it];
-    const int pos = vt_pos(key);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) vt[dc * 8 + j][pos] = st.v[it][j];
+    *reinterpret_cast<bf16x8*>(&vs[key][dc * 8]) = st.v[it];
   }
+}
+
+// A fragment of X^T (rows of X are the contraction index) from a row-major
+// LDS tile X[row][col] with row stride TPAD: lane (lr, g) receives
+// X[r0 + 4g + j][c0 + lr] for j < 4 and X[r0 + 16 + 4g + j - 4][c0 + lr] for
+// j >= 4, i.e. 8 rows of one column in the permuted order of the B operand.
+__device__ __forceinline__ bf16x8 tr_frag(__bf16 (*x)[TPAD], int r0, int c0, int lr, int g) {
+  const __bf16* p = &x[r0 + 4 * g + (lr >> 2)][c0 + 4 * (lr & 3)];
+  const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 16 * TPAD));
+  // Assemble at dword granularity (elements 0-3 from a, 4-7 from b).
+  const u32x2 aw = __builtin_bit_cast(u32x2, a);
+  const u32x2 bw = __builtin_bit_cast(u32x2, b);
+  const u32x4 w = {aw[0], aw[1], bw[0], bw[1]};
+  return __builtin_bit_cast(bf16x8, w);
 }
 
 __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
   __shared__ __bf16 ks[2][VBN][KPAD];
-  __shared__ __bf16 vt[2][VD][VPAD];
+  __shared__ __bf16 vs[2][VBN][TPAD];
   const int task = blockIdx.x;
   const int tile = task / a.H;
   const int h = task - tile * a.H;
@@ -152,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
 
   KvStage stage;
   load_kv(stage, kh, vh, row_stride, s0, s1);
-  store_kv(stage, ks[0], vt[0]);
+  store_kv(stage, ks[0], vs[0]);
   for (int it = 0; it < n_kv; ++it) {
     __syncthreads();
     const int buf = it & 1;
@@ -229,13 +239,13 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
     for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const bf16x8 vf = ld_bf16x8(&vt[buf][16 * dt + lr][32 * k2 + 8 * g]);
+        const bf16x8 vf = tr_frag(vs[buf], 32 * k2, 16 * dt, lr, g);
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) o[dt][qt] = mfma(vf, pf[qt][k2], o[dt][qt]);
       }
     }
     }
-    if (more) store_kv(stage, ks[buf ^ 1], vt[buf ^ 1]);
+    if (more) store_kv(stage, ks[buf ^ 1], vs[buf ^ 1]);
   }
 
   // Finalize: l summed over the 4 lane groups, O = O^T / l, natural-log lse.
@@ -338,35 +348,23 @@ __device__ __forceinline__ void load2(Stage2& st, const __bf16* xa, const __bf16
   }
 }
 
-// Row-major copy of `a` into ra, and transposed (permuted row order) copies
-// of a and b into ta and tb (any may be null).
-__device__ __forceinline__ void store2(const Stage2& st, __bf16 (*ra)[KPAD], __bf16 (*rb)[KPAD],
-                                       __bf16 (*ta)[VPAD], __bf16 (*tb)[VPAD]) {
+// Row-major copies of the two staged tensors (either may be skipped).
+template <int SA, int SB>
+__device__ __forceinline__ void store2(const Stage2& st, __bf16 (*ra)[SA], __bf16 (*rb)[SB]) {
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int idx = threadIdx.x + 256 * it;
     const int row = idx >> 4;
     const int dc = idx & 15;
-    if (ra) *reinterpret_cast<bf16x8*>(&ra[row][dc * 8]) = st.a[it];
-    if (rb) *reinterpret_cast<bf16x8*>(&rb[row][dc * 8]) = st.b[it];
-    const int pos = vt_pos(row);
-    if (ta) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ta[dc * 8 + j][pos] = st.a[it][j];
-    }
-    if (tb) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) tb[dc * 8 + j][pos] = st.b[it][j];
-    }
+    *reinterpret_cast<bf16x8*>(&ra[row][dc * 8]) = st.a[it];
+    *reinterpret_cast<bf16x8*>(&rb[row][dc * 8]) = st.b[it];
   }
 }
 
 // dK/dV: workgroup = (64-key tile, head); wave w owns keys k0 + 16w .. +16.
 __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
-  __shared__ __bf16 qs[VBN][KPAD];    // Q rows of the query block
-  __shared__ __bf16 dos[VBN][KPAD];   // dO rows
-  __shared__ __bf16 qt_s[VD][VPAD];   // Q^T (permuted query order)
-  __shared__ __bf16 dot_s[VD][VPAD];  // dO^T
+  __shared__ __bf16 qs[VBN][TPAD];    // Q rows of the query block
+  __shared__ __bf16 dos[VBN][TPAD];   // dO rows
   __shared__ float lse_s[VBN], del_s[VBN];
   const int task = blockIdx.x;
   const int tile = task / a.H;
@@ -406,7 +404,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
   for (int ib = 0; ib < n_qb; ++ib) {
     const int qbase = k0 + ib * VBN;
     __syncthreads();   // previous block's LDS reads are done
-    store2(st, qs, dos, qt_s, dot_s);
+    store2<TPAD, TPAD>(st, qs, dos);
     if (threadIdx.x < VBN) {
       const int qq = qbase + threadIdx.x;
       lse_s[threadIdx.x] = qq < s1 ? a.lse[static_cast<int64_t>(qq) * a.H + h] * kLog2e
@@ -456,8 +454,8 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
     for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const bf16x8 ot = ld_bf16x8(&dot_s[16 * dt + lr][32 * k2 + 8 * g]);
-        const bf16x8 qtv = ld_bf16x8(&qt_s[16 * dt + lr][32 * k2 + 8 * g]);
+        const bf16x8 ot = tr_frag(dos, 32 * k2, 16 * dt, lr, g);
+        const bf16x8 qtv = tr_frag(qs, 32 * k2, 16 * dt, lr, g);
         dvt[dt] = mfma(ot, pb[k2], dvt[dt]);
         dkt[dt] = mfma(qtv, sb[k2], dkt[dt]);
       }
@@ -481,9 +479,8 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
 
 // dQ: workgroup = (128-query tile, head), wave w owns queries q0 + 32w .. +32.
 __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
-  __shared__ __bf16 ks[VBN][KPAD];     // K rows of the key tile
+  __shared__ __bf16 ks[VBN][TPAD];     // K rows of the key tile
   __shared__ __bf16 vs[VBN][KPAD];     // V rows
-  __shared__ __bf16 kt_s[VD][VPAD];    // K^T (permuted key order)
   const int task = blockIdx.x;
   const int tile = task / a.H;
   const int h = task - tile * a.H;
@@ -524,7 +521,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
   for (int it = 0; it < n_kv; ++it) {
     const int kbase = s0 + it * VBN;
     __syncthreads();
-    store2(st, ks, vs, kt_s, nullptr);
+    store2<TPAD, KPAD>(st, ks, vs);
     __syncthreads();
     if (it + 1 < n_kv) load2(st, kh, vh, row_stride, kbase + VBN, s1);
     if (kbase > qb + 31) continue;
@@ -570,7 +567,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
     for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const bf16x8 kta = ld_bf16x8(&kt_s[16 * dt + lr][32 * k2 + 8 * g]);
+        const bf16x8 kta = tr_frag(ks, 32 * k2, 16 * dt, lr, g);
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) dqt[dt][qt] = mfma(kta, sb[qt][k2], dqt[dt][qt]);
       }
