@@ -46,8 +46,11 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 constexpr int VD = 128;    // head dim
 constexpr int VBM = 128;   // queries per workgroup (4 waves x 32)
 constexpr int VBN = 64;    // keys per iteration
-constexpr int KPAD = 136;  // row stride for 16 B row-fragment reads (bf16): 272 B
-constexpr int TPAD = 144;  // row stride for transposing reads (bf16): 288 B
+// LDS row stride (bf16) of every staged tile: 288 B rows keep both the 16 B
+// row-fragment reads and the transposing 8 B reads free of bank conflicts
+// (measured: SQ_LDS_BANK_CONFLICT = 0).
+constexpr int TPAD = 144;
+constexpr int KPAD = TPAD;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -525,42 +528,39 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
     __syncthreads();
     if (it + 1 < n_kv) load2(st, kh, vh, row_stride, kbase + VBN, s1);
     if (kbase > qb + 31) continue;
-    // S^T = K Q^T and dP^T = V dO^T: C tiles [key = 16 kt + 4g + r][q].
-    f32x4v sc[4][2], dp[4][2];
+    // S^T = K Q^T and dP^T = V dO^T one 16-key subtile at a time (C tiles
+    // [key = 16 kt + 4g + r][q]), turned straight into dS^T fragments.
+    bf16x8 sb[2][2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < 4; ++kt) {
+      f32x4v sc[2], dp[2];
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        sc[kt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
-        dp[kt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        sc[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        dp[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kc = 0; kc < 4; ++kc) {
         const bf16x8 ka = ld_bf16x8(&ks[16 * kt + lr][32 * kc + 8 * g]);
         const bf16x8 va = ld_bf16x8(&vs[16 * kt + lr][32 * kc + 8 * g]);
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-          sc[kt][qt] = mfma(ka, qf[qt][kc], sc[kt][qt]);
-          dp[kt][qt] = mfma(va, df[qt][kc], dp[kt][qt]);
+          sc[qt] = mfma(ka, qf[qt][kc], sc[qt]);
+          dp[qt] = mfma(va, df[qt][kc], dp[qt]);
         }
       }
-    }
-    bf16x8 sb[2][2];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const int qq = qb + 16 * qt + lr;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int qt = 0; qt < 2; ++qt) {
+        const int qq = qb + 16 * qt + lr;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int kk = kbase + 16 * kt + 4 * g + r;
-          float p = exp2f(sc[kt][qt][r] * a.scale_log2 - lse2[qt]);
+          float p = exp2f(sc[qt][r] * a.scale_log2 - lse2[qt]);
           if (kk > qq || kk >= s1) p = 0.f;
-          const float ds = p * (dp[kt][qt][r] - del[qt]);
+          const float ds = p * (dp[qt][r] - del[qt]);
           sb[qt][kt >> 1][4 * (kt & 1) + r] = static_cast<__bf16>(ds);
         }
+      }
     }
     // dQ^T += K^T dS^T.
 #pragma unroll
