@@ -19,6 +19,10 @@
  *     (transposed CSR, permutations, plans) are int32.
  *   - CSR is destination-row: row i lists the sources of destination i
  *     (reference Graph.from_csr, python/tiga/interop/torch/graph.py:153-190).
+ *   - kernels trust the CSR: row_ptr must be monotonic from 0 to n_edges and
+ *     every col_idx value must lie in [0, n_src); gathers are not
+ *     bounds-checked on the device (the Python front end checks once per
+ *     graph before the first launch, tiga/graph.py Graph._kernel_csr).
  */
 #ifndef TGX_H_
 #define TGX_H_

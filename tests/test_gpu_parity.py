@@ -313,3 +313,18 @@ def test_dot_hub_row_split_matches_unsplit():
     f = lambda t: t.detach().float().cpu().numpy()
     e_out, _ = ref.dot_fwd(rp, col, f(q), f(k), f(v), 0.125)
     assert rel_err(f(out), e_out) <= RTOL_BF16
+
+
+
+def test_mixed_index_dtypes_and_invalid_columns_fail_closed():
+    rp = np.array([0, 2, 3, 5])
+    col = np.array([0, 2, 1, 0, 1])
+    x = torch.tensor([1.0, 2.0, 3.0], device=DEV)
+    w = torch.tensor([2.0, 3.0, 4.0, 5.0, 6.0], device=DEV)
+    mixed = tg.Graph.from_csr(to_dev(rp, torch.int64), to_dev(col, torch.int32), num_src=3)
+    out = WeightedSum()(graph=mixed, src={"x": x}, dst={}, edge={"weight": w})
+    assert out.tolist() == [11.0, 8.0, 17.0]
+    bad = tg.Graph.from_csr(to_dev(rp, torch.int64), to_dev([0, 2, 1, 0, 9], torch.int64),
+                            num_src=3, validate="basic")
+    with pytest.raises(ValueError, match="out-of-range"):
+        WeightedSum()(graph=bad, src={"x": x}, dst={}, edge={"weight": w})

@@ -229,3 +229,18 @@ def test_block_prune_threshold_rejected_on_csr():
     graph = tg.Graph.from_csr(torch.tensor([0, 1]), torch.tensor([0]), num_src=1)
     with pytest.raises(NotImplementedError):
         Pruned()(graph=graph, src={"s": torch.ones(1), "v": torch.ones(1)}, dst={})
+
+
+def test_kernel_csr_unifies_dtypes_and_rejects_bad_columns():
+    rp = torch.tensor([0, 2, 3, 5], dtype=torch.int64)
+    g = tg.Graph.from_csr(rp, torch.tensor([0, 2, 1, 0, 1], dtype=torch.int32), num_src=3)
+    r, c = g._kernel_csr()
+    assert r.dtype == c.dtype == torch.int64 and c.tolist() == [0, 2, 1, 0, 1]
+    for col, msg in (([0, 2, 1, 0, 3], "out-of-range"), ([0, -1, 1, 0, 1], "out-of-range")):
+        bad = tg.Graph.from_csr(rp, torch.tensor(col), num_src=3)
+        with pytest.raises(ValueError, match=msg):
+            bad._kernel_csr()
+    bad_rp = tg.Graph.from_csr(torch.tensor([0, 3, 2, 5]), torch.tensor([0, 2, 1, 0, 1]),
+                               num_src=3)
+    with pytest.raises(ValueError, match="monotonic"):
+        bad_rp._kernel_csr()

@@ -33,7 +33,7 @@ class CsrSumFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, w: torch.Tensor | None, graph: Graph):
-        row_ptr, col_idx = graph.resolve_csr()
+        row_ptr, col_idx = graph._kernel_csr()
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
         feat_shape = tuple(x.shape[1:])
         F = 1
@@ -85,7 +85,7 @@ class GatFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h: torch.Tensor, a_src: torch.Tensor, a_dst: torch.Tensor,
                 slope: float, graph: Graph):
-        row_ptr, col_idx = graph.resolve_csr()
+        row_ptr, col_idx = graph._kernel_csr()
         N, H, D = h.shape
         hc = h.contiguous()
         asc = a_src.reshape(H, D).contiguous()
@@ -108,7 +108,7 @@ class GatFunction(torch.autograd.Function):
     def backward(ctx, dout: torch.Tensor):
         hc, asc, adc, out, ns = ctx.saved_tensors
         graph: Graph = ctx.graph
-        row_ptr, col_idx = graph.resolve_csr()
+        row_ptr, col_idx = graph._kernel_csr()
         N, H, D = hc.shape
         E = graph.num_edges
         dout = dout.contiguous()
@@ -140,7 +140,7 @@ class DotAttnFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, bias, scale: float, graph: Graph):
-        row_ptr, col_idx = graph.resolve_csr()
+        row_ptr, col_idx = graph._kernel_csr()
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
         _, H, D = q.shape
         qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
@@ -163,7 +163,7 @@ class DotAttnFunction(torch.autograd.Function):
     def backward(ctx, dout):
         qc, kc, vc, bc, out, ml = ctx.saved_tensors
         graph: Graph = ctx.graph
-        row_ptr, col_idx = graph.resolve_csr()
+        row_ptr, col_idx = graph._kernel_csr()
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
         _, H, D = qc.shape
         E = graph.num_edges

@@ -370,6 +370,38 @@ class Graph:
         return "\n".join(lines)
 
     # ---- native device structures (built once per graph) -----------------
+    def _kernel_csr(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(row_ptr, col_idx) as the HIP kernels read them: one index dtype
+        for both arrays, values checked once per graph.
+
+        A kernel that gathered through an out-of-range column id would read
+        outside the source table, so the first native use of a graph checks
+        what ``validate="basic"`` leaves unchecked (one host sync, cached).
+        """
+        got = self._native_cache.get("csr")
+        if got is None:
+            row_ptr, col_idx = self.resolve_csr()
+            if col_idx.dtype != row_ptr.dtype:
+                col_idx = col_idx.to(row_ptr.dtype)
+            E = col_idx.numel()
+            checks = [row_ptr[0], row_ptr[-1]]
+            if self._schema.num_dst:
+                checks.append((row_ptr[1:] < row_ptr[:-1]).any().to(row_ptr.dtype))
+            if E:
+                checks += [col_idx.min(), col_idx.max()]
+            vals = torch.stack([c.to(torch.int64) for c in checks]).cpu().tolist()
+            if vals[0] != 0 or vals[1] != E:
+                raise ValueError("row_ptr must start at 0 and end at the number of edges")
+            if self._schema.num_dst and vals[2]:
+                raise ValueError("row_ptr must be monotonic")
+            if E and (vals[-2] < 0 or vals[-1] >= self._schema.num_src):
+                raise ValueError("col_idx contains an out-of-range source index")
+            if E >= (1 << 31) or max(self._schema.num_src, self._schema.num_dst) >= (1 << 31):
+                raise ValueError("the HIP provider supports fewer than 2**31 edges and nodes")
+            got = (row_ptr, col_idx)
+            self._native_cache["csr"] = got
+        return got
+
     def _varlen_tiles(self, kind: int, block: int):
         """(cu_seqlens int32 on device, tiles [n, 2] int32 on device, n) for the
         varlen kernels; kind 0 = query tiles, 1 = key tiles."""
@@ -395,7 +427,7 @@ class Graph:
         key = ("plan", wave_max, chunk_edges)
         handle = self._native_cache.get(key)
         if handle is None:
-            row_ptr, _ = self.resolve_csr()
+            row_ptr, _ = self._kernel_csr()
             handle = build_row_plan(row_ptr, self._schema.num_dst, wave_max=wave_max,
                                     chunk_edges=chunk_edges)
             self._native_cache[key] = handle
@@ -405,7 +437,7 @@ class Graph:
         key = ("transpose", wave_max, chunk_edges)
         t = self._native_cache.get(key)
         if t is None:
-            row_ptr, col_idx = self.resolve_csr()
+            row_ptr, col_idx = self._kernel_csr()
             row_ptr_t, col_t, perm, inv_perm = build_transpose(
                 row_ptr, col_idx, self._schema.num_dst, self._schema.num_src)
             plan = build_row_plan(row_ptr_t, self._schema.num_src, wave_max=wave_max,
