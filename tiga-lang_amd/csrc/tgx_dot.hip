@@ -492,10 +492,11 @@ bool dot_shape(int H, int D, DotShape* s) {
   X(16, 16) X(16, 8) X(16, 4) X(16, 2) X(16, 1)
 
 // Loads in flight per lane group (each covers a k and a v row, or a q and a
-// dout row): 2 measured best on R-MAT scale 21 (3: +1%, 4: +2%, 6: +8%).
+// dout row).  For H*D = 256 (two edges per wave-load) 2 measured best on
+// R-MAT scale 21, H=4, D=64 (3: +1%, 4: +2%, 6: +8% in the source pass).
 template <int G>
 constexpr int dot_unroll() {
-  return (kWave / G) >= 4 ? 1 : 2;
+  return 2;
 }
 
 template <typename I, int G, int HL>
