@@ -376,6 +376,7 @@ def run_c3c4(args):
     out = fwd()
     out.backward(dout, retain_graph=True)
     graph._transposed()
+    setup = setup_times(graph, N)
     deg = (row_ptr[1:] - row_ptr[:-1])
     stats = {"max_in_degree": int(deg.max()), "empty_rows": int((deg == 0).sum())}
     for _ in range(args.warmup):
@@ -422,7 +423,47 @@ def run_c3c4(args):
         "kernels": {kk: {"launches": n, "avg_ms": t / n,
                          "gbs": (bytes_per[kk] / (t / n * 1e-3) / 1e9) if kk in bytes_per else None}
                     for kk, (n, t) in sorted(timer.totals.items())},
+        "setup_ms": setup,
     }
+
+
+def setup_times(graph, N, reps=3):
+    """One-off per-graph work, timed apart from the steps: building the CSR
+    from edge lists on the device (this library vs the Torch ops the
+    reference's Graph.from_coo runs, interop/torch/graph.py:219-227), the
+    stable transpose, and the degree-binned row plan."""
+    import torch
+
+    from tiga.graph import build_coo_csr, build_row_plan, build_transpose
+
+    row_ptr, col = graph._kernel_csr()
+    dst = graph.destination_index()
+
+    def torch_coo():
+        order = torch.argsort(dst, stable=True)
+        c = col[order]
+        counts = torch.bincount(dst, minlength=N)
+        rp = torch.empty(N + 1, dtype=dst.dtype, device=dst.device)
+        rp[0] = 0
+        torch.cumsum(counts, dim=0, out=rp[1:])
+        return rp, c
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / reps
+
+    rp_n, col_n = build_coo_csr(col, dst, N)
+    rp_t, col_t = torch_coo()
+    assert torch.equal(rp_n.cpu(), rp_t.cpu()) and torch.equal(col_n.cpu(), col_t.cpu())
+    return {"from_coo_device": timed(lambda: build_coo_csr(col, dst, N)),
+            "from_coo_torch_ops": timed(torch_coo),
+            "transpose": timed(lambda: build_transpose(row_ptr, col, N, N)),
+            "row_plan": timed(lambda: build_row_plan(row_ptr, N))}
 
 
 def run_c5(args):

@@ -82,6 +82,43 @@ int tgx_csr_transpose(const void* row_ptr_dev, const void* col_dev, int idx_bits
                       int32_t* perm_dev, int32_t* inv_perm_dev,
                       void* workspace_dev, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes needed by tgx_coo_to_csr. */
+int tgx_coo_to_csr_workspace(int64_t n_src, int64_t n_dst, int64_t n_edges,
+                             size_t* bytes);
+
+/* Destination-row CSR from edge lists (src[e] -> dst[e]).
+ * Replaces Graph.from_coo's construction step (interop/torch/graph.py:
+ * 219-227: argsort(dst, stable=True), col_idx = src[order],
+ * row_ptr = [0, cumsum(bincount(dst, minlength=num_dst))]); the range checks
+ * of :210-218 stay with the caller.
+ *   row_ptr_dev [n_dst+1] in dst's width (dst_bits)
+ *   col_dev     [n_edges] in src's width (src_bits): src in stable dst order
+ *   perm_dev    [n_edges] int32: argsort(dst, stable=True); may be NULL
+ * Every dst must lie in [0, n_dst).  Supports n_edges, n_dst < 2^31.
+ * Deterministic: output is bit-identical across runs. */
+int tgx_coo_to_csr(const void* src_dev, int src_bits, const void* dst_dev,
+                   int dst_bits, int64_t n_src, int64_t n_dst, int64_t n_edges,
+                   void* row_ptr_dev, void* col_dev, int32_t* perm_dev,
+                   void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes needed by tgx_varlen_csr. */
+int tgx_varlen_csr_workspace(int64_t n_seq, size_t* bytes);
+
+/* Materialized block-diagonal varlen relation.  Replaces the CSR build of
+ * Graph.cu_seqlens (interop/torch/graph.py:260-294): position i of sequence
+ * k (cu_seqlens[k] <= i < cu_seqlens[k+1]) relates to sources
+ * cu_seqlens[k]..i when causal != 0, else to its whole sequence.
+ *   cu_seqlens_dev [n_seq+1] (idx_bits), starting at 0, non-decreasing,
+ *                  ending at total
+ *   row_ptr_dev    [total+1] (idx_bits), col_dev [n_edges] (idx_bits)
+ * n_edges must equal the relation's edge count (sum of L(L+1)/2 causal, L*L
+ * otherwise; checked on the device, one stream synchronisation) and be
+ * < 2^31. */
+int tgx_varlen_csr(const void* cu_seqlens_dev, int idx_bits, int64_t n_seq,
+                   int64_t total, int64_t n_edges, int causal, void* row_ptr_dev,
+                   void* col_dev, void* workspace_dev, size_t workspace_bytes,
+                   void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Row partition / load balancing                                            */
 /* ------------------------------------------------------------------------ */

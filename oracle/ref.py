@@ -63,7 +63,13 @@ def transpose(row_ptr, col_idx, num_src):
 
 
 def from_coo(src, dst, num_src=None, num_dst=None):
-    """Graph.from_coo (interop/torch/graph.py:193-231)."""
+    """Graph.from_coo (interop/torch/graph.py:193-231): stable argsort of dst,
+    col_idx = src[order], row_ptr = [0, cumsum(bincount(dst))].
+
+    Pinned by: brute force (per destination, edges in input order) and the
+    round trip from_coo(destination_index, col_idx) == the CSR it came from
+    (tests/test_oracle.py).
+    """
     src = np.asarray(src, dtype=np.int64)
     dst = np.asarray(dst, dtype=np.int64)
     if num_src is None:

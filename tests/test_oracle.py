@@ -55,6 +55,26 @@ def test_transpose_brute_force_and_round_trip():
     assert rp2.tolist() == rp.tolist() and col2.tolist() == col.tolist()
 
 
+def test_from_coo_brute_force_and_round_trip():
+    rng = np.random.default_rng(2)
+    for n_src, n_dst, E in [(5, 7, 0), (9, 6, 40), (30, 25, 200)]:
+        src = rng.integers(0, n_src, E)
+        dst = rng.integers(0, n_dst, E)
+        rp, col, ns = ref.from_coo(src, dst, num_src=n_src, num_dst=n_dst)
+        exp_rp, exp_col = [0], []
+        for i in range(n_dst):
+            exp_col += [int(src[e]) for e in range(E) if dst[e] == i]
+            exp_rp.append(len(exp_col))
+        assert rp.tolist() == exp_rp and col.tolist() == exp_col and ns == n_src
+        # from_coo over a CSR's own edge list gives the CSR back.
+        rp2, col2, _ = ref.from_coo(col, ref.destination_index(rp), num_dst=n_dst)
+        assert rp2.tolist() == rp.tolist() and col2.tolist() == col.tolist()
+    # non-causal cu_seqlens relation equals the brute-force block-diagonal one
+    rp, col = ref.cu_seqlens_csr([0, 2, 2, 5], causal=False)
+    assert rp.tolist() == [0, 2, 4, 7, 10, 13]
+    assert col.tolist() == [0, 1, 0, 1, 2, 3, 4, 2, 3, 4, 2, 3, 4]
+
+
 def test_cu_seqlens_matches_cat_of_triangles():
     # Reference property: cat([triangular(L)]) == cu_seqlens(cumsum(L))
     # (tests/python/test_graph_constructors.py:56-110).

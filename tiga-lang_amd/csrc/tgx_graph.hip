@@ -227,20 +227,70 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
   }
 }
 
-// row_ptr_t[k+1] = (one past the last position holding key <= k).  Built from
-// run ends: fill missing keys with the previous run end.
+// out[k] for k in [0, n_keys] = number of sorted keys < k (lower bound), i.e.
+// the CSR row pointer of the rows the keys name.
+template <typename O>
 __global__ __launch_bounds__(kBlock) void run_end_fill_kernel(
-    const uint32_t* __restrict__ sorted_keys, int64_t n, int64_t n_src,
-    int32_t* __restrict__ row_ptr_t) {
-  // row_ptr_t[k] for k in [0, n_src]: number of keys < k = lower_bound(k).
+    const uint32_t* __restrict__ sorted_keys, int64_t n, int64_t n_keys,
+    O* __restrict__ row_ptr) {
   const int64_t k = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (k > n_src) return;
+  if (k > n_keys) return;
   int64_t lo = 0, hi = n;
   while (lo < hi) {
     int64_t mid = (lo + hi) >> 1;
     if (static_cast<int64_t>(sorted_keys[mid]) < k) lo = mid + 1; else hi = mid;
   }
-  row_ptr_t[k] = static_cast<int32_t>(lo);
+  row_ptr[k] = static_cast<O>(lo);
+}
+
+// col[i] = src[perm[i]]: the source id of each edge in destination order.
+template <typename S>
+__global__ __launch_bounds__(kBlock) void gather_src_kernel(
+    const int32_t* __restrict__ perm, const S* __restrict__ src, int64_t n,
+    S* __restrict__ col) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  col[i] = src[perm[i]];
+}
+
+// Varlen block-diagonal relation: sequence k owns positions [cu[k], cu[k+1]).
+template <typename I>
+__global__ __launch_bounds__(kBlock) void varlen_seq_edges_kernel(
+    const I* __restrict__ cu, int64_t n_seq, int causal, int32_t* __restrict__ out) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (k >= n_seq) return;
+  const int64_t len = ld_idx(cu, k + 1) - ld_idx(cu, k);
+  out[k] = static_cast<int32_t>(causal ? len * (len + 1) / 2 : len * len);
+}
+
+// One wave per position: row i of sequence k (start s, length L) relates to
+// sources s..i (causal) or s..s+L-1; its edges start at the sequence's first
+// edge plus the edges of the earlier rows of the same sequence.
+template <typename I>
+__global__ __launch_bounds__(kBlock) void varlen_rows_kernel(
+    const I* __restrict__ cu, int64_t n_seq, const int32_t* __restrict__ seq_edge0,
+    int causal, int64_t total, I* __restrict__ row_ptr, I* __restrict__ col) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) +
+                      threadIdx.x / kWave;
+  if (row >= total) return;
+  // Largest k < n_seq with cu[k] <= row (empty sequences share a start).
+  int64_t lo = 0, hi = n_seq - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (ld_idx(cu, mid) <= row) lo = mid; else hi = mid - 1;
+  }
+  const int64_t s = ld_idx(cu, lo);
+  const int64_t len = ld_idx(cu, lo + 1) - s;
+  const int64_t p = row - s;
+  if (p < 0 || p >= len) return;  // only when cu_seqlens is malformed
+  const int64_t start = static_cast<int64_t>(seq_edge0[lo]) +
+                        (causal ? p * (p + 1) / 2 : p * len);
+  const int64_t deg = causal ? p + 1 : len;
+  if (lane_id() == 0) {
+    row_ptr[row] = static_cast<I>(start);
+    if (row == total - 1) row_ptr[total] = static_cast<I>(start + deg);
+  }
+  for (int64_t j = lane_id(); j < deg; j += kWave) col[start + j] = static_cast<I>(s + j);
 }
 
 __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
@@ -361,27 +411,73 @@ extern "C" int tgx_destination_index(const void* row_ptr, int idx_bits, int64_t 
 
 namespace {
 
-struct TransposeLayout {
-  int64_t nblocks;
-  size_t bytes;
-};
+// Scratch of one stable sort of n keys: two key and two payload buffers, the
+// per-block digit histogram and its scan scratch.
+void carve_sort(Carve& c, int64_t n) {
+  const int64_t nblocks = ceil_div(n, kSortTile);
+  c.take<uint32_t>(n);
+  c.take<uint32_t>(n);
+  c.take<int32_t>(n);
+  c.take<int32_t>(n);
+  c.take<int32_t>(256 * nblocks);
+  c.take<int32_t>(scan_scratch_ints(256 * nblocks));
+}
 
-TransposeLayout transpose_layout(int64_t n_dst, int64_t n_src, int64_t n_edges) {
-  (void)n_src;
-  TransposeLayout L;
-  L.nblocks = ceil_div(n_edges, kSortTile);
+// Stable LSD radix sort (8-bit digits) of keys in [0, key_range) carrying the
+// element index.  Writes the sorting permutation to perm and returns the
+// buffer that holds the sorted keys.  Scratch is carved from c in the order
+// carve_sort lays it out.
+template <typename K>
+uint32_t* stable_sort_by_key(const K* keys, int64_t n, int64_t key_range, int32_t* perm,
+                             Carve& c, hipStream_t s, int* status) {
+  const int nb = static_cast<int>(ceil_div(n, kSortTile));
+  uint32_t* kbuf[2] = {c.take<uint32_t>(n), c.take<uint32_t>(n)};
+  int32_t* vbuf[2] = {c.take<int32_t>(n), c.take<int32_t>(n)};
+  const int64_t hist_n = 256 * static_cast<int64_t>(nb);
+  int32_t* hist = c.take<int32_t>(hist_n);
+  int32_t* scratch = c.take<int32_t>(scan_scratch_ints(hist_n));
+  int bits = 0;
+  while (bits < 32 && (static_cast<int64_t>(1) << bits) < key_range) ++bits;
+  const int passes = bits == 0 ? 1 : (bits + 7) / 8;
+  *status = TGX_OK;
+  for (int p = 0; p < passes; ++p) {
+    const int shift = 8 * p;
+    uint32_t* kout = kbuf[p % 2];
+    int32_t* vout = (p == passes - 1) ? perm : vbuf[p % 2];
+    if (p == 0)
+      radix_hist_kernel<K><<<nb, kBlock, 0, s>>>(keys, n, shift, nb, hist);
+    else
+      radix_hist_kernel<uint32_t><<<nb, kBlock, 0, s>>>(kbuf[(p - 1) % 2], n, shift, nb,
+                                                        hist);
+    if (hipGetLastError() != hipSuccess) {
+      set_error("radix_hist_kernel launch failed");
+      *status = TGX_INTERNAL;
+      return nullptr;
+    }
+    *status = scan_exclusive_i32(hist, hist, hist_n, nullptr, scratch, s);
+    if (*status != TGX_OK) return nullptr;
+    // The first pass reads the keys in place with the element index as
+    // payload; the last pass writes its payload straight into perm.
+    if (p == 0)
+      radix_scatter_kernel<K><<<nb, kBlock, 0, s>>>(keys, nullptr, n, shift, nb, hist,
+                                                    kout, vout);
+    else
+      radix_scatter_kernel<uint32_t><<<nb, kBlock, 0, s>>>(
+          kbuf[(p - 1) % 2], vbuf[(p - 1) % 2], n, shift, nb, hist, kout, vout);
+    if (hipGetLastError() != hipSuccess) {
+      set_error("radix_scatter_kernel launch failed");
+      *status = TGX_INTERNAL;
+      return nullptr;
+    }
+  }
+  return kbuf[(passes - 1) % 2];
+}
+
+size_t transpose_bytes(int64_t n_edges) {
   Carve c{nullptr, 0};
-  c.take<uint32_t>(n_edges);         // keys a
-  c.take<uint32_t>(n_edges);         // keys b
-  c.take<int32_t>(n_edges);          // vals a
-  c.take<int32_t>(n_edges);          // vals b
-  c.take<int32_t>(n_edges);          // destination row per edge
-  const int64_t hist = 256 * L.nblocks;
-  c.take<int32_t>(hist);             // digit histogram / offsets
-  c.take<int32_t>(scan_scratch_ints(hist));
-  (void)n_dst;
-  L.bytes = align_up(c.used);
-  return L;
+  carve_sort(c, n_edges);
+  c.take<int32_t>(n_edges);  // destination row per edge
+  return align_up(c.used);
 }
 
 }  // namespace
@@ -390,7 +486,7 @@ extern "C" int tgx_csr_transpose_workspace(int64_t n_dst, int64_t n_src,
                                            int64_t n_edges, size_t* bytes) {
   TGX_REQUIRE(bytes, "null bytes");
   TGX_REQUIRE(n_dst >= 0 && n_src >= 0 && n_edges >= 0, "negative size");
-  *bytes = transpose_layout(n_dst, n_src, n_edges).bytes;
+  *bytes = transpose_bytes(n_edges);
   return TGX_OK;
 }
 
@@ -399,49 +495,16 @@ static int transpose_impl(const I* row_ptr, const I* col, int64_t n_dst, int64_t
                           int64_t E, int32_t* row_ptr_t, int32_t* col_t,
                           int32_t* perm, int32_t* inv_perm, void* ws, size_t ws_bytes,
                           hipStream_t s) {
-  TransposeLayout L = transpose_layout(n_dst, n_src, E);
-  TGX_REQUIRE(ws_bytes >= L.bytes, "workspace too small: need %zu bytes", L.bytes);
+  const size_t need = transpose_bytes(E);
+  TGX_REQUIRE(ws_bytes >= need, "workspace too small: need %zu bytes", need);
   Carve c{static_cast<char*>(ws), ws_bytes};
-  uint32_t* ka = c.take<uint32_t>(E);
-  uint32_t* kb = c.take<uint32_t>(E);
-  int32_t* va = c.take<int32_t>(E);
-  int32_t* vb = c.take<int32_t>(E);
+  int st = TGX_OK;
+  const uint32_t* sorted = stable_sort_by_key(col, E, n_src, perm, c, s, &st);
+  if (st != TGX_OK) return st;
   int32_t* erow = c.take<int32_t>(E);
-  const int64_t hist_n = 256 * L.nblocks;
-  int32_t* hist = c.take<int32_t>(hist_n);
-  int32_t* scratch = c.take<int32_t>(scan_scratch_ints(hist_n));
-  int bits = 0;
-  while (bits < 32 && (static_cast<int64_t>(1) << bits) < n_src) ++bits;
-  const int passes = bits == 0 ? 1 : (bits + 7) / 8;
-  const int nb = static_cast<int>(L.nblocks);
-  uint32_t* kbuf[2] = {ka, kb};
-  int32_t* vbuf[2] = {va, vb};
-  for (int p = 0; p < passes; ++p) {
-    const int shift = 8 * p;
-    uint32_t* kout = kbuf[p % 2];
-    int32_t* vout = (p == passes - 1) ? perm : vbuf[p % 2];
-    if (p == 0)
-      radix_hist_kernel<I><<<nb, kBlock, 0, s>>>(col, E, shift, nb, hist);
-    else
-      radix_hist_kernel<uint32_t><<<nb, kBlock, 0, s>>>(kbuf[(p - 1) % 2], E, shift, nb,
-                                                        hist);
-    TGX_LAUNCHED("radix_hist_kernel");
-    int st = scan_exclusive_i32(hist, hist, hist_n, nullptr, scratch, s);
-    if (st != TGX_OK) return st;
-    // The first pass reads col_idx directly with the edge id as payload; the
-    // last pass writes its payload straight into perm.
-    if (p == 0)
-      radix_scatter_kernel<I><<<nb, kBlock, 0, s>>>(col, nullptr, E, shift, nb, hist,
-                                                    kout, vout);
-    else
-      radix_scatter_kernel<uint32_t><<<nb, kBlock, 0, s>>>(
-          kbuf[(p - 1) % 2], vbuf[(p - 1) % 2], E, shift, nb, hist, kout, vout);
-    TGX_LAUNCHED("radix_scatter_kernel");
-  }
-  ka = kbuf[(passes - 1) % 2];
-  // ka: sorted keys.  row_ptr_t = lower_bound of every key in [0, n_src].
-  run_end_fill_kernel<<<ceil_div(n_src + 1, kBlock), kBlock, 0, s>>>(ka, E, n_src,
-                                                                       row_ptr_t);
+  // row_ptr_t = lower bound of every source id in [0, n_src].
+  run_end_fill_kernel<int32_t><<<ceil_div(n_src + 1, kBlock), kBlock, 0, s>>>(
+      sorted, E, n_src, row_ptr_t);
   TGX_LAUNCHED("run_end_fill_kernel");
   destination_index_kernel<<<ceil_div(n_dst, kBlock / kWave), kBlock, 0, s>>>(
       row_ptr, n_dst, erow);
@@ -604,4 +667,147 @@ extern "C" int tgx_plan_split_chunks(const void* row_ptr, int idx_bits,
   TGX_HIP(hipStreamSynchronize(s));
   *n_chunks_host = total;
   return TGX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Graph builders.
+namespace {
+
+size_t coo_bytes(int64_t n_edges) {
+  Carve c{nullptr, 0};
+  carve_sort(c, n_edges);
+  c.take<int32_t>(n_edges);  // permutation when the caller does not want it
+  return align_up(c.used);
+}
+
+template <typename S, typename D>
+int coo_impl(const S* src, const D* dst, int64_t n_dst, int64_t E, D* row_ptr, S* col,
+             int32_t* perm, void* ws, size_t ws_bytes, hipStream_t s) {
+  const size_t need = coo_bytes(E);
+  TGX_REQUIRE(ws_bytes >= need, "workspace too small: need %zu bytes", need);
+  Carve c{static_cast<char*>(ws), ws_bytes};
+  int st = TGX_OK;
+  // The permutation buffer is carved after the sort scratch, so carve the
+  // sort first and take the fallback permutation from what follows.
+  Carve probe = c;
+  carve_sort(probe, E);
+  int32_t* own_perm = probe.take<int32_t>(E);
+  if (!perm) perm = own_perm;
+  const uint32_t* sorted = stable_sort_by_key(dst, E, n_dst, perm, c, s, &st);
+  if (st != TGX_OK) return st;
+  run_end_fill_kernel<D><<<ceil_div(n_dst + 1, kBlock), kBlock, 0, s>>>(sorted, E, n_dst,
+                                                                          row_ptr);
+  TGX_LAUNCHED("run_end_fill_kernel");
+  gather_src_kernel<S><<<ceil_div(E, kBlock), kBlock, 0, s>>>(perm, src, E, col);
+  TGX_LAUNCHED("gather_src_kernel");
+  return TGX_OK;
+}
+
+template <typename S>
+int coo_dispatch_dst(const S* src, const void* dst, int dst_bits, int64_t n_dst, int64_t E,
+                     void* row_ptr, void* col, int32_t* perm, void* ws, size_t ws_bytes,
+                     hipStream_t s) {
+  if (dst_bits == 32)
+    return coo_impl(src, static_cast<const int32_t*>(dst), n_dst, E,
+                    static_cast<int32_t*>(row_ptr), static_cast<S*>(col), perm, ws,
+                    ws_bytes, s);
+  return coo_impl(src, static_cast<const int64_t*>(dst), n_dst, E,
+                  static_cast<int64_t*>(row_ptr), static_cast<S*>(col), perm, ws, ws_bytes,
+                  s);
+}
+
+size_t varlen_csr_bytes(int64_t n_seq) {
+  Carve c{nullptr, 0};
+  c.take<int32_t>(n_seq + 1);
+  c.take<int32_t>(scan_scratch_ints(n_seq));
+  return align_up(c.used);
+}
+
+template <typename I>
+int varlen_csr_impl(const I* cu, int64_t n_seq, int64_t total, int64_t n_edges, int causal,
+                    I* row_ptr, I* col, void* ws, size_t ws_bytes, hipStream_t s) {
+  const size_t need = varlen_csr_bytes(n_seq);
+  TGX_REQUIRE(ws_bytes >= need, "workspace too small: need %zu bytes", need);
+  Carve c{static_cast<char*>(ws), ws_bytes};
+  int32_t* edge0 = c.take<int32_t>(n_seq + 1);
+  int32_t* scratch = c.take<int32_t>(scan_scratch_ints(n_seq));
+  varlen_seq_edges_kernel<I><<<ceil_div(n_seq, kBlock), kBlock, 0, s>>>(cu, n_seq, causal,
+                                                                         edge0);
+  TGX_LAUNCHED("varlen_seq_edges_kernel");
+  int st = scan_exclusive_i32(edge0, edge0, n_seq, edge0 + n_seq, scratch, s);
+  if (st != TGX_OK) return st;
+  int32_t got = 0;
+  TGX_HIP(hipMemcpyAsync(&got, edge0 + n_seq, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  TGX_HIP(hipStreamSynchronize(s));
+  TGX_REQUIRE(got == n_edges, "cu_seqlens describe %d edges, caller sized %lld", got,
+              static_cast<long long>(n_edges));
+  varlen_rows_kernel<I><<<ceil_div(total, kBlock / kWave), kBlock, 0, s>>>(
+      cu, n_seq, edge0, causal, total, row_ptr, col);
+  TGX_LAUNCHED("varlen_rows_kernel");
+  return TGX_OK;
+}
+
+}  // namespace
+
+extern "C" int tgx_coo_to_csr_workspace(int64_t n_src, int64_t n_dst, int64_t n_edges,
+                                        size_t* bytes) {
+  TGX_REQUIRE(bytes, "null bytes");
+  TGX_REQUIRE(n_src >= 0 && n_dst >= 0 && n_edges >= 0, "negative size");
+  *bytes = coo_bytes(n_edges);
+  return TGX_OK;
+}
+
+extern "C" int tgx_coo_to_csr(const void* src, int src_bits, const void* dst, int dst_bits,
+                              int64_t n_src, int64_t n_dst, int64_t n_edges, void* row_ptr,
+                              void* col, int32_t* perm, void* ws, size_t ws_bytes,
+                              void* stream) {
+  TGX_REQUIRE(src_bits == 32 || src_bits == 64, "src_bits must be 32 or 64");
+  TGX_REQUIRE(dst_bits == 32 || dst_bits == 64, "dst_bits must be 32 or 64");
+  TGX_REQUIRE(n_src >= 0 && n_dst >= 0 && n_edges >= 0, "negative size");
+  TGX_REQUIRE(n_edges <= INT32_MAX && n_dst < INT32_MAX,
+              "the device builder supports < 2^31 edges and destinations");
+  TGX_REQUIRE(row_ptr, "null row_ptr");
+  hipStream_t s = as_stream(stream);
+  if (n_edges == 0) {
+    TGX_HIP(hipMemsetAsync(row_ptr, 0, (dst_bits / 8) * (n_dst + 1), s));
+    return TGX_OK;
+  }
+  TGX_REQUIRE(src && dst && col && ws, "null pointer");
+  if (src_bits == 32)
+    return coo_dispatch_dst(static_cast<const int32_t*>(src), dst, dst_bits, n_dst, n_edges,
+                            row_ptr, col, perm, ws, ws_bytes, s);
+  return coo_dispatch_dst(static_cast<const int64_t*>(src), dst, dst_bits, n_dst, n_edges,
+                          row_ptr, col, perm, ws, ws_bytes, s);
+}
+
+extern "C" int tgx_varlen_csr_workspace(int64_t n_seq, size_t* bytes) {
+  TGX_REQUIRE(bytes, "null bytes");
+  TGX_REQUIRE(n_seq >= 0, "negative size");
+  *bytes = varlen_csr_bytes(n_seq);
+  return TGX_OK;
+}
+
+extern "C" int tgx_varlen_csr(const void* cu_seqlens, int idx_bits, int64_t n_seq,
+                              int64_t total, int64_t n_edges, int causal, void* row_ptr,
+                              void* col, void* ws, size_t ws_bytes, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(n_seq >= 0 && total >= 0 && n_edges >= 0, "negative size");
+  TGX_REQUIRE(n_edges <= INT32_MAX, "the device builder supports < 2^31 edges");
+  TGX_REQUIRE(idx_bits == 64 || total <= INT32_MAX, "positions overflow int32");
+  TGX_REQUIRE(row_ptr, "null row_ptr");
+  hipStream_t s = as_stream(stream);
+  if (total == 0 || n_seq == 0) {
+    TGX_REQUIRE(total == 0 && n_edges == 0, "no sequences but %lld positions",
+                static_cast<long long>(total));
+    TGX_HIP(hipMemsetAsync(row_ptr, 0, idx_bits / 8, s));
+    return TGX_OK;
+  }
+  TGX_REQUIRE(cu_seqlens && col && ws, "null pointer");
+  if (idx_bits == 32)
+    return varlen_csr_impl(static_cast<const int32_t*>(cu_seqlens), n_seq, total, n_edges,
+                           causal, static_cast<int32_t*>(row_ptr),
+                           static_cast<int32_t*>(col), ws, ws_bytes, s);
+  return varlen_csr_impl(static_cast<const int64_t*>(cu_seqlens), n_seq, total, n_edges,
+                         causal, static_cast<int64_t*>(row_ptr), static_cast<int64_t*>(col),
+                         ws, ws_bytes, s);
 }

@@ -48,6 +48,12 @@ _SIGNATURES: dict[str, list] = {
     "tgx_csr_transpose_workspace": [c_i64, c_i64, c_i64, P(c_size)],
     "tgx_csr_transpose": [c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
                           c_vp, c_vp, c_size, c_vp],
+    "tgx_coo_to_csr_workspace": [c_i64, c_i64, c_i64, P(c_size)],
+    "tgx_coo_to_csr": [c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
+                       c_vp, c_size, c_vp],
+    "tgx_varlen_csr_workspace": [c_i64, P(c_size)],
+    "tgx_varlen_csr": [c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_size,
+                       c_vp],
     "tgx_plan_degree_bins_workspace": [c_i64, c_int, P(c_size)],
     "tgx_plan_degree_bins": [c_vp, c_int, c_i64, P(c_i64), c_int, c_vp, P(c_i64), c_vp,
                              c_size, c_vp],

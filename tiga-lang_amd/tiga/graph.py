@@ -118,6 +118,43 @@ def build_transpose(row_ptr: torch.Tensor, col_idx: torch.Tensor, num_dst: int,
     return row_ptr_t, col_t[:E], perm[:E], inv_perm[:E]
 
 
+def _native_builder_ok(t: torch.Tensor, n_edges: int, n_rows: int) -> bool:
+    """Device builders run for GPU tensors below 2^31 edges and rows; other
+    cases (CPU tensors, larger graphs) use Torch ops, as the reference does."""
+    return t.is_cuda and n_edges < 2**31 and n_rows < 2**31 - 1
+
+
+def build_coo_csr(src: torch.Tensor, dst: torch.Tensor, num_dst: int):
+    """(row_ptr in dst's dtype, col_idx in src's dtype) for ``from_coo``:
+    stable sort of the edges by destination (reference graph.py:219-227)."""
+    device = dst.device
+    E = src.numel()
+    row_ptr = torch.empty(num_dst + 1, dtype=dst.dtype, device=device)
+    col = torch.empty(max(E, 1), dtype=src.dtype, device=device)
+    ws_bytes = ctypes.c_size_t()
+    _native.call("tgx_coo_to_csr_workspace", 0, num_dst, E, ctypes.byref(ws_bytes))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=device)
+    _native.call("tgx_coo_to_csr", _native.ptr(src), _native.idx_bits(src), _native.ptr(dst),
+                 _native.idx_bits(dst), 0, num_dst, E, row_ptr.data_ptr(), col.data_ptr(),
+                 None, ws.data_ptr(), ws_bytes.value, _native.stream_of(dst))
+    return row_ptr, col[:E]
+
+
+def build_varlen_csr(cu_seqlens: torch.Tensor, causal: bool, total: int, n_edges: int):
+    """Materialized block-diagonal varlen CSR (reference graph.py:276-294)."""
+    device, dtype = cu_seqlens.device, cu_seqlens.dtype
+    n_seq = cu_seqlens.numel() - 1
+    row_ptr = torch.empty(total + 1, dtype=dtype, device=device)
+    col = torch.empty(max(n_edges, 1), dtype=dtype, device=device)
+    ws_bytes = ctypes.c_size_t()
+    _native.call("tgx_varlen_csr_workspace", n_seq, ctypes.byref(ws_bytes))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=device)
+    _native.call("tgx_varlen_csr", _native.ptr(cu_seqlens), _native.idx_bits(cu_seqlens),
+                 n_seq, total, n_edges, int(causal), row_ptr.data_ptr(), col.data_ptr(),
+                 ws.data_ptr(), ws_bytes.value, _native.stream_of(cu_seqlens))
+    return row_ptr, col[:n_edges]
+
+
 class Graph:
     """Torch realization of a Tiga relation (destination-row CSR)."""
 
@@ -205,12 +242,15 @@ class Graph:
                 raise ValueError("src contains an out-of-range source index")
             if int(dst.min().item()) < 0 or int(dst.max().item()) >= num_dst:
                 raise ValueError("dst contains an out-of-range destination index")
-        order = torch.argsort(dst, stable=True)
-        col_idx = src[order]
-        counts = torch.bincount(dst.to(torch.int64), minlength=num_dst)
-        row_ptr = torch.empty(num_dst + 1, device=dst.device, dtype=dst.dtype)
-        row_ptr[0] = 0
-        torch.cumsum(counts, dim=0, out=row_ptr[1:])
+        if _native_builder_ok(dst, src.numel(), num_dst):
+            row_ptr, col_idx = build_coo_csr(src, dst, num_dst)
+        else:
+            order = torch.argsort(dst, stable=True)
+            col_idx = src[order]
+            counts = torch.bincount(dst.to(torch.int64), minlength=num_dst)
+            row_ptr = torch.empty(num_dst + 1, device=dst.device, dtype=dst.dtype)
+            row_ptr[0] = 0
+            torch.cumsum(counts, dim=0, out=row_ptr[1:])
         return cls.from_csr(row_ptr, col_idx, num_src=num_src, validate="basic")
 
     @classmethod
@@ -318,7 +358,14 @@ class Graph:
 
     def resolve_csr(self) -> tuple[torch.Tensor, torch.Tensor]:
         if self._row_ptr is None and self.is_varlen:
-            self._row_ptr, self._col_idx = _varlen_csr(self._cu_seqlens, self._causal)
+            total = self._schema.num_dst
+            n_edges = self.num_edges
+            n_seq = self._cu_seqlens.numel() - 1
+            if _native_builder_ok(self._cu_seqlens, n_edges, max(total, n_seq)):
+                self._row_ptr, self._col_idx = build_varlen_csr(
+                    self._cu_seqlens, self._causal, total, n_edges)
+            else:
+                self._row_ptr, self._col_idx = _varlen_csr(self._cu_seqlens, self._causal)
         return self._row_ptr, self._col_idx
 
     def transpose(self) -> "Graph":
@@ -332,9 +379,26 @@ class Graph:
             return self._destination_index_cache
         if row_ptr is None:
             row_ptr, _ = self.resolve_csr()
-        degree = row_ptr[1:] - row_ptr[:-1]
-        dst = torch.repeat_interleave(
-            torch.arange(self._schema.num_dst, device=row_ptr.device), degree)
+        native = False
+        if row_ptr.is_cuda and row_ptr.numel() == self._schema.num_dst + 1 > 1:
+            # One sync: the edge count, and whether row_ptr is well formed
+            # (starts at 0, non-decreasing) so the kernel's writes stay in
+            # [0, row_ptr[-1]).
+            stats = torch.stack([row_ptr[-1].to(torch.int64),
+                                 (row_ptr[0] == 0).to(torch.int64),
+                                 (row_ptr[1:] >= row_ptr[:-1]).all().to(torch.int64)]).cpu()
+            n_edges = int(stats[0])
+            native = bool(stats[1]) and bool(stats[2]) and _native_builder_ok(
+                row_ptr, n_edges, self._schema.num_dst)
+        if native:
+            dst = torch.empty(n_edges, dtype=torch.int64, device=row_ptr.device)
+            _native.call("tgx_destination_index", _native.ptr(row_ptr),
+                         _native.idx_bits(row_ptr), self._schema.num_dst, n_edges,
+                         _native.ptr(dst), 64, _native.stream_of(row_ptr))
+        else:
+            degree = row_ptr[1:] - row_ptr[:-1]
+            dst = torch.repeat_interleave(
+                torch.arange(self._schema.num_dst, device=row_ptr.device), degree)
         if self._row_ptr is row_ptr:
             self._destination_index_cache = dst
         return dst
@@ -465,4 +529,5 @@ def _varlen_csr(cu_seqlens: torch.Tensor, causal: bool):
     return row_ptr, col_idx
 
 
-__all__ = ["Graph", "GraphSchema", "build_row_plan", "build_transpose"]
+__all__ = ["Graph", "GraphSchema", "build_coo_csr", "build_row_plan", "build_transpose",
+           "build_varlen_csr"]
