@@ -27,6 +27,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "tgx_device.h"
@@ -75,7 +76,10 @@ struct VarlenFwdArgs {
   float scale_log2;       // softmax scale * log2(e)
 };
 
-// Stage one 64-key tile: thread t holds 4 rows x 16 B of K and of V.
+// Stage one 64-key tile: thread t holds 4 rows x 16 B of K and of V.  Rows
+// past the sequence end are clamped to its last row (finite values whose
+// scores the causal mask removes), so the loads need no branches; every tile
+// handed to a workgroup has at least one key (s1 > s0).
 struct KvStage {
   bf16x8 k[4], v[4];
 };
@@ -85,18 +89,41 @@ __device__ __forceinline__ void load_kv(KvStage& st, const __bf16* kb, const __b
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int idx = threadIdx.x + 256 * it;
-    const int key = idx >> 4;
-    const int dc = idx & 15;
-    if (kbase + key < s1) {
-      const int64_t off = static_cast<int64_t>(kbase + key) * row_stride + dc * 8;
-      st.k[it] = ld_bf16x8(kb + off);
-      st.v[it] = ld_bf16x8(vb + off);
-    } else {
-      st.k[it] = bf16x8{};
-      st.v[it] = bf16x8{};
-    }
+    const int key = min(kbase + (idx >> 4), s1 - 1);
+    const int64_t off = static_cast<int64_t>(key) * row_stride + (idx & 15) * 8;
+    st.k[it] = ld_bf16x8(kb + off);
+    st.v[it] = ld_bf16x8(vb + off);
   }
 }
+
+// Max / sum of a value over the four 16-lane groups (lanes l, l^16, l^32,
+// l^48) with gfx950's row-swap permutes: with both operands equal, each swap
+// hands every lane its partner's value in one of the two results.
+__device__ __forceinline__ float group4_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float group4_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// 2^x on the hardware unit (v_exp_f32): exact 0 for -inf; results below the
+// fp32 normal range flush to zero, which softmax weights tolerate.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The running max is only moved when a tile's max exceeds it by more than
+// this many (log2 units): weights then stay below 2^8, exact in the final
+// normalisation, and the O rescale is skipped for nearly every tile.
+constexpr float kRescaleLog2 = 8.f;
 
 __device__ __forceinline__ void store_kv(const KvStage& st, __bf16 (*ks)[KPAD],
                                          __bf16 (*vs)[TPAD]) {
@@ -155,8 +182,15 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
 
   const int kv_end = (q0 + VBM < s1) ? q0 + VBM : s1;
   const int n_kv = (kv_end - s0 + VBN - 1) / VBN;
+  const float sl2 = a.scale_log2;
+  // Running max in scaled log2 units (-inf until a score is seen); lp is this
+  // lane's share of the softmax denominator.
   float m[2] = {kNegInf, kNegInf};
   float lp[2] = {0.f, 0.f};
+  // Last unmasked key of each query row (padded rows past s1 use s1 - 1).
+  int qlim[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) qlim[qt] = min(qb + 16 * qt + lr, s1 - 1);
   f32x4v o[8][2];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
@@ -191,49 +225,60 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
       }
     }
 
-    // Causal/sequence mask and online softmax (base-2 exponent).
-    const bool edge_tile = kbase + VBN > qb || kbase + VBN > s1;
-    bf16x8 pf[2][2];
+    // Causal/sequence mask (diagonal and last tiles only), then the tile max
+    // of the raw scores (scale > 0, so scaling commutes with max).
+    if (kbase + VBN > qb || kbase + VBN > s1) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (kbase + 16 * kt + 4 * g + r > qlim[qt]) c[kt][qt][r] = kNegInf;
+    }
+    float mt[2];
+    bool grow = false;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const int qq = qb + 16 * qt + lr;
-      float sv[4][4];
-      float mt = kNegInf;
+      float x = kNegInf;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float s = c[kt][qt][r] * a.scale_log2;
-          if (edge_tile) {
-            const int key = kbase + 16 * kt + 4 * g + r;
-            if (key > qq || key >= s1) s = kNegInf;
-          }
-          sv[kt][r] = s;
-          mt = fmaxf(mt, s);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float mn = fmaxf(m[qt], mt);
-      const float alpha = (m[qt] == kNegInf) ? 0.f : exp2f(m[qt] - mn);
+        for (int r = 0; r < 4; ++r) x = fmaxf(x, c[kt][qt][r]);
+      mt[qt] = group4_max(x) * sl2;
+      grow |= mt[qt] > m[qt] + kRescaleLog2;
+    }
+    if (__any(grow)) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const float mn = fmaxf(m[qt], mt[qt]);
+        const float alpha = mn == kNegInf ? 1.f : exp2_hw(m[qt] - mn);
+        lp[qt] *= alpha;
+        m[qt] = mn;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+      }
+    }
+    bf16x8 pf[2][2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const float mo = m[qt] == kNegInf ? 0.f : m[qt];
+      float p[4][4];
       float rs = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = (sv[kt][r] == kNegInf) ? 0.f : exp2f(sv[kt][r] - mn);
-          sv[kt][r] = p;
-          rs += p;
+          p[kt][r] = exp2_hw(c[kt][qt][r] * sl2 - mo);
+          rs += p[kt][r];
         }
-      lp[qt] = lp[qt] * alpha + rs;
-      m[qt] = mn;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+      lp[qt] += rs;
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          pf[qt][k2][j] = static_cast<__bf16>(sv[2 * k2][j]);
-          pf[qt][k2][4 + j] = static_cast<__bf16>(sv[2 * k2 + 1][j]);
+          pf[qt][k2][j] = static_cast<__bf16>(p[2 * k2][j]);
+          pf[qt][k2][4 + j] = static_cast<__bf16>(p[2 * k2 + 1][j]);
         }
     }
 
@@ -254,9 +299,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
   // Finalize: l summed over the 4 lane groups, O = O^T / l, natural-log lse.
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    float l = lp[qt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = group4_sum(lp[qt]);
     const int qq = qb + 16 * qt + lr;
     if (qq >= s1) continue;
     const float inv = 1.f / l;
@@ -438,20 +481,27 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
       }
     }
     // P = exp(S*scale - lse), dS = P (dP - delta); packed per 32-query step.
+    // Only the first block holds queries that precede keys of the tile, so
+    // only it is masked (padded queries have lse = +inf, so P = 0).
     bf16x8 pb[2], sb[2];
+    auto weights = [&](auto masked) {
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
+      for (int qt = 0; qt < 4; ++qt) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int qi = 16 * qt + 4 * g + r;
-        const int qq = qbase + qi;
-        float p = exp2f(sc[qt][r] * a.scale_log2 - lse_s[qi]);
-        if (qq < key) p = 0.f;
-        const float ds = p * (dp[qt][r] - del_s[qi]);
-        pb[qt >> 1][4 * (qt & 1) + r] = static_cast<__bf16>(p);
-        sb[qt >> 1][4 * (qt & 1) + r] = static_cast<__bf16>(ds);
+        for (int r = 0; r < 4; ++r) {
+          const int qi = 16 * qt + 4 * g + r;
+          float p = exp2_hw(sc[qt][r] * a.scale_log2 - lse_s[qi]);
+          if (decltype(masked)::value && qbase + qi < key) p = 0.f;
+          const float ds = p * (dp[qt][r] - del_s[qi]);
+          pb[qt >> 1][4 * (qt & 1) + r] = static_cast<__bf16>(p);
+          sb[qt >> 1][4 * (qt & 1) + r] = static_cast<__bf16>(ds);
+        }
       }
-    }
+    };
+    if (ib == 0)
+      weights(std::true_type{});
+    else
+      weights(std::false_type{});
     // dV^T += dO^T P, dK^T += Q^T dS over the block's 64 queries.
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
@@ -510,6 +560,9 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
     lse2[qt] = ok ? a.lse[static_cast<int64_t>(qq) * a.H + h] * kLog2e : __builtin_huge_valf();
     del[qt] = ok ? a.delta[static_cast<int64_t>(qq) * a.H + h] : 0.f;
   }
+  int qlim[2];         // last key each query row may see
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) qlim[qt] = min(qb + 16 * qt + lr, s1 - 1);
   f32x4v dqt[8][2];   // dQ^T [d = 16 dt + 4g + r][q]
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
@@ -528,6 +581,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
     __syncthreads();
     if (it + 1 < n_kv) load2(st, kh, vh, row_stride, kbase + VBN, s1);
     if (kbase > qb + 31) continue;
+    const bool edge_tile = kbase + VBN > qb || kbase + VBN > s1;
     // S^T = K Q^T and dP^T = V dO^T one 16-key subtile at a time (C tiles
     // [key = 16 kt + 4g + r][q]), turned straight into dS^T fragments.
     bf16x8 sb[2][2];
@@ -549,18 +603,24 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
           dp[qt] = mfma(va, df[qt][kc], dp[qt]);
         }
       }
+      // Keys past a query (diagonal and last tiles only) get no weight;
+      // padded queries have lse = +inf, so their P is 0.
+      auto weights = [&](auto masked) {
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        const int qq = qb + 16 * qt + lr;
+        for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int kk = kbase + 16 * kt + 4 * g + r;
-          float p = exp2f(sc[qt][r] * a.scale_log2 - lse2[qt]);
-          if (kk > qq || kk >= s1) p = 0.f;
-          const float ds = p * (dp[qt][r] - del[qt]);
-          sb[qt][kt >> 1][4 * (kt & 1) + r] = static_cast<__bf16>(ds);
+          for (int r = 0; r < 4; ++r) {
+            float p = exp2_hw(sc[qt][r] * a.scale_log2 - lse2[qt]);
+            if (decltype(masked)::value && kbase + 16 * kt + 4 * g + r > qlim[qt]) p = 0.f;
+            const float ds = p * (dp[qt][r] - del[qt]);
+            sb[qt][kt >> 1][4 * (kt & 1) + r] = static_cast<__bf16>(ds);
+          }
         }
-      }
+      };
+      if (edge_tile)
+        weights(std::true_type{});
+      else
+        weights(std::false_type{});
     }
     // dQ^T += K^T dS^T.
 #pragma unroll
