@@ -309,29 +309,36 @@ int tgx_dot_attn_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
 /*   relation: Graph.cu_seqlens(causal=True), token i attends [s_k, i]        */
 /* ------------------------------------------------------------------------ */
 
-/* Host: work tiles (sequence, first row) of `block` rows, heaviest first.
+/* Host: the work list of one varlen launch, in dispatch order.  A task is
+ * four int32 (sequence, first row, head, 0) naming `block` rows of one head:
  * kind 0: query tiles (block 128, forward and dQ), work = causal key range;
  * kind 1: key tiles (block 64, dK/dV), work = queries after the tile.
- * Call with tiles_host = NULL to get the count.  Replaces materializing the
+ * Every tile of one (sequence, head) goes to the same XCD (workgroup i runs
+ * on XCD i % 8, each XCD has its own L2) and the tiles are queued together,
+ * heaviest first, so they read the same key/query blocks at about the same
+ * time; (sequence, head) groups are spread over the 8 XCDs longest first.
+ * Slots past the end of a shorter XCD queue hold sequence -1 (skipped).
+ * Call with tasks_host = NULL to get n_tasks.  Replaces materializing the
  * block-diagonal CSR (interop/torch/graph.py:260-294). */
-int tgx_varlen_causal_tiles(const int32_t* cu_seqlens_host, int n_seq, int block, int kind,
-                            int32_t* tiles_host, int64_t* n_tiles);
+int tgx_varlen_causal_tasks(const int32_t* cu_seqlens_host, int n_seq, int H, int block,
+                            int kind, int32_t* tasks_host, int64_t* n_tasks);
 
 /* Forward.  q/k/v/out [T, H, 128] bf16, lse [T, H] fp32 (natural log).
- * tiles_dev from tgx_varlen_causal_tiles with block_q = 128.  The reference's
+ * tasks_dev from tgx_varlen_causal_tasks (kind 0, block 128, same H) on the
+ * device; the kernels trust it to match cu_seqlens and H.  The reference's
  * compiled streaming tile covers dense/triangular fp16 forward only
  * (lib/Target/Triton/Translate.cpp:1603-1912); varlen runs its eager oracle
  * (examples/varlen_causal_attention.py:46-48). */
-int tgx_varlen_causal_fwd(const int32_t* cu_seqlens_dev, const int32_t* tiles_dev,
-                          int64_t n_tiles, const void* q_dev, const void* k_dev,
+int tgx_varlen_causal_fwd(const int32_t* cu_seqlens_dev, const int32_t* tasks_dev,
+                          int64_t n_tasks, const void* q_dev, const void* k_dev,
                           const void* v_dev, float scale, void* out_dev, float* lse_dev,
                           int64_t total_tokens, int H, int D, void* stream);
 
 /* Backward (no atomics): delta = <dout, out> into delta_dev [T, H] fp32,
- * then dK/dV over key tiles (k_tiles: kind 1, block 64) and dQ over query
- * tiles (q_tiles: kind 0, block 128).  dq/dk/dv [T, H, 128] bf16. */
-int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_t* q_tiles_dev,
-                          int64_t n_q_tiles, const int32_t* k_tiles_dev, int64_t n_k_tiles,
+ * then dK/dV over key tiles (k_tasks: kind 1, block 64) and dQ over query
+ * tiles (q_tasks: kind 0, block 128).  dq/dk/dv [T, H, 128] bf16. */
+int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_t* q_tasks_dev,
+                          int64_t n_q_tasks, const int32_t* k_tasks_dev, int64_t n_k_tasks,
                           const void* q_dev, const void* k_dev, const void* v_dev,
                           const void* out_dev, const float* lse_dev, const void* dout_dev,
                           float scale, void* dq_dev, void* dk_dev, void* dv_dev,

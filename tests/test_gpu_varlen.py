@@ -21,24 +21,24 @@ def rel_err(actual, expected):
     return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
 
 
-def tiles_for(cu, block=128, kind=0):
+def tasks_for(cu, H, block=128, kind=0):
     n = ctypes.c_int64()
     cu_h = np.ascontiguousarray(cu, dtype=np.int32)
-    _native.call("tgx_varlen_causal_tiles", cu_h.ctypes.data, cu_h.size - 1, block, kind,
+    _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, H, block, kind,
                  None, ctypes.byref(n))
-    tiles = np.zeros(2 * max(n.value, 1), dtype=np.int32)
-    _native.call("tgx_varlen_causal_tiles", cu_h.ctypes.data, cu_h.size - 1, block, kind,
-                 tiles.ctypes.data, ctypes.byref(n))
-    return torch.as_tensor(tiles, device=DEV), n.value
+    tasks = np.zeros(4 * max(n.value, 1), dtype=np.int32)
+    _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, H, block, kind,
+                 tasks.ctypes.data, ctypes.byref(n))
+    return torch.as_tensor(tasks, device=DEV), n.value
 
 
 def varlen_fwd_capi(cu, q, k, v, scale):
     T, H, D = q.shape
-    tiles, n = tiles_for(cu)
+    tasks, n = tasks_for(cu, H)
     cu_d = torch.as_tensor(np.asarray(cu, dtype=np.int32), device=DEV)
     out = torch.empty_like(q)
     lse = torch.empty(T, H, dtype=torch.float32, device=DEV)
-    _native.call("tgx_varlen_causal_fwd", cu_d.data_ptr(), tiles.data_ptr(), n, q.data_ptr(),
+    _native.call("tgx_varlen_causal_fwd", cu_d.data_ptr(), tasks.data_ptr(), n, q.data_ptr(),
                  k.data_ptr(), v.data_ptr(), scale, out.data_ptr(), lse.data_ptr(), T, H, D,
                  _native.stream_of(q))
     torch.cuda.synchronize()
@@ -62,20 +62,6 @@ def test_varlen_fwd_parity(lengths, H):
     e_out, e_lse = ref.varlen_causal_fwd(cu, f(q), f(k), f(v), scale)
     assert rel_err(f(out), e_out) <= 2e-2
     assert rel_err(lse.cpu().numpy(), e_lse) <= 1e-3
-
-
-def test_varlen_tiles_order():
-    cu = np.array([0, 3, 300, 301], dtype=np.int32)
-    tiles, n = tiles_for(cu)
-    t = tiles.cpu().numpy()[: 2 * n].reshape(n, 2)
-    # every query covered once; heaviest (longest causal prefix) first
-    assert sorted(map(tuple, t.tolist())) == [(0, 0), (1, 3), (1, 131), (1, 259), (2, 300)]
-    work = [min(q0 + 128, cu[s + 1]) - cu[s] for s, q0 in t]
-    assert work == sorted(work, reverse=True)
-    tiles, n = tiles_for(cu, block=64, kind=1)
-    t = tiles.cpu().numpy()[: 2 * n].reshape(n, 2)
-    work = [cu[s + 1] - k0 for s, k0 in t]
-    assert work == sorted(work, reverse=True) and len(t) == 1 + 5 + 1
 
 
 class VarlenAttention(tg.MessagePassing):

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_native.exported_symbols())
-    assert lib.tgx_abi_version() == 1
+    assert lib.tgx_abi_version() == 2
     assert lib.tgx_status_string(1) == b"invalid argument"
 
 
@@ -244,3 +244,63 @@ def test_kernel_csr_unifies_dtypes_and_rejects_bad_columns():
                                num_src=3)
     with pytest.raises(ValueError, match="monotonic"):
         bad_rp._kernel_csr()
+
+
+def _varlen_tasks(cu, H, block, kind):
+    n = ctypes.c_int64()
+    cu_h = np.ascontiguousarray(cu, dtype=np.int32)
+    _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, H, block, kind,
+                 None, ctypes.byref(n))
+    tasks = np.zeros(4 * max(n.value, 1), dtype=np.int32)
+    _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, H, block, kind,
+                 tasks.ctypes.data, ctypes.byref(n))
+    return tasks[: 4 * n.value].reshape(n.value, 4)
+
+
+@pytest.mark.parametrize("kind,block", [(0, 128), (1, 64)])
+def test_varlen_tasks_cover_once_grouped_per_xcd(kind, block):
+    """Host-side work list of the varlen kernels: every (sequence, tile, head)
+    exactly once; all tiles of one (sequence, head) on one XCD (slot % 8),
+    consecutive in that XCD's queue and heaviest first; XCD loads balanced."""
+    cu = np.array([0, 3, 300, 300, 301, 1500, 1700, 4000], dtype=np.int32)
+    H = 3
+    t = _varlen_tasks(cu, H, block, kind)
+    assert t.shape[0] % 8 == 0
+    real = t[t[:, 0] >= 0]
+    assert (t[t[:, 0] < 0][:, 1:] == 0).all()
+    expect = sorted((s, r0, h) for s in range(len(cu) - 1) for h in range(H)
+                    for r0 in range(cu[s], cu[s + 1], block))
+    assert sorted(map(tuple, real[:, :3].tolist())) == expect
+    assert (real[:, 3] == 0).all()
+
+    def work(s, r0):
+        s0, s1 = int(cu[s]), int(cu[s + 1])
+        return min(r0 + block, s1) - s0 if kind == 0 else s1 - r0
+
+    loads = [0] * 8
+    for x in range(8):
+        queue = [tuple(row[:3]) for row in t[x::8] if row[0] >= 0]
+        # padding only after the queue's end
+        col = t[x::8, 0]
+        assert all(col[i] >= 0 for i in range(len(queue)))
+        groups = []
+        for s, r0, h in queue:
+            if not groups or groups[-1][0] != (s, h):
+                groups.append(((s, h), []))
+            groups[-1][1].append(work(s, r0))
+            loads[x] += work(s, r0)
+        keys = [g[0] for g in groups]
+        assert len(keys) == len(set(keys)), "a group's tiles are split in the queue"
+        for _, ws in groups:
+            assert ws == sorted(ws, reverse=True)
+    # LPT balance: no XCD exceeds the mean by more than the largest group
+    group_work = {}
+    for s, r0, h in expect:
+        group_work[(s, h)] = group_work.get((s, h), 0) + work(s, r0)
+    assert max(loads) - min(loads) <= max(group_work.values())
+    # every group's tiles sit on one XCD
+    where = {}
+    for slot, row in enumerate(t):
+        if row[0] >= 0:
+            where.setdefault((row[0], row[2]), set()).add(slot % 8)
+    assert all(len(v) == 1 for v in where.values())

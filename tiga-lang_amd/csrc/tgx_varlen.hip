@@ -54,6 +54,9 @@ constexpr int TPAD = 144;
 constexpr int KPAD = TPAD;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// gfx950 (MI355X) has 8 XCDs, each with its own L2; workgroup i of a launch
+// runs on XCD i % 8.
+constexpr int kXcds = 8;
 
 __device__ __forceinline__ f32x4v mfma(bf16x8 a, bf16x8 b, f32x4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -65,8 +68,7 @@ __device__ __forceinline__ bf16x8 ld_bf16x8(const __bf16* p) {
 
 struct VarlenFwdArgs {
   const int32_t* cu;      // [n_seq + 1]
-  const int32_t* tiles;   // [n_tiles, 2] = (sequence, first query), heaviest first
-  int n_tiles;
+  const int32_t* tasks;   // [n_tasks, 4] = (sequence, first query, head, 0)
   int H;
   const __bf16* q;
   const __bf16* k;
@@ -155,11 +157,11 @@ __device__ __forceinline__ bf16x8 tr_frag(__bf16 (*x)[TPAD], int r0, int c0, int
 __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
   __shared__ __bf16 ks[2][VBN][KPAD];
   __shared__ __bf16 vs[2][VBN][TPAD];
-  const int task = blockIdx.x;
-  const int tile = task / a.H;
-  const int h = task - tile * a.H;
-  const int seq = a.tiles[2 * tile];
-  const int q0 = a.tiles[2 * tile + 1];
+  const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
+  const int seq = task[0];
+  if (seq < 0) return;   // padding slot of a shorter XCD queue
+  const int q0 = task[1];
+  const int h = task[2];
   const int s0 = a.cu[seq], s1 = a.cu[seq + 1];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -329,8 +331,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
 
 struct VarlenBwdArgs {
   const int32_t* cu;
-  const int32_t* tiles;   // dK/dV: (sequence, first key) per 64-key tile; dQ: query tiles
-  int n_tiles;
+  const int32_t* tasks;   // [n_tasks, 4] = (sequence, first key or query, head, 0)
   int H;
   const __bf16* q;
   const __bf16* k;
@@ -412,11 +413,11 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
   __shared__ __bf16 qs[VBN][TPAD];    // Q rows of the query block
   __shared__ __bf16 dos[VBN][TPAD];   // dO rows
   __shared__ float lse_s[VBN], del_s[VBN];
-  const int task = blockIdx.x;
-  const int tile = task / a.H;
-  const int h = task - tile * a.H;
-  const int seq = a.tiles[2 * tile];
-  const int k0 = a.tiles[2 * tile + 1];
+  const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
+  const int seq = task[0];
+  if (seq < 0) return;   // padding slot of a shorter XCD queue
+  const int k0 = task[1];
+  const int h = task[2];
   const int s1 = a.cu[seq + 1];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -444,10 +445,15 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
   }
   const __bf16* qh = a.q + h * VD;
   const __bf16* doh = a.dout + h * VD;
+  // Query blocks run last to first: every key tile of a (sequence, head)
+  // starts on the sequence's last block, so tiles that run together (they
+  // are queued together on one XCD) read each block at about the same time
+  // and share it through L2.
   const int n_qb = (s1 - k0 + VBN - 1) / VBN;
   Stage2 st;
-  load2(st, qh, doh, row_stride, k0, s1);
-  for (int ib = 0; ib < n_qb; ++ib) {
+  load2(st, qh, doh, row_stride, k0 + (n_qb - 1) * VBN, s1);
+  for (int step = 0; step < n_qb; ++step) {
+    const int ib = n_qb - 1 - step;
     const int qbase = k0 + ib * VBN;
     __syncthreads();   // previous block's LDS reads are done
     store2<TPAD, TPAD>(st, qs, dos);
@@ -458,7 +464,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
       del_s[threadIdx.x] = qq < s1 ? a.delta[static_cast<int64_t>(qq) * a.H + h] : 0.f;
     }
     __syncthreads();
-    if (ib + 1 < n_qb) load2(st, qh, doh, row_stride, qbase + VBN, s1);
+    if (ib > 0) load2(st, qh, doh, row_stride, qbase - VBN, s1);
     // Keys of this wave that precede every query of the block all count;
     // a wave whose keys all exceed the block's last query skips it.
     if (k0 + 16 * wave > qbase + VBN - 1) continue;
@@ -534,11 +540,11 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
 __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
   __shared__ __bf16 ks[VBN][TPAD];     // K rows of the key tile
   __shared__ __bf16 vs[VBN][KPAD];     // V rows
-  const int task = blockIdx.x;
-  const int tile = task / a.H;
-  const int h = task - tile * a.H;
-  const int seq = a.tiles[2 * tile];
-  const int q0 = a.tiles[2 * tile + 1];
+  const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
+  const int seq = task[0];
+  if (seq < 0) return;   // padding slot of a shorter XCD queue
+  const int q0 = task[1];
+  const int h = task[2];
   const int s0 = a.cu[seq], s1 = a.cu[seq + 1];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -653,67 +659,96 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
 
 using namespace tgx;
 
-extern "C" int tgx_varlen_causal_tiles(const int32_t* cu_seqlens_host, int n_seq, int block,
-                                       int kind, int32_t* tiles_host, int64_t* n_tiles) {
-  TGX_REQUIRE(cu_seqlens_host && n_tiles && n_seq >= 0 && block > 0, "bad arguments");
+extern "C" int tgx_varlen_causal_tasks(const int32_t* cu_seqlens_host, int n_seq, int H,
+                                       int block, int kind, int32_t* tasks_host,
+                                       int64_t* n_tasks) {
+  TGX_REQUIRE(cu_seqlens_host && n_tasks && n_seq >= 0 && H > 0 && block > 0,
+              "bad arguments");
   TGX_REQUIRE(kind == 0 || kind == 1, "kind must be 0 (query tiles) or 1 (key tiles)");
-  const int block_q = block;
-  struct T {
-    int seq, q0;
+  // Work of a tile: the causal keys a query tile sees, or the queries that
+  // see a key tile.  A group is every tile of one (sequence, head).
+  struct Group {
+    int seq, head;
     int64_t work;
   };
-  std::vector<T> list;
+  std::vector<Group> groups;
   for (int b = 0; b < n_seq; ++b) {
     const int s0 = cu_seqlens_host[b], s1 = cu_seqlens_host[b + 1];
     TGX_REQUIRE(s1 >= s0 && s0 >= 0, "cu_seqlens must be non-decreasing from 0");
-    for (int q0 = s0; q0 < s1; q0 += block_q) {
-      const int end = q0 + block_q < s1 ? q0 + block_q : s1;
-      // Causal work of a query tile grows with its end; of a key tile, with
-      // the number of queries after it.
-      list.push_back(T{b, q0, static_cast<int64_t>(kind == 0 ? end - s0 : s1 - q0)});
+    if (s1 == s0) continue;
+    int64_t w = 0;
+    for (int r0 = s0; r0 < s1; r0 += block)
+      w += kind == 0 ? std::min(r0 + block, s1) - s0 : s1 - r0;
+    for (int h = 0; h < H; ++h) groups.push_back(Group{b, h, w});
+  }
+  // Longest-processing-time assignment of groups to the XCDs (stable, so
+  // ties keep sequence then head order).
+  std::stable_sort(groups.begin(), groups.end(),
+                   [](const Group& x, const Group& y) { return x.work > y.work; });
+  std::vector<std::vector<int32_t>> queue(kXcds);
+  int64_t load[kXcds] = {};
+  for (const Group& gr : groups) {
+    int x = 0;
+    for (int i = 1; i < kXcds; ++i)
+      if (load[i] < load[x]) x = i;
+    load[x] += gr.work;
+    const int s0 = cu_seqlens_host[gr.seq], s1 = cu_seqlens_host[gr.seq + 1];
+    // Heaviest tile first: the last query tile, or the first key tile.
+    const int n_t = (s1 - s0 + block - 1) / block;
+    for (int t = 0; t < n_t; ++t) {
+      const int r0 = kind == 0 ? s0 + (n_t - 1 - t) * block : s0 + t * block;
+      queue[x].insert(queue[x].end(), {gr.seq, r0, gr.head, 0});
     }
   }
-  // Heaviest tiles first, ties by position: a deterministic
-  // longest-processing-time order.
-  std::stable_sort(list.begin(), list.end(),
-                   [](const T& x, const T& y) { return x.work > y.work; });
-  if (tiles_host) {
-    for (size_t i = 0; i < list.size(); ++i) {
-      tiles_host[2 * i] = list[i].seq;
-      tiles_host[2 * i + 1] = list[i].q0;
-    }
+  size_t longest = 0;
+  for (const auto& qx : queue) longest = std::max(longest, qx.size() / 4);
+  const int64_t n = static_cast<int64_t>(longest) * kXcds;
+  TGX_REQUIRE(n < (int64_t{1} << 31), "too many tasks");
+  *n_tasks = n;
+  if (tasks_host) {
+    // Dispatch hands workgroup i to XCD i % 8: slot 8 i + x is XCD x's i-th
+    // task, or padding (sequence -1) once its queue is exhausted.
+    for (size_t i = 0; i < longest; ++i)
+      for (int x = 0; x < kXcds; ++x) {
+        int32_t* dst = tasks_host + 4 * (static_cast<int64_t>(i) * kXcds + x);
+        if (4 * i < queue[x].size()) {
+          for (int c = 0; c < 4; ++c) dst[c] = queue[x][4 * i + c];
+        } else {
+          dst[0] = -1;
+          dst[1] = dst[2] = dst[3] = 0;
+        }
+      }
   }
-  *n_tiles = static_cast<int64_t>(list.size());
   return TGX_OK;
 }
 
-extern "C" int tgx_varlen_causal_fwd(const int32_t* cu_seqlens_dev, const int32_t* tiles_dev,
-                                     int64_t n_tiles, const void* q, const void* k,
+extern "C" int tgx_varlen_causal_fwd(const int32_t* cu_seqlens_dev, const int32_t* tasks_dev,
+                                     int64_t n_tasks, const void* q, const void* k,
                                      const void* v, float scale, void* out, float* lse,
                                      int64_t total_tokens, int H, int D, void* stream) {
   if (D != VD) {
     set_error("varlen causal attention supports head_dim 128 (got %d)", D);
     return TGX_UNSUPPORTED;
   }
-  TGX_REQUIRE(H > 0 && n_tiles >= 0 && total_tokens >= 0, "bad sizes");
+  TGX_REQUIRE(H > 0 && n_tasks >= 0 && total_tokens >= 0, "bad sizes");
   TGX_REQUIRE(total_tokens * H * VD < (int64_t{1} << 31), "tensor too large for 32-bit offsets");
-  if (n_tiles == 0) return TGX_OK;
-  TGX_REQUIRE(cu_seqlens_dev && tiles_dev && q && k && v && out && lse, "null pointer");
-  TGX_REQUIRE(n_tiles * H < (int64_t{1} << 31), "too many tiles");
+  if (n_tasks == 0) return TGX_OK;
+  TGX_REQUIRE(cu_seqlens_dev && tasks_dev && q && k && v && out && lse, "null pointer");
+  TGX_REQUIRE(n_tasks < (int64_t{1} << 31), "too many tasks");
   hipStream_t s = as_stream(stream);
-  VarlenFwdArgs a{cu_seqlens_dev, tiles_dev, static_cast<int>(n_tiles), H,
+  VarlenFwdArgs a{cu_seqlens_dev, tasks_dev, H,
                   static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
                   static_cast<const __bf16*>(v), static_cast<__bf16*>(out), lse,
                   scale * kLog2e};
   TGX_PROFILE("varlen_fwd_kernel", s);
-  varlen_fwd_kernel<<<static_cast<unsigned>(n_tiles * H), 256, 0, s>>>(a);
+  varlen_fwd_kernel<<<static_cast<unsigned>(n_tasks), 256, 0, s>>>(a);
   TGX_LAUNCHED("varlen_fwd_kernel");
   return TGX_OK;
 }
 
-extern "C" int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_t* q_tiles_dev,
-                                     int64_t n_q_tiles, const int32_t* k_tiles_dev,
-                                     int64_t n_k_tiles, const void* q, const void* k,
+extern "C" int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_t* q_tasks_dev,
+                                     int64_t n_q_tasks, const int32_t* k_tasks_dev,
+                                     int64_t n_k_tasks, const void* q, const void* k,
                                      const void* v, const void* out, const float* lse,
                                      const void* dout, float scale, void* dq, void* dk, void* dv,
                                      float* delta, int64_t total_tokens, int H, int D,
@@ -722,10 +757,12 @@ extern "C" int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_
     set_error("varlen causal attention supports head_dim 128 (got %d)", D);
     return TGX_UNSUPPORTED;
   }
-  TGX_REQUIRE(H > 0 && n_q_tiles >= 0 && n_k_tiles >= 0 && total_tokens >= 0, "bad sizes");
+  TGX_REQUIRE(H > 0 && n_q_tasks >= 0 && n_k_tasks >= 0 && total_tokens >= 0, "bad sizes");
+  TGX_REQUIRE(n_q_tasks < (int64_t{1} << 31) && n_k_tasks < (int64_t{1} << 31),
+              "too many tasks");
   TGX_REQUIRE(total_tokens * H * VD < (int64_t{1} << 31), "tensor too large for 32-bit offsets");
   if (total_tokens == 0) return TGX_OK;
-  TGX_REQUIRE(cu_seqlens_dev && q_tiles_dev && k_tiles_dev && q && k && v && out && lse &&
+  TGX_REQUIRE(cu_seqlens_dev && q_tasks_dev && k_tasks_dev && q && k && v && out && lse &&
                   dout && dq && dk && dv && delta,
               "null pointer");
   hipStream_t s = as_stream(stream);
@@ -737,21 +774,20 @@ extern "C" int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_
         H);
     TGX_LAUNCHED("varlen_delta_kernel");
   }
-  VarlenBwdArgs a{cu_seqlens_dev, k_tiles_dev, static_cast<int>(n_k_tiles), H,
+  VarlenBwdArgs a{cu_seqlens_dev, k_tasks_dev, H,
                   static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
                   static_cast<const __bf16*>(v), static_cast<const __bf16*>(dout), lse, delta,
                   static_cast<__bf16*>(dq), static_cast<__bf16*>(dk), static_cast<__bf16*>(dv),
                   scale, scale * kLog2e};
-  if (n_k_tiles > 0) {
+  if (n_k_tasks > 0) {
     TGX_PROFILE("varlen_dkdv_kernel", s);
-    varlen_dkdv_kernel<<<static_cast<unsigned>(n_k_tiles * H), 256, 0, s>>>(a);
+    varlen_dkdv_kernel<<<static_cast<unsigned>(n_k_tasks), 256, 0, s>>>(a);
     TGX_LAUNCHED("varlen_dkdv_kernel");
   }
-  a.tiles = q_tiles_dev;
-  a.n_tiles = static_cast<int>(n_q_tiles);
-  if (n_q_tiles > 0) {
+  a.tasks = q_tasks_dev;
+  if (n_q_tasks > 0) {
     TGX_PROFILE("varlen_dq_kernel", s);
-    varlen_dq_kernel<<<static_cast<unsigned>(n_q_tiles * H), 256, 0, s>>>(a);
+    varlen_dq_kernel<<<static_cast<unsigned>(n_q_tasks), 256, 0, s>>>(a);
     TGX_LAUNCHED("varlen_dq_kernel");
   }
   return TGX_OK;

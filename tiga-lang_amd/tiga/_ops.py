@@ -199,10 +199,10 @@ class VarlenCausalFunction(torch.autograd.Function):
     def forward(ctx, q, k, v, scale: float, graph: Graph):
         T, H, D = q.shape
         qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
-        cu, tiles, n = graph._varlen_tiles(0, 128)
+        cu, tasks, n = graph._varlen_tasks(0, 128, H)
         out = torch.empty_like(qc)
         lse = torch.empty((T, H), dtype=torch.float32, device=q.device)
-        _native.call("tgx_varlen_causal_fwd", cu.data_ptr(), tiles.data_ptr(), n,
+        _native.call("tgx_varlen_causal_fwd", cu.data_ptr(), tasks.data_ptr(), n,
                      qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), float(scale), out.data_ptr(),
                      lse.data_ptr(), T, H, D, _native.stream_of(q))
         ctx.graph = graph
@@ -218,12 +218,12 @@ class VarlenCausalFunction(torch.autograd.Function):
         dout = dout.contiguous()
         if dout.dtype != qc.dtype:
             dout = dout.to(qc.dtype)
-        cu, qtiles, nq = graph._varlen_tiles(0, 128)
-        _, ktiles, nk = graph._varlen_tiles(1, 64)
+        cu, qtasks, nq = graph._varlen_tasks(0, 128, H)
+        _, ktasks, nk = graph._varlen_tasks(1, 64, H)
         dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
         delta = torch.empty((T, H), dtype=torch.float32, device=qc.device)
-        _native.call("tgx_varlen_causal_bwd", cu.data_ptr(), qtiles.data_ptr(), nq,
-                     ktiles.data_ptr(), nk, qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+        _native.call("tgx_varlen_causal_bwd", cu.data_ptr(), qtasks.data_ptr(), nq,
+                     ktasks.data_ptr(), nk, qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
                      out.data_ptr(), lse.data_ptr(), dout.data_ptr(), ctx.scale, dq.data_ptr(),
                      dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), T, H, D,
                      _native.stream_of(qc))

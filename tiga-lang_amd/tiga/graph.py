@@ -466,26 +466,26 @@ class Graph:
             self._native_cache["csr"] = got
         return got
 
-    def _varlen_tiles(self, kind: int, block: int):
-        """(cu_seqlens int32 on device, tiles [n, 2] int32 on device, n) for the
-        varlen kernels; kind 0 = query tiles, 1 = key tiles."""
-        key = ("varlen", kind, block)
+    def _varlen_tasks(self, kind: int, block: int, heads: int):
+        """(cu_seqlens int32 on device, tasks [n, 4] int32 on device, n) for the
+        varlen kernels of a `heads`-head launch; kind 0 = query tiles, 1 = key
+        tiles (tgx_varlen_causal_tasks: XCD-grouped dispatch order)."""
+        key = ("varlen", kind, block, heads)
         got = self._native_cache.get(key)
         if got is None:
             import numpy as np
 
             cu_h = np.ascontiguousarray(self._cu_seqlens.cpu().numpy(), dtype=np.int32)
             n = ctypes.c_int64()
-            _native.call("tgx_varlen_causal_tiles", cu_h.ctypes.data, cu_h.size - 1, block,
-                         kind, None, ctypes.byref(n))
-            tiles = np.zeros(2 * max(n.value, 1), dtype=np.int32)
-            _native.call("tgx_varlen_causal_tiles", cu_h.ctypes.data, cu_h.size - 1, block,
-                         kind, tiles.ctypes.data, ctypes.byref(n))
+            _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, heads,
+                         block, kind, None, ctypes.byref(n))
+            tasks = np.zeros(4 * max(n.value, 1), dtype=np.int32)
+            _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, heads,
+                         block, kind, tasks.ctypes.data, ctypes.byref(n))
             cu_d = torch.as_tensor(cu_h, device=self.device)
-            got = (cu_d, torch.as_tensor(tiles, device=self.device), n.value)
+            got = (cu_d, torch.as_tensor(tasks, device=self.device), n.value)
             self._native_cache[key] = got
         return got
-
 
     def _row_plan(self, wave_max: int = WAVE_MAX, chunk_edges: int = CHUNK_EDGES) -> RowPlanHandle:
         key = ("plan", wave_max, chunk_edges)
