@@ -305,44 +305,67 @@ int tgx_dot_attn_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                      size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
-/* Varlen causal attention on MFMA (bf16 in, fp32 accumulate, head_dim 128)  */
-/*   relation: Graph.cu_seqlens(causal=True), token i attends [s_k, i]        */
+/* Dense attention tiles on MFMA over block-diagonal relations               */
+/*   block k relates queries [cu_q[k], cu_q[k+1]) to keys                    */
+/*   [cu_k[k], cu_k[k+1]): every pair (causal = 0) or key <= query           */
+/*   (causal = 1, which needs cu_q == cu_k).  Graph.cu_seqlens(causal=...)   */
+/*   passes cu_q = cu_k = cu_seqlens; Graph.dense(num_src, num_dst) one       */
+/*   block [0, num_dst) x [0, num_src); Graph.triangular(n) one causal block */
+/*   (interop/torch/graph.py:260-294, 535-592).                              */
 /* ------------------------------------------------------------------------ */
 
-/* Host: the work list of one varlen launch, in dispatch order.  A task is
- * four int32 (sequence, first row, head, 0) naming `block` rows of one head:
- * kind 0: query tiles (block 128, forward and dQ), work = causal key range;
- * kind 1: key tiles (block 64, dK/dV), work = queries after the tile.
- * Every tile of one (sequence, head) goes to the same XCD (workgroup i runs
- * on XCD i % 8, each XCD has its own L2) and the tiles are queued together,
+/* Element types of the attention tiles. */
+enum { TGX_DTYPE_BF16 = 0, TGX_DTYPE_F16 = 1 };
+
+/* Host: the work list of one attention launch, in dispatch order.  A task is
+ * four int32 (block, first row, head, 0) naming `block` rows of one head:
+ * kind 0: query tiles (block 128, forward and dQ), work = keys seen;
+ * kind 1: key tiles (block 64, dK/dV), work = queries that see the tile.
+ * Every tile of one (block, head) goes to the same XCD (workgroup i runs on
+ * XCD i % 8, each XCD has its own L2) and the tiles are queued together,
  * heaviest first, so they read the same key/query blocks at about the same
- * time; (sequence, head) groups are spread over the 8 XCDs longest first.
- * Slots past the end of a shorter XCD queue hold sequence -1 (skipped).
- * Call with tasks_host = NULL to get n_tasks.  Replaces materializing the
- * block-diagonal CSR (interop/torch/graph.py:260-294). */
-int tgx_varlen_causal_tasks(const int32_t* cu_seqlens_host, int n_seq, int H, int block,
-                            int kind, int32_t* tasks_host, int64_t* n_tasks);
+ * time; (block, head) groups are spread over the 8 XCDs longest first.
+ * Slots past the end of a shorter XCD queue hold block -1 (skipped).
+ * Call with tasks_host = NULL to get n_tasks. */
+int tgx_attn_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host, int n_blocks, int H,
+                   int block, int kind, int causal, int32_t* tasks_host, int64_t* n_tasks);
 
-/* Forward.  q/k/v/out [T, H, 128] bf16, lse [T, H] fp32 (natural log).
- * tasks_dev from tgx_varlen_causal_tasks (kind 0, block 128, same H) on the
- * device; the kernels trust it to match cu_seqlens and H.  The reference's
- * compiled streaming tile covers dense/triangular fp16 forward only
- * (lib/Target/Triton/Translate.cpp:1603-1912); varlen runs its eager oracle
- * (examples/varlen_causal_attention.py:46-48). */
-int tgx_varlen_causal_fwd(const int32_t* cu_seqlens_dev, const int32_t* tasks_dev,
-                          int64_t n_tasks, const void* q_dev, const void* k_dev,
-                          const void* v_dev, float scale, void* out_dev, float* lse_dev,
-                          int64_t total_tokens, int H, int D, void* stream);
+/* Forward: out = softmax(scale * q k^T over the relation) v per head.
+ * q [n_q, H, D] and k/v [n_k, H, D] (D = 64 or 128, dtype TGX_DTYPE_*) have
+ * element strides strides[0..3] = (q token, q head, k/v token, k/v head),
+ * innermost stride 1: contiguous [n, H, D], or the reference's lane-major
+ * [H, n, D] storage viewed as [n, H, D]
+ * (interop/torch/message_passing.py:1944-1947); `strides` is a host array;
+ * out is contiguous [n_q, H, D],
+ * lse [n_q, H] fp32 natural log (-inf, and out 0, for a row without keys).
+ * tasks_dev from tgx_attn_tasks (kind 0, block 128, same H and causal) on the
+ * device; the kernels trust it to match cu_q/cu_k and H.
+ * prune_threshold = 0 is exact softmax; in (0, 1] it is the reference's
+ * block_prune_threshold (reducer/core.py:176-190): a 64-key tile is skipped
+ * for a 128-query block when the tile's maximum scaled score is below the
+ * block's running maximum by more than log2(threshold)
+ * (lib/Target/Triton/Translate.cpp:1793-1815), a schedule-dependent
+ * approximation with no gradient.  The reference's compiled tile covers
+ * dense/triangular fp16 forward (Translate.cpp:1603-1912); varlen runs its
+ * eager oracle (examples/varlen_causal_attention.py:46-48). */
+int tgx_attn_fwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev, const int32_t* tasks_dev,
+                 int64_t n_tasks, int causal, int dtype, const void* q_dev,
+                 const void* k_dev, const void* v_dev, const int64_t* strides,
+                 float scale, float prune_threshold, void* out_dev, float* lse_dev,
+                 int64_t n_q, int64_t n_k, int H, int D, void* stream);
 
-/* Backward (no atomics): delta = <dout, out> into delta_dev [T, H] fp32,
- * then dK/dV over key tiles (k_tasks: kind 1, block 64) and dQ over query
- * tiles (q_tasks: kind 0, block 128).  dq/dk/dv [T, H, 128] bf16. */
-int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_t* q_tasks_dev,
-                          int64_t n_q_tasks, const int32_t* k_tasks_dev, int64_t n_k_tasks,
-                          const void* q_dev, const void* k_dev, const void* v_dev,
-                          const void* out_dev, const float* lse_dev, const void* dout_dev,
-                          float scale, void* dq_dev, void* dk_dev, void* dv_dev,
-                          float* delta_dev, int64_t total_tokens, int H, int D, void* stream);
+/* Backward of the exact forward (no atomics): delta = <dout, out> into
+ * delta_dev [n_q, H] fp32, then dK/dV over key tiles (k_tasks: kind 1,
+ * block 64) and dQ over query tiles (q_tasks: kind 0, block 128).  dout, dq
+ * [n_q, H, D] and dk, dv [n_k, H, D] are contiguous; q/k/v and strides (a
+ * host array of four) as in the forward. */
+int tgx_attn_bwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
+                 const int32_t* q_tasks_dev, int64_t n_q_tasks, const int32_t* k_tasks_dev,
+                 int64_t n_k_tasks, int causal, int dtype, const void* q_dev,
+                 const void* k_dev, const void* v_dev, const int64_t* strides,
+                 const void* out_dev, const float* lse_dev, const void* dout_dev,
+                 float scale, void* dq_dev, void* dk_dev, void* dv_dev, float* delta_dev,
+                 int64_t n_q, int64_t n_k, int H, int D, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Per-kernel timing (no reference counterpart; used by the benchmark)       */

@@ -359,6 +359,132 @@ def dot_bwd(row_ptr, col_idx, q, k, v, scale, bias, dout):
 # Varlen causal attention (dense per sequence)
 
 
+def _block_scores(qs, ks, scale, causal, r0=0, c0=0):
+    """scale * q.k per head as [H, rows, cols], -inf where the boundary
+    excludes the pair (key index > query index when causal)."""
+    sc = np.einsum("ihd,jhd->hij", qs, ks) * scale
+    if causal:
+        rows = np.arange(qs.shape[0])[:, None] + r0
+        cols = np.arange(ks.shape[0])[None, :] + c0
+        sc = np.where((cols <= rows)[None], sc, -np.inf)
+    return sc
+
+
+def block_attention_fwd(cu_q, cu_k, q, k, v, scale, causal):
+    """Softmax attention per block of a block-diagonal relation, fp64: block b
+    relates queries [cu_q[b], cu_q[b+1]) to keys [cu_k[b], cu_k[b+1]), all
+    pairs or key <= query (causal, square blocks).  Covers Graph.cu_seqlens
+    (interop/torch/graph.py:260-294), Graph.dense and Graph.triangular
+    (:535-592) under the dot-product edge function and online softmax
+    (reducer_oracle.py:60-137).  A query with no keys gets 0 and lse -inf.
+
+    Pinned by: equality with dot_fwd on the materialized CSR of the same
+    relation and with the reference's per-sequence SDPA property
+    (tests/python/test_attention_examples.py:25-72), tests/test_oracle.py.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    out = np.zeros(q.shape[:2] + v.shape[2:])
+    lse = np.full(q.shape[:2], -np.inf)
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_k = np.asarray(cu_k, dtype=np.int64)
+    for b in range(cu_q.size - 1):
+        q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        if q1 == q0 or k1 == k0:
+            continue
+        sc = _block_scores(q[q0:q1], k[k0:k1], scale, causal, q0, k0)
+        m = sc.max(-1, keepdims=True)
+        p = np.exp(sc - m)
+        den = p.sum(-1, keepdims=True)
+        out[q0:q1] = np.einsum("hij,jhd->ihd", p / den, v[k0:k1])
+        lse[q0:q1] = (m[..., 0] + np.log(den[..., 0])).T
+    return out, lse
+
+
+def block_attention_bwd(cu_q, cu_k, q, k, v, scale, causal, dout):
+    """Gradients of block_attention_fwd (Jacobian d_s = alpha (<dout, v> -
+    <dout, out>), compiler/edge_nn_attention.py:569-575).  Pinned by finite
+    differences (tests/test_oracle.py)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    dout = np.asarray(dout, dtype=np.float64)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_k = np.asarray(cu_k, dtype=np.int64)
+    for b in range(cu_q.size - 1):
+        q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        if q1 == q0 or k1 == k0:
+            continue
+        qs, ks, vs, gs = q[q0:q1], k[k0:k1], v[k0:k1], dout[q0:q1]
+        sc = _block_scores(qs, ks, scale, causal, q0, k0)
+        p = np.exp(sc - sc.max(-1, keepdims=True))
+        p = p / p.sum(-1, keepdims=True)
+        o = np.einsum("hij,jhd->ihd", p, vs)
+        dv[k0:k1] = np.einsum("hij,ihd->jhd", p, gs)
+        dp = np.einsum("ihd,jhd->hij", gs, vs)
+        delta = np.einsum("ihd,ihd->hi", gs, o)[..., None]
+        ds = p * (dp - delta)
+        dq[q0:q1] = np.einsum("hij,jhd->ihd", ds, ks) * scale
+        dk[k0:k1] = np.einsum("hij,ihd->jhd", ds, qs) * scale
+    return dq, dk, dv
+
+
+def block_pruned_attention_fwd(cu_q, cu_k, q, k, v, scale, threshold, causal,
+                               block_m=128, block_n=64):
+    """online_softmax(block_prune_threshold=threshold) on a dense relation,
+    restating the reference's tile admission (lib/Target/Triton/
+    Translate.cpp:1760-1815): for each head and block of `block_m` queries,
+    key tiles of `block_n` are visited in order; a tile whose maximum scaled
+    log2 score (over the query block, masked pairs excluded) is below the
+    block's running maximum by more than log2(threshold) is skipped, else the
+    running maximum absorbs it and its keys count.  The result is exact
+    softmax over the admitted tiles.  The schedule (block_m x block_n) is part
+    of the semantics; this build's tiles are 128 queries x 64 keys.
+
+    Pinned by: threshold -> 0 equals block_attention_fwd, and a hand-built
+    case whose pruned tile is known (tests/test_oracle.py).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    H = q.shape[1]
+    out = np.zeros(q.shape[:2] + v.shape[2:])
+    lse = np.full(q.shape[:2], -np.inf)
+    prune_log2 = np.log2(threshold)
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_k = np.asarray(cu_k, dtype=np.int64)
+    for b in range(cu_q.size - 1):
+        q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        for r0 in range(q0, q1, block_m):
+            r1 = min(r0 + block_m, q1)
+            kend = min(r0 + block_m, k1) if causal else k1
+            for h in range(H):
+                sc = _block_scores(q[r0:r1, h:h + 1], k[k0:kend, h:h + 1], scale, causal,
+                                   r0, k0)[0]
+                keep = np.zeros(kend - k0, dtype=bool)
+                block_max = -np.inf
+                for c0 in range(0, kend - k0, block_n):
+                    tile = sc[:, c0:c0 + block_n] * np.log2(np.e)
+                    tile_max = tile.max()
+                    diff = tile_max - block_max
+                    if diff < prune_log2:      # NaN (both -inf) is admitted
+                        continue
+                    block_max = max(block_max, tile_max)
+                    keep[c0:c0 + block_n] = True
+                s = np.where(keep[None, :], sc, -np.inf)
+                m = s.max(-1, keepdims=True)
+                ok = np.isfinite(m[:, 0])
+                p = np.where(ok[:, None], np.exp(s - np.where(ok[:, None], m, 0)), 0.0)
+                den = p.sum(-1)
+                out[r0:r1, h] = np.where(den[:, None] > 0, p @ v[k0:kend, h] /
+                                         np.where(den > 0, den, 1)[:, None], 0.0)
+                lse[r0:r1, h] = np.where(den > 0, m[:, 0] + np.log(np.where(den > 0, den, 1)),
+                                         -np.inf)
+    return out, lse
+
+
 def varlen_causal_fwd(cu_seqlens, q, k, v, scale):
     """Per-sequence causal softmax attention, fp64: the dot-product relation
     on Graph.cu_seqlens(causal=True).  Pinned by equality with dot_fwd on the

@@ -21,26 +21,27 @@ def rel_err(actual, expected):
     return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
 
 
-def tasks_for(cu, H, block=128, kind=0):
+def tasks_for(cu, H, block=128, kind=0, causal=True):
     n = ctypes.c_int64()
     cu_h = np.ascontiguousarray(cu, dtype=np.int32)
-    _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, H, block, kind,
-                 None, ctypes.byref(n))
+    args = (cu_h.ctypes.data, cu_h.ctypes.data, cu_h.size - 1, H, block, kind, int(causal))
+    _native.call("tgx_attn_tasks", *args, None, ctypes.byref(n))
     tasks = np.zeros(4 * max(n.value, 1), dtype=np.int32)
-    _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, H, block, kind,
-                 tasks.ctypes.data, ctypes.byref(n))
+    _native.call("tgx_attn_tasks", *args, tasks.ctypes.data, ctypes.byref(n))
     return torch.as_tensor(tasks, device=DEV), n.value
 
 
 def varlen_fwd_capi(cu, q, k, v, scale):
+    """The forward entry point called directly (bf16, contiguous [T, H, D])."""
     T, H, D = q.shape
     tasks, n = tasks_for(cu, H)
     cu_d = torch.as_tensor(np.asarray(cu, dtype=np.int32), device=DEV)
     out = torch.empty_like(q)
     lse = torch.empty(T, H, dtype=torch.float32, device=DEV)
-    _native.call("tgx_varlen_causal_fwd", cu_d.data_ptr(), tasks.data_ptr(), n, q.data_ptr(),
-                 k.data_ptr(), v.data_ptr(), scale, out.data_ptr(), lse.data_ptr(), T, H, D,
-                 _native.stream_of(q))
+    strides = (ctypes.c_int64 * 4)(H * D, D, H * D, D)
+    _native.call("tgx_attn_fwd", cu_d.data_ptr(), cu_d.data_ptr(), tasks.data_ptr(), n, 1, 0,
+                 q.data_ptr(), k.data_ptr(), v.data_ptr(), strides, scale, 0.0,
+                 out.data_ptr(), lse.data_ptr(), T, T, H, D, _native.stream_of(q))
     torch.cuda.synchronize()
     return out, lse
 
@@ -96,7 +97,7 @@ def test_varlen_fwd_bwd_through_api(lengths, H):
         scale = D ** -0.5
         out = kernel(graph=graph, src={"key": k, "value": v}, dst={"query": q}, scale=scale)
         assert kernel.last_variant.backend == "hip"
-        assert kernel.last_variant.pattern == "varlen-causal"
+        assert kernel.last_variant.pattern == "block-attention"
         out.backward(dout)
         f = lambda t: t.detach().float().cpu().numpy()
         e_out, _ = ref.varlen_causal_fwd(cu, f(q), f(k), f(v), scale)

@@ -246,61 +246,65 @@ def test_kernel_csr_unifies_dtypes_and_rejects_bad_columns():
         bad_rp._kernel_csr()
 
 
-def _varlen_tasks(cu, H, block, kind):
+def _attn_tasks(cu_q, cu_k, H, block, kind, causal):
     n = ctypes.c_int64()
-    cu_h = np.ascontiguousarray(cu, dtype=np.int32)
-    _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, H, block, kind,
-                 None, ctypes.byref(n))
+    cq = np.ascontiguousarray(cu_q, dtype=np.int32)
+    ck = np.ascontiguousarray(cu_k, dtype=np.int32)
+    args = (cq.ctypes.data, ck.ctypes.data, cq.size - 1, H, block, kind, int(causal))
+    _native.call("tgx_attn_tasks", *args, None, ctypes.byref(n))
     tasks = np.zeros(4 * max(n.value, 1), dtype=np.int32)
-    _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, H, block, kind,
-                 tasks.ctypes.data, ctypes.byref(n))
+    _native.call("tgx_attn_tasks", *args, tasks.ctypes.data, ctypes.byref(n))
     return tasks[: 4 * n.value].reshape(n.value, 4)
 
 
 @pytest.mark.parametrize("kind,block", [(0, 128), (1, 64)])
-def test_varlen_tasks_cover_once_grouped_per_xcd(kind, block):
-    """Host-side work list of the varlen kernels: every (sequence, tile, head)
-    exactly once; all tiles of one (sequence, head) on one XCD (slot % 8),
+@pytest.mark.parametrize("causal,rect", [(True, False), (False, False), (False, True)])
+def test_attn_tasks_cover_once_grouped_per_xcd(kind, block, causal, rect):
+    """Host-side work list of the attention tiles: every (block, tile, head)
+    exactly once; all tiles of one (block, head) on one XCD (slot % 8),
     consecutive in that XCD's queue and heaviest first; XCD loads balanced."""
-    cu = np.array([0, 3, 300, 300, 301, 1500, 1700, 4000], dtype=np.int32)
+    cu_q = np.array([0, 3, 300, 300, 301, 1500, 1700, 4000], dtype=np.int32)
+    cu_k = (np.array([0, 10, 10, 90, 91, 1000, 1300, 1310], dtype=np.int32) if rect else cu_q)
     H = 3
-    t = _varlen_tasks(cu, H, block, kind)
+    t = _attn_tasks(cu_q, cu_k, H, block, kind, causal)
     assert t.shape[0] % 8 == 0
     real = t[t[:, 0] >= 0]
     assert (t[t[:, 0] < 0][:, 1:] == 0).all()
-    expect = sorted((s, r0, h) for s in range(len(cu) - 1) for h in range(H)
-                    for r0 in range(cu[s], cu[s + 1], block))
+    rows = cu_q if kind == 0 else cu_k
+    expect = sorted((b, r0, h) for b in range(len(rows) - 1) for h in range(H)
+                    for r0 in range(rows[b], rows[b + 1], block))
     assert sorted(map(tuple, real[:, :3].tolist())) == expect
     assert (real[:, 3] == 0).all()
 
-    def work(s, r0):
-        s0, s1 = int(cu[s]), int(cu[s + 1])
-        return min(r0 + block, s1) - s0 if kind == 0 else s1 - r0
+    def work(b, r0):
+        q0, q1, k0, k1 = (int(x) for x in (cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]))
+        if kind == 0:
+            return (min(r0 + block, q1) - k0) if causal else (k1 - k0)
+        return (q1 - r0) if causal else (q1 - q0)
 
     loads = [0] * 8
     for x in range(8):
         queue = [tuple(row[:3]) for row in t[x::8] if row[0] >= 0]
-        # padding only after the queue's end
         col = t[x::8, 0]
-        assert all(col[i] >= 0 for i in range(len(queue)))
+        assert all(col[i] >= 0 for i in range(len(queue)))   # padding only at the end
         groups = []
-        for s, r0, h in queue:
-            if not groups or groups[-1][0] != (s, h):
-                groups.append(((s, h), []))
-            groups[-1][1].append(work(s, r0))
-            loads[x] += work(s, r0)
-        keys = [g[0] for g in groups]
+        for b, r0, h in queue:
+            if not groups or groups[-1][0] != (b, h):
+                groups.append(((b, h), []))
+            groups[-1][1].append(work(b, r0))
+        keys = [gr[0] for gr in groups]
         assert len(keys) == len(set(keys)), "a group's tiles are split in the queue"
         for _, ws in groups:
             assert ws == sorted(ws, reverse=True)
-    # LPT balance: no XCD exceeds the mean by more than the largest group
+            loads[x] += max(sum(ws), 1)
     group_work = {}
-    for s, r0, h in expect:
-        group_work[(s, h)] = group_work.get((s, h), 0) + work(s, r0)
-    assert max(loads) - min(loads) <= max(group_work.values())
-    # every group's tiles sit on one XCD
+    for b, r0, h in expect:
+        group_work[(b, h)] = group_work.get((b, h), 0) + work(b, r0)
+    assert max(loads) - min(loads) <= max(max(group_work.values()), 1)
     where = {}
     for slot, row in enumerate(t):
         if row[0] >= 0:
             where.setdefault((row[0], row[2]), set()).add(slot % 8)
     assert all(len(v) == 1 for v in where.values())
+    with pytest.raises(RuntimeError, match="square"):
+        _attn_tasks(cu_q, np.array([0, 1, 2, 3, 4, 5, 6, 7]), H, block, kind, True)

@@ -252,6 +252,87 @@ def test_varlen_matches_dot_on_materialized_csr():
         np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
 
 
+def _dense_csr(n_dst, n_src, causal):
+    rows, cols = [0], []
+    for i in range(n_dst):
+        cols += list(range(min(i + 1, n_src) if causal else n_src))
+        rows.append(len(cols))
+    return np.asarray(rows), np.asarray(cols, dtype=np.int64)
+
+
+@pytest.mark.parametrize("n_dst,n_src,causal", [(7, 5, False), (6, 6, True), (3, 9, False)])
+def test_block_attention_matches_dot_on_materialized_dense(n_dst, n_src, causal):
+    """Graph.dense / Graph.triangular as one block: the tile oracle equals the
+    CSR oracle on the materialized relation, forward and backward."""
+    rng = np.random.default_rng(n_dst * 10 + n_src)
+    H, D = 2, 4
+    q = rng.standard_normal((n_dst, H, D))
+    k, v = (rng.standard_normal((n_src, H, D)) for _ in range(2))
+    rp, col = _dense_csr(n_dst, n_src, causal)
+    o1, l1 = ref.block_attention_fwd([0, n_dst], [0, n_src], q, k, v, 0.4, causal)
+    o2, l2 = ref.dot_fwd(rp, col, q, k, v, 0.4)
+    np.testing.assert_allclose(o1, o2, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(l1, l2, rtol=1e-12)
+    dout = rng.standard_normal((n_dst, H, D))
+    g1 = ref.block_attention_bwd([0, n_dst], [0, n_src], q, k, v, 0.4, causal, dout)
+    g2 = ref.dot_bwd(rp, col, q, k, v, 0.4, None, dout)[:3]
+    for a, b in zip(g1, g2):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
+    # non-causal varlen blocks equal the materialized cu_seqlens(causal=False)
+    cu = np.array([0, 3, 3, 7])
+    qv, kv, vv = (rng.standard_normal((7, H, D)) for _ in range(3))
+    rp, col = ref.cu_seqlens_csr(cu, causal=False)
+    o1, _ = ref.block_attention_fwd(cu, cu, qv, kv, vv, 0.4, False)
+    o2, _ = ref.dot_fwd(rp, col, qv, kv, vv, 0.4)
+    np.testing.assert_allclose(o1, o2, rtol=1e-12, atol=1e-12)
+
+
+def test_block_attention_bwd_finite_differences():
+    rng = np.random.default_rng(12)
+    q, k, v, g = (rng.standard_normal((4, 1, 3)) for _ in range(4))
+    grads = ref.block_attention_bwd([0, 4], [0, 4], q, k, v, 0.7, True, g)
+    eps = 1e-6
+    for t, dt in zip((q, k, v), grads):
+        for idx in np.ndindex(t.shape):
+            t[idx] += eps
+            fp = (ref.block_attention_fwd([0, 4], [0, 4], q, k, v, 0.7, True)[0] * g).sum()
+            t[idx] -= 2 * eps
+            fm = (ref.block_attention_fwd([0, 4], [0, 4], q, k, v, 0.7, True)[0] * g).sum()
+            t[idx] += eps
+            assert abs((fp - fm) / (2 * eps) - dt[idx]) < 1e-6
+
+
+def test_block_pruned_attention_known_answers():
+    """Tile admission (Translate.cpp:1793-1815) on hand-built scores: every
+    query is the same vector u and each 4-key tile holds +a u or -a u keys, so
+    every score of a tile is equal and the admitted set is known."""
+    D, a, scale = 4, 3.0, 0.5
+    u = np.ones(D)
+    q = np.tile(u, (8, 1, 1))                       # 8 queries, H = 1
+    signs = [+1, -1, +1]                             # three tiles of 4 keys
+    k = np.concatenate([np.tile(s * a * u, (4, 1, 1)) for s in signs])
+    v = np.arange(12 * D, dtype=np.float64).reshape(12, 1, D)
+    # tile 1's log2 scores trail tile 0's by 2*a*|u|^2*scale*log2(e) = 17.3
+    thr = 2.0 ** -10
+    out, lse = ref.block_pruned_attention_fwd([0, 8], [0, 12], q, k, v, scale, thr, False,
+                                              block_m=8, block_n=4)
+    expect = v[[0, 1, 2, 3, 8, 9, 10, 11], 0].mean(0)          # tiles 0 and 2, equal weights
+    np.testing.assert_allclose(out[:, 0], np.tile(expect, (8, 1)), rtol=1e-12)
+    np.testing.assert_allclose(lse[:, 0], a * D * scale + np.log(8.0), rtol=1e-12)
+    # a threshold the gap passes admits everything: exact softmax
+    exact = ref.block_attention_fwd([0, 8], [0, 12], q, k, v, scale, False)
+    loose = ref.block_pruned_attention_fwd([0, 8], [0, 12], q, k, v, scale, 2.0 ** -20, False,
+                                           block_m=8, block_n=4)
+    np.testing.assert_allclose(loose[0], exact[0], rtol=1e-12)
+    # order matters: a low first tile is always admitted (running max -inf)
+    k2 = k[[4, 5, 6, 7, 0, 1, 2, 3, 8, 9, 10, 11]]
+    v2 = v[[4, 5, 6, 7, 0, 1, 2, 3, 8, 9, 10, 11]]
+    out2, _ = ref.block_pruned_attention_fwd([0, 8], [0, 12], q, k2, v2, scale, thr, False,
+                                             block_m=8, block_n=4)
+    exact2 = ref.block_attention_fwd([0, 8], [0, 12], q, k2, v2, scale, False)[0]
+    np.testing.assert_allclose(out2, exact2, rtol=1e-12)
+
+
 # ---- planner ---------------------------------------------------------------
 
 @pytest.mark.parametrize("case", GOLD["planner"], ids=lambda c: c["cite"].split(":")[0].split("/")[-1])

@@ -1,17 +1,26 @@
-// Varlen causal attention on MFMA (gfx950, bf16 in, fp32 accumulate).
+// Dense attention tiles on MFMA (gfx950, bf16 or fp16 in, fp32 accumulate)
+// over block-diagonal relations: block k relates queries
+// [cu_q[k], cu_q[k+1]) to keys [cu_k[k], cu_k[k+1]), either every pair
+// (causal = false) or key <= query (causal = true, cu_q == cu_k).
 //
-// The relation is Graph.cu_seqlens(causal=True) (reference
-// python/tiga/interop/torch/graph.py:260-294): token i of sequence k attends
-// to keys [s_k, i].  The edge function is the dot-product score
-// scale * q[i].k[j] with value v[j]; the reference evaluates it on its eager
-// oracle (examples/varlen_causal_attention.py:46-48) and its only compiled
-// streaming tile is dense/triangular fp16 forward (lib/Target/Triton/
-// Translate.cpp:1603-1912).  Here it stays implicit (no materialized CSR).
+// Relations covered (reference python/tiga/interop/torch/graph.py):
+//   Graph.cu_seqlens(causal=True/False)  (:260-294)  varlen, cu_q = cu_k
+//   Graph.dense(num_src, num_dst)        (:535-574)  one block, all pairs
+//   Graph.triangular(n)                  (:576-592)  one block, key <= query
+// The edge function is the dot-product score scale * q[i].k[j] with value
+// v[j] under online softmax; the reference evaluates varlen on its eager
+// oracle (examples/varlen_causal_attention.py) and dense/triangular with one
+// compiled fp16 streaming forward tile (lib/Target/Triton/Translate.cpp:
+// 1603-1912), whose optional block pruning (:1760-1860) this file restates.
+// The relation stays implicit (no materialized CSR).
 //
-// Layout: q, k, v, out, dout are [T, H, 128] bf16 (token-major); lse and
-// delta are [T, H] fp32.
+// Layout: q, k, v are [N, H, D] with element strides (sn, sh, 1), one pair
+// for q and one shared by k and v (contiguous [N, H, D], or [H, N, D] storage
+// viewed as [N, H, D]);
+// out, dout, dq, dk, dv are contiguous [N, H, D]; lse and delta are [N, H]
+// fp32.  D is 64 or 128.
 //
-// MFMA: v_mfma_f32_16x16x32_bf16 with lane l, g = l / 16:
+// MFMA: v_mfma_f32_16x16x32_{bf16,f16} with lane l, g = l / 16:
 //   A[i = l % 16][k = 8g + j], B[k = 8g + j][n = l % 16], C[4g + r][n = l % 16].
 // The forward computes S^T = K Q^T, so each lane's accumulators hold 4 keys of
 // one query; two 16-key tiles together are exactly the B operand of
@@ -39,19 +48,37 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-constexpr int VD = 128;    // head dim
+template <typename T>
+struct Vec;
+template <>
+struct Vec<__bf16> {
+  typedef bf16x8 v8;
+  typedef bf16x4 v4;
+};
+template <>
+struct Vec<_Float16> {
+  typedef f16x8 v8;
+  typedef f16x4 v4;
+};
+template <typename T>
+using vec8 = typename Vec<T>::v8;
+template <typename T>
+using vec4 = typename Vec<T>::v4;
+
 constexpr int VBM = 128;   // queries per workgroup (4 waves x 32)
 constexpr int VBN = 64;    // keys per iteration
-// LDS row stride (bf16) of every staged tile: 288 B rows keep both the 16 B
-// row-fragment reads and the transposing 8 B reads free of bank conflicts
-// (measured: SQ_LDS_BANK_CONFLICT = 0).
+// LDS row stride (elements) of every staged tile: 288 B rows keep both the
+// 16 B row-fragment reads and the transposing 8 B reads free of bank
+// conflicts (measured: SQ_LDS_BANK_CONFLICT = 0).  D = 64 uses the first half
+// of each row.
 constexpr int TPAD = 144;
-constexpr int KPAD = TPAD;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 // gfx950 (MI355X) has 8 XCDs, each with its own L2; workgroup i of a launch
@@ -61,41 +88,13 @@ constexpr int kXcds = 8;
 __device__ __forceinline__ f32x4v mfma(bf16x8 a, bf16x8 b, f32x4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-
-__device__ __forceinline__ bf16x8 ld_bf16x8(const __bf16* p) {
-  return *reinterpret_cast<const bf16x8*>(p);
+__device__ __forceinline__ f32x4v mfma(f16x8 a, f16x8 b, f32x4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-struct VarlenFwdArgs {
-  const int32_t* cu;      // [n_seq + 1]
-  const int32_t* tasks;   // [n_tasks, 4] = (sequence, first query, head, 0)
-  int H;
-  const __bf16* q;
-  const __bf16* k;
-  const __bf16* v;
-  __bf16* out;
-  float* lse;             // [T, H]
-  float scale_log2;       // softmax scale * log2(e)
-};
-
-// Stage one 64-key tile: thread t holds 4 rows x 16 B of K and of V.  Rows
-// past the sequence end are clamped to its last row (finite values whose
-// scores the causal mask removes), so the loads need no branches; every tile
-// handed to a workgroup has at least one key (s1 > s0).
-struct KvStage {
-  bf16x8 k[4], v[4];
-};
-
-__device__ __forceinline__ void load_kv(KvStage& st, const __bf16* kb, const __bf16* vb,
-                                        int64_t row_stride, int kbase, int s1) {
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int idx = threadIdx.x + 256 * it;
-    const int key = min(kbase + (idx >> 4), s1 - 1);
-    const int64_t off = static_cast<int64_t>(key) * row_stride + (idx & 15) * 8;
-    st.k[it] = ld_bf16x8(kb + off);
-    st.v[it] = ld_bf16x8(vb + off);
-  }
+template <typename T>
+__device__ __forceinline__ vec8<T> ld8(const T* p) {
+  return *reinterpret_cast<const vec8<T>*>(p);
 }
 
 // Max / sum of a value over the four 16-lane groups (lanes l, l^16, l^32,
@@ -127,15 +126,48 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // normalisation, and the O rescale is skipped for nearly every tile.
 constexpr float kRescaleLog2 = 8.f;
 
-__device__ __forceinline__ void store_kv(const KvStage& st, __bf16 (*ks)[KPAD],
-                                         __bf16 (*vs)[TPAD]) {
+// Staging of one 64-row block of two [N, H, D] tensors by 256 threads:
+// thread t holds D / 32 chunks of 16 B of each.  Rows at or past `end` are
+// clamped to row end - 1 (finite values the caller masks; every staged
+// block has end > base) when CLAMP, else zero-filled.
+template <typename T, int D>
+struct Stage {
+  static constexpr int N = D / 32;
+  vec8<T> a[N], b[N];
+};
+
+template <typename T, int D, bool CLAMP>
+__device__ __forceinline__ void stage_load(Stage<T, D>& st, const T* xa, int64_t sa,
+                                           const T* xb, int64_t sb, int base, int end) {
+  constexpr int CPR = D / 8;   // 16-byte chunks per row
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
+  for (int it = 0; it < Stage<T, D>::N; ++it) {
     const int idx = threadIdx.x + 256 * it;
-    const int key = idx >> 4;
-    const int dc = idx & 15;
-    *reinterpret_cast<bf16x8*>(&ks[key][dc * 8]) = st.k[it];
-    *reinterpret_cast<bf16x8*>(&vs[key][dc * 8]) = st.v[it];
+    const int row = base + idx / CPR;
+    const int dc = (idx % CPR) * 8;
+    if (CLAMP) {
+      const int64_t r = min(row, end - 1);
+      st.a[it] = ld8(xa + r * sa + dc);
+      st.b[it] = ld8(xb + r * sb + dc);
+    } else if (row < end) {
+      st.a[it] = ld8(xa + static_cast<int64_t>(row) * sa + dc);
+      st.b[it] = ld8(xb + static_cast<int64_t>(row) * sb + dc);
+    } else {
+      st.a[it] = vec8<T>{};
+      st.b[it] = vec8<T>{};
+    }
+  }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void stage_store(const Stage<T, D>& st, T (*ra)[TPAD],
+                                            T (*rb)[TPAD]) {
+  constexpr int CPR = D / 8;
+#pragma unroll
+  for (int it = 0; it < Stage<T, D>::N; ++it) {
+    const int idx = threadIdx.x + 256 * it;
+    *reinterpret_cast<vec8<T>*>(&ra[idx / CPR][(idx % CPR) * 8]) = st.a[it];
+    *reinterpret_cast<vec8<T>*>(&rb[idx / CPR][(idx % CPR) * 8]) = st.b[it];
   }
 }
 
@@ -143,177 +175,228 @@ __device__ __forceinline__ void store_kv(const KvStage& st, __bf16 (*ks)[KPAD],
 // LDS tile X[row][col] with row stride TPAD: lane (lr, g) receives
 // X[r0 + 4g + j][c0 + lr] for j < 4 and X[r0 + 16 + 4g + j - 4][c0 + lr] for
 // j >= 4, i.e. 8 rows of one column in the permuted order of the B operand.
-__device__ __forceinline__ bf16x8 tr_frag(__bf16 (*x)[TPAD], int r0, int c0, int lr, int g) {
-  const __bf16* p = &x[r0 + 4 * g + (lr >> 2)][c0 + 4 * (lr & 3)];
+template <typename T>
+__device__ __forceinline__ vec8<T> tr_frag(T (*x)[TPAD], int r0, int c0, int lr, int g) {
+  const T* p = &x[r0 + 4 * g + (lr >> 2)][c0 + 4 * (lr & 3)];
   const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
   const i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 16 * TPAD));
   // Assemble at dword granularity (elements 0-3 from a, 4-7 from b).
   const u32x2 aw = __builtin_bit_cast(u32x2, a);
   const u32x2 bw = __builtin_bit_cast(u32x2, b);
   const u32x4 w = {aw[0], aw[1], bw[0], bw[1]};
-  return __builtin_bit_cast(bf16x8, w);
+  return __builtin_bit_cast(vec8<T>, w);
 }
 
-__global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
-  __shared__ __bf16 ks[2][VBN][KPAD];
-  __shared__ __bf16 vs[2][VBN][TPAD];
+// ---------------------------------------------------------------------------
+// Forward
+
+template <typename T>
+struct FwdArgs {
+  const int32_t* cu_q;    // [n_blocks + 1] query ranges
+  const int32_t* cu_k;    // [n_blocks + 1] key ranges
+  const int32_t* tasks;   // [n_tasks, 4] = (block, first query, head, 0)
+  int H;
+  const T* q;
+  const T* k;
+  const T* v;
+  int64_t qsn, qsh;       // element strides of q (token, head)
+  int64_t ksn, ksh;       // element strides of k and v
+  T* out;                 // [n_q, H, D]
+  float* lse;             // [n_q, H]
+  float scale_log2;       // softmax scale * log2(e)
+  float prune_log2;       // log2(block_prune_threshold) (PRUNE only)
+};
+
+template <typename T, int D, bool CAUSAL, bool PRUNE>
+__global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
+  constexpr int KC = D / 32;   // contraction steps of S over D
+  constexpr int DT = D / 16;   // 16-row tiles of O^T
+  __shared__ T ks[2][VBN][TPAD];
+  __shared__ T vs[2][VBN][TPAD];
+  __shared__ float wave_max[PRUNE ? 4 : 1];
   const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
-  const int seq = task[0];
-  if (seq < 0) return;   // padding slot of a shorter XCD queue
+  const int blk = task[0];
+  if (blk < 0) return;   // padding slot of a shorter XCD queue
   const int q0 = task[1];
   const int h = task[2];
-  const int s0 = a.cu[seq], s1 = a.cu[seq + 1];
+  const int qs1 = a.cu_q[blk + 1];
+  const int ks0 = a.cu_k[blk], ks1 = a.cu_k[blk + 1];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, lr = lane & 15;
-  const int64_t row_stride = static_cast<int64_t>(a.H) * VD;
-  const __bf16* qh = a.q + h * VD;
-  const __bf16* kh = a.k + h * VD;
-  const __bf16* vh = a.v + h * VD;
+  const T* qh = a.q + h * a.qsh;
+  const T* kh = a.k + h * a.ksh;
+  const T* vh = a.v + h * a.ksh;
   const int qb = q0 + wave * 32;
 
-  // Q^T fragments (B operand): lane holds Q[q = qb + 16 qt + lr][32 ks + 8g .. +8].
-  bf16x8 qf[2][4];
+  // Q^T fragments (B operand): lane holds Q[q = qb + 16 qt + lr][32 kc + 8g .. +8].
+  vec8<T> qf[2][KC];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int qq = qb + 16 * qt + lr;
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc)
-      qf[qt][kc] = qq < s1 ? ld_bf16x8(qh + qq * row_stride + 32 * kc + 8 * g) : bf16x8{};
+    for (int kc = 0; kc < KC; ++kc)
+      qf[qt][kc] = qq < qs1 ? ld8(qh + qq * a.qsn + 32 * kc + 8 * g) : vec8<T>{};
   }
 
-  const int kv_end = (q0 + VBM < s1) ? q0 + VBM : s1;
-  const int n_kv = (kv_end - s0 + VBN - 1) / VBN;
+  const int kv_end = CAUSAL ? min(q0 + VBM, ks1) : ks1;
+  const int n_kv = (kv_end - ks0 + VBN - 1) / VBN;
   const float sl2 = a.scale_log2;
   // Running max in scaled log2 units (-inf until a score is seen); lp is this
   // lane's share of the softmax denominator.
   float m[2] = {kNegInf, kNegInf};
   float lp[2] = {0.f, 0.f};
-  // Last unmasked key of each query row (padded rows past s1 use s1 - 1).
+  // Last key each query row may see (padded rows past the block use the
+  // last key, their output is discarded).
   int qlim[2];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) qlim[qt] = min(qb + 16 * qt + lr, s1 - 1);
-  f32x4v o[8][2];
+  for (int qt = 0; qt < 2; ++qt)
+    qlim[qt] = CAUSAL ? min(qb + 16 * qt + lr, ks1 - 1) : ks1 - 1;
+  f32x4v o[DT][2];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) o[dt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  // Running max over the whole workgroup tile (PRUNE), scaled log2 units.
+  float block_m = kNegInf;
 
-  KvStage stage;
-  load_kv(stage, kh, vh, row_stride, s0, s1);
-  store_kv(stage, ks[0], vs[0]);
+  Stage<T, D> stage;
+  if (n_kv > 0) {
+    stage_load<T, D, true>(stage, kh, a.ksn, vh, a.ksn, ks0, ks1);
+    stage_store<T, D>(stage, ks[0], vs[0]);
+  }
   for (int it = 0; it < n_kv; ++it) {
     __syncthreads();
     const int buf = it & 1;
-    const int kbase = s0 + it * VBN;
+    const int kbase = ks0 + it * VBN;
     const bool more = it + 1 < n_kv;
-    if (more) load_kv(stage, kh, vh, row_stride, kbase + VBN, s1);
+    if (more) stage_load<T, D, true>(stage, kh, a.ksn, vh, a.ksn, kbase + VBN, ks1);
 
     // A wave whose 32 queries all precede this key tile has nothing to add.
-    if (kbase <= qb + 31) {
-    // S^T = K Q^T over D = 128 (4 k-steps of 32).
+    const bool active = !CAUSAL || kbase <= qb + 31;
     f32x4v c[4][2];
+    float mt[2] = {kNegInf, kNegInf};
+    if (active) {
+      // S^T = K Q^T over D (k-steps of 32).
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) c[kt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        for (int qt = 0; qt < 2; ++qt) c[kt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
+      for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const bf16x8 kf = ld_bf16x8(&ks[buf][16 * kt + lr][32 * kc + 8 * g]);
+        for (int kt = 0; kt < 4; ++kt) {
+          const vec8<T> kf = ld8(&ks[buf][16 * kt + lr][32 * kc + 8 * g]);
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) c[kt][qt] = mfma(kf, qf[qt][kc], c[kt][qt]);
+          for (int qt = 0; qt < 2; ++qt) c[kt][qt] = mfma(kf, qf[qt][kc], c[kt][qt]);
+        }
       }
-    }
-
-    // Causal/sequence mask (diagonal and last tiles only), then the tile max
-    // of the raw scores (scale > 0, so scaling commutes with max).
-    if (kbase + VBN > qb || kbase + VBN > s1) {
+      // Causal/sequence mask (diagonal and last tiles only), then the tile
+      // max of the raw scores (scale > 0, so scaling commutes with max).
+      const bool edge = CAUSAL ? (kbase + VBN > qb || kbase + VBN > ks1) : kbase + VBN > ks1;
+      if (edge) {
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (kbase + 16 * kt + 4 * g + r > qlim[qt]) c[kt][qt][r] = kNegInf;
+      }
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        float x = kNegInf;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (kbase + 16 * kt + 4 * g + r > qlim[qt]) c[kt][qt][r] = kNegInf;
+          for (int r = 0; r < 4; ++r) x = fmaxf(x, c[kt][qt][r]);
+        mt[qt] = group4_max(x) * sl2;
+      }
     }
-    float mt[2];
-    bool grow = false;
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      float x = kNegInf;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) x = fmaxf(x, c[kt][qt][r]);
-      mt[qt] = group4_max(x) * sl2;
-      grow |= mt[qt] > m[qt] + kRescaleLog2;
+    bool admit = active;
+    if constexpr (PRUNE) {
+      // Tile admission (Translate.cpp:1793-1815): the tile's max over the
+      // whole query block against the block's running max; a tile whose
+      // best weight is below threshold x the best weight so far is skipped.
+      const float wm = group_max<16>(fmaxf(mt[0], mt[1]));
+      if (lane == 0) wave_max[wave] = wm;
+      __syncthreads();
+      const float tile_m =
+          fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+      const bool skip = tile_m - block_m < a.prune_log2;
+      if (!skip) block_m = fmaxf(block_m, tile_m);
+      admit = admit && !skip;
     }
-    if (__any(grow)) {
+    if (admit) {
+      bool grow = false;
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) grow |= mt[qt] > m[qt] + kRescaleLog2;
+      if (__any(grow)) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          const float mn = fmaxf(m[qt], mt[qt]);
+          const float alpha = mn == kNegInf ? 1.f : exp2_hw(m[qt] - mn);
+          lp[qt] *= alpha;
+          m[qt] = mn;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) o[dt][qt] *= alpha;
+        }
+      }
+      vec8<T> pf[2][2];
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        const float mn = fmaxf(m[qt], mt[qt]);
-        const float alpha = mn == kNegInf ? 1.f : exp2_hw(m[qt] - mn);
-        lp[qt] *= alpha;
-        m[qt] = mn;
+        const float mo = m[qt] == kNegInf ? 0.f : m[qt];
+        float p[4][4];
+        float rs = 0.f;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[kt][r] = exp2_hw(c[kt][qt][r] * sl2 - mo);
+            rs += p[kt][r];
+          }
+        lp[qt] += rs;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            pf[qt][k2][j] = static_cast<T>(p[2 * k2][j]);
+            pf[qt][k2][4 + j] = static_cast<T>(p[2 * k2 + 1][j]);
+          }
+      }
+      // O^T += V^T P^T over the 64 keys (2 k-steps of 32).
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const vec8<T> vf = tr_frag(vs[buf], 32 * k2, 16 * dt, lr, g);
+#pragma unroll
+          for (int qt = 0; qt < 2; ++qt) o[dt][qt] = mfma(vf, pf[qt][k2], o[dt][qt]);
+        }
       }
     }
-    bf16x8 pf[2][2];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const float mo = m[qt] == kNegInf ? 0.f : m[qt];
-      float p[4][4];
-      float rs = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[kt][r] = exp2_hw(c[kt][qt][r] * sl2 - mo);
-          rs += p[kt][r];
-        }
-      lp[qt] += rs;
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          pf[qt][k2][j] = static_cast<__bf16>(p[2 * k2][j]);
-          pf[qt][k2][4 + j] = static_cast<__bf16>(p[2 * k2 + 1][j]);
-        }
-    }
-
-    // O^T += V^T P^T over the 64 keys (2 k-steps of 32).
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const bf16x8 vf = tr_frag(vs[buf], 32 * k2, 16 * dt, lr, g);
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) o[dt][qt] = mfma(vf, pf[qt][k2], o[dt][qt]);
-      }
-    }
-    }
-    if (more) store_kv(stage, ks[buf ^ 1], vs[buf ^ 1]);
+    if (more) stage_store<T, D>(stage, ks[buf ^ 1], vs[buf ^ 1]);
   }
 
-  // Finalize: l summed over the 4 lane groups, O = O^T / l, natural-log lse.
+  // Finalize: l summed over the 4 lane groups, O = O^T / l, natural-log lse
+  // (a row that sees no key gets 0 and -inf).
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const float l = group4_sum(lp[qt]);
     const int qq = qb + 16 * qt + lr;
-    if (qq >= s1) continue;
-    const float inv = 1.f / l;
-    __bf16* orow = a.out + qq * row_stride + h * VD;
+    if (qq >= qs1) continue;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    T* orow = a.out + (static_cast<int64_t>(qq) * a.H + h) * D;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      bf16x4 w;
+    for (int dt = 0; dt < DT; ++dt) {
+      vec4<T> w;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) w[r] = static_cast<__bf16>(o[dt][qt][r] * inv);
-      *reinterpret_cast<bf16x4*>(orow + 16 * dt + 4 * g) = w;
+      for (int r = 0; r < 4; ++r) w[r] = static_cast<T>(o[dt][qt][r] * inv);
+      *reinterpret_cast<vec4<T>*>(orow + 16 * dt + 4 * g) = w;
     }
-    if (g == 0) a.lse[static_cast<int64_t>(qq) * a.H + h] = (m[qt] + __log2f(l)) * kLn2;
+    if (g == 0)
+      a.lse[static_cast<int64_t>(qq) * a.H + h] = l > 0.f ? (m[qt] + __log2f(l)) * kLn2
+                                                           : kNegInf;
   }
 }
 
@@ -321,153 +404,129 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(VarlenFwdArgs a) {
 // Backward.  Three launches, no atomics:
 //   delta[t, h] = <dout, out>;
 //   dK/dV: one workgroup per 64-key tile (4 waves x 16 keys), looping over
-//          64-query blocks q >= key; S = Q K^T and dP = dO V^T give P and dS
-//          in C layout [q][key], which (two q-tiles, permuted) is directly the
-//          B operand of dV^T = dO^T P and dK^T = Q^T dS;
+//          64-query blocks (q >= key when causal); S = Q K^T and dP = dO V^T
+//          give P and dS in C layout [q][key], which (two q-tiles, permuted)
+//          is directly the B operand of dV^T = dO^T P and dK^T = Q^T dS;
 //   dQ:    one workgroup per 128-query tile like the forward; S^T = K Q^T and
 //          dP^T = V dO^T give dS^T, the B operand of dQ^T = K^T dS^T.
 // dO^T, Q^T and K^T operands are staged transposed in LDS in the same
 // permuted order as V^T in the forward.
 
-struct VarlenBwdArgs {
-  const int32_t* cu;
-  const int32_t* tasks;   // [n_tasks, 4] = (sequence, first key or query, head, 0)
+template <typename T>
+struct BwdArgs {
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* tasks;   // [n_tasks, 4] = (block, first key or query, head, 0)
   int H;
-  const __bf16* q;
-  const __bf16* k;
-  const __bf16* v;
-  const __bf16* dout;
-  const float* lse;       // [T, H]
-  const float* delta;     // [T, H]
-  __bf16* dq;
-  __bf16* dk;
-  __bf16* dv;
+  const T* q;
+  const T* k;
+  const T* v;
+  int64_t qsn, qsh;       // element strides of q
+  int64_t ksn, ksh;       // element strides of k and v
+  const T* dout;          // contiguous [n_q, H, D]
+  const float* lse;       // [n_q, H]
+  const float* delta;     // [n_q, H]
+  T* dq;
+  T* dk;
+  T* dv;
   float scale;            // softmax scale
   float scale_log2;       // scale * log2(e)
 };
 
-__global__ __launch_bounds__(256) void varlen_delta_kernel(const __bf16* __restrict__ dout,
-                                                           const __bf16* __restrict__ out,
+template <typename T, int D>
+__global__ __launch_bounds__(256) void varlen_delta_kernel(const T* __restrict__ dout,
+                                                           const T* __restrict__ out,
                                                            float* __restrict__ delta,
-                                                           int64_t T, int H) {
-  // One wave per (token, group of 4 heads): lane l covers 8 elements of head
-  // 4 * blockpart + l / 16.
+                                                           int64_t n, int H) {
+  // One wave per (token, group of heads): a head spans D / 8 lanes of 8
+  // elements each.
+  constexpr int LPH = D / 8;
+  constexpr int HPW = kWave / LPH;
   const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int groups = (H + 3) / 4;
+  const int groups = (H + HPW - 1) / HPW;
   const int64_t t = wid / groups;
   const int hg = static_cast<int>(wid - t * groups);
-  if (t >= T) return;
+  if (t >= n) return;
   const int lane = threadIdx.x & 63;
-  const int h = 4 * hg + (lane >> 4);
+  const int h = HPW * hg + lane / LPH;
   float s = 0.f;
   if (h < H) {
-    const int64_t off = (t * H + h) * VD + (lane & 15) * 8;
-    const bf16x8 a = ld_bf16x8(dout + off);
-    const bf16x8 b = ld_bf16x8(out + off);
+    const int64_t off = (t * H + h) * D + (lane % LPH) * 8;
+    const vec8<T> x = ld8(dout + off);
+    const vec8<T> y = ld8(out + off);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += static_cast<float>(a[j]) * static_cast<float>(b[j]);
+    for (int j = 0; j < 8; ++j) s += static_cast<float>(x[j]) * static_cast<float>(y[j]);
   }
-  s = group_sum<16>(s);
-  if (h < H && (lane & 15) == 0) delta[t * H + h] = s;
-}
-
-// Staging of one 64-row block of two [T, H, 128] tensors: thread t holds 4
-// rows x 16 B of each (rows beyond `end` are zero).
-struct Stage2 {
-  bf16x8 a[4], b[4];
-};
-
-__device__ __forceinline__ void load2(Stage2& st, const __bf16* xa, const __bf16* xb,
-                                      int64_t row_stride, int base, int end) {
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int idx = threadIdx.x + 256 * it;
-    const int row = idx >> 4;
-    const int dc = idx & 15;
-    if (base + row < end) {
-      const int64_t off = static_cast<int64_t>(base + row) * row_stride + dc * 8;
-      st.a[it] = ld_bf16x8(xa + off);
-      st.b[it] = ld_bf16x8(xb + off);
-    } else {
-      st.a[it] = bf16x8{};
-      st.b[it] = bf16x8{};
-    }
-  }
-}
-
-// Row-major copies of the two staged tensors (either may be skipped).
-template <int SA, int SB>
-__device__ __forceinline__ void store2(const Stage2& st, __bf16 (*ra)[SA], __bf16 (*rb)[SB]) {
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int idx = threadIdx.x + 256 * it;
-    const int row = idx >> 4;
-    const int dc = idx & 15;
-    *reinterpret_cast<bf16x8*>(&ra[row][dc * 8]) = st.a[it];
-    *reinterpret_cast<bf16x8*>(&rb[row][dc * 8]) = st.b[it];
-  }
+  s = group_sum<LPH>(s);
+  if (h < H && lane % LPH == 0) delta[t * H + h] = s;
 }
 
 // dK/dV: workgroup = (64-key tile, head); wave w owns keys k0 + 16w .. +16.
-__global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
-  __shared__ __bf16 qs[VBN][TPAD];    // Q rows of the query block
-  __shared__ __bf16 dos[VBN][TPAD];   // dO rows
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
+  constexpr int KC = D / 32;
+  constexpr int DT = D / 16;
+  __shared__ T qs[VBN][TPAD];    // Q rows of the query block
+  __shared__ T dos[VBN][TPAD];   // dO rows
   __shared__ float lse_s[VBN], del_s[VBN];
   const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
-  const int seq = task[0];
-  if (seq < 0) return;   // padding slot of a shorter XCD queue
+  const int blk = task[0];
+  if (blk < 0) return;   // padding slot of a shorter XCD queue
   const int k0 = task[1];
   const int h = task[2];
-  const int s1 = a.cu[seq + 1];
+  const int qs0 = a.cu_q[blk], qs1 = a.cu_q[blk + 1];
+  const int ks1 = a.cu_k[blk + 1];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, lr = lane & 15;
-  const int64_t row_stride = static_cast<int64_t>(a.H) * VD;
+  const int64_t cs = static_cast<int64_t>(a.H) * D;   // contiguous token stride
   const int key = k0 + 16 * wave + lr;   // this lane's key (B operand column)
 
   // K^T and V^T fragments (B operands): K[key][32 kc + 8g .. +8].
-  bf16x8 kf[4], vf[4];
+  vec8<T> kf[KC], vf[KC];
 #pragma unroll
-  for (int kc = 0; kc < 4; ++kc) {
-    if (key < s1) {
-      kf[kc] = ld_bf16x8(a.k + key * row_stride + h * VD + 32 * kc + 8 * g);
-      vf[kc] = ld_bf16x8(a.v + key * row_stride + h * VD + 32 * kc + 8 * g);
+  for (int kc = 0; kc < KC; ++kc) {
+    if (key < ks1) {
+      kf[kc] = ld8(a.k + key * a.ksn + h * a.ksh + 32 * kc + 8 * g);
+      vf[kc] = ld8(a.v + key * a.ksn + h * a.ksh + 32 * kc + 8 * g);
     } else {
-      kf[kc] = bf16x8{};
-      vf[kc] = bf16x8{};
+      kf[kc] = vec8<T>{};
+      vf[kc] = vec8<T>{};
     }
   }
-  f32x4v dkt[8], dvt[8];   // dK^T / dV^T tiles [d = 16 dt + 4g + r][key]
+  f32x4v dkt[DT], dvt[DT];   // dK^T / dV^T tiles [d = 16 dt + 4g + r][key]
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
+  for (int dt = 0; dt < DT; ++dt) {
     dkt[dt] = f32x4v{0.f, 0.f, 0.f, 0.f};
     dvt[dt] = f32x4v{0.f, 0.f, 0.f, 0.f};
   }
-  const __bf16* qh = a.q + h * VD;
-  const __bf16* doh = a.dout + h * VD;
-  // Query blocks run last to first: every key tile of a (sequence, head)
-  // starts on the sequence's last block, so tiles that run together (they
-  // are queued together on one XCD) read each block at about the same time
-  // and share it through L2.
-  const int n_qb = (s1 - k0 + VBN - 1) / VBN;
-  Stage2 st;
-  load2(st, qh, doh, row_stride, k0 + (n_qb - 1) * VBN, s1);
+  const T* qh = a.q + h * a.qsh;
+  const T* doh = a.dout + h * D;
+  // Queries that see the tile: from the tile's first key (causal) or the
+  // block's first query.  Blocks run last to first: every key tile of a
+  // (block, head) starts on the same last query block, so tiles that run
+  // together (queued together on one XCD) read each block at about the same
+  // time and share it through L2.
+  const int qstart = CAUSAL ? k0 : qs0;
+  const int n_qb = (qs1 - qstart + VBN - 1) / VBN;
+  Stage<T, D> st;
+  if (n_qb > 0)
+    stage_load<T, D, false>(st, qh, a.qsn, doh, cs, qstart + (n_qb - 1) * VBN, qs1);
   for (int step = 0; step < n_qb; ++step) {
     const int ib = n_qb - 1 - step;
-    const int qbase = k0 + ib * VBN;
+    const int qbase = qstart + ib * VBN;
     __syncthreads();   // previous block's LDS reads are done
-    store2<TPAD, TPAD>(st, qs, dos);
+    stage_store<T, D>(st, qs, dos);
     if (threadIdx.x < VBN) {
       const int qq = qbase + threadIdx.x;
-      lse_s[threadIdx.x] = qq < s1 ? a.lse[static_cast<int64_t>(qq) * a.H + h] * kLog2e
-                                   : __builtin_huge_valf();
-      del_s[threadIdx.x] = qq < s1 ? a.delta[static_cast<int64_t>(qq) * a.H + h] : 0.f;
+      lse_s[threadIdx.x] = qq < qs1 ? a.lse[static_cast<int64_t>(qq) * a.H + h] * kLog2e
+                                    : __builtin_huge_valf();
+      del_s[threadIdx.x] = qq < qs1 ? a.delta[static_cast<int64_t>(qq) * a.H + h] : 0.f;
     }
     __syncthreads();
-    if (ib > 0) load2(st, qh, doh, row_stride, qbase - VBN, s1);
-    // Keys of this wave that precede every query of the block all count;
-    // a wave whose keys all exceed the block's last query skips it.
-    if (k0 + 16 * wave > qbase + VBN - 1) continue;
+    if (ib > 0) stage_load<T, D, false>(st, qh, a.qsn, doh, cs, qbase - VBN, qs1);
+    // Causal: a wave whose keys all exceed the block's last query skips it.
+    if (CAUSAL && k0 + 16 * wave > qbase + VBN - 1) continue;
 
     // S = Q K^T, dP = dO V^T: C tiles [q = 16 qt + 4g + r][key].
     f32x4v sc[4], dp[4];
@@ -477,19 +536,19 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
       dp[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
+    for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
       for (int qt = 0; qt < 4; ++qt) {
-        const bf16x8 qa = ld_bf16x8(&qs[16 * qt + lr][32 * kc + 8 * g]);
-        const bf16x8 da = ld_bf16x8(&dos[16 * qt + lr][32 * kc + 8 * g]);
+        const vec8<T> qa = ld8(&qs[16 * qt + lr][32 * kc + 8 * g]);
+        const vec8<T> da = ld8(&dos[16 * qt + lr][32 * kc + 8 * g]);
         sc[qt] = mfma(qa, kf[kc], sc[qt]);
         dp[qt] = mfma(da, vf[kc], dp[qt]);
       }
     }
     // P = exp(S*scale - lse), dS = P (dP - delta); packed per 32-query step.
-    // Only the first block holds queries that precede keys of the tile, so
-    // only it is masked (padded queries have lse = +inf, so P = 0).
-    bf16x8 pb[2], sb[2];
+    // Causal: only the first block holds queries that precede keys of the
+    // tile, so only it is masked (padded queries have lse = +inf, so P = 0).
+    vec8<T> pb[2], sb[2];
     auto weights = [&](auto masked) {
 #pragma unroll
       for (int qt = 0; qt < 4; ++qt) {
@@ -499,12 +558,12 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
           float p = exp2_hw(sc[qt][r] * a.scale_log2 - lse_s[qi]);
           if (decltype(masked)::value && qbase + qi < key) p = 0.f;
           const float ds = p * (dp[qt][r] - del_s[qi]);
-          pb[qt >> 1][4 * (qt & 1) + r] = static_cast<__bf16>(p);
-          sb[qt >> 1][4 * (qt & 1) + r] = static_cast<__bf16>(ds);
+          pb[qt >> 1][4 * (qt & 1) + r] = static_cast<T>(p);
+          sb[qt >> 1][4 * (qt & 1) + r] = static_cast<T>(ds);
         }
       }
     };
-    if (ib == 0)
+    if (CAUSAL && ib == 0)
       weights(std::true_type{});
     else
       weights(std::false_type{});
@@ -512,85 +571,89 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(VarlenBwdArgs a) {
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const bf16x8 ot = tr_frag(dos, 32 * k2, 16 * dt, lr, g);
-        const bf16x8 qtv = tr_frag(qs, 32 * k2, 16 * dt, lr, g);
+      for (int dt = 0; dt < DT; ++dt) {
+        const vec8<T> ot = tr_frag(dos, 32 * k2, 16 * dt, lr, g);
+        const vec8<T> qtv = tr_frag(qs, 32 * k2, 16 * dt, lr, g);
         dvt[dt] = mfma(ot, pb[k2], dvt[dt]);
         dkt[dt] = mfma(qtv, sb[k2], dkt[dt]);
       }
     }
   }
-  if (key >= s1) return;
-  __bf16* dkrow = a.dk + key * row_stride + h * VD;
-  __bf16* dvrow = a.dv + key * row_stride + h * VD;
+  if (key >= ks1) return;
+  T* dkrow = a.dk + key * cs + h * D;
+  T* dvrow = a.dv + key * cs + h * D;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
-    bf16x4 wk, wv;
+  for (int dt = 0; dt < DT; ++dt) {
+    vec4<T> wk, wv;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      wk[r] = static_cast<__bf16>(dkt[dt][r] * a.scale);
-      wv[r] = static_cast<__bf16>(dvt[dt][r]);
+      wk[r] = static_cast<T>(dkt[dt][r] * a.scale);
+      wv[r] = static_cast<T>(dvt[dt][r]);
     }
-    *reinterpret_cast<bf16x4*>(dkrow + 16 * dt + 4 * g) = wk;
-    *reinterpret_cast<bf16x4*>(dvrow + 16 * dt + 4 * g) = wv;
+    *reinterpret_cast<vec4<T>*>(dkrow + 16 * dt + 4 * g) = wk;
+    *reinterpret_cast<vec4<T>*>(dvrow + 16 * dt + 4 * g) = wv;
   }
 }
 
 // dQ: workgroup = (128-query tile, head), wave w owns queries q0 + 32w .. +32.
-__global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
-  __shared__ __bf16 ks[VBN][TPAD];     // K rows of the key tile
-  __shared__ __bf16 vs[VBN][KPAD];     // V rows
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void varlen_dq_kernel(BwdArgs<T> a) {
+  constexpr int KC = D / 32;
+  constexpr int DT = D / 16;
+  __shared__ T ks[VBN][TPAD];   // K rows of the key tile
+  __shared__ T vs[VBN][TPAD];   // V rows
   const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
-  const int seq = task[0];
-  if (seq < 0) return;   // padding slot of a shorter XCD queue
+  const int blk = task[0];
+  if (blk < 0) return;   // padding slot of a shorter XCD queue
   const int q0 = task[1];
   const int h = task[2];
-  const int s0 = a.cu[seq], s1 = a.cu[seq + 1];
+  const int qs1 = a.cu_q[blk + 1];
+  const int ks0 = a.cu_k[blk], ks1 = a.cu_k[blk + 1];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, lr = lane & 15;
-  const int64_t row_stride = static_cast<int64_t>(a.H) * VD;
+  const int64_t cs = static_cast<int64_t>(a.H) * D;
   const int qb = q0 + wave * 32;
-  bf16x8 qf[2][4], df[2][4];
+  vec8<T> qf[2][KC], df[2][KC];
   float lse2[2], del[2];
+  int qlim[2];         // last key each query row may see
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int qq = qb + 16 * qt + lr;
-    const bool ok = qq < s1;
+    const bool ok = qq < qs1;
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      qf[qt][kc] = ok ? ld_bf16x8(a.q + qq * row_stride + h * VD + 32 * kc + 8 * g) : bf16x8{};
-      df[qt][kc] = ok ? ld_bf16x8(a.dout + qq * row_stride + h * VD + 32 * kc + 8 * g)
-                      : bf16x8{};
+    for (int kc = 0; kc < KC; ++kc) {
+      qf[qt][kc] = ok ? ld8(a.q + qq * a.qsn + h * a.qsh + 32 * kc + 8 * g) : vec8<T>{};
+      df[qt][kc] = ok ? ld8(a.dout + qq * cs + h * D + 32 * kc + 8 * g) : vec8<T>{};
     }
     lse2[qt] = ok ? a.lse[static_cast<int64_t>(qq) * a.H + h] * kLog2e : __builtin_huge_valf();
     del[qt] = ok ? a.delta[static_cast<int64_t>(qq) * a.H + h] : 0.f;
+    qlim[qt] = CAUSAL ? min(qq, ks1 - 1) : ks1 - 1;
   }
-  int qlim[2];         // last key each query row may see
+  f32x4v dqt[DT][2];   // dQ^T [d = 16 dt + 4g + r][q]
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) qlim[qt] = min(qb + 16 * qt + lr, s1 - 1);
-  f32x4v dqt[8][2];   // dQ^T [d = 16 dt + 4g + r][q]
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) dqt[dt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
-  const __bf16* kh = a.k + h * VD;
-  const __bf16* vh = a.v + h * VD;
-  const int kv_end = (q0 + VBM < s1) ? q0 + VBM : s1;
-  const int n_kv = (kv_end - s0 + VBN - 1) / VBN;
-  Stage2 st;
-  load2(st, kh, vh, row_stride, s0, s1);
+  const T* kh = a.k + h * a.ksh;
+  const T* vh = a.v + h * a.ksh;
+  const int kv_end = CAUSAL ? min(q0 + VBM, ks1) : ks1;
+  const int n_kv = (kv_end - ks0 + VBN - 1) / VBN;
+  Stage<T, D> st;
+  // Key rows past the block are zero: their dS^T meets a zero K row, so
+  // non-causal tiles need no mask.
+  if (n_kv > 0) stage_load<T, D, false>(st, kh, a.ksn, vh, a.ksn, ks0, ks1);
   for (int it = 0; it < n_kv; ++it) {
-    const int kbase = s0 + it * VBN;
+    const int kbase = ks0 + it * VBN;
     __syncthreads();
-    store2<TPAD, KPAD>(st, ks, vs);
+    stage_store<T, D>(st, ks, vs);
     __syncthreads();
-    if (it + 1 < n_kv) load2(st, kh, vh, row_stride, kbase + VBN, s1);
-    if (kbase > qb + 31) continue;
-    const bool edge_tile = kbase + VBN > qb || kbase + VBN > s1;
+    if (it + 1 < n_kv) stage_load<T, D, false>(st, kh, a.ksn, vh, a.ksn, kbase + VBN, ks1);
+    if (CAUSAL && kbase > qb + 31) continue;
+    const bool edge_tile = CAUSAL && (kbase + VBN > qb || kbase + VBN > ks1);
     // S^T = K Q^T and dP^T = V dO^T one 16-key subtile at a time (C tiles
     // [key = 16 kt + 4g + r][q]), turned straight into dS^T fragments.
-    bf16x8 sb[2][2];
+    vec8<T> sb[2][2];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
       f32x4v sc[2], dp[2];
@@ -600,9 +663,9 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
         dp[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        const bf16x8 ka = ld_bf16x8(&ks[16 * kt + lr][32 * kc + 8 * g]);
-        const bf16x8 va = ld_bf16x8(&vs[16 * kt + lr][32 * kc + 8 * g]);
+      for (int kc = 0; kc < KC; ++kc) {
+        const vec8<T> ka = ld8(&ks[16 * kt + lr][32 * kc + 8 * g]);
+        const vec8<T> va = ld8(&vs[16 * kt + lr][32 * kc + 8 * g]);
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
           sc[qt] = mfma(ka, qf[qt][kc], sc[qt]);
@@ -619,7 +682,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
             float p = exp2_hw(sc[qt][r] * a.scale_log2 - lse2[qt]);
             if (decltype(masked)::value && kbase + 16 * kt + 4 * g + r > qlim[qt]) p = 0.f;
             const float ds = p * (dp[qt][r] - del[qt]);
-            sb[qt][kt >> 1][4 * (kt & 1) + r] = static_cast<__bf16>(ds);
+            sb[qt][kt >> 1][4 * (kt & 1) + r] = static_cast<T>(ds);
           }
         }
       };
@@ -632,8 +695,8 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const bf16x8 kta = tr_frag(ks, 32 * k2, 16 * dt, lr, g);
+      for (int dt = 0; dt < DT; ++dt) {
+        const vec8<T> kta = tr_frag(ks, 32 * k2, 16 * dt, lr, g);
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) dqt[dt][qt] = mfma(kta, sb[qt][k2], dqt[dt][qt]);
       }
@@ -642,16 +705,128 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int qq = qb + 16 * qt + lr;
-    if (qq >= s1) continue;
-    __bf16* row = a.dq + qq * row_stride + h * VD;
+    if (qq >= qs1) continue;
+    T* row = a.dq + qq * cs + h * D;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      bf16x4 w;
+    for (int dt = 0; dt < DT; ++dt) {
+      vec4<T> w;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) w[r] = static_cast<__bf16>(dqt[dt][qt][r] * a.scale);
-      *reinterpret_cast<bf16x4*>(row + 16 * dt + 4 * g) = w;
+      for (int r = 0; r < 4; ++r) w[r] = static_cast<T>(dqt[dt][qt][r] * a.scale);
+      *reinterpret_cast<vec4<T>*>(row + 16 * dt + 4 * g) = w;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Launch helpers (dtype x head dim x causal x prune dispatch).
+
+struct AttnShape {
+  int64_t n_q, n_k;
+  int H, D, dtype, causal;
+  int64_t qsn, qsh, ksn, ksh;
+};
+
+int check_shape(const AttnShape& s) {
+  if (s.D != 64 && s.D != 128) {
+    set_error("dense attention tiles support head_dim 64 and 128 (got %d)", s.D);
+    return TGX_UNSUPPORTED;
+  }
+  if (s.dtype != TGX_DTYPE_BF16 && s.dtype != TGX_DTYPE_F16) {
+    set_error("dense attention tiles support bf16 and fp16 (dtype code %d)", s.dtype);
+    return TGX_UNSUPPORTED;
+  }
+  TGX_REQUIRE(s.H > 0 && s.n_q >= 0 && s.n_k >= 0, "bad sizes");
+  TGX_REQUIRE(s.qsn > 0 && s.qsh > 0 && s.ksn > 0 && s.ksh > 0, "strides must be positive");
+  TGX_REQUIRE(s.n_q < (int64_t{1} << 31) && s.n_k < (int64_t{1} << 31),
+              "token counts must fit int32");
+  return TGX_OK;
+}
+
+template <typename T, int D>
+int launch_fwd(const AttnShape& s, FwdArgs<T> a, int64_t n_tasks, bool prune,
+               hipStream_t stream) {
+  const unsigned grid = static_cast<unsigned>(n_tasks);
+  TGX_PROFILE("varlen_fwd_kernel", stream);
+  if (s.causal) {
+    if (prune)
+      varlen_fwd_kernel<T, D, true, true><<<grid, 256, 0, stream>>>(a);
+    else
+      varlen_fwd_kernel<T, D, true, false><<<grid, 256, 0, stream>>>(a);
+  } else {
+    if (prune)
+      varlen_fwd_kernel<T, D, false, true><<<grid, 256, 0, stream>>>(a);
+    else
+      varlen_fwd_kernel<T, D, false, false><<<grid, 256, 0, stream>>>(a);
+  }
+  TGX_LAUNCHED("varlen_fwd_kernel");
+  return TGX_OK;
+}
+
+template <typename T, int D>
+int launch_bwd(const AttnShape& s, BwdArgs<T> a, const T* out, const int32_t* q_tasks,
+               int64_t n_q_tasks, const int32_t* k_tasks, int64_t n_k_tasks, float* delta,
+               hipStream_t stream) {
+  {
+    TGX_PROFILE("varlen_delta_kernel", stream);
+    const int hpw = kWave / (D / 8);
+    const int64_t waves = s.n_q * ((s.H + hpw - 1) / hpw);
+    if (waves > 0) {
+      varlen_delta_kernel<T, D><<<ceil_div(waves, 4), 256, 0, stream>>>(a.dout, out, delta,
+                                                                         s.n_q, s.H);
+      TGX_LAUNCHED("varlen_delta_kernel");
+    }
+  }
+  a.delta = delta;
+  if (n_k_tasks > 0) {
+    TGX_PROFILE("varlen_dkdv_kernel", stream);
+    a.tasks = k_tasks;
+    if (s.causal)
+      varlen_dkdv_kernel<T, D, true><<<static_cast<unsigned>(n_k_tasks), 256, 0, stream>>>(a);
+    else
+      varlen_dkdv_kernel<T, D, false><<<static_cast<unsigned>(n_k_tasks), 256, 0, stream>>>(a);
+    TGX_LAUNCHED("varlen_dkdv_kernel");
+  }
+  if (n_q_tasks > 0) {
+    TGX_PROFILE("varlen_dq_kernel", stream);
+    a.tasks = q_tasks;
+    if (s.causal)
+      varlen_dq_kernel<T, D, true><<<static_cast<unsigned>(n_q_tasks), 256, 0, stream>>>(a);
+    else
+      varlen_dq_kernel<T, D, false><<<static_cast<unsigned>(n_q_tasks), 256, 0, stream>>>(a);
+    TGX_LAUNCHED("varlen_dq_kernel");
+  }
+  return TGX_OK;
+}
+
+template <typename T>
+int fwd_dtype(const AttnShape& s, const int32_t* cu_q, const int32_t* cu_k,
+              const int32_t* tasks, int64_t n_tasks, const void* q, const void* k,
+              const void* v, float scale, float prune, void* out, float* lse,
+              hipStream_t stream) {
+  FwdArgs<T> a{cu_q, cu_k, tasks, s.H,
+               static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+               s.qsn, s.qsh, s.ksn, s.ksh, static_cast<T*>(out), lse, scale * kLog2e,
+               prune > 0.f ? __builtin_log2f(prune) : 0.f};
+  if (s.D == 64) return launch_fwd<T, 64>(s, a, n_tasks, prune > 0.f, stream);
+  return launch_fwd<T, 128>(s, a, n_tasks, prune > 0.f, stream);
+}
+
+template <typename T>
+int bwd_dtype(const AttnShape& s, const int32_t* cu_q, const int32_t* cu_k,
+              const int32_t* q_tasks, int64_t n_q_tasks, const int32_t* k_tasks,
+              int64_t n_k_tasks, const void* q, const void* k, const void* v, const void* out,
+              const float* lse, const void* dout, float scale, void* dq, void* dk, void* dv,
+              float* delta, hipStream_t stream) {
+  BwdArgs<T> a{cu_q, cu_k, nullptr, s.H,
+               static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+               s.qsn, s.qsh, s.ksn, s.ksh, static_cast<const T*>(dout), lse, delta,
+               static_cast<T*>(dq), static_cast<T*>(dk), static_cast<T*>(dv),
+               scale, scale * kLog2e};
+  if (s.D == 64)
+    return launch_bwd<T, 64>(s, a, static_cast<const T*>(out), q_tasks, n_q_tasks, k_tasks,
+                             n_k_tasks, delta, stream);
+  return launch_bwd<T, 128>(s, a, static_cast<const T*>(out), q_tasks, n_q_tasks, k_tasks,
+                            n_k_tasks, delta, stream);
 }
 
 }  // namespace
@@ -659,30 +834,39 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(VarlenBwdArgs a) {
 
 using namespace tgx;
 
-extern "C" int tgx_varlen_causal_tasks(const int32_t* cu_seqlens_host, int n_seq, int H,
-                                       int block, int kind, int32_t* tasks_host,
-                                       int64_t* n_tasks) {
-  TGX_REQUIRE(cu_seqlens_host && n_tasks && n_seq >= 0 && H > 0 && block > 0,
+extern "C" int tgx_attn_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host, int n_blocks,
+                              int H, int block, int kind, int causal, int32_t* tasks_host,
+                              int64_t* n_tasks) {
+  TGX_REQUIRE(cu_q_host && cu_k_host && n_tasks && n_blocks >= 0 && H > 0 && block > 0,
               "bad arguments");
   TGX_REQUIRE(kind == 0 || kind == 1, "kind must be 0 (query tiles) or 1 (key tiles)");
-  // Work of a tile: the causal keys a query tile sees, or the queries that
-  // see a key tile.  A group is every tile of one (sequence, head).
+  // Work of a tile: the keys a query tile sees, or the queries that see a
+  // key tile.  A group is every tile of one (block, head).
   struct Group {
-    int seq, head;
+    int blk, head;
     int64_t work;
   };
   std::vector<Group> groups;
-  for (int b = 0; b < n_seq; ++b) {
-    const int s0 = cu_seqlens_host[b], s1 = cu_seqlens_host[b + 1];
-    TGX_REQUIRE(s1 >= s0 && s0 >= 0, "cu_seqlens must be non-decreasing from 0");
-    if (s1 == s0) continue;
+  for (int b = 0; b < n_blocks; ++b) {
+    const int q0 = cu_q_host[b], q1 = cu_q_host[b + 1];
+    const int k0 = cu_k_host[b], k1 = cu_k_host[b + 1];
+    TGX_REQUIRE(q1 >= q0 && q0 >= 0 && k1 >= k0 && k0 >= 0,
+                "cu_seqlens must be non-decreasing from 0");
+    TGX_REQUIRE(!causal || (q0 == k0 && q1 == k1), "causal blocks must be square");
+    const int r0 = kind == 0 ? q0 : k0, r1 = kind == 0 ? q1 : k1;
+    if (r1 == r0) continue;
     int64_t w = 0;
-    for (int r0 = s0; r0 < s1; r0 += block)
-      w += kind == 0 ? std::min(r0 + block, s1) - s0 : s1 - r0;
-    for (int h = 0; h < H; ++h) groups.push_back(Group{b, h, w});
+    for (int r = r0; r < r1; r += block) {
+      const int end = std::min(r + block, r1);
+      if (kind == 0)
+        w += causal ? end - k0 : k1 - k0;
+      else
+        w += causal ? q1 - r : q1 - q0;
+    }
+    for (int h = 0; h < H; ++h) groups.push_back(Group{b, h, std::max<int64_t>(w, 1)});
   }
   // Longest-processing-time assignment of groups to the XCDs (stable, so
-  // ties keep sequence then head order).
+  // ties keep block then head order).
   std::stable_sort(groups.begin(), groups.end(),
                    [](const Group& x, const Group& y) { return x.work > y.work; });
   std::vector<std::vector<int32_t>> queue(kXcds);
@@ -692,12 +876,14 @@ extern "C" int tgx_varlen_causal_tasks(const int32_t* cu_seqlens_host, int n_seq
     for (int i = 1; i < kXcds; ++i)
       if (load[i] < load[x]) x = i;
     load[x] += gr.work;
-    const int s0 = cu_seqlens_host[gr.seq], s1 = cu_seqlens_host[gr.seq + 1];
-    // Heaviest tile first: the last query tile, or the first key tile.
-    const int n_t = (s1 - s0 + block - 1) / block;
+    const int r0 = kind == 0 ? cu_q_host[gr.blk] : cu_k_host[gr.blk];
+    const int r1 = kind == 0 ? cu_q_host[gr.blk + 1] : cu_k_host[gr.blk + 1];
+    // Heaviest tile first: causal query tiles from the last, key tiles from
+    // the first (equal work otherwise: in order).
+    const int n_t = (r1 - r0 + block - 1) / block;
     for (int t = 0; t < n_t; ++t) {
-      const int r0 = kind == 0 ? s0 + (n_t - 1 - t) * block : s0 + t * block;
-      queue[x].insert(queue[x].end(), {gr.seq, r0, gr.head, 0});
+      const int tt = (kind == 0 && causal) ? n_t - 1 - t : t;
+      queue[x].insert(queue[x].end(), {gr.blk, r0 + tt * block, gr.head, 0});
     }
   }
   size_t longest = 0;
@@ -707,7 +893,7 @@ extern "C" int tgx_varlen_causal_tasks(const int32_t* cu_seqlens_host, int n_seq
   *n_tasks = n;
   if (tasks_host) {
     // Dispatch hands workgroup i to XCD i % 8: slot 8 i + x is XCD x's i-th
-    // task, or padding (sequence -1) once its queue is exhausted.
+    // task, or padding (block -1) once its queue is exhausted.
     for (size_t i = 0; i < longest; ++i)
       for (int x = 0; x < kXcds; ++x) {
         int32_t* dst = tasks_host + 4 * (static_cast<int64_t>(i) * kXcds + x);
@@ -722,73 +908,53 @@ extern "C" int tgx_varlen_causal_tasks(const int32_t* cu_seqlens_host, int n_seq
   return TGX_OK;
 }
 
-extern "C" int tgx_varlen_causal_fwd(const int32_t* cu_seqlens_dev, const int32_t* tasks_dev,
-                                     int64_t n_tasks, const void* q, const void* k,
-                                     const void* v, float scale, void* out, float* lse,
-                                     int64_t total_tokens, int H, int D, void* stream) {
-  if (D != VD) {
-    set_error("varlen causal attention supports head_dim 128 (got %d)", D);
-    return TGX_UNSUPPORTED;
-  }
-  TGX_REQUIRE(H > 0 && n_tasks >= 0 && total_tokens >= 0, "bad sizes");
-  TGX_REQUIRE(total_tokens * H * VD < (int64_t{1} << 31), "tensor too large for 32-bit offsets");
+extern "C" int tgx_attn_fwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
+                            const int32_t* tasks_dev, int64_t n_tasks, int causal, int dtype,
+                            const void* q, const void* k, const void* v, const int64_t* strides,
+                            float scale, float prune_threshold, void* out, float* lse,
+                            int64_t n_q, int64_t n_k, int H, int D, void* stream) {
+  TGX_REQUIRE(strides, "null strides");
+  const AttnShape s{n_q, n_k, H, D, dtype, causal != 0,
+                    strides[0], strides[1], strides[2], strides[3]};
+  int st = check_shape(s);
+  if (st != TGX_OK) return st;
+  TGX_REQUIRE(!(prune_threshold < 0.f) && prune_threshold <= 1.f,
+              "block_prune_threshold must be in (0, 1] (0 = exact)");
+  TGX_REQUIRE(n_tasks >= 0 && n_tasks < (int64_t{1} << 31), "bad task count");
   if (n_tasks == 0) return TGX_OK;
-  TGX_REQUIRE(cu_seqlens_dev && tasks_dev && q && k && v && out && lse, "null pointer");
-  TGX_REQUIRE(n_tasks < (int64_t{1} << 31), "too many tasks");
-  hipStream_t s = as_stream(stream);
-  VarlenFwdArgs a{cu_seqlens_dev, tasks_dev, H,
-                  static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
-                  static_cast<const __bf16*>(v), static_cast<__bf16*>(out), lse,
-                  scale * kLog2e};
-  TGX_PROFILE("varlen_fwd_kernel", s);
-  varlen_fwd_kernel<<<static_cast<unsigned>(n_tasks), 256, 0, s>>>(a);
-  TGX_LAUNCHED("varlen_fwd_kernel");
-  return TGX_OK;
+  TGX_REQUIRE(cu_q_dev && cu_k_dev && tasks_dev && q && k && v && out && lse, "null pointer");
+  hipStream_t hs = as_stream(stream);
+  if (dtype == TGX_DTYPE_BF16)
+    return fwd_dtype<__bf16>(s, cu_q_dev, cu_k_dev, tasks_dev, n_tasks, q, k, v, scale,
+                             prune_threshold, out, lse, hs);
+  return fwd_dtype<_Float16>(s, cu_q_dev, cu_k_dev, tasks_dev, n_tasks, q, k, v, scale,
+                             prune_threshold, out, lse, hs);
 }
 
-extern "C" int tgx_varlen_causal_bwd(const int32_t* cu_seqlens_dev, const int32_t* q_tasks_dev,
-                                     int64_t n_q_tasks, const int32_t* k_tasks_dev,
-                                     int64_t n_k_tasks, const void* q, const void* k,
-                                     const void* v, const void* out, const float* lse,
-                                     const void* dout, float scale, void* dq, void* dk, void* dv,
-                                     float* delta, int64_t total_tokens, int H, int D,
-                                     void* stream) {
-  if (D != VD) {
-    set_error("varlen causal attention supports head_dim 128 (got %d)", D);
-    return TGX_UNSUPPORTED;
-  }
-  TGX_REQUIRE(H > 0 && n_q_tasks >= 0 && n_k_tasks >= 0 && total_tokens >= 0, "bad sizes");
-  TGX_REQUIRE(n_q_tasks < (int64_t{1} << 31) && n_k_tasks < (int64_t{1} << 31),
-              "too many tasks");
-  TGX_REQUIRE(total_tokens * H * VD < (int64_t{1} << 31), "tensor too large for 32-bit offsets");
-  if (total_tokens == 0) return TGX_OK;
-  TGX_REQUIRE(cu_seqlens_dev && q_tasks_dev && k_tasks_dev && q && k && v && out && lse &&
-                  dout && dq && dk && dv && delta,
+extern "C" int tgx_attn_bwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
+                            const int32_t* q_tasks_dev, int64_t n_q_tasks,
+                            const int32_t* k_tasks_dev, int64_t n_k_tasks, int causal,
+                            int dtype, const void* q, const void* k, const void* v,
+                            const int64_t* strides, const void* out, const float* lse,
+                            const void* dout, float scale, void* dq, void* dk, void* dv,
+                            float* delta, int64_t n_q, int64_t n_k, int H, int D,
+                            void* stream) {
+  TGX_REQUIRE(strides, "null strides");
+  const AttnShape s{n_q, n_k, H, D, dtype, causal != 0,
+                    strides[0], strides[1], strides[2], strides[3]};
+  int st = check_shape(s);
+  if (st != TGX_OK) return st;
+  TGX_REQUIRE(n_q_tasks >= 0 && n_k_tasks >= 0 && n_q_tasks < (int64_t{1} << 31) &&
+                  n_k_tasks < (int64_t{1} << 31),
+              "bad task count");
+  if (n_q == 0 && n_k == 0) return TGX_OK;
+  TGX_REQUIRE(cu_q_dev && cu_k_dev && q_tasks_dev && k_tasks_dev && q && k && v && out &&
+                  lse && dout && dq && dk && dv && delta,
               "null pointer");
-  hipStream_t s = as_stream(stream);
-  {
-    TGX_PROFILE("varlen_delta_kernel", s);
-    const int64_t waves = total_tokens * ((H + 3) / 4);
-    varlen_delta_kernel<<<ceil_div(waves, 4), 256, 0, s>>>(
-        static_cast<const __bf16*>(dout), static_cast<const __bf16*>(out), delta, total_tokens,
-        H);
-    TGX_LAUNCHED("varlen_delta_kernel");
-  }
-  VarlenBwdArgs a{cu_seqlens_dev, k_tasks_dev, H,
-                  static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
-                  static_cast<const __bf16*>(v), static_cast<const __bf16*>(dout), lse, delta,
-                  static_cast<__bf16*>(dq), static_cast<__bf16*>(dk), static_cast<__bf16*>(dv),
-                  scale, scale * kLog2e};
-  if (n_k_tasks > 0) {
-    TGX_PROFILE("varlen_dkdv_kernel", s);
-    varlen_dkdv_kernel<<<static_cast<unsigned>(n_k_tasks), 256, 0, s>>>(a);
-    TGX_LAUNCHED("varlen_dkdv_kernel");
-  }
-  a.tasks = q_tasks_dev;
-  if (n_q_tasks > 0) {
-    TGX_PROFILE("varlen_dq_kernel", s);
-    varlen_dq_kernel<<<static_cast<unsigned>(n_q_tasks), 256, 0, s>>>(a);
-    TGX_LAUNCHED("varlen_dq_kernel");
-  }
-  return TGX_OK;
+  hipStream_t hs = as_stream(stream);
+  if (dtype == TGX_DTYPE_BF16)
+    return bwd_dtype<__bf16>(s, cu_q_dev, cu_k_dev, q_tasks_dev, n_q_tasks, k_tasks_dev,
+                             n_k_tasks, q, k, v, out, lse, dout, scale, dq, dk, dv, delta, hs);
+  return bwd_dtype<_Float16>(s, cu_q_dev, cu_k_dev, q_tasks_dev, n_q_tasks, k_tasks_dev,
+                             n_k_tasks, q, k, v, out, lse, dout, scale, dq, dk, dv, delta, hs);
 }

@@ -79,11 +79,12 @@ _SIGNATURES: dict[str, list] = {
     "tgx_dot_attn_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, P(RowPlan), c_vp,
                          c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                          c_i64, c_i64, c_int, c_int, c_vp, c_size, c_vp],
-    "tgx_varlen_causal_tasks": [c_vp, c_int, c_int, c_int, c_int, c_vp, P(c_i64)],
-    "tgx_varlen_causal_fwd": [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_i64,
-                              c_int, c_int, c_vp],
-    "tgx_varlen_causal_bwd": [c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp,
-                              c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_vp],
+    "tgx_attn_tasks": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp, P(c_i64)],
+    "tgx_attn_fwd": [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_vp, c_vp, c_vp, P(c_i64),
+                     c_f32, c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_vp],
+    "tgx_attn_bwd": [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp, c_vp,
+                     P(c_i64), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
+                     c_int, c_int, c_vp],
     "tgx_profile_begin": [],
     "tgx_profile_end": [],
     "tgx_profile_count": [],

@@ -192,39 +192,70 @@ class DotAttnFunction(torch.autograd.Function):
         return dq, dk, dv, dbias, None, None
 
 
-class VarlenCausalFunction(torch.autograd.Function):
-    """Causal attention on a Graph.cu_seqlens relation: q/k/v [T, H, 128] bf16."""
+_ATTN_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
+
+
+def attn_strides(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    """(q, k, v, strides) with the innermost dim dense and k, v sharing
+    token/head strides, as the attention tiles read them: contiguous
+    [n, H, D], or [H, n, D] storage viewed as [n, H, D] (the layout of the
+    reference's dense streaming path, message_passing.py:1944-1947), are
+    used in place; anything else is made contiguous."""
+    if q.stride(-1) != 1 or min(q.stride(0), q.stride(1)) <= 0:
+        q = q.contiguous()
+    if k.stride(-1) != 1 or v.stride() != k.stride() or min(k.stride(0), k.stride(1)) <= 0:
+        k, v = k.contiguous(), v.contiguous()
+    strides = (ctypes.c_int64 * 4)(q.stride(0), q.stride(1), k.stride(0), k.stride(1))
+    return q, k, v, strides
+
+
+class BlockAttentionFunction(torch.autograd.Function):
+    """Dot-product attention over a block-diagonal relation: Graph.cu_seqlens
+    (causal or not), Graph.dense, Graph.triangular.  q [n_dst, H, D], k/v
+    [n_src, H, D], bf16 or fp16, D in {64, 128}; out contiguous [n_dst, H, D].
+    prune > 0 is the reference's block_prune_threshold (forward only)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale: float, graph: Graph):
-        T, H, D = q.shape
-        qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
-        cu, tasks, n = graph._varlen_tasks(0, 128, H)
-        out = torch.empty_like(qc)
-        lse = torch.empty((T, H), dtype=torch.float32, device=q.device)
-        _native.call("tgx_varlen_causal_fwd", cu.data_ptr(), tasks.data_ptr(), n,
-                     qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), float(scale), out.data_ptr(),
-                     lse.data_ptr(), T, H, D, _native.stream_of(q))
+    def forward(ctx, q, k, v, scale: float, prune: float, graph: Graph):
+        n_q, H, D = q.shape
+        n_k = k.shape[0]
+        q, k, v, strides = attn_strides(q, k, v)
+        cu_q, cu_k, tasks, n, causal = graph._attn_tasks(0, 128, H)
+        out = torch.empty((n_q, H, D), dtype=q.dtype, device=q.device)
+        lse = torch.empty((n_q, H), dtype=torch.float32, device=q.device)
+        _native.call("tgx_attn_fwd", cu_q.data_ptr(), cu_k.data_ptr(), tasks.data_ptr(), n,
+                     int(causal), _ATTN_DTYPES[q.dtype], q.data_ptr(), k.data_ptr(),
+                     v.data_ptr(), strides, float(scale), float(prune), out.data_ptr(),
+                     lse.data_ptr(), n_q, n_k, H, D, _native.stream_of(q))
         ctx.graph = graph
         ctx.scale = float(scale)
-        ctx.save_for_backward(qc, kc, vc, out, lse)
+        ctx.pruned = prune > 0
+        ctx.save_for_backward(q, k, v, out, lse)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        qc, kc, vc, out, lse = ctx.saved_tensors
+        if ctx.pruned:
+            raise NotImplementedError(
+                "block_prune_threshold is a forward-only approximation: it has no gradient")
+        q, k, v, out, lse = ctx.saved_tensors
         graph: Graph = ctx.graph
-        T, H, D = qc.shape
+        n_q, H, D = q.shape
+        n_k = k.shape[0]
         dout = dout.contiguous()
-        if dout.dtype != qc.dtype:
-            dout = dout.to(qc.dtype)
-        cu, qtasks, nq = graph._varlen_tasks(0, 128, H)
-        _, ktasks, nk = graph._varlen_tasks(1, 64, H)
-        dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
-        delta = torch.empty((T, H), dtype=torch.float32, device=qc.device)
-        _native.call("tgx_varlen_causal_bwd", cu.data_ptr(), qtasks.data_ptr(), nq,
-                     ktasks.data_ptr(), nk, qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                     out.data_ptr(), lse.data_ptr(), dout.data_ptr(), ctx.scale, dq.data_ptr(),
-                     dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), T, H, D,
-                     _native.stream_of(qc))
-        return dq, dk, dv, None, None
+        if dout.dtype != q.dtype:
+            dout = dout.to(q.dtype)
+        strides = attn_strides(q, k, v)[3]   # saved tensors already have tile strides
+        cu_q, cu_k, qtasks, nq, causal = graph._attn_tasks(0, 128, H)
+        _, _, ktasks, nk, _ = graph._attn_tasks(1, 64, H)
+        dq = torch.empty((n_q, H, D), dtype=q.dtype, device=q.device)
+        dk = torch.empty((n_k, H, D), dtype=q.dtype, device=q.device)
+        dv = torch.empty((n_k, H, D), dtype=q.dtype, device=q.device)
+        delta = torch.empty((n_q, H), dtype=torch.float32, device=q.device)
+        _native.call("tgx_attn_bwd", cu_q.data_ptr(), cu_k.data_ptr(), qtasks.data_ptr(), nq,
+                     ktasks.data_ptr(), nk, int(causal), _ATTN_DTYPES[q.dtype], q.data_ptr(),
+                     k.data_ptr(), v.data_ptr(), strides, out.data_ptr(), lse.data_ptr(),
+                     dout.data_ptr(), ctx.scale, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                     delta.data_ptr(), n_q, n_k, H, D, _native.stream_of(q))
+        return dq, dk, dv, None, None, None
+

@@ -167,6 +167,8 @@ class Graph:
         self._col_idx = col_idx
         self._cu_seqlens = cu_seqlens
         self._causal = causal
+        # Implicit dense relations: None (every pair) or "lower_inclusive".
+        self._dense_boundary = None
         self._device = torch.device(device) if device is not None else None
         self._destination_index_cache = None
         self._degree_bounds_cache = None
@@ -284,13 +286,37 @@ class Graph:
         return cls(schema, cu_seqlens=cu_seqlens, causal=causal, device=cu_seqlens.device)
 
     @classmethod
-    def triangular(cls, n: int, *, device="cpu") -> "Graph":
-        """Lower-triangular (causal) relation on n positions: row i relates to
-        sources 0..i.  Kept implicit, as one causal cu_seqlens sequence."""
-        if not isinstance(n, int) or n < 0:
-            raise ValueError("n must be a non-negative integer")
-        return cls.cu_seqlens(torch.tensor([0, n], dtype=torch.int64, device=device),
-                              causal=True)
+    def dense(cls, num_src: int, num_dst: int | None = None, *, device=None,
+              index_dtype: torch.dtype = torch.int64) -> "Graph":
+        """Implicit Cartesian relation: every (dst, src) pair, no adjacency
+        stored (reference graph.py:535-574).  Dot-product attention over it
+        runs in MFMA tiles; other edge functions materialize the CSR."""
+        if not isinstance(num_src, int) or num_src < 0:
+            raise ValueError("num_src must be a non-negative integer")
+        if num_dst is None:
+            num_dst = num_src
+        if not isinstance(num_dst, int) or num_dst < 0:
+            raise ValueError("num_dst must be a non-negative integer")
+        if index_dtype not in _INDEX_DTYPES:
+            raise TypeError("index_dtype must be torch.int32 or torch.int64")
+        resolved = torch.device("cpu" if device is None else device)
+        if resolved.type == "cuda" and resolved.index is None and torch.cuda.is_available():
+            resolved = torch.device("cuda", torch.cuda.current_device())
+        schema = GraphSchema(num_src=num_src, num_dst=num_dst, origin="cartesian",
+                             realization="implicit_dense", index_dtype=index_dtype)
+        return cls(schema, device=resolved)
+
+    @classmethod
+    def triangular(cls, num_entities: int, *, device=None,
+                   index_dtype: torch.dtype = torch.int64) -> "Graph":
+        """Lower-inclusive dense relation: row i relates to sources 0..i
+        (reference graph.py:576-592)."""
+        graph = cls.dense(num_entities, num_entities, device=device, index_dtype=index_dtype)
+        graph._schema = GraphSchema(num_src=num_entities, num_dst=num_entities,
+                                    origin="lower_triangular", realization="implicit_dense",
+                                    index_dtype=index_dtype)
+        graph._dense_boundary = "lower_inclusive"
+        return graph
 
     @classmethod
     def cat(cls, graphs) -> "Graph":
@@ -303,15 +329,17 @@ class Graph:
         device = blocks[0].device
         if any(str(block.device) != str(device) for block in blocks):
             raise ValueError("all blocks must share a device")
-        # Causal varlen blocks stay implicit: their cat is one cu_seqlens.
-        if all(b.is_varlen and b._causal and b._row_ptr is None for b in blocks):
-            parts = [torch.zeros(1, dtype=torch.int64, device=device)]
-            offset = 0
-            for b in blocks:
-                cu = b._cu_seqlens.to(torch.int64)
-                parts.append(cu[1:] + offset)
-                offset += int(cu[-1].item())
-            return cls.cu_seqlens(torch.cat(parts), causal=True)
+        # Causal (or all-pairs) square blocks stay implicit: their cat is one
+        # cu_seqlens relation.
+        for causal in (True, False):
+            if all(b._square_blocks(causal) is not None for b in blocks):
+                parts = [torch.zeros(1, dtype=torch.int64, device=device)]
+                offset = 0
+                for b in blocks:
+                    cu = b._square_blocks(causal)
+                    parts.append(cu[1:] + offset)
+                    offset += int(cu[-1].item())
+                return cls.cu_seqlens(torch.cat(parts), causal=causal)
         dtype = (torch.int64 if any(b.schema.index_dtype == torch.int64 for b in blocks)
                  else torch.int32)
         row_parts = [torch.zeros(1, device=device, dtype=dtype)]
@@ -348,7 +376,28 @@ class Graph:
         return self._schema.realization == "implicit_varlen"
 
     @property
+    def is_dense(self) -> bool:
+        return self._schema.realization == "implicit_dense"
+
+    def _square_blocks(self, causal: bool):
+        """cu_seqlens (int64, on the graph's device) of an implicit relation
+        made of square blocks with the given boundary, else None."""
+        if self._row_ptr is not None:
+            return None
+        if self.is_varlen and self._causal == causal:
+            return self._cu_seqlens.to(torch.int64)
+        if self.is_dense and (self._dense_boundary == "lower_inclusive") == causal and \
+                self._schema.num_src == self._schema.num_dst:
+            return torch.tensor([0, self._schema.num_dst], dtype=torch.int64, device=self.device)
+        return None
+
+    @property
     def num_edges(self) -> int:
+        if self.is_dense and self._row_ptr is None:
+            n = self._schema.num_dst
+            if self._dense_boundary == "lower_inclusive":
+                return n * (n + 1) // 2
+            return self._schema.num_src * n
         if self.is_varlen and self._row_ptr is None:
             lengths = (self._cu_seqlens[1:] - self._cu_seqlens[:-1]).to(torch.int64)
             if self._causal:
@@ -357,6 +406,21 @@ class Graph:
         return self._col_idx.numel()
 
     def resolve_csr(self) -> tuple[torch.Tensor, torch.Tensor]:
+        if self._row_ptr is None and self.is_dense:
+            # Only an edge function no tile covers gets here (eager path).
+            dtype, dev = self._schema.index_dtype, self.device
+            n_dst, n_src = self._schema.num_dst, self._schema.num_src
+            if self._dense_boundary == "lower_inclusive":
+                cu = torch.tensor([0, n_dst], dtype=dtype, device=dev)
+                if _native_builder_ok(cu, self.num_edges, n_dst):
+                    self._row_ptr, self._col_idx = build_varlen_csr(cu, True, n_dst,
+                                                                    self.num_edges)
+                else:
+                    self._row_ptr, self._col_idx = _varlen_csr(cu, True)
+            else:
+                self._row_ptr = torch.arange(n_dst + 1, dtype=dtype, device=dev) * n_src
+                self._col_idx = torch.arange(n_src, dtype=dtype, device=dev).repeat(n_dst)
+            return self._row_ptr, self._col_idx
         if self._row_ptr is None and self.is_varlen:
             total = self._schema.num_dst
             n_edges = self.num_edges
@@ -466,24 +530,42 @@ class Graph:
             self._native_cache["csr"] = got
         return got
 
-    def _varlen_tasks(self, kind: int, block: int, heads: int):
-        """(cu_seqlens int32 on device, tasks [n, 4] int32 on device, n) for the
-        varlen kernels of a `heads`-head launch; kind 0 = query tiles, 1 = key
-        tiles (tgx_varlen_causal_tasks: XCD-grouped dispatch order)."""
-        key = ("varlen", kind, block, heads)
+    def _attn_blocks(self):
+        """(cu_q, cu_k, causal) of a block-diagonal relation as int32 host
+        arrays: cu_seqlens for varlen, one block for dense/triangular."""
+        import numpy as np
+
+        if self.is_varlen:
+            cu = np.ascontiguousarray(self._cu_seqlens.cpu().numpy(), dtype=np.int64)
+            if cu.size and cu[-1] >= 2**31:
+                raise ValueError("the HIP attention tiles support fewer than 2**31 tokens")
+            cu = cu.astype(np.int32)
+            return cu, cu, bool(self._causal)
+        n_dst, n_src = self._schema.num_dst, self._schema.num_src
+        if max(n_dst, n_src) >= 2**31:
+            raise ValueError("the HIP attention tiles support fewer than 2**31 tokens")
+        return (np.array([0, n_dst], dtype=np.int32), np.array([0, n_src], dtype=np.int32),
+                self._dense_boundary == "lower_inclusive")
+
+    def _attn_tasks(self, kind: int, block: int, heads: int):
+        """(cu_q, cu_k on device, tasks [n, 4] int32 on device, n, causal) for
+        the attention tiles of a `heads`-head launch; kind 0 = query tiles,
+        1 = key tiles (tgx_attn_tasks: XCD-grouped dispatch order)."""
+        key = ("attn", kind, block, heads)
         got = self._native_cache.get(key)
         if got is None:
             import numpy as np
 
-            cu_h = np.ascontiguousarray(self._cu_seqlens.cpu().numpy(), dtype=np.int32)
+            cu_q, cu_k, causal = self._attn_blocks()
             n = ctypes.c_int64()
-            _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, heads,
-                         block, kind, None, ctypes.byref(n))
+            args = (cu_q.ctypes.data, cu_k.ctypes.data, cu_q.size - 1, heads, block, kind,
+                    int(causal))
+            _native.call("tgx_attn_tasks", *args, None, ctypes.byref(n))
             tasks = np.zeros(4 * max(n.value, 1), dtype=np.int32)
-            _native.call("tgx_varlen_causal_tasks", cu_h.ctypes.data, cu_h.size - 1, heads,
-                         block, kind, tasks.ctypes.data, ctypes.byref(n))
-            cu_d = torch.as_tensor(cu_h, device=self.device)
-            got = (cu_d, torch.as_tensor(tasks, device=self.device), n.value)
+            _native.call("tgx_attn_tasks", *args, tasks.ctypes.data, ctypes.byref(n))
+            dev = self.device
+            got = (torch.as_tensor(cu_q, device=dev), torch.as_tensor(cu_k, device=dev),
+                   torch.as_tensor(tasks, device=dev), n.value, causal)
             self._native_cache[key] = got
         return got
 

@@ -89,15 +89,23 @@ class MessagePassing(Kernel):
         device = graph.device
         self._validate_fields("src", src, graph.schema.num_src, device)
         self._validate_fields("dst", dst, graph.schema.num_dst, device)
-        if isinstance(self.reducer, OnlineSoftmaxReducer) and \
-                self.reducer.block_prune_threshold is not None:
+        prune = (self.reducer.block_prune_threshold
+                 if isinstance(self.reducer, OnlineSoftmaxReducer) else None)
+        if prune is not None and not graph.is_dense:
+            # reference message_passing/core.py:500-505
             raise NotImplementedError(
-                "block_prune_threshold is defined for dense streaming relations only; "
-                "refusing to run exact softmax on a CSR relation")
+                "block_prune_threshold is defined for dense relations only; refusing to "
+                "run exact softmax on a CSR relation")
         captured = self._captured(params)
         result = None
         if device.type == "cuda" and captured is not None:
             result = self._execute_native(captured, graph, src, dst, edge, params)
+        if result is None and prune is not None:
+            # reference interop/torch/message_passing.py:1611-1616
+            raise NotImplementedError(
+                "block_prune_threshold requires the dense attention tile (dot-product "
+                "score, bf16/fp16, head_dim 64 or 128, on the GPU); refusing to silently "
+                "execute exact softmax or materialize the Cartesian relation")
         if result is None:
             if config.strict:
                 raise RuntimeError(
@@ -131,7 +139,7 @@ class MessagePassing(Kernel):
         from . import _ops
 
         if isinstance(self.reducer, SumReducer):
-            if self.reducer.identity_value != 0 or graph.is_varlen:
+            if self.reducer.identity_value != 0 or graph.is_varlen or graph.is_dense:
                 return None
             pat = cap.recognize_weighted_sum(captured)
             if pat is None or pat.src_field not in src:
@@ -158,7 +166,7 @@ class MessagePassing(Kernel):
         if not isinstance(self.reducer, OnlineSoftmaxReducer):
             return None
         gat = cap.recognize_gat(captured)
-        if gat is not None and not graph.is_varlen:
+        if gat is not None and not graph.is_varlen and not graph.is_dense:
             h = src.get(gat.h_field)
             hd = dst.get(gat.dst_field)
             if h is None or hd is None or hd is not h:
@@ -196,23 +204,13 @@ class MessagePassing(Kernel):
             return None
         if q.ndim != 3 or k.shape[1:] != q.shape[1:] or v.shape[1:] != q.shape[1:]:
             return None
-        if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
-            return None
         _, H, D = q.shape
         if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
             return None
-        if graph.is_varlen:
-            if dot.bias_field is not None or not graph._causal or D != 128:
-                return None
-            if not (q.shape[0] == k.shape[0] == v.shape[0] == graph.schema.num_dst):
-                return None
-            _native.lib()
-            out = _ops.VarlenCausalFunction.apply(q, k, v, dot.scale, graph)
-            self._record_native(graph, "varlen-causal", ("tgx_varlen_causal_fwd",
-                                                         "tgx_varlen_causal_bwd"),
-                                "MFMA 16x16x32 bf16 flash tiles over cu_seqlens (implicit "
-                                "causal relation); atomic-free dK/dV and dQ passes")
-            return out
+        if graph.is_varlen or graph.is_dense:
+            return self._execute_block_attention(dot, graph, q, k, v)
+        if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+            return None
         if D % 8 or H * D not in (128, 256, 512):
             return None
         bias = None
@@ -233,6 +231,42 @@ class MessagePassing(Kernel):
                             "bf16 gathers, fp32 online softmax per (row, head); hub rows "
                             "split and merged; backward over CSR (dq, dbias) and transposed "
                             "CSR (dk, dv)")
+        return out
+
+
+    def _execute_block_attention(self, dot, graph, q, k, v):
+        """Dot-product attention over Graph.cu_seqlens / dense / triangular
+        on MFMA tiles (reference: eager oracle for varlen, compiled fp16
+        dense streaming tile for dense/triangular, message_passing.py:
+        1910-2020)."""
+        from . import _ops
+
+        if dot.bias_field is not None:
+            return None
+        if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _ops._ATTN_DTYPES:
+            return None
+        _, H, D = q.shape
+        if D not in (64, 128):
+            return None
+        if q.shape[0] != graph.schema.num_dst or k.shape[0] != graph.schema.num_src or \
+                v.shape[0] != graph.schema.num_src:
+            return None
+        prune = self.reducer.block_prune_threshold
+        if prune is not None and torch.is_grad_enabled() and \
+                any(t.requires_grad for t in (q, k, v)):
+            raise NotImplementedError(
+                "block_prune_threshold is a forward-only approximation (no gradient); run "
+                "it under torch.no_grad() or drop the threshold for exact softmax")
+        _native.lib()
+        out = _ops.BlockAttentionFunction.apply(q, k, v, dot.scale, float(prune or 0.0), graph)
+        relation = ("cu_seqlens" if graph.is_varlen else graph.schema.origin)
+        causal = graph._attn_blocks()[2]
+        self._record_native(
+            graph, "block-attention", ("tgx_attn_fwd", "tgx_attn_bwd"),
+            f"MFMA 16x16x32 {str(q.dtype).split('.')[-1]} flash tiles over the implicit "
+            f"{relation} relation ({'causal' if causal else 'all pairs'}); XCD-grouped "
+            "tasks; atomic-free dK/dV and dQ passes",
+            remarks=(("block-pruned tile admission (approximate)",) if prune else ()))
         return out
 
 
