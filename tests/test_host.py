@@ -308,3 +308,72 @@ def test_attn_tasks_cover_once_grouped_per_xcd(kind, block, causal, rect):
     assert all(len(v) == 1 for v in where.values())
     with pytest.raises(RuntimeError, match="square"):
         _attn_tasks(cu_q, np.array([0, 1, 2, 3, 4, 5, 6, 7]), H, block, kind, True)
+
+
+def test_torch_library_registration_reference_example():
+    """The reference's torch.library test (tests/python/test_torch_provider.py:
+    80-112, examples/torch_library.py) on CPU tensors (eager path): call,
+    gradients, opcheck and torch.compile(fullgraph=True)."""
+
+    class Weighted(tg.MessagePassing):
+        reducer = tg.sum()
+
+        def edge(self, src, dst, edge):
+            return edge.weight * src.x
+
+    row_ptr = torch.tensor([0, 2, 4], dtype=torch.int64)
+    col_idx = torch.tensor([0, 1, 1, 2], dtype=torch.int64)
+    graph = tg.Graph.from_csr(row_ptr, col_idx, num_src=3)
+    x = torch.tensor([1.0, 2.0, 4.0], requires_grad=True)
+    weight = torch.tensor([2.0, 3.0, 5.0, 7.0], requires_grad=True)
+    registered = tg.interop.torch.register_message_passing(
+        Weighted(), graph=graph, src={"x": x}, dst={}, edge={"weight": weight})
+    assert registered.qualified_name.startswith("tiga::message_passing_")
+    output = registered(src={"x": x}, dst={}, edge={"weight": weight})
+    assert output.tolist() == [8.0, 38.0]
+    dx, dweight = torch.autograd.grad(output.sum(), (x, weight))
+    torch.testing.assert_close(dx, torch.tensor([2.0, 8.0, 7.0]))
+    torch.testing.assert_close(dweight, torch.tensor([1.0, 2.0, 2.0, 4.0]))
+    checked = registered.opcheck(x.detach(), weight.detach())
+    assert all(result == "SUCCESS" for result in checked.values()), checked
+    compiled = torch.compile(
+        lambda a, b: registered(src={"x": a}, dst={}, edge={"weight": b}), fullgraph=True)
+    cx = x.detach().clone().requires_grad_(True)
+    cw = weight.detach().clone().requires_grad_(True)
+    out_c = compiled(cx, cw)
+    grads_c = torch.autograd.grad(out_c.sum(), (cx, cw))
+    torch.testing.assert_close(out_c, output)
+    torch.testing.assert_close(grads_c[0], dx)
+    torch.testing.assert_close(grads_c[1], dweight)
+    # the same specialization registers once; field names are checked
+    again = tg.interop.torch.register_message_passing(
+        Weighted(), graph=graph, src={"x": x}, dst={}, edge={"weight": weight})
+    assert again is registered
+    with pytest.raises(ValueError, match="edge fields"):
+        registered(src={"x": x}, dst={}, edge={"w": weight})
+    with pytest.raises(NotImplementedError, match="static CSR"):
+        tg.interop.torch.register_message_passing(
+            Weighted(), graph=tg.Graph.dense(3), src={"x": x}, dst={}, edge={})
+
+
+def test_reference_method_runs_eager_even_when_covered():
+    class Weighted(tg.MessagePassing):
+        reducer = tg.sum()
+
+        def edge(self, src, dst, edge):
+            return edge.weight * src.x
+
+    graph = tg.Graph.from_csr(torch.tensor([0, 2, 4]), torch.tensor([0, 1, 1, 2]), num_src=3)
+    out = Weighted().reference(graph=graph, src={"x": torch.tensor([1.0, 2.0, 4.0])}, dst={},
+                               edge={"weight": torch.tensor([2.0, 3.0, 5.0, 7.0])})
+    assert out.tolist() == [8.0, 38.0]
+
+    class Pruned(tg.MessagePassing):
+        reducer = tg.online_softmax(block_prune_threshold=0.5)
+
+        def edge(self, src, dst, edge):
+            return self.reducer((src.k * dst.q).sum(-1), src.k)
+
+    with pytest.raises(NotImplementedError, match="no eager"):
+        Pruned().reference(graph=tg.Graph.dense(2), src={"k": torch.ones(2, 3)},
+                           dst={"q": torch.ones(2, 3)})

@@ -4,7 +4,7 @@ Public names follow the reference package (python/tiga/__init__.py:45-66):
 ``tiga.MessagePassing``, ``tiga.Graph``, ``tiga.sum``, ``tiga.online_softmax``.
 """
 
-from . import reducer
+from . import interop, reducer
 from .graph import Graph
 from .kernel import CompiledVariant, Kernel
 from .message_passing import MessagePassing, config
@@ -31,6 +31,7 @@ __all__ = [
     "ReducerCall",
     "SumReducer",
     "config",
+    "interop",
     "online_softmax",
     "reducer",
     "sum",

@@ -125,6 +125,30 @@ class MessagePassing(Kernel):
             return aggregate
         return _call_region(self.node, (SimpleNamespace(**dst), aggregate), params)
 
+    def reference(self, *, graph: Graph, src: Mapping[str, torch.Tensor],
+                  dst: Mapping[str, torch.Tensor],
+                  edge: Mapping[str, torch.Tensor] | None = None, **params: Any):
+        """Run the eager Torch evaluator even where a HIP kernel exists
+        (reference interop/torch/message_passing.py:2818-2894)."""
+        if isinstance(self.reducer, OnlineSoftmaxReducer) and \
+                self.reducer.block_prune_threshold is not None:
+            raise NotImplementedError(
+                "the schedule-dependent block-pruned approximation has no eager "
+                "edge-materializing reference; compare against an exact online-softmax "
+                "result with an explicit accuracy budget")
+        if not getattr(graph, "_tiga_graph", False):
+            raise TypeError("graph must be a tiga.Graph")
+        edge = {} if edge is None else edge
+        device = graph.device
+        self._validate_fields("src", src, graph.schema.num_src, device)
+        self._validate_fields("dst", dst, graph.schema.num_dst, device)
+        if not graph.is_varlen:
+            self._validate_fields("edge", edge, graph.num_edges, device)
+        aggregate = _eager.evaluate(self, graph, src, dst, edge, params)
+        if type(self).node is MessagePassing.node:
+            return aggregate
+        return _call_region(self.node, (SimpleNamespace(**dst), aggregate), params)
+
     # ------------------------------------------------------------------
     def _record_native(self, graph, pattern: str, entry_points, lowering, remarks=()):
         plan = graph._native_cache.get(("plan", 512, 512))
