@@ -73,7 +73,13 @@ def test_registered_op_runs_hip_path_and_matches_direct_call():
     (dh,) = torch.autograd.grad(out, (h,), dout)
     assert torch.equal(dh, dh_direct)
 
+    # opcheck clones every operand separately, so dst.h is no longer src.h and
+    # the GAT kernel (which needs one shared h) does not apply: the clones run
+    # on the eager evaluator.  opcheck checks the registration (schema, fake
+    # kernel, autograd formula, AOT); the HIP path is checked above.
+    tg.config.strict = False
     checked = op.opcheck(h.detach(), h.detach())
+    tg.config.strict = True
     assert all(result == "SUCCESS" for result in checked.values()), checked
 
     compiled = torch.compile(lambda x: op(src={"h": x}, dst={"h": x}), fullgraph=True)
