@@ -8,7 +8,11 @@ HBM.  Prints ONE JSON line (rank 0): edges/s, ms/step, the dominant kernel's
 roofline (algorithmic bytes / its live HIP-event duration) and the
 reference's CPU path timed on a bounded sample of the same workload.
 
-  python bench.py [--steps K] [--warmup W] [--config c2|c1] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--config c1..c5|dense|dense-causal|dense-pruned]
+                  [--no-cpu]
+
+c1-c5 are BASELINE.json's configurations; dense* are the reference's dense
+attention benchmark shapes (N=4096, H=16, D=64, fp16, forward).
 """
 
 from __future__ import annotations
@@ -26,7 +30,7 @@ for p in (str(ROOT / "tiga-lang_amd"), str(ROOT)):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
-BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 (and fp16) MFMA
 
 
 def measured_traffic(config, kernel):
@@ -46,7 +50,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "c5", "dense", "dense-causal",
+                             "dense-pruned"])
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=None)
@@ -542,6 +548,80 @@ def run_c5(args):
     }
 
 
+def run_dense(args):
+    """The reference's dense attention benchmark shapes
+    (benchmarks/neural_networks/dense_attention.py, sparse_attention.py;
+    evidence cases b1_h16_n4096_d64_fp16[_causal]): Graph.dense /
+    Graph.triangular with 4096 nodes, 16 heads, head_dim 64, fp16 inputs in
+    the lane-major [H, N, D] storage viewed as [N, H, D], forward only; the
+    pruned case uses block_prune_threshold = D / N as the reference's."""
+    import torch
+
+    import tiga as tg
+    from tiga import _native
+
+    dev = torch.device("cuda")
+    N, H, D = (args.nodes or 4096), 16, 64
+    causal = args.config == "dense-causal"
+    prune = args.config == "dense-pruned"
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q, k, v = (torch.randn(H, N, D, device=dev, dtype=torch.float16, generator=g).permute(1, 0, 2)
+               for _ in range(3))
+    graph = tg.Graph.triangular(N, device=dev) if causal else tg.Graph.dense(N, device=dev)
+    tg.config.strict = True
+
+    class Attention(tg.MessagePassing):
+        def __init__(self, threshold):
+            super().__init__()
+            self.reducer = tg.online_softmax(block_prune_threshold=threshold)
+
+        def edge(self, src, dst, edge, scale):
+            score = (src.key * dst.query).sum(dim=-1) * scale
+            return self.reducer(score, src.value)
+
+    kernel = Attention(D / N if prune else None)
+
+    def step():
+        with torch.no_grad():
+            return kernel(graph=graph, src={"key": k, "value": v}, dst={"query": q},
+                          scale=D ** -0.5)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    assert kernel.last_variant.backend == "hip"
+    with _native.KernelTimer() as timer:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    pairs = N * (N + 1) // 2 if causal else N * N
+    flops = 4.0 * H * D * pairs            # useful: q.k and p.v per pair (pruned: as if dense)
+    ms = elapsed * 1e3 / args.steps
+    n_launch, total_ms = timer.totals["varlen_fwd_kernel"]
+    kernel_ms = total_ms / n_launch
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    what = {"dense": "all pairs", "dense-causal": "lower-triangular",
+            "dense-pruned": f"all pairs, block_prune_threshold={D / N:g}"}[args.config]
+    return {
+        "metric": f"dense attention forward TFLOP/s ({what}), N={N}, H={H}, D={D}, fp16, "
+                  "1xMI355X",
+        "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (q,k,v ~N(0,1), lane-major storage)",
+        "config": {"workload": args.config, "nodes": N, "heads": H, "head_dim": D,
+                   "pairs": pairs, "flop_convention": "4*H*D per pair (the reference counts "
+                   "(4D+5) per pair and head)"},
+        "roofline": {"kernel": "varlen_fwd_kernel", "bound": "mfma", "achieved": achieved,
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
+                     "avg_ms": kernel_ms},
+        "kernels": {kk: {"launches": n, "avg_ms": t / n} for kk, (n, t) in timer.totals.items()},
+    }
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
@@ -552,7 +632,8 @@ def main():
               "(collectives and sharding are out of scope); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-    runners = {"c1": run_c1, "c2": run_c2, "c3": run_c3c4, "c4": run_c3c4, "c5": run_c5}
+    runners = {"c1": run_c1, "c2": run_c2, "c3": run_c3c4, "c4": run_c3c4, "c5": run_c5,
+               "dense": run_dense, "dense-causal": run_dense, "dense-pruned": run_dense}
     result = runners[args.config](args)
     print(json.dumps(result), flush=True)
 
