@@ -368,6 +368,80 @@ int tgx_attn_bwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
                  int64_t n_q, int64_t n_k, int H, int D, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* nn-scored edge attention: score_e = MLP(concat of gathered fields),       */
+/* out_i = sum_e softmax_i(score)_e value[col_e]                             */
+/*   reference: tg.nn.trace score networks (compiler/nn_capture.py:1-33)     */
+/*   evaluated by compiler/edge_nn_attention.py and                          */
+/*   interop/torch/message_passing.py:2372-2577                             */
+/* ------------------------------------------------------------------------ */
+
+/* Activations between linear layers. */
+enum {
+  TGX_ACT_IDENTITY = 0,
+  TGX_ACT_RELU = 1,
+  TGX_ACT_LEAKY_RELU = 2,   /* act_param = negative slope */
+  TGX_ACT_TANH = 3,
+  TGX_ACT_SIGMOID = 4,
+  TGX_ACT_SILU = 5,
+  TGX_ACT_GELU = 6,         /* exact (erf) form */
+  TGX_ACT_ELU = 7           /* act_param = alpha */
+};
+
+/* Row of an edge that a score-input segment is gathered from. */
+enum { TGX_ROLE_SRC = 0, TGX_ROLE_DST = 1, TGX_ROLE_EDGE = 2 };
+
+/* A score network: n_layers linear layers (1..3), the last with one output,
+ * with an activation after every layer but the last, applied to the
+ * concatenation of up to four fp32 input segments gathered per edge (from the
+ * source row col[e], the destination row, or edge row e).  Every layer is
+ * zero-padded to `width` (16, 32 or 64 >= every layer's in and out size):
+ * weights_dev holds n_layers blocks of [width*width weights (out-major) |
+ * width biases]. */
+typedef struct tgx_edge_mlp {
+  int32_t n_layers;
+  int32_t width;
+  int32_t act[3];
+  float act_param[3];
+  const float* weights_dev;
+  int32_t n_segments;
+  int32_t seg_role[4];
+  int32_t seg_width[4];
+  int64_t seg_stride[4];      /* row stride in floats */
+  const float* seg_dev[4];
+} tgx_edge_mlp;
+
+/* scores[e] = MLP(x_e) for every edge.  dst_index_dev [n_edges] int32 is the
+ * destination row of each edge (tgx_destination_index with out_bits 32). */
+int tgx_edge_mlp_scores(const void* col_dev, const int32_t* dst_index_dev, int idx_bits,
+                        int64_t n_edges, const tgx_edge_mlp* mlp, float* scores_dev,
+                        void* stream);
+
+/* Segment softmax over CSR rows: alpha[e] = exp(s_e - lse_i) and lse[i]
+ * (-inf for an empty row), one wave per row (reducer_oracle.py:60-137). */
+int tgx_segment_softmax_fwd(const void* row_ptr_dev, int idx_bits, int64_t n_rows,
+                            const float* scores_dev, float* alpha_dev, float* lse_dev,
+                            void* stream);
+
+/* Its backward: dscore[e] = alpha_e (dalpha_e - sum over the row of
+ * alpha dalpha). */
+int tgx_segment_softmax_bwd(const void* row_ptr_dev, int idx_bits, int64_t n_rows,
+                            const float* alpha_dev, const float* dalpha_dev,
+                            float* dscore_dev, void* stream);
+
+/* Per-edge backward of the score network given dscore: writes, per layer l,
+ * its input acts_dev[l] and the gradient of its pre-activation output
+ * dz_dev[l] (each n_layers planes of [n_edges, width] fp32; the weight
+ * gradients are dz[l]^T acts[l] and the bias gradients the column sums of
+ * dz[l]), and the gradient of every input segment dseg[s]
+ * ([n_edges, seg_width[s]] fp32 device buffers; dseg is a host array), which
+ * the caller reduces per source row over the transposed CSR and per
+ * destination row over the CSR. */
+int tgx_edge_mlp_backward(const void* col_dev, const int32_t* dst_index_dev, int idx_bits,
+                          int64_t n_edges, const tgx_edge_mlp* mlp, const float* dscore_dev,
+                          float* acts_dev, float* dz_dev, float* const* dseg,
+                          void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Per-kernel timing (no reference counterpart; used by the benchmark)       */
 /* ------------------------------------------------------------------------ */
 

@@ -539,3 +539,132 @@ def varlen_causal_bwd(cu_seqlens, q, k, v, scale, dout):
         dq[s0:s1] = np.einsum("hij,jhd->ihd", ds, ks) * scale
         dk[s0:s1] = np.einsum("hij,ihd->jhd", ds, qs) * scale
     return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
+# nn-scored edge attention
+
+
+def _act(name, z, p):
+    from scipy.special import erf
+
+    if name == "relu":
+        return np.maximum(z, 0.0)
+    if name == "leaky_relu":
+        return np.where(z > 0, z, p * z)
+    if name == "tanh":
+        return np.tanh(z)
+    if name == "sigmoid":
+        return 1.0 / (1.0 + np.exp(-z))
+    if name == "silu":
+        return z / (1.0 + np.exp(-z))
+    if name == "gelu":
+        return 0.5 * z * (1.0 + erf(z / np.sqrt(2.0)))
+    if name == "elu":
+        return np.where(z > 0, z, p * (np.exp(np.minimum(z, 0.0)) - 1.0))
+    return z
+
+
+def _act_grad(name, z, p):
+    from scipy.special import erf
+
+    if name == "relu":
+        return (z > 0).astype(np.float64)
+    if name == "leaky_relu":
+        return np.where(z > 0, 1.0, p)
+    if name == "tanh":
+        return 1.0 - np.tanh(z) ** 2
+    if name == "sigmoid":
+        s = 1.0 / (1.0 + np.exp(-z))
+        return s * (1.0 - s)
+    if name == "silu":
+        s = 1.0 / (1.0 + np.exp(-z))
+        return s * (1.0 + z * (1.0 - s))
+    if name == "gelu":
+        return 0.5 * (1.0 + erf(z / np.sqrt(2.0))) + z * np.exp(-0.5 * z * z) / np.sqrt(2 * np.pi)
+    if name == "elu":
+        return np.where(z > 0, 1.0, p * np.exp(np.minimum(z, 0.0)))
+    return np.ones_like(z)
+
+
+def _edge_inputs(row_ptr, col_idx, inputs):
+    dst = destination_index(row_ptr)
+    col = np.asarray(col_idx, dtype=np.int64)
+    parts = []
+    for role, arr in inputs:
+        arr = np.asarray(arr, dtype=np.float64)
+        arr = arr.reshape(arr.shape[0], -1)
+        parts.append(arr[col] if role == "src" else arr[dst] if role == "dst" else arr)
+    return np.concatenate(parts, axis=1), dst, col
+
+
+def nn_attention_fwd(row_ptr, col_idx, inputs, layers, value):
+    """online_softmax(score = net(concat of gathered fields), value = src.v),
+    fp64: the eager semantics of a tg.nn.trace score (compiler/nn_capture.py:
+    1-33: the module applied to the feature-concatenation of its inputs)
+    under _evaluate_reference + reduce_online_softmax (message_passing.py:
+    2848-2894, reducer_oracle.py:60-137).  inputs = [(role, [rows, w])],
+    layers = [(W [out, in], b [out] or None, act, param)], activation after
+    every layer but the last.  Returns (out, lse).
+
+    Pinned by: finite differences of nn_attention_bwd and equality with Torch
+    float64 autograd of the same composition (tests/test_oracle.py), and the
+    single-Linear reduction to a bias-only score.
+    """
+    x, dst, col = _edge_inputs(row_ptr, col_idx, inputs)
+    a = x
+    for i, (W, b, act, p) in enumerate(layers):
+        a = a @ np.asarray(W, dtype=np.float64).T + (0.0 if b is None else np.asarray(b, np.float64))
+        if i + 1 < len(layers):
+            a = _act(act, a, p)
+    value = np.asarray(value, dtype=np.float64)
+    return segment_softmax(row_ptr, a[:, 0], value[col])
+
+
+def nn_attention_bwd(row_ptr, col_idx, inputs, layers, value, dout):
+    """Gradients of nn_attention_fwd: (d inputs list, d value, [(dW, db)])."""
+    x, dst, col = _edge_inputs(row_ptr, col_idx, inputs)
+    acts, zs = [x], []
+    a = x
+    for i, (W, b, act, p) in enumerate(layers):
+        z = a @ np.asarray(W, dtype=np.float64).T + (0.0 if b is None else np.asarray(b, np.float64))
+        zs.append(z)
+        if i + 1 < len(layers):
+            a = _act(act, z, p)
+            acts.append(a)
+    s = zs[-1][:, 0]
+    value = np.asarray(value, dtype=np.float64)
+    dout = np.asarray(dout, dtype=np.float64)
+    out, lse = segment_softmax(row_ptr, s, value[col])
+    alpha = np.exp(s - lse[dst])
+    dvalue = np.zeros_like(value)
+    np.add.at(dvalue, col, alpha[:, None] * dout[dst])
+    dalpha = (dout[dst] * value[col]).sum(-1)
+    n = np.asarray(row_ptr).size - 1
+    red = np.zeros(n)
+    np.add.at(red, dst, alpha * dalpha)
+    g = (alpha * (dalpha - red[dst]))[:, None]             # d z_last
+    grads = [None] * len(layers)
+    for i in range(len(layers) - 1, -1, -1):
+        W, b, act, p = layers[i]
+        W = np.asarray(W, dtype=np.float64)
+        grads[i] = (g.T @ acts[i], None if b is None else g.sum(0))
+        g = g @ W
+        if i > 0:
+            _, _, act_prev, p_prev = layers[i - 1]
+            g = g * _act_grad(act_prev, zs[i - 1], p_prev)
+    dinputs, off = [], 0
+    for role, arr in inputs:
+        arr = np.asarray(arr, dtype=np.float64)
+        w = arr.reshape(arr.shape[0], -1).shape[1]
+        part = g[:, off:off + w]
+        off += w
+        d = np.zeros((arr.shape[0], w))
+        if role == "src":
+            np.add.at(d, col, part)
+        elif role == "dst":
+            np.add.at(d, dst, part)
+        else:
+            d = part.copy()
+        dinputs.append(d.reshape(arr.shape))
+    return dinputs, dvalue, grads

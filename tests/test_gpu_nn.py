@@ -1,0 +1,216 @@
+"""GPU parity of nn-scored edge attention (tg.nn.trace score networks) on the
+HIP edge-MLP kernels against the fp64 oracle: outputs and the gradients of
+every input field, the value and every weight and bias.
+
+Tolerance (fp32 path): max|gpu - oracle| <= 1e-5 * max|oracle| per tensor;
+weight and bias gradients, which sum over every edge, 3e-5 (bias gradients in
+the scale of their layer's weight gradient: the last bias's exact gradient
+is 0).
+"""
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+import tiga as tg
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+RTOL = 1e-5
+
+
+def rel_err(actual, expected):
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
+
+
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def random_graph(n_dst, n_src, mean_deg, seed, hub=0, empty=0.1):
+    rng = np.random.default_rng(seed)
+    deg = rng.poisson(mean_deg, n_dst)
+    deg[rng.random(n_dst) < empty] = 0
+    if hub:
+        deg[n_dst // 2] = hub
+    rp = np.concatenate([[0], np.cumsum(deg)])
+    col = rng.integers(0, n_src, int(rp[-1]))
+    return torch.as_tensor(rp, device=DEV), torch.as_tensor(col, device=DEV)
+
+
+class GAT(tg.MessagePassing):
+    """The reference example's kernel (examples/gat_edge_attention.py:18-29),
+    with the displacement given as an explicit edge field."""
+
+    reducer = tg.online_softmax()
+
+    def __init__(self, attn):
+        super().__init__()
+        self.attn = tg.nn.trace(attn)
+
+    def edge(self, src, dst, edge):
+        return self.reducer(self.attn(edge.displacement, src.x, dst.x), src.x)
+
+
+def layers_of(net):
+    out, acts = [], []
+    mods = list(net) if isinstance(net, nn.Sequential) else [net]
+    for m in mods:
+        if isinstance(m, nn.Linear):
+            out.append([f64(m.weight), None if m.bias is None else f64(m.bias), "identity", 0.0])
+        elif isinstance(m, nn.LeakyReLU):
+            out[-1][2:] = ["leaky_relu", m.negative_slope]
+        elif isinstance(m, nn.ELU):
+            out[-1][2:] = ["elu", m.alpha]
+        elif isinstance(m, nn.GELU):
+            out[-1][2:] = ["gelu", 0.0]
+        else:
+            out[-1][2:] = [{nn.ReLU: "relu", nn.Tanh: "tanh", nn.Sigmoid: "sigmoid",
+                            nn.SiLU: "silu"}[type(m)], 0.0]
+    return [tuple(x) for x in out]
+
+
+@pytest.fixture(autouse=True)
+def strict():
+    tg.config.strict = True
+    yield
+    tg.config.strict = False
+
+
+def check(graph, kernel, net, inputs, value, fields, dout):
+    """Run kernel forward + backward and compare with the oracle."""
+    rp, col = (f64(t).astype(np.int64) for t in graph.resolve_csr())
+    out = kernel(**fields)
+    assert kernel.last_variant.backend == "hip"
+    assert kernel.last_variant.pattern == "nn-attention"
+    out.backward(dout)
+    o_inputs = [(role, f64(t)) for role, t in inputs]
+    layers = layers_of(net)
+    e_out, _ = ref.nn_attention_fwd(rp, col, o_inputs, layers, f64(value))
+    assert rel_err(f64(out), e_out) <= RTOL
+    dinputs, dvalue, dlayers = ref.nn_attention_bwd(rp, col, o_inputs, layers, f64(value),
+                                                    f64(dout))
+    # a tensor used at several places (x as src, dst and value) sums its parts
+    expect = {}
+    for (role, t), d in zip(inputs, dinputs):
+        expect[id(t)] = expect.get(id(t), 0) + d
+    expect[id(value)] = expect.get(id(value), 0) + dvalue
+    # A field whose score contribution is the same for every edge of a row
+    # (dst fields under a single Linear score) has an exact gradient of 0 by
+    # softmax shift invariance; gradients are compared in the scale of the
+    # largest gradient of the check.
+    scale = max(np.abs(g).max() for g in expect.values())
+    for role, t in inputs + [("value", value)]:
+        err = np.abs(f64(t.grad) - expect[id(t)]).max()
+        assert err <= RTOL * max(np.abs(expect[id(t)]).max(), 0.1 * scale), role
+    linears = [m for m in (net if isinstance(net, nn.Sequential) else [net])
+               if isinstance(m, nn.Linear)]
+    for lin, (dW, db) in zip(linears, dlayers):
+        assert rel_err(f64(lin.weight.grad), dW) <= 3 * RTOL
+        if db is not None:
+            # The last layer's bias shifts every score of a row equally, so its
+            # exact gradient is 0 (softmax shift invariance): bias gradients are
+            # compared in the scale of their layer's weight gradient.
+            scale = max(np.abs(db).max(), np.abs(dW).max())
+            assert np.abs(f64(lin.bias.grad) - db).max() <= 3 * RTOL * scale
+
+
+def test_reference_gat_example_shape():
+    """nodes 512, f_in 8, hidden 16: Linear(3 + 2*8, 16), LeakyReLU(0.2),
+    Linear(16, 1) over [displacement | x_src | x_dst], value x_src."""
+    print("nn attention reference example", flush=True)
+    torch.manual_seed(0)
+    nodes, f_in, hidden = 512, 8, 16
+    rp, col = random_graph(nodes, nodes, 7, 1)
+    graph = tg.Graph.from_csr(rp, col, num_src=nodes)
+    pos = torch.rand(nodes, 3, device=DEV)
+    dst_idx = graph.destination_index()
+    disp = (pos[col] - pos[dst_idx]).requires_grad_(True)
+    x = torch.randn(nodes, f_in, device=DEV, requires_grad=True)
+    attn = nn.Sequential(nn.Linear(3 + 2 * f_in, hidden), nn.LeakyReLU(0.2),
+                         nn.Linear(hidden, 1)).to(DEV)
+    kernel = GAT(attn)
+    dout = torch.randn(nodes, f_in, device=DEV)
+    check(graph, kernel, attn, [("edge", disp), ("src", x), ("dst", x)], x,
+          dict(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp}), dout)
+
+
+@pytest.mark.parametrize("width,acts,hub", [
+    (12, ("tanh",), 0),                       # W = 16, two layers
+    (40, ("gelu", "silu"), 300),               # W = 64, three layers, hub row > 64 edges
+    (24, ("elu", "sigmoid"), 0),               # W = 32, three layers
+    (20, (), 0),                               # one Linear: bias-free linear score
+])
+def test_score_chains(width, acts, hub):
+    print(f"nn attention chain width={width} acts={acts} hub={hub}", flush=True)
+    torch.manual_seed(width)
+    n_dst, n_src = 300, 200
+    rp, col = random_graph(n_dst, n_src, 9, width, hub=hub)
+    graph = tg.Graph.from_csr(rp, col, num_src=n_src)
+    E = col.numel()
+    xs = torch.randn(n_src, 6, device=DEV, requires_grad=True)
+    xd = torch.randn(n_dst, 5, device=DEV, requires_grad=True)
+    ef = torch.randn(E, 3, device=DEV, requires_grad=True)
+    v = torch.randn(n_src, 10, device=DEV, requires_grad=True)
+    mods = []
+    dims = [14] + [width] * len(acts) + [1]
+    names = {"tanh": nn.Tanh, "gelu": nn.GELU, "silu": nn.SiLU, "elu": lambda: nn.ELU(0.7),
+             "sigmoid": nn.Sigmoid}
+    for i in range(len(dims) - 1):
+        mods.append(nn.Linear(dims[i], dims[i + 1], bias=bool(acts) or i > 0))
+        if i < len(acts):
+            mods.append(names[acts[i]]())
+    net = nn.Sequential(*mods).to(DEV)
+
+    class Scored(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def __init__(self):
+            super().__init__()
+            self.net = tg.nn.trace(net)
+
+        def edge(self, src, dst, edge):
+            return self.reducer(self.net(src.a, dst.b, edge.c), src.v)
+
+    dout = torch.randn(n_dst, 10, device=DEV)
+    check(graph, Scored(), net, [("src", xs), ("dst", xd), ("edge", ef)], v,
+          dict(graph=graph, src={"a": xs, "v": v}, dst={"b": xd}, edge={"c": ef}), dout)
+
+
+def test_uncovered_networks_fall_back_or_refuse():
+    """LayerNorm or widths above 64 are not covered: strict mode refuses,
+    otherwise the eager evaluator runs them (reference fail-closed rungs)."""
+    n = 50
+    rp, col = random_graph(n, n, 4, 5)
+    graph = tg.Graph.from_csr(rp, col, num_src=n)
+    x = torch.randn(n, 4, device=DEV)
+    for net in (nn.Sequential(nn.Linear(8, 8), nn.LayerNorm(8), nn.Linear(8, 1)),
+                nn.Sequential(nn.Linear(8, 100), nn.ReLU(), nn.Linear(100, 1))):
+        net = net.to(DEV)
+
+        class Scored(tg.MessagePassing):
+            reducer = tg.online_softmax()
+
+            def __init__(self):
+                super().__init__()
+                self.net = tg.nn.trace(net)
+
+            def edge(self, src, dst, edge):
+                return self.reducer(self.net(src.x, dst.x), src.x)
+
+        k = Scored()
+        with pytest.raises(RuntimeError, match="strict"):
+            k(graph=graph, src={"x": x}, dst={"x": x})
+        tg.config.strict = False
+        out = k(graph=graph, src={"x": x}, dst={"x": x})
+        tg.config.strict = True
+        assert k.last_variant.backend == "torch-eager"
+        dst = graph.destination_index()
+        s = net(torch.cat([x[col], x[dst]], 1))[:, 0]
+        rp_np = f64(rp).astype(np.int64)
+        e_out, _ = ref.segment_softmax(rp_np, f64(s), f64(x)[f64(col).astype(np.int64)])
+        assert rel_err(f64(out), e_out) <= RTOL

@@ -10,6 +10,7 @@ from pathlib import Path
 
 import numpy as np
 import pytest
+import torch
 
 from oracle import planner, ref
 
@@ -340,3 +341,81 @@ def test_planner_lit_vectors(case):
     res = planner.plan(case["rows"], case["max"], case["sum"], case["histogram"], case["has_node"])
     for key, value in case["expect"].items():
         assert res[key] == value, (key, res[key], value)
+
+
+# ---- nn-scored attention ----------------------------------------------------
+
+def _nn_case(seed):
+    rng = np.random.default_rng(seed)
+    rp, col = random_csr(rng, 7, 6, 4)
+    E = col.size
+    x = rng.standard_normal((6, 3))
+    y = rng.standard_normal((7, 2))
+    ef = rng.standard_normal((E, 2))
+    inputs = [("src", x), ("dst", y), ("edge", ef)]
+    layers = [(rng.standard_normal((5, 7)) * 0.5, rng.standard_normal(5) * 0.1, "gelu", 0.0),
+              (rng.standard_normal((4, 5)) * 0.5, None, "leaky_relu", 0.2),
+              (rng.standard_normal((1, 4)) * 0.5, rng.standard_normal(1) * 0.1, "identity", 0.0)]
+    value = rng.standard_normal((6, 3))
+    dout = rng.standard_normal((7, 3))
+    return rp, col, inputs, layers, value, dout
+
+
+def test_nn_attention_bwd_finite_differences():
+    rp, col, inputs, layers, value, dout = _nn_case(21)
+    dinputs, dvalue, dlayers = ref.nn_attention_bwd(rp, col, inputs, layers, value, dout)
+    f = lambda: (ref.nn_attention_fwd(rp, col, inputs, layers, value)[0] * dout).sum()
+    eps = 1e-6
+
+    def check(arr, grad):
+        for idx in np.ndindex(arr.shape):
+            arr[idx] += eps
+            fp = f()
+            arr[idx] -= 2 * eps
+            fm = f()
+            arr[idx] += eps
+            assert abs((fp - fm) / (2 * eps) - grad[idx]) < 1e-6, idx
+
+    for (_, arr), g in zip(inputs, dinputs):
+        check(arr, g)
+    check(value, dvalue)
+    for (W, b, _, _), (dW, db) in zip(layers, dlayers):
+        check(W, dW)
+        if b is not None:
+            check(b, db)
+
+
+def test_nn_attention_matches_torch_autograd_float64():
+    """The same composition written with Torch ops in float64 (gather,
+    concatenation, the nn.Module chain, segment softmax by index ops) and
+    differentiated by autograd."""
+    rp, col, inputs, layers, value, dout = _nn_case(22)
+    dst = torch.as_tensor(ref.destination_index(rp))
+    colt = torch.as_tensor(col)
+    ts = [torch.tensor(a, requires_grad=True) for _, a in inputs]
+    gathered = [t[colt] if r == "src" else t[dst] if r == "dst" else t
+                for (r, _), t in zip(inputs, ts)]
+    net = torch.nn.Sequential(torch.nn.Linear(7, 5), torch.nn.GELU(), torch.nn.Linear(5, 4, bias=False),
+                              torch.nn.LeakyReLU(0.2), torch.nn.Linear(4, 1)).double()
+    with torch.no_grad():
+        for lin, (W, b, _, _) in zip([net[0], net[2], net[4]], layers):
+            lin.weight.copy_(torch.as_tensor(W))
+            if b is not None:
+                lin.bias.copy_(torch.as_tensor(b))
+    s = net(torch.cat(gathered, dim=1))[:, 0]
+    v = torch.tensor(value, requires_grad=True)
+    n = rp.size - 1
+    m = torch.full((n,), -torch.inf, dtype=torch.float64).scatter_reduce(0, dst, s, "amax")
+    p = torch.exp(s - m[dst])
+    den = torch.zeros(n, dtype=torch.float64).index_add(0, dst, p)
+    out = torch.zeros(n, 3, dtype=torch.float64).index_add(0, dst, v[colt] * p[:, None])
+    out = torch.where(den[:, None] > 0, out / den.clamp_min(1e-300)[:, None], 0.0)
+    e_out, _ = ref.nn_attention_fwd(rp, col, inputs, layers, value)
+    np.testing.assert_allclose(out.detach().numpy(), e_out, rtol=1e-12, atol=1e-12)
+    params = [net[0].weight, net[0].bias, net[2].weight, net[4].weight, net[4].bias]
+    got = torch.autograd.grad(out, ts + [v] + params, torch.as_tensor(dout))
+    dinputs, dvalue, dlayers = ref.nn_attention_bwd(rp, col, inputs, layers, value, dout)
+    expect = dinputs + [dvalue, dlayers[0][0], dlayers[0][1], dlayers[1][0], dlayers[2][0],
+                        dlayers[2][1]]
+    for a, b in zip(got, expect):
+        np.testing.assert_allclose(a.numpy(), b, rtol=1e-10, atol=1e-12)

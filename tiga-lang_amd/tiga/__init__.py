@@ -4,7 +4,7 @@ Public names follow the reference package (python/tiga/__init__.py:45-66):
 ``tiga.MessagePassing``, ``tiga.Graph``, ``tiga.sum``, ``tiga.online_softmax``.
 """
 
-from . import interop, reducer
+from . import interop, nn, reducer
 from .graph import Graph
 from .kernel import CompiledVariant, Kernel
 from .message_passing import MessagePassing, config
@@ -32,6 +32,7 @@ __all__ = [
     "SumReducer",
     "config",
     "interop",
+    "nn",
     "online_softmax",
     "reducer",
     "sum",

@@ -41,6 +41,16 @@ class RowPlan(ctypes.Structure):
     ]
 
 
+class EdgeMlp(ctypes.Structure):
+    """Mirror of ``tgx_edge_mlp``."""
+
+    _fields_ = [("n_layers", ctypes.c_int32), ("width", ctypes.c_int32),
+                ("act", ctypes.c_int32 * 3), ("act_param", ctypes.c_float * 3),
+                ("weights_dev", c_vp), ("n_segments", ctypes.c_int32),
+                ("seg_role", ctypes.c_int32 * 4), ("seg_width", ctypes.c_int32 * 4),
+                ("seg_stride", ctypes.c_int64 * 4), ("seg_dev", c_vp * 4)]
+
+
 # name -> argtypes (all return int status except where noted)
 _SIGNATURES: dict[str, list] = {
     "tgx_abi_version": [],
@@ -85,6 +95,11 @@ _SIGNATURES: dict[str, list] = {
     "tgx_attn_bwd": [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp, c_vp,
                      P(c_i64), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                      c_int, c_int, c_vp],
+    "tgx_edge_mlp_scores": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp],
+    "tgx_edge_mlp_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, c_vp,
+                              P(c_vp), c_vp],
+    "tgx_segment_softmax_fwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
+    "tgx_segment_softmax_bwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tgx_profile_begin": [],
     "tgx_profile_end": [],
     "tgx_profile_count": [],

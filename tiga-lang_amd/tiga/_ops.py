@@ -259,3 +259,183 @@ class BlockAttentionFunction(torch.autograd.Function):
                      delta.data_ptr(), n_q, n_k, H, D, _native.stream_of(q))
         return dq, dk, dv, None, None, None
 
+
+
+# ---------------------------------------------------------------------------
+# nn-scored edge attention (tgx_nn.hip)
+
+_ROLE = {"src": 0, "dst": 1, "edge": 2}
+
+
+def _padded_width(chain, in_width: int) -> int:
+    widest = max([in_width] + [max(l.linear.in_features, l.linear.out_features) for l in chain])
+    return next(w for w in (16, 32, 64) if w >= widest)
+
+
+def _mlp_struct(chain, roles, segs, weights_buf, width):
+    from .nn import _ACT
+
+    m = _native.EdgeMlp()
+    m.n_layers = len(chain)
+    m.width = width
+    for l, layer in enumerate(chain):
+        m.act[l] = _ACT[layer.act]
+        m.act_param[l] = layer.param
+    m.weights_dev = weights_buf.data_ptr()
+    m.n_segments = len(segs)
+    for s, (role, seg) in enumerate(zip(roles, segs)):
+        m.seg_role[s] = _ROLE[role]
+        m.seg_width[s] = seg.shape[1]
+        m.seg_stride[s] = seg.stride(0)
+        m.seg_dev[s] = seg.data_ptr()
+    return m
+
+
+def _as_rows(t: torch.Tensor) -> torch.Tensor:
+    """A field as [rows, width] fp32 with unit column stride."""
+    t2 = t.reshape(t.shape[0], -1) if t.ndim != 2 else t
+    if t2.stride(-1) != 1 or t2.stride(0) < t2.shape[1]:
+        t2 = t2.contiguous()
+    return t2
+
+
+class EdgeMlpFunction(torch.autograd.Function):
+    """scores[e] = net(concat of the fields gathered for edge e).
+
+    Inputs after (graph, chain, roles, n_seg): the n_seg field tensors, then
+    weight and bias (None allowed) of every Linear layer."""
+
+    @staticmethod
+    def forward(ctx, graph: Graph, chain, roles, n_seg: int, *tensors):
+        segs = [_as_rows(t) for t in tensors[:n_seg]]
+        params = tensors[n_seg:]
+        row_ptr, col_idx = graph._kernel_csr()
+        E = col_idx.numel()
+        in_width = sum(s.shape[1] for s in segs)
+        W = _padded_width(chain, in_width)
+        dev = col_idx.device
+        buf = torch.zeros(len(chain), W * W + W, dtype=torch.float32, device=dev)
+        for l, layer in enumerate(chain):
+            weight, bias = params[2 * l], params[2 * l + 1]
+            out_f, in_f = weight.shape
+            buf[l, :W * W].view(W, W)[:out_f, :in_f] = weight.detach()
+            if bias is not None:
+                buf[l, W * W:W * W + out_f] = bias.detach()
+        mlp = _mlp_struct(chain, roles, segs, buf, W)
+        scores = torch.empty(E, dtype=torch.float32, device=dev)
+        _native.call("tgx_edge_mlp_scores", col_idx.data_ptr(), graph._dst_index32().data_ptr(),
+                     _native.idx_bits(row_ptr), E, ctypes.byref(mlp), scores.data_ptr(),
+                     _native.stream_of(col_idx))
+        ctx.graph, ctx.chain, ctx.roles, ctx.n_seg, ctx.W = graph, chain, roles, n_seg, W
+        ctx.shapes = [t.shape for t in tensors[:n_seg]]
+        ctx.has_bias = [params[2 * l + 1] is not None for l in range(len(chain))]
+        ctx.save_for_backward(buf, *segs)
+        return scores
+
+    @staticmethod
+    def backward(ctx, dscore):
+        buf, *segs = ctx.saved_tensors
+        graph, chain, roles, W = ctx.graph, ctx.chain, ctx.roles, ctx.W
+        row_ptr, col_idx = graph._kernel_csr()
+        E = col_idx.numel()
+        dev = col_idx.device
+        L = len(chain)
+        dscore = dscore.contiguous()
+        acts = torch.empty(L, E, W, dtype=torch.float32, device=dev)
+        dz = torch.empty(L, E, W, dtype=torch.float32, device=dev)
+        dsegs = [torch.empty(E, s.shape[1], dtype=torch.float32, device=dev) for s in segs]
+        mlp = _mlp_struct(chain, roles, segs, buf, W)
+        ptrs = (ctypes.c_void_p * 4)(*[d.data_ptr() for d in dsegs], *([None] * (4 - len(dsegs))))
+        _native.call("tgx_edge_mlp_backward", col_idx.data_ptr(),
+                     graph._dst_index32().data_ptr(), _native.idx_bits(row_ptr), E,
+                     ctypes.byref(mlp), dscore.data_ptr(), acts.data_ptr(), dz.data_ptr(),
+                     ptrs, _native.stream_of(col_idx))
+        grads = []
+        for s, (role, d, shape) in enumerate(zip(roles, dsegs, ctx.shapes)):
+            if not ctx.needs_input_grad[4 + s]:
+                grads.append(None)
+                continue
+            if role == "edge":
+                g = d
+            elif role == "src":
+                g = _reduce_rows_transposed(graph, d)
+            else:
+                g = _reduce_rows(graph, d)
+            grads.append(g.reshape(shape))
+        for l, layer in enumerate(chain):
+            out_f, in_f = layer.linear.out_features, layer.linear.in_features
+            k = 4 + ctx.n_seg + 2 * l
+            dW = torch.mm(dz[l].t(), acts[l])[:out_f, :in_f] if ctx.needs_input_grad[k] else None
+            db = (dz[l].sum(0)[:out_f] if ctx.has_bias[l] and ctx.needs_input_grad[k + 1]
+                  else None)
+            grads += [dW, db]
+        return (None, None, None, None, *grads)
+
+
+def _reduce_rows(graph: Graph, x: torch.Tensor) -> torch.Tensor:
+    """out[i] = sum of x[e] over the edges e of destination row i (CSR sum
+    with the edge ids as columns)."""
+    row_ptr, _ = graph._kernel_csr()
+    n_dst, E = graph.schema.num_dst, x.shape[0]
+    F = x.shape[1]
+    out = torch.empty(n_dst, F, dtype=torch.float32, device=x.device)
+    if n_dst:
+        plan = graph._row_plan()
+        partial = _partial(plan, F, x.device)
+        _native.call("tgx_csr_sum_fwd", row_ptr.data_ptr(), graph._edge_iota().data_ptr(),
+                     _native.idx_bits(row_ptr), plan.ref, x.data_ptr(), None, out.data_ptr(),
+                     n_dst, E, F, _p(partial), _native.stream_of(x))
+    return out
+
+
+def _reduce_rows_transposed(graph: Graph, x: torch.Tensor) -> torch.Tensor:
+    """out[j] = sum of x[e] over the edges e whose source is j (CSR sum over
+    the transposed CSR with perm as columns)."""
+    t = graph._transposed()
+    n_src, E, F = graph.schema.num_src, x.shape[0], x.shape[1]
+    out = torch.empty(n_src, F, dtype=torch.float32, device=x.device)
+    if n_src:
+        partial = _partial(t.plan, F, x.device)
+        _native.call("tgx_csr_sum_fwd", t.row_ptr_t.data_ptr(), t.perm.data_ptr(), 32,
+                     t.plan.ref, x.data_ptr(), None, out.data_ptr(), n_src, E, F,
+                     _p(partial), _native.stream_of(x))
+    return out
+
+
+class SegmentSoftmaxFunction(torch.autograd.Function):
+    """alpha[e] = softmax of the scores over the edges of each CSR row."""
+
+    @staticmethod
+    def forward(ctx, scores: torch.Tensor, graph: Graph):
+        row_ptr, _ = graph._kernel_csr()
+        n = graph.schema.num_dst
+        alpha = torch.empty_like(scores)
+        lse = torch.empty(max(n, 1), dtype=torch.float32, device=scores.device)
+        _native.call("tgx_segment_softmax_fwd", row_ptr.data_ptr(), _native.idx_bits(row_ptr),
+                     n, scores.data_ptr(), alpha.data_ptr(), lse.data_ptr(),
+                     _native.stream_of(scores))
+        ctx.graph = graph
+        ctx.save_for_backward(alpha)
+        return alpha
+
+    @staticmethod
+    def backward(ctx, dalpha):
+        (alpha,) = ctx.saved_tensors
+        graph = ctx.graph
+        row_ptr, _ = graph._kernel_csr()
+        dalpha = dalpha.contiguous()
+        dscore = torch.empty_like(alpha)
+        _native.call("tgx_segment_softmax_bwd", row_ptr.data_ptr(), _native.idx_bits(row_ptr),
+                     graph.schema.num_dst, alpha.data_ptr(), dalpha.data_ptr(),
+                     dscore.data_ptr(), _native.stream_of(alpha))
+        return dscore, None
+
+
+def nn_attention(graph: Graph, chain, roles, fields, value: torch.Tensor) -> torch.Tensor:
+    """out[i] = sum_e softmax_i(net(fields_e)) value[col[e]] on the HIP path."""
+    params = []
+    for layer in chain:
+        params += [layer.linear.weight, layer.linear.bias]
+    scores = EdgeMlpFunction.apply(graph, chain, tuple(roles), len(fields), *fields, *params)
+    alpha = SegmentSoftmaxFunction.apply(scores, graph)
+    return CsrSumFunction.apply(value, alpha, graph)

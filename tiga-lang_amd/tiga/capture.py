@@ -11,7 +11,8 @@ kernels:
 * GAT additive   ``leaky_relu((src.h*a_s).sum(-1) + (dst.h*a_d).sum(-1))``,
                  value ``src.h``                            with online softmax
 * dot product    ``(src.k*dst.q).sum(-1) [* scale] [+ edge.b]``, value ``src.v``
-* varlen causal  the dot product on a ``Graph.cu_seqlens(causal=True)`` graph
+* varlen / dense the dot product on ``Graph.cu_seqlens`` / ``dense`` / ``triangular``
+* nn-scored      ``reducer(tg.nn.trace(net)(fields...), src.v)``
 
 Anything else is not an error: the call runs on the eager Torch evaluator.
 """
@@ -278,6 +279,34 @@ def recognize_dot(item) -> DotProduct | None:
                       bias_field=bias)
 
 
+@dataclass(frozen=True)
+class NnAttention:
+    module: Any                               # tiga.nn.TracedModule
+    inputs: tuple[tuple[str, str], ...]       # (role, field) in concatenation order
+    value_field: str                          # src.v
+
+
+def recognize_nn_attention(item) -> NnAttention | None:
+    """reducer(trace(net)(fields...), src.v) with a score chain the edge MLP
+    kernels cover (reference compiler/edge_nn_attention.py:66-107)."""
+    if not isinstance(item, OnlineSoftmaxItem):
+        return None
+    score, value = item.score, item.value
+    if not _is_field(value, "src"):
+        return None
+    if not (isinstance(score, Sym) and score.op == "nn"):
+        return None
+    module, inputs = score.args
+    if not inputs or module.chain() is None:
+        return None
+    fields = []
+    for x in inputs:
+        if not _is_field(x):
+            return None
+        fields.append(tuple(x.args))
+    return NnAttention(module=module, inputs=tuple(fields), value_field=value.args[1])
+
+
 def capture(edge_fn, params: dict[str, Any]):
     """Run ``edge_fn`` on symbolic namespaces; None when it cannot be captured."""
     sym_params = {}
@@ -302,10 +331,12 @@ __all__ = [
     "DotProduct",
     "FieldNamespace",
     "GatAdditive",
+    "NnAttention",
     "Sym",
     "WeightedSum",
     "capture",
     "recognize_dot",
     "recognize_gat",
+    "recognize_nn_attention",
     "recognize_weighted_sum",
 ]

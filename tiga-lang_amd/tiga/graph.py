@@ -530,6 +530,28 @@ class Graph:
             self._native_cache["csr"] = got
         return got
 
+    def _dst_index32(self) -> torch.Tensor:
+        """Destination row of every edge, int32, on the device (cached)."""
+        got = self._native_cache.get("dst32")
+        if got is None:
+            row_ptr, col_idx = self._kernel_csr()
+            E = col_idx.numel()
+            got = torch.empty(max(E, 1), dtype=torch.int32, device=row_ptr.device)
+            _native.call("tgx_destination_index", row_ptr.data_ptr(), _native.idx_bits(row_ptr),
+                         self._schema.num_dst, E, got.data_ptr(), 32,
+                         _native.stream_of(row_ptr))
+            self._native_cache["dst32"] = got
+        return got
+
+    def _edge_iota(self) -> torch.Tensor:
+        """0..E-1 in the CSR's index dtype: the edge ids as CSR columns."""
+        got = self._native_cache.get("iota")
+        if got is None:
+            row_ptr, col_idx = self._kernel_csr()
+            got = torch.arange(col_idx.numel(), dtype=row_ptr.dtype, device=row_ptr.device)
+            self._native_cache["iota"] = got
+        return got
+
     def _attn_blocks(self):
         """(cu_q, cu_k, causal) of a block-diagonal relation as int32 host
         arrays: cu_seqlens for varlen, one block for dense/triangular."""

@@ -218,7 +218,53 @@ class MessagePassing(Kernel):
         dot = cap.recognize_dot(captured)
         if dot is not None:
             return self._execute_dot(dot, graph, src, dst, edge)
+        nn_item = cap.recognize_nn_attention(captured)
+        if nn_item is not None:
+            return self._execute_nn_attention(nn_item, graph, src, dst, edge)
         return None
+
+    def _execute_nn_attention(self, item, graph, src, dst, edge):
+        """tg.nn.trace-scored attention on the edge MLP kernels (reference
+        interop/torch/message_passing.py:2372-2577, envelope: fp32, CSR
+        relation, one score per edge, one gathered value field)."""
+        from . import _ops
+
+        if graph.is_varlen or graph.is_dense:
+            return None
+        if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
+            return None
+        groups = {"src": src, "dst": dst, "edge": edge}
+        rows = {"src": graph.schema.num_src, "dst": graph.schema.num_dst,
+                "edge": graph.num_edges}
+        fields, roles = [], []
+        for role, name in item.inputs:
+            t = groups[role].get(name)
+            if t is None or t.dtype != torch.float32 or t.ndim not in (1, 2) or \
+                    t.shape[0] != rows[role]:
+                return None
+            fields.append(t if t.ndim == 2 else t.unsqueeze(-1))
+            roles.append(role)
+        if len(fields) > 4 or sum(f.shape[1] for f in fields) > 64:
+            return None
+        value = src.get(item.value_field)
+        if value is None or value.dtype != torch.float32:
+            return None
+        chain = item.module.chain()
+        for layer in chain:
+            for p in (layer.linear.weight, layer.linear.bias):
+                if p is not None and (p.dtype != torch.float32 or p.device != value.device):
+                    return None
+        _native.lib()
+        out = _ops.nn_attention(graph, chain, roles, fields, value)
+        widths = "-".join(str(l.linear.in_features) for l in chain) + "-1"
+        self._record_native(
+            graph, "nn-attention",
+            ("tgx_edge_mlp_scores", "tgx_segment_softmax_fwd", "tgx_csr_sum_fwd",
+             "tgx_csr_sum_bwd", "tgx_segment_softmax_bwd", "tgx_edge_mlp_backward"),
+            f"edge-parallel score network {widths} (one edge per lane, uniform weights), "
+            "segment softmax per row, weighted CSR sum of the value; backward through the "
+            "softmax Jacobian, per-edge network replay, weight gradients as GEMMs")
+        return out
 
     def _execute_dot(self, dot, graph, src, dst, edge):
         from . import _ops
