@@ -8,11 +8,13 @@ HBM.  Prints ONE JSON line (rank 0): edges/s, ms/step, the dominant kernel's
 roofline (algorithmic bytes / its live HIP-event duration) and the
 reference's CPU path timed on a bounded sample of the same workload.
 
-  python bench.py [--steps K] [--warmup W] [--config c1..c5|dense|dense-causal|dense-pruned]
+  python bench.py [--steps K] [--warmup W]
+                  [--config c1..c5|dense|dense-causal|dense-pruned|nn]
                   [--no-cpu]
 
 c1-c5 are BASELINE.json's configurations; dense* are the reference's dense
-attention benchmark shapes (N=4096, H=16, D=64, fp16, forward).
+attention benchmark shapes (N=4096, H=16, D=64, fp16, forward); nn is the
+reference's nn-scored GAT training step (131072 nodes, net 19-16-1).
 """
 
 from __future__ import annotations
@@ -52,7 +54,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2",
                     choices=["c1", "c2", "c3", "c4", "c5", "dense", "dense-causal",
-                             "dense-pruned"])
+                             "dense-pruned", "nn"])
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=None)
@@ -622,6 +624,93 @@ def run_dense(args):
     }
 
 
+def run_nn(args):
+    """The reference's nn-scored GAT training step (benchmarks/neural_networks/
+    gat_attention.py, evidence case cuda_n131072_degree32): 131072 nodes,
+    about 4.0M edges, score network Linear(3 + 2*8, 16) -> LeakyReLU(0.2) ->
+    Linear(16, 1) over [displacement | x_src | x_dst], value x_src (width 8),
+    fp32, forward + backward (gradients of x, the displacement and the
+    network).  The reference builds a radius graph (Graph.radius, out of scope
+    here); this uses the same node and mean edge count with Poisson(30.6)
+    in-degrees and uniformly random sources, and the displacement as an edge
+    field."""
+    import torch
+    from torch import nn
+
+    import tiga as tg
+    from tiga import _native
+
+    dev = torch.device("cuda")
+    N = args.nodes or 131072
+    row_ptr, col = poisson_self_loop_csr(N, 29.6, args.seed, dev)
+    E = col.numel()
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    pos = torch.rand(N, 3, device=dev, generator=g)
+    x = torch.randn(N, 8, device=dev, generator=g).requires_grad_(True)
+    graph = tg.Graph.from_csr(row_ptr, col, num_src=N)
+    disp = (pos[col] - pos[graph.destination_index()]).requires_grad_(True)
+    torch.manual_seed(args.seed)
+    attn = nn.Sequential(nn.Linear(19, 16), nn.LeakyReLU(0.2), nn.Linear(16, 1)).to(dev)
+    dout = torch.randn(N, 8, device=dev, generator=g)
+    tg.config.strict = True
+
+    class GAT(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def __init__(self):
+            super().__init__()
+            self.attn = tg.nn.trace(attn)
+
+        def edge(self, src, dst, edge):
+            return self.reducer(self.attn(edge.displacement, src.x, dst.x), src.x)
+
+    kernel = GAT()
+
+    def step():
+        x.grad = disp.grad = None
+        attn.zero_grad(set_to_none=True)
+        kernel(graph=graph, src={"x": x}, dst={"x": x},
+               edge={"displacement": disp}).backward(dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    assert kernel.last_variant.backend == "hip"
+    with _native.KernelTimer() as timer:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / args.steps
+    # Algorithmic bytes per pass (no-reuse model, 4 B indices): scores read
+    # col, dst, disp (12 B) and x twice (2 x 32 B) per edge and write 4 B.
+    bytes_per = {
+        "edge_mlp_fwd_kernel": E * (4 + 4 + 12 + 64 + 4),
+        "edge_mlp_bwd_kernel": E * (4 + 4 + 12 + 64 + 4 + 2 * 2 * 16 * 4 + 12 + 2 * 32),
+        "csr_sum_fwd": E * (4 + 4 + 32) + N * (4 + 32),
+    }
+    per = timer.totals
+    dominant = max((k for k in per if k in bytes_per), key=lambda k: per[k][1])
+    n_launch, total_ms = per[dominant]
+    achieved = bytes_per[dominant] / (total_ms / n_launch * 1e-3) / 1e9
+    return {
+        "metric": "nn-scored GAT training step edges/s (score net 19-16-1, value 8, fp32), "
+                  "131072 nodes, 1xMI355X",
+        "value": E * args.steps / elapsed, "unit": "edges/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (Poisson(30.6) in-degree, uniform sources, x ~N(0,1), "
+                "displacement from uniform positions)",
+        "config": {"workload": "nn-gat-fwd-bwd", "nodes": N, "edges": E, "attn": "19-16-1",
+                   "value_width": 8, "reference_ms_own_gpu": 10.97},
+        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None, "algorithmic_bytes": bytes_per[dominant]},
+        "kernels": {k: {"launches": n, "avg_ms": t / n} for k, (n, t) in sorted(per.items())},
+    }
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
@@ -633,7 +722,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     runners = {"c1": run_c1, "c2": run_c2, "c3": run_c3c4, "c4": run_c3c4, "c5": run_c5,
-               "dense": run_dense, "dense-causal": run_dense, "dense-pruned": run_dense}
+               "dense": run_dense, "dense-causal": run_dense, "dense-pruned": run_dense,
+               "nn": run_nn}
     result = runners[args.config](args)
     print(json.dumps(result), flush=True)
 

@@ -441,6 +441,17 @@ int tgx_edge_mlp_backward(const void* col_dev, const int32_t* dst_index_dev, int
                           float* acts_dev, float* dz_dev, float* const* dseg,
                           void* stream);
 
+/* Workspace bytes needed by tgx_edge_outer_sum. */
+int tgx_edge_outer_sum_workspace(int64_t n_edges, int width, size_t* bytes);
+
+/* Weight and bias gradients of one score-network layer from the planes of
+ * tgx_edge_mlp_backward: dw[o*width + i] = sum_e g[e][o] a[e][i] and
+ * db[o] = sum_e g[e][o] (db may be NULL); g, a [n_edges, width] fp32.
+ * Two passes, partial sums added in a fixed order: deterministic. */
+int tgx_edge_outer_sum(const float* g_dev, const float* a_dev, int64_t n_edges, int width,
+                       float* dw_dev, float* db_dev, void* workspace_dev,
+                       size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Per-kernel timing (no reference counterpart; used by the benchmark)       */
 /* ------------------------------------------------------------------------ */

@@ -28,6 +28,8 @@
 // per destination row over the CSR by the caller).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "tgx_device.h"
 #include "tgx_host.h"
 #include "tgx_profile.h"
@@ -122,17 +124,44 @@ __device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const
   }
 }
 
-// z = W_l a + b_l over the padded width.
+// Keeps v's computation at this point of the program.  Without it the
+// optimizer sinks each dot product to its first use, behind the uniform
+// branches of the activation that follows, i.e. after every weight load of
+// the layer, and all W*W weights of the layer end up live at once.
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+
+// f(integral_constant<0>) ... f(integral_constant<N-1>): a loop whose index
+// is a compile-time constant in the body (register arrays indexed by it stay
+// in registers whatever the body's size).
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+}
+
+// z = W_l a + b_l over the padded width, one weight row at a time (wl is
+// uniform across the wave).
 template <int W>
-__device__ __forceinline__ void linear(const float* __restrict__ wl, const float (&a)[W],
-                                       float (&z)[W]) {
+__device__ __forceinline__ void linear(const float* wl, const float (&a)[W], float (&z)[W]) {
 #pragma unroll
   for (int o = 0; o < W; ++o) {
     float acc = wl[W * W + o];
 #pragma unroll
     for (int i = 0; i < W; ++i) acc = fmaf(wl[o * W + i], a[i], acc);
+    pin(acc);
     z[o] = acc;
+    __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// The weights of all layers, staged once per workgroup in LDS (every lane
+// then reads the same address: a broadcast).
+template <int W, int L>
+__device__ __forceinline__ void stage_weights(const float* __restrict__ w, float* wsh) {
+  for (int i = threadIdx.x; i < L * (W * W + W); i += 256) wsh[i] = w[i];
+  __syncthreads();
 }
 
 template <typename I, int W, int L>
@@ -140,19 +169,21 @@ __global__ __launch_bounds__(256) void edge_mlp_fwd_kernel(const I* __restrict__
                                                            const int32_t* __restrict__ dst,
                                                            int64_t n_edges, MlpView m,
                                                            float* __restrict__ scores) {
+  __shared__ float wsh[L * (W * W + W)];
+  stage_weights<W, L>(m.w, wsh);
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (e >= n_edges) return;
   float a[W], z[W];
   gather_inputs<I, W>(m, e, col, dst, a);
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
-    linear<W>(m.w + l * (W * W + W), a, z);
+    linear<W>(wsh + l * (W * W + W), a, z);
     const int act = m.act[l];
     const float p = m.param[l];
 #pragma unroll
     for (int o = 0; o < W; ++o) a[o] = activate(z[o], act, p);
   }
-  const float* wl = m.w + (L - 1) * (W * W + W);
+  const float* wl = wsh + (L - 1) * (W * W + W);
   float s = wl[W * W];
 #pragma unroll
   for (int i = 0; i < W; ++i) s = fmaf(wl[i], a[i], s);
@@ -167,29 +198,31 @@ template <typename I, int W, int L>
 __global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
     const I* __restrict__ col, const int32_t* __restrict__ dst, int64_t n_edges, MlpView m,
     const float* __restrict__ dscore, float* __restrict__ acts, float* __restrict__ dz_out) {
+  __shared__ float wsh[L * (W * W + W)];
+  stage_weights<W, L>(m.w, wsh);
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (e >= n_edges) return;
   const int64_t plane = n_edges * W;
   float a[W];                       // input of the current layer
   float z[L > 1 ? L - 1 : 1][W];    // pre-activations of the hidden layers
   gather_inputs<I, W>(m, e, col, dst, a);
-#pragma unroll
-  for (int l = 0; l < L; ++l) {
+  static_for<L>([&](auto lc) {
+    constexpr int l = decltype(lc)::value;
     float* out = acts + l * plane + e * W;
 #pragma unroll
     for (int i = 0; i < W; i += 4)
       *reinterpret_cast<f32x4*>(out + i) = f32x4{a[i], a[i + 1], a[i + 2], a[i + 3]};
-    if (l + 1 < L) {
-      linear<W>(m.w + l * (W * W + W), a, z[l]);
+    if constexpr (l + 1 < L) {
+      linear<W>(wsh + l * (W * W + W), a, z[l]);
 #pragma unroll
       for (int o = 0; o < W; ++o) a[o] = activate(z[l][o], m.act[l], m.param[l]);
     }
-  }
+  });
   // Last layer: one output, gradient ds.
   const float ds = dscore[e];
   float g[W];
   {
-    const float* wl = m.w + (L - 1) * (W * W + W);
+    const float* wl = wsh + (L - 1) * (W * W + W);
     float* out = dz_out + (L - 1) * plane + e * W;
 #pragma unroll
     for (int i = 0; i < W; i += 4)
@@ -197,24 +230,32 @@ __global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
 #pragma unroll
     for (int i = 0; i < W; ++i) g[i] = ds * wl[i];   // d a[L-1]
   }
-#pragma unroll
-  for (int l = L - 2; l >= 0; --l) {
+  static_for<L - 1>([&](auto kc) {
+    constexpr int l = L - 2 - decltype(kc)::value;
     float dzl[W];
 #pragma unroll
-    for (int o = 0; o < W; ++o) dzl[o] = g[o] * activate_grad(z[l][o], m.act[l], m.param[l]);
+    for (int o = 0; o < W; ++o) {
+      dzl[o] = g[o] * activate_grad(z[l][o], m.act[l], m.param[l]);
+      pin(dzl[o]);
+    }
     float* out = dz_out + l * plane + e * W;
 #pragma unroll
     for (int i = 0; i < W; i += 4)
       *reinterpret_cast<f32x4*>(out + i) = f32x4{dzl[i], dzl[i + 1], dzl[i + 2], dzl[i + 3]};
-    const float* wl = m.w + l * (W * W + W);
+    // d a[l] = W_l^T dz, accumulated row by row so W_l is read in order.
+    const float* wl = wsh + l * (W * W + W);
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
-      float acc = 0.f;
+    for (int i = 0; i < W; ++i) g[i] = 0.f;
+    static_for<W>([&](auto oc) {
+      constexpr int o = decltype(oc)::value;
 #pragma unroll
-      for (int o = 0; o < W; ++o) acc = fmaf(wl[o * W + i], dzl[o], acc);
-      g[i] = acc;   // d a[l]
-    }
-  }
+      for (int i = 0; i < W; ++i) {
+        g[i] = fmaf(wl[o * W + i], dzl[o], g[i]);
+        pin(g[i]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  });
   // g = d x: split per segment.
 #pragma unroll
   for (int s = 0; s < kMaxSegments; ++s) {
@@ -261,6 +302,108 @@ __global__ __launch_bounds__(256) void segment_softmax_bwd_kernel(
   for (int64_t e = e0 + lane; e < e1; e += kWave) d += alpha[e] * dalpha[e];
   d = group_sum<kWave>(d);
   for (int64_t e = e0 + lane; e < e1; e += kWave) dscore[e] = alpha[e] * (dalpha[e] - d);
+}
+
+// v[0..B) = p[0..B) as 8- or 16-byte vector loads (p aligned to 4 B floats).
+template <int B>
+__device__ __forceinline__ void load_vec(const float* __restrict__ p, float (&v)[B]) {
+  if constexpr (B % 4 == 0) {
+#pragma unroll
+    for (int j = 0; j < B; j += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(p + j);
+      v[j] = t[0], v[j + 1] = t[1], v[j + 2] = t[2], v[j + 3] = t[3];
+    }
+  } else {
+    static_assert(B == 2, "2, 4 or 8 floats");
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x, v[1] = t.y;
+  }
+}
+
+// Weight gradients of one layer: S[o][i] = sum_e G[e][o] A[e][i] and
+// b[o] = sum_e G[e][o] over [n_edges, W] planes.  Each workgroup sums a chunk
+// of edges (its four waves take every fourth edge), lane (ob, ib) of a wave
+// owning the (W/8 x W/8) block of S at (ob, ib); the waves are added in LDS
+// and every workgroup writes its partial.  A second kernel adds the partials
+// in workgroup order: deterministic.
+template <int W>
+__global__ __launch_bounds__(256) void outer_sum_kernel(const float* __restrict__ g,
+                                                        const float* __restrict__ a,
+                                                        int64_t n_edges, int64_t chunk,
+                                                        float* __restrict__ partial) {
+  constexpr int B = W / 8;
+  constexpr int N = W * W + W;
+  __shared__ float red[4][N];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ob = lane / 8, ib = lane % 8;
+  float acc[B][B], bacc[B];
+#pragma unroll
+  for (int p = 0; p < B; ++p) {
+    bacc[p] = 0.f;
+#pragma unroll
+    for (int q = 0; q < B; ++q) acc[p][q] = 0.f;
+  }
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t e1 = e0 + chunk < n_edges ? e0 + chunk : n_edges;
+  auto accumulate = [&](const float (&gv)[B], const float (&av)[B]) {
+#pragma unroll
+    for (int p = 0; p < B; ++p) {
+      bacc[p] += gv[p];
+#pragma unroll
+      for (int q = 0; q < B; ++q) acc[p][q] = fmaf(gv[p], av[q], acc[p][q]);
+    }
+  };
+  // Whole steps of U edges per wave (four row loads per lane in flight, as
+  // vector loads), then the remainder one edge at a time.
+  constexpr int U = 4;
+  const int64_t full = e0 + (e1 - e0) / (4 * U) * (4 * U);
+  for (int64_t base = e0 + wave; base < full; base += 4 * U) {
+    float gv[U][B], av[U][B];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      load_vec<B>(g + (base + 4 * u) * W + ob * B, gv[u]);
+      load_vec<B>(a + (base + 4 * u) * W + ib * B, av[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) accumulate(gv[u], av[u]);
+  }
+  for (int64_t e = full + wave; e < e1; e += 4) {
+    float gv[B], av[B];
+    load_vec<B>(g + e * W + ob * B, gv);
+    load_vec<B>(a + e * W + ib * B, av);
+    accumulate(gv, av);
+  }
+#pragma unroll
+  for (int p = 0; p < B; ++p) {
+#pragma unroll
+    for (int q = 0; q < B; ++q) red[wave][(ob * B + p) * W + ib * B + q] = acc[p][q];
+    if (ib == 0) red[wave][W * W + ob * B + p] = bacc[p];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < N; idx += 256)
+    partial[static_cast<int64_t>(blockIdx.x) * N + idx] =
+        (red[0][idx] + red[1][idx]) + (red[2][idx] + red[3][idx]);
+}
+
+__global__ __launch_bounds__(256) void outer_sum_final_kernel(
+    const float* __restrict__ partial, int n_blocks, int n, int w, float* __restrict__ dw,
+    float* __restrict__ db) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= n) return;
+  float s = 0.f;
+  for (int b = 0; b < n_blocks; ++b) s += partial[static_cast<int64_t>(b) * n + idx];
+  if (idx < w * w)
+    dw[idx] = s;
+  else if (db)
+    db[idx - w * w] = s;
+}
+
+int outer_blocks(int64_t n_edges, int64_t* chunk) {
+  // About four workgroups per CU; chunks of whole waves of edges.
+  int64_t c = ceil_div(n_edges, 1024);
+  c = c < 64 ? 64 : align_up(static_cast<size_t>(c), 64);
+  *chunk = c;
+  return static_cast<int>(ceil_div(n_edges, c));
 }
 
 int check_mlp(const tgx_edge_mlp* mlp, MlpView* view) {
@@ -432,5 +575,42 @@ extern "C" int tgx_segment_softmax_bwd(const void* row_ptr, int idx_bits, int64_
     segment_softmax_bwd_kernel<<<ceil_div(n_rows, 4), 256, 0, s>>>(
         static_cast<const int64_t*>(row_ptr), n_rows, alpha, dalpha, dscore);
   TGX_LAUNCHED("segment_softmax_bwd_kernel");
+  return TGX_OK;
+}
+
+extern "C" int tgx_edge_outer_sum_workspace(int64_t n_edges, int width, size_t* bytes) {
+  TGX_REQUIRE(bytes, "null bytes");
+  TGX_REQUIRE(n_edges >= 0 && (width == 16 || width == 32 || width == 64), "bad sizes");
+  int64_t chunk = 0;
+  const int nb = n_edges ? outer_blocks(n_edges, &chunk) : 0;
+  *bytes = align_up(static_cast<size_t>(nb) * (width * width + width) * sizeof(float));
+  return TGX_OK;
+}
+
+extern "C" int tgx_edge_outer_sum(const float* g, const float* a, int64_t n_edges, int width,
+                                  float* dw, float* db, void* ws, size_t ws_bytes,
+                                  void* stream) {
+  TGX_REQUIRE(n_edges >= 0 && (width == 16 || width == 32 || width == 64), "bad sizes");
+  TGX_REQUIRE(dw, "null dw");
+  hipStream_t s = as_stream(stream);
+  const int n = width * width + width;
+  if (n_edges == 0) {
+    // Zero sums, written by a kernel rather than a memset.
+    outer_sum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(nullptr, 0, n, width, dw, db);
+    TGX_LAUNCHED("outer_sum_final_kernel");
+    return TGX_OK;
+  }
+  TGX_REQUIRE(g && a && ws, "null pointer");
+  int64_t chunk = 0;
+  const int nb = outer_blocks(n_edges, &chunk);
+  TGX_REQUIRE(ws_bytes >= static_cast<size_t>(nb) * n * sizeof(float), "workspace too small");
+  float* partial = static_cast<float*>(ws);
+  TGX_PROFILE("outer_sum_kernel", s);
+  if (width == 16) outer_sum_kernel<16><<<nb, 256, 0, s>>>(g, a, n_edges, chunk, partial);
+  if (width == 32) outer_sum_kernel<32><<<nb, 256, 0, s>>>(g, a, n_edges, chunk, partial);
+  if (width == 64) outer_sum_kernel<64><<<nb, 256, 0, s>>>(g, a, n_edges, chunk, partial);
+  TGX_LAUNCHED("outer_sum_kernel");
+  outer_sum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(partial, nb, n, width, dw, db);
+  TGX_LAUNCHED("outer_sum_final_kernel");
   return TGX_OK;
 }

@@ -362,12 +362,22 @@ class EdgeMlpFunction(torch.autograd.Function):
             else:
                 g = _reduce_rows(graph, d)
             grads.append(g.reshape(shape))
+        ws_bytes = ctypes.c_size_t()
+        _native.call("tgx_edge_outer_sum_workspace", E, W, ctypes.byref(ws_bytes))
+        ws = torch.empty(max(ws_bytes.value, 4), dtype=torch.uint8, device=dev)
         for l, layer in enumerate(chain):
             out_f, in_f = layer.linear.out_features, layer.linear.in_features
             k = 4 + ctx.n_seg + 2 * l
-            dW = torch.mm(dz[l].t(), acts[l])[:out_f, :in_f] if ctx.needs_input_grad[k] else None
-            db = (dz[l].sum(0)[:out_f] if ctx.has_bias[l] and ctx.needs_input_grad[k + 1]
-                  else None)
+            if not (ctx.needs_input_grad[k] or ctx.needs_input_grad[k + 1]):
+                grads += [None, None]
+                continue
+            dw_full = torch.empty(W, W, dtype=torch.float32, device=dev)
+            db_full = torch.empty(W, dtype=torch.float32, device=dev)
+            _native.call("tgx_edge_outer_sum", dz[l].data_ptr(), acts[l].data_ptr(), E, W,
+                         dw_full.data_ptr(), db_full.data_ptr(), ws.data_ptr(), ws_bytes.value,
+                         _native.stream_of(dz))
+            dW = dw_full[:out_f, :in_f] if ctx.needs_input_grad[k] else None
+            db = db_full[:out_f] if ctx.has_bias[l] and ctx.needs_input_grad[k + 1] else None
             grads += [dW, db]
         return (None, None, None, None, *grads)
 
