@@ -10,7 +10,7 @@ reference's CPU path timed on a bounded sample of the same workload.
 
   python bench.py [--steps K] [--warmup W]
                   [--config c1..c5|dense|dense-causal|dense-pruned|nn]
-                  [--no-cpu]
+                  [--no-cpu] [--no-cold]
 
 c1-c5 are BASELINE.json's configurations; dense* are the reference's dense
 attention benchmark shapes (N=4096, H=16, D=64, fp16, forward); nn is the
@@ -57,6 +57,9 @@ def parse():
                              "dense-pruned", "nn"])
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cold", action="store_true",
+                    help="skip the cold-cache samples (kernel traces then hold only the "
+                         "warmup and timed launches)")
     ap.add_argument("--cpu-rows", type=int, default=None)
     ap.add_argument("--seed", type=int, default=20260821)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -206,6 +209,136 @@ def cpu_baseline_gat(row_ptr, col, h, a_src, a_dst, slope, rows):
                       f"({e} edges) gathering from the full 1M-node table, {reps} reps"}
 
 
+def cold_step_ms(step, samples=5):
+    """Median step time with L2 and the 256 MB MALL flushed before each
+    sample (a 1 GiB fill), HIP events on Torch's current stream, which is
+    where every kernel of the step runs.  None with --no-cold."""
+    import torch
+
+    if ARGS.no_cold:
+        return None
+
+    flush = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    times = []
+    for _ in range(samples):
+        flush.fill_(1.0)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        step()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+    del flush
+    return sorted(times)[len(times) // 2]
+
+
+def _timed_reps(fn, budget_s=10.0, max_reps=3):
+    fn()
+    reps, t = 0, 0.0
+    while reps < max_reps and (reps == 0 or t < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        t += time.perf_counter() - t0
+        reps += 1
+    return reps, t
+
+
+def cpu_baseline_sum(row_ptr, col, x, w):
+    """C1 on the host: the reference's native CPU runtime loop
+    (oracle/cpu_native.c, forward; T = min(32, cores) threads as its default
+    pool, and T = cores) and the Torch CPU path the reference dispatches for
+    Torch tensors (torch.sparse.mm forward + autograd backward), whole graph."""
+    import numpy as np
+    import torch
+
+    from oracle import eager_torch, native
+
+    threads = cpu_cores()
+    torch.set_num_threads(threads)
+    rp, c = row_ptr.cpu(), col.cpu()
+    xc, wc = x.detach().cpu(), w.detach().cpu().reshape(-1)
+    E = c.numel()
+    dout = torch.ones(rp.numel() - 1, xc.shape[1])
+    reps, t = _timed_reps(lambda: eager_torch.sum_step(rp, c, xc, wc, dout))
+    rp_np, c_np, x_np, w_np = rp.numpy(), c.numpy(), xc.numpy(), wc.numpy()
+    out = np.empty((rp_np.size - 1, x_np.shape[1]), dtype=np.float32)
+    native_fwd = {}
+    for t_native in sorted({min(32, threads), threads}):
+        r, tn = _timed_reps(lambda: native.csr_sum_fwd(rp_np, c_np, x_np, w_np, t_native, out),
+                            budget_s=5.0, max_reps=10)
+        native_fwd[f"threads_{t_native}"] = E * r / tn
+    return {"value": E * reps / t, "unit": "edges/s", "cores": threads, "kind": "port",
+            "sample": f"whole C1 graph ({E} edges), fwd+bwd, reference's Torch CPU path "
+                      f"(torch.sparse.mm + autograd), {reps} reps",
+            "native_runtime_fwd_edges_per_s": native_fwd,
+            "native_runtime_bwd": "not run: the reference's lowered native backward is an "
+                                  "O(N_src*E) scan (~1e13 operations at C1 scale)"}
+
+
+def cpu_baseline_dot(row_ptr, col, q, k, v, bias, scale, dout, edges=1_000_000):
+    """C3/C4 on the host: the reference's eager Torch CPU path (gather,
+    scatter_reduce amax, exp, index_add, autograd) on the leading destination
+    rows holding about `edges` edges, gathering from the full tables.
+    Returns forward edges/s and backward edges/s (fwd+bwd minus fwd)."""
+    import torch
+
+    from oracle import eager_torch
+
+    threads = cpu_cores()
+    torch.set_num_threads(threads)
+    rpc = row_ptr.cpu()
+    rows = max(1, int(torch.searchsorted(rpc, edges, right=True)) - 1)
+    rp = rpc[: rows + 1]
+    e = int(rp[-1])
+    c = col[:e].cpu()
+    qc, kc, vc = (t.detach().cpu() for t in (q, k, v))
+    bc = bias.detach()[:e].cpu()
+    dc = dout[:rows].cpu()
+    qs = qc[:rows]
+    r_f, t_f = _timed_reps(lambda: eager_torch.dot_step(rp, c, qs, kc, vc, bc, scale))
+    r_s, t_s = _timed_reps(lambda: eager_torch.dot_step(rp, c, qs, kc, vc, bc, scale, dc))
+    fwd_s, step_s = t_f / r_f, t_s / r_s
+    sample = (f"reference eager Torch CPU path, bf16 inputs with fp32 accumulate, on the "
+              f"first {rows} destination rows ({e} edges) gathering from the full tables")
+    return e / fwd_s, e / max(step_s - fwd_s, 1e-9), threads, sample
+
+
+def cpu_baseline_varlen(lengths, q, k, v, dout, scale, pairs_target=120_000):
+    """C5 on the host: the reference's eager CPU path materializes every
+    causal pair (about 400 GB per gathered tensor at C5), so it runs on a
+    row chunk of the first sequence's materialized CSR (the last rows, about
+    `pairs_target` pairs), fwd + bwd; TFLOP/s uses the same FLOP convention
+    as the GPU figure (fwd 4*H*D per pair, bwd 2.5x)."""
+    import torch
+
+    from oracle import eager_torch
+
+    threads = cpu_cores()
+    torch.set_num_threads(threads)
+    L = int(lengths[0])
+    H, D = q.shape[1], q.shape[2]
+    r1 = L
+    r0 = r1
+    while r0 > 0 and (r1 * (r1 + 1) - r0 * (r0 + 1)) // 2 < pairs_target:
+        r0 -= 1
+    deg = torch.arange(r0 + 1, r1 + 1)
+    rp = torch.zeros(r1 - r0 + 1, dtype=torch.int64)
+    rp[1:] = torch.cumsum(deg, 0)
+    c = torch.cat([torch.arange(i + 1) for i in range(r0, r1)])
+    pairs = int(rp[-1])
+    qc, kc, vc = (t.detach()[:L].cpu() for t in (q, k, v))
+    dc = dout[r0:r1].cpu()
+    bias = torch.zeros(pairs, H)
+    reps, t = _timed_reps(lambda: eager_torch.dot_step(rp, c, qc[r0:r1], kc, vc, bias, scale,
+                                                       dc))
+    flops = 3.5 * 4.0 * H * D * pairs
+    return {"value": flops * reps / t / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"reference eager Torch CPU path (gathered pairs, scatter softmax, "
+                      f"autograd), fwd+bwd on query rows {r0}..{r1 - 1} of sequence 0 "
+                      f"(length {L}, {pairs} causal pairs), bf16 inputs, {reps} reps"}
+
+
 def run_c2(args):
     import torch
     import torch.nn.functional as F
@@ -252,6 +385,7 @@ def run_c2(args):
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
     per_kernel = {k: (n, ms) for k, (n, ms) in timer.totals.items()}
+    cold_ms = cold_step_ms(step)
     bytes_per = gat_kernel_bytes(N, E, H, D)
     step_bytes = sum(bytes_per.values())
     dominant = max((k for k in per_kernel if k in bytes_per), key=lambda k: per_kernel[k][1])
@@ -275,6 +409,7 @@ def run_c2(args):
         "config": {"workload": "c2-gat-additive-fwd-bwd", "nodes": N, "edges": E,
                    "heads": H, "head_dim": D, "index_dtype": "int64"},
         "hbm_frac_step": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "cold_ms_per_step": cold_ms,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic("c2", dominant)[0],
@@ -328,22 +463,29 @@ def run_c1(args):
             step()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
+    cold_ms = cold_step_ms(step)
     bytes_per = sum_kernel_bytes(N, N, E, F_)
     dominant = max((k for k in timer.totals if k in bytes_per), key=lambda k: timer.totals[k][1])
     n_launch, total_ms = timer.totals[dominant]
     achieved = bytes_per[dominant] / (total_ms / n_launch * 1e-3) / 1e9
-    return {
+    result = {
         "metric": "weighted-sum fwd+bwd edges/s, 100k x deg-16, F=64, 1xMI355X",
         "value": E * args.steps / elapsed, "unit": "edges/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": elapsed * 1e3 / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic", "config": {"workload": "c1-weighted-sum-fwd-bwd", "nodes": N,
                                         "edges": E, "features": F_},
+        "cold_ms_per_step": cold_ms,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None},
+                     "traffic": measured_traffic("c1", dominant)[0],
+                     "traffic_source": measured_traffic("c1", dominant)[1],
+                     "algorithmic_bytes": bytes_per[dominant]},
         "kernels": {k: {"launches": n, "avg_ms": ms / n} for k, (n, ms) in timer.totals.items()},
     }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_sum(row_ptr, col, x, w)
+    return result
 
 
 def run_c3c4(args):
@@ -405,6 +547,16 @@ def run_c3c4(args):
                 out.backward(dout, retain_graph=True)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
+
+    def cold():
+        if args.config == "c3":
+            with torch.no_grad():
+                fwd()
+        else:
+            q.grad = k.grad = v.grad = bias.grad = None
+            out.backward(dout, retain_graph=True)
+
+    cold_ms = cold_step_ms(cold)
     bytes_per = dot_kernel_bytes(N, E, H, D)
     names = ["dot_fwd_kernel"] if args.config == "c3" else [
         "dot_delta_kernel", "dot_bwd_dst_kernel", "dot_bwd_src_kernel"]
@@ -414,7 +566,7 @@ def run_c3c4(args):
     achieved = bytes_per[dominant] / (total_ms / n_launch * 1e-3) / 1e9
     ms = elapsed * 1e3 / args.steps
     what = "forward" if args.config == "c3" else "fused backward"
-    return {
+    result = {
         "metric": f"dot-product edge attention {what} edges/s, R-MAT scale 21, bf16, 1xMI355X",
         "value": E * args.steps / elapsed, "unit": "edges/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
@@ -423,6 +575,7 @@ def run_c3c4(args):
         "config": {"workload": f"{args.config}-dot-attention-{'fwd' if args.config == 'c3' else 'bwd'}",
                    "nodes": N, "edges": E, "heads": H, "head_dim": D, **stats},
         "hbm_frac_step": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "cold_ms_per_step": cold_ms,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic(args.config, dominant)[0],
@@ -433,6 +586,15 @@ def run_c3c4(args):
                     for kk, (n, t) in sorted(timer.totals.items())},
         "setup_ms": setup,
     }
+    if not args.no_cpu:
+        fwd_rate, bwd_rate, threads, sample = cpu_baseline_dot(
+            row_ptr, col, q, k, v, bias, 1.0 / 8.0, dout)
+        result["cpu_baseline"] = {
+            "value": fwd_rate if args.config == "c3" else bwd_rate, "unit": "edges/s",
+            "cores": threads, "kind": "port",
+            "sample": sample + (", forward" if args.config == "c3" else
+                                ", backward = (fwd+bwd) - fwd")}
+    return result
 
 
 def setup_times(graph, N, reps=3):
@@ -518,6 +680,7 @@ def run_c5(args):
             step()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
+    cold_ms = cold_step_ms(step)
     pairs = int((lengths * (lengths + 1) // 2).sum())
     fwd_flops = 4.0 * H * D * pairs
     step_flops = 3.5 * fwd_flops              # FA2 convention: bwd = 2.5 x fwd
@@ -529,7 +692,7 @@ def run_c5(args):
     dominant = max((kk for kk in per if kk in kflops), key=lambda kk: per[kk][1])
     n_launch, total_ms = per[dominant]
     achieved = kflops[dominant] / (total_ms / n_launch * 1e-3) / 1e12
-    return {
+    result = {
         "metric": "varlen causal attention fwd+bwd TFLOP/s, 32 seqs U[512,4096], H=16 D=128, "
                   "bf16, 1xMI355X",
         "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -541,6 +704,7 @@ def run_c5(args):
                    "flop_convention": "fwd 4*H*D*pairs, bwd 2.5x fwd (useful FLOPs; the dQ "
                                       "pass recomputes S and dP, not counted)"},
         "mfma_utilization": tflops / BF16_PEAK_TFLOPS,
+        "cold_ms_per_step": cold_ms,
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved,
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None},
@@ -548,6 +712,9 @@ def run_c5(args):
                          "tflops": (kflops[kk] / (t / n * 1e-3) / 1e12) if kk in kflops else None}
                     for kk, (n, t) in sorted(per.items())},
     }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_varlen(lengths, q, k, v, dout, D ** -0.5)
+    return result
 
 
 def run_dense(args):
@@ -683,11 +850,15 @@ def run_nn(args):
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
     ms = elapsed * 1e3 / args.steps
-    # Algorithmic bytes per pass (no-reuse model, 4 B indices): scores read
-    # col, dst, disp (12 B) and x twice (2 x 32 B) per edge and write 4 B.
+    # Algorithmic bytes per pass (no-reuse model, 4 B indices).  Per edge the
+    # score pass reads col, dst, the 19 input floats (displacement 3, x_src 8,
+    # x_dst 8) and writes the score; the backward reads the same plus dscore
+    # and writes the 19 input-gradient floats (the weight gradients are summed
+    # on chip).
+    inputs = 4 * (3 + 8 + 8)
     bytes_per = {
-        "edge_mlp_fwd_kernel": E * (4 + 4 + 12 + 64 + 4),
-        "edge_mlp_bwd_kernel": E * (4 + 4 + 12 + 64 + 4 + 2 * 2 * 16 * 4 + 12 + 2 * 32),
+        "edge_mlp_fwd_kernel": E * (4 + 4 + inputs + 4),
+        "edge_mlp_bwd_kernel": E * (4 + 4 + inputs + 4 + inputs),
         "csr_sum_fwd": E * (4 + 4 + 32) + N * (4 + 32),
     }
     per = timer.totals
@@ -706,13 +877,21 @@ def run_nn(args):
                    "value_width": 8, "reference_ms_own_gpu": 10.97},
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "algorithmic_bytes": bytes_per[dominant]},
+                     "traffic": measured_traffic("nn", dominant)[0],
+                     "traffic_source": measured_traffic("nn", dominant)[1],
+                     "algorithmic_bytes": bytes_per[dominant],
+                     "note": "the edge MLP kernels are latency-bound (fp32 FMAs on LDS-staged "
+                             "weights at 2 waves per SIMD), far from the HBM roof"},
         "kernels": {k: {"launches": n, "avg_ms": t / n} for k, (n, t) in sorted(per.items())},
     }
 
 
+ARGS = None
+
+
 def main():
-    args = parse()
+    global ARGS
+    args = ARGS = parse()
     if args.calibrate_copy:
         calibrate_copy()
         return

@@ -428,29 +428,22 @@ int tgx_segment_softmax_bwd(const void* row_ptr_dev, int idx_bits, int64_t n_row
                             const float* alpha_dev, const float* dalpha_dev,
                             float* dscore_dev, void* stream);
 
-/* Per-edge backward of the score network given dscore: writes, per layer l,
- * its input acts_dev[l] and the gradient of its pre-activation output
- * dz_dev[l] (each n_layers planes of [n_edges, width] fp32; the weight
- * gradients are dz[l]^T acts[l] and the bias gradients the column sums of
- * dz[l]), and the gradient of every input segment dseg[s]
+/* Workspace bytes needed by tgx_edge_mlp_backward for n_edges edges. */
+int tgx_edge_mlp_backward_workspace(int64_t n_edges, const tgx_edge_mlp* mlp, size_t* bytes);
+
+/* Backward of the score network given dscore (the reference differentiates
+ * the same chain with Torch autograd, interop/torch/message_passing.py:
+ * 2372-2577): writes the gradient of every input segment per edge, dseg[s]
  * ([n_edges, seg_width[s]] fp32 device buffers; dseg is a host array), which
  * the caller reduces per source row over the transposed CSR and per
- * destination row over the CSR. */
+ * destination row over the CSR, and the weight and bias gradients summed
+ * over all edges into dweights_dev, laid out as weights_dev (n_layers blocks
+ * of [width*width | width], padding entries 0).  The sums are formed on the
+ * device from per-block partials added in a fixed order: deterministic. */
 int tgx_edge_mlp_backward(const void* col_dev, const int32_t* dst_index_dev, int idx_bits,
                           int64_t n_edges, const tgx_edge_mlp* mlp, const float* dscore_dev,
-                          float* acts_dev, float* dz_dev, float* const* dseg,
-                          void* stream);
-
-/* Workspace bytes needed by tgx_edge_outer_sum. */
-int tgx_edge_outer_sum_workspace(int64_t n_edges, int width, size_t* bytes);
-
-/* Weight and bias gradients of one score-network layer from the planes of
- * tgx_edge_mlp_backward: dw[o*width + i] = sum_e g[e][o] a[e][i] and
- * db[o] = sum_e g[e][o] (db may be NULL); g, a [n_edges, width] fp32.
- * Two passes, partial sums added in a fixed order: deterministic. */
-int tgx_edge_outer_sum(const float* g_dev, const float* a_dev, int64_t n_edges, int width,
-                       float* dw_dev, float* db_dev, void* workspace_dev,
-                       size_t workspace_bytes, void* stream);
+                          float* dweights_dev, float* const* dseg, void* workspace_dev,
+                          size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Per-kernel timing (no reference counterpart; used by the benchmark)       */

@@ -11,4 +11,5 @@ imports, links or runs anything in this directory.
   eager_torch.py  the reference's eager Torch CPU path (timed CPU baseline)
   cpu_native.c    the reference's native CPU forward loop for the sum reducer
                   (timed CPU baseline), built by oracle/Makefile
+  native.py       ctypes binding of cpu_native.c
 """

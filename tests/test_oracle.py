@@ -419,3 +419,64 @@ def test_nn_attention_matches_torch_autograd_float64():
                         dlayers[2][1]]
     for a, b in zip(got, expect):
         np.testing.assert_allclose(a.numpy(), b, rtol=1e-10, atol=1e-12)
+
+
+# ---- timed CPU baselines (bench.py's cpu_baseline legs) ---------------------
+
+def test_native_sum_loop_matches_oracle():
+    """oracle/cpu_native.c: the README known answer exactly, the fp64 oracle
+    within fp32 rounding, and the same bits for any thread count (chunking
+    splits output elements, it never reorders a row's sum)."""
+    from oracle import native
+
+    g = GOLD["readme_weighted_sum"]
+    x = np.asarray(g["x"], dtype=np.float32).reshape(-1, 1)
+    out = native.csr_sum_fwd(g["row_ptr"], g["col_idx"], x, g["weight"], threads=2)
+    assert out.reshape(-1).tolist() == g["out"]
+    rng = np.random.default_rng(11)
+    rp, col = random_csr(rng, 300, 120, 20)
+    x = rng.standard_normal((120, 7)).astype(np.float32)
+    w = rng.random(col.size).astype(np.float32)
+    want = ref.sum_fwd(rp, col, x.astype(np.float64), w.astype(np.float64))
+    one = native.csr_sum_fwd(rp, col, x, w, threads=1)
+    np.testing.assert_allclose(one, want, rtol=1e-5, atol=1e-5)
+    for t in (3, 8):
+        assert np.array_equal(native.csr_sum_fwd(rp, col, x, w, threads=t), one)
+
+
+def test_eager_torch_cpu_path_matches_oracle():
+    """oracle/eager_torch.py (the reference's eager Torch CPU path) agrees
+    with the pinned fp64 oracle for the sum, GAT and dot-product steps."""
+    from oracle import eager_torch
+
+    rng = np.random.default_rng(12)
+    rp, col = random_csr(rng, 40, 40, 9)
+    rpt, colt = torch.tensor(rp), torch.tensor(col)
+    H, D = 2, 4
+    x = rng.standard_normal((40, 5))
+    w = rng.random(col.size)
+    dout = rng.standard_normal((40, 5))
+    out, dx, dw = eager_torch.sum_step(rpt, colt, torch.tensor(x), torch.tensor(w),
+                                       torch.tensor(dout))
+    e_dx, e_dw = ref.sum_bwd(rp, col, x, w, dout)
+    np.testing.assert_allclose(out.detach().numpy(), ref.sum_fwd(rp, col, x, w), rtol=1e-12,
+                               atol=1e-12)
+    np.testing.assert_allclose(dx.numpy(), e_dx, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dw.numpy(), e_dw, rtol=1e-12, atol=1e-12)
+
+    h = rng.standard_normal((40, H, D))
+    a_s, a_d = rng.standard_normal((H, D)), rng.standard_normal((H, D))
+    dout = rng.standard_normal((40, H, D))
+    out, dh, das, dad = eager_torch.gat_step(rpt, colt, torch.tensor(h), torch.tensor(a_s),
+                                             torch.tensor(a_d), 0.2, torch.tensor(dout))
+    e_out, _ = ref.gat_fwd(rp, col, h, a_s, a_d, 0.2)
+    e_grads = ref.gat_bwd(rp, col, h, a_s, a_d, 0.2, dout)
+    np.testing.assert_allclose(out.detach().numpy(), e_out, rtol=1e-10, atol=1e-12)
+    for got, want in zip((dh, das, dad), e_grads):
+        np.testing.assert_allclose(got.numpy(), want, rtol=1e-10, atol=1e-12)
+
+    q, k, v = (rng.standard_normal((40, H, D)) for _ in range(3))
+    bias = rng.standard_normal((col.size, H))
+    out = eager_torch.dot_step(rpt, colt, *(torch.tensor(a) for a in (q, k, v, bias)), 0.5)
+    e_out, _ = ref.dot_fwd(rp, col, q, k, v, 0.5, bias)
+    np.testing.assert_allclose(out.detach().numpy(), e_out, rtol=1e-10, atol=1e-12)

@@ -12,8 +12,9 @@
 // MI355X design: the score network is evaluated edge-parallel, one edge per
 // lane, so every lane does useful work whatever the row degrees; its inputs
 // are gathered straight from the field tables (no [E, K] tensor) and its
-// weights are uniform across the wave, so they are read once per wave
-// through scalar loads and used as SGPR operands of v_fma_f32.  Every layer
+// weights are uniform across the wave: staged once per workgroup in LDS and
+// read row by row (a broadcast), the next row in flight while the current
+// one is applied.  Every layer
 // is zero-padded to a common width W (16, 32 or 64) on the host, which keeps
 // every register index compile-time.  The softmax and the value gather are
 // separate row passes (segment softmax here, the weighted CSR sum of
@@ -22,154 +23,30 @@
 //
 // Backward: segment softmax backward per row (ds = a (da - <a, da>)), then
 // the per-edge MLP backward replays the chain, back-propagates ds, writes the
-// per-layer inputs and pre-activation gradients (the weight gradients are
-// their products over the edges, plain GEMMs) and the per-edge gradients of
-// every input segment (reduced per source row over the transposed CSR and
-// per destination row over the CSR by the caller).
+// per-edge gradients of every input segment (reduced per source row over the
+// transposed CSR and per destination row over the CSR by the caller) and
+// sums the weight and bias gradients (sum over edges of dz_l (x) a_l) in the
+// same pass on fp32 MFMA, from rows each wave stages in LDS; per-block
+// partial sums are added in a fixed order, so every gradient is
+// deterministic and nothing per layer and edge goes to HBM.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
 
-#include "tgx_device.h"
-#include "tgx_host.h"
+#include "tgx_nn_common.h"
 #include "tgx_profile.h"
 
 namespace tgx {
 namespace {
 
-constexpr int kMaxLayers = 3;
-constexpr int kMaxSegments = 4;
-
-struct MlpView {
-  int n_layers;
-  int in_width;
-  int act[kMaxLayers];
-  float param[kMaxLayers];
-  const float* w;   // n_layers x [W*W | W]
-  int n_seg;
-  int role[kMaxSegments];
-  int width[kMaxSegments];
-  int64_t stride[kMaxSegments];
-  const float* ptr[kMaxSegments];
-  int off[kMaxSegments];              // first input column of each segment
-  float* grad[kMaxSegments];          // backward: per-segment input gradients
-};
-
-__device__ __forceinline__ float sigmoid(float z) { return 1.f / (1.f + __expf(-z)); }
-
-// Component-wise activation (code uniform across the wave).
-__device__ __forceinline__ float activate(float z, int act, float p) {
-  switch (act) {
-    case TGX_ACT_RELU: return fmaxf(z, 0.f);
-    case TGX_ACT_LEAKY_RELU: return z > 0.f ? z : p * z;
-    case TGX_ACT_TANH: return tanhf(z);
-    case TGX_ACT_SIGMOID: return sigmoid(z);
-    case TGX_ACT_SILU: return z * sigmoid(z);
-    case TGX_ACT_GELU: return 0.5f * z * (1.f + erff(z * 0.70710678118654752f));
-    case TGX_ACT_ELU: return z > 0.f ? z : p * (__expf(z) - 1.f);
-    default: return z;
-  }
-}
-
-// d activate / dz at z.
-__device__ __forceinline__ float activate_grad(float z, int act, float p) {
-  switch (act) {
-    case TGX_ACT_RELU: return z > 0.f ? 1.f : 0.f;
-    case TGX_ACT_LEAKY_RELU: return z > 0.f ? 1.f : p;
-    case TGX_ACT_TANH: {
-      const float t = tanhf(z);
-      return 1.f - t * t;
-    }
-    case TGX_ACT_SIGMOID: {
-      const float s = sigmoid(z);
-      return s * (1.f - s);
-    }
-    case TGX_ACT_SILU: {
-      const float s = sigmoid(z);
-      return s * (1.f + z * (1.f - s));
-    }
-    case TGX_ACT_GELU:
-      // Phi(z) + z phi(z)
-      return 0.5f * (1.f + erff(z * 0.70710678118654752f)) +
-             z * 0.39894228040143268f * __expf(-0.5f * z * z);
-    case TGX_ACT_ELU: return z > 0.f ? 1.f : p * __expf(z);
-    default: return 1.f;
-  }
-}
-
-template <typename I>
-__device__ __forceinline__ int64_t seg_row(int role, int64_t e, const I* col,
-                                           const int32_t* dst) {
-  return role == TGX_ROLE_SRC ? static_cast<int64_t>(col[e])
-                              : (role == TGX_ROLE_DST ? static_cast<int64_t>(dst[e]) : e);
-}
-
-// x[k] for k < in_width from the concatenated segments (zero beyond).  The
-// segment loop is compile-time, so each segment's row pointer is a plain
-// per-lane value and every x index is a constant (no indexed register
-// arrays); which columns a segment fills is a uniform range test.
-template <typename I, int W>
-__device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const I* col,
-                                              const int32_t* dst, float (&x)[W]) {
-#pragma unroll
-  for (int k = 0; k < W; ++k) x[k] = 0.f;
-#pragma unroll
-  for (int s = 0; s < kMaxSegments; ++s) {
-    if (s >= m.n_seg) break;
-    const int off = m.off[s], wd = m.width[s];
-    const float* p = m.ptr[s] + seg_row(m.role[s], e, col, dst) * m.stride[s] - off;
-#pragma unroll
-    for (int k = 0; k < W; ++k)
-      if (k >= off && k < off + wd) x[k] = p[k];
-  }
-}
-
-// Keeps v's computation at this point of the program.  Without it the
-// optimizer sinks each dot product to its first use, behind the uniform
-// branches of the activation that follows, i.e. after every weight load of
-// the layer, and all W*W weights of the layer end up live at once.
-__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
-
-// f(integral_constant<0>) ... f(integral_constant<N-1>): a loop whose index
-// is a compile-time constant in the body (register arrays indexed by it stay
-// in registers whatever the body's size).
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (N > 0) {
-    static_for<N - 1>(f);
-    f(std::integral_constant<int, N - 1>{});
-  }
-}
-
-// z = W_l a + b_l over the padded width, one weight row at a time (wl is
-// uniform across the wave).
-template <int W>
-__device__ __forceinline__ void linear(const float* wl, const float (&a)[W], float (&z)[W]) {
-#pragma unroll
-  for (int o = 0; o < W; ++o) {
-    float acc = wl[W * W + o];
-#pragma unroll
-    for (int i = 0; i < W; ++i) acc = fmaf(wl[o * W + i], a[i], acc);
-    pin(acc);
-    z[o] = acc;
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// The weights of all layers, staged once per workgroup in LDS (every lane
-// then reads the same address: a broadcast).
-template <int W, int L>
-__device__ __forceinline__ void stage_weights(const float* __restrict__ w, float* wsh) {
-  for (int i = threadIdx.x; i < L * (W * W + W); i += 256) wsh[i] = w[i];
-  __syncthreads();
-}
+using namespace mlp;
 
 template <typename I, int W, int L>
 __global__ __launch_bounds__(256) void edge_mlp_fwd_kernel(const I* __restrict__ col,
                                                            const int32_t* __restrict__ dst,
                                                            int64_t n_edges, MlpView m,
                                                            float* __restrict__ scores) {
-  __shared__ float wsh[L * (W * W + W)];
+  __shared__ __align__(16) float wsh[L * (W * W + W)];
   stage_weights<W, L>(m.w, wsh);
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (e >= n_edges) return;
@@ -177,7 +54,7 @@ __global__ __launch_bounds__(256) void edge_mlp_fwd_kernel(const I* __restrict__
   gather_inputs<I, W>(m, e, col, dst, a);
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
-    linear<W>(wsh + l * (W * W + W), a, z);
+    linear<W, false>(wsh + l * (W * W + W), a, z);
     const int act = m.act[l];
     const float p = m.param[l];
 #pragma unroll
@@ -190,81 +67,243 @@ __global__ __launch_bounds__(256) void edge_mlp_fwd_kernel(const I* __restrict__
   scores[e] = s;
 }
 
-// Per-edge backward of the score chain.  ds_e arrives from the softmax
-// backward.  Writes, for every layer l: its input acts[l][e][:] and the
-// gradient of its pre-activation output dz[l][e][:] (padded width W), and the
-// input gradient split per segment dseg[s][e][:width_s].
+// ---- weight gradients on fp32 MFMA ------------------------------------------
+//
+// dW_l = sum over edges of dz_l[e] (x) a_l[e] (pre-activation gradient times
+// layer input) is a [W x E] x [E x W] product.  Each wave stages the rows of
+// its edges in LDS (32 edges per round, row stride W + 4 floats) and feeds
+// them to fp32 MFMA, which takes exact fp32 products and fp32 sums like
+// v_fma_f32:
+//   W = 16: v_mfma_f32_16x16x4_f32, lane l gives G[4s + l/16][l%16] (A
+//           operand, G^T) and A[4s + l/16][l%16] (B operand);
+//           D[o][i]: i = l%16, o = 4(l/16) + q for accumulator q.
+//   W = 32, 64: v_mfma_f32_32x32x2_f32 per 32 x 32 tile, lane l gives row
+//           2s + l/32, column l%32 (+32 per tile); D[o][i]: i = l%32,
+//           o = 8(q/4) + 4(l/32) + q%4.
+// The bias gradient (the column sums of G) is summed from the same reads.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int W>
+constexpr int mlp_ld() { return W + 4; }
+
+template <int W>
+struct OuterAcc {
+  static constexpr int kTiles = W == 64 ? 4 : 1;
+  using Tile = typename std::conditional<W == 16, f32x4, f32x16>::type;
+  Tile c[kTiles];
+  float b[W == 64 ? 2 : 1];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) c[t] = Tile{};
+#pragma unroll
+    for (int t = 0; t < (W == 64 ? 2 : 1); ++t) b[t] = 0.f;
+  }
+};
+
+// acc += G^T A over the 32 staged rows of this wave.
+template <int W>
+__device__ __forceinline__ void outer_accumulate(const float* sg, const float* sa,
+                                                 OuterAcc<W>& acc) {
+  constexpr int LD = mlp_ld<W>();
+  const int l = lane_id();
+  if constexpr (W == 16) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int at = (4 * s + l / 16) * LD + l % 16;
+      const float g = sg[at], a = sa[at];
+      acc.b[0] += g;
+      acc.c[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(g, a, acc.c[0], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int at = (2 * s + l / 32) * LD + l % 32;
+      const float g0 = sg[at], a0 = sa[at];
+      acc.b[0] += g0;
+      acc.c[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(g0, a0, acc.c[0], 0, 0, 0);
+      if constexpr (W == 64) {
+        const float g1 = sg[at + 32], a1 = sa[at + 32];
+        acc.b[1] += g1;
+        acc.c[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(g0, a1, acc.c[1], 0, 0, 0);
+        acc.c[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(g1, a0, acc.c[2], 0, 0, 0);
+        acc.c[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(g1, a1, acc.c[3], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Orders this wave's LDS accesses around an exchange between its lanes: a
+// wave's LDS instructions execute in issue order, so only the compiler has
+// to be kept from moving accesses across (rocPRIM's wave_barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Stage this wave's (G, A) rows and add G^T A to acc: lanes 0..31 first,
+// then lanes 32..63, through the wave's own LDS region (no block barrier:
+// the waves of a block progress independently).
+template <int W>
+__device__ __forceinline__ void outer_layer(float* sg, float* sa, const float (&g)[W],
+                                            const float (&a)[W], OuterAcc<W>& acc) {
+  constexpr int LD = mlp_ld<W>();
+  const int l = lane_id();
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+    if ((l >> 5) == round) {
+      float* pg = sg + (l & 31) * LD;
+      float* pa = sa + (l & 31) * LD;
+#pragma unroll
+      for (int k = 0; k < W; k += 4) {
+        *reinterpret_cast<f32x4*>(pg + k) = f32x4{g[k], g[k + 1], g[k + 2], g[k + 3]};
+        *reinterpret_cast<f32x4*>(pa + k) = f32x4{a[k], a[k + 1], a[k + 2], a[k + 3]};
+      }
+    }
+    wave_lds_sync();
+    outer_accumulate<W>(sg, sa, acc);
+    wave_lds_sync();
+  }
+}
+
+// The wave's accumulated [W x W | W] block, written row-major into red.
+template <int W>
+__device__ __forceinline__ void outer_store(const OuterAcc<W>& acc, float* red) {
+  const int l = lane_id();
+  if constexpr (W == 16) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[(4 * (l / 16) + q) * W + l % 16] = acc.c[0][q];
+    float b = acc.b[0];
+    b += __shfl_xor(b, 16, 64);
+    b += __shfl_xor(b, 32, 64);
+    if (l < 16) red[W * W + l] = b;
+  } else {
+#pragma unroll
+    for (int t = 0; t < OuterAcc<W>::kTiles; ++t) {
+      const int ro = 32 * (t >> 1), ci = 32 * (t & 1);
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        red[(ro + 8 * (q / 4) + 4 * (l / 32) + q % 4) * W + ci + l % 32] = acc.c[t][q];
+    }
+#pragma unroll
+    for (int t = 0; t < (W == 64 ? 2 : 1); ++t) {
+      const float b = acc.b[t] + __shfl_xor(acc.b[t], 32, 64);
+      if (l < 32) red[W * W + 32 * t + l] = b;
+    }
+  }
+}
+
+// Per-edge backward of the score chain plus the weight-gradient sums.  ds_e
+// arrives from the softmax backward.  Each block walks a contiguous range of
+// edges in steps of 256 (one edge per lane), replays the chain, back-
+// propagates ds, writes the input gradient of every segment per edge
+// (dseg[s][e][:width_s]) and accumulates dW_l, db_l for every layer on MFMA;
+// the block's sums go to partial[block] (n_layers x [W*W | W]) in a fixed
+// order.
 template <typename I, int W, int L>
 __global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
-    const I* __restrict__ col, const int32_t* __restrict__ dst, int64_t n_edges, MlpView m,
-    const float* __restrict__ dscore, float* __restrict__ acts, float* __restrict__ dz_out) {
-  __shared__ float wsh[L * (W * W + W)];
+    const I* __restrict__ col, const int32_t* __restrict__ dst, int64_t n_edges, int64_t chunk,
+    MlpView m, const float* __restrict__ dscore, float* __restrict__ partial) {
+  constexpr int NW = W * W + W;
+  constexpr int LD = mlp_ld<W>();
+  constexpr int SW = 2 * 32 * LD;  // one wave's staging: G rows | A rows
+  static_assert(SW >= NW, "a wave's staging holds one layer's block");
+  __shared__ __align__(16) float wsh[L * NW];
+  __shared__ __align__(16) float stage[4 * SW];
   stage_weights<W, L>(m.w, wsh);
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (e >= n_edges) return;
-  const int64_t plane = n_edges * W;
-  float a[W];                       // input of the current layer
-  float z[L > 1 ? L - 1 : 1][W];    // pre-activations of the hidden layers
-  gather_inputs<I, W>(m, e, col, dst, a);
-  static_for<L>([&](auto lc) {
-    constexpr int l = decltype(lc)::value;
-    float* out = acts + l * plane + e * W;
+  const int wave = threadIdx.x >> 6;
+  float* sg = stage + wave * SW;
+  float* sa = sg + 32 * LD;
+  OuterAcc<W> acc[L];
 #pragma unroll
-    for (int i = 0; i < W; i += 4)
-      *reinterpret_cast<f32x4*>(out + i) = f32x4{a[i], a[i + 1], a[i + 2], a[i + 3]};
-    if constexpr (l + 1 < L) {
-      linear<W>(wsh + l * (W * W + W), a, z[l]);
+  for (int l = 0; l < L; ++l) acc[l].zero();
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t e1 = e0 + chunk < n_edges ? e0 + chunk : n_edges;
+  for (int64_t base = e0; base < e1; base += 256) {
+    const int64_t e = base + threadIdx.x;
+    const bool valid = e < e1;
+    float x[W];                        // gathered input (layer 0's input)
+    float z[L > 1 ? L - 1 : 1][W];     // pre-activations of the hidden layers
+    if (valid) {
+      gather_inputs<I, W>(m, e, col, dst, x);
+    } else {
 #pragma unroll
-      for (int o = 0; o < W; ++o) a[o] = activate(z[l][o], m.act[l], m.param[l]);
+      for (int k = 0; k < W; ++k) x[k] = 0.f;
     }
-  });
-  // Last layer: one output, gradient ds.
-  const float ds = dscore[e];
-  float g[W];
-  {
-    const float* wl = wsh + (L - 1) * (W * W + W);
-    float* out = dz_out + (L - 1) * plane + e * W;
+    {
+      float a[W];
 #pragma unroll
-    for (int i = 0; i < W; i += 4)
-      *reinterpret_cast<f32x4*>(out + i) = f32x4{i == 0 ? ds : 0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < W; ++k) a[k] = x[k];
+      static_for<L - 1>([&](auto lc) {
+        constexpr int l = decltype(lc)::value;
+        linear<W>(wsh + l * NW, a, z[l]);
 #pragma unroll
-    for (int i = 0; i < W; ++i) g[i] = ds * wl[i];   // d a[L-1]
-  }
-  static_for<L - 1>([&](auto kc) {
-    constexpr int l = L - 2 - decltype(kc)::value;
-    float dzl[W];
-#pragma unroll
-    for (int o = 0; o < W; ++o) {
-      dzl[o] = g[o] * activate_grad(z[l][o], m.act[l], m.param[l]);
-      pin(dzl[o]);
+        for (int o = 0; o < W; ++o) a[o] = activate(z[l][o], m.act[l], m.param[l]);
+      });
     }
-    float* out = dz_out + l * plane + e * W;
+    // Input of layer l: x, or the activation of z[l-1].
+    auto layer_input = [&](auto lc, float (&a)[W]) {
+      constexpr int l = decltype(lc)::value;
+      if constexpr (l == 0) {
 #pragma unroll
-    for (int i = 0; i < W; i += 4)
-      *reinterpret_cast<f32x4*>(out + i) = f32x4{dzl[i], dzl[i + 1], dzl[i + 2], dzl[i + 3]};
-    // d a[l] = W_l^T dz, accumulated row by row so W_l is read in order.
-    const float* wl = wsh + l * (W * W + W);
+        for (int k = 0; k < W; ++k) a[k] = x[k];
+      } else {
 #pragma unroll
-    for (int i = 0; i < W; ++i) g[i] = 0.f;
-    static_for<W>([&](auto oc) {
-      constexpr int o = decltype(oc)::value;
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        g[i] = fmaf(wl[o * W + i], dzl[o], g[i]);
-        pin(g[i]);
+        for (int k = 0; k < W; ++k) a[k] = activate(z[l - 1][k], m.act[l - 1], m.param[l - 1]);
       }
-      __builtin_amdgcn_sched_barrier(0);
+    };
+    // Last layer: one output, gradient ds (0 on lanes past the range).
+    const float ds = valid ? dscore[e] : 0.f;
+    float g[W];
+    {
+      const float* wl = wsh + (L - 1) * NW;
+      float dzl[W], a[W];
+#pragma unroll
+      for (int i = 0; i < W; ++i) dzl[i] = i == 0 ? ds : 0.f;
+      layer_input(std::integral_constant<int, L - 1>{}, a);
+      outer_layer<W>(sg, sa, dzl, a, acc[L - 1]);
+#pragma unroll
+      for (int i = 0; i < W; ++i) g[i] = ds * wl[i];   // d a[L-1]
+    }
+    static_for<L - 1>([&](auto kc) {
+      constexpr int l = L - 2 - decltype(kc)::value;
+      float dzl[W];
+#pragma unroll
+      for (int o = 0; o < W; ++o) {
+        dzl[o] = g[o] * activate_grad(z[l][o], m.act[l], m.param[l]);
+        pin(dzl[o]);
+      }
+      {
+        float a[W];
+        layer_input(std::integral_constant<int, l>{}, a);
+        outer_layer<W>(sg, sa, dzl, a, acc[l]);
+      }
+      // d a[l] = W_l^T dz.
+      linear_t<W>(wsh + l * NW, dzl, g);
     });
-  });
-  // g = d x: split per segment.
+    // g = d x: split per segment.
+    if (valid) {
 #pragma unroll
-  for (int s = 0; s < kMaxSegments; ++s) {
-    if (s >= m.n_seg) break;
-    const int off = m.off[s], wd = m.width[s];
-    float* q = m.grad[s] + e * wd - off;
+      for (int s = 0; s < kMaxSegments; ++s) {
+        if (s >= m.n_seg) break;
+        const int off = m.off[s], wd = m.width[s];
+        float* q = m.grad[s] + e * wd - off;
 #pragma unroll
-    for (int k = 0; k < W; ++k)
-      if (k >= off && k < off + wd) q[k] = g[k];
+        for (int k = 0; k < W; ++k)
+          if (k >= off && k < off + wd) q[k] = g[k];
+      }
+    }
+  }
+  // Block sums, layer by layer: each wave's block into its staging region,
+  // then the four added in wave order.
+  float* out = partial + static_cast<int64_t>(blockIdx.x) * L * NW;
+#pragma unroll
+  for (int l = 0; l < L; ++l) {
+    outer_store<W>(acc[l], sg);
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < NW; idx += 256)
+      out[l * NW + idx] = (stage[idx] + stage[SW + idx]) + (stage[2 * SW + idx] + stage[3 * SW + idx]);
+    __syncthreads();
   }
 }
 
@@ -304,104 +343,48 @@ __global__ __launch_bounds__(256) void segment_softmax_bwd_kernel(
   for (int64_t e = e0 + lane; e < e1; e += kWave) dscore[e] = alpha[e] * (dalpha[e] - d);
 }
 
-// v[0..B) = p[0..B) as 8- or 16-byte vector loads (p aligned to 4 B floats).
-template <int B>
-__device__ __forceinline__ void load_vec(const float* __restrict__ p, float (&v)[B]) {
-  if constexpr (B % 4 == 0) {
-#pragma unroll
-    for (int j = 0; j < B; j += 4) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(p + j);
-      v[j] = t[0], v[j + 1] = t[1], v[j + 2] = t[2], v[j + 3] = t[3];
-    }
-  } else {
-    static_assert(B == 2, "2, 4 or 8 floats");
-    const float2 t = *reinterpret_cast<const float2*>(p);
-    v[0] = t.x, v[1] = t.y;
+// out[c] = sum over rows r of p[r][c] in a fixed order, two levels: block
+// (column block, slice) sums a contiguous range of rows with coalesced
+// reads, then one thread per column adds the kColSlices slice sums.
+constexpr int kColSlices = 16;
+
+__global__ __launch_bounds__(256) void colsum_slice_kernel(const float* __restrict__ p,
+                                                           int64_t rows, int n,
+                                                           float* __restrict__ slices) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= n) return;
+  const int64_t per = (rows + kColSlices - 1) / kColSlices;
+  const int64_t r0 = blockIdx.y * per;
+  const int64_t r1 = r0 + per < rows ? r0 + per : rows;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int64_t r = r0;
+  for (; r + 4 <= r1; r += 4) {
+    s0 += p[(r + 0) * n + c];
+    s1 += p[(r + 1) * n + c];
+    s2 += p[(r + 2) * n + c];
+    s3 += p[(r + 3) * n + c];
   }
+  for (; r < r1; ++r) s0 += p[r * n + c];
+  slices[static_cast<int64_t>(blockIdx.y) * n + c] = (s0 + s1) + (s2 + s3);
 }
 
-// Weight gradients of one layer: S[o][i] = sum_e G[e][o] A[e][i] and
-// b[o] = sum_e G[e][o] over [n_edges, W] planes.  Each workgroup sums a chunk
-// of edges (its four waves take every fourth edge), lane (ob, ib) of a wave
-// owning the (W/8 x W/8) block of S at (ob, ib); the waves are added in LDS
-// and every workgroup writes its partial.  A second kernel adds the partials
-// in workgroup order: deterministic.
-template <int W>
-__global__ __launch_bounds__(256) void outer_sum_kernel(const float* __restrict__ g,
-                                                        const float* __restrict__ a,
-                                                        int64_t n_edges, int64_t chunk,
-                                                        float* __restrict__ partial) {
-  constexpr int B = W / 8;
-  constexpr int N = W * W + W;
-  __shared__ float red[4][N];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int ob = lane / 8, ib = lane % 8;
-  float acc[B][B], bacc[B];
-#pragma unroll
-  for (int p = 0; p < B; ++p) {
-    bacc[p] = 0.f;
-#pragma unroll
-    for (int q = 0; q < B; ++q) acc[p][q] = 0.f;
-  }
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk;
-  const int64_t e1 = e0 + chunk < n_edges ? e0 + chunk : n_edges;
-  auto accumulate = [&](const float (&gv)[B], const float (&av)[B]) {
-#pragma unroll
-    for (int p = 0; p < B; ++p) {
-      bacc[p] += gv[p];
-#pragma unroll
-      for (int q = 0; q < B; ++q) acc[p][q] = fmaf(gv[p], av[q], acc[p][q]);
-    }
-  };
-  // Whole steps of U edges per wave (four row loads per lane in flight, as
-  // vector loads), then the remainder one edge at a time.
-  constexpr int U = 4;
-  const int64_t full = e0 + (e1 - e0) / (4 * U) * (4 * U);
-  for (int64_t base = e0 + wave; base < full; base += 4 * U) {
-    float gv[U][B], av[U][B];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      load_vec<B>(g + (base + 4 * u) * W + ob * B, gv[u]);
-      load_vec<B>(a + (base + 4 * u) * W + ib * B, av[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) accumulate(gv[u], av[u]);
-  }
-  for (int64_t e = full + wave; e < e1; e += 4) {
-    float gv[B], av[B];
-    load_vec<B>(g + e * W + ob * B, gv);
-    load_vec<B>(a + e * W + ib * B, av);
-    accumulate(gv, av);
-  }
-#pragma unroll
-  for (int p = 0; p < B; ++p) {
-#pragma unroll
-    for (int q = 0; q < B; ++q) red[wave][(ob * B + p) * W + ib * B + q] = acc[p][q];
-    if (ib == 0) red[wave][W * W + ob * B + p] = bacc[p];
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < N; idx += 256)
-    partial[static_cast<int64_t>(blockIdx.x) * N + idx] =
-        (red[0][idx] + red[1][idx]) + (red[2][idx] + red[3][idx]);
-}
-
-__global__ __launch_bounds__(256) void outer_sum_final_kernel(
-    const float* __restrict__ partial, int n_blocks, int n, int w, float* __restrict__ dw,
-    float* __restrict__ db) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= n) return;
+// n_slices = 0 writes zeros (no reads).
+__global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ slices,
+                                                           int n_slices, int n,
+                                                           float* __restrict__ out) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= n) return;
   float s = 0.f;
-  for (int b = 0; b < n_blocks; ++b) s += partial[static_cast<int64_t>(b) * n + idx];
-  if (idx < w * w)
-    dw[idx] = s;
-  else if (db)
-    db[idx - w * w] = s;
+  for (int k = 0; k < n_slices; ++k) s += slices[static_cast<int64_t>(k) * n + c];
+  out[c] = s;
 }
 
-int outer_blocks(int64_t n_edges, int64_t* chunk) {
-  // About four workgroups per CU; chunks of whole waves of edges.
-  int64_t c = ceil_div(n_edges, 1024);
-  c = c < 64 ? 64 : align_up(static_cast<size_t>(c), 64);
+// Persistent backward grid: as many blocks as the device holds at once
+// (`resident`, from the occupancy query of the kernel), chunks of whole
+// 256-edge steps.
+int mlp_bwd_blocks(int64_t n_edges, int64_t resident, int64_t* chunk) {
+  int64_t c = ceil_div(n_edges, resident > 0 ? resident : 1);
+  c = align_up(static_cast<size_t>(c < 256 ? 256 : c), 256);
   *chunk = c;
   return static_cast<int>(ceil_div(n_edges, c));
 }
@@ -461,13 +444,54 @@ void launch_fwd(int L, const I* col, const int32_t* dst, int64_t E, const MlpVie
   if (L == 3) edge_mlp_fwd_kernel<I, W, 3><<<blocks, 256, 0, s>>>(col, dst, E, v, scores);
 }
 
+// Blocks of edge_mlp_bwd_kernel<int64_t, W, L> resident on the current
+// device at once: per CU, the smaller of what the 160 KB of LDS and the 512
+// registers per SIMD lane allow (each 256-thread block puts one wave on each
+// of the CU's four SIMDs), from the kernel's attributes; the larger of that
+// and the runtime's occupancy query.
+template <int W, int L>
+int64_t bwd_resident_blocks() {
+  static int64_t cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    const void* fn = reinterpret_cast<const void*>(edge_mlp_bwd_kernel<int64_t, W, L>);
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess)
+      per_cu = 0;
+    hipFuncAttributes attr{};
+    if (hipFuncGetAttributes(&attr, fn) == hipSuccess && attr.numRegs > 0) {
+      const int regs = (attr.numRegs + 7) / 8 * 8;
+      const int by_regs = 512 / regs;
+      const int by_lds = attr.sharedSizeBytes > 0
+                             ? static_cast<int>((160 * 1024) / attr.sharedSizeBytes)
+                             : by_regs;
+      const int mine = by_regs < by_lds ? by_regs : by_lds;
+      if (mine > per_cu) per_cu = mine;
+    }
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      cus = 256;
+    cached[dev] = static_cast<int64_t>(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  }
+  return cached[dev];
+}
+
+int64_t resident_blocks(int W, int L) {
+  if (W == 16) return L == 1 ? bwd_resident_blocks<16, 1>() : L == 2 ? bwd_resident_blocks<16, 2>()
+                                                                       : bwd_resident_blocks<16, 3>();
+  return L == 1 ? bwd_resident_blocks<32, 1>() : L == 2 ? bwd_resident_blocks<32, 2>()
+                                                          : bwd_resident_blocks<32, 3>();
+}
+
 template <typename I, int W>
-void launch_bwd(int L, const I* col, const int32_t* dst, int64_t E, const MlpView& v,
-                const float* ds, float* acts, float* dz, hipStream_t s) {
-  const int64_t blocks = ceil_div(E, 256);
-  if (L == 1) edge_mlp_bwd_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, v, ds, acts, dz);
-  if (L == 2) edge_mlp_bwd_kernel<I, W, 2><<<blocks, 256, 0, s>>>(col, dst, E, v, ds, acts, dz);
-  if (L == 3) edge_mlp_bwd_kernel<I, W, 3><<<blocks, 256, 0, s>>>(col, dst, E, v, ds, acts, dz);
+void launch_bwd(int L, const I* col, const int32_t* dst, int64_t E, int blocks, int64_t chunk,
+                const MlpView& v, const float* ds, float* partial, hipStream_t s) {
+  if (L == 1)
+    edge_mlp_bwd_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds, partial);
+  if (L == 2)
+    edge_mlp_bwd_kernel<I, W, 2><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds, partial);
+  if (L == 3)
+    edge_mlp_bwd_kernel<I, W, 3><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds, partial);
 }
 
 template <typename I>
@@ -479,12 +503,13 @@ void dispatch_fwd(int W, int L, const I* col, const int32_t* dst, int64_t E, con
 }
 
 template <typename I>
-void dispatch_bwd(int W, int L, const I* col, const int32_t* dst, int64_t E, const MlpView& v,
-                  const float* ds, float* acts, float* dz, hipStream_t s) {
-  if (W == 16) launch_bwd<I, 16>(L, col, dst, E, v, ds, acts, dz, s);
-  if (W == 32) launch_bwd<I, 32>(L, col, dst, E, v, ds, acts, dz, s);
-  if (W == 64) launch_bwd<I, 64>(L, col, dst, E, v, ds, acts, dz, s);
+void dispatch_bwd(int W, int L, const I* col, const int32_t* dst, int64_t E, int blocks,
+                  int64_t chunk, const MlpView& v, const float* ds, float* partial,
+                  hipStream_t s) {
+  if (W == 16) launch_bwd<I, 16>(L, col, dst, E, blocks, chunk, v, ds, partial, s);
+  if (W == 32) launch_bwd<I, 32>(L, col, dst, E, blocks, chunk, v, ds, partial, s);
 }
+
 
 }  // namespace
 }  // namespace tgx
@@ -513,30 +538,89 @@ extern "C" int tgx_edge_mlp_scores(const void* col, const int32_t* dst_index, in
   return TGX_OK;
 }
 
+extern "C" int tgx_edge_mlp_backward_workspace(int64_t n_edges, const tgx_edge_mlp* mlp,
+                                               size_t* bytes) {
+  TGX_REQUIRE(bytes, "null bytes");
+  TGX_REQUIRE(n_edges >= 0, "negative size");
+  MlpView v;
+  int st = check_mlp(mlp, &v);
+  if (st != TGX_OK) return st;
+  const int64_t n = static_cast<int64_t>(mlp->n_layers) * (mlp->width * mlp->width + mlp->width);
+  int64_t chunk = 0;
+  const int blocks = n_edges == 0 ? 0
+                     : mlp->width == 64
+                         ? outer_blocks(n_edges, &chunk)
+                         : mlp_bwd_blocks(n_edges, resident_blocks(mlp->width, mlp->n_layers),
+                                          &chunk);
+  size_t planes = 0;
+  if (mlp->width == 64)
+    planes = 2 * align_up(static_cast<size_t>(mlp->n_layers) * n_edges * 64 * sizeof(float));
+  *bytes = align_up(static_cast<size_t>(blocks) * n * sizeof(float)) +
+           align_up(static_cast<size_t>(kColSlices) * n * sizeof(float)) + planes;
+  return TGX_OK;
+}
+
 extern "C" int tgx_edge_mlp_backward(const void* col, const int32_t* dst_index, int idx_bits,
                                      int64_t n_edges, const tgx_edge_mlp* mlp,
-                                     const float* dscore, float* acts, float* dz,
-                                     float* const* dseg, void* stream) {
+                                     const float* dscore, float* dweights, float* const* dseg,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
   int st = check_mlp(mlp, &v);
   if (st != TGX_OK) return st;
-  if (n_edges == 0) return TGX_OK;
-  TGX_REQUIRE(col && dst_index && dscore && acts && dz && dseg, "null pointer");
-  for (int s = 0; s < mlp->n_segments; ++s) {
-    TGX_REQUIRE(dseg[s], "null gradient for segment %d", s);
-    v.grad[s] = dseg[s];
-  }
+  TGX_REQUIRE(dweights && dseg, "null pointer");
+  const int n = mlp->n_layers * (mlp->width * mlp->width + mlp->width);
   hipStream_t s = as_stream(stream);
-  TGX_PROFILE("edge_mlp_bwd_kernel", s);
-  if (idx_bits == 32)
-    dispatch_bwd(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col), dst_index,
-                 n_edges, v, dscore, acts, dz, s);
-  else
-    dispatch_bwd(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col), dst_index,
-                 n_edges, v, dscore, acts, dz, s);
-  TGX_LAUNCHED("edge_mlp_bwd_kernel");
+  if (n_edges == 0) {
+    // Zero sums, written by a kernel rather than a memset.
+    colsum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(nullptr, 0, n, dweights);
+    TGX_LAUNCHED("colsum_final_kernel");
+    return TGX_OK;
+  }
+  TGX_REQUIRE(col && dst_index && dscore && workspace, "null pointer");
+  for (int k = 0; k < mlp->n_segments; ++k) {
+    TGX_REQUIRE(dseg[k], "null gradient for segment %d", k);
+    v.grad[k] = dseg[k];
+  }
+  size_t need = 0;
+  TGX_REQUIRE(tgx_edge_mlp_backward_workspace(n_edges, mlp, &need) == TGX_OK &&
+                  workspace_bytes >= need,
+              "workspace too small");
+  int64_t chunk = 0;
+  const int blocks =
+      mlp->width == 64
+          ? outer_blocks(n_edges, &chunk)
+          : mlp_bwd_blocks(n_edges, resident_blocks(mlp->width, mlp->n_layers), &chunk);
+  const size_t part_bytes = align_up(static_cast<size_t>(blocks) * n * sizeof(float));
+  const size_t slice_bytes = align_up(static_cast<size_t>(kColSlices) * n * sizeof(float));
+  float* partial = static_cast<float*>(workspace);
+  float* slices = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
+  if (mlp->width == 64) {
+    const size_t plane = align_up(static_cast<size_t>(mlp->n_layers) * n_edges * 64 * sizeof(float));
+    float* acts = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes + slice_bytes);
+    float* dz = reinterpret_cast<float*>(reinterpret_cast<char*>(acts) + plane);
+    st = tgx::mlp::planes_backward(mlp->n_layers, idx_bits, col, dst_index, n_edges, v, dscore,
+                                   acts, dz, blocks, chunk, partial, s);
+    if (st != TGX_OK) return st;
+  } else {
+    TGX_PROFILE("edge_mlp_bwd_kernel", s);
+    if (idx_bits == 32)
+      dispatch_bwd(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col), dst_index,
+                   n_edges, blocks, chunk, v, dscore, partial, s);
+    else
+      dispatch_bwd(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col), dst_index,
+                   n_edges, blocks, chunk, v, dscore, partial, s);
+    TGX_LAUNCHED("edge_mlp_bwd_kernel");
+  }
+  {
+    TGX_PROFILE("colsum_kernels", s);
+    colsum_slice_kernel<<<dim3(ceil_div(n, 256), kColSlices), 256, 0, s>>>(partial, blocks,
+                                                                           n, slices);
+    TGX_LAUNCHED("colsum_slice_kernel");
+    colsum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(slices, kColSlices, n, dweights);
+    TGX_LAUNCHED("colsum_final_kernel");
+  }
   return TGX_OK;
 }
 
@@ -575,42 +659,5 @@ extern "C" int tgx_segment_softmax_bwd(const void* row_ptr, int idx_bits, int64_
     segment_softmax_bwd_kernel<<<ceil_div(n_rows, 4), 256, 0, s>>>(
         static_cast<const int64_t*>(row_ptr), n_rows, alpha, dalpha, dscore);
   TGX_LAUNCHED("segment_softmax_bwd_kernel");
-  return TGX_OK;
-}
-
-extern "C" int tgx_edge_outer_sum_workspace(int64_t n_edges, int width, size_t* bytes) {
-  TGX_REQUIRE(bytes, "null bytes");
-  TGX_REQUIRE(n_edges >= 0 && (width == 16 || width == 32 || width == 64), "bad sizes");
-  int64_t chunk = 0;
-  const int nb = n_edges ? outer_blocks(n_edges, &chunk) : 0;
-  *bytes = align_up(static_cast<size_t>(nb) * (width * width + width) * sizeof(float));
-  return TGX_OK;
-}
-
-extern "C" int tgx_edge_outer_sum(const float* g, const float* a, int64_t n_edges, int width,
-                                  float* dw, float* db, void* ws, size_t ws_bytes,
-                                  void* stream) {
-  TGX_REQUIRE(n_edges >= 0 && (width == 16 || width == 32 || width == 64), "bad sizes");
-  TGX_REQUIRE(dw, "null dw");
-  hipStream_t s = as_stream(stream);
-  const int n = width * width + width;
-  if (n_edges == 0) {
-    // Zero sums, written by a kernel rather than a memset.
-    outer_sum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(nullptr, 0, n, width, dw, db);
-    TGX_LAUNCHED("outer_sum_final_kernel");
-    return TGX_OK;
-  }
-  TGX_REQUIRE(g && a && ws, "null pointer");
-  int64_t chunk = 0;
-  const int nb = outer_blocks(n_edges, &chunk);
-  TGX_REQUIRE(ws_bytes >= static_cast<size_t>(nb) * n * sizeof(float), "workspace too small");
-  float* partial = static_cast<float*>(ws);
-  TGX_PROFILE("outer_sum_kernel", s);
-  if (width == 16) outer_sum_kernel<16><<<nb, 256, 0, s>>>(g, a, n_edges, chunk, partial);
-  if (width == 32) outer_sum_kernel<32><<<nb, 256, 0, s>>>(g, a, n_edges, chunk, partial);
-  if (width == 64) outer_sum_kernel<64><<<nb, 256, 0, s>>>(g, a, n_edges, chunk, partial);
-  TGX_LAUNCHED("outer_sum_kernel");
-  outer_sum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(partial, nb, n, width, dw, db);
-  TGX_LAUNCHED("outer_sum_final_kernel");
   return TGX_OK;
 }

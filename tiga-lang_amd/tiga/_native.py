@@ -96,10 +96,9 @@ _SIGNATURES: dict[str, list] = {
                      P(c_i64), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                      c_int, c_int, c_vp],
     "tgx_edge_mlp_scores": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp],
-    "tgx_edge_mlp_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, c_vp,
-                              P(c_vp), c_vp],
-    "tgx_edge_outer_sum_workspace": [c_i64, c_int, P(c_size)],
-    "tgx_edge_outer_sum": [c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_size, c_vp],
+    "tgx_edge_mlp_backward_workspace": [c_i64, P(EdgeMlp), P(c_size)],
+    "tgx_edge_mlp_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, P(c_vp),
+                              c_vp, c_size, c_vp],
     "tgx_segment_softmax_fwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tgx_segment_softmax_bwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tgx_profile_begin": [],

@@ -341,15 +341,18 @@ class EdgeMlpFunction(torch.autograd.Function):
         dev = col_idx.device
         L = len(chain)
         dscore = dscore.contiguous()
-        acts = torch.empty(L, E, W, dtype=torch.float32, device=dev)
-        dz = torch.empty(L, E, W, dtype=torch.float32, device=dev)
         dsegs = [torch.empty(E, s.shape[1], dtype=torch.float32, device=dev) for s in segs]
         mlp = _mlp_struct(chain, roles, segs, buf, W)
+        ws_bytes = ctypes.c_size_t()
+        _native.call("tgx_edge_mlp_backward_workspace", E, ctypes.byref(mlp),
+                     ctypes.byref(ws_bytes))
+        ws = torch.empty(max(ws_bytes.value, 4), dtype=torch.uint8, device=dev)
+        dweights = torch.empty(L, W * W + W, dtype=torch.float32, device=dev)
         ptrs = (ctypes.c_void_p * 4)(*[d.data_ptr() for d in dsegs], *([None] * (4 - len(dsegs))))
         _native.call("tgx_edge_mlp_backward", col_idx.data_ptr(),
                      graph._dst_index32().data_ptr(), _native.idx_bits(row_ptr), E,
-                     ctypes.byref(mlp), dscore.data_ptr(), acts.data_ptr(), dz.data_ptr(),
-                     ptrs, _native.stream_of(col_idx))
+                     ctypes.byref(mlp), dscore.data_ptr(), dweights.data_ptr(), ptrs,
+                     ws.data_ptr(), ws_bytes.value, _native.stream_of(col_idx))
         grads = []
         for s, (role, d, shape) in enumerate(zip(roles, dsegs, ctx.shapes)):
             if not ctx.needs_input_grad[4 + s]:
@@ -362,22 +365,13 @@ class EdgeMlpFunction(torch.autograd.Function):
             else:
                 g = _reduce_rows(graph, d)
             grads.append(g.reshape(shape))
-        ws_bytes = ctypes.c_size_t()
-        _native.call("tgx_edge_outer_sum_workspace", E, W, ctypes.byref(ws_bytes))
-        ws = torch.empty(max(ws_bytes.value, 4), dtype=torch.uint8, device=dev)
         for l, layer in enumerate(chain):
             out_f, in_f = layer.linear.out_features, layer.linear.in_features
             k = 4 + ctx.n_seg + 2 * l
-            if not (ctx.needs_input_grad[k] or ctx.needs_input_grad[k + 1]):
-                grads += [None, None]
-                continue
-            dw_full = torch.empty(W, W, dtype=torch.float32, device=dev)
-            db_full = torch.empty(W, dtype=torch.float32, device=dev)
-            _native.call("tgx_edge_outer_sum", dz[l].data_ptr(), acts[l].data_ptr(), E, W,
-                         dw_full.data_ptr(), db_full.data_ptr(), ws.data_ptr(), ws_bytes.value,
-                         _native.stream_of(dz))
-            dW = dw_full[:out_f, :in_f] if ctx.needs_input_grad[k] else None
-            db = db_full[:out_f] if ctx.has_bias[l] and ctx.needs_input_grad[k + 1] else None
+            blk = dweights[l]
+            dW = blk[:W * W].view(W, W)[:out_f, :in_f] if ctx.needs_input_grad[k] else None
+            db = (blk[W * W:W * W + out_f] if ctx.has_bias[l] and ctx.needs_input_grad[k + 1]
+                  else None)
             grads += [dW, db]
         return (None, None, None, None, *grads)
 
