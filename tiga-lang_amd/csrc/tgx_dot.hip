@@ -492,11 +492,13 @@ bool dot_shape(int H, int D, DotShape* s) {
   X(16, 16) X(16, 8) X(16, 4) X(16, 2) X(16, 1)
 
 // Loads in flight per lane group (each covers a k and a v row, or a q and a
-// dout row).  For H*D = 256 (two edges per wave-load) 2 measured best on
-// R-MAT scale 21, H=4, D=64 (3: +1%, 4: +2%, 6: +8% in the source pass).
+// dout row).  For H*D = 256 (32 lanes per row, two edges per wave-load) 1
+// measured best on R-MAT scale 21, H=4, D=64 (2: +1.6% forward, +2.2%
+// backward; 3: +4.6%), i.e. two edges' rows per wave in flight; other
+// widths keep 2.
 template <int G>
 constexpr int dot_unroll() {
-  return 2;
+  return G == 32 ? 1 : 2;
 }
 
 template <typename I, int G, int HL>
