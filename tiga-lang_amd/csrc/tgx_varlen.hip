@@ -126,6 +126,11 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // normalisation, and the O rescale is skipped for nearly every tile.
 constexpr float kRescaleLog2 = 8.f;
 
+// MFMA clusters run at wave priority 1 (s_setprio) and the softmax work
+// between them at 0: of the two waves sharing a SIMD, the one with MFMAs
+// ready issues them back to back while the other fills the VALU (dK/dV
+// 2.32 -> 2.26 ms on C5; forward and dQ unchanged).
+
 // Staging of one 64-row block of two [N, H, D] tensors by 256 threads:
 // thread t holds D / 32 chunks of 16 B of each.  Rows at or past `end` are
 // clamped to row end - 1 (finite values the caller masks; every staged
@@ -282,6 +287,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) c[kt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
@@ -291,6 +297,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
           for (int qt = 0; qt < 2; ++qt) c[kt][qt] = mfma(kf, qf[qt][kc], c[kt][qt]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       // Causal/sequence mask (diagonal and last tiles only), then the tile
       // max of the raw scores (scale > 0, so scaling commutes with max).
       const bool edge = CAUSAL ? (kbase + VBN > qb || kbase + VBN > ks1) : kbase + VBN > ks1;
@@ -365,6 +372,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
           }
       }
       // O^T += V^T P^T over the 64 keys (2 k-steps of 32).
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
@@ -374,6 +382,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
           for (int qt = 0; qt < 2; ++qt) o[dt][qt] = mfma(vf, pf[qt][k2], o[dt][qt]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     }
     if (more) stage_store<T, D>(stage, ks[buf ^ 1], vs[buf ^ 1]);
   }
@@ -535,6 +544,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
       sc[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
       dp[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
     }
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
@@ -545,6 +555,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
         dp[qt] = mfma(da, vf[kc], dp[qt]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     // P = exp(S*scale - lse), dS = P (dP - delta); packed per 32-query step.
     // Causal: only the first block holds queries that precede keys of the
     // tile, so only it is masked (padded queries have lse = +inf, so P = 0).
@@ -568,6 +579,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
     else
       weights(std::false_type{});
     // dV^T += dO^T P, dK^T += Q^T dS over the block's 64 queries.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
@@ -578,6 +590,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
         dkt[dt] = mfma(qtv, sb[k2], dkt[dt]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   }
   if (key >= ks1) return;
   T* dkrow = a.dk + key * cs + h * D;
@@ -662,6 +675,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(BwdArgs<T> a) {
         sc[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
         dp[qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
       }
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
         const vec8<T> ka = ld8(&ks[16 * kt + lr][32 * kc + 8 * g]);
@@ -672,6 +686,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(BwdArgs<T> a) {
           dp[qt] = mfma(va, df[qt][kc], dp[qt]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       // Keys past a query (diagonal and last tiles only) get no weight;
       // padded queries have lse = +inf, so their P is 0.
       auto weights = [&](auto masked) {
@@ -692,6 +707,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(BwdArgs<T> a) {
         weights(std::false_type{});
     }
     // dQ^T += K^T dS^T.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
@@ -701,6 +717,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(BwdArgs<T> a) {
         for (int qt = 0; qt < 2; ++qt) dqt[dt][qt] = mfma(kta, sb[qt][k2], dqt[dt][qt]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   }
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
