@@ -214,3 +214,69 @@ def test_uncovered_networks_fall_back_or_refuse():
         rp_np = f64(rp).astype(np.int64)
         e_out, _ = ref.segment_softmax(rp_np, f64(s), f64(x)[f64(col).astype(np.int64)])
         assert rel_err(f64(out), e_out) <= RTOL
+
+
+def _bench_net(f_in=8, hidden=16):
+    return nn.Sequential(nn.Linear(3 + 2 * f_in, hidden), nn.LeakyReLU(0.2),
+                         nn.Linear(hidden, 1)).to(DEV)
+
+
+@pytest.mark.parametrize("idx", [torch.int32, torch.int64])
+def test_many_steps_per_block_and_index_dtypes(idx):
+    """About 330k edges: every block of the fused backward walks several
+    256-edge steps and the last one is partial; int32 and int64 CSR."""
+    print(f"nn attention 330k edges idx={idx}", flush=True)
+    torch.manual_seed(7)
+    nodes, f_in = 20000, 8
+    rp, col = random_graph(nodes, nodes, 18, 11, hub=2000)
+    rp, col = rp.to(idx), col.to(idx)
+    graph = tg.Graph.from_csr(rp, col, num_src=nodes)
+    E = col.numel()
+    assert E > 300000
+    disp = torch.randn(E, 3, device=DEV, requires_grad=True)
+    x = torch.randn(nodes, f_in, device=DEV, requires_grad=True)
+    attn = _bench_net(f_in)
+    dout = torch.randn(nodes, f_in, device=DEV)
+    check(graph, GAT(attn), attn, [("edge", disp), ("src", x), ("dst", x)], x,
+          dict(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp}), dout)
+
+
+def test_weight_gradients_bit_identical_across_runs():
+    """Weight and bias gradients are block sums added in a fixed order."""
+    torch.manual_seed(3)
+    nodes = 5000
+    rp, col = random_graph(nodes, nodes, 20, 5)
+    graph = tg.Graph.from_csr(rp, col, num_src=nodes)
+    disp = torch.randn(col.numel(), 3, device=DEV)
+    x = torch.randn(nodes, 8, device=DEV)
+    attn = _bench_net()
+    kernel = GAT(attn)
+    dout = torch.randn(nodes, 8, device=DEV)
+    grads = []
+    for _ in range(3):
+        attn.zero_grad(set_to_none=True)
+        kernel(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp}).backward(dout)
+        assert kernel.last_variant.backend == "hip"
+        grads.append([p.grad.clone() for p in attn.parameters()])
+    for other in grads[1:]:
+        for a, b in zip(grads[0], other):
+            assert torch.equal(a, b)
+
+
+def test_graph_without_edges():
+    """No edges: zero outputs and zero gradients everywhere."""
+    nodes = 40
+    rp = torch.zeros(nodes + 1, dtype=torch.int64, device=DEV)
+    col = torch.zeros(0, dtype=torch.int64, device=DEV)
+    graph = tg.Graph.from_csr(rp, col, num_src=nodes)
+    disp = torch.randn(0, 3, device=DEV, requires_grad=True)
+    x = torch.randn(nodes, 8, device=DEV, requires_grad=True)
+    attn = _bench_net()
+    kernel = GAT(attn)
+    out = kernel(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp})
+    assert kernel.last_variant.backend == "hip"
+    out.backward(torch.randn(nodes, 8, device=DEV))
+    assert torch.count_nonzero(out) == 0
+    assert torch.count_nonzero(x.grad) == 0
+    for p in attn.parameters():
+        assert p.grad is not None and torch.count_nonzero(p.grad) == 0

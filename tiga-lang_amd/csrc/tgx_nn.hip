@@ -389,7 +389,9 @@ int mlp_bwd_blocks(int64_t n_edges, int64_t resident, int64_t* chunk) {
   return static_cast<int>(ceil_div(n_edges, c));
 }
 
-int check_mlp(const tgx_edge_mlp* mlp, MlpView* view) {
+// need_data: the segment rows are read (some edge exists); with no edges an
+// empty field may come with a null pointer.
+int check_mlp(const tgx_edge_mlp* mlp, MlpView* view, bool need_data) {
   TGX_REQUIRE(mlp, "null mlp");
   TGX_REQUIRE(mlp->n_layers >= 1 && mlp->n_layers <= kMaxLayers, "1 to %d linear layers",
               kMaxLayers);
@@ -403,7 +405,7 @@ int check_mlp(const tgx_edge_mlp* mlp, MlpView* view) {
     TGX_REQUIRE(mlp->seg_role[s] >= TGX_ROLE_SRC && mlp->seg_role[s] <= TGX_ROLE_EDGE,
                 "bad segment role");
     TGX_REQUIRE(mlp->seg_width[s] > 0 && mlp->seg_stride[s] >= mlp->seg_width[s] &&
-                    mlp->seg_dev[s],
+                    (mlp->seg_dev[s] || !need_data),
                 "bad segment %d", s);
     in_width += mlp->seg_width[s];
   }
@@ -522,7 +524,7 @@ extern "C" int tgx_edge_mlp_scores(const void* col, const int32_t* dst_index, in
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
-  int st = check_mlp(mlp, &v);
+  int st = check_mlp(mlp, &v, n_edges > 0);
   if (st != TGX_OK) return st;
   if (n_edges == 0) return TGX_OK;
   TGX_REQUIRE(col && dst_index && scores, "null pointer");
@@ -543,7 +545,7 @@ extern "C" int tgx_edge_mlp_backward_workspace(int64_t n_edges, const tgx_edge_m
   TGX_REQUIRE(bytes, "null bytes");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
-  int st = check_mlp(mlp, &v);
+  int st = check_mlp(mlp, &v, n_edges > 0);
   if (st != TGX_OK) return st;
   const int64_t n = static_cast<int64_t>(mlp->n_layers) * (mlp->width * mlp->width + mlp->width);
   int64_t chunk = 0;
@@ -567,7 +569,7 @@ extern "C" int tgx_edge_mlp_backward(const void* col, const int32_t* dst_index, 
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
-  int st = check_mlp(mlp, &v);
+  int st = check_mlp(mlp, &v, n_edges > 0);
   if (st != TGX_OK) return st;
   TGX_REQUIRE(dweights && dseg, "null pointer");
   const int n = mlp->n_layers * (mlp->width * mlp->width + mlp->width);
