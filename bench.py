@@ -707,7 +707,9 @@ def run_c5(args):
         "cold_ms_per_step": cold_ms,
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved,
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None},
+                     "frac": achieved / BF16_PEAK_TFLOPS,
+                     "traffic": measured_traffic("c5", dominant)[0],
+                     "traffic_source": measured_traffic("c5", dominant)[1]},
         "kernels": {kk: {"launches": n, "avg_ms": t / n,
                          "tflops": (kflops[kk] / (t / n * 1e-3) / 1e12) if kk in kflops else None}
                     for kk, (n, t) in sorted(per.items())},
