@@ -10,7 +10,7 @@ reference's CPU path timed on a bounded sample of the same workload.
 
   python bench.py [--steps K] [--warmup W]
                   [--config c1..c5|dense|dense-causal|dense-pruned|nn]
-                  [--no-cpu] [--no-cold]
+                  [--no-cpu] [--no-cold] [--no-graph]
 
 c1-c5 are BASELINE.json's configurations; dense* are the reference's dense
 attention benchmark shapes (N=4096, H=16, D=64, fp16, forward); nn is the
@@ -57,6 +57,8 @@ def parse():
                              "dense-pruned", "nn"])
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip the HIP-graph replay measurement (c1, c2)")
     ap.add_argument("--no-cold", action="store_true",
                     help="skip the cold-cache samples (kernel traces then hold only the "
                          "warmup and timed launches)")
@@ -232,6 +234,52 @@ def cold_step_ms(step, samples=5):
     return sorted(times)[len(times) // 2]
 
 
+def graph_step_ms(leaves, capture_step, replays=20):
+    """Mean time of one step replayed from a HIP graph
+    (torch.cuda.graph): warm-up on a side stream (per-graph plans and the
+    transposed CSR are built there, with their host synchronisations), one
+    capture of `capture_step` (forward + backward into the leaves' .grad),
+    `replays` timed replays between HIP events on the current stream.  The
+    last replay's gradients are checked bit for bit against an eager step.
+    Returns None with --no-graph."""
+    import torch
+
+    if ARGS.no_graph:
+        return None
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            for t in leaves:
+                t.grad = None
+            capture_step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    for t in leaves:
+        t.grad = None
+    with torch.cuda.graph(g):
+        capture_step()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / replays
+    got = [t.grad.clone() for t in leaves]
+    for t in leaves:
+        t.grad = None
+    capture_step()
+    torch.cuda.synchronize()
+    for a, b in zip(got, leaves):
+        assert torch.equal(a, b.grad), "graph replay differs from the eager step"
+    del g
+    return ms
+
+
 def _timed_reps(fn, budget_s=10.0, max_reps=3):
     fn()
     reps, t = 0, 0.0
@@ -386,6 +434,9 @@ def run_c2(args):
         elapsed = time.perf_counter() - t0
     per_kernel = {k: (n, ms) for k, (n, ms) in timer.totals.items()}
     cold_ms = cold_step_ms(step)
+    graph_ms = graph_step_ms(
+        [h, a_src, a_dst],
+        lambda: kernel(graph=graph, src={"h": h}, dst={"h": h}).backward(dout))
     bytes_per = gat_kernel_bytes(N, E, H, D)
     step_bytes = sum(bytes_per.values())
     dominant = max((k for k in per_kernel if k in bytes_per), key=lambda k: per_kernel[k][1])
@@ -410,6 +461,7 @@ def run_c2(args):
                    "heads": H, "head_dim": D, "index_dtype": "int64"},
         "hbm_frac_step": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "cold_ms_per_step": cold_ms,
+        "graph_ms_per_step": graph_ms,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic("c2", dominant)[0],
@@ -464,6 +516,10 @@ def run_c1(args):
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
     cold_ms = cold_step_ms(step)
+    ones = torch.ones(N, F_, device=dev)
+    graph_ms = graph_step_ms(
+        [x, w],
+        lambda: kernel(graph=graph, src={"x": x}, dst={}, edge={"weight": w}).backward(ones))
     bytes_per = sum_kernel_bytes(N, N, E, F_)
     dominant = max((k for k in timer.totals if k in bytes_per), key=lambda k: timer.totals[k][1])
     n_launch, total_ms = timer.totals[dominant]
@@ -476,6 +532,7 @@ def run_c1(args):
         "data": "synthetic", "config": {"workload": "c1-weighted-sum-fwd-bwd", "nodes": N,
                                         "edges": E, "features": F_},
         "cold_ms_per_step": cold_ms,
+        "graph_ms_per_step": graph_ms,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic("c1", dominant)[0],
