@@ -408,6 +408,9 @@ typedef struct tgx_edge_mlp {
   int32_t seg_width[4];
   int64_t seg_stride[4];      /* row stride in floats */
   const float* seg_dev[4];
+  /* Real output width of each layer (1..width, the last one 1; 0 = width):
+   * rows and columns past the real shapes are zero padding the kernels skip. */
+  int32_t out_width[3];
 } tgx_edge_mlp;
 
 /* scores[e] = MLP(x_e) for every edge.  dst_index_dev [n_edges] int32 is the

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void edge_mlp_fwd_kernel(const I* __restrict__
   gather_inputs<I, W>(m, e, col, dst, a);
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
-    linear<W, false>(wsh + l * (W * W + W), a, z);
+    linear<W, false>(wsh + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
     const int act = m.act[l];
     const float p = m.param[l];
 #pragma unroll
@@ -63,7 +63,10 @@ __global__ __launch_bounds__(256) void edge_mlp_fwd_kernel(const I* __restrict__
   const float* wl = wsh + (L - 1) * (W * W + W);
   float s = wl[W * W];
 #pragma unroll
-  for (int i = 0; i < W; ++i) s = fmaf(wl[i], a[i], s);
+  for (int k = 0; k < W / 4; ++k)
+    if (k < m.nb_in[L - 1])
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s = fmaf(wl[4 * k + j], a[4 * k + j], s);
   scores[e] = s;
 }
 
@@ -236,7 +239,7 @@ __global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
       for (int k = 0; k < W; ++k) a[k] = x[k];
       static_for<L - 1>([&](auto lc) {
         constexpr int l = decltype(lc)::value;
-        linear<W>(wsh + l * NW, a, z[l]);
+        linear<W>(wsh + l * NW, a, z[l], m.n_out[l], m.nb_in[l]);
 #pragma unroll
         for (int o = 0; o < W; ++o) a[o] = activate(z[l][o], m.act[l], m.param[l]);
       });
@@ -279,7 +282,7 @@ __global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
         outer_layer<W>(sg, sa, dzl, a, acc[l]);
       }
       // d a[l] = W_l^T dz.
-      linear_t<W>(wsh + l * NW, dzl, g);
+      linear_t<W>(wsh + l * NW, dzl, g, m.n_out[l], m.nb_in[l]);
     });
     // g = d x: split per segment.
     if (valid) {
@@ -416,6 +419,18 @@ int check_mlp(const tgx_edge_mlp* mlp, MlpView* view, bool need_data) {
   MlpView v{};
   v.n_layers = mlp->n_layers;
   v.in_width = in_width;
+  int n_in = in_width;
+  for (int l = 0; l < kMaxLayers; ++l) {
+    int n_out = mlp->width;
+    if (l < mlp->n_layers && mlp->out_width[l] != 0) n_out = mlp->out_width[l];
+    if (l + 1 == mlp->n_layers) TGX_REQUIRE(n_out == 1 || mlp->out_width[l] == 0,
+                                            "the last layer has one output");
+    TGX_REQUIRE(n_out >= 1 && n_out <= mlp->width, "layer %d output width %d outside 1..%d", l,
+                n_out, mlp->width);
+    v.n_out[l] = n_out;
+    v.nb_in[l] = (n_in + 3) / 4;
+    n_in = n_out;
+  }
   for (int l = 0; l < kMaxLayers; ++l) {
     v.act[l] = l + 1 < mlp->n_layers ? mlp->act[l] : TGX_ACT_IDENTITY;
     v.param[l] = mlp->act_param[l];

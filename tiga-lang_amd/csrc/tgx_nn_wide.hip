@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
     for (int i = 0; i < W; i += 4)
       *reinterpret_cast<f32x4*>(out + i) = f32x4{a[i], a[i + 1], a[i + 2], a[i + 3]};
     if constexpr (l + 1 < L) {
-      linear<W>(wsh + l * (W * W + W), a, z[l]);
+      linear<W>(wsh + l * (W * W + W), a, z[l], m.n_out[l], m.nb_in[l]);
 #pragma unroll
       for (int o = 0; o < W; ++o) a[o] = activate(z[l][o], m.act[l], m.param[l]);
     }

@@ -48,7 +48,8 @@ class EdgeMlp(ctypes.Structure):
                 ("act", ctypes.c_int32 * 3), ("act_param", ctypes.c_float * 3),
                 ("weights_dev", c_vp), ("n_segments", ctypes.c_int32),
                 ("seg_role", ctypes.c_int32 * 4), ("seg_width", ctypes.c_int32 * 4),
-                ("seg_stride", ctypes.c_int64 * 4), ("seg_dev", c_vp * 4)]
+                ("seg_stride", ctypes.c_int64 * 4), ("seg_dev", c_vp * 4),
+                ("out_width", ctypes.c_int32 * 3)]
 
 
 # name -> argtypes (all return int status except where noted)

@@ -281,6 +281,7 @@ def _mlp_struct(chain, roles, segs, weights_buf, width):
     for l, layer in enumerate(chain):
         m.act[l] = _ACT[layer.act]
         m.act_param[l] = layer.param
+        m.out_width[l] = layer.linear.out_features
     m.weights_dev = weights_buf.data_ptr()
     m.n_segments = len(segs)
     for s, (role, seg) in enumerate(zip(roles, segs)):
