@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_native.exported_symbols())
-    assert lib.tgx_abi_version() == 2
+    assert lib.tgx_abi_version() == 3
     assert lib.tgx_status_string(1) == b"invalid argument"
 
 
@@ -377,3 +377,32 @@ def test_reference_method_runs_eager_even_when_covered():
     with pytest.raises(NotImplementedError, match="no eager"):
         Pruned().reference(graph=tg.Graph.dense(2), src={"k": torch.ones(2, 3)},
                            dst={"q": torch.ones(2, 3)})
+
+
+def test_edge_mlp_validation_of_layer_widths():
+    """tgx_edge_mlp: out_width beyond the padded width, or a last layer with
+    more than one output, is rejected before anything is launched."""
+    lib = _native.lib()
+    buf = torch.zeros(2, 32 * 32 + 32)
+    seg = torch.zeros(4, 8)
+
+    def mlp(out_width):
+        m = _native.EdgeMlp()
+        m.n_layers, m.width = 2, 32
+        m.act[0] = 1
+        m.weights_dev = buf.data_ptr()
+        m.n_segments = 1
+        m.seg_role[0], m.seg_width[0], m.seg_stride[0] = 0, 8, 8
+        m.seg_dev[0] = seg.data_ptr()
+        for i, w in enumerate(out_width):
+            m.out_width[i] = w
+        return m
+
+    size = ctypes.c_size_t()
+    for bad in ((40, 1), (16, 2), (-1, 1)):
+        m = mlp(bad)
+        assert lib.tgx_edge_mlp_backward_workspace(0, ctypes.byref(m), ctypes.byref(size)) == 1
+        assert b"width" in lib.tgx_last_error() or b"output" in lib.tgx_last_error()
+    for good in ((16, 1), (0, 0), (32, 1)):
+        m = mlp(good)
+        assert lib.tgx_edge_mlp_backward_workspace(0, ctypes.byref(m), ctypes.byref(size)) == 0
