@@ -83,3 +83,19 @@ def sum_step(row_ptr, col, x, w, dout):
     out = torch.sparse.mm(a, x)
     out.backward(dout)
     return out, x.grad, w.grad
+
+
+def nn_gat_step(row_ptr, col, x, disp, net, dout):
+    """The nn-scored GAT step on the eager path (CPU tensors): score =
+    net(cat[displacement, x_src, x_dst]) per edge (a tg.nn.trace module
+    applied to its concatenated inputs, compiler/nn_capture.py:1-33), online
+    softmax over each destination row, value x_src; forward + backward into
+    x, the displacement and the network's parameters."""
+    destination = destination_index(row_ptr)
+    num_dst = row_ptr.numel() - 1
+    x = x.detach().requires_grad_(True)
+    disp = disp.detach().requires_grad_(True)
+    score = net(torch.cat([disp, x[col], x[destination]], dim=1))[:, 0]
+    out = reduce_online_softmax(score, x[col], destination, num_dst)
+    out.backward(dout)
+    return out, x.grad, disp.grad

@@ -480,3 +480,29 @@ def test_eager_torch_cpu_path_matches_oracle():
     out = eager_torch.dot_step(rpt, colt, *(torch.tensor(a) for a in (q, k, v, bias)), 0.5)
     e_out, _ = ref.dot_fwd(rp, col, q, k, v, 0.5, bias)
     np.testing.assert_allclose(out.detach().numpy(), e_out, rtol=1e-10, atol=1e-12)
+
+
+def test_eager_nn_step_matches_oracle():
+    """oracle/eager_torch.nn_gat_step (the timed CPU leg of the nn bench)
+    agrees with ref.nn_attention_fwd/bwd in float64."""
+    from torch import nn
+
+    from oracle import eager_torch
+
+    rng = np.random.default_rng(13)
+    rp, col = random_csr(rng, 30, 30, 6)
+    x = rng.standard_normal((30, 4))
+    disp = rng.standard_normal((col.size, 3))
+    torch.manual_seed(0)
+    net = nn.Sequential(nn.Linear(11, 6), nn.LeakyReLU(0.2), nn.Linear(6, 1)).double()
+    dout = rng.standard_normal((30, 4))
+    out, dx, ddisp = eager_torch.nn_gat_step(torch.tensor(rp), torch.tensor(col), torch.tensor(x),
+                                             torch.tensor(disp), net, torch.tensor(dout))
+    layers = [(net[0].weight.detach().numpy(), net[0].bias.detach().numpy(), "leaky_relu", 0.2),
+              (net[2].weight.detach().numpy(), net[2].bias.detach().numpy(), "identity", 0.0)]
+    inputs = [("edge", disp), ("src", x), ("dst", x)]
+    e_out, _ = ref.nn_attention_fwd(rp, col, inputs, layers, x)
+    np.testing.assert_allclose(out.detach().numpy(), e_out, rtol=1e-10, atol=1e-12)
+    (d_edge, d_src, d_dst), d_value, _ = ref.nn_attention_bwd(rp, col, inputs, layers, x, dout)
+    np.testing.assert_allclose(ddisp.numpy(), d_edge, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(dx.numpy(), d_src + d_dst + d_value, rtol=1e-9, atol=1e-12)
