@@ -12,11 +12,11 @@
 // MI355X design: the score network is evaluated edge-parallel, one edge per
 // lane, so every lane does useful work whatever the row degrees; its inputs
 // are gathered straight from the field tables (no [E, K] tensor) and its
-// weights are uniform across the wave: staged once per workgroup in LDS and
-// read row by row (a broadcast), the next row in flight while the current
-// one is applied.  Every layer
-// is zero-padded to a common width W (16, 32 or 64) on the host, which keeps
-// every register index compile-time.  The softmax and the value gather are
+// weights, uniform across the wave, are read through the scalar cache into
+// scalar registers that feed the FMAs directly.  Every layer is zero-padded
+// to a common width W (16, 32 or 64) on the host, which keeps every
+// register index compile-time; the real widths bound the loops through
+// uniform branches.  The softmax and the value gather are
 // separate row passes (segment softmax here, the weighted CSR sum of
 // tgx_sum.hip for the values), which adds 8 bytes per edge (score, weight)
 // to a gather of 4 F bytes per edge.
@@ -41,33 +41,30 @@ namespace {
 
 using namespace mlp;
 
+// Occupancy targets (blocks of 256 per CU, i.e. waves per SIMD): left to
+// itself the register allocator spends registers on scheduling freedom and
+// lands just above a step (one fewer wave per SIMD).
+template <int W, int L>
+constexpr int fwd_blocks_per_cu() { return W <= 32 ? (L <= 2 ? 6 : 5) : 3; }
+template <int W, int L>
+constexpr int bwd_blocks_per_cu() { return W == 16 ? 3 : (L <= 2 ? 2 : 1); }
+
 template <typename I, int W, int L>
-__global__ __launch_bounds__(256) void edge_mlp_fwd_kernel(const I* __restrict__ col,
+__global__ __launch_bounds__(256, (fwd_blocks_per_cu<W, L>())) void edge_mlp_fwd_kernel(const I* __restrict__ col,
                                                            const int32_t* __restrict__ dst,
                                                            int64_t n_edges, MlpView m,
                                                            float* __restrict__ scores) {
-  __shared__ __align__(16) float wsh[L * (W * W + W)];
-  stage_weights<W, L>(m.w, wsh);
+  cfloat* wg = scalar_weights(m.w);
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (e >= n_edges) return;
   float a[W], z[W];
   gather_inputs<I, W>(m, e, col, dst, a);
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
-    linear<W, false>(wsh + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
-    const int act = m.act[l];
-    const float p = m.param[l];
-#pragma unroll
-    for (int o = 0; o < W; ++o) a[o] = activate(z[o], act, p);
+    linear<W>(wg + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
+    activate_all<W>(z, a, m.act[l], m.param[l], m.nb_in[l + 1]);
   }
-  const float* wl = wsh + (L - 1) * (W * W + W);
-  float s = wl[W * W];
-#pragma unroll
-  for (int k = 0; k < W / 4; ++k)
-    if (k < m.nb_in[L - 1])
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s = fmaf(wl[4 * k + j], a[4 * k + j], s);
-  scores[e] = s;
+  scores[e] = linear_out1<W>(wg + (L - 1) * (W * W + W), a, m.nb_in[L - 1]);
 }
 
 // ---- weight gradients on fp32 MFMA ------------------------------------------
@@ -204,16 +201,15 @@ __device__ __forceinline__ void outer_store(const OuterAcc<W>& acc, float* red) 
 // the block's sums go to partial[block] (n_layers x [W*W | W]) in a fixed
 // order.
 template <typename I, int W, int L>
-__global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
+__global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd_kernel(
     const I* __restrict__ col, const int32_t* __restrict__ dst, int64_t n_edges, int64_t chunk,
-    MlpView m, const float* __restrict__ dscore, float* __restrict__ partial) {
+    MlpView m_arg, const float* __restrict__ dscore, float* __restrict__ partial) {
   constexpr int NW = W * W + W;
   constexpr int LD = mlp_ld<W>();
   constexpr int SW = 2 * 32 * LD;  // one wave's staging: G rows | A rows
   static_assert(SW >= NW, "a wave's staging holds one layer's block");
-  __shared__ __align__(16) float wsh[L * NW];
   __shared__ __align__(16) float stage[4 * SW];
-  stage_weights<W, L>(m.w, wsh);
+  cfloat* const w_all = scalar_weights(m_arg.w);
   const int wave = threadIdx.x >> 6;
   float* sg = stage + wave * SW;
   float* sa = sg + 32 * LD;
@@ -223,6 +219,13 @@ __global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk;
   const int64_t e1 = e0 + chunk < n_edges ? e0 + chunk : n_edges;
   for (int64_t base = e0; base < e1; base += 256) {
+    // The weights are reloaded (scalar-cache hits) and the network's shape
+    // fields re-read in every step: hoisted out of the loop, the weights and
+    // the tile guards derived from the shape would all be live at once and
+    // spill.
+    cfloat* wg = opaque(w_all);
+    MlpView m = m_arg;
+    launder(m);
     const int64_t e = base + threadIdx.x;
     const bool valid = e < e1;
     float x[W];                        // gathered input (layer 0's input)
@@ -239,9 +242,8 @@ __global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
       for (int k = 0; k < W; ++k) a[k] = x[k];
       static_for<L - 1>([&](auto lc) {
         constexpr int l = decltype(lc)::value;
-        linear<W>(wsh + l * NW, a, z[l], m.n_out[l], m.nb_in[l]);
-#pragma unroll
-        for (int o = 0; o < W; ++o) a[o] = activate(z[l][o], m.act[l], m.param[l]);
+        linear<W>(wg + l * NW, a, z[l], m.n_out[l], m.nb_in[l]);
+        activate_all<W>(z[l], a, m.act[l], m.param[l], m.nb_in[l + 1]);
       });
     }
     // Input of layer l: x, or the activation of z[l-1].
@@ -251,51 +253,37 @@ __global__ __launch_bounds__(256) void edge_mlp_bwd_kernel(
 #pragma unroll
         for (int k = 0; k < W; ++k) a[k] = x[k];
       } else {
-#pragma unroll
-        for (int k = 0; k < W; ++k) a[k] = activate(z[l - 1][k], m.act[l - 1], m.param[l - 1]);
+        activate_all<W>(z[l - 1], a, m.act[l - 1], m.param[l - 1], m.nb_in[l]);
       }
     };
     // Last layer: one output, gradient ds (0 on lanes past the range).
     const float ds = valid ? dscore[e] : 0.f;
     float g[W];
     {
-      const float* wl = wsh + (L - 1) * NW;
+      cfloat* wl = wg + (L - 1) * NW;
       float dzl[W], a[W];
 #pragma unroll
       for (int i = 0; i < W; ++i) dzl[i] = i == 0 ? ds : 0.f;
       layer_input(std::integral_constant<int, L - 1>{}, a);
       outer_layer<W>(sg, sa, dzl, a, acc[L - 1]);
-#pragma unroll
-      for (int i = 0; i < W; ++i) g[i] = ds * wl[i];   // d a[L-1]
+      linear_t_out1<W>(wl, ds, g, m.nb_in[L - 1]);   // d a[L-1] = ds w
     }
     static_for<L - 1>([&](auto kc) {
       constexpr int l = L - 2 - decltype(kc)::value;
       float dzl[W];
+      activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.nb_in[l + 1]);
 #pragma unroll
-      for (int o = 0; o < W; ++o) {
-        dzl[o] = g[o] * activate_grad(z[l][o], m.act[l], m.param[l]);
-        pin(dzl[o]);
-      }
+      for (int o = 0; o < W; ++o) pin(dzl[o]);
       {
         float a[W];
         layer_input(std::integral_constant<int, l>{}, a);
         outer_layer<W>(sg, sa, dzl, a, acc[l]);
       }
       // d a[l] = W_l^T dz.
-      linear_t<W>(wsh + l * NW, dzl, g, m.n_out[l], m.nb_in[l]);
+      linear_t<W>(wg + l * NW, dzl, g, m.n_out[l], m.nb_in[l]);
     });
     // g = d x: split per segment.
-    if (valid) {
-#pragma unroll
-      for (int s = 0; s < kMaxSegments; ++s) {
-        if (s >= m.n_seg) break;
-        const int off = m.off[s], wd = m.width[s];
-        float* q = m.grad[s] + e * wd - off;
-#pragma unroll
-        for (int k = 0; k < W; ++k)
-          if (k >= off && k < off + wd) q[k] = g[k];
-      }
-    }
+    if (valid) scatter_segments<W>(m, e, g);
   }
   // Block sums, layer by layer: each wave's block into its staging region,
   // then the four added in wave order.

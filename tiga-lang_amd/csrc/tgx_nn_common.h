@@ -1,6 +1,6 @@
 // Device code shared by the edge-MLP kernels (tgx_nn.hip, tgx_nn_wide.hip):
-// the network view, activations, per-edge input gathers and the row-by-row
-// dense layers over LDS-staged weights.
+// the network view, activations, per-edge input gathers and the dense
+// layers over weights held in scalar registers.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -85,7 +85,8 @@ __device__ __forceinline__ int64_t seg_row(int role, int64_t e, const I* col,
 // x[k] for k < in_width from the concatenated segments (zero beyond).  The
 // segment loop is compile-time, so each segment's row pointer is a plain
 // per-lane value and every x index is a constant (no indexed register
-// arrays); which columns a segment fills is a uniform range test.
+// arrays); which columns a segment fills is a uniform range test, made per
+// block of 4 columns first.
 template <typename I, int W>
 __device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const I* col,
                                               const int32_t* dst, float (&x)[W]) {
@@ -94,11 +95,46 @@ __device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const
 #pragma unroll
   for (int s = 0; s < kMaxSegments; ++s) {
     if (s >= m.n_seg) break;
-    const int off = m.off[s], wd = m.width[s];
+    const int off = m.off[s], end = m.off[s] + m.width[s];
     const float* p = m.ptr[s] + seg_row(m.role[s], e, col, dst) * m.stride[s] - off;
 #pragma unroll
-    for (int k = 0; k < W; ++k)
-      if (k >= off && k < off + wd) x[k] = p[k];
+    for (int b = 0; b < W; b += 4) {
+      if (b + 4 > off && b < end) {
+        if (b >= off && b + 4 <= end) {
+#pragma unroll
+          for (int k = b; k < b + 4; ++k) x[k] = p[k];
+        } else {
+#pragma unroll
+          for (int k = b; k < b + 4; ++k)
+            if (k >= off && k < end) x[k] = p[k];
+        }
+      }
+    }
+  }
+}
+
+// q_s[e][k - off_s] = g[k] for every segment s (the per-edge input gradient
+// split per segment), with the same block-then-column range tests.
+template <int W>
+__device__ __forceinline__ void scatter_segments(const MlpView& m, int64_t e, const float (&g)[W]) {
+#pragma unroll
+  for (int s = 0; s < kMaxSegments; ++s) {
+    if (s >= m.n_seg) break;
+    const int off = m.off[s], wd = m.width[s], end = off + wd;
+    float* q = m.grad[s] + e * wd - off;
+#pragma unroll
+    for (int b = 0; b < W; b += 4) {
+      if (b + 4 > off && b < end) {
+        if (b >= off && b + 4 <= end) {
+#pragma unroll
+          for (int k = b; k < b + 4; ++k) q[k] = g[k];
+        } else {
+#pragma unroll
+          for (int k = b; k < b + 4; ++k)
+            if (k >= off && k < end) q[k] = g[k];
+        }
+      }
+    }
   }
 }
 
@@ -119,101 +155,172 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// One weight row of a layer held in LDS (16-byte reads) and its bias.
-template <int W>
-struct WRow {
-  f32x4 w[W / 4];
-  float b;
-};
-template <int W>
-__device__ __forceinline__ void load_row(const float* wl, int o, WRow<W>& r) {
-#pragma unroll
-  for (int k = 0; k < W / 4; ++k) r.w[k] = *reinterpret_cast<const f32x4*>(wl + o * W + 4 * k);
-  r.b = wl[W * W + o];
+// Layer weights are read through the scalar data cache: every lane of a
+// wave needs the same weight at the same time, so a uniform load from the
+// constant address space puts it in a scalar register that feeds the FMA
+// directly (one scalar operand per VALU instruction).  No LDS staging, no
+// LDS read latency and no vector registers are spent on weights.
+typedef __attribute__((address_space(4))) const float cfloat;
+
+__device__ __forceinline__ cfloat* scalar_weights(const float* p) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wold-style-cast"
+  return (cfloat*)p;   // generic -> constant address space (same address)
+#pragma clang diagnostic pop
 }
 
-// z = W_l a + b_l, one weight row at a time (wl is uniform across the wave).
-// Up to 32 wide and with kPrefetchRows, row o+1 is read from LDS while row
-// o's dot product runs, so the read latency overlaps the FMAs (at the cost
-// of one row of registers).  Otherwise only the layer's real shape is
-// computed: rows o < n_out and the first nb column blocks of 4 (nb =
-// ceil(n_in / 4)), padded rows getting z = 0; the skipped terms are products
-// with zero padding weights (forward scores 0.205 -> 0.166 ms on the 19-16-1
-// bench network).
-template <int W, bool kPrefetchRows = true>
-__device__ __forceinline__ void linear(const float* wl, const float (&a)[W], float (&z)[W],
-                                       int n_out, int nb) {
-  if constexpr (W <= 32 && kPrefetchRows) {
-    // Every padded row and column is multiplied here: the kernel using this
-    // path runs one wave per SIMD, where branches cost more than the FMAs
-    // they skip.  Each dot product is four interleaved partial sums, so
-    // consecutive FMAs are independent.
-    WRow<W> cur, nxt;
-    load_row<W>(wl, 0, cur);
-    static_for<W>([&](auto oc) {
-      constexpr int o = decltype(oc)::value;
-      if constexpr (o + 1 < W) load_row<W>(wl, o + 1, nxt);
-      float p[4] = {cur.b, 0.f, 0.f, 0.f};
+// p, with the compiler kept from knowing it is p (loads through it are not
+// hoisted out of the enclosing loop).
+__device__ __forceinline__ cfloat* opaque(cfloat* p) {
+  asm volatile("" : "+s"(p));
+  return p;
+}
+
+// The network's shape fields, hidden from the optimizer at this point (what
+// is derived from them is recomputed after it rather than hoisted).
+__device__ __forceinline__ void launder(MlpView& v) {
+  asm volatile("" : "+s"(v.n_seg), "+s"(v.in_width));
 #pragma unroll
-      for (int k = 0; k < W / 4; ++k)
+  for (int l = 0; l < kMaxLayers; ++l)
+    asm volatile("" : "+s"(v.n_out[l]), "+s"(v.nb_in[l]), "+s"(v.act[l]), "+s"(v.param[l]));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = fmaf(cur.w[k][j], a[4 * k + j], p[j]);
-      float acc = (p[0] + p[1]) + (p[2] + p[3]);
-      pin(acc);
-      z[o] = acc;
-      if constexpr (o + 1 < W) cur = nxt;
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  } else {
+  for (int s = 0; s < kMaxSegments; ++s)
+    asm volatile("" : "+s"(v.role[s]), "+s"(v.width[s]), "+s"(v.off[s]));
+}
+
+// z = W_l a + b_l over the layer's real shape, in tiles of 8 rows x 8
+// columns: a row tile runs when it holds a real output (o < n_out) and a
+// column tile when it holds a real input (4 nb = n_in rounded up to 4), so
+// one uniform branch skips 64 products with zero padding and the eight
+// weights of a tile row are one scalar load.  Each z[o] is the bias plus
+// its products in ascending column order; padded rows get z = 0.  The
+// padding of a column tile beyond n_in multiplies zero weights by the zero
+// (or finite) padded inputs.
+template <int W>
+__device__ __forceinline__ void linear(cfloat* wl, const float (&a)[W], float (&z)[W], int n_out,
+                                       int nb) {
+  static_assert(W % 8 == 0, "tiles of 8");
+  static_for<W / 8>([&](auto rc) {
+    constexpr int r0 = 8 * decltype(rc)::value;
+    if (r0 < n_out) {
 #pragma unroll
-    for (int o = 0; o < W; ++o) {
-      if (o < n_out) {
-        float acc = wl[W * W + o];
+      for (int r = 0; r < 8; ++r) z[r0 + r] = wl[W * W + r0 + r];
 #pragma unroll
-        for (int k = 0; k < W / 4; ++k)
-          if (k < nb)
+      for (int c = 0; c < W / 8; ++c) {
+        if (2 * c < nb) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = fmaf(wl[o * W + 4 * k + j], a[4 * k + j], acc);
-        pin(acc);
-        z[o] = acc;
-      } else {
-        z[o] = 0.f;
+          for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              z[r0 + r] = fmaf(wl[(r0 + r) * W + 8 * c + j], a[8 * c + j], z[r0 + r]);
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) z[r0 + r] = 0.f;
+    }
+  });
+}
+
+// g = W_l^T dz over the layer's real shape in the same 8 x 8 tiles (g is 0
+// beyond the real column tiles); each g[i] adds its rows in ascending order.
+template <int W>
+__device__ __forceinline__ void linear_t(cfloat* wl, const float (&dz)[W], float (&g)[W],
+                                         int n_out, int nb) {
+  static_assert(W % 8 == 0, "tiles of 8");
+#pragma unroll
+  for (int i = 0; i < W; ++i) g[i] = 0.f;
+  static_for<W / 8>([&](auto cc) {
+    constexpr int c0 = 8 * decltype(cc)::value;
+    if (c0 < 4 * nb) {
+#pragma unroll
+      for (int t = 0; t < W / 8; ++t) {
+        if (8 * t < n_out) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              g[c0 + j] = fmaf(wl[(8 * t + r) * W + c0 + j], dz[8 * t + r], g[c0 + j]);
+        }
+      }
+    }
+  });
+}
+
+// The one output of a last layer: b + w . a over the real column tiles.
+template <int W>
+__device__ __forceinline__ float linear_out1(cfloat* wl, const float (&a)[W], int nb) {
+  float z = wl[W * W];
+#pragma unroll
+  for (int c = 0; c < W / 8; ++c)
+    if (2 * c < nb)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) z = fmaf(wl[8 * c + j], a[8 * c + j], z);
+  return z;
+}
+
+// g = ds w (the input gradient of a one-output last layer), 0 beyond the
+// real column tiles.
+template <int W>
+__device__ __forceinline__ void linear_t_out1(cfloat* wl, float ds, float (&g)[W], int nb) {
+#pragma unroll
+  for (int c = 0; c < W / 8; ++c) {
+    if (2 * c < nb) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) g[8 * c + j] = ds * wl[8 * c + j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) g[8 * c + j] = 0.f;
     }
   }
 }
 
-// g = W_l^T dz (n_out and nb are unused: padded rows have dz = 0 and
-// padded columns zero weights, and the one-wave-per-SIMD kernel that uses
-// this runs faster without branches), W_l read row by row in order, row o+1
-// fetched while row o is applied.
-template <int W>
-__device__ __forceinline__ void linear_t(const float* wl, const float (&dz)[W], float (&g)[W],
-                                         int n_out, int nb) {
+// out[k] = f(z[k]) for the layer's real outputs (k < 4 nb, nb = its real
+// width in blocks of 4), 0 beyond.  The switch on the activation code is
+// taken once per layer; each case is a straight run over the elements.
+template <int W, typename F>
+__device__ __forceinline__ void map_real(const float (&z)[W], float (&out)[W], int nb, F f) {
 #pragma unroll
-  for (int i = 0; i < W; ++i) g[i] = 0.f;
-  WRow<W> cur, nxt;
-  load_row<W>(wl, 0, cur);
-  static_for<W>([&](auto oc) {
-    constexpr int o = decltype(oc)::value;
-    if constexpr (o + 1 < W) load_row<W>(wl, o + 1, nxt);
+  for (int k = 0; k < W / 4; ++k) {
+    if (k < nb) {
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
-      g[i] = fmaf(cur.w[i / 4][i % 4], dz[o], g[i]);
-      pin(g[i]);
+      for (int j = 0; j < 4; ++j) out[4 * k + j] = f(z[4 * k + j], 4 * k + j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[4 * k + j] = 0.f;
     }
-    if constexpr (o + 1 < W) cur = nxt;
-    __builtin_amdgcn_sched_barrier(0);
-  });
+  }
 }
 
-// The weights of all layers, staged once per workgroup in LDS (every lane
-// then reads the same address: a broadcast).
-template <int W, int L>
-__device__ __forceinline__ void stage_weights(const float* __restrict__ w, float* wsh) {
-  for (int i = threadIdx.x; i < L * (W * W + W); i += 256) wsh[i] = w[i];
-  __syncthreads();
+template <int W>
+__device__ __forceinline__ void activate_all(const float (&z)[W], float (&a)[W], int act,
+                                             float p, int nb) {
+  switch (act) {
+    case TGX_ACT_RELU: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_RELU, 0.f); }); break;
+    case TGX_ACT_LEAKY_RELU: map_real<W>(z, a, nb, [p](float v, int) { return activate(v, TGX_ACT_LEAKY_RELU, p); }); break;
+    case TGX_ACT_TANH: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_TANH, 0.f); }); break;
+    case TGX_ACT_SIGMOID: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_SIGMOID, 0.f); }); break;
+    case TGX_ACT_SILU: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_SILU, 0.f); }); break;
+    case TGX_ACT_GELU: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_GELU, 0.f); }); break;
+    case TGX_ACT_ELU: map_real<W>(z, a, nb, [p](float v, int) { return activate(v, TGX_ACT_ELU, p); }); break;
+    default: map_real<W>(z, a, nb, [](float v, int) { return v; }); break;
+  }
+}
+
+// dz[k] = g[k] * activate'(z[k]) for the real outputs, 0 beyond.
+template <int W>
+__device__ __forceinline__ void activate_grad_all(const float (&z)[W], const float (&g)[W],
+                                                  float (&dz)[W], int act, float p, int nb) {
+  switch (act) {
+    case TGX_ACT_RELU: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_RELU, 0.f); }); break;
+    case TGX_ACT_LEAKY_RELU: map_real<W>(z, dz, nb, [&g, p](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_LEAKY_RELU, p); }); break;
+    case TGX_ACT_TANH: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_TANH, 0.f); }); break;
+    case TGX_ACT_SIGMOID: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_SIGMOID, 0.f); }); break;
+    case TGX_ACT_SILU: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_SILU, 0.f); }); break;
+    case TGX_ACT_GELU: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_GELU, 0.f); }); break;
+    case TGX_ACT_ELU: map_real<W>(z, dz, nb, [&g, p](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_ELU, p); }); break;
+    default: map_real<W>(z, dz, nb, [&g](float, int k) { return g[k]; }); break;
+  }
 }
 
 // 64-wide chains: backward in two passes (tgx_nn_wide.hip).  Blocks and

@@ -23,8 +23,7 @@ template <typename I, int W, int L>
 __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
     const I* __restrict__ col, const int32_t* __restrict__ dst, int64_t n_edges, MlpView m,
     const float* __restrict__ dscore, float* __restrict__ acts, float* __restrict__ dz_out) {
-  __shared__ float wsh[L * (W * W + W)];
-  stage_weights<W, L>(m.w, wsh);
+  cfloat* wg = scalar_weights(m.w);
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (e >= n_edges) return;
   const int64_t plane = n_edges * W;
@@ -38,16 +37,15 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
     for (int i = 0; i < W; i += 4)
       *reinterpret_cast<f32x4*>(out + i) = f32x4{a[i], a[i + 1], a[i + 2], a[i + 3]};
     if constexpr (l + 1 < L) {
-      linear<W>(wsh + l * (W * W + W), a, z[l], m.n_out[l], m.nb_in[l]);
-#pragma unroll
-      for (int o = 0; o < W; ++o) a[o] = activate(z[l][o], m.act[l], m.param[l]);
+      linear<W>(wg + l * (W * W + W), a, z[l], m.n_out[l], m.nb_in[l]);
+      activate_all<W>(z[l], a, m.act[l], m.param[l], m.nb_in[l + 1]);
     }
   });
   // Last layer: one output, gradient ds.
   const float ds = dscore[e];
   float g[W];
   {
-    const float* wl = wsh + (L - 1) * (W * W + W);
+    cfloat* wl = wg + (L - 1) * (W * W + W);
     float* out = dz_out + (L - 1) * plane + e * W;
 #pragma unroll
     for (int i = 0; i < W; i += 4)
@@ -58,39 +56,18 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
   static_for<L - 1>([&](auto kc) {
     constexpr int l = L - 2 - decltype(kc)::value;
     float dzl[W];
+    activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.nb_in[l + 1]);
 #pragma unroll
-    for (int o = 0; o < W; ++o) {
-      dzl[o] = g[o] * activate_grad(z[l][o], m.act[l], m.param[l]);
-      pin(dzl[o]);
-    }
+    for (int o = 0; o < W; ++o) pin(dzl[o]);
     float* out = dz_out + l * plane + e * W;
 #pragma unroll
     for (int i = 0; i < W; i += 4)
       *reinterpret_cast<f32x4*>(out + i) = f32x4{dzl[i], dzl[i + 1], dzl[i + 2], dzl[i + 3]};
-    // d a[l] = W_l^T dz, accumulated row by row so W_l is read in order.
-    const float* wl = wsh + l * (W * W + W);
-#pragma unroll
-    for (int i = 0; i < W; ++i) g[i] = 0.f;
-    static_for<W>([&](auto oc) {
-      constexpr int o = decltype(oc)::value;
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        g[i] = fmaf(wl[o * W + i], dzl[o], g[i]);
-        pin(g[i]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    });
+    // d a[l] = W_l^T dz.
+    linear_t<W>(wg + l * (W * W + W), dzl, g, m.n_out[l], m.nb_in[l]);
   });
   // g = d x: split per segment.
-#pragma unroll
-  for (int s = 0; s < kMaxSegments; ++s) {
-    if (s >= m.n_seg) break;
-    const int off = m.off[s], wd = m.width[s];
-    float* q = m.grad[s] + e * wd - off;
-#pragma unroll
-    for (int k = 0; k < W; ++k)
-      if (k >= off && k < off + wd) q[k] = g[k];
-  }
+  scatter_segments<W>(m, e, g);
 }
 
 // v[0..B) = p[0..B) as 8- or 16-byte vector loads (p aligned to 4 B floats).
