@@ -26,7 +26,8 @@
 // per-edge gradients of every input segment (reduced per source row over the
 // transposed CSR and per destination row over the CSR by the caller) and
 // sums the weight and bias gradients (sum over edges of dz_l (x) a_l) in the
-// same pass on fp32 MFMA, from rows each wave stages in LDS; per-block
+// same pass: the hidden layers' on fp32 MFMA, from rows each wave stages in
+// LDS, the one-output last layer's (ds a) in per-lane registers; per-block
 // partial sums are added in a fixed order, so every gradient is
 // deterministic and nothing per layer and edge goes to HBM.
 #include <hip/hip_runtime.h>
@@ -213,11 +214,21 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
   const int wave = threadIdx.x >> 6;
   float* sg = stage + wave * SW;
   float* sa = sg + 32 * LD;
-  OuterAcc<W> acc[L];
+  OuterAcc<W> acc[L > 1 ? L - 1 : 1];   // the hidden layers' sums
+  float last_w[W];   // this lane's sum of ds a for the last layer, and of ds
+  float last_b = 0.f;
 #pragma unroll
-  for (int l = 0; l < L; ++l) acc[l].zero();
+  for (int i = 0; i < W; ++i) last_w[i] = 0.f;
+#pragma unroll
+  for (int l = 0; l < (L > 1 ? L - 1 : 1); ++l) acc[l].zero();
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk;
   const int64_t e1 = e0 + chunk < n_edges ? e0 + chunk : n_edges;
+  // Each step's source and destination row ids are loaded one step ahead.
+  int64_t next_src = 0, next_dst = 0;
+  if (e0 + threadIdx.x < e1) {
+    next_src = col[e0 + threadIdx.x];
+    next_dst = dst[e0 + threadIdx.x];
+  }
   for (int64_t base = e0; base < e1; base += 256) {
     // The weights are reloaded (scalar-cache hits) and the network's shape
     // fields re-read in every step: hoisted out of the loop, the weights and
@@ -231,10 +242,14 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
     float x[W];                        // gathered input (layer 0's input)
     float z[L > 1 ? L - 1 : 1][W];     // pre-activations of the hidden layers
     if (valid) {
-      gather_inputs<I, W>(m, e, col, dst, x);
+      gather_rows<W>(m, e, next_src, next_dst, x);
     } else {
 #pragma unroll
       for (int k = 0; k < W; ++k) x[k] = 0.f;
+    }
+    if (e + 256 < e1) {
+      next_src = col[e + 256];
+      next_dst = dst[e + 256];
     }
     {
       float a[W];
@@ -261,11 +276,16 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
     float g[W];
     {
       cfloat* wl = wg + (L - 1) * NW;
-      float dzl[W], a[W];
-#pragma unroll
-      for (int i = 0; i < W; ++i) dzl[i] = i == 0 ? ds : 0.f;
+      float a[W];
       layer_input(std::integral_constant<int, L - 1>{}, a);
-      outer_layer<W>(sg, sa, dzl, a, acc[L - 1]);
+      // One output row: its gradient ds a is summed per lane (an MFMA outer
+      // product would spend a 32 x 32 tile on it).
+      last_b += ds;
+#pragma unroll
+      for (int c = 0; c < W / 8; ++c)
+        if (2 * c < m.nb_in[L - 1])
+#pragma unroll
+          for (int j = 0; j < 8; ++j) last_w[8 * c + j] = fmaf(ds, a[8 * c + j], last_w[8 * c + j]);
       linear_t_out1<W>(wl, ds, g, m.nb_in[L - 1]);   // d a[L-1] = ds w
     }
     static_for<L - 1>([&](auto kc) {
@@ -290,7 +310,26 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
   float* out = partial + static_cast<int64_t>(blockIdx.x) * L * NW;
 #pragma unroll
   for (int l = 0; l < L; ++l) {
-    outer_store<W>(acc[l], sg);
+    if (l == L - 1) {
+      // The last layer: the wave's lanes summed by a butterfly, then the
+      // [W x W | W] block with only row 0 and bias 0 nonzero.
+      const int lane = lane_id();
+#pragma unroll
+      for (int i = 0; i < W; ++i)
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) last_w[i] += __shfl_xor(last_w[i], d, 64);
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) last_b += __shfl_xor(last_b, d, 64);
+      for (int idx = lane; idx < NW; idx += 64) sg[idx] = 0.f;
+      wave_lds_sync();
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < W; ++i) sg[i] = last_w[i];
+        sg[W * W] = last_b;
+      }
+    } else {
+      outer_store<W>(acc[l], sg);
+    }
     __syncthreads();
     for (int idx = threadIdx.x; idx < NW; idx += 256)
       out[l * NW + idx] = (stage[idx] + stage[SW + idx]) + (stage[2 * SW + idx] + stage[3 * SW + idx]);

@@ -75,28 +75,23 @@ __device__ __forceinline__ float activate_grad(float z, int act, float p) {
   }
 }
 
-template <typename I>
-__device__ __forceinline__ int64_t seg_row(int role, int64_t e, const I* col,
-                                           const int32_t* dst) {
-  return role == TGX_ROLE_SRC ? static_cast<int64_t>(col[e])
-                              : (role == TGX_ROLE_DST ? static_cast<int64_t>(dst[e]) : e);
-}
-
-// x[k] for k < in_width from the concatenated segments (zero beyond).  The
-// segment loop is compile-time, so each segment's row pointer is a plain
-// per-lane value and every x index is a constant (no indexed register
-// arrays); which columns a segment fills is a uniform range test, made per
-// block of 4 columns first.
-template <typename I, int W>
-__device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const I* col,
-                                              const int32_t* dst, float (&x)[W]) {
+// x[k] for k < in_width from the concatenated segments (zero beyond), the
+// edge's source and destination row ids given.  The segment loop is
+// compile-time, so each segment's row pointer is a plain per-lane value and
+// every x index is a constant (no indexed register arrays); which columns a
+// segment fills is a uniform range test, made per block of 4 columns first.
+template <int W>
+__device__ __forceinline__ void gather_rows(const MlpView& m, int64_t e, int64_t src_row,
+                                            int64_t dst_row, float (&x)[W]) {
 #pragma unroll
   for (int k = 0; k < W; ++k) x[k] = 0.f;
 #pragma unroll
   for (int s = 0; s < kMaxSegments; ++s) {
     if (s >= m.n_seg) break;
     const int off = m.off[s], end = m.off[s] + m.width[s];
-    const float* p = m.ptr[s] + seg_row(m.role[s], e, col, dst) * m.stride[s] - off;
+    const int64_t row =
+        m.role[s] == TGX_ROLE_SRC ? src_row : (m.role[s] == TGX_ROLE_DST ? dst_row : e);
+    const float* p = m.ptr[s] + row * m.stride[s] - off;
 #pragma unroll
     for (int b = 0; b < W; b += 4) {
       if (b + 4 > off && b < end) {
@@ -111,6 +106,20 @@ __device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const
       }
     }
   }
+}
+
+// gather_rows, reading the row ids that the segments use.
+template <typename I, int W>
+__device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const I* col,
+                                              const int32_t* dst, float (&x)[W]) {
+  bool need_src = false, need_dst = false;
+#pragma unroll
+  for (int s = 0; s < kMaxSegments; ++s) {
+    need_src |= s < m.n_seg && m.role[s] == TGX_ROLE_SRC;
+    need_dst |= s < m.n_seg && m.role[s] == TGX_ROLE_DST;
+  }
+  gather_rows<W>(m, e, need_src ? static_cast<int64_t>(col[e]) : 0,
+                 need_dst ? static_cast<int64_t>(dst[e]) : 0, x);
 }
 
 // q_s[e][k - off_s] = g[k] for every segment s (the per-edge input gradient
