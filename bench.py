@@ -963,8 +963,8 @@ def run_nn(args):
                      "traffic": measured_traffic("nn", dominant)[0],
                      "traffic_source": measured_traffic("nn", dominant)[1],
                      "algorithmic_bytes": bytes_per[dominant],
-                     "note": "the edge MLP kernels are latency-bound (fp32 FMAs on LDS-staged "
-                             "weights), far from the HBM roof"},
+                     "note": "the edge MLP kernels are issue- and latency-bound fp32 work "
+                             "(weights in scalar registers), far from the HBM roof"},
         "kernels": {k: {"launches": n, "avg_ms": t / n} for k, (n, t) in sorted(per.items())},
     }
     if not args.no_cpu:
