@@ -181,6 +181,33 @@ def test_score_chains(width, acts, hub):
           dict(graph=graph, src={"a": xs, "v": v}, dst={"b": xd}, edge={"c": ef}), dout)
 
 
+def test_weights_updated_in_place_between_steps():
+    """An optimizer updates the network in place between steps; every launch
+    must read the current weights (the kernels load them through the scalar
+    cache)."""
+    print("nn attention: weights updated in place between steps", flush=True)
+    torch.manual_seed(3)
+    n = 400
+    rp, col = random_graph(n, n, 8, 3)
+    graph = tg.Graph.from_csr(rp, col, num_src=n)
+    x = torch.randn(n, 8, device=DEV, requires_grad=True)
+    disp = torch.randn(col.numel(), 3, device=DEV, requires_grad=True)
+    net = nn.Sequential(nn.Linear(19, 16), nn.ReLU(), nn.Linear(16, 1)).to(DEV)
+    kernel = GAT(net)
+    opt = torch.optim.SGD(list(net.parameters()), lr=0.05)
+    fields = dict(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp})
+    before = [p.detach().clone() for p in net.parameters()]
+    for _ in range(3):
+        opt.zero_grad(set_to_none=True)
+        kernel(**fields).square().sum().backward()
+        opt.step()
+    assert all(not torch.equal(a, p) for a, p in zip(before, net.parameters()))
+    opt.zero_grad(set_to_none=True)
+    x.grad = disp.grad = None
+    dout = torch.randn(n, 8, device=DEV)
+    check(graph, kernel, net, [("edge", disp), ("src", x), ("dst", x)], x, fields, dout)
+
+
 def test_uncovered_networks_fall_back_or_refuse():
     """LayerNorm or widths above 64 are not covered: strict mode refuses,
     otherwise the eager evaluator runs them (reference fail-closed rungs)."""
