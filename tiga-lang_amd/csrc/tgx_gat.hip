@@ -21,9 +21,10 @@
 //   B2 source pass over the transposed CSR (row j = source): recompute
 //      alpha_e = exp(s_e - lse[i]) and dz_e = alpha_e (<dout[i], h[j]> - delta[i])
 //      * LeakyReLU'(z_e); dh[j] = sum alpha_e dout[i] + (sum dz_e) a_src;
-//      dz_e stored at its original edge id; da_src += (sum dz_e) h[j].
+//      dz_e stored at its transposed position (coalesced writes); da_src +=
+//      (sum dz_e) h[j].
 //   B3 destination pass over the CSR: dh[i] += (sum_e dz_e) a_dst and
-//      da_dst += (sum_e dz_e) h[i] from the coalesced dz rows.
+//      da_dst += (sum_e dz_e) h[i], each edge's dz read through inv_perm.
 //   da_* partials are fp64 per wave (static task striding), reduced in a
 //   fixed order, so every output is deterministic.
 #include <hip/hip_runtime.h>
