@@ -406,3 +406,15 @@ def test_edge_mlp_validation_of_layer_widths():
     for good in ((16, 1), (0, 0), (32, 1)):
         m = mlp(good)
         assert lib.tgx_edge_mlp_backward_workspace(0, ctypes.byref(m), ctypes.byref(size)) == 0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message before any
+    GPU work."""
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
