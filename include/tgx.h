@@ -201,6 +201,9 @@ int tgx_plan_reference_buckets(int64_t n_rows, int64_t max_degree,
  * interop/torch/message_passing.py:2903-3345; fp32).
  *   x_dev [n_src, F] fp32, w_dev [n_edges] fp32 or NULL (weight 1),
  *   out_dev [n_dst, F] fp32, fully written.
+ *   col_dev NULL: the columns are the edge ids, i.e. x_dev [n_edges, F] is a
+ *   per-edge field summed per destination row (n_src = n_edges < 2^31; the
+ *   per-edge input gradients of an edge network reduce this way).
  * F may be any positive width; widths that are multiples of 4 with
  * F*4 <= 1024 bytes take the vectorised path. */
 int tgx_csr_sum_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,

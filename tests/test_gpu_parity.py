@@ -168,6 +168,22 @@ def test_sum_unweighted_and_empty_graph():
     assert torch.count_nonzero(o0).item() == 0 and torch.count_nonzero(x0.grad).item() == 0
 
 
+@pytest.mark.parametrize("F_", [8, 3, 64])
+@pytest.mark.parametrize("idx", [torch.int32, torch.int64])
+def test_sum_of_edge_field_per_row(F_, idx):
+    """tgx_csr_sum_fwd without a column array sums a per-edge field per
+    destination row (edge ids as columns), hub rows split into chunks."""
+    from tiga._ops import _reduce_rows
+
+    print(f"edge-field row sums F={F_} {idx}", flush=True)
+    rp, col = skewed_csr(31, 3000, 1000, mean_deg=9, hubs=(6000, 700))
+    E = col.size
+    x = np.random.default_rng(F_).standard_normal((E, F_)).astype(np.float32)
+    graph = tg.Graph.from_csr(to_dev(rp, idx), to_dev(col, idx), num_src=1000)
+    out = _reduce_rows(graph, to_dev(x, torch.float32))
+    assert rel_err(out.cpu(), ref.sum_fwd(rp, np.arange(E), x)) <= RTOL32
+
+
 # ---- GAT additive ----------------------------------------------------------
 
 class GAT(tg.MessagePassing):

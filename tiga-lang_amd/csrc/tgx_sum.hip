@@ -105,7 +105,9 @@ __global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I> a) {
     float my_w = 0.f;
     int my_widx = 0;
     if (lane < n) {
-      my_col = static_cast<int>(a.col[base + lane]);
+      // No column array: the columns are the edge ids (a per-edge field
+      // summed per row, read contiguously).
+      my_col = a.col ? static_cast<int>(a.col[base + lane]) : static_cast<int>(base + lane);
       my_widx = a.wperm ? a.wperm[base + lane] : static_cast<int>(base + lane);
       my_w = a.w ? a.w[my_widx] : 1.f;
     }
@@ -243,7 +245,8 @@ extern "C" int tgx_csr_sum_fwd(const void* row_ptr, const void* col, int idx_bit
   if (st != TGX_OK) return st;
   if (n_dst == 0) return TGX_OK;
   TGX_REQUIRE(row_ptr && out && (x || n_src == 0), "null pointer");
-  // col may be null for a graph without edges (no task reads it then).
+  // A null col means the columns are the edge ids (x holds one row per edge).
+  TGX_REQUIRE(col || n_src < (int64_t{1} << 31), "edge-id columns need fewer than 2^31 edges");
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("csr_sum_fwd", s);

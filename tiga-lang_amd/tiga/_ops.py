@@ -387,7 +387,7 @@ def _reduce_rows(graph: Graph, x: torch.Tensor) -> torch.Tensor:
     if n_dst:
         plan = graph._row_plan()
         partial = _partial(plan, F, x.device)
-        _native.call("tgx_csr_sum_fwd", row_ptr.data_ptr(), graph._edge_iota().data_ptr(),
+        _native.call("tgx_csr_sum_fwd", row_ptr.data_ptr(), None,
                      _native.idx_bits(row_ptr), plan.ref, x.data_ptr(), None, out.data_ptr(),
                      n_dst, E, F, _p(partial), _native.stream_of(x))
     return out

@@ -543,15 +543,6 @@ class Graph:
             self._native_cache["dst32"] = got
         return got
 
-    def _edge_iota(self) -> torch.Tensor:
-        """0..E-1 in the CSR's index dtype: the edge ids as CSR columns."""
-        got = self._native_cache.get("iota")
-        if got is None:
-            row_ptr, col_idx = self._kernel_csr()
-            got = torch.arange(col_idx.numel(), dtype=row_ptr.dtype, device=row_ptr.device)
-            self._native_cache["iota"] = got
-        return got
-
     def _attn_blocks(self):
         """(cu_q, cu_k, causal) of a block-diagonal relation as int32 host
         arrays: cu_seqlens for varlen, one block for dense/triangular."""
