@@ -201,7 +201,9 @@ __device__ __forceinline__ void launder(MlpView& v) {
 // columns: a row tile runs when it holds a real output (o < n_out) and a
 // column tile when it holds a real input (4 nb = n_in rounded up to 4), so
 // one uniform branch skips 64 products with zero padding and the eight
-// weights of a tile row are one scalar load.  Each z[o] is the bias plus
+// weights of a tile row are one scalar load.  Rows go in pairs, the next
+// pair's weights loaded ahead of this pair's FMAs (the scheduling barriers
+// keep the compiler from moving the loads back next to their use).  Each z[o] is the bias plus
 // its products in ascending column order; padded rows get z = 0.  The
 // padding of a column tile beyond n_in multiplies zero weights by the zero
 // (or finite) padded inputs.
@@ -217,11 +219,30 @@ __device__ __forceinline__ void linear(cfloat* wl, const float (&a)[W], float (&
 #pragma unroll
       for (int c = 0; c < W / 8; ++c) {
         if (2 * c < nb) {
+          // Rows in pairs; the next pair's weights are loaded before this
+          // pair's FMAs so the scalar-cache latency overlaps them.
+          float wp[2][2][8];
 #pragma unroll
-          for (int r = 0; r < 8; ++r)
+          for (int r = 0; r < 2; ++r)
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-              z[r0 + r] = fmaf(wl[(r0 + r) * W + 8 * c + j], a[8 * c + j], z[r0 + r]);
+            for (int j = 0; j < 8; ++j) wp[0][r][j] = wl[(r0 + r) * W + 8 * c + j];
+          static_for<4>([&](auto pc) {
+            constexpr int p = decltype(pc)::value;
+            if constexpr (p + 1 < 4) {
+#pragma unroll
+              for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                  wp[(p + 1) & 1][r][j] = wl[(r0 + 2 * p + 2 + r) * W + 8 * c + j];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                z[r0 + 2 * p + r] = fmaf(wp[p & 1][r][j], a[8 * c + j], z[r0 + 2 * p + r]);
+            __builtin_amdgcn_sched_barrier(0);
+          });
         }
       }
     } else {
@@ -245,11 +266,28 @@ __device__ __forceinline__ void linear_t(cfloat* wl, const float (&dz)[W], float
 #pragma unroll
       for (int t = 0; t < W / 8; ++t) {
         if (8 * t < n_out) {
+          float wp[2][2][8];
 #pragma unroll
-          for (int r = 0; r < 8; ++r)
+          for (int r = 0; r < 2; ++r)
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-              g[c0 + j] = fmaf(wl[(8 * t + r) * W + c0 + j], dz[8 * t + r], g[c0 + j]);
+            for (int j = 0; j < 8; ++j) wp[0][r][j] = wl[(8 * t + r) * W + c0 + j];
+          static_for<4>([&](auto pc) {
+            constexpr int p = decltype(pc)::value;
+            if constexpr (p + 1 < 4) {
+#pragma unroll
+              for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                  wp[(p + 1) & 1][r][j] = wl[(8 * t + 2 * p + 2 + r) * W + c0 + j];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                g[c0 + j] = fmaf(wp[p & 1][r][j], dz[8 * t + 2 * p + r], g[c0 + j]);
+            __builtin_amdgcn_sched_barrier(0);
+          });
         }
       }
     }
