@@ -397,7 +397,7 @@ enum { TGX_ROLE_SRC = 0, TGX_ROLE_DST = 1, TGX_ROLE_EDGE = 2 };
  * with an activation after every layer but the last, applied to the
  * concatenation of up to four fp32 input segments gathered per edge (from the
  * source row col[e], the destination row, or edge row e).  Every layer is
- * zero-padded to `width` (16, 32 or 64 >= every layer's in and out size):
+ * zero-padded to `width` (16, 24, 32 or 64 >= every layer's in and out size):
  * weights_dev holds n_layers blocks of [width*width weights (out-major) |
  * width biases]. */
 typedef struct tgx_edge_mlp {

@@ -14,7 +14,7 @@
 // are gathered straight from the field tables (no [E, K] tensor) and its
 // weights, uniform across the wave, are read through the scalar cache into
 // scalar registers that feed the FMAs directly.  Every layer is zero-padded
-// to a common width W (16, 32 or 64) on the host, which keeps every
+// to a common width W (16, 24, 32 or 64) on the host, which keeps every
 // register index compile-time; the real widths bound the loops through
 // uniform branches.  The softmax and the value gather are
 // separate row passes (segment softmax here, the weighted CSR sum of
@@ -48,7 +48,9 @@ using namespace mlp;
 template <int W, int L>
 constexpr int fwd_blocks_per_cu() { return W <= 32 ? (L <= 2 ? 6 : 5) : 3; }
 template <int W, int L>
-constexpr int bwd_blocks_per_cu() { return W == 16 ? 3 : (L <= 2 ? 2 : 1); }
+constexpr int bwd_blocks_per_cu() {
+  return W == 16 ? 3 : W == 24 ? (L <= 2 ? 3 : 2) : (L <= 2 ? 2 : 1);
+}
 
 template <typename I, int W, int L>
 __global__ __launch_bounds__(256, (fwd_blocks_per_cu<W, L>())) void edge_mlp_fwd_kernel(const I* __restrict__ col,
@@ -84,8 +86,10 @@ __global__ __launch_bounds__(256, (fwd_blocks_per_cu<W, L>())) void edge_mlp_fwd
 // The bias gradient (the column sums of G) is summed from the same reads.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Staging row stride: 24-wide layers use the 32-wide MFMA tiles, their
+// columns 24..31 staying zero.
 template <int W>
-constexpr int mlp_ld() { return W + 4; }
+constexpr int mlp_ld() { return (W == 24 ? 32 : W) + 4; }
 
 template <int W>
 struct OuterAcc {
@@ -183,13 +187,15 @@ __device__ __forceinline__ void outer_store(const OuterAcc<W>& acc, float* red) 
     for (int t = 0; t < OuterAcc<W>::kTiles; ++t) {
       const int ro = 32 * (t >> 1), ci = 32 * (t & 1);
 #pragma unroll
-      for (int q = 0; q < 16; ++q)
-        red[(ro + 8 * (q / 4) + 4 * (l / 32) + q % 4) * W + ci + l % 32] = acc.c[t][q];
+      for (int q = 0; q < 16; ++q) {
+        const int o = ro + 8 * (q / 4) + 4 * (l / 32) + q % 4, i = ci + l % 32;
+        if (W != 24 || (o < W && i < W)) red[o * W + i] = acc.c[t][q];
+      }
     }
 #pragma unroll
     for (int t = 0; t < (W == 64 ? 2 : 1); ++t) {
       const float b = acc.b[t] + __shfl_xor(acc.b[t], 32, 64);
-      if (l < 32) red[W * W + 32 * t + l] = b;
+      if (l < (W == 24 ? 24 : 32)) red[W * W + 32 * t + l] = b;
     }
   }
 }
@@ -214,6 +220,11 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
   const int wave = threadIdx.x >> 6;
   float* sg = stage + wave * SW;
   float* sa = sg + 32 * LD;
+  if constexpr (W == 24) {
+    // Staging columns 24..35 are never written by the rounds: zero once.
+    for (int i = threadIdx.x; i < 4 * SW; i += 256) stage[i] = 0.f;
+    __syncthreads();
+  }
   OuterAcc<W> acc[L > 1 ? L - 1 : 1];   // the hidden layers' sums
   float last_w[W];   // this lane's sum of ds a for the last layer, and of ds
   float last_b = 0.f;
@@ -425,8 +436,8 @@ int check_mlp(const tgx_edge_mlp* mlp, MlpView* view, bool need_data) {
   TGX_REQUIRE(mlp, "null mlp");
   TGX_REQUIRE(mlp->n_layers >= 1 && mlp->n_layers <= kMaxLayers, "1 to %d linear layers",
               kMaxLayers);
-  TGX_REQUIRE(mlp->width == 16 || mlp->width == 32 || mlp->width == 64,
-              "padded width must be 16, 32 or 64");
+  TGX_REQUIRE(mlp->width == 16 || mlp->width == 24 || mlp->width == 32 || mlp->width == 64,
+              "padded width must be 16, 24, 32 or 64");
   TGX_REQUIRE(mlp->n_segments >= 1 && mlp->n_segments <= kMaxSegments,
               "1 to %d input segments", kMaxSegments);
   TGX_REQUIRE(mlp->weights_dev, "null weights");
@@ -523,6 +534,8 @@ int64_t bwd_resident_blocks() {
 int64_t resident_blocks(int W, int L) {
   if (W == 16) return L == 1 ? bwd_resident_blocks<16, 1>() : L == 2 ? bwd_resident_blocks<16, 2>()
                                                                        : bwd_resident_blocks<16, 3>();
+  if (W == 24) return L == 1 ? bwd_resident_blocks<24, 1>() : L == 2 ? bwd_resident_blocks<24, 2>()
+                                                                       : bwd_resident_blocks<24, 3>();
   return L == 1 ? bwd_resident_blocks<32, 1>() : L == 2 ? bwd_resident_blocks<32, 2>()
                                                           : bwd_resident_blocks<32, 3>();
 }
@@ -542,6 +555,7 @@ template <typename I>
 void dispatch_fwd(int W, int L, const I* col, const int32_t* dst, int64_t E, const MlpView& v,
                   float* scores, hipStream_t s) {
   if (W == 16) launch_fwd<I, 16>(L, col, dst, E, v, scores, s);
+  if (W == 24) launch_fwd<I, 24>(L, col, dst, E, v, scores, s);
   if (W == 32) launch_fwd<I, 32>(L, col, dst, E, v, scores, s);
   if (W == 64) launch_fwd<I, 64>(L, col, dst, E, v, scores, s);
 }
@@ -551,6 +565,7 @@ void dispatch_bwd(int W, int L, const I* col, const int32_t* dst, int64_t E, int
                   int64_t chunk, const MlpView& v, const float* ds, float* partial,
                   hipStream_t s) {
   if (W == 16) launch_bwd<I, 16>(L, col, dst, E, blocks, chunk, v, ds, partial, s);
+  if (W == 24) launch_bwd<I, 24>(L, col, dst, E, blocks, chunk, v, ds, partial, s);
   if (W == 32) launch_bwd<I, 32>(L, col, dst, E, blocks, chunk, v, ds, partial, s);
 }
 

@@ -269,7 +269,7 @@ _ROLE = {"src": 0, "dst": 1, "edge": 2}
 
 def _padded_width(chain, in_width: int) -> int:
     widest = max([in_width] + [max(l.linear.in_features, l.linear.out_features) for l in chain])
-    return next(w for w in (16, 32, 64) if w >= widest)
+    return next(w for w in (16, 24, 32, 64) if w >= widest)
 
 
 def _mlp_struct(chain, roles, segs, weights_buf, width):
