@@ -142,7 +142,8 @@ def test_reference_gat_example_shape():
 @pytest.mark.parametrize("width,acts,hub", [
     (12, ("tanh",), 0),                       # W = 16, two layers
     (40, ("gelu", "silu"), 300),               # W = 64, three layers, hub row > 64 edges
-    (24, ("elu", "sigmoid"), 0),               # W = 32, three layers
+    (24, ("elu", "sigmoid"), 0),               # W = 24, three layers
+    (30, ("relu",), 0),                        # W = 32, two layers
     (20, (), 0),                               # one Linear: bias-free linear score
 ])
 def test_score_chains(width, acts, hub):
@@ -159,7 +160,7 @@ def test_score_chains(width, acts, hub):
     mods = []
     dims = [14] + [width] * len(acts) + [1]
     names = {"tanh": nn.Tanh, "gelu": nn.GELU, "silu": nn.SiLU, "elu": lambda: nn.ELU(0.7),
-             "sigmoid": nn.Sigmoid}
+             "sigmoid": nn.Sigmoid, "relu": nn.ReLU}
     for i in range(len(dims) - 1):
         mods.append(nn.Linear(dims[i], dims[i + 1], bias=bool(acts) or i > 0))
         if i < len(acts):
