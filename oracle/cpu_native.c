@@ -63,3 +63,40 @@ int tgx_oracle_csr_sum_fwd(const int64_t* row_ptr, const int64_t* col, const flo
   free(ch);
   return 0;
 }
+
+/*
+ * The same runtime's backward of w[e] * x[col[e]] summed per row, as its CPU
+ * lowering emits it (lib/Transforms/LowerTensorToCPU.cpp): the message
+ * gradient dmsg = csr_expand_rows(dout) finds each edge's row with a select
+ * chain over every row (emitCSRExpandRows, :641-670), dx =
+ * segment_sum(dmsg * w, col) scans every edge for every output element
+ * (emitSegmentSum, :608-639), and dw[e] = <dmsg[e], x[col[e]]>.  Sequential
+ * (one thread); O(E * N_dst * F + N_src * E * F).  dmsg_scratch holds
+ * E * F floats.
+ */
+int tgx_oracle_csr_sum_bwd_lowered(const int64_t* row_ptr, const int64_t* col,
+                                   const float* x, const float* w, const float* dout,
+                                   float* dx, float* dw, float* dmsg_scratch,
+                                   int64_t n_dst, int64_t n_src, int64_t F) {
+  const int64_t E = row_ptr[n_dst];
+  for (int64_t e = 0; e < E; ++e)
+    for (int64_t f = 0; f < F; ++f) {
+      int64_t src_row = 0;
+      for (int64_t r = 0; r < n_dst; ++r)
+        src_row = (e >= row_ptr[r] && e < row_ptr[r + 1]) ? r : src_row;
+      dmsg_scratch[e * F + f] = dout[src_row * F + f];
+    }
+  for (int64_t j = 0; j < n_src; ++j)
+    for (int64_t f = 0; f < F; ++f) {
+      float acc = 0.0f;
+      for (int64_t e = 0; e < E; ++e)
+        acc += (col[e] == j) ? dmsg_scratch[e * F + f] * w[e] : 0.0f;
+      dx[j * F + f] = acc;
+    }
+  for (int64_t e = 0; e < E; ++e) {
+    float acc = 0.0f;
+    for (int64_t f = 0; f < F; ++f) acc += dmsg_scratch[e * F + f] * x[col[e] * F + f];
+    dw[e] = acc;
+  }
+  return 0;
+}

@@ -27,6 +27,8 @@ def lib():
         _lib.tgx_oracle_csr_sum_fwd.argtypes = [p, p, p, p, p, ctypes.c_int64, ctypes.c_int64,
                                                 ctypes.c_int]
         _lib.tgx_oracle_csr_sum_fwd.restype = ctypes.c_int
+        _lib.tgx_oracle_csr_sum_bwd_lowered.argtypes = [p] * 8 + [ctypes.c_int64] * 3
+        _lib.tgx_oracle_csr_sum_bwd_lowered.restype = ctypes.c_int
     return _lib
 
 
@@ -47,3 +49,25 @@ def csr_sum_fwd(row_ptr, col_idx, x, w, threads=1, out=None):
     if rc != 0:
         raise RuntimeError(f"tgx_oracle_csr_sum_fwd failed ({rc})")
     return out
+
+
+def csr_sum_bwd_lowered(row_ptr, col_idx, x, w, dout):
+    """(dx, dw) of the weighted sum by the reference runtime's lowered native
+    backward (LowerTensorToCPU.cpp:608-670): a select chain over every row per
+    message element, then a scan over every edge per dx element.  Sequential;
+    only for small graphs (O(E * N * F))."""
+    row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int64)
+    col_idx = np.ascontiguousarray(col_idx, dtype=np.int64)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(np.asarray(w).reshape(-1), dtype=np.float32)
+    dout = np.ascontiguousarray(dout, dtype=np.float32)
+    n_dst, n_src, F = row_ptr.size - 1, x.shape[0], x.shape[1]
+    dx = np.empty((n_src, F), dtype=np.float32)
+    dw = np.empty(col_idx.size, dtype=np.float32)
+    scratch = np.empty((col_idx.size, F), dtype=np.float32)
+    rc = lib().tgx_oracle_csr_sum_bwd_lowered(
+        row_ptr.ctypes.data, col_idx.ctypes.data, x.ctypes.data, w.ctypes.data,
+        dout.ctypes.data, dx.ctypes.data, dw.ctypes.data, scratch.ctypes.data, n_dst, n_src, F)
+    if rc != 0:
+        raise RuntimeError(f"tgx_oracle_csr_sum_bwd_lowered failed ({rc})")
+    return dx, dw

@@ -444,6 +444,30 @@ def test_native_sum_loop_matches_oracle():
         assert np.array_equal(native.csr_sum_fwd(rp, col, x, w, threads=t), one)
 
 
+def test_native_lowered_backward_matches_oracle():
+    """oracle/cpu_native.c's restatement of the reference runtime's lowered
+    backward: the README known answer (dx, dw) exactly and the fp64 oracle
+    within fp32 rounding."""
+    from oracle import native
+
+    g = GOLD["readme_weighted_sum"]
+    x = np.asarray(g["x"], dtype=np.float32).reshape(-1, 1)
+    dout = np.ones((len(g["row_ptr"]) - 1, 1), dtype=np.float32)
+    dx, dw = native.csr_sum_bwd_lowered(g["row_ptr"], g["col_idx"], x, g["weight"], dout)
+    assert dx.reshape(-1).tolist() == g["dx"]
+    assert dw.tolist() == g["dw"]
+    rng = np.random.default_rng(12)
+    rp, col = random_csr(rng, 60, 40, 12)
+    x = rng.standard_normal((40, 5)).astype(np.float32)
+    w = rng.random(col.size).astype(np.float32)
+    dout = rng.standard_normal((60, 5)).astype(np.float32)
+    e_dx, e_dw = ref.sum_bwd(rp, col, x.astype(np.float64), w.astype(np.float64),
+                             dout.astype(np.float64))
+    dx, dw = native.csr_sum_bwd_lowered(rp, col, x, w, dout)
+    np.testing.assert_allclose(dx, e_dx, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(dw, np.asarray(e_dw).reshape(-1), rtol=1e-5, atol=1e-5)
+
+
 def test_eager_torch_cpu_path_matches_oracle():
     """oracle/eager_torch.py (the reference's eager Torch CPU path) agrees
     with the pinned fp64 oracle for the sum, GAT and dot-product steps."""
