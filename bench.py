@@ -995,6 +995,17 @@ def run_nn(args):
 ARGS = None
 
 
+def cpu_model():
+    """The host CPU's model name (the CPU baselines' hardware)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def measured_roofs(samples=10):
     """In-run roof calibration, as the reference's benchmarks measure theirs
     (benchmarks/common/hardware_roofline.py:102-120): the bytes read plus
@@ -1053,6 +1064,8 @@ def main():
                "dense": run_dense, "dense-causal": run_dense, "dense-pruned": run_dense,
                "nn": run_nn}
     result = runners[args.config](args)
+    if isinstance(result.get("cpu_baseline"), dict):
+        result["cpu_baseline"]["cpu_model"] = cpu_model()
     roofs = measured_roofs()
     result["measured_roofs"] = roofs
     rl = result.get("roofline")
