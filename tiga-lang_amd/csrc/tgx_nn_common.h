@@ -148,9 +148,8 @@ __device__ __forceinline__ void scatter_segments(const MlpView& m, int64_t e, co
 }
 
 // Keeps v's computation at this point of the program.  Without it the
-// optimizer sinks each dot product to its first use, behind the uniform
-// branches of the activation that follows, i.e. after every weight load of
-// the layer, and all W*W weights of the layer end up live at once.
+// optimizer sinks each value to its first use, past the uniform branches and
+// weight loads in between, and the operands it needs stay live that long.
 __device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
 
 // f(integral_constant<0>) ... f(integral_constant<N-1>): a loop whose index
