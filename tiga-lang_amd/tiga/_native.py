@@ -168,9 +168,13 @@ def ptr(tensor) -> int | None:
 
 
 def stream_of(tensor) -> int:
+    """Torch's current stream on the tensor's device (a raw hipStream_t)."""
     import torch
 
-    return torch.cuda.current_stream(tensor.device).cuda_stream
+    index = tensor.device.index
+    if index is None:
+        index = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def idx_bits(tensor) -> int:

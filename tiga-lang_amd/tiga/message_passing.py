@@ -18,6 +18,7 @@ ran.  Setting ``tiga.config.strict = True`` turns that fallback into an error.
 
 from __future__ import annotations
 
+import functools
 import inspect
 from collections.abc import Mapping
 from types import SimpleNamespace
@@ -39,12 +40,19 @@ class _Config:
 config = _Config()
 
 
-def _call_region(method, positional: tuple, params: Mapping[str, Any]):
-    signature = inspect.signature(method)
+@functools.lru_cache(maxsize=512)
+def _parameter_names(function) -> tuple[bool, frozenset]:
+    """(takes **kwargs, parameter names) of a function, computed once."""
+    signature = inspect.signature(function)
     accepts_rest = any(p.kind is inspect.Parameter.VAR_KEYWORD
                        for p in signature.parameters.values())
+    return accepts_rest, frozenset(signature.parameters)
+
+
+def _call_region(method, positional: tuple, params: Mapping[str, Any]):
+    accepts_rest, names = _parameter_names(getattr(method, "__func__", method))
     selected = params if accepts_rest else {
-        name: value for name, value in params.items() if name in signature.parameters}
+        name: value for name, value in params.items() if name in names}
     return method(*positional, **selected)
 
 
@@ -152,12 +160,21 @@ class MessagePassing(Kernel):
     # ------------------------------------------------------------------
     def _record_native(self, graph, pattern: str, entry_points, lowering, remarks=()):
         plan = graph._native_cache.get(("plan", 512, 512))
-        extra = () if plan is None else (f"row plan: {plan.counts()}",)
-        self._record_variant(CompiledVariant(
-            key=(type(self).__qualname__, pattern, graph.planning_key()),
-            backend="hip", provider="libtgx_hip.so (gfx950)", pattern=pattern,
-            lowering=lowering, entry_points=tuple(entry_points),
-            remarks=tuple(remarks) + extra))
+        # The record of a (kernel, pattern) on this graph is built once and
+        # kept with the graph's other per-graph structures.
+        memo = graph._native_cache.setdefault("variants", {})
+        memo_key = (type(self).__qualname__, plan is not None, pattern, tuple(entry_points),
+                    lowering, tuple(remarks))
+        variant = memo.get(memo_key)
+        if variant is None:
+            extra = () if plan is None else (f"row plan: {plan.counts()}",)
+            variant = CompiledVariant(
+                key=(type(self).__qualname__, pattern, graph.planning_key()),
+                backend="hip", provider="libtgx_hip.so (gfx950)", pattern=pattern,
+                lowering=lowering, entry_points=tuple(entry_points),
+                remarks=tuple(remarks) + extra)
+            memo[memo_key] = variant
+        self._record_variant(variant)
 
     def _execute_native(self, captured, graph, src, dst, edge, params):
         from . import _ops
