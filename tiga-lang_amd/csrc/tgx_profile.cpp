@@ -28,6 +28,8 @@ struct Totals {
   double ms = 0.0;
 };
 
+constexpr size_t kEventReserve = 2048;   // start + stop of 1024 launches
+
 std::atomic<bool> g_enabled{false};
 std::mutex g_mu;
 std::vector<Pending> g_pending;
@@ -70,6 +72,14 @@ using namespace tgx;
 extern "C" int tgx_profile_begin(void) {
   std::lock_guard<std::mutex> lock(g_mu);
   g_totals.clear();
+  // Events are created here, not at the first launches of the profiled
+  // region: hipEventCreate inside a timed loop would add its cost to every
+  // launch it times.
+  while (g_pool.size() < kEventReserve) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) break;
+    g_pool.push_back(e);
+  }
   g_enabled.store(true);
   return TGX_OK;
 }
