@@ -32,6 +32,7 @@
 // deterministic and nothing per layer and edge goes to HBM.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "tgx_nn_common.h"
@@ -506,10 +507,12 @@ void launch_fwd(int L, const I* col, const int32_t* dst, int64_t E, const MlpVie
 // and the runtime's occupancy query.
 template <int W, int L>
 int64_t bwd_resident_blocks() {
-  static int64_t cached[64] = {};
+  // Per device, computed once; concurrent first calls compute the same value.
+  static std::atomic<int64_t> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
+  int64_t known = cached[dev].load(std::memory_order_relaxed);
+  if (known == 0) {
     const void* fn = reinterpret_cast<const void*>(edge_mlp_bwd_kernel<int64_t, W, L>);
     int per_cu = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess)
@@ -526,9 +529,10 @@ int64_t bwd_resident_blocks() {
     }
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       cus = 256;
-    cached[dev] = static_cast<int64_t>(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    known = static_cast<int64_t>(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    cached[dev].store(known, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return known;
 }
 
 int64_t resident_blocks(int W, int L) {
