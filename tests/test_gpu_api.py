@@ -1,0 +1,237 @@
+"""GPU tests of the call forms around the HIP launches: field validation
+before any launch, ``ndata=``, ``prepare()`` and the guarded warm-call cache
+(every warm or prepared result bit-identical to a cold call), and the
+reference planner report in ``explain()``."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import tiga as tg
+from tiga import _native
+
+from graphs import skewed_csr
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+@pytest.fixture(autouse=True)
+def _strict():
+    tg.config.strict = True
+    yield
+    tg.config.strict = False
+
+
+class WeightedSum(tg.MessagePassing):
+    reducer = tg.sum()
+
+    def edge(self, src, dst, edge):
+        return edge.w * src.x
+
+
+class Dot(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge, scale):
+        return self.reducer((src.k * dst.q).sum(dim=-1) * scale + edge.b, src.v)
+
+
+class GatParams(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge, a_src, a_dst):
+        s = F.leaky_relu((src.h * a_src).sum(-1) + (dst.h * a_dst).sum(-1), 0.2)
+        return self.reducer(s, src.h)
+
+
+def _graph(seed=0, n=3000, hubs=(900,), idx=torch.int64):
+    rp, col = skewed_csr(seed, n, n, mean_deg=7, hubs=hubs)
+    return tg.Graph.from_csr(torch.tensor(rp, device=DEV, dtype=idx),
+                             torch.tensor(col, device=DEV, dtype=idx), num_src=n)
+
+
+def test_host_edge_fields_are_rejected_before_any_launch():
+    print("host edge fields", flush=True)
+    g = _graph(1)
+    x = torch.randn(3000, 8, device=DEV)
+    with pytest.raises(ValueError, match="edge.w is on cpu"):
+        WeightedSum()(graph=g, src={"x": x}, dst={}, edge={"w": torch.rand(g.num_edges)})
+    q = torch.randn(3000, 2, 64, device=DEV).to(torch.bfloat16)
+    with pytest.raises(ValueError, match="edge.b is on cpu"):
+        Dot()(graph=g, src={"k": q, "v": q}, dst={"q": q},
+              edge={"b": torch.randn(g.num_edges, 2)}, scale=0.125)
+    with pytest.raises(ValueError, match="leading dimension"):
+        WeightedSum()(graph=g, src={"x": x}, dst={},
+                      edge={"w": torch.rand(g.num_edges + 1, device=DEV)})
+    torch.cuda.synchronize()
+
+
+def test_nn_score_width_mismatch_is_not_launched():
+    print("nn width mismatch", flush=True)
+    g = _graph(2)
+    net = torch.nn.Sequential(torch.nn.Linear(5, 8), torch.nn.ReLU(),
+                              torch.nn.Linear(8, 1)).to(DEV)
+
+    class NnAttn(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            return self.reducer(tg.nn.trace(net)(src.p, dst.p), src.v)
+
+    p = torch.randn(3000, 3, device=DEV)    # 3 + 3 inputs for a 5-wide network
+    v = torch.randn(3000, 4, device=DEV)
+    tg.config.strict = False
+    with pytest.raises(RuntimeError):
+        NnAttn()(graph=g, src={"p": p, "v": v}, dst={"p": p})
+
+
+def test_ndata_equals_src_dst_on_the_hip_path():
+    print("ndata", flush=True)
+    g = _graph(3)
+    h = torch.randn(3000, 4, 32, device=DEV)
+    a_s = 0.1 * torch.randn(4, 32, device=DEV)
+    a_d = 0.1 * torch.randn(4, 32, device=DEV)
+    k = GatParams()
+    a = k(graph=g, ndata={"h": h}, a_src=a_s, a_dst=a_d)
+    assert k.last_variant.backend == "hip"
+    b = GatParams()(graph=g, src={"h": h}, dst={"h": h}, a_src=a_s, a_dst=a_d)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("idx", [torch.int32, torch.int64])
+def test_warm_calls_hit_the_guarded_launch_and_match_cold_calls(idx):
+    print(f"guarded weighted sum {idx}", flush=True)
+    g = _graph(4, idx=idx)
+    x = torch.randn(3000, 16, device=DEV, requires_grad=True)
+    w = torch.rand(g.num_edges, 1, device=DEV, requires_grad=True)
+    k = WeightedSum()
+    outs, grads = [], []
+    for _ in range(3):
+        x.grad = w.grad = None
+        out = k(graph=g, src={"x": x}, dst={}, edge={"w": w})
+        out.backward(torch.ones_like(out))
+        outs.append(out.detach())
+        grads.append((x.grad.clone(), w.grad.clone()))
+    assert k.cache_info["misses"] == 1 and k.cache_info["hits"] == 2
+    assert k.last_variant.backend == "hip"
+    cold = WeightedSum()(graph=g, src={"x": x}, dst={}, edge={"w": w})
+    for o, (gx, gw) in zip(outs, grads):
+        assert torch.equal(o, cold.detach())
+        assert torch.equal(gx, grads[0][0]) and torch.equal(gw, grads[0][1])
+    # a different shape, dtype-preserving: the guard misses, the result is right
+    x2 = torch.randn(3000, 8, device=DEV)
+    out2 = k(graph=g, src={"x": x2}, dst={}, edge={"w": w})
+    assert k.cache_info["misses"] == 2
+    assert torch.equal(out2, WeightedSum()(graph=g, src={"x": x2}, dst={}, edge={"w": w}))
+    # a different graph object misses too
+    g2 = _graph(4, idx=idx)
+    k(graph=g2, src={"x": x2}, dst={}, edge={"w": w})
+    assert k.cache_info["misses"] == 3
+
+
+def test_tensor_parameters_are_read_from_each_warm_call():
+    print("guarded gat params", flush=True)
+    g = _graph(5)
+    h = torch.randn(3000, 4, 32, device=DEV)
+    a_s = 0.1 * torch.randn(4, 32, device=DEV)
+    a_d = 0.1 * torch.randn(4, 32, device=DEV)
+    k = GatParams()
+    first = k(graph=g, src={"h": h}, dst={"h": h}, a_src=a_s, a_dst=a_d)
+    a_s2 = 0.1 * torch.randn(4, 32, device=DEV)
+    warm = k(graph=g, src={"h": h}, dst={"h": h}, a_src=a_s2, a_dst=a_d)
+    assert k.cache_info["hits"] == 1
+    cold = GatParams()(graph=g, src={"h": h}, dst={"h": h}, a_src=a_s2, a_dst=a_d)
+    assert torch.equal(warm, cold) and not torch.equal(warm, first)
+    # a scalar parameter baked into the capture: a new value is a cold call
+    kd = Dot()
+    q = torch.randn(3000, 2, 64, device=DEV).to(torch.bfloat16)
+    b = torch.randn(g.num_edges, 2, device=DEV)
+    o1 = kd(graph=g, src={"k": q, "v": q}, dst={"q": q}, edge={"b": b}, scale=0.125)
+    o2 = kd(graph=g, src={"k": q, "v": q}, dst={"q": q}, edge={"b": b}, scale=0.25)
+    assert kd.cache_info == {"hits": 0, "misses": 2, "variants": 1}
+    assert torch.equal(o2, Dot()(graph=g, src={"k": q, "v": q}, dst={"q": q}, edge={"b": b},
+                                 scale=0.25))
+    assert not torch.equal(o1, o2)
+
+
+def test_closure_tensors_are_recaptured_every_call():
+    print("closure tensors", flush=True)
+    g = _graph(6)
+    h = torch.randn(3000, 4, 32, device=DEV)
+    holder = {"a": 0.1 * torch.randn(4, 32, device=DEV)}
+
+    class Gat(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            s = F.leaky_relu((src.h * holder["a"]).sum(-1) + (dst.h * holder["a"]).sum(-1))
+            return self.reducer(s, src.h)
+
+    k = Gat()
+    first = k(graph=g, src={"h": h}, dst={"h": h})
+    holder["a"] = 0.1 * torch.randn(4, 32, device=DEV)
+    second = k(graph=g, src={"h": h}, dst={"h": h})
+    assert k.cache_info["hits"] == 0
+    a = holder["a"]
+
+    class GatFixed(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            s = F.leaky_relu((src.h * a).sum(-1) + (dst.h * a).sum(-1))
+            return self.reducer(s, src.h)
+
+    assert torch.equal(second, GatFixed()(graph=g, src={"h": h}, dst={"h": h}))
+    assert not torch.equal(first, second)
+
+
+def test_prepare_is_bit_identical_and_sees_in_place_updates():
+    print("prepare", flush=True)
+    g = _graph(7)
+    x = torch.randn(3000, 16, device=DEV)
+    w = torch.rand(g.num_edges, device=DEV)
+
+    class Shifted(WeightedSum):
+        def node(self, dst, aggregate, shift):
+            return aggregate + shift
+
+    k = Shifted()
+    launch = k.prepare(graph=g, src={"x": x}, dst={}, edge={"w": w}, shift=2.0)
+    assert launch.variant.backend == "hip" and launch.graph is g
+    eager = Shifted()(graph=g, src={"x": x}, dst={}, edge={"w": w}, shift=2.0)
+    assert torch.equal(launch(), eager)
+    x.mul_(3.0)
+    again = launch()
+    assert torch.equal(again, Shifted()(graph=g, src={"x": x}, dst={}, edge={"w": w},
+                                        shift=2.0))
+    assert not torch.equal(again, eager)
+    # nn-scored attention (operands from outside the call) can still be prepared
+    net = torch.nn.Sequential(torch.nn.Linear(6, 16), torch.nn.Tanh(),
+                              torch.nn.Linear(16, 1)).to(DEV)
+
+    class NnAttn(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            return self.reducer(tg.nn.trace(net)(src.p, dst.p), src.v)
+
+    p = torch.randn(3000, 3, device=DEV)
+    v = torch.randn(3000, 4, device=DEV)
+    kn = NnAttn()
+    run = kn.prepare(graph=g, src={"p": p, "v": v}, dst={"p": p})
+    assert torch.equal(run(), NnAttn()(graph=g, src={"p": p, "v": v}, dst={"p": p}))
+
+
+def test_explain_reports_the_row_plan_and_the_reference_planner():
+    print("explain", flush=True)
+    g = _graph(8, hubs=(900, 120))
+    x = torch.randn(3000, 4, device=DEV)
+    w = torch.rand(g.num_edges, device=DEV)
+    k = WeightedSum()
+    k(graph=g, src={"x": x}, dst={}, edge={"w": w})
+    text = k.explain()
+    assert "row plan:" in text
+    assert "reference planner: high-degree-tail-chunked" in text, text
+    assert "reference planner" in g.explain()

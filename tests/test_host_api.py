@@ -1,0 +1,183 @@
+"""CPU tests of the user-facing API added on top of the call form: ``ndata=``,
+``prepare()``, the guarded warm-call cache's bookkeeping, the degree
+statistics, ``planning_key``, the materialized ``Graph.cat`` and the
+reference planner report.  Everything here runs on CPU tensors (the eager
+evaluator) and the host-only parts of the C ABI."""
+
+import numpy as np
+import pytest
+import torch
+
+import tiga as tg
+from oracle import planner, ref
+
+from graphs import skewed_csr
+
+
+class WeightedSum(tg.MessagePassing):
+    reducer = tg.sum()
+
+    def edge(self, src, dst, edge):
+        return edge.w * src.x
+
+
+def _graph(seed=0, n_dst=40, n_src=40, **kw):
+    rp, col = skewed_csr(seed, n_dst, n_src, **kw)
+    return tg.Graph.from_csr(torch.tensor(rp), torch.tensor(col), num_src=n_src), rp, col
+
+
+def test_ndata_binds_both_roles_on_a_homogeneous_graph():
+    g, rp, col = _graph(1)
+    x = torch.randn(40, 3, dtype=torch.float64)
+    w = torch.rand(g.num_edges, 1, dtype=torch.float64)
+
+    class Mix(tg.MessagePassing):
+        reducer = tg.sum()
+
+        def edge(self, src, dst, edge):
+            return edge.w * (src.x - dst.x)
+
+    k = Mix()
+    a = k(graph=g, ndata={"x": x}, edge={"w": w})
+    b = k(graph=g, src={"x": x}, dst={"x": x}, edge={"w": w})
+    assert torch.equal(a, b)
+    dst_idx = ref.destination_index(rp)
+    want = np.zeros((40, 3))
+    np.add.at(want, dst_idx, w.numpy() * (x.numpy()[col] - x.numpy()[dst_idx]))
+    assert np.allclose(a.numpy(), want, rtol=1e-12, atol=1e-12)
+
+
+def test_ndata_errors_follow_the_reference():
+    g, _, _ = _graph(2)
+    x = torch.randn(40, 2)
+    with pytest.raises(TypeError, match="cannot be combined"):
+        WeightedSum()(graph=g, ndata={"x": x}, src={"x": x}, edge={})
+    with pytest.raises(TypeError, match="requires ndata= or both"):
+        WeightedSum()(graph=g, src={"x": x})
+    bip, _, _ = _graph(3, n_dst=30, n_src=40)
+    with pytest.raises(ValueError, match="homogeneous"):
+        WeightedSum()(graph=bip, ndata={"x": x})
+
+
+def test_prepare_requires_a_hip_launch():
+    g, _, _ = _graph(4)
+    x = torch.randn(40, 2)
+    w = torch.rand(g.num_edges)
+    with pytest.raises(NotImplementedError, match="torch-eager"):
+        WeightedSum().prepare(graph=g, src={"x": x}, dst={}, edge={"w": w[:, None]})
+
+
+def test_cache_info_counts_cold_calls_on_the_eager_path():
+    g, _, _ = _graph(5)
+    x = torch.randn(40, 2)
+    w = torch.rand(g.num_edges, 1)
+    k = WeightedSum()
+    for _ in range(3):
+        k(graph=g, src={"x": x}, dst={}, edge={"w": w})
+    info = k.cache_info
+    assert info == {"hits": 0, "misses": 3, "variants": 1}
+    assert "variant cache: hits=0, misses=3" in k.explain()
+    with pytest.raises(KeyError):
+        k.last_variant.code("ptx")
+
+
+def test_degree_statistics_histogram_and_span_ratio_against_brute_force():
+    g, rp, col = _graph(6, n_dst=300, n_src=250, hubs=(90, 70))
+    deg = np.diff(rp)
+    assert g.degree_bounds() == (int(deg.min()), int(deg.max()))
+    assert g.degree_statistics() == (int(deg.min()), int(deg.max()), int(deg.sum()))
+    hist = g.degree_histogram()
+    assert isinstance(hist, tuple)
+    assert list(hist) == np.bincount(deg, minlength=deg.max() + 1).tolist()
+    # span ratio: mean |col - row| over evenly spaced slots, normalised
+    E = col.size
+    count = min(4096, E)
+    slots = np.floor(np.arange(count) * ((E - 1) / (count - 1))).astype(np.int64)
+    rows = np.searchsorted(rp[1:], slots, side="right")
+    want = np.abs(col[slots] - rows).mean() / max(1, 250, 300)
+    assert abs(g.source_index_span_ratio() - want) < 1e-12
+    # a ring relation (col = row) is perfectly local
+    ring = tg.Graph.from_csr(torch.arange(11), torch.arange(10), num_src=10)
+    assert ring.source_index_span_ratio() == 0.0
+
+
+def test_degree_statistics_of_implicit_relations_are_closed_forms():
+    tri = tg.Graph.triangular(7)
+    assert tri.degree_statistics() == (1, 7, 28)
+    assert tri.degree_histogram() == (0, 1, 1, 1, 1, 1, 1, 1)
+    dense = tg.Graph.dense(5, 3)
+    assert dense.degree_statistics() == (5, 5, 15)
+    assert dense.degree_histogram() == (0, 0, 0, 0, 0, 3)
+    cu = torch.tensor([0, 3, 3, 7])
+    var = tg.Graph.cu_seqlens(cu, causal=True)
+    assert var.degree_statistics() == (1, 4, 6 + 10)
+    assert var.degree_histogram() == (0, 2, 2, 2, 1)
+    full = tg.Graph.cu_seqlens(cu, causal=False)
+    assert full.degree_statistics() == (3, 4, 9 + 16)
+    assert full.degree_histogram() == (0, 0, 0, 3, 4)
+    # the implicit statistics equal those of the materialized CSR
+    rp, _ = ref.cu_seqlens_csr(cu.numpy(), causal=True)
+    deg = np.diff(rp)
+    assert var.degree_statistics() == (int(deg.min()), int(deg.max()), int(deg.sum()))
+
+
+def test_degree_histogram_limit():
+    rp = torch.tensor([0, 5000])
+    g = tg.Graph.from_csr(rp, torch.zeros(5000, dtype=torch.int64), num_src=1)
+    with pytest.raises(ValueError, match="4096"):
+        g.degree_histogram()
+
+
+def test_planning_key_carries_degree_statistics_and_locality():
+    g, rp, _ = _graph(7)
+    key = g.planning_key()
+    deg = np.diff(rp)
+    assert (int(deg.min()), int(deg.max()), int(deg.sum())) in key
+    assert g.source_index_span_ratio() in key
+    assert key == g.planning_key()
+    other, _, _ = _graph(8)
+    assert other.planning_key() != key
+
+
+def test_materialized_cat_matches_block_diagonal_brute_force():
+    blocks, shift_e, shift_s = [], 0, 0
+    want_rp, want_col = [0], []
+    for seed, (nd, ns) in enumerate([(5, 7), (0, 3), (9, 4), (6, 6)]):
+        rp, col = skewed_csr(seed + 20, nd, ns, mean_deg=3)
+        blocks.append(tg.Graph.from_csr(torch.tensor(rp, dtype=torch.int32),
+                                        torch.tensor(col, dtype=torch.int32), num_src=ns))
+        want_rp += (rp[1:] + shift_e).tolist()
+        want_col += (col + shift_s).tolist()
+        shift_e += int(rp[-1])
+        shift_s += ns
+    g = tg.Graph.cat(blocks)
+    rp, col = g.resolve_csr()
+    assert rp.dtype == torch.int32
+    assert rp.tolist() == want_rp and col.tolist() == want_col
+    assert g.schema.num_src == shift_s and g.schema.num_dst == 20
+
+
+@pytest.mark.parametrize("case", [
+    dict(seed=0, n_dst=128, n_src=128, mean_deg=16, empty_frac=0.0),       # regular
+    dict(seed=1, n_dst=512, n_src=600, mean_deg=4, hubs=(300, 200, 90)),  # power law
+    dict(seed=2, n_dst=100, n_src=100, mean_deg=40, empty_frac=0.7),       # padding-poor
+])
+@pytest.mark.parametrize("has_node", [False, True])
+def test_reference_plan_of_a_graph_matches_the_oracle_planner(case, has_node):
+    rp, col = skewed_csr(**case)
+    g = tg.Graph.from_csr(torch.tensor(rp), torch.tensor(col), num_src=case["n_src"])
+    deg = np.diff(rp)
+    hist = np.bincount(deg, minlength=deg.max() + 1).tolist()
+    want = planner.plan(len(deg), int(deg.max()), int(deg.sum()), hist, has_node)
+    got = g.reference_plan(has_node)
+    for key, value in want.items():
+        assert got[key] == value, key
+    assert got["plan"] in tg.graph.describe_reference_plan(got)
+
+
+def test_reference_plan_defers_above_the_histogram_limit():
+    deg = np.array([5000, 3, 2, 0])
+    rp = np.concatenate([[0], np.cumsum(deg)])
+    g = tg.Graph.from_csr(torch.tensor(rp), torch.zeros(int(rp[-1]), dtype=torch.int64),
+                          num_src=1)
+    assert g.reference_plan()["plan"] == "provider-deferred-high-degree"

@@ -638,34 +638,37 @@ extern "C" int tgx_plan_split_chunks(const void* row_ptr, int idx_bits,
         static_cast<const int64_t*>(row_ptr), split_rows, n_split, chunk_edges,
         chunk_offsets);
   TGX_LAUNCHED("split_count_kernel");
-  // The scan needs scratch only above one tile; n_split above 4096 uses the
-  // tail of chunk_offsets' own allocation is not allowed, so scan in place
-  // by tiles with a small host-driven carry when needed.
+  // Up to one scan tile of split rows the device scan needs no scratch and
+  // writes the total in place.  Above that (this call has no workspace
+  // argument) the per-row counts come to the host, are scanned there and go
+  // back; the host buffer lives until the stream has finished both copies.
   if (n_split <= kScanTile) {
     int st = scan_exclusive_i32(chunk_offsets, chunk_offsets, n_split,
                                 chunk_offsets + n_split, nullptr, s);
     if (st != TGX_OK) return st;
-  } else {
-    std::vector<int32_t> host(n_split + 1);
-    TGX_HIP(hipMemcpyAsync(host.data(), chunk_offsets, sizeof(int32_t) * n_split,
+    int32_t total = 0;
+    TGX_HIP(hipMemcpyAsync(&total, chunk_offsets + n_split, sizeof(int32_t),
                            hipMemcpyDeviceToHost, s));
     TGX_HIP(hipStreamSynchronize(s));
-    int64_t run = 0;
-    for (int64_t k = 0; k < n_split; ++k) {
-      int32_t v = host[k];
-      host[k] = static_cast<int32_t>(run);
-      run += v;
-    }
-    TGX_REQUIRE(run <= INT32_MAX, "chunk count overflows int32");
-    host[n_split] = static_cast<int32_t>(run);
-    TGX_HIP(hipMemcpyAsync(chunk_offsets, host.data(), sizeof(int32_t) * (n_split + 1),
-                           hipMemcpyHostToDevice, s));
+    *n_chunks_host = total;
+    return TGX_OK;
   }
-  int32_t total = 0;
-  TGX_HIP(hipMemcpyAsync(&total, chunk_offsets + n_split, sizeof(int32_t),
+  std::vector<int32_t> host(n_split + 1);
+  TGX_HIP(hipMemcpyAsync(host.data(), chunk_offsets, sizeof(int32_t) * n_split,
                          hipMemcpyDeviceToHost, s));
   TGX_HIP(hipStreamSynchronize(s));
-  *n_chunks_host = total;
+  int64_t run = 0;
+  for (int64_t k = 0; k < n_split; ++k) {
+    const int32_t v = host[k];
+    host[k] = static_cast<int32_t>(run);
+    run += v;
+  }
+  TGX_REQUIRE(run <= INT32_MAX, "chunk count overflows int32");
+  host[n_split] = static_cast<int32_t>(run);
+  TGX_HIP(hipMemcpyAsync(chunk_offsets, host.data(), sizeof(int32_t) * (n_split + 1),
+                         hipMemcpyHostToDevice, s));
+  TGX_HIP(hipStreamSynchronize(s));
+  *n_chunks_host = run;
   return TGX_OK;
 }
 

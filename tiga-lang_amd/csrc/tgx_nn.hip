@@ -504,7 +504,10 @@ void launch_fwd(int L, const I* col, const int32_t* dst, int64_t E, const MlpVie
 // device at once: per CU, the smaller of what the 160 KB of LDS and the 512
 // registers per SIMD lane allow (each 256-thread block puts one wave on each
 // of the CU's four SIMDs), from the kernel's attributes; the larger of that
-// and the runtime's occupancy query.
+// and the runtime's occupancy query.  The int64 instance sizes int32 launches
+// too: the workspace query has no index width, and it must size the partial
+// buffer for the same grid the launch uses.  No block waits for another, so a
+// grid larger than what is resident only costs a second round of blocks.
 template <int W, int L>
 int64_t bwd_resident_blocks() {
   // Per device, computed once; concurrent first calls compute the same value.

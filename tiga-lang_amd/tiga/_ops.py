@@ -28,11 +28,21 @@ def _p(t):
     return None if t is None else t.data_ptr()
 
 
+def _on_graph_device(graph: Graph, *tensors) -> None:
+    """Every operand of a launch must live on the graph's device: the kernels
+    dereference raw pointers, and a host pointer would fault the GPU."""
+    device = graph.device
+    for t in tensors:
+        if t is not None and t.device != device:
+            raise ValueError(f"operand on {t.device} for a graph on {device}")
+
+
 class CsrSumFunction(torch.autograd.Function):
     """out[i] = sum_e w[e] * x[col[e]]  (w optional), fp32."""
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, w: torch.Tensor | None, graph: Graph):
+        _on_graph_device(graph, x, w)
         row_ptr, col_idx = graph._kernel_csr()
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
         feat_shape = tuple(x.shape[1:])
@@ -85,6 +95,7 @@ class GatFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h: torch.Tensor, a_src: torch.Tensor, a_dst: torch.Tensor,
                 slope: float, graph: Graph):
+        _on_graph_device(graph, h, a_src, a_dst)
         row_ptr, col_idx = graph._kernel_csr()
         N, H, D = h.shape
         hc = h.contiguous()
@@ -140,6 +151,7 @@ class DotAttnFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, bias, scale: float, graph: Graph):
+        _on_graph_device(graph, q, k, v, bias)
         row_ptr, col_idx = graph._kernel_csr()
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
         _, H, D = q.shape
@@ -217,6 +229,7 @@ class BlockAttentionFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, scale: float, prune: float, graph: Graph):
+        _on_graph_device(graph, q, k, v)
         n_q, H, D = q.shape
         n_k = k.shape[0]
         q, k, v, strides = attn_strides(q, k, v)
@@ -308,6 +321,7 @@ class EdgeMlpFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, graph: Graph, chain, roles, n_seg: int, *tensors):
+        _on_graph_device(graph, *tensors)
         segs = [_as_rows(t) for t in tensors[:n_seg]]
         params = tensors[n_seg:]
         row_ptr, col_idx = graph._kernel_csr()
@@ -412,6 +426,7 @@ class SegmentSoftmaxFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, scores: torch.Tensor, graph: Graph):
+        _on_graph_device(graph, scores)
         row_ptr, _ = graph._kernel_csr()
         n = graph.schema.num_dst
         alpha = torch.empty_like(scores)

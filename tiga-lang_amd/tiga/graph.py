@@ -4,7 +4,7 @@ Public constructors and queries mirror the reference Torch graph
 (python/tiga/interop/torch/graph.py): ``from_csr`` 153-190 (validation
 595-617), ``from_coo`` 193-231, ``regular`` 233-257, ``cu_seqlens`` 260-294,
 ``cat`` 297-340, ``transpose`` 675-685, ``destination_index`` 1212-1222,
-``degree_bounds`` 1224-1245.
+degree statistics and ``planning_key`` 1224-1351.
 
 On top of that, a graph caches the device-side structures the HIP kernels
 need, built once per graph by the native planner (one host sync each):
@@ -153,6 +153,60 @@ def build_varlen_csr(cu_seqlens: torch.Tensor, causal: bool, total: int, n_edges
                  n_seq, total, n_edges, int(causal), row_ptr.data_ptr(), col.data_ptr(),
                  ws.data_ptr(), ws_bytes.value, _native.stream_of(cu_seqlens))
     return row_ptr, col[:n_edges]
+
+
+_PLAN_NAMES = ("row-neighbor-tile", "degree-bucketing-required", "high-degree-tail-split",
+               "provider-deferred-high-degree", "bounded-row-preferred",
+               "high-degree-tail-chunked", "high-degree-tail-split-rows")
+_MAPPING_NAMES = ("worklist", "direct-filter", "worklist-chunked")
+
+
+def reference_plan(n_rows: int, max_degree: int, degree_sum: int, histogram=None,
+                   has_node_epilogue: bool = False) -> dict:
+    """The reference's load-balance decision for a CSR with these degree
+    statistics (native ``tgx_plan_reference_buckets``)."""
+    hist = None
+    if histogram is not None:
+        hist = (ctypes.c_int64 * len(histogram))(*histogram)
+    code, util = ctypes.c_int(), ctypes.c_int64()
+    bounds = (ctypes.c_int64 * 64)()
+    mapping = (ctypes.c_int * 64)()
+    rows_in = (ctypes.c_int64 * 64)()
+    n, per_row, active = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64()
+    _native.call("tgx_plan_reference_buckets", n_rows, max_degree, degree_sum, hist,
+                 int(bool(has_node_epilogue)), ctypes.byref(code), ctypes.byref(util), bounds,
+                 mapping, rows_in, ctypes.byref(n), ctypes.byref(per_row), ctypes.byref(active))
+    k = n.value
+    plan = {"plan": _PLAN_NAMES[code.value], "utilization_milli": util.value,
+            "bounds": list(bounds[:k]), "mapping": [_MAPPING_NAMES[m] for m in mapping[:k]],
+            "rows_in_bucket": list(rows_in[:k]), "partials_per_row": per_row.value,
+            "active_rows": active.value}
+    # Launch sizing of the reference's bucket tasks (Translate.cpp:4728-4830):
+    # rows per program min(16, 256 / nextpow2(bound)); a direct-filter bucket
+    # scans every row, the others their worklist.
+    grid = []
+    for bound, how, rows in zip(plan["bounds"], plan["mapping"], plan["rows_in_bucket"]):
+        per_program = max(1, min(16, 256 // (1 << max(0, (bound - 1).bit_length()))))
+        scanned = n_rows if how == "direct-filter" else rows
+        grid.append(-(-scanned // per_program))
+    plan["grid_x"] = grid
+    plan["worklist_elements"] = n_rows + 2 * k + 1
+    plan["partial_bytes"] = 4 * plan["partials_per_row"] * plan["active_rows"]
+    return plan
+
+
+def describe_reference_plan(plan: dict) -> str:
+    text = f"reference planner: {plan['plan']}"
+    if plan["utilization_milli"] >= 0:
+        text += f", padding utilization {plan['utilization_milli']}/1000"
+    if plan["bounds"]:
+        buckets = ", ".join(f"<={b} {m} ({r} rows)" for b, m, r in
+                            zip(plan["bounds"], plan["mapping"], plan["rows_in_bucket"]))
+        text += f"; buckets {buckets}"
+    if plan["partials_per_row"]:
+        text += (f"; row split {plan['partials_per_row']} partials x "
+                 f"{plan['active_rows']} rows")
+    return text
 
 
 class Graph:
@@ -340,23 +394,22 @@ class Graph:
                     parts.append(cu[1:] + offset)
                     offset += int(cu[-1].item())
                 return cls.cu_seqlens(torch.cat(parts), causal=causal)
+        # Materialized blocks: every block's CSR shifted by the edges and
+        # sources of the blocks before it; the block edge counts come back in
+        # one host transfer.
         dtype = (torch.int64 if any(b.schema.index_dtype == torch.int64 for b in blocks)
                  else torch.int32)
-        row_parts = [torch.zeros(1, device=device, dtype=dtype)]
-        col_parts = []
-        edge_offset = 0
-        src_offset = 0
-        for block in blocks:
-            block_rows, block_cols = block.resolve_csr()
-            block_rows = block_rows.to(dtype)
-            col_parts.append(block_cols.to(dtype) + src_offset)
-            row_parts.append(block_rows[1:] + edge_offset)
-            edge_offset += int(block_rows[-1].item())
-            src_offset += block.schema.num_src
-        row_ptr = torch.cat(row_parts)
-        col_idx = (torch.cat(col_parts) if any(p.numel() for p in col_parts)
-                   else torch.empty(0, device=device, dtype=dtype))
-        return cls.from_csr(row_ptr, col_idx, num_src=src_offset)
+        csrs = [b.resolve_csr() for b in blocks]
+        ends = torch.stack([rp[-1].to(torch.int64) for rp, _ in csrs]).cpu().tolist()
+        edge_base = [0]
+        src_base = [0]
+        for b, n in zip(blocks, ends):
+            edge_base.append(edge_base[-1] + int(n))
+            src_base.append(src_base[-1] + b.schema.num_src)
+        row_ptr = torch.cat([torch.zeros(1, dtype=dtype, device=device)] +
+                            [rp[1:].to(dtype) + eb for (rp, _), eb in zip(csrs, edge_base)])
+        col_idx = torch.cat([ci.to(dtype) + sb for (_, ci), sb in zip(csrs, src_base)])
+        return cls.from_csr(row_ptr, col_idx, num_src=src_base[-1])
 
     # ---- queries ---------------------------------------------------------
     @property
@@ -467,27 +520,139 @@ class Graph:
             self._destination_index_cache = dst
         return dst
 
-    def degree_bounds(self) -> tuple[int, int]:
-        if self._degree_bounds_cache is not None:
-            return self._degree_bounds_cache
-        row_ptr, _ = self.resolve_csr()
-        if self._schema.num_dst == 0:
-            bounds = (0, 0)
+    def _degree_stats(self) -> tuple[int, int, int]:
+        """(min, max, sum) of the destination-row degrees: closed forms for
+        implicit relations, else one device reduction and one host transfer,
+        cached for the graph (an immutable snapshot)."""
+        got = self._degree_bounds_cache
+        if got is not None:
+            return got
+        n_dst, n_src = self._schema.num_dst, self._schema.num_src
+        if self.is_dense and self._row_ptr is None:
+            if self._dense_boundary == "lower_inclusive":
+                got = (1, n_dst, n_dst * (n_dst + 1) // 2) if n_dst else (0, 0, 0)
+            else:
+                got = (n_src, n_src, n_src * n_dst)
+        elif self.is_varlen and self._row_ptr is None:
+            lengths = (self._cu_seqlens[1:] - self._cu_seqlens[:-1]).to(torch.int64).cpu()
+            lengths = lengths[lengths > 0]
+            if lengths.numel() == 0:
+                got = (0, 0, 0)
+            elif self._causal:
+                got = (1, int(lengths.max()), int((lengths * (lengths + 1) // 2).sum()))
+            else:
+                got = (int(lengths.min()), int(lengths.max()), int((lengths * lengths).sum()))
+        elif n_dst == 0:
+            got = (0, 0, 0)
         else:
-            degrees = row_ptr[1:] - row_ptr[:-1]
-            extrema = torch.stack((degrees.min(), degrees.max())).cpu()
-            bounds = int(extrema[0]), int(extrema[1])
-        self._degree_bounds_cache = bounds
-        return bounds
+            row_ptr, _ = self.resolve_csr()
+            degree = (row_ptr[1:] - row_ptr[:-1]).to(torch.int64)
+            got = tuple(int(v) for v in torch.stack(
+                (degree.min(), degree.max(), row_ptr[-1].to(torch.int64))).cpu())
+        self._degree_bounds_cache = got
+        return got
 
-    def degree_histogram(self) -> torch.Tensor:
-        row_ptr, _ = self.resolve_csr()
-        degrees = (row_ptr[1:] - row_ptr[:-1]).to(torch.int64)
-        return torch.bincount(degrees).cpu()
+    def degree_bounds(self) -> tuple[int, int]:
+        """(minimum, maximum) destination-row degree (reference graph.py:1224-1245;
+        the first call may synchronize the device)."""
+        return self._degree_stats()[:2]
+
+    def degree_statistics(self) -> tuple[int, int, int]:
+        """(minimum, maximum, sum) of the destination-row degrees (reference
+        graph.py:1247-1256)."""
+        return self._degree_stats()
+
+    def degree_histogram(self) -> tuple[int, ...]:
+        """Exact row counts indexed by degree 0..max (reference graph.py:
+        1258-1277); limited to a maximum degree of 4096, as there."""
+        _, maximum, _ = self._degree_stats()
+        if maximum > 4096:
+            raise ValueError("exact degree histogram is limited to degree_max <= 4096")
+        got = self._native_cache.get("histogram")
+        if got is None:
+            n_dst = self._schema.num_dst
+            if self.is_dense and self._row_ptr is None:
+                counts = [0] * (maximum + 1)
+                if self._dense_boundary == "lower_inclusive":
+                    counts[1:] = [1] * maximum
+                else:
+                    counts[maximum] = n_dst
+            else:
+                row_ptr, _ = self.resolve_csr() if not self.is_varlen else (None, None)
+                if row_ptr is None:
+                    cu = self._cu_seqlens.to(torch.int64).cpu()
+                    counts = [0] * (maximum + 1)
+                    for length in (cu[1:] - cu[:-1]).tolist():
+                        if self._causal:
+                            for d in range(1, length + 1):
+                                counts[d] += 1
+                        else:
+                            counts[length] += length
+                    counts[0] += n_dst - sum(counts)
+                else:
+                    degree = (row_ptr[1:] - row_ptr[:-1]).to(torch.int64)
+                    counts = torch.bincount(degree, minlength=maximum + 1).cpu().tolist()
+            got = tuple(int(c) for c in counts)
+            self._native_cache["histogram"] = got
+        return got
+
+    def source_index_span_ratio(self, samples: int = 4096) -> float:
+        """Locality of the gathers (reference graph.py:1279-1311): the mean
+        |source id - destination id| over `samples` evenly spaced edge slots,
+        over max(1, num_src, num_dst), clipped to [0, 1]; about 1/3 for random
+        numbering, near 0 for index-local graphs.  Planning information only."""
+        key = ("span_ratio", samples)
+        got = self._native_cache.get(key)
+        if got is not None:
+            return got
+        if self.is_dense and self._row_ptr is None:
+            return 1.0 / 3.0
+        row_ptr, col_idx = self.resolve_csr()
+        E = col_idx.numel()
+        if E == 0:
+            ratio = 0.0
+        else:
+            count = min(samples, E)
+            step = (E - 1) / (count - 1) if count > 1 else 0.0
+            slots = torch.floor(torch.arange(count, dtype=torch.float64) * step)
+            slots = slots.clamp_(max=E - 1).to(torch.int64).to(col_idx.device)
+            rows = torch.searchsorted(row_ptr[1:].to(torch.int64), slots, right=True)
+            span = (col_idx[slots].to(torch.int64) - rows).abs().to(torch.float64).mean()
+            scale = max(1, self._schema.num_src, self._schema.num_dst)
+            ratio = min(1.0, max(0.0, float(span.cpu()) / scale))
+        self._native_cache[key] = ratio
+        return ratio
 
     def planning_key(self) -> tuple[object, ...]:
-        return (self._schema.realization, self._schema.num_src, self._schema.num_dst,
-                str(self._schema.index_dtype), str(self.device))
+        """What a specialization depends on (reference graph.py:1317-1351):
+        the relation's kind and sizes, index dtype and device, the degree
+        statistics, the gather locality and the dense boundary."""
+        s = self._schema
+        locality = (self.source_index_span_ratio()
+                    if self._row_ptr is not None else "implicit")
+        return (s.origin, s.realization, s.num_src, s.num_dst, str(s.index_dtype),
+                str(self.device), self.degree_statistics(), locality, self._dense_boundary)
+
+    def _reference_plan_remarks(self, has_node_epilogue: bool = False) -> tuple[str, ...]:
+        """The reference planner's decision for this CSR
+        (tgx_plan_reference_buckets: SelectKernelSchedule.cpp:136-163,
+        PlanDegreeBuckets.cpp:32-143, PlanSplitRows.cpp:84-147), given the
+        degree statistics and, up to degree 4096, the exact histogram."""
+        key = ("reference_plan", bool(has_node_epilogue))
+        got = self._native_cache.get(key)
+        if got is None:
+            got = (describe_reference_plan(self.reference_plan(has_node_epilogue)),)
+            self._native_cache[key] = got
+        return got
+
+    def reference_plan(self, has_node_epilogue: bool = False) -> dict:
+        """The reference planner's decision for this graph as a dict: plan name,
+        padding utilization (per mille, -1 when not computed), bucket upper
+        bounds, their mappings and row counts, row-split sizing."""
+        _, maximum, total = self._degree_stats()
+        histogram = self.degree_histogram() if maximum <= 4096 else None
+        return reference_plan(self._schema.num_dst, maximum, total, histogram,
+                              has_node_epilogue)
 
     def explain(self) -> str:
         lines = [f"relation: {self._schema.realization}",
@@ -495,6 +660,7 @@ class Graph:
         plan = self._native_cache.get(("plan", WAVE_MAX, CHUNK_EDGES))
         if plan is not None:
             lines.append(f"row plan: {plan.counts()}")
+            lines.extend(self._reference_plan_remarks())
         return "\n".join(lines)
 
     # ---- native device structures (built once per graph) -----------------
@@ -625,4 +791,4 @@ def _varlen_csr(cu_seqlens: torch.Tensor, causal: bool):
 
 
 __all__ = ["Graph", "GraphSchema", "build_coo_csr", "build_row_plan", "build_transpose",
-           "build_varlen_csr"]
+           "build_varlen_csr", "describe_reference_plan", "reference_plan"]

@@ -1,43 +1,54 @@
-"""``torch.library`` registration of MessagePassing specializations.
+"""MessagePassing specializations as ``torch.library`` operators.
 
-Mirrors the reference facade (python/tiga/interop/torch/library.py:23-208):
-``register_message_passing(kernel, graph=..., src=..., dst=..., edge=...,
-name=None, **params)`` defines one functional dispatcher op
+Public surface kept from the reference (python/tiga/interop/torch/
+library.py:63-205): ``register_message_passing(kernel, graph=..., src=...,
+dst=..., edge=..., name=None, **params)`` returns a
+``RegisteredMessagePassingOp`` (``qualified_name``, ``operation``,
+``topology``, ``bindings``, ``static_params``; callable with ``src=``,
+``dst=``, ``edge=``; ``opcheck(*values)``), and the operator's schema is
 ``tiga::<name>(Tensor row_ptr, Tensor col_idx, Tensor input_0, ...) ->
-Tensor`` whose operands are the field tensors in (src, dst, edge) order,
-sorted by name, so ``torch.compile(fullgraph=True)``, FakeTensor tracing and
-AOT autograd see one opaque op.
+Tensor`` with the field tensors in (src, dst, edge) order, names sorted.
 
-Implementation: the op's kernel calls the MessagePassing kernel itself, so
-on ROCm tensors it runs this package's HIP path (below autograd).  Its
-registered autograd formula recomputes the call with autograd enabled and
-differentiates it: on the HIP path that replays the HIP forward and runs the
-fused HIP backward (the reference replays its eager oracle instead).  The
-fake kernel returns an empty tensor of the specialization's output shape and
-dtype, taken from one call at registration.
+Design.  A ``_Specialization`` object owns everything one registration
+fixes: the kernel, the graph (and with it the per-graph device structures:
+row plans, transposed CSR), the operand layout, the non-tensor parameters
+and the output's shape and dtype.  Two dispatcher operators are defined
+from it:
+
+* ``tiga::<name>`` runs the MessagePassing kernel below autograd, so on
+  ROCm tensors it is the HIP path;
+* ``tiga::<name>_backward(grad, row_ptr, col_idx, inputs..., needs)``
+  recomputes the forward with autograd enabled and differentiates it, which
+  on the HIP path replays the HIP forward and runs the fused HIP backward.
+  Being an operator of its own, AOT autograd and ``torch.compile`` treat it
+  as opaque instead of tracing into the ctypes calls.
+
+Fake kernels give both operators their shapes, so FakeTensor tracing and
+``torch.compile(fullgraph=True)`` work.  No hot-path entry point allocates,
+copies or synchronises, so the registered op can be captured in a HIP graph
+once the per-graph structures exist.
 """
 
 from __future__ import annotations
 
 import hashlib
+import re
 from dataclasses import dataclass
 from typing import Any, Mapping
 
 import torch
 
-_LIBRARIES: list[Any] = []
-_REGISTERED: dict[str, "RegisteredMessagePassingOp"] = {}
-
-
-def _ordered_fields(*groups: Mapping[str, Any]):
-    return tuple((role, name)
-                 for role, group in zip(("src", "dst", "edge"), groups, strict=True)
-                 for name in sorted(group))
+_ROLES = ("src", "dst", "edge")
+# Registered operators by qualified name; the Library objects must stay alive
+# for their dispatcher registrations to stay valid.
+_OPS: dict[str, "RegisteredMessagePassingOp"] = {}
+_KEEP_ALIVE: list[torch.library.Library] = []
 
 
 @dataclass(frozen=True)
 class RegisteredMessagePassingOp:
-    """One dispatcher binding for a MessagePassing specialization."""
+    """A registered specialization: call it with the field mappings, or
+    call ``operation`` with (row_ptr, col_idx, *inputs) in ``bindings`` order."""
 
     qualified_name: str
     operation: Any
@@ -47,170 +58,179 @@ class RegisteredMessagePassingOp:
 
     def __call__(self, *, src: Mapping[str, Any], dst: Mapping[str, Any],
                  edge: Mapping[str, Any] | None = None):
-        edge = {} if edge is None else edge
-        groups = {"src": src, "dst": dst, "edge": edge}
-        expected = {role: {name for candidate, name in self.bindings if candidate == role}
-                    for role in ("src", "dst", "edge")}
-        for role, group in groups.items():
-            if set(group) != expected[role]:
-                raise ValueError(f"{role} fields must be {sorted(expected[role])}, "
-                                 f"got {sorted(group)}")
-        return self.operation(*self.topology,
-                              *(groups[role][name] for role, name in self.bindings))
+        given = {"src": src, "dst": dst, "edge": {} if edge is None else edge}
+        for role in _ROLES:
+            want = sorted(name for r, name in self.bindings if r == role)
+            if sorted(given[role]) != want:
+                raise ValueError(f"{role} fields must be {want}, got {sorted(given[role])}")
+        inputs = [given[role][name] for role, name in self.bindings]
+        return self.operation(*self.topology, *inputs)
 
     def opcheck(self, *values: Any) -> dict[str, str]:
-        """PyTorch's schema / autograd / FakeTensor / AOT conformance checks."""
+        """torch.library.opcheck (schema, autograd registration, fake kernel,
+        AOT dispatch) on the registered topology and these field values."""
         return torch.library.opcheck(self.operation, (*self.topology, *values))
+
+
+class _Specialization:
+    """What one registration fixes, and the three functions the dispatcher
+    calls: forward, backward and the fake (shape-only) forward."""
+
+    def __init__(self, kernel, graph, bindings, params, out_shape, out_dtype):
+        self.kernel = kernel
+        self.graph = graph
+        self.bindings = bindings
+        self.params = dict(params)
+        self.out_shape = out_shape
+        self.out_dtype = out_dtype
+        row_ptr, col_idx = graph.resolve_csr()
+        self.topology = (row_ptr, col_idx)
+
+    # -- operand handling ----------------------------------------------------
+    def graph_for(self, row_ptr, col_idx):
+        """The registered graph when the op receives its own topology tensors
+        (so its cached device structures are reused), else a new CSR graph
+        over the given tensors."""
+        from ..graph import Graph
+
+        if row_ptr is self.topology[0] and col_idx is self.topology[1]:
+            return self.graph
+        same = all(a.data_ptr() == b.data_ptr() and a.shape == b.shape and
+                   a.device == b.device for a, b in zip((row_ptr, col_idx), self.topology))
+        if same:
+            return self.graph
+        return Graph.from_csr(row_ptr, col_idx, num_src=self.graph.schema.num_src)
+
+    @staticmethod
+    def merge_aliases(inputs):
+        """Operands that view the same memory the same way become one tensor
+        object again (a field bound both as src and dst, like GAT's h, must
+        be one object for the kernel to see the alias)."""
+        first: dict[tuple, torch.Tensor] = {}
+        merged = []
+        for t in inputs:
+            key = (t.data_ptr(), t.dtype, t.device, tuple(t.shape), t.stride())
+            merged.append(first.setdefault(key, t))
+        return merged
+
+    def fields(self, inputs):
+        groups: dict[str, dict[str, torch.Tensor]] = {role: {} for role in _ROLES}
+        for (role, name), t in zip(self.bindings, inputs):
+            groups[role][name] = t
+        return groups
+
+    def run(self, row_ptr, col_idx, inputs):
+        groups = self.fields(inputs)
+        return self.kernel(graph=self.graph_for(row_ptr, col_idx), src=groups["src"],
+                           dst=groups["dst"], edge=groups["edge"], **self.params)
+
+    # -- dispatcher functions ------------------------------------------------
+    def forward(self, row_ptr, col_idx, *inputs):
+        out = self.run(row_ptr, col_idx, self.merge_aliases(inputs))
+        # The operator is functional: its result may not alias an operand.
+        for t in (row_ptr, col_idx, *inputs):
+            if out is t or out._base is t:
+                return out.clone()
+        return out
+
+    def fake_forward(self, row_ptr, col_idx, *inputs):
+        return inputs[0].new_empty(self.out_shape, dtype=self.out_dtype)
+
+    def backward(self, grad, row_ptr, col_idx, *rest):
+        inputs, needs = rest[:-1], rest[-1]
+        grads = [torch.zeros_like(t) for t in inputs]
+        replay = self.merge_aliases([t.detach() for t in inputs])
+        wanted: list[tuple[int, torch.Tensor]] = []
+        for i, (t, need) in enumerate(zip(replay, needs)):
+            # One leaf per distinct tensor: an operand bound twice gets its
+            # whole gradient at its first position.
+            if need and t.is_floating_point() and all(t is not w for _, w in wanted):
+                wanted.append((i, t.requires_grad_(True)))
+        if wanted:
+            with torch.enable_grad():
+                out = self.run(row_ptr, col_idx, replay)
+                got = torch.autograd.grad(out, [t for _, t in wanted], grad,
+                                          allow_unused=True)
+            for (i, _), g in zip(wanted, got):
+                if g is not None:
+                    grads[i].copy_(g)   # keeps the layout the fake kernel promises
+        return grads
+
+    @staticmethod
+    def fake_backward(grad, row_ptr, col_idx, *rest):
+        return [torch.empty_like(t) for t in rest[:-1]]
+
+
+def _op_name(kernel, graph, bindings, inputs, params, out_shape, out_dtype) -> str:
+    """A stable operator name for a specialization: the kernel class and a
+    digest of everything the specialization fixes."""
+    key = (type(kernel).__module__, type(kernel).__qualname__, kernel.reducer.specialization_key(),
+           graph.planning_key(), bindings,
+           [(tuple(t.shape), str(t.dtype)) for t in inputs],
+           sorted((k, repr(v)) for k, v in params.items()), out_shape, str(out_dtype))
+    digest = hashlib.blake2b(repr(key).encode(), digest_size=10).hexdigest()
+    stem = re.sub(r"[^0-9A-Za-z]+", "_", type(kernel).__name__).strip("_").lower() or "kernel"
+    return f"mp_{stem}_{digest}"
 
 
 def register_message_passing(kernel, *, graph, src: Mapping[str, Any], dst: Mapping[str, Any],
                              edge: Mapping[str, Any] | None = None, name: str | None = None,
                              **params: Any) -> RegisteredMessagePassingOp:
-    """Register a MessagePassing specialization as a functional Torch op
-    (reference library.py:63-205).  Tensor fields stay dispatcher operands;
-    the graph topology, field names and non-Tensor parameters are fixed."""
-    from ..graph import Graph
-
+    """Register one MessagePassing specialization as a functional Torch
+    operator.  The field tensors stay operands; the graph's topology, the
+    field names and the non-tensor parameters are fixed by the registration."""
     edge = {} if edge is None else edge
     if graph.schema.realization != "materialized_csr":
         raise NotImplementedError(
             "torch.library registration currently requires a static CSR graph")
-    row_ptr, col_idx = graph.resolve_csr()
-    bindings = _ordered_fields(src, dst, edge)
     groups = {"src": src, "dst": dst, "edge": edge}
-    values = tuple(groups[role][field] for role, field in bindings)
-    if not values or any(not isinstance(value, torch.Tensor) for value in values):
+    bindings = tuple((role, n) for role in _ROLES for n in sorted(groups[role]))
+    inputs = [groups[role][n] for role, n in bindings]
+    if not inputs or not all(isinstance(t, torch.Tensor) for t in inputs):
         raise TypeError("registered MessagePassing fields must be torch.Tensor values")
-    if any(isinstance(value, torch.Tensor) for value in params.values()):
+    if any(isinstance(v, torch.Tensor) for v in params.values()):
         raise TypeError("Tensor parameters must be expressed as src/dst/edge fields")
-
     with torch.no_grad():
         sample = kernel(graph=graph, src=src, dst=dst, edge=edge, **params)
     if not isinstance(sample, torch.Tensor):
         raise NotImplementedError("the torch.library facade requires one Tensor result")
-    output_shape, output_dtype = tuple(sample.shape), sample.dtype
-    signature = repr((type(kernel).__module__, type(kernel).__qualname__,
-                      kernel.reducer.specialization_key(), graph.planning_key(), bindings,
-                      tuple((tuple(v.shape), str(v.dtype)) for v in values),
-                      tuple(sorted((k, repr(v)) for k, v in params.items())),
-                      output_shape, str(output_dtype)))
-    op_name = name or f"message_passing_{hashlib.sha256(signature.encode()).hexdigest()[:20]}"
-    if not op_name.replace("_", "").isalnum() or not op_name[0].isalpha():
+    out_shape, out_dtype = tuple(sample.shape), sample.dtype
+    op = name or _op_name(kernel, graph, bindings, inputs, params, out_shape, out_dtype)
+    if not re.fullmatch(r"[A-Za-z][A-Za-z0-9_]*", op):
         raise ValueError("Torch op name must begin with a letter and be alphanumeric/_")
-    qualified = f"tiga::{op_name}"
-    found = _REGISTERED.get(qualified)
-    if found is not None:
-        return found
+    qualified = f"tiga::{op}"
+    if qualified in _OPS:
+        return _OPS[qualified]
 
-    library = torch.library.Library("tiga", "FRAGMENT")
-    arguments = ", ".join(["Tensor row_ptr", "Tensor col_idx",
-                           *(f"Tensor input_{i}" for i in range(len(bindings)))])
-    library.define(f"{op_name}({arguments}) -> Tensor")
-    num_src = graph.schema.num_src
+    spec = _Specialization(kernel, graph, bindings, params, out_shape, out_dtype)
+    operands = ", ".join(["Tensor row_ptr", "Tensor col_idx"] +
+                         [f"Tensor input_{i}" for i in range(len(bindings))])
+    lib = torch.library.Library("tiga", "FRAGMENT")
+    lib.define(f"{op}({operands}) -> Tensor")
+    lib.define(f"{op}_backward(Tensor grad, {operands}, bool[] needs) -> Tensor[]")
+    lib.impl(op, spec.forward, "CompositeExplicitAutograd")
+    lib.impl(f"{op}_backward", spec.backward, "CompositeExplicitAutograd")
+    torch.library.register_fake(qualified, spec.fake_forward, lib=lib)
+    torch.library.register_fake(f"{qualified}_backward", spec.fake_backward, lib=lib)
+    backward_op = getattr(torch.ops.tiga, f"{op}_backward").default
 
-    def topology_key(rp, ci):
-        return (rp.data_ptr(), ci.data_ptr(), tuple(rp.shape), tuple(ci.shape), str(rp.device))
-
-    registered_key = topology_key(row_ptr, col_idx)
-
-    def runtime_graph(flat):
-        # The registered topology keeps its graph object, and with it the
-        # per-graph device structures (row plans, transposed CSR).
-        if topology_key(flat[0], flat[1]) == registered_key:
-            return graph
-        return Graph.from_csr(flat[0], flat[1], num_src=num_src, validate="basic")
-
-    def canonical(values):
-        """Operands that are one tensor (same storage, layout and dtype) become
-        one object again, as the kernel saw them at registration (a field used
-        as both src and dst, like GAT's h)."""
-        seen, out = {}, []
-        for value in values:
-            key = (value.data_ptr(), tuple(value.shape), tuple(value.stride()), value.dtype,
-                   str(value.device))
-            out.append(seen.setdefault(key, value))
-        return out
-
-    def unpack(flat):
-        groups_out = {"src": {}, "dst": {}, "edge": {}}
-        for (role, field), value in zip(bindings, flat, strict=True):
-            groups_out[role][field] = value
-        return groups_out
-
-    def implementation(*flat):
-        fields = unpack(canonical(flat[2:]))
-        out = kernel(graph=runtime_graph(flat), src=fields["src"], dst=fields["dst"],
-                     edge=fields["edge"], **params)
-        # A functional op must not return an alias of an operand.
-        return out.clone() if any(out is t or out._base is t for t in flat) else out
-
-    library.impl(op_name, implementation, "CompositeExplicitAutograd")
-
-    def fake(*flat):
-        return flat[2].new_empty(output_shape, dtype=output_dtype)
-
-    torch.library.register_fake(qualified, fake, lib=library)
-
-    # The backward is an opaque op of its own, so AOT autograd and
-    # torch.compile trace it like the forward instead of tracing into the
-    # HIP calls it makes.
-    library.define(f"{op_name}_backward(Tensor grad, {arguments}, bool[] needs) -> Tensor[]")
-
-    def backward_implementation(grad, *rest):
-        flat, needs = rest[:-1], rest[-1]
-        replay = list(flat[:2]) + canonical([t.detach() for t in flat[2:]])
-        differentiable, positions = [], []
-        for index, need in enumerate(needs):
-            local = replay[2 + index]
-            # A tensor given at several positions gets its whole gradient at
-            # the first one that needs it (the others stay zero).
-            if need and (local.is_floating_point() or local.is_complex()) and \
-                    not any(local is d for d in differentiable):
-                local.requires_grad_(True)
-                differentiable.append(local)
-                positions.append(index)
-        gradients = [torch.zeros_like(t) for t in flat[2:]]
-        if differentiable:
-            fields = unpack(replay[2:])
-            with torch.enable_grad():
-                output = kernel(graph=runtime_graph(replay), src=fields["src"],
-                                dst=fields["dst"], edge=fields["edge"], **params)
-                computed = torch.autograd.grad(output, differentiable, grad,
-                                               allow_unused=True)
-            # Copied into zeros_like(input) so the result has exactly the
-            # layout the fake kernel promises.
-            for position, gradient in zip(positions, computed, strict=True):
-                if gradient is not None:
-                    gradients[position].copy_(gradient)
-        return gradients
-
-    library.impl(f"{op_name}_backward", backward_implementation, "CompositeExplicitAutograd")
-
-    def backward_fake(grad, *rest):
-        return [torch.empty_like(t) for t in rest[2:-1]]
-
-    torch.library.register_fake(f"{qualified}_backward", backward_fake, lib=library)
-    backward_op = getattr(getattr(torch.ops.tiga, f"{op_name}_backward"), "default")
-
-    def setup_context(ctx, inputs, output):
-        del output
+    def save_operands(ctx, inputs, output):
         ctx.save_for_backward(*inputs)
 
-    def backward(context, grad_output):
-        needs = [bool(n) for n in context.needs_input_grad[2:]]
+    def differentiate(ctx, grad):
+        needs = [bool(n) for n in ctx.needs_input_grad[2:]]
         if not any(needs):
-            return (None,) * len(context.needs_input_grad)
-        grads = backward_op(grad_output, *context.saved_tensors, needs)
-        return (None, None, *(g if need else None for g, need in zip(grads, needs)))
+            return (None,) * len(ctx.needs_input_grad)
+        grads = backward_op(grad, *ctx.saved_tensors, needs)
+        return (None, None, *(g if n else None for g, n in zip(grads, needs)))
 
-    torch.library.register_autograd(qualified, backward, setup_context=setup_context,
-                                    lib=library)
-    operation = getattr(getattr(torch.ops.tiga, op_name), "default")
-    registered = RegisteredMessagePassingOp(qualified_name=qualified, operation=operation,
-                                            topology=(row_ptr, col_idx), bindings=bindings,
-                                            static_params=dict(params))
-    _LIBRARIES.append(library)   # dispatcher registrations live as long as the Library
-    _REGISTERED[qualified] = registered
+    torch.library.register_autograd(qualified, differentiate, setup_context=save_operands,
+                                    lib=lib)
+    registered = RegisteredMessagePassingOp(
+        qualified_name=qualified, operation=getattr(torch.ops.tiga, op).default,
+        topology=spec.topology, bindings=bindings, static_params=dict(params))
+    _KEEP_ALIVE.append(lib)
+    _OPS[qualified] = registered
     return registered
 
 

@@ -1,9 +1,13 @@
-"""Variant bookkeeping and ``explain()`` (reference python/tiga/kernel/model.py:99-229).
+"""What a kernel ran, for ``explain()`` (reference python/tiga/kernel/model.py:99-229).
 
-Each call records which execution path ran (``backend``: ``hip`` for the
-gfx950 kernels, ``torch-eager`` for edge functions no HIP kernel covers), the
-native entry points it used and the row-partition plan, so users can inspect
-the chosen plan exactly as with the reference's ``kernel.explain()``.
+The public surface is the reference's observability API: ``last_variant``,
+``variants``, ``explain()``, ``cache_info`` and ``CompiledVariant.code()``.
+Here a variant is one (kernel, execution path, graph shape) combination: the
+``hip`` backend with the libtgx_hip.so entry points it calls and the row
+partition it uses, or ``torch-eager`` for an edge function no HIP kernel
+covers.  ``cache_info`` counts calls: a *hit* is a warm call served by the
+guarded launch of the previous call (no capture, recognition or
+validation), a *miss* is a call that went through capture and dispatch.
 """
 
 from __future__ import annotations
@@ -13,6 +17,10 @@ from dataclasses import dataclass, field
 
 @dataclass(frozen=True)
 class CompiledVariant:
+    """One execution path a kernel took: backend, provider, the recognized
+    edge-function pattern, how it is lowered, the entry points it calls and
+    free-form remarks (row plan, reference planner decision)."""
+
     key: tuple[object, ...]
     backend: str
     provider: str
@@ -23,59 +31,59 @@ class CompiledVariant:
     artifacts: dict[str, str] = field(default_factory=dict)
 
     def explain(self) -> str:
-        lines = [
-            f"backend: {self.backend}",
-            f"provider: {self.provider}",
-            f"pattern: {self.pattern}",
-            f"lowering: {self.lowering or '(unspecified)'}",
-            f"entry points: {', '.join(self.entry_points) if self.entry_points else '(none)'}",
-        ]
-        lines.extend(f"remark: {remark}" for remark in self.remarks)
-        return "\n".join(lines)
+        calls = ", ".join(self.entry_points) or "(none)"
+        text = [f"backend: {self.backend}", f"provider: {self.provider}",
+                f"pattern: {self.pattern}", f"lowering: {self.lowering or '(unspecified)'}",
+                f"entry points: {calls}"]
+        text += [f"remark: {r}" for r in self.remarks]
+        return "\n".join(text)
 
     def code(self, kind: str) -> str:
-        try:
-            return self.artifacts[kind]
-        except KeyError as exc:
-            raise KeyError(
-                f"artifact {kind!r} is unavailable for provider {self.provider!r}") from exc
+        """A stored artifact by kind.  The HIP provider is compiled ahead of
+        time, so it keeps none and every kind raises KeyError."""
+        if kind not in self.artifacts:
+            raise KeyError(f"no {kind!r} artifact: provider {self.provider!r} keeps "
+                           f"{sorted(self.artifacts) or 'none'}")
+        return self.artifacts[kind]
 
 
 class Kernel:
+    """Base of ``MessagePassing``: the variants a kernel instance has run and
+    its call counters."""
+
     def __init__(self) -> None:
-        self._variants: dict[tuple[object, ...], CompiledVariant] = {}
-        self._last_variant: CompiledVariant | None = None
-        self._cache_hits = 0
-        self._cache_misses = 0
+        self._seen: dict[tuple[object, ...], CompiledVariant] = {}
+        self._current: CompiledVariant | None = None
+        self._warm_calls = 0
+        self._cold_calls = 0
 
     @property
     def variants(self) -> tuple[CompiledVariant, ...]:
-        return tuple(self._variants.values())
+        return tuple(self._seen.values())
 
     @property
     def last_variant(self) -> CompiledVariant:
-        if self._last_variant is None:
+        if self._current is None:
             raise RuntimeError("kernel has not been called, so no variant exists")
-        return self._last_variant
+        return self._current
 
     def explain(self) -> str:
-        return "\n".join((
-            self.last_variant.explain(),
-            f"variant cache: hits={self._cache_hits}, misses={self._cache_misses}",
-        ))
+        info = self.cache_info
+        return (f"{self.last_variant.explain()}\n"
+                f"variant cache: hits={info['hits']}, misses={info['misses']}")
 
     @property
     def cache_info(self) -> dict[str, int]:
-        return {
-            "hits": self._cache_hits,
-            "misses": self._cache_misses,
-            "variants": len(self._variants),
-        }
+        return {"hits": self._warm_calls, "misses": self._cold_calls,
+                "variants": len(self._seen)}
 
     def _record_variant(self, variant: CompiledVariant) -> None:
-        if variant.key in self._variants:
-            self._cache_hits += 1
-        else:
-            self._cache_misses += 1
-        self._variants[variant.key] = variant
-        self._last_variant = variant
+        """A cold call ran `variant`."""
+        self._cold_calls += 1
+        self._seen[variant.key] = variant
+        self._current = variant
+
+    def _record_warm(self, variant: CompiledVariant) -> None:
+        """A warm call re-ran `variant` through its guarded launch."""
+        self._warm_calls += 1
+        self._current = variant

@@ -1,26 +1,43 @@
 """``tiga.MessagePassing``: the Torch-facing facade of the HIP provider.
 
-Call form and validation follow the reference adapter
-(python/tiga/interop/torch/message_passing.py:1490-1651, 3565-3586):
-``K()(graph=G, src={...}, dst={...}, edge={...}, **params) -> torch.Tensor``,
-``edge(self, src, dst, edge, **params)`` and ``node(self, dst, aggregate,
-**params)``.
+Call forms follow the reference (python/tiga/message_passing/core.py:32-50,
+543-766 and python/tiga/interop/torch/message_passing.py:1490-1651,
+3565-3586, 3827-3879):
 
-Dispatch: the edge function is captured once per parameter structure and
-matched against the patterns that have gfx950 kernels (``capture.py``).  A
-recognized pattern on ROCm tensors of a supported dtype/shape runs through
-``torch.autograd.Function`` bridges over libtgx_hip.so and nothing else: if
-the library is missing it raises.  Edge functions no kernel covers (and CPU
-tensors) run on the eager Torch evaluator, which restates the reference's own
-fallback (``_evaluate_reference`` 2848-2894); ``explain()`` reports which path
-ran.  Setting ``tiga.config.strict = True`` turns that fallback into an error.
+* ``K()(graph=G, src={...}, dst={...}, edge={...}, **params) -> Tensor``,
+  or ``ndata={...}`` in place of ``src``/``dst`` on a homogeneous relation;
+* ``K().prepare(graph=G, ...)`` -> a zero-argument launch with the graph,
+  the bindings, shapes and strides frozen (tensor contents stay live);
+* ``edge(self, src, dst, edge, **params)``, ``node(self, dst, aggregate,
+  **params)``; ``explain()``, ``last_variant``, ``cache_info``.
+
+Dispatch.  A cold call validates the fields, captures ``edge()`` on symbolic
+proxies and matches the capture against the patterns with gfx950 kernels
+(``capture.py``).  A match on ROCm tensors of a supported dtype/shape becomes
+a *launch*: the pattern's operands named by binding (``src.x``, ``edge.w``,
+a tensor parameter) and a runner over ``torch.autograd.Function`` bridges
+into libtgx_hip.so, which raises if the library is missing.  When every
+operand comes from the call's own fields or parameters, the launch is kept
+with guards (same graph object, same reducer, same parameter values, every
+operand with the same dtype/shape/strides/device, required aliases); a warm
+call that passes the guards runs it directly, skipping capture, recognition
+and validation, like the reference's guarded executable (:974-1008).  A
+launch that holds a tensor from outside the call (a closure or attribute)
+is re-captured on every call instead, so rebinding that name is seen.
+
+Edge functions no kernel covers (and CPU tensors) run the eager Torch
+evaluator, the reference's own fallback (``_evaluate_reference``
+2848-2894); ``explain()`` reports which path ran and
+``tiga.config.strict = True`` turns that fallback into an error.
 """
 
 from __future__ import annotations
 
 import functools
 import inspect
-from collections.abc import Mapping
+import numbers
+from collections.abc import Callable, Mapping
+from dataclasses import dataclass
 from types import SimpleNamespace
 from typing import Any
 
@@ -39,6 +56,8 @@ class _Config:
 
 config = _Config()
 
+_MISS = object()
+
 
 @functools.lru_cache(maxsize=512)
 def _parameter_names(function) -> tuple[bool, frozenset]:
@@ -56,11 +75,113 @@ def _call_region(method, positional: tuple, params: Mapping[str, Any]):
     return method(*positional, **selected)
 
 
+def _resolve_node_fields(graph, src, dst, ndata):
+    """``ndata=`` binds one mapping to both endpoint roles of a homogeneous
+    relation (reference message_passing/core.py:32-50)."""
+    if ndata is not None:
+        if src is not None or dst is not None:
+            raise TypeError("ndata= cannot be combined with src=/dst=")
+        if graph.schema.num_src != graph.schema.num_dst:
+            raise ValueError(
+                "ndata= requires a homogeneous relation (num_src == num_dst); "
+                "declare src= and dst= separately for bipartite graphs")
+        src = dst = dict(ndata)
+    if src is None or dst is None:
+        raise TypeError("message passing requires ndata= or both src= and dst= mappings")
+    return src, dst
+
+
+def _spec(t: torch.Tensor) -> tuple:
+    return (t.dtype, t.shape, t.stride(), t.device)
+
+
+def _param_signature(params: Mapping[str, Any]) -> tuple:
+    """Parameter names with the values a capture may have baked in: numbers
+    and other hashable values by value, tensors by kind only (a launch
+    reads its tensor operands from the call), anything else by identity."""
+    sig = []
+    for name in sorted(params):
+        value = params[name]
+        if isinstance(value, torch.Tensor):
+            sig.append((name, "tensor"))
+        elif isinstance(value, (numbers.Number, str, bytes, type(None))):
+            sig.append((name, type(value), value))
+        else:
+            sig.append((name, "object", id(value)))
+    return tuple(sig)
+
+
+@dataclass
+class _Launch:
+    """A recognized pattern bound to its HIP runner.
+
+    operands: (role, name) per runner argument, role in src/dst/edge/param,
+    or ("fixed", object) for something the capture took from outside the
+    call.  aliases: pairs of bindings that must be the same tensor."""
+
+    graph: Graph
+    operands: tuple
+    runner: Callable
+    describe: Callable[[], CompiledVariant]
+    aliases: tuple = ()
+    variant: CompiledVariant | None = None
+
+    @property
+    def guardable(self) -> bool:
+        return all(role != "fixed" for role, _ in self.operands)
+
+    def gather(self, src, dst, edge, params) -> list:
+        groups = {"src": src, "dst": dst, "edge": edge, "param": params}
+        return [name if role == "fixed" else groups[role][name]
+                for role, name in self.operands]
+
+
+class _Guarded:
+    """A launch plus the guards under which a warm call may re-run it."""
+
+    def __init__(self, launch: _Launch, reducer, operands, params):
+        self.launch = launch
+        self.reducer = reducer
+        self.specs = tuple(_spec(t) for t in operands)
+        self.param_sig = _param_signature(params)
+        self.names: tuple | None = None
+
+    @staticmethod
+    def _names(src, dst, edge) -> tuple:
+        # Which fields are bound can steer Python code inside edge().
+        return tuple(src), tuple(dst), tuple(edge)
+
+    def try_run(self, kernel, graph, src, dst, edge, params):
+        launch = self.launch
+        if graph is not launch.graph or kernel.reducer is not self.reducer:
+            return _MISS
+        try:
+            operands = launch.gather(src, dst, edge, params)
+        except (KeyError, TypeError):
+            return _MISS
+        for t, spec in zip(operands, self.specs):
+            if not isinstance(t, torch.Tensor) or _spec(t) != spec:
+                return _MISS
+        if launch.aliases:
+            groups = {"src": src, "dst": dst, "edge": edge, "param": params}
+            for (ra, na), (rb, nb) in launch.aliases:
+                if groups[ra].get(na) is not groups[rb].get(nb):
+                    return _MISS
+        if self._names(src, dst, edge) != self.names or \
+                _param_signature(params) != self.param_sig:
+            return _MISS
+        return launch.runner(*operands)
+
+
 class MessagePassing(Kernel):
     reducer = SumReducer()
+    _guarded: _Guarded | None = None
+    _launch: _Launch | None = None
 
     def __init__(self) -> None:
         super().__init__()
+        self._guarded: _Guarded | None = None
+        self._launch: _Launch | None = None
 
     def edge(self, src, dst, edge, **params):
         raise NotImplementedError
@@ -84,19 +205,39 @@ class MessagePassing(Kernel):
                 raise ValueError(f"{role}.{name} is on {value.device}, but graph is on {device}")
 
     def _captured(self, params):
-        # Captured afresh on every call: the tree holds the module's current
-        # tensors (e.g. attention vectors), which a cache could leave stale.
         return cap.capture(lambda s, d, e, p: _call_region(self.edge, (s, d, e), p), params)
 
-    def __call__(self, *, graph: Graph, src: Mapping[str, torch.Tensor],
-                 dst: Mapping[str, torch.Tensor], edge: Mapping[str, torch.Tensor] | None = None,
-                 **params: Any):
+    def _epilogue(self, dst, aggregate, params):
+        if type(self).node is MessagePassing.node:
+            return aggregate
+        return _call_region(self.node, (SimpleNamespace(**dst), aggregate), params)
+
+    def __call__(self, *, graph: Graph, src: Mapping[str, torch.Tensor] | None = None,
+                 dst: Mapping[str, torch.Tensor] | None = None,
+                 edge: Mapping[str, torch.Tensor] | None = None,
+                 ndata: Mapping[str, torch.Tensor] | None = None, **params: Any):
         if not getattr(graph, "_tiga_graph", False):
             raise TypeError("graph must be a tiga.Graph")
+        src, dst = _resolve_node_fields(graph, src, dst, ndata)
         edge = {} if edge is None else edge
+        guarded = self._guarded
+        if guarded is not None:
+            result = guarded.try_run(self, graph, src, dst, edge, params)
+            if result is not _MISS:
+                self._launch = guarded.launch
+                self._record_warm(guarded.launch.variant)
+                return self._epilogue(dst, result, params)
+        return self._epilogue(dst, self._dispatch(graph, src, dst, edge, params), params)
+
+    def _dispatch(self, graph, src, dst, edge, params):
+        """The cold path: validate, capture, recognize, run."""
         device = graph.device
         self._validate_fields("src", src, graph.schema.num_src, device)
         self._validate_fields("dst", dst, graph.schema.num_dst, device)
+        if edge:
+            # Before any launch: a kernel would dereference a host pointer
+            # (reference interop/torch/message_passing.py:1633-1634).
+            self._validate_fields("edge", edge, graph.num_edges, device)
         prune = (self.reducer.block_prune_threshold
                  if isinstance(self.reducer, OnlineSoftmaxReducer) else None)
         if prune is not None and not graph.is_dense:
@@ -105,37 +246,74 @@ class MessagePassing(Kernel):
                 "block_prune_threshold is defined for dense relations only; refusing to "
                 "run exact softmax on a CSR relation")
         captured = self._captured(params)
-        result = None
+        launch = None
         if device.type == "cuda" and captured is not None:
-            result = self._execute_native(captured, graph, src, dst, edge, params)
-        if result is None and prune is not None:
-            # reference interop/torch/message_passing.py:1611-1616
-            raise NotImplementedError(
-                "block_prune_threshold requires the dense attention tile (dot-product "
-                "score, bf16/fp16, head_dim 64 or 128, on the GPU); refusing to silently "
-                "execute exact softmax or materialize the Cartesian relation")
-        if result is None:
+            launch = self._plan_native(captured, graph, src, dst, edge, params)
+        if launch is None:
+            self._launch = None
+            if prune is not None:
+                # reference interop/torch/message_passing.py:1611-1616
+                raise NotImplementedError(
+                    "block_prune_threshold requires the dense attention tile (dot-product "
+                    "score, bf16/fp16, head_dim 64 or 128, on the GPU); refusing to silently "
+                    "execute exact softmax or materialize the Cartesian relation")
             if config.strict:
                 raise RuntimeError(
                     f"{type(self).__qualname__}: no HIP kernel covers this edge function / "
                     "dtype / shape and tiga.config.strict is set")
-            if not graph.is_varlen:
-                self._validate_fields("edge", edge, graph.num_edges, device)
             self._record_variant(CompiledVariant(
                 key=(type(self).__qualname__, "eager", graph.planning_key()),
                 backend="torch-eager", provider="torch", pattern="generic",
                 lowering="gather -> edge() -> scatter reduce (Torch ops)",
                 remarks=("edge function not covered by a HIP kernel",)))
-            aggregate = _eager.evaluate(self, graph, src, dst, edge, params)
-        else:
-            aggregate = result
-        if type(self).node is MessagePassing.node:
-            return aggregate
-        return _call_region(self.node, (SimpleNamespace(**dst), aggregate), params)
+            return _eager.evaluate(self, graph, src, dst, edge, params)
+        operands = launch.gather(src, dst, edge, params)
+        result = launch.runner(*operands)
+        # Described after the first run, which builds the per-graph row plan
+        # the description reports.
+        launch.variant = launch.describe()
+        self._launch = launch
+        self._record_variant(launch.variant)
+        if launch.guardable:
+            guarded = _Guarded(launch, self.reducer, operands, params)
+            guarded.names = _Guarded._names(src, dst, edge)
+            self._guarded = guarded
+        return result
 
-    def reference(self, *, graph: Graph, src: Mapping[str, torch.Tensor],
-                  dst: Mapping[str, torch.Tensor],
-                  edge: Mapping[str, torch.Tensor] | None = None, **params: Any):
+    def prepare(self, *, graph: Graph, src: Mapping[str, torch.Tensor] | None = None,
+                dst: Mapping[str, torch.Tensor] | None = None,
+                edge: Mapping[str, torch.Tensor] | None = None,
+                ndata: Mapping[str, torch.Tensor] | None = None, **params: Any):
+        """One ordinary call (validation, capture, planning), then the HIP
+        launch it ran frozen as a zero-argument callable: the graph object,
+        the bound tensors, shapes and strides are fixed; their contents stay
+        live, so in-place updates between launches are seen (reference
+        message_passing/core.py:563-590, interop/torch/message_passing.py:
+        3827-3879).  The callable carries ``.variant`` and ``.graph``.
+        Raises NotImplementedError when the call ran the eager evaluator."""
+        src, dst = _resolve_node_fields(graph, src, dst, ndata)
+        edge = {} if edge is None else edge
+        self(graph=graph, src=src, dst=dst, edge=edge, **params)
+        launch = self._launch
+        if launch is None or launch.graph is not graph:
+            raise NotImplementedError(
+                "prepared MessagePassing needs an edge function, dtype and shape that a HIP "
+                f"kernel covers; this call ran {self.last_variant.backend}")
+        operands = tuple(launch.gather(src, dst, edge, params))
+        runner, epilogue = launch.runner, self._epilogue
+        frozen_dst, frozen_params = dict(dst), dict(params)
+
+        def run():
+            return epilogue(frozen_dst, runner(*operands), frozen_params)
+
+        run.variant = launch.variant
+        run.graph = graph
+        return run
+
+    def reference(self, *, graph: Graph, src: Mapping[str, torch.Tensor] | None = None,
+                  dst: Mapping[str, torch.Tensor] | None = None,
+                  edge: Mapping[str, torch.Tensor] | None = None,
+                  ndata: Mapping[str, torch.Tensor] | None = None, **params: Any):
         """Run the eager Torch evaluator even where a HIP kernel exists
         (reference interop/torch/message_passing.py:2818-2894)."""
         if isinstance(self.reducer, OnlineSoftmaxReducer) and \
@@ -146,101 +324,133 @@ class MessagePassing(Kernel):
                 "result with an explicit accuracy budget")
         if not getattr(graph, "_tiga_graph", False):
             raise TypeError("graph must be a tiga.Graph")
+        src, dst = _resolve_node_fields(graph, src, dst, ndata)
         edge = {} if edge is None else edge
         device = graph.device
         self._validate_fields("src", src, graph.schema.num_src, device)
         self._validate_fields("dst", dst, graph.schema.num_dst, device)
-        if not graph.is_varlen:
+        if edge:
             self._validate_fields("edge", edge, graph.num_edges, device)
         aggregate = _eager.evaluate(self, graph, src, dst, edge, params)
-        if type(self).node is MessagePassing.node:
-            return aggregate
-        return _call_region(self.node, (SimpleNamespace(**dst), aggregate), params)
+        return self._epilogue(dst, aggregate, params)
 
     # ------------------------------------------------------------------
-    def _record_native(self, graph, pattern: str, entry_points, lowering, remarks=()):
+    def _variant(self, graph, pattern: str, entry_points, lowering, remarks=()):
+        """The variant record of a (kernel, pattern) on `graph`, built once and
+        kept with the graph's other per-graph structures."""
         plan = graph._native_cache.get(("plan", 512, 512))
-        # The record of a (kernel, pattern) on this graph is built once and
-        # kept with the graph's other per-graph structures.
         memo = graph._native_cache.setdefault("variants", {})
         memo_key = (type(self).__qualname__, plan is not None, pattern, tuple(entry_points),
                     lowering, tuple(remarks))
         variant = memo.get(memo_key)
         if variant is None:
-            extra = () if plan is None else (f"row plan: {plan.counts()}",)
+            extra = () if plan is None else (f"row plan: {plan.counts()}",
+                                            *graph._reference_plan_remarks(
+                                                type(self).node is not MessagePassing.node))
             variant = CompiledVariant(
                 key=(type(self).__qualname__, pattern, graph.planning_key()),
                 backend="hip", provider="libtgx_hip.so (gfx950)", pattern=pattern,
                 lowering=lowering, entry_points=tuple(entry_points),
                 remarks=tuple(remarks) + extra)
             memo[memo_key] = variant
-        self._record_variant(variant)
+        return variant
 
-    def _execute_native(self, captured, graph, src, dst, edge, params):
-        from . import _ops
+    @staticmethod
+    def _binding(tensor, params) -> tuple:
+        """Binding of a tensor the capture found inside the edge function: the
+        parameter it was passed as, else ("fixed", tensor)."""
+        for name, value in params.items():
+            if value is tensor:
+                return ("param", name)
+        return ("fixed", tensor)
 
+    def _plan_native(self, captured, graph, src, dst, edge, params) -> _Launch | None:
         if isinstance(self.reducer, SumReducer):
-            if self.reducer.identity_value != 0 or graph.is_varlen or graph.is_dense:
-                return None
-            pat = cap.recognize_weighted_sum(captured)
-            if pat is None or pat.src_field not in src:
-                return None
-            x = src[pat.src_field]
-            w = None
-            if pat.edge_field is not None:
-                if pat.edge_field not in edge:
-                    return None
-                w = edge[pat.edge_field]
-                E = graph.num_edges
-                if tuple(w.shape) not in ((E,), (E, 1)) or w.dtype != torch.float32:
-                    return None
-                if x.ndim == 1 and w.ndim == 2:
-                    return None
-            if x.dtype != torch.float32:
-                return None
-            _native.lib()
-            out = _ops.CsrSumFunction.apply(x, w, graph)
-            self._record_native(graph, "weighted-sum", ("tgx_csr_sum_fwd", "tgx_csr_sum_bwd"),
-                                "degree-binned rows -> wave gather-FMA (fp32)")
-            return out
-
+            return self._plan_sum(captured, graph, src, edge)
         if not isinstance(self.reducer, OnlineSoftmaxReducer):
             return None
+        if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
+            return None
         gat = cap.recognize_gat(captured)
-        if gat is not None and not graph.is_varlen and not graph.is_dense:
-            h = src.get(gat.h_field)
-            hd = dst.get(gat.dst_field)
-            if h is None or hd is None or hd is not h:
-                return None
-            if graph.schema.num_src != graph.schema.num_dst or h.ndim != 3:
-                return None
-            N, H, D = h.shape
-            if h.dtype != torch.float32 or tuple(gat.a_src.shape) not in ((H, D), (1, H, D)) \
-                    or tuple(gat.a_dst.shape) not in ((H, D), (1, H, D)):
-                return None
-            if gat.a_src.dtype != torch.float32 or gat.a_dst.dtype != torch.float32:
-                return None
-            if gat.a_src.device != h.device or gat.a_dst.device != h.device:
-                return None
-            if H * D not in (64, 128, 256) or D % 4:
-                return None
-            if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
-                return None
-            _native.lib()
-            out = _ops.GatFunction.apply(h, gat.a_src, gat.a_dst, gat.slope, graph)
-            self._record_native(graph, "gat-additive", ("tgx_gat_fwd", "tgx_gat_bwd"),
-                                "online softmax per (row, head), logsumexp saved; "
-                                "backward recomputes alpha over the transposed CSR")
-            return out
+        if gat is not None:
+            return self._plan_gat(gat, graph, src, dst, params)
         dot = cap.recognize_dot(captured)
         if dot is not None:
-            return self._execute_dot(dot, graph, src, dst, edge)
+            return self._plan_dot(dot, graph, src, dst, edge)
         nn_item = cap.recognize_nn_attention(captured)
         if nn_item is not None:
-            return self._execute_nn_attention(nn_item, graph, src, dst, edge)
+            return self._plan_nn_attention(nn_item, graph, src, dst, edge)
         return None
 
-    def _execute_nn_attention(self, item, graph, src, dst, edge):
+    def _plan_sum(self, captured, graph, src, edge) -> _Launch | None:
+        from . import _ops
+
+        if self.reducer.identity_value != 0 or graph.is_varlen or graph.is_dense:
+            return None
+        pat = cap.recognize_weighted_sum(captured)
+        if pat is None or pat.src_field not in src:
+            return None
+        x = src[pat.src_field]
+        if x.dtype != torch.float32:
+            return None
+        operands = [("src", pat.src_field)]
+        if pat.edge_field is not None:
+            w = edge.get(pat.edge_field)
+            if w is None:
+                return None
+            E = graph.num_edges
+            if tuple(w.shape) not in ((E,), (E, 1)) or w.dtype != torch.float32:
+                return None
+            if x.ndim == 1 and w.ndim == 2:
+                return None
+            operands.append(("edge", pat.edge_field))
+        _native.lib()
+
+        def run(x, w=None):
+            return _ops.CsrSumFunction.apply(x, w, graph)
+
+        describe = lambda: self._variant(
+            graph, "weighted-sum", ("tgx_csr_sum_fwd", "tgx_csr_sum_bwd"),
+            "degree-binned rows -> wave gather-FMA (fp32)")
+        return _Launch(graph, tuple(operands), run, describe)
+
+    def _plan_gat(self, gat, graph, src, dst, params) -> _Launch | None:
+        from . import _ops
+
+        if graph.is_varlen or graph.is_dense:
+            return None
+        h = src.get(gat.h_field)
+        hd = dst.get(gat.dst_field)
+        if h is None or hd is None or hd is not h:
+            return None
+        if graph.schema.num_src != graph.schema.num_dst or h.ndim != 3:
+            return None
+        N, H, D = h.shape
+        if h.dtype != torch.float32 or tuple(gat.a_src.shape) not in ((H, D), (1, H, D)) \
+                or tuple(gat.a_dst.shape) not in ((H, D), (1, H, D)):
+            return None
+        if gat.a_src.dtype != torch.float32 or gat.a_dst.dtype != torch.float32:
+            return None
+        if gat.a_src.device != h.device or gat.a_dst.device != h.device:
+            return None
+        if H * D not in (64, 128, 256) or D % 4:
+            return None
+        _native.lib()
+        slope = gat.slope
+
+        def run(h, _h_dst, a_src, a_dst):
+            return _ops.GatFunction.apply(h, a_src, a_dst, slope, graph)
+
+        describe = lambda: self._variant(
+            graph, "gat-additive", ("tgx_gat_fwd", "tgx_gat_bwd"),
+            "online softmax per (row, head), logsumexp saved; backward recomputes alpha "
+            "over the transposed CSR")
+        operands = (("src", gat.h_field), ("dst", gat.dst_field),
+                    self._binding(gat.a_src, params), self._binding(gat.a_dst, params))
+        return _Launch(graph, operands, run, describe,
+                       aliases=((("src", gat.h_field), ("dst", gat.dst_field)),))
+
+    def _plan_nn_attention(self, item, graph, src, dst, edge) -> _Launch | None:
         """tg.nn.trace-scored attention on the edge MLP kernels (reference
         interop/torch/message_passing.py:2372-2577, envelope: fp32, CSR
         relation, one score per edge, one gathered value field)."""
@@ -248,42 +458,51 @@ class MessagePassing(Kernel):
 
         if graph.is_varlen or graph.is_dense:
             return None
-        if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
-            return None
         groups = {"src": src, "dst": dst, "edge": edge}
         rows = {"src": graph.schema.num_src, "dst": graph.schema.num_dst,
                 "edge": graph.num_edges}
-        fields, roles = [], []
+        widths, roles = [], []
         for role, name in item.inputs:
             t = groups[role].get(name)
             if t is None or t.dtype != torch.float32 or t.ndim not in (1, 2) or \
                     t.shape[0] != rows[role]:
                 return None
-            fields.append(t if t.ndim == 2 else t.unsqueeze(-1))
+            widths.append(1 if t.ndim == 1 else t.shape[1])
             roles.append(role)
-        if len(fields) > 4 or sum(f.shape[1] for f in fields) > 64:
+        if len(widths) > 4 or sum(widths) > 64:
+            return None
+        chain = item.module.chain()
+        if sum(widths) != chain[0].linear.in_features:
+            # The eager evaluator raises the network's own shape error.
             return None
         value = src.get(item.value_field)
         if value is None or value.dtype != torch.float32:
             return None
-        chain = item.module.chain()
         for layer in chain:
             for p in (layer.linear.weight, layer.linear.bias):
                 if p is not None and (p.dtype != torch.float32 or p.device != value.device):
                     return None
         _native.lib()
-        out = _ops.nn_attention(graph, chain, roles, fields, value)
-        widths = "-".join(str(l.linear.in_features) for l in chain) + "-1"
-        self._record_native(
+        roles = tuple(roles)
+
+        def run(module, value, *fields):
+            return _ops.nn_attention(graph, module.chain(), roles,
+                                     [f if f.ndim == 2 else f.unsqueeze(-1) for f in fields],
+                                     value)
+
+        layer_widths = "-".join(str(l.linear.in_features) for l in chain) + "-1"
+        describe = lambda: self._variant(
             graph, "nn-attention",
             ("tgx_edge_mlp_scores", "tgx_segment_softmax_fwd", "tgx_csr_sum_fwd",
              "tgx_csr_sum_bwd", "tgx_segment_softmax_bwd", "tgx_edge_mlp_backward"),
-            f"edge-parallel score network {widths} (one edge per lane, uniform weights), "
-            "segment softmax per row, weighted CSR sum of the value; backward through the "
-            "softmax Jacobian, per-edge network replay, weight gradients as GEMMs")
-        return out
+            f"edge-parallel score network {layer_widths} (one edge per lane, uniform "
+            "weights), segment softmax per row, weighted CSR sum of the value; backward "
+            "through the softmax Jacobian, per-edge network replay, on-chip weight-gradient "
+            "sums")
+        operands = (("fixed", item.module), ("src", item.value_field), *item.inputs)
+        return _Launch(graph, operands, run, describe)
 
-    def _execute_dot(self, dot, graph, src, dst, edge):
+    def _plan_dot(self, dot, graph, src, dst, edge) -> _Launch | None:
         from . import _ops
 
         q, k, v = dst.get(dot.q_field), src.get(dot.k_field), src.get(dot.v_field)
@@ -291,37 +510,36 @@ class MessagePassing(Kernel):
             return None
         if q.ndim != 3 or k.shape[1:] != q.shape[1:] or v.shape[1:] != q.shape[1:]:
             return None
-        _, H, D = q.shape
-        if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
-            return None
         if graph.is_varlen or graph.is_dense:
-            return self._execute_block_attention(dot, graph, q, k, v)
+            return self._plan_block_attention(dot, graph, q, k, v)
+        _, H, D = q.shape
         if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
             return None
         if D % 8 or H * D not in (128, 256, 512):
             return None
-        bias = None
+        operands = [("dst", dot.q_field), ("src", dot.k_field), ("src", dot.v_field)]
         if dot.bias_field is not None:
             bias = edge.get(dot.bias_field)
             if bias is None or bias.dtype != torch.float32:
                 return None
-            if graph.is_varlen:
-                return None
             if tuple(bias.shape) not in ((graph.num_edges, H), (graph.num_edges, H, 1)):
                 return None
-            bias = bias.reshape(graph.num_edges, H)
-        if graph.is_varlen:
-            return None
+            operands.append(("edge", dot.bias_field))
         _native.lib()
-        out = _ops.DotAttnFunction.apply(q, k, v, bias, dot.scale, graph)
-        self._record_native(graph, "dot-product", ("tgx_dot_attn_fwd", "tgx_dot_attn_bwd"),
-                            "bf16 gathers, fp32 online softmax per (row, head); hub rows "
-                            "split and merged; backward over CSR (dq, dbias) and transposed "
-                            "CSR (dk, dv)")
-        return out
+        scale, E = dot.scale, graph.num_edges
 
+        def run(q, k, v, bias=None):
+            if bias is not None:
+                bias = bias.reshape(E, H)
+            return _ops.DotAttnFunction.apply(q, k, v, bias, scale, graph)
 
-    def _execute_block_attention(self, dot, graph, q, k, v):
+        describe = lambda: self._variant(
+            graph, "dot-product", ("tgx_dot_attn_fwd", "tgx_dot_attn_bwd"),
+            "bf16 gathers, fp32 online softmax per (row, head); hub rows split and merged; "
+            "backward over CSR (dq, dbias) and transposed CSR (dk, dv)")
+        return _Launch(graph, tuple(operands), run, describe)
+
+    def _plan_block_attention(self, dot, graph, q, k, v) -> _Launch | None:
         """Dot-product attention over Graph.cu_seqlens / dense / triangular
         on MFMA tiles (reference: eager oracle for varlen, compiled fp16
         dense streaming tile for dense/triangular, message_passing.py:
@@ -339,22 +557,27 @@ class MessagePassing(Kernel):
                 v.shape[0] != graph.schema.num_src:
             return None
         prune = self.reducer.block_prune_threshold
-        if prune is not None and torch.is_grad_enabled() and \
-                any(t.requires_grad for t in (q, k, v)):
-            raise NotImplementedError(
-                "block_prune_threshold is a forward-only approximation (no gradient); run "
-                "it under torch.no_grad() or drop the threshold for exact softmax")
         _native.lib()
-        out = _ops.BlockAttentionFunction.apply(q, k, v, dot.scale, float(prune or 0.0), graph)
-        relation = ("cu_seqlens" if graph.is_varlen else graph.schema.origin)
+        scale = dot.scale
+
+        def run(q, k, v):
+            if prune is not None and torch.is_grad_enabled() and \
+                    any(t.requires_grad for t in (q, k, v)):
+                raise NotImplementedError(
+                    "block_prune_threshold is a forward-only approximation (no gradient); run "
+                    "it under torch.no_grad() or drop the threshold for exact softmax")
+            return _ops.BlockAttentionFunction.apply(q, k, v, scale, float(prune or 0.0), graph)
+
+        relation = "cu_seqlens" if graph.is_varlen else graph.schema.origin
         causal = graph._attn_blocks()[2]
-        self._record_native(
+        describe = lambda: self._variant(
             graph, "block-attention", ("tgx_attn_fwd", "tgx_attn_bwd"),
             f"MFMA 16x16x32 {str(q.dtype).split('.')[-1]} flash tiles over the implicit "
             f"{relation} relation ({'causal' if causal else 'all pairs'}); XCD-grouped "
             "tasks; atomic-free dK/dV and dQ passes",
             remarks=(("block-pruned tile admission (approximate)",) if prune else ()))
-        return out
+        operands = (("dst", dot.q_field), ("src", dot.k_field), ("src", dot.v_field))
+        return _Launch(graph, operands, run, describe)
 
 
 __all__ = ["MessagePassing", "config"]

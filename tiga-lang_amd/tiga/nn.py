@@ -19,10 +19,15 @@ at most 64.  Anything else runs on the eager evaluator.
 
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 
 import torch
 from torch import nn
+
+# Score chains by module object: tracing a module with torch.fx costs
+# milliseconds, and edge() usually wraps the same module on every call.
+_CHAINS: "weakref.WeakKeyDictionary[nn.Module, object]" = weakref.WeakKeyDictionary()
 
 _ACT = {"identity": 0, "relu": 1, "leaky_relu": 2, "tanh": 3, "sigmoid": 4, "silu": 5,
         "gelu": 6, "elu": 7}
@@ -62,12 +67,18 @@ class TracedModule(nn.Module):
         return super().__call__(*inputs)
 
     def chain(self) -> tuple[ScoreLayer, ...] | None:
-        """The module as a score chain the HIP kernels cover, else None."""
+        """The module as a score chain the HIP kernels cover, else None.
+        Computed once per module object (a module whose layers are replaced
+        afterwards must be wrapped anew by a fresh module object)."""
         if self._chain is False:
-            try:
-                self._chain = _extract_chain(self.module)
-            except NotImplementedError:
-                self._chain = None
+            got = _CHAINS.get(self.module, False)
+            if got is False:
+                try:
+                    got = _extract_chain(self.module)
+                except NotImplementedError:
+                    got = None
+                _CHAINS[self.module] = got
+            self._chain = got
         return self._chain
 
 

@@ -15,7 +15,8 @@ from typing import Any
 
 @dataclass(frozen=True)
 class ReducerCall:
-    """A staged binding between one reducer and its edge-local messages."""
+    """What ``reducer(*messages)`` returns inside ``edge()``: the reducer and
+    the per-edge message expressions it will reduce."""
 
     reducer: "Reducer"
     messages: tuple[Any, ...]
@@ -23,7 +24,8 @@ class ReducerCall:
 
 @dataclass(frozen=True)
 class OnlineSoftmaxItem:
-    """Staged (score, value) pair accepted by ``OnlineSoftmaxReducer``."""
+    """What ``online_softmax()(score, value)`` returns inside ``edge()``: the
+    per-edge score [E, *lanes] and value [E, *lanes, *payload] to reduce."""
 
     score: Any
     value: Any
