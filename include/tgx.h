@@ -289,6 +289,23 @@ int tgx_dot_attn_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                      void* out_dev, float* ml_dev, int64_t n_dst, int64_t n_src, int H,
                      int D, float* partial_dev, void* stream);
 
+/* tgx_dot_attn_fwd without the partial_dev argument: the split-row partials
+ * go to a static device array of 64 MiB per device (held until the process
+ * ends), so the call allocates nothing.  No counterpart in the reference: it
+ * is for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  Plans whose chunks need more than
+ * 64 MiB of partials ((H*D + 2*H) * 4 bytes per chunk) are rejected with
+ * TGX_INVALID_ARGUMENT before any launch.  Uses the current device's array
+ * (`stream` must belong to the current device); every call on one device
+ * shares it, so calls that overlap on one device (concurrent streams or
+ * threads) race.  No part of the array needs to start at zero: every chunk
+ * writes its partial before the merge reads it. */
+int tgx_dot_attn_fwd_noalloc(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                             const tgx_row_plan* plan, const void* q_dev, const void* k_dev,
+                             const void* v_dev, const float* bias_dev, float scale,
+                             void* out_dev, float* ml_dev, int64_t n_dst, int64_t n_src,
+                             int H, int D, void* stream);
+
 /* Workspace bytes for tgx_dot_attn_bwd with these plans. */
 int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
                                int H, int D, size_t* bytes);

@@ -43,17 +43,25 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def build(verbose: bool = False, jobs: int = 8) -> Path:
-    """Compile every source to an object in parallel, then link the .so."""
+def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Path:
+    """Compile every source to an object in parallel, then link the .so.
+
+    incremental=True reuses an object that is newer than its source and
+    every header (for development; the default compiles everything)."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     obj_dir = HERE / "_build"
     obj_dir.mkdir(exist_ok=True)
     hipcc = _hipcc()
     procs = []
     objects = []
+    headers = [*CSRC.glob("*.h"), *INCLUDE.glob("*.h")]
+    newest_header = max((h.stat().st_mtime for h in headers), default=0.0)
     for src in sources():
         obj = obj_dir / (src.name + ".o")
         objects.append(obj)
+        if incremental and obj.exists() and \
+                obj.stat().st_mtime > max(src.stat().st_mtime, newest_header):
+            continue
         cmd = [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
         if src.suffix == ".cpp":
             cmd = [hipcc, f"--offload-arch={ARCH}", "-O2", "-fPIC", "-std=c++17",
@@ -86,5 +94,5 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv)
     print(path)

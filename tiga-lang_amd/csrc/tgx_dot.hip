@@ -24,6 +24,9 @@
 //   summed in chunk order.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "tgx_device.h"
 #include "tgx_host.h"
 #include "tgx_profile.h"
@@ -684,4 +687,73 @@ extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bi
 #undef TGX_DOT_BWD
   set_error("unsupported dot attention shape");
   return TGX_UNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
+// Forward without a caller buffer: the split-row partials live in a static
+// device array.  For callers that cannot allocate (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc).
+namespace tgx {
+namespace {
+
+constexpr size_t kScratchBytes = size_t(64) << 20;   // 64 MiB per device
+// Host code must never use this name as an address: it is a host-side
+// stand-in.  The device address comes from hipGetSymbolAddress, per device.
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_init;
+
+// Device address of `scratch` on the current device, looked up on the first
+// call on that device (with that device current) and kept.
+int scratch_on_current_device(float** out) {
+  int dev = -1;
+  TGX_HIP(hipGetDevice(&dev));
+  TGX_REQUIRE(dev >= 0 && dev < kMaxDevices, "device ordinal %d out of range", dev);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_init);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      TGX_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+      TGX_REQUIRE(ptr != nullptr, "no device address for the static scratch");
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = static_cast<float*>(ptr);
+  return TGX_OK;
+}
+
+}  // namespace
+}  // namespace tgx
+
+extern "C" int tgx_dot_attn_fwd_noalloc(const void* row_ptr, const void* col, int idx_bits,
+                                        const tgx_row_plan* plan, const void* q,
+                                        const void* k, const void* v, const float* bias,
+                                        float scale, void* out, float* ml, int64_t n_dst,
+                                        int64_t n_src, int H, int D, void* stream) {
+  // Every size check comes before any HIP call.
+  TGX_REQUIRE(plan != nullptr, "null plan");
+  DotShape shp;
+  if (!dot_shape(H, D, &shp)) {
+    set_error("dot attention supports D %% 8 == 0 and H*D in {128,256,512} (got H=%d D=%d)",
+              H, D);
+    return TGX_UNSUPPORTED;
+  }
+  TGX_REQUIRE(plan->n_chunks >= 0, "inconsistent plan");
+  const size_t per_chunk = (static_cast<size_t>(H) * D + 2 * static_cast<size_t>(H)) *
+                           sizeof(float);
+  TGX_REQUIRE(static_cast<size_t>(plan->n_chunks) <= kScratchBytes / per_chunk,
+              "%lld split-row chunks need %zu bytes of partials; the static scratch holds "
+              "%zu bytes (64 MiB): use tgx_dot_attn_fwd with a caller buffer",
+              static_cast<long long>(plan->n_chunks),
+              static_cast<size_t>(plan->n_chunks) * per_chunk, kScratchBytes);
+  float* partial = nullptr;
+  if (plan->n_chunks > 0 && n_dst > 0) {
+    const int st = scratch_on_current_device(&partial);
+    if (st != TGX_OK) return st;
+  }
+  return tgx_dot_attn_fwd(row_ptr, col, idx_bits, plan, q, k, v, bias, scale, out, ml, n_dst,
+                          n_src, H, D, partial, stream);
 }

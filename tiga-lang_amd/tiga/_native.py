@@ -86,6 +86,8 @@ _SIGNATURES: dict[str, list] = {
                     c_int, c_int, c_vp, c_size, c_vp],
     "tgx_dot_attn_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_f32, c_vp,
                          c_vp, c_i64, c_i64, c_int, c_int, c_vp, c_vp],
+    "tgx_dot_attn_fwd_noalloc": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp,
+                                 c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_vp],
     "tgx_dot_attn_bwd_workspace": [P(RowPlan), P(RowPlan), c_int, c_int, P(c_size)],
     "tgx_dot_attn_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, P(RowPlan), c_vp,
                          c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
