@@ -9,9 +9,12 @@ roofline (algorithmic bytes / its live HIP-event duration) and the
 reference's CPU path timed on a bounded sample of the same workload.
 
   python bench.py [--steps K] [--warmup W]
-                  [--config c1..c5|dense|dense-causal|dense-pruned|nn]
+                  [--config all|c1..c5|dense|dense-causal|dense-pruned|nn]
                   [--no-cpu] [--no-cold] [--no-graph]
 
+By default (--config all) the line is C2's and carries C1, C3, C4 and C5 as
+complete sub-lines under "configs" (same fields, each with the roofline of
+its own dominant kernel and its CPU baseline), all measured in this run.
 c1-c5 are BASELINE.json's configurations; dense* are the reference's dense
 attention benchmark shapes (N=4096, H=16, D=64, fp16, forward); nn is the
 reference's nn-scored GAT training step (131072 nodes, net 19-16-1).
@@ -52,9 +55,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "c5", "dense", "dense-causal",
-                             "dense-pruned", "nn"])
+    ap.add_argument("--config", default="all",
+                    choices=["all", "c1", "c2", "c3", "c4", "c5", "dense", "dense-causal",
+                             "dense-pruned", "nn"],
+                    help="all (default): C2 as the headline line with C1, C3, C4 and C5 "
+                         "under its 'configs' key")
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true",
@@ -209,6 +214,33 @@ def cpu_baseline_gat(row_ptr, col, h, a_src, a_dst, slope, rows):
             "sample": f"reference eager Torch CPU path (gather, scatter_reduce amax, exp, "
                       f"index_add, autograd), fwd+bwd on the first {rows} destination rows "
                       f"({e} edges) gathering from the full 1M-node table, {reps} reps"}
+
+
+def timed_steps(step, steps):
+    """(seconds for `steps` steps, per-kernel totals).  The steps are timed
+    twice, back to back: first as they run for a user, bracketed by device
+    synchronisations (this gives `value` and `ms_per_step`); then again with
+    the library's HIP-event timer around every launch (tgx_profile_*), whose
+    per-kernel averages give the roofline.  The events cost host time per
+    launch (about 10 us each), which would inflate host-bound steps like C1's
+    if both came from one region; the kernels' own durations do not change."""
+    import torch
+
+    from tiga import _native
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    with _native.KernelTimer() as timer:
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        profiled = time.perf_counter() - t1
+    return elapsed, profiled, dict(timer.totals)
 
 
 def cold_step_ms(step, samples=5):
@@ -469,14 +501,7 @@ def run_c2(args):
         step()
     torch.cuda.synchronize()
     assert kernel.last_variant.backend == "hip"
-    with _native.KernelTimer() as timer:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-    per_kernel = {k: (n, ms) for k, (n, ms) in timer.totals.items()}
+    elapsed, profiled, per_kernel = timed_steps(step, args.steps)
     cold_ms = cold_step_ms(step)
     graph_ms = graph_step_ms(
         [h, a_src, a_dst],
@@ -515,6 +540,7 @@ def run_c2(args):
                         "gbs": (bytes_per[k] / (ms / n * 1e-3) / 1e9) if k in bytes_per else None}
                     for k, (n, ms) in sorted(per_kernel.items())},
     }
+    result["profiled_ms_per_step"] = profiled * 1e3 / args.steps
     if not args.no_cpu:
         rows = args.cpu_rows or min(N, 65536)
         result["cpu_baseline"] = cpu_baseline_gat(row_ptr, col, h, a_src, a_dst, slope, rows)
@@ -553,20 +579,14 @@ def run_c1(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    with _native.KernelTimer() as timer:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+    elapsed, profiled, totals = timed_steps(step, args.steps)
     cold_ms = cold_step_ms(step)
-    ones = torch.ones(N, F_, device=dev)
     graph_ms = graph_step_ms(
         [x, w],
-        lambda: kernel(graph=graph, src={"x": x}, dst={}, edge={"weight": w}).backward(ones))
+        lambda: kernel(graph=graph, src={"x": x}, dst={}, edge={"weight": w}).sum().backward())
     bytes_per = sum_kernel_bytes(N, N, E, F_)
-    dominant = max((k for k in timer.totals if k in bytes_per), key=lambda k: timer.totals[k][1])
-    n_launch, total_ms = timer.totals[dominant]
+    dominant = max((k for k in totals if k in bytes_per), key=lambda k: totals[k][1])
+    n_launch, total_ms = totals[dominant]
     achieved = bytes_per[dominant] / (total_ms / n_launch * 1e-3) / 1e9
     result = {
         "metric": "weighted-sum fwd+bwd edges/s, 100k x deg-16, F=64, 1xMI355X",
@@ -582,16 +602,18 @@ def run_c1(args):
                      "traffic": measured_traffic("c1", dominant)[0],
                      "traffic_source": measured_traffic("c1", dominant)[1],
                      "algorithmic_bytes": bytes_per[dominant]},
-        "kernels": {k: {"launches": n, "avg_ms": ms / n} for k, (n, ms) in timer.totals.items()},
+        "kernels": {k: {"launches": n, "avg_ms": ms / n} for k, (n, ms) in totals.items()},
+        "profiled_ms_per_step": profiled * 1e3 / args.steps,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_sum(row_ptr, col, x, w)
     return result
 
 
-def run_c3c4(args):
+def run_dot(args, phases=("c3", "c4")):
     """C3: dot-product attention forward, bf16, on R-MAT scale 21; C4: its
-    fused backward (transposed CSR built once, untimed)."""
+    fused backward (transposed CSR built once, untimed).  One graph and one
+    set of inputs serve both phases; returns {phase: result line}."""
     import torch
 
     import tiga as tg
@@ -630,72 +652,70 @@ def run_c3c4(args):
     setup = setup_times(graph, N)
     deg = (row_ptr[1:] - row_ptr[:-1])
     stats = {"max_in_degree": int(deg.max()), "empty_rows": int((deg == 0).sum())}
-    for _ in range(args.warmup):
-        if args.config == "c3":
-            with torch.no_grad():
-                fwd()
-        else:
-            out.backward(dout, retain_graph=True)
-    torch.cuda.synchronize()
-    with _native.KernelTimer() as timer:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            if args.config == "c3":
-                with torch.no_grad():
-                    fwd()
-            else:
-                q.grad = k.grad = v.grad = bias.grad = None
-                out.backward(dout, retain_graph=True)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-
-    def cold():
-        if args.config == "c3":
-            with torch.no_grad():
-                fwd()
-        else:
-            q.grad = k.grad = v.grad = bias.grad = None
-            out.backward(dout, retain_graph=True)
-
-    cold_ms = cold_step_ms(cold)
     bytes_per = dot_kernel_bytes(N, E, H, D)
-    names = ["dot_fwd_kernel"] if args.config == "c3" else [
-        "dot_delta_kernel", "dot_bwd_dst_kernel", "dot_bwd_src_kernel"]
-    step_bytes = sum(bytes_per[n] for n in names)
-    dominant = max((n for n in names if n in timer.totals), key=lambda n: timer.totals[n][1])
-    n_launch, total_ms = timer.totals[dominant]
-    achieved = bytes_per[dominant] / (total_ms / n_launch * 1e-3) / 1e9
-    ms = elapsed * 1e3 / args.steps
-    what = "forward" if args.config == "c3" else "fused backward"
-    result = {
-        "metric": f"dot-product edge attention {what} edges/s, R-MAT scale 21, bf16, 1xMI355X",
-        "value": E * args.steps / elapsed, "unit": "edges/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded R-MAT a=.57 b=.19 c=.19 d=.05, dedup; q,k,v,bias ~N(0,1))",
-        "config": {"workload": f"{args.config}-dot-attention-{'fwd' if args.config == 'c3' else 'bwd'}",
-                   "nodes": N, "edges": E, "heads": H, "head_dim": D, **stats},
-        "hbm_frac_step": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "cold_ms_per_step": cold_ms,
-        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": measured_traffic(args.config, dominant)[0],
-                     "traffic_source": measured_traffic(args.config, dominant)[1],
-                     "algorithmic_bytes": bytes_per[dominant]},
-        "kernels": {kk: {"launches": n, "avg_ms": t / n,
-                         "gbs": (bytes_per[kk] / (t / n * 1e-3) / 1e9) if kk in bytes_per else None}
-                    for kk, (n, t) in sorted(timer.totals.items())},
-        "setup_ms": setup,
-    }
+    cpu = None
     if not args.no_cpu:
-        fwd_rate, bwd_rate, threads, sample = cpu_baseline_dot(
-            row_ptr, col, q, k, v, bias, 1.0 / 8.0, dout)
-        result["cpu_baseline"] = {
-            "value": fwd_rate if args.config == "c3" else bwd_rate, "unit": "edges/s",
-            "cores": threads, "kind": "port",
-            "sample": sample + (", forward" if args.config == "c3" else
-                                ", backward = (fwd+bwd) - fwd")}
-    return result
+        cpu = cpu_baseline_dot(row_ptr, col, q, k, v, bias, 1.0 / 8.0, dout)
+
+    def forward_step():
+        with torch.no_grad():
+            fwd()
+
+    def backward_step():
+        q.grad = k.grad = v.grad = bias.grad = None
+        out.backward(dout, retain_graph=True)
+
+    results = {}
+    for phase in phases:
+        step = forward_step if phase == "c3" else backward_step
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        assert kernel.last_variant.backend == "hip"
+        elapsed, profiled, totals = timed_steps(step, args.steps)
+        cold_ms = cold_step_ms(step)
+        names = ["dot_fwd_kernel"] if phase == "c3" else [
+            "dot_delta_kernel", "dot_bwd_dst_kernel", "dot_bwd_src_kernel"]
+        step_bytes = sum(bytes_per[n] for n in names)
+        dominant = max((n for n in names if n in totals), key=lambda n: totals[n][1])
+        n_launch, total_ms = totals[dominant]
+        avg_ms = total_ms / n_launch
+        achieved = bytes_per[dominant] / (avg_ms * 1e-3) / 1e9
+        ms = elapsed * 1e3 / args.steps
+        what = "forward" if phase == "c3" else "fused backward"
+        traffic, source = measured_traffic(phase, dominant)
+        result = {
+            "metric": f"dot-product edge attention {what} edges/s, R-MAT scale 21, bf16, "
+                      "1xMI355X",
+            "value": E * args.steps / elapsed, "unit": "edges/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded R-MAT a=.57 b=.19 c=.19 d=.05, dedup; q,k,v,bias "
+                    "~N(0,1))",
+            "config": {"workload": f"{phase}-dot-attention-{'fwd' if phase == 'c3' else 'bwd'}",
+                       "nodes": N, "edges": E, "heads": H, "head_dim": D, **stats},
+            "hbm_frac_step": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "cold_ms_per_step": cold_ms,
+            "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                         "traffic": traffic, "traffic_source": source, "avg_ms": avg_ms,
+                         "algorithmic_bytes": bytes_per[dominant]},
+            "kernels": {kk: {"launches": n, "avg_ms": t / n,
+                             "gbs": (bytes_per[kk] / (t / n * 1e-3) / 1e9)
+                             if kk in bytes_per else None}
+                        for kk, (n, t) in sorted(totals.items())},
+            "profiled_ms_per_step": profiled * 1e3 / args.steps,
+            "setup_ms": setup,
+        }
+        if cpu is not None:
+            fwd_rate, bwd_rate, threads, sample = cpu
+            result["cpu_baseline"] = {
+                "value": fwd_rate if phase == "c3" else bwd_rate, "unit": "edges/s",
+                "cores": threads, "kind": "port",
+                "sample": sample + (", forward" if phase == "c3" else
+                                    ", backward = (fwd+bwd) - fwd")}
+        results[phase] = result
+    return results
 
 
 def setup_times(graph, N, reps=3):
@@ -775,12 +795,7 @@ def run_c5(args):
         step()
     torch.cuda.synchronize()
     assert kernel.last_variant.backend == "hip"
-    with _native.KernelTimer() as timer:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+    elapsed, profiled, totals = timed_steps(step, args.steps)
     cold_ms = cold_step_ms(step)
     pairs = int((lengths * (lengths + 1) // 2).sum())
     fwd_flops = 4.0 * H * D * pairs
@@ -789,7 +804,7 @@ def run_c5(args):
     tflops = step_flops / (ms * 1e-3) / 1e12
     kflops = {"varlen_fwd_kernel": fwd_flops, "varlen_dkdv_kernel": 2.0 * fwd_flops,
               "varlen_dq_kernel": 0.5 * fwd_flops}
-    per = {kk: (n, t) for kk, (n, t) in timer.totals.items()}
+    per = totals
     dominant = max((kk for kk in per if kk in kflops), key=lambda kk: per[kk][1])
     n_launch, total_ms = per[dominant]
     achieved = kflops[dominant] / (total_ms / n_launch * 1e-3) / 1e12
@@ -815,6 +830,7 @@ def run_c5(args):
                          "tflops": (kflops[kk] / (t / n * 1e-3) / 1e12) if kk in kflops else None}
                     for kk, (n, t) in sorted(per.items())},
     }
+    result["profiled_ms_per_step"] = profiled * 1e3 / args.steps
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_varlen(lengths, q, k, v, dout, D ** -0.5)
     return result
@@ -862,16 +878,11 @@ def run_dense(args):
         step()
     torch.cuda.synchronize()
     assert kernel.last_variant.backend == "hip"
-    with _native.KernelTimer() as timer:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+    elapsed, profiled, totals = timed_steps(step, args.steps)
     pairs = N * (N + 1) // 2 if causal else N * N
     flops = 4.0 * H * D * pairs            # useful: q.k and p.v per pair (pruned: as if dense)
     ms = elapsed * 1e3 / args.steps
-    n_launch, total_ms = timer.totals["varlen_fwd_kernel"]
+    n_launch, total_ms = totals["varlen_fwd_kernel"]
     kernel_ms = total_ms / n_launch
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     what = {"dense": "all pairs", "dense-causal": "lower-triangular",
@@ -890,7 +901,8 @@ def run_dense(args):
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
                      "avg_ms": kernel_ms},
-        "kernels": {kk: {"launches": n, "avg_ms": t / n} for kk, (n, t) in timer.totals.items()},
+        "kernels": {kk: {"launches": n, "avg_ms": t / n} for kk, (n, t) in totals.items()},
+        "profiled_ms_per_step": profiled * 1e3 / args.steps,
     }
 
 
@@ -946,12 +958,7 @@ def run_nn(args):
         step()
     torch.cuda.synchronize()
     assert kernel.last_variant.backend == "hip"
-    with _native.KernelTimer() as timer:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+    elapsed, profiled, totals = timed_steps(step, args.steps)
     ms = elapsed * 1e3 / args.steps
     # Algorithmic bytes per pass (no-reuse model, 4 B indices).  Per edge the
     # score pass reads col, dst, the 19 input floats (displacement 3, x_src 8,
@@ -964,7 +971,7 @@ def run_nn(args):
         "edge_mlp_bwd_kernel": E * (4 + 4 + inputs + 4 + inputs),
         "csr_sum_fwd": E * (4 + 4 + 32) + N * (4 + 32),
     }
-    per = timer.totals
+    per = totals
     dominant = max((k for k in per if k in bytes_per), key=lambda k: per[k][1])
     n_launch, total_ms = per[dominant]
     achieved = bytes_per[dominant] / (total_ms / n_launch * 1e-3) / 1e9
@@ -987,8 +994,49 @@ def run_nn(args):
                              "(weights in scalar registers), far from the HBM roof"},
         "kernels": {k: {"launches": n, "avg_ms": t / n} for k, (n, t) in sorted(per.items())},
     }
+    result["profiled_ms_per_step"] = profiled * 1e3 / args.steps
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_nn(row_ptr, col, x, disp, attn, min(N, 32768))
+    return result
+
+
+def _release_gpu_memory():
+    import gc
+
+    import torch
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def run_all(args):
+    """Every BASELINE configuration in one process: C2 (the headline) as the
+    top-level line, C1, C3, C4 and C5 under "configs", each with its own
+    step time, roofline of its dominant kernel and CPU baseline.  Progress
+    goes to stderr; stdout gets the one JSON line."""
+    t_all = time.perf_counter()
+
+    def progress(name, t0):
+        print(f"bench: {name} done in {time.perf_counter() - t0:.1f} s", file=sys.stderr,
+              flush=True)
+
+    t0 = time.perf_counter()
+    result = run_c2(args)
+    progress("c2", t0)
+    configs = {}
+    for name, fn in (("c1", run_c1), ("c3+c4", lambda a: run_dot(a, ("c3", "c4"))),
+                     ("c5", run_c5)):
+        _release_gpu_memory()
+        t0 = time.perf_counter()
+        got = fn(args)
+        configs.update(got if name == "c3+c4" else {name: got})
+        progress(name, t0)
+    for sub in configs.values():
+        if isinstance(sub.get("cpu_baseline"), dict):
+            sub["cpu_baseline"]["cpu_model"] = cpu_model()
+    result["configs"] = configs
+    result["bench_wall_s"] = time.perf_counter() - t_all
     return result
 
 
@@ -1060,10 +1108,14 @@ def main():
               "(collectives and sharding are out of scope); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-    runners = {"c1": run_c1, "c2": run_c2, "c3": run_c3c4, "c4": run_c3c4, "c5": run_c5,
+    runners = {"c1": run_c1, "c2": run_c2, "c3": lambda a: run_dot(a, ("c3",))["c3"],
+               "c4": lambda a: run_dot(a, ("c4",))["c4"], "c5": run_c5,
                "dense": run_dense, "dense-causal": run_dense, "dense-pruned": run_dense,
                "nn": run_nn}
-    result = runners[args.config](args)
+    if args.config == "all":
+        result = run_all(args)
+    else:
+        result = runners[args.config](args)
     if isinstance(result.get("cpu_baseline"), dict):
         result["cpu_baseline"]["cpu_model"] = cpu_model()
     roofs = measured_roofs()

@@ -99,3 +99,23 @@ def nn_gat_step(row_ptr, col, x, disp, net, dout):
     out = reduce_online_softmax(score, x[col], destination, num_dst)
     out.backward(dout)
     return out, x.grad, disp.grad
+
+
+def dot_reference(row_ptr, col, q, k, v, bias, scale, dout):
+    """The reference's eager arithmetic for dot-product attention, forward
+    and backward, in the inputs' own dtypes: for bf16 q/k/v the products
+    k[col] * q[dst] and their sum over D are bf16 (Torch's bf16 ops), the
+    fp32 bias promotes the score to fp32, reduce_online_softmax accumulates
+    in fp32 and casts the output back to bf16 (reducer_oracle.py:22-41, 87-91,
+    137); Torch autograd gives the gradients.  Returns (out, dq, dk, dv,
+    dbias) (dbias None without a bias)."""
+    destination = destination_index(row_ptr)
+    num_dst = row_ptr.numel() - 1
+    q, k, v = (t.detach().requires_grad_(True) for t in (q, k, v))
+    b = None if bias is None else bias.detach().requires_grad_(True)
+    score = (k[col] * q[destination]).sum(dim=-1) * scale
+    if b is not None:
+        score = score + b
+    out = reduce_online_softmax(score, v[col], destination, num_dst)
+    out.backward(dout)
+    return out.detach(), q.grad, k.grad, v.grad, None if b is None else b.grad

@@ -1,0 +1,193 @@
+"""GPU value parity at the benchmark configurations' full sizes, and against
+the reference's own bf16 arithmetic.
+
+* C2 (GAT fp32, 1M nodes, 17M edges): out, dh, da_src and da_dst against
+  the row-chunked float64 restatement (oracle/chunked.py, pinned against
+  oracle/ref.py in tests/test_oracle.py), max|gpu - oracle| <= 1e-5 *
+  max|oracle| per tensor.  da_src / da_dst are 17M-edge reductions.
+  LeakyReLU's derivative jumps at z = 0: among 136M (edge, head) pairs a
+  few have fp32 and fp64 values of z on opposite sides of 0, where the two
+  derivatives differ by (1 - slope) * dscore.  The checker takes the piece
+  from the kernel's own fp32 z (its saved node state holds both halves of
+  z; the kernel adds them in fp32, which the checker repeats exactly), after
+  checking those halves against fp64 math; the count of such pairs is
+  printed.
+* C3 (dot-product bf16, R-MAT scale 21): out on every row above 512 edges
+  (the split hub rows) and on a seeded sample of other rows, 2e-2.
+* C4 (its fused backward): dq, dk, dv and dbias over the whole graph, 2e-2.
+* bf16 arithmetic: on an R-MAT scale-12 graph the HIP dot-product forward
+  and backward against the reference's eager path run in bf16 on the CPU
+  (oracle/eager_torch.dot_reference: bf16 q*k products and sums, fp32 bias
+  and softmax accumulation, bf16 output) and against float64 math.  Against
+  float64 the bar is 2e-2.  Against the reference's bf16 results it is 2e-2
+  plus that result's own distance from float64: the reference's autograd
+  sums dk and dv into bf16 leaves (index_add in bf16), which over a hub's
+  many out-edges moves it several 1e-2 from exact math, while these kernels
+  accumulate in fp32.
+
+The float64 checker runs with Torch's own float64 kernels on the GPU (the
+CPU would take minutes at these sizes); the bf16 inputs enter it exactly.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import tiga as tg
+from oracle import chunked, eager_torch, ref
+
+from test_gpu_fullsize import DotAttention, gat, poisson_self_loop, rmat
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+SEED = 20260822
+
+
+@pytest.fixture(autouse=True)
+def _strict():
+    tg.config.strict = True
+    yield
+    tg.config.strict = False
+
+
+def rel(actual, expected) -> float:
+    a, e = actual.double(), expected.double()
+    return float((a - e).abs().max() / e.abs().max().clamp_min(1e-300))
+
+
+def test_c2_full_size_values_against_float64():
+    print("c2 full size values: 1M nodes, fp64 checker", flush=True)
+    row_ptr, col = poisson_self_loop(1_000_000, 16.0, SEED)
+    N, H, D = row_ptr.numel() - 1, 8, 32
+    graph = tg.Graph.from_csr(row_ptr, col, num_src=N)
+    g = torch.Generator(device=DEV).manual_seed(SEED + 1)
+    h = torch.randn(N, H, D, device=DEV, generator=g).requires_grad_(True)
+    a_src = (0.1 * torch.randn(H, D, device=DEV, generator=g)).requires_grad_(True)
+    a_dst = (0.1 * torch.randn(H, D, device=DEV, generator=g)).requires_grad_(True)
+    dout = torch.randn(N, H, D, device=DEV, generator=g)
+    kernel = gat(a_src, a_dst)
+    out = kernel(graph=graph, src={"h": h}, dst={"h": h})
+    assert kernel.last_variant.backend == "hip"
+    # The kernel's own fp32 halves of z (node state slots 3 and 2: a_src.h,
+    # a_dst.h), read before the backward reuses slot 1.
+    node_state = out.grad_fn.saved_tensors[4]
+    branch = (node_state[..., 3].clone(), node_state[..., 2].clone())
+    out.backward(dout)
+    torch.cuda.synchronize()
+    d = lambda t: t.detach().double()
+    # The halves agree with fp64 math to fp32 rounding.
+    assert rel(branch[0], (d(h) * d(a_src)).sum(-1)) <= 1e-6
+    assert rel(branch[1], (d(h) * d(a_dst)).sum(-1)) <= 1e-6
+    e_out, _ = chunked.gat_fwd(row_ptr, col, d(h), d(a_src), d(a_dst), 0.2)
+    assert rel(out.detach(), e_out) <= 1e-5
+    del e_out
+    stats = {}
+    e_dh, e_das, e_dad = chunked.gat_bwd(row_ptr, col, d(h), d(a_src), d(a_dst), 0.2, d(dout),
+                                         branch=branch, stats=stats)
+    errs = {"dh": rel(h.grad, e_dh), "da_src": rel(a_src.grad, e_das),
+            "da_dst": rel(a_dst.grad, e_dad)}
+    print(f"c2 relative errors {errs}; (edge, head) pairs whose fp32 and fp64 z straddle "
+          f"the LeakyReLU kink: {stats['kink_flips']}", flush=True)
+    assert all(e <= 1e-5 for e in errs.values()), errs
+
+
+@pytest.fixture(scope="module")
+def c34():
+    row_ptr, col = rmat(21, 16, SEED)
+    N, E, H, D = row_ptr.numel() - 1, col.numel(), 4, 64
+    g = torch.Generator(device=DEV).manual_seed(SEED + 1)
+    mk = lambda: torch.randn(N, H, D, device=DEV, generator=g).to(torch.bfloat16)
+    q, k, v = (mk().requires_grad_(True) for _ in range(3))
+    bias = torch.randn(E, H, device=DEV, generator=g).requires_grad_(True)
+    dout = mk()
+    return row_ptr, col, tg.Graph.from_csr(row_ptr, col, num_src=N), q, k, v, bias, dout
+
+
+def test_c3_full_size_hub_rows_and_a_sample_against_float64(c34):
+    row_ptr, col, graph, q, k, v, bias, _ = c34
+    D = q.shape[2]
+    kernel = DotAttention()
+    with torch.no_grad():
+        out = kernel(graph=graph, src={"k": k, "v": v}, dst={"q": q}, edge={"bias": bias},
+                     scale=D ** -0.5)
+    assert kernel.last_variant.backend == "hip"
+    deg = (row_ptr[1:] - row_ptr[:-1]).cpu()
+    hubs = torch.nonzero(deg > 512).flatten()
+    rng = np.random.default_rng(SEED)
+    others = torch.nonzero((deg > 0) & (deg <= 512)).flatten().numpy()
+    sample = rng.choice(others, size=min(20000, others.size), replace=False)
+    rows = np.unique(np.concatenate([hubs.numpy(), sample]))
+    print(f"c3 full size values: {hubs.numel()} hub rows + {sample.size} sampled rows",
+          flush=True)
+    d = lambda t: t.detach().double()
+    e_out, _ = chunked.dot_fwd(row_ptr, col, d(q), d(k), d(v), D ** -0.5, d(bias), rows=rows)
+    sel = torch.as_tensor(rows, device=DEV)
+    err_hub = rel(out[hubs.to(DEV)], e_out[hubs.to(DEV)])
+    err_all = rel(out[sel], e_out[sel])
+    print(f"c3 relative errors hub {err_hub:.3e} sampled {err_all:.3e}", flush=True)
+    assert err_hub <= 2e-2 and err_all <= 2e-2
+
+
+def test_c4_full_size_gradients_against_float64(c34):
+    print("c4 full size values: dq, dk, dv, dbias", flush=True)
+    row_ptr, col, graph, q, k, v, bias, dout = c34
+    D = q.shape[2]
+    kernel = DotAttention()
+    out = kernel(graph=graph, src={"k": k, "v": v}, dst={"q": q}, edge={"bias": bias},
+                 scale=D ** -0.5)
+    assert kernel.last_variant.backend == "hip"
+    q.grad = k.grad = v.grad = bias.grad = None
+    out.backward(dout)
+    torch.cuda.synchronize()
+    d = lambda t: t.detach().double()
+    want = chunked.dot_bwd(row_ptr, col, d(q), d(k), d(v), D ** -0.5, d(bias), d(dout))
+    errs = {n: rel(g, w) for n, g, w in zip(("dq", "dk", "dv", "dbias"),
+                                            (q.grad, k.grad, v.grad, bias.grad), want)}
+    print(f"c4 relative errors {errs}", flush=True)
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_dot_against_the_reference_bf16_arithmetic(with_bias):
+    print(f"bf16 reference arithmetic, R-MAT scale 12, bias={with_bias}", flush=True)
+    row_ptr, col = rmat(12, 16, SEED + 7)
+    N, E, H, D = row_ptr.numel() - 1, col.numel(), 4, 64
+    graph = tg.Graph.from_csr(row_ptr, col, num_src=N)
+    g = torch.Generator(device=DEV).manual_seed(SEED + 8)
+    mk = lambda: torch.randn(N, H, D, device=DEV, generator=g).to(torch.bfloat16)
+    q, k, v = (mk().requires_grad_(True) for _ in range(3))
+    bias = torch.randn(E, H, device=DEV, generator=g).requires_grad_(with_bias)
+    dout = mk()
+
+    class Plain(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge, scale):
+            return self.reducer((src.k * dst.q).sum(dim=-1) * scale, src.v)
+
+    kernel = DotAttention() if with_bias else Plain()
+    fields = {"edge": {"bias": bias}} if with_bias else {}
+    out = kernel(graph=graph, src={"k": k, "v": v}, dst={"q": q}, scale=D ** -0.5, **fields)
+    assert kernel.last_variant.backend == "hip"
+    out.backward(dout)
+    got = [out.detach(), q.grad, k.grad, v.grad] + ([bias.grad] if with_bias else [])
+    cpu = lambda t: t.detach().cpu()
+    rp, c = row_ptr.cpu(), col.cpu()
+    b = cpu(bias) if with_bias else None
+    eager = eager_torch.dot_reference(rp, c, cpu(q), cpu(k), cpu(v), b, D ** -0.5, cpu(dout))
+    f64 = lambda t: t.detach().double().cpu().numpy()
+    e_out, _ = ref.dot_fwd(rp.numpy(), c.numpy(), f64(q), f64(k), f64(v), D ** -0.5,
+                           None if b is None else f64(b))
+    e_grads = ref.dot_bwd(rp.numpy(), c.numpy(), f64(q), f64(k), f64(v), D ** -0.5,
+                          None if b is None else f64(b), f64(dout))
+    exact = [e_out, *e_grads[:3]] + ([e_grads[3]] if with_bias else [])
+    for name, gpu, e16, e64 in zip(("out", "dq", "dk", "dv", "dbias"), got, eager, exact):
+        e64 = torch.as_tensor(e64)
+        err16 = rel(gpu.cpu(), e16)
+        err64 = rel(gpu.cpu(), e64)
+        own = rel(e16, e64)   # the reference's bf16 path against exact math
+        print(f"  {name}: vs reference bf16 {err16:.3e}, vs fp64 {err64:.3e}; reference bf16 "
+              f"vs fp64 {own:.3e}", flush=True)
+        assert err64 <= 2e-2, name
+        assert err16 <= 2e-2 + own, name

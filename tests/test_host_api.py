@@ -181,3 +181,39 @@ def test_reference_plan_defers_above_the_histogram_limit():
     g = tg.Graph.from_csr(torch.tensor(rp), torch.zeros(int(rp[-1]), dtype=torch.int64),
                           num_src=1)
     assert g.reference_plan()["plan"] == "provider-deferred-high-degree"
+
+
+class Diffusion(tg.MessagePassing):
+    """The reference's diffusion example (examples/diffusion.py), unchanged."""
+
+    reducer = tg.sum()
+
+    def edge(self, src, dst, edge):
+        return edge.conductivity * (src.u + (-1.0) * dst.u)
+
+    def node(self, dst, flux, dt):
+        return dst.u + dt * flux
+
+
+def test_reference_diffusion_example_with_ndata():
+    """examples/diffusion.py: the stated flux and gradients, and the
+    reference's ndata test (tests/python/test_reference.py:366-390)."""
+    row_ptr = torch.tensor([0, 2, 4, 6, 8], dtype=torch.int64)
+    col_idx = torch.tensor([3, 1, 0, 2, 1, 3, 2, 0], dtype=torch.int64)
+    graph = tg.Graph.from_csr(row_ptr, col_idx, num_src=4, validate="full")
+    u = torch.tensor([0.0, 1.0, 0.5, -0.5], requires_grad=True)
+    conductivity = torch.tensor([1.0] * 8, requires_grad=True)
+    next_u = Diffusion()(graph=graph, ndata={"u": u}, edge={"conductivity": conductivity},
+                         dt=0.1)
+    flux = torch.tensor([0.5, -1.5, -0.5, 1.5])
+    torch.testing.assert_close(next_u, u.detach() + 0.1 * flux)
+    du, dc = torch.autograd.grad(next_u.sum(), (u, conductivity))
+    torch.testing.assert_close(du, torch.ones(4))
+    dst = np.repeat(np.arange(4), 2)
+    want = 0.1 * (u.detach().numpy()[col_idx.numpy()] - u.detach().numpy()[dst])
+    torch.testing.assert_close(dc, torch.tensor(want, dtype=torch.float32))
+    via_roles = Diffusion()(graph=graph, src={"u": u}, dst={"u": u},
+                            edge={"conductivity": conductivity}, dt=0.1)
+    torch.testing.assert_close(next_u, via_roles)
+    with pytest.raises(TypeError, match="cannot be combined"):
+        Diffusion()(graph=graph, ndata={"u": u}, dst={}, edge={})

@@ -530,3 +530,112 @@ def test_eager_nn_step_matches_oracle():
     (d_edge, d_src, d_dst), d_value, _ = ref.nn_attention_bwd(rp, col, inputs, layers, x, dout)
     np.testing.assert_allclose(ddisp.numpy(), d_edge, rtol=1e-9, atol=1e-12)
     np.testing.assert_allclose(dx.numpy(), d_src + d_dst + d_value, rtol=1e-9, atol=1e-12)
+
+
+# ---- row-chunked fp64 restatement (oracle/chunked.py) ---------------------------
+
+@pytest.mark.parametrize("edges_per_block", [1, 7, 1 << 20])
+def test_chunked_gat_matches_ref(edges_per_block):
+    """The full-size checker equals ref.gat_fwd/gat_bwd (itself pinned by
+    finite differences and the uniform closed form) for any block size."""
+    from oracle import chunked
+
+    rng = np.random.default_rng(21)
+    rp, col = random_csr(rng, 60, 60, 12, empty_frac=0.25)
+    H, D = 3, 4
+    h = rng.standard_normal((60, H, D))
+    a_s, a_d = rng.standard_normal((H, D)), rng.standard_normal((H, D))
+    dout = rng.standard_normal((60, H, D))
+    t = lambda a: torch.tensor(a, dtype=torch.float64)
+    rpt, colt = torch.tensor(rp), torch.tensor(col)
+    out, lse = chunked.gat_fwd(rpt, colt, t(h), t(a_s), t(a_d), 0.2, edges_per_block)
+    e_out, e_lse = ref.gat_fwd(rp, col, h, a_s, a_d, 0.2)
+    np.testing.assert_allclose(out.numpy(), e_out, rtol=1e-12, atol=1e-13)
+    np.testing.assert_array_equal(np.isinf(lse.numpy()), np.isinf(e_lse))
+    np.testing.assert_allclose(lse.numpy()[np.isfinite(e_lse)], e_lse[np.isfinite(e_lse)],
+                               rtol=1e-12)
+    got = chunked.gat_bwd(rpt, colt, t(h), t(a_s), t(a_d), 0.2, t(dout), edges_per_block)
+    for g, w in zip(got, ref.gat_bwd(rp, col, h, a_s, a_d, 0.2, dout)):
+        np.testing.assert_allclose(g.numpy(), w, rtol=1e-11, atol=1e-12)
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_chunked_dot_matches_ref(with_bias):
+    from oracle import chunked
+
+    rng = np.random.default_rng(22)
+    rp, col = random_csr(rng, 50, 70, 15, empty_frac=0.3)
+    H, D = 2, 8
+    q = rng.standard_normal((50, H, D))
+    k, v = rng.standard_normal((70, H, D)), rng.standard_normal((70, H, D))
+    bias = rng.standard_normal((col.size, H)) if with_bias else None
+    dout = rng.standard_normal((50, H, D))
+    t = lambda a: None if a is None else torch.tensor(a, dtype=torch.float64)
+    rpt, colt = torch.tensor(rp), torch.tensor(col)
+    out, _ = chunked.dot_fwd(rpt, colt, t(q), t(k), t(v), 0.3, t(bias), edges_per_block=9)
+    e_out, _ = ref.dot_fwd(rp, col, q, k, v, 0.3, bias)
+    np.testing.assert_allclose(out.numpy(), e_out, rtol=1e-12, atol=1e-13)
+    # a row subset evaluates exactly those rows
+    rows = np.array([3, 4, 17, 49])
+    sub, _ = chunked.dot_fwd(rpt, colt, t(q), t(k), t(v), 0.3, t(bias), rows=rows)
+    np.testing.assert_allclose(sub.numpy()[rows], e_out[rows], rtol=1e-12, atol=1e-13)
+    others = np.setdiff1d(np.arange(50), rows)
+    assert not sub.numpy()[others].any()
+    got = chunked.dot_bwd(rpt, colt, t(q), t(k), t(v), 0.3, t(bias), t(dout),
+                          edges_per_block=5)
+    for g, w in zip(got, ref.dot_bwd(rp, col, q, k, v, 0.3, bias, dout)):
+        np.testing.assert_allclose(g.numpy(), w, rtol=1e-11, atol=1e-12)
+
+
+def test_reference_bf16_dot_arithmetic_is_the_eager_path():
+    """eager_torch.dot_reference: in float64 it equals the pinned ref
+    forward and backward; in bf16 it differs from them by the bf16 rounding
+    of q*k and of the output, well inside the 2e-2 bound."""
+    from oracle import eager_torch
+
+    rng = np.random.default_rng(23)
+    rp, col = random_csr(rng, 40, 40, 10)
+    H, D = 2, 16
+    q, k, v = (rng.standard_normal((40, H, D)) for _ in range(3))
+    bias = rng.standard_normal((col.size, H))
+    dout = rng.standard_normal((40, H, D))
+    rpt, colt = torch.tensor(rp), torch.tensor(col)
+    got = eager_torch.dot_reference(rpt, colt, *(torch.tensor(a) for a in (q, k, v, bias)),
+                                    0.25, torch.tensor(dout))
+    want = (ref.dot_fwd(rp, col, q, k, v, 0.25, bias)[0],
+            *ref.dot_bwd(rp, col, q, k, v, 0.25, bias, dout))
+    for g, w in zip(got, want):
+        np.testing.assert_allclose(g.numpy(), w, rtol=1e-11, atol=1e-12)
+    b16 = lambda a: torch.tensor(a, dtype=torch.float32).to(torch.bfloat16)
+    got16 = eager_torch.dot_reference(rpt, colt, b16(q), b16(k), b16(v),
+                                      torch.tensor(bias, dtype=torch.float32), 0.25, b16(dout))
+    assert got16[0].dtype == torch.bfloat16 and got16[4].dtype == torch.float32
+    for g, w in zip(got16, want):
+        err = np.abs(g.double().numpy() - w).max() / np.abs(w).max()
+        assert 0 < err < 2e-2
+
+
+def test_row_plan_chunk_offsets_brute_force():
+    """ref.row_plan's split rows and chunk offsets against a direct walk:
+    every split row in ascending order, cut into consecutive chunk_edges-edge
+    pieces, the offsets counting the pieces before each row."""
+    rng = np.random.default_rng(24)
+    rp, _ = random_csr(rng, 200, 10, 30, empty_frac=0.2)
+    deg = np.diff(rp)
+    deg[[5, 77, 150]] = (130, 64, 1000)
+    rp = np.concatenate([[0], np.cumsum(deg)])
+    rows, n_empty, n_wave, n_split, offsets = ref.row_plan(rp, 40, 16)
+    split = [i for i in range(200) if deg[i] > 40]
+    assert rows[n_empty + n_wave:].tolist() == split
+    pieces = []
+    for i in split:
+        e = rp[i]
+        while e < rp[i + 1]:
+            pieces.append((i, e, min(e + 16, rp[i + 1])))
+            e += 16
+    assert offsets[-1] == len(pieces)
+    for j, i in enumerate(split):
+        mine = [p for p in pieces if p[0] == i]
+        assert offsets[j + 1] - offsets[j] == len(mine)
+        assert pieces[offsets[j]] == mine[0]
+    assert n_empty == int((deg == 0).sum()) and n_wave == int(((deg > 0) & (deg <= 40)).sum())
