@@ -445,6 +445,19 @@ int tgx_segment_softmax_fwd(const void* row_ptr_dev, int idx_bits, int64_t n_row
                             const float* scores_dev, float* alpha_dev, float* lse_dev,
                             void* stream);
 
+/* Segment softmax of raw per-edge scores read where the score field lives:
+ * s_e = scale * scores[col[e]] (role TGX_ROLE_SRC, a source-node table),
+ * scale * scores[i] (TGX_ROLE_DST, one per destination row) or
+ * scale * scores[e] (TGX_ROLE_EDGE); alpha[e] = exp(s_e - lse_i) and lse[i]
+ * (-inf, no weights, for an empty row).  With tgx_csr_sum_fwd (weights
+ * alpha) this is the reference's online softmax over a raw score field,
+ * reducer(src.score, src.value) (reducer_oracle.py:60-137; the compiled
+ * stable-weighted row tile, lib/Target/Triton/Translate.cpp:3004-3450). */
+int tgx_segment_softmax_gather_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                                   int64_t n_rows, const float* scores_dev, int role,
+                                   float scale, float* alpha_dev, float* lse_dev,
+                                   void* stream);
+
 /* Its backward: dscore[e] = alpha_e (dalpha_e - sum over the row of
  * alpha dalpha). */
 int tgx_segment_softmax_bwd(const void* row_ptr_dev, int idx_bits, int64_t n_rows,

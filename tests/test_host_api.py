@@ -217,3 +217,51 @@ def test_reference_diffusion_example_with_ndata():
     torch.testing.assert_close(next_u, via_roles)
     with pytest.raises(TypeError, match="cannot be combined"):
         Diffusion()(graph=graph, ndata={"u": u}, dst={}, edge={})
+
+
+def test_raw_score_softmax_recognition():
+    from tiga import capture as cap
+
+    class Attn(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def __init__(self, form):
+            super().__init__()
+            self.form = form
+
+        def edge(self, src, dst, edge, t=2.0):
+            score = {"src": src.s, "edge": edge.s * 0.5, "dst": -dst.s, "div": edge.s / t,
+                     "sum": src.s + dst.s}[self.form]
+            return self.reducer(score, src.v)
+
+    want = {"src": ("src", 1.0), "edge": ("edge", 0.5), "dst": ("dst", -1.0),
+            "div": ("edge", 0.5)}
+    for form, (role, scale) in want.items():
+        got = cap.recognize_score_softmax(Attn(form)._captured({"t": 2.0}))
+        assert got == cap.ScoreSoftmax(role, "s", scale, "v"), form
+    assert cap.recognize_score_softmax(Attn("sum")._captured({})) is None
+
+
+def test_raw_score_softmax_known_answer_on_cpu_eager():
+    """The reference's known answer on the eager evaluator (CPU tensors)."""
+    import json
+    from pathlib import Path
+
+    g = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+    g = g["online_softmax_large_scores"]
+
+    class OnlineAttention(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            return self.reducer(src.score, src.value)
+
+    graph = tg.Graph.from_csr(torch.tensor(g["row_ptr"]), torch.tensor(g["col_idx"]),
+                              num_src=g["num_src"])
+    score = torch.tensor(g["score"], requires_grad=True)
+    value = torch.tensor(g["value"], requires_grad=True)
+    out = OnlineAttention()(graph=graph, src={"score": score, "value": value}, dst={})
+    dscore, dvalue = torch.autograd.grad(out.sum(), (score, value))
+    np.testing.assert_allclose(out.detach().numpy(), g["out"], atol=5e-6, rtol=0)
+    np.testing.assert_allclose(dscore.numpy(), g["dscore"], atol=5e-6, rtol=0)
+    np.testing.assert_allclose(dvalue.numpy(), g["dvalue"], atol=5e-6, rtol=0)

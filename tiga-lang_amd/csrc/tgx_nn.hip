@@ -366,7 +366,48 @@ __global__ __launch_bounds__(256) void segment_softmax_fwd_kernel(
   for (int64_t e = e0 + lane; e < e1; e += kWave) l += __expf(scores[e] - m);
   l = group_sum<kWave>(l);
   const float ls = e1 > e0 ? m + __logf(l) : kNegInf;
-  for (int64_t e = e0 + lane; e < e1; e += kWave) alpha[e] = __expf(scores[e] - ls);
+  // exp(s - m) / l rather than exp(s - lse): s - m is exact (two nearby
+  // fp32 values), while lse carries the rounding of a large score (about
+  // 6e-5 at 1000, the reference's overflow test).
+  const float inv = 1.f / l;
+  for (int64_t e = e0 + lane; e < e1; e += kWave) alpha[e] = __expf(scores[e] - m) * inv;
+  if (lane == 0) lse[row] = ls;
+}
+
+// The same with the scores read where a field lives: role 0 a source-node
+// table read through col[e], role 1 a destination-node table (one score per
+// row), role 2 one score per edge; each multiplied by `scale`.  This is the
+// reference's stable-weighted row tile over a raw per-edge score
+// (Translate.cpp:3004-3450, reducer_oracle.py:60-137) minus the value sum.
+template <typename I, int ROLE>
+__device__ __forceinline__ float role_score(const float* scores, const I* col, int64_t e,
+                                            int64_t row, float scale) {
+  if constexpr (ROLE == 0) return scale * scores[static_cast<int64_t>(col[e])];
+  if constexpr (ROLE == 1) return scale * scores[row];
+  return scale * scores[e];
+}
+
+template <typename I, int ROLE>
+__global__ __launch_bounds__(256) void segment_softmax_gather_kernel(
+    const I* __restrict__ row_ptr, const I* __restrict__ col, int64_t n_rows,
+    const float* __restrict__ scores, float scale, float* __restrict__ alpha,
+    float* __restrict__ lse) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const int lane = lane_id();
+  const int64_t e0 = row_ptr[row], e1 = row_ptr[row + 1];
+  float m = kNegInf;
+  for (int64_t e = e0 + lane; e < e1; e += kWave)
+    m = fmaxf(m, role_score<I, ROLE>(scores, col, e, row, scale));
+  m = group_max<kWave>(m);
+  float l = 0.f;
+  for (int64_t e = e0 + lane; e < e1; e += kWave)
+    l += __expf(role_score<I, ROLE>(scores, col, e, row, scale) - m);
+  l = group_sum<kWave>(l);
+  const float ls = e1 > e0 ? m + __logf(l) : kNegInf;
+  const float inv = 1.f / l;   // exp(s - m) / l: see segment_softmax_fwd_kernel
+  for (int64_t e = e0 + lane; e < e1; e += kWave)
+    alpha[e] = __expf(role_score<I, ROLE>(scores, col, e, row, scale) - m) * inv;
   if (lane == 0) lse[row] = ls;
 }
 
@@ -706,6 +747,49 @@ extern "C" int tgx_segment_softmax_fwd(const void* row_ptr, int idx_bits, int64_
     segment_softmax_fwd_kernel<<<ceil_div(n_rows, 4), 256, 0, s>>>(
         static_cast<const int64_t*>(row_ptr), n_rows, scores, alpha, lse);
   TGX_LAUNCHED("segment_softmax_fwd_kernel");
+  return TGX_OK;
+}
+
+namespace tgx {
+namespace {
+template <typename I>
+void launch_gather_softmax(const I* row_ptr, const I* col, int64_t n_rows,
+                           const float* scores, int role, float scale, float* alpha,
+                           float* lse, hipStream_t s) {
+  const unsigned blocks = static_cast<unsigned>(ceil_div(n_rows, 4));
+  if (role == TGX_ROLE_SRC)
+    segment_softmax_gather_kernel<I, 0><<<blocks, 256, 0, s>>>(row_ptr, col, n_rows, scores,
+                                                               scale, alpha, lse);
+  else if (role == TGX_ROLE_DST)
+    segment_softmax_gather_kernel<I, 1><<<blocks, 256, 0, s>>>(row_ptr, col, n_rows, scores,
+                                                               scale, alpha, lse);
+  else
+    segment_softmax_gather_kernel<I, 2><<<blocks, 256, 0, s>>>(row_ptr, col, n_rows, scores,
+                                                               scale, alpha, lse);
+}
+}  // namespace
+}  // namespace tgx
+
+extern "C" int tgx_segment_softmax_gather_fwd(const void* row_ptr, const void* col,
+                                              int idx_bits, int64_t n_rows,
+                                              const float* scores, int role, float scale,
+                                              float* alpha, float* lse, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(n_rows >= 0, "negative size");
+  TGX_REQUIRE(role == TGX_ROLE_SRC || role == TGX_ROLE_DST || role == TGX_ROLE_EDGE,
+              "role must be TGX_ROLE_SRC, TGX_ROLE_DST or TGX_ROLE_EDGE");
+  if (n_rows == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && lse, "null pointer");
+  TGX_REQUIRE(role != TGX_ROLE_SRC || col, "source-role scores need col");
+  hipStream_t s = as_stream(stream);
+  TGX_PROFILE("segment_softmax_gather_kernel", s);
+  if (idx_bits == 32)
+    launch_gather_softmax(static_cast<const int32_t*>(row_ptr), static_cast<const int32_t*>(col),
+                          n_rows, scores, role, scale, alpha, lse, s);
+  else
+    launch_gather_softmax(static_cast<const int64_t*>(row_ptr), static_cast<const int64_t*>(col),
+                          n_rows, scores, role, scale, alpha, lse, s);
+  TGX_LAUNCHED("segment_softmax_gather_kernel");
   return TGX_OK;
 }
 

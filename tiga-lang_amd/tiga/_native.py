@@ -104,6 +104,8 @@ _SIGNATURES: dict[str, list] = {
                               c_vp, c_size, c_vp],
     "tgx_segment_softmax_fwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tgx_segment_softmax_bwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
+    "tgx_segment_softmax_gather_fwd": [c_vp, c_vp, c_int, c_i64, c_vp, c_int, c_f32, c_vp,
+                                       c_vp, c_vp],
     "tgx_profile_begin": [],
     "tgx_profile_end": [],
     "tgx_profile_count": [],

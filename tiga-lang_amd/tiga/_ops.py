@@ -459,3 +459,59 @@ def nn_attention(graph: Graph, chain, roles, fields, value: torch.Tensor) -> tor
     scores = EdgeMlpFunction.apply(graph, chain, tuple(roles), len(fields), *fields, *params)
     alpha = SegmentSoftmaxFunction.apply(scores, graph)
     return CsrSumFunction.apply(value, alpha, graph)
+
+
+# ---------------------------------------------------------------------------
+# Online softmax over a raw score field (tgx_segment_softmax_gather_fwd)
+
+_ROLE_CODE = {"src": 0, "dst": 1, "edge": 2}
+
+
+class ScoreSoftmaxFunction(torch.autograd.Function):
+    """alpha[e] = softmax over row i of scale * score(e), the score read from
+    a source-node table through col[e], a destination-node table, or one
+    value per edge; [E] fp32."""
+
+    @staticmethod
+    def forward(ctx, table: torch.Tensor, role: str, scale: float, graph: Graph):
+        _on_graph_device(graph, table)
+        row_ptr, col_idx = graph._kernel_csr()
+        n = graph.schema.num_dst
+        flat = table.reshape(-1).contiguous()
+        alpha = torch.empty(max(col_idx.numel(), 1), dtype=torch.float32,
+                            device=table.device)[:col_idx.numel()]
+        lse = torch.empty(max(n, 1), dtype=torch.float32, device=table.device)
+        _native.call("tgx_segment_softmax_gather_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
+                     _native.idx_bits(row_ptr), n, flat.data_ptr(), _ROLE_CODE[role],
+                     float(scale), alpha.data_ptr(), lse.data_ptr(), _native.stream_of(table))
+        ctx.graph, ctx.role, ctx.scale, ctx.shape = graph, role, float(scale), table.shape
+        ctx.save_for_backward(alpha)
+        return alpha
+
+    @staticmethod
+    def backward(ctx, dalpha):
+        (alpha,) = ctx.saved_tensors
+        graph: Graph = ctx.graph
+        row_ptr, _ = graph._kernel_csr()
+        dalpha = dalpha.contiguous()
+        dscore = torch.empty_like(alpha)
+        _native.call("tgx_segment_softmax_bwd", row_ptr.data_ptr(), _native.idx_bits(row_ptr),
+                     graph.schema.num_dst, alpha.data_ptr(), dalpha.data_ptr(),
+                     dscore.data_ptr(), _native.stream_of(alpha))
+        if ctx.role == "src":
+            grad = _reduce_rows_transposed(graph, dscore[:, None])[:, 0]
+        elif ctx.role == "dst":
+            grad = _reduce_rows(graph, dscore[:, None])[:, 0]
+        else:
+            grad = dscore
+        if ctx.scale != 1.0:
+            grad = grad * ctx.scale
+        return grad.reshape(ctx.shape), None, None, None
+
+
+def score_attention(graph: Graph, table: torch.Tensor, role: str, scale: float,
+                    value: torch.Tensor) -> torch.Tensor:
+    """out[i] = sum_e softmax_i(scale * score(e)) value[col[e]] on the HIP path:
+    the gathered segment softmax, then the weighted CSR sum."""
+    alpha = ScoreSoftmaxFunction.apply(table, role, scale, graph)
+    return CsrSumFunction.apply(value, alpha, graph)

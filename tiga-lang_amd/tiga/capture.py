@@ -13,6 +13,7 @@ kernels:
 * dot product    ``(src.k*dst.q).sum(-1) [* scale] [+ edge.b]``, value ``src.v``
 * varlen / dense the dot product on ``Graph.cu_seqlens`` / ``dense`` / ``triangular``
 * nn-scored      ``reducer(tg.nn.trace(net)(fields...), src.v)``
+* raw score      ``reducer(role.s [* c], src.v)``, role src, dst or edge
 
 Anything else is not an error: the call runs on the eager Torch evaluator.
 """
@@ -280,6 +281,47 @@ def recognize_dot(item) -> DotProduct | None:
 
 
 @dataclass(frozen=True)
+class ScoreSoftmax:
+    score_role: str       # src | dst | edge: where the raw score field lives
+    score_field: str
+    scale: float
+    value_field: str      # src.v
+
+
+def _scaled_field(s):
+    """field, scalar * field, field * scalar, field / scalar or -field ->
+    (field Sym, scale); else None."""
+    if _is_field(s):
+        return s, 1.0
+    if isinstance(s, Sym) and s.op == "neg" and _is_field(s.args[0]):
+        return s.args[0], -1.0
+    if isinstance(s, Sym) and s.op == "mul":
+        m = _pair(s, _is_field, _is_scalar)
+        if m is not None:
+            return m[0], m[1].args[0]
+    if isinstance(s, Sym) and s.op == "div" and _is_field(s.args[0]) and \
+            _is_scalar(s.args[1]) and s.args[1].args[0] != 0:
+        return s.args[0], 1.0 / s.args[1].args[0]
+    return None
+
+
+def recognize_score_softmax(item) -> ScoreSoftmax | None:
+    """reducer(score_field [* c], src.value): online softmax over a raw
+    per-edge score read from a node or edge field (the reference's known
+    answer, tests/python/test_message_passing_autograd.py:318-351)."""
+    if not isinstance(item, OnlineSoftmaxItem):
+        return None
+    if not _is_field(item.value, "src"):
+        return None
+    got = _scaled_field(item.score)
+    if got is None:
+        return None
+    field, scale = got
+    return ScoreSoftmax(score_role=field.args[0], score_field=field.args[1], scale=float(scale),
+                        value_field=item.value.args[1])
+
+
+@dataclass(frozen=True)
 class NnAttention:
     module: Any                               # tiga.nn.TracedModule
     inputs: tuple[tuple[str, str], ...]       # (role, field) in concatenation order
@@ -332,11 +374,13 @@ __all__ = [
     "FieldNamespace",
     "GatAdditive",
     "NnAttention",
+    "ScoreSoftmax",
     "Sym",
     "WeightedSum",
     "capture",
     "recognize_dot",
     "recognize_gat",
     "recognize_nn_attention",
+    "recognize_score_softmax",
     "recognize_weighted_sum",
 ]

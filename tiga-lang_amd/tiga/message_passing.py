@@ -380,7 +380,47 @@ class MessagePassing(Kernel):
         nn_item = cap.recognize_nn_attention(captured)
         if nn_item is not None:
             return self._plan_nn_attention(nn_item, graph, src, dst, edge)
+        raw = cap.recognize_score_softmax(captured)
+        if raw is not None:
+            return self._plan_score_softmax(raw, graph, src, dst, edge)
         return None
+
+    def _plan_score_softmax(self, raw, graph, src, dst, edge) -> _Launch | None:
+        """reducer(role.score [* c], src.value) on the gathered segment softmax
+        and the weighted CSR sum (reference: the eager oracle for Torch
+        tensors, reducer_oracle.py:60-137; its compiled stable-weighted row
+        tile for 1-D f32 fields, message_passing.py:2579-2619).  Scalar
+        scores (one lane) and fp32; an empty row gives 0, as the reference's
+        Torch path does."""
+        from . import _ops
+
+        if graph.is_varlen or graph.is_dense:
+            return None
+        groups = {"src": src, "dst": dst, "edge": edge}
+        rows = {"src": graph.schema.num_src, "dst": graph.schema.num_dst,
+                "edge": graph.num_edges}
+        table = groups[raw.score_role].get(raw.score_field)
+        value = src.get(raw.value_field)
+        if table is None or value is None:
+            return None
+        if table.dtype != torch.float32 or value.dtype != torch.float32:
+            return None
+        if tuple(table.shape) not in ((rows[raw.score_role],), (rows[raw.score_role], 1)):
+            return None
+        _native.lib()
+        role, scale = raw.score_role, raw.scale
+
+        def run(table, value):
+            return _ops.score_attention(graph, table, role, scale, value)
+
+        describe = lambda: self._variant(
+            graph, "score-softmax",
+            ("tgx_segment_softmax_gather_fwd", "tgx_csr_sum_fwd", "tgx_segment_softmax_bwd",
+             "tgx_csr_sum_bwd"),
+            f"segment softmax of the {role} score field per row (one wave per row), "
+            "weighted CSR sum of src.value; backward through the softmax Jacobian, "
+            f"score gradient reduced per {role} row")
+        return _Launch(graph, ((role, raw.score_field), ("src", raw.value_field)), run, describe)
 
     def _plan_sum(self, captured, graph, src, edge) -> _Launch | None:
         from . import _ops
