@@ -404,7 +404,13 @@ enum {
   TGX_ACT_SIGMOID = 4,
   TGX_ACT_SILU = 5,
   TGX_ACT_GELU = 6,         /* exact (erf) form */
-  TGX_ACT_ELU = 7           /* act_param = alpha */
+  TGX_ACT_ELU = 7,          /* act_param = alpha */
+  TGX_ACT_HARDTANH = 8,     /* clamp to [act_param, act_param2] (relu6, clamp) */
+  TGX_ACT_SOFTPLUS = 9,     /* act_param = beta, act_param2 = threshold */
+  TGX_ACT_SELU = 10,
+  TGX_ACT_MISH = 11,
+  TGX_ACT_HARDSIGMOID = 12,
+  TGX_ACT_HARDSWISH = 13
 };
 
 /* Row of an edge that a score-input segment is gathered from. */
@@ -431,6 +437,9 @@ typedef struct tgx_edge_mlp {
   /* Real output width of each layer (1..width, the last one 1; 0 = width):
    * rows and columns past the real shapes are zero padding the kernels skip. */
   int32_t out_width[3];
+  /* Second parameter of each activation (hardtanh's upper bound, softplus's
+   * threshold; unused by the others). */
+  float act_param2[3];
 } tgx_edge_mlp;
 
 /* scores[e] = MLP(x_e) for every edge.  dst_index_dev [n_edges] int32 is the
@@ -438,6 +447,36 @@ typedef struct tgx_edge_mlp {
 int tgx_edge_mlp_scores(const void* col_dev, const int32_t* dst_index_dev, int idx_bits,
                         int64_t n_edges, const tgx_edge_mlp* mlp, float* scores_dev,
                         void* stream);
+
+/* Edge-network messages summed per destination row (the reference's
+ * edge-NN tile, python/tiga/compiler/edge_nn_tile.py:1-30, dispatched by
+ * interop/torch/message_passing.py:2134-2300: tg.sum() over
+ * tg.nn.trace(net)(fields)).  The last Linear layer is linear, so
+ *   sum_e net(x_e) = W_L (sum_e a_e) + deg(i) b_L,   a_e = the last layer's
+ * input for edge e; these entry points evaluate everything before the last
+ * layer, and the caller applies W_L to the row sums.  The network is given
+ * as for tgx_edge_mlp_scores (the last layer's weight block is not read;
+ * its out_width entry may be 1), width 16, 24 or 32.
+ *
+ * hidden_dev [n_edges, hidden_width] fp32 receives a_e, hidden_width being
+ * the last layer's input width (the previous layer's real output width, or
+ * the concatenated input width for a one-layer network). */
+int tgx_edge_mlp_hidden(const void* col_dev, const int32_t* dst_index_dev, int idx_bits,
+                        int64_t n_edges, const tgx_edge_mlp* mlp, float* hidden_dev,
+                        int32_t hidden_width, void* stream);
+
+/* Backward of tgx_edge_mlp_hidden given the gradient at the last layer's
+ * input per destination row, seed_dev [n_dst, seed_width] (the edge e takes
+ * row dst_index[e]): per-edge input-segment gradients dseg as in
+ * tgx_edge_mlp_backward, and the hidden layers' weight and bias gradients
+ * summed over all edges into dweights_dev (the last layer's block is
+ * written as zeros).  Deterministic; workspace as
+ * tgx_edge_mlp_backward_workspace. */
+int tgx_edge_mlp_backward_seeded(const void* col_dev, const int32_t* dst_index_dev,
+                                 int idx_bits, int64_t n_edges, const tgx_edge_mlp* mlp,
+                                 const float* seed_dev, int32_t seed_width,
+                                 float* dweights_dev, float* const* dseg, void* workspace_dev,
+                                 size_t workspace_bytes, void* stream);
 
 /* Segment softmax over CSR rows: alpha[e] = exp(s_e - lse_i) and lse[i]
  * (-inf for an empty row), one wave per row (reducer_oracle.py:60-137). */

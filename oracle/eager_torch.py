@@ -119,3 +119,45 @@ def dot_reference(row_ptr, col, q, k, v, bias, scale, dout):
     out = reduce_online_softmax(score, v[col], destination, num_dst)
     out.backward(dout)
     return out.detach(), q.grad, k.grad, v.grad, None if b is None else b.grad
+
+
+def _gathered(row_ptr, col, inputs):
+    """Feature-concatenation of the fields gathered per edge, and the leaves
+    (inputs = [(role, tensor [rows] or [rows, k])])."""
+    destination = destination_index(row_ptr)
+    leaves, parts = [], []
+    for role, t in inputs:
+        leaf = t.detach().requires_grad_(True)
+        leaves.append(leaf)
+        x = leaf if leaf.ndim == 2 else leaf[:, None]
+        parts.append(x[col] if role == "src" else x[destination] if role == "dst" else x)
+    return torch.cat(parts, dim=1), destination, leaves
+
+
+def nn_message_sum(row_ptr, col, inputs, net, dout):
+    """The eager path of tg.sum() over tg.nn.trace(net)(fields...): the
+    module on the concatenated gathered fields, index_add per destination
+    row (reduce_sum, reducer_oracle.py:44-57), Torch autograd.  Runs in the
+    inputs' dtype (float64 for checking).  Returns (out, input grads,
+    parameter grads in net.parameters() order)."""
+    x, destination, leaves = _gathered(row_ptr, col, inputs)
+    msg = net(x)
+    out = torch.zeros(row_ptr.numel() - 1, msg.shape[1], dtype=msg.dtype).index_add(
+        0, destination, msg)
+    params = [p for p in net.parameters()]
+    grads = torch.autograd.grad(out, leaves + params, dout, allow_unused=True)
+    return out.detach(), list(grads[:len(leaves)]), list(grads[len(leaves):])
+
+
+def nn_attention(row_ptr, col, inputs, net, value, dout, out_scale=1.0):
+    """The eager path of online_softmax(score = out_scale * net(fields...),
+    value = src.value) with Torch autograd (reducer_oracle.py:60-137).
+    Returns (out, input grads, value grad, parameter grads)."""
+    x, destination, leaves = _gathered(row_ptr, col, inputs)
+    v = value.detach().requires_grad_(True)
+    score = net(x)[:, 0] * out_scale
+    out = reduce_online_softmax(score, v[col], destination, row_ptr.numel() - 1)
+    params = [p for p in net.parameters()]
+    grads = torch.autograd.grad(out, leaves + [v] + params, dout, allow_unused=True)
+    n = len(leaves)
+    return out.detach(), list(grads[:n]), grads[n], list(grads[n + 1:])

@@ -639,3 +639,56 @@ def test_row_plan_chunk_offsets_brute_force():
         assert offsets[j + 1] - offsets[j] == len(mine)
         assert pieces[offsets[j]] == mine[0]
     assert n_empty == int((deg == 0).sum()) and n_wave == int(((deg > 0) & (deg <= 40)).sum())
+
+
+def test_eager_nn_message_sum_closed_form_and_nn_attention_agrees_with_ref():
+    """oracle/eager_torch.nn_message_sum: for one Linear layer the row sum is
+    W (sum of the row's gathered inputs) + degree * b; nn_attention equals
+    the pinned ref.nn_attention_fwd/bwd for a two-layer tanh network."""
+    from torch import nn
+
+    from oracle import eager_torch
+
+    rng = np.random.default_rng(31)
+    rp, col = random_csr(rng, 30, 25, 8)
+    rpt, colt = torch.tensor(rp), torch.tensor(col)
+    xs = rng.standard_normal((25, 3))
+    xd = rng.standard_normal((30, 2))
+    xe = rng.standard_normal((col.size,))
+    net = nn.Linear(6, 4).double()
+    inputs = [("src", torch.tensor(xs)), ("dst", torch.tensor(xd)), ("edge", torch.tensor(xe))]
+    dout = torch.tensor(rng.standard_normal((30, 4)))
+    out, gin, gp = eager_torch.nn_message_sum(rpt, colt, inputs, net, dout)
+    dst = ref.destination_index(rp)
+    gathered = np.concatenate([xs[col], xd[dst], xe[:, None]], axis=1)
+    rows = np.zeros((30, 6))
+    np.add.at(rows, dst, gathered)
+    W, b = net.weight.detach().numpy(), net.bias.detach().numpy()
+    want = rows @ W.T + np.diff(rp)[:, None] * b
+    np.testing.assert_allclose(out.numpy(), want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(gp[0].numpy(), dout.numpy().T @ rows, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(gp[1].numpy(), (np.diff(rp)[:, None] * dout.numpy()).sum(0),
+                               rtol=1e-12, atol=1e-12)
+    # the src field's gradient: sum over its out-edges of dout[dst] W (first 3 columns)
+    g_edge = dout.numpy()[dst] @ W
+    e_src = np.zeros((25, 3))
+    np.add.at(e_src, col, g_edge[:, :3])
+    np.testing.assert_allclose(gin[0].numpy(), e_src, rtol=1e-12, atol=1e-12)
+
+    net2 = nn.Sequential(nn.Linear(6, 5), nn.Tanh(), nn.Linear(5, 1)).double()
+    value = rng.standard_normal((25, 4))
+    dout2 = rng.standard_normal((30, 4))
+    out2, gin2, gv2, gp2 = eager_torch.nn_attention(rpt, colt, inputs, net2,
+                                                    torch.tensor(value), torch.tensor(dout2))
+    layers = [(net2[0].weight.detach().numpy(), net2[0].bias.detach().numpy(), "tanh", 0.0),
+              (net2[2].weight.detach().numpy(), net2[2].bias.detach().numpy(), "identity", 0.0)]
+    np_inputs = [("src", xs), ("dst", xd), ("edge", xe)]
+    e_out, _ = ref.nn_attention_fwd(rp, col, np_inputs, layers, value)
+    e_din, e_dv, e_grads = ref.nn_attention_bwd(rp, col, np_inputs, layers, value, dout2)
+    np.testing.assert_allclose(out2.numpy(), e_out, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(gv2.numpy(), e_dv, rtol=1e-10, atol=1e-12)
+    for g, w in zip(gin2, e_din):
+        np.testing.assert_allclose(g.numpy(), w, rtol=1e-10, atol=1e-12)
+    for (gw, gb), (ew, eb) in zip(zip(gp2[0::2], gp2[1::2]), e_grads):
+        np.testing.assert_allclose(gw.numpy(), ew, rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(gb.numpy(), eb, rtol=1e-10, atol=1e-11)

@@ -66,9 +66,33 @@ __global__ __launch_bounds__(256, (fwd_blocks_per_cu<W, L>())) void edge_mlp_fwd
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
     linear<W>(wg + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
-    activate_all<W>(z, a, m.act[l], m.param[l], m.nb_in[l + 1]);
+    activate_all<W>(z, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1]);
   }
   scores[e] = linear_out1<W>(wg + (L - 1) * (W * W + W), a, m.nb_in[L - 1]);
+}
+
+// The last layer's input per edge (the activation after layer L - 2, or the
+// gathered input when L = 1): hidden[e][0..hw).
+template <typename I, int W, int L>
+__global__ __launch_bounds__(256) void edge_mlp_hidden_kernel(const I* __restrict__ col,
+                                                              const int32_t* __restrict__ dst,
+                                                              int64_t n_edges, MlpView m,
+                                                              float* __restrict__ hidden,
+                                                              int hw) {
+  cfloat* wg = scalar_weights(m.w);
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= n_edges) return;
+  float a[W], z[W];
+  gather_inputs<I, W>(m, e, col, dst, a);
+#pragma unroll
+  for (int l = 0; l + 1 < L; ++l) {
+    linear<W>(wg + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
+    activate_all<W>(z, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1]);
+  }
+  float* out = hidden + e * hw;
+#pragma unroll
+  for (int k = 0; k < W; ++k)
+    if (k < hw) out[k] = a[k];
 }
 
 // ---- weight gradients on fp32 MFMA ------------------------------------------
@@ -208,10 +232,15 @@ __device__ __forceinline__ void outer_store(const OuterAcc<W>& acc, float* red) 
 // (dseg[s][e][:width_s]) and accumulates dW_l, db_l for every layer on MFMA;
 // the block's sums go to partial[block] (n_layers x [W*W | W]) in a fixed
 // order.
-template <typename I, int W, int L>
+//
+// SEED: the gradient at the last layer's input is given per destination row
+// (seed[dst[e]][0..hw), the edge-network sum's backward) instead of coming
+// from a one-output last layer; the last layer's sums then stay zero.
+template <typename I, int W, int L, bool SEED>
 __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd_kernel(
     const I* __restrict__ col, const int32_t* __restrict__ dst, int64_t n_edges, int64_t chunk,
-    MlpView m_arg, const float* __restrict__ dscore, float* __restrict__ partial) {
+    MlpView m_arg, const float* __restrict__ dscore, float* __restrict__ partial,
+    const float* __restrict__ seed, int hw) {
   constexpr int NW = W * W + W;
   constexpr int LD = mlp_ld<W>();
   constexpr int SW = 2 * 32 * LD;  // one wave's staging: G rows | A rows
@@ -253,6 +282,7 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
     const bool valid = e < e1;
     float x[W];                        // gathered input (layer 0's input)
     float z[L > 1 ? L - 1 : 1][W];     // pre-activations of the hidden layers
+    const int64_t cur_dst = next_dst;
     if (valid) {
       gather_rows<W>(m, e, next_src, next_dst, x);
     } else {
@@ -270,7 +300,7 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
       static_for<L - 1>([&](auto lc) {
         constexpr int l = decltype(lc)::value;
         linear<W>(wg + l * NW, a, z[l], m.n_out[l], m.nb_in[l]);
-        activate_all<W>(z[l], a, m.act[l], m.param[l], m.nb_in[l + 1]);
+        activate_all<W>(z[l], a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1]);
       });
     }
     // Input of layer l: x, or the activation of z[l-1].
@@ -280,13 +310,19 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
 #pragma unroll
         for (int k = 0; k < W; ++k) a[k] = x[k];
       } else {
-        activate_all<W>(z[l - 1], a, m.act[l - 1], m.param[l - 1], m.nb_in[l]);
+        activate_all<W>(z[l - 1], a, m.act[l - 1], m.param[l - 1], m.param2[l - 1],
+                         m.nb_in[l]);
       }
     };
-    // Last layer: one output, gradient ds (0 on lanes past the range).
-    const float ds = valid ? dscore[e] : 0.f;
     float g[W];
-    {
+    if constexpr (SEED) {
+      // The gradient at the last layer's input, gathered from the edge's row.
+      const float* q = seed + cur_dst * hw;
+#pragma unroll
+      for (int k = 0; k < W; ++k) g[k] = (valid && k < hw) ? q[k] : 0.f;
+    } else {
+      // Last layer: one output, gradient ds (0 on lanes past the range).
+      const float ds = valid ? dscore[e] : 0.f;
       cfloat* wl = wg + (L - 1) * NW;
       float a[W];
       layer_input(std::integral_constant<int, L - 1>{}, a);
@@ -303,7 +339,8 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
     static_for<L - 1>([&](auto kc) {
       constexpr int l = L - 2 - decltype(kc)::value;
       float dzl[W];
-      activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.nb_in[l + 1]);
+      activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.param2[l],
+                         m.nb_in[l + 1]);
 #pragma unroll
       for (int o = 0; o < W; ++o) pin(dzl[o]);
       {
@@ -494,7 +531,7 @@ int check_mlp(const tgx_edge_mlp* mlp, MlpView* view, bool need_data) {
   }
   TGX_REQUIRE(in_width <= mlp->width, "inputs (%d) exceed the padded width", in_width);
   for (int l = 0; l + 1 < mlp->n_layers; ++l)
-    TGX_REQUIRE(mlp->act[l] >= TGX_ACT_IDENTITY && mlp->act[l] <= TGX_ACT_ELU,
+    TGX_REQUIRE(mlp->act[l] >= TGX_ACT_IDENTITY && mlp->act[l] <= TGX_ACT_HARDSWISH,
                 "bad activation code");
   MlpView v{};
   v.n_layers = mlp->n_layers;
@@ -514,6 +551,7 @@ int check_mlp(const tgx_edge_mlp* mlp, MlpView* view, bool need_data) {
   for (int l = 0; l < kMaxLayers; ++l) {
     v.act[l] = l + 1 < mlp->n_layers ? mlp->act[l] : TGX_ACT_IDENTITY;
     v.param[l] = mlp->act_param[l];
+    v.param2[l] = mlp->act_param2[l];
   }
   v.w = mlp->weights_dev;
   v.n_seg = mlp->n_segments;
@@ -557,7 +595,7 @@ int64_t bwd_resident_blocks() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
   int64_t known = cached[dev].load(std::memory_order_relaxed);
   if (known == 0) {
-    const void* fn = reinterpret_cast<const void*>(edge_mlp_bwd_kernel<int64_t, W, L>);
+    const void* fn = reinterpret_cast<const void*>(edge_mlp_bwd_kernel<int64_t, W, L, false>);
     int per_cu = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess)
       per_cu = 0;
@@ -588,15 +626,28 @@ int64_t resident_blocks(int W, int L) {
                                                           : bwd_resident_blocks<32, 3>();
 }
 
-template <typename I, int W>
+template <typename I, int W, bool SEED>
 void launch_bwd(int L, const I* col, const int32_t* dst, int64_t E, int blocks, int64_t chunk,
-                const MlpView& v, const float* ds, float* partial, hipStream_t s) {
+                const MlpView& v, const float* ds, float* partial, const float* seed, int hw,
+                hipStream_t s) {
   if (L == 1)
-    edge_mlp_bwd_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds, partial);
+    edge_mlp_bwd_kernel<I, W, 1, SEED><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds,
+                                                              partial, seed, hw);
   if (L == 2)
-    edge_mlp_bwd_kernel<I, W, 2><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds, partial);
+    edge_mlp_bwd_kernel<I, W, 2, SEED><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds,
+                                                              partial, seed, hw);
   if (L == 3)
-    edge_mlp_bwd_kernel<I, W, 3><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds, partial);
+    edge_mlp_bwd_kernel<I, W, 3, SEED><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds,
+                                                              partial, seed, hw);
+}
+
+template <typename I, int W>
+void launch_hidden(int L, const I* col, const int32_t* dst, int64_t E, const MlpView& v,
+                   float* hidden, int hw, hipStream_t s) {
+  const int64_t blocks = ceil_div(E, 256);
+  if (L == 1) edge_mlp_hidden_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, v, hidden, hw);
+  if (L == 2) edge_mlp_hidden_kernel<I, W, 2><<<blocks, 256, 0, s>>>(col, dst, E, v, hidden, hw);
+  if (L == 3) edge_mlp_hidden_kernel<I, W, 3><<<blocks, 256, 0, s>>>(col, dst, E, v, hidden, hw);
 }
 
 template <typename I>
@@ -608,13 +659,27 @@ void dispatch_fwd(int W, int L, const I* col, const int32_t* dst, int64_t E, con
   if (W == 64) launch_fwd<I, 64>(L, col, dst, E, v, scores, s);
 }
 
-template <typename I>
+template <typename I, bool SEED = false>
 void dispatch_bwd(int W, int L, const I* col, const int32_t* dst, int64_t E, int blocks,
                   int64_t chunk, const MlpView& v, const float* ds, float* partial,
-                  hipStream_t s) {
-  if (W == 16) launch_bwd<I, 16>(L, col, dst, E, blocks, chunk, v, ds, partial, s);
-  if (W == 24) launch_bwd<I, 24>(L, col, dst, E, blocks, chunk, v, ds, partial, s);
-  if (W == 32) launch_bwd<I, 32>(L, col, dst, E, blocks, chunk, v, ds, partial, s);
+                  hipStream_t s, const float* seed = nullptr, int hw = 0) {
+  if (W == 16) launch_bwd<I, 16, SEED>(L, col, dst, E, blocks, chunk, v, ds, partial, seed, hw, s);
+  if (W == 24) launch_bwd<I, 24, SEED>(L, col, dst, E, blocks, chunk, v, ds, partial, seed, hw, s);
+  if (W == 32) launch_bwd<I, 32, SEED>(L, col, dst, E, blocks, chunk, v, ds, partial, seed, hw, s);
+}
+
+template <typename I>
+void dispatch_hidden(int W, int L, const I* col, const int32_t* dst, int64_t E, const MlpView& v,
+                     float* hidden, int hw, hipStream_t s) {
+  if (W == 16) launch_hidden<I, 16>(L, col, dst, E, v, hidden, hw, s);
+  if (W == 24) launch_hidden<I, 24>(L, col, dst, E, v, hidden, hw, s);
+  if (W == 32) launch_hidden<I, 32>(L, col, dst, E, v, hidden, hw, s);
+}
+
+// Width of the last layer's input: the previous layer's real output, or the
+// concatenated input of a one-layer network.
+int last_input_width(const tgx_edge_mlp* mlp, const MlpView& v) {
+  return mlp->n_layers > 1 ? v.n_out[mlp->n_layers - 2] : v.in_width;
 }
 
 
@@ -809,5 +874,97 @@ extern "C" int tgx_segment_softmax_bwd(const void* row_ptr, int idx_bits, int64_
     segment_softmax_bwd_kernel<<<ceil_div(n_rows, 4), 256, 0, s>>>(
         static_cast<const int64_t*>(row_ptr), n_rows, alpha, dalpha, dscore);
   TGX_LAUNCHED("segment_softmax_bwd_kernel");
+  return TGX_OK;
+}
+
+extern "C" int tgx_edge_mlp_hidden(const void* col, const int32_t* dst_index, int idx_bits,
+                                   int64_t n_edges, const tgx_edge_mlp* mlp, float* hidden,
+                                   int32_t hidden_width, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(n_edges >= 0, "negative size");
+  MlpView v;
+  int st = check_mlp(mlp, &v, n_edges > 0);
+  if (st != TGX_OK) return st;
+  if (mlp->width == 64) {
+    set_error("edge-network sums support padded widths 16, 24 and 32");
+    return TGX_UNSUPPORTED;
+  }
+  TGX_REQUIRE(hidden_width == last_input_width(mlp, v),
+              "hidden_width %d is not the last layer's input width %d", hidden_width,
+              last_input_width(mlp, v));
+  if (n_edges == 0) return TGX_OK;
+  TGX_REQUIRE(col && dst_index && hidden, "null pointer");
+  hipStream_t s = as_stream(stream);
+  TGX_PROFILE("edge_mlp_hidden_kernel", s);
+  if (idx_bits == 32)
+    dispatch_hidden(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col), dst_index,
+                    n_edges, v, hidden, hidden_width, s);
+  else
+    dispatch_hidden(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col), dst_index,
+                    n_edges, v, hidden, hidden_width, s);
+  TGX_LAUNCHED("edge_mlp_hidden_kernel");
+  return TGX_OK;
+}
+
+extern "C" int tgx_edge_mlp_backward_seeded(const void* col, const int32_t* dst_index,
+                                            int idx_bits, int64_t n_edges,
+                                            const tgx_edge_mlp* mlp, const float* seed,
+                                            int32_t seed_width, float* dweights,
+                                            float* const* dseg, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(n_edges >= 0, "negative size");
+  MlpView v;
+  int st = check_mlp(mlp, &v, n_edges > 0);
+  if (st != TGX_OK) return st;
+  if (mlp->width == 64) {
+    set_error("edge-network sums support padded widths 16, 24 and 32");
+    return TGX_UNSUPPORTED;
+  }
+  TGX_REQUIRE(seed_width == last_input_width(mlp, v),
+              "seed_width %d is not the last layer's input width %d", seed_width,
+              last_input_width(mlp, v));
+  TGX_REQUIRE(dweights && dseg, "null pointer");
+  const int n = mlp->n_layers * (mlp->width * mlp->width + mlp->width);
+  hipStream_t s = as_stream(stream);
+  if (n_edges == 0) {
+    colsum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(nullptr, 0, n, dweights);
+    TGX_LAUNCHED("colsum_final_kernel");
+    return TGX_OK;
+  }
+  TGX_REQUIRE(col && dst_index && seed && workspace, "null pointer");
+  for (int k = 0; k < mlp->n_segments; ++k) {
+    TGX_REQUIRE(dseg[k], "null gradient for segment %d", k);
+    v.grad[k] = dseg[k];
+  }
+  size_t need = 0;
+  TGX_REQUIRE(tgx_edge_mlp_backward_workspace(n_edges, mlp, &need) == TGX_OK &&
+                  workspace_bytes >= need,
+              "workspace too small");
+  int64_t chunk = 0;
+  const int blocks = mlp_bwd_blocks(n_edges, resident_blocks(mlp->width, mlp->n_layers), &chunk);
+  const size_t part_bytes = align_up(static_cast<size_t>(blocks) * n * sizeof(float));
+  float* partial = static_cast<float*>(workspace);
+  float* slices = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
+  {
+    TGX_PROFILE("edge_mlp_bwd_seeded_kernel", s);
+    if (idx_bits == 32)
+      dispatch_bwd<int32_t, true>(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col),
+                                  dst_index, n_edges, blocks, chunk, v, nullptr, partial, s,
+                                  seed, seed_width);
+    else
+      dispatch_bwd<int64_t, true>(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col),
+                                  dst_index, n_edges, blocks, chunk, v, nullptr, partial, s,
+                                  seed, seed_width);
+    TGX_LAUNCHED("edge_mlp_bwd_seeded_kernel");
+  }
+  {
+    TGX_PROFILE("colsum_kernels", s);
+    colsum_slice_kernel<<<dim3(ceil_div(n, 256), kColSlices), 256, 0, s>>>(partial, blocks,
+                                                                           n, slices);
+    TGX_LAUNCHED("colsum_slice_kernel");
+    colsum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(slices, kColSlices, n, dweights);
+    TGX_LAUNCHED("colsum_final_kernel");
+  }
   return TGX_OK;
 }

@@ -23,6 +23,7 @@ struct MlpView {
   int nb_in[kMaxLayers];   // column blocks of 4 covering each layer's real input
   int act[kMaxLayers];
   float param[kMaxLayers];
+  float param2[kMaxLayers];
   const float* w;   // n_layers x [W*W | W]
   int n_seg;
   int role[kMaxSegments];
@@ -35,8 +36,20 @@ struct MlpView {
 
 __device__ __forceinline__ float sigmoid(float z) { return 1.f / (1.f + __expf(-z)); }
 
-// Component-wise activation (code uniform across the wave).
-__device__ __forceinline__ float activate(float z, int act, float p) {
+// softplus with Torch's convention: z where beta z > threshold, else
+// log(1 + exp(beta z)) / beta.
+__device__ __forceinline__ float softplus(float z, float beta, float threshold) {
+  const float bz = beta * z;
+  return bz > threshold ? z : log1pf(__expf(bz)) / beta;
+}
+
+constexpr float kSeluAlpha = 1.6732632423543772848f;
+constexpr float kSeluScale = 1.0507009873554804934f;
+
+// Component-wise activation (code uniform across the wave).  Derivatives
+// follow Torch's at the kinks (hardtanh's bounds excluded, hardswish's
+// boundaries as its backward).
+__device__ __forceinline__ float activate(float z, int act, float p, float p2) {
   switch (act) {
     case TGX_ACT_RELU: return fmaxf(z, 0.f);
     case TGX_ACT_LEAKY_RELU: return z > 0.f ? z : p * z;
@@ -45,12 +58,19 @@ __device__ __forceinline__ float activate(float z, int act, float p) {
     case TGX_ACT_SILU: return z * sigmoid(z);
     case TGX_ACT_GELU: return 0.5f * z * (1.f + erff(z * 0.70710678118654752f));
     case TGX_ACT_ELU: return z > 0.f ? z : p * (__expf(z) - 1.f);
+    case TGX_ACT_HARDTANH: return fminf(fmaxf(z, p), p2);
+    case TGX_ACT_SOFTPLUS: return softplus(z, p, p2);
+    case TGX_ACT_SELU: return kSeluScale * (z > 0.f ? z : kSeluAlpha * (__expf(z) - 1.f));
+    case TGX_ACT_MISH: return z * tanhf(softplus(z, 1.f, 20.f));
+    case TGX_ACT_HARDSIGMOID: return fminf(fmaxf(z * (1.f / 6.f) + 0.5f, 0.f), 1.f);
+    case TGX_ACT_HARDSWISH:
+      return z <= -3.f ? 0.f : (z >= 3.f ? z : z * (z + 3.f) * (1.f / 6.f));
     default: return z;
   }
 }
 
 // d activate / dz at z.
-__device__ __forceinline__ float activate_grad(float z, int act, float p) {
+__device__ __forceinline__ float activate_grad(float z, int act, float p, float p2) {
   switch (act) {
     case TGX_ACT_RELU: return z > 0.f ? 1.f : 0.f;
     case TGX_ACT_LEAKY_RELU: return z > 0.f ? 1.f : p;
@@ -71,6 +91,15 @@ __device__ __forceinline__ float activate_grad(float z, int act, float p) {
       return 0.5f * (1.f + erff(z * 0.70710678118654752f)) +
              z * 0.39894228040143268f * __expf(-0.5f * z * z);
     case TGX_ACT_ELU: return z > 0.f ? 1.f : p * __expf(z);
+    case TGX_ACT_HARDTANH: return (z > p && z < p2) ? 1.f : 0.f;
+    case TGX_ACT_SOFTPLUS: return p * z > p2 ? 1.f : sigmoid(p * z);
+    case TGX_ACT_SELU: return kSeluScale * (z > 0.f ? 1.f : kSeluAlpha * __expf(z));
+    case TGX_ACT_MISH: {
+      const float t = tanhf(softplus(z, 1.f, 20.f));
+      return t + z * sigmoid(z) * (1.f - t * t);
+    }
+    case TGX_ACT_HARDSIGMOID: return (z > -3.f && z < 3.f) ? (1.f / 6.f) : 0.f;
+    case TGX_ACT_HARDSWISH: return z < -3.f ? 0.f : (z <= 3.f ? z * (1.f / 3.f) + 0.5f : 1.f);
     default: return 1.f;
   }
 }
@@ -190,7 +219,8 @@ __device__ __forceinline__ void launder(MlpView& v) {
   asm volatile("" : "+s"(v.n_seg), "+s"(v.in_width));
 #pragma unroll
   for (int l = 0; l < kMaxLayers; ++l)
-    asm volatile("" : "+s"(v.n_out[l]), "+s"(v.nb_in[l]), "+s"(v.act[l]), "+s"(v.param[l]));
+    asm volatile("" : "+s"(v.n_out[l]), "+s"(v.nb_in[l]), "+s"(v.act[l]), "+s"(v.param[l]),
+                 "+s"(v.param2[l]));
 #pragma unroll
   for (int s = 0; s < kMaxSegments; ++s)
     asm volatile("" : "+s"(v.role[s]), "+s"(v.width[s]), "+s"(v.off[s]));
@@ -338,17 +368,21 @@ __device__ __forceinline__ void map_real(const float (&z)[W], float (&out)[W], i
   }
 }
 
+#define TGX_ACT_CASES(X)                                                                 \
+  X(TGX_ACT_RELU) X(TGX_ACT_LEAKY_RELU) X(TGX_ACT_TANH) X(TGX_ACT_SIGMOID) X(TGX_ACT_SILU) \
+  X(TGX_ACT_GELU) X(TGX_ACT_ELU) X(TGX_ACT_HARDTANH) X(TGX_ACT_SOFTPLUS) X(TGX_ACT_SELU)   \
+  X(TGX_ACT_MISH) X(TGX_ACT_HARDSIGMOID) X(TGX_ACT_HARDSWISH)
+
 template <int W>
 __device__ __forceinline__ void activate_all(const float (&z)[W], float (&a)[W], int act,
-                                             float p, int nb) {
+                                             float p, float p2, int nb) {
   switch (act) {
-    case TGX_ACT_RELU: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_RELU, 0.f); }); break;
-    case TGX_ACT_LEAKY_RELU: map_real<W>(z, a, nb, [p](float v, int) { return activate(v, TGX_ACT_LEAKY_RELU, p); }); break;
-    case TGX_ACT_TANH: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_TANH, 0.f); }); break;
-    case TGX_ACT_SIGMOID: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_SIGMOID, 0.f); }); break;
-    case TGX_ACT_SILU: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_SILU, 0.f); }); break;
-    case TGX_ACT_GELU: map_real<W>(z, a, nb, [](float v, int) { return activate(v, TGX_ACT_GELU, 0.f); }); break;
-    case TGX_ACT_ELU: map_real<W>(z, a, nb, [p](float v, int) { return activate(v, TGX_ACT_ELU, p); }); break;
+#define TGX_ACT_CASE(CODE)                                                                     \
+  case CODE:                                                                                   \
+    map_real<W>(z, a, nb, [p, p2](float v, int) { return activate(v, CODE, p, p2); });       \
+    break;
+    TGX_ACT_CASES(TGX_ACT_CASE)
+#undef TGX_ACT_CASE
     default: map_real<W>(z, a, nb, [](float v, int) { return v; }); break;
   }
 }
@@ -356,15 +390,16 @@ __device__ __forceinline__ void activate_all(const float (&z)[W], float (&a)[W],
 // dz[k] = g[k] * activate'(z[k]) for the real outputs, 0 beyond.
 template <int W>
 __device__ __forceinline__ void activate_grad_all(const float (&z)[W], const float (&g)[W],
-                                                  float (&dz)[W], int act, float p, int nb) {
+                                                  float (&dz)[W], int act, float p, float p2,
+                                                  int nb) {
   switch (act) {
-    case TGX_ACT_RELU: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_RELU, 0.f); }); break;
-    case TGX_ACT_LEAKY_RELU: map_real<W>(z, dz, nb, [&g, p](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_LEAKY_RELU, p); }); break;
-    case TGX_ACT_TANH: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_TANH, 0.f); }); break;
-    case TGX_ACT_SIGMOID: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_SIGMOID, 0.f); }); break;
-    case TGX_ACT_SILU: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_SILU, 0.f); }); break;
-    case TGX_ACT_GELU: map_real<W>(z, dz, nb, [&g](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_GELU, 0.f); }); break;
-    case TGX_ACT_ELU: map_real<W>(z, dz, nb, [&g, p](float v, int k) { return g[k] * activate_grad(v, TGX_ACT_ELU, p); }); break;
+#define TGX_ACT_CASE(CODE)                                                                     \
+  case CODE:                                                                                   \
+    map_real<W>(z, dz, nb,                                                                     \
+                [&g, p, p2](float v, int k) { return g[k] * activate_grad(v, CODE, p, p2); }); \
+    break;
+    TGX_ACT_CASES(TGX_ACT_CASE)
+#undef TGX_ACT_CASE
     default: map_real<W>(z, dz, nb, [&g](float, int k) { return g[k]; }); break;
   }
 }

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
       *reinterpret_cast<f32x4*>(out + i) = f32x4{a[i], a[i + 1], a[i + 2], a[i + 3]};
     if constexpr (l + 1 < L) {
       linear<W>(wg + l * (W * W + W), a, z[l], m.n_out[l], m.nb_in[l]);
-      activate_all<W>(z[l], a, m.act[l], m.param[l], m.nb_in[l + 1]);
+      activate_all<W>(z[l], a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1]);
     }
   });
   // Last layer: one output, gradient ds.
@@ -56,7 +56,8 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
   static_for<L - 1>([&](auto kc) {
     constexpr int l = L - 2 - decltype(kc)::value;
     float dzl[W];
-    activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.nb_in[l + 1]);
+    activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.param2[l],
+                         m.nb_in[l + 1]);
 #pragma unroll
     for (int o = 0; o < W; ++o) pin(dzl[o]);
     float* out = dz_out + l * plane + e * W;

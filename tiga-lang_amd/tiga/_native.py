@@ -49,7 +49,7 @@ class EdgeMlp(ctypes.Structure):
                 ("weights_dev", c_vp), ("n_segments", ctypes.c_int32),
                 ("seg_role", ctypes.c_int32 * 4), ("seg_width", ctypes.c_int32 * 4),
                 ("seg_stride", ctypes.c_int64 * 4), ("seg_dev", c_vp * 4),
-                ("out_width", ctypes.c_int32 * 3)]
+                ("out_width", ctypes.c_int32 * 3), ("act_param2", ctypes.c_float * 3)]
 
 
 # name -> argtypes (all return int status except where noted)
@@ -102,6 +102,9 @@ _SIGNATURES: dict[str, list] = {
     "tgx_edge_mlp_backward_workspace": [c_i64, P(EdgeMlp), P(c_size)],
     "tgx_edge_mlp_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, P(c_vp),
                               c_vp, c_size, c_vp],
+    "tgx_edge_mlp_hidden": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, ctypes.c_int32, c_vp],
+    "tgx_edge_mlp_backward_seeded": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp,
+                                     ctypes.c_int32, c_vp, P(c_vp), c_vp, c_size, c_vp],
     "tgx_segment_softmax_fwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tgx_segment_softmax_bwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tgx_segment_softmax_gather_fwd": [c_vp, c_vp, c_int, c_i64, c_vp, c_int, c_f32, c_vp,

@@ -280,9 +280,28 @@ class BlockAttentionFunction(torch.autograd.Function):
 _ROLE = {"src": 0, "dst": 1, "edge": 2}
 
 
-def _padded_width(chain, in_width: int) -> int:
-    widest = max([in_width] + [max(l.linear.in_features, l.linear.out_features) for l in chain])
+def _padded_width(chain, in_width: int, vector: bool = False) -> int:
+    """The common padded width of a chain's layers: every input and output
+    width, except the last layer's output for an edge-network sum (the
+    kernels never evaluate that layer)."""
+    outs = [l.linear.out_features for l in (chain[:-1] if vector else chain)]
+    widest = max([in_width] + [l.linear.in_features for l in chain] + outs)
     return next(w for w in (16, 24, 32, 64) if w >= widest)
+
+
+def _fill_weights(buf, chain, params, W, layers):
+    """Padded weight blocks for `layers`: W' = scale W, b' = scale b + shift
+    (the scalar affine map folded after each Linear)."""
+    for l in range(layers):
+        layer = chain[l]
+        weight, bias = params[2 * l], params[2 * l + 1]
+        out_f, in_f = weight.shape
+        buf[l, :W * W].view(W, W)[:out_f, :in_f] = weight.detach() * layer.scale
+        b = buf[l, W * W:W * W + out_f]
+        if bias is not None:
+            b.copy_(bias.detach() * layer.scale)
+        if layer.shift != 0.0:
+            b.add_(layer.shift)
 
 
 def _mlp_struct(chain, roles, segs, weights_buf, width):
@@ -294,7 +313,10 @@ def _mlp_struct(chain, roles, segs, weights_buf, width):
     for l, layer in enumerate(chain):
         m.act[l] = _ACT[layer.act]
         m.act_param[l] = layer.param
-        m.out_width[l] = layer.linear.out_features
+        m.act_param2[l] = layer.param2
+        # The last layer of an edge-network sum is applied by the caller;
+        # the kernels see it as a one-output layer they do not evaluate.
+        m.out_width[l] = layer.linear.out_features if l + 1 < len(chain) else 1
     m.weights_dev = weights_buf.data_ptr()
     m.n_segments = len(segs)
     for s, (role, seg) in enumerate(zip(roles, segs)):
@@ -330,12 +352,7 @@ class EdgeMlpFunction(torch.autograd.Function):
         W = _padded_width(chain, in_width)
         dev = col_idx.device
         buf = torch.zeros(len(chain), W * W + W, dtype=torch.float32, device=dev)
-        for l, layer in enumerate(chain):
-            weight, bias = params[2 * l], params[2 * l + 1]
-            out_f, in_f = weight.shape
-            buf[l, :W * W].view(W, W)[:out_f, :in_f] = weight.detach()
-            if bias is not None:
-                buf[l, W * W:W * W + out_f] = bias.detach()
+        _fill_weights(buf, chain, params, W, len(chain))
         mlp = _mlp_struct(chain, roles, segs, buf, W)
         scores = torch.empty(E, dtype=torch.float32, device=dev)
         _native.call("tgx_edge_mlp_scores", col_idx.data_ptr(), graph._dst_index32().data_ptr(),
@@ -368,27 +385,45 @@ class EdgeMlpFunction(torch.autograd.Function):
                      graph._dst_index32().data_ptr(), _native.idx_bits(row_ptr), E,
                      ctypes.byref(mlp), dscore.data_ptr(), dweights.data_ptr(), ptrs,
                      ws.data_ptr(), ws_bytes.value, _native.stream_of(col_idx))
-        grads = []
-        for s, (role, d, shape) in enumerate(zip(roles, dsegs, ctx.shapes)):
-            if not ctx.needs_input_grad[4 + s]:
-                grads.append(None)
-                continue
-            if role == "edge":
-                g = d
-            elif role == "src":
-                g = _reduce_rows_transposed(graph, d)
-            else:
-                g = _reduce_rows(graph, d)
-            grads.append(g.reshape(shape))
-        for l, layer in enumerate(chain):
-            out_f, in_f = layer.linear.out_features, layer.linear.in_features
-            k = 4 + ctx.n_seg + 2 * l
-            blk = dweights[l]
-            dW = blk[:W * W].view(W, W)[:out_f, :in_f] if ctx.needs_input_grad[k] else None
-            db = (blk[W * W:W * W + out_f] if ctx.has_bias[l] and ctx.needs_input_grad[k + 1]
-                  else None)
-            grads += [dW, db]
+        grads = _segment_grads(graph, roles, dsegs, ctx.shapes, ctx.needs_input_grad, 4)
+        grads += _layer_grads(chain, dweights, W, ctx.has_bias, ctx.needs_input_grad,
+                              4 + ctx.n_seg, len(chain))
         return (None, None, None, None, *grads)
+
+
+def _layer_grads(chain, dweights, W, has_bias, needs, first, layers):
+    """Weight and bias gradients of the module's own parameters from the
+    folded blocks' sums: dW = scale dW', db = scale db'."""
+    grads = []
+    for l in range(layers):
+        layer = chain[l]
+        out_f, in_f = layer.linear.out_features, layer.linear.in_features
+        k = first + 2 * l
+        blk = dweights[l]
+        dW = blk[:W * W].view(W, W)[:out_f, :in_f] if needs[k] else None
+        db = blk[W * W:W * W + out_f] if has_bias[l] and needs[k + 1] else None
+        if layer.scale != 1.0:
+            dW = None if dW is None else dW * layer.scale
+            db = None if db is None else db * layer.scale
+        grads += [dW, db]
+    return grads
+
+
+def _segment_grads(graph, roles, dsegs, shapes, needs, first):
+    """Per-edge input-segment gradients reduced onto their fields' rows."""
+    grads = []
+    for s, (role, d, shape) in enumerate(zip(roles, dsegs, shapes)):
+        if not needs[first + s]:
+            grads.append(None)
+            continue
+        if role == "edge":
+            g = d
+        elif role == "src":
+            g = _reduce_rows_transposed(graph, d)
+        else:
+            g = _reduce_rows(graph, d)
+        grads.append(g.reshape(shape))
+    return grads
 
 
 def _reduce_rows(graph: Graph, x: torch.Tensor) -> torch.Tensor:
@@ -515,3 +550,111 @@ def score_attention(graph: Graph, table: torch.Tensor, role: str, scale: float,
     the gathered segment softmax, then the weighted CSR sum."""
     alpha = ScoreSoftmaxFunction.apply(table, role, scale, graph)
     return CsrSumFunction.apply(value, alpha, graph)
+
+
+# ---------------------------------------------------------------------------
+# Edge-network messages summed per row (tg.sum() over tg.nn.trace(net)(...))
+
+def _row_degrees(graph: Graph) -> torch.Tensor:
+    row_ptr, _ = graph._kernel_csr()
+    got = graph._native_cache.get("degree_f32")
+    if got is None:
+        got = (row_ptr[1:] - row_ptr[:-1]).to(torch.float32)
+        graph._native_cache["degree_f32"] = got
+    return got
+
+
+class EdgeMlpSumFunction(torch.autograd.Function):
+    """out[i] = sum over row i's edges of net(concat of the fields gathered
+    for the edge).  The last Linear layer is linear, so the kernels evaluate
+    the layers before it per edge (tgx_edge_mlp_hidden), the CSR sum adds
+    those per row, and the last layer acts once per row:
+    out = S W'^T + deg b' (W', b' its folded weights).  Backward: the
+    last layer's gradients from S, and the gradient at its input,
+    dS = dout W', seeds the per-edge backward of the other layers
+    (tgx_edge_mlp_backward_seeded).
+
+    Inputs after (graph, chain, roles, n_seg): the n_seg field tensors, then
+    weight and bias (None allowed) of every Linear layer."""
+
+    @staticmethod
+    def forward(ctx, graph: Graph, chain, roles, n_seg: int, *tensors):
+        _on_graph_device(graph, *tensors)
+        segs = [_as_rows(t) for t in tensors[:n_seg]]
+        params = tensors[n_seg:]
+        row_ptr, col_idx = graph._kernel_csr()
+        E, L = col_idx.numel(), len(chain)
+        dev = col_idx.device
+        in_width = sum(x.shape[1] for x in segs)
+        W = _padded_width(chain, in_width, vector=True)
+        hw = chain[-1].linear.in_features
+        buf = torch.zeros(L, W * W + W, dtype=torch.float32, device=dev)
+        _fill_weights(buf, chain, params, W, L - 1)
+        mlp = _mlp_struct(chain, roles, segs, buf, W)
+        hidden = torch.empty(max(E, 1), hw, dtype=torch.float32, device=dev)[:E]
+        _native.call("tgx_edge_mlp_hidden", col_idx.data_ptr(), graph._dst_index32().data_ptr(),
+                     _native.idx_bits(row_ptr), E, ctypes.byref(mlp), hidden.data_ptr(), hw,
+                     _native.stream_of(col_idx))
+        sums = _reduce_rows(graph, hidden)
+        last = chain[-1]
+        w_last = params[2 * L - 2].detach() * last.scale
+        out = sums @ w_last.t()
+        b_last = params[2 * L - 1]
+        shift = torch.zeros(w_last.shape[0], dtype=torch.float32, device=dev) \
+            if b_last is None else b_last.detach() * last.scale
+        if last.shift != 0.0:
+            shift = shift + last.shift
+        if b_last is not None or last.shift != 0.0:
+            out = out + _row_degrees(graph)[:, None] * shift
+        ctx.graph, ctx.chain, ctx.roles, ctx.n_seg, ctx.W = graph, chain, roles, n_seg, W
+        ctx.shapes = [t.shape for t in tensors[:n_seg]]
+        ctx.has_bias = [params[2 * l + 1] is not None for l in range(L)]
+        ctx.save_for_backward(buf, sums, w_last, *segs)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        buf, sums, w_last, *segs = ctx.saved_tensors
+        graph, chain, roles, W = ctx.graph, ctx.chain, ctx.roles, ctx.W
+        row_ptr, col_idx = graph._kernel_csr()
+        E, L = col_idx.numel(), len(chain)
+        dev = col_idx.device
+        dout = dout.contiguous()
+        needs = ctx.needs_input_grad
+        last = chain[-1]
+        k_last = 4 + ctx.n_seg + 2 * (L - 1)
+        d_w_last = (dout.t() @ sums) * last.scale if needs[k_last] else None
+        d_b_last = None
+        if ctx.has_bias[L - 1] and needs[k_last + 1]:
+            d_b_last = (_row_degrees(graph)[:, None] * dout).sum(0) * last.scale
+        grads = [None] * ctx.n_seg
+        grads += [None] * (2 * (L - 1))
+        upstream = any(needs[4:k_last])
+        if upstream:
+            seed = (dout @ w_last).contiguous()
+            hw = seed.shape[1]
+            dsegs = [torch.empty(max(E, 1), x.shape[1], dtype=torch.float32,
+                                 device=dev)[:E] for x in segs]
+            mlp = _mlp_struct(chain, roles, segs, buf, W)
+            ws_bytes = ctypes.c_size_t()
+            _native.call("tgx_edge_mlp_backward_workspace", E, ctypes.byref(mlp),
+                         ctypes.byref(ws_bytes))
+            ws = torch.empty(max(ws_bytes.value, 4), dtype=torch.uint8, device=dev)
+            dweights = torch.empty(L, W * W + W, dtype=torch.float32, device=dev)
+            ptrs = (ctypes.c_void_p * 4)(*[d.data_ptr() for d in dsegs],
+                                         *([None] * (4 - len(dsegs))))
+            _native.call("tgx_edge_mlp_backward_seeded", col_idx.data_ptr(),
+                         graph._dst_index32().data_ptr(), _native.idx_bits(row_ptr), E,
+                         ctypes.byref(mlp), seed.data_ptr(), hw, dweights.data_ptr(), ptrs,
+                         ws.data_ptr(), ws_bytes.value, _native.stream_of(col_idx))
+            grads = _segment_grads(graph, roles, dsegs, ctx.shapes, needs, 4)
+            grads += _layer_grads(chain, dweights, W, ctx.has_bias, needs, 4 + ctx.n_seg, L - 1)
+        return (None, None, None, None, *grads, d_w_last, d_b_last)
+
+
+def nn_message_sum(graph: Graph, chain, roles, fields) -> torch.Tensor:
+    """out[i] = sum_e net(fields_e) over row i's edges on the HIP path."""
+    params = []
+    for layer in chain:
+        params += [layer.linear.weight, layer.linear.bias]
+    return EdgeMlpSumFunction.apply(graph, chain, tuple(roles), len(fields), *fields, *params)

@@ -8,6 +8,7 @@ The captured tree is then matched against the four patterns that have HIP
 kernels:
 
 * weighted sum   ``[edge.w *] src.x``                      with ``tg.sum()``
+* edge network   ``tg.nn.trace(net)(fields...) [* c]``     with ``tg.sum()``
 * GAT additive   ``leaky_relu((src.h*a_s).sum(-1) + (dst.h*a_d).sum(-1))``,
                  value ``src.h``                            with online softmax
 * dot product    ``(src.k*dst.q).sum(-1) [* scale] [+ edge.b]``, value ``src.v``
@@ -326,27 +327,78 @@ class NnAttention:
     module: Any                               # tiga.nn.TracedModule
     inputs: tuple[tuple[str, str], ...]       # (role, field) in concatenation order
     value_field: str                          # src.v
+    out_scale: float = 1.0                    # scalar applied to the score
 
 
-def recognize_nn_attention(item) -> NnAttention | None:
-    """reducer(trace(net)(fields...), src.v) with a score chain the edge MLP
-    kernels cover (reference compiler/edge_nn_attention.py:66-107)."""
-    if not isinstance(item, OnlineSoftmaxItem):
-        return None
-    score, value = item.score, item.value
-    if not _is_field(value, "src"):
-        return None
-    if not (isinstance(score, Sym) and score.op == "nn"):
-        return None
-    module, inputs = score.args
-    if not inputs or module.chain() is None:
-        return None
+def _scaled_nn(s):
+    """trace(net)(fields...) optionally times a scalar: (nn Sym, scale)."""
+    if isinstance(s, Sym) and s.op == "nn":
+        return s, 1.0
+    if isinstance(s, Sym) and s.op == "neg" and isinstance(s.args[0], Sym) and \
+            s.args[0].op == "nn":
+        return s.args[0], -1.0
+    if isinstance(s, Sym) and s.op == "mul":
+        m = _pair(s, lambda x: isinstance(x, Sym) and x.op == "nn", _is_scalar)
+        if m is not None:
+            return m[0], m[1].args[0]
+    if isinstance(s, Sym) and s.op == "div" and isinstance(s.args[0], Sym) and \
+            s.args[0].op == "nn" and _is_scalar(s.args[1]) and s.args[1].args[0] != 0:
+        return s.args[0], 1.0 / s.args[1].args[0]
+    return None
+
+
+def _nn_fields(inputs):
     fields = []
     for x in inputs:
         if not _is_field(x):
             return None
         fields.append(tuple(x.args))
-    return NnAttention(module=module, inputs=tuple(fields), value_field=value.args[1])
+    return tuple(fields) if fields else None
+
+
+def recognize_nn_attention(item) -> NnAttention | None:
+    """reducer(trace(net)(fields...) [* c], src.v) with a score chain the
+    edge MLP kernels cover (reference compiler/edge_nn_attention.py:66-107)."""
+    if not isinstance(item, OnlineSoftmaxItem):
+        return None
+    value = item.value
+    if not _is_field(value, "src"):
+        return None
+    got = _scaled_nn(item.score)
+    if got is None:
+        return None
+    node, scale = got
+    module, inputs = node.args
+    fields = _nn_fields(inputs)
+    if fields is None or module.chain() is None:
+        return None
+    return NnAttention(module=module, inputs=fields, value_field=value.args[1],
+                       out_scale=float(scale))
+
+
+@dataclass(frozen=True)
+class NnSum:
+    module: Any                               # tiga.nn.TracedModule
+    inputs: tuple[tuple[str, str], ...]
+    out_scale: float = 1.0
+
+
+def recognize_nn_sum(message) -> NnSum | None:
+    """tg.sum() of trace(net)(fields...) [* c]: the reference's edge-NN tile
+    (compiler/edge_nn_tile.py:1-30, message_passing.py:2134-2300)."""
+    if isinstance(message, ReducerCall):
+        if len(message.messages) != 1:
+            return None
+        message = message.messages[0]
+    got = _scaled_nn(message)
+    if got is None:
+        return None
+    node, scale = got
+    module, inputs = node.args
+    fields = _nn_fields(inputs)
+    if fields is None or module.chain(vector=True) is None:
+        return None
+    return NnSum(module=module, inputs=fields, out_scale=float(scale))
 
 
 def capture(edge_fn, params: dict[str, Any]):
@@ -374,6 +426,7 @@ __all__ = [
     "FieldNamespace",
     "GatAdditive",
     "NnAttention",
+    "NnSum",
     "ScoreSoftmax",
     "Sym",
     "WeightedSum",
@@ -381,6 +434,7 @@ __all__ = [
     "recognize_dot",
     "recognize_gat",
     "recognize_nn_attention",
+    "recognize_nn_sum",
     "recognize_score_softmax",
     "recognize_weighted_sum",
 ]

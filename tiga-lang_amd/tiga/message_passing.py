@@ -366,7 +366,7 @@ class MessagePassing(Kernel):
 
     def _plan_native(self, captured, graph, src, dst, edge, params) -> _Launch | None:
         if isinstance(self.reducer, SumReducer):
-            return self._plan_sum(captured, graph, src, edge)
+            return self._plan_sum(captured, graph, src, dst, edge)
         if not isinstance(self.reducer, OnlineSoftmaxReducer):
             return None
         if self.reducer.accumulation_dtype not in (None, torch.float32, "float32"):
@@ -422,13 +422,16 @@ class MessagePassing(Kernel):
             f"score gradient reduced per {role} row")
         return _Launch(graph, ((role, raw.score_field), ("src", raw.value_field)), run, describe)
 
-    def _plan_sum(self, captured, graph, src, edge) -> _Launch | None:
+    def _plan_sum(self, captured, graph, src, dst, edge) -> _Launch | None:
         from . import _ops
 
         if self.reducer.identity_value != 0 or graph.is_varlen or graph.is_dense:
             return None
         pat = cap.recognize_weighted_sum(captured)
-        if pat is None or pat.src_field not in src:
+        if pat is None:
+            nn_sum = cap.recognize_nn_sum(captured)
+            return None if nn_sum is None else self._plan_nn_sum(nn_sum, graph, src, dst, edge)
+        if pat.src_field not in src:
             return None
         x = src[pat.src_field]
         if x.dtype != torch.float32:
@@ -490,6 +493,77 @@ class MessagePassing(Kernel):
         return _Launch(graph, operands, run, describe,
                        aliases=((("src", gat.h_field), ("dst", gat.dst_field)),))
 
+    @staticmethod
+    def _nn_fields(inputs, graph, src, dst, edge):
+        """(widths, roles) of an edge network's input fields if every one is a
+        fp32 [rows] or [rows, k] tensor of its role, else None."""
+        groups = {"src": src, "dst": dst, "edge": edge}
+        rows = {"src": graph.schema.num_src, "dst": graph.schema.num_dst,
+                "edge": graph.num_edges}
+        widths, roles = [], []
+        for role, name in inputs:
+            t = groups[role].get(name)
+            if t is None or t.dtype != torch.float32 or t.ndim not in (1, 2) or \
+                    t.shape[0] != rows[role]:
+                return None
+            widths.append(1 if t.ndim == 1 else t.shape[1])
+            roles.append(role)
+        if len(widths) > 4:
+            return None
+        return widths, tuple(roles)
+
+    @staticmethod
+    def _scaled_chain(chain, out_scale):
+        """The chain with a scalar applied to its output folded into its last
+        layer."""
+        if out_scale == 1.0:
+            return chain
+        import dataclasses
+
+        last = chain[-1]
+        return (*chain[:-1], dataclasses.replace(last, scale=last.scale * out_scale,
+                                                 shift=last.shift * out_scale))
+
+    def _plan_nn_sum(self, item, graph, src, dst, edge) -> _Launch | None:
+        """tg.sum() over a tg.nn.trace message (reference edge-NN tile,
+        interop/torch/message_passing.py:2134-2300; fp32 fields): the layers
+        before the last per edge on the edge MLP kernels, summed per row, the
+        last layer once per row."""
+        from . import _ops
+
+        got = self._nn_fields(item.inputs, graph, src, dst, edge)
+        if got is None:
+            return None
+        widths, roles = got
+        chain = item.module.chain(vector=True)
+        if sum(widths) != chain[0].linear.in_features:
+            return None     # the eager evaluator raises the network's own shape error
+        if _ops._padded_width(chain, sum(widths), vector=True) > 32:
+            return None
+        device = graph.device
+        for layer in chain:
+            for p in (layer.linear.weight, layer.linear.bias):
+                if p is not None and (p.dtype != torch.float32 or p.device != device):
+                    return None
+        _native.lib()
+        out_scale = item.out_scale
+
+        def run(module, *fields):
+            return _ops.nn_message_sum(graph, self._scaled_chain(module.chain(vector=True),
+                                                                 out_scale), roles,
+                                       [f if f.ndim == 2 else f.unsqueeze(-1) for f in fields])
+
+        layer_widths = "-".join(str(l.linear.in_features) for l in chain)
+        describe = lambda: self._variant(
+            graph, "edge-network-sum",
+            ("tgx_edge_mlp_hidden", "tgx_csr_sum_fwd", "tgx_edge_mlp_backward_seeded",
+             "tgx_csr_sum_bwd"),
+            f"edge network {layer_widths}-{chain[-1].linear.out_features}: layers before the "
+            "last evaluated per edge (one edge per lane), summed per row by the CSR sum, the "
+            "last Linear applied once per row; backward seeds the per-edge replay with the "
+            "last layer's input gradient gathered per row")
+        return _Launch(graph, (("fixed", item.module), *item.inputs), run, describe)
+
     def _plan_nn_attention(self, item, graph, src, dst, edge) -> _Launch | None:
         """tg.nn.trace-scored attention on the edge MLP kernels (reference
         interop/torch/message_passing.py:2372-2577, envelope: fp32, CSR
@@ -525,8 +599,10 @@ class MessagePassing(Kernel):
         _native.lib()
         roles = tuple(roles)
 
+        out_scale = item.out_scale
+
         def run(module, value, *fields):
-            return _ops.nn_attention(graph, module.chain(), roles,
+            return _ops.nn_attention(graph, self._scaled_chain(module.chain(), out_scale), roles,
                                      [f if f.ndim == 2 else f.unsqueeze(-1) for f in fields],
                                      value)
 

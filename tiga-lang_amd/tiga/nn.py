@@ -10,11 +10,17 @@ python/tiga/nn/__init__.py): ``trace(module)`` wraps a module so one
   field expressions, which the nn-attention recognizer lowers to the HIP edge
   MLP kernels when the module is a chain the kernels cover.
 
-Covered chains: ``nn.Linear`` layers (bias optional) separated by one
-component-wise activation each (relu, leaky_relu, tanh, sigmoid, silu, exact
-gelu, elu; module or functional form; ``nn.Identity`` is skipped), ending in
-a Linear layer with one output, at most three Linear layers, every width
-at most 64.  Anything else runs on the eager evaluator.
+Covered chains: ``nn.Linear`` layers (bias optional), each optionally
+followed by scalar-constant arithmetic (``x * c``, ``x / c``, ``x + c``,
+``x - c``, ``c - x``, ``-x``: folded into that layer's weights and bias) and
+by one component-wise activation (relu, leaky_relu, tanh, sigmoid, silu,
+exact gelu, elu, hardtanh / relu6 / clamp, softplus, selu, mish,
+hardsigmoid, hardswish; module or functional form; ``nn.Identity`` is
+skipped), at most three Linear layers.  A score network ends in a Linear
+layer with one output and every width is at most 64; an edge-network
+message summed per row (``tg.sum()``) ends in a Linear layer of any width
+and its other widths are at most 32.  Anything else (LayerNorm, arithmetic
+after an activation, ...) runs on the eager evaluator.
 """
 
 from __future__ import annotations
@@ -30,16 +36,21 @@ from torch import nn
 _CHAINS: "weakref.WeakKeyDictionary[nn.Module, object]" = weakref.WeakKeyDictionary()
 
 _ACT = {"identity": 0, "relu": 1, "leaky_relu": 2, "tanh": 3, "sigmoid": 4, "silu": 5,
-        "gelu": 6, "elu": 7}
+        "gelu": 6, "elu": 7, "hardtanh": 8, "softplus": 9, "selu": 10, "mish": 11,
+        "hardsigmoid": 12, "hardswish": 13}
 
 
 @dataclass(frozen=True)
 class ScoreLayer:
-    """One Linear layer of a score chain and the activation that follows it."""
+    """One Linear layer of a chain, the scalar affine map folded after it
+    (z = scale * (W a + b) + shift) and the activation that follows."""
 
     linear: nn.Linear
     act: str = "identity"
     param: float = 0.0
+    param2: float = 0.0
+    scale: float = 1.0
+    shift: float = 0.0
 
 
 class TracedModule(nn.Module):
@@ -48,7 +59,6 @@ class TracedModule(nn.Module):
     def __init__(self, module: nn.Module):
         super().__init__()
         self.module = module
-        self._chain: tuple[ScoreLayer, ...] | None | bool = False
 
     def forward(self, *inputs):
         from .capture import Sym
@@ -66,20 +76,23 @@ class TracedModule(nn.Module):
             return Sym("nn", (self, tuple(inputs)))
         return super().__call__(*inputs)
 
-    def chain(self) -> tuple[ScoreLayer, ...] | None:
-        """The module as a score chain the HIP kernels cover, else None.
-        Computed once per module object (a module whose layers are replaced
-        afterwards must be wrapped anew by a fresh module object)."""
-        if self._chain is False:
-            got = _CHAINS.get(self.module, False)
-            if got is False:
-                try:
-                    got = _extract_chain(self.module)
-                except NotImplementedError:
-                    got = None
-                _CHAINS[self.module] = got
-            self._chain = got
-        return self._chain
+    def chain(self, vector: bool = False) -> tuple[ScoreLayer, ...] | None:
+        """The module as a chain the HIP kernels cover, else None: a score
+        chain (one output) or, with vector=True, an edge-network message of
+        any output width.  Computed once per module object (a module whose
+        layers are replaced afterwards must be wrapped by a new object)."""
+        got = _CHAINS.get(self.module)
+        if got is None:
+            try:
+                got = _extract_chain(self.module)
+            except NotImplementedError:
+                got = ()
+            _CHAINS[self.module] = got
+        if not got:
+            return None
+        if not vector and got[-1].linear.out_features != 1:
+            return None
+        return got
 
 
 def trace(module: nn.Module) -> TracedModule:
@@ -92,17 +105,31 @@ def trace(module: nn.Module) -> TracedModule:
 
 
 def _module_activation(m: nn.Module):
-    simple = {nn.ReLU: "relu", nn.Tanh: "tanh", nn.Sigmoid: "sigmoid", nn.SiLU: "silu"}
+    simple = {nn.ReLU: "relu", nn.Tanh: "tanh", nn.Sigmoid: "sigmoid", nn.SiLU: "silu",
+              nn.SELU: "selu", nn.Mish: "mish", nn.Hardsigmoid: "hardsigmoid",
+              nn.Hardswish: "hardswish"}
     for cls, name in simple.items():
         if type(m) is cls:
-            return name, 0.0
+            return name, 0.0, 0.0
     if type(m) is nn.LeakyReLU:
-        return "leaky_relu", float(m.negative_slope)
+        return "leaky_relu", float(m.negative_slope), 0.0
     if type(m) is nn.ELU:
-        return "elu", float(m.alpha)
+        return "elu", float(m.alpha), 0.0
     if type(m) is nn.GELU and m.approximate == "none":
-        return "gelu", 0.0
+        return "gelu", 0.0, 0.0
+    if type(m) is nn.ReLU6:
+        return "hardtanh", 0.0, 6.0
+    if type(m) is nn.Hardtanh:
+        return "hardtanh", float(m.min_val), float(m.max_val)
+    if type(m) is nn.Softplus:
+        return "softplus", float(m.beta), float(m.threshold)
     return None
+
+
+def _arg(args, kwargs, index, name, default):
+    if len(args) > index:
+        return args[index]
+    return kwargs.get(name, default)
 
 
 def _function_activation(target, args, kwargs, previous):
@@ -110,68 +137,137 @@ def _function_activation(target, args, kwargs, previous):
 
     if not args or args[0] is not previous:
         return None
-    simple = {torch.relu: "relu", F.relu: "relu", torch.tanh: "tanh",
-              torch.sigmoid: "sigmoid", F.silu: "silu"}
-    if target in simple and len(args) == 1 and not kwargs:
-        return simple[target], 0.0
+    simple = {torch.relu: "relu", F.relu: "relu", torch.tanh: "tanh", F.tanh: "tanh",
+              torch.sigmoid: "sigmoid", F.sigmoid: "sigmoid", F.silu: "silu", F.selu: "selu",
+              torch.selu: "selu", F.mish: "mish", F.hardsigmoid: "hardsigmoid",
+              F.hardswish: "hardswish", F.relu6: "relu6"}
+    if target in simple and len(args) == 1 and set(kwargs) <= {"inplace"}:
+        name = simple[target]
+        return ("hardtanh", 0.0, 6.0) if name == "relu6" else (name, 0.0, 0.0)
     if target is F.leaky_relu:
-        slope = kwargs.get("negative_slope", args[1] if len(args) > 1 else 0.01)
-        return "leaky_relu", float(slope)
+        return "leaky_relu", float(_arg(args, kwargs, 1, "negative_slope", 0.01)), 0.0
     if target is F.elu:
-        return "elu", float(kwargs.get("alpha", args[1] if len(args) > 1 else 1.0))
+        return "elu", float(_arg(args, kwargs, 1, "alpha", 1.0)), 0.0
     if target is F.gelu and kwargs.get("approximate", "none") == "none":
-        return "gelu", 0.0
+        return "gelu", 0.0, 0.0
+    if target is F.hardtanh:
+        return ("hardtanh", float(_arg(args, kwargs, 1, "min_val", -1.0)),
+                float(_arg(args, kwargs, 2, "max_val", 1.0)))
+    if target is F.softplus:
+        return ("softplus", float(_arg(args, kwargs, 1, "beta", 1.0)),
+                float(_arg(args, kwargs, 2, "threshold", 20.0)))
+    if target in (torch.clamp, torch.clip):
+        lo = _arg(args, kwargs, 1, "min", None)
+        hi = _arg(args, kwargs, 2, "max", None)
+        if lo is None and hi is None:
+            return None
+        return ("hardtanh", -float("inf") if lo is None else float(lo),
+                float("inf") if hi is None else float(hi))
+    return None
+
+
+def _scalar_affine(node, previous):
+    """(scale, shift) of a scalar-constant arithmetic node applied to
+    `previous`: y = scale * x + shift; None if it is not one."""
+    import numbers
+    import operator
+
+    if node.op != "call_function" or not node.args:
+        return None
+    a = node.args
+    number = lambda v: isinstance(v, numbers.Number) and not isinstance(v, bool)
+    t = node.target
+    if t in (operator.neg, torch.neg) and len(a) == 1 and a[0] is previous:
+        return -1.0, 0.0
+    if len(a) != 2:
+        return None
+    if t in (operator.mul, torch.mul):
+        if a[0] is previous and number(a[1]):
+            return float(a[1]), 0.0
+        if a[1] is previous and number(a[0]):
+            return float(a[0]), 0.0
+    if t in (operator.truediv, torch.div) and a[0] is previous and number(a[1]) and a[1] != 0:
+        return 1.0 / float(a[1]), 0.0
+    if t in (operator.add, torch.add):
+        if a[0] is previous and number(a[1]):
+            return 1.0, float(a[1])
+        if a[1] is previous and number(a[0]):
+            return 1.0, float(a[0])
+    if t in (operator.sub, torch.sub):
+        if a[0] is previous and number(a[1]):
+            return 1.0, -float(a[1])
+        if a[1] is previous and number(a[0]):
+            return -1.0, float(a[0])
     return None
 
 
 def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
-    """Linear (act Linear)* with one output, via torch.fx (reference
-    nn_capture.py:281-380 translates the same graphs)."""
+    """Linear [affine]* [act] ... Linear [affine]*, via torch.fx (reference
+    nn_capture.py:281-380 translates the same graphs).  Scalar affine maps
+    are only taken directly after a Linear layer, where they fold into it."""
     import torch.fx
 
+    if isinstance(module, nn.Linear):
+        # A bare Linear traced as the root shows its functional body.
+        if max(module.in_features, module.out_features) > 64:
+            raise NotImplementedError("network widths above 64")
+        return (ScoreLayer(module),)
     gm = torch.fx.symbolic_trace(module)
-    layers: list[list] = []          # [linear, act, param]
+    layers: list[dict] = []
     previous = None
     for node in gm.graph.nodes:
         if node.op == "placeholder":
             if previous is not None:
-                raise NotImplementedError("score networks take one input")
+                raise NotImplementedError("networks take one input")
             previous = node
             continue
         if node.op == "output":
             if node.args[0] is not previous:
-                raise NotImplementedError("score network output is not the chain's end")
+                raise NotImplementedError("network output is not the chain's end")
             break
         if node.op == "call_module":
             target = gm.get_submodule(node.target)
             if node.args != (previous,):
-                raise NotImplementedError("score networks must be single-input chains")
+                raise NotImplementedError("networks must be single-input chains")
             if isinstance(target, nn.Identity):
                 previous = node
                 continue
             if isinstance(target, nn.Linear):
-                layers.append([target, None, 0.0])
+                layers.append({"linear": target, "act": None, "param": 0.0, "param2": 0.0,
+                               "scale": 1.0, "shift": 0.0})
                 previous = node
                 continue
             act = _module_activation(target)
         elif node.op == "call_function":
+            affine = _scalar_affine(node, previous)
+            if affine is not None:
+                if not layers or layers[-1]["act"] is not None:
+                    raise NotImplementedError("scalar arithmetic only directly after a Linear")
+                c, b = affine
+                layers[-1]["scale"] *= c
+                layers[-1]["shift"] = c * layers[-1]["shift"] + b
+                previous = node
+                continue
             act = _function_activation(node.target, node.args, node.kwargs, previous)
         else:
-            raise NotImplementedError(f"unsupported score network node {node.op}")
-        if act is None or not layers or layers[-1][1] is not None:
+            raise NotImplementedError(f"unsupported network node {node.op}")
+        if act is None or not layers or layers[-1]["act"] is not None:
             raise NotImplementedError("activations must follow a Linear layer, one each")
-        layers[-1][1], layers[-1][2] = act
+        layers[-1]["act"], layers[-1]["param"], layers[-1]["param2"] = act
         previous = node
     if not layers or len(layers) > 3:
-        raise NotImplementedError("score networks have one to three Linear layers")
-    if layers[-1][1] is not None or layers[-1][0].out_features != 1:
-        raise NotImplementedError("the last layer must be a Linear with one output")
-    for (a, _, _), (b, _, _) in zip(layers, layers[1:]):
-        if a.out_features != b.in_features:
-            raise NotImplementedError("score network widths do not chain")
-    if max(max(l.in_features, l.out_features) for l, _, _ in layers) > 64:
-        raise NotImplementedError("score network widths above 64")
-    return tuple(ScoreLayer(l, a or "identity", p) for l, a, p in layers)
+        raise NotImplementedError("networks have one to three Linear layers")
+    if layers[-1]["act"] is not None:
+        raise NotImplementedError("the chain must end in a Linear layer")
+    for a, b in zip(layers, layers[1:]):
+        if a["linear"].out_features != b["linear"].in_features:
+            raise NotImplementedError("network widths do not chain")
+    widths = [l["linear"].in_features for l in layers] + \
+        [l["linear"].out_features for l in layers[:-1]]
+    if max(widths) > 64:
+        raise NotImplementedError("network widths above 64")
+    return tuple(ScoreLayer(l["linear"], l["act"] or "identity", l["param"], l["param2"],
+                            l["scale"], l["shift"]) for l in layers)
 
 
 __all__ = ["ScoreLayer", "TracedModule", "trace"]
