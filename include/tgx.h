@@ -239,8 +239,10 @@ int tgx_csr_sum_bwd(const int32_t* row_ptr_t_dev, const int32_t* col_t_dev,
  * [0] logsumexp of the row's scores (-inf for an empty row), [1] reserved for
  * the backward (delta = <dout, out>), [2] a_dst.h[i], [3] a_src.h[i].
  * partial_dev: tgx_partial_bytes(plan, H*D + 2*H) bytes (NULL if no split rows).
- * Supported shapes: D % 4 == 0 and H*D in {64, 128, 256}; others return
- * TGX_UNSUPPORTED.
+ * Supported shapes: any H >= 1 with D in {4, 8, 16, 32, 64, 128, 256}
+ * (others return TGX_UNSUPPORTED).  Heads run in groups of a power-of-two
+ * count with at most 256 floats per node (H = 8, D = 64: two groups of 4),
+ * one after another on `stream`, each over its strided slice of the rows.
  * The reference evaluates this edge function with its eager oracle
  * (interop/torch/message_passing.py:2848-2894 -> reducer_oracle.py:60-137). */
 int tgx_gat_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
@@ -280,7 +282,9 @@ int tgx_gat_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
  * 16-bit storage); bias [E, H] fp32 or NULL.  ml [n_dst, H, 2] fp32 receives
  * {logsumexp (-inf for an empty row), 0}.  partial_dev:
  * tgx_partial_bytes(plan, H*D + 2*H) bytes (NULL without split rows).
- * Supported: D % 8 == 0, H*D in {128, 256, 512}.
+ * Supported: any H >= 1 with D in {8, 16, 32, 64, 128, 256, 512}.  Heads run
+ * in groups of a power-of-two count with at most 512 values per node (H = 16,
+ * D = 64: two groups of 8), one after another on `stream`.
  * Replaces the eager evaluation of (src.k*dst.q).sum(-1)*scale + edge.bias
  * (interop/torch/message_passing.py:2848-2894, reducer_oracle.py:60-137). */
 int tgx_dot_attn_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,

@@ -198,7 +198,12 @@ class GAT(tg.MessagePassing):
         return self.reducer(s, src.h)
 
 
-@pytest.mark.parametrize("H,D", [(8, 32), (4, 32), (2, 32), (16, 16), (4, 64)])
+# Heads run in groups of at most 256 floats per node: (8, 64) is two groups
+# of 4 heads, (3, 64) groups 2 + 1, (6, 16) 4 + 2, (5, 8) 4 + 1, (12, 32)
+# 8 + 4, (2, 256) two one-head groups of 64 lanes; (1, 4) is one lane per head.
+@pytest.mark.parametrize("H,D", [(8, 32), (4, 32), (2, 32), (16, 16), (4, 64), (8, 64),
+                                 (3, 64), (6, 16), (5, 8), (12, 32), (1, 128), (2, 256),
+                                 (1, 4)])
 @pytest.mark.parametrize("idx", [torch.int32, torch.int64])
 def test_gat_fwd_bwd_parity(H, D, idx):
     print(f"gat H={H} D={D} {idx}", flush=True)
@@ -273,7 +278,11 @@ def _bf16(a):
     return torch.as_tensor(a, device=DEV).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("H,D", [(4, 64), (2, 64), (8, 64), (16, 16)])
+# Heads run in groups of at most 512 values per node: (16, 64) is two groups
+# of 8 heads, (3, 64) groups 2 + 1, (6, 128) 4 + 2, (5, 32) 4 + 1, (12, 16)
+# 8 + 4, (1, 512) one head over 64 lanes; (1, 8) is one lane per head.
+@pytest.mark.parametrize("H,D", [(4, 64), (2, 64), (8, 64), (16, 16), (16, 64), (3, 64),
+                                 (6, 128), (5, 32), (12, 16), (1, 512), (1, 8)])
 @pytest.mark.parametrize("idx", [torch.int32, torch.int64])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_dot_fwd_bwd_parity_rmat(H, D, idx, with_bias):

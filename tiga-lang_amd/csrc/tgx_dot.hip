@@ -91,6 +91,9 @@ struct DotFwdArgs {
   uint16_t* out;
   float* ml;          // [N, H, 2]
   float* partial;     // per chunk: acc[8G] | m[H] | l[H]
+  int64_t ld;         // values between consecutive nodes' rows of q, k, v, out
+  int64_t mld;        // floats between consecutive nodes' rows of ml
+  int64_t bld;        // floats between consecutive edges' rows of bias
 };
 
 template <typename I, int G, int HL, int U>
@@ -109,10 +112,10 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
     for (int r = 0; r < t.n_empty; ++r) {
       const int64_t i = uniform(a.plan.rows[t.empty0 + r]);
       if (g == 0) {
-        stv(a.out + i * HD + 8 * c, u32x4{0u, 0u, 0u, 0u});
+        stv(a.out + i * a.ld + 8 * c, u32x4{0u, 0u, 0u, 0u});
         if (head_lead) {
-          a.ml[(i * H + hd) * 2] = kNegInf;
-          a.ml[(i * H + hd) * 2 + 1] = 0.f;
+          a.ml[i * a.mld + hd * 2] = kNegInf;
+          a.ml[i * a.mld + hd * 2 + 1] = 0.f;
         }
       }
     }
@@ -120,7 +123,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
   }
   const int64_t row = t.row;
   float qf[8];
-  unpack8(ldv(a.q + row * HD + 8 * c), qf);
+  unpack8(ldv(a.q + row * a.ld + 8 * c), qf);
   SoftState<8> st;
   st.init();
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
@@ -133,9 +136,9 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
-        kk[u] = ldv(a.k + static_cast<int64_t>(j) * HD + 8 * c);
-        vv[u] = ldv(a.v + static_cast<int64_t>(j) * HD + 8 * c);
-        bb[u] = (a.bias && slot < n) ? a.bias[(base + slot) * H + hd] : 0.f;
+        kk[u] = ldv(a.k + static_cast<int64_t>(j) * a.ld + 8 * c);
+        vv[u] = ldv(a.v + static_cast<int64_t>(j) * a.ld + 8 * c);
+        bb[u] = (a.bias && slot < n) ? a.bias[(base + slot) * a.bld + hd] : 0.f;
       }
       float s[U];
       float mc = kNegInf;
@@ -174,17 +177,17 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
   float o[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) o[q] = st.acc[q] * inv;
-  stv(a.out + row * HD + 8 * c, pack8(o));
+  stv(a.out + row * a.ld + 8 * c, pack8(o));
   if (head_lead) {
-    a.ml[(row * H + hd) * 2] = st.m + __logf(st.l);
-    a.ml[(row * H + hd) * 2 + 1] = 0.f;
+    a.ml[row * a.mld + hd * 2] = st.m + __logf(st.l);
+    a.ml[row * a.mld + hd * 2 + 1] = 0.f;
   }
 }
 
 template <int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
     PlanView plan, const float* __restrict__ partial, uint16_t* __restrict__ out,
-    float* __restrict__ ml) {
+    float* __restrict__ ml, int64_t ld, int64_t mld) {
   constexpr int HD = 8 * G;
   constexpr int H = G / HL;
   const int64_t k = global_wave();
@@ -206,10 +209,10 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
   float o[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) o[q] = st.acc[q] * inv;
-  stv(out + row * HD + 8 * c, pack8(o));
+  stv(out + row * ld + 8 * c, pack8(o));
   if (c % HL == 0) {
-    ml[(row * H + hd) * 2] = st.m + __logf(st.l);
-    ml[(row * H + hd) * 2 + 1] = 0.f;
+    ml[row * mld + hd * 2] = st.m + __logf(st.l);
+    ml[row * mld + hd * 2 + 1] = 0.f;
   }
 }
 
@@ -219,18 +222,16 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
 template <int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void dot_delta_kernel(
     const uint16_t* __restrict__ dout, const uint16_t* __restrict__ out,
-    float* __restrict__ ml, int64_t n_nodes) {
+    float* __restrict__ ml, int64_t n_nodes, int64_t ld, int64_t mld) {
   constexpr int EPW = kWave / G;
-  constexpr int HD = 8 * G;
-  constexpr int H = G / HL;
   const int lane = lane_id();
   const int c = lane % G, hd = c / HL;
   const int64_t node = global_wave() * EPW + lane / G;
   if (node >= n_nodes) return;
   float d[8];
-  unpack8(ldv(dout + node * HD + 8 * c), d);
-  const float delta = group_sum<HL>(dot8(d, ldv(out + node * HD + 8 * c)));
-  if (c % HL == 0) ml[(node * H + hd) * 2 + 1] = delta;
+  unpack8(ldv(dout + node * ld + 8 * c), d);
+  const float delta = group_sum<HL>(dot8(d, ldv(out + node * ld + 8 * c)));
+  if (c % HL == 0) ml[node * mld + hd * 2 + 1] = delta;
 }
 
 template <typename I>
@@ -248,13 +249,15 @@ struct DotDstArgs {
   uint16_t* dq;
   float* dbias;     // [E, H] or null
   float* partial;   // per chunk: [8G] unscaled dq
+  int64_t ld;       // values between consecutive nodes' rows of q, k, v, dout, dq
+  int64_t mld;      // floats between consecutive nodes' rows of ml
+  int64_t bld;      // floats between consecutive edges' rows of bias and dbias
 };
 
 template <typename I, int G, int HL, int U>
 __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a) {
   constexpr int EPW = kWave / G;
   constexpr int HD = 8 * G;
-  constexpr int H = G / HL;
   const Task t = decode_task(a.plan, a.row_ptr, global_wave());
   if (t.kind == kTaskNone) return;
   const int lane = lane_id();
@@ -265,16 +268,16 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a
   if (t.kind == kTaskEmpty) {
     for (int r = 0; r < t.n_empty; ++r) {
       const int64_t i = uniform(a.plan.rows[t.empty0 + r]);
-      if (g == 0) stv(a.dq + i * HD + 8 * c, u32x4{0u, 0u, 0u, 0u});
+      if (g == 0) stv(a.dq + i * a.ld + 8 * c, u32x4{0u, 0u, 0u, 0u});
     }
     return;
   }
   const int64_t row = t.row;
   float qf[8], df[8];
-  unpack8(ldv(a.q + row * HD + 8 * c), qf);
-  unpack8(ldv(a.dout + row * HD + 8 * c), df);
-  const float lse = a.ml[(row * H + hd) * 2];
-  const float delta = a.ml[(row * H + hd) * 2 + 1];
+  unpack8(ldv(a.q + row * a.ld + 8 * c), qf);
+  unpack8(ldv(a.dout + row * a.ld + 8 * c), df);
+  const float lse = a.ml[row * a.mld + hd * 2];
+  const float delta = a.ml[row * a.mld + hd * 2 + 1];
   float dq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
     const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
@@ -286,9 +289,9 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
-        kk[u] = ldv(a.k + static_cast<int64_t>(j) * HD + 8 * c);
-        vv[u] = ldv(a.v + static_cast<int64_t>(j) * HD + 8 * c);
-        bb[u] = (a.bias && slot < n) ? a.bias[(base + slot) * H + hd] : 0.f;
+        kk[u] = ldv(a.k + static_cast<int64_t>(j) * a.ld + 8 * c);
+        vv[u] = ldv(a.v + static_cast<int64_t>(j) * a.ld + 8 * c);
+        bb[u] = (a.bias && slot < n) ? a.bias[(base + slot) * a.bld + hd] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -298,7 +301,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a
         const float alpha = valid ? fast_exp(s - lse) : 0.f;
         const float dalpha = group_sum<HL>(dot8(df, vv[u]));
         const float ds = alpha * (dalpha - delta);
-        if (a.dbias && valid && head_lead) a.dbias[(base + slot) * H + hd] = ds;
+        if (a.dbias && valid && head_lead) a.dbias[(base + slot) * a.bld + hd] = ds;
         float kf[8];
         unpack8(kk[u], kf);
 #pragma unroll
@@ -314,12 +317,13 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a
   }
 #pragma unroll
   for (int q = 0; q < 8; ++q) dq[q] *= a.scale;
-  stv(a.dq + row * HD + 8 * c, pack8(dq));
+  stv(a.dq + row * a.ld + 8 * c, pack8(dq));
 }
 
 template <int G>
 __global__ __launch_bounds__(kTaskBlock) void dot_dq_merge_kernel(
-    PlanView plan, const float* __restrict__ partial, float scale, uint16_t* __restrict__ dq) {
+    PlanView plan, const float* __restrict__ partial, float scale, uint16_t* __restrict__ dq,
+    int64_t ld) {
   constexpr int HD = 8 * G;
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_dq_merge_kernel(
   }
 #pragma unroll
   for (int r = 0; r < 8; ++r) s[r] *= scale;
-  stv(dq + row * HD + 8 * c, pack8(s));
+  stv(dq + row * ld + 8 * c, pack8(s));
 }
 
 struct DotSrcArgs {
@@ -354,13 +358,15 @@ struct DotSrcArgs {
   uint16_t* dk;
   uint16_t* dv;
   float* partial;   // per chunk: [8G] unscaled dk | [8G] dv
+  int64_t ld;       // values between consecutive nodes' rows of q, k, v, dout, dk, dv
+  int64_t mld;      // floats between consecutive nodes' rows of ml
+  int64_t bld;      // floats between consecutive edges' rows of bias
 };
 
 template <int G, int HL, int U>
 __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
   constexpr int EPW = kWave / G;
   constexpr int HD = 8 * G;
-  constexpr int H = G / HL;
   const Task t = decode_task(a.plan, a.row_ptr_t, global_wave());
   if (t.kind == kTaskNone) return;
   const int lane = lane_id();
@@ -371,16 +377,16 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
     for (int r = 0; r < t.n_empty; ++r) {
       const int64_t j = uniform(a.plan.rows[t.empty0 + r]);
       if (g == 0) {
-        stv(a.dk + j * HD + 8 * c, u32x4{0u, 0u, 0u, 0u});
-        stv(a.dv + j * HD + 8 * c, u32x4{0u, 0u, 0u, 0u});
+        stv(a.dk + j * a.ld + 8 * c, u32x4{0u, 0u, 0u, 0u});
+        stv(a.dv + j * a.ld + 8 * c, u32x4{0u, 0u, 0u, 0u});
       }
     }
     return;
   }
   const int64_t j = t.row;
   float kf[8], vf[8];
-  unpack8(ldv(a.k + j * HD + 8 * c), kf);
-  unpack8(ldv(a.v + j * HD + 8 * c), vf);
+  unpack8(ldv(a.k + j * a.ld + 8 * c), kf);
+  unpack8(ldv(a.v + j * a.ld + 8 * c), vf);
   float dk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float dv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
@@ -399,11 +405,11 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
         const int src = slot < n ? slot : 0;
         const int64_t i = fetch_lane<EPW>(my_i, src);
         const int64_t e = fetch_lane<EPW>(my_e, src);
-        qq[u] = ldv(a.q + i * HD + 8 * c);
-        dd[u] = ldv(a.dout + i * HD + 8 * c);
-        lse[u] = a.ml[(i * H + hd) * 2];
-        dl[u] = a.ml[(i * H + hd) * 2 + 1];
-        bb[u] = a.bias ? a.bias[e * H + hd] : 0.f;
+        qq[u] = ldv(a.q + i * a.ld + 8 * c);
+        dd[u] = ldv(a.dout + i * a.ld + 8 * c);
+        lse[u] = a.ml[i * a.mld + hd * 2];
+        dl[u] = a.ml[i * a.mld + hd * 2 + 1];
+        bb[u] = a.bias ? a.bias[e * a.bld + hd] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -440,14 +446,14 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
   }
 #pragma unroll
   for (int q = 0; q < 8; ++q) dk[q] *= a.scale;
-  stv(a.dk + j * HD + 8 * c, pack8(dk));
-  stv(a.dv + j * HD + 8 * c, pack8(dv));
+  stv(a.dk + j * a.ld + 8 * c, pack8(dk));
+  stv(a.dv + j * a.ld + 8 * c, pack8(dv));
 }
 
 template <int G>
 __global__ __launch_bounds__(kTaskBlock) void dot_kv_merge_kernel(
     PlanView plan, const float* __restrict__ partial, float scale, uint16_t* __restrict__ dk,
-    uint16_t* __restrict__ dv) {
+    uint16_t* __restrict__ dv, int64_t ld) {
   constexpr int HD = 8 * G;
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
@@ -469,8 +475,8 @@ __global__ __launch_bounds__(kTaskBlock) void dot_kv_merge_kernel(
   }
 #pragma unroll
   for (int r = 0; r < 8; ++r) sk[r] *= scale;
-  stv(dk + row * HD + 8 * c, pack8(sk));
-  stv(dv + row * HD + 8 * c, pack8(sv));
+  stv(dk + row * ld + 8 * c, pack8(sk));
+  stv(dv + row * ld + 8 * c, pack8(sv));
 }
 
 // ---------------------------------------------------------------------------
@@ -480,19 +486,37 @@ struct DotShape {
   int G, HL;
 };
 
-bool dot_shape(int H, int D, DotShape* s) {
-  if (H <= 0 || D <= 0 || D % 8 != 0) return false;
-  const int HD = H * D;
-  if (HD != 128 && HD != 256 && HD != 512) return false;
-  s->G = HD / 8;
-  s->HL = D / 8;
-  return s->HL >= 1 && s->HL <= 16 && s->G % s->HL == 0;
+// Heads run in groups whose row slice fits one wave at 8 bf16 per lane: a
+// group of Hg heads (a power of two) with Hg * D <= 512 values.  Any H splits
+// greedily into such groups (H = 6, D = 128 -> 4 + 2); each group launches
+// the kernels over its strided slice of q, k, v, out, dout, dq, dk, dv, ml,
+// bias and dbias.
+constexpr int kDotGroupValues = 512;
+
+bool dot_heads_ok(int H, int D) {
+  if (H < 1 || D <= 0 || D % 8 != 0 || D > kDotGroupValues) return false;
+  const int hl = D / 8;
+  return (hl & (hl - 1)) == 0;
 }
 
-#define TGX_DOT_SHAPES(X) \
-  X(64, 16) X(64, 8) X(64, 4) X(64, 2) X(64, 1) \
-  X(32, 16) X(32, 8) X(32, 4) X(32, 2) X(32, 1) \
-  X(16, 16) X(16, 8) X(16, 4) X(16, 2) X(16, 1)
+// Heads in the group starting at head h0.
+int dot_group_heads(int H, int D, int h0) {
+  int hg = kDotGroupValues / D;
+  while (hg > H - h0) hg >>= 1;
+  return hg;
+}
+
+DotShape dot_shape(int Hg, int D) { return DotShape{Hg * D / 8, D / 8}; }
+
+// Every (G, HL) a group can take: G = Hg * HL lanes, HL = D / 8 lanes per head.
+#define TGX_DOT_SHAPES(X)                                                        \
+  X(64, 64) X(64, 32) X(64, 16) X(64, 8) X(64, 4) X(64, 2) X(64, 1)            \
+  X(32, 32) X(32, 16) X(32, 8) X(32, 4) X(32, 2) X(32, 1)                       \
+  X(16, 16) X(16, 8) X(16, 4) X(16, 2) X(16, 1)                                 \
+  X(8, 8) X(8, 4) X(8, 2) X(8, 1)                                               \
+  X(4, 4) X(4, 2) X(4, 1)                                                       \
+  X(2, 2) X(2, 1)                                                               \
+  X(1, 1)
 
 // Loads in flight per lane group (each covers a k and a v row, or a q and a
 // dout row).  For H*D = 256 (32 lanes per row, two edges per wave-load) 1
@@ -516,7 +540,7 @@ int dot_fwd_launch(const DotFwdArgs<I>& a, hipStream_t s) {
   if (a.plan.n_split > 0) {
     TGX_PROFILE("dot_fwd_merge_kernel", s);
     dot_fwd_merge_kernel<G, HL><<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        a.plan, a.partial, a.out, a.ml);
+        a.plan, a.partial, a.out, a.ml, a.ld, a.mld);
     TGX_LAUNCHED("dot_fwd_merge_kernel");
   }
   return TGX_OK;
@@ -544,7 +568,7 @@ int dot_bwd_launch(const DotDstArgs<I>& da, DotSrcArgs sa, const uint16_t* out,
   {
     TGX_PROFILE("dot_delta_kernel", s);
     dot_delta_kernel<G, HL><<<ceil_div(ceil_div(n_nodes, EPW), kWavesPerBlock), kTaskBlock, 0,
-                              s>>>(da.dout, out, ml, n_nodes);
+                              s>>>(da.dout, out, ml, n_nodes, da.ld, da.mld);
     TGX_LAUNCHED("dot_delta_kernel");
   }
   const int64_t dst_waves = plan_waves(da.plan);
@@ -556,7 +580,7 @@ int dot_bwd_launch(const DotDstArgs<I>& da, DotSrcArgs sa, const uint16_t* out,
   if (da.plan.n_split > 0) {
     TGX_PROFILE("dot_dq_merge_kernel", s);
     dot_dq_merge_kernel<G><<<ceil_div(da.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        da.plan, da.partial, da.scale, da.dq);
+        da.plan, da.partial, da.scale, da.dq, da.ld);
     TGX_LAUNCHED("dot_dq_merge_kernel");
   }
   const int64_t src_waves = plan_waves(sa.plan);
@@ -568,7 +592,7 @@ int dot_bwd_launch(const DotDstArgs<I>& da, DotSrcArgs sa, const uint16_t* out,
   if (sa.plan.n_split > 0) {
     TGX_PROFILE("dot_kv_merge_kernel", s);
     dot_kv_merge_kernel<G><<<ceil_div(sa.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        sa.plan, sa.partial, sa.scale, sa.dk, sa.dv);
+        sa.plan, sa.partial, sa.scale, sa.dk, sa.dv, sa.ld);
     TGX_LAUNCHED("dot_kv_merge_kernel");
   }
   return TGX_OK;
@@ -585,10 +609,9 @@ extern "C" int tgx_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bi
                                 float* ml, int64_t n_dst, int64_t n_src, int H, int D,
                                 float* partial, void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
-  DotShape shp;
-  if (!dot_shape(H, D, &shp)) {
-    set_error("dot attention supports D %% 8 == 0 and H*D in {128,256,512} (got H=%d D=%d)",
-              H, D);
+  if (!dot_heads_ok(H, D)) {
+    set_error("dot attention supports H >= 1 and D in {8, 16, 32, 64, 128, 256, 512} "
+              "(got H=%d D=%d)", H, D);
     return TGX_UNSUPPORTED;
   }
   int st = check_plan(plan, n_dst);
@@ -597,39 +620,52 @@ extern "C" int tgx_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bi
   TGX_REQUIRE(row_ptr && q && out && ml && ((k && v) || n_src == 0), "null pointer");
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
   hipStream_t s = as_stream(stream);
-  const auto* qq = static_cast<const uint16_t*>(q);
-  const auto* kk = static_cast<const uint16_t*>(k);
-  const auto* vv = static_cast<const uint16_t*>(v);
-  auto* oo = static_cast<uint16_t*>(out);
-#define TGX_DOT_FWD(GG, HH)                                                                 \
-  if (shp.G == GG && shp.HL == HH) {                                                        \
-    if (idx_bits == 32)                                                                     \
-      return dot_fwd_launch<int32_t, GG, HH>(                                               \
-          DotFwdArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                         \
-                              static_cast<const int32_t*>(col), plan_view(*plan), qq, kk,   \
-                              vv, bias, scale, oo, ml, partial},                            \
-          s);                                                                               \
-    return dot_fwd_launch<int64_t, GG, HH>(                                                 \
-        DotFwdArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                           \
-                            static_cast<const int64_t*>(col), plan_view(*plan), qq, kk, vv, \
-                            bias, scale, oo, ml, partial},                                  \
-        s);                                                                                 \
-  }
-  TGX_DOT_SHAPES(TGX_DOT_FWD)
+  const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
+  for (int h0 = 0; h0 < H;) {
+    const int hg = dot_group_heads(H, D, h0);
+    const DotShape shp = dot_shape(hg, D);
+    const int64_t off = static_cast<int64_t>(h0) * D;
+    const auto* qq = static_cast<const uint16_t*>(q) + off;
+    const auto* kk = k ? static_cast<const uint16_t*>(k) + off : nullptr;
+    const auto* vv = v ? static_cast<const uint16_t*>(v) + off : nullptr;
+    auto* oo = static_cast<uint16_t*>(out) + off;
+    const float* bb = bias ? bias + h0 : nullptr;
+    float* mm = ml + 2 * h0;
+    st = TGX_UNSUPPORTED;
+#define TGX_DOT_FWD(GG, HH)                                                                  \
+    if (shp.G == GG && shp.HL == HH) {                                                       \
+      if (idx_bits == 32)                                                                    \
+        st = dot_fwd_launch<int32_t, GG, HH>(                                                \
+            DotFwdArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                        \
+                                static_cast<const int32_t*>(col), plan_view(*plan), qq, kk,  \
+                                vv, bb, scale, oo, mm, partial, ld, mld, bld},               \
+            s);                                                                              \
+      else                                                                                   \
+        st = dot_fwd_launch<int64_t, GG, HH>(                                                \
+            DotFwdArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                        \
+                                static_cast<const int64_t*>(col), plan_view(*plan), qq, kk,  \
+                                vv, bb, scale, oo, mm, partial, ld, mld, bld},               \
+            s);                                                                              \
+    } else
+    TGX_DOT_SHAPES(TGX_DOT_FWD)
+    set_error("unsupported dot attention head group G=%d HL=%d", shp.G, shp.HL);
 #undef TGX_DOT_FWD
-  set_error("unsupported dot attention shape");
-  return TGX_UNSUPPORTED;
+    if (st != TGX_OK) return st;
+    h0 += hg;
+  }
+  return TGX_OK;
 }
 
 extern "C" int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
                                           int H, int D, size_t* bytes) {
   TGX_REQUIRE(plan && plan_t && bytes, "null pointer");
-  DotShape shp;
-  if (!dot_shape(H, D, &shp)) {
+  if (!dot_heads_ok(H, D)) {
     set_error("unsupported dot attention shape H=%d D=%d", H, D);
     return TGX_UNSUPPORTED;
   }
-  *bytes = dot_bwd_layout(*plan, *plan_t, H, D).bytes;
+  // Head groups run one after another on one stream and share the
+  // workspace; the first group is the widest.
+  *bytes = dot_bwd_layout(*plan, *plan_t, dot_group_heads(H, D, 0), D).bytes;
   return TGX_OK;
 }
 
@@ -642,8 +678,7 @@ extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bi
                                 float* dbias, int64_t n_dst, int64_t n_src, int H, int D,
                                 void* ws, size_t ws_bytes, void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
-  DotShape shp;
-  if (!dot_shape(H, D, &shp)) {
+  if (!dot_heads_ok(H, D)) {
     set_error("unsupported dot attention shape H=%d D=%d", H, D);
     return TGX_UNSUPPORTED;
   }
@@ -654,39 +689,54 @@ extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bi
   TGX_REQUIRE(row_ptr && row_ptr_t && q && out && ml && dout && dq &&
                   ((k && v && dk && dv) || n_src == 0),
               "null pointer");
-  const DotBwdLayout L = dot_bwd_layout(*plan, *plan_t, H, D);
+  const DotBwdLayout L = dot_bwd_layout(*plan, *plan_t, dot_group_heads(H, D, 0), D);
   TGX_REQUIRE(ws && ws_bytes >= L.bytes, "workspace too small: need %zu bytes", L.bytes);
   hipStream_t s = as_stream(stream);
   char* w = static_cast<char*>(ws);
   float* dst_part = reinterpret_cast<float*>(w + L.dst_part_off);
   float* src_part = reinterpret_cast<float*>(w + L.src_part_off);
-  const auto* qq = static_cast<const uint16_t*>(q);
-  const auto* kk = static_cast<const uint16_t*>(k);
-  const auto* vv = static_cast<const uint16_t*>(v);
-  const auto* oo = static_cast<const uint16_t*>(out);
-  const auto* gg = static_cast<const uint16_t*>(dout);
-  DotSrcArgs sa{row_ptr_t, col_t, perm, plan_view(*plan_t), qq, kk, vv, bias, scale, ml, gg,
-                static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv), src_part};
-#define TGX_DOT_BWD(GG, HH)                                                                  \
-  if (shp.G == GG && shp.HL == HH) {                                                         \
-    if (idx_bits == 32)                                                                      \
-      return dot_bwd_launch<int32_t, GG, HH>(                                                \
-          DotDstArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                          \
-                              static_cast<const int32_t*>(col), plan_view(*plan), qq, kk,    \
-                              vv, bias, scale, ml, gg, static_cast<uint16_t*>(dq), dbias,    \
-                              dst_part},                                                     \
-          sa, oo, ml, n_dst, s);                                                             \
-    return dot_bwd_launch<int64_t, GG, HH>(                                                  \
-        DotDstArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                            \
-                            static_cast<const int64_t*>(col), plan_view(*plan), qq, kk, vv,  \
-                            bias, scale, ml, gg, static_cast<uint16_t*>(dq), dbias,          \
-                            dst_part},                                                       \
-        sa, oo, ml, n_dst, s);                                                               \
-  }
-  TGX_DOT_SHAPES(TGX_DOT_BWD)
+  const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
+  auto at = [](const void* p, int64_t off) {
+    return p ? static_cast<const uint16_t*>(p) + off : nullptr;
+  };
+  auto at_mut = [](void* p, int64_t off) {
+    return p ? static_cast<uint16_t*>(p) + off : nullptr;
+  };
+  for (int h0 = 0; h0 < H;) {
+    const int hg = dot_group_heads(H, D, h0);
+    const DotShape shp = dot_shape(hg, D);
+    const int64_t off = static_cast<int64_t>(h0) * D;
+    const uint16_t *qq = at(q, off), *kk = at(k, off), *vv = at(v, off), *oo = at(out, off),
+                   *gg = at(dout, off);
+    uint16_t *dqq = at_mut(dq, off), *dkk = at_mut(dk, off), *dvv = at_mut(dv, off);
+    const float* bb = bias ? bias + h0 : nullptr;
+    float* dbb = dbias ? dbias + h0 : nullptr;
+    float* mm = ml + 2 * h0;
+    DotSrcArgs sa{row_ptr_t, col_t, perm, plan_view(*plan_t), qq, kk, vv, bb, scale, mm, gg,
+                  dkk, dvv, src_part, ld, mld, bld};
+    st = TGX_UNSUPPORTED;
+#define TGX_DOT_BWD(GG, HH)                                                                   \
+    if (shp.G == GG && shp.HL == HH) {                                                        \
+      if (idx_bits == 32)                                                                     \
+        st = dot_bwd_launch<int32_t, GG, HH>(                                                 \
+            DotDstArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                         \
+                                static_cast<const int32_t*>(col), plan_view(*plan), qq, kk,   \
+                                vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld, bld},     \
+            sa, oo, mm, n_dst, s);                                                            \
+      else                                                                                    \
+        st = dot_bwd_launch<int64_t, GG, HH>(                                                 \
+            DotDstArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                         \
+                                static_cast<const int64_t*>(col), plan_view(*plan), qq, kk,   \
+                                vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld, bld},     \
+            sa, oo, mm, n_dst, s);                                                            \
+    } else
+    TGX_DOT_SHAPES(TGX_DOT_BWD)
+    set_error("unsupported dot attention head group G=%d HL=%d", shp.G, shp.HL);
 #undef TGX_DOT_BWD
-  set_error("unsupported dot attention shape");
-  return TGX_UNSUPPORTED;
+    if (st != TGX_OK) return st;
+    h0 += hg;
+  }
+  return TGX_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -735,10 +785,9 @@ extern "C" int tgx_dot_attn_fwd_noalloc(const void* row_ptr, const void* col, in
                                         int64_t n_src, int H, int D, void* stream) {
   // Every size check comes before any HIP call.
   TGX_REQUIRE(plan != nullptr, "null plan");
-  DotShape shp;
-  if (!dot_shape(H, D, &shp)) {
-    set_error("dot attention supports D %% 8 == 0 and H*D in {128,256,512} (got H=%d D=%d)",
-              H, D);
+  if (!dot_heads_ok(H, D)) {
+    set_error("dot attention supports H >= 1 and D in {8, 16, 32, 64, 128, 256, 512} "
+              "(got H=%d D=%d)", H, D);
     return TGX_UNSUPPORTED;
   }
   TGX_REQUIRE(plan->n_chunks >= 0, "inconsistent plan");

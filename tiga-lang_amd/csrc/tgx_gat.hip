@@ -64,6 +64,8 @@ struct GatFwdArgs {
   float* out;
   float* ns;
   float* partial;  // per chunk: acc[4G] | m[H] | l[H]
+  int64_t ld;      // floats between consecutive nodes' rows of h and out
+  int64_t nsld;    // floats between consecutive nodes' rows of ns
 };
 
 // Index of lane `src` in a wave, read by every lane (edge groups differ).
@@ -91,19 +93,19 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
   if (t.kind == kTaskEmpty) {
     for (int k = 0; k < t.n_empty; ++k) {
       const int64_t i = uniform(a.plan.rows[t.empty0 + k]);
-      const f32x4 hi = ld4(a.h + i * HD + 4 * c);
+      const f32x4 hi = ld4(a.h + i * a.ld + 4 * c);
       const float sdst = group_sum<HL>(dot4(ad4, hi));
       const float ssrc = group_sum<HL>(dot4(as4, hi));
       if (g == 0) {
-        st4(a.out + i * HD + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
-        if (head_lead) st4(a.ns + (i * H + hd) * 4, f32x4{kNegInf, 0.f, sdst, ssrc});
+        st4(a.out + i * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+        if (head_lead) st4(a.ns + i * a.nsld + hd * 4, f32x4{kNegInf, 0.f, sdst, ssrc});
       }
     }
     return;
   }
 
   const int64_t row = t.row;
-  const f32x4 hi = ld4(a.h + row * HD + 4 * c);
+  const f32x4 hi = ld4(a.h + row * a.ld + 4 * c);
   const float sdst = group_sum<HL>(dot4(ad4, hi));
 
   SoftState<4> st;
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
-        x[u] = ld4(a.h + static_cast<int64_t>(j) * HD + 4 * c);
+        x[u] = ld4(a.h + static_cast<int64_t>(j) * a.ld + 4 * c);
       }
       float s[U];
       float mc = kNegInf;
@@ -151,17 +153,17 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
     return;
   }
   const float inv = 1.f / st.l;
-  st4(a.out + row * HD + 4 * c,
+  st4(a.out + row * a.ld + 4 * c,
       f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
   const float ssrc_i = group_sum<HL>(dot4(as4, hi));
-  if (head_lead) st4(a.ns + (row * H + hd) * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc_i});
+  if (head_lead) st4(a.ns + row * a.nsld + hd * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc_i});
 }
 
 template <int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
     PlanView plan, const float* __restrict__ partial, const float* __restrict__ h,
     const float* __restrict__ a_src, const float* __restrict__ a_dst,
-    float* __restrict__ out, float* __restrict__ ns) {
+    float* __restrict__ out, float* __restrict__ ns, int64_t ld, int64_t nsld) {
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
   const int64_t k = global_wave();
@@ -180,12 +182,12 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
     st.merge(p[HD + hd], p[HD + H + hd], accs);
   }
   const float inv = 1.f / st.l;
-  st4(out + row * HD + 4 * c,
+  st4(out + row * ld + 4 * c,
       f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
-  const f32x4 hi = ld4(h + row * HD + 4 * c);
+  const f32x4 hi = ld4(h + row * ld + 4 * c);
   const float sdst = group_sum<HL>(dot4(ld4(a_dst + 4 * c), hi));
   const float ssrc = group_sum<HL>(dot4(ld4(a_src + 4 * c), hi));
-  if (c % HL == 0) st4(ns + (row * H + hd) * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc});
+  if (c % HL == 0) st4(ns + row * nsld + hd * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc});
 }
 
 // ---------------------------------------------------------------------------
@@ -194,16 +196,14 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
 template <int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_delta_kernel(
     const float* __restrict__ dout, const float* __restrict__ out, float* __restrict__ ns,
-    int64_t n_nodes) {
+    int64_t n_nodes, int64_t ld, int64_t nsld) {
   constexpr int EPW = kWave / G;
-  constexpr int HD = 4 * G;
-  constexpr int H = G / HL;
   const int lane = lane_id();
   const int c = lane % G, hd = c / HL;
   const int64_t node = global_wave() * EPW + lane / G;
   if (node >= n_nodes) return;
-  const float d = group_sum<HL>(dot4(ld4(dout + node * HD + 4 * c), ld4(out + node * HD + 4 * c)));
-  if (c % HL == 0) ns[(node * H + hd) * 4 + 1] = d;
+  const float d = group_sum<HL>(dot4(ld4(dout + node * ld + 4 * c), ld4(out + node * ld + 4 * c)));
+  if (c % HL == 0) ns[node * nsld + hd * 4 + 1] = d;
 }
 
 struct GatSrcArgs {
@@ -220,6 +220,8 @@ struct GatSrcArgs {
   float* partial;   // per chunk: [4G] dh contribution | [H] sum of dz
   float* dz;        // [E, H] in transposed edge order (coalesced)
   float* sdz_src;   // [N, H] sum of dz over each source's out-edges
+  int64_t ld;       // floats between consecutive nodes' rows of h, dout, dh
+  int64_t nsld;     // floats between consecutive nodes' rows of ns
 };
 
 // One wave per task of the transposed-CSR plan (source rows).
@@ -239,7 +241,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
     for (int k = 0; k < t.n_empty; ++k) {
       const int64_t j = uniform(a.plan.rows[t.empty0 + k]);
       if (g == 0) {
-        st4(a.dh + j * HD + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+        st4(a.dh + j * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
         if (head_lead) a.sdz_src[j * H + hd] = 0.f;
       }
     }
@@ -247,8 +249,8 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
   }
   const f32x4 as4 = ld4(a.a_src + 4 * c);
   const int64_t j = t.row;
-  const f32x4 hj = ld4(a.h + j * HD + 4 * c);
-  const float ssrc = a.ns[(j * H + hd) * 4 + 3];
+  const f32x4 hj = ld4(a.h + j * a.ld + 4 * c);
+  const float ssrc = a.ns[j * a.nsld + hd * 4 + 3];
   f32x4 dha = {0.f, 0.f, 0.f, 0.f};
   float sdz = 0.f;
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
@@ -261,8 +263,8 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const int64_t i = fetch_lane<EPW>(my_i, slot < n ? slot : 0);
-        d[u] = ld4(a.dout + i * HD + 4 * c);
-        nst[u] = ld3(a.ns + (i * H + hd) * 4);
+        d[u] = ld4(a.dout + i * a.ld + 4 * c);
+        nst[u] = ld3(a.ns + i * a.nsld + hd * 4);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -295,7 +297,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
     st4(p + 4 * c, contrib);
     if (head_lead) p[HD + hd] = sdz;
   } else {
-    st4(a.dh + j * HD + 4 * c, contrib);
+    st4(a.dh + j * a.ld + 4 * c, contrib);
     if (head_lead) a.sdz_src[j * H + hd] = sdz;
   }
 }
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
 template <int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
     PlanView plan, const float* __restrict__ partial, float* __restrict__ dh,
-    float* __restrict__ sdz_src) {
+    float* __restrict__ sdz_src, int64_t ld) {
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
   const int64_t k = global_wave();
@@ -320,7 +322,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
     s += ld4(p + 4 * c);
     z += p[HD + hd];
   }
-  st4(dh + row * HD + 4 * c, s);
+  st4(dh + row * ld + 4 * c, s);
   if (c % HL == 0) sdz_src[row * H + hd] = z;
 }
 
@@ -338,6 +340,7 @@ struct GatDstArgs {
   double* dap_src;       // [waves, 4G]
   double* dap_dst;       // [waves, 4G]
   int64_t n_tasks;
+  int64_t ld;            // floats between consecutive nodes' rows of h and dh
 };
 
 __device__ __forceinline__ void acc_f64(f64x4& acc, float scale, f32x4 v) {
@@ -369,7 +372,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a
     if (t.kind == kTaskEmpty) {
       for (int k = 0; k < t.n_empty; ++k) {
         const int64_t i = uniform(a.plan.rows[t.empty0 + k]);
-        if (g == 0) acc_f64(ds, a.sdz_src[i * H + hd], ld4(a.h + i * HD + 4 * c));
+        if (g == 0) acc_f64(ds, a.sdz_src[i * H + hd], ld4(a.h + i * a.ld + 4 * c));
       }
       continue;
     }
@@ -401,12 +404,12 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a
     if (t.kind == kTaskChunk && lane < H)
       a.partial[static_cast<int64_t>(t.slot) * H + lane] = s;
     if (g == 0) {
-      const f32x4 hi = ld4(a.h + i * HD + 4 * c);
+      const f32x4 hi = ld4(a.h + i * a.ld + 4 * c);
       acc_f64(dd, sdz, hi);
       const bool first = t.kind == kTaskRow || t.e0 == static_cast<int64_t>(a.row_ptr[i]);
       if (first) acc_f64(ds, a.sdz_src[i * H + hd], hi);
       if (t.kind == kTaskRow) {
-        float* q = a.dh + i * HD + 4 * c;
+        float* q = a.dh + i * a.ld + 4 * c;
         st4(q, ld4(q) + sdz * ad4);
       }
     }
@@ -422,8 +425,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a
 template <int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_merge_kernel(
     PlanView plan, const float* __restrict__ partial, const float* __restrict__ a_dst,
-    float* __restrict__ dh) {
-  constexpr int HD = 4 * G;
+    float* __restrict__ dh, int64_t ld) {
   constexpr int H = G / HL;
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
@@ -434,7 +436,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_merge_kernel(
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
   float s = 0.f;
   for (int q = c0; q < c1; ++q) s += partial[static_cast<int64_t>(q) * H + hd];
-  float* p = dh + row * HD + 4 * c;
+  float* p = dh + row * ld + 4 * c;
   st4(p, ld4(p) + s * ld4(a_dst + 4 * c));
 }
 
@@ -487,14 +489,29 @@ struct GatShape {
   int G, HL;
 };
 
-bool gat_shape(int H, int D, GatShape* s) {
-  if (H <= 0 || D <= 0 || D % 4 != 0) return false;
-  const int HD = H * D;
-  if (HD != 64 && HD != 128 && HD != 256) return false;
-  s->G = HD / 4;
-  s->HL = D / 4;
-  return s->HL >= 1 && s->HL <= 16 && s->G % s->HL == 0;
+// Heads run in groups whose row slice fits one lane group at a float4 per
+// lane: a group of Hg heads (a power of two) with Hg * D <= 256 floats.  Any
+// H splits greedily into such groups (H = 3 -> 2 + 1); each group launches
+// the kernels over its strided slice of h, out, dout, dh and the node state,
+// and its own contiguous slice of a_src, a_dst, da_src and da_dst.
+constexpr int kGatGroupFloats = 256;
+
+bool gat_head_dim_ok(int D) {
+  if (D <= 0 || D % 4 != 0 || D > kGatGroupFloats) return false;
+  const int hl = D / 4;
+  return (hl & (hl - 1)) == 0;
 }
+
+bool gat_heads_ok(int H, int D) { return H >= 1 && gat_head_dim_ok(D); }
+
+// Heads in the group starting at head h0.
+int gat_group_heads(int H, int D, int h0) {
+  int hg = kGatGroupFloats / D;
+  while (hg > H - h0) hg >>= 1;
+  return hg;
+}
+
+GatShape gat_shape(int Hg, int D) { return GatShape{Hg * D / 4, D / 4}; }
 
 // Persistent grid: enough workgroups for the tasks, at most what stays
 // resident at once, at most kPersistBlocks (the partial buffers' capacity).
@@ -505,10 +522,15 @@ int64_t persist_blocks(int64_t tasks, int64_t resident) {
   return b > 0 ? b : 1;
 }
 
-#define TGX_GAT_SHAPES(X) \
-  X(64, 16) X(64, 8) X(64, 4) X(64, 2) X(64, 1) \
-  X(32, 16) X(32, 8) X(32, 4) X(32, 2) X(32, 1) \
-  X(16, 16) X(16, 8) X(16, 4) X(16, 2) X(16, 1)
+// Every (G, HL) a group can take: G = Hg * HL lanes, HL = D / 4 lanes per head.
+#define TGX_GAT_SHAPES(X)                                                        \
+  X(64, 64) X(64, 32) X(64, 16) X(64, 8) X(64, 4) X(64, 2) X(64, 1)            \
+  X(32, 32) X(32, 16) X(32, 8) X(32, 4) X(32, 2) X(32, 1)                       \
+  X(16, 16) X(16, 8) X(16, 4) X(16, 2) X(16, 1)                                 \
+  X(8, 8) X(8, 4) X(8, 2) X(8, 1)                                               \
+  X(4, 4) X(4, 2) X(4, 1)                                                       \
+  X(2, 2) X(2, 1)                                                               \
+  X(1, 1)
 
 template <typename I, int G, int HL>
 int gat_fwd_launch(const GatFwdArgs<I>& a, hipStream_t s) {
@@ -525,7 +547,7 @@ int gat_fwd_launch(const GatFwdArgs<I>& a, hipStream_t s) {
   if (a.plan.n_split > 0) {
     TGX_PROFILE("gat_fwd_merge_kernel", s);
     gat_fwd_merge_kernel<G, HL><<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        a.plan, a.partial, a.h, a.a_src, a.a_dst, a.out, a.ns);
+        a.plan, a.partial, a.h, a.a_src, a.a_dst, a.out, a.ns, a.ld, a.nsld);
     TGX_LAUNCHED("gat_fwd_merge_kernel");
   }
   return TGX_OK;
@@ -563,8 +585,8 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
                    const tgx_row_plan& plan_t,
                    const float* h, const float* a_src, const float* a_dst, float slope,
                    const float* out, float* ns, const float* dout, float* dh, float* da_src,
-                   float* da_dst, int64_t n_nodes, int64_t n_edges, char* ws,
-                   const GatBwdLayout& L, hipStream_t s) {
+                   float* da_dst, int64_t n_nodes, int64_t n_edges, int64_t ld,
+                   int64_t nsld, char* ws, const GatBwdLayout& L, hipStream_t s) {
   constexpr int EPW = kWave / G;
   // The source pass holds dout rows plus node state per edge: 4 in flight
   // per wave measured best (2: +4%, 3: +2%, 6: +5%, 8: +6% time).
@@ -582,14 +604,14 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
   {
   TGX_PROFILE("gat_delta_kernel", s);
   gat_delta_kernel<G, HL><<<ceil_div(ceil_div(n_nodes, EPW), kWavesPerBlock), kTaskBlock, 0, s>>>(
-      dout, out, ns, n_nodes);
+      dout, out, ns, n_nodes, ld, nsld);
   TGX_LAUNCHED("gat_delta_kernel");
   }
 
   GatSrcArgs sa{row_ptr_t, col_t, perm, pt, h, a_src, slope, ns, dout, dh, src_part, dz,
-                sdz_src};
+                sdz_src, ld, nsld};
   GatDstArgs<I> da{row_ptr, pv, h, a_dst, dz, inv_perm, sdz_src, dh, dst_part, dap_src,
-                   dap_dst, plan_waves(pv)};
+                   dap_dst, plan_waves(pv), ld};
   const int64_t dst_blocks =
       persist_blocks(plan_waves(pv), resident_blocks(gat_bwd_dst_kernel<I, G, HL>, kTaskBlock));
   {
@@ -601,7 +623,7 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
   if (pt.n_split > 0) {
     TGX_PROFILE("gat_bwd_src_merge_kernel", s);
     gat_bwd_src_merge_kernel<G, HL><<<ceil_div(pt.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        pt, src_part, dh, sdz_src);
+        pt, src_part, dh, sdz_src, ld);
     TGX_LAUNCHED("gat_bwd_src_merge_kernel");
   }
   {
@@ -612,7 +634,7 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
   if (pv.n_split > 0) {
     TGX_PROFILE("gat_bwd_dst_merge_kernel", s);
     gat_bwd_dst_merge_kernel<G, HL><<<ceil_div(pv.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        pv, dst_part, a_dst, dh);
+        pv, dst_part, a_dst, dh, ld);
     TGX_LAUNCHED("gat_bwd_dst_merge_kernel");
   }
   if (da_src || da_dst) {
@@ -639,9 +661,9 @@ extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
                            const float* a_dst, float slope, float* out, float* ns,
                            int64_t n_nodes, int H, int D, float* partial, void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
-  GatShape shp;
-  if (!gat_shape(H, D, &shp)) {
-    set_error("GAT kernel supports H*D in {64,128,256} with D %% 4 == 0 (got H=%d D=%d)", H, D);
+  if (!gat_heads_ok(H, D)) {
+    set_error("GAT kernel supports H >= 1 and D in {4, 8, 16, 32, 64, 128, 256} "
+              "(got H=%d D=%d)", H, D);
     return TGX_UNSUPPORTED;
   }
   int st = check_plan(plan, n_nodes);
@@ -650,35 +672,48 @@ extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
   TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns, "null pointer");
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
   hipStream_t s = as_stream(stream);
-#define TGX_GAT_FWD(GG, HH)                                                              \
-  if (shp.G == GG && shp.HL == HH) {                                                     \
-    if (idx_bits == 32)                                                                  \
-      return gat_fwd_launch<int32_t, GG, HH>(                                            \
-          GatFwdArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                      \
-                              static_cast<const int32_t*>(col), plan_view(*plan), h,     \
-                              a_src, a_dst, slope, out, ns, partial},                    \
-          s);                                                                            \
-    return gat_fwd_launch<int64_t, GG, HH>(                                              \
-        GatFwdArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                        \
-                            static_cast<const int64_t*>(col), plan_view(*plan), h, a_src, \
-                            a_dst, slope, out, ns, partial},                             \
-        s);                                                                              \
-  }
-  TGX_GAT_SHAPES(TGX_GAT_FWD)
+  const int64_t ld = static_cast<int64_t>(H) * D, nsld = 4 * static_cast<int64_t>(H);
+  for (int h0 = 0; h0 < H;) {
+    const int hg = gat_group_heads(H, D, h0);
+    const GatShape shp = gat_shape(hg, D);
+    const int64_t off = static_cast<int64_t>(h0) * D;
+    st = TGX_UNSUPPORTED;
+#define TGX_GAT_FWD(GG, HH)                                                                  \
+    if (shp.G == GG && shp.HL == HH) {                                                       \
+      if (idx_bits == 32)                                                                    \
+        st = gat_fwd_launch<int32_t, GG, HH>(                                                \
+            GatFwdArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                        \
+                                static_cast<const int32_t*>(col), plan_view(*plan), h + off, \
+                                a_src + off, a_dst + off, slope, out + off, ns + 4 * h0,     \
+                                partial, ld, nsld},                                          \
+            s);                                                                              \
+      else                                                                                   \
+        st = gat_fwd_launch<int64_t, GG, HH>(                                                \
+            GatFwdArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                        \
+                                static_cast<const int64_t*>(col), plan_view(*plan), h + off, \
+                                a_src + off, a_dst + off, slope, out + off, ns + 4 * h0,     \
+                                partial, ld, nsld},                                          \
+            s);                                                                              \
+    } else
+    TGX_GAT_SHAPES(TGX_GAT_FWD)
+    set_error("unsupported GAT head group G=%d HL=%d", shp.G, shp.HL);
 #undef TGX_GAT_FWD
-  set_error("unsupported GAT shape");
-  return TGX_UNSUPPORTED;
+    if (st != TGX_OK) return st;
+    h0 += hg;
+  }
+  return TGX_OK;
 }
 
 extern "C" int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
                                      int64_t n_edges, int H, int D, size_t* bytes) {
   TGX_REQUIRE(plan && plan_t && bytes, "null pointer");
-  GatShape shp;
-  if (!gat_shape(H, D, &shp)) {
+  if (!gat_heads_ok(H, D)) {
     set_error("unsupported GAT shape H=%d D=%d", H, D);
     return TGX_UNSUPPORTED;
   }
-  *bytes = gat_bwd_layout(*plan, *plan_t, n_edges, H, D).bytes;
+  // Head groups run one after another on one stream and share the
+  // workspace; the first group is the widest.
+  *bytes = gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D).bytes;
   return TGX_OK;
 }
 
@@ -692,8 +727,7 @@ extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
                            size_t ws_bytes, void* stream) {
   (void)col;
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
-  GatShape shp;
-  if (!gat_shape(H, D, &shp)) {
+  if (!gat_heads_ok(H, D)) {
     set_error("unsupported GAT shape H=%d D=%d", H, D);
     return TGX_UNSUPPORTED;
   }
@@ -705,26 +739,38 @@ extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
   TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns && dout && dh && da_src && da_dst,
               "null pointer");
   TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && inv_perm), "null transposed CSR");
-  const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, H, D);
-  TGX_REQUIRE(ws && ws_bytes >= L.bytes, "workspace too small: need %zu bytes", L.bytes);
+  const size_t need =
+      gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D).bytes;
+  TGX_REQUIRE(ws && ws_bytes >= need, "workspace too small: need %zu bytes", need);
   hipStream_t s = as_stream(stream);
   char* w = static_cast<char*>(ws);
-#define TGX_GAT_BWD(GG, HH)                                                                \
-  if (shp.G == GG && shp.HL == HH) {                                                       \
-    if (idx_bits == 32)                                                                    \
-      return gat_bwd_launch<int32_t, GG, HH>(static_cast<const int32_t*>(row_ptr), *plan,  \
-                                             row_ptr_t, col_t, perm, inv_perm, *plan_t, h, \
-                                             a_src,                                        \
-                                             a_dst, slope, out, ns, dout, dh, da_src,      \
-                                             da_dst, n_nodes, n_edges, w, L, s);           \
-    return gat_bwd_launch<int64_t, GG, HH>(static_cast<const int64_t*>(row_ptr), *plan,    \
-                                           row_ptr_t, col_t, perm, inv_perm, *plan_t, h,   \
-                                           a_src,                                          \
-                                           a_dst, slope, out, ns, dout, dh, da_src, da_dst, \
-                                           n_nodes, n_edges, w, L, s);                     \
-  }
-  TGX_GAT_SHAPES(TGX_GAT_BWD)
+  const int64_t ld = static_cast<int64_t>(H) * D, nsld = 4 * static_cast<int64_t>(H);
+  for (int h0 = 0; h0 < H;) {
+    const int hg = gat_group_heads(H, D, h0);
+    const GatShape shp = gat_shape(hg, D);
+    const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, hg, D);
+    const int64_t off = static_cast<int64_t>(h0) * D;
+    st = TGX_UNSUPPORTED;
+#define TGX_GAT_BWD(GG, HH)                                                                 \
+    if (shp.G == GG && shp.HL == HH) {                                                      \
+      if (idx_bits == 32)                                                                   \
+        st = gat_bwd_launch<int32_t, GG, HH>(                                               \
+            static_cast<const int32_t*>(row_ptr), *plan, row_ptr_t, col_t, perm, inv_perm,  \
+            *plan_t, h + off, a_src + off, a_dst + off, slope, out + off, ns + 4 * h0,      \
+            dout + off, dh + off, da_src + off, da_dst + off, n_nodes, n_edges, ld, nsld, w, \
+            L, s);                                                                          \
+      else                                                                                  \
+        st = gat_bwd_launch<int64_t, GG, HH>(                                               \
+            static_cast<const int64_t*>(row_ptr), *plan, row_ptr_t, col_t, perm, inv_perm,  \
+            *plan_t, h + off, a_src + off, a_dst + off, slope, out + off, ns + 4 * h0,      \
+            dout + off, dh + off, da_src + off, da_dst + off, n_nodes, n_edges, ld, nsld, w, \
+            L, s);                                                                          \
+    } else
+    TGX_GAT_SHAPES(TGX_GAT_BWD)
+    set_error("unsupported GAT head group G=%d HL=%d", shp.G, shp.HL);
 #undef TGX_GAT_BWD
-  set_error("unsupported GAT shape");
-  return TGX_UNSUPPORTED;
+    if (st != TGX_OK) return st;
+    h0 += hg;
+  }
+  return TGX_OK;
 }

@@ -476,7 +476,9 @@ class MessagePassing(Kernel):
             return None
         if gat.a_src.device != h.device or gat.a_dst.device != h.device:
             return None
-        if H * D not in (64, 128, 256) or D % 4:
+        # Any head count: the kernels run heads in groups of at most 256
+        # floats per node; the head width is 4 * 2^k floats, up to 256.
+        if D % 4 or D > 256 or (D // 4) & (D // 4 - 1):
             return None
         _native.lib()
         slope = gat.slope
@@ -631,7 +633,9 @@ class MessagePassing(Kernel):
         _, H, D = q.shape
         if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
             return None
-        if D % 8 or H * D not in (128, 256, 512):
+        # Any head count: the kernels run heads in groups of at most 512
+        # values per node; the head width is 8 * 2^k values, up to 512.
+        if D % 8 or D > 512 or (D // 8) & (D // 8 - 1):
             return None
         operands = [("dst", dot.q_field), ("src", dot.k_field), ("src", dot.v_field)]
         if dot.bias_field is not None:
