@@ -21,9 +21,11 @@ GOLD = json.loads((ROOT / "tests" / "golden" / "reference_vectors.json").read_te
 
 
 def declared_symbols():
-    text = (ROOT / "include" / "tgx.h").read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(tgx_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for header in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(tgx_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():

@@ -1,14 +1,18 @@
 """Host code under AddressSanitizer and UndefinedBehaviorSanitizer.
 
 The product's host-only C ABI code (tiga-lang_amd/csrc/tgx_capi.cpp: status
-strings, per-thread error messages, the reference planner restatement) and
+strings, per-thread error messages, the reference planner restatement; and
+tiga-lang_amd/csrc/tgx_cpu.cpp: the CPU twins of the device entry points) and
 the oracle's C CPU baseline (oracle/cpu_native.c: the threaded forward loop
 and the lowered backward) are compiled with g++/gcc and
 -fsanitize=address,undefined (host code only; no GPU code is involved) into
 a small harness (tests/sanitize/harness.cpp), which then runs the planner on
-the lit vectors and on random histograms and the CPU loops on random graphs.
+the lit vectors and on random histograms, the CPU loops on random graphs, and
+every CPU twin on random graphs with split hub rows (at 1 and 4 threads,
+compared bit for bit) and on broken inputs they must reject.
 Any sanitizer report fails the run (halt_on_error, non-zero exit); the
-results are also checked against the Python oracle.
+planner and loop results are also checked against the Python oracle (the
+twins' values are checked against it in tests/test_cpu_twins.py).
 """
 
 import json
@@ -37,10 +41,11 @@ def harness(tmp_path_factory):
     subprocess.run(["gcc", *SAN, "-std=c11", "-c", str(ROOT / "oracle" / "cpu_native.c"),
                     "-o", str(obj)], check=True)
     exe = out / "harness"
-    subprocess.run(["g++", *SAN, "-std=c++17", f"-I{ROOT / 'include'}",
+    csrc = ROOT / "tiga-lang_amd" / "csrc"
+    subprocess.run(["g++", *SAN, "-std=c++17", f"-I{ROOT / 'include'}", f"-I{csrc}",
                     str(ROOT / "tests" / "sanitize" / "harness.cpp"),
-                    str(ROOT / "tiga-lang_amd" / "csrc" / "tgx_capi.cpp"), str(obj),
-                    "-lpthread", "-o", str(exe)], check=True)
+                    str(csrc / "tgx_capi.cpp"), str(csrc / "tgx_cpu.cpp"), str(obj),
+                    "-pthread", "-o", str(exe)], check=True)
     return exe
 
 
@@ -119,3 +124,11 @@ def test_cpu_baseline_loops_under_sanitizers(harness):
                                    atol=1e-6)
         np.testing.assert_allclose(got[1], np.asarray(e_dx).ravel(), rtol=1e-5, atol=1e-6)
         np.testing.assert_allclose(got[2], np.asarray(e_dw).ravel(), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("H,D", [(4, 64), (3, 32), (1, 128), (5, 8)])
+def test_cpu_twins_under_sanitizers(harness, H, D):
+    # Random graphs with split hub rows; 1 and 4 threads must agree bit for
+    # bit; broken columns, plans and permutations must be rejected.
+    out = _run(harness, [f"twins {11 + H} 1200 {H} {D}"])
+    assert out == ["twins ok"], out

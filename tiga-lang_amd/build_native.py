@@ -64,7 +64,7 @@ def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Pa
             continue
         cmd = [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
         if src.suffix == ".cpp":
-            cmd = [hipcc, f"--offload-arch={ARCH}", "-O2", "-fPIC", "-std=c++17",
+            cmd = [hipcc, f"--offload-arch={ARCH}", "-O2", "-fPIC", "-std=c++17", "-pthread",
                    "-Wno-unused-result", f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o",
                    str(obj)]
         if verbose:
@@ -84,7 +84,7 @@ def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Pa
     if failed:
         raise RuntimeError("HIP build failed:\n" + "\n".join(failed))
     tmp = LIB.with_suffix(".so.tmp")
-    link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+    link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", "-o", str(tmp),
             *map(str, objects)]
     if verbose:
         print(" ".join(link), flush=True)

@@ -486,25 +486,10 @@ struct DotShape {
   int G, HL;
 };
 
-// Heads run in groups whose row slice fits one wave at 8 bf16 per lane: a
-// group of Hg heads (a power of two) with Hg * D <= 512 values.  Any H splits
-// greedily into such groups (H = 6, D = 128 -> 4 + 2); each group launches
-// the kernels over its strided slice of q, k, v, out, dout, dq, dk, dv, ml,
-// bias and dbias.
-constexpr int kDotGroupValues = 512;
-
-bool dot_heads_ok(int H, int D) {
-  if (H < 1 || D <= 0 || D % 8 != 0 || D > kDotGroupValues) return false;
-  const int hl = D / 8;
-  return (hl & (hl - 1)) == 0;
-}
-
-// Heads in the group starting at head h0.
-int dot_group_heads(int H, int D, int h0) {
-  int hg = kDotGroupValues / D;
-  while (hg > H - h0) hg >>= 1;
-  return hg;
-}
+// Heads run in groups (group_heads, kDotGroupValues): each group launches the
+// kernels over its strided slice of q, k, v, out, dout, dq, dk, dv, ml, bias
+// and dbias.
+int dot_group_heads(int H, int D, int h0) { return group_heads(H, D, h0, kDotGroupValues); }
 
 DotShape dot_shape(int Hg, int D) { return DotShape{Hg * D / 8, D / 8}; }
 

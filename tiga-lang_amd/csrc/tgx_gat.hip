@@ -489,27 +489,10 @@ struct GatShape {
   int G, HL;
 };
 
-// Heads run in groups whose row slice fits one lane group at a float4 per
-// lane: a group of Hg heads (a power of two) with Hg * D <= 256 floats.  Any
-// H splits greedily into such groups (H = 3 -> 2 + 1); each group launches
-// the kernels over its strided slice of h, out, dout, dh and the node state,
-// and its own contiguous slice of a_src, a_dst, da_src and da_dst.
-constexpr int kGatGroupFloats = 256;
-
-bool gat_head_dim_ok(int D) {
-  if (D <= 0 || D % 4 != 0 || D > kGatGroupFloats) return false;
-  const int hl = D / 4;
-  return (hl & (hl - 1)) == 0;
-}
-
-bool gat_heads_ok(int H, int D) { return H >= 1 && gat_head_dim_ok(D); }
-
-// Heads in the group starting at head h0.
-int gat_group_heads(int H, int D, int h0) {
-  int hg = kGatGroupFloats / D;
-  while (hg > H - h0) hg >>= 1;
-  return hg;
-}
+// Heads run in groups (group_heads, kGatGroupFloats): each group launches the
+// kernels over its strided slice of h, out, dout, dh and the node state, and
+// its own contiguous slice of a_src, a_dst, da_src and da_dst.
+int gat_group_heads(int H, int D, int h0) { return group_heads(H, D, h0, kGatGroupFloats); }
 
 GatShape gat_shape(int Hg, int D) { return GatShape{Hg * D / 4, D / 4}; }
 

@@ -8,19 +8,9 @@
 #include <stdio.h>
 
 #include "tgx.h"
+#include "tgx_check.h"
 
 namespace tgx {
-
-// Last error message for the calling thread; read by tgx_last_error().
-void set_error(const char* fmt, ...);
-
-#define TGX_REQUIRE(cond, ...)                  \
-  do {                                          \
-    if (!(cond)) {                              \
-      ::tgx::set_error(__VA_ARGS__);            \
-      return TGX_INVALID_ARGUMENT;              \
-    }                                           \
-  } while (0)
 
 #define TGX_HIP(call)                                                  \
   do {                                                                 \
@@ -45,9 +35,6 @@ void set_error(const char* fmt, ...);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
-
-inline size_t align_up(size_t v, size_t a = 256) { return (v + a - 1) / a * a; }
 
 // Bump allocator over a caller-provided workspace.
 struct Carve {
@@ -82,21 +69,6 @@ inline int64_t resident_blocks(Kernel kernel, int block) {
     return 1;
   const int64_t n = static_cast<int64_t>(cus) * (per_cu > 0 ? per_cu : 1);
   return n > 0 ? n : 1;
-}
-
-// Validate a row plan against the number of rows it must cover.
-inline int check_plan(const tgx_row_plan* p, int64_t rows) {
-  TGX_REQUIRE(p != nullptr, "null plan");
-  TGX_REQUIRE(p->n_rows == rows, "plan covers %lld rows, expected %lld",
-              static_cast<long long>(p->n_rows), static_cast<long long>(rows));
-  TGX_REQUIRE(p->n_empty >= 0 && p->n_wave >= 0 && p->n_split >= 0 &&
-                  p->n_chunks >= 0 && p->n_empty + p->n_wave + p->n_split == p->n_rows,
-              "inconsistent plan");
-  TGX_REQUIRE(p->n_rows == 0 || p->rows_dev, "plan without rows");
-  TGX_REQUIRE(p->n_split == 0 || (p->chunk_offsets_dev && p->chunk_edges > 0 &&
-                                  p->n_chunks >= p->n_split),
-              "plan without chunk offsets");
-  return TGX_OK;
 }
 
 }  // namespace tgx

@@ -109,6 +109,30 @@ _SIGNATURES: dict[str, list] = {
     "tgx_segment_softmax_bwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tgx_segment_softmax_gather_fwd": [c_vp, c_vp, c_int, c_i64, c_vp, c_int, c_f32, c_vp,
                                        c_vp, c_vp],
+    # CPU twins (include/tgx_cpu.h): host pointers, no stream.
+    "tgx_cpu_set_threads": [c_int],
+    "tgx_cpu_destination_index": [c_vp, c_int, c_i64, c_i64, c_vp, c_int],
+    "tgx_cpu_csr_transpose": [c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp],
+    "tgx_cpu_plan_degree_bins": [c_vp, c_int, c_i64, P(c_i64), c_int, c_vp, P(c_i64)],
+    "tgx_cpu_plan_split_chunks": [c_vp, c_int, c_vp, c_i64, ctypes.c_int32, c_vp, P(c_i64)],
+    "tgx_cpu_csr_sum_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64,
+                            c_i64],
+    "tgx_cpu_csr_sum_bwd": [c_vp, c_vp, c_vp, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
+                            c_i64, c_i64],
+    "tgx_cpu_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
+                        c_i64, c_int, c_int],
+    "tgx_cpu_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, P(RowPlan),
+                        c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
+                        c_i64, c_int, c_int],
+    "tgx_cpu_dot_attn_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_f32,
+                             c_vp, c_vp, c_i64, c_i64, c_int, c_int],
+    "tgx_cpu_dot_attn_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, P(RowPlan),
+                             c_vp, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                             c_vp, c_i64, c_i64, c_int, c_int],
+    "tgx_cpu_attn_fwd": [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, P(c_i64), c_f32,
+                         c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int],
+    "tgx_cpu_attn_bwd": [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, P(c_i64), c_vp,
+                         c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_int, c_int],
     "tgx_profile_begin": [],
     "tgx_profile_end": [],
     "tgx_profile_count": [],
