@@ -43,6 +43,11 @@ enum {
   TGX_INTERNAL = 4
 };
 
+/* Element types: TGX_DTYPE_BF16 / TGX_DTYPE_F16 are raw 16-bit storage,
+ * TGX_DTYPE_F32 is float.  The attention tiles take BF16 and F16; the sum
+ * takes all three (its weights, partials and sums stay fp32). */
+enum { TGX_DTYPE_BF16 = 0, TGX_DTYPE_F16 = 1, TGX_DTYPE_F32 = 2 };
+
 /* Human-readable name of a status code. */
 const char* tgx_status_string(int status);
 /* Message recorded by the last failing call on this thread ("" if none). */
@@ -198,18 +203,20 @@ int tgx_plan_reference_buckets(int64_t n_rows, int64_t max_degree,
 
 /* Forward of the weighted-sum message (reference WeightedSumPattern,
  * python/tiga/compiler/capture.py:123-145, executed by _execute_weighted_sum,
- * interop/torch/message_passing.py:2903-3345; fp32).
- *   x_dev [n_src, F] fp32, w_dev [n_edges] fp32 or NULL (weight 1),
- *   out_dev [n_dst, F] fp32, fully written.
+ * interop/torch/message_passing.py:2903-3345; its eager reduce_sum keeps the
+ * message dtype, interop/torch/reducer_oracle.py:44-57).
+ *   x_dev [n_src, F] and out_dev [n_dst, F] (fully written) of element type
+ *   dtype (TGX_DTYPE_F32, _BF16 or _F16), w_dev [n_edges] fp32 or NULL
+ *   (weight 1); products and sums in fp32, one rounding per output.
  *   col_dev NULL: the columns are the edge ids, i.e. x_dev [n_edges, F] is a
  *   per-edge field summed per destination row (n_src = n_edges < 2^31; the
  *   per-edge input gradients of an edge network reduce this way).
  * F may be any positive width; widths that are multiples of 4 with
  * F*4 <= 1024 bytes take the vectorised path. */
 int tgx_csr_sum_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
-                    const tgx_row_plan* plan, const float* x_dev,
-                    const float* w_dev, float* out_dev, int64_t n_dst,
-                    int64_t n_src, int64_t F, float* partial_dev,
+                    const tgx_row_plan* plan, const void* x_dev,
+                    const float* w_dev, void* out_dev, int64_t n_dst,
+                    int64_t n_src, int64_t F, int dtype, float* partial_dev,
                     void* stream);
 
 /* Bytes of partial_dev scratch the sum/attention kernels need for a plan. */
@@ -220,12 +227,13 @@ int tgx_partial_bytes(const tgx_row_plan* plan, int64_t state_floats,
  *   dx[j, :] = sum over transposed edges e' of j: w[perm[e']] * dout[col_t[e'], :]
  *   dw[e]    = <dout[row(e), :], x[col[e], :]>   (written at perm[e'])
  * Replaces the reference's Torch replay (message_passing.py:378-409).
- * plan_t partitions the transposed CSR.  dx_dev / dw_dev may be NULL to skip. */
+ * plan_t partitions the transposed CSR.  dx_dev / dw_dev may be NULL to skip.
+ * x, dout and dx are of element type dtype; w and dw are fp32. */
 int tgx_csr_sum_bwd(const int32_t* row_ptr_t_dev, const int32_t* col_t_dev,
                     const int32_t* perm_dev, const tgx_row_plan* plan_t,
-                    const float* x_dev, const float* w_dev,
-                    const float* dout_dev, float* dx_dev, float* dw_dev,
-                    int64_t n_dst, int64_t n_src, int64_t F,
+                    const void* x_dev, const float* w_dev,
+                    const void* dout_dev, void* dx_dev, float* dw_dev,
+                    int64_t n_dst, int64_t n_src, int64_t F, int dtype,
                     float* partial_dev, void* stream);
 
 /* ------------------------------------------------------------------------ */
@@ -337,9 +345,6 @@ int tgx_dot_attn_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
 /*   block [0, num_dst) x [0, num_src); Graph.triangular(n) one causal block */
 /*   (interop/torch/graph.py:260-294, 535-592).                              */
 /* ------------------------------------------------------------------------ */
-
-/* Element types of the attention tiles. */
-enum { TGX_DTYPE_BF16 = 0, TGX_DTYPE_F16 = 1 };
 
 /* Host: the work list of one attention launch, in dispatch order.  A task is
  * four int32 (block, first row, head, 0) naming `block` rows of one head:

@@ -65,15 +65,15 @@ int tgx_cpu_plan_split_chunks(const void* row_ptr, int idx_bits, const int32_t* 
  * reducer_oracle.py:44-58).  plan holds host arrays.  col may be NULL (the
  * columns are the edge ids). */
 int tgx_cpu_csr_sum_fwd(const void* row_ptr, const void* col, int idx_bits,
-                        const tgx_row_plan* plan, const float* x, const float* w, float* out,
-                        int64_t n_dst, int64_t n_src, int64_t F);
+                        const tgx_row_plan* plan, const void* x, const float* w, void* out,
+                        int64_t n_dst, int64_t n_src, int64_t F, int dtype);
 
 /* Twin of tgx_csr_sum_bwd (reference Torch replay,
  * interop/torch/message_passing.py:378-409).  dx / dw may be NULL. */
 int tgx_cpu_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_t, const int32_t* perm,
-                        const tgx_row_plan* plan_t, const float* x, const float* w,
-                        const float* dout, float* dx, float* dw, int64_t n_dst, int64_t n_src,
-                        int64_t F);
+                        const tgx_row_plan* plan_t, const void* x, const float* w,
+                        const void* dout, void* dx, float* dw, int64_t n_dst, int64_t n_src,
+                        int64_t F, int dtype);
 
 /* Twin of tgx_gat_fwd (eager evaluation of the additive edge function,
  * interop/torch/message_passing.py:2848-2894, reducer_oracle.py:60-137).

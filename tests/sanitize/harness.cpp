@@ -125,9 +125,9 @@ std::string run_twins(uint64_t seed, int64_t n, int H, int D) {
     tgx_cpu_set_threads(r == 0 ? 1 : 4);
     std::vector<float> out(n * F), dx(n * F), dw(E);
     if (tgx_cpu_csr_sum_fwd(rp.data(), col.data(), 64, &plan.p, x.data(), w.data(), out.data(),
-                            n, n, F) != TGX_OK ||
+                            n, n, F, TGX_DTYPE_F32) != TGX_OK ||
         tgx_cpu_csr_sum_bwd(rpt.data(), colt.data(), perm.data(), &plan_t.p, x.data(), w.data(),
-                            g.data(), dx.data(), dw.data(), n, n, F) != TGX_OK)
+                            g.data(), dx.data(), dw.data(), n, n, F, TGX_DTYPE_F32) != TGX_OK)
       return "sum";
     sums[r] = out;
     sums[r].insert(sums[r].end(), dx.begin(), dx.end());
@@ -183,20 +183,20 @@ std::string run_twins(uint64_t seed, int64_t n, int H, int D) {
   std::vector<int64_t> bad_col = col;
   bad_col[E / 2] = n + 7;
   if (tgx_cpu_csr_sum_fwd(rp.data(), bad_col.data(), 64, &plan.p, x.data(), w.data(),
-                          out.data(), n, n, F) != TGX_INVALID_ARGUMENT)
+                          out.data(), n, n, F, TGX_DTYPE_F32) != TGX_INVALID_ARGUMENT)
     return "column out of range accepted";
   Plan twice = plan;
   twice.rows[1] = twice.rows[0];
   twice.p.rows_dev = twice.rows.data();
   twice.p.chunk_offsets_dev = twice.chunks.data();
   if (tgx_cpu_csr_sum_fwd(rp.data(), col.data(), 64, &twice.p, x.data(), w.data(), out.data(),
-                          n, n, F) != TGX_INVALID_ARGUMENT)
+                          n, n, F, TGX_DTYPE_F32) != TGX_INVALID_ARGUMENT)
     return "plan with a repeated row accepted";
   std::vector<int32_t> bad_perm = perm;
   bad_perm[0] = bad_perm[1];
   std::vector<float> dx(n * F);
   if (tgx_cpu_csr_sum_bwd(rpt.data(), colt.data(), bad_perm.data(), &plan_t.p, x.data(),
-                          w.data(), g.data(), dx.data(), nullptr, n, n, F) !=
+                          w.data(), g.data(), dx.data(), nullptr, n, n, F, TGX_DTYPE_F32) !=
       TGX_INVALID_ARGUMENT)
     return "broken perm accepted";
   return "";

@@ -24,6 +24,7 @@ from graphs import rmat_csr, skewed_csr
 
 WAVE_MAX = 512
 CHUNK = 512
+F32 = _native.DTYPE_F32
 
 
 def call(name, *args):
@@ -148,22 +149,46 @@ def test_sum_twin_against_oracle(bits, F, weighted):
     dout = rng.standard_normal((2500, F)).astype(np.float32)
     out = np.empty((2500, F), np.float32)
     call("tgx_cpu_csr_sum_fwd", p(g.rp), p(g.col), bits, g.plan.ref, p(x), p(w), p(out), 2500,
-         2500, F)
+         2500, F, F32)
     assert rel(out, ref.sum_fwd(rp, col, x, w)) <= 1e-5
     dx = np.empty_like(x)
     dw = np.empty(g.E, np.float32)
     call("tgx_cpu_csr_sum_bwd", p(g.rpt), p(g.colt), p(g.perm), g.plan_t.ref, p(x), p(w),
-         p(dout), p(dx), p(dw), 2500, 2500, F)
+         p(dout), p(dx), p(dw), 2500, 2500, F, F32)
     e_dx, e_dw = ref.sum_bwd(rp, col, x, w, dout)
     assert rel(dx, e_dx) <= 1e-5
     assert rel(dw, e_dw) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("F", [3, 64])
+def test_sum_twin_with_16_bit_features(dtype, F):
+    rp, col, g = _graph(12 + F, 2000, 32)
+    rng = np.random.default_rng(F)
+    x = torch.as_tensor(rng.standard_normal((2000, F)), dtype=torch.float32).to(dtype)
+    dout = torch.as_tensor(rng.standard_normal((2000, F)), dtype=torch.float32).to(dtype)
+    w = rng.standard_normal(g.E).astype(np.float32)
+    code = _native.dtype_code(x)
+    out = np.zeros((2000, F), np.int16)
+    call("tgx_cpu_csr_sum_fwd", p(g.rp), p(g.col), 32, g.plan.ref, p(_raw(x)), p(w), p(out),
+         2000, 2000, F, code)
+    xf, gf = x.float().numpy(), dout.float().numpy()
+    assert rel(_from_raw(out, dtype), ref.sum_fwd(rp, col, xf, w)) <= 1e-2
+    dx = np.zeros((2000, F), np.int16)
+    dw = np.empty(g.E, np.float32)
+    call("tgx_cpu_csr_sum_bwd", p(g.rpt), p(g.colt), p(g.perm), g.plan_t.ref, p(_raw(x)), p(w),
+         p(_raw(dout)), p(dx), p(dw), 2000, 2000, F, code)
+    e_dx, e_dw = ref.sum_bwd(rp, col, xf, w, gf)
+    assert rel(_from_raw(dx, dtype), e_dx) <= 1e-2
+    assert rel(dw, e_dw) <= 1e-5     # fp32 dot products of exact 16-bit inputs
 
 
 def test_sum_twin_of_an_edge_field_per_row():
     rp, col, g = _graph(9, 1500, 64)
     x = np.random.default_rng(9).standard_normal((g.E, 5)).astype(np.float32)
     out = np.empty((1500, 5), np.float32)
-    call("tgx_cpu_csr_sum_fwd", p(g.rp), None, 64, g.plan.ref, p(x), None, p(out), 1500, g.E, 5)
+    call("tgx_cpu_csr_sum_fwd", p(g.rp), None, 64, g.plan.ref, p(x), None, p(out), 1500, g.E, 5,
+         F32)
     assert rel(out, ref.sum_fwd(rp, np.arange(g.E), x)) <= 1e-5
 
 
@@ -312,12 +337,12 @@ def test_twin_checks_reject_bad_indices_and_plans():
     bad[17] = 600
     with pytest.raises(RuntimeError, match="outside"):
         call("tgx_cpu_csr_sum_fwd", p(g.rp), p(bad), 64, g.plan.ref, p(x), None, p(out), 600,
-             600, 4)
+             600, 4, F32)
     drop = g.rp.copy()
     drop[5] = drop[6] + 1
     with pytest.raises(RuntimeError, match="decreases"):
         call("tgx_cpu_csr_sum_fwd", p(drop), p(g.col), 64, g.plan.ref, p(x), None, p(out), 600,
-             600, 4)
+             600, 4, F32)
     # A plan whose rows repeat, or whose chunk offsets miscount a split row.
     rows = g.plan.rows.copy()
     rows[1] = rows[0]
@@ -325,7 +350,7 @@ def test_twin_checks_reject_bad_indices_and_plans():
     twice.rows_dev = p(rows)
     with pytest.raises(RuntimeError, match="twice"):
         call("tgx_cpu_csr_sum_fwd", p(g.rp), p(g.col), 64, ctypes.byref(twice), p(x), None,
-             p(out), 600, 600, 4)
+             p(out), 600, 600, 4, F32)
     chunks = g.plan.chunks.copy()
     chunks[1:] += 1
     miscount = _native.RowPlan(*[getattr(g.plan.plan, f) for f, _ in _native.RowPlan._fields_])
@@ -333,13 +358,13 @@ def test_twin_checks_reject_bad_indices_and_plans():
     miscount.n_chunks += 1
     with pytest.raises(RuntimeError, match="chunks"):
         call("tgx_cpu_csr_sum_fwd", p(g.rp), p(g.col), 64, ctypes.byref(miscount), p(x), None,
-             p(out), 600, 600, 4)
+             p(out), 600, 600, 4, F32)
     # perm that is not a permutation.
     perm = g.perm.copy()
     perm[0] = perm[1]
     with pytest.raises(RuntimeError, match="permutation"):
         call("tgx_cpu_csr_sum_bwd", p(g.rpt), p(g.colt), p(perm), g.plan_t.ref, p(x), None,
-             p(out), p(np.empty_like(x)), None, 600, 600, 4)
+             p(out), p(np.empty_like(x)), None, 600, 600, 4, F32)
     # Exact softmax only in the block-attention twin.
     cu = np.array([0, 64], np.int32)
     z = np.zeros((64, 1, 64), np.int16)

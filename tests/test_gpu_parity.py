@@ -151,6 +151,58 @@ def test_sum_fwd_bwd_parity(F_, idx):
     assert rel_err(wt.grad.cpu(), e_dw) <= RTOL32
 
 
+# 16-bit features: the message w * x has Torch's promoted dtype, as in the
+# reference's eager reduce_sum (reducer_oracle.py:44-57): bf16 x with bf16 (or
+# no) weights sums to bf16, bf16 x with fp32 weights to fp32.  The kernels
+# multiply and add in fp32 and round once per output.  Bars: against float64
+# math, 1e-2 of the largest |value| for a 16-bit output (one rounding: 2^-8
+# for bf16) and 1e-5 for an fp32 output (the 16-bit inputs are exact in
+# fp32); against the reference's own arithmetic (bf16 products, index_add in
+# bf16, on the CPU) 1e-2 plus that result's own distance from float64.
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("w_dtype", [None, "same", torch.float32])
+@pytest.mark.parametrize("F_", [3, 64, 300])
+def test_sum_16_bit_features(dtype, w_dtype, F_):
+    print(f"sum 16-bit {dtype} w={w_dtype} F={F_}", flush=True)
+    rp, col = skewed_csr(40 + F_, 3000, 2500, mean_deg=8, hubs=(1500, 600), hot_src=7,
+                         hot_frac=0.3)
+    rng = np.random.default_rng(F_)
+    graph = tg.Graph.from_csr(to_dev(rp, torch.int64), to_dev(col, torch.int64), num_src=2500)
+    xt = to_dev(rng.standard_normal((2500, F_)), dtype).requires_grad_(True)
+    wd = None if w_dtype is None else (dtype if w_dtype == "same" else w_dtype)
+    wt = None if wd is None else to_dev(rng.random(col.size), wd).requires_grad_(True)
+    out_dtype = dtype if wd is None else torch.promote_types(dtype, wd)
+    k = WeightedSum() if wt is not None else PlainSum()
+    edge = {} if wt is None else {"weight": wt}
+    out = k(graph=graph, src={"x": xt}, dst={}, edge=edge)
+    assert k.last_variant.backend == "hip"
+    assert out.dtype == out_dtype
+    dout = to_dev(rng.standard_normal((3000, F_)), out_dtype)
+    out.backward(dout)
+    assert xt.grad.dtype == dtype and (wt is None or wt.grad.dtype == wd)
+    f = lambda t: t.detach().double().cpu().numpy()
+    w64 = None if wt is None else f(wt)
+    e_out = ref.sum_fwd(rp, col, f(xt), w64)
+    e_dx, e_dw = ref.sum_bwd(rp, col, f(xt), w64, f(dout))
+    bar = 1e-2 if out_dtype != torch.float32 else RTOL32
+    assert rel_err(f(out), e_out) <= bar
+    # dx is rounded to the 16-bit input type.
+    assert rel_err(f(xt.grad), e_dx) <= 1e-2
+    if wt is not None:
+        assert rel_err(f(wt.grad), e_dw) <= (1e-2 if wd != torch.float32 else RTOL32)
+    # The reference's eager arithmetic in the message dtype, on the CPU.
+    xc, dst = xt.detach().cpu(), torch.as_tensor(ref.destination_index(rp))
+    msg = xc[torch.as_tensor(col)]
+    if wt is not None:
+        msg = wt.detach().cpu()[:, None] * msg
+    ref16 = torch.zeros(3000, F_, dtype=msg.dtype).index_add_(0, dst, msg)
+    own = rel_err(ref16.double().numpy(), e_out)
+    err16 = rel_err(f(out), ref16.double().numpy())
+    print(f"  out vs reference {msg.dtype} arithmetic {err16:.3e} (its own error {own:.3e})",
+          flush=True)
+    assert err16 <= 1e-2 + own
+
+
 def test_sum_unweighted_and_empty_graph():
     rp, col = skewed_csr(20, 500, 400, mean_deg=3)
     x = np.random.default_rng(0).standard_normal((400, 16)).astype(np.float32)

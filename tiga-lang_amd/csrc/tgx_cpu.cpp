@@ -414,18 +414,49 @@ extern "C" int tgx_cpu_plan_split_chunks(const void* row_ptr, int idx_bits,
 
 // ---- Weighted sum -----------------------------------------------------------------
 
+namespace {
+
+// Feature storage of the sum (x, out, dout, dx) by dtype code.
+struct Feat {
+  int dtype;
+  float load(const void* p, int64_t i) const {
+    if (dtype == TGX_DTYPE_F32) return static_cast<const float*>(p)[i];
+    return Half16{dtype}.load(static_cast<const uint16_t*>(p), i);
+  }
+  void store(void* p, int64_t i, float v) const {
+    if (dtype == TGX_DTYPE_F32)
+      static_cast<float*>(p)[i] = v;
+    else
+      static_cast<uint16_t*>(p)[i] = Half16{dtype}.store(v);
+  }
+};
+
+int check_sum_dtype(int dtype) {
+  if (dtype != TGX_DTYPE_F32 && dtype != TGX_DTYPE_BF16 && dtype != TGX_DTYPE_F16) {
+    set_error("sum supports fp32, bf16 and fp16 features (dtype code %d)", dtype);
+    return TGX_UNSUPPORTED;
+  }
+  return TGX_OK;
+}
+
+}  // namespace
+
 extern "C" int tgx_cpu_csr_sum_fwd(const void* row_ptr, const void* col, int idx_bits,
-                                   const tgx_row_plan* plan, const float* x, const float* w,
-                                   float* out, int64_t n_dst, int64_t n_src, int64_t F) {
+                                   const tgx_row_plan* plan, const void* x, const float* w,
+                                   void* out, int64_t n_dst, int64_t n_src, int64_t F,
+                                   int dtype) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(F > 0 && n_dst >= 0 && n_src >= 0, "bad sizes");
-  int st = check_plan(plan, n_dst);
+  int st = check_sum_dtype(dtype);
+  if (st != TGX_OK) return st;
+  st = check_plan(plan, n_dst);
   if (st != TGX_OK) return st;
   if (n_dst == 0) return TGX_OK;
   TGX_REQUIRE(row_ptr && out && (x || n_src == 0), "null pointer");
   TGX_REQUIRE(col || n_src < (int64_t{1} << 31), "edge-id columns need fewer than 2^31 edges");
   return guarded([&]() -> int {
     const Idx rp{row_ptr, idx_bits}, c{col, idx_bits};
+    const Feat ft{dtype};
     int64_t E = 0;
     int s = check_csr(rp, col ? &c : nullptr, n_dst, n_src, &E);
     if (s != TGX_OK) return s;
@@ -435,39 +466,45 @@ extern "C" int tgx_cpu_csr_sum_fwd(const void* row_ptr, const void* col, int idx
     auto range = [&](int64_t e0, int64_t e1, float* acc) {
       for (int64_t e = e0; e < e1; ++e) {
         const float we = w ? w[e] : 1.f;
-        const float* xr = x + (col ? c[e] : e) * F;
-        for (int64_t f = 0; f < F; ++f) acc[f] += we * xr[f];
+        const int64_t base = (col ? c[e] : e) * F;
+        for (int64_t f = 0; f < F; ++f) acc[f] += we * ft.load(x, base + f);
       }
+    };
+    auto store = [&](int64_t row, const float* acc) {
+      for (int64_t f = 0; f < F; ++f) ft.store(out, row * F + f, acc[f]);
     };
     walk_plan(
         *plan, rp,
         [&](int64_t row, int64_t e0, int64_t e1) {
-          float* o = out + row * F;
-          std::fill(o, o + F, 0.f);
-          range(e0, e1, o);
+          std::vector<float> acc(static_cast<size_t>(F), 0.f);
+          range(e0, e1, acc.data());
+          store(row, acc.data());
         },
         [&](int64_t row, const std::vector<std::pair<int64_t, int64_t>>& chunks) {
-          float* o = out + row * F;
-          std::fill(o, o + F, 0.f);
-          std::vector<float> part(static_cast<size_t>(F));
+          std::vector<float> acc(static_cast<size_t>(F), 0.f), part(acc.size());
           for (const auto& ch : chunks) {
             std::fill(part.begin(), part.end(), 0.f);
             range(ch.first, ch.second, part.data());
-            for (int64_t f = 0; f < F; ++f) o[f] += part[f];
+            for (int64_t f = 0; f < F; ++f) acc[f] += part[f];
           }
+          store(row, acc.data());
         },
-        [&](int64_t row) { std::fill(out + row * F, out + (row + 1) * F, 0.f); });
+        [&](int64_t row) {
+          for (int64_t f = 0; f < F; ++f) ft.store(out, row * F + f, 0.f);
+        });
     return TGX_OK;
   });
 }
 
 extern "C" int tgx_cpu_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_t,
                                    const int32_t* perm, const tgx_row_plan* plan_t,
-                                   const float* x, const float* w, const float* dout,
-                                   float* dx, float* dw, int64_t n_dst, int64_t n_src,
-                                   int64_t F) {
+                                   const void* x, const float* w, const void* dout, void* dx,
+                                   float* dw, int64_t n_dst, int64_t n_src, int64_t F,
+                                   int dtype) {
   TGX_REQUIRE(F > 0 && n_dst >= 0 && n_src >= 0, "bad sizes");
-  int st = check_plan(plan_t, n_src);
+  int st = check_sum_dtype(dtype);
+  if (st != TGX_OK) return st;
+  st = check_plan(plan_t, n_src);
   if (st != TGX_OK) return st;
   if (n_src == 0) return TGX_OK;
   TGX_REQUIRE(row_ptr_t && dout, "null pointer");
@@ -477,44 +514,47 @@ extern "C" int tgx_cpu_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_
     int s = check_transposed(row_ptr_t, col_t, perm, nullptr, n_src, n_dst, &E);
     if (s != TGX_OK) return s;
     const Idx rpt{row_ptr_t, 32};
+    const Feat ft{dtype};
     s = check_plan_rows(plan_t, rpt, n_src);
     if (s != TGX_OK) return s;
     auto range = [&](int64_t j, int64_t e0, int64_t e1, float* acc) {
       for (int64_t k = e0; k < e1; ++k) {
         const int64_t e = perm[k];
-        const float* g = dout + static_cast<int64_t>(col_t[k]) * F;
+        const int64_t gb = static_cast<int64_t>(col_t[k]) * F;
         if (acc) {
           const float we = w ? w[e] : 1.f;
-          for (int64_t f = 0; f < F; ++f) acc[f] += we * g[f];
+          for (int64_t f = 0; f < F; ++f) acc[f] += we * ft.load(dout, gb + f);
         }
         if (dw) {
-          const float* xr = x + j * F;
           float d = 0.f;
-          for (int64_t f = 0; f < F; ++f) d += g[f] * xr[f];
+          for (int64_t f = 0; f < F; ++f) d += ft.load(dout, gb + f) * ft.load(x, j * F + f);
           dw[e] = d;
         }
       }
     };
+    auto store = [&](int64_t j, const float* acc) {
+      if (dx)
+        for (int64_t f = 0; f < F; ++f) ft.store(dx, j * F + f, acc[f]);
+    };
     walk_plan(
         *plan_t, rpt,
         [&](int64_t j, int64_t e0, int64_t e1) {
-          float* o = dx ? dx + j * F : nullptr;
-          if (o) std::fill(o, o + F, 0.f);
-          range(j, e0, e1, o);
+          std::vector<float> acc(static_cast<size_t>(F), 0.f);
+          range(j, e0, e1, dx ? acc.data() : nullptr);
+          store(j, acc.data());
         },
         [&](int64_t j, const std::vector<std::pair<int64_t, int64_t>>& chunks) {
-          float* o = dx ? dx + j * F : nullptr;
-          if (o) std::fill(o, o + F, 0.f);
-          std::vector<float> part(static_cast<size_t>(F));
+          std::vector<float> acc(static_cast<size_t>(F), 0.f), part(acc.size());
           for (const auto& ch : chunks) {
             std::fill(part.begin(), part.end(), 0.f);
-            range(j, ch.first, ch.second, o ? part.data() : nullptr);
-            if (o)
-              for (int64_t f = 0; f < F; ++f) o[f] += part[f];
+            range(j, ch.first, ch.second, dx ? part.data() : nullptr);
+            for (int64_t f = 0; f < F; ++f) acc[f] += part[f];
           }
+          store(j, acc.data());
         },
         [&](int64_t j) {
-          if (dx) std::fill(dx + j * F, dx + (j + 1) * F, 0.f);
+          const std::vector<float> zero(static_cast<size_t>(F), 0.f);
+          store(j, zero.data());
         });
     return TGX_OK;
   });

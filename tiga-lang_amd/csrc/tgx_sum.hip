@@ -21,32 +21,79 @@
 namespace tgx {
 namespace {
 
-template <typename I>
+// Element storage of the feature tables (x, out, dout, dx); weights and the
+// split-row partials are always fp32, and so is every sum.
+template <int DT>
+struct Elem;
+template <>
+struct Elem<TGX_DTYPE_F32> {
+  typedef float S;
+  static __device__ __forceinline__ f32x4 load4(const S* p) {
+    return *reinterpret_cast<const f32x4*>(p);
+  }
+  static __device__ __forceinline__ void store4(S* p, f32x4 v) {
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+  static __device__ __forceinline__ float load1(const S* p) { return *p; }
+  static __device__ __forceinline__ void store1(S* p, float v) { *p = v; }
+};
+template <>
+struct Elem<TGX_DTYPE_BF16> {
+  typedef uint16_t S;
+  static __device__ __forceinline__ f32x4 load4(const S* p) {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    return f32x4{bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+  }
+  static __device__ __forceinline__ void store4(S* p, f32x4 v) {
+    *reinterpret_cast<uint2*>(p) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  }
+  static __device__ __forceinline__ float load1(const S* p) { return bf16_lo(*p); }
+  static __device__ __forceinline__ void store1(S* p, float v) {
+    *p = static_cast<uint16_t>(f32_to_bf16_bits(v));
+  }
+};
+template <>
+struct Elem<TGX_DTYPE_F16> {
+  typedef _Float16 S;
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x4 load4(const S* p) {
+    const h4 h = *reinterpret_cast<const h4*>(p);
+    return f32x4{static_cast<float>(h[0]), static_cast<float>(h[1]), static_cast<float>(h[2]),
+                 static_cast<float>(h[3])};
+  }
+  static __device__ __forceinline__ void store4(S* p, f32x4 v) {
+    *reinterpret_cast<h4*>(p) = h4{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]),
+                                   static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+  }
+  static __device__ __forceinline__ float load1(const S* p) { return static_cast<float>(*p); }
+  static __device__ __forceinline__ void store1(S* p, float v) { *p = static_cast<_Float16>(v); }
+};
+
+template <typename I, int DT>
 struct SumArgs {
+  typedef typename Elem<DT>::S S;
   const I* row_ptr;
   const I* col;
   PlanView plan;
-  const float* x;          // gathered table [*, F]
+  const S* x;              // gathered table [*, F]
   const float* w;          // per-edge weight or null (=1)
   const int32_t* wperm;    // weight index = wperm[e] when non-null
-  float* out;              // [rows, F]
+  S* out;                  // [rows, F]
   float* partial;          // [n_chunks, F]
-  const float* self_x;     // dw: row's own features [rows, F] (null = no dw)
+  const S* self_x;         // dw: row's own features [rows, F] (null = no dw)
   float* dw;               // dw output, written at wperm ? wperm[e] : e
   int64_t F;
 };
 
-template <int VEC>
+// VEC consecutive features per lane, held in fp32.
+template <int VEC, int DT>
 struct Vec;
-template <>
-struct Vec<4> {
+template <int DT>
+struct Vec<4, DT> {
   typedef f32x4 T;
-  static __device__ __forceinline__ T load(const float* p) {
-    return *reinterpret_cast<const f32x4*>(p);
-  }
-  static __device__ __forceinline__ void store(float* p, T v) {
-    *reinterpret_cast<f32x4*>(p) = v;
-  }
+  typedef typename Elem<DT>::S S;
+  static __device__ __forceinline__ T load(const S* p) { return Elem<DT>::load4(p); }
+  static __device__ __forceinline__ void store(S* p, T v) { Elem<DT>::store4(p, v); }
   static __device__ __forceinline__ T zero() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
   static __device__ __forceinline__ float dot(T a, T b) {
     return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
@@ -56,11 +103,12 @@ struct Vec<4> {
                  __shfl_xor(v[2], m, 64), __shfl_xor(v[3], m, 64)};
   }
 };
-template <>
-struct Vec<1> {
+template <int DT>
+struct Vec<1, DT> {
   typedef float T;
-  static __device__ __forceinline__ T load(const float* p) { return *p; }
-  static __device__ __forceinline__ void store(float* p, T v) { *p = v; }
+  typedef typename Elem<DT>::S S;
+  static __device__ __forceinline__ T load(const S* p) { return Elem<DT>::load1(p); }
+  static __device__ __forceinline__ void store(S* p, T v) { Elem<DT>::store1(p, v); }
   static __device__ __forceinline__ T zero() { return 0.f; }
   static __device__ __forceinline__ float dot(T a, T b) { return a * b; }
   static __device__ __forceinline__ T shfl_xor(T v, int m) { return __shfl_xor(v, m, 64); }
@@ -72,9 +120,9 @@ __device__ __forceinline__ float group_reduce_sum(float v) {
   return group_sum<G>(v);
 }
 
-template <typename I, int VEC, int G, int U>
-__global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I> a) {
-  typedef Vec<VEC> V;
+template <typename I, int DT, int VEC, int G, int U>
+__global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I, DT> a) {
+  typedef Vec<VEC, DT> V;
   typedef typename V::T T;
   constexpr int EPW = kWave / G;  // edges per wave-wide load
   const Task t = decode_task(a.plan, a.row_ptr, global_wave());
@@ -144,15 +192,16 @@ __global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I> a) {
   for (int m = G; m < kWave; m <<= 1) acc += V::shfl_xor(acc, m);
   if (g != 0 || !active) return;
   if (t.kind == kTaskChunk)
-    V::store(a.partial + static_cast<int64_t>(t.slot) * F + fo, acc);
+    Vec<VEC, TGX_DTYPE_F32>::store(a.partial + static_cast<int64_t>(t.slot) * F + fo, acc);
   else
     V::store(a.out + static_cast<int64_t>(t.row) * F + fo, acc);
 }
 
 // Combine split-row chunk partials in chunk order (deterministic).
-__global__ __launch_bounds__(kTaskBlock) void sum_merge_kernel(PlanView plan,
-                                                               const float* __restrict__ partial,
-                                                               float* __restrict__ out, int64_t F) {
+template <int DT>
+__global__ __launch_bounds__(kTaskBlock) void sum_merge_kernel(
+    PlanView plan, const float* __restrict__ partial, typename Elem<DT>::S* __restrict__ out,
+    int64_t F) {
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
   const int row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
@@ -160,42 +209,42 @@ __global__ __launch_bounds__(kTaskBlock) void sum_merge_kernel(PlanView plan,
   for (int64_t f = lane_id(); f < F; f += kWave) {
     float s = 0.f;
     for (int c = c0; c < c1; ++c) s += partial[static_cast<int64_t>(c) * F + f];
-    out[static_cast<int64_t>(row) * F + f] = s;
+    Elem<DT>::store1(out + static_cast<int64_t>(row) * F + f, s);
   }
 }
 
-template <typename I, int VEC, int G>
-void launch_sum(const SumArgs<I>& a, int64_t ftiles, hipStream_t s) {
+template <typename I, int DT, int VEC, int G>
+void launch_sum(const SumArgs<I, DT>& a, int64_t ftiles, hipStream_t s) {
   const int64_t waves = plan_waves(a.plan);
   dim3 grid(static_cast<unsigned>(ceil_div(waves, kWavesPerBlock)), static_cast<unsigned>(ftiles));
   constexpr int U = (kWave / G) >= 16 ? 1 : (16 / (kWave / G) < 8 ? 16 / (kWave / G) : 8);
-  sum_rows_kernel<I, VEC, G, U><<<grid, kTaskBlock, 0, s>>>(a);
+  sum_rows_kernel<I, DT, VEC, G, U><<<grid, kTaskBlock, 0, s>>>(a);
 }
 
-template <typename I>
-int sum_dispatch(const SumArgs<I>& a, hipStream_t s) {
+template <typename I, int DT>
+int sum_dispatch(const SumArgs<I, DT>& a, hipStream_t s) {
   const int64_t F = a.F;
   if (F % 4 == 0) {
     const int64_t lanes = F / 4;
-    if (lanes <= 1) launch_sum<I, 4, 1>(a, 1, s);
-    else if (lanes <= 2) launch_sum<I, 4, 2>(a, 1, s);
-    else if (lanes <= 4) launch_sum<I, 4, 4>(a, 1, s);
-    else if (lanes <= 8) launch_sum<I, 4, 8>(a, 1, s);
-    else if (lanes <= 16) launch_sum<I, 4, 16>(a, 1, s);
-    else if (lanes <= 32) launch_sum<I, 4, 32>(a, 1, s);
-    else launch_sum<I, 4, 64>(a, ceil_div(lanes, 64), s);
+    if (lanes <= 1) launch_sum<I, DT, 4, 1>(a, 1, s);
+    else if (lanes <= 2) launch_sum<I, DT, 4, 2>(a, 1, s);
+    else if (lanes <= 4) launch_sum<I, DT, 4, 4>(a, 1, s);
+    else if (lanes <= 8) launch_sum<I, DT, 4, 8>(a, 1, s);
+    else if (lanes <= 16) launch_sum<I, DT, 4, 16>(a, 1, s);
+    else if (lanes <= 32) launch_sum<I, DT, 4, 32>(a, 1, s);
+    else launch_sum<I, DT, 4, 64>(a, ceil_div(lanes, 64), s);
   } else {
-    if (F <= 1) launch_sum<I, 1, 1>(a, 1, s);
-    else if (F <= 2) launch_sum<I, 1, 2>(a, 1, s);
-    else if (F <= 4) launch_sum<I, 1, 4>(a, 1, s);
-    else if (F <= 8) launch_sum<I, 1, 8>(a, 1, s);
-    else if (F <= 16) launch_sum<I, 1, 16>(a, 1, s);
-    else if (F <= 32) launch_sum<I, 1, 32>(a, 1, s);
-    else launch_sum<I, 1, 64>(a, ceil_div(F, 64), s);
+    if (F <= 1) launch_sum<I, DT, 1, 1>(a, 1, s);
+    else if (F <= 2) launch_sum<I, DT, 1, 2>(a, 1, s);
+    else if (F <= 4) launch_sum<I, DT, 1, 4>(a, 1, s);
+    else if (F <= 8) launch_sum<I, DT, 1, 8>(a, 1, s);
+    else if (F <= 16) launch_sum<I, DT, 1, 16>(a, 1, s);
+    else if (F <= 32) launch_sum<I, DT, 1, 32>(a, 1, s);
+    else launch_sum<I, DT, 1, 64>(a, ceil_div(F, 64), s);
   }
   TGX_LAUNCHED("sum_rows_kernel");
   if (a.plan.n_split > 0) {
-    sum_merge_kernel<<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+    sum_merge_kernel<DT><<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
         a.plan, a.partial, a.out, F);
     TGX_LAUNCHED("sum_merge_kernel");
   }
@@ -204,21 +253,46 @@ int sum_dispatch(const SumArgs<I>& a, hipStream_t s) {
 
 // dw for feature widths that span several tiles: one wave per edge group of
 // the transposed CSR row, full-width dot product.
-template <typename I>
+template <int DT>
 __global__ __launch_bounds__(kTaskBlock) void sum_dw_wide_kernel(
     const int32_t* __restrict__ row_ptr_t, const int32_t* __restrict__ col_t,
-    const int32_t* __restrict__ perm, const float* __restrict__ x,
-    const float* __restrict__ dout, float* __restrict__ dw, int64_t n_src, int64_t F) {
+    const int32_t* __restrict__ perm, const typename Elem<DT>::S* __restrict__ x,
+    const typename Elem<DT>::S* __restrict__ dout, float* __restrict__ dw, int64_t n_src,
+    int64_t F) {
   const int64_t j = global_wave();
   if (j >= n_src) return;
   const int64_t b = row_ptr_t[j], e = row_ptr_t[j + 1];
   for (int64_t k = b; k < e; ++k) {
     const int64_t i = col_t[k];
     float s = 0.f;
-    for (int64_t f = lane_id(); f < F; f += kWave) s += dout[i * F + f] * x[j * F + f];
+    for (int64_t f = lane_id(); f < F; f += kWave)
+      s += Elem<DT>::load1(dout + i * F + f) * Elem<DT>::load1(x + j * F + f);
     s = group_sum<64>(s);
     if (lane_id() == 0) dw[perm[k]] = s;
   }
+}
+
+template <int V>
+struct DtConst {
+  static constexpr int value = V;
+};
+template <typename T>
+struct IdxType {
+  typedef T type;
+};
+
+// Calls f(DtConst<dtype>, IdxType<index type>) for a checked dtype code and
+// index width.
+template <typename F>
+int with_types(int dtype, int idx_bits, F f) {
+  if (dtype == TGX_DTYPE_BF16)
+    return idx_bits == 32 ? f(DtConst<TGX_DTYPE_BF16>{}, IdxType<int32_t>{})
+                          : f(DtConst<TGX_DTYPE_BF16>{}, IdxType<int64_t>{});
+  if (dtype == TGX_DTYPE_F16)
+    return idx_bits == 32 ? f(DtConst<TGX_DTYPE_F16>{}, IdxType<int32_t>{})
+                          : f(DtConst<TGX_DTYPE_F16>{}, IdxType<int64_t>{});
+  return idx_bits == 32 ? f(DtConst<TGX_DTYPE_F32>{}, IdxType<int32_t>{})
+                        : f(DtConst<TGX_DTYPE_F32>{}, IdxType<int64_t>{});
 }
 
 }  // namespace
@@ -236,11 +310,15 @@ extern "C" int tgx_partial_bytes(const tgx_row_plan* plan, int64_t state_floats,
 }
 
 extern "C" int tgx_csr_sum_fwd(const void* row_ptr, const void* col, int idx_bits,
-                               const tgx_row_plan* plan, const float* x, const float* w,
-                               float* out, int64_t n_dst, int64_t n_src, int64_t F,
+                               const tgx_row_plan* plan, const void* x, const float* w,
+                               void* out, int64_t n_dst, int64_t n_src, int64_t F, int dtype,
                                float* partial, void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(F > 0 && n_dst >= 0 && n_src >= 0, "bad sizes");
+  if (dtype != TGX_DTYPE_F32 && dtype != TGX_DTYPE_BF16 && dtype != TGX_DTYPE_F16) {
+    set_error("sum supports fp32, bf16 and fp16 features (dtype code %d)", dtype);
+    return TGX_UNSUPPORTED;
+  }
   int st = check_plan(plan, n_dst);
   if (st != TGX_OK) return st;
   if (n_dst == 0) return TGX_OK;
@@ -250,22 +328,28 @@ extern "C" int tgx_csr_sum_fwd(const void* row_ptr, const void* col, int idx_bit
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("csr_sum_fwd", s);
-  if (idx_bits == 32) {
-    SumArgs<int32_t> a{static_cast<const int32_t*>(row_ptr), static_cast<const int32_t*>(col),
-                       plan_view(*plan), x, w, nullptr, out, partial, nullptr, nullptr, F};
+  auto run = [&](auto dt, auto idx) -> int {
+    constexpr int DT = decltype(dt)::value;
+    typedef typename decltype(idx)::type I;
+    typedef typename Elem<DT>::S S;
+    SumArgs<I, DT> a{static_cast<const I*>(row_ptr), static_cast<const I*>(col),
+                     plan_view(*plan), static_cast<const S*>(x), w, nullptr,
+                     static_cast<S*>(out), partial, nullptr, nullptr, F};
     return sum_dispatch(a, s);
-  }
-  SumArgs<int64_t> a{static_cast<const int64_t*>(row_ptr), static_cast<const int64_t*>(col),
-                     plan_view(*plan), x, w, nullptr, out, partial, nullptr, nullptr, F};
-  return sum_dispatch(a, s);
+  };
+  return with_types(dtype, idx_bits, run);
 }
 
 extern "C" int tgx_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_t,
                                const int32_t* perm, const tgx_row_plan* plan_t,
-                               const float* x, const float* w, const float* dout,
-                               float* dx, float* dw, int64_t n_dst, int64_t n_src,
-                               int64_t F, float* partial, void* stream) {
+                               const void* x, const float* w, const void* dout, void* dx,
+                               float* dw, int64_t n_dst, int64_t n_src, int64_t F, int dtype,
+                               float* partial, void* stream) {
   TGX_REQUIRE(F > 0 && n_dst >= 0 && n_src >= 0, "bad sizes");
+  if (dtype != TGX_DTYPE_F32 && dtype != TGX_DTYPE_BF16 && dtype != TGX_DTYPE_F16) {
+    set_error("sum supports fp32, bf16 and fp16 features (dtype code %d)", dtype);
+    return TGX_UNSUPPORTED;
+  }
   int st = check_plan(plan_t, n_src);
   if (st != TGX_OK) return st;
   if (n_src == 0) return TGX_OK;
@@ -276,17 +360,25 @@ extern "C" int tgx_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_t,
   hipStream_t s = as_stream(stream);
   const bool single_tile = (F % 4 == 0) ? (F / 4 <= 64) : (F <= 64);
   TGX_PROFILE("csr_sum_bwd", s);
-  if (dx) {
-    SumArgs<int32_t> a{row_ptr_t, col_t, plan_view(*plan_t), dout, w, perm, dx, partial,
-                       (dw && single_tile) ? x : nullptr, (dw && single_tile) ? dw : nullptr,
-                       F};
-    st = sum_dispatch(a, s);
-    if (st != TGX_OK) return st;
-  }
-  if (dw && (!dx || !single_tile)) {
-    sum_dw_wide_kernel<int32_t><<<ceil_div(n_src, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        row_ptr_t, col_t, perm, x, dout, dw, n_src, F);
-    TGX_LAUNCHED("sum_dw_wide_kernel");
-  }
-  return TGX_OK;
+  auto run = [&](auto dt, auto) -> int {
+    constexpr int DT = decltype(dt)::value;
+    typedef typename Elem<DT>::S S;
+    const S* xs = static_cast<const S*>(x);
+    const S* gs = static_cast<const S*>(dout);
+    if (dx) {
+      SumArgs<int32_t, DT> a{row_ptr_t, col_t, plan_view(*plan_t), gs, w, perm,
+                             static_cast<S*>(dx), partial,
+                             (dw && single_tile) ? xs : nullptr,
+                             (dw && single_tile) ? dw : nullptr, F};
+      const int r = sum_dispatch(a, s);
+      if (r != TGX_OK) return r;
+    }
+    if (dw && (!dx || !single_tile)) {
+      sum_dw_wide_kernel<DT><<<ceil_div(n_src, kWavesPerBlock), kTaskBlock, 0, s>>>(
+          row_ptr_t, col_t, perm, xs, gs, dw, n_src, F);
+      TGX_LAUNCHED("sum_dw_wide_kernel");
+    }
+    return TGX_OK;
+  };
+  return with_types(dtype, 32, run);
 }

@@ -75,9 +75,9 @@ _SIGNATURES: dict[str, list] = {
                                    P(c_i64), P(c_i64)],
     "tgx_partial_bytes": [P(RowPlan), c_i64, P(c_size)],
     "tgx_csr_sum_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64,
-                        c_i64, c_vp, c_vp],
+                        c_i64, c_int, c_vp, c_vp],
     "tgx_csr_sum_bwd": [c_vp, c_vp, c_vp, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_vp,
-                        c_i64, c_i64, c_i64, c_vp, c_vp],
+                        c_i64, c_i64, c_i64, c_int, c_vp, c_vp],
     "tgx_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
                     c_i64, c_int, c_int, c_vp, c_vp],
     "tgx_gat_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, P(c_size)],
@@ -116,9 +116,9 @@ _SIGNATURES: dict[str, list] = {
     "tgx_cpu_plan_degree_bins": [c_vp, c_int, c_i64, P(c_i64), c_int, c_vp, P(c_i64)],
     "tgx_cpu_plan_split_chunks": [c_vp, c_int, c_vp, c_i64, ctypes.c_int32, c_vp, P(c_i64)],
     "tgx_cpu_csr_sum_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64,
-                            c_i64],
+                            c_i64, c_int],
     "tgx_cpu_csr_sum_bwd": [c_vp, c_vp, c_vp, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
-                            c_i64, c_i64],
+                            c_i64, c_i64, c_int],
     "tgx_cpu_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
                         c_i64, c_int, c_int],
     "tgx_cpu_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, P(RowPlan),
@@ -206,6 +206,17 @@ def stream_of(tensor) -> int:
     if index is None:
         index = torch.cuda.current_device()
     return torch._C._cuda_getCurrentRawStream(index)
+
+
+DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
+
+
+def dtype_code(tensor) -> int:
+    """TGX_DTYPE_* code of a bf16, fp16 or fp32 tensor."""
+    import torch
+
+    return {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16,
+            torch.float32: DTYPE_F32}[tensor.dtype]
 
 
 def idx_bits(tensor) -> int:

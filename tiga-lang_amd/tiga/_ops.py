@@ -37,8 +37,15 @@ def _on_graph_device(graph: Graph, *tensors) -> None:
             raise ValueError(f"operand on {t.device} for a graph on {device}")
 
 
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous with a 16-byte aligned start (the kernels' vector loads)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 class CsrSumFunction(torch.autograd.Function):
-    """out[i] = sum_e w[e] * x[col[e]]  (w optional), fp32."""
+    """out[i] = sum_e w[e] * x[col[e]]  (w optional): x fp32, bf16 or fp16
+    (out, dout and dx of the same type), w fp32; fp32 products and sums."""
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, w: torch.Tensor | None, graph: Graph):
@@ -49,7 +56,7 @@ class CsrSumFunction(torch.autograd.Function):
         F = 1
         for d in feat_shape:
             F *= d
-        xc = x.contiguous()
+        xc = _aligned(x)
         wc = None if w is None else w.reshape(-1).contiguous()
         out = torch.empty((n_dst, *feat_shape), dtype=x.dtype, device=x.device)
         if n_dst and F:
@@ -57,7 +64,8 @@ class CsrSumFunction(torch.autograd.Function):
             partial = _partial(plan, F, x.device)
             _native.call("tgx_csr_sum_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
                          _native.idx_bits(row_ptr), plan.ref, xc.data_ptr(), _p(wc),
-                         out.data_ptr(), n_dst, n_src, F, _p(partial), _native.stream_of(x))
+                         out.data_ptr(), n_dst, n_src, F, _native.dtype_code(xc), _p(partial),
+                         _native.stream_of(x))
         ctx.graph = graph
         ctx.F = F
         ctx.w_shape = None if w is None else w.shape
@@ -74,16 +82,16 @@ class CsrSumFunction(torch.autograd.Function):
             return None, None, None
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
         E = graph.num_edges
-        dout = dout.contiguous()
+        dout = _aligned(dout.to(xc.dtype))
         dx = torch.empty_like(xc) if need_dx else None
-        dw = torch.empty(E, dtype=xc.dtype, device=xc.device) if need_dw else None
+        dw = torch.empty(E, dtype=torch.float32, device=xc.device) if need_dw else None
         if n_src and ctx.F and (E or need_dx):
             t = graph._transposed()
             partial = _partial(t.plan, ctx.F, xc.device) if need_dx else None
             _native.call("tgx_csr_sum_bwd", t.row_ptr_t.data_ptr(), t.col_t.data_ptr(),
                          t.perm.data_ptr(), t.plan.ref, xc.data_ptr(), _p(wc),
-                         dout.data_ptr(), _p(dx), _p(dw), n_dst, n_src, ctx.F, _p(partial),
-                         _native.stream_of(xc))
+                         dout.data_ptr(), _p(dx), _p(dw), n_dst, n_src, ctx.F,
+                         _native.dtype_code(xc), _p(partial), _native.stream_of(xc))
         if dw is not None:
             dw = dw.reshape(ctx.w_shape)
         return dx, dw, None
@@ -438,7 +446,7 @@ def _reduce_rows(graph: Graph, x: torch.Tensor) -> torch.Tensor:
         partial = _partial(plan, F, x.device)
         _native.call("tgx_csr_sum_fwd", row_ptr.data_ptr(), None,
                      _native.idx_bits(row_ptr), plan.ref, x.data_ptr(), None, out.data_ptr(),
-                     n_dst, E, F, _p(partial), _native.stream_of(x))
+                     n_dst, E, F, _native.DTYPE_F32, _p(partial), _native.stream_of(x))
     return out
 
 
@@ -452,7 +460,7 @@ def _reduce_rows_transposed(graph: Graph, x: torch.Tensor) -> torch.Tensor:
         partial = _partial(t.plan, F, x.device)
         _native.call("tgx_csr_sum_fwd", t.row_ptr_t.data_ptr(), t.perm.data_ptr(), 32,
                      t.plan.ref, x.data_ptr(), None, out.data_ptr(), n_src, E, F,
-                     _p(partial), _native.stream_of(x))
+                     _native.DTYPE_F32, _p(partial), _native.stream_of(x))
     return out
 
 

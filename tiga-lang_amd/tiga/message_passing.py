@@ -434,27 +434,38 @@ class MessagePassing(Kernel):
         if pat.src_field not in src:
             return None
         x = src[pat.src_field]
-        if x.dtype != torch.float32:
+        floats = (torch.float32, torch.bfloat16, torch.float16)
+        if x.dtype not in floats:
             return None
+        out_dtype = x.dtype
         operands = [("src", pat.src_field)]
         if pat.edge_field is not None:
             w = edge.get(pat.edge_field)
             if w is None:
                 return None
             E = graph.num_edges
-            if tuple(w.shape) not in ((E,), (E, 1)) or w.dtype != torch.float32:
+            if tuple(w.shape) not in ((E,), (E, 1)) or w.dtype not in floats:
                 return None
             if x.ndim == 1 and w.ndim == 2:
                 return None
+            # The message w * x has Torch's promoted dtype (bf16 * fp32 is
+            # fp32), as in the reference's eager reduce_sum.
+            out_dtype = torch.promote_types(x.dtype, w.dtype)
             operands.append(("edge", pat.edge_field))
         _native.lib()
 
         def run(x, w=None):
-            return _ops.CsrSumFunction.apply(x, w, graph)
+            # The kernels read x in the output dtype and fp32 weights; both
+            # conversions are differentiable Torch ops (no-ops when the
+            # dtypes already match).
+            xk = x.to(out_dtype)
+            wk = None if w is None else w.to(torch.float32)
+            return _ops.CsrSumFunction.apply(xk, wk, graph)
 
+        kind = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}[out_dtype]
         describe = lambda: self._variant(
             graph, "weighted-sum", ("tgx_csr_sum_fwd", "tgx_csr_sum_bwd"),
-            "degree-binned rows -> wave gather-FMA (fp32)")
+            f"degree-binned rows -> wave gather-FMA ({kind} features, fp32 sums)")
         return _Launch(graph, tuple(operands), run, describe)
 
     def _plan_gat(self, gat, graph, src, dst, params) -> _Launch | None:
