@@ -58,8 +58,8 @@ def parse():
     ap.add_argument("--config", default="all",
                     choices=["all", "c1", "c2", "c3", "c4", "c5", "dense", "dense-causal",
                              "dense-pruned", "nn"],
-                    help="all (default): C2 as the headline line with C1, C3, C4 and C5 "
-                         "under its 'configs' key")
+                    help="all (default): C2 as the headline line with C1, C3, C4, C5, "
+                         "nn and the dense attention shapes under its 'configs' key")
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true",
@@ -1013,8 +1013,11 @@ def _release_gpu_memory():
 def run_all(args):
     """Every BASELINE configuration in one process: C2 (the headline) as the
     top-level line, C1, C3, C4 and C5 under "configs", each with its own
-    step time, roofline of its dominant kernel and CPU baseline.  Progress
-    goes to stderr; stdout gets the one JSON line."""
+    step time, roofline of its dominant kernel and CPU baseline; then the
+    reference's own benchmark shapes this path also covers (the nn-scored
+    GAT step, with its CPU baseline, and the dense / triangular / pruned
+    attention forwards).  Progress goes to stderr; stdout gets the one JSON
+    line."""
     t_all = time.perf_counter()
 
     def progress(name, t0):
@@ -1031,6 +1034,13 @@ def run_all(args):
         t0 = time.perf_counter()
         got = fn(args)
         configs.update(got if name == "c3+c4" else {name: got})
+        progress(name, t0)
+    for name in ("nn", "dense", "dense-causal", "dense-pruned"):
+        _release_gpu_memory()
+        t0 = time.perf_counter()
+        sub_args = argparse.Namespace(**vars(args))
+        sub_args.config = name
+        configs[name] = run_nn(sub_args) if name == "nn" else run_dense(sub_args)
         progress(name, t0)
     for sub in configs.values():
         if isinstance(sub.get("cpu_baseline"), dict):

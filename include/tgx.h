@@ -236,6 +236,17 @@ int tgx_csr_sum_bwd(const int32_t* row_ptr_t_dev, const int32_t* col_t_dev,
                     int64_t n_dst, int64_t n_src, int64_t F, int dtype,
                     float* partial_dev, void* stream);
 
+/* Per-edge dot products in edge order over the destination-row CSR:
+ *   dw[e] = <dout[row(e), :], x[col[e], :]>,  e = 0 .. n_edges-1
+ * (the weight gradient of the weighted sum, written contiguously; the
+ * reference's Torch replay, message_passing.py:378-409).  x [n_src, F] and
+ * dout [n_dst, F] of element type dtype, dw fp32.  F <= 32 (wider rows:
+ * tgx_csr_sum_bwd's dw output); others return TGX_UNSUPPORTED. */
+int tgx_csr_edge_dot(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                     const tgx_row_plan* plan, const void* x_dev, const void* dout_dev,
+                     float* dw_dev, int64_t n_dst, int64_t n_src, int64_t F, int dtype,
+                     void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* GAT additive edge attention (fp32)                                        */
 /*   z_e = a_src . h[j] + a_dst . h[i]   per head,  s_e = LeakyReLU(z_e)     */

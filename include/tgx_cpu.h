@@ -75,6 +75,11 @@ int tgx_cpu_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_t, const in
                         const void* dout, void* dx, float* dw, int64_t n_dst, int64_t n_src,
                         int64_t F, int dtype);
 
+/* Twin of tgx_csr_edge_dot (F <= 32). */
+int tgx_cpu_csr_edge_dot(const void* row_ptr, const void* col, int idx_bits,
+                         const tgx_row_plan* plan, const void* x, const void* dout, float* dw,
+                         int64_t n_dst, int64_t n_src, int64_t F, int dtype);
+
 /* Twin of tgx_gat_fwd (eager evaluation of the additive edge function,
  * interop/torch/message_passing.py:2848-2894, reducer_oracle.py:60-137).
  * Same node_state layout [N, H, 4]. */

@@ -183,6 +183,21 @@ def test_sum_twin_with_16_bit_features(dtype, F):
     assert rel(dw, e_dw) <= 1e-5     # fp32 dot products of exact 16-bit inputs
 
 
+@pytest.mark.parametrize("F", [1, 8, 32])
+def test_edge_dot_twin_against_oracle(F):
+    rp, col, g = _graph(70 + F, 1800, 64)
+    rng = np.random.default_rng(F)
+    x = rng.standard_normal((1800, F)).astype(np.float32)
+    dout = rng.standard_normal((1800, F)).astype(np.float32)
+    dw = np.empty(g.E, np.float32)
+    call("tgx_cpu_csr_edge_dot", p(g.rp), p(g.col), 64, g.plan.ref, p(x), p(dout), p(dw), 1800,
+         1800, F, F32)
+    assert rel(dw, ref.sum_bwd(rp, col, x, None, dout)[1]) <= 1e-5
+    with pytest.raises(NotImplementedError, match="F <= 32"):
+        call("tgx_cpu_csr_edge_dot", p(g.rp), p(g.col), 64, g.plan.ref, p(x), p(dout), p(dw),
+             1800, 1800, 33, F32)
+
+
 def test_sum_twin_of_an_edge_field_per_row():
     rp, col, g = _graph(9, 1500, 64)
     x = np.random.default_rng(9).standard_normal((g.E, 5)).astype(np.float32)

@@ -560,6 +560,47 @@ extern "C" int tgx_cpu_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_
   });
 }
 
+extern "C" int tgx_cpu_csr_edge_dot(const void* row_ptr, const void* col, int idx_bits,
+                                    const tgx_row_plan* plan, const void* x, const void* dout,
+                                    float* dw, int64_t n_dst, int64_t n_src, int64_t F,
+                                    int dtype) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(F > 0 && n_dst >= 0 && n_src >= 0, "bad sizes");
+  int st = check_sum_dtype(dtype);
+  if (st != TGX_OK) return st;
+  if (F > 32) {
+    set_error("tgx_csr_edge_dot covers F <= 32 (got %lld); wider rows take the dw output "
+              "of tgx_csr_sum_bwd", static_cast<long long>(F));
+    return TGX_UNSUPPORTED;
+  }
+  st = check_plan(plan, n_dst);
+  if (st != TGX_OK) return st;
+  if (n_dst == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && col && x && dout && dw, "null pointer");
+  return guarded([&]() -> int {
+    const Idx rp{row_ptr, idx_bits}, c{col, idx_bits};
+    const Feat ft{dtype};
+    int s = check_csr(rp, &c, n_dst, n_src, nullptr);
+    if (s != TGX_OK) return s;
+    s = check_plan_rows(plan, rp, n_dst);
+    if (s != TGX_OK) return s;
+    auto range = [&](int64_t i, int64_t e0, int64_t e1) {
+      for (int64_t e = e0; e < e1; ++e) {
+        float d = 0.f;
+        for (int64_t f = 0; f < F; ++f) d += ft.load(dout, i * F + f) * ft.load(x, c[e] * F + f);
+        dw[e] = d;
+      }
+    };
+    walk_plan(
+        *plan, rp, [&](int64_t i, int64_t e0, int64_t e1) { range(i, e0, e1); },
+        [&](int64_t i, const std::vector<std::pair<int64_t, int64_t>>& chunks) {
+          for (const auto& ch : chunks) range(i, ch.first, ch.second);
+        },
+        [](int64_t) {});
+    return TGX_OK;
+  });
+}
+
 // ---- GAT additive attention -------------------------------------------------------
 
 extern "C" int tgx_cpu_gat_fwd(const void* row_ptr, const void* col, int idx_bits,

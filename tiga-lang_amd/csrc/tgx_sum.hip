@@ -120,12 +120,12 @@ __device__ __forceinline__ float group_reduce_sum(float v) {
   return group_sum<G>(v);
 }
 
+// One whole-wave task (a row, a split-row chunk or a group of empty rows).
 template <typename I, int DT, int VEC, int G, int U>
-__global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I, DT> a) {
+__device__ __forceinline__ void sum_task(const SumArgs<I, DT>& a, const Task& t) {
   typedef Vec<VEC, DT> V;
   typedef typename V::T T;
   constexpr int EPW = kWave / G;  // edges per wave-wide load
-  const Task t = decode_task(a.plan, a.row_ptr, global_wave());
   if (t.kind == kTaskNone) return;
   const int lane = lane_id();
   const int g = lane / G;
@@ -137,7 +137,8 @@ __global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I, DT> a) 
   if (t.kind == kTaskEmpty) {
     for (int k = 0; k < t.n_empty; ++k) {
       const int row = uniform(a.plan.rows[t.empty0 + k]);
-      if (g == 0 && active) V::store(a.out + static_cast<int64_t>(row) * F + fo, V::zero());
+      if (g == 0 && active && a.out)
+        V::store(a.out + static_cast<int64_t>(row) * F + fo, V::zero());
     }
     return;
   }
@@ -190,11 +191,106 @@ __global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I, DT> a) 
   // Fold the EPW edge groups (lanes with equal c).
 #pragma unroll
   for (int m = G; m < kWave; m <<= 1) acc += V::shfl_xor(acc, m);
-  if (g != 0 || !active) return;
+  // A null out: only the per-edge dot products (dw) are wanted.
+  if (g != 0 || !active || !a.out) return;
   if (t.kind == kTaskChunk)
     Vec<VEC, TGX_DTYPE_F32>::store(a.partial + static_cast<int64_t>(t.slot) * F + fo, acc);
   else
     V::store(a.out + static_cast<int64_t>(t.row) * F + fo, acc);
+}
+
+template <typename I, int DT, int VEC, int G, int U>
+__global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I, DT> a) {
+  sum_task<I, DT, VEC, G, U>(a, decode_task(a.plan, a.row_ptr, global_wave()));
+}
+
+// Narrow rows (G <= 8 lanes per edge): two rows of the wave bin per wave, one
+// per 32-lane half, so a wave's fixed cost (task decode, the dependent
+// row_ptr -> col -> gather chain) covers two rows.  Each half keeps 32 edges
+// in flight (U = G loads of 32 / G edges).  The task list is
+//   [split-row chunks | row pairs | empty-row groups];
+// chunks and empty groups run as whole-wave tasks.
+template <typename I, int DT, int VEC, int G, int UC>
+__global__ __launch_bounds__(kTaskBlock) void sum_pairs_kernel(SumArgs<I, DT> a) {
+  typedef Vec<VEC, DT> V;
+  typedef typename V::T T;
+  constexpr int EPH = 32 / G;   // edges per half-wave load
+  constexpr int U = G;          // loads in flight: 32 edges per half
+  const PlanView& p = a.plan;
+  const int64_t w = global_wave();
+  const int64_t n_pairs = (p.n_wave + 1) / 2;
+  if (w < p.n_chunks) {
+    sum_task<I, DT, VEC, G, UC>(a, decode_task(p, a.row_ptr, w));
+    return;
+  }
+  const int64_t pw = w - p.n_chunks;
+  if (pw >= n_pairs) {
+    sum_task<I, DT, VEC, G, UC>(a, decode_task(p, a.row_ptr, p.n_chunks + p.n_wave + (pw - n_pairs)));
+    return;
+  }
+  const int lane = lane_id();
+  const int half = lane >> 5, hl = lane & 31;
+  const int g = hl / G, c = hl % G;
+  const int64_t F = a.F;
+  const int64_t fo = c * VEC;   // G * VEC <= F's tile: one feature tile
+  const bool active = fo < F;
+  const int64_t k = 2 * pw + half;   // this half's position in the wave bin
+  const bool has = k < p.n_wave;
+  const int row = has ? p.rows[p.n_empty + k] : 0;
+  const int64_t e0 = has ? static_cast<int64_t>(a.row_ptr[row]) : 0;
+  const int len = has ? static_cast<int>(static_cast<int64_t>(a.row_ptr[row + 1]) - e0) : 0;
+  // Both halves loop to the longer row (wave-uniform bounds keep every
+  // shuffle's source lanes active); a half masks its own tail.
+  const int len_max = max(len, __shfl_xor(len, 32, 64));
+  T self = V::zero();
+  const bool want_dw = a.self_x != nullptr;
+  if (want_dw && active && has) self = V::load(a.self_x + static_cast<int64_t>(row) * F + fo);
+  T acc = V::zero();
+  for (int base = 0; base < len_max; base += 32) {
+    const int n = min(max(len - base, 0), 32);          // this half's edges
+    const int n_max = min(len_max - base, 32);           // wave-uniform
+    int my_col = 0, my_widx = 0;
+    float my_w = 0.f;
+    if (hl < n) {
+      const int64_t e = e0 + base + hl;
+      my_col = a.col ? static_cast<int>(a.col[e]) : static_cast<int>(e);
+      my_widx = a.wperm ? a.wperm[e] : static_cast<int>(e);
+      my_w = a.w ? a.w[my_widx] : 1.f;
+    }
+    for (int kk = 0; kk < n_max; kk += EPH * U) {
+      T v[U];
+      float wt[U];
+      int slot[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        slot[u] = kk + u * EPH + g;
+        const int src = 32 * half + (slot[u] < n ? slot[u] : 0);
+        const int j = __shfl(my_col, src, 64);
+        wt[u] = __shfl(my_w, src, 64);
+        v[u] = (slot[u] < n && active) ? V::load(a.x + static_cast<int64_t>(j) * F + fo)
+                                       : V::zero();
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (slot[u] < n) acc += wt[u] * v[u];
+      }
+      if (want_dw) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float d = group_reduce_sum<G>(V::dot(v[u], self));
+          const int src = 32 * half + (slot[u] < n ? slot[u] : 0);
+          const int widx = __shfl(my_widx, src, 64);
+          if (c == 0 && slot[u] < n) a.dw[widx] = d;
+        }
+      }
+    }
+  }
+  // Fold the half's edge groups (lanes with equal c; masks below 32 stay
+  // inside the half).
+#pragma unroll
+  for (int m = G; m < 32; m <<= 1) acc += V::shfl_xor(acc, m);
+  if (g == 0 && active && has && a.out)
+    V::store(a.out + static_cast<int64_t>(row) * F + fo, acc);
 }
 
 // Combine split-row chunk partials in chunk order (deterministic).
@@ -215,10 +311,20 @@ __global__ __launch_bounds__(kTaskBlock) void sum_merge_kernel(
 
 template <typename I, int DT, int VEC, int G>
 void launch_sum(const SumArgs<I, DT>& a, int64_t ftiles, hipStream_t s) {
-  const int64_t waves = plan_waves(a.plan);
-  dim3 grid(static_cast<unsigned>(ceil_div(waves, kWavesPerBlock)), static_cast<unsigned>(ftiles));
   constexpr int U = (kWave / G) >= 16 ? 1 : (16 / (kWave / G) < 8 ? 16 / (kWave / G) : 8);
-  sum_rows_kernel<I, DT, VEC, G, U><<<grid, kTaskBlock, 0, s>>>(a);
+  if constexpr (G <= 8) {
+    // ftiles == 1 here: G * VEC <= 32 covers F.
+    const PlanView& p = a.plan;
+    const int64_t waves = p.n_chunks + (p.n_wave + 1) / 2 +
+                          (p.n_empty + kEmptyPerWave - 1) / kEmptyPerWave;
+    sum_pairs_kernel<I, DT, VEC, G, U>
+        <<<static_cast<unsigned>(ceil_div(waves, kWavesPerBlock)), kTaskBlock, 0, s>>>(a);
+  } else {
+    const int64_t waves = plan_waves(a.plan);
+    dim3 grid(static_cast<unsigned>(ceil_div(waves, kWavesPerBlock)),
+              static_cast<unsigned>(ftiles));
+    sum_rows_kernel<I, DT, VEC, G, U><<<grid, kTaskBlock, 0, s>>>(a);
+  }
 }
 
 template <typename I, int DT>
@@ -243,7 +349,7 @@ int sum_dispatch(const SumArgs<I, DT>& a, hipStream_t s) {
     else launch_sum<I, DT, 1, 64>(a, ceil_div(F, 64), s);
   }
   TGX_LAUNCHED("sum_rows_kernel");
-  if (a.plan.n_split > 0) {
+  if (a.plan.n_split > 0 && a.out) {
     sum_merge_kernel<DT><<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
         a.plan, a.partial, a.out, F);
     TGX_LAUNCHED("sum_merge_kernel");
@@ -381,4 +487,39 @@ extern "C" int tgx_csr_sum_bwd(const int32_t* row_ptr_t, const int32_t* col_t,
     return TGX_OK;
   };
   return with_types(dtype, 32, run);
+}
+
+extern "C" int tgx_csr_edge_dot(const void* row_ptr, const void* col, int idx_bits,
+                                const tgx_row_plan* plan, const void* x, const void* dout,
+                                float* dw, int64_t n_dst, int64_t n_src, int64_t F, int dtype,
+                                void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(F > 0 && n_dst >= 0 && n_src >= 0, "bad sizes");
+  if (dtype != TGX_DTYPE_F32 && dtype != TGX_DTYPE_BF16 && dtype != TGX_DTYPE_F16) {
+    set_error("sum supports fp32, bf16 and fp16 features (dtype code %d)", dtype);
+    return TGX_UNSUPPORTED;
+  }
+  if (F > 32) {
+    set_error("tgx_csr_edge_dot covers F <= 32 (got %lld); wider rows take the dw output "
+              "of tgx_csr_sum_bwd", static_cast<long long>(F));
+    return TGX_UNSUPPORTED;
+  }
+  int st = check_plan(plan, n_dst);
+  if (st != TGX_OK) return st;
+  if (n_dst == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && col && x && dout && dw, "null pointer");
+  hipStream_t s = as_stream(stream);
+  TGX_PROFILE("csr_edge_dot", s);
+  auto run = [&](auto dt, auto idx) -> int {
+    constexpr int DT = decltype(dt)::value;
+    typedef typename decltype(idx)::type I;
+    typedef typename Elem<DT>::S S;
+    // The sum kernel over the CSR with the row's own dout as `self`: it
+    // writes dw[e] = <dout[i], x[col[e]]> in edge order and no sums.
+    SumArgs<I, DT> a{static_cast<const I*>(row_ptr), static_cast<const I*>(col),
+                     plan_view(*plan), static_cast<const S*>(x), nullptr, nullptr, nullptr,
+                     nullptr, static_cast<const S*>(dout), dw, F};
+    return sum_dispatch(a, s);
+  };
+  return with_types(dtype, idx_bits, run);
 }

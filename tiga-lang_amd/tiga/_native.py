@@ -78,6 +78,8 @@ _SIGNATURES: dict[str, list] = {
                         c_i64, c_int, c_vp, c_vp],
     "tgx_csr_sum_bwd": [c_vp, c_vp, c_vp, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_vp,
                         c_i64, c_i64, c_i64, c_int, c_vp, c_vp],
+    "tgx_csr_edge_dot": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
+                         c_int, c_vp],
     "tgx_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
                     c_i64, c_int, c_int, c_vp, c_vp],
     "tgx_gat_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, P(c_size)],
@@ -119,6 +121,8 @@ _SIGNATURES: dict[str, list] = {
                             c_i64, c_int],
     "tgx_cpu_csr_sum_bwd": [c_vp, c_vp, c_vp, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
                             c_i64, c_i64, c_int],
+    "tgx_cpu_csr_edge_dot": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64,
+                             c_i64, c_int],
     "tgx_cpu_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
                         c_i64, c_int, c_int],
     "tgx_cpu_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, P(RowPlan),

@@ -85,13 +85,23 @@ class CsrSumFunction(torch.autograd.Function):
         dout = _aligned(dout.to(xc.dtype))
         dx = torch.empty_like(xc) if need_dx else None
         dw = torch.empty(E, dtype=torch.float32, device=xc.device) if need_dw else None
-        if n_src and ctx.F and (E or need_dx):
+        # Narrow rows (F <= 32): dw in edge order from a pass over the CSR
+        # (contiguous writes) instead of scattered through the transpose.
+        dw_in_csr = dw is not None and ctx.F <= 32 and E > 0
+        if n_src and ctx.F and (need_dx or (E and not dw_in_csr)):
             t = graph._transposed()
             partial = _partial(t.plan, ctx.F, xc.device) if need_dx else None
             _native.call("tgx_csr_sum_bwd", t.row_ptr_t.data_ptr(), t.col_t.data_ptr(),
                          t.perm.data_ptr(), t.plan.ref, xc.data_ptr(), _p(wc),
-                         dout.data_ptr(), _p(dx), _p(dw), n_dst, n_src, ctx.F,
-                         _native.dtype_code(xc), _p(partial), _native.stream_of(xc))
+                         dout.data_ptr(), _p(dx), None if dw_in_csr else _p(dw), n_dst,
+                         n_src, ctx.F, _native.dtype_code(xc), _p(partial),
+                         _native.stream_of(xc))
+        if dw_in_csr:
+            row_ptr, col_idx = graph._kernel_csr()
+            _native.call("tgx_csr_edge_dot", row_ptr.data_ptr(), col_idx.data_ptr(),
+                         _native.idx_bits(row_ptr), graph._row_plan().ref, xc.data_ptr(),
+                         dout.data_ptr(), dw.data_ptr(), n_dst, n_src, ctx.F,
+                         _native.dtype_code(xc), _native.stream_of(xc))
         if dw is not None:
             dw = dw.reshape(ctx.w_shape)
         return dx, dw, None
