@@ -415,7 +415,11 @@ int tgx_attn_bwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
 /*   interop/torch/message_passing.py:2372-2577                             */
 /* ------------------------------------------------------------------------ */
 
-/* Activations between linear layers. */
+/* Component-wise functions between linear layers.  Derivatives follow
+ * Torch's backward (at kinks too).  For log and the powers (sqrt, rsqrt,
+ * square, reciprocal, pow) the padding columns of a layer are not evaluated
+ * (their 0 input would give inf).  Chains that use one of the codes from
+ * TGX_ACT_EXP on run on kernels built for that set, at the same interface. */
 enum {
   TGX_ACT_IDENTITY = 0,
   TGX_ACT_RELU = 1,
@@ -430,7 +434,17 @@ enum {
   TGX_ACT_SELU = 10,
   TGX_ACT_MISH = 11,
   TGX_ACT_HARDSIGMOID = 12,
-  TGX_ACT_HARDSWISH = 13
+  TGX_ACT_HARDSWISH = 13,
+  TGX_ACT_EXP = 14,
+  TGX_ACT_LOG = 15,
+  TGX_ACT_SQRT = 16,
+  TGX_ACT_RSQRT = 17,
+  TGX_ACT_ABS = 18,         /* derivative sign(z), 0 at 0 */
+  TGX_ACT_SIN = 19,
+  TGX_ACT_COS = 20,
+  TGX_ACT_SQUARE = 21,
+  TGX_ACT_RECIPROCAL = 22,  /* act_param / z */
+  TGX_ACT_POW = 23          /* z ** act_param; derivative 0 for exponent 0 */
 };
 
 /* Row of an edge that a score-input segment is gathered from. */

@@ -1,7 +1,10 @@
 """Edge networks on the HIP path: tg.sum() over a tg.nn.trace message (the
 reference's edge-NN tile, compiler/edge_nn_tile.py, message_passing.py:
 2134-2300) and nn-scored attention with the wider activation set and scalar
-arithmetic (compiler/nn_capture.py:17-31).
+arithmetic (compiler/nn_capture.py:17-31): exp, log, sqrt, rsqrt, abs, sin,
+cos, squares, powers and c / x among the functions, scalar maps after them
+folded into the next Linear layer, hidden widths that leave padding columns
+in the kernels' 4-wide blocks.
 
 Checked against Torch float64 autograd of the same module on the gathered
 fields (oracle/eager_torch.nn_message_sum / nn_attention, the reference's
@@ -50,8 +53,43 @@ class Affine(nn.Module):
         return self.b(F.softplus(2.0 - self.a(x) * 0.5, beta=2.0)) / 4.0 + 1.0
 
 
+class ThreeLayer(nn.Module):
+    """Linear a -> f -> Linear b -> g -> Linear c with the component-wise
+    functions of `kind` and scalar arithmetic before and after them."""
+
+    def __init__(self, i, kind, h1, h2, o):
+        super().__init__()
+        self.kind = kind
+        self.a, self.b, self.c = nn.Linear(i, h1), nn.Linear(h1, h2), nn.Linear(h2, o)
+
+    def forward(self, x):
+        if self.kind == "exp-log":
+            h = torch.exp(self.a(x) * 0.5)
+            h = torch.log(self.b(h) * 0.1 + 3.0)
+            return self.c(h * 2.0 - 1.0)
+        if self.kind == "roots":
+            h = torch.sqrt(self.a(x) * 0.3 + 2.0)
+            h = (self.b(h) * 0.5 + 2.0).rsqrt()
+            return self.c(1.0 - 2.0 * h)
+        if self.kind == "trig":
+            h = torch.sin(self.a(x))
+            return self.c(-self.b(h).cos())
+        if self.kind == "powers":
+            h = self.a(x).abs()
+            return self.c(2.0 / (self.b(h) * 0.1 + 3.0))
+        h = self.a(x)
+        h = h * h
+        h = (self.b(h) * 0.1 + 2.0) ** 1.5
+        return self.c(h / 3.0)
+
+
 def nets(i):
     return {
+        "exp-log": ThreeLayer(i, "exp-log", 10, 9, 3),
+        "roots": ThreeLayer(i, "roots", 12, 7, 2),
+        "trig": ThreeLayer(i, "trig", 11, 6, 4),
+        "powers": ThreeLayer(i, "powers", 10, 30, 2),
+        "squares": ThreeLayer(i, "squares", 9, 20, 3),
         "relu-2": nn.Sequential(nn.Linear(i, 16), nn.ReLU(), nn.Linear(16, 8)),
         "mish-selu-3": nn.Sequential(nn.Linear(i, 24), nn.Mish(), nn.Linear(24, 12), nn.SELU(),
                                      nn.Linear(12, 5)),
@@ -104,7 +142,8 @@ def test_edge_network_sum_against_float64_autograd(name, idx):
         assert rel(g, w) <= 3e-5
 
 
-@pytest.mark.parametrize("name", ["mish-selu-3", "hard-3", "relu6-hardtanh", "affine-softplus"])
+@pytest.mark.parametrize("name", ["mish-selu-3", "hard-3", "relu6-hardtanh", "affine-softplus",
+                                  "exp-log", "roots", "trig", "powers", "squares"])
 def test_nn_attention_wider_op_set_against_float64_autograd(name):
     print(f"nn attention {name}", flush=True)
     N = 2000
@@ -115,13 +154,10 @@ def test_nn_attention_wider_op_set_against_float64_autograd(name):
     value = torch.tensor(rng.standard_normal((N, 5)), dtype=torch.float32, device=DEV)
     torch.manual_seed(4)
     body = nets(6)[name]
-    last = [m for m in (body.modules()) if isinstance(m, nn.Linear)][-1]
+    name_last, last = [(n, m) for n, m in body.named_modules() if isinstance(m, nn.Linear)][-1]
     # one-output score network: the same body with its last layer cut to 1
     net = copy.deepcopy(body)
-    if isinstance(net, nn.Sequential):
-        net[-1] = nn.Linear(last.in_features, 1)
-    else:
-        net.b = nn.Linear(last.in_features, 1)
+    setattr(net, name_last, nn.Linear(last.in_features, 1))
     net = net.to(DEV)
     graph = tg.Graph.from_csr(torch.tensor(rp, device=DEV), torch.tensor(col, device=DEV),
                               num_src=N)

@@ -1,0 +1,260 @@
+"""Capture of edge networks (tg.nn.trace) into the kernels' layer chain, on
+the CPU: which modules become a chain of folded Linear layers, and that the
+folded weights and the gradient unfolding reproduce the module itself.
+
+The reference captures the same op set (compiler/nn_capture.py:17-31,
+281-380: Linear, the component-wise functions, scalar arithmetic).  The
+checks run the module in float64 and the captured chain in float64 (each
+activation code evaluated by its Torch function) on random inputs; the
+gradients of the module's own weights and biases come from autograd through
+the module and, for the chain, from autograd at the folded weights mapped
+back by the same routine the HIP path uses (_ops._unfolded_grads).
+"""
+
+import operator
+
+import pytest
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from tiga import _ops
+from tiga.nn import _extract_chain
+
+# Each activation code evaluated in float64 by Torch (the kernels' functions
+# are compared against these through the GPU tests).
+ACT = {
+    "identity": lambda z, p, q: z,
+    "relu": lambda z, p, q: torch.relu(z),
+    "leaky_relu": lambda z, p, q: F.leaky_relu(z, p),
+    "tanh": lambda z, p, q: torch.tanh(z),
+    "sigmoid": lambda z, p, q: torch.sigmoid(z),
+    "silu": lambda z, p, q: F.silu(z),
+    "gelu": lambda z, p, q: F.gelu(z),
+    "elu": lambda z, p, q: F.elu(z, p),
+    "hardtanh": lambda z, p, q: torch.clamp(z, p, q),
+    "softplus": lambda z, p, q: F.softplus(z, p, q),
+    "exp": lambda z, p, q: torch.exp(z),
+    "log": lambda z, p, q: torch.log(z),
+    "sqrt": lambda z, p, q: torch.sqrt(z),
+    "rsqrt": lambda z, p, q: torch.rsqrt(z),
+    "abs": lambda z, p, q: torch.abs(z),
+    "sin": lambda z, p, q: torch.sin(z),
+    "cos": lambda z, p, q: torch.cos(z),
+    "square": lambda z, p, q: z * z,
+    "reciprocal": lambda z, p, q: p / z,
+    "pow": lambda z, p, q: torch.pow(z, p),
+}
+
+
+class ExpLog(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b, self.c = nn.Linear(5, 10), nn.Linear(10, 9), nn.Linear(9, 3)
+
+    def forward(self, x):
+        h = torch.exp(self.a(x) * 0.5)
+        h = torch.log(self.b(h) * 0.1 + 3.0)
+        return self.c(h * 2.0 - 1.0)
+
+
+class Roots(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b, self.c = nn.Linear(5, 12), nn.Linear(12, 7), nn.Linear(7, 2)
+
+    def forward(self, x):
+        h = torch.sqrt(self.a(x) * 0.2 + 2.0)
+        h = (self.b(h) * 0.1 + 1.5).rsqrt()
+        return self.c(0.5 - h)
+
+
+class Trig(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b, self.c = nn.Linear(5, 11), nn.Linear(11, 6), nn.Linear(6, 4)
+
+    def forward(self, x):
+        h = torch.sin(self.a(x))
+        h = self.b(h).cos()
+        return self.c(-h)
+
+
+class Powers(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b, self.c = nn.Linear(5, 10), nn.Linear(10, 10), nn.Linear(10, 2)
+
+    def forward(self, x):
+        h = self.a(x).abs()
+        h = 2.0 / (self.b(h) * 0.1 + 3.0)
+        return self.c(h)
+
+
+class Squares(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b, self.c = nn.Linear(5, 9), nn.Linear(9, 12), nn.Linear(12, 3)
+
+    def forward(self, x):
+        h = self.a(x)
+        h = h * h
+        h = (self.b(h) * 0.1 + 2.0) ** 1.5
+        return self.c(h / 3.0)
+
+
+class Square2(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b = nn.Linear(5, 8), nn.Linear(8, 1)
+
+    def forward(self, x):
+        return self.b(torch.square(self.a(x)) + 1.0) * 2.0
+
+
+NETS = {
+    "exp-log": (ExpLog, [("exp", 0.0), ("log", 0.0), ("identity", 0.0)]),
+    "roots": (Roots, [("sqrt", 0.0), ("rsqrt", 0.0), ("identity", 0.0)]),
+    "trig": (Trig, [("sin", 0.0), ("cos", 0.0), ("identity", 0.0)]),
+    "powers": (Powers, [("abs", 0.0), ("reciprocal", 2.0), ("identity", 0.0)]),
+    "squares": (Squares, [("square", 0.0), ("pow", 1.5), ("identity", 0.0)]),
+    "square-2": (Square2, [("square", 0.0), ("identity", 0.0)]),
+    "sequential": (lambda: nn.Sequential(nn.Linear(5, 8), nn.Softplus(2.0), nn.Linear(8, 8),
+                                         nn.ELU(0.5), nn.Linear(8, 1)),
+                   [("softplus", 2.0), ("elu", 0.5), ("identity", 0.0)]),
+}
+
+
+def run_chain(chain, x, weights):
+    """The captured chain in float64 with the folded weights `weights`
+    ([(W', b' or None)] per layer)."""
+    a = x
+    for layer, (w, b) in zip(chain, weights):
+        z = a @ w.t()
+        if b is not None:
+            z = z + b
+        a = ACT[layer.act](z, layer.param, layer.param2)
+    return a
+
+
+@pytest.mark.parametrize("name", sorted(NETS))
+def test_capture_codes_and_folded_chain_match_the_module(name):
+    make, codes = NETS[name]
+    torch.manual_seed(7)
+    net = make().double()
+    chain = _extract_chain(net)
+    assert [(l.act, l.param) for l in chain] == codes
+    x = torch.randn(64, 5, dtype=torch.float64)
+    params = [t for l in chain for t in (l.linear.weight, l.linear.bias)]
+    folded = [_ops._folded(l, params[2 * i], params[2 * i + 1]) for i, l in enumerate(chain)]
+    expect = net(x)
+    got = run_chain(chain, x, folded)
+    assert torch.isfinite(expect).all()
+    torch.testing.assert_close(got, expect, rtol=1e-12, atol=1e-12)
+
+    # Gradients of the module's own parameters: through the module, and at
+    # the folded weights then unfolded.
+    dout = torch.randn_like(expect)
+    grads = torch.autograd.grad(net(x), params, dout, allow_unused=True)
+    leaves = [(w.clone().requires_grad_(True),
+               None if b is None else b.clone().requires_grad_(True)) for w, b in folded]
+    # A folded bias exists whenever the module's bias does (the shifts only
+    # add to it); a chain layer without one has a zero folded-bias gradient
+    # seed all the same, as the kernels sum it for every layer.
+    flat = [t for w, b in leaves for t in (w, b) if t is not None]
+    dflat = torch.autograd.grad(run_chain(chain, x, leaves), flat, dout)
+    it = iter(dflat)
+    for i, (layer, (w, b)) in enumerate(zip(chain, leaves)):
+        dwf = next(it)
+        if b is not None:
+            dbf = next(it)
+        else:
+            # dz summed over the rows: the gradient a zero bias would get.
+            zb = torch.zeros(w.shape[0], dtype=torch.float64, requires_grad=True)
+            trial = [(lw.detach(), lb.detach() if lb is not None else None)
+                     for lw, lb in leaves]
+            trial[i] = (w.detach(), zb)
+            dbf = torch.autograd.grad(run_chain(chain, x, trial), zb, dout)[0]
+        dW, db = _ops._unfolded_grads(layer, dwf, dbf, True, layer.linear.bias is not None)
+        torch.testing.assert_close(dW, grads[2 * i], rtol=1e-10, atol=1e-12)
+        if layer.linear.bias is not None:
+            torch.testing.assert_close(db, grads[2 * i + 1], rtol=1e-10, atol=1e-12)
+
+
+def test_affine_maps_fold_into_the_right_layer():
+    """x * c / c + b directly after a Linear folds into its output map; after
+    an activation into the next Linear's input map."""
+    chain = _extract_chain(ExpLog())
+    assert (chain[0].scale, chain[0].shift) == (0.5, 0.0)
+    assert (chain[1].scale, chain[1].shift) == (0.1, 3.0)
+    assert (chain[2].in_scale, chain[2].in_shift) == (2.0, -1.0)
+    chain = _extract_chain(Roots())
+    assert (chain[2].in_scale, chain[2].in_shift) == (-1.0, 0.5)
+    chain = _extract_chain(Square2())
+    assert (chain[1].in_scale, chain[1].in_shift, chain[1].scale) == (1.0, 1.0, 2.0)
+
+
+class TwoFunctions(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b = nn.Linear(4, 4), nn.Linear(4, 1)
+
+    def forward(self, x):
+        return self.b(torch.exp(torch.sin(self.a(x))))
+
+
+class ShiftAtEnd(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a = nn.Linear(4, 4)
+
+    def forward(self, x):
+        return torch.exp(self.a(x)) + 1.0
+
+
+class Rounded(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b = nn.Linear(4, 4), nn.Linear(4, 1)
+
+    def forward(self, x):
+        return self.b(torch.div(self.a(x), 2.0, rounding_mode="floor"))
+
+
+class Before(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a = nn.Linear(4, 1)
+
+    def forward(self, x):
+        return self.a(x * 2.0)
+
+
+@pytest.mark.parametrize("net", [TwoFunctions, ShiftAtEnd, Rounded, Before,
+                                 lambda: nn.Sequential(nn.Linear(4, 4), nn.LayerNorm(4),
+                                                       nn.Linear(4, 1))])
+def test_uncovered_networks_are_refused(net):
+    """Two functions in a row, arithmetic after the last activation, a
+    rounding division, arithmetic before the first Linear, LayerNorm: not
+    captured (the eager evaluator runs them)."""
+    with pytest.raises(NotImplementedError):
+        _extract_chain(net())
+
+
+def test_operator_forms_are_the_same_codes():
+    """x ** p, torch.pow, x.pow and c / x forms reach the same codes."""
+    for fn, code in [(lambda h: h ** 2.5, ("pow", 2.5)), (lambda h: torch.pow(h, 3), ("pow", 3.0)),
+                     (lambda h: h.pow(0.5), ("pow", 0.5)), (lambda h: 3.0 / h, ("reciprocal", 3.0)),
+                     (lambda h: torch.div(1.0, h), ("reciprocal", 1.0)),
+                     (lambda h: h.exp(), ("exp", 0.0)), (lambda h: torch.abs(h), ("abs", 0.0)),
+                     (lambda h: operator.mul(h, h), ("square", 0.0))]:
+        class Net(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.a, self.b = nn.Linear(3, 3), nn.Linear(3, 1)
+
+            def forward(self, x):
+                return self.b(fn(self.a(x)))
+
+        chain = _extract_chain(Net())
+        assert (chain[0].act, chain[0].param) == code

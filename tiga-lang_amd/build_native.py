@@ -8,6 +8,7 @@ Run ``python tiga-lang_amd/build_native.py`` or call :func:`build`.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -39,8 +40,19 @@ def _hipcc() -> str:
     return path
 
 
+def _included_sources(src: Path) -> list[Path]:
+    """The source files `src` includes (a .hip built again with other
+    settings), for the incremental check."""
+    names = re.findall(r'^#include "([^"]+\.hip)"', src.read_text(), re.M)
+    return [CSRC / n for n in names]
+
+
 def sources() -> list[Path]:
-    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+    """Every source, the largest (with what it includes) first: the
+    kernel-heavy files take minutes and should start before the rest."""
+    def size(src: Path) -> int:
+        return sum(f.stat().st_size for f in [src, *_included_sources(src)])
+    return sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")], key=lambda f: (-size(f), f.name))
 
 
 def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Path:
@@ -59,8 +71,9 @@ def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Pa
     for src in sources():
         obj = obj_dir / (src.name + ".o")
         objects.append(obj)
+        newest_source = max(f.stat().st_mtime for f in [src, *_included_sources(src)])
         if incremental and obj.exists() and \
-                obj.stat().st_mtime > max(src.stat().st_mtime, newest_header):
+                obj.stat().st_mtime > max(newest_source, newest_header):
             continue
         cmd = [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
         if src.suffix == ".cpp":

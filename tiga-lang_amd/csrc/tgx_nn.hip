@@ -38,6 +38,19 @@
 #include "tgx_nn_common.h"
 #include "tgx_profile.h"
 
+// Built twice: here the public entry points, and as tgx_nn_math.hip
+// (TGX_NN_MATH 1) the tgx_edge_mlp_*_math functions they call for chains
+// that use exp, log, abs, sin, cos or a power (the segment softmax entry
+// points are built here only).
+#if TGX_NN_MATH
+#define TGX_NN_ENTRY(name) int name##_math
+#define TGX_TO_MATH(mlp, call)
+#else
+#define TGX_NN_ENTRY(name) extern "C" int name
+#define TGX_TO_MATH(mlp, call) \
+  if (tgx::mlp::uses_math_tier(mlp)) return call
+#endif
+
 namespace tgx {
 namespace {
 
@@ -66,7 +79,8 @@ __global__ __launch_bounds__(256, (fwd_blocks_per_cu<W, L>())) void edge_mlp_fwd
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
     linear<W>(wg + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
-    activate_all<W>(z, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1]);
+    activate_all<W>(z, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
+                    m.n_out[l]);
   }
   scores[e] = linear_out1<W>(wg + (L - 1) * (W * W + W), a, m.nb_in[L - 1]);
 }
@@ -87,7 +101,8 @@ __global__ __launch_bounds__(256) void edge_mlp_hidden_kernel(const I* __restric
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
     linear<W>(wg + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
-    activate_all<W>(z, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1]);
+    activate_all<W>(z, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
+                    m.n_out[l]);
   }
   float* out = hidden + e * hw;
 #pragma unroll
@@ -297,21 +312,22 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
       float a[W];
 #pragma unroll
       for (int k = 0; k < W; ++k) a[k] = x[k];
-      static_for<L - 1>([&](auto lc) {
+      static_for<L - 1>([&](auto lc) TGX_INLINE_LAMBDA {
         constexpr int l = decltype(lc)::value;
         linear<W>(wg + l * NW, a, z[l], m.n_out[l], m.nb_in[l]);
-        activate_all<W>(z[l], a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1]);
+        activate_all<W>(z[l], a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
+                    m.n_out[l]);
       });
     }
     // Input of layer l: x, or the activation of z[l-1].
-    auto layer_input = [&](auto lc, float (&a)[W]) {
+    auto layer_input = [&](auto lc, float (&a)[W]) TGX_INLINE_LAMBDA {
       constexpr int l = decltype(lc)::value;
       if constexpr (l == 0) {
 #pragma unroll
         for (int k = 0; k < W; ++k) a[k] = x[k];
       } else {
         activate_all<W>(z[l - 1], a, m.act[l - 1], m.param[l - 1], m.param2[l - 1],
-                         m.nb_in[l]);
+                         m.nb_in[l], m.n_out[l - 1]);
       }
     };
     float g[W];
@@ -336,11 +352,11 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
           for (int j = 0; j < 8; ++j) last_w[8 * c + j] = fmaf(ds, a[8 * c + j], last_w[8 * c + j]);
       linear_t_out1<W>(wl, ds, g, m.nb_in[L - 1]);   // d a[L-1] = ds w
     }
-    static_for<L - 1>([&](auto kc) {
+    static_for<L - 1>([&](auto kc) TGX_INLINE_LAMBDA {
       constexpr int l = L - 2 - decltype(kc)::value;
       float dzl[W];
       activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.param2[l],
-                         m.nb_in[l + 1]);
+                         m.nb_in[l + 1], m.n_out[l]);
 #pragma unroll
       for (int o = 0; o < W; ++o) pin(dzl[o]);
       {
@@ -531,7 +547,8 @@ int check_mlp(const tgx_edge_mlp* mlp, MlpView* view, bool need_data) {
   }
   TGX_REQUIRE(in_width <= mlp->width, "inputs (%d) exceed the padded width", in_width);
   for (int l = 0; l + 1 < mlp->n_layers; ++l)
-    TGX_REQUIRE(mlp->act[l] >= TGX_ACT_IDENTITY && mlp->act[l] <= TGX_ACT_HARDSWISH,
+    TGX_REQUIRE(mlp->act[l] >= TGX_ACT_IDENTITY &&
+                    mlp->act[l] <= (TGX_NN_MATH ? TGX_ACT_POW : TGX_ACT_HARDSWISH),
                 "bad activation code");
   MlpView v{};
   v.n_layers = mlp->n_layers;
@@ -688,9 +705,11 @@ int last_input_width(const tgx_edge_mlp* mlp, const MlpView& v) {
 
 using namespace tgx;
 
-extern "C" int tgx_edge_mlp_scores(const void* col, const int32_t* dst_index, int idx_bits,
-                                   int64_t n_edges, const tgx_edge_mlp* mlp, float* scores,
-                                   void* stream) {
+TGX_NN_ENTRY(tgx_edge_mlp_scores)(const void* col, const int32_t* dst_index, int idx_bits,
+                                  int64_t n_edges, const tgx_edge_mlp* mlp, float* scores,
+                                  void* stream) {
+  TGX_TO_MATH(mlp, tgx_edge_mlp_scores_math(col, dst_index, idx_bits, n_edges, mlp, scores,
+                                            stream));
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
@@ -710,8 +729,9 @@ extern "C" int tgx_edge_mlp_scores(const void* col, const int32_t* dst_index, in
   return TGX_OK;
 }
 
-extern "C" int tgx_edge_mlp_backward_workspace(int64_t n_edges, const tgx_edge_mlp* mlp,
-                                               size_t* bytes) {
+TGX_NN_ENTRY(tgx_edge_mlp_backward_workspace)(int64_t n_edges, const tgx_edge_mlp* mlp,
+                                              size_t* bytes) {
+  TGX_TO_MATH(mlp, tgx_edge_mlp_backward_workspace_math(n_edges, mlp, bytes));
   TGX_REQUIRE(bytes, "null bytes");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
@@ -721,7 +741,7 @@ extern "C" int tgx_edge_mlp_backward_workspace(int64_t n_edges, const tgx_edge_m
   int64_t chunk = 0;
   const int blocks = n_edges == 0 ? 0
                      : mlp->width == 64
-                         ? outer_blocks(n_edges, &chunk)
+                         ? TGX_TIER(outer_blocks)(n_edges, &chunk)
                          : mlp_bwd_blocks(n_edges, resident_blocks(mlp->width, mlp->n_layers),
                                           &chunk);
   size_t planes = 0;
@@ -732,10 +752,13 @@ extern "C" int tgx_edge_mlp_backward_workspace(int64_t n_edges, const tgx_edge_m
   return TGX_OK;
 }
 
-extern "C" int tgx_edge_mlp_backward(const void* col, const int32_t* dst_index, int idx_bits,
-                                     int64_t n_edges, const tgx_edge_mlp* mlp,
-                                     const float* dscore, float* dweights, float* const* dseg,
-                                     void* workspace, size_t workspace_bytes, void* stream) {
+TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, int idx_bits,
+                                    int64_t n_edges, const tgx_edge_mlp* mlp,
+                                    const float* dscore, float* dweights, float* const* dseg,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  TGX_TO_MATH(mlp, tgx_edge_mlp_backward_math(col, dst_index, idx_bits, n_edges, mlp, dscore,
+                                              dweights, dseg, workspace, workspace_bytes,
+                                              stream));
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
@@ -756,13 +779,13 @@ extern "C" int tgx_edge_mlp_backward(const void* col, const int32_t* dst_index, 
     v.grad[k] = dseg[k];
   }
   size_t need = 0;
-  TGX_REQUIRE(tgx_edge_mlp_backward_workspace(n_edges, mlp, &need) == TGX_OK &&
+  TGX_REQUIRE(TGX_TIER(tgx_edge_mlp_backward_workspace)(n_edges, mlp, &need) == TGX_OK &&
                   workspace_bytes >= need,
               "workspace too small");
   int64_t chunk = 0;
   const int blocks =
       mlp->width == 64
-          ? outer_blocks(n_edges, &chunk)
+          ? TGX_TIER(outer_blocks)(n_edges, &chunk)
           : mlp_bwd_blocks(n_edges, resident_blocks(mlp->width, mlp->n_layers), &chunk);
   const size_t part_bytes = align_up(static_cast<size_t>(blocks) * n * sizeof(float));
   const size_t slice_bytes = align_up(static_cast<size_t>(kColSlices) * n * sizeof(float));
@@ -772,7 +795,7 @@ extern "C" int tgx_edge_mlp_backward(const void* col, const int32_t* dst_index, 
     const size_t plane = align_up(static_cast<size_t>(mlp->n_layers) * n_edges * 64 * sizeof(float));
     float* acts = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes + slice_bytes);
     float* dz = reinterpret_cast<float*>(reinterpret_cast<char*>(acts) + plane);
-    st = tgx::mlp::planes_backward(mlp->n_layers, idx_bits, col, dst_index, n_edges, v, dscore,
+    st = tgx::mlp::TGX_TIER(planes_backward)(mlp->n_layers, idx_bits, col, dst_index, n_edges, v, dscore,
                                    acts, dz, blocks, chunk, partial, s);
     if (st != TGX_OK) return st;
   } else {
@@ -796,6 +819,7 @@ extern "C" int tgx_edge_mlp_backward(const void* col, const int32_t* dst_index, 
   return TGX_OK;
 }
 
+#if !TGX_NN_MATH
 extern "C" int tgx_segment_softmax_fwd(const void* row_ptr, int idx_bits, int64_t n_rows,
                                        const float* scores, float* alpha, float* lse,
                                        void* stream) {
@@ -877,9 +901,13 @@ extern "C" int tgx_segment_softmax_bwd(const void* row_ptr, int idx_bits, int64_
   return TGX_OK;
 }
 
-extern "C" int tgx_edge_mlp_hidden(const void* col, const int32_t* dst_index, int idx_bits,
-                                   int64_t n_edges, const tgx_edge_mlp* mlp, float* hidden,
-                                   int32_t hidden_width, void* stream) {
+#endif  // !TGX_NN_MATH
+
+TGX_NN_ENTRY(tgx_edge_mlp_hidden)(const void* col, const int32_t* dst_index, int idx_bits,
+                                  int64_t n_edges, const tgx_edge_mlp* mlp, float* hidden,
+                                  int32_t hidden_width, void* stream) {
+  TGX_TO_MATH(mlp, tgx_edge_mlp_hidden_math(col, dst_index, idx_bits, n_edges, mlp, hidden,
+                                            hidden_width, stream));
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
@@ -906,12 +934,15 @@ extern "C" int tgx_edge_mlp_hidden(const void* col, const int32_t* dst_index, in
   return TGX_OK;
 }
 
-extern "C" int tgx_edge_mlp_backward_seeded(const void* col, const int32_t* dst_index,
-                                            int idx_bits, int64_t n_edges,
-                                            const tgx_edge_mlp* mlp, const float* seed,
-                                            int32_t seed_width, float* dweights,
-                                            float* const* dseg, void* workspace,
-                                            size_t workspace_bytes, void* stream) {
+TGX_NN_ENTRY(tgx_edge_mlp_backward_seeded)(const void* col, const int32_t* dst_index,
+                                           int idx_bits, int64_t n_edges,
+                                           const tgx_edge_mlp* mlp, const float* seed,
+                                           int32_t seed_width, float* dweights,
+                                           float* const* dseg, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  TGX_TO_MATH(mlp, tgx_edge_mlp_backward_seeded_math(col, dst_index, idx_bits, n_edges, mlp, seed,
+                                                     seed_width, dweights, dseg, workspace,
+                                                     workspace_bytes, stream));
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   MlpView v;
@@ -938,7 +969,7 @@ extern "C" int tgx_edge_mlp_backward_seeded(const void* col, const int32_t* dst_
     v.grad[k] = dseg[k];
   }
   size_t need = 0;
-  TGX_REQUIRE(tgx_edge_mlp_backward_workspace(n_edges, mlp, &need) == TGX_OK &&
+  TGX_REQUIRE(TGX_TIER(tgx_edge_mlp_backward_workspace)(n_edges, mlp, &need) == TGX_OK &&
                   workspace_bytes >= need,
               "workspace too small");
   int64_t chunk = 0;

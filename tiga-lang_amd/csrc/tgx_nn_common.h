@@ -10,6 +10,23 @@
 #include "tgx_device.h"
 #include "tgx_host.h"
 
+// The component-wise functions a translation unit's kernels evaluate: the
+// activations relu ... hardswish (TGX_NN_MATH 0), or those and exp, log,
+// abs, sin, cos and the powers (1).  The second set goes into kernels of
+// their own (tgx_nn_math.hip and tgx_nn_wide_math.hip compile the same
+// sources with TGX_NN_MATH 1), which the entry points call for a chain that
+// uses one of them: the larger switch costs the backward kernels registers
+// (spills at widths 16 and 24, one wave per SIMD less at width 32) that
+// chains without them do not pay.
+#ifndef TGX_NN_MATH
+#define TGX_NN_MATH 0
+#endif
+#if TGX_NN_MATH
+#define TGX_TIER(name) name##_math
+#else
+#define TGX_TIER(name) name
+#endif
+
 namespace tgx {
 namespace mlp {
 
@@ -181,6 +198,11 @@ __device__ __forceinline__ void scatter_segments(const MlpView& m, int64_t e, co
 // weight loads in between, and the operands it needs stay live that long.
 __device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
 
+// Lambdas in the kernels are inlined whatever the kernel's size: one left
+// as a call takes the arrays it captures by reference out of registers (into
+// private memory, spilled per lane).
+#define TGX_INLINE_LAMBDA __attribute__((always_inline))
+
 // f(integral_constant<0>) ... f(integral_constant<N-1>): a loop whose index
 // is a compile-time constant in the body (register arrays indexed by it stay
 // in registers whatever the body's size).
@@ -240,7 +262,7 @@ template <int W>
 __device__ __forceinline__ void linear(cfloat* wl, const float (&a)[W], float (&z)[W], int n_out,
                                        int nb) {
   static_assert(W % 8 == 0, "tiles of 8");
-  static_for<W / 8>([&](auto rc) {
+  static_for<W / 8>([&](auto rc) TGX_INLINE_LAMBDA {
     constexpr int r0 = 8 * decltype(rc)::value;
     if (r0 < n_out) {
 #pragma unroll
@@ -255,7 +277,7 @@ __device__ __forceinline__ void linear(cfloat* wl, const float (&a)[W], float (&
           for (int r = 0; r < 2; ++r)
 #pragma unroll
             for (int j = 0; j < 8; ++j) wp[0][r][j] = wl[(r0 + r) * W + 8 * c + j];
-          static_for<4>([&](auto pc) {
+          static_for<4>([&](auto pc) TGX_INLINE_LAMBDA {
             constexpr int p = decltype(pc)::value;
             if constexpr (p + 1 < 4) {
 #pragma unroll
@@ -289,7 +311,7 @@ __device__ __forceinline__ void linear_t(cfloat* wl, const float (&dz)[W], float
   static_assert(W % 8 == 0, "tiles of 8");
 #pragma unroll
   for (int i = 0; i < W; ++i) g[i] = 0.f;
-  static_for<W / 8>([&](auto cc) {
+  static_for<W / 8>([&](auto cc) TGX_INLINE_LAMBDA {
     constexpr int c0 = 8 * decltype(cc)::value;
     if (c0 < 4 * nb) {
 #pragma unroll
@@ -300,7 +322,7 @@ __device__ __forceinline__ void linear_t(cfloat* wl, const float (&dz)[W], float
           for (int r = 0; r < 2; ++r)
 #pragma unroll
             for (int j = 0; j < 8; ++j) wp[0][r][j] = wl[(8 * t + r) * W + c0 + j];
-          static_for<4>([&](auto pc) {
+          static_for<4>([&](auto pc) TGX_INLINE_LAMBDA {
             constexpr int p = decltype(pc)::value;
             if constexpr (p + 1 < 4) {
 #pragma unroll
@@ -373,49 +395,185 @@ __device__ __forceinline__ void map_real(const float (&z)[W], float (&out)[W], i
   X(TGX_ACT_GELU) X(TGX_ACT_ELU) X(TGX_ACT_HARDTANH) X(TGX_ACT_SOFTPLUS) X(TGX_ACT_SELU)   \
   X(TGX_ACT_MISH) X(TGX_ACT_HARDSIGMOID) X(TGX_ACT_HARDSWISH)
 
-template <int W>
-__device__ __forceinline__ void activate_all(const float (&z)[W], float (&a)[W], int act,
-                                             float p, float p2, int nb) {
+// The power functions as c z^e: sqrt (e = 1/2), rsqrt (-1/2), square (2),
+// reciprocal p / z (e = -1, c = p), pow z^p.  One code path for the five
+// keeps the kernels' size down (each case is a straight run over W values).
+__device__ __forceinline__ void power_form(int act, float p, float& e, float& c) {
+  c = 1.f;
   switch (act) {
-#define TGX_ACT_CASE(CODE)                                                                     \
-  case CODE:                                                                                   \
-    map_real<W>(z, a, nb, [p, p2](float v, int) { return activate(v, CODE, p, p2); });       \
-    break;
-    TGX_ACT_CASES(TGX_ACT_CASE)
-#undef TGX_ACT_CASE
-    default: map_real<W>(z, a, nb, [](float v, int) { return v; }); break;
+    case TGX_ACT_SQRT: e = 0.5f; break;
+    case TGX_ACT_RSQRT: e = -0.5f; break;
+    case TGX_ACT_SQUARE: e = 2.f; break;
+    case TGX_ACT_RECIPROCAL: e = -1.f; c = p; break;
+    default: e = p; break;
   }
 }
 
-// dz[k] = g[k] * activate'(z[k]) for the real outputs, 0 beyond.
+#define TGX_POWER_CASES \
+  case TGX_ACT_SQRT: case TGX_ACT_RSQRT: case TGX_ACT_SQUARE: case TGX_ACT_RECIPROCAL: \
+  case TGX_ACT_POW
+
+// The per-layer activation sweeps differ between the two sets of functions:
+// a namespace of their own per set keeps the two definitions apart.
+namespace TGX_TIER(tier) {
+
+// Activation of the n real outputs.  log and the power functions may not be
+// finite at 0 (a padding column's 0 would become inf, and inf times a zero
+// weight NaN downstream): their padding columns get 0.
 template <int W>
-__device__ __forceinline__ void activate_grad_all(const float (&z)[W], const float (&g)[W],
-                                                  float (&dz)[W], int act, float p, float p2,
-                                                  int nb) {
+__device__ __forceinline__ void activate_all(const float (&z)[W], float (&a)[W], int act,
+                                             float p, float p2, int nb, int n) {
   switch (act) {
-#define TGX_ACT_CASE(CODE)                                                                     \
-  case CODE:                                                                                   \
-    map_real<W>(z, dz, nb,                                                                     \
-                [&g, p, p2](float v, int k) { return g[k] * activate_grad(v, CODE, p, p2); }); \
+#define TGX_ACT_CASE(CODE)                                                             \
+  case CODE:                                                                           \
+    map_real<W>(z, a, nb, [p, p2](float v, int) TGX_INLINE_LAMBDA {                    \
+      return activate(v, CODE, p, p2);                                                 \
+    });                                                                                \
     break;
     TGX_ACT_CASES(TGX_ACT_CASE)
 #undef TGX_ACT_CASE
-    default: map_real<W>(z, dz, nb, [&g](float, int k) { return g[k]; }); break;
+#if TGX_NN_MATH
+    case TGX_ACT_EXP:
+      map_real<W>(z, a, nb, [](float v, int) TGX_INLINE_LAMBDA { return expf(v); });
+      break;
+    case TGX_ACT_LOG:
+      map_real<W>(z, a, nb, [n](float v, int k) TGX_INLINE_LAMBDA {
+        return k < n ? logf(v) : 0.f;
+      });
+      break;
+    case TGX_ACT_ABS:
+      map_real<W>(z, a, nb, [](float v, int) TGX_INLINE_LAMBDA { return fabsf(v); });
+      break;
+    case TGX_ACT_SIN:
+    case TGX_ACT_COS: {
+      const bool cosine = act == TGX_ACT_COS;
+      map_real<W>(z, a, nb, [cosine](float v, int) TGX_INLINE_LAMBDA {
+        float sv, cv;
+        sincosf(v, &sv, &cv);
+        return cosine ? cv : sv;
+      });
+      break;
+    }
+    TGX_POWER_CASES: {
+      float e, c;
+      power_form(act, p, e, c);
+      map_real<W>(z, a, nb, [e, c, n](float v, int k) TGX_INLINE_LAMBDA {
+        return k < n ? c * powf(v, e) : 0.f;
+      });
+      break;
+    }
+#endif
+    default:
+      map_real<W>(z, a, nb, [](float v, int) TGX_INLINE_LAMBDA { return v; });
+      break;
   }
+}
+
+// dz[k] = g[k] * activate'(z[k]) for the n real outputs, 0 beyond for log
+// and the power functions.  Torch's pow backward is 0 for a zero exponent.
+template <int W>
+__device__ __forceinline__ void activate_grad_all(const float (&z)[W], const float (&g)[W],
+                                                  float (&dz)[W], int act, float p, float p2,
+                                                  int nb, int n) {
+  switch (act) {
+#define TGX_ACT_CASE(CODE)                                                             \
+  case CODE:                                                                           \
+    map_real<W>(z, dz, nb, [&g, p, p2](float v, int k) TGX_INLINE_LAMBDA {             \
+      return g[k] * activate_grad(v, CODE, p, p2);                                     \
+    });                                                                                \
+    break;
+    TGX_ACT_CASES(TGX_ACT_CASE)
+#undef TGX_ACT_CASE
+#if TGX_NN_MATH
+    case TGX_ACT_EXP:
+      map_real<W>(z, dz, nb, [&g](float v, int k) TGX_INLINE_LAMBDA { return g[k] * expf(v); });
+      break;
+    case TGX_ACT_LOG:
+      map_real<W>(z, dz, nb, [&g, n](float v, int k) TGX_INLINE_LAMBDA {
+        return k < n ? g[k] / v : 0.f;
+      });
+      break;
+    case TGX_ACT_ABS:
+      map_real<W>(z, dz, nb, [&g](float v, int k) TGX_INLINE_LAMBDA {
+        return v > 0.f ? g[k] : (v < 0.f ? -g[k] : 0.f);
+      });
+      break;
+    case TGX_ACT_SIN:
+    case TGX_ACT_COS: {
+      const bool cosine = act == TGX_ACT_COS;
+      map_real<W>(z, dz, nb, [&g, cosine](float v, int k) TGX_INLINE_LAMBDA {
+        float sv, cv;
+        sincosf(v, &sv, &cv);
+        return cosine ? -g[k] * sv : g[k] * cv;
+      });
+      break;
+    }
+    TGX_POWER_CASES: {
+      float e, c;
+      power_form(act, p, e, c);
+      const float ce = e == 0.f ? 0.f : c * e;
+      map_real<W>(z, dz, nb, [&g, e, ce, n](float v, int k) TGX_INLINE_LAMBDA {
+        return k < n ? g[k] * (ce * powf(v, e - 1.f)) : 0.f;
+      });
+      break;
+    }
+#endif
+    default:
+      map_real<W>(z, dz, nb, [&g](float, int k) TGX_INLINE_LAMBDA { return g[k]; });
+      break;
+  }
+}
+
+}  // namespace TGX_TIER(tier)
+using namespace TGX_TIER(tier);
+
+// Whether a chain uses a function of the second set (above).
+inline bool uses_math_tier(const tgx_edge_mlp* mlp) {
+  if (!mlp || mlp->n_layers < 1 || mlp->n_layers > kMaxLayers) return false;
+  for (int l = 0; l + 1 < mlp->n_layers; ++l)
+    if (mlp->act[l] >= TGX_ACT_EXP && mlp->act[l] <= TGX_ACT_POW) return true;
+  return false;
 }
 
 // 64-wide chains: backward in two passes (tgx_nn_wide.hip).  Blocks and
 // chunk of the outer-sum pass for n_edges edges.
-int outer_blocks(int64_t n_edges, int64_t* chunk);
+int TGX_TIER(outer_blocks)(int64_t n_edges, int64_t* chunk);
 
 // Per-edge planes (acts, dz: n_layers x [n_edges, 64] each) and the
 // per-segment input gradients, then the per-layer weight-gradient partial
 // sums of outer_nb blocks into partial[block * n_layers * NW + l * NW + ...]
 // (NW = 64 * 64 + 64).  Launches on `s`; TGX_* status.
-int planes_backward(int n_layers, int idx_bits, const void* col, const int32_t* dst,
-                    int64_t n_edges, const MlpView& v, const float* dscore, float* acts,
-                    float* dz, int outer_nb, int64_t outer_chunk, float* partial,
-                    hipStream_t s);
+int TGX_TIER(planes_backward)(int n_layers, int idx_bits, const void* col, const int32_t* dst,
+                              int64_t n_edges, const MlpView& v, const float* dscore,
+                              float* acts, float* dz, int outer_nb, int64_t outer_chunk,
+                              float* partial, hipStream_t s);
 
 }  // namespace mlp
 }  // namespace tgx
+
+// The edge-MLP entry points of tgx.h built with the second set of functions
+// (tgx_nn_math.hip); the public entry points call them for chains that use
+// one of those functions.  Same arguments and status codes.
+#define TGX_NN_HIDDEN __attribute__((visibility("hidden")))
+TGX_NN_HIDDEN int tgx_edge_mlp_scores_math(const void* col, const int32_t* dst_index,
+                                           int idx_bits, int64_t n_edges,
+                                           const tgx_edge_mlp* mlp, float* scores,
+                                           void* stream);
+TGX_NN_HIDDEN int tgx_edge_mlp_backward_workspace_math(int64_t n_edges, const tgx_edge_mlp* mlp,
+                                                       size_t* bytes);
+TGX_NN_HIDDEN int tgx_edge_mlp_backward_math(const void* col, const int32_t* dst_index,
+                                             int idx_bits, int64_t n_edges,
+                                             const tgx_edge_mlp* mlp, const float* dscore,
+                                             float* dweights, float* const* dseg,
+                                             void* workspace, size_t workspace_bytes,
+                                             void* stream);
+TGX_NN_HIDDEN int tgx_edge_mlp_hidden_math(const void* col, const int32_t* dst_index,
+                                           int idx_bits, int64_t n_edges,
+                                           const tgx_edge_mlp* mlp, float* hidden,
+                                           int32_t hidden_width, void* stream);
+TGX_NN_HIDDEN int tgx_edge_mlp_backward_seeded_math(const void* col, const int32_t* dst_index,
+                                                    int idx_bits, int64_t n_edges,
+                                                    const tgx_edge_mlp* mlp, const float* seed,
+                                                    int32_t seed_width, float* dweights,
+                                                    float* const* dseg, void* workspace,
+                                                    size_t workspace_bytes, void* stream);

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
   float a[W];                       // input of the current layer
   float z[L > 1 ? L - 1 : 1][W];    // pre-activations of the hidden layers
   gather_inputs<I, W>(m, e, col, dst, a);
-  static_for<L>([&](auto lc) {
+  static_for<L>([&](auto lc) TGX_INLINE_LAMBDA {
     constexpr int l = decltype(lc)::value;
     float* out = acts + l * plane + e * W;
 #pragma unroll
@@ -38,7 +38,8 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
       *reinterpret_cast<f32x4*>(out + i) = f32x4{a[i], a[i + 1], a[i + 2], a[i + 3]};
     if constexpr (l + 1 < L) {
       linear<W>(wg + l * (W * W + W), a, z[l], m.n_out[l], m.nb_in[l]);
-      activate_all<W>(z[l], a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1]);
+      activate_all<W>(z[l], a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
+                    m.n_out[l]);
     }
   });
   // Last layer: one output, gradient ds.
@@ -53,11 +54,11 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
 #pragma unroll
     for (int i = 0; i < W; ++i) g[i] = ds * wl[i];   // d a[L-1]
   }
-  static_for<L - 1>([&](auto kc) {
+  static_for<L - 1>([&](auto kc) TGX_INLINE_LAMBDA {
     constexpr int l = L - 2 - decltype(kc)::value;
     float dzl[W];
     activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.param2[l],
-                         m.nb_in[l + 1]);
+                         m.nb_in[l + 1], m.n_out[l]);
 #pragma unroll
     for (int o = 0; o < W; ++o) pin(dzl[o]);
     float* out = dz_out + l * plane + e * W;
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(256) void outer_sum_kernel(const float* __restrict_
 
 }  // namespace
 
-int outer_blocks(int64_t n_edges, int64_t* chunk) {
+int TGX_TIER(outer_blocks)(int64_t n_edges, int64_t* chunk) {
   // About four workgroups per CU; chunks of whole waves of edges.
   int64_t c = ceil_div(n_edges, 1024);
   c = c < 64 ? 64 : align_up(static_cast<size_t>(c), 64);
@@ -191,10 +192,10 @@ int planes_bwd_t(int L, const I* col, const int32_t* dst, int64_t E, const MlpVi
 }
 }  // namespace
 
-int planes_backward(int n_layers, int idx_bits, const void* col, const int32_t* dst,
-                    int64_t n_edges, const MlpView& v, const float* dscore, float* acts,
-                    float* dz, int outer_nb, int64_t outer_chunk, float* partial,
-                    hipStream_t s) {
+int TGX_TIER(planes_backward)(int n_layers, int idx_bits, const void* col, const int32_t* dst,
+                              int64_t n_edges, const MlpView& v, const float* dscore,
+                              float* acts, float* dz, int outer_nb, int64_t outer_chunk,
+                              float* partial, hipStream_t s) {
   return idx_bits == 32
              ? planes_bwd_t(n_layers, static_cast<const int32_t*>(col), dst, n_edges, v, dscore,
                             acts, dz, outer_nb, outer_chunk, partial, s)

@@ -307,19 +307,44 @@ def _padded_width(chain, in_width: int, vector: bool = False) -> int:
     return next(w for w in (16, 24, 32, 64) if w >= widest)
 
 
+def _folded(layer, weight, bias):
+    """The folded weights of one layer, z = W' a + b', with the scalar maps
+    on its input (in_scale, in_shift) and output (scale, shift):
+    W' = scale in_scale W, b' = scale (b + in_shift W 1) + shift.  b' is
+    None when it is identically zero."""
+    w = weight.detach()
+    wf = w * (layer.scale * layer.in_scale)
+    bf = None if bias is None else bias.detach() * layer.scale
+    if layer.in_shift != 0.0:
+        extra = w.sum(1) * (layer.scale * layer.in_shift)
+        bf = extra if bf is None else bf + extra
+    if layer.shift != 0.0:
+        bf = torch.full_like(wf[:, 0], layer.shift) if bf is None else bf + layer.shift
+    return wf, bf
+
+
+def _unfolded_grads(layer, dwf, dbf, need_w, need_b):
+    """Gradients of a layer's own weight and bias from those of its folded
+    weights W', b' (see _folded): dW = scale in_scale dW' + scale in_shift
+    db' 1^T, db = scale db'."""
+    dW = db = None
+    if need_w and dwf is not None:
+        dW = dwf * (layer.scale * layer.in_scale)
+        if layer.in_shift != 0.0:
+            dW = dW + (dbf * (layer.scale * layer.in_shift))[:, None]
+    if need_b and dbf is not None:
+        db = dbf * layer.scale
+    return dW, db
+
+
 def _fill_weights(buf, chain, params, W, layers):
-    """Padded weight blocks for `layers`: W' = scale W, b' = scale b + shift
-    (the scalar affine map folded after each Linear)."""
+    """Padded blocks of the folded weights (_folded) of `layers`."""
     for l in range(layers):
-        layer = chain[l]
-        weight, bias = params[2 * l], params[2 * l + 1]
-        out_f, in_f = weight.shape
-        buf[l, :W * W].view(W, W)[:out_f, :in_f] = weight.detach() * layer.scale
-        b = buf[l, W * W:W * W + out_f]
-        if bias is not None:
-            b.copy_(bias.detach() * layer.scale)
-        if layer.shift != 0.0:
-            b.add_(layer.shift)
+        wf, bf = _folded(chain[l], params[2 * l], params[2 * l + 1])
+        out_f, in_f = wf.shape
+        buf[l, :W * W].view(W, W)[:out_f, :in_f] = wf
+        if bf is not None:
+            buf[l, W * W:W * W + out_f] = bf
 
 
 def _mlp_struct(chain, roles, segs, weights_buf, width):
@@ -411,19 +436,16 @@ class EdgeMlpFunction(torch.autograd.Function):
 
 def _layer_grads(chain, dweights, W, has_bias, needs, first, layers):
     """Weight and bias gradients of the module's own parameters from the
-    folded blocks' sums: dW = scale dW', db = scale db'."""
+    folded blocks' sums (_unfolded_grads)."""
     grads = []
     for l in range(layers):
         layer = chain[l]
         out_f, in_f = layer.linear.out_features, layer.linear.in_features
         k = first + 2 * l
         blk = dweights[l]
-        dW = blk[:W * W].view(W, W)[:out_f, :in_f] if needs[k] else None
-        db = blk[W * W:W * W + out_f] if has_bias[l] and needs[k + 1] else None
-        if layer.scale != 1.0:
-            dW = None if dW is None else dW * layer.scale
-            db = None if db is None else db * layer.scale
-        grads += [dW, db]
+        grads += list(_unfolded_grads(layer, blk[:W * W].view(W, W)[:out_f, :in_f],
+                                      blk[W * W:W * W + out_f], needs[k],
+                                      has_bias[l] and needs[k + 1]))
     return grads
 
 
@@ -614,16 +636,10 @@ class EdgeMlpSumFunction(torch.autograd.Function):
                      _native.idx_bits(row_ptr), E, ctypes.byref(mlp), hidden.data_ptr(), hw,
                      _native.stream_of(col_idx))
         sums = _reduce_rows(graph, hidden)
-        last = chain[-1]
-        w_last = params[2 * L - 2].detach() * last.scale
+        w_last, b_last = _folded(chain[-1], params[2 * L - 2], params[2 * L - 1])
         out = sums @ w_last.t()
-        b_last = params[2 * L - 1]
-        shift = torch.zeros(w_last.shape[0], dtype=torch.float32, device=dev) \
-            if b_last is None else b_last.detach() * last.scale
-        if last.shift != 0.0:
-            shift = shift + last.shift
-        if b_last is not None or last.shift != 0.0:
-            out = out + _row_degrees(graph)[:, None] * shift
+        if b_last is not None:
+            out = out + _row_degrees(graph)[:, None] * b_last
         ctx.graph, ctx.chain, ctx.roles, ctx.n_seg, ctx.W = graph, chain, roles, n_seg, W
         ctx.shapes = [t.shape for t in tensors[:n_seg]]
         ctx.has_bias = [params[2 * l + 1] is not None for l in range(L)]
@@ -641,10 +657,11 @@ class EdgeMlpSumFunction(torch.autograd.Function):
         needs = ctx.needs_input_grad
         last = chain[-1]
         k_last = 4 + ctx.n_seg + 2 * (L - 1)
-        d_w_last = (dout.t() @ sums) * last.scale if needs[k_last] else None
-        d_b_last = None
-        if ctx.has_bias[L - 1] and needs[k_last + 1]:
-            d_b_last = (_row_degrees(graph)[:, None] * dout).sum(0) * last.scale
+        need_w, need_b = needs[k_last], ctx.has_bias[L - 1] and needs[k_last + 1]
+        dwf = (dout.t() @ sums) if need_w else None
+        dbf = (_row_degrees(graph)[:, None] * dout).sum(0) \
+            if need_b or (need_w and last.in_shift != 0.0) else None
+        d_w_last, d_b_last = _unfolded_grads(last, dwf, dbf, need_w, need_b)
         grads = [None] * ctx.n_seg
         grads += [None] * (2 * (L - 1))
         upstream = any(needs[4:k_last])

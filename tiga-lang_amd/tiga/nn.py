@@ -13,14 +13,17 @@ python/tiga/nn/__init__.py): ``trace(module)`` wraps a module so one
 Covered chains: ``nn.Linear`` layers (bias optional), each optionally
 followed by scalar-constant arithmetic (``x * c``, ``x / c``, ``x + c``,
 ``x - c``, ``c - x``, ``-x``: folded into that layer's weights and bias) and
-by one component-wise activation (relu, leaky_relu, tanh, sigmoid, silu,
+by one component-wise function (relu, leaky_relu, tanh, sigmoid, silu,
 exact gelu, elu, hardtanh / relu6 / clamp, softplus, selu, mish,
-hardsigmoid, hardswish; module or functional form; ``nn.Identity`` is
-skipped), at most three Linear layers.  A score network ends in a Linear
-layer with one output and every width is at most 64; an edge-network
-message summed per row (``tg.sum()``) ends in a Linear layer of any width
-and its other widths are at most 32.  Anything else (LayerNorm, arithmetic
-after an activation, ...) runs on the eager evaluator.
+hardsigmoid, hardswish, exp, log, sqrt, rsqrt, abs, sin, cos, square,
+``c / x``, ``x ** p``; module, functional or Tensor-method form;
+``nn.Identity`` is skipped), whose output may again be scaled and shifted by
+constants (folded into the next Linear layer's input), at most three Linear
+layers.  A score network ends in a Linear layer with one output and every
+width is at most 64; an edge-network message summed per row (``tg.sum()``)
+ends in a Linear layer of any width and its other widths are at most 32.
+Anything else (LayerNorm, two functions in a row, ...) runs on the eager
+evaluator.
 """
 
 from __future__ import annotations
@@ -37,13 +40,20 @@ _CHAINS: "weakref.WeakKeyDictionary[nn.Module, object]" = weakref.WeakKeyDiction
 
 _ACT = {"identity": 0, "relu": 1, "leaky_relu": 2, "tanh": 3, "sigmoid": 4, "silu": 5,
         "gelu": 6, "elu": 7, "hardtanh": 8, "softplus": 9, "selu": 10, "mish": 11,
-        "hardsigmoid": 12, "hardswish": 13}
+        "hardsigmoid": 12, "hardswish": 13, "exp": 14, "log": 15, "sqrt": 16, "rsqrt": 17,
+        "abs": 18, "sin": 19, "cos": 20, "square": 21, "reciprocal": 22, "pow": 23}
+
+# Component-wise Torch functions without parameters that have a code of
+# the same name.
+_UNARY = ("exp", "log", "sqrt", "rsqrt", "abs", "sin", "cos", "square")
 
 
 @dataclass(frozen=True)
 class ScoreLayer:
-    """One Linear layer of a chain, the scalar affine map folded after it
-    (z = scale * (W a + b) + shift) and the activation that follows."""
+    """One Linear layer of a chain: the scalar affine map on its input
+    (in_scale * a + in_shift, from arithmetic after the previous
+    activation), the one folded after it, z = scale * (W a' + b) + shift,
+    and the activation that follows."""
 
     linear: nn.Linear
     act: str = "identity"
@@ -51,6 +61,8 @@ class ScoreLayer:
     param2: float = 0.0
     scale: float = 1.0
     shift: float = 0.0
+    in_scale: float = 1.0
+    in_shift: float = 0.0
 
 
 class TracedModule(nn.Module):
@@ -132,11 +144,32 @@ def _arg(args, kwargs, index, name, default):
     return kwargs.get(name, default)
 
 
+def _number(v) -> bool:
+    import numbers
+
+    return isinstance(v, numbers.Number) and not isinstance(v, bool)
+
+
 def _function_activation(target, args, kwargs, previous):
+    import operator
+
     from torch.nn import functional as F
 
+    # c / x (x / c is a scalar affine map, taken earlier).
+    if target in (operator.truediv, torch.div, torch.true_divide) and len(args) == 2 and \
+            args[1] is previous and _number(args[0]) and not kwargs:
+        return "reciprocal", float(args[0]), 0.0
     if not args or args[0] is not previous:
         return None
+    unary = {getattr(torch, name): name for name in _UNARY}
+    if target in unary and len(args) == 1 and not kwargs:
+        return unary[target], 0.0, 0.0
+    if target in (operator.mul, torch.mul) and tuple(args) == (previous, previous) and \
+            not kwargs:
+        return "square", 0.0, 0.0
+    if target in (operator.pow, torch.pow) and len(args) == 2 and _number(args[1]) and \
+            not kwargs:
+        return "pow", float(args[1]), 0.0
     simple = {torch.relu: "relu", F.relu: "relu", torch.tanh: "tanh", F.tanh: "tanh",
               torch.sigmoid: "sigmoid", F.sigmoid: "sigmoid", F.silu: "silu", F.selu: "selu",
               torch.selu: "selu", F.mish: "mish", F.hardsigmoid: "hardsigmoid",
@@ -166,17 +199,14 @@ def _function_activation(target, args, kwargs, previous):
     return None
 
 
-def _scalar_affine(node, previous):
-    """(scale, shift) of a scalar-constant arithmetic node applied to
-    `previous`: y = scale * x + shift; None if it is not one."""
-    import numbers
+def _scalar_affine(t, a, kwargs, previous):
+    """(scale, shift) of scalar-constant arithmetic `t(*a, **kwargs)` applied
+    to `previous`: y = scale * x + shift; None if it is not one."""
     import operator
 
-    if node.op != "call_function" or not node.args:
+    if not a or kwargs:
         return None
-    a = node.args
-    number = lambda v: isinstance(v, numbers.Number) and not isinstance(v, bool)
-    t = node.target
+    number = _number
     if t in (operator.neg, torch.neg) and len(a) == 1 and a[0] is previous:
         return -1.0, 0.0
     if len(a) != 2:
@@ -203,8 +233,9 @@ def _scalar_affine(node, previous):
 
 def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
     """Linear [affine]* [act] ... Linear [affine]*, via torch.fx (reference
-    nn_capture.py:281-380 translates the same graphs).  Scalar affine maps
-    are only taken directly after a Linear layer, where they fold into it."""
+    nn_capture.py:281-380 translates the same graphs).  A scalar affine map
+    directly after a Linear layer folds into that layer's output, one after
+    an activation into the next Linear layer's input."""
     import torch.fx
 
     if isinstance(module, nn.Linear):
@@ -215,6 +246,7 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
     gm = torch.fx.symbolic_trace(module)
     layers: list[dict] = []
     previous = None
+    pending = (1.0, 0.0)   # affine map after the last activation, for the next Linear
     for node in gm.graph.nodes:
         if node.op == "placeholder":
             if previous is not None:
@@ -224,6 +256,8 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
         if node.op == "output":
             if node.args[0] is not previous:
                 raise NotImplementedError("network output is not the chain's end")
+            if pending != (1.0, 0.0):
+                raise NotImplementedError("scalar arithmetic after the last activation")
             break
         if node.op == "call_module":
             target = gm.get_submodule(node.target)
@@ -234,21 +268,35 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
                 continue
             if isinstance(target, nn.Linear):
                 layers.append({"linear": target, "act": None, "param": 0.0, "param2": 0.0,
-                               "scale": 1.0, "shift": 0.0})
+                               "scale": 1.0, "shift": 0.0, "in_scale": pending[0],
+                               "in_shift": pending[1]})
+                pending = (1.0, 0.0)
                 previous = node
                 continue
             act = _module_activation(target)
-        elif node.op == "call_function":
-            affine = _scalar_affine(node, previous)
+        elif node.op in ("call_function", "call_method"):
+            target = node.target
+            if node.op == "call_method":
+                # x.exp(), x.mul(c), x.pow(p), ...: the Torch function of the
+                # same name on the same arguments.
+                target = getattr(torch, target, None)
+                if target is None:
+                    raise NotImplementedError(f"unsupported method {node.target}")
+            affine = _scalar_affine(target, node.args, node.kwargs, previous)
             if affine is not None:
-                if not layers or layers[-1]["act"] is not None:
-                    raise NotImplementedError("scalar arithmetic only directly after a Linear")
                 c, b = affine
-                layers[-1]["scale"] *= c
-                layers[-1]["shift"] = c * layers[-1]["shift"] + b
+                if not layers:
+                    raise NotImplementedError("scalar arithmetic before the first Linear")
+                if layers[-1]["act"] is None:
+                    # Directly after a Linear: folded into that layer.
+                    layers[-1]["scale"] *= c
+                    layers[-1]["shift"] = c * layers[-1]["shift"] + b
+                else:
+                    # After an activation: folded into the next Linear's input.
+                    pending = (c * pending[0], c * pending[1] + b)
                 previous = node
                 continue
-            act = _function_activation(node.target, node.args, node.kwargs, previous)
+            act = _function_activation(target, node.args, node.kwargs, previous)
         else:
             raise NotImplementedError(f"unsupported network node {node.op}")
         if act is None or not layers or layers[-1]["act"] is not None:
@@ -267,7 +315,8 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
     if max(widths) > 64:
         raise NotImplementedError("network widths above 64")
     return tuple(ScoreLayer(l["linear"], l["act"] or "identity", l["param"], l["param2"],
-                            l["scale"], l["shift"]) for l in layers)
+                            l["scale"], l["shift"], l["in_scale"], l["in_shift"])
+                 for l in layers)
 
 
 __all__ = ["ScoreLayer", "TracedModule", "trace"]
