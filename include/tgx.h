@@ -474,6 +474,14 @@ typedef struct tgx_edge_mlp {
   /* Second parameter of each activation (hardtanh's upper bound, softplus's
    * threshold; unused by the others). */
   float act_param2[3];
+  /* LayerNorm over a hidden layer's real outputs before its activation
+   * (nonzero = on; not on the last layer; padded widths up to 32), Torch's
+   * nn.LayerNorm: (z - mean) / sqrt(var + norm_eps) * gamma + beta with the
+   * biased variance.  With any layer normalized, every layer's block of
+   * weights_dev (and of the weight gradients) is [width*width | width bias |
+   * width gamma | width beta]. */
+  int32_t norm[3];
+  float norm_eps[3];
 } tgx_edge_mlp;
 
 /* scores[e] = MLP(x_e) for every edge.  dst_index_dev [n_edges] int32 is the

@@ -3,8 +3,9 @@ reference's edge-NN tile, compiler/edge_nn_tile.py, message_passing.py:
 2134-2300) and nn-scored attention with the wider activation set and scalar
 arithmetic (compiler/nn_capture.py:17-31): exp, log, sqrt, rsqrt, abs, sin,
 cos, squares, powers and c / x among the functions, scalar maps after them
-folded into the next Linear layer, hidden widths that leave padding columns
-in the kernels' 4-wide blocks.
+folded into the next Linear layer, LayerNorm between hidden layers and their
+functions, hidden widths that leave padding columns in the kernels' 4-wide
+blocks.
 
 Checked against Torch float64 autograd of the same module on the gathered
 fields (oracle/eager_torch.nn_message_sum / nn_attention, the reference's
@@ -83,8 +84,32 @@ class ThreeLayer(nn.Module):
         return self.c(h / 3.0)
 
 
+class Normed(nn.Module):
+    """LayerNorm between hidden Linear layers and their functions (with and
+    without its affine parameters, constants around it)."""
+
+    def __init__(self, i, h1, h2, o):
+        super().__init__()
+        self.a, self.b, self.c = nn.Linear(i, h1), nn.Linear(h1, h2), nn.Linear(h2, o)
+        self.na = nn.LayerNorm(h1)
+        self.nb = nn.LayerNorm(h2, elementwise_affine=False, eps=1e-3)
+        with torch.no_grad():
+            self.na.weight.uniform_(0.5, 1.5)
+            self.na.bias.uniform_(-0.5, 0.5)
+
+    def forward(self, x):
+        h = F.gelu(self.na(self.a(x) * 3.0) * 2.0 + 0.5)
+        return self.c(torch.tanh(self.nb(self.b(h))) - 0.25)
+
+
 def nets(i):
     return {
+        "layernorm-3": Normed(i, 12, 7, 3),
+        "layernorm-2": nn.Sequential(nn.Linear(i, 16), nn.LayerNorm(16), nn.ReLU(),
+                                     nn.Linear(16, 4)),
+        "layernorm-32": nn.Sequential(nn.Linear(i, 30), nn.LayerNorm(30), nn.SiLU(),
+                                      nn.Linear(30, 20), nn.LayerNorm(20), nn.Sigmoid(),
+                                      nn.Linear(20, 2)),
         "exp-log": ThreeLayer(i, "exp-log", 10, 9, 3),
         "roots": ThreeLayer(i, "roots", 12, 7, 2),
         "trig": ThreeLayer(i, "trig", 11, 6, 4),
@@ -143,7 +168,8 @@ def test_edge_network_sum_against_float64_autograd(name, idx):
 
 
 @pytest.mark.parametrize("name", ["mish-selu-3", "hard-3", "relu6-hardtanh", "affine-softplus",
-                                  "exp-log", "roots", "trig", "powers", "squares"])
+                                  "exp-log", "roots", "trig", "powers", "squares",
+                                  "layernorm-3", "layernorm-2", "layernorm-32"])
 def test_nn_attention_wider_op_set_against_float64_autograd(name):
     print(f"nn attention {name}", flush=True)
     N = 2000

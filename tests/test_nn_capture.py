@@ -1,6 +1,7 @@
 """Capture of edge networks (tg.nn.trace) into the kernels' layer chain, on
-the CPU: which modules become a chain of folded Linear layers, and that the
-folded weights and the gradient unfolding reproduce the module itself.
+the CPU: which modules become a chain of folded Linear (and LayerNorm)
+layers, and that the folded weights and the gradient unfolding reproduce the
+module itself.
 
 The reference captures the same op set (compiler/nn_capture.py:17-31,
 281-380: Linear, the component-wise functions, scalar arithmetic).  The
@@ -112,6 +113,25 @@ class Square2(nn.Module):
         return self.b(torch.square(self.a(x)) + 1.0) * 2.0
 
 
+class Normed(nn.Module):
+    """LayerNorm after hidden Linear layers, with and without its affine
+    parameters, constants between it and the function."""
+
+    def __init__(self):
+        super().__init__()
+        self.a, self.b, self.c = nn.Linear(5, 12), nn.Linear(12, 7), nn.Linear(7, 3)
+        self.na = nn.LayerNorm(12)
+        self.nb = nn.LayerNorm(7, elementwise_affine=False, eps=1e-3)
+        with torch.no_grad():
+            self.na.weight.uniform_(0.5, 1.5)
+            self.na.bias.uniform_(-0.5, 0.5)
+
+    def forward(self, x):
+        h = F.gelu(self.na(self.a(x) * 3.0) * 2.0 + 0.5)
+        h = torch.tanh(self.nb(self.b(h)))
+        return self.c(h)
+
+
 NETS = {
     "exp-log": (ExpLog, [("exp", 0.0), ("log", 0.0), ("identity", 0.0)]),
     "roots": (Roots, [("sqrt", 0.0), ("rsqrt", 0.0), ("identity", 0.0)]),
@@ -119,6 +139,10 @@ NETS = {
     "powers": (Powers, [("abs", 0.0), ("reciprocal", 2.0), ("identity", 0.0)]),
     "squares": (Squares, [("square", 0.0), ("pow", 1.5), ("identity", 0.0)]),
     "square-2": (Square2, [("square", 0.0), ("identity", 0.0)]),
+    "layernorm": (Normed, [("gelu", 0.0), ("tanh", 0.0), ("identity", 0.0)]),
+    "layernorm-sequential": (lambda: nn.Sequential(nn.Linear(5, 10), nn.LayerNorm(10),
+                                                   nn.ReLU(), nn.Linear(10, 1)),
+                             [("relu", 0.0), ("identity", 0.0)]),
     "sequential": (lambda: nn.Sequential(nn.Linear(5, 8), nn.Softplus(2.0), nn.Linear(8, 8),
                                          nn.ELU(0.5), nn.Linear(8, 1)),
                    [("softplus", 2.0), ("elu", 0.5), ("identity", 0.0)]),
@@ -127,14 +151,27 @@ NETS = {
 
 def run_chain(chain, x, weights):
     """The captured chain in float64 with the folded weights `weights`
-    ([(W', b' or None)] per layer)."""
+    ([(W', b' or None, gamma' or None, beta' or None)] per layer)."""
     a = x
-    for layer, (w, b) in zip(chain, weights):
+    for layer, (w, b, g, beta) in zip(chain, weights):
         z = a @ w.t()
         if b is not None:
             z = z + b
+        if layer.norm is not None:
+            z = F.layer_norm(z, (z.shape[1],), g, beta, layer.norm.eps)
         a = ACT[layer.act](z, layer.param, layer.param2)
     return a
+
+
+def folded_weights(chain, params):
+    out = []
+    for i, layer in enumerate(chain):
+        w, b = _ops._folded(layer, params[4 * i], params[4 * i + 1])
+        g = beta = None
+        if layer.norm is not None:
+            g, beta = _ops._folded_norm(layer, params[4 * i + 2], params[4 * i + 3])
+        out.append((w, b, g, beta))
+    return out
 
 
 @pytest.mark.parametrize("name", sorted(NETS))
@@ -145,45 +182,57 @@ def test_capture_codes_and_folded_chain_match_the_module(name):
     chain = _extract_chain(net)
     assert [(l.act, l.param) for l in chain] == codes
     x = torch.randn(64, 5, dtype=torch.float64)
-    params = [t for l in chain for t in (l.linear.weight, l.linear.bias)]
-    folded = [_ops._folded(l, params[2 * i], params[2 * i + 1]) for i, l in enumerate(chain)]
+    params = _ops._layer_params(chain)
+    folded = folded_weights(chain, params)
     expect = net(x)
     got = run_chain(chain, x, folded)
     assert torch.isfinite(expect).all()
     torch.testing.assert_close(got, expect, rtol=1e-12, atol=1e-12)
 
     # Gradients of the module's own parameters: through the module, and at
-    # the folded weights then unfolded.
+    # the folded weights then mapped back as the HIP path does.  The kernels
+    # sum a bias gradient for every layer, also where the module has no bias
+    # (it unfolds into the weight gradient through in_shift): the chain here
+    # gets a zero bias in its place.
     dout = torch.randn_like(expect)
-    grads = torch.autograd.grad(net(x), params, dout, allow_unused=True)
-    leaves = [(w.clone().requires_grad_(True),
-               None if b is None else b.clone().requires_grad_(True)) for w, b in folded]
-    # A folded bias exists whenever the module's bias does (the shifts only
-    # add to it); a chain layer without one has a zero folded-bias gradient
-    # seed all the same, as the kernels sum it for every layer.
-    flat = [t for w, b in leaves for t in (w, b) if t is not None]
-    dflat = torch.autograd.grad(run_chain(chain, x, leaves), flat, dout)
-    it = iter(dflat)
-    for i, (layer, (w, b)) in enumerate(zip(chain, leaves)):
-        dwf = next(it)
-        if b is not None:
-            dbf = next(it)
-        else:
-            # dz summed over the rows: the gradient a zero bias would get.
-            zb = torch.zeros(w.shape[0], dtype=torch.float64, requires_grad=True)
-            trial = [(lw.detach(), lb.detach() if lb is not None else None)
-                     for lw, lb in leaves]
-            trial[i] = (w.detach(), zb)
-            dbf = torch.autograd.grad(run_chain(chain, x, trial), zb, dout)[0]
-        dW, db = _ops._unfolded_grads(layer, dwf, dbf, True, layer.linear.bias is not None)
-        torch.testing.assert_close(dW, grads[2 * i], rtol=1e-10, atol=1e-12)
-        if layer.linear.bias is not None:
-            torch.testing.assert_close(db, grads[2 * i + 1], rtol=1e-10, atol=1e-12)
+    present = [p is not None for p in params]
+    grads = torch.autograd.grad(net(x), [p for p in params if p is not None], dout)
+    grads = iter(grads)
+    expect_grads = [next(grads) if ok else None for ok in present]
+    leaves = []
+    for layer, (w, b, g, beta) in zip(chain, folded):
+        b = torch.zeros(w.shape[0], dtype=torch.float64) if b is None else b
+        if layer.norm is not None:
+            g = torch.ones(w.shape[0], dtype=torch.float64) if g is None else g
+            beta = torch.zeros(w.shape[0], dtype=torch.float64) if beta is None else beta
+        leaves.append(tuple(None if t is None else t.clone().requires_grad_(True)
+                            for t in (w, b, g, beta)))
+    flat = [t for grp in leaves for t in grp if t is not None]
+    dflat = iter(torch.autograd.grad(run_chain(chain, x, leaves), flat, dout))
+    blocks = []
+    for grp in leaves:
+        blocks.append([None if t is None else next(dflat) for t in grp])
+    W = 16
+    dweights = torch.zeros(len(chain), _ops._block_floats(chain, W), dtype=torch.float64)
+    for l, (layer, (dw, db, dg, dbeta)) in enumerate(zip(chain, blocks)):
+        o, i = dw.shape
+        dweights[l, :W * W].view(W, W)[:o, :i] = dw
+        dweights[l, W * W:W * W + o] = db
+        if dg is not None:
+            dweights[l, W * W + W:W * W + W + o] = dg
+            dweights[l, W * W + 2 * W:W * W + 2 * W + o] = dbeta
+    needs = [True] * (4 * len(chain))
+    got_grads = _ops._layer_grads(chain, dweights, W, present, needs, 0, len(chain))
+    for k, (g, e) in enumerate(zip(got_grads, expect_grads)):
+        assert (g is None) == (e is None), k
+        if e is not None:
+            torch.testing.assert_close(g, e, rtol=1e-10, atol=1e-12)
 
 
 def test_affine_maps_fold_into_the_right_layer():
     """x * c / c + b directly after a Linear folds into its output map; after
-    an activation into the next Linear's input map."""
+    a LayerNorm into its gamma and beta; after an activation into the next
+    Linear's input map."""
     chain = _extract_chain(ExpLog())
     assert (chain[0].scale, chain[0].shift) == (0.5, 0.0)
     assert (chain[1].scale, chain[1].shift) == (0.1, 3.0)
@@ -192,6 +241,9 @@ def test_affine_maps_fold_into_the_right_layer():
     assert (chain[2].in_scale, chain[2].in_shift) == (-1.0, 0.5)
     chain = _extract_chain(Square2())
     assert (chain[1].in_scale, chain[1].in_shift, chain[1].scale) == (1.0, 1.0, 2.0)
+    chain = _extract_chain(Normed())
+    assert (chain[0].scale, chain[0].norm_scale, chain[0].norm_shift) == (3.0, 2.0, 0.5)
+    assert chain[1].norm is not None and chain[1].norm.eps == 1e-3
 
 
 class TwoFunctions(nn.Module):
@@ -231,12 +283,15 @@ class Before(nn.Module):
 
 
 @pytest.mark.parametrize("net", [TwoFunctions, ShiftAtEnd, Rounded, Before,
-                                 lambda: nn.Sequential(nn.Linear(4, 4), nn.LayerNorm(4),
-                                                       nn.Linear(4, 1))])
+                                 lambda: nn.Sequential(nn.Linear(4, 4), nn.ReLU(),
+                                                       nn.LayerNorm(4), nn.Linear(4, 1)),
+                                 lambda: nn.Sequential(nn.Linear(4, 4), nn.ReLU(),
+                                                       nn.Linear(4, 2), nn.LayerNorm(2))])
 def test_uncovered_networks_are_refused(net):
     """Two functions in a row, arithmetic after the last activation, a
-    rounding division, arithmetic before the first Linear, LayerNorm: not
-    captured (the eager evaluator runs them)."""
+    rounding division, arithmetic before the first Linear, a LayerNorm after
+    an activation or after the last Linear layer: not captured (the eager
+    evaluator runs them)."""
     with pytest.raises(NotImplementedError):
         _extract_chain(net())
 

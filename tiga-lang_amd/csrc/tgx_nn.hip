@@ -40,8 +40,8 @@
 
 // Built twice: here the public entry points, and as tgx_nn_math.hip
 // (TGX_NN_MATH 1) the tgx_edge_mlp_*_math functions they call for chains
-// that use exp, log, abs, sin, cos or a power (the segment softmax entry
-// points are built here only).
+// that use exp, log, abs, sin, cos, a power or LayerNorm (the segment
+// softmax entry points are built here only).
 #if TGX_NN_MATH
 #define TGX_NN_ENTRY(name) int name##_math
 #define TGX_TO_MATH(mlp, call)
@@ -61,9 +61,13 @@ using namespace mlp;
 // lands just above a step (one fewer wave per SIMD).
 template <int W, int L>
 constexpr int fwd_blocks_per_cu() { return W <= 32 ? (L <= 2 ? 6 : 5) : 3; }
+// The kernels with the second set of functions and LayerNorm hold more
+// per lane (LayerNorm sums, the larger switch): one wave per SIMD fewer
+// keeps them from spilling.
 template <int W, int L>
 constexpr int bwd_blocks_per_cu() {
-  return W == 16 ? 3 : W == 24 ? (L <= 2 ? 3 : 2) : (L <= 2 ? 2 : 1);
+  constexpr int n = W == 16 ? 3 : W == 24 ? (L <= 2 ? 3 : 2) : (L <= 2 ? 2 : 1);
+  return TGX_NN_MATH && n > 1 ? n - 1 : n;
 }
 
 template <typename I, int W, int L>
@@ -76,13 +80,15 @@ __global__ __launch_bounds__(256, (fwd_blocks_per_cu<W, L>())) void edge_mlp_fwd
   if (e >= n_edges) return;
   float a[W], z[W];
   gather_inputs<I, W>(m, e, col, dst, a);
+  const int nw = layer_stride<W>(m);
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
-    linear<W>(wg + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
+    linear<W>(wg + l * nw, a, z, m.n_out[l], m.nb_in[l]);
+    norm_layer<W>(m, l, wg + l * nw, z);
     activate_all<W>(z, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
                     m.n_out[l]);
   }
-  scores[e] = linear_out1<W>(wg + (L - 1) * (W * W + W), a, m.nb_in[L - 1]);
+  scores[e] = linear_out1<W>(wg + (L - 1) * nw, a, m.nb_in[L - 1]);
 }
 
 // The last layer's input per edge (the activation after layer L - 2, or the
@@ -98,9 +104,11 @@ __global__ __launch_bounds__(256) void edge_mlp_hidden_kernel(const I* __restric
   if (e >= n_edges) return;
   float a[W], z[W];
   gather_inputs<I, W>(m, e, col, dst, a);
+  const int nw = layer_stride<W>(m);
 #pragma unroll
   for (int l = 0; l + 1 < L; ++l) {
-    linear<W>(wg + l * (W * W + W), a, z, m.n_out[l], m.nb_in[l]);
+    linear<W>(wg + l * nw, a, z, m.n_out[l], m.nb_in[l]);
+    norm_layer<W>(m, l, wg + l * nw, z);
     activate_all<W>(z, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
                     m.n_out[l]);
   }
@@ -176,6 +184,33 @@ __device__ __forceinline__ void outer_accumulate(const float* sg, const float* s
     }
   }
 }
+
+#if TGX_NN_MATH
+// The diagonal of the wave's accumulated W x W block and its column sums:
+// red[i] = acc[i][i], red[W + i] = b[i] (a LayerNorm's d gamma, d beta).
+template <int W>
+__device__ __forceinline__ void outer_store_norm(const OuterAcc<W>& acc, float* red) {
+  static_assert(W <= 32, "normalized layers are at most 32 wide");
+  const int l = lane_id();
+  if constexpr (W == 16) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (4 * (l / 16) + q == l % 16) red[l % 16] = acc.c[0][q];
+    float b = acc.b[0];
+    b += __shfl_xor(b, 16, 64);
+    b += __shfl_xor(b, 32, 64);
+    if (l < 16) red[W + l] = b;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int o = 8 * (q / 4) + 4 * (l / 32) + q % 4, i = l % 32;
+      if (o == i && i < W) red[i] = acc.c[0][q];
+    }
+    const float b = acc.b[0] + __shfl_xor(acc.b[0], 32, 64);
+    if (l < W) red[W + l] = b;
+  }
+}
+#endif
 
 // Orders this wave's LDS accesses around an exchange between its lanes: a
 // wave's LDS instructions execute in issue order, so only the compiler has
@@ -277,6 +312,13 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
   for (int i = 0; i < W; ++i) last_w[i] = 0.f;
 #pragma unroll
   for (int l = 0; l < (L > 1 ? L - 1 : 1); ++l) acc[l].zero();
+#if TGX_NN_MATH
+  // LayerNorm parameter sums of the hidden layers: sum dy (x) x_hat, whose
+  // diagonal is d gamma, and sum dy = d beta, on the same MFMA path.
+  OuterAcc<W> acc_n[L > 1 ? L - 1 : 1];
+#pragma unroll
+  for (int l = 0; l < (L > 1 ? L - 1 : 1); ++l) acc_n[l].zero();
+#endif
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * chunk;
   const int64_t e1 = e0 + chunk < n_edges ? e0 + chunk : n_edges;
   // Each step's source and destination row ids are loaded one step ahead.
@@ -293,10 +335,28 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
     cfloat* wg = opaque(w_all);
     MlpView m = m_arg;
     launder(m);
+    const int nw = layer_stride<W>(m);
     const int64_t e = base + threadIdx.x;
     const bool valid = e < e1;
     float x[W];                        // gathered input (layer 0's input)
-    float z[L > 1 ? L - 1 : 1][W];     // pre-activations of the hidden layers
+    // Pre-activations of the hidden layers (x_hat for a normalized layer,
+    // with 1 / sqrt(var + eps) in rstd).
+    float z[L > 1 ? L - 1 : 1][W];
+#if TGX_NN_MATH
+    float rstd[L > 1 ? L - 1 : 1];
+#endif
+    // The activation's input of hidden layer l: z[l], or gamma x_hat + beta.
+    auto act_input = [&](auto lc, float (&y)[W]) TGX_INLINE_LAMBDA {
+      constexpr int l = decltype(lc)::value;
+#if TGX_NN_MATH
+      if (m.norm[l]) {
+        norm_affine<W>(wg + l * nw + W * W + W, z[l], y);
+        return;
+      }
+#endif
+#pragma unroll
+      for (int k = 0; k < W; ++k) y[k] = z[l][k];
+    };
     const int64_t cur_dst = next_dst;
     if (valid) {
       gather_rows<W>(m, e, next_src, next_dst, x);
@@ -314,9 +374,14 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
       for (int k = 0; k < W; ++k) a[k] = x[k];
       static_for<L - 1>([&](auto lc) TGX_INLINE_LAMBDA {
         constexpr int l = decltype(lc)::value;
-        linear<W>(wg + l * NW, a, z[l], m.n_out[l], m.nb_in[l]);
-        activate_all<W>(z[l], a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
-                    m.n_out[l]);
+        linear<W>(wg + l * nw, a, z[l], m.n_out[l], m.nb_in[l]);
+#if TGX_NN_MATH
+        if (m.norm[l]) rstd[l] = norm_rows<W>(z[l], m.n_out[l], m.eps[l]);
+#endif
+        float y[W];
+        act_input(lc, y);
+        activate_all<W>(y, a, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
+                        m.n_out[l]);
       });
     }
     // Input of layer l: x, or the activation of z[l-1].
@@ -326,8 +391,10 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
 #pragma unroll
         for (int k = 0; k < W; ++k) a[k] = x[k];
       } else {
-        activate_all<W>(z[l - 1], a, m.act[l - 1], m.param[l - 1], m.param2[l - 1],
-                         m.nb_in[l], m.n_out[l - 1]);
+        float y[W];
+        act_input(std::integral_constant<int, l - 1>{}, y);
+        activate_all<W>(y, a, m.act[l - 1], m.param[l - 1], m.param2[l - 1], m.nb_in[l],
+                        m.n_out[l - 1]);
       }
     };
     float g[W];
@@ -339,7 +406,7 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
     } else {
       // Last layer: one output, gradient ds (0 on lanes past the range).
       const float ds = valid ? dscore[e] : 0.f;
-      cfloat* wl = wg + (L - 1) * NW;
+      cfloat* wl = wg + (L - 1) * nw;
       float a[W];
       layer_input(std::integral_constant<int, L - 1>{}, a);
       // One output row: its gradient ds a is summed per lane (an MFMA outer
@@ -355,8 +422,20 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
     static_for<L - 1>([&](auto kc) TGX_INLINE_LAMBDA {
       constexpr int l = L - 2 - decltype(kc)::value;
       float dzl[W];
-      activate_grad_all<W>(z[l], g, dzl, m.act[l], m.param[l], m.param2[l],
-                         m.nb_in[l + 1], m.n_out[l]);
+      {
+        float y[W];
+        act_input(std::integral_constant<int, l>{}, y);
+        activate_grad_all<W>(y, g, dzl, m.act[l], m.param[l], m.param2[l], m.nb_in[l + 1],
+                             m.n_out[l]);
+      }
+#if TGX_NN_MATH
+      if (m.norm[l]) {
+        // dzl is the gradient at y here: the gamma and beta sums, then the
+        // gradient at z through the normalization.
+        outer_layer<W>(sg, sa, dzl, z[l], acc_n[l]);
+        norm_rows_grad<W>(wg + l * nw + W * W + W, z[l], dzl, m.n_out[l], rstd[l]);
+      }
+#endif
 #pragma unroll
       for (int o = 0; o < W; ++o) pin(dzl[o]);
       {
@@ -365,14 +444,15 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
         outer_layer<W>(sg, sa, dzl, a, acc[l]);
       }
       // d a[l] = W_l^T dz.
-      linear_t<W>(wg + l * NW, dzl, g, m.n_out[l], m.nb_in[l]);
+      linear_t<W>(wg + l * nw, dzl, g, m.n_out[l], m.nb_in[l]);
     });
     // g = d x: split per segment.
     if (valid) scatter_segments<W>(m, e, g);
   }
   // Block sums, layer by layer: each wave's block into its staging region,
   // then the four added in wave order.
-  float* out = partial + static_cast<int64_t>(blockIdx.x) * L * NW;
+  const int nwb = layer_stride<W>(m_arg);
+  float* out = partial + static_cast<int64_t>(blockIdx.x) * L * nwb;
 #pragma unroll
   for (int l = 0; l < L; ++l) {
     if (l == L - 1) {
@@ -397,8 +477,20 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < NW; idx += 256)
-      out[l * NW + idx] = (stage[idx] + stage[SW + idx]) + (stage[2 * SW + idx] + stage[3 * SW + idx]);
+      out[l * nwb + idx] = (stage[idx] + stage[SW + idx]) + (stage[2 * SW + idx] + stage[3 * SW + idx]);
     __syncthreads();
+#if TGX_NN_MATH
+    if (nwb > NW) {
+      // [d gamma | d beta] after the layer's block (zero for the last layer).
+      if (l + 1 < L) outer_store_norm<W>(acc_n[l < L - 1 ? l : 0], sg);
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < 2 * W; idx += 256)
+        out[l * nwb + NW + idx] =
+            l + 1 < L ? (stage[idx] + stage[SW + idx]) + (stage[2 * SW + idx] + stage[3 * SW + idx])
+                      : 0.f;
+      __syncthreads();
+    }
+#endif
   }
 }
 
@@ -569,7 +661,20 @@ int check_mlp(const tgx_edge_mlp* mlp, MlpView* view, bool need_data) {
     v.act[l] = l + 1 < mlp->n_layers ? mlp->act[l] : TGX_ACT_IDENTITY;
     v.param[l] = mlp->act_param[l];
     v.param2[l] = mlp->act_param2[l];
+    v.norm[l] = 0;
+    v.eps[l] = 0.f;
+    if (l < mlp->n_layers && mlp->norm[l]) {
+      TGX_REQUIRE(TGX_NN_MATH, "internal: a normalized chain on the kernels without LayerNorm");
+      TGX_REQUIRE(l + 1 < mlp->n_layers, "the last layer cannot be normalized");
+      TGX_REQUIRE(mlp->width <= 32, "normalized layers need a padded width of at most 32");
+      TGX_REQUIRE(mlp->norm_eps[l] >= 0.f && mlp->norm_eps[l] <= 1e30f,
+                  "norm_eps must be finite and >= 0");
+      TGX_REQUIRE(v.n_out[l] >= 1, "empty normalized layer");
+      v.norm[l] = 1;
+      v.eps[l] = mlp->norm_eps[l];
+    }
   }
+  v.nw = block_floats(mlp);
   v.w = mlp->weights_dev;
   v.n_seg = mlp->n_segments;
   int k = 0;
@@ -737,7 +842,7 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward_workspace)(int64_t n_edges, const tgx_edge_ml
   MlpView v;
   int st = check_mlp(mlp, &v, n_edges > 0);
   if (st != TGX_OK) return st;
-  const int64_t n = static_cast<int64_t>(mlp->n_layers) * (mlp->width * mlp->width + mlp->width);
+  const int64_t n = static_cast<int64_t>(mlp->n_layers) * block_floats(mlp);
   int64_t chunk = 0;
   const int blocks = n_edges == 0 ? 0
                      : mlp->width == 64
@@ -765,7 +870,7 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, i
   int st = check_mlp(mlp, &v, n_edges > 0);
   if (st != TGX_OK) return st;
   TGX_REQUIRE(dweights && dseg, "null pointer");
-  const int n = mlp->n_layers * (mlp->width * mlp->width + mlp->width);
+  const int n = mlp->n_layers * block_floats(mlp);
   hipStream_t s = as_stream(stream);
   if (n_edges == 0) {
     // Zero sums, written by a kernel rather than a memset.
@@ -956,7 +1061,7 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward_seeded)(const void* col, const int32_t* dst_i
               "seed_width %d is not the last layer's input width %d", seed_width,
               last_input_width(mlp, v));
   TGX_REQUIRE(dweights && dseg, "null pointer");
-  const int n = mlp->n_layers * (mlp->width * mlp->width + mlp->width);
+  const int n = mlp->n_layers * block_floats(mlp);
   hipStream_t s = as_stream(stream);
   if (n_edges == 0) {
     colsum_final_kernel<<<ceil_div(n, 256), 256, 0, s>>>(nullptr, 0, n, dweights);

@@ -12,7 +12,7 @@
 
 // The component-wise functions a translation unit's kernels evaluate: the
 // activations relu ... hardswish (TGX_NN_MATH 0), or those and exp, log,
-// abs, sin, cos and the powers (1).  The second set goes into kernels of
+// abs, sin, cos, the powers and LayerNorm (1).  The second set goes into kernels of
 // their own (tgx_nn_math.hip and tgx_nn_wide_math.hip compile the same
 // sources with TGX_NN_MATH 1), which the entry points call for a chain that
 // uses one of them: the larger switch costs the backward kernels registers
@@ -49,7 +49,22 @@ struct MlpView {
   const float* ptr[kMaxSegments];
   int off[kMaxSegments];              // first input column of each segment
   float* grad[kMaxSegments];          // backward: per-segment input gradients
+  // LayerNorm over a hidden layer's real outputs before its activation
+  // (kernels with the second set of functions only), and the floats per
+  // layer of the weight blocks: W*W + W, or W*W + 3W (gamma, beta) when
+  // some layer is normalized.
+  int norm[kMaxLayers];
+  float eps[kMaxLayers];
+  int nw;
 };
+
+// Floats per layer of a chain's weight (and weight-gradient) blocks.
+inline int block_floats(const tgx_edge_mlp* mlp) {
+  int w = mlp->width * mlp->width + mlp->width;
+  for (int l = 0; l + 1 < mlp->n_layers && l < kMaxLayers; ++l)
+    if (mlp->norm[l]) return w + 2 * mlp->width;
+  return w;
+}
 
 __device__ __forceinline__ float sigmoid(float z) { return 1.f / (1.f + __expf(-z)); }
 
@@ -246,6 +261,88 @@ __device__ __forceinline__ void launder(MlpView& v) {
 #pragma unroll
   for (int s = 0; s < kMaxSegments; ++s)
     asm volatile("" : "+s"(v.role[s]), "+s"(v.width[s]), "+s"(v.off[s]));
+#if TGX_NN_MATH
+  asm volatile("" : "+s"(v.nw));
+#pragma unroll
+  for (int l = 0; l < kMaxLayers; ++l) asm volatile("" : "+s"(v.norm[l]), "+s"(v.eps[l]));
+#endif
+}
+
+// Floats per layer of the weight blocks (compile-time without LayerNorm).
+template <int W>
+__device__ __forceinline__ int layer_stride(const MlpView& m) {
+#if TGX_NN_MATH
+  return m.nw;
+#else
+  (void)m;
+  return W * W + W;
+#endif
+}
+
+#if TGX_NN_MATH
+// LayerNorm over the n real outputs of a layer (Torch's nn.LayerNorm over
+// the last axis: biased variance, eps inside the square root): z becomes
+// x_hat = (z - mean) / sqrt(var + eps), 0 past n.  Returns 1 / sqrt(var + eps).
+template <int W>
+__device__ __forceinline__ float norm_rows(float (&z)[W], int n, float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < W; ++k) s += k < n ? z[k] : 0.f;
+  const float inv_n = 1.f / static_cast<float>(n);
+  const float mean = s * inv_n;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const float d = z[k] - mean;
+    q = k < n ? fmaf(d, d, q) : q;
+  }
+  const float rstd = 1.f / sqrtf(q * inv_n + eps);
+#pragma unroll
+  for (int k = 0; k < W; ++k) z[k] = k < n ? (z[k] - mean) * rstd : 0.f;
+  return rstd;
+}
+
+// y = gamma x_hat + beta (gb: the layer's gamma, then beta; zero padding).
+template <int W>
+__device__ __forceinline__ void norm_affine(cfloat* gb, const float (&xh)[W], float (&y)[W]) {
+#pragma unroll
+  for (int k = 0; k < W; ++k) y[k] = fmaf(gb[k], xh[k], gb[W + k]);
+}
+
+// d (in: the gradient at y) becomes the gradient at the layer's z:
+// d x_hat = gamma d, dz = rstd (d x_hat - mean(d x_hat) - x_hat mean(d x_hat
+// x_hat)) over the n real outputs, 0 past n.
+template <int W>
+__device__ __forceinline__ void norm_rows_grad(cfloat* gb, const float (&xh)[W], float (&d)[W],
+                                               int n, float rstd) {
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    d[k] *= gb[k];
+    s1 += k < n ? d[k] : 0.f;
+    s2 = k < n ? fmaf(d[k], xh[k], s2) : s2;
+  }
+  const float inv_n = 1.f / static_cast<float>(n);
+  const float m1 = s1 * inv_n, m2 = s2 * inv_n;
+#pragma unroll
+  for (int k = 0; k < W; ++k) d[k] = k < n ? rstd * (d[k] - m1 - xh[k] * m2) : 0.f;
+}
+#endif
+
+// A hidden layer's LayerNorm, when it has one, on its pre-activation z in
+// place (wl: the layer's weight block).
+template <int W>
+__device__ __forceinline__ void norm_layer(const MlpView& m, int l, cfloat* wl, float (&z)[W]) {
+#if TGX_NN_MATH
+  if constexpr (W <= 32) {
+    if (m.norm[l]) {
+      norm_rows<W>(z, m.n_out[l], m.eps[l]);
+      norm_affine<W>(wl + W * W + W, z, z);
+    }
+  }
+#else
+  (void)m, (void)l, (void)wl, (void)z;
+#endif
 }
 
 // z = W_l a + b_l over the layer's real shape, in tiles of 8 rows x 8
@@ -527,11 +624,13 @@ __device__ __forceinline__ void activate_grad_all(const float (&z)[W], const flo
 }  // namespace TGX_TIER(tier)
 using namespace TGX_TIER(tier);
 
-// Whether a chain uses a function of the second set (above).
+// Whether a chain uses a function of the second set (above) or LayerNorm.
 inline bool uses_math_tier(const tgx_edge_mlp* mlp) {
   if (!mlp || mlp->n_layers < 1 || mlp->n_layers > kMaxLayers) return false;
-  for (int l = 0; l + 1 < mlp->n_layers; ++l)
-    if (mlp->act[l] >= TGX_ACT_EXP && mlp->act[l] <= TGX_ACT_POW) return true;
+  for (int l = 0; l < mlp->n_layers; ++l)
+    if ((l + 1 < mlp->n_layers && mlp->act[l] >= TGX_ACT_EXP && mlp->act[l] <= TGX_ACT_POW) ||
+        mlp->norm[l])
+      return true;
   return false;
 }
 

@@ -49,7 +49,12 @@ class EdgeMlp(ctypes.Structure):
                 ("weights_dev", c_vp), ("n_segments", ctypes.c_int32),
                 ("seg_role", ctypes.c_int32 * 4), ("seg_width", ctypes.c_int32 * 4),
                 ("seg_stride", ctypes.c_int64 * 4), ("seg_dev", c_vp * 4),
-                ("out_width", ctypes.c_int32 * 3), ("act_param2", ctypes.c_float * 3)]
+                ("out_width", ctypes.c_int32 * 3), ("act_param2", ctypes.c_float * 3),
+                ("norm", ctypes.c_int32 * 3), ("norm_eps", ctypes.c_float * 3)]
+
+
+# tgx_abi_version() of the library these signatures and structs mirror.
+ABI_VERSION = 6
 
 
 # name -> argtypes (all return int status except where noted)
@@ -177,6 +182,10 @@ def lib():
             raise RuntimeError(f"{path} does not export {name}")
         fn.restype = c_int
         fn.argtypes = argtypes
+    if handle.tgx_abi_version() != ABI_VERSION:
+        raise RuntimeError(
+            f"{path} has ABI version {handle.tgx_abi_version()}, this package expects "
+            f"{ABI_VERSION}; rebuild it with `python tiga-lang_amd/build_native.py`")
     _lib = handle
     return _lib
 

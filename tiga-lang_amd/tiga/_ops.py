@@ -337,14 +337,50 @@ def _unfolded_grads(layer, dwf, dbf, need_w, need_b):
     return dW, db
 
 
+def _folded_norm(layer, gamma, beta):
+    """A LayerNorm's folded gamma', beta' (the scalar map between it and the
+    activation, c y + d, folded in: gamma' = c gamma, beta' = c beta + d)."""
+    n = layer.linear.out_features
+    like = layer.linear.weight
+    g = torch.ones(n, dtype=like.dtype, device=like.device) if gamma is None else gamma.detach()
+    b = torch.zeros(n, dtype=like.dtype, device=like.device) if beta is None else beta.detach()
+    return g * layer.norm_scale, b * layer.norm_scale + layer.norm_shift
+
+
+def _block_floats(chain, W: int) -> int:
+    """Floats per layer of the weight blocks: [W*W | W bias], and [W gamma |
+    W beta] after them when some layer has a LayerNorm."""
+    return W * W + W + (2 * W if any(l.norm is not None for l in chain) else 0)
+
+
+# Parameters per layer passed to the autograd functions: Linear weight and
+# bias, LayerNorm weight and bias (None where absent).
+_PER_LAYER = 4
+
+
+def _layer_params(chain):
+    params = []
+    for layer in chain:
+        norm = layer.norm
+        params += [layer.linear.weight, layer.linear.bias,
+                   None if norm is None else norm.weight, None if norm is None else norm.bias]
+    return params
+
+
 def _fill_weights(buf, chain, params, W, layers):
-    """Padded blocks of the folded weights (_folded) of `layers`."""
+    """Padded blocks of the folded weights (_folded, _folded_norm) of
+    `layers` (buf: [layers or more, _block_floats])."""
     for l in range(layers):
-        wf, bf = _folded(chain[l], params[2 * l], params[2 * l + 1])
+        k = _PER_LAYER * l
+        wf, bf = _folded(chain[l], params[k], params[k + 1])
         out_f, in_f = wf.shape
         buf[l, :W * W].view(W, W)[:out_f, :in_f] = wf
         if bf is not None:
             buf[l, W * W:W * W + out_f] = bf
+        if chain[l].norm is not None:
+            g, b = _folded_norm(chain[l], params[k + 2], params[k + 3])
+            buf[l, W * W + W:W * W + W + out_f] = g
+            buf[l, W * W + 2 * W:W * W + 2 * W + out_f] = b
 
 
 def _mlp_struct(chain, roles, segs, weights_buf, width):
@@ -357,6 +393,9 @@ def _mlp_struct(chain, roles, segs, weights_buf, width):
         m.act[l] = _ACT[layer.act]
         m.act_param[l] = layer.param
         m.act_param2[l] = layer.param2
+        if layer.norm is not None:
+            m.norm[l] = 1
+            m.norm_eps[l] = float(layer.norm.eps)
         # The last layer of an edge-network sum is applied by the caller;
         # the kernels see it as a one-output layer they do not evaluate.
         m.out_width[l] = layer.linear.out_features if l + 1 < len(chain) else 1
@@ -382,7 +421,8 @@ class EdgeMlpFunction(torch.autograd.Function):
     """scores[e] = net(concat of the fields gathered for edge e).
 
     Inputs after (graph, chain, roles, n_seg): the n_seg field tensors, then
-    weight and bias (None allowed) of every Linear layer."""
+    per layer the Linear weight and bias and the LayerNorm weight and bias
+    (None allowed)."""
 
     @staticmethod
     def forward(ctx, graph: Graph, chain, roles, n_seg: int, *tensors):
@@ -394,7 +434,7 @@ class EdgeMlpFunction(torch.autograd.Function):
         in_width = sum(s.shape[1] for s in segs)
         W = _padded_width(chain, in_width)
         dev = col_idx.device
-        buf = torch.zeros(len(chain), W * W + W, dtype=torch.float32, device=dev)
+        buf = torch.zeros(len(chain), _block_floats(chain, W), dtype=torch.float32, device=dev)
         _fill_weights(buf, chain, params, W, len(chain))
         mlp = _mlp_struct(chain, roles, segs, buf, W)
         scores = torch.empty(E, dtype=torch.float32, device=dev)
@@ -403,7 +443,7 @@ class EdgeMlpFunction(torch.autograd.Function):
                      _native.stream_of(col_idx))
         ctx.graph, ctx.chain, ctx.roles, ctx.n_seg, ctx.W = graph, chain, roles, n_seg, W
         ctx.shapes = [t.shape for t in tensors[:n_seg]]
-        ctx.has_bias = [params[2 * l + 1] is not None for l in range(len(chain))]
+        ctx.present = [t is not None for t in params]
         ctx.save_for_backward(buf, *segs)
         return scores
 
@@ -422,30 +462,40 @@ class EdgeMlpFunction(torch.autograd.Function):
         _native.call("tgx_edge_mlp_backward_workspace", E, ctypes.byref(mlp),
                      ctypes.byref(ws_bytes))
         ws = torch.empty(max(ws_bytes.value, 4), dtype=torch.uint8, device=dev)
-        dweights = torch.empty(L, W * W + W, dtype=torch.float32, device=dev)
+        dweights = torch.empty(L, buf.shape[1], dtype=torch.float32, device=dev)
         ptrs = (ctypes.c_void_p * 4)(*[d.data_ptr() for d in dsegs], *([None] * (4 - len(dsegs))))
         _native.call("tgx_edge_mlp_backward", col_idx.data_ptr(),
                      graph._dst_index32().data_ptr(), _native.idx_bits(row_ptr), E,
                      ctypes.byref(mlp), dscore.data_ptr(), dweights.data_ptr(), ptrs,
                      ws.data_ptr(), ws_bytes.value, _native.stream_of(col_idx))
         grads = _segment_grads(graph, roles, dsegs, ctx.shapes, ctx.needs_input_grad, 4)
-        grads += _layer_grads(chain, dweights, W, ctx.has_bias, ctx.needs_input_grad,
+        grads += _layer_grads(chain, dweights, W, ctx.present, ctx.needs_input_grad,
                               4 + ctx.n_seg, len(chain))
         return (None, None, None, None, *grads)
 
 
-def _layer_grads(chain, dweights, W, has_bias, needs, first, layers):
-    """Weight and bias gradients of the module's own parameters from the
-    folded blocks' sums (_unfolded_grads)."""
+def _layer_grads(chain, dweights, W, present, needs, first, layers):
+    """Gradients of the module's own parameters (per layer: Linear weight and
+    bias, LayerNorm weight and bias) from the folded blocks' sums
+    (_unfolded_grads; d gamma = c d gamma', d beta = c d beta' for the scalar
+    map c y + d after the LayerNorm)."""
     grads = []
     for l in range(layers):
         layer = chain[l]
         out_f, in_f = layer.linear.out_features, layer.linear.in_features
-        k = first + 2 * l
+        j = _PER_LAYER * l
+        k = first + j
         blk = dweights[l]
         grads += list(_unfolded_grads(layer, blk[:W * W].view(W, W)[:out_f, :in_f],
                                       blk[W * W:W * W + out_f], needs[k],
-                                      has_bias[l] and needs[k + 1]))
+                                      present[j + 1] and needs[k + 1]))
+        dg = db = None
+        if layer.norm is not None:
+            if present[j + 2] and needs[k + 2]:
+                dg = blk[W * W + W:W * W + W + out_f] * layer.norm_scale
+            if present[j + 3] and needs[k + 3]:
+                db = blk[W * W + 2 * W:W * W + 2 * W + out_f] * layer.norm_scale
+        grads += [dg, db]
     return grads
 
 
@@ -528,9 +578,7 @@ class SegmentSoftmaxFunction(torch.autograd.Function):
 
 def nn_attention(graph: Graph, chain, roles, fields, value: torch.Tensor) -> torch.Tensor:
     """out[i] = sum_e softmax_i(net(fields_e)) value[col[e]] on the HIP path."""
-    params = []
-    for layer in chain:
-        params += [layer.linear.weight, layer.linear.bias]
+    params = _layer_params(chain)
     scores = EdgeMlpFunction.apply(graph, chain, tuple(roles), len(fields), *fields, *params)
     alpha = SegmentSoftmaxFunction.apply(scores, graph)
     return CsrSumFunction.apply(value, alpha, graph)
@@ -615,7 +663,8 @@ class EdgeMlpSumFunction(torch.autograd.Function):
     (tgx_edge_mlp_backward_seeded).
 
     Inputs after (graph, chain, roles, n_seg): the n_seg field tensors, then
-    weight and bias (None allowed) of every Linear layer."""
+    per layer the Linear weight and bias and the LayerNorm weight and bias
+    (None allowed; the last layer has no LayerNorm)."""
 
     @staticmethod
     def forward(ctx, graph: Graph, chain, roles, n_seg: int, *tensors):
@@ -628,7 +677,7 @@ class EdgeMlpSumFunction(torch.autograd.Function):
         in_width = sum(x.shape[1] for x in segs)
         W = _padded_width(chain, in_width, vector=True)
         hw = chain[-1].linear.in_features
-        buf = torch.zeros(L, W * W + W, dtype=torch.float32, device=dev)
+        buf = torch.zeros(L, _block_floats(chain, W), dtype=torch.float32, device=dev)
         _fill_weights(buf, chain, params, W, L - 1)
         mlp = _mlp_struct(chain, roles, segs, buf, W)
         hidden = torch.empty(max(E, 1), hw, dtype=torch.float32, device=dev)[:E]
@@ -636,13 +685,14 @@ class EdgeMlpSumFunction(torch.autograd.Function):
                      _native.idx_bits(row_ptr), E, ctypes.byref(mlp), hidden.data_ptr(), hw,
                      _native.stream_of(col_idx))
         sums = _reduce_rows(graph, hidden)
-        w_last, b_last = _folded(chain[-1], params[2 * L - 2], params[2 * L - 1])
+        w_last, b_last = _folded(chain[-1], params[_PER_LAYER * (L - 1)],
+                                 params[_PER_LAYER * (L - 1) + 1])
         out = sums @ w_last.t()
         if b_last is not None:
             out = out + _row_degrees(graph)[:, None] * b_last
         ctx.graph, ctx.chain, ctx.roles, ctx.n_seg, ctx.W = graph, chain, roles, n_seg, W
         ctx.shapes = [t.shape for t in tensors[:n_seg]]
-        ctx.has_bias = [params[2 * l + 1] is not None for l in range(L)]
+        ctx.present = [t is not None for t in params]
         ctx.save_for_backward(buf, sums, w_last, *segs)
         return out
 
@@ -656,14 +706,15 @@ class EdgeMlpSumFunction(torch.autograd.Function):
         dout = dout.contiguous()
         needs = ctx.needs_input_grad
         last = chain[-1]
-        k_last = 4 + ctx.n_seg + 2 * (L - 1)
-        need_w, need_b = needs[k_last], ctx.has_bias[L - 1] and needs[k_last + 1]
+        k_last = 4 + ctx.n_seg + _PER_LAYER * (L - 1)
+        need_w = needs[k_last]
+        need_b = ctx.present[_PER_LAYER * (L - 1) + 1] and needs[k_last + 1]
         dwf = (dout.t() @ sums) if need_w else None
         dbf = (_row_degrees(graph)[:, None] * dout).sum(0) \
             if need_b or (need_w and last.in_shift != 0.0) else None
         d_w_last, d_b_last = _unfolded_grads(last, dwf, dbf, need_w, need_b)
         grads = [None] * ctx.n_seg
-        grads += [None] * (2 * (L - 1))
+        grads += [None] * (_PER_LAYER * (L - 1))
         upstream = any(needs[4:k_last])
         if upstream:
             seed = (dout @ w_last).contiguous()
@@ -675,7 +726,7 @@ class EdgeMlpSumFunction(torch.autograd.Function):
             _native.call("tgx_edge_mlp_backward_workspace", E, ctypes.byref(mlp),
                          ctypes.byref(ws_bytes))
             ws = torch.empty(max(ws_bytes.value, 4), dtype=torch.uint8, device=dev)
-            dweights = torch.empty(L, W * W + W, dtype=torch.float32, device=dev)
+            dweights = torch.empty(L, buf.shape[1], dtype=torch.float32, device=dev)
             ptrs = (ctypes.c_void_p * 4)(*[d.data_ptr() for d in dsegs],
                                          *([None] * (4 - len(dsegs))))
             _native.call("tgx_edge_mlp_backward_seeded", col_idx.data_ptr(),
@@ -683,13 +734,11 @@ class EdgeMlpSumFunction(torch.autograd.Function):
                          ctypes.byref(mlp), seed.data_ptr(), hw, dweights.data_ptr(), ptrs,
                          ws.data_ptr(), ws_bytes.value, _native.stream_of(col_idx))
             grads = _segment_grads(graph, roles, dsegs, ctx.shapes, needs, 4)
-            grads += _layer_grads(chain, dweights, W, ctx.has_bias, needs, 4 + ctx.n_seg, L - 1)
-        return (None, None, None, None, *grads, d_w_last, d_b_last)
+            grads += _layer_grads(chain, dweights, W, ctx.present, needs, 4 + ctx.n_seg, L - 1)
+        return (None, None, None, None, *grads, d_w_last, d_b_last, None, None)
 
 
 def nn_message_sum(graph: Graph, chain, roles, fields) -> torch.Tensor:
     """out[i] = sum_e net(fields_e) over row i's edges on the HIP path."""
-    params = []
-    for layer in chain:
-        params += [layer.linear.weight, layer.linear.bias]
+    params = _layer_params(chain)
     return EdgeMlpSumFunction.apply(graph, chain, tuple(roles), len(fields), *fields, *params)

@@ -526,6 +526,15 @@ class MessagePassing(Kernel):
         return widths, tuple(roles)
 
     @staticmethod
+    def _nn_params_ok(layer, device) -> bool:
+        """A layer's Linear and LayerNorm parameters are fp32 on `device`."""
+        params = [layer.linear.weight, layer.linear.bias]
+        if layer.norm is not None:
+            params += [layer.norm.weight, layer.norm.bias]
+        return all(p is None or (p.dtype == torch.float32 and p.device == device)
+                   for p in params)
+
+    @staticmethod
     def _scaled_chain(chain, out_scale):
         """The chain with a scalar applied to its output folded into its last
         layer."""
@@ -555,9 +564,8 @@ class MessagePassing(Kernel):
             return None
         device = graph.device
         for layer in chain:
-            for p in (layer.linear.weight, layer.linear.bias):
-                if p is not None and (p.dtype != torch.float32 or p.device != device):
-                    return None
+            if not self._nn_params_ok(layer, device):
+                return None
         _native.lib()
         out_scale = item.out_scale
 
@@ -606,9 +614,10 @@ class MessagePassing(Kernel):
         if value is None or value.dtype != torch.float32:
             return None
         for layer in chain:
-            for p in (layer.linear.weight, layer.linear.bias):
-                if p is not None and (p.dtype != torch.float32 or p.device != value.device):
-                    return None
+            if not self._nn_params_ok(layer, value.device):
+                return None
+        if any(l.norm is not None for l in chain) and _ops._padded_width(chain, sum(widths)) > 32:
+            return None     # LayerNorm kernels cover padded widths up to 32
         _native.lib()
         roles = tuple(roles)
 

@@ -18,12 +18,14 @@ exact gelu, elu, hardtanh / relu6 / clamp, softplus, selu, mish,
 hardsigmoid, hardswish, exp, log, sqrt, rsqrt, abs, sin, cos, square,
 ``c / x``, ``x ** p``; module, functional or Tensor-method form;
 ``nn.Identity`` is skipped), whose output may again be scaled and shifted by
-constants (folded into the next Linear layer's input), at most three Linear
-layers.  A score network ends in a Linear layer with one output and every
-width is at most 64; an edge-network message summed per row (``tg.sum()``)
-ends in a Linear layer of any width and its other widths are at most 32.
-Anything else (LayerNorm, two functions in a row, ...) runs on the eager
-evaluator.
+constants (folded into the next Linear layer's input), and optionally by a
+feature-wise ``nn.LayerNorm`` between a hidden Linear layer and its function
+(constants between the two folded into its weight and bias), at most three
+Linear layers.  A score network ends in a Linear layer with one output and
+every width is at most 64 (32 with a LayerNorm); an edge-network message
+summed per row (``tg.sum()``) ends in a Linear layer of any width and its
+other widths are at most 32.  Anything else (two functions in a row, a
+LayerNorm after the last Linear layer, ...) runs on the eager evaluator.
 """
 
 from __future__ import annotations
@@ -53,7 +55,8 @@ class ScoreLayer:
     """One Linear layer of a chain: the scalar affine map on its input
     (in_scale * a + in_shift, from arithmetic after the previous
     activation), the one folded after it, z = scale * (W a' + b) + shift,
-    and the activation that follows."""
+    an optional LayerNorm over z followed by the scalar map norm_scale * y +
+    norm_shift, and the activation that follows."""
 
     linear: nn.Linear
     act: str = "identity"
@@ -63,6 +66,9 @@ class ScoreLayer:
     shift: float = 0.0
     in_scale: float = 1.0
     in_shift: float = 0.0
+    norm: nn.LayerNorm | None = None
+    norm_scale: float = 1.0
+    norm_shift: float = 0.0
 
 
 class TracedModule(nn.Module):
@@ -232,10 +238,11 @@ def _scalar_affine(t, a, kwargs, previous):
 
 
 def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
-    """Linear [affine]* [act] ... Linear [affine]*, via torch.fx (reference
-    nn_capture.py:281-380 translates the same graphs).  A scalar affine map
-    directly after a Linear layer folds into that layer's output, one after
-    an activation into the next Linear layer's input."""
+    """Linear [affine]* [LayerNorm [affine]*] [act [affine]*] ... Linear
+    [affine]*, via torch.fx (reference nn_capture.py:281-380 translates the
+    same graphs).  A scalar affine map directly after a Linear layer folds
+    into that layer's output, one after a LayerNorm into its gamma and beta,
+    one after an activation into the next Linear layer's input."""
     import torch.fx
 
     if isinstance(module, nn.Linear):
@@ -269,8 +276,20 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
             if isinstance(target, nn.Linear):
                 layers.append({"linear": target, "act": None, "param": 0.0, "param2": 0.0,
                                "scale": 1.0, "shift": 0.0, "in_scale": pending[0],
-                               "in_shift": pending[1]})
+                               "in_shift": pending[1], "norm": None, "norm_scale": 1.0,
+                               "norm_shift": 0.0})
                 pending = (1.0, 0.0)
+                previous = node
+                continue
+            if isinstance(target, nn.LayerNorm):
+                # Feature-wise LayerNorm of a Linear layer's output, before
+                # its activation.
+                if not layers or layers[-1]["act"] is not None or \
+                        layers[-1]["norm"] is not None:
+                    raise NotImplementedError("LayerNorm only directly after a Linear layer")
+                if tuple(target.normalized_shape) != (layers[-1]["linear"].out_features,):
+                    raise NotImplementedError("LayerNorm over other than the layer's features")
+                layers[-1]["norm"] = target
                 previous = node
                 continue
             act = _module_activation(target)
@@ -287,7 +306,12 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
                 c, b = affine
                 if not layers:
                     raise NotImplementedError("scalar arithmetic before the first Linear")
-                if layers[-1]["act"] is None:
+                if layers[-1]["act"] is None and layers[-1]["norm"] is not None:
+                    # Between a LayerNorm and the activation: folded into the
+                    # LayerNorm's gamma and beta.
+                    layers[-1]["norm_scale"] *= c
+                    layers[-1]["norm_shift"] = c * layers[-1]["norm_shift"] + b
+                elif layers[-1]["act"] is None:
                     # Directly after a Linear: folded into that layer.
                     layers[-1]["scale"] *= c
                     layers[-1]["shift"] = c * layers[-1]["shift"] + b
@@ -307,6 +331,8 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
         raise NotImplementedError("networks have one to three Linear layers")
     if layers[-1]["act"] is not None:
         raise NotImplementedError("the chain must end in a Linear layer")
+    if layers[-1]["norm"] is not None:
+        raise NotImplementedError("LayerNorm after the last Linear layer")
     for a, b in zip(layers, layers[1:]):
         if a["linear"].out_features != b["linear"].in_features:
             raise NotImplementedError("network widths do not chain")
@@ -315,7 +341,8 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
     if max(widths) > 64:
         raise NotImplementedError("network widths above 64")
     return tuple(ScoreLayer(l["linear"], l["act"] or "identity", l["param"], l["param2"],
-                            l["scale"], l["shift"], l["in_scale"], l["in_shift"])
+                            l["scale"], l["shift"], l["in_scale"], l["in_shift"], l["norm"],
+                            l["norm_scale"], l["norm_shift"])
                  for l in layers)
 
 
