@@ -47,12 +47,20 @@ def _included_sources(src: Path) -> list[Path]:
     return [CSRC / n for n in names]
 
 
+# The edge-MLP translation units take minutes each (most of the build):
+# they start first.
+_SLOW_FIRST = ("tgx_nn_math.hip", "tgx_nn_math_i64.hip", "tgx_nn.hip", "tgx_nn_i64.hip",
+               "tgx_nn_wide_math.hip", "tgx_nn_wide.hip")
+
+
 def sources() -> list[Path]:
-    """Every source, the largest (with what it includes) first: the
-    kernel-heavy files take minutes and should start before the rest."""
-    def size(src: Path) -> int:
-        return sum(f.stat().st_size for f in [src, *_included_sources(src)])
-    return sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")], key=lambda f: (-size(f), f.name))
+    """Every source: the slow edge-MLP units first, then the largest (with
+    what it includes) first."""
+    def key(src: Path):
+        size = sum(f.stat().st_size for f in [src, *_included_sources(src)])
+        slow = _SLOW_FIRST.index(src.name) if src.name in _SLOW_FIRST else len(_SLOW_FIRST)
+        return (slow, -size, src.name)
+    return sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")], key=key)
 
 
 def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Path:

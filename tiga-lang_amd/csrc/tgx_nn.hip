@@ -42,6 +42,14 @@
 // (TGX_NN_MATH 1) the tgx_edge_mlp_*_math functions they call for chains
 // that use exp, log, abs, sin, cos, a power or LayerNorm (the segment
 // softmax entry points are built here only).
+// Each tier is also split by column index type, so the halves compile in
+// parallel: built directly, this file holds the int32_t kernels and the
+// entry points; tgx_nn_i64.hip (and tgx_nn_math_i64.hip) build it with
+// TGX_NN_INDEX 64 for the int64_t kernels alone.
+#ifndef TGX_NN_INDEX
+#define TGX_NN_INDEX 32
+#endif
+
 #if TGX_NN_MATH
 #define TGX_NN_ENTRY(name) int name##_math
 #define TGX_TO_MATH(mlp, call)
@@ -696,11 +704,13 @@ template <typename I, int W>
 void launch_fwd(int L, const I* col, const int32_t* dst, int64_t E, const MlpView& v,
                 float* scores, hipStream_t s) {
   const int64_t blocks = ceil_div(E, 256);
-  if (L == 1) edge_mlp_fwd_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, v, scores);
+  if constexpr (!TGX_NN_MATH)   // one layer: no function, never the second set
+    if (L == 1) edge_mlp_fwd_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, v, scores);
   if (L == 2) edge_mlp_fwd_kernel<I, W, 2><<<blocks, 256, 0, s>>>(col, dst, E, v, scores);
   if (L == 3) edge_mlp_fwd_kernel<I, W, 3><<<blocks, 256, 0, s>>>(col, dst, E, v, scores);
 }
 
+#if TGX_NN_INDEX == 64
 // Blocks of edge_mlp_bwd_kernel<int64_t, W, L> resident on the current
 // device at once: per CU, the smaller of what the 160 KB of LDS and the 512
 // registers per SIMD lane allow (each 256-thread block puts one wave on each
@@ -739,22 +749,26 @@ int64_t bwd_resident_blocks() {
   return known;
 }
 
-int64_t resident_blocks(int W, int L) {
-  if (W == 16) return L == 1 ? bwd_resident_blocks<16, 1>() : L == 2 ? bwd_resident_blocks<16, 2>()
-                                                                       : bwd_resident_blocks<16, 3>();
-  if (W == 24) return L == 1 ? bwd_resident_blocks<24, 1>() : L == 2 ? bwd_resident_blocks<24, 2>()
-                                                                       : bwd_resident_blocks<24, 3>();
-  return L == 1 ? bwd_resident_blocks<32, 1>() : L == 2 ? bwd_resident_blocks<32, 2>()
-                                                          : bwd_resident_blocks<32, 3>();
+int64_t resident_blocks_any(int W, int L) {
+  if constexpr (!TGX_NN_MATH) {
+    if (L == 1)
+      return W == 16 ? bwd_resident_blocks<16, 1>()
+                     : W == 24 ? bwd_resident_blocks<24, 1>() : bwd_resident_blocks<32, 1>();
+  }
+  if (W == 16) return L <= 2 ? bwd_resident_blocks<16, 2>() : bwd_resident_blocks<16, 3>();
+  if (W == 24) return L <= 2 ? bwd_resident_blocks<24, 2>() : bwd_resident_blocks<24, 3>();
+  return L <= 2 ? bwd_resident_blocks<32, 2>() : bwd_resident_blocks<32, 3>();
 }
+#endif
 
 template <typename I, int W, bool SEED>
 void launch_bwd(int L, const I* col, const int32_t* dst, int64_t E, int blocks, int64_t chunk,
                 const MlpView& v, const float* ds, float* partial, const float* seed, int hw,
                 hipStream_t s) {
-  if (L == 1)
-    edge_mlp_bwd_kernel<I, W, 1, SEED><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds,
-                                                              partial, seed, hw);
+  if constexpr (!TGX_NN_MATH)
+    if (L == 1)
+      edge_mlp_bwd_kernel<I, W, 1, SEED><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds,
+                                                                partial, seed, hw);
   if (L == 2)
     edge_mlp_bwd_kernel<I, W, 2, SEED><<<blocks, 256, 0, s>>>(col, dst, E, chunk, v, ds,
                                                               partial, seed, hw);
@@ -767,7 +781,8 @@ template <typename I, int W>
 void launch_hidden(int L, const I* col, const int32_t* dst, int64_t E, const MlpView& v,
                    float* hidden, int hw, hipStream_t s) {
   const int64_t blocks = ceil_div(E, 256);
-  if (L == 1) edge_mlp_hidden_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, v, hidden, hw);
+  if constexpr (!TGX_NN_MATH)
+    if (L == 1) edge_mlp_hidden_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, v, hidden, hw);
   if (L == 2) edge_mlp_hidden_kernel<I, W, 2><<<blocks, 256, 0, s>>>(col, dst, E, v, hidden, hw);
   if (L == 3) edge_mlp_hidden_kernel<I, W, 3><<<blocks, 256, 0, s>>>(col, dst, E, v, hidden, hw);
 }
@@ -800,13 +815,43 @@ void dispatch_hidden(int W, int L, const I* col, const int32_t* dst, int64_t E, 
 
 // Width of the last layer's input: the previous layer's real output, or the
 // concatenated input of a one-layer network.
-int last_input_width(const tgx_edge_mlp* mlp, const MlpView& v) {
+[[maybe_unused]] int last_input_width(const tgx_edge_mlp* mlp, const MlpView& v) {
   return mlp->n_layers > 1 ? v.n_out[mlp->n_layers - 2] : v.in_width;
 }
 
-
 }  // namespace
+
+// The launches for this build's column index type (declared in
+// tgx_nn_common.h).
+namespace mlp {
+using IndexT = std::conditional<TGX_NN_INDEX == 64, int64_t, int32_t>::type;
+
+void TGX_TIER(mlp_fwd)(int W, int L, const IndexT* col, const int32_t* dst, int64_t E,
+                       const MlpView& v, float* scores, hipStream_t s) {
+  dispatch_fwd(W, L, col, dst, E, v, scores, s);
+}
+
+void TGX_TIER(mlp_hidden)(int W, int L, const IndexT* col, const int32_t* dst, int64_t E,
+                          const MlpView& v, float* hidden, int hw, hipStream_t s) {
+  dispatch_hidden(W, L, col, dst, E, v, hidden, hw, s);
+}
+
+void TGX_TIER(mlp_bwd)(bool seeded, int W, int L, const IndexT* col, const int32_t* dst,
+                       int64_t E, int blocks, int64_t chunk, const MlpView& v, const float* ds,
+                       float* partial, const float* seed, int hw, hipStream_t s) {
+  if (seeded)
+    dispatch_bwd<IndexT, true>(W, L, col, dst, E, blocks, chunk, v, ds, partial, s, seed, hw);
+  else
+    dispatch_bwd<IndexT, false>(W, L, col, dst, E, blocks, chunk, v, ds, partial, s);
+}
+
+#if TGX_NN_INDEX == 64
+int64_t TGX_TIER(mlp_bwd_resident)(int W, int L) { return resident_blocks_any(W, L); }
+#endif
+}  // namespace mlp
 }  // namespace tgx
+
+#if TGX_NN_INDEX == 32
 
 using namespace tgx;
 
@@ -825,11 +870,11 @@ TGX_NN_ENTRY(tgx_edge_mlp_scores)(const void* col, const int32_t* dst_index, int
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("edge_mlp_fwd_kernel", s);
   if (idx_bits == 32)
-    dispatch_fwd(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col), dst_index,
-                 n_edges, v, scores, s);
+    tgx::mlp::TGX_TIER(mlp_fwd)(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col),
+                                dst_index, n_edges, v, scores, s);
   else
-    dispatch_fwd(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col), dst_index,
-                 n_edges, v, scores, s);
+    tgx::mlp::TGX_TIER(mlp_fwd)(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col),
+                                dst_index, n_edges, v, scores, s);
   TGX_LAUNCHED("edge_mlp_fwd_kernel");
   return TGX_OK;
 }
@@ -847,7 +892,7 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward_workspace)(int64_t n_edges, const tgx_edge_ml
   const int blocks = n_edges == 0 ? 0
                      : mlp->width == 64
                          ? TGX_TIER(outer_blocks)(n_edges, &chunk)
-                         : mlp_bwd_blocks(n_edges, resident_blocks(mlp->width, mlp->n_layers),
+                         : mlp_bwd_blocks(n_edges, tgx::mlp::TGX_TIER(mlp_bwd_resident)(mlp->width, mlp->n_layers),
                                           &chunk);
   size_t planes = 0;
   if (mlp->width == 64)
@@ -891,7 +936,7 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, i
   const int blocks =
       mlp->width == 64
           ? TGX_TIER(outer_blocks)(n_edges, &chunk)
-          : mlp_bwd_blocks(n_edges, resident_blocks(mlp->width, mlp->n_layers), &chunk);
+          : mlp_bwd_blocks(n_edges, tgx::mlp::TGX_TIER(mlp_bwd_resident)(mlp->width, mlp->n_layers), &chunk);
   const size_t part_bytes = align_up(static_cast<size_t>(blocks) * n * sizeof(float));
   const size_t slice_bytes = align_up(static_cast<size_t>(kColSlices) * n * sizeof(float));
   float* partial = static_cast<float*>(workspace);
@@ -906,11 +951,13 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, i
   } else {
     TGX_PROFILE("edge_mlp_bwd_kernel", s);
     if (idx_bits == 32)
-      dispatch_bwd(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col), dst_index,
-                   n_edges, blocks, chunk, v, dscore, partial, s);
+      tgx::mlp::TGX_TIER(mlp_bwd)(false, mlp->width, mlp->n_layers,
+                                  static_cast<const int32_t*>(col), dst_index, n_edges, blocks,
+                                  chunk, v, dscore, partial, nullptr, 0, s);
     else
-      dispatch_bwd(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col), dst_index,
-                   n_edges, blocks, chunk, v, dscore, partial, s);
+      tgx::mlp::TGX_TIER(mlp_bwd)(false, mlp->width, mlp->n_layers,
+                                  static_cast<const int64_t*>(col), dst_index, n_edges, blocks,
+                                  chunk, v, dscore, partial, nullptr, 0, s);
     TGX_LAUNCHED("edge_mlp_bwd_kernel");
   }
   {
@@ -1030,11 +1077,11 @@ TGX_NN_ENTRY(tgx_edge_mlp_hidden)(const void* col, const int32_t* dst_index, int
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("edge_mlp_hidden_kernel", s);
   if (idx_bits == 32)
-    dispatch_hidden(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col), dst_index,
-                    n_edges, v, hidden, hidden_width, s);
+    tgx::mlp::TGX_TIER(mlp_hidden)(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col),
+                                   dst_index, n_edges, v, hidden, hidden_width, s);
   else
-    dispatch_hidden(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col), dst_index,
-                    n_edges, v, hidden, hidden_width, s);
+    tgx::mlp::TGX_TIER(mlp_hidden)(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col),
+                                   dst_index, n_edges, v, hidden, hidden_width, s);
   TGX_LAUNCHED("edge_mlp_hidden_kernel");
   return TGX_OK;
 }
@@ -1078,20 +1125,20 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward_seeded)(const void* col, const int32_t* dst_i
                   workspace_bytes >= need,
               "workspace too small");
   int64_t chunk = 0;
-  const int blocks = mlp_bwd_blocks(n_edges, resident_blocks(mlp->width, mlp->n_layers), &chunk);
+  const int blocks = mlp_bwd_blocks(n_edges, tgx::mlp::TGX_TIER(mlp_bwd_resident)(mlp->width, mlp->n_layers), &chunk);
   const size_t part_bytes = align_up(static_cast<size_t>(blocks) * n * sizeof(float));
   float* partial = static_cast<float*>(workspace);
   float* slices = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
   {
     TGX_PROFILE("edge_mlp_bwd_seeded_kernel", s);
     if (idx_bits == 32)
-      dispatch_bwd<int32_t, true>(mlp->width, mlp->n_layers, static_cast<const int32_t*>(col),
-                                  dst_index, n_edges, blocks, chunk, v, nullptr, partial, s,
-                                  seed, seed_width);
+      tgx::mlp::TGX_TIER(mlp_bwd)(true, mlp->width, mlp->n_layers,
+                                  static_cast<const int32_t*>(col), dst_index, n_edges, blocks,
+                                  chunk, v, nullptr, partial, seed, seed_width, s);
     else
-      dispatch_bwd<int64_t, true>(mlp->width, mlp->n_layers, static_cast<const int64_t*>(col),
-                                  dst_index, n_edges, blocks, chunk, v, nullptr, partial, s,
-                                  seed, seed_width);
+      tgx::mlp::TGX_TIER(mlp_bwd)(true, mlp->width, mlp->n_layers,
+                                  static_cast<const int64_t*>(col), dst_index, n_edges, blocks,
+                                  chunk, v, nullptr, partial, seed, seed_width, s);
     TGX_LAUNCHED("edge_mlp_bwd_seeded_kernel");
   }
   {
@@ -1104,3 +1151,5 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward_seeded)(const void* col, const int32_t* dst_i
   }
   return TGX_OK;
 }
+
+#endif  // TGX_NN_INDEX == 32

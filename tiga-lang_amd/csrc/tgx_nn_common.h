@@ -634,6 +634,30 @@ inline bool uses_math_tier(const tgx_edge_mlp* mlp) {
   return false;
 }
 
+// The edge-MLP kernel launches per column index type: tgx_nn.hip builds the
+// int32_t ones (with the entry points), tgx_nn_i64.hip the int64_t ones and
+// the occupancy query (separately per tier, TGX_TIER).
+void TGX_TIER(mlp_fwd)(int W, int L, const int32_t* col, const int32_t* dst, int64_t E,
+                       const MlpView& v, float* scores, hipStream_t s);
+void TGX_TIER(mlp_fwd)(int W, int L, const int64_t* col, const int32_t* dst, int64_t E,
+                       const MlpView& v, float* scores, hipStream_t s);
+void TGX_TIER(mlp_hidden)(int W, int L, const int32_t* col, const int32_t* dst, int64_t E,
+                          const MlpView& v, float* hidden, int hw, hipStream_t s);
+void TGX_TIER(mlp_hidden)(int W, int L, const int64_t* col, const int32_t* dst, int64_t E,
+                          const MlpView& v, float* hidden, int hw, hipStream_t s);
+// seeded: the edge-network sum's backward (seed per destination row, hw
+// wide) in place of the score gradient ds.
+void TGX_TIER(mlp_bwd)(bool seeded, int W, int L, const int32_t* col, const int32_t* dst,
+                       int64_t E, int blocks, int64_t chunk, const MlpView& v, const float* ds,
+                       float* partial, const float* seed, int hw, hipStream_t s);
+void TGX_TIER(mlp_bwd)(bool seeded, int W, int L, const int64_t* col, const int32_t* dst,
+                       int64_t E, int blocks, int64_t chunk, const MlpView& v, const float* ds,
+                       float* partial, const float* seed, int hw, hipStream_t s);
+// Blocks of the fused backward kernel (W <= 32) resident on the current
+// device, from the int64_t instance's occupancy; it sizes the grid (and the
+// workspace) of both index types.
+int64_t TGX_TIER(mlp_bwd_resident)(int W, int L);
+
 // 64-wide chains: backward in two passes (tgx_nn_wide.hip).  Blocks and
 // chunk of the outer-sum pass for n_edges edges.
 int TGX_TIER(outer_blocks)(int64_t n_edges, int64_t* chunk);

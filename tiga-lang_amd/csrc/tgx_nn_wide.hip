@@ -177,7 +177,8 @@ int planes_bwd_t(int L, const I* col, const int32_t* dst, int64_t E, const MlpVi
   const int64_t blocks = ceil_div(E, 256);
   {
     TGX_PROFILE("edge_mlp_bwd_kernel", s);
-    if (L == 1) edge_mlp_planes_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, v, ds, acts, dz);
+    if constexpr (!TGX_NN_MATH)   // one layer: no function, never the second set
+      if (L == 1) edge_mlp_planes_kernel<I, W, 1><<<blocks, 256, 0, s>>>(col, dst, E, v, ds, acts, dz);
     if (L == 2) edge_mlp_planes_kernel<I, W, 2><<<blocks, 256, 0, s>>>(col, dst, E, v, ds, acts, dz);
     if (L == 3) edge_mlp_planes_kernel<I, W, 3><<<blocks, 256, 0, s>>>(col, dst, E, v, ds, acts, dz);
     TGX_LAUNCHED("edge_mlp_planes_kernel");
