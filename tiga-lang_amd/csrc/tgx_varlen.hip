@@ -141,22 +141,33 @@ struct Stage {
   vec8<T> a[N], b[N];
 };
 
+// Row strides (elements) of the staged tensors stay below this, so a row's
+// byte offset inside a 64-row block is one 24-bit multiply (checked by the
+// entry points).
+constexpr int64_t kMaxRowStride = (int64_t{1} << 24) / 8;
+
+// The block's first row is a uniform address; each chunk is a 32-bit byte
+// offset from it (local row x row bytes + column bytes, one v_mad_u32_u24),
+// so the loads take the scalar-base form and no 64-bit address arithmetic
+// runs per block.
 template <typename T, int D, bool CLAMP>
 __device__ __forceinline__ void stage_load(Stage<T, D>& st, const T* xa, int64_t sa,
                                            const T* xb, int64_t sb, int base, int end) {
   constexpr int CPR = D / 8;   // 16-byte chunks per row
+  const char* ta = reinterpret_cast<const char*>(xa + static_cast<int64_t>(base) * sa);
+  const char* tb = reinterpret_cast<const char*>(xb + static_cast<int64_t>(base) * sb);
+  const uint32_t rba = static_cast<uint32_t>(sa) * sizeof(T);
+  const uint32_t rbb = static_cast<uint32_t>(sb) * sizeof(T);
+  const int last = end - 1 - base;   // last local row inside the tensor
 #pragma unroll
   for (int it = 0; it < Stage<T, D>::N; ++it) {
     const int idx = threadIdx.x + 256 * it;
-    const int row = base + idx / CPR;
-    const int dc = (idx % CPR) * 8;
-    if (CLAMP) {
-      const int64_t r = min(row, end - 1);
-      st.a[it] = ld8(xa + r * sa + dc);
-      st.b[it] = ld8(xb + r * sb + dc);
-    } else if (row < end) {
-      st.a[it] = ld8(xa + static_cast<int64_t>(row) * sa + dc);
-      st.b[it] = ld8(xb + static_cast<int64_t>(row) * sb + dc);
+    const int r = idx / CPR;
+    const uint32_t cb = static_cast<uint32_t>(idx % CPR) * 16;
+    if (CLAMP || r <= last) {
+      const uint32_t rr = static_cast<uint32_t>(CLAMP ? min(r, last) : r);
+      st.a[it] = *reinterpret_cast<const vec8<T>*>(ta + (__umul24(rr, rba) + cb));
+      st.b[it] = *reinterpret_cast<const vec8<T>*>(tb + (__umul24(rr, rbb) + cb));
     } else {
       st.a[it] = vec8<T>{};
       st.b[it] = vec8<T>{};
@@ -247,10 +258,8 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
   const int kv_end = CAUSAL ? min(q0 + VBM, ks1) : ks1;
   const int n_kv = (kv_end - ks0 + VBN - 1) / VBN;
   const float sl2 = a.scale_log2;
-  // Running max in scaled log2 units (-inf until a score is seen); lp is this
-  // lane's share of the softmax denominator.
+  // Running max in scaled log2 units (-inf until a score is seen).
   float m[2] = {kNegInf, kNegInf};
-  float lp[2] = {0.f, 0.f};
   // Last key each query row may see (padded rows past the block use the
   // last key, their output is discarded).
   int qlim[2];
@@ -262,6 +271,14 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) o[dt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  // The softmax denominators: a row of ones times P^T on the MFMA (four
+  // products per key tile in place of 32 adds per lane), every element of
+  // lsum[qt] the sum over the tile's keys for query lr.  The sum is of the
+  // same rounded weights that multiply V.
+  f32x4v lsum[2] = {f32x4v{0.f, 0.f, 0.f, 0.f}, f32x4v{0.f, 0.f, 0.f, 0.f}};
+  vec8<T> ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = static_cast<T>(1.f);
   // Running max over the whole workgroup tile (PRUNE), scaled log2 units.
   float block_m = kNegInf;
 
@@ -343,7 +360,7 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
         for (int qt = 0; qt < 2; ++qt) {
           const float mn = fmaxf(m[qt], mt[qt]);
           const float alpha = mn == kNegInf ? 1.f : exp2_hw(m[qt] - mn);
-          lp[qt] *= alpha;
+          lsum[qt] *= alpha;
           m[qt] = mn;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) o[dt][qt] *= alpha;
@@ -354,15 +371,10 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
       for (int qt = 0; qt < 2; ++qt) {
         const float mo = m[qt] == kNegInf ? 0.f : m[qt];
         float p[4][4];
-        float rs = 0.f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[kt][r] = exp2_hw(c[kt][qt][r] * sl2 - mo);
-            rs += p[kt][r];
-          }
-        lp[qt] += rs;
+          for (int r = 0; r < 4; ++r) p[kt][r] = exp2_hw(c[kt][qt][r] * sl2 - mo);
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
@@ -381,17 +393,19 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
 #pragma unroll
           for (int qt = 0; qt < 2; ++qt) o[dt][qt] = mfma(vf, pf[qt][k2], o[dt][qt]);
         }
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) lsum[qt] = mfma(ones, pf[qt][k2], lsum[qt]);
       }
       __builtin_amdgcn_s_setprio(0);
     }
     if (more) stage_store<T, D>(stage, ks[buf ^ 1], vs[buf ^ 1]);
   }
 
-  // Finalize: l summed over the 4 lane groups, O = O^T / l, natural-log lse
-  // (a row that sees no key gets 0 and -inf).
+  // Finalize: O = O^T / l, natural-log lse (a row that sees no key gets 0
+  // and -inf).
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    const float l = group4_sum(lp[qt]);
+    const float l = lsum[qt][0];
     const int qq = qb + 16 * qt + lr;
     if (qq >= qs1) continue;
     const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -754,6 +768,12 @@ int check_shape(const AttnShape& s) {
   }
   TGX_REQUIRE(s.H > 0 && s.n_q >= 0 && s.n_k >= 0, "bad sizes");
   TGX_REQUIRE(s.qsn > 0 && s.qsh > 0 && s.ksn > 0 && s.ksh > 0, "strides must be positive");
+  if (s.qsn >= kMaxRowStride || s.ksn >= kMaxRowStride ||
+      static_cast<int64_t>(s.H) * s.D >= kMaxRowStride) {
+    set_error("dense attention tiles need token strides below %lld elements",
+              static_cast<long long>(kMaxRowStride));
+    return TGX_UNSUPPORTED;
+  }
   TGX_REQUIRE(s.n_q < (int64_t{1} << 31) && s.n_k < (int64_t{1} << 31),
               "token counts must fit int32");
   return TGX_OK;
