@@ -210,14 +210,16 @@ def test_weights_updated_in_place_between_steps():
 
 
 def test_uncovered_networks_fall_back_or_refuse():
-    """A LayerNorm after an activation or in a chain wider than 32, or widths
-    above 64, are not covered: strict mode refuses, otherwise the eager
-    evaluator runs them (reference fail-closed rungs)."""
+    """Chains needing more than three layers (identity layers counted), a
+    LayerNorm in a chain wider than 32, or widths above 64, are not covered:
+    strict mode refuses, otherwise the eager evaluator runs them (reference
+    fail-closed rungs)."""
     n = 50
     rp, col = random_graph(n, n, 4, 5)
     graph = tg.Graph.from_csr(rp, col, num_src=n)
     x = torch.randn(n, 4, device=DEV)
-    for net in (nn.Sequential(nn.Linear(8, 8), nn.ReLU(), nn.LayerNorm(8), nn.Linear(8, 1)),
+    for net in (nn.Sequential(nn.Linear(8, 8), nn.ReLU(), nn.Linear(8, 8), nn.ReLU(),
+                              nn.LayerNorm(8), nn.Linear(8, 1)),
                 nn.Sequential(nn.Linear(8, 40), nn.LayerNorm(40), nn.ReLU(), nn.Linear(40, 1)),
                 nn.Sequential(nn.Linear(8, 100), nn.ReLU(), nn.Linear(100, 1))):
         net = net.to(DEV)

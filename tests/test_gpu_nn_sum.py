@@ -77,7 +77,7 @@ class ThreeLayer(nn.Module):
             return self.c(-self.b(h).cos())
         if self.kind == "powers":
             h = self.a(x).abs()
-            return self.c(2.0 / (self.b(h) * 0.1 + 3.0))
+            return self.c(2.0 / (self.b(h) * 0.5 + 3.0))
         h = self.a(x)
         h = h * h
         h = (self.b(h) * 0.1 + 2.0) ** 1.5
@@ -102,8 +102,25 @@ class Normed(nn.Module):
         return self.c(torch.tanh(self.nb(self.b(h))) - 0.25)
 
 
+class TwoFunctions(nn.Module):
+    """Two functions in a row (an identity layer between them)."""
+
+    def __init__(self, i, h, o):
+        super().__init__()
+        self.a, self.b = nn.Linear(i, h), nn.Linear(h, o)
+
+    def forward(self, x):
+        return self.b(torch.exp(torch.sin(self.a(x)) * 0.5))
+
+
 def nets(i):
     return {
+        # Identity layers: a function after the last Linear layer, LayerNorm
+        # before the first, two functions in a row.
+        "act-last": nn.Sequential(nn.Linear(i, 12), nn.ReLU(), nn.Linear(12, 5), nn.Sigmoid()),
+        "norm-first": nn.Sequential(nn.LayerNorm(i), nn.Linear(i, 8), nn.Tanh(),
+                                    nn.Linear(8, 3)),
+        "two-functions": TwoFunctions(i, 10, 4),
         "layernorm-3": Normed(i, 12, 7, 3),
         # 64-wide score chains (the two-pass backward) with the second set of
         # functions; as edge-network sums these run eager (wider than 32).
@@ -174,7 +191,7 @@ def test_edge_network_sum_against_float64_autograd(name, idx):
 @pytest.mark.parametrize("name", ["mish-selu-3", "hard-3", "relu6-hardtanh", "affine-softplus",
                                   "exp-log", "roots", "trig", "powers", "squares",
                                   "layernorm-3", "layernorm-2", "layernorm-32", "wide-trig",
-                                  "wide-powers"])
+                                  "wide-powers", "act-last", "norm-first", "two-functions"])
 def test_nn_attention_wider_op_set_against_float64_autograd(name):
     print(f"nn attention {name}", flush=True)
     N = 2000

@@ -132,6 +132,42 @@ class Normed(nn.Module):
         return self.c(h)
 
 
+class TwoFunctions(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b = nn.Linear(5, 4), nn.Linear(4, 1)
+
+    def forward(self, x):
+        return self.b(torch.exp(torch.sin(self.a(x))))
+
+
+class ShiftAtEnd(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a = nn.Linear(5, 4)
+
+    def forward(self, x):
+        return torch.exp(self.a(x)) + 1.0
+
+
+class Rounded(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a, self.b = nn.Linear(5, 4), nn.Linear(4, 1)
+
+    def forward(self, x):
+        return self.b(torch.div(self.a(x), 2.0, rounding_mode="floor"))
+
+
+class Before(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.a = nn.Linear(5, 1)
+
+    def forward(self, x):
+        return self.a(x * 2.0)
+
+
 NETS = {
     "exp-log": (ExpLog, [("exp", 0.0), ("log", 0.0), ("identity", 0.0)]),
     "roots": (Roots, [("sqrt", 0.0), ("rsqrt", 0.0), ("identity", 0.0)]),
@@ -143,6 +179,20 @@ NETS = {
     "layernorm-sequential": (lambda: nn.Sequential(nn.Linear(5, 10), nn.LayerNorm(10),
                                                    nn.ReLU(), nn.Linear(10, 1)),
                              [("relu", 0.0), ("identity", 0.0)]),
+    # Identity layers: two functions in a row, arithmetic and a function after
+    # the last Linear layer, arithmetic before the first, LayerNorm after a
+    # function and before the first Linear layer.
+    "two-functions": (lambda: TwoFunctions(), [("sin", 0.0), ("exp", 0.0), ("identity", 0.0)]),
+    "shift-at-end": (lambda: ShiftAtEnd(), [("exp", 0.0), ("identity", 0.0)]),
+    "before": (lambda: Before(), [("identity", 0.0)]),
+    "norm-after-act": (lambda: nn.Sequential(nn.Linear(5, 6), nn.ReLU(), nn.LayerNorm(6),
+                                             nn.Linear(6, 1)),
+                       [("relu", 0.0), ("identity", 0.0), ("identity", 0.0)]),
+    "norm-first": (lambda: nn.Sequential(nn.LayerNorm(5), nn.Linear(5, 4), nn.Sigmoid()),
+                   [("identity", 0.0), ("sigmoid", 0.0), ("identity", 0.0)]),
+    "norm-last": (lambda: nn.Sequential(nn.Linear(5, 4), nn.ReLU(), nn.Linear(4, 2),
+                                        nn.LayerNorm(2)),
+                  [("relu", 0.0), ("identity", 0.0), ("identity", 0.0)]),
     "sequential": (lambda: nn.Sequential(nn.Linear(5, 8), nn.Softplus(2.0), nn.Linear(8, 8),
                                          nn.ELU(0.5), nn.Linear(8, 1)),
                    [("softplus", 2.0), ("elu", 0.5), ("identity", 0.0)]),
@@ -196,9 +246,11 @@ def test_capture_codes_and_folded_chain_match_the_module(name):
     # gets a zero bias in its place.
     dout = torch.randn_like(expect)
     present = [p is not None for p in params]
-    grads = torch.autograd.grad(net(x), [p for p in params if p is not None], dout)
+    # Identity layers' weights are fixed (no gradient; not module parameters).
+    trained = [p is not None and p.requires_grad for p in params]
+    grads = torch.autograd.grad(net(x), [p for p, t in zip(params, trained) if t], dout)
     grads = iter(grads)
-    expect_grads = [next(grads) if ok else None for ok in present]
+    expect_grads = [next(grads) if t else None for t in trained]
     leaves = []
     for layer, (w, b, g, beta) in zip(chain, folded):
         b = torch.zeros(w.shape[0], dtype=torch.float64) if b is None else b
@@ -221,8 +273,7 @@ def test_capture_codes_and_folded_chain_match_the_module(name):
         if dg is not None:
             dweights[l, W * W + W:W * W + W + o] = dg
             dweights[l, W * W + 2 * W:W * W + 2 * W + o] = dbeta
-    needs = [True] * (4 * len(chain))
-    got_grads = _ops._layer_grads(chain, dweights, W, present, needs, 0, len(chain))
+    got_grads = _ops._layer_grads(chain, dweights, W, present, trained, 0, len(chain))
     for k, (g, e) in enumerate(zip(got_grads, expect_grads)):
         assert (g is None) == (e is None), k
         if e is not None:
@@ -246,51 +297,19 @@ def test_affine_maps_fold_into_the_right_layer():
     assert chain[1].norm is not None and chain[1].norm.eps == 1e-3
 
 
-class TwoFunctions(nn.Module):
-    def __init__(self):
-        super().__init__()
-        self.a, self.b = nn.Linear(4, 4), nn.Linear(4, 1)
-
-    def forward(self, x):
-        return self.b(torch.exp(torch.sin(self.a(x))))
-
-
-class ShiftAtEnd(nn.Module):
-    def __init__(self):
-        super().__init__()
-        self.a = nn.Linear(4, 4)
-
-    def forward(self, x):
-        return torch.exp(self.a(x)) + 1.0
-
-
-class Rounded(nn.Module):
-    def __init__(self):
-        super().__init__()
-        self.a, self.b = nn.Linear(4, 4), nn.Linear(4, 1)
-
-    def forward(self, x):
-        return self.b(torch.div(self.a(x), 2.0, rounding_mode="floor"))
-
-
-class Before(nn.Module):
-    def __init__(self):
-        super().__init__()
-        self.a = nn.Linear(4, 1)
-
-    def forward(self, x):
-        return self.a(x * 2.0)
-
-
-@pytest.mark.parametrize("net", [TwoFunctions, ShiftAtEnd, Rounded, Before,
+@pytest.mark.parametrize("net", [Rounded,
                                  lambda: nn.Sequential(nn.Linear(4, 4), nn.ReLU(),
-                                                       nn.LayerNorm(4), nn.Linear(4, 1)),
+                                                       nn.Linear(4, 4), nn.ReLU(),
+                                                       nn.Linear(4, 2), nn.LayerNorm(2)),
+                                 lambda: nn.Sequential(*[m for _ in range(4) for m in
+                                                         (nn.Linear(4, 4), nn.ReLU())]),
                                  lambda: nn.Sequential(nn.Linear(4, 4), nn.ReLU(),
-                                                       nn.Linear(4, 2), nn.LayerNorm(2))])
+                                                       nn.Tanh(), nn.Sigmoid(),
+                                                       nn.Linear(4, 1))])
 def test_uncovered_networks_are_refused(net):
-    """Two functions in a row, arithmetic after the last activation, a
-    rounding division, arithmetic before the first Linear, a LayerNorm after
-    an activation or after the last Linear layer: not captured (the eager
+    """A rounding division, or chains that need more than three layers with
+    the identity layers counted (a LayerNorm after the last Linear layer,
+    four Linear layers, three functions in a row): not captured (the eager
     evaluator runs them)."""
     with pytest.raises(NotImplementedError):
         _extract_chain(net())

@@ -18,14 +18,15 @@ exact gelu, elu, hardtanh / relu6 / clamp, softplus, selu, mish,
 hardsigmoid, hardswish, exp, log, sqrt, rsqrt, abs, sin, cos, square,
 ``c / x``, ``x ** p``; module, functional or Tensor-method form;
 ``nn.Identity`` is skipped), whose output may again be scaled and shifted by
-constants (folded into the next Linear layer's input), and optionally by a
-feature-wise ``nn.LayerNorm`` between a hidden Linear layer and its function
-(constants between the two folded into its weight and bias), at most three
-Linear layers.  A score network ends in a Linear layer with one output and
-every width is at most 64 (32 with a LayerNorm); an edge-network message
-summed per row (``tg.sum()``) ends in a Linear layer of any width and its
-other widths are at most 32.  Anything else (two functions in a row, a
-LayerNorm after the last Linear layer, ...) runs on the eager evaluator.
+constants (folded into the next Linear layer's input), and feature-wise
+``nn.LayerNorm`` (constants between it and the function folded into its
+weight and bias).  A function or LayerNorm with no Linear layer of its own
+in front -- two in a row, one before the first Linear layer or after the
+last -- gets a fixed identity Linear layer, and the kernels take at most
+three layers in all.  A score network ends with one output and every width
+is at most 64 (32 with a LayerNorm); an edge-network message summed per row
+(``tg.sum()``) may be of any width, its other widths at most 32.  Anything
+else runs on the eager evaluator.
 """
 
 from __future__ import annotations
@@ -237,23 +238,26 @@ def _scalar_affine(t, a, kwargs, previous):
     return None
 
 
-def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
-    """Linear [affine]* [LayerNorm [affine]*] [act [affine]*] ... Linear
-    [affine]*, via torch.fx (reference nn_capture.py:281-380 translates the
-    same graphs).  A scalar affine map directly after a Linear layer folds
-    into that layer's output, one after a LayerNorm into its gamma and beta,
-    one after an activation into the next Linear layer's input."""
+def _identity_linear(n: int, like: torch.Tensor) -> nn.Linear:
+    """A fixed n x n identity Linear layer (no bias, no gradient) on like's
+    device and dtype: inserted where the chain has a function or LayerNorm
+    with no Linear layer of its own in front (or after the last one)."""
+    layer = nn.Linear(n, n, bias=False, device=like.device, dtype=like.dtype)
+    with torch.no_grad():
+        layer.weight.copy_(torch.eye(n, device=like.device, dtype=like.dtype))
+    layer.weight.requires_grad_(False)
+    return layer
+
+
+def _chain_ops(module: nn.Module) -> list[tuple[str, object]]:
+    """The module's fx graph as a list of ("linear", nn.Linear), ("norm",
+    nn.LayerNorm), ("act", (name, param, param2)) and ("affine", (c, b))
+    steps of a single-input chain."""
     import torch.fx
 
-    if isinstance(module, nn.Linear):
-        # A bare Linear traced as the root shows its functional body.
-        if max(module.in_features, module.out_features) > 64:
-            raise NotImplementedError("network widths above 64")
-        return (ScoreLayer(module),)
     gm = torch.fx.symbolic_trace(module)
-    layers: list[dict] = []
+    ops: list[tuple[str, object]] = []
     previous = None
-    pending = (1.0, 0.0)   # affine map after the last activation, for the next Linear
     for node in gm.graph.nodes:
         if node.op == "placeholder":
             if previous is not None:
@@ -263,36 +267,24 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
         if node.op == "output":
             if node.args[0] is not previous:
                 raise NotImplementedError("network output is not the chain's end")
-            if pending != (1.0, 0.0):
-                raise NotImplementedError("scalar arithmetic after the last activation")
             break
         if node.op == "call_module":
             target = gm.get_submodule(node.target)
             if node.args != (previous,):
                 raise NotImplementedError("networks must be single-input chains")
             if isinstance(target, nn.Identity):
-                previous = node
-                continue
-            if isinstance(target, nn.Linear):
-                layers.append({"linear": target, "act": None, "param": 0.0, "param2": 0.0,
-                               "scale": 1.0, "shift": 0.0, "in_scale": pending[0],
-                               "in_shift": pending[1], "norm": None, "norm_scale": 1.0,
-                               "norm_shift": 0.0})
-                pending = (1.0, 0.0)
-                previous = node
-                continue
-            if isinstance(target, nn.LayerNorm):
-                # Feature-wise LayerNorm of a Linear layer's output, before
-                # its activation.
-                if not layers or layers[-1]["act"] is not None or \
-                        layers[-1]["norm"] is not None:
-                    raise NotImplementedError("LayerNorm only directly after a Linear layer")
-                if tuple(target.normalized_shape) != (layers[-1]["linear"].out_features,):
-                    raise NotImplementedError("LayerNorm over other than the layer's features")
-                layers[-1]["norm"] = target
-                previous = node
-                continue
-            act = _module_activation(target)
+                pass
+            elif isinstance(target, nn.Linear):
+                ops.append(("linear", target))
+            elif isinstance(target, nn.LayerNorm):
+                if len(target.normalized_shape) != 1:
+                    raise NotImplementedError("feature-wise LayerNorm only")
+                ops.append(("norm", target))
+            else:
+                act = _module_activation(target)
+                if act is None:
+                    raise NotImplementedError(f"unsupported module {type(target).__name__}")
+                ops.append(("act", act))
         elif node.op in ("call_function", "call_method"):
             target = node.target
             if node.op == "call_method":
@@ -303,39 +295,85 @@ def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
                     raise NotImplementedError(f"unsupported method {node.target}")
             affine = _scalar_affine(target, node.args, node.kwargs, previous)
             if affine is not None:
-                c, b = affine
-                if not layers:
-                    raise NotImplementedError("scalar arithmetic before the first Linear")
-                if layers[-1]["act"] is None and layers[-1]["norm"] is not None:
-                    # Between a LayerNorm and the activation: folded into the
-                    # LayerNorm's gamma and beta.
-                    layers[-1]["norm_scale"] *= c
-                    layers[-1]["norm_shift"] = c * layers[-1]["norm_shift"] + b
-                elif layers[-1]["act"] is None:
-                    # Directly after a Linear: folded into that layer.
-                    layers[-1]["scale"] *= c
-                    layers[-1]["shift"] = c * layers[-1]["shift"] + b
-                else:
-                    # After an activation: folded into the next Linear's input.
-                    pending = (c * pending[0], c * pending[1] + b)
-                previous = node
-                continue
-            act = _function_activation(target, node.args, node.kwargs, previous)
+                ops.append(("affine", affine))
+            else:
+                act = _function_activation(target, node.args, node.kwargs, previous)
+                if act is None:
+                    raise NotImplementedError(f"unsupported function {node.target}")
+                ops.append(("act", act))
         else:
             raise NotImplementedError(f"unsupported network node {node.op}")
-        if act is None or not layers or layers[-1]["act"] is not None:
-            raise NotImplementedError("activations must follow a Linear layer, one each")
-        layers[-1]["act"], layers[-1]["param"], layers[-1]["param2"] = act
         previous = node
-    if not layers or len(layers) > 3:
-        raise NotImplementedError("networks have one to three Linear layers")
-    if layers[-1]["act"] is not None:
-        raise NotImplementedError("the chain must end in a Linear layer")
-    if layers[-1]["norm"] is not None:
-        raise NotImplementedError("LayerNorm after the last Linear layer")
-    for a, b in zip(layers, layers[1:]):
-        if a["linear"].out_features != b["linear"].in_features:
-            raise NotImplementedError("network widths do not chain")
+    return ops
+
+
+def _extract_chain(module: nn.Module) -> tuple[ScoreLayer, ...]:
+    """The kernels' chain of layers, each Linear [LayerNorm] [function], for
+    a single-input network of Linear layers, component-wise functions,
+    feature-wise LayerNorms and scalar arithmetic (via torch.fx; reference
+    nn_capture.py:281-380 translates the same graphs).  A scalar affine map
+    directly after a Linear layer folds into that layer's output, one after
+    a LayerNorm into its gamma and beta, one after a function (or before the
+    first Linear layer) into the next Linear layer's input.  A function or
+    LayerNorm with no Linear layer of its own in front (two in a row, one
+    before the first Linear layer or after the last) gets a fixed identity
+    Linear layer; at most three layers in all."""
+    if isinstance(module, nn.Linear):
+        # A bare Linear traced as the root shows its functional body.
+        if max(module.in_features, module.out_features) > 64:
+            raise NotImplementedError("network widths above 64")
+        return (ScoreLayer(module),)
+    ops = _chain_ops(module)
+    linears = [m for kind, m in ops if kind == "linear"]
+    if not linears:
+        raise NotImplementedError("networks have at least one Linear layer")
+    like = linears[0].weight
+    width = linears[0].in_features      # features flowing between the steps
+    layers: list[dict] = []
+    pending = (1.0, 0.0)   # affine map for the next layer's input
+
+    def add_layer(linear):
+        nonlocal pending
+        layers.append({"linear": linear, "act": None, "param": 0.0, "param2": 0.0,
+                       "scale": 1.0, "shift": 0.0, "in_scale": pending[0],
+                       "in_shift": pending[1], "norm": None, "norm_scale": 1.0,
+                       "norm_shift": 0.0})
+        pending = (1.0, 0.0)
+
+    for kind, op in ops:
+        if kind == "linear":
+            if op.in_features != width:
+                raise NotImplementedError("network widths do not chain")
+            add_layer(op)
+            width = op.out_features
+        elif kind == "affine":
+            c, b = op
+            last = layers[-1] if layers else None
+            if last is not None and last["act"] is None and last["norm"] is not None:
+                last["norm_scale"] *= c
+                last["norm_shift"] = c * last["norm_shift"] + b
+            elif last is not None and last["act"] is None:
+                last["scale"] *= c
+                last["shift"] = c * last["shift"] + b
+            else:
+                pending = (c * pending[0], c * pending[1] + b)
+        elif kind == "norm":
+            if tuple(op.normalized_shape) != (width,):
+                raise NotImplementedError("LayerNorm over other than the stream's features")
+            if not layers or layers[-1]["act"] is not None or layers[-1]["norm"] is not None \
+                    or pending != (1.0, 0.0):
+                add_layer(_identity_linear(width, like))
+            layers[-1]["norm"] = op
+        else:   # a component-wise function
+            if not layers or layers[-1]["act"] is not None or pending != (1.0, 0.0):
+                add_layer(_identity_linear(width, like))
+            layers[-1]["act"], layers[-1]["param"], layers[-1]["param2"] = op
+    if layers[-1]["act"] is not None or layers[-1]["norm"] is not None or \
+            pending != (1.0, 0.0):
+        # The chain must end in a Linear layer without LayerNorm or function.
+        add_layer(_identity_linear(width, like))
+    if len(layers) > 3:
+        raise NotImplementedError("networks have one to three layers (identity layers counted)")
     widths = [l["linear"].in_features for l in layers] + \
         [l["linear"].out_features for l in layers[:-1]]
     if max(widths) > 64:
