@@ -332,3 +332,15 @@ def test_operator_forms_are_the_same_codes():
 
         chain = _extract_chain(Net())
         assert (chain[0].act, chain[0].param) == code
+
+
+def test_trace_accepts_the_reference_launch_geometry():
+    """tg.nn.trace(module, block_e=..., num_warps=...) as in the reference:
+    powers of two in [16, 1024] and [1, 16], else ValueError."""
+    import tiga as tg
+
+    net = nn.Linear(3, 1)
+    assert tg.nn.trace(net, block_e=64, num_warps=4).module is net
+    for kwargs in ({"block_e": 48}, {"block_e": 8}, {"num_warps": 32}, {"num_warps": 3}):
+        with pytest.raises(ValueError):
+            tg.nn.trace(net, **kwargs)

@@ -114,8 +114,21 @@ class TracedModule(nn.Module):
         return got
 
 
-def trace(module: nn.Module) -> TracedModule:
-    """Wrap ``module`` for use inside ``MessagePassing.edge``."""
+def _check_geometry(name: str, value, low: int, high: int) -> None:
+    if value is not None and (value < low or value > high or value & (value - 1)):
+        raise ValueError(f"{name} must be a power of two in [{low}, {high}], got {value}")
+
+
+def trace(module: nn.Module, *, block_e: int | None = None,
+          num_warps: int | None = None) -> TracedModule:
+    """Wrap ``module`` for use inside ``MessagePassing.edge`` (reference
+    compiler/nn_capture.py:418-428).  ``block_e`` and ``num_warps`` are the
+    reference's launch geometry for its tiles (edges per program, warps);
+    they are checked as the reference checks them and otherwise unused: the
+    HIP kernels here run one edge per lane with their own geometry, and
+    geometry never changes numerics."""
+    _check_geometry("block_e", block_e, 16, 1024)
+    _check_geometry("num_warps", num_warps, 1, 16)
     if isinstance(module, TracedModule):
         return module
     if not isinstance(module, nn.Module):
