@@ -5,7 +5,7 @@ Public names follow the reference package (python/tiga/__init__.py:45-66):
 """
 
 from . import interop, nn, reducer
-from .graph import Graph
+from .graph import Graph, GraphSchema
 from .kernel import CompiledVariant, Kernel
 from .message_passing import MessagePassing, config
 from .reducer import (
@@ -23,6 +23,7 @@ __version__ = "0.1.0"
 __all__ = [
     "CompiledVariant",
     "Graph",
+    "GraphSchema",
     "Kernel",
     "MessagePassing",
     "OnlineSoftmaxItem",
@@ -30,6 +31,7 @@ __all__ = [
     "Reducer",
     "ReducerCall",
     "SumReducer",
+    "__version__",
     "config",
     "interop",
     "nn",
