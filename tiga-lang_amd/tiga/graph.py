@@ -32,12 +32,22 @@ CHUNK_EDGES = 512
 
 @dataclass(frozen=True)
 class GraphSchema:
+    """What a relation is, independent of its index values (reference
+    interop/torch/graph.py:51-70); every relation here is static (built
+    once, not regenerated per call like the reference's radius and kNN
+    relations)."""
+
     num_src: int
     num_dst: int
     origin: str
     realization: str
     index_dtype: torch.dtype
     sorted_by_dst: bool = True
+    lifecycle: str = "static"
+
+    def specialization_key(self) -> tuple[object, ...]:
+        return (self.num_src, self.num_dst, self.origin, self.lifecycle, self.realization,
+                str(self.index_dtype), self.sorted_by_dst)
 
 
 class RowPlanHandle:
@@ -654,8 +664,17 @@ class Graph:
         return reference_plan(self._schema.num_dst, maximum, total, histogram,
                               has_node_epilogue)
 
+    def __repr__(self) -> str:
+        # The reference's summary line (interop/torch/graph.py:1444-1478).
+        s = self._schema
+        return (f"Graph(origin={s.origin}, lifecycle={s.lifecycle}, "
+                f"realization={s.realization}, src={s.num_src:,}, dst={s.num_dst:,}, "
+                f"edges={self.num_edges:,}, device={self.device})")
+
     def explain(self) -> str:
-        lines = [f"relation: {self._schema.realization}",
+        """The reference's summary line, then this provider's row plan and
+        the reference planner's decision once a HIP launch has built them."""
+        lines = [repr(self), f"relation: {self._schema.realization}",
                  f"num_src: {self._schema.num_src}", f"num_dst: {self._schema.num_dst}"]
         plan = self._native_cache.get(("plan", WAVE_MAX, CHUNK_EDGES))
         if plan is not None:
