@@ -265,3 +265,28 @@ def test_raw_score_softmax_known_answer_on_cpu_eager():
     np.testing.assert_allclose(out.detach().numpy(), g["out"], atol=5e-6, rtol=0)
     np.testing.assert_allclose(dscore.numpy(), g["dscore"], atol=5e-6, rtol=0)
     np.testing.assert_allclose(dvalue.numpy(), g["dvalue"], atol=5e-6, rtol=0)
+
+
+def test_kernel_observability_surface_matches_the_reference():
+    """ir("domain"), code(), diagnostics and schedules (reference
+    kernel/model.py:113-195) on an eager-path call."""
+    import tiga.kernel as tk
+
+    class Copy(tg.MessagePassing):
+        reducer = tg.sum()
+
+        def edge(self, src, dst, edge):
+            return src.x
+
+    g = tg.Graph.from_csr(torch.tensor([0, 1, 2]), torch.tensor([1, 0]), num_src=2)
+    k = Copy()
+    k(graph=g, src={"x": torch.ones(2, 3)}, dst={})
+    assert "backend:" in k.ir("domain") and k.ir() == k.ir("domain-plan")
+    with pytest.raises(KeyError):
+        k.ir("gf.kernel")
+    with pytest.raises(KeyError):
+        k.code()
+    assert all(isinstance(f, tk.AnalysisFinding) for f in k.diagnostics)
+    assert k.schedules == ()
+    with pytest.raises(ValueError):
+        tk.AnalysisFinding("planning", "maybe", "x")
