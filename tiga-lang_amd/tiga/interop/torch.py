@@ -234,4 +234,8 @@ def register_message_passing(kernel, *, graph, src: Mapping[str, Any], dst: Mapp
     return registered
 
 
-__all__ = ["RegisteredMessagePassingOp", "register_message_passing"]
+# The reference's interop.torch.Graph is the Torch-backed relation, which
+# here is tiga.Graph itself.
+from ..graph import Graph  # noqa: E402
+
+__all__ = ["Graph", "RegisteredMessagePassingOp", "register_message_passing"]
