@@ -358,7 +358,9 @@ int tgx_dot_attn_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
 /* ------------------------------------------------------------------------ */
 
 /* Host: the work list of one attention launch, in dispatch order.  A task is
- * four int32 (block, first row, head, 0) naming `block` rows of one head:
+ * four int32 (block, first row, head, tile0) naming `block` rows of one
+ * head, tile0 the first stored dS tile of (block, head) for
+ * tgx_attn_bwd_stored (0 when tgx_attn_ds_tiles refuses the relation):
  * kind 0: query tiles (block 128, forward and dQ), work = keys seen;
  * kind 1: key tiles (block 64, dK/dV), work = queries that see the tile.
  * Every tile of one (block, head) goes to the same XCD (workgroup i runs on
@@ -406,6 +408,26 @@ int tgx_attn_bwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
                  const void* out_dev, const float* lse_dev, const void* dout_dev,
                  float scale, void* dq_dev, void* dk_dev, void* dv_dev, float* delta_dev,
                  int64_t n_q, int64_t n_k, int H, int D, void* stream);
+
+/* Host: the stored dS tiles of a backward (64 x 64 elements of the q/k/v
+ * dtype each; per (block, head) the tiles qi >= kj of a causal block, all
+ * of a non-causal one).  TGX_UNSUPPORTED past 2^31 tiles. */
+int tgx_attn_ds_tiles(const int32_t* cu_q_host, const int32_t* cu_k_host, int n_blocks, int H,
+                      int causal, int64_t* n_tiles);
+
+/* tgx_attn_bwd with dS stored: the dK/dV kernel also writes every dS tile
+ * to ds_dev (tgx_attn_ds_tiles x 64 x 64 elements, the task lists' tile0
+ * offsets), and the dQ kernel reads them back instead of recomputing S and
+ * dP (one product per tile instead of three).  Same results up to the
+ * rounding of S computed as Q K^T instead of K Q^T. */
+int tgx_attn_bwd_stored(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
+                        const int32_t* q_tasks_dev, int64_t n_q_tasks,
+                        const int32_t* k_tasks_dev, int64_t n_k_tasks, int causal, int dtype,
+                        const void* q_dev, const void* k_dev, const void* v_dev,
+                        const int64_t* strides, const void* out_dev, const float* lse_dev,
+                        const void* dout_dev, float scale, void* dq_dev, void* dk_dev,
+                        void* dv_dev, float* delta_dev, void* ds_dev, int64_t n_q, int64_t n_k,
+                        int H, int D, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* nn-scored edge attention: score_e = MLP(concat of gathered fields),       */

@@ -75,13 +75,20 @@ class VarlenAttention(tg.MessagePassing):
         return self.reducer(score, src.value)
 
 
+@pytest.mark.parametrize("stored", [True, False])
 @pytest.mark.parametrize("lengths,H", [
     ([1, 5, 17, 64, 65, 128, 129, 300, 2], 2),
     ([384, 1, 96, 640, 57], 4),
     ([700, 129], 16),
 ])
-def test_varlen_fwd_bwd_through_api(lengths, H):
-    print(f"varlen api lengths={lengths} H={H}", flush=True)
+def test_varlen_fwd_bwd_through_api(lengths, H, stored, monkeypatch):
+    """Both backward forms: dS stored by the dK/dV pass and read back by the
+    dQ pass (tgx_attn_bwd_stored), and S/dP recomputed (tgx_attn_bwd)."""
+    from tiga import _ops
+
+    print(f"varlen api lengths={lengths} H={H} stored={stored}", flush=True)
+    if not stored:
+        monkeypatch.setattr(_ops, "STORED_DS_MAX_BYTES", 0)
     tg.config.strict = True
     try:
         cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
@@ -108,3 +115,28 @@ def test_varlen_fwd_bwd_through_api(lengths, H):
         assert rel_err(f(v.grad), e_dv) <= 2e-2
     finally:
         tg.config.strict = False
+
+
+def test_stored_and_recomputed_backward_agree(monkeypatch):
+    """dK/dV are the same computation either way (bit-identical); dQ differs
+    only by the rounding of S = Q K^T against S^T = K Q^T."""
+    from tiga import _ops
+
+    lengths, H, D = [1, 63, 64, 65, 200, 517], 4, 128
+    print(f"stored vs recomputed dS lengths={lengths}", flush=True)
+    rng = np.random.default_rng(7)
+    T = sum(lengths)
+    base = [torch.as_tensor(rng.standard_normal((T, H, D)), device=DEV).to(torch.bfloat16)
+            for _ in range(4)]
+    graph = tg.Graph.cat([tg.Graph.triangular(L, device=DEV) for L in lengths])
+    grads = []
+    for limit in (_ops.STORED_DS_MAX_BYTES, 0):
+        monkeypatch.setattr(_ops, "STORED_DS_MAX_BYTES", limit)
+        q, k, v = (t.clone().requires_grad_(True) for t in base[:3])
+        out = VarlenAttention()(graph=graph, src={"key": k, "value": v}, dst={"query": q},
+                                scale=D ** -0.5)
+        out.backward(base[3])
+        grads.append((q.grad.float(), k.grad.float(), v.grad.float()))
+    (dq1, dk1, dv1), (dq0, dk0, dv0) = grads
+    assert torch.equal(dk1, dk0) and torch.equal(dv1, dv0)
+    assert float((dq1 - dq0).abs().max() / dq0.abs().max()) <= 1e-2

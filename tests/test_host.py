@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_native.exported_symbols())
-    assert lib.tgx_abi_version() == 6
+    assert lib.tgx_abi_version() == 7
     assert lib.tgx_status_string(1) == b"invalid argument"
 
 
@@ -276,7 +276,17 @@ def test_attn_tasks_cover_once_grouped_per_xcd(kind, block, causal, rect):
     expect = sorted((b, r0, h) for b in range(len(rows) - 1) for h in range(H)
                     for r0 in range(rows[b], rows[b + 1], block))
     assert sorted(map(tuple, real[:, :3].tolist())) == expect
-    assert (real[:, 3] == 0).all()
+    # tile0: the first stored dS tile of (block, head) (tgx_attn_ds_tiles).
+    nt = [(-(-(cu_q[b + 1] - cu_q[b]) // 64)) * (-(-(cu_q[b + 1] - cu_q[b]) // 64) + 1) // 2
+          if causal else -(-(cu_q[b + 1] - cu_q[b]) // 64) * -(-(cu_k[b + 1] - cu_k[b]) // 64)
+          for b in range(len(cu_q) - 1)]
+    base = np.concatenate([[0], np.cumsum(np.array(nt) * H)])
+    for b, _, h, t0 in real.tolist():
+        assert t0 == base[b] + h * nt[b]
+    n = ctypes.c_int64()
+    _native.call("tgx_attn_ds_tiles", cu_q.ctypes.data, cu_k.ctypes.data, len(cu_q) - 1, H,
+                 int(causal), ctypes.byref(n))
+    assert n.value == base[-1]
 
     def work(b, r0):
         q0, q1, k0, k1 = (int(x) for x in (cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]))

@@ -85,6 +85,23 @@ constexpr float kLn2 = 0.6931471805599453f;
 // runs on XCD i % 8.
 constexpr int kXcds = 8;
 
+// Stored dS (the dK/dV kernel writes it, the dQ kernel reads it back instead
+// of recomputing S and dP): 64 x 64 tiles per (block, head), query blocks qi
+// and key blocks kj of 64 rows from the block's start; a causal (square)
+// block keeps the tiles qi >= kj.  A tile is dS^T, row = key, 64 queries
+// per row: the dK/dV lanes hold runs of four queries of one key, and the dQ
+// kernel stages the rows in LDS and reads them down the key columns
+// (ds_read_b64_tr_b16), as it reads K^T.
+constexpr int kDsTile = 64 * 64;
+__host__ __device__ inline int64_t ds_tiles(int64_t lq, int64_t lk, bool causal) {
+  const int64_t nq = (lq + 63) / 64, nk = (lk + 63) / 64;
+  return causal ? nq * (nq + 1) / 2 : nq * nk;
+}
+__host__ __device__ inline int64_t ds_tile(int qi, int kj, int nk, bool causal) {
+  return causal ? static_cast<int64_t>(qi) * (qi + 1) / 2 + kj
+                : static_cast<int64_t>(qi) * nk + kj;
+}
+
 __device__ __forceinline__ f32x4v mfma(bf16x8 a, bf16x8 b, f32x4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -454,6 +471,7 @@ struct BwdArgs {
   T* dv;
   float scale;            // softmax scale
   float scale_log2;       // scale * log2(e)
+  T* ds;                  // stored dS tiles (null: the dQ kernel recomputes)
 };
 
 template <typename T, int D>
@@ -485,13 +503,19 @@ __global__ __launch_bounds__(256) void varlen_delta_kernel(const T* __restrict__
 }
 
 // dK/dV: workgroup = (64-key tile, head); wave w owns keys k0 + 16w .. +16.
-template <typename T, int D, bool CAUSAL>
+// STORE: dS of every (query block, key tile) also goes to a.ds, the tiles of
+// (block, head) from task[3].
+template <typename T, int D, bool CAUSAL, bool STORE>
 __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
   constexpr int KC = D / 32;
   constexpr int DT = D / 16;
+  constexpr int DSP = VBN + 8;   // row stride of the staged dS^T tile
   __shared__ T qs[VBN][TPAD];    // Q rows of the query block
   __shared__ T dos[VBN][TPAD];   // dO rows
   __shared__ float lse_s[VBN], del_s[VBN];
+  // STORE: the block's dS^T tile, written to a.ds in the next step (or after
+  // the loop) with full-row 16-byte stores.
+  __shared__ T dsw[STORE ? VBN : 1][STORE ? DSP : 1];
   const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
   const int blk = task[0];
   if (blk < 0) return;   // padding slot of a shorter XCD queue
@@ -532,24 +556,56 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
   // time and share it through L2.
   const int qstart = CAUSAL ? k0 : qs0;
   const int n_qb = (qs1 - qstart + VBN - 1) / VBN;
+  // Stored dS: this key tile's column of tiles, (qi, kj) for the blocks qi.
+  const int ks0 = a.cu_k[blk];
+  const int kj = (k0 - ks0) / VBN, nk = (ks1 - ks0 + VBN - 1) / VBN;
+  T* const ds_blk = STORE ? a.ds + static_cast<int64_t>(task[3]) * kDsTile : nullptr;
+  // The staged dS^T tile of query block qi (its 64 x 64 elements, thread t
+  // the 16-byte chunks t and t + 256) to its place in a.ds.
+  auto flush_ds = [&](int qi) {
+    T* tile = ds_blk + ds_tile(qi, kj, nk, CAUSAL) * kDsTile;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int row = c >> 3, col = 8 * (c & 7);
+      *reinterpret_cast<vec8<T>*>(tile + row * VBN + col) =
+          *reinterpret_cast<const vec8<T>*>(&dsw[row][col]);
+    }
+  };
+  // The block's Q/dO rows and its lse/delta are loaded one block ahead, all
+  // before this block's dS stores: a wait for them then never waits for
+  // the stores (vector memory counts complete in order).
   Stage<T, D> st;
-  if (n_qb > 0)
-    stage_load<T, D, false>(st, qh, a.qsn, doh, cs, qstart + (n_qb - 1) * VBN, qs1);
+  // Raw lse/delta of the next block's rows (rows past the block read the
+  // last row; replaced when stored to LDS, so no use of the loaded values
+  // comes before the stores).
+  float lse_n = 0.f, del_n = 0.f;
+  auto load_rows = [&](int qbase) {
+    stage_load<T, D, false>(st, qh, a.qsn, doh, cs, qbase, qs1);
+    if (threadIdx.x < VBN) {
+      const int64_t qq = min(qbase + static_cast<int>(threadIdx.x), qs1 - 1);
+      lse_n = a.lse[qq * a.H + h];
+      del_n = a.delta[qq * a.H + h];
+    }
+  };
+  if (n_qb > 0) load_rows(qstart + (n_qb - 1) * VBN);
   for (int step = 0; step < n_qb; ++step) {
     const int ib = n_qb - 1 - step;
     const int qbase = qstart + ib * VBN;
     __syncthreads();   // previous block's LDS reads are done
+    if constexpr (STORE) {
+      if (step > 0) flush_ds((qbase + VBN - qs0) / VBN);
+    }
     stage_store<T, D>(st, qs, dos);
     if (threadIdx.x < VBN) {
-      const int qq = qbase + threadIdx.x;
-      lse_s[threadIdx.x] = qq < qs1 ? a.lse[static_cast<int64_t>(qq) * a.H + h] * kLog2e
-                                    : __builtin_huge_valf();
-      del_s[threadIdx.x] = qq < qs1 ? a.delta[static_cast<int64_t>(qq) * a.H + h] : 0.f;
+      const bool ok = qbase + static_cast<int>(threadIdx.x) < qs1;
+      lse_s[threadIdx.x] = ok ? lse_n * kLog2e : __builtin_huge_valf();
+      del_s[threadIdx.x] = ok ? del_n : 0.f;
     }
     __syncthreads();
-    if (ib > 0) stage_load<T, D, false>(st, qh, a.qsn, doh, cs, qbase - VBN, qs1);
-    // Causal: a wave whose keys all exceed the block's last query skips it.
-    if (CAUSAL && k0 + 16 * wave > qbase + VBN - 1) continue;
+    if (ib > 0) load_rows(qbase - VBN);
+    // (Causal blocks start at the tile's first key, so every wave has a key
+    // at or before the block's last query: no wave skips a block.)
 
     // S = Q K^T, dP = dO V^T: C tiles [q = 16 qt + 4g + r][key].
     f32x4v sc[4], dp[4];
@@ -592,6 +648,19 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
       weights(std::true_type{});
     else
       weights(std::false_type{});
+    if constexpr (STORE) {
+      // dS^T row of this lane's key over the block's 64 queries, four
+      // consecutive queries per 8-byte LDS write (keys past the block: 0).
+      const bool kvalid = key < ks1;
+#pragma unroll
+      for (int qt = 0; qt < 4; ++qt) {
+        vec4<T> w;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          w[r] = kvalid ? sb[qt >> 1][4 * (qt & 1) + r] : static_cast<T>(0.f);
+        *reinterpret_cast<vec4<T>*>(&dsw[16 * wave + lr][16 * qt + 4 * g]) = w;
+      }
+    }
     // dV^T += dO^T P, dK^T += Q^T dS over the block's 64 queries.
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -605,6 +674,12 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
       }
     }
     __builtin_amdgcn_s_setprio(0);
+  }
+  if constexpr (STORE) {
+    if (n_qb > 0) {
+      __syncthreads();
+      flush_ds((qstart - qs0) / VBN);
+    }
   }
   if (key >= ks1) return;
   T* dkrow = a.dk + key * cs + h * D;
@@ -748,6 +823,152 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_kernel(BwdArgs<T> a) {
   }
 }
 
+// Staging of one 64-row block of one [N, H, D] tensor (K for the stored-dS
+// dQ kernel); rows past `end` zero-filled.
+template <typename T, int D>
+struct Stage1 {
+  static constexpr int N = D / 32;
+  vec8<T> a[N];
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void stage1_load(Stage1<T, D>& st, const T* x, int64_t sx, int base,
+                                            int end) {
+  constexpr int CPR = D / 8;
+  const char* t = reinterpret_cast<const char*>(x + static_cast<int64_t>(base) * sx);
+  const uint32_t rb = static_cast<uint32_t>(sx) * sizeof(T);
+  const int last = end - 1 - base;
+#pragma unroll
+  for (int it = 0; it < Stage1<T, D>::N; ++it) {
+    const int idx = threadIdx.x + 256 * it;
+    const int r = idx / CPR;
+    const uint32_t cb = static_cast<uint32_t>(idx % CPR) * 16;
+    st.a[it] = r <= last ? *reinterpret_cast<const vec8<T>*>(
+                               t + (__umul24(static_cast<uint32_t>(r), rb) + cb))
+                         : vec8<T>{};
+  }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void stage1_store(const Stage1<T, D>& st, T (*x)[TPAD]) {
+  constexpr int CPR = D / 8;
+#pragma unroll
+  for (int it = 0; it < Stage1<T, D>::N; ++it) {
+    const int idx = threadIdx.x + 256 * it;
+    *reinterpret_cast<vec8<T>*>(&x[idx / CPR][(idx % CPR) * 8]) = st.a[it];
+  }
+}
+
+// dQ from stored dS: workgroup = (128-query tile, head), wave w owns queries
+// q0 + 32w .. +32, i.e. rows 32 (w % 2) .. +32 of query block qi0 + w / 2.
+// Per 64-key tile: K and the two stored dS^T tiles (qi0, kj), (qi0 + 1, kj)
+// staged in LDS (loaded one tile ahead), then dQ^T += K^T dS^T with both
+// operands read down their key columns: one product per tile instead of
+// three.
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void varlen_dq_stored_kernel(BwdArgs<T> a) {
+  constexpr int DT = D / 16;
+  __shared__ T ks[VBN][TPAD];    // K rows of the key tile
+  __shared__ T dss[VBN][TPAD];   // dS^T rows: keys x the workgroup's 128 queries
+  const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
+  const int blk = task[0];
+  if (blk < 0) return;   // padding slot of a shorter XCD queue
+  const int q0 = task[1];
+  const int h = task[2];
+  const int qs0 = a.cu_q[blk], qs1 = a.cu_q[blk + 1];
+  const int ks0 = a.cu_k[blk], ks1 = a.cu_k[blk + 1];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, lr = lane & 15;
+  const int64_t cs = static_cast<int64_t>(a.H) * D;
+  const int qb = q0 + wave * 32;
+  const int qi0 = (q0 - qs0) / VBN;
+  const int nq = (qs1 - qs0 + VBN - 1) / VBN;
+  const int nk = (ks1 - ks0 + VBN - 1) / VBN;
+  const T* tiles = a.ds + static_cast<int64_t>(task[3]) * kDsTile;
+  f32x4v dqt[DT][2];   // dQ^T [d = 16 dt + 4g + r][q]
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) dqt[dt][qt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  const T* kh = a.k + h * a.ksh;
+  const int kv_end = CAUSAL ? min(q0 + VBM, ks1) : ks1;
+  const int n_kv = (kv_end - ks0 + VBN - 1) / VBN;
+  // Key tiles this wave has stored dS for (causal: those at or before its
+  // query block; none when its queries all lie past the block).
+  const int qi = qi0 + (wave >> 1);
+  const int n_own = qb >= qs1 ? 0 : CAUSAL ? min(n_kv, qi + 1) : n_kv;
+  // Staging of the two dS^T tiles: 2 x 64 rows x 128 B, four 16-byte
+  // chunks per thread (chunk c: tile c / 512, row (c % 512) / 8, column
+  // 8 (c % 8)); a tile that does not exist is zero-filled.
+  vec8<T> dstage[4];
+  auto ds_load = [&](int kj) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int t = c >> 9, row = (c & 511) >> 3, col = 8 * (c & 7);
+      const int tq = qi0 + t;
+      const bool ok = tq < nq && (!CAUSAL || kj <= tq);
+      dstage[i] = ok ? ld8(tiles + ds_tile(tq, kj, nk, CAUSAL) * kDsTile + row * VBN + col)
+                     : vec8<T>{};
+    }
+  };
+  auto ds_store = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int t = c >> 9, row = (c & 511) >> 3, col = 8 * (c & 7);
+      *reinterpret_cast<vec8<T>*>(&dss[row][VBN * t + col]) = dstage[i];
+    }
+  };
+  Stage1<T, D> st;
+  if (n_kv > 0) {
+    stage1_load<T, D>(st, kh, a.ksn, ks0, ks1);
+    ds_load(0);
+  }
+  const int c0 = 32 * wave;   // this wave's first query column in dss
+  for (int it = 0; it < n_kv; ++it) {
+    const int kbase = ks0 + it * VBN;
+    __syncthreads();
+    stage1_store<T, D>(st, ks);
+    ds_store();
+    __syncthreads();
+    if (it + 1 < n_kv) {
+      stage1_load<T, D>(st, kh, a.ksn, kbase + VBN, ks1);
+      ds_load(it + 1);
+    }
+    if (it >= n_own) continue;
+    // dQ^T += K^T dS^T (key rows past the block are zero in ks and dss).
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      vec8<T> sb[2];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) sb[qt] = tr_frag(dss, 32 * k2, c0 + 16 * qt, lr, g);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const vec8<T> kta = tr_frag(ks, 32 * k2, 16 * dt, lr, g);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) dqt[dt][qt] = mfma(kta, sb[qt], dqt[dt][qt]);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qq = qb + 16 * qt + lr;
+    if (qq >= qs1) continue;
+    T* row = a.dq + qq * cs + h * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      vec4<T> w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = static_cast<T>(dqt[dt][qt][r] * a.scale);
+      *reinterpret_cast<vec4<T>*>(row + 16 * dt + 4 * g) = w;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Launch helpers (dtype x head dim x causal x prune dispatch).
 
@@ -814,22 +1035,37 @@ int launch_bwd(const AttnShape& s, BwdArgs<T> a, const T* out, const int32_t* q_
     }
   }
   a.delta = delta;
+  const unsigned gk = static_cast<unsigned>(n_k_tasks), gq = static_cast<unsigned>(n_q_tasks);
   if (n_k_tasks > 0) {
     TGX_PROFILE("varlen_dkdv_kernel", stream);
     a.tasks = k_tasks;
-    if (s.causal)
-      varlen_dkdv_kernel<T, D, true><<<static_cast<unsigned>(n_k_tasks), 256, 0, stream>>>(a);
-    else
-      varlen_dkdv_kernel<T, D, false><<<static_cast<unsigned>(n_k_tasks), 256, 0, stream>>>(a);
+    if (a.ds) {
+      if (s.causal)
+        varlen_dkdv_kernel<T, D, true, true><<<gk, 256, 0, stream>>>(a);
+      else
+        varlen_dkdv_kernel<T, D, false, true><<<gk, 256, 0, stream>>>(a);
+    } else {
+      if (s.causal)
+        varlen_dkdv_kernel<T, D, true, false><<<gk, 256, 0, stream>>>(a);
+      else
+        varlen_dkdv_kernel<T, D, false, false><<<gk, 256, 0, stream>>>(a);
+    }
     TGX_LAUNCHED("varlen_dkdv_kernel");
   }
   if (n_q_tasks > 0) {
     TGX_PROFILE("varlen_dq_kernel", stream);
     a.tasks = q_tasks;
-    if (s.causal)
-      varlen_dq_kernel<T, D, true><<<static_cast<unsigned>(n_q_tasks), 256, 0, stream>>>(a);
-    else
-      varlen_dq_kernel<T, D, false><<<static_cast<unsigned>(n_q_tasks), 256, 0, stream>>>(a);
+    if (a.ds) {
+      if (s.causal)
+        varlen_dq_stored_kernel<T, D, true><<<gq, 256, 0, stream>>>(a);
+      else
+        varlen_dq_stored_kernel<T, D, false><<<gq, 256, 0, stream>>>(a);
+    } else {
+      if (s.causal)
+        varlen_dq_kernel<T, D, true><<<gq, 256, 0, stream>>>(a);
+      else
+        varlen_dq_kernel<T, D, false><<<gq, 256, 0, stream>>>(a);
+    }
     TGX_LAUNCHED("varlen_dq_kernel");
   }
   return TGX_OK;
@@ -853,12 +1089,12 @@ int bwd_dtype(const AttnShape& s, const int32_t* cu_q, const int32_t* cu_k,
               const int32_t* q_tasks, int64_t n_q_tasks, const int32_t* k_tasks,
               int64_t n_k_tasks, const void* q, const void* k, const void* v, const void* out,
               const float* lse, const void* dout, float scale, void* dq, void* dk, void* dv,
-              float* delta, hipStream_t stream) {
+              float* delta, void* ds, hipStream_t stream) {
   BwdArgs<T> a{cu_q, cu_k, nullptr, s.H,
                static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                s.qsn, s.qsh, s.ksn, s.ksh, static_cast<const T*>(dout), lse, delta,
                static_cast<T*>(dq), static_cast<T*>(dk), static_cast<T*>(dv),
-               scale, scale * kLog2e};
+               scale, scale * kLog2e, static_cast<T*>(ds)};
   if (s.D == 64)
     return launch_bwd<T, 64>(s, a, static_cast<const T*>(out), q_tasks, n_q_tasks, k_tasks,
                              n_k_tasks, delta, stream);
@@ -882,14 +1118,19 @@ extern "C" int tgx_attn_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host
   struct Group {
     int blk, head;
     int64_t work;
+    int64_t tile0;   // first stored dS tile of (block, head)
   };
   std::vector<Group> groups;
+  int64_t tiles = 0;   // stored dS tiles of the blocks before b, all heads
   for (int b = 0; b < n_blocks; ++b) {
     const int q0 = cu_q_host[b], q1 = cu_q_host[b + 1];
     const int k0 = cu_k_host[b], k1 = cu_k_host[b + 1];
     TGX_REQUIRE(q1 >= q0 && q0 >= 0 && k1 >= k0 && k0 >= 0,
                 "cu_seqlens must be non-decreasing from 0");
     TGX_REQUIRE(!causal || (q0 == k0 && q1 == k1), "causal blocks must be square");
+    const int64_t nt = ds_tiles(q1 - q0, k1 - k0, causal != 0);
+    const int64_t tile_b = tiles;
+    tiles += nt * H;
     const int r0 = kind == 0 ? q0 : k0, r1 = kind == 0 ? q1 : k1;
     if (r1 == r0) continue;
     int64_t w = 0;
@@ -900,7 +1141,8 @@ extern "C" int tgx_attn_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host
       else
         w += causal ? q1 - r : q1 - q0;
     }
-    for (int h = 0; h < H; ++h) groups.push_back(Group{b, h, std::max<int64_t>(w, 1)});
+    for (int h = 0; h < H; ++h)
+      groups.push_back(Group{b, h, std::max<int64_t>(w, 1), tile_b + h * nt});
   }
   // Longest-processing-time assignment of groups to the XCDs (stable, so
   // ties keep block then head order).
@@ -920,7 +1162,10 @@ extern "C" int tgx_attn_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host
     const int n_t = (r1 - r0 + block - 1) / block;
     for (int t = 0; t < n_t; ++t) {
       const int tt = (kind == 0 && causal) ? n_t - 1 - t : t;
-      queue[x].insert(queue[x].end(), {gr.blk, r0 + tt * block, gr.head, 0});
+      // The dS tile offset fits int32 when the stored path can hold it
+      // (tgx_attn_ds_tiles refuses more); past that it is unused.
+      const int32_t t0 = gr.tile0 < (int64_t{1} << 31) ? static_cast<int32_t>(gr.tile0) : 0;
+      queue[x].insert(queue[x].end(), {gr.blk, r0 + tt * block, gr.head, t0});
     }
   }
   size_t longest = 0;
@@ -991,7 +1236,59 @@ extern "C" int tgx_attn_bwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
   hipStream_t hs = as_stream(stream);
   if (dtype == TGX_DTYPE_BF16)
     return bwd_dtype<__bf16>(s, cu_q_dev, cu_k_dev, q_tasks_dev, n_q_tasks, k_tasks_dev,
-                             n_k_tasks, q, k, v, out, lse, dout, scale, dq, dk, dv, delta, hs);
+                             n_k_tasks, q, k, v, out, lse, dout, scale, dq, dk, dv, delta,
+                             nullptr, hs);
   return bwd_dtype<_Float16>(s, cu_q_dev, cu_k_dev, q_tasks_dev, n_q_tasks, k_tasks_dev,
-                             n_k_tasks, q, k, v, out, lse, dout, scale, dq, dk, dv, delta, hs);
+                             n_k_tasks, q, k, v, out, lse, dout, scale, dq, dk, dv, delta,
+                             nullptr, hs);
+}
+
+extern "C" int tgx_attn_ds_tiles(const int32_t* cu_q_host, const int32_t* cu_k_host,
+                                 int n_blocks, int H, int causal, int64_t* n_tiles) {
+  TGX_REQUIRE(cu_q_host && cu_k_host && n_tiles && n_blocks >= 0 && H > 0, "bad arguments");
+  int64_t tiles = 0;
+  for (int b = 0; b < n_blocks; ++b) {
+    const int64_t lq = int64_t{cu_q_host[b + 1]} - cu_q_host[b];
+    const int64_t lk = int64_t{cu_k_host[b + 1]} - cu_k_host[b];
+    TGX_REQUIRE(lq >= 0 && lk >= 0, "cu_seqlens must be non-decreasing");
+    TGX_REQUIRE(!causal || lq == lk, "causal blocks must be square");
+    tiles += ds_tiles(lq, lk, causal != 0) * H;
+  }
+  if (tiles >= (int64_t{1} << 31)) {
+    set_error("%lld stored dS tiles exceed the task list's int32 offsets",
+              static_cast<long long>(tiles));
+    return TGX_UNSUPPORTED;
+  }
+  *n_tiles = tiles;
+  return TGX_OK;
+}
+
+extern "C" int tgx_attn_bwd_stored(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
+                                   const int32_t* q_tasks_dev, int64_t n_q_tasks,
+                                   const int32_t* k_tasks_dev, int64_t n_k_tasks, int causal,
+                                   int dtype, const void* q, const void* k, const void* v,
+                                   const int64_t* strides, const void* out, const float* lse,
+                                   const void* dout, float scale, void* dq, void* dk, void* dv,
+                                   float* delta, void* ds, int64_t n_q, int64_t n_k, int H,
+                                   int D, void* stream) {
+  TGX_REQUIRE(strides, "null strides");
+  const AttnShape s{n_q, n_k, H, D, dtype, causal != 0,
+                    strides[0], strides[1], strides[2], strides[3]};
+  int st = check_shape(s);
+  if (st != TGX_OK) return st;
+  TGX_REQUIRE(n_q_tasks >= 0 && n_k_tasks >= 0 && n_q_tasks < (int64_t{1} << 31) &&
+                  n_k_tasks < (int64_t{1} << 31),
+              "bad task count");
+  if (n_q == 0 && n_k == 0) return TGX_OK;
+  TGX_REQUIRE(cu_q_dev && cu_k_dev && q_tasks_dev && k_tasks_dev && q && k && v && out &&
+                  lse && dout && dq && dk && dv && delta && ds,
+              "null pointer");
+  hipStream_t hs = as_stream(stream);
+  if (dtype == TGX_DTYPE_BF16)
+    return bwd_dtype<__bf16>(s, cu_q_dev, cu_k_dev, q_tasks_dev, n_q_tasks, k_tasks_dev,
+                             n_k_tasks, q, k, v, out, lse, dout, scale, dq, dk, dv, delta, ds,
+                             hs);
+  return bwd_dtype<_Float16>(s, cu_q_dev, cu_k_dev, q_tasks_dev, n_q_tasks, k_tasks_dev,
+                             n_k_tasks, q, k, v, out, lse, dout, scale, dq, dk, dv, delta, ds,
+                             hs);
 }

@@ -54,7 +54,7 @@ class EdgeMlp(ctypes.Structure):
 
 
 # tgx_abi_version() of the library these signatures and structs mirror.
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 # name -> argtypes (all return int status except where noted)
@@ -105,6 +105,10 @@ _SIGNATURES: dict[str, list] = {
     "tgx_attn_bwd": [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp, c_vp,
                      P(c_i64), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                      c_int, c_int, c_vp],
+    "tgx_attn_ds_tiles": [c_vp, c_vp, c_int, c_int, c_int, P(c_i64)],
+    "tgx_attn_bwd_stored": [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
+                            c_vp, P(c_i64), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp,
+                            c_vp, c_i64, c_i64, c_int, c_int, c_vp],
     "tgx_edge_mlp_scores": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp],
     "tgx_edge_mlp_backward_workspace": [c_i64, P(EdgeMlp), P(c_size)],
     "tgx_edge_mlp_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, P(c_vp),

@@ -239,6 +239,12 @@ def attn_strides(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
     return q, k, v, strides
 
 
+# The attention backward stores dS (tgx_attn_bwd_stored: the dQ pass reads
+# it back instead of recomputing S and dP) when its workspace is at most this
+# many bytes; larger relations recompute (tgx_attn_bwd).
+STORED_DS_MAX_BYTES = 8 << 30
+
+
 class BlockAttentionFunction(torch.autograd.Function):
     """Dot-product attention over a block-diagonal relation: Graph.cu_seqlens
     (causal or not), Graph.dense, Graph.triangular.  q [n_dst, H, D], k/v
@@ -283,11 +289,17 @@ class BlockAttentionFunction(torch.autograd.Function):
         dk = torch.empty((n_k, H, D), dtype=q.dtype, device=q.device)
         dv = torch.empty((n_k, H, D), dtype=q.dtype, device=q.device)
         delta = torch.empty((n_q, H), dtype=torch.float32, device=q.device)
-        _native.call("tgx_attn_bwd", cu_q.data_ptr(), cu_k.data_ptr(), qtasks.data_ptr(), nq,
-                     ktasks.data_ptr(), nk, int(causal), _ATTN_DTYPES[q.dtype], q.data_ptr(),
-                     k.data_ptr(), v.data_ptr(), strides, out.data_ptr(), lse.data_ptr(),
-                     dout.data_ptr(), ctx.scale, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                     delta.data_ptr(), n_q, n_k, H, D, _native.stream_of(q))
+        args = (cu_q.data_ptr(), cu_k.data_ptr(), qtasks.data_ptr(), nq, ktasks.data_ptr(), nk,
+                int(causal), _ATTN_DTYPES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                strides, out.data_ptr(), lse.data_ptr(), dout.data_ptr(), ctx.scale,
+                dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr())
+        tail = (n_q, n_k, H, D, _native.stream_of(q))
+        tiles = graph._attn_ds_tiles(H)
+        if tiles is not None and tiles * 64 * 64 * q.element_size() <= STORED_DS_MAX_BYTES:
+            ds = torch.empty(max(tiles, 1) * 64 * 64, dtype=q.dtype, device=q.device)
+            _native.call("tgx_attn_bwd_stored", *args, ds.data_ptr(), *tail)
+        else:
+            _native.call("tgx_attn_bwd", *args, *tail)
         return dq, dk, dv, None, None, None
 
 

@@ -767,6 +767,21 @@ class Graph:
             self._native_cache[key] = got
         return got
 
+    def _attn_ds_tiles(self, heads: int) -> int | None:
+        """Stored dS tiles of a `heads`-head attention backward
+        (tgx_attn_ds_tiles), None when the relation has too many."""
+        key = ("attn-ds", heads)
+        if key not in self._native_cache:
+            cu_q, cu_k, causal = self._attn_blocks()
+            n = ctypes.c_int64()
+            try:
+                _native.call("tgx_attn_ds_tiles", cu_q.ctypes.data, cu_k.ctypes.data,
+                             cu_q.size - 1, heads, int(causal), ctypes.byref(n))
+                self._native_cache[key] = n.value
+            except NotImplementedError:
+                self._native_cache[key] = None
+        return self._native_cache[key]
+
     def _row_plan(self, wave_max: int = WAVE_MAX, chunk_edges: int = CHUNK_EDGES) -> RowPlanHandle:
         key = ("plan", wave_max, chunk_edges)
         handle = self._native_cache.get(key)
