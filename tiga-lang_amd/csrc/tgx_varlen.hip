@@ -509,12 +509,15 @@ template <typename T, int D, bool CAUSAL, bool STORE>
 __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
   constexpr int KC = D / 32;
   constexpr int DT = D / 16;
-  constexpr int DSP = VBN + 8;   // row stride of the staged dS^T tile
   __shared__ T qs[VBN][TPAD];    // Q rows of the query block
   __shared__ T dos[VBN][TPAD];   // dO rows
   __shared__ float lse_s[VBN], del_s[VBN];
   // STORE: the block's dS^T tile, written to a.ds in the next step (or after
-  // the loop) with full-row 16-byte stores.
+  // the loop) with full-row 16-byte stores.  Row stride 34 dwords: the 16
+  // lanes an 8-byte LDS access serves together (16 rows, or two rows of 8
+  // chunks) fall on 32 distinct banks.  (A 36-dword stride or a 16-byte
+  // chunk swizzle gives 2-way conflicts on the writes.)
+  constexpr int DSP = VBN + 4;
   __shared__ T dsw[STORE ? VBN : 1][STORE ? DSP : 1];
   const int32_t* task = a.tasks + 4 * static_cast<int64_t>(blockIdx.x);
   const int blk = task[0];
@@ -561,15 +564,18 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
   const int kj = (k0 - ks0) / VBN, nk = (ks1 - ks0 + VBN - 1) / VBN;
   T* const ds_blk = STORE ? a.ds + static_cast<int64_t>(task[3]) * kDsTile : nullptr;
   // The staged dS^T tile of query block qi (its 64 x 64 elements, thread t
-  // the 16-byte chunks t and t + 256) to its place in a.ds.
+  // the 16-byte chunks t and t + 256, each read as two 8-byte halves) to its
+  // place in a.ds.
   auto flush_ds = [&](int qi) {
     T* tile = ds_blk + ds_tile(qi, kj, nk, CAUSAL) * kDsTile;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int c = threadIdx.x + 256 * i;
       const int row = c >> 3, col = 8 * (c & 7);
+      const vec4<T> lo = *reinterpret_cast<const vec4<T>*>(&dsw[row][col]);
+      const vec4<T> hi = *reinterpret_cast<const vec4<T>*>(&dsw[row][col + 4]);
       *reinterpret_cast<vec8<T>*>(tile + row * VBN + col) =
-          *reinterpret_cast<const vec8<T>*>(&dsw[row][col]);
+          vec8<T>{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   };
   // The block's Q/dO rows and its lse/delta are loaded one block ahead, all
