@@ -803,7 +803,7 @@ def run_c5(args):
     ms = elapsed * 1e3 / args.steps
     tflops = step_flops / (ms * 1e-3) / 1e12
     kflops = {"varlen_fwd_kernel": fwd_flops, "varlen_dkdv_kernel": 2.0 * fwd_flops,
-              "varlen_dq_kernel": 0.5 * fwd_flops}
+              "varlen_dq_kernel": 0.5 * fwd_flops, "varlen_dq_stored_kernel": 0.5 * fwd_flops}
     per = totals
     dominant = max((kk for kk in per if kk in kflops), key=lambda kk: per[kk][1])
     n_launch, total_ms = per[dominant]
@@ -817,8 +817,9 @@ def run_c5(args):
         "data": "synthetic (seeded lengths, q,k,v,dout ~N(0,1))",
         "config": {"workload": "c5-varlen-causal-fwd-bwd", "tokens": T, "sequences": 32,
                    "heads": H, "head_dim": D, "causal_pairs": pairs,
-                   "flop_convention": "fwd 4*H*D*pairs, bwd 2.5x fwd (useful FLOPs; the dQ "
-                                      "pass recomputes S and dP, not counted)"},
+                   "flop_convention": "fwd 4*H*D*pairs, bwd 2.5x fwd (useful FLOPs: the "
+                                      "dK/dV pass computes S, dP, dV and dK and stores dS, "
+                                      "the dQ pass reads dS back)"},
         "mfma_utilization": tflops / BF16_PEAK_TFLOPS,
         "cold_ms_per_step": cold_ms,
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": achieved,

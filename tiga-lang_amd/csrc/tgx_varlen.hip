@@ -1059,7 +1059,8 @@ int launch_bwd(const AttnShape& s, BwdArgs<T> a, const T* out, const int32_t* q_
     TGX_LAUNCHED("varlen_dkdv_kernel");
   }
   if (n_q_tasks > 0) {
-    TGX_PROFILE("varlen_dq_kernel", stream);
+    const char* dq_name = a.ds ? "varlen_dq_stored_kernel" : "varlen_dq_kernel";
+    TGX_PROFILE(dq_name, stream);
     a.tasks = q_tasks;
     if (a.ds) {
       if (s.causal)
@@ -1072,7 +1073,7 @@ int launch_bwd(const AttnShape& s, BwdArgs<T> a, const T* out, const int32_t* q_
       else
         varlen_dq_kernel<T, D, false><<<gq, 256, 0, stream>>>(a);
     }
-    TGX_LAUNCHED("varlen_dq_kernel");
+    TGX_LAUNCHED(dq_name);
   }
   return TGX_OK;
 }
