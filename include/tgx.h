@@ -419,7 +419,9 @@ int tgx_attn_ds_tiles(const int32_t* cu_q_host, const int32_t* cu_k_host, int n_
  * to ds_dev (tgx_attn_ds_tiles x 64 x 64 elements, the task lists' tile0
  * offsets), and the dQ kernel reads them back instead of recomputing S and
  * dP (one product per tile instead of three).  Same results up to the
- * rounding of S computed as Q K^T instead of K Q^T. */
+ * rounding of S computed as Q K^T instead of K Q^T.  ds_dev is workspace:
+ * the rows of keys past a block's last key are written but not meaningful
+ * (the dQ kernel does not read them). */
 int tgx_attn_bwd_stored(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
                         const int32_t* q_tasks_dev, int64_t n_q_tasks,
                         const int32_t* k_tasks_dev, int64_t n_k_tasks, int causal, int dtype,

@@ -656,14 +656,13 @@ __global__ __launch_bounds__(256, 2) void varlen_dkdv_kernel(BwdArgs<T> a) {
       weights(std::false_type{});
     if constexpr (STORE) {
       // dS^T row of this lane's key over the block's 64 queries, four
-      // consecutive queries per 8-byte LDS write (keys past the block: 0).
-      const bool kvalid = key < ks1;
+      // consecutive queries per 8-byte LDS write.  (Rows of keys past the
+      // block hold P (0 - delta) of a zero K row; the dQ pass skips them.)
 #pragma unroll
       for (int qt = 0; qt < 4; ++qt) {
         vec4<T> w;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          w[r] = kvalid ? sb[qt >> 1][4 * (qt & 1) + r] : static_cast<T>(0.f);
+        for (int r = 0; r < 4; ++r) w[r] = sb[qt >> 1][4 * (qt & 1) + r];
         *reinterpret_cast<vec4<T>*>(&dsw[16 * wave + lr][16 * qt + 4 * g]) = w;
       }
     }
@@ -906,7 +905,8 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_stored_kernel(BwdArgs<T> a) 
   const int n_own = qb >= qs1 ? 0 : CAUSAL ? min(n_kv, qi + 1) : n_kv;
   // Staging of the two dS^T tiles: 2 x 64 rows x 128 B, four 16-byte
   // chunks per thread (chunk c: tile c / 512, row (c % 512) / 8, column
-  // 8 (c % 8)); a tile that does not exist is zero-filled.
+  // 8 (c % 8)); a tile that does not exist, and the rows of keys past the
+  // block (written by the dK/dV pass but not zero), are zero-filled.
   vec8<T> dstage[4];
   auto ds_load = [&](int kj) {
 #pragma unroll
@@ -914,7 +914,7 @@ __global__ __launch_bounds__(256, 2) void varlen_dq_stored_kernel(BwdArgs<T> a) 
       const int c = threadIdx.x + 256 * i;
       const int t = c >> 9, row = (c & 511) >> 3, col = 8 * (c & 7);
       const int tq = qi0 + t;
-      const bool ok = tq < nq && (!CAUSAL || kj <= tq);
+      const bool ok = tq < nq && (!CAUSAL || kj <= tq) && ks0 + VBN * kj + row < ks1;
       dstage[i] = ok ? ld8(tiles + ds_tile(tq, kj, nk, CAUSAL) * kDsTile + row * VBN + col)
                      : vec8<T>{};
     }
