@@ -9,7 +9,7 @@ roofline (algorithmic bytes / its live HIP-event duration) and the
 reference's CPU path timed on a bounded sample of the same workload.
 
   python bench.py [--steps K] [--warmup W]
-                  [--config all|c1..c5|dense|dense-causal|dense-pruned|nn]
+                  [--config all|c1..c5|dense|dense-causal|dense-pruned|nn|refcases]
                   [--no-cpu] [--no-cold] [--no-graph]
 
 By default (--config all) the line is C2's and carries C1, C3, C4 and C5 as
@@ -17,7 +17,9 @@ complete sub-lines under "configs" (same fields, each with the roofline of
 its own dominant kernel and its CPU baseline), all measured in this run.
 c1-c5 are BASELINE.json's configurations; dense* are the reference's dense
 attention benchmark shapes (N=4096, H=16, D=64, fp16, forward); nn is the
-reference's nn-scored GAT training step (131072 nodes, net 19-16-1).
+reference's nn-scored GAT training step (131072 nodes, net 19-16-1);
+refcases are the reference's archived sum and segmented-softmax GPU cases
+(131072 nodes), each beside the figure the reference publishes for it.
 """
 
 from __future__ import annotations
@@ -57,7 +59,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="all",
                     choices=["all", "c1", "c2", "c3", "c4", "c5", "dense", "dense-causal",
-                             "dense-pruned", "nn"],
+                             "dense-pruned", "nn", "refcases"],
                     help="all (default): C2 as the headline line with C1, C3, C4, C5, "
                          "nn and the dense attention shapes under its 'configs' key")
     ap.add_argument("--nodes", type=int, default=None, help="override node count (testing)")
@@ -1001,6 +1003,197 @@ def run_nn(args):
     return result
 
 
+def reference_case_graph(nodes, degree, topology, locality, seed, device):
+    """The reference's sparse benchmark graphs (benchmarks/sparse_compute/
+    cases.py:42-117): "regular" rows of `degree` edges, or "powerlaw" rows of
+    degree/2, 4 degree and 16 degree edges with probabilities 0.90, 0.09 and
+    0.01; sources "local" (dst + 1 + (edge ordinal mod degree), mod nodes)
+    or "random" (uniform).  int64 row_ptr/col.  Torch's generator here is
+    not the reference's, so the random draws differ; the shapes do not."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    if topology == "regular":
+        deg = torch.full((nodes,), degree, device=device, dtype=torch.int64)
+    else:
+        u = torch.rand(nodes, device=device, generator=g)
+        deg = torch.where(u < 0.90, max(1, degree // 2),
+                          torch.where(u < 0.99, 4 * degree, 16 * degree)).to(torch.int64)
+    row_ptr = torch.zeros(nodes + 1, dtype=torch.int64, device=device)
+    row_ptr[1:] = torch.cumsum(deg, 0)
+    E = int(row_ptr[-1].item())
+    dst = torch.repeat_interleave(torch.arange(nodes, device=device), deg)
+    if locality == "local":
+        col = (dst + 1 + torch.arange(E, device=device) % max(1, degree)) % nodes
+    else:
+        col = torch.randint(nodes, (E,), device=device, generator=g)
+    return row_ptr, col, dst
+
+
+def _event_median_ms(fn, reps=50, warmup=5):
+    """Median of `reps` HIP-event samples of fn() on Torch's stream, hot
+    cache (the reference's samples_ms protocol, benchmarks/common/
+    hardware_roofline.py)."""
+    import statistics
+
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b))
+    return statistics.median(out)
+
+
+def run_refcases(args):
+    """The reference's own archived GPU benchmark cases for this path, run on
+    this build at the same shapes (hot cache, medians of HIP-event samples),
+    each beside the reference's published figure.  The reference's numbers
+    come from an RTX 5070 Ti (benchmarks/evidence_snapshot/output/roofline/),
+    so the ratio compares two machines, not two implementations on one.
+    Every case is checked against a Torch computation before it is timed."""
+    import torch
+
+    import tiga as tg
+
+    dev = torch.device("cuda")
+    tg.config.strict = True
+    N = 131072
+
+    class WeightedAggregation(tg.MessagePassing):
+        # benchmarks/sparse_compute/weighted_aggregation.py:62-67
+        reducer = tg.sum()
+
+        def edge(self, src, dst, edge):
+            return edge.weight * src.x
+
+    class SegmentedSoftmax(tg.MessagePassing):
+        # benchmarks/neural_networks/online_softmax.py:54-58 (its user-defined
+        # stable weighted mean is the online softmax reducer's algebra)
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            return self.reducer(src.score, src.value)
+
+    cases = {}
+
+    def record(name, E, ms, ms_prepared, ref_gedges, ref_ms, source, note):
+        best = min(ms, ms_prepared) if ms_prepared is not None else ms
+        cases[name] = {
+            "edges": E, "ms": ms, "ms_prepared": ms_prepared,
+            "gedges_per_s": E / (best * 1e-3) / 1e9,
+            "reference_gedges_per_s": ref_gedges, "reference_ms": ref_ms,
+            "reference_hardware": "RTX 5070 Ti", "reference_source": source,
+            "ratio_to_reference": ref_ms / best, "what": note}
+
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    # Weighted sum forward (weighted_aggregation.py:252-314): x [N, F] (or
+    # [N] for F = 1), weight [E, 1] (or [E]), tg.sum() of weight * x.
+    for name, F_, topology, locality, ref, ref_ms, src_file in (
+            ("sum_fwd_regular_local_i64_f64", 64, "regular", "local", 22.06, 0.0951,
+             "weighted_aggregation/regular_local_cuda_i64_n131072_degree16_f1_16_64"),
+            ("sum_fwd_regular_local_i64_f1", 1, "regular", "local", 102.5, 0.0205,
+             "weighted_aggregation/regular_local_cuda_i64_n131072_degree16_f1_16_64"),
+            ("sum_fwd_powerlaw_random_i64_f1", 1, "powerlaw", "random", 38.2, 0.0536,
+             "weighted_aggregation/powerlaw_random_cuda_i64_n131072_degree16_f1")):
+        row_ptr, col, dst = reference_case_graph(N, 16, topology, locality, 20260807, dev)
+        E = col.numel()
+        x = torch.rand((N,) if F_ == 1 else (N, F_), device=dev, generator=g)
+        w = torch.rand((E,) if F_ == 1 else (E, 1), device=dev, generator=g)
+        graph = tg.Graph.from_csr(row_ptr, col, num_src=N)
+        kernel = WeightedAggregation()
+        call = lambda: kernel(graph=graph, src={"x": x}, dst={"x": x}, edge={"weight": w})
+        got = call()
+        assert kernel.last_variant.backend == "hip", name
+        want = torch.zeros_like(x).index_add_(0, dst, w * x[col])
+        torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
+        prepared = kernel.prepare(graph=graph, src={"x": x}, dst={"x": x}, edge={"weight": w})
+        record(name, E, _event_median_ms(call), _event_median_ms(prepared), ref, ref_ms,
+               src_file, f"tg.sum() of edge.weight * src.x, {topology} {locality} rows, F={F_}")
+        del graph, kernel, prepared, x, w, row_ptr, col, dst
+    # Segmented online softmax forward (online_softmax.py:92-127): 32 random
+    # sources per row, scalar score (N(0,1) + 1000) and value per source.
+    E = N * 32
+    row_ptr = torch.arange(0, E + 1, 32, dtype=torch.int64, device=dev)
+    col = torch.randint(N, (E,), dtype=torch.int64, device=dev, generator=g)
+    score = torch.randn(N, device=dev, generator=g) + 1000
+    value = torch.randn(N, device=dev, generator=g)
+    graph = tg.Graph.from_csr(row_ptr, col, num_src=N)
+    kernel = SegmentedSoftmax()
+    call = lambda: kernel(graph=graph, src={"score": score, "value": value}, dst={})
+    got = call()
+    assert kernel.last_variant.backend == "hip"
+    want = (torch.softmax(score[col].reshape(N, 32), dim=1) * value[col].reshape(N, 32)).sum(1)
+    torch.testing.assert_close(got, want, rtol=3e-4, atol=3e-4)
+    prepared = kernel.prepare(graph=graph, src={"score": score, "value": value}, dst={})
+    record("online_softmax_fwd_random_i64_deg32_f1", E, _event_median_ms(call),
+           _event_median_ms(prepared), 25.0, 0.1678,
+           "online_softmax/cuda_n131072_degree32_f1",
+           "softmax over each row's 32 source scores, weighted sum of the source values")
+    del graph, kernel, prepared, score, value, row_ptr, col
+    # Sum backward (autograd/message_passing_backward.py:99-160): regular
+    # random rows, x and weight N(0,1), a random cotangent; dx alone for
+    # F = 1, the per-edge weight gradient alone for F = 64.  The reference
+    # times dx as its generated source VJP (compile_source_vjp: the weighted
+    # sum of the cotangent over the transposed relation with the weights in
+    # transposed edge order), so `ms_prepared` is that sum here, prepared;
+    # `ms` is torch.autograd.grad through this build's backward.
+    for name, F_, wrt, ref, ref_ms, src_file in (
+            ("sum_bwd_dx_regular_random_i64_f1", 1, "x", 35.85, 0.0585,
+             "message_passing_backward/regular_random_cuda_i64_n131072_degree16_dx"),
+            ("sum_bwd_dweight_regular_random_i64_f64", 64, "weight", 0.91, 2.30,
+             "message_passing_backward/regular_random_cuda_i64_n131072_degree16_dweight_f64")):
+        row_ptr, col, dst = reference_case_graph(N, 16, "regular", "random", 20260807, dev)
+        E = col.numel()
+        x = torch.randn((N,) if F_ == 1 else (N, F_), device=dev, generator=g,
+                        requires_grad=True)
+        w = torch.randn((E,) if F_ == 1 else (E, 1), device=dev, generator=g,
+                        requires_grad=True)
+        cot = torch.randn((N,) if F_ == 1 else (N, F_), device=dev, generator=g)
+        graph = tg.Graph.from_csr(row_ptr, col, num_src=N)
+        kernel = WeightedAggregation()
+        out = kernel(graph=graph, src={"x": x}, dst={}, edge={"weight": w})
+        assert kernel.last_variant.backend == "hip", name
+        target = x if wrt == "x" else w
+        grad = lambda: torch.autograd.grad(out, target, cot, retain_graph=True)[0]
+        got = grad()
+        with torch.no_grad():
+            if wrt == "x":
+                want = torch.zeros_like(x).index_add_(0, col, (w * cot[dst]))
+            else:
+                want = (cot[dst] * x[col]).sum(1, keepdim=True)
+        torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
+        ms_vjp = None
+        if wrt == "x":
+            graph_t = graph.transpose()
+            w_t = w.detach()[torch.argsort(col, stable=True)]
+            vjp = WeightedAggregation()
+            torch.testing.assert_close(
+                vjp(graph=graph_t, src={"x": cot}, dst={}, edge={"weight": w_t}), want,
+                rtol=1e-4, atol=1e-4)
+            ms_vjp = _event_median_ms(
+                vjp.prepare(graph=graph_t, src={"x": cot}, dst={}, edge={"weight": w_t}))
+            del graph_t, w_t, vjp
+        record(name, E, _event_median_ms(grad), ms_vjp, ref, ref_ms, src_file,
+               f"torch.autograd.grad of the weighted sum with respect to {wrt} alone, F={F_}"
+               + ("; prepared: the sum of the cotangent over the transposed relation"
+                  if wrt == "x" else ""))
+        del graph, kernel, out, x, w, cot, row_ptr, col, dst
+    return {
+        "metric": "the reference's archived GPU cases for this path, edges/s on 1xMI355X",
+        "unit": "edges/s", "n_gpus": 1, "data": "synthetic (the reference's generators)",
+        "config": {"workload": "reference-benchmark-cases", "nodes": N},
+        "cases": cases,
+    }
+
+
 def _release_gpu_memory():
     import gc
 
@@ -1016,8 +1209,8 @@ def run_all(args):
     top-level line, C1, C3, C4 and C5 under "configs", each with its own
     step time, roofline of its dominant kernel and CPU baseline; then the
     reference's own benchmark shapes this path also covers (the nn-scored
-    GAT step, with its CPU baseline, and the dense / triangular / pruned
-    attention forwards).  Progress goes to stderr; stdout gets the one JSON
+    GAT step, with its CPU baseline, the dense / triangular / pruned
+    attention forwards, and the reference's archived sum and softmax cases).  Progress goes to stderr; stdout gets the one JSON
     line."""
     t_all = time.perf_counter()
 
@@ -1036,12 +1229,13 @@ def run_all(args):
         got = fn(args)
         configs.update(got if name == "c3+c4" else {name: got})
         progress(name, t0)
-    for name in ("nn", "dense", "dense-causal", "dense-pruned"):
+    for name in ("nn", "dense", "dense-causal", "dense-pruned", "refcases"):
         _release_gpu_memory()
         t0 = time.perf_counter()
         sub_args = argparse.Namespace(**vars(args))
         sub_args.config = name
-        configs[name] = run_nn(sub_args) if name == "nn" else run_dense(sub_args)
+        runner = {"nn": run_nn, "refcases": run_refcases}.get(name, run_dense)
+        configs[name] = runner(sub_args)
         progress(name, t0)
     for sub in configs.values():
         if isinstance(sub.get("cpu_baseline"), dict):
@@ -1122,7 +1316,7 @@ def main():
     runners = {"c1": run_c1, "c2": run_c2, "c3": lambda a: run_dot(a, ("c3",))["c3"],
                "c4": lambda a: run_dot(a, ("c4",))["c4"], "c5": run_c5,
                "dense": run_dense, "dense-causal": run_dense, "dense-pruned": run_dense,
-               "nn": run_nn}
+               "nn": run_nn, "refcases": run_refcases}
     if args.config == "all":
         result = run_all(args)
     else:

@@ -187,6 +187,37 @@ def test_closure_tensors_are_recaptured_every_call():
     assert not torch.equal(first, second)
 
 
+def test_no_grad_launch_matches_autograd_launch():
+    """Calls whose operands need no gradient launch the kernels without an
+    autograd node; the result is the same launch's, bit for bit."""
+    print("no-grad launch", flush=True)
+    g = _graph(11)
+    x = torch.randn(3000, 5, device=DEV)
+    w = torch.rand(g.num_edges, device=DEV)
+    plain = WeightedSum()(graph=g, src={"x": x}, dst={}, edge={"w": w})
+    assert plain.grad_fn is None
+    xg = x.clone().requires_grad_(True)
+    tracked = WeightedSum()(graph=g, src={"x": xg}, dst={}, edge={"w": w})
+    assert tracked.grad_fn is not None
+    assert torch.equal(plain, tracked.detach())
+
+    class ScoreSoftmax(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            return self.reducer(src.s, src.v)
+
+    s, v = torch.randn(3000, device=DEV), torch.randn(3000, 3, device=DEV)
+    k = ScoreSoftmax()
+    plain = k(graph=g, src={"s": s, "v": v}, dst={})
+    assert k.last_variant.backend == "hip" and plain.grad_fn is None
+    sg = s.clone().requires_grad_(True)
+    tracked = ScoreSoftmax()(graph=g, src={"s": sg, "v": v}, dst={})
+    assert torch.equal(plain, tracked.detach())
+    tracked.sum().backward()
+    assert sg.grad is not None and torch.isfinite(sg.grad).all()
+
+
 def test_prepare_is_bit_identical_and_sees_in_place_updates():
     print("prepare", flush=True)
     g = _graph(7)

@@ -127,7 +127,7 @@ def test_readme_known_answer_on_gpu():
     assert dw.tolist() == [1.0, 3.0, 2.0, 1.0, 2.0]
 
 
-@pytest.mark.parametrize("F_", [1, 3, 64, 100, 300])
+@pytest.mark.parametrize("F_", [1, 3, 4, 64, 100, 300])
 @pytest.mark.parametrize("idx", [torch.int32, torch.int64])
 def test_sum_fwd_bwd_parity(F_, idx):
     print(f"sum F={F_} {idx}", flush=True)

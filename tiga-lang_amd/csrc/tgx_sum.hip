@@ -204,93 +204,126 @@ __global__ __launch_bounds__(kTaskBlock) void sum_rows_kernel(SumArgs<I, DT> a) 
   sum_task<I, DT, VEC, G, U>(a, decode_task(a.plan, a.row_ptr, global_wave()));
 }
 
-// Narrow rows (G <= 8 lanes per edge): two rows of the wave bin per wave, one
-// per 32-lane half, so a wave's fixed cost (task decode, the dependent
-// row_ptr -> col -> gather chain) covers two rows.  Each half keeps 32 edges
-// in flight (U = G loads of 32 / G edges).  The task list is
-//   [split-row chunks | row pairs | empty-row groups];
-// chunks and empty groups run as whole-wave tasks.
-template <typename I, int DT, int VEC, int G, int UC>
+// Narrow rows (G <= 8 lanes per edge): the wave splits into 64 / SLOT lane
+// slots of SLOT lanes, each taking P rows of the wave bin, so a wave's fixed
+// cost (task decode, the dependent row_ptr -> col -> gather chain) covers
+// (64 / SLOT) P rows, and the loads of a slot's P rows are in flight
+// together.  A slot keeps SLOT edges per row in flight (U = G loads of
+// SLOT / G edges).  The task list is
+//   [split-row chunks | row groups | empty-row groups];
+// chunks and empty groups run as whole-wave tasks.  Slot s of group w takes
+// the wave-bin rows S P w + S q + s, q < P, S = 64 / SLOT.
+template <typename I, int DT, int VEC, int G, int UC, int SLOT, int P>
 __global__ __launch_bounds__(kTaskBlock) void sum_pairs_kernel(SumArgs<I, DT> a) {
   typedef Vec<VEC, DT> V;
   typedef typename V::T T;
-  constexpr int EPH = 32 / G;   // edges per half-wave load
-  constexpr int U = G;          // loads in flight: 32 edges per half
+  constexpr int NS = kWave / SLOT;   // slots per wave
+  constexpr int EPH = SLOT / G;      // edges per slot load
+  constexpr int U = G;               // loads in flight per row: SLOT edges
   const PlanView& p = a.plan;
   const int64_t w = global_wave();
-  const int64_t n_pairs = (p.n_wave + 1) / 2;
+  const int64_t n_groups = (p.n_wave + NS * P - 1) / (NS * P);
   if (w < p.n_chunks) {
     sum_task<I, DT, VEC, G, UC>(a, decode_task(p, a.row_ptr, w));
     return;
   }
   const int64_t pw = w - p.n_chunks;
-  if (pw >= n_pairs) {
-    sum_task<I, DT, VEC, G, UC>(a, decode_task(p, a.row_ptr, p.n_chunks + p.n_wave + (pw - n_pairs)));
+  if (pw >= n_groups) {
+    sum_task<I, DT, VEC, G, UC>(a, decode_task(p, a.row_ptr, p.n_chunks + p.n_wave + (pw - n_groups)));
     return;
   }
   const int lane = lane_id();
-  const int half = lane >> 5, hl = lane & 31;
+  const int slot_id = lane / SLOT, hl = lane % SLOT;
   const int g = hl / G, c = hl % G;
   const int64_t F = a.F;
   const int64_t fo = c * VEC;   // G * VEC <= F's tile: one feature tile
   const bool active = fo < F;
-  const int64_t k = 2 * pw + half;   // this half's position in the wave bin
-  const bool has = k < p.n_wave;
-  const int row = has ? p.rows[p.n_empty + k] : 0;
-  const int64_t e0 = has ? static_cast<int64_t>(a.row_ptr[row]) : 0;
-  const int len = has ? static_cast<int>(static_cast<int64_t>(a.row_ptr[row + 1]) - e0) : 0;
-  // Both halves loop to the longer row (wave-uniform bounds keep every
-  // shuffle's source lanes active); a half masks its own tail.
-  const int len_max = max(len, __shfl_xor(len, 32, 64));
-  T self = V::zero();
   const bool want_dw = a.self_x != nullptr;
-  if (want_dw && active && has) self = V::load(a.self_x + static_cast<int64_t>(row) * F + fo);
-  T acc = V::zero();
-  for (int base = 0; base < len_max; base += 32) {
-    const int n = min(max(len - base, 0), 32);          // this half's edges
-    const int n_max = min(len_max - base, 32);           // wave-uniform
-    int my_col = 0, my_widx = 0;
-    float my_w = 0.f;
-    if (hl < n) {
-      const int64_t e = e0 + base + hl;
-      my_col = a.col ? static_cast<int>(a.col[e]) : static_cast<int>(e);
-      my_widx = a.wperm ? a.wperm[e] : static_cast<int>(e);
-      my_w = a.w ? a.w[my_widx] : 1.f;
+  int row[P], len[P];
+  int64_t e0[P];
+  bool has[P];
+  int len_max = 0;
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    const int64_t k = NS * P * pw + NS * q + slot_id;   // position in the wave bin
+    has[q] = k < p.n_wave;
+    row[q] = has[q] ? p.rows[p.n_empty + k] : 0;
+    e0[q] = has[q] ? static_cast<int64_t>(a.row_ptr[row[q]]) : 0;
+    len[q] = has[q] ? static_cast<int>(static_cast<int64_t>(a.row_ptr[row[q] + 1]) - e0[q]) : 0;
+    len_max = max(len_max, len[q]);
+  }
+  // Every slot loops to the longest row (wave-uniform bounds keep every
+  // shuffle's source lanes active); each row masks its own tail.
+#pragma unroll
+  for (int m = SLOT; m < kWave; m <<= 1) len_max = max(len_max, __shfl_xor(len_max, m, 64));
+  T self[P], acc[P];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    self[q] = V::zero();
+    acc[q] = V::zero();
+    if (want_dw && active && has[q])
+      self[q] = V::load(a.self_x + static_cast<int64_t>(row[q]) * F + fo);
+  }
+  for (int base = 0; base < len_max; base += SLOT) {
+    int n[P], my_col[P], my_widx[P];
+    float my_w[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      n[q] = min(max(len[q] - base, 0), SLOT);   // this row's edges
+      my_col[q] = 0;
+      my_widx[q] = 0;
+      my_w[q] = 0.f;
+      if (hl < n[q]) {
+        const int64_t e = e0[q] + base + hl;
+        my_col[q] = a.col ? static_cast<int>(a.col[e]) : static_cast<int>(e);
+        my_widx[q] = a.wperm ? a.wperm[e] : static_cast<int>(e);
+        my_w[q] = a.w ? a.w[my_widx[q]] : 1.f;
+      }
     }
+    const int n_max = min(len_max - base, SLOT);   // wave-uniform
     for (int kk = 0; kk < n_max; kk += EPH * U) {
-      T v[U];
-      float wt[U];
+      T v[P][U];
+      float wt[P][U];
       int slot[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        slot[u] = kk + u * EPH + g;
-        const int src = 32 * half + (slot[u] < n ? slot[u] : 0);
-        const int j = __shfl(my_col, src, 64);
-        wt[u] = __shfl(my_w, src, 64);
-        v[u] = (slot[u] < n && active) ? V::load(a.x + static_cast<int64_t>(j) * F + fo)
-                                       : V::zero();
-      }
+      for (int u = 0; u < U; ++u) slot[u] = kk + u * EPH + g;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (slot[u] < n) acc += wt[u] * v[u];
-      }
-      if (want_dw) {
+      for (int q = 0; q < P; ++q)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const float d = group_reduce_sum<G>(V::dot(v[u], self));
-          const int src = 32 * half + (slot[u] < n ? slot[u] : 0);
-          const int widx = __shfl(my_widx, src, 64);
-          if (c == 0 && slot[u] < n) a.dw[widx] = d;
+          const int src = SLOT * slot_id + (slot[u] < n[q] ? slot[u] : 0);
+          const int j = __shfl(my_col[q], src, 64);
+          wt[q][u] = __shfl(my_w[q], src, 64);
+          v[q][u] = (slot[u] < n[q] && active) ? V::load(a.x + static_cast<int64_t>(j) * F + fo)
+                                               : V::zero();
         }
+#pragma unroll
+      for (int q = 0; q < P; ++q)
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (slot[u] < n[q]) acc[q] += wt[q][u] * v[q][u];
+      if (want_dw) {
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const float d = group_reduce_sum<G>(V::dot(v[q][u], self[q]));
+            const int src = SLOT * slot_id + (slot[u] < n[q] ? slot[u] : 0);
+            const int widx = __shfl(my_widx[q], src, 64);
+            if (c == 0 && slot[u] < n[q]) a.dw[widx] = d;
+          }
       }
     }
   }
-  // Fold the half's edge groups (lanes with equal c; masks below 32 stay
-  // inside the half).
+  // Fold each row's edge groups (lanes with equal c; masks below SLOT stay
+  // inside the slot).
 #pragma unroll
-  for (int m = G; m < 32; m <<= 1) acc += V::shfl_xor(acc, m);
-  if (g == 0 && active && has && a.out)
-    V::store(a.out + static_cast<int64_t>(row) * F + fo, acc);
+  for (int q = 0; q < P; ++q) {
+#pragma unroll
+    for (int m = G; m < SLOT; m <<= 1) acc[q] += V::shfl_xor(acc[q], m);
+    if (g == 0 && active && has[q] && a.out)
+      V::store(a.out + static_cast<int64_t>(row[q]) * F + fo, acc[q]);
+  }
 }
 
 // Combine split-row chunk partials in chunk order (deterministic).
@@ -314,10 +347,18 @@ void launch_sum(const SumArgs<I, DT>& a, int64_t ftiles, hipStream_t s) {
   constexpr int U = (kWave / G) >= 16 ? 1 : (16 / (kWave / G) < 8 ? 16 / (kWave / G) : 8);
   if constexpr (G <= 8) {
     // ftiles == 1 here: G * VEC <= 32 covers F.
+    // One lane per edge (F = 1, or F = 4 as one 4-wide vector): 16-lane
+    // slots of 2 rows each, 8 rows per wave (the reference's F = 1 case,
+    // 131072 rows of 16 edges: 0.0254 ms with 32-lane slots of 2 rows,
+    // 0.0182 ms with these).  Wider rows: 32-lane slots of one row (two rows
+    // per wave measured 5% faster than four on 8-wide rows).
+    constexpr int SLOT = G == 1 ? 16 : 32;
+    constexpr int P = G == 1 ? 2 : 1;
+    constexpr int NS = kWave / SLOT;
     const PlanView& p = a.plan;
-    const int64_t waves = p.n_chunks + (p.n_wave + 1) / 2 +
+    const int64_t waves = p.n_chunks + (p.n_wave + NS * P - 1) / (NS * P) +
                           (p.n_empty + kEmptyPerWave - 1) / kEmptyPerWave;
-    sum_pairs_kernel<I, DT, VEC, G, U>
+    sum_pairs_kernel<I, DT, VEC, G, U, SLOT, P>
         <<<static_cast<unsigned>(ceil_div(waves, kWavesPerBlock)), kTaskBlock, 0, s>>>(a);
   } else {
     const int64_t waves = plan_waves(a.plan);

@@ -43,29 +43,45 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def _csr_sum_launch(x: torch.Tensor, w: torch.Tensor | None, graph: Graph):
+    """The forward launch of tg.sum() of [w *] x: (out, x and w as the
+    kernel read them, F)."""
+    _on_graph_device(graph, x, w)
+    row_ptr, col_idx = graph._kernel_csr()
+    n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
+    feat_shape = tuple(x.shape[1:])
+    F = 1
+    for d in feat_shape:
+        F *= d
+    xc = _aligned(x)
+    wc = None if w is None else w.reshape(-1).contiguous()
+    out = torch.empty((n_dst, *feat_shape), dtype=x.dtype, device=x.device)
+    if n_dst and F:
+        plan = graph._row_plan()
+        partial = _partial(plan, F, x.device)
+        _native.call("tgx_csr_sum_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
+                     _native.idx_bits(row_ptr), plan.ref, xc.data_ptr(), _p(wc),
+                     out.data_ptr(), n_dst, n_src, F, _native.dtype_code(xc), _p(partial),
+                     _native.stream_of(x))
+    return out, xc, wc, F
+
+
+def csr_sum(x: torch.Tensor, w: torch.Tensor | None, graph: Graph) -> torch.Tensor:
+    """tg.sum() of [w *] x with autograd when an operand needs a gradient,
+    else the bare launch (no autograd node: the prepared and no-grad calls'
+    host cost is the launch's own)."""
+    if torch.is_grad_enabled() and (x.requires_grad or (w is not None and w.requires_grad)):
+        return CsrSumFunction.apply(x, w, graph)
+    return _csr_sum_launch(x, w, graph)[0]
+
+
 class CsrSumFunction(torch.autograd.Function):
     """out[i] = sum_e w[e] * x[col[e]]  (w optional): x fp32, bf16 or fp16
     (out, dout and dx of the same type), w fp32; fp32 products and sums."""
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, w: torch.Tensor | None, graph: Graph):
-        _on_graph_device(graph, x, w)
-        row_ptr, col_idx = graph._kernel_csr()
-        n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
-        feat_shape = tuple(x.shape[1:])
-        F = 1
-        for d in feat_shape:
-            F *= d
-        xc = _aligned(x)
-        wc = None if w is None else w.reshape(-1).contiguous()
-        out = torch.empty((n_dst, *feat_shape), dtype=x.dtype, device=x.device)
-        if n_dst and F:
-            plan = graph._row_plan()
-            partial = _partial(plan, F, x.device)
-            _native.call("tgx_csr_sum_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
-                         _native.idx_bits(row_ptr), plan.ref, xc.data_ptr(), _p(wc),
-                         out.data_ptr(), n_dst, n_src, F, _native.dtype_code(xc), _p(partial),
-                         _native.stream_of(x))
+        out, xc, wc, F = _csr_sum_launch(x, w, graph)
         ctx.graph = graph
         ctx.F = F
         ctx.w_shape = None if w is None else w.shape
@@ -593,13 +609,28 @@ def nn_attention(graph: Graph, chain, roles, fields, value: torch.Tensor) -> tor
     params = _layer_params(chain)
     scores = EdgeMlpFunction.apply(graph, chain, tuple(roles), len(fields), *fields, *params)
     alpha = SegmentSoftmaxFunction.apply(scores, graph)
-    return CsrSumFunction.apply(value, alpha, graph)
+    return csr_sum(value, alpha, graph)
 
 
 # ---------------------------------------------------------------------------
 # Online softmax over a raw score field (tgx_segment_softmax_gather_fwd)
 
 _ROLE_CODE = {"src": 0, "dst": 1, "edge": 2}
+
+
+def _score_softmax_launch(table: torch.Tensor, role: str, scale: float,
+                          graph: Graph) -> torch.Tensor:
+    _on_graph_device(graph, table)
+    row_ptr, col_idx = graph._kernel_csr()
+    n = graph.schema.num_dst
+    flat = table.reshape(-1).contiguous()
+    alpha = torch.empty(max(col_idx.numel(), 1), dtype=torch.float32,
+                        device=table.device)[:col_idx.numel()]
+    lse = torch.empty(max(n, 1), dtype=torch.float32, device=table.device)
+    _native.call("tgx_segment_softmax_gather_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
+                 _native.idx_bits(row_ptr), n, flat.data_ptr(), _ROLE_CODE[role],
+                 float(scale), alpha.data_ptr(), lse.data_ptr(), _native.stream_of(table))
+    return alpha
 
 
 class ScoreSoftmaxFunction(torch.autograd.Function):
@@ -609,16 +640,7 @@ class ScoreSoftmaxFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, table: torch.Tensor, role: str, scale: float, graph: Graph):
-        _on_graph_device(graph, table)
-        row_ptr, col_idx = graph._kernel_csr()
-        n = graph.schema.num_dst
-        flat = table.reshape(-1).contiguous()
-        alpha = torch.empty(max(col_idx.numel(), 1), dtype=torch.float32,
-                            device=table.device)[:col_idx.numel()]
-        lse = torch.empty(max(n, 1), dtype=torch.float32, device=table.device)
-        _native.call("tgx_segment_softmax_gather_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
-                     _native.idx_bits(row_ptr), n, flat.data_ptr(), _ROLE_CODE[role],
-                     float(scale), alpha.data_ptr(), lse.data_ptr(), _native.stream_of(table))
+        alpha = _score_softmax_launch(table, role, scale, graph)
         ctx.graph, ctx.role, ctx.scale, ctx.shape = graph, role, float(scale), table.shape
         ctx.save_for_backward(alpha)
         return alpha
@@ -648,8 +670,11 @@ def score_attention(graph: Graph, table: torch.Tensor, role: str, scale: float,
                     value: torch.Tensor) -> torch.Tensor:
     """out[i] = sum_e softmax_i(scale * score(e)) value[col[e]] on the HIP path:
     the gathered segment softmax, then the weighted CSR sum."""
-    alpha = ScoreSoftmaxFunction.apply(table, role, scale, graph)
-    return CsrSumFunction.apply(value, alpha, graph)
+    if torch.is_grad_enabled() and (table.requires_grad or value.requires_grad):
+        alpha = ScoreSoftmaxFunction.apply(table, role, scale, graph)
+    else:
+        alpha = _score_softmax_launch(table, role, scale, graph)
+    return csr_sum(value, alpha, graph)
 
 
 # ---------------------------------------------------------------------------

@@ -460,7 +460,7 @@ class MessagePassing(Kernel):
             # dtypes already match).
             xk = x.to(out_dtype)
             wk = None if w is None else w.to(torch.float32)
-            return _ops.CsrSumFunction.apply(xk, wk, graph)
+            return _ops.csr_sum(xk, wk, graph)
 
         kind = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}[out_dtype]
         describe = lambda: self._variant(
