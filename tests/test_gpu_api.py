@@ -216,6 +216,23 @@ def test_no_grad_launch_matches_autograd_launch():
     assert torch.equal(plain, tracked.detach())
     tracked.sum().backward()
     assert sg.grad is not None and torch.isfinite(sg.grad).all()
+    # prepare() binds the native arguments of a no-grad sum; a strided x
+    # (which the launch would copy) stays on the per-call path; both see
+    # in-place updates, and a gradient requested later gets autograd.
+    for xs in (torch.randn(3000, 5, device=DEV), torch.randn(3000, 10, device=DEV)[:, ::2]):
+        launch = WeightedSum().prepare(graph=g, src={"x": xs}, dst={}, edge={"w": w})
+        first = launch()
+        assert torch.equal(first, WeightedSum()(graph=g, src={"x": xs}, dst={}, edge={"w": w}))
+        xs.mul_(2.0)
+        assert torch.equal(launch(), WeightedSum()(graph=g, src={"x": xs}, dst={},
+                                                   edge={"w": w}))
+        w.requires_grad_(True)
+        again = launch()
+        assert again.grad_fn is not None
+        again.sum().backward()
+        assert w.grad is not None
+        w.grad = None
+        w.requires_grad_(False)
 
 
 def test_prepare_is_bit_identical_and_sees_in_place_updates():

@@ -502,29 +502,81 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
   }
 }
 
-// One wave per row: alpha_e = exp(s_e - lse_i), lse_i = log sum exp s over
-// the row (-inf and no weights for an empty row).
+// Segment softmax kernels: each wave takes four consecutive rows.  When
+// the longest of them has at most 16 edges, each row gets a 16-lane slot
+// (one edge per lane, the whole wave at once); at most 32, the rows go
+// two at a time in 32-lane slots; longer, one at a time over the whole
+// wave.  fn(row, slot width, lane in slot) runs for every row of the group
+// (rows past n_rows included, with no edges) on all lanes of its slot.
+constexpr int kSoftmaxRowsPerWave = 4;
+
+template <typename I, typename Fn>
+__device__ __forceinline__ void softmax_row_groups(const I* row_ptr, int64_t n_rows, Fn&& fn) {
+  const int64_t row0 =
+      (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kSoftmaxRowsPerWave;
+  if (row0 >= n_rows) return;   // wave-uniform
+  const int lane = lane_id();
+  const int64_t r = row0 + (lane & 3);
+  const int64_t len =
+      r < n_rows ? static_cast<int64_t>(row_ptr[r + 1]) - static_cast<int64_t>(row_ptr[r]) : 0;
+  int longest = static_cast<int>(len < 64 ? len : 64);
+  longest = max(longest, __shfl_xor(longest, 1, 64));
+  longest = max(longest, __shfl_xor(longest, 2, 64));
+  longest = uniform(longest);
+  if (longest <= 16) {
+    fn(row0 + (lane >> 4), std::integral_constant<int, 16>{}, lane & 15);
+  } else if (longest <= 32) {
+    for (int h = 0; h < 2; ++h) fn(row0 + 2 * h + (lane >> 5), std::integral_constant<int, 32>{},
+                                   lane & 31);
+  } else {
+    for (int q = 0; q < kSoftmaxRowsPerWave; ++q)
+      fn(row0 + q, std::integral_constant<int, 64>{}, lane);
+  }
+}
+
+// alpha_e = exp(s_e - m) / l over one row in a slot of S lanes, lse = m +
+// log l (-inf and no weights for an empty row).  exp(s - m) / l rather than
+// exp(s - lse): s - m is exact (two nearby fp32 values), while lse carries
+// the rounding of a large score (about 6e-5 at 1000, the reference's
+// overflow test).  A row of at most S edges keeps its scores in registers.
+template <int S, typename Score>
+__device__ __forceinline__ void softmax_row(int64_t row, bool has, int64_t e0, int64_t e1,
+                                            int hl, Score&& score, float* __restrict__ alpha,
+                                            float* __restrict__ lse) {
+  const int64_t len = e1 - e0;
+  float m, l;
+  if (len <= S) {
+    const bool on = hl < len;
+    const float sc = on ? score(e0 + hl) : kNegInf;
+    m = group_max<S>(sc);
+    const float p = on ? __expf(sc - m) : 0.f;
+    l = group_sum<S>(p);
+    if (on) alpha[e0 + hl] = p * (1.f / l);
+  } else {
+    m = kNegInf;
+    for (int64_t e = e0 + hl; e < e1; e += S) m = fmaxf(m, score(e));
+    m = group_max<S>(m);
+    l = 0.f;
+    for (int64_t e = e0 + hl; e < e1; e += S) l += __expf(score(e) - m);
+    l = group_sum<S>(l);
+    const float inv = 1.f / l;
+    for (int64_t e = e0 + hl; e < e1; e += S) alpha[e] = __expf(score(e) - m) * inv;
+  }
+  if (has && hl == 0) lse[row] = len > 0 ? m + __logf(l) : kNegInf;
+}
+
+// Scores stored per edge.
 template <typename I>
 __global__ __launch_bounds__(256) void segment_softmax_fwd_kernel(
     const I* __restrict__ row_ptr, int64_t n_rows, const float* __restrict__ scores,
     float* __restrict__ alpha, float* __restrict__ lse) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= n_rows) return;
-  const int lane = lane_id();
-  const int64_t e0 = row_ptr[row], e1 = row_ptr[row + 1];
-  float m = kNegInf;
-  for (int64_t e = e0 + lane; e < e1; e += kWave) m = fmaxf(m, scores[e]);
-  m = group_max<kWave>(m);
-  float l = 0.f;
-  for (int64_t e = e0 + lane; e < e1; e += kWave) l += __expf(scores[e] - m);
-  l = group_sum<kWave>(l);
-  const float ls = e1 > e0 ? m + __logf(l) : kNegInf;
-  // exp(s - m) / l rather than exp(s - lse): s - m is exact (two nearby
-  // fp32 values), while lse carries the rounding of a large score (about
-  // 6e-5 at 1000, the reference's overflow test).
-  const float inv = 1.f / l;
-  for (int64_t e = e0 + lane; e < e1; e += kWave) alpha[e] = __expf(scores[e] - m) * inv;
-  if (lane == 0) lse[row] = ls;
+  softmax_row_groups(row_ptr, n_rows, [&](int64_t row, auto slot, int hl) {
+    const bool has = row < n_rows;
+    const int64_t e0 = has ? static_cast<int64_t>(row_ptr[row]) : 0;
+    const int64_t e1 = has ? static_cast<int64_t>(row_ptr[row + 1]) : 0;
+    softmax_row<decltype(slot)::value>(row, has, e0, e1, hl,
+                                       [&](int64_t e) { return scores[e]; }, alpha, lse);
+  });
 }
 
 // The same with the scores read where a field lives: role 0 a source-node
@@ -545,38 +597,39 @@ __global__ __launch_bounds__(256) void segment_softmax_gather_kernel(
     const I* __restrict__ row_ptr, const I* __restrict__ col, int64_t n_rows,
     const float* __restrict__ scores, float scale, float* __restrict__ alpha,
     float* __restrict__ lse) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= n_rows) return;
-  const int lane = lane_id();
-  const int64_t e0 = row_ptr[row], e1 = row_ptr[row + 1];
-  float m = kNegInf;
-  for (int64_t e = e0 + lane; e < e1; e += kWave)
-    m = fmaxf(m, role_score<I, ROLE>(scores, col, e, row, scale));
-  m = group_max<kWave>(m);
-  float l = 0.f;
-  for (int64_t e = e0 + lane; e < e1; e += kWave)
-    l += __expf(role_score<I, ROLE>(scores, col, e, row, scale) - m);
-  l = group_sum<kWave>(l);
-  const float ls = e1 > e0 ? m + __logf(l) : kNegInf;
-  const float inv = 1.f / l;   // exp(s - m) / l: see segment_softmax_fwd_kernel
-  for (int64_t e = e0 + lane; e < e1; e += kWave)
-    alpha[e] = __expf(role_score<I, ROLE>(scores, col, e, row, scale) - m) * inv;
-  if (lane == 0) lse[row] = ls;
+  softmax_row_groups(row_ptr, n_rows, [&](int64_t row, auto slot, int hl) {
+    const bool has = row < n_rows;
+    const int64_t e0 = has ? static_cast<int64_t>(row_ptr[row]) : 0;
+    const int64_t e1 = has ? static_cast<int64_t>(row_ptr[row + 1]) : 0;
+    softmax_row<decltype(slot)::value>(
+        row, has, e0, e1, hl,
+        [&](int64_t e) { return role_score<I, ROLE>(scores, col, e, row, scale); }, alpha, lse);
+  });
 }
 
-// One wave per row: ds_e = alpha_e (dalpha_e - sum_row alpha dalpha).
+// ds_e = alpha_e (dalpha_e - sum_row alpha dalpha).
 template <typename I>
 __global__ __launch_bounds__(256) void segment_softmax_bwd_kernel(
     const I* __restrict__ row_ptr, int64_t n_rows, const float* __restrict__ alpha,
     const float* __restrict__ dalpha, float* __restrict__ dscore) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= n_rows) return;
-  const int lane = lane_id();
-  const int64_t e0 = row_ptr[row], e1 = row_ptr[row + 1];
-  float d = 0.f;
-  for (int64_t e = e0 + lane; e < e1; e += kWave) d += alpha[e] * dalpha[e];
-  d = group_sum<kWave>(d);
-  for (int64_t e = e0 + lane; e < e1; e += kWave) dscore[e] = alpha[e] * (dalpha[e] - d);
+  softmax_row_groups(row_ptr, n_rows, [&](int64_t row, auto slot, int hl) {
+    constexpr int S = decltype(slot)::value;
+    const bool has = row < n_rows;
+    const int64_t e0 = has ? static_cast<int64_t>(row_ptr[row]) : 0;
+    const int64_t e1 = has ? static_cast<int64_t>(row_ptr[row + 1]) : 0;
+    if (e1 - e0 <= S) {
+      const bool on = hl < e1 - e0;
+      const float al = on ? alpha[e0 + hl] : 0.f;
+      const float da = on ? dalpha[e0 + hl] : 0.f;
+      const float d = group_sum<S>(al * da);
+      if (on) dscore[e0 + hl] = al * (da - d);
+    } else {
+      float d = 0.f;
+      for (int64_t e = e0 + hl; e < e1; e += S) d += alpha[e] * dalpha[e];
+      d = group_sum<S>(d);
+      for (int64_t e = e0 + hl; e < e1; e += S) dscore[e] = alpha[e] * (dalpha[e] - d);
+    }
+  });
 }
 
 // out[c] = sum over rows r of p[r][c] in a fixed order, two levels: block
@@ -982,10 +1035,10 @@ extern "C" int tgx_segment_softmax_fwd(const void* row_ptr, int idx_bits, int64_
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("segment_softmax_fwd_kernel", s);
   if (idx_bits == 32)
-    segment_softmax_fwd_kernel<<<ceil_div(n_rows, 4), 256, 0, s>>>(
+    segment_softmax_fwd_kernel<<<ceil_div(n_rows, 4 * kSoftmaxRowsPerWave), 256, 0, s>>>(
         static_cast<const int32_t*>(row_ptr), n_rows, scores, alpha, lse);
   else
-    segment_softmax_fwd_kernel<<<ceil_div(n_rows, 4), 256, 0, s>>>(
+    segment_softmax_fwd_kernel<<<ceil_div(n_rows, 4 * kSoftmaxRowsPerWave), 256, 0, s>>>(
         static_cast<const int64_t*>(row_ptr), n_rows, scores, alpha, lse);
   TGX_LAUNCHED("segment_softmax_fwd_kernel");
   return TGX_OK;
@@ -997,7 +1050,7 @@ template <typename I>
 void launch_gather_softmax(const I* row_ptr, const I* col, int64_t n_rows,
                            const float* scores, int role, float scale, float* alpha,
                            float* lse, hipStream_t s) {
-  const unsigned blocks = static_cast<unsigned>(ceil_div(n_rows, 4));
+  const unsigned blocks = static_cast<unsigned>(ceil_div(n_rows, 4 * kSoftmaxRowsPerWave));
   if (role == TGX_ROLE_SRC)
     segment_softmax_gather_kernel<I, 0><<<blocks, 256, 0, s>>>(row_ptr, col, n_rows, scores,
                                                                scale, alpha, lse);
@@ -1044,10 +1097,10 @@ extern "C" int tgx_segment_softmax_bwd(const void* row_ptr, int idx_bits, int64_
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("segment_softmax_bwd_kernel", s);
   if (idx_bits == 32)
-    segment_softmax_bwd_kernel<<<ceil_div(n_rows, 4), 256, 0, s>>>(
+    segment_softmax_bwd_kernel<<<ceil_div(n_rows, 4 * kSoftmaxRowsPerWave), 256, 0, s>>>(
         static_cast<const int32_t*>(row_ptr), n_rows, alpha, dalpha, dscore);
   else
-    segment_softmax_bwd_kernel<<<ceil_div(n_rows, 4), 256, 0, s>>>(
+    segment_softmax_bwd_kernel<<<ceil_div(n_rows, 4 * kSoftmaxRowsPerWave), 256, 0, s>>>(
         static_cast<const int64_t*>(row_ptr), n_rows, alpha, dalpha, dscore);
   TGX_LAUNCHED("segment_softmax_bwd_kernel");
   return TGX_OK;

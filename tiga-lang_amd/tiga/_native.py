@@ -198,10 +198,16 @@ def call(name: str, *args) -> None:
     handle = lib()
     status = getattr(handle, name)(*args)
     if status != 0:
-        message = handle.tgx_last_error().decode(errors="replace")
-        kind = handle.tgx_status_string(status).decode()
-        error = NotImplementedError if status == 2 else RuntimeError
-        raise error(f"{name}: {kind}: {message}")
+        raise_status(name, status)
+
+
+def raise_status(name: str, status: int) -> None:
+    """Raise the error a nonzero status of entry point `name` stands for."""
+    handle = lib()
+    message = handle.tgx_last_error().decode(errors="replace")
+    kind = handle.tgx_status_string(status).decode()
+    error = NotImplementedError if status == 2 else RuntimeError
+    raise error(f"{name}: {kind}: {message}")
 
 
 def exported_symbols() -> list[str]:

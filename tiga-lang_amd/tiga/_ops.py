@@ -75,6 +75,46 @@ def csr_sum(x: torch.Tensor, w: torch.Tensor | None, graph: Graph) -> torch.Tens
     return _csr_sum_launch(x, w, graph)[0]
 
 
+def bind_csr_sum(x: torch.Tensor, w: torch.Tensor | None, graph: Graph):
+    """The forward launch of tg.sum() of [w *] x with every native argument
+    but the output bound: a zero-argument callable returning a new output
+    per call, or None when the kernel would not read x and w in place (a
+    converted or compacted copy would hide later in-place updates)."""
+    _on_graph_device(graph, x, w)
+    xc = _aligned(x)
+    wc = None if w is None else w.reshape(-1).contiguous()
+    if xc.data_ptr() != x.data_ptr() or (wc is not None and wc.data_ptr() != w.data_ptr()):
+        return None
+    row_ptr, col_idx = graph._kernel_csr()
+    n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
+    feat_shape = tuple(x.shape[1:])
+    F = 1
+    for d in feat_shape:
+        F *= d
+    out_shape, dtype, device = (n_dst, *feat_shape), x.dtype, x.device
+    if not (n_dst and F):
+        return lambda: torch.empty(out_shape, dtype=dtype, device=device)
+    plan = graph._row_plan()
+    partial = _partial(plan, F, device)
+    fn = _native.lib().tgx_csr_sum_fwd
+    head = (row_ptr.data_ptr(), col_idx.data_ptr(), _native.idx_bits(row_ptr), plan.ref,
+            xc.data_ptr(), _p(wc))
+    tail = (n_dst, n_src, F, _native.dtype_code(xc), _p(partial))
+    keep = (row_ptr, col_idx, plan, xc, wc, partial)   # alive as long as the launch
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    raw_stream = torch._C._cuda_getCurrentRawStream
+
+    def launch():
+        out = torch.empty(out_shape, dtype=dtype, device=device)
+        status = fn(*head, out.data_ptr(), *tail, raw_stream(index))
+        if status != 0:
+            _native.raise_status("tgx_csr_sum_fwd", status)
+        return out
+
+    launch.keep = keep
+    return launch
+
+
 class CsrSumFunction(torch.autograd.Function):
     """out[i] = sum_e w[e] * x[col[e]]  (w optional): x fp32, bf16 or fp16
     (out, dout and dx of the same type), w fp32; fp32 products and sums."""

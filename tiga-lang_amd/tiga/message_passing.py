@@ -125,6 +125,9 @@ class _Launch:
     describe: Callable[[], CompiledVariant]
     aliases: tuple = ()
     variant: CompiledVariant | None = None
+    # Optional: operands -> a zero-argument launch with its native arguments
+    # bound (prepare()'s no-grad form), or None where that does not apply.
+    bind: Callable | None = None
 
     @property
     def guardable(self) -> bool:
@@ -302,8 +305,12 @@ class MessagePassing(Kernel):
         operands = tuple(launch.gather(src, dst, edge, params))
         runner, epilogue = launch.runner, self._epilogue
         frozen_dst, frozen_params = dict(dst), dict(params)
+        bound = launch.bind(*operands) if launch.bind is not None else None
+        tensors = tuple(t for t in operands if isinstance(t, torch.Tensor))
 
         def run():
+            if bound is not None and not any(t.requires_grad for t in tensors):
+                return epilogue(frozen_dst, bound(), frozen_params)
             return epilogue(frozen_dst, runner(*operands), frozen_params)
 
         run.variant = launch.variant
@@ -462,11 +469,18 @@ class MessagePassing(Kernel):
             wk = None if w is None else w.to(torch.float32)
             return _ops.csr_sum(xk, wk, graph)
 
+        def bind(x, w=None):
+            # Only where the kernel reads the bound tensors themselves (no
+            # dtype conversion), so later in-place updates are seen.
+            if x.dtype != out_dtype or (w is not None and w.dtype != torch.float32):
+                return None
+            return _ops.bind_csr_sum(x, w, graph)
+
         kind = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}[out_dtype]
         describe = lambda: self._variant(
             graph, "weighted-sum", ("tgx_csr_sum_fwd", "tgx_csr_sum_bwd"),
             f"degree-binned rows -> wave gather-FMA ({kind} features, fp32 sums)")
-        return _Launch(graph, tuple(operands), run, describe)
+        return _Launch(graph, tuple(operands), run, describe, bind=bind)
 
     def _plan_gat(self, gat, graph, src, dst, params) -> _Launch | None:
         from . import _ops
