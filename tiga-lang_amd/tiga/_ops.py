@@ -95,18 +95,20 @@ def bind_csr_sum(x: torch.Tensor, w: torch.Tensor | None, graph: Graph):
     if not (n_dst and F):
         return lambda: torch.empty(out_shape, dtype=dtype, device=device)
     plan = graph._row_plan()
-    partial = _partial(plan, F, device)
+    n_partial = plan.plan.n_chunks * F   # split-row partials: fresh per call
     fn = _native.lib().tgx_csr_sum_fwd
     head = (row_ptr.data_ptr(), col_idx.data_ptr(), _native.idx_bits(row_ptr), plan.ref,
             xc.data_ptr(), _p(wc))
-    tail = (n_dst, n_src, F, _native.dtype_code(xc), _p(partial))
-    keep = (row_ptr, col_idx, plan, xc, wc, partial)   # alive as long as the launch
+    tail = (n_dst, n_src, F, _native.dtype_code(xc))
+    keep = (row_ptr, col_idx, plan, xc, wc)   # alive as long as the launch
     index = device.index if device.index is not None else torch.cuda.current_device()
     raw_stream = torch._C._cuda_getCurrentRawStream
 
     def launch():
         out = torch.empty(out_shape, dtype=dtype, device=device)
-        status = fn(*head, out.data_ptr(), *tail, raw_stream(index))
+        partial = (torch.empty(n_partial, dtype=torch.float32, device=device)
+                   if n_partial else None)
+        status = fn(*head, out.data_ptr(), *tail, _p(partial), raw_stream(index))
         if status != 0:
             _native.raise_status("tgx_csr_sum_fwd", status)
         return out
@@ -381,8 +383,11 @@ def _folded(layer, weight, bias):
     W' = scale in_scale W, b' = scale (b + in_shift W 1) + shift.  b' is
     None when it is identically zero."""
     w = weight.detach()
-    wf = w * (layer.scale * layer.in_scale)
-    bf = None if bias is None else bias.detach() * layer.scale
+    f = layer.scale * layer.in_scale
+    # (Factors of 1 are skipped: each product is a launch of its own.)
+    wf = w if f == 1.0 else w * f
+    bf = None if bias is None else (bias.detach() if layer.scale == 1.0
+                                    else bias.detach() * layer.scale)
     if layer.in_shift != 0.0:
         extra = w.sum(1) * (layer.scale * layer.in_shift)
         bf = extra if bf is None else bf + extra
@@ -397,11 +402,12 @@ def _unfolded_grads(layer, dwf, dbf, need_w, need_b):
     db' 1^T, db = scale db'."""
     dW = db = None
     if need_w and dwf is not None:
-        dW = dwf * (layer.scale * layer.in_scale)
+        f = layer.scale * layer.in_scale
+        dW = dwf if f == 1.0 else dwf * f
         if layer.in_shift != 0.0:
             dW = dW + (dbf * (layer.scale * layer.in_shift))[:, None]
     if need_b and dbf is not None:
-        db = dbf * layer.scale
+        db = dbf if layer.scale == 1.0 else dbf * layer.scale
     return dW, db
 
 
