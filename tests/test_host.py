@@ -420,6 +420,20 @@ def test_edge_mlp_validation_of_layer_widths():
         assert lib.tgx_edge_mlp_backward_workspace(0, ctypes.byref(m), ctypes.byref(size)) == 0
 
 
+def test_sum_rejects_source_tables_past_32_bit_rows():
+    """The sum kernels hold gathered row indices in 32 bits: a source table of
+    2^31 rows or more is refused before anything is launched."""
+    lib = _native.lib()
+    plan = _native.RowPlan(4, 0, 4, 0, 0, 512, 512, 0x1000, 0x1000)
+    dummy = 0x1000   # never dereferenced: validation fails first
+    st = lib.tgx_csr_sum_fwd(dummy, dummy, 64, ctypes.byref(plan), dummy, None, dummy, 4,
+                             1 << 31, 1, _native.DTYPE_F32, None, None)
+    assert st == 1 and b"2^31 rows" in lib.tgx_last_error()
+    st = lib.tgx_csr_edge_dot(dummy, dummy, 64, ctypes.byref(plan), dummy, dummy, dummy, 4,
+                              1 << 31, 1, _native.DTYPE_F32, None)
+    assert st == 1 and b"2^31 rows" in lib.tgx_last_error()
+
+
 def test_bench_refuses_more_than_one_gpu():
     """bench.py measures one GPU; --gpus N > 1 exits with a message before any
     GPU work."""

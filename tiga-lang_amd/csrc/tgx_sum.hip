@@ -152,13 +152,14 @@ __device__ __forceinline__ void sum_task(const SumArgs<I, DT>& a, const Task& t)
     const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
     int my_col = 0;
     float my_w = 0.f;
-    int my_widx = 0;
+    int my_wp = 0;   // wperm[e] (int32: a permuted relation has < 2^31 edges)
     if (lane < n) {
       // No column array: the columns are the edge ids (a per-edge field
       // summed per row, read contiguously).
-      my_col = a.col ? static_cast<int>(a.col[base + lane]) : static_cast<int>(base + lane);
-      my_widx = a.wperm ? a.wperm[base + lane] : static_cast<int>(base + lane);
-      my_w = a.w ? a.w[my_widx] : 1.f;
+      const int64_t e = base + lane;
+      my_col = a.col ? static_cast<int>(a.col[e]) : static_cast<int>(e);
+      if (a.wperm) my_wp = a.wperm[e];
+      my_w = a.w ? a.w[a.wperm ? static_cast<int64_t>(my_wp) : e] : 1.f;
     }
     for (int k = 0; k < n; k += EPW * U) {
       T v[U];
@@ -182,7 +183,8 @@ __device__ __forceinline__ void sum_task(const SumArgs<I, DT>& a, const Task& t)
         for (int u = 0; u < U; ++u) {
           float d = group_reduce_sum<G>(V::dot(v[u], self));
           const int src = slot[u] < n ? slot[u] : 0;
-          const int widx = __shfl(my_widx, src, 64);
+          const int wp = __shfl(my_wp, src, 64);
+          const int64_t widx = a.wperm ? static_cast<int64_t>(wp) : base + src;
           if (c == 0 && slot[u] < n) a.dw[widx] = d;
         }
       }
@@ -265,19 +267,19 @@ __global__ __launch_bounds__(kTaskBlock) void sum_pairs_kernel(SumArgs<I, DT> a)
       self[q] = V::load(a.self_x + static_cast<int64_t>(row[q]) * F + fo);
   }
   for (int base = 0; base < len_max; base += SLOT) {
-    int n[P], my_col[P], my_widx[P];
+    int n[P], my_col[P], my_wp[P];
     float my_w[P];
 #pragma unroll
     for (int q = 0; q < P; ++q) {
       n[q] = min(max(len[q] - base, 0), SLOT);   // this row's edges
       my_col[q] = 0;
-      my_widx[q] = 0;
+      my_wp[q] = 0;
       my_w[q] = 0.f;
       if (hl < n[q]) {
         const int64_t e = e0[q] + base + hl;
         my_col[q] = a.col ? static_cast<int>(a.col[e]) : static_cast<int>(e);
-        my_widx[q] = a.wperm ? a.wperm[e] : static_cast<int>(e);
-        my_w[q] = a.w ? a.w[my_widx[q]] : 1.f;
+        if (a.wperm) my_wp[q] = a.wperm[e];
+        my_w[q] = a.w ? a.w[a.wperm ? static_cast<int64_t>(my_wp[q]) : e] : 1.f;
       }
     }
     const int n_max = min(len_max - base, SLOT);   // wave-uniform
@@ -308,8 +310,9 @@ __global__ __launch_bounds__(kTaskBlock) void sum_pairs_kernel(SumArgs<I, DT> a)
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             const float d = group_reduce_sum<G>(V::dot(v[q][u], self[q]));
-            const int src = SLOT * slot_id + (slot[u] < n[q] ? slot[u] : 0);
-            const int widx = __shfl(my_widx[q], src, 64);
+            const int k = slot[u] < n[q] ? slot[u] : 0;
+            const int wp = __shfl(my_wp[q], SLOT * slot_id + k, 64);
+            const int64_t widx = a.wperm ? static_cast<int64_t>(wp) : e0[q] + base + k;
             if (c == 0 && slot[u] < n[q]) a.dw[widx] = d;
           }
       }
@@ -472,6 +475,8 @@ extern "C" int tgx_csr_sum_fwd(const void* row_ptr, const void* col, int idx_bit
   TGX_REQUIRE(row_ptr && out && (x || n_src == 0), "null pointer");
   // A null col means the columns are the edge ids (x holds one row per edge).
   TGX_REQUIRE(col || n_src < (int64_t{1} << 31), "edge-id columns need fewer than 2^31 edges");
+  // Gathered row indices are held in 32 bits.
+  TGX_REQUIRE(n_src < (int64_t{1} << 31), "source tables need fewer than 2^31 rows");
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("csr_sum_fwd", s);
@@ -549,6 +554,7 @@ extern "C" int tgx_csr_edge_dot(const void* row_ptr, const void* col, int idx_bi
   if (st != TGX_OK) return st;
   if (n_dst == 0) return TGX_OK;
   TGX_REQUIRE(row_ptr && col && x && dout && dw, "null pointer");
+  TGX_REQUIRE(n_src < (int64_t{1} << 31), "source tables need fewer than 2^31 rows");
   hipStream_t s = as_stream(stream);
   TGX_PROFILE("csr_edge_dot", s);
   auto run = [&](auto dt, auto idx) -> int {
