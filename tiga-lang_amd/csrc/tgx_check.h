@@ -33,6 +33,7 @@ inline int check_plan(const tgx_row_plan* p, int64_t rows) {
                   p->n_chunks >= 0 && p->n_empty + p->n_wave + p->n_split == p->n_rows,
               "inconsistent plan");
   TGX_REQUIRE(p->n_rows == 0 || p->rows_dev, "plan without rows");
+  TGX_REQUIRE(p->n_rows < (int64_t{1} << 31), "plan rows are 32-bit: fewer than 2^31 rows");
   TGX_REQUIRE(p->n_split == 0 || (p->chunk_offsets_dev && p->chunk_edges > 0 &&
                                   p->n_chunks >= p->n_split),
               "plan without chunk offsets");

@@ -604,6 +604,8 @@ extern "C" int tgx_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bi
   if (n_dst == 0) return TGX_OK;
   TGX_REQUIRE(row_ptr && q && out && ml && ((k && v) || n_src == 0), "null pointer");
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
+  // Gathered row indices are held in 32 bits.
+  TGX_REQUIRE(n_src < (int64_t{1} << 31), "source tables need fewer than 2^31 rows");
   hipStream_t s = as_stream(stream);
   const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
   for (int h0 = 0; h0 < H;) {
