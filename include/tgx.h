@@ -396,6 +396,42 @@ int tgx_attn_fwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev, const int32_t
                  float scale, float prune_threshold, void* out_dev, float* lse_dev,
                  int64_t n_q, int64_t n_k, int H, int D, void* stream);
 
+/* Host: forward tasks with long query tiles' key ranges split, for
+ * relations whose tiles are too few and too uneven to fill the GPU (one
+ * causal block of a few thousand tokens: the last query tile sees all keys
+ * and would alone set the launch time).  `slots` is the number of forward
+ * workgroups resident at once (2 per CU).  The balanced load is the total
+ * of 64-key tiles over all query tiles and heads divided by `slots` (at
+ * least 8); when the longest tile sees at least 5/4 of it, every tile seeing
+ * more is cut into chunks of *chunk_tiles = that many key tiles, else
+ * nothing is split (*n_merge = 0: use tgx_attn_tasks kind 0 and
+ * tgx_attn_fwd).  tasks_host [n_tasks, 4] = (block, first query, head,
+ * code): code -1 a whole tile, else the partial slot of a chunk, chunk c =
+ * slot % *max_chunks of split tile slot / *max_chunks; merge_host [n_merge,
+ * 4] = (block, first query, head, chunks) per split tile, in slot order.
+ * Groups (block, head) go to the XCDs as in tgx_attn_tasks, each group's
+ * tasks heaviest first.  Call with tasks_host = merge_host = NULL for the
+ * counts.  No counterpart in the reference, whose dense tile runs one
+ * program per query block (Translate.cpp:1603-1912). */
+int tgx_attn_fwd_split_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host, int n_blocks,
+                             int H, int causal, int slots, int32_t* tasks_host,
+                             int64_t* n_tasks, int32_t* merge_host, int64_t* n_merge,
+                             int32_t* chunk_tiles, int32_t* max_chunks);
+
+/* tgx_attn_fwd (exact: no pruning) over tgx_attn_fwd_split_tasks' lists:
+ * key chunks write unnormalized O, running max and sum to partial_dev
+ * (n_merge * max_chunks * 128 * (D + 2) fp32), then one merge workgroup per
+ * split tile combines its chunks in chunk order and writes out and lse as
+ * the whole-tile epilogue does.  Same results as tgx_attn_fwd up to the
+ * order of the softmax sums (chunk by chunk instead of one running sum). */
+int tgx_attn_fwd_split(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
+                       const int32_t* tasks_dev, int64_t n_tasks, const int32_t* merge_dev,
+                       int64_t n_merge, int32_t chunk_tiles, int32_t max_chunks, int causal,
+                       int dtype, const void* q_dev, const void* k_dev, const void* v_dev,
+                       const int64_t* strides, float scale, void* out_dev, float* lse_dev,
+                       float* partial_dev, int64_t n_q, int64_t n_k, int H, int D,
+                       void* stream);
+
 /* Backward of the exact forward (no atomics): delta = <dout, out> into
  * delta_dev [n_q, H] fp32, then dK/dV over key tiles (k_tasks: kind 1,
  * block 64) and dQ over query tiles (q_tasks: kind 0, block 128).  dout, dq

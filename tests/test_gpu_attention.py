@@ -251,3 +251,48 @@ def test_dense_uncovered_edge_function_runs_eager_on_materialized_relation():
     p /= p.sum(-1, keepdims=True)
     np.testing.assert_allclose(f64(out), np.einsum("hij,jhd->ihd", p, f64(v)), rtol=1e-5,
                                atol=1e-6)
+
+
+def torch_block_attention(q, k, v, scale, causal):
+    """fp32 Torch attention over one block ([n, H, D] in, [n, H, D] out)."""
+    qf, kf, vf = (t.detach().float().permute(1, 0, 2).contiguous() for t in (q, k, v))
+    s = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * scale
+    if causal:
+        n = s.shape[-1]
+        s.masked_fill_(torch.ones(n, n, dtype=torch.bool, device=DEV).triu(1), float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vf).permute(1, 0, 2)
+
+
+@pytest.mark.parametrize("n,H,D,causal,dtype", [
+    (4096, 16, 64, True, torch.float16),     # the reference's causal dense case: 2 chunks
+    (8192, 2, 128, True, torch.bfloat16),    # up to 8 chunks per tile
+    (4096, 4, 64, False, torch.bfloat16),    # few, equal tiles: 4 chunks each
+])
+def test_split_key_ranges_match_whole_tiles(n, H, D, causal, dtype):
+    """Relations with too few query tiles to fill the GPU run the longest key
+    ranges in chunks (tgx_attn_fwd_split) and merge them: the output matches
+    fp32 attention, and the forward and the gradients match the whole-tile
+    forward's up to the order of the softmax sums."""
+    print(f"split forward n={n} H={H} D={D} causal={causal} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(n + H + D)
+    base = [torch.randn(n, H, D, device=DEV, generator=g).to(dtype) for _ in range(4)]
+    results = []
+    for split in (True, False):
+        graph = tg.Graph.triangular(n, device=DEV) if causal else tg.Graph.dense(n, device=DEV)
+        if split:
+            plan = graph._attn_fwd_split(H)
+            assert plan is not None and plan[3] > 0
+        else:
+            graph._native_cache[("attn-split", H)] = None   # whole tiles only
+        q, k, v = (t.clone().requires_grad_(True) for t in base[:3])
+        kernel = DotAttention()
+        out = kernel(graph=graph, src={"key": k, "value": v}, dst={"query": q},
+                     scale=D ** -0.5)
+        assert kernel.last_variant.backend == "hip"
+        out.backward(base[3])
+        results.append((out.detach().float(), q.grad.float(), k.grad.float(), v.grad.float()))
+    tol = TOL[dtype]
+    expect = torch_block_attention(base[0], base[1], base[2], D ** -0.5, causal)
+    assert float((results[0][0] - expect).abs().max() / expect.abs().max()) <= tol
+    for a, b in zip(results[0], results[1]):
+        assert float((a - b).abs().max() / b.abs().max()) <= tol

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_native.exported_symbols())
-    assert lib.tgx_abi_version() == 7
+    assert lib.tgx_abi_version() == 8
     assert lib.tgx_status_string(1) == b"invalid argument"
 
 
@@ -432,6 +432,60 @@ def test_sum_rejects_source_tables_past_32_bit_rows():
     st = lib.tgx_csr_edge_dot(dummy, dummy, 64, ctypes.byref(plan), dummy, dummy, dummy, 4,
                               1 << 31, 1, _native.DTYPE_F32, None)
     assert st == 1 and b"2^31 rows" in lib.tgx_last_error()
+
+
+@pytest.mark.parametrize("cu,H,causal", [
+    ([0, 4096], 16, 1),                 # one causal block: two chunks for the long tiles
+    ([0, 8192], 2, 1),                  # up to eight chunks
+    ([0, 4096], 4, 0),                  # non-causal, few equal tiles
+    ([0, 700, 705, 3000], 3, 1),        # several blocks, a short one
+    ([0, 512, 1024], 16, 1),            # balanced: nothing split
+])
+def test_attn_fwd_split_tasks_cover_every_key_tile_once(cu, H, causal):
+    """tgx_attn_fwd_split_tasks: every (query tile, head) is one whole task or
+    chunks that cover its 64-key tiles exactly once, each chunk at most
+    chunk_tiles long, with one merge entry per split tile naming its chunks."""
+    lib = _native.lib()
+    cu = np.asarray(cu, dtype=np.int32)
+    n, nm = ctypes.c_int64(), ctypes.c_int64()
+    chunk, mc = ctypes.c_int32(), ctypes.c_int32()
+    args = (cu.ctypes.data, cu.ctypes.data, cu.size - 1, H, causal, 512)
+    assert lib.tgx_attn_fwd_split_tasks(*args, None, ctypes.byref(n), None, ctypes.byref(nm),
+                                        ctypes.byref(chunk), ctypes.byref(mc)) == 0
+    tasks = np.zeros(4 * max(n.value, 1), dtype=np.int32)
+    merge = np.zeros(4 * max(nm.value, 1), dtype=np.int32)
+    assert lib.tgx_attn_fwd_split_tasks(*args, tasks.ctypes.data, ctypes.byref(n),
+                                        merge.ctypes.data, ctypes.byref(nm),
+                                        ctypes.byref(chunk), ctypes.byref(mc)) == 0
+    tasks = tasks.reshape(-1, 4)[:n.value]
+    merge = merge.reshape(-1, 4)[:nm.value]
+    assert n.value % 8 == 0
+    covered = {}
+    for blk, q0, h, code in tasks:
+        if blk < 0:
+            continue
+        k0, k1 = cu[blk], cu[blk + 1]
+        nk = -(-((min(q0 + 128, k1) if causal else k1) - k0) // 64)
+        if code < 0:
+            assert nk <= chunk.value
+            tiles = range(nk)
+        else:
+            m, c = divmod(int(code), mc.value)
+            assert tuple(merge[m][:3]) == (blk, q0, h) and c < merge[m][3]
+            tiles = range(c * chunk.value, min(nk, (c + 1) * chunk.value))
+            assert len(tiles) > 0
+        for t in tiles:
+            key = (int(blk), int(q0), int(h), t)
+            assert key not in covered
+            covered[key] = True
+    expect = 0
+    for b in range(cu.size - 1):
+        for q0 in range(cu[b], cu[b + 1], 128):
+            nk = -(-((min(q0 + 128, cu[b + 1]) if causal else cu[b + 1]) - cu[b]) // 64)
+            expect += nk * H
+    assert len(covered) == expect
+    if cu.tolist() == [0, 512, 1024]:
+        assert nm.value == 0
 
 
 def test_bench_refuses_more_than_one_gpu():

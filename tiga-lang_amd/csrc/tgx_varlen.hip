@@ -238,7 +238,20 @@ struct FwdArgs {
   float* lse;             // [n_q, H]
   float scale_log2;       // softmax scale * log2(e)
   float prune_log2;       // log2(block_prune_threshold) (PRUNE only)
+  // Split key ranges (chunk_tiles > 0): task[3] >= 0 is the partial slot of
+  // a key chunk, which covers the tile's 64-key tiles [c, c + 1) *
+  // chunk_tiles, c = slot % max_chunks, and writes its unnormalized O, its
+  // running max and its sum to partial (kPartialFloats<D> per slot) for
+  // varlen_fwd_merge_kernel; task[3] = -1 is a whole tile.
+  int chunk_tiles;
+  int max_chunks;
+  float* partial;
 };
+
+// Floats of one key chunk's partial: O [128 queries][D], then the running
+// max (scaled log2 units) and the sum per query.
+template <int D>
+constexpr int64_t kPartialFloats = static_cast<int64_t>(VBM) * (D + 2);
 
 template <typename T, int D, bool CAUSAL, bool PRUNE>
 __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
@@ -273,7 +286,11 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
   }
 
   const int kv_end = CAUSAL ? min(q0 + VBM, ks1) : ks1;
-  const int n_kv = (kv_end - ks0 + VBN - 1) / VBN;
+  const int n_kv_all = (kv_end - ks0 + VBN - 1) / VBN;
+  // The key tiles this task covers: all, or one chunk of them.
+  const int slot = a.chunk_tiles > 0 ? task[3] : -1;
+  const int it0 = slot >= 0 ? (slot % a.max_chunks) * a.chunk_tiles : 0;
+  const int n_kv = slot >= 0 ? min(n_kv_all, it0 + a.chunk_tiles) : n_kv_all;
   const float sl2 = a.scale_log2;
   // Running max in scaled log2 units (-inf until a score is seen).
   float m[2] = {kNegInf, kNegInf};
@@ -300,11 +317,11 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
   float block_m = kNegInf;
 
   Stage<T, D> stage;
-  if (n_kv > 0) {
-    stage_load<T, D, true>(stage, kh, a.ksn, vh, a.ksn, ks0, ks1);
-    stage_store<T, D>(stage, ks[0], vs[0]);
+  if (it0 < n_kv) {
+    stage_load<T, D, true>(stage, kh, a.ksn, vh, a.ksn, ks0 + it0 * VBN, ks1);
+    stage_store<T, D>(stage, ks[it0 & 1], vs[it0 & 1]);
   }
-  for (int it = 0; it < n_kv; ++it) {
+  for (int it = it0; it < n_kv; ++it) {
     __syncthreads();
     const int buf = it & 1;
     const int kbase = ks0 + it * VBN;
@@ -418,6 +435,24 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
     if (more) stage_store<T, D>(stage, ks[buf ^ 1], vs[buf ^ 1]);
   }
 
+  if (slot >= 0) {
+    // A key chunk: O^T (not normalized), the running max and the sum of
+    // each of the tile's queries, for the merge.
+    float* part = a.partial + static_cast<int64_t>(slot) * kPartialFloats<D>;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int qr = qb - q0 + 16 * qt + lr;   // query row in the tile
+      if (qb + 16 * qt + lr >= qs1) continue;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<f32x4v*>(part + qr * D + 16 * dt + 4 * g) = o[dt][qt];
+      if (g == 0) {
+        part[VBM * D + qr] = m[qt];
+        part[VBM * D + VBM + qr] = lsum[qt][0];
+      }
+    }
+    return;
+  }
   // Finalize: O = O^T / l, natural-log lse (a row that sees no key gets 0
   // and -inf).
 #pragma unroll
@@ -437,6 +472,51 @@ __global__ __launch_bounds__(256, 2) void varlen_fwd_kernel(FwdArgs<T> a) {
     if (g == 0)
       a.lse[static_cast<int64_t>(qq) * a.H + h] = l > 0.f ? (m[qt] + __log2f(l)) * kLn2
                                                            : kNegInf;
+  }
+}
+
+// Combine the key chunks of each split query tile (merge[m] = (block, first
+// query, head, chunks), slots m * max_chunks + c) in chunk order: the
+// largest running max M, l = sum_c l_c 2^(m_c - M), O = sum_c O_c 2^(m_c -
+// M) / l; then out and lse as the whole-tile epilogue writes them.  A
+// thread per (query, 4 features): kMergeBlocks<D> workgroups per split tile.
+template <int D>
+constexpr int kMergeBlocks = VBM * (D / 4) / 256;
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void varlen_fwd_merge_kernel(
+    const int32_t* __restrict__ merge, const int32_t* __restrict__ cu_q, int H,
+    int max_chunks, const float* __restrict__ partial, T* __restrict__ out,
+    float* __restrict__ lse) {
+  const int64_t mi = blockIdx.x / kMergeBlocks<D>;
+  const int32_t* mt = merge + 4 * mi;
+  const int blk = mt[0], q0 = mt[1], h = mt[2], nc = mt[3];
+  const int qs1 = cu_q[blk + 1];
+  const float* base = partial + mi * max_chunks * kPartialFloats<D>;
+  constexpr int CPR = D / 4;   // 4-feature chunks per query row
+  {
+    const int w = (blockIdx.x % kMergeBlocks<D>) * 256 + threadIdx.x;
+    const int qr = w / CPR, d4 = 4 * (w % CPR);
+    const int qq = q0 + qr;
+    if (qq >= qs1) return;
+    float mx = kNegInf;
+    for (int c = 0; c < nc; ++c) mx = fmaxf(mx, base[c * kPartialFloats<D> + VBM * D + qr]);
+    float l = 0.f;
+    f32x4v acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nc; ++c) {
+      const float* pc = base + c * kPartialFloats<D>;
+      const float mc = pc[VBM * D + qr];
+      const float f = mc == kNegInf ? 0.f : exp2_hw(mc - mx);
+      l += pc[VBM * D + VBM + qr] * f;
+      acc += *reinterpret_cast<const f32x4v*>(pc + qr * D + d4) * f;
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    vec4<T> wv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv[r] = static_cast<T>(acc[r] * inv);
+    *reinterpret_cast<vec4<T>*>(out + (static_cast<int64_t>(qq) * H + h) * D + d4) = wv;
+    if (d4 == 0)
+      lse[static_cast<int64_t>(qq) * H + h] = l > 0.f ? (mx + __log2f(l)) * kLn2 : kNegInf;
   }
 }
 
@@ -1197,6 +1277,111 @@ extern "C" int tgx_attn_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host
   return TGX_OK;
 }
 
+extern "C" int tgx_attn_fwd_split_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host,
+                                        int n_blocks, int H, int causal, int slots,
+                                        int32_t* tasks_host, int64_t* n_tasks,
+                                        int32_t* merge_host, int64_t* n_merge,
+                                        int32_t* chunk_tiles, int32_t* max_chunks) {
+  TGX_REQUIRE(cu_q_host && cu_k_host && n_tasks && n_merge && chunk_tiles && max_chunks &&
+                  n_blocks >= 0 && H > 0 && slots > 0,
+              "bad arguments");
+  // Key tiles (64 keys) each 128-query tile sees; their total over the
+  // relation and heads spread over the resident workgroup slots is the
+  // balanced load.  Tiles seeing more than that are split into chunks of
+  // that many key tiles (when the longest tile is at least 5/4 of it).
+  int64_t total = 0, longest = 0;
+  for (int b = 0; b < n_blocks; ++b) {
+    const int q0 = cu_q_host[b], q1 = cu_q_host[b + 1];
+    const int k0 = cu_k_host[b], k1 = cu_k_host[b + 1];
+    TGX_REQUIRE(q1 >= q0 && q0 >= 0 && k1 >= k0 && k0 >= 0,
+                "cu_seqlens must be non-decreasing from 0");
+    TGX_REQUIRE(!causal || (q0 == k0 && q1 == k1), "causal blocks must be square");
+    for (int r = q0; r < q1; r += VBM) {
+      const int kv_end = causal ? std::min(r + VBM, k1) : k1;
+      const int64_t nk = (kv_end - k0 + VBN - 1) / VBN;
+      total += nk * H;
+      longest = std::max(longest, nk);
+    }
+  }
+  const int64_t balanced = std::max<int64_t>((total + slots - 1) / slots, 8);
+  const bool split = 4 * longest >= 5 * balanced;
+  const int64_t chunk = split ? balanced : std::max<int64_t>(longest, 1);
+  TGX_REQUIRE(chunk < (int64_t{1} << 31), "too many key tiles");
+  const int64_t mc = (longest + chunk - 1) / chunk;
+  *chunk_tiles = static_cast<int32_t>(chunk);
+  *max_chunks = static_cast<int32_t>(std::max<int64_t>(mc, 1));
+  // Tasks per (block, head) group, groups over the XCDs as in
+  // tgx_attn_tasks; within a group the heaviest task first.
+  struct Task4 {
+    int64_t work;
+    int32_t v[4];
+  };
+  struct Group {
+    int blk, head;
+    int64_t work;
+  };
+  std::vector<Group> groups;
+  for (int b = 0; b < n_blocks; ++b) {
+    const int q0 = cu_q_host[b], q1 = cu_q_host[b + 1], k0 = cu_k_host[b], k1 = cu_k_host[b + 1];
+    if (q1 == q0) continue;
+    int64_t w = 0;
+    for (int r = q0; r < q1; r += VBM) w += causal ? std::min(r + VBM, k1) - k0 : k1 - k0;
+    for (int h = 0; h < H; ++h) groups.push_back(Group{b, h, std::max<int64_t>(w, 1)});
+  }
+  std::stable_sort(groups.begin(), groups.end(),
+                   [](const Group& x, const Group& y) { return x.work > y.work; });
+  std::vector<std::vector<int32_t>> queue(kXcds);
+  std::vector<int32_t> merges;
+  int64_t load[kXcds] = {};
+  for (const Group& gr : groups) {
+    int x = 0;
+    for (int i = 1; i < kXcds; ++i)
+      if (load[i] < load[x]) x = i;
+    load[x] += gr.work;
+    const int q0 = cu_q_host[gr.blk], q1 = cu_q_host[gr.blk + 1];
+    const int k0 = cu_k_host[gr.blk], k1 = cu_k_host[gr.blk + 1];
+    std::vector<Task4> tasks;
+    for (int r = q0; r < q1; r += VBM) {
+      const int kv_end = causal ? std::min(r + VBM, k1) : k1;
+      const int64_t nk = (kv_end - k0 + VBN - 1) / VBN;
+      if (nk <= chunk) {
+        tasks.push_back(Task4{std::max<int64_t>(nk, 1), {gr.blk, r, gr.head, -1}});
+        continue;
+      }
+      const int64_t m = static_cast<int64_t>(merges.size()) / 4;
+      const int64_t nc = (nk + chunk - 1) / chunk;
+      TGX_REQUIRE((m + 1) * *max_chunks < (int64_t{1} << 31), "too many split tiles");
+      merges.insert(merges.end(), {gr.blk, r, gr.head, static_cast<int32_t>(nc)});
+      for (int64_t c = 0; c < nc; ++c)
+        tasks.push_back(Task4{std::min(chunk, nk - c * chunk),
+                              {gr.blk, r, gr.head, static_cast<int32_t>(m * *max_chunks + c)}});
+    }
+    std::stable_sort(tasks.begin(), tasks.end(),
+                     [](const Task4& a, const Task4& b) { return a.work > b.work; });
+    for (const Task4& t : tasks) queue[x].insert(queue[x].end(), t.v, t.v + 4);
+  }
+  size_t deepest = 0;
+  for (const auto& qx : queue) deepest = std::max(deepest, qx.size() / 4);
+  const int64_t n = static_cast<int64_t>(deepest) * kXcds;
+  TGX_REQUIRE(n < (int64_t{1} << 31), "too many tasks");
+  *n_tasks = n;
+  *n_merge = static_cast<int64_t>(merges.size()) / 4;
+  if (tasks_host) {
+    for (size_t i = 0; i < deepest; ++i)
+      for (int x = 0; x < kXcds; ++x) {
+        int32_t* dst = tasks_host + 4 * (static_cast<int64_t>(i) * kXcds + x);
+        if (4 * i < queue[x].size()) {
+          for (int c = 0; c < 4; ++c) dst[c] = queue[x][4 * i + c];
+        } else {
+          dst[0] = -1;
+          dst[1] = dst[2] = dst[3] = 0;
+        }
+      }
+  }
+  if (merge_host) std::copy(merges.begin(), merges.end(), merge_host);
+  return TGX_OK;
+}
+
 extern "C" int tgx_attn_fwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
                             const int32_t* tasks_dev, int64_t n_tasks, int causal, int dtype,
                             const void* q, const void* k, const void* v, const int64_t* strides,
@@ -1218,6 +1403,52 @@ extern "C" int tgx_attn_fwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
                              prune_threshold, out, lse, hs);
   return fwd_dtype<_Float16>(s, cu_q_dev, cu_k_dev, tasks_dev, n_tasks, q, k, v, scale,
                              prune_threshold, out, lse, hs);
+}
+
+extern "C" int tgx_attn_fwd_split(const int32_t* cu_q_dev, const int32_t* cu_k_dev,
+                                  const int32_t* tasks_dev, int64_t n_tasks,
+                                  const int32_t* merge_dev, int64_t n_merge,
+                                  int32_t chunk_tiles, int32_t max_chunks, int causal, int dtype,
+                                  const void* q, const void* k, const void* v,
+                                  const int64_t* strides, float scale, void* out, float* lse,
+                                  float* partial_dev, int64_t n_q, int64_t n_k, int H, int D,
+                                  void* stream) {
+  TGX_REQUIRE(strides, "null strides");
+  const AttnShape s{n_q, n_k, H, D, dtype, causal != 0,
+                    strides[0], strides[1], strides[2], strides[3]};
+  int st = check_shape(s);
+  if (st != TGX_OK) return st;
+  TGX_REQUIRE(n_tasks >= 0 && n_tasks < (int64_t{1} << 31), "bad task count");
+  TGX_REQUIRE(n_merge >= 0 && chunk_tiles > 0 && max_chunks > 0 &&
+                  n_merge * max_chunks < (int64_t{1} << 31) && n_merge < (int64_t{1} << 26),
+              "bad split plan");
+  if (n_tasks == 0) return TGX_OK;
+  TGX_REQUIRE(cu_q_dev && cu_k_dev && tasks_dev && q && k && v && out && lse, "null pointer");
+  TGX_REQUIRE(n_merge == 0 || (merge_dev && partial_dev), "split tiles need merge and partial");
+  hipStream_t hs = as_stream(stream);
+  auto run = [&](auto tag) -> int {
+    typedef decltype(tag) T;
+    FwdArgs<T> a{cu_q_dev, cu_k_dev, tasks_dev, s.H,
+                 static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                 s.qsn, s.qsh, s.ksn, s.ksh, static_cast<T*>(out), lse, scale * kLog2e, 0.f,
+                 chunk_tiles, max_chunks, partial_dev};
+    int r = D == 64 ? launch_fwd<T, 64>(s, a, n_tasks, false, hs)
+                    : launch_fwd<T, 128>(s, a, n_tasks, false, hs);
+    if (r != TGX_OK || n_merge == 0) return r;
+    TGX_PROFILE("varlen_fwd_merge_kernel", hs);
+    const unsigned grid =
+        static_cast<unsigned>(n_merge * (D == 64 ? kMergeBlocks<64> : kMergeBlocks<128>));
+    if (D == 64)
+      varlen_fwd_merge_kernel<T, 64><<<grid, 256, 0, hs>>>(
+          merge_dev, cu_q_dev, s.H, max_chunks, partial_dev, static_cast<T*>(out), lse);
+    else
+      varlen_fwd_merge_kernel<T, 128><<<grid, 256, 0, hs>>>(
+          merge_dev, cu_q_dev, s.H, max_chunks, partial_dev, static_cast<T*>(out), lse);
+    TGX_LAUNCHED("varlen_fwd_merge_kernel");
+    return TGX_OK;
+  };
+  if (dtype == TGX_DTYPE_BF16) return run(__bf16{});
+  return run(_Float16{});
 }
 
 extern "C" int tgx_attn_bwd(const int32_t* cu_q_dev, const int32_t* cu_k_dev,

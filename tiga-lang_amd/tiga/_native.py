@@ -54,7 +54,7 @@ class EdgeMlp(ctypes.Structure):
 
 
 # tgx_abi_version() of the library these signatures and structs mirror.
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 # name -> argtypes (all return int status except where noted)
@@ -106,6 +106,11 @@ _SIGNATURES: dict[str, list] = {
                      P(c_i64), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                      c_int, c_int, c_vp],
     "tgx_attn_ds_tiles": [c_vp, c_vp, c_int, c_int, c_int, P(c_i64)],
+    "tgx_attn_fwd_split_tasks": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, P(c_i64), c_vp,
+                                 P(c_i64), P(ctypes.c_int32), P(ctypes.c_int32)],
+    "tgx_attn_fwd_split": [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, ctypes.c_int32, ctypes.c_int32,
+                           c_int, c_int, c_vp, c_vp, c_vp, P(c_i64), c_f32, c_vp, c_vp, c_vp,
+                           c_i64, c_i64, c_int, c_int, c_vp],
     "tgx_attn_bwd_stored": [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
                             c_vp, P(c_i64), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp,
                             c_vp, c_i64, c_i64, c_int, c_int, c_vp],

@@ -318,10 +318,23 @@ class BlockAttentionFunction(torch.autograd.Function):
         cu_q, cu_k, tasks, n, causal = graph._attn_tasks(0, 128, H)
         out = torch.empty((n_q, H, D), dtype=q.dtype, device=q.device)
         lse = torch.empty((n_q, H), dtype=torch.float32, device=q.device)
-        _native.call("tgx_attn_fwd", cu_q.data_ptr(), cu_k.data_ptr(), tasks.data_ptr(), n,
-                     int(causal), _ATTN_DTYPES[q.dtype], q.data_ptr(), k.data_ptr(),
-                     v.data_ptr(), strides, float(scale), float(prune), out.data_ptr(),
-                     lse.data_ptr(), n_q, n_k, H, D, _native.stream_of(q))
+        split = None if prune > 0 else graph._attn_fwd_split(H)
+        if split is not None:
+            # Too few, too uneven query tiles: the longest key ranges run in
+            # chunks, merged afterwards (tgx_attn_fwd_split).
+            stasks, sn, merge, n_merge, chunk, max_chunks = split
+            partial = torch.empty(n_merge * max_chunks * 128 * (D + 2), dtype=torch.float32,
+                                  device=q.device)
+            _native.call("tgx_attn_fwd_split", cu_q.data_ptr(), cu_k.data_ptr(),
+                         stasks.data_ptr(), sn, merge.data_ptr(), n_merge, chunk, max_chunks,
+                         int(causal), _ATTN_DTYPES[q.dtype], q.data_ptr(), k.data_ptr(),
+                         v.data_ptr(), strides, float(scale), out.data_ptr(), lse.data_ptr(),
+                         partial.data_ptr(), n_q, n_k, H, D, _native.stream_of(q))
+        else:
+            _native.call("tgx_attn_fwd", cu_q.data_ptr(), cu_k.data_ptr(), tasks.data_ptr(), n,
+                         int(causal), _ATTN_DTYPES[q.dtype], q.data_ptr(), k.data_ptr(),
+                         v.data_ptr(), strides, float(scale), float(prune), out.data_ptr(),
+                         lse.data_ptr(), n_q, n_k, H, D, _native.stream_of(q))
         ctx.graph = graph
         ctx.scale = float(scale)
         ctx.pruned = prune > 0

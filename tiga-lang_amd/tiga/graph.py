@@ -767,6 +767,37 @@ class Graph:
             self._native_cache[key] = got
         return got
 
+    def _attn_fwd_split(self, heads: int):
+        """The forward's split-key-range task lists for a `heads`-head launch
+        (tgx_attn_fwd_split_tasks with two resident workgroups per CU):
+        (tasks, n_tasks, merge, n_merge, chunk_tiles, max_chunks) on the
+        device, or None when no tile is worth splitting."""
+        key = ("attn-split", heads)
+        if key not in self._native_cache:
+            import numpy as np
+
+            cu_q, cu_k, causal = self._attn_blocks()
+            slots = 2 * torch.cuda.get_device_properties(self.device).multi_processor_count
+            n, n_merge = ctypes.c_int64(), ctypes.c_int64()
+            chunk, max_chunks = ctypes.c_int32(), ctypes.c_int32()
+            args = (cu_q.ctypes.data, cu_k.ctypes.data, cu_q.size - 1, heads, int(causal),
+                    slots)
+            _native.call("tgx_attn_fwd_split_tasks", *args, None, ctypes.byref(n), None,
+                         ctypes.byref(n_merge), ctypes.byref(chunk), ctypes.byref(max_chunks))
+            got = None
+            if n_merge.value > 0:
+                tasks = np.zeros(4 * max(n.value, 1), dtype=np.int32)
+                merge = np.zeros(4 * n_merge.value, dtype=np.int32)
+                _native.call("tgx_attn_fwd_split_tasks", *args, tasks.ctypes.data,
+                             ctypes.byref(n), merge.ctypes.data, ctypes.byref(n_merge),
+                             ctypes.byref(chunk), ctypes.byref(max_chunks))
+                dev = self.device
+                got = (torch.as_tensor(tasks, device=dev), n.value,
+                       torch.as_tensor(merge, device=dev), n_merge.value, chunk.value,
+                       max_chunks.value)
+            self._native_cache[key] = got
+        return self._native_cache[key]
+
     def _attn_ds_tiles(self, heads: int) -> int | None:
         """Stored dS tiles of a `heads`-head attention backward
         (tgx_attn_ds_tiles), None when the relation has too many."""
