@@ -902,7 +902,9 @@ def run_dense(args):
                    "(4D+5) per pair and head)"},
         "roofline": {"kernel": "varlen_fwd_kernel", "bound": "mfma", "achieved": achieved,
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
+                     "frac": achieved / BF16_PEAK_TFLOPS,
+                     "traffic": measured_traffic(args.config, "varlen_fwd_kernel")[0],
+                     "traffic_source": measured_traffic(args.config, "varlen_fwd_kernel")[1],
                      "avg_ms": kernel_ms},
         "kernels": {kk: {"launches": n, "avg_ms": t / n} for kk, (n, t) in totals.items()},
         "profiled_ms_per_step": profiled * 1e3 / args.steps,
