@@ -908,6 +908,12 @@ def run_dense(args):
                      "avg_ms": kernel_ms},
         "kernels": {kk: {"launches": n, "avg_ms": t / n} for kk, (n, t) in totals.items()},
         "profiled_ms_per_step": profiled * 1e3 / args.steps,
+        # The reference's own FLOP convention and published time for this
+        # case (benchmarks/evidence_snapshot/output/roofline/dense_attention/
+        # b1_h16_n4096_d64_fp16[_causal]; its own GPU, not an MI355X).
+        "reference_convention_tflops": (4 * D + 5) * H * pairs / (ms * 1e-3) / 1e12,
+        "reference_ms_own_gpu": {"dense": 0.772, "dense-causal": 0.4459,
+                                 "dense-pruned": 0.907}[args.config],
     }
 
 
