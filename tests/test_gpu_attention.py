@@ -267,6 +267,7 @@ def torch_block_attention(q, k, v, scale, causal):
     (4096, 16, 64, True, torch.float16),     # the reference's causal dense case: 2 chunks
     (8192, 2, 128, True, torch.bfloat16),    # up to 8 chunks per tile
     (4096, 4, 64, False, torch.bfloat16),    # few, equal tiles: 4 chunks each
+    ((4096, 3000, 100), 4, 128, True, torch.float16),   # causal cu_seqlens, 3 blocks
 ])
 def test_split_key_ranges_match_whole_tiles(n, H, D, causal, dtype):
     """Relations with too few query tiles to fill the GPU run the longest key
@@ -274,11 +275,18 @@ def test_split_key_ranges_match_whole_tiles(n, H, D, causal, dtype):
     fp32 attention, and the forward and the gradients match the whole-tile
     forward's up to the order of the softmax sums."""
     print(f"split forward n={n} H={H} D={D} causal={causal} {dtype}", flush=True)
+    lengths = n if isinstance(n, tuple) else None
+    n = sum(lengths) if lengths else n
     g = torch.Generator(device=DEV).manual_seed(n + H + D)
     base = [torch.randn(n, H, D, device=DEV, generator=g).to(dtype) for _ in range(4)]
     results = []
     for split in (True, False):
-        graph = tg.Graph.triangular(n, device=DEV) if causal else tg.Graph.dense(n, device=DEV)
+        if lengths:
+            cu = torch.tensor([0, *np.cumsum(lengths)], dtype=torch.int64, device=DEV)
+            graph = tg.Graph.cu_seqlens(cu, causal=True)
+        else:
+            graph = (tg.Graph.triangular(n, device=DEV) if causal
+                     else tg.Graph.dense(n, device=DEV))
         if split:
             plan = graph._attn_fwd_split(H)
             assert plan is not None and plan[3] > 0
@@ -292,7 +300,11 @@ def test_split_key_ranges_match_whole_tiles(n, H, D, causal, dtype):
         out.backward(base[3])
         results.append((out.detach().float(), q.grad.float(), k.grad.float(), v.grad.float()))
     tol = TOL[dtype]
-    expect = torch_block_attention(base[0], base[1], base[2], D ** -0.5, causal)
-    assert float((results[0][0] - expect).abs().max() / expect.abs().max()) <= tol
+    starts = np.cumsum([0, *lengths]) if lengths else [0, n]
+    for s0, s1 in zip(starts[:-1], starts[1:]):
+        expect = torch_block_attention(base[0][s0:s1], base[1][s0:s1], base[2][s0:s1],
+                                       D ** -0.5, causal)
+        got = results[0][0][s0:s1]
+        assert float((got - expect).abs().max() / expect.abs().max()) <= tol
     for a, b in zip(results[0], results[1]):
         assert float((a - b).abs().max() / b.abs().max()) <= tol
