@@ -13,8 +13,10 @@ reference's CPU path timed on a bounded sample of the same workload.
                   [--no-cpu] [--no-cold] [--no-graph]
 
 By default (--config all) the line is C2's and carries C1, C3, C4 and C5 as
-complete sub-lines under "configs" (same fields, each with the roofline of
-its own dominant kernel and its CPU baseline), all measured in this run.
+sub-lines under "configs" (step time, throughput, per-kernel averages, the
+roofline of each one's dominant kernel and its CPU baseline), all measured in
+this run, plus one summary each of the other shapes.  The line is kept to a
+few KB; --detail PATH writes the full record (per-kernel tables, every case).
 c1-c5 are BASELINE.json's configurations; dense* are the reference's dense
 attention benchmark shapes (N=4096, H=16, D=64, fp16, forward); nn is the
 reference's nn-scored GAT training step (131072 nodes, net 19-16-1);
@@ -41,15 +43,19 @@ BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 (and fp16) MFMA
 
 
 def measured_traffic(config, kernel):
-    """HBM bytes per launch of `kernel` measured by rocprofv3 --pmc FETCH_SIZE /
-    WRITE_SIZE (scaled by the copy calibration) and recorded in
-    profiles/traffic.json; None when no measurement is recorded."""
+    """L2-to-memory bytes per launch of `kernel` (or the sum over a
+    "+"-joined list of kernels that run once per step each) measured by
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by the copy calibration)
+    and recorded in profiles/traffic.json; None when any is unrecorded.
+    These are L2-miss bytes: they include Infinity-Cache (MALL) hits, so
+    they bound HBM traffic from above rather than equal it."""
     path = ROOT / "profiles" / "traffic.json"
     try:
-        rec = json.loads(path.read_text())[config][kernel]
+        table = json.loads(path.read_text())[config]
+        recs = [table[k] for k in kernel.split("+")]
     except (OSError, KeyError, ValueError):
         return None, None
-    return rec["fetch_bytes"] + rec["write_bytes"], rec["source"]
+    return sum(r["fetch_bytes"] + r["write_bytes"] for r in recs), recs[0]["source"]
 
 
 def parse():
@@ -71,6 +77,9 @@ def parse():
                          "warmup and timed launches)")
     ap.add_argument("--cpu-rows", type=int, default=None)
     ap.add_argument("--seed", type=int, default=20260821)
+    ap.add_argument("--detail", default=None, metavar="PATH",
+                    help="also write the full record (per-kernel tables, every case) as JSON "
+                         "to PATH; stdout keeps the compact line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 1 GiB device copy (PMC byte-counter calibration)")
     return ap.parse_args()
@@ -597,13 +606,14 @@ def run_c1(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic", "config": {"workload": "c1-weighted-sum-fwd-bwd", "nodes": N,
                                         "edges": E, "features": F_},
+        "hbm_frac_step": sum(bytes_per.values()) / (elapsed / args.steps) / 1e9 / HBM_PEAK_GBS,
         "cold_ms_per_step": cold_ms,
         "graph_ms_per_step": graph_ms,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic("c1", dominant)[0],
                      "traffic_source": measured_traffic("c1", dominant)[1],
-                     "algorithmic_bytes": bytes_per[dominant]},
+                     "avg_ms": total_ms / n_launch, "algorithmic_bytes": bytes_per[dominant]},
         "kernels": {k: {"launches": n, "avg_ms": ms / n} for k, (n, ms) in totals.items()},
         "profiled_ms_per_step": profiled * 1e3 / args.steps,
     }
@@ -828,7 +838,8 @@ def run_c5(args):
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS,
                      "traffic": measured_traffic("c5", dominant)[0],
-                     "traffic_source": measured_traffic("c5", dominant)[1]},
+                     "traffic_source": measured_traffic("c5", dominant)[1],
+                     "avg_ms": total_ms / n_launch, "algorithmic_flops": kflops[dominant]},
         "kernels": {kk: {"launches": n, "avg_ms": t / n,
                          "tflops": (kflops[kk] / (t / n * 1e-3) / 1e12) if kk in kflops else None}
                     for kk, (n, t) in sorted(per.items())},
@@ -885,7 +896,13 @@ def run_dense(args):
     pairs = N * (N + 1) // 2 if causal else N * N
     flops = 4.0 * H * D * pairs            # useful: q.k and p.v per pair (pruned: as if dense)
     ms = elapsed * 1e3 / args.steps
+    # The forward kernel plus, where the key ranges are split, the merge of
+    # its chunks: both run every step, so both count in the roofline's time.
     n_launch, total_ms = totals["varlen_fwd_kernel"]
+    roof_kernels = ["varlen_fwd_kernel"]
+    if "varlen_fwd_merge_kernel" in totals:
+        roof_kernels.append("varlen_fwd_merge_kernel")
+        total_ms += totals["varlen_fwd_merge_kernel"][1]
     kernel_ms = total_ms / n_launch
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     what = {"dense": "all pairs", "dense-causal": "lower-triangular",
@@ -900,11 +917,12 @@ def run_dense(args):
         "config": {"workload": args.config, "nodes": N, "heads": H, "head_dim": D,
                    "pairs": pairs, "flop_convention": "4*H*D per pair (the reference counts "
                    "(4D+5) per pair and head)"},
-        "roofline": {"kernel": "varlen_fwd_kernel", "bound": "mfma", "achieved": achieved,
+        "roofline": {"kernel": "+".join(roof_kernels), "bound": "mfma", "achieved": achieved,
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS,
-                     "traffic": measured_traffic(args.config, "varlen_fwd_kernel")[0],
-                     "traffic_source": measured_traffic(args.config, "varlen_fwd_kernel")[1],
+                     "traffic": measured_traffic(args.config, "+".join(roof_kernels))[0],
+                     "traffic_source": measured_traffic(args.config,
+                                                        "+".join(roof_kernels))[1],
                      "avg_ms": kernel_ms},
         "kernels": {kk: {"launches": n, "avg_ms": t / n} for kk, (n, t) in totals.items()},
         "profiled_ms_per_step": profiled * 1e3 / args.steps,
@@ -1093,13 +1111,18 @@ def run_refcases(args):
     cases = {}
 
     def record(name, E, ms, ms_prepared, ref_gedges, ref_ms, source, note):
-        best = min(ms, ms_prepared) if ms_prepared is not None else ms
+        # Both ratios are reported: the ordinary call (through autograd for
+        # the backward cases) and the prepared launch, where there is one.
         cases[name] = {
             "edges": E, "ms": ms, "ms_prepared": ms_prepared,
-            "gedges_per_s": E / (best * 1e-3) / 1e9,
+            "gedges_per_s": E / (ms * 1e-3) / 1e9,
+            "gedges_per_s_prepared": (E / (ms_prepared * 1e-3) / 1e9
+                                      if ms_prepared is not None else None),
             "reference_gedges_per_s": ref_gedges, "reference_ms": ref_ms,
             "reference_hardware": "RTX 5070 Ti", "reference_source": source,
-            "ratio_to_reference": ref_ms / best, "what": note}
+            "ratio_call": ref_ms / ms,
+            "ratio_prepared": ref_ms / ms_prepared if ms_prepared is not None else None,
+            "what": note}
 
     g = torch.Generator(device=dev).manual_seed(args.seed)
     # Weighted sum forward (weighted_aggregation.py:252-314): x [N, F] (or
@@ -1310,6 +1333,86 @@ def measured_roofs(samples=10):
                    f"median of {samples} HIP-event samples"}
 
 
+def _sig(x, digits=4):
+    """Floats rounded to `digits` significant digits (the compact line)."""
+    if isinstance(x, float):
+        return float(f"{x:.{digits}g}")
+    if isinstance(x, dict):
+        return {k: _sig(v, digits) for k, v in x.items()}
+    if isinstance(x, list):
+        return [_sig(v, digits) for v in x]
+    return x
+
+
+_ROOF_KEYS = ("kernel", "bound", "achieved", "peak", "unit", "frac", "traffic", "avg_ms",
+              "algorithmic_bytes", "algorithmic_flops", "achieved_over_measured")
+
+
+def _compact_roofline(rl):
+    return {k: rl[k] for k in _ROOF_KEYS if k in rl}
+
+
+def _compact_cpu(cb):
+    if not isinstance(cb, dict):
+        return cb
+    out = {k: cb[k] for k in ("value", "unit", "cores", "kind") if k in cb}
+    out["sample"] = cb.get("sample", "")[:110]
+    return out
+
+
+def _kernel_ms(sub):
+    return {k: v["avg_ms"] for k, v in sub.get("kernels", {}).items()}
+
+
+def compact_line(result):
+    """The one stdout line of the default run, kept to a few KB so that a
+    driver storing only the tail of stdout keeps all of it: the headline
+    (C2) fields; for C1, C3, C4 and C5 the step time, throughput, dominant
+    kernel's roofline, per-kernel averages and CPU baseline; for the
+    reference's other shapes (nn, dense, refcases) one summary each.  The
+    full record goes to --detail PATH."""
+    top = {k: v for k, v in result.items()
+           if k not in ("configs", "kernels", "roofline", "cpu_baseline", "measured_roofs",
+                        "profiled_ms_per_step")}
+    top["roofline"] = _compact_roofline(result["roofline"])
+    top["kernels_ms"] = _kernel_ms(result)
+    if "cpu_baseline" in result:
+        top["cpu_baseline"] = _compact_cpu(result["cpu_baseline"])
+    if "measured_roofs" in result:
+        mr = result["measured_roofs"]
+        top["measured_roofs"] = {"copy_GBps": mr["copy_GBps"],
+                                 "bf16_gemm_TFLOPs": mr["bf16_gemm_TFLOPs"]}
+    configs = {}
+    for name, sub in result.get("configs", {}).items():
+        if name in ("c1", "c3", "c4", "c5"):
+            c = {k: sub[k] for k in ("value", "unit", "ms_per_step", "dtype", "hbm_frac_step",
+                                     "mfma_utilization", "cold_ms_per_step") if k in sub}
+            c["config"] = {k: v for k, v in sub["config"].items() if k != "flop_convention"}
+            c["roofline"] = _compact_roofline(sub["roofline"])
+            c["kernels_ms"] = _kernel_ms(sub)
+            if "cpu_baseline" in sub:
+                c["cpu_baseline"] = _compact_cpu(sub["cpu_baseline"])
+        elif name == "refcases":
+            c = {case: [v["ms"], v["ms_prepared"], v["reference_ms"]]
+                 for case, v in sub["cases"].items()}
+            c["columns"] = "ms, ms_prepared, reference_ms (reference: RTX 5070 Ti)"
+        else:
+            c = {k: sub[k] for k in ("value", "unit", "ms_per_step", "dtype") if k in sub}
+            c["workload"] = sub["config"]["workload"]
+            rl = sub["roofline"]
+            c["roofline"] = {k: rl[k] for k in ("kernel", "bound", "achieved", "unit", "frac",
+                                                "avg_ms") if k in rl}
+            if isinstance(sub.get("cpu_baseline"), dict):
+                c["cpu_baseline"] = {k: sub["cpu_baseline"][k] for k in ("value", "unit")}
+        configs[name] = c
+    if configs:
+        top["configs"] = configs
+    out = _sig(top)
+    for k in ("value", "ms_per_step"):      # the headline figures at full precision
+        out[k] = result[k]
+    return out
+
+
 def main():
     global ARGS
     args = ARGS = parse()
@@ -1339,7 +1442,11 @@ def main():
         # plain copy (which gathers can beat) or a library GEMM.
         measured = roofs["copy_GBps"] if rl.get("unit") == "GB/s" else roofs["bf16_gemm_TFLOPs"]
         rl["achieved_over_measured"] = rl["achieved"] / measured
-    print(json.dumps(result), flush=True)
+    if args.detail:
+        Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.detail).write_text(json.dumps(result, indent=1) + "\n")
+    line = compact_line(result) if args.config == "all" else result
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

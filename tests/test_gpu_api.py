@@ -156,6 +156,99 @@ def test_tensor_parameters_are_read_from_each_warm_call():
     assert not torch.equal(o1, o2)
 
 
+SCORE_SCALE = 0.125
+
+
+class GatSlopeAttr(tg.MessagePassing):
+    reducer = tg.online_softmax()
+    slope = 0.2
+
+    def edge(self, src, dst, edge, a_src, a_dst):
+        s = F.leaky_relu((src.h * a_src).sum(-1) + (dst.h * a_dst).sum(-1), self.slope)
+        return self.reducer(s, src.h)
+
+
+def _with_slope(slope):
+    k = GatSlopeAttr()
+    k.slope = slope
+    return k
+
+
+class DotGlobalScale(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge):
+        return self.reducer((src.k * dst.q).sum(dim=-1) * SCORE_SCALE + edge.b, src.v)
+
+
+def test_outside_scalars_changed_between_warm_calls_are_seen():
+    """A slope or scale edge() reads from the kernel's attributes, its class,
+    a module global or a closure is baked into the capture: changing it
+    makes the next call a cold one, whose result is the new value's."""
+    global SCORE_SCALE
+    print("outside scalars", flush=True)
+    g = _graph(7)
+    h = torch.randn(3000, 4, 32, device=DEV)
+    a_s = 0.1 * torch.randn(4, 32, device=DEV)
+    a_d = 0.1 * torch.randn(4, 32, device=DEV)
+    call = lambda k: k(graph=g, src={"h": h}, dst={"h": h}, a_src=a_s, a_dst=a_d)
+    k = GatSlopeAttr()
+    first = call(k)
+    assert torch.equal(call(k), first) and k.cache_info["hits"] == 1
+    k.slope = 0.2                                    # same value: still a hit
+    call(k)
+    assert k.cache_info == {"hits": 2, "misses": 1, "variants": 1}
+    k.slope = 0.01                                   # instance attribute
+    second = call(k)
+    assert k.cache_info["misses"] == 2 and k.last_variant.backend == "hip"
+    assert torch.equal(second, call(_with_slope(0.01)))
+    assert not torch.equal(first, second)
+    k2 = GatSlopeAttr()
+    call(k2)
+    try:                                             # class attribute
+        GatSlopeAttr.slope = 0.05
+        third = call(k2)
+        assert k2.cache_info["misses"] == 2
+        assert torch.equal(third, call(_with_slope(0.05)))
+        assert not torch.equal(third, first)
+    finally:
+        GatSlopeAttr.slope = 0.2
+
+    q = torch.randn(3000, 2, 64, device=DEV).to(torch.bfloat16)
+    b = torch.randn(g.num_edges, 2, device=DEV)
+    fields = dict(graph=g, src={"k": q, "v": q}, dst={"q": q}, edge={"b": b})
+    kd = DotGlobalScale()
+    o1 = kd(**fields)
+    try:                                             # module global
+        SCORE_SCALE = 0.25
+        o2 = kd(**fields)
+        assert kd.cache_info["misses"] == 2 and kd.last_variant.backend == "hip"
+        assert torch.equal(o2, DotGlobalScale()(**fields)) and not torch.equal(o1, o2)
+    finally:
+        SCORE_SCALE = 0.125
+
+    def closure_kernel():
+        scale = 0.125
+
+        class DotClosure(tg.MessagePassing):
+            reducer = tg.online_softmax()
+
+            def edge(self, src, dst, edge):
+                return self.reducer((src.k * dst.q).sum(dim=-1) * scale + edge.b, src.v)
+
+        def set_scale(value):
+            nonlocal scale
+            scale = value
+        return DotClosure(), set_scale
+
+    kc, set_scale = closure_kernel()
+    c1 = kc(**fields)
+    assert torch.equal(c1, o1)
+    set_scale(0.25)                                  # closure cell
+    c2 = kc(**fields)
+    assert kc.cache_info["misses"] == 2 and torch.equal(c2, o2)
+
+
 def test_closure_tensors_are_recaptured_every_call():
     print("closure tensors", flush=True)
     g = _graph(6)

@@ -498,3 +498,18 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("idx", [torch.int32, torch.int64])
+def test_cpu_varlen_csr_matches_the_oracle_with_empty_sequences(causal, idx):
+    """The CPU materialization of Graph.cu_seqlens against the oracle's
+    per-position loop, with empty sequences at the start, middle and end,
+    in the index dtype of cu_seqlens."""
+    cu = torch.tensor([0, 0, 5, 5, 6, 13, 13], dtype=idx)
+    g = tg.Graph.cu_seqlens(cu, causal=causal)
+    rp, col = ref.cu_seqlens_csr(cu.numpy(), causal=causal)
+    r, c = g.resolve_csr()
+    assert r.dtype == idx and c.dtype == idx
+    assert r.tolist() == rp.tolist() and c.tolist() == col.tolist()
+    assert g.num_edges == int(rp[-1])

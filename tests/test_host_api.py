@@ -290,3 +290,55 @@ def test_kernel_observability_surface_matches_the_reference():
     assert k.schedules == ()
     with pytest.raises(ValueError):
         tk.AnalysisFinding("planning", "maybe", "x")
+
+
+GUARD_SCALE = 0.5
+
+
+def test_warm_call_environment_tracks_outside_scalars():
+    """The guard of a warm launch snapshots the scalars edge() reads from
+    outside the call (instance and class attributes, module globals,
+    closure cells) and fails when any changes; tensors and other objects
+    are not part of it (they are operands or re-captured)."""
+    global GUARD_SCALE
+    from tiga.message_passing import _Environment
+
+    offset = 1.0
+
+    class K(tg.MessagePassing):
+        reducer = tg.online_softmax()
+        slope = 0.2
+        weights = torch.ones(3)
+
+        def edge(self, src, dst, edge):
+            s = (src.k * dst.q).sum(-1) * GUARD_SCALE * self.slope + offset
+            return self.reducer(s * self.weights.sum(), src.v)
+
+    k = K()
+    env = _Environment(k)
+    kinds = {key for key in env.keys}
+    assert ("attr", "slope") in kinds and ("global", "GUARD_SCALE") in kinds
+    assert any(kind == "cell" for kind, _ in kinds)
+    assert ("attr", "weights") not in kinds and ("attr", "reducer") not in kinds
+    assert env.holds(k)
+    k.slope = 0.2
+    assert env.holds(k)
+    k.slope = 0.3
+    assert not env.holds(k)
+    del k.slope
+    assert env.holds(k)
+    K.slope = 0.25
+    assert not env.holds(k)
+    K.slope = 0.2
+    GUARD_SCALE = 0.75
+    try:
+        assert not env.holds(k)
+    finally:
+        GUARD_SCALE = 0.5
+    assert env.holds(k)
+    offset = 2.0          # the closure cell edge() reads
+    assert not env.holds(k)
+    offset = 1.0
+    assert env.holds(k)
+    k.slope = 1           # an int where a float was baked in
+    assert not env.holds(k)

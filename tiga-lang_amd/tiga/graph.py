@@ -838,20 +838,33 @@ class Graph:
 
 
 def _varlen_csr(cu_seqlens: torch.Tensor, causal: bool):
-    """Materialize the block-diagonal varlen CSR (reference graph.py:260-294)."""
+    """The block-diagonal relation of `cu_seqlens` as an explicit CSR, for
+    the tensors the device builder does not take (CPU tensors).  Same
+    relation as the reference's materialization (graph.py:260-294): row i of
+    sequence [s, e) reads columns s..i when causal, s..e-1 otherwise.
+
+    Built one sequence block at a time: a causal block of length L is the
+    lower triangle of an L x L block, whose columns in row order are the
+    second row of ``torch.tril_indices(L, L)``; a full block repeats its L
+    columns once per row."""
     device, dtype = cu_seqlens.device, cu_seqlens.dtype
-    lengths = cu_seqlens.diff()
-    total = int(cu_seqlens[-1].item())
-    positions = torch.arange(total, device=device, dtype=dtype)
-    sequence = torch.repeat_interleave(
-        torch.arange(lengths.numel(), device=device, dtype=dtype), lengths.to(torch.int64))
-    start = cu_seqlens[:-1][sequence]
-    degree = positions - start + 1 if causal else lengths[sequence]
-    row_ptr = torch.cat([cu_seqlens.new_zeros(1), degree.cumsum(0, dtype=dtype)])
-    repeats = degree.to(torch.int64)
-    offset = torch.arange(int(row_ptr[-1].item()), device=device, dtype=dtype)
-    col_idx = start.repeat_interleave(repeats) + (
-        offset - row_ptr[:-1].repeat_interleave(repeats))
+    bounds = cu_seqlens.tolist()
+    degrees, columns = [], []
+    for first, stop in zip(bounds[:-1], bounds[1:]):
+        length = stop - first
+        if length <= 0:
+            continue
+        if causal:
+            degrees.append(torch.arange(1, length + 1, device=device, dtype=dtype))
+            block = torch.tril_indices(length, length, device=device, dtype=dtype)[1]
+        else:
+            degrees.append(torch.full((length,), length, device=device, dtype=dtype))
+            block = torch.arange(length, device=device, dtype=dtype).repeat(length)
+        columns.append(block.add_(first))
+    row_ptr = torch.zeros(bounds[-1] + 1 if bounds else 1, device=device, dtype=dtype)
+    if degrees:
+        torch.cumsum(torch.cat(degrees), 0, out=row_ptr[1:])
+    col_idx = torch.cat(columns) if columns else torch.zeros(0, device=device, dtype=dtype)
     return row_ptr, col_idx
 
 

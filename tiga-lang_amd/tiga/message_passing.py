@@ -19,9 +19,11 @@ a tensor parameter) and a runner over ``torch.autograd.Function`` bridges
 into libtgx_hip.so, which raises if the library is missing.  When every
 operand comes from the call's own fields or parameters, the launch is kept
 with guards (same graph object, same reducer, same parameter values, every
-operand with the same dtype/shape/strides/device, required aliases); a warm
-call that passes the guards runs it directly, skipping capture, recognition
-and validation, like the reference's guarded executable (:974-1008).  A
+operand with the same dtype/shape/strides/device, required aliases, and
+the same values for the scalars edge() reads from the kernel's attributes,
+its module's globals and its closure); a warm call that passes the guards
+runs it directly, skipping capture, recognition and validation, like the
+reference's guarded executable (:974-1008).  A
 launch that holds a tensor from outside the call (a closure or attribute)
 is re-captured on every call instead, so rebinding that name is seen.
 
@@ -38,7 +40,7 @@ import inspect
 import numbers
 from collections.abc import Callable, Mapping
 from dataclasses import dataclass
-from types import SimpleNamespace
+from types import CodeType, SimpleNamespace
 from typing import Any
 
 import torch
@@ -111,6 +113,79 @@ def _param_signature(params: Mapping[str, Any]) -> tuple:
     return tuple(sig)
 
 
+_SCALARS = (numbers.Number, str, bytes, type(None))
+
+
+def _scalar(value) -> bool:
+    """A value a capture bakes into the launch as a constant (a number, a
+    string, or a tuple of them), as opposed to an operand it reads."""
+    return isinstance(value, _SCALARS) or (
+        isinstance(value, tuple) and all(isinstance(v, _SCALARS) for v in value))
+
+
+@functools.lru_cache(maxsize=512)
+def _code_names(function) -> tuple:
+    """Attribute and global names read by `function`'s code and the code
+    objects nested in it (lambdas, comprehensions)."""
+    names, stack = set(), [function.__code__]
+    while stack:
+        code = stack.pop()
+        names.update(code.co_names)
+        stack.extend(c for c in code.co_consts if isinstance(c, CodeType))
+    return tuple(sorted(names))
+
+
+def _lookup(kernel, function, kind: str, name):
+    """The current value of one outside name edge() reads: an attribute of
+    the kernel (instance, then class; descriptors such as properties are
+    not run), a global of edge()'s module, or a closure cell."""
+    if kind == "attr":
+        if name in kernel.__dict__:
+            return kernel.__dict__[name]
+        for cls in type(kernel).__mro__:
+            if name in cls.__dict__:
+                return cls.__dict__[name]
+        return _MISS
+    if kind == "global":
+        return function.__globals__.get(name, _MISS)
+    try:
+        return function.__closure__[name].cell_contents
+    except (TypeError, IndexError, ValueError):
+        return _MISS
+
+
+class _Environment:
+    """The scalars edge() reads from outside the call: kernel attributes
+    (self.slope), class attributes, module globals and closure variables
+    that held a number or string when the launch was captured.  The capture
+    bakes these in as constants (a LeakyReLU slope, a score scale), so a
+    warm call re-runs the launch only while every one still has its value.
+    Scalars reached other ways (through another object's attribute, or a
+    helper function's globals) are not tracked."""
+
+    def __init__(self, kernel):
+        function = getattr(kernel.edge, "__func__", kernel.edge)
+        keys = []
+        for name in _code_names(function):
+            for kind in ("attr", "global"):
+                if _scalar(_lookup(kernel, function, kind, name)):
+                    keys.append((kind, name))
+        for index in range(len(function.__closure__ or ())):
+            if _scalar(_lookup(kernel, function, "cell", index)):
+                keys.append(("cell", index))
+        self.keys = tuple(keys)
+        self.values = self.snapshot(kernel)
+
+    def snapshot(self, kernel) -> tuple:
+        function = getattr(kernel.edge, "__func__", kernel.edge)
+        return tuple(_lookup(kernel, function, kind, name) for kind, name in self.keys)
+
+    def holds(self, kernel) -> bool:
+        now = self.snapshot(kernel)
+        # Compared by type and value: 1 and 1.0 can bake in differently.
+        return all(type(a) is type(b) and a == b for a, b in zip(now, self.values))
+
+
 @dataclass
 class _Launch:
     """A recognized pattern bound to its HIP runner.
@@ -142,11 +217,12 @@ class _Launch:
 class _Guarded:
     """A launch plus the guards under which a warm call may re-run it."""
 
-    def __init__(self, launch: _Launch, reducer, operands, params):
+    def __init__(self, launch: _Launch, kernel, operands, params):
         self.launch = launch
-        self.reducer = reducer
+        self.reducer = kernel.reducer
         self.specs = tuple(_spec(t) for t in operands)
         self.param_sig = _param_signature(params)
+        self.environment = _Environment(kernel)
         self.names: tuple | None = None
 
     @staticmethod
@@ -171,7 +247,8 @@ class _Guarded:
                 if groups[ra].get(na) is not groups[rb].get(nb):
                     return _MISS
         if self._names(src, dst, edge) != self.names or \
-                _param_signature(params) != self.param_sig:
+                _param_signature(params) != self.param_sig or \
+                not self.environment.holds(kernel):
             return _MISS
         return launch.runner(*operands)
 
@@ -278,7 +355,7 @@ class MessagePassing(Kernel):
         self._launch = launch
         self._record_variant(launch.variant)
         if launch.guardable:
-            guarded = _Guarded(launch, self.reducer, operands, params)
+            guarded = _Guarded(launch, self, operands, params)
             guarded.names = _Guarded._names(src, dst, edge)
             self._guarded = guarded
         return result
