@@ -176,3 +176,52 @@ def dot_bwd(row_ptr, col, q, k, v, scale, bias, dout, edges_per_block=1 << 19):
         dk.index_add_(0, src, dscore[..., None] * qd * scale)
         dv.index_add_(0, src, alpha[..., None] * g)
     return dq, dk, dv, dbias
+
+
+def causal_sequence(q, k, v, scale, dout=None, query_block=512):
+    """One sequence of causal softmax attention, float64, over blocks of
+    query rows: (out [L, H, D], lse [L, H]) and, with `dout`, also
+    (dq, dk, dv).  The arithmetic of ``ref.varlen_causal_fwd/bwd`` (the
+    dot-product relation on Graph.cu_seqlens(causal=True); per-sequence
+    causal SDPA as the reference's tests/python/test_attention_examples.py:
+    53-72 checks it) with the score matrix formed `query_block` rows at a
+    time, so a 4096-token, 16-head sequence needs about 270 MB at once.
+
+    The backward's row term is delta_i = <dout_i, out_i> from the float64
+    output; probabilities are recomputed from the saved logsumexp."""
+    L, H, D = q.shape
+    qh, kh, vh = (t.permute(1, 0, 2).contiguous() for t in (q, k, v))     # [H, L, D]
+    out = torch.empty((H, L, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((H, L), dtype=q.dtype, device=q.device)
+    keys = torch.arange(L, device=q.device)
+
+    def probabilities(i0, i1):
+        s = torch.matmul(qh[:, i0:i1], kh[:, :i1].transpose(1, 2).contiguous()) * scale
+        mask = keys[None, :i1] <= torch.arange(i0, i1, device=q.device)[:, None]
+        return s.masked_fill(~mask[None], -torch.inf)
+
+    for i0 in range(0, L, query_block):
+        i1 = min(i0 + query_block, L)
+        s = probabilities(i0, i1)
+        m = s.amax(-1, keepdim=True)
+        p = torch.exp(s - m)
+        den = p.sum(-1, keepdim=True)
+        out[:, i0:i1] = torch.matmul(p / den, vh[:, :i1])
+        lse[:, i0:i1] = (m + torch.log(den))[..., 0]
+    if dout is None:
+        return out.permute(1, 0, 2), lse.T
+    gh = dout.permute(1, 0, 2).contiguous()
+    delta = (gh * out).sum(-1)                                              # [H, L]
+    dq = torch.empty_like(qh)
+    dk = torch.zeros_like(kh)
+    dv = torch.zeros_like(vh)
+    for i0 in range(0, L, query_block):
+        i1 = min(i0 + query_block, L)
+        p = torch.exp(probabilities(i0, i1) - lse[:, i0:i1, None])          # [H, b, i1]
+        dp = torch.matmul(gh[:, i0:i1], vh[:, :i1].transpose(1, 2).contiguous())
+        ds = p * (dp - delta[:, i0:i1, None])
+        dq[:, i0:i1] = torch.matmul(ds, kh[:, :i1]) * scale
+        dk[:, :i1] += torch.matmul(ds.transpose(1, 2).contiguous(), qh[:, i0:i1]) * scale
+        dv[:, :i1] += torch.matmul(p.transpose(1, 2).contiguous(), gh[:, i0:i1])
+    back = lambda t: t.permute(1, 0, 2)
+    return back(out), lse.T, back(dq), back(dk), back(dv)

@@ -15,6 +15,9 @@ the reference's own bf16 arithmetic.
 * C3 (dot-product bf16, R-MAT scale 21): out on every row above 512 edges
   (the split hub rows) and on a seeded sample of other rows, 2e-2.
 * C4 (its fused backward): dq, dk, dv and dbias over the whole graph, 2e-2.
+* C5 (varlen causal, 32 sequences of U[512, 4096] tokens, bf16): out, dq, dk
+  and dv of the longest sequence and two seeded others, against the
+  query-chunked float64 per-sequence attention, 2e-2.
 * bf16 arithmetic: on an R-MAT scale-12 graph the HIP dot-product forward
   and backward against the reference's eager path run in bf16 on the CPU
   (oracle/eager_torch.dot_reference: bf16 q*k products and sums, fp32 bias
@@ -27,6 +30,9 @@ the reference's own bf16 arithmetic.
 
 The float64 checker runs with Torch's own float64 kernels on the GPU (the
 CPU would take minutes at these sizes); the bf16 inputs enter it exactly.
+Beside each max-norm error the tests print element-wise relative errors
+(median, 99.9th percentile, maximum over elements above 1e-3 of the
+largest), so small elements are visible too.
 """
 
 import numpy as np
@@ -56,6 +62,20 @@ def rel(actual, expected) -> float:
     return float((a - e).abs().max() / e.abs().max().clamp_min(1e-300))
 
 
+def elementwise(actual, expected) -> str:
+    """Element-wise relative errors |a - e| / |e|, printed beside the
+    max-norm bound: median, 99.9th percentile and maximum over the elements
+    with |e| >= 1e-3 max|e| (a strided sample of at most 4M of them)."""
+    a, e = actual.detach().double().flatten(), expected.detach().double().flatten()
+    keep = e.abs() >= 1e-3 * e.abs().max()
+    r = (a - e).abs()[keep] / e.abs()[keep]
+    if r.numel() == 0:
+        return "elementwise: no elements"
+    sample = r[::max(1, r.numel() // (1 << 22))].float()
+    p50, p999 = torch.quantile(sample, torch.tensor([0.5, 0.999], device=sample.device))
+    return f"elementwise p50 {float(p50):.2e} p99.9 {float(p999):.2e} max {float(r.max()):.2e}"
+
+
 def test_c2_full_size_values_against_float64():
     print("c2 full size values: 1M nodes, fp64 checker", flush=True)
     row_ptr, col = poisson_self_loop(1_000_000, 16.0, SEED)
@@ -80,6 +100,7 @@ def test_c2_full_size_values_against_float64():
     assert rel(branch[0], (d(h) * d(a_src)).sum(-1)) <= 1e-6
     assert rel(branch[1], (d(h) * d(a_dst)).sum(-1)) <= 1e-6
     e_out, _ = chunked.gat_fwd(row_ptr, col, d(h), d(a_src), d(a_dst), 0.2)
+    print(f"c2 out {rel(out.detach(), e_out):.3e}, {elementwise(out, e_out)}", flush=True)
     assert rel(out.detach(), e_out) <= 1e-5
     del e_out
     stats = {}
@@ -88,7 +109,8 @@ def test_c2_full_size_values_against_float64():
     errs = {"dh": rel(h.grad, e_dh), "da_src": rel(a_src.grad, e_das),
             "da_dst": rel(a_dst.grad, e_dad)}
     print(f"c2 relative errors {errs}; (edge, head) pairs whose fp32 and fp64 z straddle "
-          f"the LeakyReLU kink: {stats['kink_flips']}", flush=True)
+          f"the LeakyReLU kink: {stats['kink_flips']}; dh {elementwise(h.grad, e_dh)}",
+          flush=True)
     assert all(e <= 1e-5 for e in errs.values()), errs
 
 
@@ -145,7 +167,52 @@ def test_c4_full_size_gradients_against_float64(c34):
     errs = {n: rel(g, w) for n, g, w in zip(("dq", "dk", "dv", "dbias"),
                                             (q.grad, k.grad, v.grad, bias.grad), want)}
     print(f"c4 relative errors {errs}", flush=True)
+    for n, g, w in zip(("dq", "dk", "dv", "dbias"), (q.grad, k.grad, v.grad, bias.grad), want):
+        print(f"  {n} {elementwise(g, w)}", flush=True)
     assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+def test_c5_full_size_sequences_against_float64():
+    """C5 as the bench runs it (32 sequences of U[512, 4096] tokens, H = 16,
+    D = 128, bf16, the bench's seed): out, dq, dk and dv of the longest
+    sequence and of two seeded others against the query-chunked float64
+    per-sequence causal attention (oracle/chunked.causal_sequence), 2e-2."""
+    seed = 20260821                           # bench.py's default seed
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(512, 4097, size=32)
+    cu_host = np.concatenate([[0], np.cumsum(lengths)])
+    T, H, D = int(lengths.sum()), 16, 128
+    picks = [int(np.argmax(lengths))]
+    others = [b for b in range(32) if b != picks[0]]
+    picks += [int(b) for b in np.random.default_rng(seed + 2).choice(others, 2, replace=False)]
+    print(f"c5 full size values: {T} tokens, sequences {picks} of lengths "
+          f"{[int(lengths[b]) for b in picks]}", flush=True)
+    cu = torch.tensor(cu_host, dtype=torch.int64, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(seed + 1)
+    mk = lambda: torch.randn(T, H, D, device=DEV, generator=g).to(torch.bfloat16)
+    q, k, v = (mk().requires_grad_(True) for _ in range(3))
+    dout = mk()
+    from test_gpu_fullsize import VarlenAttention
+    kernel = VarlenAttention()
+    out = kernel(graph=tg.Graph.cu_seqlens(cu, causal=True), src={"key": k, "value": v},
+                 dst={"query": q}, scale=D ** -0.5)
+    assert kernel.last_variant.backend == "hip"
+    out.backward(dout)
+    torch.cuda.synchronize()
+    got = (out.detach(), q.grad, k.grad, v.grad)
+    d = lambda t: t.detach().double()
+    worst = {}
+    for b in picks:
+        s0, s1 = int(cu_host[b]), int(cu_host[b + 1])
+        e_out, _, e_dq, e_dk, e_dv = chunked.causal_sequence(
+            d(q[s0:s1]), d(k[s0:s1]), d(v[s0:s1]), D ** -0.5, d(dout[s0:s1]))
+        for name, gpu, want in zip(("out", "dq", "dk", "dv"), got, (e_out, e_dq, e_dk, e_dv)):
+            err = rel(gpu[s0:s1], want)
+            worst[name] = max(worst.get(name, 0.0), err)
+            print(f"  sequence {b} (L={s1 - s0}) {name}: {err:.3e}, "
+                  f"{elementwise(gpu[s0:s1], want)}", flush=True)
+        del e_out, e_dq, e_dk, e_dv
+    assert all(e <= 2e-2 for e in worst.values()), worst
 
 
 @pytest.mark.parametrize("with_bias", [False, True])

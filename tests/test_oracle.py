@@ -587,6 +587,33 @@ def test_chunked_dot_matches_ref(with_bias):
         np.testing.assert_allclose(g.numpy(), w, rtol=1e-11, atol=1e-12)
 
 
+@pytest.mark.parametrize("query_block", [1, 7, 64, 512])
+def test_chunked_causal_sequence_matches_ref(query_block):
+    """The full-size C5 checker equals ref.varlen_causal_fwd/bwd (pinned by
+    equality with the dot-product relation on the materialized cu_seqlens
+    CSR) for any query block, and its logsumexp equals the per-row closed
+    form log(sum_j<=i exp(s_ij))."""
+    from oracle import chunked
+
+    rng = np.random.default_rng(24)
+    L, H, D, scale = 70, 3, 8, 0.35
+    q, k, v, dout = (rng.standard_normal((L, H, D)) for _ in range(4))
+    t = lambda a: torch.tensor(a, dtype=torch.float64)
+    out, lse, dq, dk, dv = chunked.causal_sequence(t(q), t(k), t(v), scale, t(dout),
+                                                   query_block=query_block)
+    cu = np.array([0, L])
+    e_out, e_lse = ref.varlen_causal_fwd(cu, q, k, v, scale)
+    np.testing.assert_allclose(out.numpy(), e_out, rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(lse.numpy(), e_lse, rtol=1e-12)
+    for g, w in zip((dq, dk, dv), ref.varlen_causal_bwd(cu, q, k, v, scale, dout)):
+        np.testing.assert_allclose(g.numpy(), w, rtol=1e-11, atol=1e-12)
+    i, h = 41, 2
+    s = (q[i, h] * k[:i + 1, h]).sum(-1) * scale
+    assert abs(lse.numpy()[i, h] - np.log(np.exp(s).sum())) < 1e-12
+    fwd_only = chunked.causal_sequence(t(q), t(k), t(v), scale, query_block=query_block)
+    assert len(fwd_only) == 2 and torch.equal(fwd_only[0], out)
+
+
 def test_reference_bf16_dot_arithmetic_is_the_eager_path():
     """eager_torch.dot_reference: in float64 it equals the pinned ref
     forward and backward; in bf16 it differs from them by the bf16 rounding
