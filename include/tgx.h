@@ -248,57 +248,69 @@ int tgx_csr_edge_dot(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                      void* stream);
 
 /* ------------------------------------------------------------------------ */
-/* GAT additive edge attention (fp32)                                        */
+/* GAT additive edge attention (fp32, bf16 or fp16 in, fp32 accumulate)     */
 /*   z_e = a_src . h[j] + a_dst . h[i]   per head,  s_e = LeakyReLU(z_e)     */
 /*   out[i] = sum_e softmax_i(s)_e * h[j]                                     */
 /* ------------------------------------------------------------------------ */
 
-/* Forward.  h [N, H, D] fp32 (src and dst node sets coincide), a_src/a_dst
- * [H, D], out [N, H, D].  node_state [N, H, 4] fp32 receives per (node,head):
- * [0] logsumexp of the row's scores (-inf for an empty row), [1] reserved for
- * the backward (delta = <dout, out>), [2] a_dst.h[i], [3] a_src.h[i].
+/* Forward.  h_src [n_src, H, D] (gathered per edge) and h_dst [n_dst, H, D]
+ * (the row's own features) of element type `dtype` (TGX_DTYPE_F32, _BF16 or
+ * _F16); pass the same pointer twice for a homogeneous relation (then
+ * n_src == n_dst).  a_src/a_dst [H, D] fp32, out [n_dst, H, D] of `dtype`.
+ * Scores, softmax sums and products are fp32; out is rounded once (the
+ * reference's eager path accumulates 16-bit scores in fp32 and casts back,
+ * reducer_oracle.py:22-41, 137).  node_state [n_dst, H, 4] fp32 receives
+ * per (node, head): [0] logsumexp of the row's scores (-inf for an empty
+ * row), [1] reserved for the backward (delta = <dout, out>), [2]
+ * a_dst.h_dst[i], [3] a_src.h_dst[i].
  * partial_dev: tgx_partial_bytes(plan, H*D + 2*H) bytes (NULL if no split rows).
  * Supported shapes: any H >= 1 with D in {4, 8, 16, 32, 64, 128, 256}
  * (others return TGX_UNSUPPORTED).  Heads run in groups of a power-of-two
- * count with at most 256 floats per node (H = 8, D = 64: two groups of 4),
+ * count with at most 256 values per node (H = 8, D = 64: two groups of 4),
  * one after another on `stream`, each over its strided slice of the rows.
  * The reference evaluates this edge function with its eager oracle
  * (interop/torch/message_passing.py:2848-2894 -> reducer_oracle.py:60-137). */
 int tgx_gat_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
-                const tgx_row_plan* plan, const float* h_dev,
+                const tgx_row_plan* plan, const void* h_src_dev, const void* h_dst_dev,
                 const float* a_src_dev, const float* a_dst_dev,
-                float negative_slope, float* out_dev, float* node_state_dev,
-                int64_t n_nodes, int H, int D, float* partial_dev,
+                float negative_slope, void* out_dev, float* node_state_dev,
+                int64_t n_dst, int64_t n_src, int H, int D, int dtype, float* partial_dev,
                 void* stream);
 
-/* Workspace bytes for tgx_gat_bwd with these plans. */
+/* Workspace bytes for tgx_gat_bwd with these plans and element type. */
 int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
-                          int64_t n_edges, int H, int D, size_t* bytes);
+                          int64_t n_edges, int H, int D, int dtype, size_t* bytes);
 
 /* Fused backward from the saved logsumexp (no per-edge alpha is stored by
- * the forward and no float atomics are used):
- *   dh, da_src, da_dst for loss gradient dout [N, H, D].
- * Uses the transposed CSR (row_ptr_t, col_t, perm, inv_perm) and its plan.
- * node_state slot 1 (delta) is overwritten. */
+ * the forward and no float atomics are used): dh_src, dh_dst (of `dtype`),
+ * da_src, da_dst (fp32) for loss gradient dout [n_dst, H, D].  One
+ * gradient buffer (dh_src == dh_dst) declares one feature tensor for both
+ * roles (then h_src == h_dst and n_src == n_dst are required) and receives
+ * both roles' terms, rounded once; two buffers receive the source and the
+ * destination terms separately.  Uses the transposed CSR (row_ptr_t, col_t, perm, inv_perm)
+ * and its plan.  node_state slot 1 (delta) is overwritten. */
 int tgx_gat_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                 const tgx_row_plan* plan, const int32_t* row_ptr_t_dev,
                 const int32_t* col_t_dev, const int32_t* perm_dev,
-                const int32_t* inv_perm_dev, const tgx_row_plan* plan_t, const float* h_dev,
-                const float* a_src_dev, const float* a_dst_dev,
-                float negative_slope, const float* out_dev,
-                float* node_state_dev, const float* dout_dev, float* dh_dev,
-                float* da_src_dev, float* da_dst_dev, int64_t n_nodes,
-                int64_t n_edges, int H, int D, void* workspace_dev,
-                size_t workspace_bytes, void* stream);
+                const int32_t* inv_perm_dev, const tgx_row_plan* plan_t,
+                const void* h_src_dev, const void* h_dst_dev, const float* a_src_dev,
+                const float* a_dst_dev, float negative_slope, const void* out_dev,
+                float* node_state_dev, const void* dout_dev, void* dh_src_dev,
+                void* dh_dst_dev, float* da_src_dev, float* da_dst_dev, int64_t n_dst,
+                int64_t n_src, int64_t n_edges, int H, int D, int dtype,
+                void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
-/* Dot-product edge attention (bf16 in, fp32 accumulate)                     */
+/* Dot-product edge attention (bf16, fp16 or fp32 in, fp32 accumulate)       */
 /*   s_e = scale * (k[j] . q[i]) + bias[e]   per head,                       */
 /*   out[i] = sum_e softmax_i(s)_e * v[j]                                     */
 /* ------------------------------------------------------------------------ */
 
-/* Forward.  q [n_dst, H, D], k/v [n_src, H, D], out [n_dst, H, D]: bf16 (raw
- * 16-bit storage); bias [E, H] fp32 or NULL.  ml [n_dst, H, 2] fp32 receives
+/* Forward.  q [n_dst, H, D], k/v [n_src, H, D], out [n_dst, H, D]: element
+ * type `dtype` (TGX_DTYPE_BF16, _F16 or _F32; scores, softmax sums and
+ * products in fp32, the output rounded to dtype once, as the reference's
+ * eager path accumulates 16-bit inputs in fp32 and casts the result back,
+ * reducer_oracle.py:22-41, 137); bias [E, H] fp32 or NULL.  ml [n_dst, H, 2] fp32 receives
  * {logsumexp (-inf for an empty row), 0}.  partial_dev:
  * tgx_partial_bytes(plan, H*D + 2*H) bytes (NULL without split rows).
  * Supported: any H >= 1 with D in {8, 16, 32, 64, 128, 256, 512}.  Heads run
@@ -310,7 +322,7 @@ int tgx_dot_attn_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                      const tgx_row_plan* plan, const void* q_dev, const void* k_dev,
                      const void* v_dev, const float* bias_dev, float scale,
                      void* out_dev, float* ml_dev, int64_t n_dst, int64_t n_src, int H,
-                     int D, float* partial_dev, void* stream);
+                     int D, int dtype, float* partial_dev, void* stream);
 
 /* tgx_dot_attn_fwd without the partial_dev argument: the split-row partials
  * go to a static device array of 64 MiB per device (held until the process
@@ -327,14 +339,14 @@ int tgx_dot_attn_fwd_noalloc(const void* row_ptr_dev, const void* col_dev, int i
                              const tgx_row_plan* plan, const void* q_dev, const void* k_dev,
                              const void* v_dev, const float* bias_dev, float scale,
                              void* out_dev, float* ml_dev, int64_t n_dst, int64_t n_src,
-                             int H, int D, void* stream);
+                             int H, int D, int dtype, void* stream);
 
 /* Workspace bytes for tgx_dot_attn_bwd with these plans. */
 int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
                                int H, int D, size_t* bytes);
 
-/* Fused backward from the saved logsumexp, no float atomics: dq (bf16) and
- * dbias (fp32 [E, H], may be NULL) on the destination-row CSR, dk/dv (bf16)
+/* Fused backward from the saved logsumexp, no float atomics: dq (dtype) and
+ * dbias (fp32 [E, H], may be NULL) on the destination-row CSR, dk/dv (dtype)
  * on the transposed CSR (row_ptr_t, col_t, perm) and its plan.  ml slot 1
  * (delta = <dout, out>) is overwritten. */
 int tgx_dot_attn_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
@@ -344,7 +356,7 @@ int tgx_dot_attn_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                      const void* v_dev, const float* bias_dev, float scale,
                      const void* out_dev, float* ml_dev, const void* dout_dev, void* dq_dev,
                      void* dk_dev, void* dv_dev, float* dbias_dev, int64_t n_dst,
-                     int64_t n_src, int H, int D, void* workspace_dev,
+                     int64_t n_src, int H, int D, int dtype, void* workspace_dev,
                      size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */

@@ -82,27 +82,28 @@ int tgx_cpu_csr_edge_dot(const void* row_ptr, const void* col, int idx_bits,
 
 /* Twin of tgx_gat_fwd (eager evaluation of the additive edge function,
  * interop/torch/message_passing.py:2848-2894, reducer_oracle.py:60-137).
- * Same node_state layout [N, H, 4]. */
+ * Same arguments and node_state layout [n_dst, H, 4]. */
 int tgx_cpu_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
-                    const tgx_row_plan* plan, const float* h, const float* a_src,
-                    const float* a_dst, float negative_slope, float* out, float* node_state,
-                    int64_t n_nodes, int H, int D);
+                    const tgx_row_plan* plan, const void* h_src, const void* h_dst,
+                    const float* a_src, const float* a_dst, float negative_slope, void* out,
+                    float* node_state, int64_t n_dst, int64_t n_src, int H, int D, int dtype);
 
 /* Twin of tgx_gat_bwd; node_state slot 1 (delta) is overwritten. */
 int tgx_cpu_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
                     const tgx_row_plan* plan, const int32_t* row_ptr_t, const int32_t* col_t,
                     const int32_t* perm, const int32_t* inv_perm, const tgx_row_plan* plan_t,
-                    const float* h, const float* a_src, const float* a_dst,
-                    float negative_slope, const float* out, float* node_state,
-                    const float* dout, float* dh, float* da_src, float* da_dst,
-                    int64_t n_nodes, int64_t n_edges, int H, int D);
+                    const void* h_src, const void* h_dst, const float* a_src,
+                    const float* a_dst, float negative_slope, const void* out,
+                    float* node_state, const void* dout, void* dh_src, void* dh_dst,
+                    float* da_src, float* da_dst, int64_t n_dst, int64_t n_src,
+                    int64_t n_edges, int H, int D, int dtype);
 
-/* Twin of tgx_dot_attn_fwd (bf16 q/k/v/out as raw 16-bit storage, fp32 bias
- * [E, H] or NULL, ml [n_dst, H, 2]). */
+/* Twin of tgx_dot_attn_fwd (q/k/v/out of element type dtype = TGX_DTYPE_BF16,
+ * _F16 or _F32, fp32 bias [E, H] or NULL, ml [n_dst, H, 2]). */
 int tgx_cpu_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bits,
                          const tgx_row_plan* plan, const void* q, const void* k,
                          const void* v, const float* bias, float scale, void* out, float* ml,
-                         int64_t n_dst, int64_t n_src, int H, int D);
+                         int64_t n_dst, int64_t n_src, int H, int D, int dtype);
 
 /* Twin of tgx_dot_attn_bwd; ml slot 1 (delta) is overwritten. */
 int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bits,
@@ -111,7 +112,8 @@ int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bits,
                          const tgx_row_plan* plan_t, const void* q, const void* k,
                          const void* v, const float* bias, float scale, const void* out,
                          float* ml, const void* dout, void* dq, void* dk, void* dv,
-                         float* dbias, int64_t n_dst, int64_t n_src, int H, int D);
+                         float* dbias, int64_t n_dst, int64_t n_src, int H, int D,
+                         int dtype);
 
 /* Twin of tgx_attn_fwd over n_blocks blocks of cu_q / cu_k (host arrays of
  * n_blocks + 1) in place of the device task list.  Only exact softmax:

@@ -269,51 +269,69 @@ def _leaky(z, slope):
     return np.where(z > 0, z, z * slope)
 
 
-def gat_scores(row_ptr, col_idx, h, a_src, a_dst, slope):
-    """z_e = sum_d h[j]*a_src + sum_d h[i]*a_dst, s = LeakyReLU(z): the edge()
-    (src.h*a_src).sum(-1) + (dst.h*a_dst).sum(-1) evaluated per edge as in
-    _evaluate_reference (interop/torch/message_passing.py:2848-2894)."""
+def gat_scores(row_ptr, col_idx, h, a_src, a_dst, slope, h_dst=None):
+    """z_e = sum_d h[j]*a_src + sum_d h_dst[i]*a_dst, s = LeakyReLU(z): the
+    edge() (src.h*a_src).sum(-1) + (dst.h*a_dst).sum(-1) evaluated per edge as
+    in _evaluate_reference (interop/torch/message_passing.py:2848-2894).
+    h_dst=None: one feature tensor for both roles (homogeneous relation)."""
     h = np.asarray(h, dtype=np.float64)
+    hd = h if h_dst is None else np.asarray(h_dst, dtype=np.float64)
     a_src = np.asarray(a_src, dtype=np.float64)
     a_dst = np.asarray(a_dst, dtype=np.float64)
     dst = destination_index(row_ptr)
     col_idx = np.asarray(col_idx, dtype=np.int64)
     ss = (h * a_src).sum(-1)
-    sd = (h * a_dst).sum(-1)
+    sd = (hd * a_dst).sum(-1)
     z = ss[col_idx] + sd[dst]
     return z, _leaky(z, slope)
 
 
-def gat_fwd(row_ptr, col_idx, h, a_src, a_dst, slope):
-    """GAT forward = segment_softmax(score = LeakyReLU(z), value = h[col]).
+def gat_fwd(row_ptr, col_idx, h, a_src, a_dst, slope, h_dst=None):
+    """GAT forward = segment_softmax(score = LeakyReLU(z), value = h[col]);
+    h holds the source features, h_dst (default: h) the destinations'.
 
     Pinned by: reduction to segment_softmax (itself pinned) and the closed
     form a_src = a_dst = 0 -> uniform mean of neighbours."""
-    _, s = gat_scores(row_ptr, col_idx, h, a_src, a_dst, slope)
+    _, s = gat_scores(row_ptr, col_idx, h, a_src, a_dst, slope, h_dst)
     h = np.asarray(h, dtype=np.float64)
     return segment_softmax(row_ptr, s, h[np.asarray(col_idx, dtype=np.int64)])
 
 
-def gat_bwd(row_ptr, col_idx, h, a_src, a_dst, slope, dout):
-    """Gradients of gat_fwd w.r.t. h, a_src, a_dst (LeakyReLU'(0) = slope, as
-    torch.nn.functional.leaky_relu's backward).
+def gat_bwd_bipartite(row_ptr, col_idx, h_src, h_dst, a_src, a_dst, slope, dout):
+    """Gradients (dh_src, dh_dst, da_src, da_dst) of gat_fwd with two feature
+    tensors (LeakyReLU'(0) = slope, as torch.nn.functional.leaky_relu's
+    backward).
 
-    Pinned by: central finite differences on small graphs (tests/test_oracle.py).
-    """
-    h = np.asarray(h, dtype=np.float64)
+    Pinned by: central finite differences on small bipartite graphs, and
+    dh_src + dh_dst == gat_bwd's dh when both tensors are one
+    (tests/test_oracle.py)."""
+    hs = np.asarray(h_src, dtype=np.float64)
+    hd = np.asarray(h_dst, dtype=np.float64)
     col_idx = np.asarray(col_idx, dtype=np.int64)
     dst = destination_index(row_ptr)
-    z, s = gat_scores(row_ptr, col_idx, h, a_src, a_dst, slope)
-    dscore, dvalue = segment_softmax_bwd(row_ptr, s, h[col_idx], dout)
+    z, s = gat_scores(row_ptr, col_idx, hs, a_src, a_dst, slope, hd)
+    dscore, dvalue = segment_softmax_bwd(row_ptr, s, hs[col_idx], dout)
     dz = np.where(z > 0, dscore, dscore * slope)
     a_src = np.asarray(a_src, dtype=np.float64)
     a_dst = np.asarray(a_dst, dtype=np.float64)
-    dh = np.zeros_like(h)
-    np.add.at(dh, col_idx, dvalue + dz[..., None] * a_src)
-    np.add.at(dh, dst, dz[..., None] * a_dst)
-    da_src = (dz[..., None] * h[col_idx]).sum(0)
-    da_dst = (dz[..., None] * h[dst]).sum(0)
-    return dh, da_src, da_dst
+    dhs = np.zeros_like(hs)
+    dhd = np.zeros_like(hd)
+    np.add.at(dhs, col_idx, dvalue + dz[..., None] * a_src)
+    np.add.at(dhd, dst, dz[..., None] * a_dst)
+    da_src = (dz[..., None] * hs[col_idx]).sum(0)
+    da_dst = (dz[..., None] * hd[dst]).sum(0)
+    return dhs, dhd, da_src, da_dst
+
+
+def gat_bwd(row_ptr, col_idx, h, a_src, a_dst, slope, dout):
+    """Gradients of gat_fwd w.r.t. h, a_src, a_dst for one feature tensor
+    (both roles' terms summed into dh).
+
+    Pinned by: central finite differences on small graphs (tests/test_oracle.py).
+    """
+    dhs, dhd, da_src, da_dst = gat_bwd_bipartite(row_ptr, col_idx, h, h, a_src, a_dst, slope,
+                                                 dout)
+    return dhs + dhd, da_src, da_dst
 
 
 # ---------------------------------------------------------------------------

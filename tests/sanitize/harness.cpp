@@ -133,12 +133,13 @@ std::string run_twins(uint64_t seed, int64_t n, int H, int D) {
     sums[r].insert(sums[r].end(), dx.begin(), dx.end());
     sums[r].insert(sums[r].end(), dw.begin(), dw.end());
     std::vector<float> ho(n * HD), ns(n * H * 4), dh(n * HD), das(HD), dad(HD);
-    if (tgx_cpu_gat_fwd(rp.data(), col.data(), 64, &plan.p, h.data(), a.data(), a.data() + HD,
-                        0.2f, ho.data(), ns.data(), n, H, D) != TGX_OK ||
+    if (tgx_cpu_gat_fwd(rp.data(), col.data(), 64, &plan.p, h.data(), h.data(), a.data(),
+                        a.data() + HD, 0.2f, ho.data(), ns.data(), n, n, H, D,
+                        TGX_DTYPE_F32) != TGX_OK ||
         tgx_cpu_gat_bwd(rp.data(), col.data(), 64, &plan.p, rpt.data(), colt.data(), perm.data(),
-                        inv.data(), &plan_t.p, h.data(), a.data(), a.data() + HD, 0.2f,
-                        ho.data(), ns.data(), dh_in.data(), dh.data(), das.data(), dad.data(), n,
-                        E, H, D) != TGX_OK)
+                        inv.data(), &plan_t.p, h.data(), h.data(), a.data(), a.data() + HD, 0.2f,
+                        ho.data(), ns.data(), dh_in.data(), dh.data(), dh.data(), das.data(),
+                        dad.data(), n, n, E, H, D, TGX_DTYPE_F32) != TGX_OK)
       return std::string("gat: ") + tgx_last_error();
     gats[r] = ho;
     gats[r].insert(gats[r].end(), dh.begin(), dh.end());
@@ -148,11 +149,12 @@ std::string run_twins(uint64_t seed, int64_t n, int H, int D) {
     std::vector<float> ml(n * H * 2), db(E * H);
     if (D % 8 == 0) {
       if (tgx_cpu_dot_attn_fwd(rp.data(), col.data(), 64, &plan.p, q.data(), k.data(), v.data(),
-                               bias.data(), 0.125f, o.data(), ml.data(), n, n, H, D) != TGX_OK ||
+                               bias.data(), 0.125f, o.data(), ml.data(), n, n, H, D,
+                               TGX_DTYPE_BF16) != TGX_OK ||
           tgx_cpu_dot_attn_bwd(rp.data(), col.data(), 64, &plan.p, rpt.data(), colt.data(),
                                perm.data(), &plan_t.p, q.data(), k.data(), v.data(), bias.data(),
                                0.125f, o.data(), ml.data(), go.data(), dq.data(), dk.data(),
-                               dv.data(), db.data(), n, n, H, D) != TGX_OK)
+                               dv.data(), db.data(), n, n, H, D, TGX_DTYPE_BF16) != TGX_OK)
         return std::string("dot: ") + tgx_last_error();
     }
     dots[r] = o;

@@ -221,8 +221,8 @@ def test_gat_twin_against_oracle(H, D, bits):
     dout = rng.standard_normal((N, H, D)).astype(np.float32)
     out = np.empty_like(h)
     ns = np.empty((N, H, 4), np.float32)
-    call("tgx_cpu_gat_fwd", p(g.rp), p(g.col), bits, g.plan.ref, p(h), p(a_s), p(a_d), 0.2,
-         p(out), p(ns), N, H, D)
+    call("tgx_cpu_gat_fwd", p(g.rp), p(g.col), bits, g.plan.ref, p(h), p(h), p(a_s), p(a_d),
+         0.2, p(out), p(ns), N, N, H, D, F32)
     e_out, e_lse = ref.gat_fwd(rp, col, h, a_s, a_d, 0.2)
     assert rel(out, e_out) <= 1e-5
     finite = np.isfinite(e_lse)
@@ -233,12 +233,57 @@ def test_gat_twin_against_oracle(H, D, bits):
     das = np.empty_like(a_s)
     dad = np.empty_like(a_d)
     call("tgx_cpu_gat_bwd", p(g.rp), p(g.col), bits, g.plan.ref, p(g.rpt), p(g.colt),
-         p(g.perm), p(g.inv), g.plan_t.ref, p(h), p(a_s), p(a_d), 0.2, p(out), p(ns), p(dout),
-         p(dh), p(das), p(dad), N, g.E, H, D)
+         p(g.perm), p(g.inv), g.plan_t.ref, p(h), p(h), p(a_s), p(a_d), 0.2, p(out), p(ns),
+         p(dout), p(dh), p(dh), p(das), p(dad), N, N, g.E, H, D, F32)
     e_dh, e_das, e_dad = ref.gat_bwd(rp, col, h, a_s, a_d, 0.2, dout)
     assert rel(dh, e_dh) <= 1e-5
     assert rel(das, e_das) <= 1e-5
     assert rel(dad, e_dad) <= 1e-5
+
+
+@pytest.mark.parametrize("kind", ["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("bipartite", [False, True])
+def test_gat_twin_element_types_and_bipartite(kind, bipartite):
+    """The GAT twin with 16-bit elements (fp32 arithmetic, outputs rounded
+    once: 2e-2) and with two feature tensors (1500 destinations, 2300
+    sources) against the fp64 oracle on the type-rounded inputs."""
+    dtype, code, tol = _DOT_DTYPES[kind]
+    n_dst, n_src, H, D = 1500, 2300 if bipartite else 1500, 4, 32
+    rp, col = skewed_csr(77, n_dst, n_src, mean_deg=8, hubs=(1200,), hot_src=5, hot_frac=0.2)
+    g = HostGraph(rp, col, n_src, 64)
+    rng = np.random.default_rng(3)
+    mk = lambda n: torch.as_tensor(rng.standard_normal((n, H, D)), dtype=torch.float32).to(dtype)
+    hs = mk(n_src)
+    hd = mk(n_dst) if bipartite else hs
+    dout = mk(n_dst)
+    a_s = (0.1 * rng.standard_normal((H, D))).astype(np.float32)
+    a_d = (0.1 * rng.standard_normal((H, D))).astype(np.float32)
+    raw = (lambda t: np.ascontiguousarray(t.numpy())) if kind == "fp32" else _raw
+    back = (lambda a: a.astype(np.float64)) if kind == "fp32" else \
+        (lambda a: _from_raw(a, dtype))
+    store = np.float32 if kind == "fp32" else np.int16
+    rhs = raw(hs)
+    rhd = raw(hd) if bipartite else rhs
+    rg = raw(dout)
+    out = np.zeros((n_dst, H, D), store)
+    ns = np.empty((n_dst, H, 4), np.float32)
+    call("tgx_cpu_gat_fwd", p(g.rp), p(g.col), 64, g.plan.ref, p(rhs), p(rhd), p(a_s), p(a_d),
+         0.2, p(out), p(ns), n_dst, n_src, H, D, code)
+    f = lambda t: t.double().numpy()
+    e_out, _ = ref.gat_fwd(rp, col, f(hs), a_s, a_d, 0.2, h_dst=f(hd) if bipartite else None)
+    assert rel(back(out), e_out) <= tol
+    dhs = np.zeros((n_src, H, D), store)
+    dhd = np.zeros((n_dst, H, D), store) if bipartite else dhs
+    das, dad = np.empty_like(a_s), np.empty_like(a_d)
+    call("tgx_cpu_gat_bwd", p(g.rp), p(g.col), 64, g.plan.ref, p(g.rpt), p(g.colt),
+         p(g.perm), p(g.inv), g.plan_t.ref, p(rhs), p(rhd), p(a_s), p(a_d), 0.2, p(out), p(ns),
+         p(rg), p(dhs), p(dhd), p(das), p(dad), n_dst, n_src, g.E, H, D, code)
+    e = ref.gat_bwd_bipartite(rp, col, f(hs), f(hd), a_s, a_d, 0.2, f(dout))
+    if bipartite:
+        assert rel(back(dhs), e[0]) <= tol and rel(back(dhd), e[1]) <= tol
+    else:
+        assert rel(back(dhs), e[0] + e[1]) <= tol
+    assert rel(das, e[2]) <= tol and rel(dad, e[3]) <= tol
 
 
 def test_twin_results_do_not_depend_on_the_thread_count():
@@ -253,12 +298,12 @@ def test_twin_results_do_not_depend_on_the_thread_count():
         prev = _native.lib().tgx_cpu_set_threads(threads)
         try:
             out, ns = np.empty_like(h), np.empty((N, H, 4), np.float32)
-            call("tgx_cpu_gat_fwd", p(g.rp), p(g.col), 64, g.plan.ref, p(h), p(a[0]), p(a[1]),
-                 0.2, p(out), p(ns), N, H, D)
+            call("tgx_cpu_gat_fwd", p(g.rp), p(g.col), 64, g.plan.ref, p(h), p(h), p(a[0]),
+                 p(a[1]), 0.2, p(out), p(ns), N, N, H, D, F32)
             dh, das, dad = np.empty_like(h), np.empty_like(a[0]), np.empty_like(a[1])
             call("tgx_cpu_gat_bwd", p(g.rp), p(g.col), 64, g.plan.ref, p(g.rpt), p(g.colt),
-                 p(g.perm), p(g.inv), g.plan_t.ref, p(h), p(a[0]), p(a[1]), 0.2, p(out), p(ns),
-                 p(dout), p(dh), p(das), p(dad), N, g.E, H, D)
+                 p(g.perm), p(g.inv), g.plan_t.ref, p(h), p(h), p(a[0]), p(a[1]), 0.2, p(out),
+                 p(ns), p(dout), p(dh), p(dh), p(das), p(dad), N, N, g.E, H, D, F32)
             runs.append((out, dh, das, dad))
         finally:
             _native.lib().tgx_cpu_set_threads(prev)
@@ -267,36 +312,50 @@ def test_twin_results_do_not_depend_on_the_thread_count():
             assert np.array_equal(x, y)
 
 
-# ---- dot-product attention (bf16) ----------------------------------------------------
+# ---- dot-product attention (bf16, fp16, fp32) ----------------------------------------
+
+_DOT_DTYPES = {"bf16": (torch.bfloat16, 0, 2e-2), "fp16": (torch.float16, 1, 2e-2),
+               "fp32": (torch.float32, 2, 1e-5)}
+
 
 @pytest.mark.parametrize("H,D", [(4, 64), (16, 64), (3, 64), (1, 8)])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_dot_twin_against_oracle(H, D, with_bias):
+@pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
+def test_dot_twin_against_oracle(H, D, with_bias, kind):
+    """The CPU twin of the dot-product entry points in each element type
+    against the fp64 oracle on the type-rounded inputs: fp32 within 1e-5,
+    the 16-bit types (one rounding of each output) within 2e-2."""
+    dtype, code, tol = _DOT_DTYPES[kind]
     rp, col = rmat_csr(5, 10)
     N, E = rp.size - 1, col.size
     g = HostGraph(rp, col, N, 64)
     rng = np.random.default_rng(H + D)
-    q, k, v, dout = (_bf16(rng.standard_normal((N, H, D))) for _ in range(4))
+    q, k, v, dout = (torch.as_tensor(rng.standard_normal((N, H, D)), dtype=torch.float32)
+                     .to(dtype) for _ in range(4))
     bias = rng.standard_normal((E, H)).astype(np.float32) if with_bias else None
-    f = lambda t: t.float().numpy()
+    f = lambda t: t.double().numpy()
+    raw = (lambda t: np.ascontiguousarray(t.numpy())) if kind == "fp32" else _raw
+    back = (lambda a: a.astype(np.float64)) if kind == "fp32" else \
+        (lambda a: _from_raw(a, dtype))
+    store = np.float32 if kind == "fp32" else np.int16
     scale = D ** -0.5
-    out = np.zeros((N, H, D), np.int16)
+    out = np.zeros((N, H, D), store)
     ml = np.empty((N, H, 2), np.float32)
-    rq, rk, rv, rg = _raw(q), _raw(k), _raw(v), _raw(dout)
+    rq, rk, rv, rg = raw(q), raw(k), raw(v), raw(dout)
     call("tgx_cpu_dot_attn_fwd", p(g.rp), p(g.col), 64, g.plan.ref, p(rq), p(rk), p(rv),
-         p(bias), scale, p(out), p(ml), N, N, H, D)
+         p(bias), scale, p(out), p(ml), N, N, H, D, code)
     e_out, _ = ref.dot_fwd(rp, col, f(q), f(k), f(v), scale, bias)
-    assert rel(_from_raw(out, torch.bfloat16), e_out) <= 2e-2
-    dq, dk, dv = (np.zeros((N, H, D), np.int16) for _ in range(3))
+    assert rel(back(out), e_out) <= tol
+    dq, dk, dv = (np.zeros((N, H, D), store) for _ in range(3))
     dbias = np.empty((E, H), np.float32) if with_bias else None
     call("tgx_cpu_dot_attn_bwd", p(g.rp), p(g.col), 64, g.plan.ref, p(g.rpt), p(g.colt),
          p(g.perm), g.plan_t.ref, p(rq), p(rk), p(rv), p(bias), scale, p(out), p(ml), p(rg),
-         p(dq), p(dk), p(dv), p(dbias), N, N, H, D)
+         p(dq), p(dk), p(dv), p(dbias), N, N, H, D, code)
     e = ref.dot_bwd(rp, col, f(q), f(k), f(v), scale, bias, f(dout))
     for got, want in zip((dq, dk, dv), e[:3]):
-        assert rel(_from_raw(got, torch.bfloat16), want) <= 2e-2
+        assert rel(back(got), want) <= tol
     if with_bias:
-        assert rel(dbias, e[3]) <= 2e-2
+        assert rel(dbias, e[3]) <= tol
 
 
 # ---- dense attention over block-diagonal relations -------------------------------------
@@ -402,16 +461,18 @@ def test_device_and_twin_reject_the_same_head_shapes(H, D):
     rp = np.zeros(1, np.int64)
     dummy = np.zeros(16, np.float32)
     gat_dev = _status("tgx_gat_fwd", p(rp), p(rp), 64, ctypes.byref(empty), p(dummy), p(dummy),
-                      p(dummy), ctypes.c_float(0.2), p(dummy), p(dummy), 0, H, D, None, None)
+                      p(dummy), p(dummy), ctypes.c_float(0.2), p(dummy), p(dummy), 0, 0, H, D,
+                      2, None, None)
     gat_cpu = _status("tgx_cpu_gat_fwd", p(rp), p(rp), 64, ctypes.byref(empty), p(dummy),
-                      p(dummy), p(dummy), ctypes.c_float(0.2), p(dummy), p(dummy), 0, H, D)
+                      p(dummy), p(dummy), p(dummy), ctypes.c_float(0.2), p(dummy), p(dummy), 0,
+                      0, H, D, 2)
     assert gat_dev == gat_cpu
     assert (gat_dev == 0) == (D % 4 == 0 and D <= 256 and (D // 4) & (D // 4 - 1) == 0)
     dot_dev = _status("tgx_dot_attn_fwd", p(rp), p(rp), 64, ctypes.byref(empty), p(dummy),
                       p(dummy), p(dummy), None, ctypes.c_float(1.0), p(dummy), p(dummy), 0, 0,
-                      H, D, None, None)
+                      H, D, 0, None, None)
     dot_cpu = _status("tgx_cpu_dot_attn_fwd", p(rp), p(rp), 64, ctypes.byref(empty), p(dummy),
                       p(dummy), p(dummy), None, ctypes.c_float(1.0), p(dummy), p(dummy), 0, 0,
-                      H, D)
+                      H, D, 0)
     assert dot_dev == dot_cpu
     assert (dot_dev == 0) == (D % 8 == 0 and D <= 512 and (D // 8) & (D // 8 - 1) == 0)

@@ -90,8 +90,10 @@ def test_c2_full_size_values_against_float64():
     out = kernel(graph=graph, src={"h": h}, dst={"h": h})
     assert kernel.last_variant.backend == "hip"
     # The kernel's own fp32 halves of z (node state slots 3 and 2: a_src.h,
-    # a_dst.h), read before the backward reuses slot 1.
-    node_state = out.grad_fn.saved_tensors[4]
+    # a_dst.h), read before the backward reuses slot 1.  The node state is
+    # the last tensor the GAT autograd function saves.
+    node_state = out.grad_fn.saved_tensors[-1]
+    assert tuple(node_state.shape) == (N, H, 4)
     branch = (node_state[..., 3].clone(), node_state[..., 2].clone())
     out.backward(dout)
     torch.cuda.synchronize()

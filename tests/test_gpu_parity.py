@@ -283,6 +283,71 @@ def test_gat_fwd_bwd_parity(H, D, idx):
     assert rel_err(adt.grad.cpu(), e_dad) <= RTOL32
 
 
+class GATBipartite(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def __init__(self, a_s, a_d, slope):
+        super().__init__()
+        self.a_s, self.a_d, self.slope = a_s, a_d, slope
+
+    def edge(self, src, dst, edge):
+        s = F.leaky_relu((src.h * self.a_s).sum(-1) + (dst.g * self.a_d).sum(-1), self.slope)
+        return self.reducer(s, src.h)
+
+
+# Element types and bipartite relations: fp32 features at 1e-5 against
+# float64, bf16 / fp16 (fp32 arithmetic, outputs rounded once) at 2e-2, with
+# fp32 or same-typed attention vectors; bipartite: 1800 destinations with
+# their own table g, 2600 sources with h, hub rows on both sides.
+@pytest.mark.parametrize("H,D", [(8, 32), (3, 64), (2, 256), (1, 4)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bipartite", [False, True])
+@pytest.mark.parametrize("a_typed", [False, True])
+def test_gat_element_types_and_bipartite_parity(H, D, dtype, bipartite, a_typed):
+    print(f"gat {dtype} H={H} D={D} bipartite={bipartite} a_typed={a_typed}", flush=True)
+    n_dst, n_src = (1800, 2600) if bipartite else (2500, 2500)
+    rp, col = skewed_csr(200 + H, n_dst, n_src, mean_deg=10, hubs=(1400, 700), hot_src=11,
+                         hot_frac=0.3)
+    rng = np.random.default_rng(H * D + 1)
+    mk = lambda n: to_dev(rng.standard_normal((n, H, D)), dtype)
+    hs = mk(n_src)
+    hd = mk(n_dst) if bipartite else hs
+    dout = mk(n_dst)
+    a_dtype = dtype if a_typed else torch.float32
+    a_s = to_dev(rng.standard_normal((H, D)) * 0.1, a_dtype).requires_grad_(True)
+    a_d = to_dev(rng.standard_normal((H, D)) * 0.1, a_dtype).requires_grad_(True)
+    graph = tg.Graph.from_csr(to_dev(rp, torch.int64), to_dev(col, torch.int64), num_src=n_src)
+    hst = hs.clone().requires_grad_(True)
+    if bipartite:
+        hdt = hd.clone().requires_grad_(True)
+        k = GATBipartite(a_s, a_d, 0.2)
+        out = k(graph=graph, src={"h": hst}, dst={"g": hdt})
+    else:
+        k = GAT(a_s, a_d, 0.2)
+        out = k(graph=graph, src={"h": hst}, dst={"h": hst})
+    assert k.last_variant.backend == "hip", k.explain()
+    assert out.dtype == dtype
+    out.backward(dout)
+    f = lambda t: t.detach().double().cpu().numpy()
+    e_out, _ = ref.gat_fwd(rp, col, f(hs), f(a_s), f(a_d), 0.2,
+                           h_dst=f(hd) if bipartite else None)
+    e_dhs, e_dhd, e_das, e_dad = ref.gat_bwd_bipartite(rp, col, f(hs), f(hd), f(a_s), f(a_d),
+                                                       0.2, f(dout))
+    tol = RTOL32 if dtype == torch.float32 else RTOL_BF16
+    assert rel_err(f(out), e_out) <= tol
+    if bipartite:
+        assert hst.grad.dtype == dtype and hdt.grad.dtype == dtype
+        assert rel_err(f(hst.grad), e_dhs) <= tol
+        assert rel_err(f(hdt.grad), e_dhd) <= tol
+    else:
+        assert rel_err(f(hst.grad), e_dhs + e_dhd) <= tol
+    assert a_s.grad.dtype == a_dtype
+    # fp32 parameter gradients are rounded once to a 16-bit a when a is.
+    a_tol = tol if a_dtype == torch.float32 else RTOL_BF16
+    assert rel_err(f(a_s.grad), e_das) <= a_tol
+    assert rel_err(f(a_d.grad), e_dad) <= a_tol
+
+
 def test_gat_large_scores_and_determinism():
     # Scores of order 1e3 (the reference's overflow case) must stay finite.
     N, H, D = 600, 8, 32
@@ -372,6 +437,51 @@ def test_dot_fwd_bwd_parity_rmat(H, D, idx, with_bias):
     # empty destination rows produce exact zeros
     empty = np.flatnonzero(np.diff(rp) == 0)
     assert empty.size > 0
+    assert torch.count_nonzero(out[torch.as_tensor(empty, device=DEV)]).item() == 0
+
+
+# fp32 q/k/v (fp32 arithmetic throughout: 1e-5 against float64) and fp16
+# (2e-2); the bias may be any float type (read as fp32).
+@pytest.mark.parametrize("H,D", [(4, 64), (3, 64), (6, 128), (1, 512), (1, 8), (16, 16)])
+@pytest.mark.parametrize("idx", [torch.int32, torch.int64])
+@pytest.mark.parametrize("dtype,bias_dtype", [(torch.float32, torch.float32),
+                                              (torch.float16, torch.float32),
+                                              (torch.float16, torch.float16),
+                                              (torch.float32, None)])
+def test_dot_fp32_and_fp16_parity_rmat(H, D, idx, dtype, bias_dtype):
+    from graphs import rmat_csr
+
+    print(f"dot {dtype} H={H} D={D} {idx} bias={bias_dtype}", flush=True)
+    rp, col = rmat_csr(5, 12)                      # 4096 nodes, hubs > 512 edges
+    N, E = rp.size - 1, col.size
+    rng = np.random.default_rng(7 * H + D)
+    mk = lambda: torch.as_tensor(rng.standard_normal((N, H, D)), device=DEV).to(dtype)
+    q, k, v, dout = mk(), mk(), mk(), mk()
+    with_bias = bias_dtype is not None
+    bias = to_dev(rng.standard_normal((E, H)), bias_dtype) if with_bias else None
+    scale = 1.0 / np.sqrt(D)
+    graph = tg.Graph.from_csr(to_dev(rp, idx), to_dev(col, idx), num_src=N)
+    qt, kt, vt = (t.clone().requires_grad_(True) for t in (q, k, v))
+    bt = bias.clone().requires_grad_(True) if with_bias else None
+    kernel = DotBias() if with_bias else DotPlain()
+    edge = {"bias": bt} if with_bias else {}
+    out = kernel(graph=graph, src={"k": kt, "v": vt}, dst={"q": qt}, edge=edge, scale=scale)
+    assert kernel.last_variant.backend == "hip"
+    assert out.dtype == dtype
+    out.backward(dout)
+    f = lambda t: t.detach().double().cpu().numpy()
+    b64 = f(bias) if with_bias else None
+    e_out, _ = ref.dot_fwd(rp, col, f(q), f(k), f(v), scale, b64)
+    e_dq, e_dk, e_dv, e_db = ref.dot_bwd(rp, col, f(q), f(k), f(v), scale, b64, f(dout))
+    tol = RTOL32 if dtype == torch.float32 else RTOL_BF16
+    assert rel_err(f(out), e_out) <= tol
+    assert rel_err(f(qt.grad), e_dq) <= tol
+    assert rel_err(f(kt.grad), e_dk) <= tol
+    assert rel_err(f(vt.grad), e_dv) <= tol
+    if with_bias:
+        assert bt.grad.dtype == bias_dtype
+        assert rel_err(f(bt.grad), e_db) <= (tol if bias_dtype == torch.float32 else RTOL_BF16)
+    empty = np.flatnonzero(np.diff(rp) == 0)
     assert torch.count_nonzero(out[torch.as_tensor(empty, device=DEV)]).item() == 0
 
 

@@ -223,6 +223,31 @@ def test_gat_finite_differences_and_uniform_closed_form():
             assert np.all(out[i] == 0)
 
 
+def test_gat_bipartite_finite_differences_and_the_homogeneous_sum():
+    """Two feature tensors (12 destinations, 9 sources): every gradient by
+    central differences; with one tensor for both roles, dh_src + dh_dst is
+    the homogeneous dh."""
+    rng = np.random.default_rng(14)
+    rp, col = random_csr(rng, 12, 9, 5)
+    H, D = 2, 3
+    hs = rng.standard_normal((9, H, D))
+    hd = rng.standard_normal((12, H, D))
+    a_s = rng.standard_normal((H, D)) * 0.5
+    a_d = rng.standard_normal((H, D)) * 0.5
+    dout = rng.standard_normal((12, H, D))
+    grads = ref.gat_bwd_bipartite(rp, col, hs, hd, a_s, a_d, 0.2, dout)
+    f = lambda: (ref.gat_fwd(rp, col, hs, a_s, a_d, 0.2, h_dst=hd)[0] * dout).sum()
+    _fd_check(f, [hs, hd, a_s, a_d], list(grads), rng)
+    rp2, col2 = random_csr(rng, 10, 10, 4)
+    h = rng.standard_normal((10, H, D))
+    g2 = rng.standard_normal((10, H, D))
+    dhs, dhd, das, dad = ref.gat_bwd_bipartite(rp2, col2, h, h, a_s, a_d, 0.2, g2)
+    dh, das1, dad1 = ref.gat_bwd(rp2, col2, h, a_s, a_d, 0.2, g2)
+    np.testing.assert_allclose(dhs + dhd, dh, rtol=1e-13, atol=1e-14)
+    np.testing.assert_array_equal(das, das1)
+    np.testing.assert_array_equal(dad, dad1)
+
+
 def test_dot_finite_differences():
     rng = np.random.default_rng(5)
     rp, col = random_csr(rng, 10, 9, 6)

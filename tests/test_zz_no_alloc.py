@@ -35,7 +35,8 @@ def _forward(name, row_ptr, col, plan, q, k, v, bias, scale, partial=()):
     ml = torch.empty(n, H, 2, device=q.device)
     _native.call(name, row_ptr.data_ptr(), col.data_ptr(), _native.idx_bits(row_ptr), plan.ref,
                  q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), scale,
-                 out.data_ptr(), ml.data_ptr(), n, n, H, D, *partial, _native.stream_of(q))
+                 out.data_ptr(), ml.data_ptr(), n, n, H, D, 0, *partial,
+                 _native.stream_of(q))
     return out, ml
 
 
@@ -62,4 +63,4 @@ def test_noalloc_forward_rejects_plans_beyond_its_scratch():
     plan = _native.RowPlan(10, 0, 9, 1, too_many, 512, 512, 1, 1)
     with pytest.raises(RuntimeError, match="static scratch holds"):
         _native.call("tgx_dot_attn_fwd_noalloc", None, None, 64, ctypes.byref(plan), None,
-                     None, None, None, 0.125, None, None, 10, 10, H, D, None)
+                     None, None, None, 0.125, None, None, 10, 10, H, D, 0, None)

@@ -601,58 +601,108 @@ extern "C" int tgx_cpu_csr_edge_dot(const void* row_ptr, const void* col, int id
   });
 }
 
+// ---- Element types ------------------------------------------------------------------
+
+namespace {
+
+// One element type of the q/k/v/out/dout/dq/dk/dv tensors, read as fp32 and
+// written with one round-to-nearest-even.
+struct Elem {
+  int dtype;  // TGX_DTYPE_*
+  float get(const void* base, int64_t i) const {
+    if (dtype == TGX_DTYPE_F32) return static_cast<const float*>(base)[i];
+    return Half16{dtype}.load(static_cast<const uint16_t*>(base), i);
+  }
+  void put(void* base, int64_t i, float v) const {
+    if (dtype == TGX_DTYPE_F32)
+      static_cast<float*>(base)[i] = v;
+    else
+      static_cast<uint16_t*>(base)[i] = Half16{dtype}.store(v);
+  }
+};
+
+bool elem_ok(int dtype) {
+  return dtype == TGX_DTYPE_BF16 || dtype == TGX_DTYPE_F16 || dtype == TGX_DTYPE_F32;
+}
+
+// n values of `base` widened to fp32.
+std::vector<float> widen_all(const Elem& el, const void* base, int64_t n) {
+  std::vector<float> v(static_cast<size_t>(n));
+  for (int64_t i = 0; i < n; ++i) v[i] = el.get(base, i);
+  return v;
+}
+
+void round_all(const Elem& el, const std::vector<float>& v, void* base) {
+  for (size_t i = 0; i < v.size(); ++i) el.put(base, static_cast<int64_t>(i), v[i]);
+}
+
+}  // namespace
+
 // ---- GAT additive attention -------------------------------------------------------
 
 extern "C" int tgx_cpu_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
-                               const tgx_row_plan* plan, const float* h, const float* a_src,
-                               const float* a_dst, float slope, float* out, float* ns,
-                               int64_t n_nodes, int H, int D) {
+                               const tgx_row_plan* plan, const void* h_src, const void* h_dst,
+                               const float* a_src, const float* a_dst, float slope, void* out,
+                               float* ns, int64_t n_dst, int64_t n_src, int H, int D,
+                               int dtype) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(elem_ok(dtype), "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)", dtype);
   if (!gat_heads_ok(H, D)) {
     set_error("GAT kernel supports H >= 1 and D in {4, 8, 16, 32, 64, 128, 256} "
               "(got H=%d D=%d)", H, D);
     return TGX_UNSUPPORTED;
   }
-  int st = check_plan(plan, n_nodes);
+  TGX_REQUIRE(h_src != h_dst || n_src == n_dst,
+              "one feature tensor for both roles needs n_src == n_dst");
+  int st = check_plan(plan, n_dst);
   if (st != TGX_OK) return st;
-  if (n_nodes == 0) return TGX_OK;
-  TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns, "null pointer");
+  if (n_dst == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && h_dst && a_src && a_dst && out && ns && (h_src || n_src == 0),
+              "null pointer");
   return guarded([&]() -> int {
     const Idx rp{row_ptr, idx_bits}, c{col, idx_bits};
-    int s = check_csr(rp, &c, n_nodes, n_nodes, nullptr);
+    int s = check_csr(rp, &c, n_dst, n_src, nullptr);
     if (s != TGX_OK) return s;
-    s = check_plan_rows(plan, rp, n_nodes);
+    s = check_plan_rows(plan, rp, n_dst);
     if (s != TGX_OK) return s;
     const int64_t HD = static_cast<int64_t>(H) * D;
-    // Per-(node, head) halves of z: a_src . h and a_dst . h.
-    std::vector<float> zs(static_cast<size_t>(n_nodes * H)), zd(zs.size());
-    parallel_ranges(n_nodes, [&](int64_t lo, int64_t hi) {
-      for (int64_t i = lo; i < hi; ++i)
-        for (int hd = 0; hd < H; ++hd) {
-          const float* hr = h + i * HD + hd * D;
-          float a = 0.f, b = 0.f;
-          for (int d = 0; d < D; ++d) {
-            a += a_src[hd * D + d] * hr[d];
-            b += a_dst[hd * D + d] * hr[d];
+    const Elem el{dtype};
+    const std::vector<float> hs = widen_all(el, h_src, n_src * HD);
+    const std::vector<float> hd_own = h_src == h_dst ? std::vector<float>()
+                                                     : widen_all(el, h_dst, n_dst * HD);
+    const float* HS = hs.data();
+    const float* HDv = h_src == h_dst ? hs.data() : hd_own.data();
+    // a . h per (node, head): a_src over the sources, a_dst and a_src over the
+    // destinations (node state slots 2 and 3).
+    auto half = [&](const float* rows, const float* a, int64_t n) {
+      std::vector<float> z(static_cast<size_t>(n * H));
+      parallel_ranges(n, [&](int64_t lo, int64_t hi) {
+        for (int64_t i = lo; i < hi; ++i)
+          for (int hd = 0; hd < H; ++hd) {
+            float acc = 0.f;
+            for (int d = 0; d < D; ++d) acc += a[hd * D + d] * rows[i * HD + hd * D + d];
+            z[i * H + hd] = acc;
           }
-          zs[i * H + hd] = a;
-          zd[i * H + hd] = b;
-        }
-    });
+      });
+      return z;
+    };
+    const std::vector<float> zs = half(HS, a_src, n_src), zd = half(HDv, a_dst, n_dst),
+                             zsd = half(HDv, a_src, n_dst);
+    std::vector<float> o32(static_cast<size_t>(n_dst * HD));
     auto state = [&](int64_t i, int hd, int64_t e0, int64_t e1) {
       Soft st(D);
       for (int64_t e = e0; e < e1; ++e) {
         const int64_t j = c[e];
-        st.add(leaky(zs[j * H + hd] + zd[i * H + hd], slope), h + j * HD + hd * D);
+        st.add(leaky(zs[j * H + hd] + zd[i * H + hd], slope), HS + j * HD + hd * D);
       }
       return st;
     };
     auto finish = [&](int64_t i, int hd, const Soft& st) {
-      float* o = out + i * HD + hd * D;
+      float* o = o32.data() + i * HD + hd * D;
       float* n = ns + (i * H + hd) * 4;
       n[1] = 0.f;
       n[2] = zd[i * H + hd];
-      n[3] = zs[i * H + hd];
+      n[3] = zsd[i * H + hd];
       if (st.l > 0.f) {
         const float inv = 1.f / st.l;
         for (int d = 0; d < D; ++d) o[d] = st.acc[d] * inv;
@@ -677,6 +727,7 @@ extern "C" int tgx_cpu_gat_fwd(const void* row_ptr, const void* col, int idx_bit
         [&](int64_t i) {
           for (int hd = 0; hd < H; ++hd) finish(i, hd, Soft(D));
         });
+    round_all(el, o32, out);
     return TGX_OK;
   });
 }
@@ -685,62 +736,80 @@ extern "C" int tgx_cpu_gat_bwd(const void* row_ptr, const void* col, int idx_bit
                                const tgx_row_plan* plan, const int32_t* row_ptr_t,
                                const int32_t* col_t, const int32_t* perm,
                                const int32_t* inv_perm, const tgx_row_plan* plan_t,
-                               const float* h, const float* a_src, const float* a_dst,
-                               float slope, const float* out, float* ns, const float* dout,
-                               float* dh, float* da_src, float* da_dst, int64_t n_nodes,
-                               int64_t n_edges, int H, int D) {
+                               const void* h_src, const void* h_dst, const float* a_src,
+                               const float* a_dst, float slope, const void* out, float* ns,
+                               const void* dout, void* dh_src, void* dh_dst, float* da_src,
+                               float* da_dst, int64_t n_dst, int64_t n_src, int64_t n_edges,
+                               int H, int D, int dtype) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(elem_ok(dtype), "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)", dtype);
   if (!gat_heads_ok(H, D)) {
     set_error("unsupported GAT shape H=%d D=%d", H, D);
     return TGX_UNSUPPORTED;
   }
-  int st = check_plan(plan, n_nodes);
+  // One gradient buffer for both roles declares one feature tensor.
+  const bool homogeneous = dh_src == dh_dst;
+  TGX_REQUIRE(!homogeneous || (h_src == h_dst && n_src == n_dst),
+              "one gradient for both roles (dh_src == dh_dst) needs one feature tensor "
+              "(h_src == h_dst) and n_src == n_dst");
+  int st = check_plan(plan, n_dst);
   if (st != TGX_OK) return st;
-  st = check_plan(plan_t, n_nodes);
+  st = check_plan(plan_t, n_src);
   if (st != TGX_OK) return st;
-  if (n_nodes == 0) return TGX_OK;
-  TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns && dout && dh && da_src && da_dst,
+  if (n_dst == 0 && n_src == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && h_src && h_dst && a_src && a_dst && out && ns && dout && dh_src &&
+                  dh_dst && da_src && da_dst,
               "null pointer");
   TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && inv_perm), "null transposed CSR");
   return guarded([&]() -> int {
     const Idx rp{row_ptr, idx_bits}, c{col, idx_bits};
     int64_t E = 0, Et = 0;
-    int s = check_csr(rp, &c, n_nodes, n_nodes, &E);
+    int s = check_csr(rp, &c, n_dst, n_src, &E);
     if (s != TGX_OK) return s;
-    TGX_REQUIRE(E == n_edges, "row_ptr[n_nodes] = %lld, expected %lld edges",
+    TGX_REQUIRE(E == n_edges, "row_ptr[n_dst] = %lld, expected %lld edges",
                 static_cast<long long>(E), static_cast<long long>(n_edges));
-    s = check_plan_rows(plan, rp, n_nodes);
+    s = check_plan_rows(plan, rp, n_dst);
     if (s != TGX_OK) return s;
-    s = check_transposed(row_ptr_t, col_t, perm, inv_perm, n_nodes, n_nodes, &Et);
+    s = check_transposed(row_ptr_t, col_t, perm, inv_perm, n_src, n_dst, &Et);
     if (s != TGX_OK) return s;
     TGX_REQUIRE(Et == E, "transposed CSR has %lld edges, expected %lld",
                 static_cast<long long>(Et), static_cast<long long>(E));
     const Idx rpt{row_ptr_t, 32};
-    s = check_plan_rows(plan_t, rpt, n_nodes);
+    s = check_plan_rows(plan_t, rpt, n_src);
     if (s != TGX_OK) return s;
     const int64_t HD = static_cast<int64_t>(H) * D;
+    const Elem el{dtype};
+    const std::vector<float> hs = widen_all(el, h_src, n_src * HD);
+    const std::vector<float> hd_own = homogeneous ? std::vector<float>()
+                                                  : widen_all(el, h_dst, n_dst * HD);
+    const float* HS = hs.data();
+    const float* HDv = homogeneous ? hs.data() : hd_own.data();
+    const std::vector<float> o32 = widen_all(el, out, n_dst * HD);
+    const std::vector<float> g32 = widen_all(el, dout, n_dst * HD);
     // B1: delta = <dout, out> per (node, head).
-    parallel_ranges(n_nodes, [&](int64_t lo, int64_t hi) {
+    parallel_ranges(n_dst, [&](int64_t lo, int64_t hi) {
       for (int64_t i = lo; i < hi; ++i)
         for (int hd = 0; hd < H; ++hd) {
           float d = 0.f;
-          for (int q = 0; q < D; ++q) d += dout[i * HD + hd * D + q] * out[i * HD + hd * D + q];
+          for (int q = 0; q < D; ++q) d += g32[i * HD + hd * D + q] * o32[i * HD + hd * D + q];
           ns[(i * H + hd) * 4 + 1] = d;
         }
     });
     // B2: source pass over the transposed CSR; dz per edge at its transposed
     // position, the source-side sums per (node, head).
-    std::vector<float> dz(static_cast<size_t>(E * H)), sdz_src(static_cast<size_t>(n_nodes * H));
+    std::vector<float> dz(static_cast<size_t>(E * H)), sdz_src(static_cast<size_t>(n_src * H));
+    std::vector<float> dhs(static_cast<size_t>(n_src * HD)), dhd(static_cast<size_t>(n_dst * HD));
     auto src_range = [&](int64_t j, int hd, int64_t k0, int64_t k1, float* dh_acc,
                          float& sdz) {
-      const float* hj = h + j * HD + hd * D;
-      const float zs = ns[(j * H + hd) * 4 + 3];
+      const float* hj = HS + j * HD + hd * D;
+      float zs = 0.f;
+      for (int q = 0; q < D; ++q) zs += a_src[hd * D + q] * hj[q];
       for (int64_t k = k0; k < k1; ++k) {
         const int64_t i = col_t[k];
         const float* n = ns + (i * H + hd) * 4;
         const float z = zs + n[2];
         const float alpha = expf(leaky(z, slope) - n[0]);
-        const float* g = dout + i * HD + hd * D;
+        const float* g = g32.data() + i * HD + hd * D;
         float dalpha = 0.f;
         for (int q = 0; q < D; ++q) dalpha += g[q] * hj[q];
         const float ds = alpha * (dalpha - n[1]);
@@ -751,7 +820,7 @@ extern "C" int tgx_cpu_gat_bwd(const void* row_ptr, const void* col, int idx_bit
       }
     };
     auto src_finish = [&](int64_t j, int hd, const float* acc, float sdz) {
-      float* o = dh + j * HD + hd * D;
+      float* o = dhs.data() + j * HD + hd * D;
       for (int q = 0; q < D; ++q) o[q] = acc[q] + sdz * a_src[hd * D + q];
       sdz_src[j * H + hd] = sdz;
     };
@@ -782,30 +851,34 @@ extern "C" int tgx_cpu_gat_bwd(const void* row_ptr, const void* col, int idx_bit
           }
         },
         [&](int64_t j) {
-          std::fill(dh + j * HD, dh + (j + 1) * HD, 0.f);
+          std::fill(dhs.begin() + j * HD, dhs.begin() + (j + 1) * HD, 0.f);
           for (int hd = 0; hd < H; ++hd) sdz_src[j * H + hd] = 0.f;
         });
-    // B3: destination pass over the CSR: dh[i] += (sum of the row's dz) a_dst,
-    // and fp64 parameter-gradient partials over fixed row blocks.
+    // B3: destination pass over the CSR: dhd[i] = (sum of the row's dz) a_dst,
+    // and fp64 parameter-gradient partials over fixed node blocks.
     constexpr int64_t kBlocks = 64;
     std::vector<double> pds(static_cast<size_t>(kBlocks * HD), 0.0), pdd(pds.size(), 0.0);
-    const int64_t per = ceil_div(n_nodes, kBlocks);
+    const int64_t per_dst = ceil_div(n_dst, kBlocks), per_src = ceil_div(n_src, kBlocks);
     parallel_ranges(kBlocks, [&](int64_t b0, int64_t b1) {
       for (int64_t b = b0; b < b1; ++b) {
         double* ps = pds.data() + b * HD;
         double* pd = pdd.data() + b * HD;
-        for (int64_t i = b * per; i < std::min(n_nodes, (b + 1) * per); ++i)
+        for (int64_t i = b * per_dst; i < std::min(n_dst, (b + 1) * per_dst); ++i)
           for (int hd = 0; hd < H; ++hd) {
             float sdz = 0.f;
             for (int64_t e = rp[i]; e < rp[i + 1]; ++e) sdz += dz[inv_perm[e] * H + hd];
-            const float* hi = h + i * HD + hd * D;
-            float* o = dh + i * HD + hd * D;
-            const double ss = sdz_src[i * H + hd];
+            const float* hi = HDv + i * HD + hd * D;
+            float* o = dhd.data() + i * HD + hd * D;
             for (int q = 0; q < D; ++q) {
-              o[q] += sdz * a_dst[hd * D + q];
+              o[q] = sdz * a_dst[hd * D + q];
               pd[hd * D + q] += static_cast<double>(sdz) * hi[q];
-              ps[hd * D + q] += ss * hi[q];
             }
+          }
+        for (int64_t j = b * per_src; j < std::min(n_src, (b + 1) * per_src); ++j)
+          for (int hd = 0; hd < H; ++hd) {
+            const double ss = sdz_src[j * H + hd];
+            const float* hj = HS + j * HD + hd * D;
+            for (int q = 0; q < D; ++q) ps[hd * D + q] += ss * hj[q];
           }
       }
     }, 1);
@@ -818,27 +891,39 @@ extern "C" int tgx_cpu_gat_bwd(const void* row_ptr, const void* col, int idx_bit
       da_src[x] = static_cast<float>(a);
       da_dst[x] = static_cast<float>(b);
     }
+    if (homogeneous) {
+      // One tensor: both roles' terms, rounded once.
+      for (size_t x = 0; x < dhs.size(); ++x) dhs[x] += dhd[x];
+      round_all(el, dhs, dh_src);
+    } else {
+      round_all(el, dhs, dh_src);
+      round_all(el, dhd, dh_dst);
+    }
     return TGX_OK;
   });
 }
 
-// ---- Dot-product attention (bf16) -----------------------------------------------
+// ---- Dot-product attention (bf16, fp16 or fp32 elements) --------------------------
 
 namespace {
 
-// Head hd of a [N, H, D] bf16 row, in fp32.
-void load_head(const uint16_t* base, int64_t node, int H, int D, int hd, float* dst) {
-  const uint16_t* p = base + (node * H + hd) * D;
-  for (int d = 0; d < D; ++d) dst[d] = bf16_to_float(p[d]);
+// Head hd of a [N, H, D] row, in fp32.
+void load_head(const Elem& el, const void* base, int64_t node, int H, int D, int hd,
+               float* dst) {
+  const int64_t o = (node * H + hd) * D;
+  for (int d = 0; d < D; ++d) dst[d] = el.get(base, o + d);
 }
+
 
 }  // namespace
 
 extern "C" int tgx_cpu_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bits,
                                     const tgx_row_plan* plan, const void* q, const void* k,
                                     const void* v, const float* bias, float scale, void* out,
-                                    float* ml, int64_t n_dst, int64_t n_src, int H, int D) {
+                                    float* ml, int64_t n_dst, int64_t n_src, int H, int D,
+                                    int dtype) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(elem_ok(dtype), "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)", dtype);
   if (!dot_heads_ok(H, D)) {
     set_error("dot attention supports H >= 1 and D in {8, 16, 32, 64, 128, 256, 512} "
               "(got H=%d D=%d)", H, D);
@@ -854,17 +939,15 @@ extern "C" int tgx_cpu_dot_attn_fwd(const void* row_ptr, const void* col, int id
     if (s != TGX_OK) return s;
     s = check_plan_rows(plan, rp, n_dst);
     if (s != TGX_OK) return s;
-    const auto* Q = static_cast<const uint16_t*>(q);
-    const auto* K = static_cast<const uint16_t*>(k);
-    const auto* V = static_cast<const uint16_t*>(v);
-    auto* O = static_cast<uint16_t*>(out);
+    const Elem el{dtype};
+    const void *Q = q, *K = k, *V = v;
     auto state = [&](int64_t i, int hd, const float* qf, int64_t e0, int64_t e1) {
       Soft st(D);
       std::vector<float> kf(static_cast<size_t>(D)), vf(static_cast<size_t>(D));
       for (int64_t e = e0; e < e1; ++e) {
         const int64_t j = c[e];
-        load_head(K, j, H, D, hd, kf.data());
-        load_head(V, j, H, D, hd, vf.data());
+        load_head(el, K, j, H, D, hd, kf.data());
+        load_head(el, V, j, H, D, hd, vf.data());
         float dotp = 0.f;
         for (int d = 0; d < D; ++d) dotp += qf[d] * kf[d];
         st.add(dotp * scale + (bias ? bias[e * H + hd] : 0.f), vf.data());
@@ -873,13 +956,13 @@ extern "C" int tgx_cpu_dot_attn_fwd(const void* row_ptr, const void* col, int id
       return st;
     };
     auto finish = [&](int64_t i, int hd, const Soft& st) {
-      uint16_t* o = O + (i * H + hd) * D;
+      const int64_t o = (i * H + hd) * D;
       if (st.l > 0.f) {
         const float inv = 1.f / st.l;
-        for (int d = 0; d < D; ++d) o[d] = float_to_bf16(st.acc[d] * inv);
+        for (int d = 0; d < D; ++d) el.put(out, o + d, st.acc[d] * inv);
         ml[(i * H + hd) * 2] = st.m + logf(st.l);
       } else {
-        std::fill(o, o + D, static_cast<uint16_t>(0));
+        for (int d = 0; d < D; ++d) el.put(out, o + d, 0.f);
         ml[(i * H + hd) * 2] = -kInf;
       }
       ml[(i * H + hd) * 2 + 1] = 0.f;
@@ -889,14 +972,14 @@ extern "C" int tgx_cpu_dot_attn_fwd(const void* row_ptr, const void* col, int id
         [&](int64_t i, int64_t e0, int64_t e1) {
           std::vector<float> qf(static_cast<size_t>(D));
           for (int hd = 0; hd < H; ++hd) {
-            load_head(Q, i, H, D, hd, qf.data());
+            load_head(el, Q, i, H, D, hd, qf.data());
             finish(i, hd, state(i, hd, qf.data(), e0, e1));
           }
         },
         [&](int64_t i, const std::vector<std::pair<int64_t, int64_t>>& chunks) {
           std::vector<float> qf(static_cast<size_t>(D));
           for (int hd = 0; hd < H; ++hd) {
-            load_head(Q, i, H, D, hd, qf.data());
+            load_head(el, Q, i, H, D, hd, qf.data());
             Soft total(D);
             for (const auto& ch : chunks) total.merge(state(i, hd, qf.data(), ch.first, ch.second));
             finish(i, hd, total);
@@ -916,8 +999,9 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
                                     const void* v, const float* bias, float scale,
                                     const void* out, float* ml, const void* dout, void* dq,
                                     void* dk, void* dv, float* dbias, int64_t n_dst,
-                                    int64_t n_src, int H, int D) {
+                                    int64_t n_src, int H, int D, int dtype) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(elem_ok(dtype), "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)", dtype);
   if (!dot_heads_ok(H, D)) {
     set_error("unsupported dot attention shape H=%d D=%d", H, D);
     return TGX_UNSUPPORTED;
@@ -943,21 +1027,15 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
     const Idx rpt{row_ptr_t, 32};
     s = check_plan_rows(plan_t, rpt, n_src);
     if (s != TGX_OK) return s;
-    const auto* Q = static_cast<const uint16_t*>(q);
-    const auto* K = static_cast<const uint16_t*>(k);
-    const auto* V = static_cast<const uint16_t*>(v);
-    const auto* Oo = static_cast<const uint16_t*>(out);
-    const auto* G = static_cast<const uint16_t*>(dout);
-    auto* DQ = static_cast<uint16_t*>(dq);
-    auto* DK = static_cast<uint16_t*>(dk);
-    auto* DV = static_cast<uint16_t*>(dv);
+    const Elem el{dtype};
+    const void *Q = q, *K = k, *V = v, *Oo = out, *G = dout;
     // B1: delta = <dout, out>.
     parallel_ranges(n_dst, [&](int64_t lo, int64_t hi) {
       std::vector<float> a(static_cast<size_t>(D)), b(static_cast<size_t>(D));
       for (int64_t i = lo; i < hi; ++i)
         for (int hd = 0; hd < H; ++hd) {
-          load_head(G, i, H, D, hd, a.data());
-          load_head(Oo, i, H, D, hd, b.data());
+          load_head(el, G, i, H, D, hd, a.data());
+          load_head(el, Oo, i, H, D, hd, b.data());
           float d = 0.f;
           for (int x = 0; x < D; ++x) d += a[x] * b[x];
           ml[(i * H + hd) * 2 + 1] = d;
@@ -970,8 +1048,8 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
       std::vector<float> kf(static_cast<size_t>(D)), vf(static_cast<size_t>(D));
       for (int64_t e = e0; e < e1; ++e) {
         const int64_t j = c[e];
-        load_head(K, j, H, D, hd, kf.data());
-        load_head(V, j, H, D, hd, vf.data());
+        load_head(el, K, j, H, D, hd, kf.data());
+        load_head(el, V, j, H, D, hd, vf.data());
         float sp = 0.f, dp = 0.f;
         for (int x = 0; x < D; ++x) {
           sp += qf[x] * kf[x];
@@ -984,16 +1062,16 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
       }
     };
     auto dq_store = [&](int64_t i, int hd, const float* acc) {
-      uint16_t* o = DQ + (i * H + hd) * D;
-      for (int x = 0; x < D; ++x) o[x] = float_to_bf16(acc[x] * scale);
+      const int64_t o = (i * H + hd) * D;
+      for (int x = 0; x < D; ++x) el.put(dq, o + x, acc[x] * scale);
     };
     walk_plan(
         *plan, rp,
         [&](int64_t i, int64_t e0, int64_t e1) {
           std::vector<float> qf(D), gf(D), acc(D);
           for (int hd = 0; hd < H; ++hd) {
-            load_head(Q, i, H, D, hd, qf.data());
-            load_head(G, i, H, D, hd, gf.data());
+            load_head(el, Q, i, H, D, hd, qf.data());
+            load_head(el, G, i, H, D, hd, gf.data());
             std::fill(acc.begin(), acc.end(), 0.f);
             dst_range(i, hd, qf.data(), gf.data(), e0, e1, acc.data());
             dq_store(i, hd, acc.data());
@@ -1002,8 +1080,8 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
         [&](int64_t i, const std::vector<std::pair<int64_t, int64_t>>& chunks) {
           std::vector<float> qf(D), gf(D), acc(D), part(D);
           for (int hd = 0; hd < H; ++hd) {
-            load_head(Q, i, H, D, hd, qf.data());
-            load_head(G, i, H, D, hd, gf.data());
+            load_head(el, Q, i, H, D, hd, qf.data());
+            load_head(el, G, i, H, D, hd, gf.data());
             std::fill(acc.begin(), acc.end(), 0.f);
             for (const auto& ch : chunks) {
               std::fill(part.begin(), part.end(), 0.f);
@@ -1014,7 +1092,7 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
           }
         },
         [&](int64_t i) {
-          std::fill(DQ + i * H * D, DQ + (i + 1) * H * D, static_cast<uint16_t>(0));
+          for (int64_t x = i * H * D; x < (i + 1) * H * D; ++x) el.put(dq, x, 0.f);
         });
     if (n_src == 0) return TGX_OK;
     // B3: source pass over the transposed CSR: dk = scale * sum ds q, dv = sum alpha dout.
@@ -1023,8 +1101,8 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
       std::vector<float> qf(static_cast<size_t>(D)), gf(static_cast<size_t>(D));
       for (int64_t t = k0; t < k1; ++t) {
         const int64_t i = col_t[t], e = perm[t];
-        load_head(Q, i, H, D, hd, qf.data());
-        load_head(G, i, H, D, hd, gf.data());
+        load_head(el, Q, i, H, D, hd, qf.data());
+        load_head(el, G, i, H, D, hd, gf.data());
         float sp = 0.f, dp = 0.f;
         for (int x = 0; x < D; ++x) {
           sp += qf[x] * kf[x];
@@ -1040,11 +1118,10 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
       }
     };
     auto kv_store = [&](int64_t j, int hd, const float* ak, const float* av) {
-      uint16_t* ok = DK + (j * H + hd) * D;
-      uint16_t* ov = DV + (j * H + hd) * D;
+      const int64_t o = (j * H + hd) * D;
       for (int x = 0; x < D; ++x) {
-        ok[x] = float_to_bf16(ak[x] * scale);
-        ov[x] = float_to_bf16(av[x]);
+        el.put(dk, o + x, ak[x] * scale);
+        el.put(dv, o + x, av[x]);
       }
     };
     walk_plan(
@@ -1052,8 +1129,8 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
         [&](int64_t j, int64_t k0, int64_t k1) {
           std::vector<float> kf(D), vf(D), ak(D), av(D);
           for (int hd = 0; hd < H; ++hd) {
-            load_head(K, j, H, D, hd, kf.data());
-            load_head(V, j, H, D, hd, vf.data());
+            load_head(el, K, j, H, D, hd, kf.data());
+            load_head(el, V, j, H, D, hd, vf.data());
             std::fill(ak.begin(), ak.end(), 0.f);
             std::fill(av.begin(), av.end(), 0.f);
             src_range(hd, kf.data(), vf.data(), k0, k1, ak.data(), av.data());
@@ -1063,8 +1140,8 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
         [&](int64_t j, const std::vector<std::pair<int64_t, int64_t>>& chunks) {
           std::vector<float> kf(D), vf(D), ak(D), av(D), pk(D), pv(D);
           for (int hd = 0; hd < H; ++hd) {
-            load_head(K, j, H, D, hd, kf.data());
-            load_head(V, j, H, D, hd, vf.data());
+            load_head(el, K, j, H, D, hd, kf.data());
+            load_head(el, V, j, H, D, hd, vf.data());
             std::fill(ak.begin(), ak.end(), 0.f);
             std::fill(av.begin(), av.end(), 0.f);
             for (const auto& ch : chunks) {
@@ -1080,8 +1157,10 @@ extern "C" int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int id
           }
         },
         [&](int64_t j) {
-          std::fill(DK + j * H * D, DK + (j + 1) * H * D, static_cast<uint16_t>(0));
-          std::fill(DV + j * H * D, DV + (j + 1) * H * D, static_cast<uint16_t>(0));
+          for (int64_t x = j * H * D; x < (j + 1) * H * D; ++x) {
+            el.put(dk, x, 0.f);
+            el.put(dv, x, 0.f);
+          }
         });
     return TGX_OK;
   });

@@ -32,19 +32,15 @@
 #include "tgx_profile.h"
 #include "tgx_softmax.h"
 #include "tgx_tasks.h"
+#include "tgx_vals.h"
 
 namespace tgx {
 namespace {
 
-__device__ __forceinline__ u32x4 ldv(const uint16_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
-__device__ __forceinline__ void stv(uint16_t* p, u32x4 v) {
-  *reinterpret_cast<u32x4*>(p) = v;
-}
-__device__ __forceinline__ float dot8(const float (&a)[8], u32x4 b) {
+template <class V>
+__device__ __forceinline__ float dot8(const float (&a)[8], typename V::Raw b) {
   float f[8];
-  unpack8(b, f);
+  V::unpack(b, f);
   float s = 0.f;
 #pragma unroll
   for (int q = 0; q < 8; ++q) s += a[q] * f[q];
@@ -78,17 +74,18 @@ __device__ __forceinline__ void fold_groups(float (&v)[8]) {
 // ---------------------------------------------------------------------------
 // Forward
 
-template <typename I>
+template <int DT, typename I>
 struct DotFwdArgs {
+  using T = typename Vals<DT, 8>::T;
   const I* row_ptr;
   const I* col;
   PlanView plan;
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
+  const T* q;
+  const T* k;
+  const T* v;
   const float* bias;  // [E, H] or null
   float scale;
-  uint16_t* out;
+  T* out;
   float* ml;          // [N, H, 2]
   float* partial;     // per chunk: acc[8G] | m[H] | l[H]
   int64_t ld;         // values between consecutive nodes' rows of q, k, v, out
@@ -96,8 +93,9 @@ struct DotFwdArgs {
   int64_t bld;        // floats between consecutive edges' rows of bias
 };
 
-template <typename I, int G, int HL, int U>
-__global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
+template <int DT, typename I, int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<DT, I> a) {
+  using V = Vals<DT, 8>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 8 * G;
   constexpr int H = G / HL;
@@ -112,7 +110,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
     for (int r = 0; r < t.n_empty; ++r) {
       const int64_t i = uniform(a.plan.rows[t.empty0 + r]);
       if (g == 0) {
-        stv(a.out + i * a.ld + 8 * c, u32x4{0u, 0u, 0u, 0u});
+        V::store_zero(a.out + i * a.ld + 8 * c);
         if (head_lead) {
           a.ml[i * a.mld + hd * 2] = kNegInf;
           a.ml[i * a.mld + hd * 2 + 1] = 0.f;
@@ -123,21 +121,21 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
   }
   const int64_t row = t.row;
   float qf[8];
-  unpack8(ldv(a.q + row * a.ld + 8 * c), qf);
+  V::unpack(V::load(a.q + row * a.ld + 8 * c), qf);
   SoftState<8> st;
   st.init();
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
     const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
     const int my_col = lane < n ? static_cast<int>(a.col[base + lane]) : 0;
     for (int k = 0; k < n; k += EPW * U) {
-      u32x4 kk[U], vv[U];
+      typename V::Raw kk[U], vv[U];
       float bb[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
-        kk[u] = ldv(a.k + static_cast<int64_t>(j) * a.ld + 8 * c);
-        vv[u] = ldv(a.v + static_cast<int64_t>(j) * a.ld + 8 * c);
+        kk[u] = V::load(a.k + static_cast<int64_t>(j) * a.ld + 8 * c);
+        vv[u] = V::load(a.v + static_cast<int64_t>(j) * a.ld + 8 * c);
         bb[u] = (a.bias && slot < n) ? a.bias[(base + slot) * a.bld + hd] : 0.f;
       }
       float s[U];
@@ -145,7 +143,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
-        const float sc = group_sum<HL>(dot8(qf, kk[u])) * a.scale + bb[u];
+        const float sc = group_sum<HL>(dot8<V>(qf, kk[u])) * a.scale + bb[u];
         s[u] = slot < n ? sc : kNegInf;
         mc = fmaxf(mc, s[u]);
       }
@@ -155,7 +153,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
         const float p = s[u] == kNegInf ? 0.f : fast_exp(s[u] - st.m);
         st.l += p;
         float vf[8];
-        unpack8(vv[u], vf);
+        V::unpack(vv[u], vf);
 #pragma unroll
         for (int q = 0; q < 8; ++q) st.acc[q] += p * vf[q];
       }
@@ -177,17 +175,18 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_kernel(DotFwdArgs<I> a) {
   float o[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) o[q] = st.acc[q] * inv;
-  stv(a.out + row * a.ld + 8 * c, pack8(o));
+  V::store(a.out + row * a.ld + 8 * c, o);
   if (head_lead) {
     a.ml[row * a.mld + hd * 2] = st.m + __logf(st.l);
     a.ml[row * a.mld + hd * 2 + 1] = 0.f;
   }
 }
 
-template <int G, int HL>
+template <int DT, int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
-    PlanView plan, const float* __restrict__ partial, uint16_t* __restrict__ out,
+    PlanView plan, const float* __restrict__ partial, typename Vals<DT, 8>::T* __restrict__ out,
     float* __restrict__ ml, int64_t ld, int64_t mld) {
+  using V = Vals<DT, 8>;
   constexpr int HD = 8 * G;
   constexpr int H = G / HL;
   const int64_t k = global_wave();
@@ -209,7 +208,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
   float o[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) o[q] = st.acc[q] * inv;
-  stv(out + row * ld + 8 * c, pack8(o));
+  V::store(out + row * ld + 8 * c, o);
   if (c % HL == 0) {
     ml[row * mld + hd * 2] = st.m + __logf(st.l);
     ml[row * mld + hd * 2 + 1] = 0.f;
@@ -219,34 +218,36 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
 // ---------------------------------------------------------------------------
 // Backward
 
-template <int G, int HL>
+template <int DT, int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void dot_delta_kernel(
-    const uint16_t* __restrict__ dout, const uint16_t* __restrict__ out,
+    const typename Vals<DT, 8>::T* __restrict__ dout, const typename Vals<DT, 8>::T* __restrict__ out,
     float* __restrict__ ml, int64_t n_nodes, int64_t ld, int64_t mld) {
+  using V = Vals<DT, 8>;
   constexpr int EPW = kWave / G;
   const int lane = lane_id();
   const int c = lane % G, hd = c / HL;
   const int64_t node = global_wave() * EPW + lane / G;
   if (node >= n_nodes) return;
   float d[8];
-  unpack8(ldv(dout + node * ld + 8 * c), d);
-  const float delta = group_sum<HL>(dot8(d, ldv(out + node * ld + 8 * c)));
+  V::unpack(V::load(dout + node * ld + 8 * c), d);
+  const float delta = group_sum<HL>(dot8<V>(d, V::load(out + node * ld + 8 * c)));
   if (c % HL == 0) ml[node * mld + hd * 2 + 1] = delta;
 }
 
-template <typename I>
+template <int DT, typename I>
 struct DotDstArgs {
+  using T = typename Vals<DT, 8>::T;
   const I* row_ptr;
   const I* col;
   PlanView plan;
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
+  const T* q;
+  const T* k;
+  const T* v;
   const float* bias;
   float scale;
   const float* ml;
-  const uint16_t* dout;
-  uint16_t* dq;
+  const T* dout;
+  T* dq;
   float* dbias;     // [E, H] or null
   float* partial;   // per chunk: [8G] unscaled dq
   int64_t ld;       // values between consecutive nodes' rows of q, k, v, dout, dq
@@ -254,8 +255,9 @@ struct DotDstArgs {
   int64_t bld;      // floats between consecutive edges' rows of bias and dbias
 };
 
-template <typename I, int G, int HL, int U>
-__global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a) {
+template <int DT, typename I, int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<DT, I> a) {
+  using V = Vals<DT, 8>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 8 * G;
   const Task t = decode_task(a.plan, a.row_ptr, global_wave());
@@ -268,14 +270,14 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a
   if (t.kind == kTaskEmpty) {
     for (int r = 0; r < t.n_empty; ++r) {
       const int64_t i = uniform(a.plan.rows[t.empty0 + r]);
-      if (g == 0) stv(a.dq + i * a.ld + 8 * c, u32x4{0u, 0u, 0u, 0u});
+      if (g == 0) V::store_zero(a.dq + i * a.ld + 8 * c);
     }
     return;
   }
   const int64_t row = t.row;
   float qf[8], df[8];
-  unpack8(ldv(a.q + row * a.ld + 8 * c), qf);
-  unpack8(ldv(a.dout + row * a.ld + 8 * c), df);
+  V::unpack(V::load(a.q + row * a.ld + 8 * c), qf);
+  V::unpack(V::load(a.dout + row * a.ld + 8 * c), df);
   const float lse = a.ml[row * a.mld + hd * 2];
   const float delta = a.ml[row * a.mld + hd * 2 + 1];
   float dq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -283,27 +285,27 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a
     const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
     const int my_col = lane < n ? static_cast<int>(a.col[base + lane]) : 0;
     for (int k = 0; k < n; k += EPW * U) {
-      u32x4 kk[U], vv[U];
+      typename V::Raw kk[U], vv[U];
       float bb[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
-        kk[u] = ldv(a.k + static_cast<int64_t>(j) * a.ld + 8 * c);
-        vv[u] = ldv(a.v + static_cast<int64_t>(j) * a.ld + 8 * c);
+        kk[u] = V::load(a.k + static_cast<int64_t>(j) * a.ld + 8 * c);
+        vv[u] = V::load(a.v + static_cast<int64_t>(j) * a.ld + 8 * c);
         bb[u] = (a.bias && slot < n) ? a.bias[(base + slot) * a.bld + hd] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const bool valid = slot < n;
-        const float s = group_sum<HL>(dot8(qf, kk[u])) * a.scale + bb[u];
+        const float s = group_sum<HL>(dot8<V>(qf, kk[u])) * a.scale + bb[u];
         const float alpha = valid ? fast_exp(s - lse) : 0.f;
-        const float dalpha = group_sum<HL>(dot8(df, vv[u]));
+        const float dalpha = group_sum<HL>(dot8<V>(df, vv[u]));
         const float ds = alpha * (dalpha - delta);
         if (a.dbias && valid && head_lead) a.dbias[(base + slot) * a.bld + hd] = ds;
         float kf[8];
-        unpack8(kk[u], kf);
+        V::unpack(kk[u], kf);
 #pragma unroll
         for (int q = 0; q < 8; ++q) dq[q] += ds * kf[q];
       }
@@ -317,13 +319,14 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<I> a
   }
 #pragma unroll
   for (int q = 0; q < 8; ++q) dq[q] *= a.scale;
-  stv(a.dq + row * a.ld + 8 * c, pack8(dq));
+  V::store(a.dq + row * a.ld + 8 * c, dq);
 }
 
-template <int G>
+template <int DT, int G>
 __global__ __launch_bounds__(kTaskBlock) void dot_dq_merge_kernel(
-    PlanView plan, const float* __restrict__ partial, float scale, uint16_t* __restrict__ dq,
-    int64_t ld) {
+    PlanView plan, const float* __restrict__ partial, float scale,
+    typename Vals<DT, 8>::T* __restrict__ dq, int64_t ld) {
+  using V = Vals<DT, 8>;
   constexpr int HD = 8 * G;
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
@@ -340,31 +343,34 @@ __global__ __launch_bounds__(kTaskBlock) void dot_dq_merge_kernel(
   }
 #pragma unroll
   for (int r = 0; r < 8; ++r) s[r] *= scale;
-  stv(dq + row * ld + 8 * c, pack8(s));
+  V::store(dq + row * ld + 8 * c, s);
 }
 
+template <int DT>
 struct DotSrcArgs {
+  using T = typename Vals<DT, 8>::T;
   const int32_t* row_ptr_t;
   const int32_t* col_t;
   const int32_t* perm;
   PlanView plan;
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
+  const T* q;
+  const T* k;
+  const T* v;
   const float* bias;
   float scale;
   const float* ml;
-  const uint16_t* dout;
-  uint16_t* dk;
-  uint16_t* dv;
+  const T* dout;
+  T* dk;
+  T* dv;
   float* partial;   // per chunk: [8G] unscaled dk | [8G] dv
   int64_t ld;       // values between consecutive nodes' rows of q, k, v, dout, dk, dv
   int64_t mld;      // floats between consecutive nodes' rows of ml
   int64_t bld;      // floats between consecutive edges' rows of bias
 };
 
-template <int G, int HL, int U>
-__global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
+template <int DT, int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs<DT> a) {
+  using V = Vals<DT, 8>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 8 * G;
   const Task t = decode_task(a.plan, a.row_ptr_t, global_wave());
@@ -377,16 +383,16 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
     for (int r = 0; r < t.n_empty; ++r) {
       const int64_t j = uniform(a.plan.rows[t.empty0 + r]);
       if (g == 0) {
-        stv(a.dk + j * a.ld + 8 * c, u32x4{0u, 0u, 0u, 0u});
-        stv(a.dv + j * a.ld + 8 * c, u32x4{0u, 0u, 0u, 0u});
+        V::store_zero(a.dk + j * a.ld + 8 * c);
+        V::store_zero(a.dv + j * a.ld + 8 * c);
       }
     }
     return;
   }
   const int64_t j = t.row;
   float kf[8], vf[8];
-  unpack8(ldv(a.k + j * a.ld + 8 * c), kf);
-  unpack8(ldv(a.v + j * a.ld + 8 * c), vf);
+  V::unpack(V::load(a.k + j * a.ld + 8 * c), kf);
+  V::unpack(V::load(a.v + j * a.ld + 8 * c), vf);
   float dk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float dv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
@@ -397,7 +403,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
       my_e = a.perm[base + lane];
     }
     for (int k = 0; k < n; k += EPW * U) {
-      u32x4 qq[U], dd[U];
+      typename V::Raw qq[U], dd[U];
       float bb[U], lse[U], dl[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -405,8 +411,8 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
         const int src = slot < n ? slot : 0;
         const int64_t i = fetch_lane<EPW>(my_i, src);
         const int64_t e = fetch_lane<EPW>(my_e, src);
-        qq[u] = ldv(a.q + i * a.ld + 8 * c);
-        dd[u] = ldv(a.dout + i * a.ld + 8 * c);
+        qq[u] = V::load(a.q + i * a.ld + 8 * c);
+        dd[u] = V::load(a.dout + i * a.ld + 8 * c);
         lse[u] = a.ml[i * a.mld + hd * 2];
         dl[u] = a.ml[i * a.mld + hd * 2 + 1];
         bb[u] = a.bias ? a.bias[e * a.bld + hd] : 0.f;
@@ -416,8 +422,8 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
         const int slot = k + u * EPW + g;
         const bool valid = slot < n;
         float qf[8], df[8];
-        unpack8(qq[u], qf);
-        unpack8(dd[u], df);
+        V::unpack(qq[u], qf);
+        V::unpack(dd[u], df);
         float sp = 0.f, dp = 0.f;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -446,14 +452,16 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs a) {
   }
 #pragma unroll
   for (int q = 0; q < 8; ++q) dk[q] *= a.scale;
-  stv(a.dk + j * a.ld + 8 * c, pack8(dk));
-  stv(a.dv + j * a.ld + 8 * c, pack8(dv));
+  V::store(a.dk + j * a.ld + 8 * c, dk);
+  V::store(a.dv + j * a.ld + 8 * c, dv);
 }
 
-template <int G>
+template <int DT, int G>
 __global__ __launch_bounds__(kTaskBlock) void dot_kv_merge_kernel(
-    PlanView plan, const float* __restrict__ partial, float scale, uint16_t* __restrict__ dk,
-    uint16_t* __restrict__ dv, int64_t ld) {
+    PlanView plan, const float* __restrict__ partial, float scale,
+    typename Vals<DT, 8>::T* __restrict__ dk, typename Vals<DT, 8>::T* __restrict__ dv,
+    int64_t ld) {
+  using V = Vals<DT, 8>;
   constexpr int HD = 8 * G;
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
@@ -475,8 +483,8 @@ __global__ __launch_bounds__(kTaskBlock) void dot_kv_merge_kernel(
   }
 #pragma unroll
   for (int r = 0; r < 8; ++r) sk[r] *= scale;
-  stv(dk + row * ld + 8 * c, pack8(sk));
-  stv(dv + row * ld + 8 * c, pack8(sv));
+  V::store(dk + row * ld + 8 * c, sk);
+  V::store(dv + row * ld + 8 * c, sv);
 }
 
 // ---------------------------------------------------------------------------
@@ -513,19 +521,20 @@ constexpr int dot_unroll() {
   return G == 32 ? 1 : 2;
 }
 
-template <typename I, int G, int HL>
-int dot_fwd_launch(const DotFwdArgs<I>& a, hipStream_t s) {
+template <int DT, typename I, int G, int HL>
+int dot_fwd_launch(const DotFwdArgs<DT, I>& a, hipStream_t s) {
   constexpr int U = dot_unroll<G>();
   const int64_t waves = plan_waves(a.plan);
   if (waves > 0) {
     TGX_PROFILE("dot_fwd_kernel", s);
-    dot_fwd_kernel<I, G, HL, U><<<ceil_div(waves, kWavesPerBlock), kTaskBlock, 0, s>>>(a);
+    dot_fwd_kernel<DT, I, G, HL, U><<<ceil_div(waves, kWavesPerBlock), kTaskBlock, 0, s>>>(a);
     TGX_LAUNCHED("dot_fwd_kernel");
   }
   if (a.plan.n_split > 0) {
     TGX_PROFILE("dot_fwd_merge_kernel", s);
-    dot_fwd_merge_kernel<G, HL><<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        a.plan, a.partial, a.out, a.ml, a.ld, a.mld);
+    dot_fwd_merge_kernel<DT, G, HL>
+        <<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(a.plan, a.partial, a.out,
+                                                                          a.ml, a.ld, a.mld);
     TGX_LAUNCHED("dot_fwd_merge_kernel");
   }
   return TGX_OK;
@@ -545,40 +554,138 @@ DotBwdLayout dot_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t
   return L;
 }
 
-template <typename I, int G, int HL>
-int dot_bwd_launch(const DotDstArgs<I>& da, DotSrcArgs sa, const uint16_t* out,
-                   float* ml, int64_t n_nodes, hipStream_t s) {
+template <int DT, typename I, int G, int HL>
+int dot_bwd_launch(const DotDstArgs<DT, I>& da, const DotSrcArgs<DT>& sa,
+                   const typename Vals<DT, 8>::T* out, float* ml, int64_t n_nodes,
+                   hipStream_t s) {
   constexpr int U = dot_unroll<G>();
   constexpr int EPW = kWave / G;
   {
     TGX_PROFILE("dot_delta_kernel", s);
-    dot_delta_kernel<G, HL><<<ceil_div(ceil_div(n_nodes, EPW), kWavesPerBlock), kTaskBlock, 0,
-                              s>>>(da.dout, out, ml, n_nodes, da.ld, da.mld);
+    dot_delta_kernel<DT, G, HL><<<ceil_div(ceil_div(n_nodes, EPW), kWavesPerBlock), kTaskBlock, 0,
+                                  s>>>(da.dout, out, ml, n_nodes, da.ld, da.mld);
     TGX_LAUNCHED("dot_delta_kernel");
   }
   const int64_t dst_waves = plan_waves(da.plan);
   if (dst_waves > 0) {
     TGX_PROFILE("dot_bwd_dst_kernel", s);
-    dot_bwd_dst_kernel<I, G, HL, U><<<ceil_div(dst_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(da);
+    dot_bwd_dst_kernel<DT, I, G, HL, U>
+        <<<ceil_div(dst_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(da);
     TGX_LAUNCHED("dot_bwd_dst_kernel");
   }
   if (da.plan.n_split > 0) {
     TGX_PROFILE("dot_dq_merge_kernel", s);
-    dot_dq_merge_kernel<G><<<ceil_div(da.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+    dot_dq_merge_kernel<DT, G><<<ceil_div(da.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
         da.plan, da.partial, da.scale, da.dq, da.ld);
     TGX_LAUNCHED("dot_dq_merge_kernel");
   }
   const int64_t src_waves = plan_waves(sa.plan);
   if (src_waves > 0) {
     TGX_PROFILE("dot_bwd_src_kernel", s);
-    dot_bwd_src_kernel<G, HL, U><<<ceil_div(src_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
+    dot_bwd_src_kernel<DT, G, HL, U>
+        <<<ceil_div(src_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
     TGX_LAUNCHED("dot_bwd_src_kernel");
   }
   if (sa.plan.n_split > 0) {
     TGX_PROFILE("dot_kv_merge_kernel", s);
-    dot_kv_merge_kernel<G><<<ceil_div(sa.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+    dot_kv_merge_kernel<DT, G><<<ceil_div(sa.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
         sa.plan, sa.partial, sa.scale, sa.dk, sa.dv, sa.ld);
     TGX_LAUNCHED("dot_kv_merge_kernel");
+  }
+  return TGX_OK;
+}
+
+// One element format's forward over every head group.
+template <int DT>
+int dot_fwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_row_plan* plan,
+                  const void* q, const void* k, const void* v, const float* bias, float scale,
+                  void* out, float* ml, int H, int D, float* partial, hipStream_t s) {
+  using T = typename Vals<DT, 8>::T;
+  const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
+  for (int h0 = 0; h0 < H;) {
+    const int hg = dot_group_heads(H, D, h0);
+    const DotShape shp = dot_shape(hg, D);
+    const int64_t off = static_cast<int64_t>(h0) * D;
+    const T* qq = static_cast<const T*>(q) + off;
+    const T* kk = k ? static_cast<const T*>(k) + off : nullptr;
+    const T* vv = v ? static_cast<const T*>(v) + off : nullptr;
+    T* oo = static_cast<T*>(out) + off;
+    const float* bb = bias ? bias + h0 : nullptr;
+    float* mm = ml + 2 * h0;
+    int st = TGX_UNSUPPORTED;
+#define TGX_DOT_FWD(GG, HH)                                                                  \
+    if (shp.G == GG && shp.HL == HH) {                                                       \
+      if (idx_bits == 32)                                                                    \
+        st = dot_fwd_launch<DT, int32_t, GG, HH>(                                            \
+            DotFwdArgs<DT, int32_t>{static_cast<const int32_t*>(row_ptr),                    \
+                                    static_cast<const int32_t*>(col), plan_view(*plan), qq,  \
+                                    kk, vv, bb, scale, oo, mm, partial, ld, mld, bld},       \
+            s);                                                                              \
+      else                                                                                   \
+        st = dot_fwd_launch<DT, int64_t, GG, HH>(                                            \
+            DotFwdArgs<DT, int64_t>{static_cast<const int64_t*>(row_ptr),                    \
+                                    static_cast<const int64_t*>(col), plan_view(*plan), qq,  \
+                                    kk, vv, bb, scale, oo, mm, partial, ld, mld, bld},       \
+            s);                                                                              \
+    } else
+    TGX_DOT_SHAPES(TGX_DOT_FWD)
+    set_error("unsupported dot attention head group G=%d HL=%d", shp.G, shp.HL);
+#undef TGX_DOT_FWD
+    if (st != TGX_OK) return st;
+    h0 += hg;
+  }
+  return TGX_OK;
+}
+
+// One element format's backward over every head group.
+template <int DT>
+int dot_bwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_row_plan* plan,
+                  const int32_t* row_ptr_t, const int32_t* col_t, const int32_t* perm,
+                  const tgx_row_plan* plan_t, const void* q, const void* k, const void* v,
+                  const float* bias, float scale, const void* out, float* ml, const void* dout,
+                  void* dq, void* dk, void* dv, float* dbias, int64_t n_dst, int H, int D,
+                  float* dst_part, float* src_part, hipStream_t s) {
+  using T = typename Vals<DT, 8>::T;
+  const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
+  auto at = [](const void* p, int64_t off) {
+    return p ? static_cast<const T*>(p) + off : nullptr;
+  };
+  auto at_mut = [](void* p, int64_t off) { return p ? static_cast<T*>(p) + off : nullptr; };
+  for (int h0 = 0; h0 < H;) {
+    const int hg = dot_group_heads(H, D, h0);
+    const DotShape shp = dot_shape(hg, D);
+    const int64_t off = static_cast<int64_t>(h0) * D;
+    const T *qq = at(q, off), *kk = at(k, off), *vv = at(v, off), *oo = at(out, off),
+            *gg = at(dout, off);
+    T *dqq = at_mut(dq, off), *dkk = at_mut(dk, off), *dvv = at_mut(dv, off);
+    const float* bb = bias ? bias + h0 : nullptr;
+    float* dbb = dbias ? dbias + h0 : nullptr;
+    float* mm = ml + 2 * h0;
+    const DotSrcArgs<DT> sa{row_ptr_t, col_t, perm, plan_view(*plan_t), qq, kk, vv, bb, scale,
+                            mm, gg, dkk, dvv, src_part, ld, mld, bld};
+    int st = TGX_UNSUPPORTED;
+#define TGX_DOT_BWD(GG, HH)                                                                   \
+    if (shp.G == GG && shp.HL == HH) {                                                        \
+      if (idx_bits == 32)                                                                     \
+        st = dot_bwd_launch<DT, int32_t, GG, HH>(                                             \
+            DotDstArgs<DT, int32_t>{static_cast<const int32_t*>(row_ptr),                     \
+                                    static_cast<const int32_t*>(col), plan_view(*plan), qq,   \
+                                    kk, vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld,   \
+                                    bld},                                                     \
+            sa, oo, mm, n_dst, s);                                                            \
+      else                                                                                    \
+        st = dot_bwd_launch<DT, int64_t, GG, HH>(                                             \
+            DotDstArgs<DT, int64_t>{static_cast<const int64_t*>(row_ptr),                     \
+                                    static_cast<const int64_t*>(col), plan_view(*plan), qq,   \
+                                    kk, vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld,   \
+                                    bld},                                                     \
+            sa, oo, mm, n_dst, s);                                                            \
+    } else
+    TGX_DOT_SHAPES(TGX_DOT_BWD)
+    set_error("unsupported dot attention head group G=%d HL=%d", shp.G, shp.HL);
+#undef TGX_DOT_BWD
+    if (st != TGX_OK) return st;
+    h0 += hg;
   }
   return TGX_OK;
 }
@@ -592,8 +699,10 @@ extern "C" int tgx_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bi
                                 const tgx_row_plan* plan, const void* q, const void* k,
                                 const void* v, const float* bias, float scale, void* out,
                                 float* ml, int64_t n_dst, int64_t n_src, int H, int D,
-                                float* partial, void* stream) {
+                                int dtype, float* partial, void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(dtype_bytes(dtype) != 0, "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)",
+              dtype);
   if (!dot_heads_ok(H, D)) {
     set_error("dot attention supports H >= 1 and D in {8, 16, 32, 64, 128, 256, 512} "
               "(got H=%d D=%d)", H, D);
@@ -607,40 +716,17 @@ extern "C" int tgx_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bi
   // Gathered row indices are held in 32 bits.
   TGX_REQUIRE(n_src < (int64_t{1} << 31), "source tables need fewer than 2^31 rows");
   hipStream_t s = as_stream(stream);
-  const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
-  for (int h0 = 0; h0 < H;) {
-    const int hg = dot_group_heads(H, D, h0);
-    const DotShape shp = dot_shape(hg, D);
-    const int64_t off = static_cast<int64_t>(h0) * D;
-    const auto* qq = static_cast<const uint16_t*>(q) + off;
-    const auto* kk = k ? static_cast<const uint16_t*>(k) + off : nullptr;
-    const auto* vv = v ? static_cast<const uint16_t*>(v) + off : nullptr;
-    auto* oo = static_cast<uint16_t*>(out) + off;
-    const float* bb = bias ? bias + h0 : nullptr;
-    float* mm = ml + 2 * h0;
-    st = TGX_UNSUPPORTED;
-#define TGX_DOT_FWD(GG, HH)                                                                  \
-    if (shp.G == GG && shp.HL == HH) {                                                       \
-      if (idx_bits == 32)                                                                    \
-        st = dot_fwd_launch<int32_t, GG, HH>(                                                \
-            DotFwdArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                        \
-                                static_cast<const int32_t*>(col), plan_view(*plan), qq, kk,  \
-                                vv, bb, scale, oo, mm, partial, ld, mld, bld},               \
-            s);                                                                              \
-      else                                                                                   \
-        st = dot_fwd_launch<int64_t, GG, HH>(                                                \
-            DotFwdArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                        \
-                                static_cast<const int64_t*>(col), plan_view(*plan), qq, kk,  \
-                                vv, bb, scale, oo, mm, partial, ld, mld, bld},               \
-            s);                                                                              \
-    } else
-    TGX_DOT_SHAPES(TGX_DOT_FWD)
-    set_error("unsupported dot attention head group G=%d HL=%d", shp.G, shp.HL);
-#undef TGX_DOT_FWD
-    if (st != TGX_OK) return st;
-    h0 += hg;
+  switch (dtype) {
+    case TGX_DTYPE_BF16:
+      return dot_fwd_dtype<TGX_DTYPE_BF16>(row_ptr, col, idx_bits, plan, q, k, v, bias, scale,
+                                           out, ml, H, D, partial, s);
+    case TGX_DTYPE_F16:
+      return dot_fwd_dtype<TGX_DTYPE_F16>(row_ptr, col, idx_bits, plan, q, k, v, bias, scale,
+                                          out, ml, H, D, partial, s);
+    default:
+      return dot_fwd_dtype<TGX_DTYPE_F32>(row_ptr, col, idx_bits, plan, q, k, v, bias, scale,
+                                          out, ml, H, D, partial, s);
   }
-  return TGX_OK;
 }
 
 extern "C" int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
@@ -663,8 +749,10 @@ extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bi
                                 const void* v, const float* bias, float scale, const void* out,
                                 float* ml, const void* dout, void* dq, void* dk, void* dv,
                                 float* dbias, int64_t n_dst, int64_t n_src, int H, int D,
-                                void* ws, size_t ws_bytes, void* stream) {
+                                int dtype, void* ws, size_t ws_bytes, void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(dtype_bytes(dtype) != 0, "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)",
+              dtype);
   if (!dot_heads_ok(H, D)) {
     set_error("unsupported dot attention shape H=%d D=%d", H, D);
     return TGX_UNSUPPORTED;
@@ -682,48 +770,20 @@ extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bi
   char* w = static_cast<char*>(ws);
   float* dst_part = reinterpret_cast<float*>(w + L.dst_part_off);
   float* src_part = reinterpret_cast<float*>(w + L.src_part_off);
-  const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
-  auto at = [](const void* p, int64_t off) {
-    return p ? static_cast<const uint16_t*>(p) + off : nullptr;
-  };
-  auto at_mut = [](void* p, int64_t off) {
-    return p ? static_cast<uint16_t*>(p) + off : nullptr;
-  };
-  for (int h0 = 0; h0 < H;) {
-    const int hg = dot_group_heads(H, D, h0);
-    const DotShape shp = dot_shape(hg, D);
-    const int64_t off = static_cast<int64_t>(h0) * D;
-    const uint16_t *qq = at(q, off), *kk = at(k, off), *vv = at(v, off), *oo = at(out, off),
-                   *gg = at(dout, off);
-    uint16_t *dqq = at_mut(dq, off), *dkk = at_mut(dk, off), *dvv = at_mut(dv, off);
-    const float* bb = bias ? bias + h0 : nullptr;
-    float* dbb = dbias ? dbias + h0 : nullptr;
-    float* mm = ml + 2 * h0;
-    DotSrcArgs sa{row_ptr_t, col_t, perm, plan_view(*plan_t), qq, kk, vv, bb, scale, mm, gg,
-                  dkk, dvv, src_part, ld, mld, bld};
-    st = TGX_UNSUPPORTED;
-#define TGX_DOT_BWD(GG, HH)                                                                   \
-    if (shp.G == GG && shp.HL == HH) {                                                        \
-      if (idx_bits == 32)                                                                     \
-        st = dot_bwd_launch<int32_t, GG, HH>(                                                 \
-            DotDstArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                         \
-                                static_cast<const int32_t*>(col), plan_view(*plan), qq, kk,   \
-                                vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld, bld},     \
-            sa, oo, mm, n_dst, s);                                                            \
-      else                                                                                    \
-        st = dot_bwd_launch<int64_t, GG, HH>(                                                 \
-            DotDstArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                         \
-                                static_cast<const int64_t*>(col), plan_view(*plan), qq, kk,   \
-                                vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld, bld},     \
-            sa, oo, mm, n_dst, s);                                                            \
-    } else
-    TGX_DOT_SHAPES(TGX_DOT_BWD)
-    set_error("unsupported dot attention head group G=%d HL=%d", shp.G, shp.HL);
-#undef TGX_DOT_BWD
-    if (st != TGX_OK) return st;
-    h0 += hg;
+  switch (dtype) {
+    case TGX_DTYPE_BF16:
+      return dot_bwd_dtype<TGX_DTYPE_BF16>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
+                                           plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
+                                           dv, dbias, n_dst, H, D, dst_part, src_part, s);
+    case TGX_DTYPE_F16:
+      return dot_bwd_dtype<TGX_DTYPE_F16>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
+                                          plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
+                                          dv, dbias, n_dst, H, D, dst_part, src_part, s);
+    default:
+      return dot_bwd_dtype<TGX_DTYPE_F32>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
+                                          plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
+                                          dv, dbias, n_dst, H, D, dst_part, src_part, s);
   }
-  return TGX_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -769,7 +829,7 @@ extern "C" int tgx_dot_attn_fwd_noalloc(const void* row_ptr, const void* col, in
                                         const tgx_row_plan* plan, const void* q,
                                         const void* k, const void* v, const float* bias,
                                         float scale, void* out, float* ml, int64_t n_dst,
-                                        int64_t n_src, int H, int D, void* stream) {
+                                        int64_t n_src, int H, int D, int dtype, void* stream) {
   // Every size check comes before any HIP call.
   TGX_REQUIRE(plan != nullptr, "null plan");
   if (!dot_heads_ok(H, D)) {
@@ -791,5 +851,5 @@ extern "C" int tgx_dot_attn_fwd_noalloc(const void* row_ptr, const void* col, in
     if (st != TGX_OK) return st;
   }
   return tgx_dot_attn_fwd(row_ptr, col, idx_bits, plan, q, k, v, bias, scale, out, ml, n_dst,
-                          n_src, H, D, partial, stream);
+                          n_src, H, D, dtype, partial, stream);
 }

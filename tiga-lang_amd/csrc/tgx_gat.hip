@@ -1,8 +1,14 @@
-// GAT additive edge attention, fp32, over a destination-row CSR.
+// GAT additive edge attention over a destination-row CSR.
 //
-//   z_e = a_src[hd] . h[j, hd] + a_dst[hd] . h[i, hd]      (j = col[e], i = row)
+//   z_e = a_src[hd] . hs[j, hd] + a_dst[hd] . hd[i, hd]    (j = col[e], i = row)
 //   s_e = LeakyReLU(z_e, slope)
-//   out[i, hd] = sum_e softmax_i(s)_e * h[j, hd]
+//   out[i, hd] = sum_e softmax_i(s)_e * hs[j, hd]
+//
+// hs (source features) and hd (destination features) are one tensor for a
+// homogeneous relation and two for a bipartite one.  Elements are fp32,
+// bf16 or fp16; scores, softmax sums and products are fp32 and every output
+// is rounded once (the reference accumulates 16-bit scores in fp32 and
+// casts the result to the value's dtype, reducer_oracle.py:22-41, 137).
 //
 // Reference semantics: an edge() returning
 //   reducer(leaky_relu((src.h*a_src).sum(-1) + (dst.h*a_dst).sum(-1)), src.h)
@@ -10,23 +16,29 @@
 // 2848-2894, reducer_oracle.py:60-137): per-(row, head) max shift, exp, sum,
 // weighted sum, empty row -> 0.
 //
-// Layout: h is [N, H, D] fp32; one node row is 4*G floats spread over G lanes
-// (float4 per lane), so head hd occupies HL = D/4 consecutive lanes and its
-// dot products reduce with DPP inside the lane group.  node_state is
-// [N, H, 4] fp32 = {logsumexp, delta, a_dst.h[i], a_src.h[i]} so one 16-byte
-// load per lane brings every per-(node, head) scalar the backward needs.
+// Layout: features are [N, H, D]; one node row is 4*G values spread over G
+// lanes (4 values per lane: 16 bytes of fp32, 8 bytes of bf16/fp16), so head
+// hd occupies HL = D/4 consecutive lanes and its dot products reduce with
+// DPP inside the lane group.  node_state is [N_dst, H, 4] fp32 = {logsumexp,
+// delta, a_dst.hd[i], a_src.hd[i]} so one 16-byte load per lane brings every
+// per-(node, head) scalar the backward needs (slot 3 is a_src.h of the same
+// node, which a homogeneous relation's source pass reads).
 //
 // Backward (no float atomics, nothing per-edge saved by the forward):
 //   B1 node pass   delta[i] = <dout[i], out[i]> per head
 //   B2 source pass over the transposed CSR (row j = source): recompute
-//      alpha_e = exp(s_e - lse[i]) and dz_e = alpha_e (<dout[i], h[j]> - delta[i])
-//      * LeakyReLU'(z_e); dh[j] = sum alpha_e dout[i] + (sum dz_e) a_src;
-//      dz_e stored at its transposed position (coalesced writes); da_src +=
-//      (sum dz_e) h[j].
-//   B3 destination pass over the CSR: dh[i] += (sum_e dz_e) a_dst and
-//      da_dst += (sum_e dz_e) h[i], each edge's dz read through inv_perm.
+//      alpha_e = exp(s_e - lse[i]) and dz_e = alpha_e (<dout[i], hs[j]> - delta[i])
+//      * LeakyReLU'(z_e); dhs[j] = sum alpha_e dout[i] + (sum dz_e) a_src;
+//      dz_e stored at its transposed position (coalesced writes).
+//   B3 destination pass over the CSR: dhd[i] = (sum_e dz_e) a_dst (added to
+//      dhs[i] when hs and hd are one tensor) and da_dst += (sum_e dz_e) hd[i],
+//      each edge's dz read through inv_perm; da_src += (sum dz_e) hs[j] over
+//      the sources, fused here for a homogeneous relation, its own pass
+//      otherwise.
 //   da_* partials are fp64 per wave (static task striding), reduced in a
-//   fixed order, so every output is deterministic.
+//   fixed order, so every output is deterministic.  With 16-bit elements and
+//   one feature tensor, the source pass's dh contribution waits in an fp32
+//   workspace until B3 adds the destination term and rounds once.
 #include <hip/hip_runtime.h>
 
 #include "tgx_device.h"
@@ -34,6 +46,7 @@
 #include "tgx_profile.h"
 #include "tgx_softmax.h"
 #include "tgx_tasks.h"
+#include "tgx_vals.h"
 
 namespace tgx {
 namespace {
@@ -52,19 +65,21 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
   return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
 }
 
-template <typename I>
+template <int DT, typename I>
 struct GatFwdArgs {
+  using T = typename Vals<DT, 4>::T;
   const I* row_ptr;
   const I* col;
   PlanView plan;
-  const float* h;
+  const T* hs;     // source features (gathered)
+  const T* hd;     // destination features (== hs for a homogeneous relation)
   const float* a_src;
   const float* a_dst;
   float slope;
-  float* out;
+  T* out;
   float* ns;
   float* partial;  // per chunk: acc[4G] | m[H] | l[H]
-  int64_t ld;      // floats between consecutive nodes' rows of h and out
+  int64_t ld;      // values between consecutive nodes' rows of hs, hd and out
   int64_t nsld;    // floats between consecutive nodes' rows of ns
 };
 
@@ -75,8 +90,9 @@ __device__ __forceinline__ int fetch_lane(int v, int src) {
   return __shfl(v, src, 64);
 }
 
-template <typename I, int G, int HL, int U>
-__global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
+template <int DT, typename I, int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<DT, I> a) {
+  using V = Vals<DT, 4>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
@@ -93,11 +109,11 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
   if (t.kind == kTaskEmpty) {
     for (int k = 0; k < t.n_empty; ++k) {
       const int64_t i = uniform(a.plan.rows[t.empty0 + k]);
-      const f32x4 hi = ld4(a.h + i * a.ld + 4 * c);
+      const f32x4 hi = V::widen(V::load(a.hd + i * a.ld + 4 * c));
       const float sdst = group_sum<HL>(dot4(ad4, hi));
       const float ssrc = group_sum<HL>(dot4(as4, hi));
       if (g == 0) {
-        st4(a.out + i * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+        V::store(a.out + i * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
         if (head_lead) st4(a.ns + i * a.nsld + hd * 4, f32x4{kNegInf, 0.f, sdst, ssrc});
       }
     }
@@ -105,7 +121,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
   }
 
   const int64_t row = t.row;
-  const f32x4 hi = ld4(a.h + row * a.ld + 4 * c);
+  const f32x4 hi = V::widen(V::load(a.hd + row * a.ld + 4 * c));
   const float sdst = group_sum<HL>(dot4(ad4, hi));
 
   SoftState<4> st;
@@ -114,19 +130,19 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
     const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
     const int my_col = lane < n ? static_cast<int>(a.col[base + lane]) : 0;
     for (int k = 0; k < n; k += EPW * U) {
-      f32x4 x[U];
+      typename V::Raw x[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const int j = fetch_lane<EPW>(my_col, slot < n ? slot : 0);
-        x[u] = ld4(a.h + static_cast<int64_t>(j) * a.ld + 4 * c);
+        x[u] = V::load(a.hs + static_cast<int64_t>(j) * a.ld + 4 * c);
       }
       float s[U];
       float mc = kNegInf;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
-        const float z = group_sum<HL>(dot4(as4, x[u])) + sdst;
+        const float z = group_sum<HL>(dot4(as4, V::widen(x[u]))) + sdst;
         s[u] = slot < n ? leaky_relu(z, a.slope) : kNegInf;
         mc = fmaxf(mc, s[u]);
       }
@@ -135,8 +151,9 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
       for (int u = 0; u < U; ++u) {
         const float p = s[u] == kNegInf ? 0.f : fast_exp(s[u] - st.m);
         st.l += p;
+        const f32x4 xv = V::widen(x[u]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) st.acc[q] += p * x[u][q];
+        for (int q = 0; q < 4; ++q) st.acc[q] += p * xv[q];
       }
     }
   }
@@ -153,17 +170,19 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<I> a) {
     return;
   }
   const float inv = 1.f / st.l;
-  st4(a.out + row * a.ld + 4 * c,
-      f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
+  V::store(a.out + row * a.ld + 4 * c,
+           f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
   const float ssrc_i = group_sum<HL>(dot4(as4, hi));
   if (head_lead) st4(a.ns + row * a.nsld + hd * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc_i});
 }
 
-template <int G, int HL>
+template <int DT, int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
-    PlanView plan, const float* __restrict__ partial, const float* __restrict__ h,
-    const float* __restrict__ a_src, const float* __restrict__ a_dst,
-    float* __restrict__ out, float* __restrict__ ns, int64_t ld, int64_t nsld) {
+    PlanView plan, const float* __restrict__ partial,
+    const typename Vals<DT, 4>::T* __restrict__ hd_rows, const float* __restrict__ a_src,
+    const float* __restrict__ a_dst, typename Vals<DT, 4>::T* __restrict__ out,
+    float* __restrict__ ns, int64_t ld, int64_t nsld) {
+  using V = Vals<DT, 4>;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
   const int64_t k = global_wave();
@@ -182,9 +201,9 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
     st.merge(p[HD + hd], p[HD + H + hd], accs);
   }
   const float inv = 1.f / st.l;
-  st4(out + row * ld + 4 * c,
-      f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
-  const f32x4 hi = ld4(h + row * ld + 4 * c);
+  V::store(out + row * ld + 4 * c,
+           f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
+  const f32x4 hi = V::widen(V::load(hd_rows + row * ld + 4 * c));
   const float sdst = group_sum<HL>(dot4(ld4(a_dst + 4 * c), hi));
   const float ssrc = group_sum<HL>(dot4(ld4(a_src + 4 * c), hi));
   if (c % HL == 0) st4(ns + row * nsld + hd * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc});
@@ -193,40 +212,47 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
 // ---------------------------------------------------------------------------
 // Backward.
 
-template <int G, int HL>
+template <int DT, int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_delta_kernel(
-    const float* __restrict__ dout, const float* __restrict__ out, float* __restrict__ ns,
-    int64_t n_nodes, int64_t ld, int64_t nsld) {
+    const typename Vals<DT, 4>::T* __restrict__ dout,
+    const typename Vals<DT, 4>::T* __restrict__ out, float* __restrict__ ns, int64_t n_nodes,
+    int64_t ld, int64_t nsld) {
+  using V = Vals<DT, 4>;
   constexpr int EPW = kWave / G;
   const int lane = lane_id();
   const int c = lane % G, hd = c / HL;
   const int64_t node = global_wave() * EPW + lane / G;
   if (node >= n_nodes) return;
-  const float d = group_sum<HL>(dot4(ld4(dout + node * ld + 4 * c), ld4(out + node * ld + 4 * c)));
+  const float d = group_sum<HL>(dot4(V::widen(V::load(dout + node * ld + 4 * c)),
+                                     V::widen(V::load(out + node * ld + 4 * c))));
   if (c % HL == 0) ns[node * nsld + hd * 4 + 1] = d;
 }
 
+template <int DT>
 struct GatSrcArgs {
+  using T = typename Vals<DT, 4>::T;
   const int32_t* row_ptr_t;
   const int32_t* col_t;
   const int32_t* perm;
   PlanView plan;
-  const float* h;
+  const T* hs;
   const float* a_src;
   float slope;
   const float* ns;
-  const float* dout;
-  float* dh;
+  const T* dout;
+  float* dh_acc;    // fp32 [N, HD] (one feature tensor: B3 adds to it), or null
+  T* dhs;           // the source gradient itself when dh_acc is null
   float* partial;   // per chunk: [4G] dh contribution | [H] sum of dz
   float* dz;        // [E, H] in transposed edge order (coalesced)
-  float* sdz_src;   // [N, H] sum of dz over each source's out-edges
-  int64_t ld;       // floats between consecutive nodes' rows of h, dout, dh
+  float* sdz_src;   // [N_src, H] sum of dz over each source's out-edges
+  int64_t ld;       // values between consecutive nodes' rows of hs, dout, dh
   int64_t nsld;     // floats between consecutive nodes' rows of ns
 };
 
 // One wave per task of the transposed-CSR plan (source rows).
-template <int G, int HL, int U>
-__global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
+template <int DT, int G, int HL, int U>
+__global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs<DT> a) {
+  using V = Vals<DT, 4>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
@@ -241,7 +267,10 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
     for (int k = 0; k < t.n_empty; ++k) {
       const int64_t j = uniform(a.plan.rows[t.empty0 + k]);
       if (g == 0) {
-        st4(a.dh + j * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+        if (a.dh_acc)
+          st4(a.dh_acc + j * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+        else
+          V::store(a.dhs + j * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
         if (head_lead) a.sdz_src[j * H + hd] = 0.f;
       }
     }
@@ -249,34 +278,36 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
   }
   const f32x4 as4 = ld4(a.a_src + 4 * c);
   const int64_t j = t.row;
-  const f32x4 hj = ld4(a.h + j * a.ld + 4 * c);
-  const float ssrc = a.ns[j * a.nsld + hd * 4 + 3];
+  const f32x4 hj = V::widen(V::load(a.hs + j * a.ld + 4 * c));
+  // a_src . hs[j], the same fp32 arithmetic as the forward's.
+  const float ssrc = group_sum<HL>(dot4(as4, hj));
   f32x4 dha = {0.f, 0.f, 0.f, 0.f};
   float sdz = 0.f;
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
     const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
     const int my_i = lane < n ? a.col_t[base + lane] : 0;
     for (int k = 0; k < n; k += EPW * U) {
-      f32x4 d[U];
-      f32x3 nst[U];  // {lse, delta, a_dst.h[i]} of the destination
+      typename V::Raw d[U];
+      f32x3 nst[U];  // {lse, delta, a_dst.hd[i]} of the destination
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const int64_t i = fetch_lane<EPW>(my_i, slot < n ? slot : 0);
-        d[u] = ld4(a.dout + i * a.ld + 4 * c);
+        d[u] = V::load(a.dout + i * a.ld + 4 * c);
         nst[u] = ld3(a.ns + i * a.nsld + hd * 4);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const bool valid = slot < n;
+        const f32x4 du = V::widen(d[u]);
         const float z = ssrc + nst[u][2];
         const float s = leaky_relu(z, a.slope);
         const float alpha = valid ? fast_exp(s - nst[u][0]) : 0.f;
-        const float dalpha = group_sum<HL>(dot4(d[u], hj));
+        const float dalpha = group_sum<HL>(dot4(du, hj));
         const float ds = alpha * (dalpha - nst[u][1]);
         const float dzv = z > 0.f ? ds : ds * a.slope;
-        dha += alpha * d[u];
+        dha += alpha * du;
         sdz += dzv;
         if (valid && head_lead) a.dz[(base + slot) * H + hd] = dzv;
       }
@@ -297,15 +328,19 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs a) {
     st4(p + 4 * c, contrib);
     if (head_lead) p[HD + hd] = sdz;
   } else {
-    st4(a.dh + j * a.ld + 4 * c, contrib);
+    if (a.dh_acc)
+      st4(a.dh_acc + j * a.ld + 4 * c, contrib);
+    else
+      V::store(a.dhs + j * a.ld + 4 * c, contrib);
     if (head_lead) a.sdz_src[j * H + hd] = sdz;
   }
 }
 
-template <int G, int HL>
+template <int DT, int G, int HL>
 __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
-    PlanView plan, const float* __restrict__ partial, float* __restrict__ dh,
-    float* __restrict__ sdz_src, int64_t ld) {
+    PlanView plan, const float* __restrict__ partial, float* __restrict__ dh_acc,
+    typename Vals<DT, 4>::T* __restrict__ dhs, float* __restrict__ sdz_src, int64_t ld) {
+  using V = Vals<DT, 4>;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
   const int64_t k = global_wave();
@@ -322,25 +357,30 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
     s += ld4(p + 4 * c);
     z += p[HD + hd];
   }
-  st4(dh + row * ld + 4 * c, s);
+  if (dh_acc)
+    st4(dh_acc + row * ld + 4 * c, s);
+  else
+    V::store(dhs + row * ld + 4 * c, s);
   if (c % HL == 0) sdz_src[row * H + hd] = z;
 }
 
-template <typename I>
+template <int DT, typename I>
 struct GatDstArgs {
+  using T = typename Vals<DT, 4>::T;
   const I* row_ptr;
   PlanView plan;
-  const float* h;
+  const T* hd;
   const float* a_dst;
   const float* dz;       // [E, H] in transposed edge order
   const int32_t* inv_perm;  // [E] transposed position of each edge
-  const float* sdz_src;  // [N, H]
-  float* dh;
+  const float* sdz_src;  // [N, H]; read only with `fused_src`
+  const float* dh_acc;   // fp32 source-pass contribution to add, or null
+  T* dhd;                // destination gradient (the one dh of a homogeneous relation)
   float* partial;        // per chunk: [H]
   double* dap_src;       // [waves, 4G]
   double* dap_dst;       // [waves, 4G]
   int64_t n_tasks;
-  int64_t ld;            // floats between consecutive nodes' rows of h and dh
+  int64_t ld;            // values between consecutive nodes' rows of hd and dhd
 };
 
 __device__ __forceinline__ void acc_f64(f64x4& acc, float scale, f32x4 v) {
@@ -351,11 +391,23 @@ __device__ __forceinline__ void acc_f64(f64x4& acc, float scale, f32x4 v) {
   acc[3] += sd * v[3];
 }
 
+// dhd[i] = base + sdz * a_dst, base = the source pass's fp32 contribution
+// (one feature tensor: FUSED) or 0, rounded once.
+template <class V, bool FUSED>
+__device__ __forceinline__ void finish_dh(typename V::T* dhd, const float* dh_acc, int64_t off,
+                                          float sdz, f32x4 ad4) {
+  f32x4 base = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (FUSED) base = ld4(dh_acc + off);
+  V::store(dhd + off, base + sdz * ad4);
+}
+
 // Persistent over the CSR plan (static task striding keeps the fp64
-// partials deterministic).  Every node's h row is read exactly once here:
-// da_dst += (sum over its in-edges of dz) h[i], da_src += sdz_src[i] h[i].
-template <typename I, int G, int HL>
-__global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a) {
+// partials deterministic).  Every destination row of hd is read exactly
+// once here: da_dst += (sum over its in-edges of dz) hd[i], and with one
+// feature tensor (FUSED) da_src += sdz_src[i] h[i].
+template <int DT, typename I, int G, int HL, bool FUSED>
+__global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<DT, I> a) {
+  using V = Vals<DT, 4>;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
   const int lane = lane_id();
@@ -372,7 +424,13 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a
     if (t.kind == kTaskEmpty) {
       for (int k = 0; k < t.n_empty; ++k) {
         const int64_t i = uniform(a.plan.rows[t.empty0 + k]);
-        if (g == 0) acc_f64(ds, a.sdz_src[i * H + hd], ld4(a.h + i * a.ld + 4 * c));
+        if (g == 0) {
+          if constexpr (FUSED)
+            acc_f64(ds, a.sdz_src[i * H + hd], V::widen(V::load(a.hd + i * a.ld + 4 * c)));
+          // An fp32 gradient of one feature tensor already holds its value.
+          if constexpr (!(FUSED && DT == TGX_DTYPE_F32))
+            finish_dh<V, FUSED>(a.dhd, a.dh_acc, i * a.ld + 4 * c, 0.f, ad4);
+        }
       }
       continue;
     }
@@ -404,28 +462,30 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_kernel(GatDstArgs<I> a
     if (t.kind == kTaskChunk && lane < H)
       a.partial[static_cast<int64_t>(t.slot) * H + lane] = s;
     if (g == 0) {
-      const f32x4 hi = ld4(a.h + i * a.ld + 4 * c);
+      const f32x4 hi = V::widen(V::load(a.hd + i * a.ld + 4 * c));
       acc_f64(dd, sdz, hi);
       const bool first = t.kind == kTaskRow || t.e0 == static_cast<int64_t>(a.row_ptr[i]);
-      if (first) acc_f64(ds, a.sdz_src[i * H + hd], hi);
-      if (t.kind == kTaskRow) {
-        float* q = a.dh + i * a.ld + 4 * c;
-        st4(q, ld4(q) + sdz * ad4);
+      if constexpr (FUSED) {
+        if (first) acc_f64(ds, a.sdz_src[i * H + hd], hi);
       }
+      if (t.kind == kTaskRow) finish_dh<V, FUSED>(a.dhd, a.dh_acc, i * a.ld + 4 * c, sdz, ad4);
     }
   }
   if (g == 0) {
-    double* p = a.dap_src + global_wave() * HD + 4 * c;
     double* q = a.dap_dst + global_wave() * HD + 4 * c;
-    p[0] = ds[0]; p[1] = ds[1]; p[2] = ds[2]; p[3] = ds[3];
     q[0] = dd[0]; q[1] = dd[1]; q[2] = dd[2]; q[3] = dd[3];
+    if constexpr (FUSED) {
+      double* p = a.dap_src + global_wave() * HD + 4 * c;
+      p[0] = ds[0]; p[1] = ds[1]; p[2] = ds[2]; p[3] = ds[3];
+    }
   }
 }
 
-template <int G, int HL>
+template <int DT, int G, int HL, bool FUSED>
 __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_merge_kernel(
     PlanView plan, const float* __restrict__ partial, const float* __restrict__ a_dst,
-    float* __restrict__ dh, int64_t ld) {
+    const float* dh_acc, typename Vals<DT, 4>::T* dhd, int64_t ld) {
+  using V = Vals<DT, 4>;
   constexpr int H = G / HL;
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
@@ -436,8 +496,38 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_merge_kernel(
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
   float s = 0.f;
   for (int q = c0; q < c1; ++q) s += partial[static_cast<int64_t>(q) * H + hd];
-  float* p = dh + row * ld + 4 * c;
-  st4(p, ld4(p) + s * ld4(a_dst + 4 * c));
+  finish_dh<V, FUSED>(dhd, dh_acc, row * ld + 4 * c, s, ld4(a_dst + 4 * c));
+}
+
+// da_src's per-wave partials over the sources of a bipartite relation:
+// sum_j sdz_src[j] hs[j], persistent with static striding (deterministic).
+template <int DT, int G, int HL>
+__global__ __launch_bounds__(kTaskBlock) void gat_da_src_kernel(
+    const typename Vals<DT, 4>::T* __restrict__ hs, const float* __restrict__ sdz_src,
+    double* __restrict__ dap_src, int64_t n_src, int64_t ld) {
+  using V = Vals<DT, 4>;
+  constexpr int EPW = kWave / G;
+  constexpr int HD = 4 * G;
+  constexpr int H = G / HL;
+  const int lane = lane_id();
+  const int g = lane / G;
+  const int c = lane % G;
+  const int hd = c / HL;
+  f64x4 ds = {0.0, 0.0, 0.0, 0.0};
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * EPW;
+  for (int64_t j = global_wave() * EPW + g; j < n_src; j += stride)
+    acc_f64(ds, sdz_src[j * H + hd], V::widen(V::load(hs + j * ld + 4 * c)));
+#pragma unroll
+  for (int mask = G; mask < kWave; mask <<= 1) {
+    ds[0] += __shfl_xor(ds[0], mask, 64);
+    ds[1] += __shfl_xor(ds[1], mask, 64);
+    ds[2] += __shfl_xor(ds[2], mask, 64);
+    ds[3] += __shfl_xor(ds[3], mask, 64);
+  }
+  if (g == 0) {
+    double* p = dap_src + global_wave() * HD + 4 * c;
+    p[0] = ds[0]; p[1] = ds[1]; p[2] = ds[2]; p[3] = ds[3];
+  }
 }
 
 // da[x] = sum over waves of dapart[w][x] in a fixed order, fp64, two levels:
@@ -515,22 +605,23 @@ int64_t persist_blocks(int64_t tasks, int64_t resident) {
   X(2, 2) X(2, 1)                                                               \
   X(1, 1)
 
-template <typename I, int G, int HL>
-int gat_fwd_launch(const GatFwdArgs<I>& a, hipStream_t s) {
+template <int DT, typename I, int G, int HL>
+int gat_fwd_launch(const GatFwdArgs<DT, I>& a, hipStream_t s) {
   constexpr int EPW = kWave / G;
   // Rows in flight per lane group: 10 x 1 KB per wave measured best for the
-  // forward (8: +2%, 12: +1%, 16: +5% time on the 1M-node graph).
+  // fp32 forward (8: +2%, 12: +1%, 16: +5% time on the 1M-node graph).
   constexpr int U = EPW >= 10 ? 1 : 10 / EPW;
   const int64_t waves = plan_waves(a.plan);
   if (waves > 0) {
     TGX_PROFILE("gat_fwd_kernel", s);
-    gat_fwd_kernel<I, G, HL, U><<<ceil_div(waves, kWavesPerBlock), kTaskBlock, 0, s>>>(a);
+    gat_fwd_kernel<DT, I, G, HL, U><<<ceil_div(waves, kWavesPerBlock), kTaskBlock, 0, s>>>(a);
     TGX_LAUNCHED("gat_fwd_kernel");
   }
   if (a.plan.n_split > 0) {
     TGX_PROFILE("gat_fwd_merge_kernel", s);
-    gat_fwd_merge_kernel<G, HL><<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        a.plan, a.partial, a.h, a.a_src, a.a_dst, a.out, a.ns, a.ld, a.nsld);
+    gat_fwd_merge_kernel<DT, G, HL>
+        <<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+            a.plan, a.partial, a.hd, a.a_src, a.a_dst, a.out, a.ns, a.ld, a.nsld);
     TGX_LAUNCHED("gat_fwd_merge_kernel");
   }
   return TGX_OK;
@@ -538,144 +629,171 @@ int gat_fwd_launch(const GatFwdArgs<I>& a, hipStream_t s) {
 
 struct GatBwdLayout {
   size_t dz_off, sdz_off, src_part_off, dst_part_off, dap_src_off, dap_dst_off, slices_off,
-      bytes;
+      dh_acc_off, bytes;
   int64_t src_waves, dst_waves;
 };
 
+// Workspace of one head group; dh_acc (fp32 [n_dst, H*D]) only for 16-bit
+// elements, where a homogeneous relation's dh waits there between passes.
 GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t,
-                            int64_t n_edges, int H, int D) {
+                            int64_t n_edges, int H, int D, int dtype) {
   GatBwdLayout L;
   const int64_t HD = static_cast<int64_t>(H) * D;
-  const PlanView pv = plan_view(plan);
   // Partial buffers are sized for the largest grid; launches may use fewer.
+  // The bipartite da_src pass takes at most one wave per source.
+  const PlanView pv = plan_view(plan);
   L.dst_waves = persist_blocks(plan_waves(pv), kPersistBlocks) * kWavesPerBlock;
-  L.src_waves = L.dst_waves;
+  L.src_waves = persist_blocks(plan_t.n_rows, kPersistBlocks) * kWavesPerBlock;
+  if (L.src_waves < L.dst_waves) L.src_waves = L.dst_waves;
+  const int64_t nodes = plan.n_rows > plan_t.n_rows ? plan.n_rows : plan_t.n_rows;
   Carve c{nullptr, 0};
   L.dz_off = reinterpret_cast<size_t>(c.take<float>(n_edges * H));
-  L.sdz_off = reinterpret_cast<size_t>(c.take<float>(plan.n_rows * H));
+  L.sdz_off = reinterpret_cast<size_t>(c.take<float>(nodes * H));
   L.src_part_off = reinterpret_cast<size_t>(c.take<float>(plan_t.n_chunks * (HD + H)));
   L.dst_part_off = reinterpret_cast<size_t>(c.take<float>(plan.n_chunks * H));
   L.dap_src_off = reinterpret_cast<size_t>(c.take<double>(L.src_waves * HD));
   L.dap_dst_off = reinterpret_cast<size_t>(c.take<double>(L.dst_waves * HD));
   L.slices_off = reinterpret_cast<size_t>(c.take<double>(2 * kDaSlices * HD));
+  L.dh_acc_off = reinterpret_cast<size_t>(
+      c.take<float>(dtype == TGX_DTYPE_F32 ? 0 : plan.n_rows * HD));
   L.bytes = align_up(c.used);
   return L;
 }
 
-template <typename I, int G, int HL>
+struct GatBwdIo {
+  const void *hs, *hd, *out, *dout;
+  const float *a_src, *a_dst;
+  void *dhs, *dhd;
+  float *ns, *da_src, *da_dst;
+  int64_t n_dst, n_src, ld, nsld;
+  float slope;
+};
+
+template <int DT, typename I, int G, int HL>
 int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* row_ptr_t,
                    const int32_t* col_t, const int32_t* perm, const int32_t* inv_perm,
-                   const tgx_row_plan& plan_t,
-                   const float* h, const float* a_src, const float* a_dst, float slope,
-                   const float* out, float* ns, const float* dout, float* dh, float* da_src,
-                   float* da_dst, int64_t n_nodes, int64_t n_edges, int64_t ld,
-                   int64_t nsld, char* ws, const GatBwdLayout& L, hipStream_t s) {
+                   const tgx_row_plan& plan_t, const GatBwdIo& io, char* ws,
+                   const GatBwdLayout& L, hipStream_t s) {
+  using T = typename Vals<DT, 4>::T;
   constexpr int EPW = kWave / G;
   // The source pass holds dout rows plus node state per edge: 4 in flight
   // per wave measured best (2: +4%, 3: +2%, 6: +5%, 8: +6% time).
   constexpr int U = EPW >= 4 ? 1 : 4 / EPW;
   constexpr int HD = 4 * G;
-  (void)n_edges;
+  const bool homogeneous = io.dhs == io.dhd;
   float* dz = reinterpret_cast<float*>(ws + L.dz_off);
   float* sdz_src = reinterpret_cast<float*>(ws + L.sdz_off);
   float* src_part = reinterpret_cast<float*>(ws + L.src_part_off);
   float* dst_part = reinterpret_cast<float*>(ws + L.dst_part_off);
   double* dap_src = reinterpret_cast<double*>(ws + L.dap_src_off);
   double* dap_dst = reinterpret_cast<double*>(ws + L.dap_dst_off);
+  // One feature tensor: the source pass's contribution to dh is completed by
+  // the destination pass, in place for fp32, in fp32 workspace otherwise.
+  float* dh_acc = nullptr;
+  if (homogeneous)
+    dh_acc = DT == TGX_DTYPE_F32 ? static_cast<float*>(io.dhd)
+                                 : reinterpret_cast<float*>(ws + L.dh_acc_off);
+  const T* hs = static_cast<const T*>(io.hs);
+  const T* hd = static_cast<const T*>(io.hd);
   const PlanView pv = plan_view(plan), pt = plan_view(plan_t);
 
   {
-  TGX_PROFILE("gat_delta_kernel", s);
-  gat_delta_kernel<G, HL><<<ceil_div(ceil_div(n_nodes, EPW), kWavesPerBlock), kTaskBlock, 0, s>>>(
-      dout, out, ns, n_nodes, ld, nsld);
-  TGX_LAUNCHED("gat_delta_kernel");
+    TGX_PROFILE("gat_delta_kernel", s);
+    gat_delta_kernel<DT, G, HL>
+        <<<ceil_div(ceil_div(io.n_dst, EPW), kWavesPerBlock), kTaskBlock, 0, s>>>(
+            static_cast<const T*>(io.dout), static_cast<const T*>(io.out), io.ns, io.n_dst,
+            io.ld, io.nsld);
+    TGX_LAUNCHED("gat_delta_kernel");
   }
 
-  GatSrcArgs sa{row_ptr_t, col_t, perm, pt, h, a_src, slope, ns, dout, dh, src_part, dz,
-                sdz_src, ld, nsld};
-  GatDstArgs<I> da{row_ptr, pv, h, a_dst, dz, inv_perm, sdz_src, dh, dst_part, dap_src,
-                   dap_dst, plan_waves(pv), ld};
+  const GatSrcArgs<DT> sa{row_ptr_t, col_t, perm, pt, hs, io.a_src, io.slope, io.ns,
+                          static_cast<const T*>(io.dout), dh_acc, static_cast<T*>(io.dhs),
+                          src_part, dz, sdz_src, io.ld, io.nsld};
+  const GatDstArgs<DT, I> da{row_ptr, pv, hd, io.a_dst, dz, inv_perm, sdz_src, dh_acc,
+                             static_cast<T*>(io.dhd), dst_part, dap_src, dap_dst,
+                             plan_waves(pv), io.ld};
+  const auto dst_kernel = homogeneous ? gat_bwd_dst_kernel<DT, I, G, HL, true>
+                                      : gat_bwd_dst_kernel<DT, I, G, HL, false>;
   const int64_t dst_blocks =
-      persist_blocks(plan_waves(pv), resident_blocks(gat_bwd_dst_kernel<I, G, HL>, kTaskBlock));
-  {
-  TGX_PROFILE("gat_bwd_src_kernel", s);
-  if (plan_waves(pt) > 0)
-    gat_bwd_src_kernel<G, HL, U><<<ceil_div(plan_waves(pt), kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
-  TGX_LAUNCHED("gat_bwd_src_kernel");
+      persist_blocks(plan_waves(pv), resident_blocks(dst_kernel, kTaskBlock));
+  if (plan_waves(pt) > 0) {
+    TGX_PROFILE("gat_bwd_src_kernel", s);
+    gat_bwd_src_kernel<DT, G, HL, U>
+        <<<ceil_div(plan_waves(pt), kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
+    TGX_LAUNCHED("gat_bwd_src_kernel");
   }
   if (pt.n_split > 0) {
     TGX_PROFILE("gat_bwd_src_merge_kernel", s);
-    gat_bwd_src_merge_kernel<G, HL><<<ceil_div(pt.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        pt, src_part, dh, sdz_src, ld);
+    gat_bwd_src_merge_kernel<DT, G, HL>
+        <<<ceil_div(pt.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+            pt, src_part, dh_acc, static_cast<T*>(io.dhs), sdz_src, io.ld);
     TGX_LAUNCHED("gat_bwd_src_merge_kernel");
   }
   {
-  TGX_PROFILE("gat_bwd_dst_kernel", s);
-  gat_bwd_dst_kernel<I, G, HL><<<dst_blocks, kTaskBlock, 0, s>>>(da);
-  TGX_LAUNCHED("gat_bwd_dst_kernel");
+    TGX_PROFILE("gat_bwd_dst_kernel", s);
+    dst_kernel<<<dst_blocks, kTaskBlock, 0, s>>>(da);
+    TGX_LAUNCHED("gat_bwd_dst_kernel");
   }
   if (pv.n_split > 0) {
     TGX_PROFILE("gat_bwd_dst_merge_kernel", s);
-    gat_bwd_dst_merge_kernel<G, HL><<<ceil_div(pv.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        pv, dst_part, a_dst, dh, ld);
+    const auto merge = homogeneous ? gat_bwd_dst_merge_kernel<DT, G, HL, true>
+                                   : gat_bwd_dst_merge_kernel<DT, G, HL, false>;
+    merge<<<ceil_div(pv.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        pv, dst_part, io.a_dst, dh_acc, static_cast<T*>(io.dhd), io.ld);
     TGX_LAUNCHED("gat_bwd_dst_merge_kernel");
   }
-  if (da_src || da_dst) {
-    // Both outputs are required by the kernel; callers pass both.
+  int64_t src_blocks = dst_blocks;
+  if (!homogeneous) {
+    src_blocks = persist_blocks(ceil_div(io.n_src, EPW),
+                                resident_blocks(gat_da_src_kernel<DT, G, HL>, kTaskBlock));
+    TGX_PROFILE("gat_da_src_kernel", s);
+    gat_da_src_kernel<DT, G, HL><<<src_blocks, kTaskBlock, 0, s>>>(hs, sdz_src, dap_src,
+                                                                    io.n_src, io.ld);
+    TGX_LAUNCHED("gat_da_src_kernel");
+  }
+  {
     TGX_PROFILE("da_reduce_kernel", s);
     double* slices = reinterpret_cast<double*>(ws + L.slices_off);
     da_slice_kernel<<<dim3(kDaSlices, 2), 256, 0, s>>>(dap_src, dap_dst,
-                                                        dst_blocks * kWavesPerBlock,
+                                                        src_blocks * kWavesPerBlock,
                                                         dst_blocks * kWavesPerBlock, HD, slices);
     TGX_LAUNCHED("da_slice_kernel");
-    da_final_kernel<<<ceil_div(2 * HD, 256), 256, 0, s>>>(slices, HD, da_src, da_dst);
+    da_final_kernel<<<ceil_div(2 * HD, 256), 256, 0, s>>>(slices, HD, io.da_src, io.da_dst);
     TGX_LAUNCHED("da_final_kernel");
   }
   return TGX_OK;
 }
 
-}  // namespace
-}  // namespace tgx
-
-using namespace tgx;
-
-extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
-                           const tgx_row_plan* plan, const float* h, const float* a_src,
-                           const float* a_dst, float slope, float* out, float* ns,
-                           int64_t n_nodes, int H, int D, float* partial, void* stream) {
-  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
-  if (!gat_heads_ok(H, D)) {
-    set_error("GAT kernel supports H >= 1 and D in {4, 8, 16, 32, 64, 128, 256} "
-              "(got H=%d D=%d)", H, D);
-    return TGX_UNSUPPORTED;
-  }
-  int st = check_plan(plan, n_nodes);
-  if (st != TGX_OK) return st;
-  if (n_nodes == 0) return TGX_OK;
-  TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns, "null pointer");
-  TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
-  hipStream_t s = as_stream(stream);
+template <int DT>
+int gat_fwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_row_plan* plan,
+                  const void* hs, const void* hd, const float* a_src, const float* a_dst,
+                  float slope, void* out, float* ns, int H, int D, float* partial,
+                  hipStream_t s) {
+  using T = typename Vals<DT, 4>::T;
   const int64_t ld = static_cast<int64_t>(H) * D, nsld = 4 * static_cast<int64_t>(H);
   for (int h0 = 0; h0 < H;) {
     const int hg = gat_group_heads(H, D, h0);
     const GatShape shp = gat_shape(hg, D);
     const int64_t off = static_cast<int64_t>(h0) * D;
-    st = TGX_UNSUPPORTED;
+    const T* hs_g = hs ? static_cast<const T*>(hs) + off : nullptr;
+    const T* hd_g = static_cast<const T*>(hd) + off;
+    T* out_g = static_cast<T*>(out) + off;
+    int st = TGX_UNSUPPORTED;
 #define TGX_GAT_FWD(GG, HH)                                                                  \
     if (shp.G == GG && shp.HL == HH) {                                                       \
       if (idx_bits == 32)                                                                    \
-        st = gat_fwd_launch<int32_t, GG, HH>(                                                \
-            GatFwdArgs<int32_t>{static_cast<const int32_t*>(row_ptr),                        \
-                                static_cast<const int32_t*>(col), plan_view(*plan), h + off, \
-                                a_src + off, a_dst + off, slope, out + off, ns + 4 * h0,     \
-                                partial, ld, nsld},                                          \
+        st = gat_fwd_launch<DT, int32_t, GG, HH>(                                            \
+            GatFwdArgs<DT, int32_t>{static_cast<const int32_t*>(row_ptr),                    \
+                                    static_cast<const int32_t*>(col), plan_view(*plan),      \
+                                    hs_g, hd_g, a_src + off, a_dst + off, slope, out_g,      \
+                                    ns + 4 * h0, partial, ld, nsld},                         \
             s);                                                                              \
       else                                                                                   \
-        st = gat_fwd_launch<int64_t, GG, HH>(                                                \
-            GatFwdArgs<int64_t>{static_cast<const int64_t*>(row_ptr),                        \
-                                static_cast<const int64_t*>(col), plan_view(*plan), h + off, \
-                                a_src + off, a_dst + off, slope, out + off, ns + 4 * h0,     \
-                                partial, ld, nsld},                                          \
+        st = gat_fwd_launch<DT, int64_t, GG, HH>(                                            \
+            GatFwdArgs<DT, int64_t>{static_cast<const int64_t*>(row_ptr),                    \
+                                    static_cast<const int64_t*>(col), plan_view(*plan),      \
+                                    hs_g, hd_g, a_src + off, a_dst + off, slope, out_g,      \
+                                    ns + 4 * h0, partial, ld, nsld},                         \
             s);                                                                              \
     } else
     TGX_GAT_SHAPES(TGX_GAT_FWD)
@@ -687,67 +805,46 @@ extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
   return TGX_OK;
 }
 
-extern "C" int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
-                                     int64_t n_edges, int H, int D, size_t* bytes) {
-  TGX_REQUIRE(plan && plan_t && bytes, "null pointer");
-  if (!gat_heads_ok(H, D)) {
-    set_error("unsupported GAT shape H=%d D=%d", H, D);
-    return TGX_UNSUPPORTED;
-  }
-  // Head groups run one after another on one stream and share the
-  // workspace; the first group is the widest.
-  *bytes = gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D).bytes;
-  return TGX_OK;
-}
-
-extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
-                           const tgx_row_plan* plan, const int32_t* row_ptr_t,
-                           const int32_t* col_t, const int32_t* perm, const int32_t* inv_perm,
-                           const tgx_row_plan* plan_t, const float* h, const float* a_src,
-                           const float* a_dst, float slope, const float* out, float* ns,
-                           const float* dout, float* dh, float* da_src, float* da_dst,
-                           int64_t n_nodes, int64_t n_edges, int H, int D, void* ws,
-                           size_t ws_bytes, void* stream) {
-  (void)col;
-  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
-  if (!gat_heads_ok(H, D)) {
-    set_error("unsupported GAT shape H=%d D=%d", H, D);
-    return TGX_UNSUPPORTED;
-  }
-  int st = check_plan(plan, n_nodes);
-  if (st != TGX_OK) return st;
-  st = check_plan(plan_t, n_nodes);
-  if (st != TGX_OK) return st;
-  if (n_nodes == 0) return TGX_OK;
-  TGX_REQUIRE(row_ptr && h && a_src && a_dst && out && ns && dout && dh && da_src && da_dst,
-              "null pointer");
-  TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && inv_perm), "null transposed CSR");
-  const size_t need =
-      gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D).bytes;
-  TGX_REQUIRE(ws && ws_bytes >= need, "workspace too small: need %zu bytes", need);
-  hipStream_t s = as_stream(stream);
-  char* w = static_cast<char*>(ws);
-  const int64_t ld = static_cast<int64_t>(H) * D, nsld = 4 * static_cast<int64_t>(H);
+template <int DT>
+int gat_bwd_dtype(const void* row_ptr, int idx_bits, const tgx_row_plan* plan,
+                  const int32_t* row_ptr_t, const int32_t* col_t, const int32_t* perm,
+                  const int32_t* inv_perm, const tgx_row_plan* plan_t, const GatBwdIo& all,
+                  int64_t n_edges, int H, int D, char* w, hipStream_t s) {
+  using T = typename Vals<DT, 4>::T;
+  auto at = [](const void* p, int64_t off) -> const void* {
+    return p ? static_cast<const T*>(p) + off : nullptr;
+  };
+  auto at_mut = [](void* p, int64_t off) -> void* {
+    return p ? static_cast<T*>(p) + off : nullptr;
+  };
   for (int h0 = 0; h0 < H;) {
     const int hg = gat_group_heads(H, D, h0);
     const GatShape shp = gat_shape(hg, D);
-    const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, hg, D);
+    const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, hg, D, DT);
     const int64_t off = static_cast<int64_t>(h0) * D;
-    st = TGX_UNSUPPORTED;
+    GatBwdIo io = all;
+    io.hs = at(all.hs, off);
+    io.hd = at(all.hd, off);
+    io.out = at(all.out, off);
+    io.dout = at(all.dout, off);
+    io.dhs = at_mut(all.dhs, off);
+    io.dhd = at_mut(all.dhd, off);
+    io.a_src = all.a_src + off;
+    io.a_dst = all.a_dst + off;
+    io.da_src = all.da_src + off;
+    io.da_dst = all.da_dst + off;
+    io.ns = all.ns + 4 * h0;
+    int st = TGX_UNSUPPORTED;
 #define TGX_GAT_BWD(GG, HH)                                                                 \
     if (shp.G == GG && shp.HL == HH) {                                                      \
       if (idx_bits == 32)                                                                   \
-        st = gat_bwd_launch<int32_t, GG, HH>(                                               \
-            static_cast<const int32_t*>(row_ptr), *plan, row_ptr_t, col_t, perm, inv_perm,  \
-            *plan_t, h + off, a_src + off, a_dst + off, slope, out + off, ns + 4 * h0,      \
-            dout + off, dh + off, da_src + off, da_dst + off, n_nodes, n_edges, ld, nsld, w, \
-            L, s);                                                                          \
+        st = gat_bwd_launch<DT, int32_t, GG, HH>(static_cast<const int32_t*>(row_ptr),      \
+                                                 *plan, row_ptr_t, col_t, perm, inv_perm,   \
+                                                 *plan_t, io, w, L, s);                     \
       else                                                                                  \
-        st = gat_bwd_launch<int64_t, GG, HH>(                                               \
-            static_cast<const int64_t*>(row_ptr), *plan, row_ptr_t, col_t, perm, inv_perm,  \
-            *plan_t, h + off, a_src + off, a_dst + off, slope, out + off, ns + 4 * h0,      \
-            dout + off, dh + off, da_src + off, da_dst + off, n_nodes, n_edges, ld, nsld, w, \
-            L, s);                                                                          \
+        st = gat_bwd_launch<DT, int64_t, GG, HH>(static_cast<const int64_t*>(row_ptr),      \
+                                                 *plan, row_ptr_t, col_t, perm, inv_perm,   \
+                                                 *plan_t, io, w, L, s);                     \
     } else
     TGX_GAT_SHAPES(TGX_GAT_BWD)
     set_error("unsupported GAT head group G=%d HL=%d", shp.G, shp.HL);
@@ -756,4 +853,114 @@ extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
     h0 += hg;
   }
   return TGX_OK;
+}
+
+}  // namespace
+}  // namespace tgx
+
+using namespace tgx;
+
+extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
+                           const tgx_row_plan* plan, const void* h_src, const void* h_dst,
+                           const float* a_src, const float* a_dst, float slope, void* out,
+                           float* ns, int64_t n_dst, int64_t n_src, int H, int D, int dtype,
+                           float* partial, void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(dtype_bytes(dtype) != 0, "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)",
+              dtype);
+  if (!gat_heads_ok(H, D)) {
+    set_error("GAT kernel supports H >= 1 and D in {4, 8, 16, 32, 64, 128, 256} "
+              "(got H=%d D=%d)", H, D);
+    return TGX_UNSUPPORTED;
+  }
+  TGX_REQUIRE(h_src != h_dst || n_src == n_dst,
+              "one feature tensor for both roles needs n_src == n_dst");
+  int st = check_plan(plan, n_dst);
+  if (st != TGX_OK) return st;
+  if (n_dst == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && h_dst && a_src && a_dst && out && ns && (h_src || n_src == 0),
+              "null pointer");
+  TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
+  TGX_REQUIRE(n_src < (int64_t{1} << 31), "source tables need fewer than 2^31 rows");
+  hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case TGX_DTYPE_F32:
+      return gat_fwd_dtype<TGX_DTYPE_F32>(row_ptr, col, idx_bits, plan, h_src, h_dst, a_src,
+                                          a_dst, slope, out, ns, H, D, partial, s);
+    case TGX_DTYPE_BF16:
+      return gat_fwd_dtype<TGX_DTYPE_BF16>(row_ptr, col, idx_bits, plan, h_src, h_dst, a_src,
+                                           a_dst, slope, out, ns, H, D, partial, s);
+    default:
+      return gat_fwd_dtype<TGX_DTYPE_F16>(row_ptr, col, idx_bits, plan, h_src, h_dst, a_src,
+                                          a_dst, slope, out, ns, H, D, partial, s);
+  }
+}
+
+extern "C" int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
+                                     int64_t n_edges, int H, int D, int dtype, size_t* bytes) {
+  TGX_REQUIRE(plan && plan_t && bytes, "null pointer");
+  TGX_REQUIRE(dtype_bytes(dtype) != 0, "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)",
+              dtype);
+  if (!gat_heads_ok(H, D)) {
+    set_error("unsupported GAT shape H=%d D=%d", H, D);
+    return TGX_UNSUPPORTED;
+  }
+  // Head groups run one after another on one stream and share the
+  // workspace; the first group is the widest.
+  *bytes = gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype).bytes;
+  return TGX_OK;
+}
+
+extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
+                           const tgx_row_plan* plan, const int32_t* row_ptr_t,
+                           const int32_t* col_t, const int32_t* perm, const int32_t* inv_perm,
+                           const tgx_row_plan* plan_t, const void* h_src, const void* h_dst,
+                           const float* a_src, const float* a_dst, float slope, const void* out,
+                           float* ns, const void* dout, void* dh_src, void* dh_dst,
+                           float* da_src, float* da_dst, int64_t n_dst, int64_t n_src,
+                           int64_t n_edges, int H, int D, int dtype, void* ws, size_t ws_bytes,
+                           void* stream) {
+  (void)col;
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(dtype_bytes(dtype) != 0, "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)",
+              dtype);
+  if (!gat_heads_ok(H, D)) {
+    set_error("unsupported GAT shape H=%d D=%d", H, D);
+    return TGX_UNSUPPORTED;
+  }
+  // One gradient buffer for both roles declares one feature tensor.
+  const bool homogeneous = dh_src == dh_dst;
+  TGX_REQUIRE(!homogeneous || (h_src == h_dst && n_src == n_dst),
+              "one gradient for both roles (dh_src == dh_dst) needs one feature tensor "
+              "(h_src == h_dst) and n_src == n_dst");
+  int st = check_plan(plan, n_dst);
+  if (st != TGX_OK) return st;
+  st = check_plan(plan_t, n_src);
+  if (st != TGX_OK) return st;
+  if (n_dst == 0 && n_src == 0) return TGX_OK;
+  TGX_REQUIRE(row_ptr && h_src && h_dst && a_src && a_dst && out && ns && dout && dh_src &&
+                  dh_dst && da_src && da_dst,
+              "null pointer");
+  TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && inv_perm), "null transposed CSR");
+  TGX_REQUIRE(n_src < (int64_t{1} << 31) && n_dst < (int64_t{1} << 31),
+              "node tables need fewer than 2^31 rows");
+  const size_t need =
+      gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype).bytes;
+  TGX_REQUIRE(ws && ws_bytes >= need, "workspace too small: need %zu bytes", need);
+  hipStream_t s = as_stream(stream);
+  const GatBwdIo io{h_src, h_dst, out, dout, a_src, a_dst, dh_src, dh_dst, ns, da_src, da_dst,
+                    n_dst, n_src, static_cast<int64_t>(H) * D, 4 * static_cast<int64_t>(H),
+                    slope};
+  char* w = static_cast<char*>(ws);
+  switch (dtype) {
+    case TGX_DTYPE_F32:
+      return gat_bwd_dtype<TGX_DTYPE_F32>(row_ptr, idx_bits, plan, row_ptr_t, col_t, perm,
+                                          inv_perm, plan_t, io, n_edges, H, D, w, s);
+    case TGX_DTYPE_BF16:
+      return gat_bwd_dtype<TGX_DTYPE_BF16>(row_ptr, idx_bits, plan, row_ptr_t, col_t, perm,
+                                           inv_perm, plan_t, io, n_edges, H, D, w, s);
+    default:
+      return gat_bwd_dtype<TGX_DTYPE_F16>(row_ptr, idx_bits, plan, row_ptr_t, col_t, perm,
+                                          inv_perm, plan_t, io, n_edges, H, D, w, s);
+  }
 }

@@ -85,20 +85,20 @@ _SIGNATURES: dict[str, list] = {
                         c_i64, c_i64, c_i64, c_int, c_vp, c_vp],
     "tgx_csr_edge_dot": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                          c_int, c_vp],
-    "tgx_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
-                    c_i64, c_int, c_int, c_vp, c_vp],
-    "tgx_gat_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, P(c_size)],
+    "tgx_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_f32, c_vp,
+                    c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_vp],
+    "tgx_gat_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, c_int, P(c_size)],
     "tgx_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, P(RowPlan), c_vp,
-                    c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
-                    c_int, c_int, c_vp, c_size, c_vp],
+                    c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
+                    c_i64, c_i64, c_int, c_int, c_int, c_vp, c_size, c_vp],
     "tgx_dot_attn_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_f32, c_vp,
-                         c_vp, c_i64, c_i64, c_int, c_int, c_vp, c_vp],
+                         c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_vp],
     "tgx_dot_attn_fwd_noalloc": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp,
-                                 c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_vp],
+                                 c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp],
     "tgx_dot_attn_bwd_workspace": [P(RowPlan), P(RowPlan), c_int, c_int, P(c_size)],
     "tgx_dot_attn_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, P(RowPlan), c_vp,
                          c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
-                         c_i64, c_i64, c_int, c_int, c_vp, c_size, c_vp],
+                         c_i64, c_i64, c_int, c_int, c_int, c_vp, c_size, c_vp],
     "tgx_attn_tasks": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp, P(c_i64)],
     "tgx_attn_fwd": [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_vp, c_vp, c_vp, P(c_i64),
                      c_f32, c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_vp],
@@ -137,16 +137,16 @@ _SIGNATURES: dict[str, list] = {
                             c_i64, c_i64, c_int],
     "tgx_cpu_csr_edge_dot": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64,
                              c_i64, c_int],
-    "tgx_cpu_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_f32, c_vp, c_vp,
-                        c_i64, c_int, c_int],
+    "tgx_cpu_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_f32, c_vp,
+                        c_vp, c_i64, c_i64, c_int, c_int, c_int],
     "tgx_cpu_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, P(RowPlan),
-                        c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
-                        c_i64, c_int, c_int],
+                        c_vp, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                        c_i64, c_i64, c_i64, c_int, c_int, c_int],
     "tgx_cpu_dot_attn_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_f32,
-                             c_vp, c_vp, c_i64, c_i64, c_int, c_int],
+                             c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_int],
     "tgx_cpu_dot_attn_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, P(RowPlan),
                              c_vp, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
-                             c_vp, c_i64, c_i64, c_int, c_int],
+                             c_vp, c_i64, c_i64, c_int, c_int, c_int],
     "tgx_cpu_attn_fwd": [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, P(c_i64), c_f32,
                          c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int],
     "tgx_cpu_attn_bwd": [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_vp, c_vp, P(c_i64), c_vp,

@@ -166,64 +166,80 @@ class CsrSumFunction(torch.autograd.Function):
 
 
 class GatFunction(torch.autograd.Function):
-    """GAT additive attention: h [N, H, D] fp32, a_src/a_dst [H, D]."""
+    """GAT additive attention: source features h_src [Ns, H, D] and
+    destination features h_dst [Nd, H, D] (None: h_src serves both roles of
+    a homogeneous relation) of one element type (fp32, bf16 or fp16; fp32
+    arithmetic, outputs in that type), a_src/a_dst fp32 [H, D]."""
 
     @staticmethod
-    def forward(ctx, h: torch.Tensor, a_src: torch.Tensor, a_dst: torch.Tensor,
+    def forward(ctx, h_src: torch.Tensor, h_dst, a_src: torch.Tensor, a_dst: torch.Tensor,
                 slope: float, graph: Graph):
-        _on_graph_device(graph, h, a_src, a_dst)
+        _on_graph_device(graph, h_src, h_dst, a_src, a_dst)
         row_ptr, col_idx = graph._kernel_csr()
-        N, H, D = h.shape
-        hc = h.contiguous()
-        asc = a_src.reshape(H, D).contiguous()
-        adc = a_dst.reshape(H, D).contiguous()
-        out = torch.empty_like(hc)
-        ns = torch.empty((N, H, 4), dtype=torch.float32, device=h.device)
+        n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
+        _, H, D = h_src.shape
+        hs = _aligned(h_src)
+        hd = hs if h_dst is None else _aligned(h_dst)
+        asc = _aligned(a_src.reshape(H, D))
+        adc = _aligned(a_dst.reshape(H, D))
+        out = torch.empty((n_dst, H, D), dtype=hs.dtype, device=hs.device)
+        ns = torch.empty((n_dst, H, 4), dtype=torch.float32, device=hs.device)
         plan = graph._row_plan()
-        partial = _partial(plan, H * D + 2 * H, h.device)
+        partial = _partial(plan, H * D + 2 * H, hs.device)
         _native.call("tgx_gat_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
-                     _native.idx_bits(row_ptr), plan.ref, hc.data_ptr(), asc.data_ptr(),
-                     adc.data_ptr(), float(slope), out.data_ptr(), ns.data_ptr(), N, H, D,
-                     _p(partial), _native.stream_of(h))
+                     _native.idx_bits(row_ptr), plan.ref, hs.data_ptr(), hd.data_ptr(),
+                     asc.data_ptr(), adc.data_ptr(), float(slope), out.data_ptr(),
+                     ns.data_ptr(), n_dst, n_src, H, D, _VALUE_DTYPES[hs.dtype], _p(partial),
+                     _native.stream_of(hs))
         ctx.graph = graph
         ctx.slope = float(slope)
         ctx.a_shapes = (a_src.shape, a_dst.shape)
-        ctx.save_for_backward(hc, asc, adc, out, ns)
+        ctx.bipartite = h_dst is not None
+        ctx.save_for_backward(hs, hd, asc, adc, out, ns)
         return out
 
     @staticmethod
     def backward(ctx, dout: torch.Tensor):
-        hc, asc, adc, out, ns = ctx.saved_tensors
+        hs, hd, asc, adc, out, ns = ctx.saved_tensors
         graph: Graph = ctx.graph
         row_ptr, col_idx = graph._kernel_csr()
-        N, H, D = hc.shape
+        n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
+        _, H, D = hs.shape
         E = graph.num_edges
-        dout = dout.contiguous()
-        dh = torch.empty_like(hc)
-        da_src = torch.empty((H, D), dtype=torch.float32, device=hc.device)
-        da_dst = torch.empty((H, D), dtype=torch.float32, device=hc.device)
+        dout = _aligned(dout.to(hs.dtype))
+        dh_src = torch.empty_like(hs)
+        dh_dst = torch.empty_like(hd) if ctx.bipartite else dh_src
+        da_src = torch.empty((H, D), dtype=torch.float32, device=hs.device)
+        da_dst = torch.empty((H, D), dtype=torch.float32, device=hs.device)
         plan = graph._row_plan()
         t = graph._transposed()
+        code = _VALUE_DTYPES[hs.dtype]
         ws_bytes = ctypes.c_size_t()
-        _native.call("tgx_gat_bwd_workspace", plan.ref, t.plan.ref, E, H, D,
+        _native.call("tgx_gat_bwd_workspace", plan.ref, t.plan.ref, E, H, D, code,
                      ctypes.byref(ws_bytes))
-        ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=hc.device)
+        ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=hs.device)
         # Slot 1 of the saved node state is backward scratch (delta); it is
         # rewritten by every backward before it is read.
         _native.call("tgx_gat_bwd", row_ptr.data_ptr(), col_idx.data_ptr(),
                      _native.idx_bits(row_ptr), plan.ref, t.row_ptr_t.data_ptr(),
                      t.col_t.data_ptr(), t.perm.data_ptr(), t.inv_perm.data_ptr(),
-                     t.plan.ref, hc.data_ptr(),
-                     asc.data_ptr(), adc.data_ptr(), ctx.slope, out.data_ptr(),
-                     ns.data_ptr(), dout.data_ptr(), dh.data_ptr(), da_src.data_ptr(),
-                     da_dst.data_ptr(), N, E, H, D, ws.data_ptr(), ws_bytes.value,
-                     _native.stream_of(hc))
-        return (dh, da_src.reshape(ctx.a_shapes[0]), da_dst.reshape(ctx.a_shapes[1]),
-                None, None)
+                     t.plan.ref, hs.data_ptr(), hd.data_ptr(), asc.data_ptr(), adc.data_ptr(),
+                     ctx.slope, out.data_ptr(), ns.data_ptr(), dout.data_ptr(),
+                     dh_src.data_ptr(), dh_dst.data_ptr(), da_src.data_ptr(),
+                     da_dst.data_ptr(), n_dst, n_src, E, H, D, code, ws.data_ptr(),
+                     ws_bytes.value, _native.stream_of(hs))
+        return (dh_src, dh_dst if ctx.bipartite else None, da_src.reshape(ctx.a_shapes[0]),
+                da_dst.reshape(ctx.a_shapes[1]), None, None)
+
+
+# Element types of the CSR dot-product and GAT kernels (TGX_DTYPE_*).
+_VALUE_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
 class DotAttnFunction(torch.autograd.Function):
-    """Dot-product attention, bf16 q [Nd,H,D], k/v [Ns,H,D], bias [E,H] fp32."""
+    """Dot-product attention: q [Nd,H,D], k/v [Ns,H,D] of one element type
+    (bf16, fp16 or fp32; fp32 arithmetic, output in that type), bias [E,H]
+    fp32."""
 
     @staticmethod
     def forward(ctx, q, k, v, bias, scale: float, graph: Graph):
@@ -231,7 +247,7 @@ class DotAttnFunction(torch.autograd.Function):
         row_ptr, col_idx = graph._kernel_csr()
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
         _, H, D = q.shape
-        qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+        qc, kc, vc = _aligned(q), _aligned(k), _aligned(v)
         bc = None if bias is None else bias.contiguous()
         out = torch.empty_like(qc)
         ml = torch.empty((n_dst, H, 2), dtype=torch.float32, device=q.device)
@@ -240,7 +256,8 @@ class DotAttnFunction(torch.autograd.Function):
         _native.call("tgx_dot_attn_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
                      _native.idx_bits(row_ptr), plan.ref, qc.data_ptr(), kc.data_ptr(),
                      vc.data_ptr(), _p(bc), float(scale), out.data_ptr(), ml.data_ptr(),
-                     n_dst, n_src, H, D, _p(partial), _native.stream_of(q))
+                     n_dst, n_src, H, D, _VALUE_DTYPES[qc.dtype], _p(partial),
+                     _native.stream_of(q))
         ctx.graph = graph
         ctx.scale = float(scale)
         ctx.has_bias = bias is not None
@@ -255,9 +272,7 @@ class DotAttnFunction(torch.autograd.Function):
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
         _, H, D = qc.shape
         E = graph.num_edges
-        dout = dout.contiguous()
-        if dout.dtype != qc.dtype:
-            dout = dout.to(qc.dtype)
+        dout = _aligned(dout.to(qc.dtype))
         dq = torch.empty_like(qc)
         dk = torch.empty_like(kc)
         dv = torch.empty_like(vc)
@@ -275,8 +290,8 @@ class DotAttnFunction(torch.autograd.Function):
                      t.col_t.data_ptr(), t.perm.data_ptr(), t.plan.ref, qc.data_ptr(),
                      kc.data_ptr(), vc.data_ptr(), _p(bc), ctx.scale, out.data_ptr(),
                      ml.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(),
-                     dv.data_ptr(), _p(dbias), n_dst, n_src, H, D, ws.data_ptr(),
-                     ws_bytes.value, _native.stream_of(qc))
+                     dv.data_ptr(), _p(dbias), n_dst, n_src, H, D, _VALUE_DTYPES[qc.dtype],
+                     ws.data_ptr(), ws_bytes.value, _native.stream_of(qc))
         return dq, dk, dv, dbias, None, None
 
 

@@ -560,42 +560,52 @@ class MessagePassing(Kernel):
         return _Launch(graph, tuple(operands), run, describe, bind=bind)
 
     def _plan_gat(self, gat, graph, src, dst, params) -> _Launch | None:
+        """The additive score on one feature tensor (src.h is dst.h) or two
+        (bipartite src and dst tables of one shape per node), fp32, bf16 or
+        fp16 features with fp32 arithmetic, any float a_src / a_dst (read as
+        fp32); the reference evaluates it eagerly (reducer_oracle.py:60-137)."""
         from . import _ops
 
         if graph.is_varlen or graph.is_dense:
             return None
         h = src.get(gat.h_field)
         hd = dst.get(gat.dst_field)
-        if h is None or hd is None or hd is not h:
-            return None
-        if graph.schema.num_src != graph.schema.num_dst or h.ndim != 3:
+        if h is None or hd is None or h.ndim != 3 or hd.ndim != 3:
             return None
         N, H, D = h.shape
-        if h.dtype != torch.float32 or tuple(gat.a_src.shape) not in ((H, D), (1, H, D)) \
+        if hd.shape[1:] != h.shape[1:] or hd.dtype != h.dtype or \
+                h.dtype not in _ops._VALUE_DTYPES:
+            return None
+        if tuple(gat.a_src.shape) not in ((H, D), (1, H, D)) \
                 or tuple(gat.a_dst.shape) not in ((H, D), (1, H, D)):
             return None
-        if gat.a_src.dtype != torch.float32 or gat.a_dst.dtype != torch.float32:
+        if not (gat.a_src.is_floating_point() and gat.a_dst.is_floating_point()):
             return None
         if gat.a_src.device != h.device or gat.a_dst.device != h.device:
             return None
         # Any head count: the kernels run heads in groups of at most 256
-        # floats per node; the head width is 4 * 2^k floats, up to 256.
+        # values per node; the head width is 4 * 2^k values, up to 256.
         if D % 4 or D > 256 or (D // 4) & (D // 4 - 1):
             return None
         _native.lib()
         slope = gat.slope
 
-        def run(h, _h_dst, a_src, a_dst):
-            return _ops.GatFunction.apply(h, a_src, a_dst, slope, graph)
+        def run(h, h_dst, a_src, a_dst):
+            # One tensor object in both roles is a homogeneous relation; the
+            # kernels read fp32 attention vectors (a no-op for fp32).
+            return _ops.GatFunction.apply(h, None if h_dst is h else h_dst,
+                                          a_src.to(torch.float32), a_dst.to(torch.float32),
+                                          slope, graph)
 
+        kind = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}[h.dtype]
+        roles = "one feature table" if hd is h else "source and destination tables"
         describe = lambda: self._variant(
             graph, "gat-additive", ("tgx_gat_fwd", "tgx_gat_bwd"),
-            "online softmax per (row, head), logsumexp saved; backward recomputes alpha "
-            "over the transposed CSR")
+            f"{kind} {roles}, online softmax per (row, head), logsumexp saved; backward "
+            "recomputes alpha over the transposed CSR")
         operands = (("src", gat.h_field), ("dst", gat.dst_field),
                     self._binding(gat.a_src, params), self._binding(gat.a_dst, params))
-        return _Launch(graph, operands, run, describe,
-                       aliases=((("src", gat.h_field), ("dst", gat.dst_field)),))
+        return _Launch(graph, operands, run, describe)
 
     @staticmethod
     def _nn_fields(inputs, graph, src, dst, edge):
@@ -742,7 +752,11 @@ class MessagePassing(Kernel):
         if graph.is_varlen or graph.is_dense:
             return self._plan_block_attention(dot, graph, q, k, v)
         _, H, D = q.shape
-        if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+        # bf16, fp16 or fp32 q, k, v of one type: fp32 scores, softmax and
+        # sums, the output in that type (the reference's eager path
+        # accumulates 16-bit scores in fp32 and casts back to the value's
+        # dtype, reducer_oracle.py:22-41, 137).
+        if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _ops._VALUE_DTYPES:
             return None
         # Any head count: the kernels run heads in groups of at most 512
         # values per node; the head width is 8 * 2^k values, up to 512.
@@ -751,7 +765,7 @@ class MessagePassing(Kernel):
         operands = [("dst", dot.q_field), ("src", dot.k_field), ("src", dot.v_field)]
         if dot.bias_field is not None:
             bias = edge.get(dot.bias_field)
-            if bias is None or bias.dtype != torch.float32:
+            if bias is None or bias.dtype not in _ops._VALUE_DTYPES:
                 return None
             if tuple(bias.shape) not in ((graph.num_edges, H), (graph.num_edges, H, 1)):
                 return None
@@ -761,12 +775,15 @@ class MessagePassing(Kernel):
 
         def run(q, k, v, bias=None):
             if bias is not None:
-                bias = bias.reshape(E, H)
+                # The kernels read an fp32 bias (a differentiable no-op for
+                # fp32; a 16-bit bias widens exactly).
+                bias = bias.reshape(E, H).to(torch.float32)
             return _ops.DotAttnFunction.apply(q, k, v, bias, scale, graph)
 
+        kind = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}[q.dtype]
         describe = lambda: self._variant(
             graph, "dot-product", ("tgx_dot_attn_fwd", "tgx_dot_attn_bwd"),
-            "bf16 gathers, fp32 online softmax per (row, head); hub rows split and merged; "
+            f"{kind} gathers, fp32 online softmax per (row, head); hub rows split and merged; "
             "backward over CSR (dq, dbias) and transposed CSR (dk, dv)")
         return _Launch(graph, tuple(operands), run, describe)
 
