@@ -634,6 +634,28 @@ int tgx_edge_mlp_backward(const void* col_dev, const int32_t* dst_index_dev, int
                           float* dweights_dev, float* const* dseg, void* workspace_dev,
                           size_t workspace_bytes, void* stream);
 
+/* The backward of online-softmax attention over the network's score
+ *   out[i] = sum_e softmax_i(net(fields_e)) value[col[e]]
+ * from what its forward keeps per row only: lse [n_dst] (logsumexp of each
+ * row's scores, tgx_segment_softmax_fwd) and out [n_dst, value_width];
+ * dout [n_dst, value_width], value [n_src, value_width], all fp32 (rows of a
+ * multiple of 4 floats 16-byte aligned).  Per edge the kernel replays the
+ * network, recomputes alpha = exp(s - lse[i]) and forms the score gradient
+ * ds = alpha (<dout[i], value[j]> - <dout[i], out[i]>) itself (no per-edge
+ * score, weight or score gradient is read), then writes dseg and dweights
+ * as tgx_edge_mlp_backward does, and alpha [n_edges] (fp32, edge order) for
+ * the value gradient (tgx_csr_sum_bwd with alpha as the weights).  The
+ * reference's fused edge-attention backward recomputes the weights from the
+ * row's (m, l) the same way (compiler/edge_nn_attention.py:344-611).
+ * Workspace: tgx_edge_mlp_backward_workspace. */
+int tgx_edge_mlp_attention_backward(const void* col_dev, const int32_t* dst_index_dev,
+                                    int idx_bits, int64_t n_edges, const tgx_edge_mlp* mlp,
+                                    const float* lse_dev, const float* out_dev,
+                                    const float* dout_dev, const float* value_dev,
+                                    int32_t value_width, float* alpha_dev, float* dweights_dev,
+                                    float* const* dseg_dev, void* workspace_dev,
+                                    size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Per-kernel timing (no reference counterpart; used by the benchmark)       */
 /* ------------------------------------------------------------------------ */

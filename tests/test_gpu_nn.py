@@ -139,6 +139,33 @@ def test_reference_gat_example_shape():
           dict(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp}), dout)
 
 
+def test_attention_keeps_no_per_edge_weights():
+    """The forward keeps per destination row only its logsumexp and output:
+    beside the caller's own per-edge fields, no [E] score, weight or score
+    gradient is saved for the backward, which recomputes them per edge."""
+    print("nn attention saved state", flush=True)
+    torch.manual_seed(1)
+    nodes, f_in = 700, 8
+    rp, col = random_graph(nodes, nodes, 9, 3, hub=200)
+    graph = tg.Graph.from_csr(rp, col, num_src=nodes)
+    E = graph.num_edges
+    disp = torch.randn(E, 3, device=DEV, requires_grad=True)
+    x = torch.randn(nodes, f_in, device=DEV, requires_grad=True)
+    attn = nn.Sequential(nn.Linear(3 + 2 * f_in, 16), nn.LeakyReLU(0.2),
+                         nn.Linear(16, 1)).to(DEV)
+    kernel = GAT(attn)
+    out = kernel(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp})
+    assert kernel.last_variant.backend == "hip"
+    saved = out.grad_fn.saved_tensors
+    per_edge = [tuple(t.shape) for t in saved
+                if t.ndim >= 1 and t.shape[0] == E and t.data_ptr() != disp.data_ptr()]
+    assert per_edge == [], per_edge
+    assert any(tuple(t.shape) == (nodes,) for t in saved)      # the row logsumexp
+    dout = torch.randn(nodes, f_in, device=DEV)
+    check(graph, kernel, attn, [("edge", disp), ("src", x), ("dst", x)], x,
+          dict(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp}), dout)
+
+
 @pytest.mark.parametrize("width,acts,hub", [
     (12, ("tanh",), 0),                       # W = 16, two layers
     (40, ("gelu", "silu"), 300),               # W = 64, three layers, hub row > 64 edges

@@ -633,10 +633,13 @@ struct GatBwdLayout {
   int64_t src_waves, dst_waves;
 };
 
-// Workspace of one head group; dh_acc (fp32 [n_dst, H*D]) only for 16-bit
-// elements, where a homogeneous relation's dh waits there between passes.
+// Workspace of one head group of H heads out of H_total.  dh_acc, only for
+// 16-bit elements (where a homogeneous relation's dh waits there between
+// passes), comes first and spans whole rows, [n_dst, H_total * D] fp32: the
+// kernels index it with the row stride of dh itself, each head group at its
+// own column offset.
 GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t,
-                            int64_t n_edges, int H, int D, int dtype) {
+                            int64_t n_edges, int H, int D, int dtype, int H_total) {
   GatBwdLayout L;
   const int64_t HD = static_cast<int64_t>(H) * D;
   // Partial buffers are sized for the largest grid; launches may use fewer.
@@ -647,6 +650,8 @@ GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t
   if (L.src_waves < L.dst_waves) L.src_waves = L.dst_waves;
   const int64_t nodes = plan.n_rows > plan_t.n_rows ? plan.n_rows : plan_t.n_rows;
   Carve c{nullptr, 0};
+  L.dh_acc_off = reinterpret_cast<size_t>(c.take<float>(
+      dtype == TGX_DTYPE_F32 ? 0 : plan.n_rows * static_cast<int64_t>(H_total) * D));
   L.dz_off = reinterpret_cast<size_t>(c.take<float>(n_edges * H));
   L.sdz_off = reinterpret_cast<size_t>(c.take<float>(nodes * H));
   L.src_part_off = reinterpret_cast<size_t>(c.take<float>(plan_t.n_chunks * (HD + H)));
@@ -654,8 +659,6 @@ GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t
   L.dap_src_off = reinterpret_cast<size_t>(c.take<double>(L.src_waves * HD));
   L.dap_dst_off = reinterpret_cast<size_t>(c.take<double>(L.dst_waves * HD));
   L.slices_off = reinterpret_cast<size_t>(c.take<double>(2 * kDaSlices * HD));
-  L.dh_acc_off = reinterpret_cast<size_t>(
-      c.take<float>(dtype == TGX_DTYPE_F32 ? 0 : plan.n_rows * HD));
   L.bytes = align_up(c.used);
   return L;
 }
@@ -667,6 +670,7 @@ struct GatBwdIo {
   float *ns, *da_src, *da_dst;
   int64_t n_dst, n_src, ld, nsld;
   float slope;
+  int64_t col_off;   // the head group's first column (h0 * D) within a row
 };
 
 template <int DT, typename I, int G, int HL>
@@ -691,8 +695,9 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
   // the destination pass, in place for fp32, in fp32 workspace otherwise.
   float* dh_acc = nullptr;
   if (homogeneous)
-    dh_acc = DT == TGX_DTYPE_F32 ? static_cast<float*>(io.dhd)
-                                 : reinterpret_cast<float*>(ws + L.dh_acc_off);
+    dh_acc = DT == TGX_DTYPE_F32
+                 ? static_cast<float*>(io.dhd)
+                 : reinterpret_cast<float*>(ws + L.dh_acc_off) + io.col_off;
   const T* hs = static_cast<const T*>(io.hs);
   const T* hd = static_cast<const T*>(io.hd);
   const PlanView pv = plan_view(plan), pt = plan_view(plan_t);
@@ -820,9 +825,10 @@ int gat_bwd_dtype(const void* row_ptr, int idx_bits, const tgx_row_plan* plan,
   for (int h0 = 0; h0 < H;) {
     const int hg = gat_group_heads(H, D, h0);
     const GatShape shp = gat_shape(hg, D);
-    const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, hg, D, DT);
+    const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, hg, D, DT, H);
     const int64_t off = static_cast<int64_t>(h0) * D;
     GatBwdIo io = all;
+    io.col_off = off;
     io.hs = at(all.hs, off);
     io.hd = at(all.hd, off);
     io.out = at(all.out, off);
@@ -907,7 +913,8 @@ extern "C" int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_pla
   }
   // Head groups run one after another on one stream and share the
   // workspace; the first group is the widest.
-  *bytes = gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype).bytes;
+  *bytes =
+      gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype, H).bytes;
   return TGX_OK;
 }
 
@@ -945,12 +952,12 @@ extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
   TGX_REQUIRE(n_src < (int64_t{1} << 31) && n_dst < (int64_t{1} << 31),
               "node tables need fewer than 2^31 rows");
   const size_t need =
-      gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype).bytes;
+      gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype, H).bytes;
   TGX_REQUIRE(ws && ws_bytes >= need, "workspace too small: need %zu bytes", need);
   hipStream_t s = as_stream(stream);
   const GatBwdIo io{h_src, h_dst, out, dout, a_src, a_dst, dh_src, dh_dst, ns, da_src, da_dst,
                     n_dst, n_src, static_cast<int64_t>(H) * D, 4 * static_cast<int64_t>(H),
-                    slope};
+                    slope, 0};
   char* w = static_cast<char*>(ws);
   switch (dtype) {
     case TGX_DTYPE_F32:

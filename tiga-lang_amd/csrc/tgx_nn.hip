@@ -366,6 +366,7 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
       for (int k = 0; k < W; ++k) y[k] = z[l][k];
     };
     const int64_t cur_dst = next_dst;
+    const int64_t cur_src = next_src;
     if (valid) {
       gather_rows<W>(m, e, next_src, next_dst, x);
     } else {
@@ -412,11 +413,20 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
 #pragma unroll
       for (int k = 0; k < W; ++k) g[k] = (valid && k < hw) ? q[k] : 0.f;
     } else {
-      // Last layer: one output, gradient ds (0 on lanes past the range).
-      const float ds = valid ? dscore[e] : 0.f;
+      // Last layer: one output, gradient ds (0 on lanes past the range):
+      // read, or formed here from the replayed score (attention backward
+      // from the saved logsumexp).
       cfloat* wl = wg + (L - 1) * nw;
       float a[W];
       layer_input(std::integral_constant<int, L - 1>{}, a);
+      float ds = 0.f;
+      if (m.att_lse != nullptr) {
+        if (valid)
+          ds = attention_score_grad(m, e, cur_dst, cur_src,
+                                    linear_out1<W>(wl, a, m.nb_in[L - 1]));
+      } else if (valid) {
+        ds = dscore[e];
+      }
       // One output row: its gradient ds a is summed per lane (an MFMA outer
       // product would spend a 32 x 32 tile on it).
       last_b += ds;
@@ -955,18 +965,15 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward_workspace)(int64_t n_edges, const tgx_edge_ml
   return TGX_OK;
 }
 
-TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, int idx_bits,
-                                    int64_t n_edges, const tgx_edge_mlp* mlp,
-                                    const float* dscore, float* dweights, float* const* dseg,
-                                    void* workspace, size_t workspace_bytes, void* stream) {
-  TGX_TO_MATH(mlp, tgx_edge_mlp_backward_math(col, dst_index, idx_bits, n_edges, mlp, dscore,
-                                              dweights, dseg, workspace, workspace_bytes,
-                                              stream));
-  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
-  TGX_REQUIRE(n_edges >= 0, "negative size");
-  MlpView v;
-  int st = check_mlp(mlp, &v, n_edges > 0);
-  if (st != TGX_OK) return st;
+namespace {
+
+// The backward of a one-output chain for a checked view `v`: the score
+// gradients come from dscore, or are formed per edge from v's attention
+// fields (dscore null).
+int mlp_backward_body(const void* col, const int32_t* dst_index, int idx_bits, int64_t n_edges,
+                      const tgx_edge_mlp* mlp, MlpView& v, const float* dscore,
+                      float* dweights, float* const* dseg, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   TGX_REQUIRE(dweights && dseg, "null pointer");
   const int n = mlp->n_layers * block_floats(mlp);
   hipStream_t s = as_stream(stream);
@@ -976,7 +983,7 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, i
     TGX_LAUNCHED("colsum_final_kernel");
     return TGX_OK;
   }
-  TGX_REQUIRE(col && dst_index && dscore && workspace, "null pointer");
+  TGX_REQUIRE(col && dst_index && (dscore || v.att_lse) && workspace, "null pointer");
   for (int k = 0; k < mlp->n_segments; ++k) {
     TGX_REQUIRE(dseg[k], "null gradient for segment %d", k);
     v.grad[k] = dseg[k];
@@ -998,8 +1005,9 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, i
     const size_t plane = align_up(static_cast<size_t>(mlp->n_layers) * n_edges * 64 * sizeof(float));
     float* acts = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes + slice_bytes);
     float* dz = reinterpret_cast<float*>(reinterpret_cast<char*>(acts) + plane);
-    st = tgx::mlp::TGX_TIER(planes_backward)(mlp->n_layers, idx_bits, col, dst_index, n_edges, v, dscore,
-                                   acts, dz, blocks, chunk, partial, s);
+    const int st = tgx::mlp::TGX_TIER(planes_backward)(mlp->n_layers, idx_bits, col, dst_index,
+                                                       n_edges, v, dscore, acts, dz, blocks,
+                                                       chunk, partial, s);
     if (st != TGX_OK) return st;
   } else {
     TGX_PROFILE("edge_mlp_bwd_kernel", s);
@@ -1022,6 +1030,57 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, i
     TGX_LAUNCHED("colsum_final_kernel");
   }
   return TGX_OK;
+}
+
+}  // namespace
+
+TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, int idx_bits,
+                                    int64_t n_edges, const tgx_edge_mlp* mlp,
+                                    const float* dscore, float* dweights, float* const* dseg,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  TGX_TO_MATH(mlp, tgx_edge_mlp_backward_math(col, dst_index, idx_bits, n_edges, mlp, dscore,
+                                              dweights, dseg, workspace, workspace_bytes,
+                                              stream));
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(n_edges >= 0, "negative size");
+  MlpView v;
+  const int st = check_mlp(mlp, &v, n_edges > 0);
+  if (st != TGX_OK) return st;
+  TGX_REQUIRE(n_edges == 0 || dscore, "null pointer");
+  return mlp_backward_body(col, dst_index, idx_bits, n_edges, mlp, v, dscore, dweights, dseg,
+                           workspace, workspace_bytes, stream);
+}
+
+TGX_NN_ENTRY(tgx_edge_mlp_attention_backward)(
+    const void* col, const int32_t* dst_index, int idx_bits, int64_t n_edges,
+    const tgx_edge_mlp* mlp, const float* lse, const float* out, const float* dout,
+    const float* value, int32_t value_width, float* alpha, float* dweights, float* const* dseg,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  TGX_TO_MATH(mlp, tgx_edge_mlp_attention_backward_math(
+                       col, dst_index, idx_bits, n_edges, mlp, lse, out, dout, value,
+                       value_width, alpha, dweights, dseg, workspace, workspace_bytes, stream));
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(n_edges >= 0, "negative size");
+  TGX_REQUIRE(value_width >= 1, "value_width must be >= 1");
+  MlpView v;
+  const int st = check_mlp(mlp, &v, n_edges > 0);
+  if (st != TGX_OK) return st;
+  if (n_edges > 0) {
+    TGX_REQUIRE(lse && out && dout && value && alpha, "null pointer");
+    if (value_width % 4 == 0)
+      TGX_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(dout) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(value) % 16 == 0,
+                  "out, dout and value rows of a multiple of 4 floats need 16-byte alignment");
+  }
+  v.att_lse = lse;
+  v.att_out = out;
+  v.att_dout = dout;
+  v.att_value = value;
+  v.att_alpha = alpha;
+  v.att_width = value_width;
+  return mlp_backward_body(col, dst_index, idx_bits, n_edges, mlp, v, nullptr, dweights, dseg,
+                           workspace, workspace_bytes, stream);
 }
 
 #if !TGX_NN_MATH

@@ -56,6 +56,17 @@ struct MlpView {
   int norm[kMaxLayers];
   float eps[kMaxLayers];
   int nw;
+  // Backward of online-softmax attention over the chain's one-output score
+  // when the forward kept only each row's logsumexp (att_lse non-null): the
+  // kernels form each edge's score gradient themselves (attention_score_grad)
+  // instead of reading it.  Rows of att_out / att_dout (destinations) and
+  // att_value (sources) hold att_width floats.
+  const float* att_lse;
+  const float* att_out;
+  const float* att_dout;
+  const float* att_value;
+  float* att_alpha;       // [n_edges]: the recomputed weights, for the value gradient
+  int att_width;
 };
 
 // Floats per layer of a chain's weight (and weight-gradient) blocks.
@@ -181,6 +192,39 @@ __device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const
   }
   gather_rows<W>(m, e, need_src ? static_cast<int64_t>(col[e]) : 0,
                  need_dst ? static_cast<int64_t>(dst[e]) : 0, x);
+}
+
+// Score gradient of edge e (destination row i, source row j) of an
+// online-softmax attention out[i] = sum_e alpha_e value[j], from the
+// replayed score s:
+//   alpha = exp(s - lse[i]),  ds = alpha (<dout[i], value[j]> - <dout[i], out[i]>),
+// the softmax Jacobian with the row term <dout, out> = sum_e alpha dalpha
+// (the reference's edge-attention VJP, compiler/edge_nn_attention.py:
+// 569-575).  alpha is stored for the value gradient's transposed sum.
+__device__ __forceinline__ float attention_score_grad(const MlpView& m, int64_t e, int64_t i,
+                                                      int64_t j, float s) {
+  const float alpha = __expf(s - m.att_lse[i]);
+  const int F = m.att_width;
+  const float* d = m.att_dout + i * F;
+  const float* o = m.att_out + i * F;
+  const float* v = m.att_value + j * F;
+  float dv = 0.f, dd = 0.f;
+  if ((F & 3) == 0) {
+    for (int f = 0; f < F; f += 4) {
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(d + f);
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(v + f);
+      const f32x4 o4 = *reinterpret_cast<const f32x4*>(o + f);
+      dv += d4[0] * v4[0] + d4[1] * v4[1] + d4[2] * v4[2] + d4[3] * v4[3];
+      dd += d4[0] * o4[0] + d4[1] * o4[1] + d4[2] * o4[2] + d4[3] * o4[3];
+    }
+  } else {
+    for (int f = 0; f < F; ++f) {
+      dv += d[f] * v[f];
+      dd += d[f] * o[f];
+    }
+  }
+  m.att_alpha[e] = alpha;
+  return alpha * (dv - dd);
 }
 
 // q_s[e][k - off_s] = g[k] for every segment s (the per-edge input gradient
@@ -690,6 +734,11 @@ TGX_NN_HIDDEN int tgx_edge_mlp_backward_math(const void* col, const int32_t* dst
                                              float* dweights, float* const* dseg,
                                              void* workspace, size_t workspace_bytes,
                                              void* stream);
+TGX_NN_HIDDEN int tgx_edge_mlp_attention_backward_math(
+    const void* col, const int32_t* dst_index, int idx_bits, int64_t n_edges,
+    const tgx_edge_mlp* mlp, const float* lse, const float* out, const float* dout,
+    const float* value, int32_t value_width, float* alpha, float* dweights, float* const* dseg,
+    void* workspace, size_t workspace_bytes, void* stream);
 TGX_NN_HIDDEN int tgx_edge_mlp_hidden_math(const void* col, const int32_t* dst_index,
                                            int idx_bits, int64_t n_edges,
                                            const tgx_edge_mlp* mlp, float* hidden,

@@ -42,11 +42,15 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
                     m.n_out[l]);
     }
   });
-  // Last layer: one output, gradient ds.
-  const float ds = dscore[e];
+  // Last layer: one output, gradient ds: read, or formed here from the
+  // replayed score (attention backward from the saved logsumexp).
   float g[W];
   {
     cfloat* wl = wg + (L - 1) * (W * W + W);
+    const float ds = m.att_lse != nullptr
+                         ? attention_score_grad(m, e, dst[e], static_cast<int64_t>(col[e]),
+                                                linear_out1<W>(wl, a, m.nb_in[L - 1]))
+                         : dscore[e];
     float* out = dz_out + (L - 1) * plane + e * W;
 #pragma unroll
     for (int i = 0; i < W; i += 4)

@@ -118,6 +118,9 @@ _SIGNATURES: dict[str, list] = {
     "tgx_edge_mlp_backward_workspace": [c_i64, P(EdgeMlp), P(c_size)],
     "tgx_edge_mlp_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, P(c_vp),
                               c_vp, c_size, c_vp],
+    "tgx_edge_mlp_attention_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, c_vp,
+                                        c_vp, ctypes.c_int32, c_vp, c_vp, P(c_vp), c_vp,
+                                        c_size, c_vp],
     "tgx_edge_mlp_hidden": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, ctypes.c_int32, c_vp],
     "tgx_edge_mlp_backward_seeded": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp,
                                      ctypes.c_int32, c_vp, P(c_vp), c_vp, c_size, c_vp],

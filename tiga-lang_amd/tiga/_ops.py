@@ -678,12 +678,96 @@ class SegmentSoftmaxFunction(torch.autograd.Function):
         return dscore, None
 
 
+class NnAttentionFunction(torch.autograd.Function):
+    """out[i] = sum_e softmax_i(net(fields_e)) value[col[e]], fp32, with the
+    logsumexp-recompute backward.  The forward keeps per destination row only
+    the logsumexp of its scores and its output (no per-edge score or weight
+    outlives it); the backward replays the network per edge and forms alpha
+    and the score gradient in the same kernel
+    (tgx_edge_mlp_attention_backward), then sums the value gradient over the
+    transposed CSR with the recomputed weights.  The reference's fused
+    edge-attention keeps the same per-row state (m, l) and recomputes the
+    weights in its VJP (compiler/edge_nn_attention.py:127-338, 344-611).
+
+    Inputs after (graph, chain, roles, n_seg): value [n_src, *F], the n_seg
+    field tensors, then per layer the Linear weight and bias and the
+    LayerNorm weight and bias (None allowed)."""
+
+    @staticmethod
+    def forward(ctx, graph: Graph, chain, roles, n_seg: int, value: torch.Tensor, *tensors):
+        _on_graph_device(graph, value, *tensors)
+        segs = [_as_rows(t) for t in tensors[:n_seg]]
+        params = tensors[n_seg:]
+        row_ptr, col_idx = graph._kernel_csr()
+        E, n_dst = col_idx.numel(), graph.schema.num_dst
+        W = _padded_width(chain, sum(s.shape[1] for s in segs))
+        dev = col_idx.device
+        buf = torch.zeros(len(chain), _block_floats(chain, W), dtype=torch.float32, device=dev)
+        _fill_weights(buf, chain, params, W, len(chain))
+        mlp = _mlp_struct(chain, roles, segs, buf, W)
+        stream = _native.stream_of(col_idx)
+        # Scores and weights live only for this forward.
+        scores = torch.empty(E, dtype=torch.float32, device=dev)
+        _native.call("tgx_edge_mlp_scores", col_idx.data_ptr(), graph._dst_index32().data_ptr(),
+                     _native.idx_bits(row_ptr), E, ctypes.byref(mlp), scores.data_ptr(), stream)
+        alpha = torch.empty_like(scores)
+        lse = torch.empty(max(n_dst, 1), dtype=torch.float32, device=dev)
+        _native.call("tgx_segment_softmax_fwd", row_ptr.data_ptr(), _native.idx_bits(row_ptr),
+                     n_dst, scores.data_ptr(), alpha.data_ptr(), lse.data_ptr(), stream)
+        del scores
+        out, vc, _, F = _csr_sum_launch(value, alpha, graph)
+        del alpha
+        ctx.graph, ctx.chain, ctx.roles, ctx.n_seg, ctx.W, ctx.F = graph, chain, roles, n_seg, W, F
+        ctx.shapes = [t.shape for t in tensors[:n_seg]]
+        ctx.present = [t is not None for t in params]
+        ctx.save_for_backward(buf, lse, out, vc, *segs)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        buf, lse, out, vc, *segs = ctx.saved_tensors
+        graph, chain, roles, W, F = ctx.graph, ctx.chain, ctx.roles, ctx.W, ctx.F
+        row_ptr, col_idx = graph._kernel_csr()
+        E, n_dst, n_src = col_idx.numel(), graph.schema.num_dst, graph.schema.num_src
+        dev = col_idx.device
+        L = len(chain)
+        g = _aligned(dout.to(torch.float32))
+        alpha = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
+        dsegs = [torch.empty(E, s.shape[1], dtype=torch.float32, device=dev) for s in segs]
+        mlp = _mlp_struct(chain, roles, segs, buf, W)
+        ws_bytes = ctypes.c_size_t()
+        _native.call("tgx_edge_mlp_backward_workspace", E, ctypes.byref(mlp),
+                     ctypes.byref(ws_bytes))
+        ws = torch.empty(max(ws_bytes.value, 4), dtype=torch.uint8, device=dev)
+        dweights = torch.empty(L, buf.shape[1], dtype=torch.float32, device=dev)
+        ptrs = (ctypes.c_void_p * 4)(*[d.data_ptr() for d in dsegs], *([None] * (4 - len(dsegs))))
+        stream = _native.stream_of(col_idx)
+        _native.call("tgx_edge_mlp_attention_backward", col_idx.data_ptr(),
+                     graph._dst_index32().data_ptr(), _native.idx_bits(row_ptr), E,
+                     ctypes.byref(mlp), lse.data_ptr(), out.data_ptr(), g.data_ptr(),
+                     vc.data_ptr(), F, alpha.data_ptr(), dweights.data_ptr(), ptrs,
+                     ws.data_ptr(), ws_bytes.value, stream)
+        dvalue = None
+        if ctx.needs_input_grad[4]:
+            dvalue = torch.empty_like(vc)
+            if n_src and F:
+                t = graph._transposed()
+                partial = _partial(t.plan, F, dev)
+                _native.call("tgx_csr_sum_bwd", t.row_ptr_t.data_ptr(), t.col_t.data_ptr(),
+                             t.perm.data_ptr(), t.plan.ref, vc.data_ptr(), alpha.data_ptr(),
+                             g.data_ptr(), dvalue.data_ptr(), None, n_dst, n_src, F,
+                             _native.DTYPE_F32, _p(partial), stream)
+        grads = _segment_grads(graph, roles, dsegs, ctx.shapes, ctx.needs_input_grad, 5)
+        grads += _layer_grads(chain, dweights, W, ctx.present, ctx.needs_input_grad,
+                              5 + ctx.n_seg, L)
+        return (None, None, None, None, dvalue, *grads)
+
+
 def nn_attention(graph: Graph, chain, roles, fields, value: torch.Tensor) -> torch.Tensor:
     """out[i] = sum_e softmax_i(net(fields_e)) value[col[e]] on the HIP path."""
     params = _layer_params(chain)
-    scores = EdgeMlpFunction.apply(graph, chain, tuple(roles), len(fields), *fields, *params)
-    alpha = SegmentSoftmaxFunction.apply(scores, graph)
-    return csr_sum(value, alpha, graph)
+    return NnAttentionFunction.apply(graph, chain, tuple(roles), len(fields), value, *fields,
+                                     *params)
 
 
 # ---------------------------------------------------------------------------

@@ -733,11 +733,12 @@ class MessagePassing(Kernel):
         describe = lambda: self._variant(
             graph, "nn-attention",
             ("tgx_edge_mlp_scores", "tgx_segment_softmax_fwd", "tgx_csr_sum_fwd",
-             "tgx_csr_sum_bwd", "tgx_segment_softmax_bwd", "tgx_edge_mlp_backward"),
+             "tgx_edge_mlp_attention_backward", "tgx_csr_sum_bwd"),
             f"edge-parallel score network {layer_widths} (one edge per lane, uniform "
-            "weights), segment softmax per row, weighted CSR sum of the value; backward "
-            "through the softmax Jacobian, per-edge network replay, on-chip weight-gradient "
-            "sums")
+            "weights), segment softmax per row, weighted CSR sum of the value; only each "
+            "row's logsumexp and output are kept; backward replays the network per edge, "
+            "recomputes the weights and the softmax Jacobian in the same kernel, on-chip "
+            "weight-gradient sums, value gradient over the transposed CSR")
         operands = (("fixed", item.module), ("src", item.value_field), *item.inputs)
         return _Launch(graph, operands, run, describe)
 
