@@ -54,7 +54,7 @@ class EdgeMlp(ctypes.Structure):
 
 
 # tgx_abi_version() of the library these signatures and structs mirror.
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 # name -> argtypes (all return int status except where noted)
