@@ -316,6 +316,9 @@ def attn_strides(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
 # it back instead of recomputing S and dP) when its workspace is at most this
 # many bytes; larger relations recompute (tgx_attn_bwd).
 STORED_DS_MAX_BYTES = 8 << 30
+# Keys per dK/dV workgroup of the attention backward (the key task lists of
+# tgx_attn_tasks, kind 1, are built with this block).
+ATTN_KEY_TILE = 64
 
 
 class BlockAttentionFunction(torch.autograd.Function):
@@ -370,7 +373,7 @@ class BlockAttentionFunction(torch.autograd.Function):
             dout = dout.to(q.dtype)
         strides = attn_strides(q, k, v)[3]   # saved tensors already have tile strides
         cu_q, cu_k, qtasks, nq, causal = graph._attn_tasks(0, 128, H)
-        _, _, ktasks, nk, _ = graph._attn_tasks(1, 64, H)
+        _, _, ktasks, nk, _ = graph._attn_tasks(1, ATTN_KEY_TILE, H)
         dq = torch.empty((n_q, H, D), dtype=q.dtype, device=q.device)
         dk = torch.empty((n_k, H, D), dtype=q.dtype, device=q.device)
         dv = torch.empty((n_k, H, D), dtype=q.dtype, device=q.device)
