@@ -643,18 +643,23 @@ int tgx_edge_mlp_backward(const void* col_dev, const int32_t* dst_index_dev, int
  * network, recomputes alpha = exp(s - lse[i]) and forms the score gradient
  * ds = alpha (<dout[i], value[j]> - <dout[i], out[i]>) itself (no per-edge
  * score, weight or score gradient is read), then writes dseg and dweights
- * as tgx_edge_mlp_backward does, and alpha [n_edges] (fp32, edge order) for
- * the value gradient (tgx_csr_sum_bwd with alpha as the weights).  The
- * reference's fused edge-attention backward recomputes the weights from the
- * row's (m, l) the same way (compiler/edge_nn_attention.py:344-611).
+ * as tgx_edge_mlp_backward does, and alpha [n_edges] (fp32, edge order;
+ * alpha_dev may be NULL) for the value gradient (tgx_csr_sum_bwd with alpha
+ * as the weights).  fold_segment >= 0 names a source segment of width
+ * value_width whose per-edge gradient rows also receive the value
+ * gradient's edge term alpha_e dout[dst_e]: when the value is that source
+ * field, the transposed reduction of dseg[fold_segment] is then its whole
+ * gradient and the value-gradient pass is not needed; -1 folds nothing.
+ * The reference's fused edge-attention backward recomputes the weights from
+ * the row's (m, l) the same way (compiler/edge_nn_attention.py:344-611).
  * Workspace: tgx_edge_mlp_backward_workspace. */
 int tgx_edge_mlp_attention_backward(const void* col_dev, const int32_t* dst_index_dev,
                                     int idx_bits, int64_t n_edges, const tgx_edge_mlp* mlp,
                                     const float* lse_dev, const float* out_dev,
                                     const float* dout_dev, const float* value_dev,
-                                    int32_t value_width, float* alpha_dev, float* dweights_dev,
-                                    float* const* dseg_dev, void* workspace_dev,
-                                    size_t workspace_bytes, void* stream);
+                                    int32_t value_width, float* alpha_dev, int fold_segment,
+                                    float* dweights_dev, float* const* dseg_dev,
+                                    void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Per-kernel timing (no reference counterpart; used by the benchmark)       */

@@ -407,6 +407,7 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
       }
     };
     float g[W];
+    float alpha = 0.f;   // attention backward: the edge's recomputed weight
     if constexpr (SEED) {
       // The gradient at the last layer's input, gathered from the edge's row.
       const float* q = seed + cur_dst * hw;
@@ -423,7 +424,7 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
       if (m.att_lse != nullptr) {
         if (valid)
           ds = attention_score_grad(m, e, cur_dst, cur_src,
-                                    linear_out1<W>(wl, a, m.nb_in[L - 1]));
+                                    linear_out1<W>(wl, a, m.nb_in[L - 1]), alpha);
       } else if (valid) {
         ds = dscore[e];
       }
@@ -465,7 +466,7 @@ __global__ __launch_bounds__(256, (bwd_blocks_per_cu<W, L>())) void edge_mlp_bwd
       linear_t<W>(wg + l * nw, dzl, g, m.n_out[l], m.nb_in[l]);
     });
     // g = d x: split per segment.
-    if (valid) scatter_segments<W>(m, e, g);
+    if (valid) scatter_segments<W>(m, e, g, alpha, cur_dst);
   }
   // Block sums, layer by layer: each wave's block into its staging region,
   // then the four added in wave order.
@@ -714,6 +715,7 @@ int check_mlp(const tgx_edge_mlp* mlp, MlpView* view, bool need_data) {
                     mlp->act[l] <= (TGX_NN_MATH ? TGX_ACT_POW : TGX_ACT_HARDSWISH),
                 "bad activation code");
   MlpView v{};
+  v.att_fold = -1;
   v.n_layers = mlp->n_layers;
   v.in_width = in_width;
   int n_in = in_width;
@@ -1054,19 +1056,26 @@ TGX_NN_ENTRY(tgx_edge_mlp_backward)(const void* col, const int32_t* dst_index, i
 TGX_NN_ENTRY(tgx_edge_mlp_attention_backward)(
     const void* col, const int32_t* dst_index, int idx_bits, int64_t n_edges,
     const tgx_edge_mlp* mlp, const float* lse, const float* out, const float* dout,
-    const float* value, int32_t value_width, float* alpha, float* dweights, float* const* dseg,
-    void* workspace, size_t workspace_bytes, void* stream) {
+    const float* value, int32_t value_width, float* alpha, int fold_segment, float* dweights,
+    float* const* dseg, void* workspace, size_t workspace_bytes, void* stream) {
   TGX_TO_MATH(mlp, tgx_edge_mlp_attention_backward_math(
                        col, dst_index, idx_bits, n_edges, mlp, lse, out, dout, value,
-                       value_width, alpha, dweights, dseg, workspace, workspace_bytes, stream));
+                       value_width, alpha, fold_segment, dweights, dseg, workspace,
+                       workspace_bytes, stream));
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(n_edges >= 0, "negative size");
   TGX_REQUIRE(value_width >= 1, "value_width must be >= 1");
   MlpView v;
   const int st = check_mlp(mlp, &v, n_edges > 0);
   if (st != TGX_OK) return st;
+  TGX_REQUIRE(fold_segment >= -1 && fold_segment < mlp->n_segments,
+              "fold_segment must be -1 or a segment index");
+  if (fold_segment >= 0)
+    TGX_REQUIRE(mlp->seg_width[fold_segment] == value_width,
+                "the folded segment's width (%d) must equal value_width (%d)",
+                mlp->seg_width[fold_segment], value_width);
   if (n_edges > 0) {
-    TGX_REQUIRE(lse && out && dout && value && alpha, "null pointer");
+    TGX_REQUIRE(lse && out && dout && value, "null pointer");
     if (value_width % 4 == 0)
       TGX_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(dout) % 16 == 0 &&
@@ -1079,6 +1088,7 @@ TGX_NN_ENTRY(tgx_edge_mlp_attention_backward)(
   v.att_value = value;
   v.att_alpha = alpha;
   v.att_width = value_width;
+  v.att_fold = fold_segment;
   return mlp_backward_body(col, dst_index, idx_bits, n_edges, mlp, v, nullptr, dweights, dseg,
                            workspace, workspace_bytes, stream);
 }

@@ -65,8 +65,12 @@ struct MlpView {
   const float* att_out;
   const float* att_dout;
   const float* att_value;
-  float* att_alpha;       // [n_edges]: the recomputed weights, for the value gradient
+  float* att_alpha;       // [n_edges]: the recomputed weights (null: not written)
   int att_width;
+  // Segment whose per-edge gradient rows also receive alpha_e att_dout[dst_e]
+  // (the value gradient's edge term, when the value is that source field),
+  // or -1.
+  int att_fold;
 };
 
 // Floats per layer of a chain's weight (and weight-gradient) blocks.
@@ -202,8 +206,9 @@ __device__ __forceinline__ void gather_inputs(const MlpView& m, int64_t e, const
 // (the reference's edge-attention VJP, compiler/edge_nn_attention.py:
 // 569-575).  alpha is stored for the value gradient's transposed sum.
 __device__ __forceinline__ float attention_score_grad(const MlpView& m, int64_t e, int64_t i,
-                                                      int64_t j, float s) {
+                                                      int64_t j, float s, float& alpha_out) {
   const float alpha = __expf(s - m.att_lse[i]);
+  alpha_out = alpha;
   const int F = m.att_width;
   const float* d = m.att_dout + i * F;
   const float* o = m.att_out + i * F;
@@ -223,19 +228,29 @@ __device__ __forceinline__ float attention_score_grad(const MlpView& m, int64_t 
       dd += d[f] * o[f];
     }
   }
-  m.att_alpha[e] = alpha;
+  if (m.att_alpha) m.att_alpha[e] = alpha;
   return alpha * (dv - dd);
 }
 
 // q_s[e][k - off_s] = g[k] for every segment s (the per-edge input gradient
-// split per segment), with the same block-then-column range tests.
+// split per segment), with the same block-then-column range tests.  Segment
+// m.att_fold (when >= 0) also receives alpha * att_dout[i][k - off_s], the
+// edge's term of the value gradient (i = the edge's destination row).
 template <int W>
-__device__ __forceinline__ void scatter_segments(const MlpView& m, int64_t e, const float (&g)[W]) {
+__device__ __forceinline__ void scatter_segments(const MlpView& m, int64_t e, const float (&g)[W],
+                                                 float alpha = 0.f, int64_t i = 0) {
 #pragma unroll
   for (int s = 0; s < kMaxSegments; ++s) {
     if (s >= m.n_seg) break;
     const int off = m.off[s], wd = m.width[s], end = off + wd;
     float* q = m.grad[s] + e * wd - off;
+    if (s == m.att_fold) {
+      const float* d = m.att_dout + i * m.att_width - off;
+#pragma unroll
+      for (int k = 0; k < W; ++k)
+        if (k >= off && k < end) q[k] = fmaf(alpha, d[k], g[k]);
+      continue;
+    }
 #pragma unroll
     for (int b = 0; b < W; b += 4) {
       if (b + 4 > off && b < end) {
@@ -737,8 +752,8 @@ TGX_NN_HIDDEN int tgx_edge_mlp_backward_math(const void* col, const int32_t* dst
 TGX_NN_HIDDEN int tgx_edge_mlp_attention_backward_math(
     const void* col, const int32_t* dst_index, int idx_bits, int64_t n_edges,
     const tgx_edge_mlp* mlp, const float* lse, const float* out, const float* dout,
-    const float* value, int32_t value_width, float* alpha, float* dweights, float* const* dseg,
-    void* workspace, size_t workspace_bytes, void* stream);
+    const float* value, int32_t value_width, float* alpha, int fold_segment, float* dweights,
+    float* const* dseg, void* workspace, size_t workspace_bytes, void* stream);
 TGX_NN_HIDDEN int tgx_edge_mlp_hidden_math(const void* col, const int32_t* dst_index,
                                            int idx_bits, int64_t n_edges,
                                            const tgx_edge_mlp* mlp, float* hidden,

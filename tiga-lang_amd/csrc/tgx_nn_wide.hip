@@ -45,11 +45,12 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
   // Last layer: one output, gradient ds: read, or formed here from the
   // replayed score (attention backward from the saved logsumexp).
   float g[W];
+  float alpha = 0.f;   // attention backward: the edge's recomputed weight
   {
     cfloat* wl = wg + (L - 1) * (W * W + W);
     const float ds = m.att_lse != nullptr
                          ? attention_score_grad(m, e, dst[e], static_cast<int64_t>(col[e]),
-                                                linear_out1<W>(wl, a, m.nb_in[L - 1]))
+                                                linear_out1<W>(wl, a, m.nb_in[L - 1]), alpha)
                          : dscore[e];
     float* out = dz_out + (L - 1) * plane + e * W;
 #pragma unroll
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(256) void edge_mlp_planes_kernel(
     linear_t<W>(wg + l * (W * W + W), dzl, g, m.n_out[l], m.nb_in[l]);
   });
   // g = d x: split per segment.
-  scatter_segments<W>(m, e, g);
+  scatter_segments<W>(m, e, g, alpha, dst[e]);
 }
 
 // v[0..B) = p[0..B) as 8- or 16-byte vector loads (p aligned to 4 B floats).

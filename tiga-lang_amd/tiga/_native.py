@@ -54,7 +54,7 @@ class EdgeMlp(ctypes.Structure):
 
 
 # tgx_abi_version() of the library these signatures and structs mirror.
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 # name -> argtypes (all return int status except where noted)
@@ -119,7 +119,7 @@ _SIGNATURES: dict[str, list] = {
     "tgx_edge_mlp_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, P(c_vp),
                               c_vp, c_size, c_vp],
     "tgx_edge_mlp_attention_backward": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, c_vp, c_vp,
-                                        c_vp, ctypes.c_int32, c_vp, c_vp, P(c_vp), c_vp,
+                                        c_vp, ctypes.c_int32, c_vp, c_int, c_vp, P(c_vp), c_vp,
                                         c_size, c_vp],
     "tgx_edge_mlp_hidden": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp, ctypes.c_int32, c_vp],
     "tgx_edge_mlp_backward_seeded": [c_vp, c_vp, c_int, c_i64, P(EdgeMlp), c_vp,

@@ -721,6 +721,13 @@ class NnAttentionFunction(torch.autograd.Function):
         out, vc, _, F = _csr_sum_launch(value, alpha, graph)
         del alpha
         ctx.graph, ctx.chain, ctx.roles, ctx.n_seg, ctx.W, ctx.F = graph, chain, roles, n_seg, W, F
+        # A value that is also a source field of the score (the reference's
+        # GAT example: value src.x, score over src.x): its two gradients meet
+        # per edge in the backward kernel, so one transposed reduction
+        # yields both and the value-gradient pass is skipped.
+        ctx.fold = next((i for i in range(n_seg)
+                         if roles[i] == "src" and tensors[i] is value
+                         and segs[i].shape[1] == F), -1)
         ctx.shapes = [t.shape for t in tensors[:n_seg]]
         ctx.present = [t is not None for t in params]
         ctx.save_for_backward(buf, lse, out, vc, *segs)
@@ -735,7 +742,9 @@ class NnAttentionFunction(torch.autograd.Function):
         dev = col_idx.device
         L = len(chain)
         g = _aligned(dout.to(torch.float32))
-        alpha = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
+        fold = ctx.fold if ctx.needs_input_grad[4] else -1
+        alpha = (torch.empty(max(E, 1), dtype=torch.float32, device=dev)
+                 if ctx.needs_input_grad[4] and fold < 0 else None)
         dsegs = [torch.empty(E, s.shape[1], dtype=torch.float32, device=dev) for s in segs]
         mlp = _mlp_struct(chain, roles, segs, buf, W)
         ws_bytes = ctypes.c_size_t()
@@ -748,10 +757,10 @@ class NnAttentionFunction(torch.autograd.Function):
         _native.call("tgx_edge_mlp_attention_backward", col_idx.data_ptr(),
                      graph._dst_index32().data_ptr(), _native.idx_bits(row_ptr), E,
                      ctypes.byref(mlp), lse.data_ptr(), out.data_ptr(), g.data_ptr(),
-                     vc.data_ptr(), F, alpha.data_ptr(), dweights.data_ptr(), ptrs,
+                     vc.data_ptr(), F, _p(alpha), fold, dweights.data_ptr(), ptrs,
                      ws.data_ptr(), ws_bytes.value, stream)
         dvalue = None
-        if ctx.needs_input_grad[4]:
+        if alpha is not None:
             dvalue = torch.empty_like(vc)
             if n_src and F:
                 t = graph._transposed()
@@ -760,6 +769,9 @@ class NnAttentionFunction(torch.autograd.Function):
                              t.perm.data_ptr(), t.plan.ref, vc.data_ptr(), alpha.data_ptr(),
                              g.data_ptr(), dvalue.data_ptr(), None, n_dst, n_src, F,
                              _native.DTYPE_F32, _p(partial), stream)
+        # Folded: the source segment's reduction is the value's whole
+        # gradient (value and field are one tensor; its gradient is returned
+        # once, for the field).
         grads = _segment_grads(graph, roles, dsegs, ctx.shapes, ctx.needs_input_grad, 5)
         grads += _layer_grads(chain, dweights, W, ctx.present, ctx.needs_input_grad,
                               5 + ctx.n_seg, L)

@@ -738,7 +738,9 @@ class MessagePassing(Kernel):
             "weights), segment softmax per row, weighted CSR sum of the value; only each "
             "row's logsumexp and output are kept; backward replays the network per edge, "
             "recomputes the weights and the softmax Jacobian in the same kernel, on-chip "
-            "weight-gradient sums, value gradient over the transposed CSR")
+            "weight-gradient sums, value gradient over the transposed CSR (a value that is "
+            "also a source field of the score gets its edge term in the same kernel and "
+            "one transposed reduction)")
         operands = (("fixed", item.module), ("src", item.value_field), *item.inputs)
         return _Launch(graph, operands, run, describe)
 
