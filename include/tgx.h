@@ -332,9 +332,12 @@ int tgx_dot_attn_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
  * 64 MiB of partials ((H*D + 2*H) * 4 bytes per chunk) are rejected with
  * TGX_INVALID_ARGUMENT before any launch.  Uses the current device's array
  * (`stream` must belong to the current device); every call on one device
- * shares it, so calls that overlap on one device (concurrent streams or
- * threads) race.  No part of the array needs to start at zero: every chunk
- * writes its partial before the merge reads it. */
+ * shares it.  Uncaptured calls are ordered in host call order whatever
+ * their streams (a call on another stream than the last one waits for an
+ * event recorded after it); calls under graph capture are not, so graph
+ * replays that overlap each other or an uncaptured call on one device race.
+ * No part of the array needs to start at zero: every chunk writes its
+ * partial before the merge reads it. */
 int tgx_dot_attn_fwd_noalloc(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                              const tgx_row_plan* plan, const void* q_dev, const void* k_dev,
                              const void* v_dev, const float* bias_dev, float scale,

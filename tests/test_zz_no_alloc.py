@@ -2,7 +2,8 @@
 partials in the library's static device scratch instead of a caller
 buffer.  Checked through the C ABI against tgx_dot_attn_fwd on the same
 plan and inputs (the same kernels, so bit-identical), on two calls in a
-row, the second smaller; and its size limit is rejected before any launch."""
+row, the second smaller, and on two streams; and its size limit is rejected
+before any launch."""
 
 import ctypes
 
@@ -53,6 +54,30 @@ def test_noalloc_forward_matches_the_caller_buffer_forward_twice():
         got = _forward("tgx_dot_attn_fwd_noalloc", row_ptr, col, plan, q, k, v, bias, 0.125)
         torch.cuda.synchronize()
         assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+
+
+@pytest.mark.gpu
+def test_noalloc_calls_on_two_streams_run_in_call_order():
+    """Two uncaptured calls on different streams share the device's scratch:
+    the second waits for the first (an event recorded after it), so both
+    match the caller-buffer forward."""
+    print("noalloc on two streams", flush=True)
+    cases = [_case(0, 20000, (9000, 5000, 2600, 700), 4, 64, torch.int64),
+             _case(1, 3000, (1500,), 2, 64, torch.int32)]
+    want = []
+    for row_ptr, col, plan, q, k, v, bias in cases:
+        n, H, D = q.shape
+        partial = torch.empty(plan.plan.n_chunks * (H * D + 2 * H), device=q.device)
+        want.append(_forward("tgx_dot_attn_fwd", row_ptr, col, plan, q, k, v, bias, 0.125,
+                             (partial.data_ptr(),)))
+    torch.cuda.synchronize()
+    got = []
+    for case, stream in zip(cases, (torch.cuda.Stream(), torch.cuda.Stream())):
+        with torch.cuda.stream(stream):
+            got.append(_forward("tgx_dot_attn_fwd_noalloc", *case, 0.125))
+    torch.cuda.synchronize()
+    for (o, ml), (wo, wml) in zip(got, want):
+        assert torch.equal(o, wo) and torch.equal(ml, wml)
 
 
 def test_noalloc_forward_rejects_plans_beyond_its_scratch():

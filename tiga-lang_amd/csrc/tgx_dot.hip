@@ -801,10 +801,20 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_init;
+// Ordering of the calls that use a device's scratch: the event recorded
+// after the last uncaptured call and the stream it ran on.  A call on
+// another stream first waits for that event, so uncaptured calls on one
+// device run one after another in the order the host made them, whatever
+// their streams.  (Set up with the address; guarded by g_scratch_order.)
+hipEvent_t g_scratch_done[kMaxDevices];
+hipStream_t g_scratch_stream[kMaxDevices];
+bool g_scratch_used[kMaxDevices];
+std::mutex g_scratch_order;
 
 // Device address of `scratch` on the current device, looked up on the first
-// call on that device (with that device current) and kept.
-int scratch_on_current_device(float** out) {
+// call on that device (with that device current) and kept, with the
+// device's ordering event.
+int scratch_on_current_device(float** out, int* device) {
   int dev = -1;
   TGX_HIP(hipGetDevice(&dev));
   TGX_REQUIRE(dev >= 0 && dev < kMaxDevices, "device ordinal %d out of range", dev);
@@ -813,12 +823,14 @@ int scratch_on_current_device(float** out) {
     std::lock_guard<std::mutex> lock(g_scratch_init);
     ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
     if (!ptr) {
+      TGX_HIP(hipEventCreateWithFlags(&g_scratch_done[dev], hipEventDisableTiming));
       TGX_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
       TGX_REQUIRE(ptr != nullptr, "no device address for the static scratch");
       g_scratch_ptr[dev].store(ptr, std::memory_order_release);
     }
   }
   *out = static_cast<float*>(ptr);
+  *device = dev;
   return TGX_OK;
 }
 
@@ -846,10 +858,30 @@ extern "C" int tgx_dot_attn_fwd_noalloc(const void* row_ptr, const void* col, in
               static_cast<long long>(plan->n_chunks),
               static_cast<size_t>(plan->n_chunks) * per_chunk, kScratchBytes);
   float* partial = nullptr;
+  int dev = -1;
   if (plan->n_chunks > 0 && n_dst > 0) {
-    const int st = scratch_on_current_device(&partial);
+    const int st = scratch_on_current_device(&partial, &dev);
     if (st != TGX_OK) return st;
   }
-  return tgx_dot_attn_fwd(row_ptr, col, idx_bits, plan, q, k, v, bias, scale, out, ml, n_dst,
-                          n_src, H, D, dtype, partial, stream);
+  if (!partial)   // no split rows: the scratch is not touched
+    return tgx_dot_attn_fwd(row_ptr, col, idx_bits, plan, q, k, v, bias, scale, out, ml,
+                            n_dst, n_src, H, D, dtype, nullptr, stream);
+  hipStream_t s = as_stream(stream);
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  TGX_HIP(hipStreamIsCapturing(s, &capture));
+  if (capture != hipStreamCaptureStatusNone)
+    // Under capture the graph's own dependencies order its replays; an
+    // event recorded outside the capture cannot be waited on inside it.
+    return tgx_dot_attn_fwd(row_ptr, col, idx_bits, plan, q, k, v, bias, scale, out, ml,
+                            n_dst, n_src, H, D, dtype, partial, stream);
+  std::lock_guard<std::mutex> lock(g_scratch_order);
+  if (g_scratch_used[dev] && g_scratch_stream[dev] != s)
+    TGX_HIP(hipStreamWaitEvent(s, g_scratch_done[dev], 0));
+  const int st = tgx_dot_attn_fwd(row_ptr, col, idx_bits, plan, q, k, v, bias, scale, out, ml,
+                                  n_dst, n_src, H, D, dtype, partial, stream);
+  if (st != TGX_OK) return st;
+  TGX_HIP(hipEventRecord(g_scratch_done[dev], s));
+  g_scratch_stream[dev] = s;
+  g_scratch_used[dev] = true;
+  return TGX_OK;
 }
