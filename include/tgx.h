@@ -388,7 +388,7 @@ int tgx_attn_tasks(const int32_t* cu_q_host, const int32_t* cu_k_host, int n_blo
                    int block, int kind, int causal, int32_t* tasks_host, int64_t* n_tasks);
 
 /* Forward: out = softmax(scale * q k^T over the relation) v per head.
- * q [n_q, H, D] and k/v [n_k, H, D] (D = 64 or 128, dtype TGX_DTYPE_*) have
+ * q [n_q, H, D] and k/v [n_k, H, D] (D = 32, 64 or 128, dtype TGX_DTYPE_*) have
  * element strides strides[0..3] = (q token, q head, k/v token, k/v head),
  * innermost stride 1: contiguous [n, H, D], or the reference's lane-major
  * [H, n, D] storage viewed as [n, H, D]

@@ -101,6 +101,8 @@ def test_causal_dense_relation_example():
     (torch.float16, 64, 513, 130, False, "contiguous"),
     (torch.bfloat16, 64, 333, 333, True, "contiguous"),
     (torch.float16, 128, 200, 200, True, "lane_major"),
+    (torch.bfloat16, 32, 300, 450, False, "lane_major"),
+    (torch.float16, 32, 333, 333, True, "contiguous"),
 ])
 def test_dense_fwd_bwd(dtype, D, n_dst, n_src, causal, layout):
     print(f"dense {dtype} D={D} {n_dst}x{n_src} causal={causal} {layout}", flush=True)
@@ -132,7 +134,8 @@ def test_dense_fwd_bwd(dtype, D, n_dst, n_src, causal, layout):
         assert rel_err(f64(got), exp) <= tol
 
 
-@pytest.mark.parametrize("dtype,D", [(torch.float16, 128), (torch.bfloat16, 64)])
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 128), (torch.bfloat16, 64),
+                                     (torch.bfloat16, 32)])
 def test_noncausal_varlen_fwd_bwd(dtype, D):
     print(f"varlen non-causal {dtype} D={D}", flush=True)
     lengths = [1, 130, 0, 64, 257, 5]
@@ -223,9 +226,9 @@ def test_pruning_fails_closed():
             prog(graph=tg.Graph.from_csr(rp, col, num_src=n), src={"key": k, "value": v},
                  dst={"query": q}, scale=0.1)
     with pytest.raises(NotImplementedError, match="dense attention tile"):
-        with torch.no_grad():   # head_dim 32 has no tile
-            prog(graph=tg.Graph.dense(n, device=DEV), src={"key": k[..., :32], "value": v[..., :32]},
-                 dst={"query": q[..., :32]}, scale=0.1)
+        with torch.no_grad():   # head_dim 48 has no tile
+            prog(graph=tg.Graph.dense(n, device=DEV), src={"key": k[..., :48], "value": v[..., :48]},
+                 dst={"query": q[..., :48]}, scale=0.1)
 
 
 def test_dense_uncovered_edge_function_runs_eager_on_materialized_relation():
@@ -268,6 +271,7 @@ def torch_block_attention(q, k, v, scale, causal):
     (8192, 2, 128, True, torch.bfloat16),    # up to 8 chunks per tile
     (4096, 4, 64, False, torch.bfloat16),    # few, equal tiles: 4 chunks each
     ((4096, 3000, 100), 4, 128, True, torch.float16),   # causal cu_seqlens, 3 blocks
+    (4096, 4, 32, True, torch.bfloat16),     # head dim 32
 ])
 def test_split_key_ranges_match_whole_tiles(n, H, D, causal, dtype):
     """Relations with too few query tiles to fill the GPU run the longest key

@@ -128,3 +128,41 @@ def test_score_softmax_against_float64(role, scale, idx, width):
         assert rel(t.grad.cpu(), e_dt) <= 1e-5
     empty = np.diff(rp) == 0
     assert not out.detach().cpu().numpy()[empty].any()
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 1e-2), (torch.float16, 2e-3)])
+@pytest.mark.parametrize("role", ["src", "edge"])
+def test_score_softmax_16bit_fields_against_float64(dtype, tol, role):
+    """16-bit score fields and values run the same fp32 softmax and sums as
+    the reference's oracle (inputs widened, output in the value's type).
+    Compared with the fp64 oracle on the 16-bit inputs; the tolerance is the
+    output type's rounding (bf16: 2^-8, fp16: 2^-11 relative) with margin."""
+    print(f"score softmax {dtype} role={role}", flush=True)
+    N = 3000
+    rp, col = skewed_csr(37, N, N, mean_deg=9, hubs=(2500,), empty_frac=0.1)
+    rng = np.random.default_rng(9)
+    rows = {"src": N, "edge": col.size}[role]
+    graph = tg.Graph.from_csr(torch.tensor(rp, device=DEV), torch.tensor(col, device=DEV),
+                              num_src=N)
+    t = torch.tensor(rng.standard_normal(rows) * 3, device=DEV).to(dtype).requires_grad_(True)
+    v = torch.tensor(rng.standard_normal((N, 6)), device=DEV).to(dtype).requires_grad_(True)
+    dout = torch.tensor(rng.standard_normal((N, 6)), device=DEV).to(dtype)
+
+    class Attn(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            return self.reducer({"src": src, "edge": edge}[role].s, src.v)
+
+    fields = {"src": {"v": v}, "edge": {}}
+    fields[role]["s"] = t
+    k = Attn()
+    out = k(graph=graph, dst={}, **fields)
+    assert k.last_variant.backend == "hip" and out.dtype == dtype
+    out.backward(dout)
+    assert t.grad.dtype == dtype and v.grad.dtype == dtype
+    f64 = lambda x: x.detach().double().cpu().numpy()
+    e_out, e_dt, e_dv = _expected(rp, col, f64(t), role, 1.0, f64(v), f64(dout))
+    assert rel(f64(out), e_out) <= tol
+    assert rel(f64(v.grad), e_dv) <= tol
+    assert rel(f64(t.grad), e_dt) <= tol

@@ -1179,8 +1179,8 @@ struct AttnView {
 
 int check_attn(const int32_t* cu_q, const int32_t* cu_k, int n_blocks, int causal, int dtype,
                const int64_t* strides, int64_t n_q, int64_t n_k, int H, int D) {
-  if (D != 64 && D != 128) {
-    set_error("dense attention tiles support head_dim 64 and 128 (got %d)", D);
+  if (D != 32 && D != 64 && D != 128) {
+    set_error("dense attention tiles support head_dim 32, 64 and 128 (got %d)", D);
     return TGX_UNSUPPORTED;
   }
   if (dtype != TGX_DTYPE_BF16 && dtype != TGX_DTYPE_F16) {

@@ -1065,8 +1065,8 @@ struct AttnShape {
 };
 
 int check_shape(const AttnShape& s) {
-  if (s.D != 64 && s.D != 128) {
-    set_error("dense attention tiles support head_dim 64 and 128 (got %d)", s.D);
+  if (s.D != 32 && s.D != 64 && s.D != 128) {
+    set_error("dense attention tiles support head_dim 32, 64 and 128 (got %d)", s.D);
     return TGX_UNSUPPORTED;
   }
   if (s.dtype != TGX_DTYPE_BF16 && s.dtype != TGX_DTYPE_F16) {
@@ -1158,6 +1158,15 @@ int launch_bwd(const AttnShape& s, BwdArgs<T> a, const T* out, const int32_t* q_
   return TGX_OK;
 }
 
+// f(std::integral_constant<int, D>) for the head dims the tiles are built for
+// (check_shape has admitted D).
+template <typename F>
+int with_head_dim(int D, F&& f) {
+  if (D == 32) return f(std::integral_constant<int, 32>{});
+  if (D == 64) return f(std::integral_constant<int, 64>{});
+  return f(std::integral_constant<int, 128>{});
+}
+
 template <typename T>
 int fwd_dtype(const AttnShape& s, const int32_t* cu_q, const int32_t* cu_k,
               const int32_t* tasks, int64_t n_tasks, const void* q, const void* k,
@@ -1167,8 +1176,9 @@ int fwd_dtype(const AttnShape& s, const int32_t* cu_q, const int32_t* cu_k,
                static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                s.qsn, s.qsh, s.ksn, s.ksh, static_cast<T*>(out), lse, scale * kLog2e,
                prune > 0.f ? __builtin_log2f(prune) : 0.f};
-  if (s.D == 64) return launch_fwd<T, 64>(s, a, n_tasks, prune > 0.f, stream);
-  return launch_fwd<T, 128>(s, a, n_tasks, prune > 0.f, stream);
+  return with_head_dim(s.D, [&](auto dc) -> int {
+    return launch_fwd<T, decltype(dc)::value>(s, a, n_tasks, prune > 0.f, stream);
+  });
 }
 
 template <typename T>
@@ -1182,11 +1192,10 @@ int bwd_dtype(const AttnShape& s, const int32_t* cu_q, const int32_t* cu_k,
                s.qsn, s.qsh, s.ksn, s.ksh, static_cast<const T*>(dout), lse, delta,
                static_cast<T*>(dq), static_cast<T*>(dk), static_cast<T*>(dv),
                scale, scale * kLog2e, static_cast<T*>(ds)};
-  if (s.D == 64)
-    return launch_bwd<T, 64>(s, a, static_cast<const T*>(out), q_tasks, n_q_tasks, k_tasks,
-                             n_k_tasks, delta, stream);
-  return launch_bwd<T, 128>(s, a, static_cast<const T*>(out), q_tasks, n_q_tasks, k_tasks,
-                            n_k_tasks, delta, stream);
+  return with_head_dim(s.D, [&](auto dc) -> int {
+    return launch_bwd<T, decltype(dc)::value>(s, a, static_cast<const T*>(out), q_tasks,
+                                              n_q_tasks, k_tasks, n_k_tasks, delta, stream);
+  });
 }
 
 }  // namespace
@@ -1432,20 +1441,17 @@ extern "C" int tgx_attn_fwd_split(const int32_t* cu_q_dev, const int32_t* cu_k_d
                  static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                  s.qsn, s.qsh, s.ksn, s.ksh, static_cast<T*>(out), lse, scale * kLog2e, 0.f,
                  chunk_tiles, max_chunks, partial_dev};
-    int r = D == 64 ? launch_fwd<T, 64>(s, a, n_tasks, false, hs)
-                    : launch_fwd<T, 128>(s, a, n_tasks, false, hs);
-    if (r != TGX_OK || n_merge == 0) return r;
-    TGX_PROFILE("varlen_fwd_merge_kernel", hs);
-    const unsigned grid =
-        static_cast<unsigned>(n_merge * (D == 64 ? kMergeBlocks<64> : kMergeBlocks<128>));
-    if (D == 64)
-      varlen_fwd_merge_kernel<T, 64><<<grid, 256, 0, hs>>>(
+    return with_head_dim(D, [&](auto dc) -> int {
+      constexpr int DD = decltype(dc)::value;
+      const int r = launch_fwd<T, DD>(s, a, n_tasks, false, hs);
+      if (r != TGX_OK || n_merge == 0) return r;
+      TGX_PROFILE("varlen_fwd_merge_kernel", hs);
+      const unsigned grid = static_cast<unsigned>(n_merge * kMergeBlocks<DD>);
+      varlen_fwd_merge_kernel<T, DD><<<grid, 256, 0, hs>>>(
           merge_dev, cu_q_dev, s.H, max_chunks, partial_dev, static_cast<T*>(out), lse);
-    else
-      varlen_fwd_merge_kernel<T, 128><<<grid, 256, 0, hs>>>(
-          merge_dev, cu_q_dev, s.H, max_chunks, partial_dev, static_cast<T*>(out), lse);
-    TGX_LAUNCHED("varlen_fwd_merge_kernel");
-    return TGX_OK;
+      TGX_LAUNCHED("varlen_fwd_merge_kernel");
+      return TGX_OK;
+    });
   };
   if (dtype == TGX_DTYPE_BF16) return run(__bf16{});
   return run(_Float16{});

@@ -324,7 +324,7 @@ ATTN_KEY_TILE = 64
 class BlockAttentionFunction(torch.autograd.Function):
     """Dot-product attention over a block-diagonal relation: Graph.cu_seqlens
     (causal or not), Graph.dense, Graph.triangular.  q [n_dst, H, D], k/v
-    [n_src, H, D], bf16 or fp16, D in {64, 128}; out contiguous [n_dst, H, D].
+    [n_src, H, D], bf16 or fp16, D in {32, 64, 128}; out contiguous [n_dst, H, D].
     prune > 0 is the reference's block_prune_threshold (forward only)."""
 
     @staticmethod
@@ -842,7 +842,11 @@ class ScoreSoftmaxFunction(torch.autograd.Function):
 def score_attention(graph: Graph, table: torch.Tensor, role: str, scale: float,
                     value: torch.Tensor) -> torch.Tensor:
     """out[i] = sum_e softmax_i(scale * score(e)) value[col[e]] on the HIP path:
-    the gathered segment softmax, then the weighted CSR sum."""
+    the gathered segment softmax, then the weighted CSR sum.  A 16-bit score
+    field is widened to fp32 first (the softmax runs in fp32, as the
+    reference's oracle accumulates); the output has the value's type."""
+    if table.dtype != torch.float32:
+        table = table.float()
     if torch.is_grad_enabled() and (table.requires_grad or value.requires_grad):
         alpha = ScoreSoftmaxFunction.apply(table, role, scale, graph)
     else:

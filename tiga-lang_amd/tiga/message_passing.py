@@ -474,8 +474,10 @@ class MessagePassing(Kernel):
         and the weighted CSR sum (reference: the eager oracle for Torch
         tensors, reducer_oracle.py:60-137; its compiled stable-weighted row
         tile for 1-D f32 fields, message_passing.py:2579-2619).  Scalar
-        scores (one lane) and fp32; an empty row gives 0, as the reference's
-        Torch path does."""
+        scores (one lane); fp32, bf16 or fp16 score fields and values, with
+        the oracle's arithmetic (scores and sums in fp32, the output in the
+        value's type, reducer_oracle.py:22-41, 60-137); an empty row gives
+        0, as the reference's Torch path does."""
         from . import _ops
 
         if graph.is_varlen or graph.is_dense:
@@ -487,7 +489,7 @@ class MessagePassing(Kernel):
         value = src.get(raw.value_field)
         if table is None or value is None:
             return None
-        if table.dtype != torch.float32 or value.dtype != torch.float32:
+        if table.dtype not in _ops._VALUE_DTYPES or value.dtype not in _ops._VALUE_DTYPES:
             return None
         if tuple(table.shape) not in ((rows[raw.score_role],), (rows[raw.score_role], 1)):
             return None
@@ -802,7 +804,7 @@ class MessagePassing(Kernel):
         if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _ops._ATTN_DTYPES:
             return None
         _, H, D = q.shape
-        if D not in (64, 128):
+        if D not in (32, 64, 128):
             return None
         if q.shape[0] != graph.schema.num_dst or k.shape[0] != graph.schema.num_src or \
                 v.shape[0] != graph.schema.num_src:
