@@ -63,8 +63,69 @@ def test_prepare_requires_a_hip_launch():
     g, _, _ = _graph(4)
     x = torch.randn(40, 2)
     w = torch.rand(g.num_edges)
-    with pytest.raises(NotImplementedError, match="torch-eager"):
+    with pytest.raises(NotImplementedError, match=r"ran cpu \(torch.sparse.mm\)"):
         WeightedSum().prepare(graph=g, src={"x": x}, dst={}, edge={"w": w[:, None]})
+
+
+@pytest.mark.parametrize("x_shape,w_shape", [((40, 3), (None,)), ((40,), (None, 1))])
+def test_host_weighted_sum_runs_the_reference_sparse_dispatch(x_shape, w_shape):
+    """edge.w * src.x on host tensors: one sparse CSR matrix of the weights
+    times the features, as the reference dispatches it
+    (interop/torch/message_passing.py:3284-3345); values and both gradients
+    against an fp64 brute force; an unweighted sum and mixed dtypes stay on
+    the eager evaluator, as in the reference."""
+    rng = np.random.default_rng(6)
+    rows = [np.sort(rng.choice(40, size=d, replace=False)) for d in rng.integers(0, 9, 50)]
+    rows[7] = np.arange(40)   # a row over every source
+    rp = np.concatenate([[0], np.cumsum([r.size for r in rows])])
+    col = np.concatenate(rows)
+    g = tg.Graph.from_csr(torch.tensor(rp), torch.tensor(col), num_src=40)
+    x = torch.randn(*x_shape, dtype=torch.float64, requires_grad=True)
+    w = torch.rand(*[g.num_edges if d is None else d for d in w_shape], dtype=torch.float64,
+                   requires_grad=True)
+    k = WeightedSum()
+    out = k(graph=g, src={"x": x}, dst={}, edge={"w": w})
+    assert k.last_variant.provider == "torch.sparse.mm" and out.shape[1:] == x.shape[1:]
+    dst = np.repeat(np.arange(50), np.diff(rp))
+    xe = x.detach().numpy().reshape(40, -1)[col]
+    we = w.detach().numpy().reshape(-1, 1)
+    want = np.zeros((50, xe.shape[1]))
+    np.add.at(want, dst, we * xe)
+    np.testing.assert_allclose(out.detach().numpy().reshape(50, -1), want, rtol=1e-12,
+                               atol=1e-12)
+    dout = torch.randn(out.shape, dtype=torch.float64)
+    out.backward(dout)
+    d2 = dout.numpy().reshape(50, -1)
+    dw = (d2[dst] * xe).sum(1)
+    dx = np.zeros((40, xe.shape[1]))
+    np.add.at(dx, col, we * d2[dst])
+    np.testing.assert_allclose(w.grad.numpy().reshape(-1), dw, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(x.grad.numpy().reshape(40, -1), dx, rtol=1e-12, atol=1e-12)
+
+    class Plain(tg.MessagePassing):
+        reducer = tg.sum()
+
+        def edge(self, src, dst, edge):
+            return src.x
+
+    p = Plain()
+    p(graph=g, src={"x": x}, dst={})
+    assert p.last_variant.backend == "torch-eager"
+    k(graph=g, src={"x": x.detach().float()}, dst={}, edge={"w": w.detach().reshape(-1, 1)})
+    assert k.last_variant.backend == "torch-eager"
+    # Repeated (row, column) pairs: sparse without a weight gradient, eager
+    # with one.
+    gm = tg.Graph.from_csr(torch.tensor([0, 3, 4]), torch.tensor([1, 1, 0, 1]), num_src=2)
+    xm = torch.tensor([[1.0], [2.0]], dtype=torch.float64)
+    wm = torch.tensor([[1.0], [2.0], [3.0], [4.0]], dtype=torch.float64)
+    torch.testing.assert_close(k(graph=gm, src={"x": xm}, dst={}, edge={"w": wm}),
+                               torch.tensor([[9.0], [8.0]], dtype=torch.float64))
+    assert k.last_variant.provider == "torch.sparse.mm"
+    wm.requires_grad_(True)
+    k(graph=gm, src={"x": xm}, dst={}, edge={"w": wm}).sum().backward()
+    assert k.last_variant.backend == "torch-eager"
+    torch.testing.assert_close(wm.grad,
+                               torch.tensor([[2.0], [2.0], [1.0], [2.0]], dtype=torch.float64))
 
 
 def test_cache_info_counts_cold_calls_on_the_eager_path():

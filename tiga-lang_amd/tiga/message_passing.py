@@ -38,6 +38,7 @@ from __future__ import annotations
 import functools
 import inspect
 import numbers
+import warnings
 from collections.abc import Callable, Mapping
 from dataclasses import dataclass
 from types import CodeType, SimpleNamespace
@@ -329,13 +330,18 @@ class MessagePassing(Kernel):
         launch = None
         if device.type == "cuda" and captured is not None:
             launch = self._plan_native(captured, graph, src, dst, edge, params)
+        elif captured is not None:
+            out = self._sparse_mm_sum(captured, graph, src, edge)
+            if out is not None:
+                self._launch = None
+                return out
         if launch is None:
             self._launch = None
             if prune is not None:
                 # reference interop/torch/message_passing.py:1611-1616
                 raise NotImplementedError(
                     "block_prune_threshold requires the dense attention tile (dot-product "
-                    "score, bf16/fp16, head_dim 64 or 128, on the GPU); refusing to silently "
+                    "score, bf16/fp16, head_dim 32, 64 or 128, on the GPU); refusing to silently "
                     "execute exact softmax or materialize the Cartesian relation")
             if config.strict:
                 raise RuntimeError(
@@ -360,6 +366,52 @@ class MessagePassing(Kernel):
             self._guarded = guarded
         return result
 
+    def _sparse_mm_sum(self, captured, graph, src, edge) -> torch.Tensor | None:
+        """tg.sum() of edge.w * src.x on host tensors as the reference runs it
+        there: one sparse CSR matrix of the weights times the features
+        (torch.sparse.mm, reference interop/torch/message_passing.py:
+        2903-2925, 3284-3345), same weight/feature conditions; None where the
+        reference also falls back to its eager evaluator, and for a weight
+        gradient over repeated (row, column) pairs, which the sparse
+        matrix's backward cannot return per edge."""
+        if not isinstance(self.reducer, SumReducer) or self.reducer.identity_value != 0 or \
+                graph.is_varlen or graph.is_dense:
+            return None
+        pat = cap.recognize_weighted_sum(captured)
+        if pat is None or pat.edge_field is None:
+            return None
+        x, w = src.get(pat.src_field), edge.get(pat.edge_field)
+        if x is None or w is None or x.ndim not in (1, 2) or w.dtype != x.dtype or \
+                not (w.ndim == 1 or (w.ndim == 2 and tuple(w.shape[1:]) == (1,))):
+            return None
+        row_ptr, col_idx = graph.resolve_csr()
+        if w.requires_grad and torch.is_grad_enabled():
+            # The sparse matrix's backward sums the gradients of repeated
+            # (row, column) entries into one value, which does not map back
+            # onto the edges of a multigraph: those stay eager.
+            unique = graph._native_cache.get("unique_pairs")
+            if unique is None:
+                rows = torch.repeat_interleave(
+                    torch.arange(graph.schema.num_dst, device=row_ptr.device),
+                    row_ptr[1:] - row_ptr[:-1])
+                keys = rows.to(torch.int64) * graph.schema.num_src + col_idx.to(torch.int64)
+                unique = bool(torch.unique(keys).numel() == keys.numel())
+                graph._native_cache["unique_pairs"] = unique
+            if not unique:
+                return None
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")   # sparse CSR support is marked beta
+            matrix = torch.sparse_csr_tensor(
+                row_ptr, col_idx, w.reshape(-1).contiguous(),
+                size=(graph.schema.num_dst, graph.schema.num_src))
+        out = torch.sparse.mm(matrix, (x[:, None] if x.ndim == 1 else x).contiguous())
+        self._record_variant(CompiledVariant(
+            key=(type(self).__qualname__, "sparse-mm", graph.planning_key()),
+            backend=graph.device.type, provider="torch.sparse.mm", pattern="weighted-sum",
+            lowering="dispatch-native-sparse-mm",
+            remarks=("host tensors: the reference's native sparse dispatch",)))
+        return out[:, 0] if x.ndim == 1 else out
+
     def prepare(self, *, graph: Graph, src: Mapping[str, torch.Tensor] | None = None,
                 dst: Mapping[str, torch.Tensor] | None = None,
                 edge: Mapping[str, torch.Tensor] | None = None,
@@ -378,7 +430,8 @@ class MessagePassing(Kernel):
         if launch is None or launch.graph is not graph:
             raise NotImplementedError(
                 "prepared MessagePassing needs an edge function, dtype and shape that a HIP "
-                f"kernel covers; this call ran {self.last_variant.backend}")
+                f"kernel covers; this call ran {self.last_variant.backend} "
+                f"({self.last_variant.provider})")
         operands = tuple(launch.gather(src, dst, edge, params))
         runner, epilogue = launch.runner, self._epilogue
         frozen_dst, frozen_params = dict(dst), dict(params)
