@@ -421,6 +421,29 @@ def test_edge_mlp_validation_of_layer_widths():
         assert lib.tgx_edge_mlp_backward_workspace(0, ctypes.byref(m), ctypes.byref(size)) == 0
 
 
+def test_attention_backward_fold_segment_is_checked_before_any_launch():
+    """tgx_edge_mlp_attention_backward: fold_segment must name a segment
+    whose width is value_width (or be -1); a bad one is rejected on the host
+    before any HIP call."""
+    lib = _native.lib()
+    buf = torch.zeros(2, 32 * 32 + 32)
+    segs = [torch.zeros(4, 8), torch.zeros(4, 3)]
+    m = _native.EdgeMlp()
+    m.n_layers, m.width = 2, 32
+    m.act[0] = 1
+    m.weights_dev = buf.data_ptr()
+    m.n_segments = 2
+    for i, t in enumerate(segs):
+        m.seg_role[i], m.seg_width[i], m.seg_stride[i] = 0, t.shape[1], t.shape[1]
+        m.seg_dev[i] = t.data_ptr()
+    m.out_width[0], m.out_width[1] = 16, 1
+    for fold, match in ((2, b"fold_segment"), (-2, b"fold_segment"), (1, b"value_width")):
+        status = lib.tgx_edge_mlp_attention_backward(
+            None, None, 64, 0, ctypes.byref(m), None, None, None, None, 8, None, fold, None,
+            None, None, 0, None)
+        assert status == 1 and match in lib.tgx_last_error(), (fold, lib.tgx_last_error())
+
+
 def test_sum_rejects_source_tables_past_32_bit_rows():
     """The sum kernels hold gathered row indices in 32 bits: a source table of
     2^31 rows or more is refused before anything is launched."""
