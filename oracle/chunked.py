@@ -1,5 +1,6 @@
 """Row-chunked float64 restatement of the GAT and dot-product attention
-passes, for checking full-size outputs.
+passes, of per-sequence causal attention and of nn-scored attention, for
+checking full-size outputs.
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py): never imported by the
 product.
@@ -225,3 +226,74 @@ def causal_sequence(q, k, v, scale, dout=None, query_block=512):
         dv[:, :i1] += torch.matmul(p.transpose(1, 2).contiguous(), gh[:, i0:i1])
     back = lambda t: t.permute(1, 0, 2)
     return back(out), lse.T, back(dq), back(dk), back(dv)
+
+
+def _activate(name, z, p):
+    """ref._act in Torch ops (the same closed forms)."""
+    if name == "relu":
+        return torch.clamp_min(z, 0.0)
+    if name == "leaky_relu":
+        return torch.where(z > 0, z, p * z)
+    if name == "tanh":
+        return torch.tanh(z)
+    if name == "sigmoid":
+        return torch.sigmoid(z)
+    if name == "silu":
+        return z * torch.sigmoid(z)
+    if name == "gelu":
+        return 0.5 * z * (1.0 + torch.erf(z / 2.0 ** 0.5))
+    if name == "elu":
+        return torch.where(z > 0, z, p * torch.expm1(torch.clamp_max(z, 0.0)))
+    return z
+
+
+def nn_attention(row_ptr, col, inputs, layers, value, dout, keep_hidden=False):
+    """``ref.nn_attention_fwd/bwd`` in float64 Torch ops with autograd (the
+    whole graph at once: a 4M-edge relation's [E, 19] float64 gathers fit
+    on the GPU).  inputs = [(role, [rows, w])], layers = [(W, b or None,
+    act, param)] as float64 tensors.  The row maximum is held constant,
+    which softmax shift-invariance makes exact.  Returns (out, [d inputs],
+    d value, [(dW, db or None)]), and with keep_hidden a fifth item: per
+    hidden layer (input a [E, in], pre-activation z [E, out], dz [E, out])."""
+    n = row_ptr.numel() - 1
+    dst = torch.repeat_interleave(torch.arange(n, device=col.device),
+                                  row_ptr[1:] - row_ptr[:-1])
+    leaves = [t.detach().clone().requires_grad_(True) for _, t in inputs]
+    parts = [t[col] if role == "src" else t[dst] if role == "dst" else t
+             for (role, _), t in zip(inputs, leaves)]
+    a = torch.cat(parts, dim=1)
+    params, hidden = [], []
+    for i, (W, b, act, p) in enumerate(layers):
+        Wl = W.detach().clone().requires_grad_(True)
+        bl = None if b is None else b.detach().clone().requires_grad_(True)
+        params.append((Wl, bl))
+        z = a @ Wl.T + (0.0 if bl is None else bl)
+        if i + 1 < len(layers):
+            hidden.append((a, z))
+            a = _activate(act, z, p)
+        else:
+            a = z
+    s = a[:, 0]
+    v = value.detach().clone().requires_grad_(True)
+    m = torch.full((n,), -torch.inf, dtype=s.dtype, device=s.device)
+    m = m.scatter_reduce(0, dst, s.detach(), "amax", include_self=True)
+    p_e = torch.exp(s - m[dst])
+    den = torch.zeros(n, dtype=s.dtype, device=s.device).index_add(0, dst, p_e)
+    num = torch.zeros((n, v.shape[1]), dtype=s.dtype, device=s.device)
+    num = num.index_add(0, dst, v[col] * p_e[:, None])
+    safe = torch.where(den > 0, den, torch.ones_like(den))
+    out = torch.where(den[:, None] > 0, num / safe[:, None], torch.zeros_like(num))
+    wanted = leaves + [v] + [t for pair in params for t in pair if t is not None]
+    if keep_hidden:
+        wanted += [z for _, z in hidden]
+    grads = torch.autograd.grad(out, wanted, dout)
+    k = len(leaves)
+    d_inputs, d_value, rest = list(grads[:k]), grads[k], list(grads[k + 1:])
+    d_layers = []
+    for Wl, bl in params:
+        dW = rest.pop(0)
+        d_layers.append((dW, rest.pop(0) if bl is not None else None))
+    if not keep_hidden:
+        return out.detach(), d_inputs, d_value, d_layers
+    kept = [(a_l.detach(), z.detach(), dz) for (a_l, z), dz in zip(hidden, rest)]
+    return out.detach(), d_inputs, d_value, d_layers, kept

@@ -18,6 +18,10 @@ the reference's own bf16 arithmetic.
 * C5 (varlen causal, 32 sequences of U[512, 4096] tokens, bf16): out, dq, dk
   and dv of the longest sequence and two seeded others, against the
   query-chunked float64 per-sequence attention, 2e-2.
+* nn-scored attention (the reference's GAT example shape, 131072 nodes,
+  4.0M edges, fp32, value = the source field): out, the field gradients and
+  the weight gradients against the float64 Torch checker
+  (oracle/chunked.nn_attention), 1e-5, away from LeakyReLU's kink.
 * bf16 arithmetic: on an R-MAT scale-12 graph the HIP dot-product forward
   and backward against the reference's eager path run in bf16 on the CPU
   (oracle/eager_torch.dot_reference: bf16 q*k products and sums, fp32 bias
@@ -260,3 +264,96 @@ def test_dot_against_the_reference_bf16_arithmetic(with_bias):
               f"vs fp64 {own:.3e}", flush=True)
         assert err64 <= 2e-2, name
         assert err16 <= 2e-2 + own, name
+
+
+# ---- nn-scored attention at the bench's size: 131072 nodes, ~4.0M edges --------
+
+def test_nn_full_size_values_against_float64():
+    """The reference's GAT example shape (score net Linear(19, 16) ->
+    LeakyReLU(0.2) -> Linear(16, 1) over [displacement | x_src | x_dst], value
+    x_src, so the backward folds the value gradient into the source field's
+    rows) at the bench configuration, against the float64 Torch checker
+    (oracle/chunked.nn_attention, pinned against ref.nn_attention_fwd/bwd):
+    out and the gradients of x and the displacement within 1e-5 of the
+    largest element (away from LeakyReLU's kink, below), the weight and bias
+    gradients (sums over all 4.0M edges) within 1e-5 plus, for the hidden
+    layer, the kink's bounded share."""
+    from torch import nn
+
+    print("nn full size values: 131072 nodes", flush=True)
+    N = 131072
+    row_ptr, col = poisson_self_loop(N, 29.6, SEED)
+    graph = tg.Graph.from_csr(row_ptr, col, num_src=N)
+    g = torch.Generator(device=DEV).manual_seed(SEED + 3)
+    pos = torch.rand(N, 3, device=DEV, generator=g)
+    x = torch.randn(N, 8, device=DEV, generator=g).requires_grad_(True)
+    disp = (pos[col] - pos[graph.destination_index()]).requires_grad_(True)
+    torch.manual_seed(SEED + 3)
+    net = nn.Sequential(nn.Linear(19, 16), nn.LeakyReLU(0.2), nn.Linear(16, 1)).to(DEV)
+    dout = torch.randn(N, 8, device=DEV, generator=g)
+
+    class GAT(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def __init__(self):
+            super().__init__()
+            self.attn = tg.nn.trace(net)
+
+        def edge(self, src, dst, edge):
+            return self.reducer(self.attn(edge.displacement, src.x, dst.x), src.x)
+
+    kernel = GAT()
+    out = kernel(graph=graph, src={"x": x}, dst={"x": x}, edge={"displacement": disp})
+    assert kernel.last_variant.backend == "hip"
+    out.backward(dout)
+    d64 = lambda t: t.detach().double()
+    layers = [(d64(net[0].weight), d64(net[0].bias), "leaky_relu", 0.2),
+              (d64(net[2].weight), d64(net[2].bias), "identity", 0.0)]
+    e_out, (e_disp, e_src, e_dst), e_val, e_layers, hidden = chunked.nn_attention(
+        row_ptr.long(), col.long(), [("edge", d64(disp)), ("src", d64(x)), ("dst", d64(x))],
+        layers, d64(x), d64(dout), keep_hidden=True)
+    e_x = e_src + e_dst + e_val
+    # LeakyReLU's derivative jumps at z = 0: a hidden pre-activation within
+    # fp32 rounding of 0 may take the other slope in fp32, which moves that
+    # unit's dz by (1 - slope) |g| (g = dz / slope, the gradient at the
+    # unit's output).  The kernel's z is a 20-term fp32 sum of exact fp32
+    # products and inputs, so |z32 - z| <= 20 * 2^-24 * sum |W a| + |b|;
+    # "near" takes 32 in place of 20.  The field gradients leave those
+    # edges and the nodes they touch out; the hidden layer's weight and bias
+    # gradients are held to 1e-5 of their largest element plus the sum of
+    # those moves.
+    a0, z0, dz0 = hidden[0]
+    dst = graph.destination_index().long()
+    w0, b0 = layers[0][0], layers[0][1]
+    near = z0.abs() <= 32 * 2.0 ** -24 * (a0.abs() @ w0.abs().T + b0.abs())
+    kink = near.any(1)
+    touched = torch.zeros(N, dtype=torch.bool, device=DEV)
+    touched[col.long()[kink]] = True
+    touched[dst[kink]] = True
+    print(f"  kink (edge, unit) pairs {int(near.sum())}, edges {int(kink.sum())}, "
+          f"nodes they touch {int(touched.sum())}", flush=True)
+    move = torch.where(near, 0.8 * (dz0 / torch.where(z0 > 0, 1.0, 0.2)).abs(),
+                       torch.zeros_like(dz0))
+    allow_w = move.T @ a0.abs()
+    allow_b = move.sum(0)
+    x_ok, e_ok = ~touched, ~kink
+    checks = [("out", out, e_out, 1e-5), ("dx", x.grad[x_ok], e_x[x_ok], 1e-5),
+              ("ddisplacement", disp.grad[e_ok], e_disp[e_ok], 1e-5),
+              ("dW1", net[2].weight.grad, e_layers[1][0], 1e-5)]
+    for name, got, want, tol in checks:
+        err = rel(got, want)
+        print(f"  {name}: max-norm {err:.2e} (bound {tol:g}); {elementwise(got, want)}",
+              flush=True)
+        assert err <= tol, name
+    for name, got, want, allow in (("dW0", net[0].weight.grad, e_layers[0][0], allow_w),
+                                   ("db0", net[0].bias.grad, e_layers[0][1], allow_b)):
+        diff = (got.double() - want).abs()
+        bound = 1e-5 * want.abs().max() + allow
+        print(f"  {name}: max-norm {rel(got, want):.2e}, largest kink allowance "
+              f"{float(allow.max() / want.abs().max()):.2e} of max; "
+              f"worst diff / bound {float((diff / bound).max()):.3f}", flush=True)
+        assert bool((diff <= bound).all()), name
+    # The last bias shifts every score of a row alike: its exact gradient is
+    # 0, so it is held to the scale of the last weight's gradient.
+    db1 = net[2].bias.grad.double()
+    assert float(db1.abs().max()) <= 1e-4 * float(e_layers[1][0].abs().max())

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import planner, ref
+from oracle import chunked, planner, ref
 
 GOLD = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
 
@@ -444,6 +444,31 @@ def test_nn_attention_matches_torch_autograd_float64():
                         dlayers[2][1]]
     for a, b in zip(got, expect):
         np.testing.assert_allclose(a.numpy(), b, rtol=1e-10, atol=1e-12)
+
+
+def test_chunked_nn_attention_matches_ref():
+    """oracle/chunked.nn_attention (the Torch float64 checker of the
+    full-size nn test) against ref.nn_attention_fwd/bwd, with a value that is
+    also a source field, as in the reference's GAT example."""
+    rp, col, inputs, layers, value, dout = _nn_case(23)
+    value = inputs[0][1]   # the value is the source field x
+    rpt, colt = torch.as_tensor(rp), torch.as_tensor(col)
+    t_in = [(r, torch.as_tensor(a)) for r, a in inputs]
+    t_layers = [(torch.as_tensor(W), None if b is None else torch.as_tensor(b), act, p)
+                for W, b, act, p in layers]
+    out, d_in, d_v, d_layers = chunked.nn_attention(rpt, colt, t_in, t_layers,
+                                                    torch.as_tensor(value),
+                                                    torch.as_tensor(dout[:, :3]))
+    e_out, _ = ref.nn_attention_fwd(rp, col, inputs, layers, value)
+    np.testing.assert_allclose(out.numpy(), e_out, rtol=1e-12, atol=1e-12)
+    e_in, e_v, e_layers = ref.nn_attention_bwd(rp, col, inputs, layers, value, dout[:, :3])
+    for a, b in zip(d_in + [d_v], e_in + [e_v]):
+        np.testing.assert_allclose(a.numpy(), b, rtol=1e-10, atol=1e-12)
+    for (dW, db), (eW, eb) in zip(d_layers, e_layers):
+        np.testing.assert_allclose(dW.numpy(), eW, rtol=1e-10, atol=1e-12)
+        assert (db is None) == (eb is None)
+        if db is not None:
+            np.testing.assert_allclose(db.numpy(), eb, rtol=1e-10, atol=1e-12)
 
 
 # ---- timed CPU baselines (bench.py's cpu_baseline legs) ---------------------
