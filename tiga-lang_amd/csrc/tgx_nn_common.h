@@ -244,23 +244,25 @@ __device__ __forceinline__ void scatter_segments(const MlpView& m, int64_t e, co
     if (s >= m.n_seg) break;
     const int off = m.off[s], wd = m.width[s], end = off + wd;
     float* q = m.grad[s] + e * wd - off;
-    if (s == m.att_fold) {
-      const float* d = m.att_dout + i * m.att_width - off;
-#pragma unroll
-      for (int k = 0; k < W; ++k)
-        if (k >= off && k < end) q[k] = fmaf(alpha, d[k], g[k]);
-      continue;
-    }
+    const bool fold = s == m.att_fold;
+    const float* d = fold ? m.att_dout + i * m.att_width - off : nullptr;   // d[k] pairs with g[k]
 #pragma unroll
     for (int b = 0; b < W; b += 4) {
       if (b + 4 > off && b < end) {
-        if (b >= off && b + 4 <= end) {
+        float v[4];
 #pragma unroll
-          for (int k = b; k < b + 4; ++k) q[k] = g[k];
+        for (int k = 0; k < 4; ++k) v[k] = g[b + k];
+        if (b >= off && b + 4 <= end) {
+          if (fold) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = fmaf(alpha, d[b + k], v[k]);
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) q[b + k] = v[k];
         } else {
 #pragma unroll
           for (int k = b; k < b + 4; ++k)
-            if (k >= off && k < end) q[k] = g[k];
+            if (k >= off && k < end) q[k] = fold ? fmaf(alpha, d[k], v[k - b]) : v[k - b];
         }
       }
     }
