@@ -614,6 +614,22 @@ int tgx_segment_softmax_gather_fwd(const void* row_ptr_dev, const void* col_dev,
                                    float scale, float* alpha_dev, float* lse_dev,
                                    void* stream);
 
+/* The segment softmax of tgx_segment_softmax_gather_fwd (same roles, scale,
+ * lse and, when alpha_dev is not NULL, alpha) and the weighted sum of the
+ * value rows in the same pass: out[i] = sum_e alpha_e value[col[e]],
+ * value_dev [n_src, F] and out_dev [n_rows, F] fp32, 1 <= F <= 8 (else
+ * TGX_UNSUPPORTED; F = 4 or 8 needs value_dev 16-byte aligned); an empty
+ * row gets 0.  TGX_ROLE_EDGE reads the per-edge
+ * scores of tgx_segment_softmax_fwd.  Per row only lse and the output are
+ * written: the reference's row-centric attention tile keeps (m, l) and the
+ * output (compiler/edge_nn_attention.py:127-338, reducer_oracle.py:60-137),
+ * and its Torch path is tgx_segment_softmax_gather_fwd + tgx_csr_sum_fwd
+ * (interop/torch/message_passing.py:2579-2619). */
+int tgx_segment_softmax_sum_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
+                                int64_t n_rows, const float* scores_dev, int role, float scale,
+                                const float* value_dev, int F, float* alpha_dev,
+                                float* lse_dev, float* out_dev, void* stream);
+
 /* Its backward: dscore[e] = alpha_e (dalpha_e - sum over the row of
  * alpha dalpha). */
 int tgx_segment_softmax_bwd(const void* row_ptr_dev, int idx_bits, int64_t n_rows,

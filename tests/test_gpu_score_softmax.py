@@ -166,3 +166,50 @@ def test_score_softmax_16bit_fields_against_float64(dtype, tol, role):
     assert rel(f64(out), e_out) <= tol
     assert rel(f64(v.grad), e_dv) <= tol
     assert rel(f64(t.grad), e_dt) <= tol
+
+
+@pytest.mark.parametrize("role,scale,width", [("src", 1.0, None), ("edge", 0.5, 8),
+                                              ("dst", -2.0, 3), ("src", 1.0, 9)])
+@pytest.mark.parametrize("idx", [torch.int32, torch.int64])
+def test_score_softmax_without_gradient_against_float64(role, scale, width, idx):
+    """Without a gradient the softmax and the value sum run in one pass
+    (tgx_segment_softmax_sum_fwd) for fp32 value rows of at most 8 floats;
+    9 floats take the softmax weights and the CSR sum.  Hub rows of 2500 and
+    700 edges and empty rows; 1e-5 against the float64 oracle; the
+    reference's known answer at scores about 1000 too."""
+    print(f"score softmax no-grad role={role} scale={scale} width={width} {idx}", flush=True)
+    N = 3000
+    rp, col = skewed_csr(41, N, N, mean_deg=9, hubs=(2500, 700), empty_frac=0.1)
+    rng = np.random.default_rng(11)
+    rows = {"src": N, "dst": N, "edge": col.size}[role]
+    table = (rng.standard_normal(rows) * 3).astype(np.float32)
+    value = rng.standard_normal((N,) if width is None else (N, width)).astype(np.float32)
+    graph = tg.Graph.from_csr(torch.tensor(rp, device=DEV, dtype=idx),
+                              torch.tensor(col, device=DEV, dtype=idx), num_src=N)
+
+    class Attn(tg.MessagePassing):
+        reducer = tg.online_softmax()
+
+        def edge(self, src, dst, edge):
+            fields = {"src": src, "dst": dst, "edge": edge}[role]
+            return self.reducer(fields.s if scale == 1.0 else fields.s * scale, src.v)
+
+    fields = {"src": {"v": torch.tensor(value, device=DEV)}, "dst": {}, "edge": {}}
+    fields[role]["s"] = torch.tensor(table, device=DEV)
+    k = Attn()
+    with torch.no_grad():
+        out = k(graph=graph, **fields)
+    assert k.last_variant.backend == "hip"
+    e_out, _, _ = _expected(rp, col, table, role, scale, value,
+                            np.zeros((N,) if width is None else (N, width)))
+    assert rel(out.cpu(), e_out) <= 1e-5
+    assert not out.cpu().numpy()[np.diff(rp) == 0].any()
+    g = GOLD["online_softmax_large_scores"]
+    kg = tg.Graph.from_csr(torch.tensor(g["row_ptr"], device=DEV),
+                           torch.tensor(g["col_idx"], device=DEV), num_src=g["num_src"])
+    with torch.no_grad():
+        o = OnlineAttention()(graph=kg, src={"score": torch.tensor(g["score"], device=DEV),
+                                             "value": torch.tensor(g["value"], device=DEV)},
+                              dst={})
+    np.testing.assert_allclose(o.cpu().numpy(), g["out"], rtol=0,
+                               atol=0.5 * 10.0 ** -g["places"])

@@ -618,6 +618,104 @@ __global__ __launch_bounds__(256) void segment_softmax_gather_kernel(
   });
 }
 
+// The segment softmax and the weighted sum of the value rows in one pass
+// (the reference's row-centric tile: per row only (m, l) and the output,
+// compiler/edge_nn_attention.py:127-338, reducer_oracle.py:60-137):
+// out[i] = sum_e alpha_e value[col[e]], value rows of F <= FV floats.  Each
+// lane forms its edges' weights, multiplies them into its running sums of
+// the gathered rows, and the slot adds the lanes' sums.  alpha may be null.
+template <int S, int FV, typename I, typename Score>
+__device__ __forceinline__ void softmax_sum_row(int64_t row, bool has, int64_t e0, int64_t e1,
+                                                int hl, Score&& score, const I* col,
+                                                const float* __restrict__ value, int F,
+                                                float* __restrict__ alpha,
+                                                float* __restrict__ lse,
+                                                float* __restrict__ out) {
+  const int64_t len = e1 - e0;
+  float m, l;
+  float acc[FV];
+#pragma unroll
+  for (int k = 0; k < FV; ++k) acc[k] = 0.f;
+  // Rows of exactly FV (a multiple of 4) floats are read as 16-byte vectors
+  // (the caller passes a 16-byte aligned table).
+  const bool vec = FV % 4 == 0 && F == FV;
+  auto load_row = [&](int64_t e, float (&v)[FV]) {
+    const float* src = value + static_cast<int64_t>(col[e]) * F;
+    if (vec) {
+#pragma unroll
+      for (int k = 0; k < FV; k += 4) {
+        const f32x4 q = *reinterpret_cast<const f32x4*>(src + k);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[k + r] = q[r];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < FV; ++k) v[k] = k < F ? src[k] : 0.f;
+    }
+  };
+  auto add_row = [&](int64_t e, float a) {
+    float v[FV];
+    load_row(e, v);
+#pragma unroll
+    for (int k = 0; k < FV; ++k) acc[k] = fmaf(a, v[k], acc[k]);
+  };
+  if (len <= S) {
+    // The row's value rows are requested with its scores, before the
+    // reductions that form the weights.
+    const bool on = hl < len;
+    float v[FV];
+    const float sc = on ? score(e0 + hl) : kNegInf;
+    if (on) load_row(e0 + hl, v);
+    m = group_max<S>(sc);
+    const float p = on ? __expf(sc - m) : 0.f;
+    l = group_sum<S>(p);
+    if (on) {
+      const float a = p * (1.f / l);
+      if (alpha) alpha[e0 + hl] = a;
+#pragma unroll
+      for (int k = 0; k < FV; ++k) acc[k] = a * v[k];
+    }
+  } else {
+    m = kNegInf;
+    for (int64_t e = e0 + hl; e < e1; e += S) m = fmaxf(m, score(e));
+    m = group_max<S>(m);
+    l = 0.f;
+    for (int64_t e = e0 + hl; e < e1; e += S) l += __expf(score(e) - m);
+    l = group_sum<S>(l);
+    const float inv = 1.f / l;
+    for (int64_t e = e0 + hl; e < e1; e += S) {
+      const float a = __expf(score(e) - m) * inv;
+      if (alpha) alpha[e] = a;
+      add_row(e, a);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < FV; ++k)
+    if (k < F) acc[k] = group_sum<S>(acc[k]);
+  if (has && hl == 0) {
+    lse[row] = len > 0 ? m + __logf(l) : kNegInf;
+#pragma unroll
+    for (int k = 0; k < FV; ++k)
+      if (k < F) out[row * F + k] = acc[k];
+  }
+}
+
+template <typename I, int ROLE, int FV>
+__global__ __launch_bounds__(256) void segment_softmax_sum_kernel(
+    const I* __restrict__ row_ptr, const I* __restrict__ col, int64_t n_rows,
+    const float* __restrict__ scores, float scale, const float* __restrict__ value, int F,
+    float* __restrict__ alpha, float* __restrict__ lse, float* __restrict__ out) {
+  softmax_row_groups(row_ptr, n_rows, [&](int64_t row, auto slot, int hl) {
+    const bool has = row < n_rows;
+    const int64_t e0 = has ? static_cast<int64_t>(row_ptr[row]) : 0;
+    const int64_t e1 = has ? static_cast<int64_t>(row_ptr[row + 1]) : 0;
+    softmax_sum_row<decltype(slot)::value, FV>(
+        row, has, e0, e1, hl,
+        [&](int64_t e) { return role_score<I, ROLE>(scores, col, e, row, scale); }, col, value,
+        F, alpha, lse, out);
+  });
+}
+
 // ds_e = alpha_e (dalpha_e - sum_row alpha dalpha).
 template <typename I>
 __global__ __launch_bounds__(256) void segment_softmax_bwd_kernel(
@@ -1153,6 +1251,77 @@ extern "C" int tgx_segment_softmax_gather_fwd(const void* row_ptr, const void* c
     launch_gather_softmax(static_cast<const int64_t*>(row_ptr), static_cast<const int64_t*>(col),
                           n_rows, scores, role, scale, alpha, lse, s);
   TGX_LAUNCHED("segment_softmax_gather_kernel");
+  return TGX_OK;
+}
+
+namespace tgx {
+namespace {
+template <typename I, int ROLE>
+void launch_softmax_sum(const I* row_ptr, const I* col, int64_t n_rows, const float* scores,
+                        float scale, const float* value, int F, float* alpha, float* lse,
+                        float* out, hipStream_t s) {
+  const unsigned blocks = static_cast<unsigned>(ceil_div(n_rows, 4 * kSoftmaxRowsPerWave));
+  if (F == 1)
+    segment_softmax_sum_kernel<I, ROLE, 1><<<blocks, 256, 0, s>>>(row_ptr, col, n_rows, scores,
+                                                                   scale, value, F, alpha, lse,
+                                                                   out);
+  else if (F <= 2)
+    segment_softmax_sum_kernel<I, ROLE, 2><<<blocks, 256, 0, s>>>(row_ptr, col, n_rows, scores,
+                                                                   scale, value, F, alpha, lse,
+                                                                   out);
+  else if (F <= 4)
+    segment_softmax_sum_kernel<I, ROLE, 4><<<blocks, 256, 0, s>>>(row_ptr, col, n_rows, scores,
+                                                                   scale, value, F, alpha, lse,
+                                                                   out);
+  else
+    segment_softmax_sum_kernel<I, ROLE, 8><<<blocks, 256, 0, s>>>(row_ptr, col, n_rows, scores,
+                                                                   scale, value, F, alpha, lse,
+                                                                   out);
+}
+
+template <typename I>
+void launch_softmax_sum_role(const I* row_ptr, const I* col, int64_t n_rows,
+                             const float* scores, int role, float scale, const float* value,
+                             int F, float* alpha, float* lse, float* out, hipStream_t s) {
+  if (role == TGX_ROLE_SRC)
+    launch_softmax_sum<I, 0>(row_ptr, col, n_rows, scores, scale, value, F, alpha, lse, out, s);
+  else if (role == TGX_ROLE_DST)
+    launch_softmax_sum<I, 1>(row_ptr, col, n_rows, scores, scale, value, F, alpha, lse, out, s);
+  else
+    launch_softmax_sum<I, 2>(row_ptr, col, n_rows, scores, scale, value, F, alpha, lse, out, s);
+}
+}  // namespace
+}  // namespace tgx
+
+extern "C" int tgx_segment_softmax_sum_fwd(const void* row_ptr, const void* col, int idx_bits,
+                                           int64_t n_rows, const float* scores, int role,
+                                           float scale, const float* value, int F,
+                                           float* alpha, float* lse, float* out,
+                                           void* stream) {
+  TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
+  TGX_REQUIRE(n_rows >= 0, "negative size");
+  TGX_REQUIRE(role == TGX_ROLE_SRC || role == TGX_ROLE_DST || role == TGX_ROLE_EDGE,
+              "role must be TGX_ROLE_SRC, TGX_ROLE_DST or TGX_ROLE_EDGE");
+  if (F < 1 || F > 8) {
+    set_error("the fused softmax sum takes value rows of 1 to 8 floats (got %d)", F);
+    return TGX_UNSUPPORTED;
+  }
+  TGX_REQUIRE((F != 4 && F != 8) || reinterpret_cast<uintptr_t>(value) % 16 == 0,
+              "value rows of 4 or 8 floats need a 16-byte aligned table");
+  if (n_rows == 0) return TGX_OK;
+  // col, scores and value are read only for rows with edges.
+  TGX_REQUIRE(row_ptr && lse && out, "null pointer");
+  hipStream_t s = as_stream(stream);
+  TGX_PROFILE("segment_softmax_sum_kernel", s);
+  if (idx_bits == 32)
+    launch_softmax_sum_role(static_cast<const int32_t*>(row_ptr),
+                            static_cast<const int32_t*>(col), n_rows, scores, role, scale, value,
+                            F, alpha, lse, out, s);
+  else
+    launch_softmax_sum_role(static_cast<const int64_t*>(row_ptr),
+                            static_cast<const int64_t*>(col), n_rows, scores, role, scale, value,
+                            F, alpha, lse, out, s);
+  TGX_LAUNCHED("segment_softmax_sum_kernel");
   return TGX_OK;
 }
 

@@ -54,7 +54,7 @@ class EdgeMlp(ctypes.Structure):
 
 
 # tgx_abi_version() of the library these signatures and structs mirror.
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 # name -> argtypes (all return int status except where noted)
@@ -128,6 +128,8 @@ _SIGNATURES: dict[str, list] = {
     "tgx_segment_softmax_bwd": [c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tgx_segment_softmax_gather_fwd": [c_vp, c_vp, c_int, c_i64, c_vp, c_int, c_f32, c_vp,
                                        c_vp, c_vp],
+    "tgx_segment_softmax_sum_fwd": [c_vp, c_vp, c_int, c_i64, c_vp, c_int, c_f32, c_vp, c_int,
+                                    c_vp, c_vp, c_vp, c_vp],
     # CPU twins (include/tgx_cpu.h): host pointers, no stream.
     "tgx_cpu_set_threads": [c_int],
     "tgx_cpu_destination_index": [c_vp, c_int, c_i64, c_i64, c_vp, c_int],

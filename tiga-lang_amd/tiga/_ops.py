@@ -709,17 +709,26 @@ class NnAttentionFunction(torch.autograd.Function):
         _fill_weights(buf, chain, params, W, len(chain))
         mlp = _mlp_struct(chain, roles, segs, buf, W)
         stream = _native.stream_of(col_idx)
-        # Scores and weights live only for this forward.
+        # The scores live only for this forward; value rows of at most 8
+        # floats are summed in the softmax pass itself (no per-edge weight
+        # is written), wider ones by the CSR sum over the weights.
         scores = torch.empty(E, dtype=torch.float32, device=dev)
         _native.call("tgx_edge_mlp_scores", col_idx.data_ptr(), graph._dst_index32().data_ptr(),
                      _native.idx_bits(row_ptr), E, ctypes.byref(mlp), scores.data_ptr(), stream)
-        alpha = torch.empty_like(scores)
         lse = torch.empty(max(n_dst, 1), dtype=torch.float32, device=dev)
-        _native.call("tgx_segment_softmax_fwd", row_ptr.data_ptr(), _native.idx_bits(row_ptr),
-                     n_dst, scores.data_ptr(), alpha.data_ptr(), lse.data_ptr(), stream)
+        out = _fused_softmax_sum(graph, scores, TGX_ROLE_EDGE, 1.0, value, lse)
+        if out is not None:
+            vc, F = _aligned(value), 1
+            for d in value.shape[1:]:
+                F *= d
+        else:
+            alpha = torch.empty_like(scores)
+            _native.call("tgx_segment_softmax_fwd", row_ptr.data_ptr(),
+                         _native.idx_bits(row_ptr), n_dst, scores.data_ptr(), alpha.data_ptr(),
+                         lse.data_ptr(), stream)
+            out, vc, _, F = _csr_sum_launch(value, alpha, graph)
+            del alpha
         del scores
-        out, vc, _, F = _csr_sum_launch(value, alpha, graph)
-        del alpha
         ctx.graph, ctx.chain, ctx.roles, ctx.n_seg, ctx.W, ctx.F = graph, chain, roles, n_seg, W, F
         # A value that is also a source field of the score (the reference's
         # GAT example: value src.x, score over src.x): its two gradients meet
@@ -776,6 +785,40 @@ class NnAttentionFunction(torch.autograd.Function):
         grads += _layer_grads(chain, dweights, W, ctx.present, ctx.needs_input_grad,
                               5 + ctx.n_seg, L)
         return (None, None, None, None, dvalue, *grads)
+
+
+TGX_ROLE_SRC, TGX_ROLE_DST, TGX_ROLE_EDGE = 0, 1, 2
+
+
+def _fusable(value: torch.Tensor) -> bool:
+    """Value rows the one-pass softmax sum takes: fp32, 1 to 8 floats."""
+    width = 1
+    for d in value.shape[1:]:
+        width *= d
+    return value.dtype == torch.float32 and 1 <= width <= 8
+
+
+def _fused_softmax_sum(graph: Graph, scores: torch.Tensor, role: int, scale: float,
+                       value: torch.Tensor, lse: torch.Tensor,
+                       alpha: torch.Tensor | None = None) -> torch.Tensor | None:
+    """out = sum_e softmax_i(scale * score) value[col[e]] in one pass
+    (tgx_segment_softmax_sum_fwd), lse (and alpha, when given) filled; None
+    when the value is not fp32 rows of at most 8 floats (the caller then
+    runs the softmax and the CSR sum)."""
+    if not _fusable(value):
+        return None
+    width = 1
+    for d in value.shape[1:]:
+        width *= d
+    row_ptr, col_idx = graph._kernel_csr()
+    n_dst = graph.schema.num_dst
+    vc = _aligned(value)
+    out = torch.empty((n_dst, *value.shape[1:]), dtype=torch.float32, device=value.device)
+    _native.call("tgx_segment_softmax_sum_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
+                 _native.idx_bits(row_ptr), n_dst, scores.data_ptr(), role, float(scale),
+                 vc.data_ptr(), width, _p(alpha), lse.data_ptr(), out.data_ptr(),
+                 _native.stream_of(value))
+    return out
 
 
 def nn_attention(graph: Graph, chain, roles, fields, value: torch.Tensor) -> torch.Tensor:
@@ -839,15 +882,93 @@ class ScoreSoftmaxFunction(torch.autograd.Function):
         return grad.reshape(ctx.shape), None, None, None
 
 
+class ScoreAttentionFunction(torch.autograd.Function):
+    """out[i] = sum_e softmax_i(scale * score(e)) value[col[e]] for fp32
+    value rows of at most 8 floats: the forward is the one-pass softmax sum
+    (keeping the weights for the backward), the backward the composition's:
+    the value gradient over the transposed CSR with the weights, the
+    weights' gradient <dout[i], value[j]> in edge order, the softmax
+    Jacobian, the score gradient reduced onto the field's rows."""
+
+    @staticmethod
+    def forward(ctx, table: torch.Tensor, value: torch.Tensor, role: str, scale: float,
+                graph: Graph):
+        _on_graph_device(graph, table, value)
+        E = graph.num_edges
+        alpha = torch.empty(max(E, 1), dtype=torch.float32, device=table.device)[:E]
+        lse = torch.empty(max(graph.schema.num_dst, 1), dtype=torch.float32,
+                          device=table.device)
+        vc = _aligned(value)
+        out = _fused_softmax_sum(graph, table.reshape(-1).contiguous(), _ROLE_CODE[role],
+                                 scale, vc, lse, alpha)
+        ctx.graph, ctx.role, ctx.scale, ctx.shape = graph, role, float(scale), table.shape
+        ctx.save_for_backward(alpha, vc)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        alpha, vc = ctx.saved_tensors
+        graph: Graph = ctx.graph
+        n_dst, n_src, E = graph.schema.num_dst, graph.schema.num_src, graph.num_edges
+        F = 1
+        for d in vc.shape[1:]:
+            F *= d
+        dout = _aligned(dout.to(torch.float32))
+        stream = _native.stream_of(vc)
+        dvalue = dtable = None
+        if ctx.needs_input_grad[1]:
+            dvalue = torch.empty_like(vc)
+            if n_src:
+                t = graph._transposed()
+                partial = _partial(t.plan, F, vc.device)
+                _native.call("tgx_csr_sum_bwd", t.row_ptr_t.data_ptr(), t.col_t.data_ptr(),
+                             t.perm.data_ptr(), t.plan.ref, vc.data_ptr(), alpha.data_ptr(),
+                             dout.data_ptr(), dvalue.data_ptr(), None, n_dst, n_src, F,
+                             _native.DTYPE_F32, _p(partial), stream)
+        if ctx.needs_input_grad[0]:
+            row_ptr, col_idx = graph._kernel_csr()
+            dalpha = torch.empty(max(E, 1), dtype=torch.float32, device=vc.device)[:E]
+            dscore = torch.empty_like(dalpha)
+            if E:
+                _native.call("tgx_csr_edge_dot", row_ptr.data_ptr(), col_idx.data_ptr(),
+                             _native.idx_bits(row_ptr), graph._row_plan().ref, vc.data_ptr(),
+                             dout.data_ptr(), dalpha.data_ptr(), n_dst, n_src, F,
+                             _native.DTYPE_F32, stream)
+                _native.call("tgx_segment_softmax_bwd", row_ptr.data_ptr(),
+                             _native.idx_bits(row_ptr), n_dst, alpha.data_ptr(),
+                             dalpha.data_ptr(), dscore.data_ptr(), stream)
+            if ctx.role == "src":
+                grad = _reduce_rows_transposed(graph, dscore[:, None])[:, 0]
+            elif ctx.role == "dst":
+                grad = _reduce_rows(graph, dscore[:, None])[:, 0]
+            else:
+                grad = dscore
+            if ctx.scale != 1.0:
+                grad = grad * ctx.scale
+            dtable = grad.reshape(ctx.shape)
+        return dtable, dvalue, None, None, None
+
+
 def score_attention(graph: Graph, table: torch.Tensor, role: str, scale: float,
                     value: torch.Tensor) -> torch.Tensor:
     """out[i] = sum_e softmax_i(scale * score(e)) value[col[e]] on the HIP path:
-    the gathered segment softmax, then the weighted CSR sum.  A 16-bit score
+    one pass (softmax and value sum) for fp32 value rows of at most 8
+    floats, else the gathered segment softmax, then the weighted CSR sum.  A
+    16-bit score
     field is widened to fp32 first (the softmax runs in fp32, as the
     reference's oracle accumulates); the output has the value's type."""
     if table.dtype != torch.float32:
         table = table.float()
-    if torch.is_grad_enabled() and (table.requires_grad or value.requires_grad):
+    tracked = torch.is_grad_enabled() and (table.requires_grad or value.requires_grad)
+    if _fusable(value):
+        if tracked:
+            return ScoreAttentionFunction.apply(table, value, role, scale, graph)
+        _on_graph_device(graph, table, value)
+        lse = torch.empty(max(graph.schema.num_dst, 1), dtype=torch.float32,
+                          device=table.device)
+        return _fused_softmax_sum(graph, table.reshape(-1).contiguous(), _ROLE_CODE[role],
+                                  scale, value, lse)
+    if tracked:
         alpha = ScoreSoftmaxFunction.apply(table, role, scale, graph)
     else:
         alpha = _score_softmax_launch(table, role, scale, graph)

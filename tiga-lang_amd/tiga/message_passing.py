@@ -554,10 +554,11 @@ class MessagePassing(Kernel):
 
         describe = lambda: self._variant(
             graph, "score-softmax",
-            ("tgx_segment_softmax_gather_fwd", "tgx_csr_sum_fwd", "tgx_segment_softmax_bwd",
-             "tgx_csr_sum_bwd"),
-            f"segment softmax of the {role} score field per row (one wave per row), "
-            "weighted CSR sum of src.value; backward through the softmax Jacobian, "
+            ("tgx_segment_softmax_sum_fwd", "tgx_segment_softmax_gather_fwd", "tgx_csr_sum_fwd",
+             "tgx_segment_softmax_bwd", "tgx_csr_sum_bwd"),
+            f"segment softmax of the {role} score field per row and the weighted sum of "
+            "src.value in one pass (fp32 values of at most 8 floats, no gradient), else the "
+            "softmax weights and a weighted CSR sum; backward through the softmax Jacobian, "
             f"score gradient reduced per {role} row")
         return _Launch(graph, ((role, raw.score_field), ("src", raw.value_field)), run, describe)
 
@@ -787,10 +788,11 @@ class MessagePassing(Kernel):
         layer_widths = "-".join(str(l.linear.in_features) for l in chain) + "-1"
         describe = lambda: self._variant(
             graph, "nn-attention",
-            ("tgx_edge_mlp_scores", "tgx_segment_softmax_fwd", "tgx_csr_sum_fwd",
-             "tgx_edge_mlp_attention_backward", "tgx_csr_sum_bwd"),
+            ("tgx_edge_mlp_scores", "tgx_segment_softmax_sum_fwd", "tgx_segment_softmax_fwd",
+             "tgx_csr_sum_fwd", "tgx_edge_mlp_attention_backward", "tgx_csr_sum_bwd"),
             f"edge-parallel score network {layer_widths} (one edge per lane, uniform "
-            "weights), segment softmax per row, weighted CSR sum of the value; only each "
+            "weights), segment softmax per row with the value sum in the same pass (value "
+            "rows of at most 8 floats; else a weighted CSR sum); only each "
             "row's logsumexp and output are kept; backward replays the network per edge, "
             "recomputes the weights and the softmax Jacobian in the same kernel, on-chip "
             "weight-gradient sums, value gradient over the transposed CSR (a value that is "
