@@ -172,6 +172,8 @@ def test_attention_keeps_no_per_edge_weights():
     (24, ("elu", "sigmoid"), 0),               # W = 24, three layers
     (30, ("relu",), 0),                        # W = 32, two layers
     (20, (), 0),                               # one Linear: bias-free linear score
+    (16, ("leaky_relu", "leaky_relu"), 120),   # W = 16, three layers: the LeakyReLU kernel
+    (24, ("leaky_relu", "tanh"), 0),           # mixed: the runtime activation switch
 ])
 def test_score_chains(width, acts, hub):
     print(f"nn attention chain width={width} acts={acts} hub={hub}", flush=True)
@@ -187,7 +189,8 @@ def test_score_chains(width, acts, hub):
     mods = []
     dims = [14] + [width] * len(acts) + [1]
     names = {"tanh": nn.Tanh, "gelu": nn.GELU, "silu": nn.SiLU, "elu": lambda: nn.ELU(0.7),
-             "sigmoid": nn.Sigmoid, "relu": nn.ReLU}
+             "sigmoid": nn.Sigmoid, "relu": nn.ReLU,
+             "leaky_relu": lambda: nn.LeakyReLU(0.1)}
     for i in range(len(dims) - 1):
         mods.append(nn.Linear(dims[i], dims[i + 1], bias=bool(acts) or i > 0))
         if i < len(acts):
