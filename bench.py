@@ -164,13 +164,17 @@ def rmat_csr(scale, edge_factor, probs, seed, device):
 # once per pass).
 
 def gat_kernel_bytes(N, E, H, D):
+    """The folded backward the Torch front end runs: the forward also writes
+    pos (a row per node); the node pass reads dout, out and pos; the source
+    pass gathers dout and the destination node state per edge (no per-edge
+    output) and reads its source's sdz_dst; the da pass reads h once."""
     row = H * D * 4
     ns = H * 16
     return {
-        "gat_fwd_kernel": E * (4 + row) + N * (4 + 2 * row + ns),
-        "gat_delta_kernel": N * (2 * row + H * 4),
-        "gat_bwd_src_kernel": E * (4 + 4 + row + ns + H * 4) + N * (4 + row + ns + row),
-        "gat_bwd_dst_kernel": E * (H * 4) + N * (4 + row + 2 * row),
+        "gat_fwd_kernel": E * (4 + row) + N * (4 + 3 * row + ns),
+        "gat_delta_kernel": N * (3 * row + 2 * H * 4),
+        "gat_bwd_src_kernel": E * (4 + row + ns) + N * (4 + 2 * row + 2 * H * 4),
+        "gat_da_nodes_kernel": N * (row + 2 * H * 4),
     }
 
 

@@ -263,7 +263,13 @@ int tgx_csr_edge_dot(const void* row_ptr_dev, const void* col_dev, int idx_bits,
  * per (node, head): [0] logsumexp of the row's scores (-inf for an empty
  * row), [1] reserved for the backward (delta = <dout, out>), [2]
  * a_dst.h_dst[i], [3] a_src.h_dst[i].
- * partial_dev: tgx_partial_bytes(plan, H*D + 2*H) bytes (NULL if no split rows).
+ * partial_dev: tgx_partial_bytes(plan, H*D + 2*H) bytes, or with pos_dev
+ * tgx_partial_bytes(plan, 2*H*D + 3*H) (NULL if no split rows).
+ * pos_dev (NULL, or 16-byte aligned fp32 [n_dst, H, D]) receives for a
+ * backward the row sums over the edges whose z_e > 0 of
+ * softmax_i(s)_e * (h_src[j] - out[i]) (fp32, unrounded out): with it
+ * tgx_gat_bwd needs no per-edge pass over the destination rows, since a
+ * row's sum of the score gradients dz_e is (1 - slope) <dout[i], pos[i]>.
  * Supported shapes: any H >= 1 with D in {4, 8, 16, 32, 64, 128, 256}
  * (others return TGX_UNSUPPORTED).  Heads run in groups of a power-of-two
  * count with at most 256 values per node (H = 8, D = 64: two groups of 4),
@@ -275,11 +281,14 @@ int tgx_gat_fwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                 const float* a_src_dev, const float* a_dst_dev,
                 float negative_slope, void* out_dev, float* node_state_dev,
                 int64_t n_dst, int64_t n_src, int H, int D, int dtype, float* partial_dev,
-                void* stream);
+                float* pos_dev, void* stream);
 
-/* Workspace bytes for tgx_gat_bwd with these plans and element type. */
+/* Workspace bytes for tgx_gat_bwd with these plans and element type;
+ * folded != 0 for a backward given the forward's pos (it needs no per-edge
+ * buffer). */
 int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
-                          int64_t n_edges, int H, int D, int dtype, size_t* bytes);
+                          int64_t n_edges, int H, int D, int dtype, int folded,
+                          size_t* bytes);
 
 /* Fused backward from the saved logsumexp (no per-edge alpha is stored by
  * the forward and no float atomics are used): dh_src, dh_dst (of `dtype`),
@@ -288,16 +297,19 @@ int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
  * roles (then h_src == h_dst and n_src == n_dst are required) and receives
  * both roles' terms, rounded once; two buffers receive the source and the
  * destination terms separately.  Uses the transposed CSR (row_ptr_t, col_t, perm, inv_perm)
- * and its plan.  node_state slot 1 (delta) is overwritten. */
+ * and its plan.  node_state slot 1 (delta) is overwritten.  pos_dev: the
+ * forward's pos (then inv_perm may be NULL: the destination terms come
+ * from node passes), or NULL for the per-edge destination pass over the
+ * CSR, which reads each edge's score gradient through inv_perm. */
 int tgx_gat_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                 const tgx_row_plan* plan, const int32_t* row_ptr_t_dev,
                 const int32_t* col_t_dev, const int32_t* perm_dev,
                 const int32_t* inv_perm_dev, const tgx_row_plan* plan_t,
                 const void* h_src_dev, const void* h_dst_dev, const float* a_src_dev,
                 const float* a_dst_dev, float negative_slope, const void* out_dev,
-                float* node_state_dev, const void* dout_dev, void* dh_src_dev,
-                void* dh_dst_dev, float* da_src_dev, float* da_dst_dev, int64_t n_dst,
-                int64_t n_src, int64_t n_edges, int H, int D, int dtype,
+                float* node_state_dev, const float* pos_dev, const void* dout_dev,
+                void* dh_src_dev, void* dh_dst_dev, float* da_src_dev, float* da_dst_dev,
+                int64_t n_dst, int64_t n_src, int64_t n_edges, int H, int D, int dtype,
                 void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */

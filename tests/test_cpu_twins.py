@@ -463,7 +463,7 @@ def test_device_and_twin_reject_the_same_head_shapes(H, D):
     dummy = np.zeros(16, np.float32)
     gat_dev = _status("tgx_gat_fwd", p(rp), p(rp), 64, ctypes.byref(empty), p(dummy), p(dummy),
                       p(dummy), p(dummy), ctypes.c_float(0.2), p(dummy), p(dummy), 0, 0, H, D,
-                      2, None, None)
+                      2, None, None, None)
     gat_cpu = _status("tgx_cpu_gat_fwd", p(rp), p(rp), 64, ctypes.byref(empty), p(dummy),
                       p(dummy), p(dummy), p(dummy), ctypes.c_float(0.2), p(dummy), p(dummy), 0,
                       0, H, D, 2)

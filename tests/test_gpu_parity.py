@@ -372,6 +372,95 @@ def test_gat_large_scores_and_determinism():
     assert rel_err(grads[0][0].cpu(), e_out) <= RTOL32
 
 
+def _gat_c_abi(graph, hs, hd, a_s, a_d, slope, dout, folded, bipartite):
+    """One GAT forward + backward through the C ABI.  folded: the forward
+    writes pos and the backward forms the destination terms from node rows
+    (no inv_perm is passed); otherwise the per-edge destination pass."""
+    from tiga._ops import _VALUE_DTYPES, _partial
+    row_ptr, col = graph._kernel_csr()
+    n_dst, n_src, E = graph.schema.num_dst, graph.schema.num_src, graph.num_edges
+    _, H, D = hs.shape
+    code, stream, bits = _VALUE_DTYPES[hs.dtype], _native.stream_of(hs), _native.idx_bits(row_ptr)
+    ptr = lambda t: None if t is None else t.data_ptr()
+    out = torch.empty((n_dst, H, D), dtype=hs.dtype, device=DEV)
+    ns = torch.empty((n_dst, H, 4), dtype=torch.float32, device=DEV)
+    pos = torch.empty((n_dst, H, D), dtype=torch.float32, device=DEV) if folded else None
+    plan = graph._row_plan()
+    partial = _partial(plan, 2 * H * D + 3 * H if folded else H * D + 2 * H, DEV)
+    _native.call("tgx_gat_fwd", row_ptr.data_ptr(), col.data_ptr(), bits, plan.ref,
+                 hs.data_ptr(), hd.data_ptr(), a_s.data_ptr(), a_d.data_ptr(), slope,
+                 out.data_ptr(), ns.data_ptr(), n_dst, n_src, H, D, code, ptr(partial), ptr(pos),
+                 stream)
+    t = graph._transposed()
+    dhs = torch.empty_like(hs)
+    dhd = torch.empty_like(hd) if bipartite else dhs
+    das = torch.empty((H, D), dtype=torch.float32, device=DEV)
+    dad = torch.empty((H, D), dtype=torch.float32, device=DEV)
+    ws_bytes = ctypes.c_size_t()
+    _native.call("tgx_gat_bwd_workspace", plan.ref, t.plan.ref, E, H, D, code, int(folded),
+                 ctypes.byref(ws_bytes))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=DEV)
+    _native.call("tgx_gat_bwd", row_ptr.data_ptr(), col.data_ptr(), bits, plan.ref,
+                 t.row_ptr_t.data_ptr(), t.col_t.data_ptr(), t.perm.data_ptr(),
+                 None if folded else t.inv_perm.data_ptr(), t.plan.ref, hs.data_ptr(),
+                 hd.data_ptr(), a_s.data_ptr(), a_d.data_ptr(), slope, out.data_ptr(),
+                 ns.data_ptr(), ptr(pos), dout.data_ptr(), dhs.data_ptr(), dhd.data_ptr(),
+                 das.data_ptr(), dad.data_ptr(), n_dst, n_src, E, H, D, code, ws.data_ptr(),
+                 ws_bytes.value, stream)
+    torch.cuda.synchronize()
+    return out, dhs, dhd, das, dad
+
+
+# The backward with the forward's pos (destination terms from node rows,
+# which the Torch front end uses whenever a gradient is needed) and the
+# per-edge destination pass (pos = NULL) against float64 and each other:
+# hub rows split over several waves on both sides, empty rows and sources
+# without out-edges, two head groups (8 x 64), 16-bit elements, and slopes
+# other than 0.2 (1.0 makes the destination terms vanish).
+@pytest.mark.parametrize("H,D", [(8, 32), (8, 64), (1, 4)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("bipartite", [False, True])
+@pytest.mark.parametrize("slope", [0.2, -0.5, 1.0])
+def test_gat_folded_and_per_edge_backwards_agree(H, D, dtype, bipartite, slope):
+    print(f"gat folded H={H} D={D} {dtype} bipartite={bipartite} slope={slope}", flush=True)
+    n_dst, n_src = (1800, 2600) if bipartite else (2500, 2500)
+    rp, col = skewed_csr(300 + H, n_dst, n_src, mean_deg=10, hubs=(1400, 700), hot_src=11,
+                         hot_frac=0.3, empty_frac=0.05)
+    rng = np.random.default_rng(H * D + 7)
+    mk = lambda n: to_dev(rng.standard_normal((n, H, D)), dtype)
+    hs = mk(n_src)
+    hd = mk(n_dst) if bipartite else hs
+    dout = mk(n_dst)
+    a_s = to_dev(rng.standard_normal((H, D)) * 0.1, torch.float32)
+    a_d = to_dev(rng.standard_normal((H, D)) * 0.1, torch.float32)
+    graph = tg.Graph.from_csr(to_dev(rp, torch.int64), to_dev(col, torch.int64), num_src=n_src)
+    folded = _gat_c_abi(graph, hs, hd, a_s, a_d, slope, dout, True, bipartite)
+    per_edge = _gat_c_abi(graph, hs, hd, a_s, a_d, slope, dout, False, bipartite)
+    f = lambda t: t.detach().double().cpu().numpy()
+    e_out, _ = ref.gat_fwd(rp, col, f(hs), f(a_s), f(a_d), slope,
+                           h_dst=f(hd) if bipartite else None)
+    e_dhs, e_dhd, e_das, e_dad = ref.gat_bwd_bipartite(rp, col, f(hs), f(hd), f(a_s), f(a_d),
+                                                       slope, f(dout))
+    expect = [e_out, e_dhs if bipartite else e_dhs + e_dhd, e_dhd, e_das, e_dad]
+    tol = RTOL32 if dtype == torch.float32 else RTOL_BF16
+    names = ["out", "dh_src", "dh_dst", "da_src", "da_dst"]
+    for k, (name, a, b, e) in enumerate(zip(names, folded, per_edge, expect)):
+        if name == "dh_dst" and not bipartite:
+            continue
+        if slope == 1.0 and name in ("dh_dst", "da_dst"):
+            # z's gradient sums to zero over every row: the folded terms are
+            # exactly zero, the per-edge ones rounding noise.
+            assert not f(a).any(), name
+            continue
+        err_f, err_p, err_fp = rel_err(f(a), e), rel_err(f(b), e), rel_err(f(a), f(b))
+        print(f"  {name}: folded {err_f:.2e}, per-edge {err_p:.2e}, between {err_fp:.2e}",
+              flush=True)
+        assert err_f <= tol and err_p <= tol, name
+        # The two forwards are one computation; the destination terms differ
+        # only in summation order.
+        assert err_fp <= (1e-6 if k == 0 and dtype == torch.float32 else tol), name
+
+
 # ---- dot-product attention (bf16, fp32 accumulate) ---------------------------
 
 RTOL_BF16 = 2e-2

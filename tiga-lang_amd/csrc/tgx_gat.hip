@@ -21,8 +21,8 @@
 // hd occupies HL = D/4 consecutive lanes and its dot products reduce with
 // DPP inside the lane group.  node_state is [N_dst, H, 4] fp32 = {logsumexp,
 // delta, a_dst.hd[i], a_src.hd[i]} so one 16-byte load per lane brings every
-// per-(node, head) scalar the backward needs (slot 3 is a_src.h of the same
-// node, which a homogeneous relation's source pass reads).
+// per-(node, head) scalar the backward needs (slot 3, a_src.h of the same
+// node, is not read by the backward).
 //
 // Backward (no float atomics, nothing per-edge saved by the forward):
 //   B1 node pass   delta[i] = <dout[i], out[i]> per head
@@ -39,6 +39,20 @@
 //   fixed order, so every output is deterministic.  With 16-bit elements and
 //   one feature tensor, the source pass's dh contribution waits in an fp32
 //   workspace until B3 adds the destination term and rounds once.
+//
+// Folded destination term (a forward that also writes `pos`): a row's sum
+// of dz needs no per-edge pass.  With ds_e = alpha_e (<dout[i], hs[j]> -
+// delta[i]), sum_e ds_e = <dout[i], out[i]> - delta[i] = 0 over a non-empty
+// row, so
+//   sum_e dz_e = sum_{z_e > 0} ds_e + slope sum_{z_e <= 0} ds_e
+//              = (1 - slope) sum_{z_e > 0} ds_e
+//              = (1 - slope) <dout[i], pos[i]>,
+//   pos[i] = sum_{z_e > 0} alpha_e (hs[j] - out[i])      (fp32, [N_dst, H, D]),
+// which the forward accumulates beside out (the z > 0 test is the same fp32
+// z the source pass branches on).  B1 then also forms sdz_dst[i], B2 adds
+// sdz_dst[j] a_dst to a homogeneous relation's dh[j] (or B1 writes a
+// bipartite relation's dhd[i] = sdz_dst[i] a_dst), no dz is stored and B3
+// becomes a node pass over h for da_src and da_dst.
 #include <hip/hip_runtime.h>
 
 #include "tgx_device.h"
@@ -78,10 +92,16 @@ struct GatFwdArgs {
   float slope;
   T* out;
   float* ns;
-  float* partial;  // per chunk: acc[4G] | m[H] | l[H]
-  int64_t ld;      // values between consecutive nodes' rows of hs, hd and out
+  float* partial;  // per chunk: acc[4G] | m[H] | l[H] (POS: | pacc[4G] | pl[H])
+  float* pos;      // POS: [N_dst, H, D] fp32, the folded destination term's rows
+  int64_t ld;      // values between consecutive nodes' rows of hs, hd, out and pos
   int64_t nsld;    // floats between consecutive nodes' rows of ns
 };
+
+// Floats per chunk of the forward's partial buffer.
+__host__ __device__ constexpr int64_t gat_partial_floats(int64_t HD, int64_t H, bool pos) {
+  return pos ? 2 * HD + 3 * H : HD + 2 * H;
+}
 
 // Index of lane `src` in a wave, read by every lane (edge groups differ).
 template <int EPW>
@@ -90,12 +110,34 @@ __device__ __forceinline__ int fetch_lane(int v, int src) {
   return __shfl(v, src, 64);
 }
 
-template <int DT, typename I, int G, int HL, int U>
-__global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<DT, I> a) {
+// A finished row: out = acc / l and (POS) pos = (pacc - pl out) / l, both
+// from the fp32 state.
+template <class V, bool POS, int NA>
+__device__ __forceinline__ void store_row(typename V::T* out, float* pos, int64_t off,
+                                          const SoftState<NA>& st) {
+  const float inv = 1.f / st.l;
+  const f32x4 o = {st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv};
+  V::store(out + off, o);
+  if constexpr (POS) {
+    const float w = st.acc[8] * inv;
+    st4(pos + off, f32x4{st.acc[4] * inv - w * o[0], st.acc[5] * inv - w * o[1],
+                         st.acc[6] * inv - w * o[2], st.acc[7] * inv - w * o[3]});
+  }
+}
+
+// POS: the softmax state also carries pacc = sum over z > 0 of p hs[j]
+// (acc[4..7]) and pl = sum over z > 0 of p (acc[8]), rescaled with acc and
+// l, so pos[i] = (pacc - pl out[i]) / l.
+// (POS adds 5 accumulators: held to 96 VGPRs, the plain kernel's 5 waves
+// per SIMD, where that needs no spill: heads of up to 64 values.)
+template <int DT, typename I, int G, int HL, int U, bool POS>
+__global__ __launch_bounds__(kTaskBlock, POS && HL <= 16 ? 5 : 1) void gat_fwd_kernel(
+    GatFwdArgs<DT, I> a) {
   using V = Vals<DT, 4>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
+  constexpr int NA = POS ? 9 : 4;
   const Task t = decode_task(a.plan, a.row_ptr, global_wave());
   if (t.kind == kTaskNone) return;
   const int lane = lane_id();
@@ -114,6 +156,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<DT, I> a
       const float ssrc = group_sum<HL>(dot4(as4, hi));
       if (g == 0) {
         V::store(a.out + i * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+        if constexpr (POS) st4(a.pos + i * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
         if (head_lead) st4(a.ns + i * a.nsld + hd * 4, f32x4{kNegInf, 0.f, sdst, ssrc});
       }
     }
@@ -124,7 +167,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<DT, I> a
   const f32x4 hi = V::widen(V::load(a.hd + row * a.ld + 4 * c));
   const float sdst = group_sum<HL>(dot4(ad4, hi));
 
-  SoftState<4> st;
+  SoftState<NA> st;
   st.init();
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
     const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
@@ -138,12 +181,14 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<DT, I> a
         x[u] = V::load(a.hs + static_cast<int64_t>(j) * a.ld + 4 * c);
       }
       float s[U];
+      bool up[U];
       float mc = kNegInf;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int slot = k + u * EPW + g;
         const float z = group_sum<HL>(dot4(as4, V::widen(x[u]))) + sdst;
         s[u] = slot < n ? leaky_relu(z, a.slope) : kNegInf;
+        up[u] = z > 0.f;
         mc = fmaxf(mc, s[u]);
       }
       if (mc > st.m) st.rescale(mc);
@@ -154,6 +199,12 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<DT, I> a
         const f32x4 xv = V::widen(x[u]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) st.acc[q] += p * xv[q];
+        if constexpr (POS) {
+          const float pp = up[u] ? p : 0.f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) st.acc[4 + q] += pp * xv[q];
+          st.acc[8] += pp;
+        }
       }
     }
   }
@@ -161,30 +212,33 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_kernel(GatFwdArgs<DT, I> a
   for (int mask = G; mask < kWave; mask <<= 1) st.merge_xor(mask);
   if (g != 0) return;
   if (t.kind == kTaskChunk) {
-    float* p = a.partial + static_cast<int64_t>(t.slot) * (HD + 2 * H);
+    float* p = a.partial + t.slot * gat_partial_floats(HD, H, POS);
     st4(p + 4 * c, f32x4{st.acc[0], st.acc[1], st.acc[2], st.acc[3]});
     if (head_lead) {
       p[HD + hd] = st.m;
       p[HD + H + hd] = st.l;
     }
+    if constexpr (POS) {
+      st4(p + HD + 2 * H + 4 * c, f32x4{st.acc[4], st.acc[5], st.acc[6], st.acc[7]});
+      if (head_lead) p[2 * HD + 2 * H + hd] = st.acc[8];
+    }
     return;
   }
-  const float inv = 1.f / st.l;
-  V::store(a.out + row * a.ld + 4 * c,
-           f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
+  store_row<V, POS>(a.out, a.pos, row * a.ld + 4 * c, st);
   const float ssrc_i = group_sum<HL>(dot4(as4, hi));
   if (head_lead) st4(a.ns + row * a.nsld + hd * 4, f32x4{st.m + __logf(st.l), 0.f, sdst, ssrc_i});
 }
 
-template <int DT, int G, int HL>
+template <int DT, int G, int HL, bool POS>
 __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
     PlanView plan, const float* __restrict__ partial,
     const typename Vals<DT, 4>::T* __restrict__ hd_rows, const float* __restrict__ a_src,
     const float* __restrict__ a_dst, typename Vals<DT, 4>::T* __restrict__ out,
-    float* __restrict__ ns, int64_t ld, int64_t nsld) {
+    float* __restrict__ pos, float* __restrict__ ns, int64_t ld, int64_t nsld) {
   using V = Vals<DT, 4>;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
+  constexpr int NA = POS ? 9 : 4;
   const int64_t k = global_wave();
   if (k >= plan.n_split) return;
   const int lane = lane_id();
@@ -192,17 +246,23 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
   const int c = lane, hd = c / HL;
   const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
-  SoftState<4> st;
+  SoftState<NA> st;
   st.init();
   for (int q = c0; q < c1; ++q) {
-    const float* p = partial + static_cast<int64_t>(q) * (HD + 2 * H);
+    const float* p = partial + static_cast<int64_t>(q) * gat_partial_floats(HD, H, POS);
     const f32x4 acc = ld4(p + 4 * c);
-    const float accs[4] = {acc[0], acc[1], acc[2], acc[3]};
+    float accs[NA];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) accs[k] = acc[k];
+    if constexpr (POS) {
+      const f32x4 pacc = ld4(p + HD + 2 * H + 4 * c);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) accs[4 + k] = pacc[k];
+      accs[8] = p[2 * HD + 2 * H + hd];
+    }
     st.merge(p[HD + hd], p[HD + H + hd], accs);
   }
-  const float inv = 1.f / st.l;
-  V::store(out + row * ld + 4 * c,
-           f32x4{st.acc[0] * inv, st.acc[1] * inv, st.acc[2] * inv, st.acc[3] * inv});
+  store_row<V, POS>(out, pos, row * ld + 4 * c, st);
   const f32x4 hi = V::widen(V::load(hd_rows + row * ld + 4 * c));
   const float sdst = group_sum<HL>(dot4(ld4(a_dst + 4 * c), hi));
   const float ssrc = group_sum<HL>(dot4(ld4(a_src + 4 * c), hi));
@@ -212,20 +272,39 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
 // ---------------------------------------------------------------------------
 // Backward.
 
-template <int DT, int G, int HL>
+// Destination term of a folded backward (B1 with `pos`).
+template <int DT>
+struct GatFold {
+  const float* pos;   // [N_dst, H, D] fp32 from the forward
+  float one_minus_slope;
+  float* sdz_dst;     // [N_dst, H] out: sum of dz over each row's in-edges
+  const float* a_dst;
+  typename Vals<DT, 4>::T* dhd;  // FOLD == 2: the bipartite destination gradient
+};
+
+// FOLD 0: delta only; 1: and sdz_dst = (1 - slope) <dout, pos>; 2: and
+// dhd[i] = sdz_dst[i] a_dst (a bipartite relation's destination gradient).
+template <int DT, int G, int HL, int FOLD>
 __global__ __launch_bounds__(kTaskBlock) void gat_delta_kernel(
     const typename Vals<DT, 4>::T* __restrict__ dout,
     const typename Vals<DT, 4>::T* __restrict__ out, float* __restrict__ ns, int64_t n_nodes,
-    int64_t ld, int64_t nsld) {
+    int64_t ld, int64_t nsld, GatFold<DT> f) {
   using V = Vals<DT, 4>;
   constexpr int EPW = kWave / G;
+  constexpr int H = G / HL;
   const int lane = lane_id();
   const int c = lane % G, hd = c / HL;
   const int64_t node = global_wave() * EPW + lane / G;
   if (node >= n_nodes) return;
-  const float d = group_sum<HL>(dot4(V::widen(V::load(dout + node * ld + 4 * c)),
-                                     V::widen(V::load(out + node * ld + 4 * c))));
+  const int64_t off = node * ld + 4 * c;
+  const f32x4 dv = V::widen(V::load(dout + off));
+  const float d = group_sum<HL>(dot4(dv, V::widen(V::load(out + off))));
   if (c % HL == 0) ns[node * nsld + hd * 4 + 1] = d;
+  if constexpr (FOLD > 0) {
+    const float sd = f.one_minus_slope * group_sum<HL>(dot4(dv, ld4(f.pos + off)));
+    if (c % HL == 0) f.sdz_dst[node * H + hd] = sd;
+    if constexpr (FOLD == 2) V::store(f.dhd + off, sd * ld4(f.a_dst + 4 * c));
+  }
 }
 
 template <int DT>
@@ -243,15 +322,21 @@ struct GatSrcArgs {
   float* dh_acc;    // fp32 [N, HD] (one feature tensor: B3 adds to it), or null
   T* dhs;           // the source gradient itself when dh_acc is null
   float* partial;   // per chunk: [4G] dh contribution | [H] sum of dz
-  float* dz;        // [E, H] in transposed edge order (coalesced)
+  float* dz;        // [E, H] in transposed edge order (coalesced); MODE 0 only
   float* sdz_src;   // [N_src, H] sum of dz over each source's out-edges
+  const float* a_dst;    // MODE 2
+  const float* sdz_dst;  // MODE 2: [N, H] from B1
   int64_t ld;       // values between consecutive nodes' rows of hs, dout, dh
   int64_t nsld;     // floats between consecutive nodes' rows of ns
 };
 
-// One wave per task of the transposed-CSR plan (source rows).
-template <int DT, int G, int HL, int U>
-__global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs<DT> a) {
+// One wave per task of the transposed-CSR plan (source rows).  MODE 0: dz
+// stored for B3; 1 (folded, bipartite): no dz; 2 (folded, one feature
+// tensor): no dz, and dh[j] also takes the destination term sdz_dst[j] a_dst.
+// (The folded modes are held to the per-edge mode's 7 waves per SIMD.)
+template <int DT, int G, int HL, int U, int MODE>
+__global__ __launch_bounds__(kTaskBlock, MODE ? 7 : 1) void gat_bwd_src_kernel(
+    GatSrcArgs<DT> a) {
   using V = Vals<DT, 4>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 4 * G;
@@ -267,7 +352,9 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs<DT> 
     for (int k = 0; k < t.n_empty; ++k) {
       const int64_t j = uniform(a.plan.rows[t.empty0 + k]);
       if (g == 0) {
-        if (a.dh_acc)
+        if constexpr (MODE == 2)
+          V::store(a.dhs + j * a.ld + 4 * c, a.sdz_dst[j * H + hd] * ld4(a.a_dst + 4 * c));
+        else if (a.dh_acc)
           st4(a.dh_acc + j * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
         else
           V::store(a.dhs + j * a.ld + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
@@ -309,7 +396,9 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs<DT> 
         const float dzv = z > 0.f ? ds : ds * a.slope;
         dha += alpha * du;
         sdz += dzv;
-        if (valid && head_lead) a.dz[(base + slot) * H + hd] = dzv;
+        if constexpr (MODE == 0) {
+          if (valid && head_lead) a.dz[(base + slot) * H + hd] = dzv;
+        }
       }
     }
   }
@@ -322,12 +411,14 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs<DT> 
     sdz += __shfl_xor(sdz, mask, 64);
   }
   if (g != 0) return;
-  const f32x4 contrib = dha + sdz * as4;
+  f32x4 contrib = dha + sdz * as4;
   if (t.kind == kTaskChunk) {
     float* p = a.partial + static_cast<int64_t>(t.slot) * (HD + H);
     st4(p + 4 * c, contrib);
     if (head_lead) p[HD + hd] = sdz;
   } else {
+    // (Folded modes run with dh_acc == null: dh is final here.)
+    if constexpr (MODE == 2) contrib = contrib + a.sdz_dst[j * H + hd] * ld4(a.a_dst + 4 * c);
     if (a.dh_acc)
       st4(a.dh_acc + j * a.ld + 4 * c, contrib);
     else
@@ -336,10 +427,12 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_kernel(GatSrcArgs<DT> 
   }
 }
 
-template <int DT, int G, int HL>
+// FOLD: a homogeneous relation's dh also takes sdz_dst[row] a_dst.
+template <int DT, int G, int HL, bool FOLD>
 __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
     PlanView plan, const float* __restrict__ partial, float* __restrict__ dh_acc,
-    typename Vals<DT, 4>::T* __restrict__ dhs, float* __restrict__ sdz_src, int64_t ld) {
+    typename Vals<DT, 4>::T* __restrict__ dhs, float* __restrict__ sdz_src,
+    const float* __restrict__ a_dst, const float* __restrict__ sdz_dst, int64_t ld) {
   using V = Vals<DT, 4>;
   constexpr int HD = 4 * G;
   constexpr int H = G / HL;
@@ -357,6 +450,7 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
     s += ld4(p + 4 * c);
     z += p[HD + hd];
   }
+  if constexpr (FOLD) s = s + sdz_dst[row * H + hd] * ld4(a_dst + 4 * c);
   if (dh_acc)
     st4(dh_acc + row * ld + 4 * c, s);
   else
@@ -499,12 +593,27 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_dst_merge_kernel(
   finish_dh<V, FUSED>(dhd, dh_acc, row * ld + 4 * c, s, ld4(a_dst + 4 * c));
 }
 
-// da_src's per-wave partials over the sources of a bipartite relation:
-// sum_j sdz_src[j] hs[j], persistent with static striding (deterministic).
-template <int DT, int G, int HL>
-__global__ __launch_bounds__(kTaskBlock) void gat_da_src_kernel(
-    const typename Vals<DT, 4>::T* __restrict__ hs, const float* __restrict__ sdz_src,
-    double* __restrict__ dap_src, int64_t n_src, int64_t ld) {
+// Per-wave partials of da over node rows: sum_j sdz_a[j] h[j] (and with
+// BOTH, sum_j sdz_b[j] h[j] from the same row read), persistent with static
+// striding (deterministic).  A bipartite relation's da_src (sdz_src over
+// hs), and in a folded backward its da_dst (sdz_dst over hd), or both of a
+// homogeneous relation's in one pass.
+template <int G>
+__device__ __forceinline__ void wave_sum_f64(f64x4& v) {
+#pragma unroll
+  for (int mask = G; mask < kWave; mask <<= 1) {
+    v[0] += __shfl_xor(v[0], mask, 64);
+    v[1] += __shfl_xor(v[1], mask, 64);
+    v[2] += __shfl_xor(v[2], mask, 64);
+    v[3] += __shfl_xor(v[3], mask, 64);
+  }
+}
+
+template <int DT, int G, int HL, bool BOTH>
+__global__ __launch_bounds__(kTaskBlock) void gat_da_nodes_kernel(
+    const typename Vals<DT, 4>::T* __restrict__ h, const float* __restrict__ sdz_a,
+    double* __restrict__ dap_a, const float* __restrict__ sdz_b, double* __restrict__ dap_b,
+    int64_t n, int64_t ld) {
   using V = Vals<DT, 4>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 4 * G;
@@ -513,20 +622,23 @@ __global__ __launch_bounds__(kTaskBlock) void gat_da_src_kernel(
   const int g = lane / G;
   const int c = lane % G;
   const int hd = c / HL;
-  f64x4 ds = {0.0, 0.0, 0.0, 0.0};
+  f64x4 da = {0.0, 0.0, 0.0, 0.0};
+  f64x4 db = {0.0, 0.0, 0.0, 0.0};
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * EPW;
-  for (int64_t j = global_wave() * EPW + g; j < n_src; j += stride)
-    acc_f64(ds, sdz_src[j * H + hd], V::widen(V::load(hs + j * ld + 4 * c)));
-#pragma unroll
-  for (int mask = G; mask < kWave; mask <<= 1) {
-    ds[0] += __shfl_xor(ds[0], mask, 64);
-    ds[1] += __shfl_xor(ds[1], mask, 64);
-    ds[2] += __shfl_xor(ds[2], mask, 64);
-    ds[3] += __shfl_xor(ds[3], mask, 64);
+  for (int64_t j = global_wave() * EPW + g; j < n; j += stride) {
+    const f32x4 hv = V::widen(V::load(h + j * ld + 4 * c));
+    acc_f64(da, sdz_a[j * H + hd], hv);
+    if constexpr (BOTH) acc_f64(db, sdz_b[j * H + hd], hv);
   }
+  wave_sum_f64<G>(da);
+  if constexpr (BOTH) wave_sum_f64<G>(db);
   if (g == 0) {
-    double* p = dap_src + global_wave() * HD + 4 * c;
-    p[0] = ds[0]; p[1] = ds[1]; p[2] = ds[2]; p[3] = ds[3];
+    double* p = dap_a + global_wave() * HD + 4 * c;
+    p[0] = da[0]; p[1] = da[1]; p[2] = da[2]; p[3] = da[3];
+    if constexpr (BOTH) {
+      double* q = dap_b + global_wave() * HD + 4 * c;
+      q[0] = db[0]; q[1] = db[1]; q[2] = db[2]; q[3] = db[3];
+    }
   }
 }
 
@@ -612,24 +724,28 @@ int gat_fwd_launch(const GatFwdArgs<DT, I>& a, hipStream_t s) {
   // fp32 forward (8: +2%, 12: +1%, 16: +5% time on the 1M-node graph).
   constexpr int U = EPW >= 10 ? 1 : 10 / EPW;
   const int64_t waves = plan_waves(a.plan);
+  const bool pos = a.pos != nullptr;
   if (waves > 0) {
     TGX_PROFILE("gat_fwd_kernel", s);
-    gat_fwd_kernel<DT, I, G, HL, U><<<ceil_div(waves, kWavesPerBlock), kTaskBlock, 0, s>>>(a);
+    const auto k = pos ? gat_fwd_kernel<DT, I, G, HL, U, true>
+                       : gat_fwd_kernel<DT, I, G, HL, U, false>;
+    k<<<ceil_div(waves, kWavesPerBlock), kTaskBlock, 0, s>>>(a);
     TGX_LAUNCHED("gat_fwd_kernel");
   }
   if (a.plan.n_split > 0) {
     TGX_PROFILE("gat_fwd_merge_kernel", s);
-    gat_fwd_merge_kernel<DT, G, HL>
-        <<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-            a.plan, a.partial, a.hd, a.a_src, a.a_dst, a.out, a.ns, a.ld, a.nsld);
+    const auto k = pos ? gat_fwd_merge_kernel<DT, G, HL, true>
+                       : gat_fwd_merge_kernel<DT, G, HL, false>;
+    k<<<ceil_div(a.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        a.plan, a.partial, a.hd, a.a_src, a.a_dst, a.out, a.pos, a.ns, a.ld, a.nsld);
     TGX_LAUNCHED("gat_fwd_merge_kernel");
   }
   return TGX_OK;
 }
 
 struct GatBwdLayout {
-  size_t dz_off, sdz_off, src_part_off, dst_part_off, dap_src_off, dap_dst_off, slices_off,
-      dh_acc_off, bytes;
+  size_t dz_off, sdz_off, sdz_dst_off, src_part_off, dst_part_off, dap_src_off, dap_dst_off,
+      slices_off, dh_acc_off, bytes;
   int64_t src_waves, dst_waves;
 };
 
@@ -638,24 +754,29 @@ struct GatBwdLayout {
 // passes), comes first and spans whole rows, [n_dst, H_total * D] fp32: the
 // kernels index it with the row stride of dh itself, each head group at its
 // own column offset.
+// Folded (the forward wrote pos): no dz, no dh_acc and no B3 partials; an
+// sdz_dst row per destination, and the dst da partials sized for a node pass.
 GatBwdLayout gat_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t,
-                            int64_t n_edges, int H, int D, int dtype, int H_total) {
+                            int64_t n_edges, int H, int D, int dtype, int H_total,
+                            bool folded) {
   GatBwdLayout L;
   const int64_t HD = static_cast<int64_t>(H) * D;
   // Partial buffers are sized for the largest grid; launches may use fewer.
-  // The bipartite da_src pass takes at most one wave per source.
+  // The node passes over da take at most one wave per node.
   const PlanView pv = plan_view(plan);
-  L.dst_waves = persist_blocks(plan_waves(pv), kPersistBlocks) * kWavesPerBlock;
+  L.dst_waves = persist_blocks(folded ? plan.n_rows : plan_waves(pv), kPersistBlocks) *
+                kWavesPerBlock;
   L.src_waves = persist_blocks(plan_t.n_rows, kPersistBlocks) * kWavesPerBlock;
   if (L.src_waves < L.dst_waves) L.src_waves = L.dst_waves;
   const int64_t nodes = plan.n_rows > plan_t.n_rows ? plan.n_rows : plan_t.n_rows;
   Carve c{nullptr, 0};
   L.dh_acc_off = reinterpret_cast<size_t>(c.take<float>(
-      dtype == TGX_DTYPE_F32 ? 0 : plan.n_rows * static_cast<int64_t>(H_total) * D));
-  L.dz_off = reinterpret_cast<size_t>(c.take<float>(n_edges * H));
+      dtype == TGX_DTYPE_F32 || folded ? 0 : plan.n_rows * static_cast<int64_t>(H_total) * D));
+  L.dz_off = reinterpret_cast<size_t>(c.take<float>(folded ? 0 : n_edges * H));
   L.sdz_off = reinterpret_cast<size_t>(c.take<float>(nodes * H));
+  L.sdz_dst_off = reinterpret_cast<size_t>(c.take<float>(folded ? plan.n_rows * H : 0));
   L.src_part_off = reinterpret_cast<size_t>(c.take<float>(plan_t.n_chunks * (HD + H)));
-  L.dst_part_off = reinterpret_cast<size_t>(c.take<float>(plan.n_chunks * H));
+  L.dst_part_off = reinterpret_cast<size_t>(c.take<float>(folded ? 0 : plan.n_chunks * H));
   L.dap_src_off = reinterpret_cast<size_t>(c.take<double>(L.src_waves * HD));
   L.dap_dst_off = reinterpret_cast<size_t>(c.take<double>(L.dst_waves * HD));
   L.slices_off = reinterpret_cast<size_t>(c.take<double>(2 * kDaSlices * HD));
@@ -668,10 +789,17 @@ struct GatBwdIo {
   const float *a_src, *a_dst;
   void *dhs, *dhd;
   float *ns, *da_src, *da_dst;
+  const float* pos;  // the forward's folded destination rows, or null
   int64_t n_dst, n_src, ld, nsld;
   float slope;
   int64_t col_off;   // the head group's first column (h0 * D) within a row
 };
+
+// Node-pass grid: one wave per EPW nodes, at most what stays resident.
+template <class Kernel>
+int64_t node_blocks(Kernel k, int64_t n, int epw) {
+  return persist_blocks(ceil_div(n, epw), resident_blocks(k, kTaskBlock));
+}
 
 template <int DT, typename I, int G, int HL>
 int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* row_ptr_t,
@@ -685,76 +813,112 @@ int gat_bwd_launch(const I* row_ptr, const tgx_row_plan& plan, const int32_t* ro
   constexpr int U = EPW >= 4 ? 1 : 4 / EPW;
   constexpr int HD = 4 * G;
   const bool homogeneous = io.dhs == io.dhd;
-  float* dz = reinterpret_cast<float*>(ws + L.dz_off);
+  const bool folded = io.pos != nullptr;
+  float* dz = folded ? nullptr : reinterpret_cast<float*>(ws + L.dz_off);
   float* sdz_src = reinterpret_cast<float*>(ws + L.sdz_off);
+  float* sdz_dst = folded ? reinterpret_cast<float*>(ws + L.sdz_dst_off) : nullptr;
   float* src_part = reinterpret_cast<float*>(ws + L.src_part_off);
   float* dst_part = reinterpret_cast<float*>(ws + L.dst_part_off);
   double* dap_src = reinterpret_cast<double*>(ws + L.dap_src_off);
   double* dap_dst = reinterpret_cast<double*>(ws + L.dap_dst_off);
-  // One feature tensor: the source pass's contribution to dh is completed by
-  // the destination pass, in place for fp32, in fp32 workspace otherwise.
+  // One feature tensor, not folded: the source pass's contribution to dh is
+  // completed by the destination pass, in place for fp32, in fp32 workspace
+  // otherwise.  Folded, the source pass writes the final dh.
   float* dh_acc = nullptr;
-  if (homogeneous)
+  if (homogeneous && !folded)
     dh_acc = DT == TGX_DTYPE_F32
                  ? static_cast<float*>(io.dhd)
                  : reinterpret_cast<float*>(ws + L.dh_acc_off) + io.col_off;
   const T* hs = static_cast<const T*>(io.hs);
   const T* hd = static_cast<const T*>(io.hd);
   const PlanView pv = plan_view(plan), pt = plan_view(plan_t);
+  const int src_mode = !folded ? 0 : homogeneous ? 2 : 1;
 
-  {
+  if (io.n_dst > 0) {
     TGX_PROFILE("gat_delta_kernel", s);
-    gat_delta_kernel<DT, G, HL>
-        <<<ceil_div(ceil_div(io.n_dst, EPW), kWavesPerBlock), kTaskBlock, 0, s>>>(
-            static_cast<const T*>(io.dout), static_cast<const T*>(io.out), io.ns, io.n_dst,
-            io.ld, io.nsld);
+    const GatFold<DT> f{io.pos, 1.f - io.slope, sdz_dst, io.a_dst, static_cast<T*>(io.dhd)};
+    const auto k = !folded ? gat_delta_kernel<DT, G, HL, 0>
+                   : homogeneous ? gat_delta_kernel<DT, G, HL, 1>
+                                 : gat_delta_kernel<DT, G, HL, 2>;
+    k<<<ceil_div(ceil_div(io.n_dst, EPW), kWavesPerBlock), kTaskBlock, 0, s>>>(
+        static_cast<const T*>(io.dout), static_cast<const T*>(io.out), io.ns, io.n_dst, io.ld,
+        io.nsld, f);
     TGX_LAUNCHED("gat_delta_kernel");
   }
 
   const GatSrcArgs<DT> sa{row_ptr_t, col_t, perm, pt, hs, io.a_src, io.slope, io.ns,
                           static_cast<const T*>(io.dout), dh_acc, static_cast<T*>(io.dhs),
-                          src_part, dz, sdz_src, io.ld, io.nsld};
-  const GatDstArgs<DT, I> da{row_ptr, pv, hd, io.a_dst, dz, inv_perm, sdz_src, dh_acc,
-                             static_cast<T*>(io.dhd), dst_part, dap_src, dap_dst,
-                             plan_waves(pv), io.ld};
-  const auto dst_kernel = homogeneous ? gat_bwd_dst_kernel<DT, I, G, HL, true>
-                                      : gat_bwd_dst_kernel<DT, I, G, HL, false>;
-  const int64_t dst_blocks =
-      persist_blocks(plan_waves(pv), resident_blocks(dst_kernel, kTaskBlock));
+                          src_part, dz, sdz_src, io.a_dst, sdz_dst, io.ld, io.nsld};
   if (plan_waves(pt) > 0) {
     TGX_PROFILE("gat_bwd_src_kernel", s);
-    gat_bwd_src_kernel<DT, G, HL, U>
-        <<<ceil_div(plan_waves(pt), kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
+    const auto k = src_mode == 0 ? gat_bwd_src_kernel<DT, G, HL, U, 0>
+                   : src_mode == 1 ? gat_bwd_src_kernel<DT, G, HL, U, 1>
+                                   : gat_bwd_src_kernel<DT, G, HL, U, 2>;
+    k<<<ceil_div(plan_waves(pt), kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
     TGX_LAUNCHED("gat_bwd_src_kernel");
   }
   if (pt.n_split > 0) {
     TGX_PROFILE("gat_bwd_src_merge_kernel", s);
-    gat_bwd_src_merge_kernel<DT, G, HL>
-        <<<ceil_div(pt.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-            pt, src_part, dh_acc, static_cast<T*>(io.dhs), sdz_src, io.ld);
+    const auto k = src_mode == 2 ? gat_bwd_src_merge_kernel<DT, G, HL, true>
+                                 : gat_bwd_src_merge_kernel<DT, G, HL, false>;
+    k<<<ceil_div(pt.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+        pt, src_part, dh_acc, static_cast<T*>(io.dhs), sdz_src, io.a_dst, sdz_dst, io.ld);
     TGX_LAUNCHED("gat_bwd_src_merge_kernel");
   }
-  {
-    TGX_PROFILE("gat_bwd_dst_kernel", s);
-    dst_kernel<<<dst_blocks, kTaskBlock, 0, s>>>(da);
-    TGX_LAUNCHED("gat_bwd_dst_kernel");
-  }
-  if (pv.n_split > 0) {
-    TGX_PROFILE("gat_bwd_dst_merge_kernel", s);
-    const auto merge = homogeneous ? gat_bwd_dst_merge_kernel<DT, G, HL, true>
-                                   : gat_bwd_dst_merge_kernel<DT, G, HL, false>;
-    merge<<<ceil_div(pv.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        pv, dst_part, io.a_dst, dh_acc, static_cast<T*>(io.dhd), io.ld);
-    TGX_LAUNCHED("gat_bwd_dst_merge_kernel");
-  }
-  int64_t src_blocks = dst_blocks;
-  if (!homogeneous) {
-    src_blocks = persist_blocks(ceil_div(io.n_src, EPW),
-                                resident_blocks(gat_da_src_kernel<DT, G, HL>, kTaskBlock));
-    TGX_PROFILE("gat_da_src_kernel", s);
-    gat_da_src_kernel<DT, G, HL><<<src_blocks, kTaskBlock, 0, s>>>(hs, sdz_src, dap_src,
-                                                                    io.n_src, io.ld);
-    TGX_LAUNCHED("gat_da_src_kernel");
+
+  int64_t src_blocks = 0, dst_blocks = 0;
+  if (folded) {
+    // da from node passes: both sums in one read of h for one feature
+    // tensor, hs and hd each read once for two.
+    if (homogeneous) {
+      const auto k = gat_da_nodes_kernel<DT, G, HL, true>;
+      src_blocks = dst_blocks = node_blocks(k, io.n_src, EPW);
+      TGX_PROFILE("gat_da_nodes_kernel", s);
+      k<<<src_blocks, kTaskBlock, 0, s>>>(hs, sdz_src, dap_src, sdz_dst, dap_dst, io.n_src,
+                                          io.ld);
+      TGX_LAUNCHED("gat_da_nodes_kernel");
+    } else {
+      const auto k = gat_da_nodes_kernel<DT, G, HL, false>;
+      src_blocks = node_blocks(k, io.n_src, EPW);
+      dst_blocks = node_blocks(k, io.n_dst, EPW);
+      TGX_PROFILE("gat_da_nodes_kernel", s);
+      k<<<src_blocks, kTaskBlock, 0, s>>>(hs, sdz_src, dap_src, nullptr, nullptr, io.n_src,
+                                          io.ld);
+      TGX_LAUNCHED("gat_da_nodes_kernel");
+      TGX_PROFILE("gat_da_nodes_kernel", s);
+      k<<<dst_blocks, kTaskBlock, 0, s>>>(hd, sdz_dst, dap_dst, nullptr, nullptr, io.n_dst,
+                                          io.ld);
+      TGX_LAUNCHED("gat_da_nodes_kernel");
+    }
+  } else {
+    const GatDstArgs<DT, I> da{row_ptr, pv, hd, io.a_dst, dz, inv_perm, sdz_src, dh_acc,
+                               static_cast<T*>(io.dhd), dst_part, dap_src, dap_dst,
+                               plan_waves(pv), io.ld};
+    const auto dst_kernel = homogeneous ? gat_bwd_dst_kernel<DT, I, G, HL, true>
+                                        : gat_bwd_dst_kernel<DT, I, G, HL, false>;
+    dst_blocks = persist_blocks(plan_waves(pv), resident_blocks(dst_kernel, kTaskBlock));
+    {
+      TGX_PROFILE("gat_bwd_dst_kernel", s);
+      dst_kernel<<<dst_blocks, kTaskBlock, 0, s>>>(da);
+      TGX_LAUNCHED("gat_bwd_dst_kernel");
+    }
+    if (pv.n_split > 0) {
+      TGX_PROFILE("gat_bwd_dst_merge_kernel", s);
+      const auto merge = homogeneous ? gat_bwd_dst_merge_kernel<DT, G, HL, true>
+                                     : gat_bwd_dst_merge_kernel<DT, G, HL, false>;
+      merge<<<ceil_div(pv.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+          pv, dst_part, io.a_dst, dh_acc, static_cast<T*>(io.dhd), io.ld);
+      TGX_LAUNCHED("gat_bwd_dst_merge_kernel");
+    }
+    src_blocks = dst_blocks;
+    if (!homogeneous) {
+      const auto k = gat_da_nodes_kernel<DT, G, HL, false>;
+      src_blocks = node_blocks(k, io.n_src, EPW);
+      TGX_PROFILE("gat_da_nodes_kernel", s);
+      k<<<src_blocks, kTaskBlock, 0, s>>>(hs, sdz_src, dap_src, nullptr, nullptr, io.n_src,
+                                          io.ld);
+      TGX_LAUNCHED("gat_da_nodes_kernel");
+    }
   }
   {
     TGX_PROFILE("da_reduce_kernel", s);
@@ -773,7 +937,7 @@ template <int DT>
 int gat_fwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_row_plan* plan,
                   const void* hs, const void* hd, const float* a_src, const float* a_dst,
                   float slope, void* out, float* ns, int H, int D, float* partial,
-                  hipStream_t s) {
+                  float* pos, hipStream_t s) {
   using T = typename Vals<DT, 4>::T;
   const int64_t ld = static_cast<int64_t>(H) * D, nsld = 4 * static_cast<int64_t>(H);
   for (int h0 = 0; h0 < H;) {
@@ -783,6 +947,7 @@ int gat_fwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_
     const T* hs_g = hs ? static_cast<const T*>(hs) + off : nullptr;
     const T* hd_g = static_cast<const T*>(hd) + off;
     T* out_g = static_cast<T*>(out) + off;
+    float* pos_g = pos ? pos + off : nullptr;
     int st = TGX_UNSUPPORTED;
 #define TGX_GAT_FWD(GG, HH)                                                                  \
     if (shp.G == GG && shp.HL == HH) {                                                       \
@@ -791,14 +956,14 @@ int gat_fwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_
             GatFwdArgs<DT, int32_t>{static_cast<const int32_t*>(row_ptr),                    \
                                     static_cast<const int32_t*>(col), plan_view(*plan),      \
                                     hs_g, hd_g, a_src + off, a_dst + off, slope, out_g,      \
-                                    ns + 4 * h0, partial, ld, nsld},                         \
+                                    ns + 4 * h0, partial, pos_g, ld, nsld},                  \
             s);                                                                              \
       else                                                                                   \
         st = gat_fwd_launch<DT, int64_t, GG, HH>(                                            \
             GatFwdArgs<DT, int64_t>{static_cast<const int64_t*>(row_ptr),                    \
                                     static_cast<const int64_t*>(col), plan_view(*plan),      \
                                     hs_g, hd_g, a_src + off, a_dst + off, slope, out_g,      \
-                                    ns + 4 * h0, partial, ld, nsld},                         \
+                                    ns + 4 * h0, partial, pos_g, ld, nsld},                  \
             s);                                                                              \
     } else
     TGX_GAT_SHAPES(TGX_GAT_FWD)
@@ -825,7 +990,8 @@ int gat_bwd_dtype(const void* row_ptr, int idx_bits, const tgx_row_plan* plan,
   for (int h0 = 0; h0 < H;) {
     const int hg = gat_group_heads(H, D, h0);
     const GatShape shp = gat_shape(hg, D);
-    const GatBwdLayout L = gat_bwd_layout(*plan, *plan_t, n_edges, hg, D, DT, H);
+    const GatBwdLayout L =
+        gat_bwd_layout(*plan, *plan_t, n_edges, hg, D, DT, H, all.pos != nullptr);
     const int64_t off = static_cast<int64_t>(h0) * D;
     GatBwdIo io = all;
     io.col_off = off;
@@ -840,6 +1006,7 @@ int gat_bwd_dtype(const void* row_ptr, int idx_bits, const tgx_row_plan* plan,
     io.da_src = all.da_src + off;
     io.da_dst = all.da_dst + off;
     io.ns = all.ns + 4 * h0;
+    io.pos = all.pos ? all.pos + off : nullptr;
     int st = TGX_UNSUPPORTED;
 #define TGX_GAT_BWD(GG, HH)                                                                 \
     if (shp.G == GG && shp.HL == HH) {                                                      \
@@ -870,7 +1037,7 @@ extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
                            const tgx_row_plan* plan, const void* h_src, const void* h_dst,
                            const float* a_src, const float* a_dst, float slope, void* out,
                            float* ns, int64_t n_dst, int64_t n_src, int H, int D, int dtype,
-                           float* partial, void* stream) {
+                           float* partial, float* pos, void* stream) {
   TGX_REQUIRE(idx_bits == 32 || idx_bits == 64, "idx_bits must be 32 or 64");
   TGX_REQUIRE(dtype_bytes(dtype) != 0, "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)",
               dtype);
@@ -887,23 +1054,25 @@ extern "C" int tgx_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
   TGX_REQUIRE(row_ptr && h_dst && a_src && a_dst && out && ns && (h_src || n_src == 0),
               "null pointer");
   TGX_REQUIRE(plan->n_chunks == 0 || partial, "split rows need a partial buffer");
+  TGX_REQUIRE(reinterpret_cast<uintptr_t>(pos) % 16 == 0, "pos must be 16-byte aligned");
   TGX_REQUIRE(n_src < (int64_t{1} << 31), "source tables need fewer than 2^31 rows");
   hipStream_t s = as_stream(stream);
   switch (dtype) {
     case TGX_DTYPE_F32:
       return gat_fwd_dtype<TGX_DTYPE_F32>(row_ptr, col, idx_bits, plan, h_src, h_dst, a_src,
-                                          a_dst, slope, out, ns, H, D, partial, s);
+                                          a_dst, slope, out, ns, H, D, partial, pos, s);
     case TGX_DTYPE_BF16:
       return gat_fwd_dtype<TGX_DTYPE_BF16>(row_ptr, col, idx_bits, plan, h_src, h_dst, a_src,
-                                           a_dst, slope, out, ns, H, D, partial, s);
+                                           a_dst, slope, out, ns, H, D, partial, pos, s);
     default:
       return gat_fwd_dtype<TGX_DTYPE_F16>(row_ptr, col, idx_bits, plan, h_src, h_dst, a_src,
-                                          a_dst, slope, out, ns, H, D, partial, s);
+                                          a_dst, slope, out, ns, H, D, partial, pos, s);
   }
 }
 
 extern "C" int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
-                                     int64_t n_edges, int H, int D, int dtype, size_t* bytes) {
+                                     int64_t n_edges, int H, int D, int dtype, int folded,
+                                     size_t* bytes) {
   TGX_REQUIRE(plan && plan_t && bytes, "null pointer");
   TGX_REQUIRE(dtype_bytes(dtype) != 0, "dtype must be TGX_DTYPE_BF16, _F16 or _F32 (got %d)",
               dtype);
@@ -913,8 +1082,9 @@ extern "C" int tgx_gat_bwd_workspace(const tgx_row_plan* plan, const tgx_row_pla
   }
   // Head groups run one after another on one stream and share the
   // workspace; the first group is the widest.
-  *bytes =
-      gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype, H).bytes;
+  *bytes = gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype, H,
+                          folded != 0)
+               .bytes;
   return TGX_OK;
 }
 
@@ -923,7 +1093,8 @@ extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
                            const int32_t* col_t, const int32_t* perm, const int32_t* inv_perm,
                            const tgx_row_plan* plan_t, const void* h_src, const void* h_dst,
                            const float* a_src, const float* a_dst, float slope, const void* out,
-                           float* ns, const void* dout, void* dh_src, void* dh_dst,
+                           float* ns, const float* pos, const void* dout, void* dh_src,
+                           void* dh_dst,
                            float* da_src, float* da_dst, int64_t n_dst, int64_t n_src,
                            int64_t n_edges, int H, int D, int dtype, void* ws, size_t ws_bytes,
                            void* stream) {
@@ -948,15 +1119,18 @@ extern "C" int tgx_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
   TGX_REQUIRE(row_ptr && h_src && h_dst && a_src && a_dst && out && ns && dout && dh_src &&
                   dh_dst && da_src && da_dst,
               "null pointer");
-  TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && inv_perm), "null transposed CSR");
+  TGX_REQUIRE(n_edges == 0 || (row_ptr_t && col_t && (pos || inv_perm)),
+              "null transposed CSR");
+  TGX_REQUIRE(reinterpret_cast<uintptr_t>(pos) % 16 == 0, "pos must be 16-byte aligned");
   TGX_REQUIRE(n_src < (int64_t{1} << 31) && n_dst < (int64_t{1} << 31),
               "node tables need fewer than 2^31 rows");
-  const size_t need =
-      gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D, dtype, H).bytes;
+  const size_t need = gat_bwd_layout(*plan, *plan_t, n_edges, gat_group_heads(H, D, 0), D,
+                                     dtype, H, pos != nullptr)
+                          .bytes;
   TGX_REQUIRE(ws && ws_bytes >= need, "workspace too small: need %zu bytes", need);
   hipStream_t s = as_stream(stream);
   const GatBwdIo io{h_src, h_dst, out, dout, a_src, a_dst, dh_src, dh_dst, ns, da_src, da_dst,
-                    n_dst, n_src, static_cast<int64_t>(H) * D, 4 * static_cast<int64_t>(H),
+                    pos, n_dst, n_src, static_cast<int64_t>(H) * D, 4 * static_cast<int64_t>(H),
                     slope, 0};
   char* w = static_cast<char*>(ws);
   switch (dtype) {

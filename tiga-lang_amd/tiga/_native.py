@@ -54,7 +54,7 @@ class EdgeMlp(ctypes.Structure):
 
 
 # tgx_abi_version() of the library these signatures and structs mirror.
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 
 # name -> argtypes (all return int status except where noted)
@@ -86,11 +86,12 @@ _SIGNATURES: dict[str, list] = {
     "tgx_csr_edge_dot": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                          c_int, c_vp],
     "tgx_gat_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_f32, c_vp,
-                    c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_vp],
-    "tgx_gat_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, c_int, P(c_size)],
+                    c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_vp, c_vp],
+    "tgx_gat_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, c_int, c_int,
+                              P(c_size)],
     "tgx_gat_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, P(RowPlan), c_vp,
-                    c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
-                    c_i64, c_i64, c_int, c_int, c_int, c_vp, c_size, c_vp],
+                    c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                    c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_size, c_vp],
     "tgx_dot_attn_fwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, c_f32, c_vp,
                          c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_vp],
     "tgx_dot_attn_fwd_noalloc": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp,

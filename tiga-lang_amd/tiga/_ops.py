@@ -184,23 +184,30 @@ class GatFunction(torch.autograd.Function):
         adc = _aligned(a_dst.reshape(H, D))
         out = torch.empty((n_dst, H, D), dtype=hs.dtype, device=hs.device)
         ns = torch.empty((n_dst, H, 4), dtype=torch.float32, device=hs.device)
+        # A forward that a backward may follow also writes pos, each row's
+        # sum over its z > 0 edges of alpha (h[j] - out[i]): the backward
+        # then forms the destination terms from node rows instead of a
+        # per-edge pass.
+        pos = (torch.empty((n_dst, H, D), dtype=torch.float32, device=hs.device)
+               if any(ctx.needs_input_grad[:4]) else None)
         plan = graph._row_plan()
-        partial = _partial(plan, H * D + 2 * H, hs.device)
+        partial = _partial(plan, 2 * H * D + 3 * H if pos is not None else H * D + 2 * H,
+                           hs.device)
         _native.call("tgx_gat_fwd", row_ptr.data_ptr(), col_idx.data_ptr(),
                      _native.idx_bits(row_ptr), plan.ref, hs.data_ptr(), hd.data_ptr(),
                      asc.data_ptr(), adc.data_ptr(), float(slope), out.data_ptr(),
                      ns.data_ptr(), n_dst, n_src, H, D, _VALUE_DTYPES[hs.dtype], _p(partial),
-                     _native.stream_of(hs))
+                     _p(pos), _native.stream_of(hs))
         ctx.graph = graph
         ctx.slope = float(slope)
         ctx.a_shapes = (a_src.shape, a_dst.shape)
         ctx.bipartite = h_dst is not None
-        ctx.save_for_backward(hs, hd, asc, adc, out, ns)
+        ctx.save_for_backward(hs, hd, asc, adc, out, pos, ns)
         return out
 
     @staticmethod
     def backward(ctx, dout: torch.Tensor):
-        hs, hd, asc, adc, out, ns = ctx.saved_tensors
+        hs, hd, asc, adc, out, pos, ns = ctx.saved_tensors
         graph: Graph = ctx.graph
         row_ptr, col_idx = graph._kernel_csr()
         n_dst, n_src = graph.schema.num_dst, graph.schema.num_src
@@ -216,7 +223,7 @@ class GatFunction(torch.autograd.Function):
         code = _VALUE_DTYPES[hs.dtype]
         ws_bytes = ctypes.c_size_t()
         _native.call("tgx_gat_bwd_workspace", plan.ref, t.plan.ref, E, H, D, code,
-                     ctypes.byref(ws_bytes))
+                     int(pos is not None), ctypes.byref(ws_bytes))
         ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=hs.device)
         # Slot 1 of the saved node state is backward scratch (delta); it is
         # rewritten by every backward before it is read.
@@ -224,7 +231,7 @@ class GatFunction(torch.autograd.Function):
                      _native.idx_bits(row_ptr), plan.ref, t.row_ptr_t.data_ptr(),
                      t.col_t.data_ptr(), t.perm.data_ptr(), t.inv_perm.data_ptr(),
                      t.plan.ref, hs.data_ptr(), hd.data_ptr(), asc.data_ptr(), adc.data_ptr(),
-                     ctx.slope, out.data_ptr(), ns.data_ptr(), dout.data_ptr(),
+                     ctx.slope, out.data_ptr(), ns.data_ptr(), _p(pos), dout.data_ptr(),
                      dh_src.data_ptr(), dh_dst.data_ptr(), da_src.data_ptr(),
                      da_dst.data_ptr(), n_dst, n_src, E, H, D, code, ws.data_ptr(),
                      ws_bytes.value, _native.stream_of(hs))
