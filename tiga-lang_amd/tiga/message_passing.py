@@ -657,8 +657,9 @@ class MessagePassing(Kernel):
         roles = "one feature table" if hd is h else "source and destination tables"
         describe = lambda: self._variant(
             graph, "gat-additive", ("tgx_gat_fwd", "tgx_gat_bwd"),
-            f"{kind} {roles}, online softmax per (row, head), logsumexp saved; backward "
-            "recomputes alpha over the transposed CSR")
+            f"{kind} {roles}, online softmax per (row, head), logsumexp and the positive-"
+            "branch rows saved; backward recomputes alpha over the transposed CSR and "
+            "forms the destination terms per node")
         operands = (("src", gat.h_field), ("dst", gat.dst_field),
                     self._binding(gat.a_src, params), self._binding(gat.a_dst, params))
         return _Launch(graph, operands, run, describe)
