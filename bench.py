@@ -179,12 +179,15 @@ def gat_kernel_bytes(N, E, H, D):
 
 
 def dot_kernel_bytes(N, E, H, D):
+    """The stored-ds backward the Torch front end runs: the source pass also
+    writes each edge's ds (transposed order); the destination pass reads it
+    through inv_perm, gathers the k row and writes dbias (C4 has a bias)."""
     row = H * D * 2
     return {
         "dot_fwd_kernel": E * (4 + 2 * row + H * 4) + N * (4 + 2 * row + H * 8),
         "dot_delta_kernel": N * (2 * row + H * 4),
-        "dot_bwd_dst_kernel": E * (4 + 2 * row + 2 * H * 4) + N * (4 + 3 * row + H * 8),
-        "dot_bwd_src_kernel": E * (4 + 4 + 2 * row + H * 4 + H * 8) + N * (4 + 4 * row),
+        "dot_bwd_dst_kernel": E * (4 + 4 + row + 2 * H * 4) + N * (4 + row),
+        "dot_bwd_src_kernel": E * (4 + 4 + 2 * row + H * 4 + H * 8 + H * 4) + N * (4 + 4 * row),
     }
 
 

@@ -356,18 +356,25 @@ int tgx_dot_attn_fwd_noalloc(const void* row_ptr_dev, const void* col_dev, int i
                              void* out_dev, float* ml_dev, int64_t n_dst, int64_t n_src,
                              int H, int D, int dtype, void* stream);
 
-/* Workspace bytes for tgx_dot_attn_bwd with these plans. */
+/* Workspace bytes for tgx_dot_attn_bwd with these plans; stored_ds != 0 for
+ * a backward given inv_perm (it keeps each edge's score gradient, 4*H bytes
+ * per edge of the n_edges). */
 int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
-                               int H, int D, size_t* bytes);
+                               int64_t n_edges, int H, int D, int stored_ds, size_t* bytes);
 
 /* Fused backward from the saved logsumexp, no float atomics: dq (dtype) and
  * dbias (fp32 [E, H], may be NULL) on the destination-row CSR, dk/dv (dtype)
  * on the transposed CSR (row_ptr_t, col_t, perm) and its plan.  ml slot 1
- * (delta = <dout, out>) is overwritten. */
+ * (delta = <dout, out>) is overwritten.  With inv_perm_dev (the transposed
+ * CSR's inverse permutation) the source pass runs first and keeps each
+ * edge's ds, and the destination pass reads it through inv_perm instead of
+ * recomputing it from gathered k and v rows; NULL recomputes.  n_edges is
+ * the CSR's edge count. */
 int tgx_dot_attn_bwd(const void* row_ptr_dev, const void* col_dev, int idx_bits,
                      const tgx_row_plan* plan, const int32_t* row_ptr_t_dev,
                      const int32_t* col_t_dev, const int32_t* perm_dev,
-                     const tgx_row_plan* plan_t, const void* q_dev, const void* k_dev,
+                     const int32_t* inv_perm_dev, const tgx_row_plan* plan_t,
+                     int64_t n_edges, const void* q_dev, const void* k_dev,
                      const void* v_dev, const float* bias_dev, float scale,
                      const void* out_dev, float* ml_dev, const void* dout_dev, void* dq_dev,
                      void* dk_dev, void* dv_dev, float* dbias_dev, int64_t n_dst,

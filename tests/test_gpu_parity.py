@@ -529,6 +529,78 @@ def test_dot_fwd_bwd_parity_rmat(H, D, idx, with_bias):
     assert torch.count_nonzero(out[torch.as_tensor(empty, device=DEV)]).item() == 0
 
 
+def _dot_bwd_c_abi(graph, q, k, v, bias, scale, dout, stored):
+    """Dot attention forward (through the front end's autograd function) and
+    backward through the C ABI: stored ds (inv_perm passed: the source pass
+    keeps each edge's ds for the destination pass) or recomputed."""
+    from tiga._ops import _VALUE_DTYPES
+    row_ptr, col = graph._kernel_csr()
+    n_dst, n_src, E = graph.schema.num_dst, graph.schema.num_src, graph.num_edges
+    _, H, D = q.shape
+    ptr = lambda t: None if t is None else t.data_ptr()
+    out = torch.empty_like(q)
+    ml = torch.empty((n_dst, H, 2), dtype=torch.float32, device=DEV)
+    plan, t = graph._row_plan(), graph._transposed()
+    from tiga._ops import _partial
+    partial = _partial(plan, H * D + 2 * H, DEV)
+    code, stream, bits = _VALUE_DTYPES[q.dtype], _native.stream_of(q), _native.idx_bits(row_ptr)
+    _native.call("tgx_dot_attn_fwd", row_ptr.data_ptr(), col.data_ptr(), bits, plan.ref,
+                 q.data_ptr(), k.data_ptr(), v.data_ptr(), ptr(bias), scale, out.data_ptr(),
+                 ml.data_ptr(), n_dst, n_src, H, D, code, ptr(partial), stream)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dbias = None if bias is None else torch.empty((E, H), dtype=torch.float32, device=DEV)
+    ws_bytes = ctypes.c_size_t()
+    _native.call("tgx_dot_attn_bwd_workspace", plan.ref, t.plan.ref, E, H, D, int(stored),
+                 ctypes.byref(ws_bytes))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=DEV)
+    _native.call("tgx_dot_attn_bwd", row_ptr.data_ptr(), col.data_ptr(), bits, plan.ref,
+                 t.row_ptr_t.data_ptr(), t.col_t.data_ptr(), t.perm.data_ptr(),
+                 t.inv_perm.data_ptr() if stored else None, t.plan.ref, E, q.data_ptr(),
+                 k.data_ptr(), v.data_ptr(), ptr(bias), scale, out.data_ptr(), ml.data_ptr(),
+                 dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ptr(dbias),
+                 n_dst, n_src, H, D, code, ws.data_ptr(), ws_bytes.value, stream)
+    torch.cuda.synchronize()
+    return dq, dk, dv, dbias
+
+
+# The dot-product backward with stored ds (the front end's path) and with ds
+# recomputed in the destination pass, against float64 and each other: R-MAT
+# hub rows split on both sides, empty rows, two head groups (16 x 64), one
+# lane per head (1 x 8), with and without a bias, bf16 and fp32.
+@pytest.mark.parametrize("H,D", [(4, 64), (16, 64), (1, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_dot_stored_and_recomputed_ds_backwards_agree(H, D, dtype, with_bias):
+    from graphs import rmat_csr
+
+    print(f"dot stored ds H={H} D={D} {dtype} bias={with_bias}", flush=True)
+    rp, col = rmat_csr(6, 12)
+    N, E = rp.size - 1, col.size
+    rng = np.random.default_rng(H * D + 3)
+    mk = lambda: to_dev(rng.standard_normal((N, H, D)), dtype)
+    q, k, v, dout = mk(), mk(), mk(), mk()
+    bias = to_dev(rng.standard_normal((E, H)), torch.float32) if with_bias else None
+    scale = 1.0 / np.sqrt(D)
+    graph = tg.Graph.from_csr(to_dev(rp, torch.int64), to_dev(col, torch.int64), num_src=N)
+    stored = _dot_bwd_c_abi(graph, q, k, v, bias, scale, dout, True)
+    recomputed = _dot_bwd_c_abi(graph, q, k, v, bias, scale, dout, False)
+    f = lambda t: t.detach().double().cpu().numpy()
+    e = ref.dot_bwd(rp, col, f(q), f(k), f(v), scale, None if bias is None else f(bias),
+                    f(dout))
+    tol = RTOL32 if dtype == torch.float32 else RTOL_BF16
+    for name, a, b, x in zip(("dq", "dk", "dv", "dbias"), stored, recomputed, e):
+        if a is None:
+            continue
+        err_s, err_r, err_sr = rel_err(f(a), x), rel_err(f(b), x), rel_err(f(a), f(b))
+        print(f"  {name}: stored {err_s:.2e}, recomputed {err_r:.2e}, between {err_sr:.2e}",
+              flush=True)
+        assert err_s <= tol and err_r <= tol, name
+        # One ds formula in both paths (the source pass's dot-product order
+        # differs from the destination pass's): fp32 agrees to rounding.
+        if dtype == torch.float32:
+            assert err_sr <= 1e-6, name
+
+
 # fp32 q/k/v (fp32 arithmetic throughout: 1e-5 against float64) and fp16
 # (2e-2); the bias may be any float type (read as fp32).
 @pytest.mark.parametrize("H,D", [(4, 64), (3, 64), (6, 128), (1, 512), (1, 8), (16, 16)])

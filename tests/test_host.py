@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_native.exported_symbols())
-    assert lib.tgx_abi_version() == 12
+    assert lib.tgx_abi_version() == 13
     assert lib.tgx_status_string(1) == b"invalid argument"
 
 

@@ -35,7 +35,7 @@ extern "C" const char* tgx_status_string(int status) {
 
 extern "C" const char* tgx_last_error(void) { return tgx::g_last_error; }
 
-extern "C" int tgx_abi_version(void) { return 12; }
+extern "C" int tgx_abi_version(void) { return 13; }
 
 // ---------------------------------------------------------------------------
 // Reference planner restatement.

@@ -22,6 +22,11 @@
 //                    dv[j] = sum alpha_e dout[i]
 //   Hub rows of either CSR are split into chunks whose fp32 partials are
 //   summed in chunk order.
+// Stored ds (the caller passes inv_perm): B3 runs first and also writes each
+// edge's ds at its transposed position (coalesced, [E, H] fp32); B2 then
+// reads ds through inv_perm instead of recomputing it, so it gathers only
+// the k row per edge (the recomputation needs k and v rows, q, dout and
+// the node state): one scattered 4H-byte read replaces a 2·D·H-byte row.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -253,9 +258,14 @@ struct DotDstArgs {
   int64_t ld;       // values between consecutive nodes' rows of q, k, v, dout, dq
   int64_t mld;      // floats between consecutive nodes' rows of ml
   int64_t bld;      // floats between consecutive edges' rows of bias and dbias
+  const int32_t* inv_perm;  // STORED: [E] transposed position of each edge
+  const float* ds_t;        // STORED: [E, H] ds in transposed order (from B3)
 };
 
-template <int DT, typename I, int G, int HL, int U>
+// STORED: ds read through inv_perm (B3 ran first); otherwise recomputed.
+// (The dbias stores stay in the loop: staging them in LDS like the source
+// pass's ds measured slower here, 3.38 -> 3.60 ms on C4.)
+template <int DT, typename I, int G, int HL, int U, bool STORED>
 __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<DT, I> a) {
   using V = Vals<DT, 8>;
   constexpr int EPW = kWave / G;
@@ -275,12 +285,45 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<DT, 
     return;
   }
   const int64_t row = t.row;
+  float dq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if constexpr (STORED) {
+    constexpr int H = G / HL;
+    for (int64_t base = t.e0; base < t.e1; base += kWave) {
+      const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
+      int my_col = 0, my_p = 0;
+      if (lane < n) {
+        my_col = static_cast<int>(a.col[base + lane]);
+        my_p = a.inv_perm[base + lane];
+      }
+      for (int k = 0; k < n; k += EPW * U) {
+        typename V::Raw kk[U];
+        float dsv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int slot = k + u * EPW + g;
+          const int src = slot < n ? slot : 0;
+          const int j = fetch_lane<EPW>(my_col, src);
+          const int64_t p = fetch_lane<EPW>(my_p, src);
+          kk[u] = V::load(a.k + static_cast<int64_t>(j) * a.ld + 8 * c);
+          dsv[u] = slot < n ? a.ds_t[p * H + hd] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int slot = k + u * EPW + g;
+          if (a.dbias && slot < n && head_lead) a.dbias[(base + slot) * a.bld + hd] = dsv[u];
+          float kf[8];
+          V::unpack(kk[u], kf);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) dq[q] += dsv[u] * kf[q];
+        }
+      }
+    }
+  } else {
   float qf[8], df[8];
   V::unpack(V::load(a.q + row * a.ld + 8 * c), qf);
   V::unpack(V::load(a.dout + row * a.ld + 8 * c), df);
   const float lse = a.ml[row * a.mld + hd * 2];
   const float delta = a.ml[row * a.mld + hd * 2 + 1];
-  float dq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
     const int n = static_cast<int>(t.e1 - base < kWave ? t.e1 - base : kWave);
     const int my_col = lane < n ? static_cast<int>(a.col[base + lane]) : 0;
@@ -310,6 +353,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<DT, 
         for (int q = 0; q < 8; ++q) dq[q] += ds * kf[q];
       }
     }
+  }
   }
   fold_groups<G>(dq);
   if (g != 0) return;
@@ -366,13 +410,22 @@ struct DotSrcArgs {
   int64_t ld;       // values between consecutive nodes' rows of q, k, v, dout, dk, dv
   int64_t mld;      // floats between consecutive nodes' rows of ml
   int64_t bld;      // floats between consecutive edges' rows of bias
+  float* ds_t;      // STORE_DS: [E, H] out, ds at each edge's transposed position
 };
 
-template <int DT, int G, int HL, int U>
+// STORE_DS: a window's ds (up to 64 edges x H) waits in LDS and leaves in
+// one coalesced pass after the window (STAGE, H <= 16): a store per edge
+// pair inside the loop would make every following gather wait for it, since
+// loads and stores share one in-order completion counter.
+template <int DT, int G, int HL, int U, bool STORE_DS>
 __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs<DT> a) {
   using V = Vals<DT, 8>;
   constexpr int EPW = kWave / G;
   constexpr int HD = 8 * G;
+  constexpr int H = G / HL;
+  constexpr bool STAGE = STORE_DS && H <= 16;
+  __shared__ float stage[STAGE ? kWavesPerBlock : 1][STAGE ? kWave * H : 1];
+  const int wave = threadIdx.x / kWave;
   const Task t = decode_task(a.plan, a.row_ptr_t, global_wave());
   if (t.kind == kTaskNone) return;
   const int lane = lane_id();
@@ -433,12 +486,28 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs<DT> 
         const float s = group_sum<HL>(sp) * a.scale + bb[u];
         const float alpha = valid ? fast_exp(s - lse[u]) : 0.f;
         const float ds = alpha * (group_sum<HL>(dp) - dl[u]);
+        if constexpr (STORE_DS) {
+          if (valid && c % HL == 0) {
+            if constexpr (STAGE)
+              stage[wave][slot * H + hd] = ds;
+            else
+              a.ds_t[(base + slot) * H + hd] = ds;
+          }
+        }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           dk[q] += ds * qf[q];
           dv[q] += alpha * df[q];
         }
       }
+    }
+    if constexpr (STAGE) {
+      // One wave's LDS accesses complete in issue order, so every lane
+      // reads the window's ds written above; the next window's writes come
+      // after these reads.
+      __builtin_amdgcn_wave_barrier();
+      for (int x = lane; x < n * H; x += kWave) a.ds_t[base * H + x] = stage[wave][x];
+      __builtin_amdgcn_wave_barrier();
     }
   }
   fold_groups<G>(dk);
@@ -541,15 +610,18 @@ int dot_fwd_launch(const DotFwdArgs<DT, I>& a, hipStream_t s) {
 }
 
 struct DotBwdLayout {
-  size_t dst_part_off, src_part_off, bytes;
+  size_t dst_part_off, src_part_off, ds_off, bytes;
 };
 
-DotBwdLayout dot_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t, int H, int D) {
+// stored: room for ds [E, H] of the widest head group.
+DotBwdLayout dot_bwd_layout(const tgx_row_plan& plan, const tgx_row_plan& plan_t, int H, int D,
+                            int64_t n_edges, bool stored) {
   DotBwdLayout L;
   const int64_t HD = static_cast<int64_t>(H) * D;
   Carve c{nullptr, 0};
   L.dst_part_off = reinterpret_cast<size_t>(c.take<float>(plan.n_chunks * HD));
   L.src_part_off = reinterpret_cast<size_t>(c.take<float>(plan_t.n_chunks * 2 * HD));
+  L.ds_off = reinterpret_cast<size_t>(c.take<float>(stored ? n_edges * H : 0));
   L.bytes = align_up(c.used) + 256;
   return L;
 }
@@ -560,30 +632,42 @@ int dot_bwd_launch(const DotDstArgs<DT, I>& da, const DotSrcArgs<DT>& sa,
                    hipStream_t s) {
   constexpr int U = dot_unroll<G>();
   constexpr int EPW = kWave / G;
+  const bool stored = da.ds_t != nullptr;
   {
     TGX_PROFILE("dot_delta_kernel", s);
     dot_delta_kernel<DT, G, HL><<<ceil_div(ceil_div(n_nodes, EPW), kWavesPerBlock), kTaskBlock, 0,
                                   s>>>(da.dout, out, ml, n_nodes, da.ld, da.mld);
     TGX_LAUNCHED("dot_delta_kernel");
   }
-  const int64_t dst_waves = plan_waves(da.plan);
-  if (dst_waves > 0) {
-    TGX_PROFILE("dot_bwd_dst_kernel", s);
-    dot_bwd_dst_kernel<DT, I, G, HL, U>
-        <<<ceil_div(dst_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(da);
-    TGX_LAUNCHED("dot_bwd_dst_kernel");
-  }
-  if (da.plan.n_split > 0) {
-    TGX_PROFILE("dot_dq_merge_kernel", s);
-    dot_dq_merge_kernel<DT, G><<<ceil_div(da.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
-        da.plan, da.partial, da.scale, da.dq, da.ld);
-    TGX_LAUNCHED("dot_dq_merge_kernel");
+  auto dst_pass = [&]() -> int {
+    const int64_t dst_waves = plan_waves(da.plan);
+    if (dst_waves > 0) {
+      TGX_PROFILE("dot_bwd_dst_kernel", s);
+      const auto k = stored ? dot_bwd_dst_kernel<DT, I, G, HL, U, true>
+                            : dot_bwd_dst_kernel<DT, I, G, HL, U, false>;
+      k<<<ceil_div(dst_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(da);
+      TGX_LAUNCHED("dot_bwd_dst_kernel");
+    }
+    if (da.plan.n_split > 0) {
+      TGX_PROFILE("dot_dq_merge_kernel", s);
+      dot_dq_merge_kernel<DT, G><<<ceil_div(da.plan.n_split, kWavesPerBlock), kTaskBlock, 0, s>>>(
+          da.plan, da.partial, da.scale, da.dq, da.ld);
+      TGX_LAUNCHED("dot_dq_merge_kernel");
+    }
+    return TGX_OK;
+  };
+  // Stored ds: the source pass (which writes ds) runs before the
+  // destination pass that reads it.
+  if (!stored) {
+    const int st = dst_pass();
+    if (st != TGX_OK) return st;
   }
   const int64_t src_waves = plan_waves(sa.plan);
   if (src_waves > 0) {
     TGX_PROFILE("dot_bwd_src_kernel", s);
-    dot_bwd_src_kernel<DT, G, HL, U>
-        <<<ceil_div(src_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
+    const auto k = stored ? dot_bwd_src_kernel<DT, G, HL, U, true>
+                          : dot_bwd_src_kernel<DT, G, HL, U, false>;
+    k<<<ceil_div(src_waves, kWavesPerBlock), kTaskBlock, 0, s>>>(sa);
     TGX_LAUNCHED("dot_bwd_src_kernel");
   }
   if (sa.plan.n_split > 0) {
@@ -592,6 +676,7 @@ int dot_bwd_launch(const DotDstArgs<DT, I>& da, const DotSrcArgs<DT>& sa,
         sa.plan, sa.partial, sa.scale, sa.dk, sa.dv, sa.ld);
     TGX_LAUNCHED("dot_kv_merge_kernel");
   }
+  if (stored) return dst_pass();
   return TGX_OK;
 }
 
@@ -644,7 +729,8 @@ int dot_bwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_
                   const tgx_row_plan* plan_t, const void* q, const void* k, const void* v,
                   const float* bias, float scale, const void* out, float* ml, const void* dout,
                   void* dq, void* dk, void* dv, float* dbias, int64_t n_dst, int H, int D,
-                  float* dst_part, float* src_part, hipStream_t s) {
+                  float* dst_part, float* src_part, const int32_t* inv_perm, float* ds_t,
+                  hipStream_t s) {
   using T = typename Vals<DT, 8>::T;
   const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
   auto at = [](const void* p, int64_t off) {
@@ -662,7 +748,7 @@ int dot_bwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_
     float* dbb = dbias ? dbias + h0 : nullptr;
     float* mm = ml + 2 * h0;
     const DotSrcArgs<DT> sa{row_ptr_t, col_t, perm, plan_view(*plan_t), qq, kk, vv, bb, scale,
-                            mm, gg, dkk, dvv, src_part, ld, mld, bld};
+                            mm, gg, dkk, dvv, src_part, ld, mld, bld, ds_t};
     int st = TGX_UNSUPPORTED;
 #define TGX_DOT_BWD(GG, HH)                                                                   \
     if (shp.G == GG && shp.HL == HH) {                                                        \
@@ -671,14 +757,14 @@ int dot_bwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_
             DotDstArgs<DT, int32_t>{static_cast<const int32_t*>(row_ptr),                     \
                                     static_cast<const int32_t*>(col), plan_view(*plan), qq,   \
                                     kk, vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld,   \
-                                    bld},                                                     \
+                                    bld, inv_perm, ds_t},                                     \
             sa, oo, mm, n_dst, s);                                                            \
       else                                                                                    \
         st = dot_bwd_launch<DT, int64_t, GG, HH>(                                             \
             DotDstArgs<DT, int64_t>{static_cast<const int64_t*>(row_ptr),                     \
                                     static_cast<const int64_t*>(col), plan_view(*plan), qq,   \
                                     kk, vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld,   \
-                                    bld},                                                     \
+                                    bld, inv_perm, ds_t},                                     \
             sa, oo, mm, n_dst, s);                                                            \
     } else
     TGX_DOT_SHAPES(TGX_DOT_BWD)
@@ -730,7 +816,8 @@ extern "C" int tgx_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bi
 }
 
 extern "C" int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_row_plan* plan_t,
-                                          int H, int D, size_t* bytes) {
+                                          int64_t n_edges, int H, int D, int stored_ds,
+                                          size_t* bytes) {
   TGX_REQUIRE(plan && plan_t && bytes, "null pointer");
   if (!dot_heads_ok(H, D)) {
     set_error("unsupported dot attention shape H=%d D=%d", H, D);
@@ -738,14 +825,17 @@ extern "C" int tgx_dot_attn_bwd_workspace(const tgx_row_plan* plan, const tgx_ro
   }
   // Head groups run one after another on one stream and share the
   // workspace; the first group is the widest.
-  *bytes = dot_bwd_layout(*plan, *plan_t, dot_group_heads(H, D, 0), D).bytes;
+  TGX_REQUIRE(n_edges >= 0, "bad edge count");
+  *bytes = dot_bwd_layout(*plan, *plan_t, dot_group_heads(H, D, 0), D, n_edges, stored_ds != 0)
+               .bytes;
   return TGX_OK;
 }
 
 extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bits,
                                 const tgx_row_plan* plan, const int32_t* row_ptr_t,
                                 const int32_t* col_t, const int32_t* perm,
-                                const tgx_row_plan* plan_t, const void* q, const void* k,
+                                const int32_t* inv_perm, const tgx_row_plan* plan_t,
+                                int64_t n_edges, const void* q, const void* k,
                                 const void* v, const float* bias, float scale, const void* out,
                                 float* ml, const void* dout, void* dq, void* dk, void* dv,
                                 float* dbias, int64_t n_dst, int64_t n_src, int H, int D,
@@ -764,25 +854,32 @@ extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bi
   TGX_REQUIRE(row_ptr && row_ptr_t && q && out && ml && dout && dq &&
                   ((k && v && dk && dv) || n_src == 0),
               "null pointer");
-  const DotBwdLayout L = dot_bwd_layout(*plan, *plan_t, dot_group_heads(H, D, 0), D);
+  TGX_REQUIRE(n_edges >= 0 && n_edges < (int64_t{1} << 31), "bad edge count");
+  const bool stored = inv_perm != nullptr && n_edges > 0;
+  const DotBwdLayout L =
+      dot_bwd_layout(*plan, *plan_t, dot_group_heads(H, D, 0), D, n_edges, stored);
   TGX_REQUIRE(ws && ws_bytes >= L.bytes, "workspace too small: need %zu bytes", L.bytes);
   hipStream_t s = as_stream(stream);
   char* w = static_cast<char*>(ws);
   float* dst_part = reinterpret_cast<float*>(w + L.dst_part_off);
   float* src_part = reinterpret_cast<float*>(w + L.src_part_off);
+  float* ds_t = stored ? reinterpret_cast<float*>(w + L.ds_off) : nullptr;
   switch (dtype) {
     case TGX_DTYPE_BF16:
       return dot_bwd_dtype<TGX_DTYPE_BF16>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
                                            plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
-                                           dv, dbias, n_dst, H, D, dst_part, src_part, s);
+                                           dv, dbias, n_dst, H, D, dst_part, src_part, inv_perm,
+                                           ds_t, s);
     case TGX_DTYPE_F16:
       return dot_bwd_dtype<TGX_DTYPE_F16>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
                                           plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
-                                          dv, dbias, n_dst, H, D, dst_part, src_part, s);
+                                          dv, dbias, n_dst, H, D, dst_part, src_part, inv_perm,
+                                          ds_t, s);
     default:
       return dot_bwd_dtype<TGX_DTYPE_F32>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
                                           plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
-                                          dv, dbias, n_dst, H, D, dst_part, src_part, s);
+                                          dv, dbias, n_dst, H, D, dst_part, src_part, inv_perm,
+                                          ds_t, s);
   }
 }
 

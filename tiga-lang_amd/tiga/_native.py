@@ -54,7 +54,7 @@ class EdgeMlp(ctypes.Structure):
 
 
 # tgx_abi_version() of the library these signatures and structs mirror.
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 
 # name -> argtypes (all return int status except where noted)
@@ -96,10 +96,11 @@ _SIGNATURES: dict[str, list] = {
                          c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_vp],
     "tgx_dot_attn_fwd_noalloc": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp,
                                  c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp],
-    "tgx_dot_attn_bwd_workspace": [P(RowPlan), P(RowPlan), c_int, c_int, P(c_size)],
-    "tgx_dot_attn_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, P(RowPlan), c_vp,
-                         c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
-                         c_i64, c_i64, c_int, c_int, c_int, c_vp, c_size, c_vp],
+    "tgx_dot_attn_bwd_workspace": [P(RowPlan), P(RowPlan), c_i64, c_int, c_int, c_int,
+                                   P(c_size)],
+    "tgx_dot_attn_bwd": [c_vp, c_vp, c_int, P(RowPlan), c_vp, c_vp, c_vp, c_vp, P(RowPlan),
+                         c_i64, c_vp, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp, c_vp, c_vp, c_vp,
+                         c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_size, c_vp],
     "tgx_attn_tasks": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp, P(c_i64)],
     "tgx_attn_fwd": [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_vp, c_vp, c_vp, P(c_i64),
                      c_f32, c_f32, c_vp, c_vp, c_i64, c_i64, c_int, c_int, c_vp],

@@ -288,13 +288,16 @@ class DotAttnFunction(torch.autograd.Function):
         plan = graph._row_plan()
         t = graph._transposed()
         ws_bytes = ctypes.c_size_t()
-        _native.call("tgx_dot_attn_bwd_workspace", plan.ref, t.plan.ref, H, D,
+        # Stored ds: the source pass keeps each edge's score gradient for the
+        # destination pass, which then gathers only k rows.
+        _native.call("tgx_dot_attn_bwd_workspace", plan.ref, t.plan.ref, E, H, D, 1,
                      ctypes.byref(ws_bytes))
         ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=qc.device)
         # Slot 1 of the saved ml is backward scratch (delta), rewritten each time.
         _native.call("tgx_dot_attn_bwd", row_ptr.data_ptr(), col_idx.data_ptr(),
                      _native.idx_bits(row_ptr), plan.ref, t.row_ptr_t.data_ptr(),
-                     t.col_t.data_ptr(), t.perm.data_ptr(), t.plan.ref, qc.data_ptr(),
+                     t.col_t.data_ptr(), t.perm.data_ptr(), t.inv_perm.data_ptr(), t.plan.ref,
+                     E, qc.data_ptr(),
                      kc.data_ptr(), vc.data_ptr(), _p(bc), ctx.scale, out.data_ptr(),
                      ml.data_ptr(), dout.data_ptr(), dq.data_ptr(), dk.data_ptr(),
                      dv.data_ptr(), _p(dbias), n_dst, n_src, H, D, _VALUE_DTYPES[qc.dtype],

@@ -845,7 +845,8 @@ class MessagePassing(Kernel):
         describe = lambda: self._variant(
             graph, "dot-product", ("tgx_dot_attn_fwd", "tgx_dot_attn_bwd"),
             f"{kind} gathers, fp32 online softmax per (row, head); hub rows split and merged; "
-            "backward over CSR (dq, dbias) and transposed CSR (dk, dv)")
+            "backward over the transposed CSR (dk, dv, each edge's ds kept) and the CSR "
+            "(dq, dbias from the kept ds)")
         return _Launch(graph, tuple(operands), run, describe)
 
     def _plan_block_attention(self, dot, graph, q, k, v) -> _Launch | None:
