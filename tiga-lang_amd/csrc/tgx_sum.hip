@@ -146,6 +146,13 @@ __device__ __forceinline__ void sum_task(const SumArgs<I, DT>& a, const Task& t)
   T self = V::zero();
   const bool want_dw = a.self_x != nullptr;
   if (want_dw && active) self = V::load(a.self_x + static_cast<int64_t>(t.row) * F + fo);
+  // A window's dw values wait in LDS and leave with one store per lane
+  // after the window, not one store per edge group inside the gather loop
+  // (whose following gathers would share its in-order completion count).
+  // Measured on C1: the backward unchanged (0.109 ms), the forward, which
+  // writes no dw, 0.061 -> 0.059 ms with this kernel shape.
+  __shared__ float dw_stage[kWavesPerBlock][kWave];
+  const int wv = threadIdx.x / kWave;
 
   T acc = V::zero();
   for (int64_t base = t.e0; base < t.e1; base += kWave) {
@@ -181,13 +188,17 @@ __device__ __forceinline__ void sum_task(const SumArgs<I, DT>& a, const Task& t)
       if (want_dw) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          float d = group_reduce_sum<G>(V::dot(v[u], self));
-          const int src = slot[u] < n ? slot[u] : 0;
-          const int wp = __shfl(my_wp, src, 64);
-          const int64_t widx = a.wperm ? static_cast<int64_t>(wp) : base + src;
-          if (c == 0 && slot[u] < n) a.dw[widx] = d;
+          const float d = group_reduce_sum<G>(V::dot(v[u], self));
+          if (c == 0 && slot[u] < n) dw_stage[wv][slot[u]] = d;
         }
       }
+    }
+    if (want_dw) {
+      // One wave's LDS accesses complete in issue order: lane e reads the
+      // value another lane wrote for edge base + e.
+      __builtin_amdgcn_wave_barrier();
+      if (lane < n) a.dw[a.wperm ? static_cast<int64_t>(my_wp) : base + lane] = dw_stage[wv][lane];
+      __builtin_amdgcn_wave_barrier();
     }
   }
   // Fold the EPW edge groups (lanes with equal c).
