@@ -566,8 +566,10 @@ def _dot_bwd_c_abi(graph, q, k, v, bias, scale, dout, stored):
 # The dot-product backward with stored ds (the front end's path) and with ds
 # recomputed in the destination pass, against float64 and each other: R-MAT
 # hub rows split on both sides, empty rows, two head groups (16 x 64), one
-# lane per head (1 x 8), with and without a bias, bf16 and fp32.
-@pytest.mark.parametrize("H,D", [(4, 64), (16, 64), (1, 8)])
+# lane per head (1 x 8), groups of more than 16 heads whose ds is stored
+# without LDS staging (32 x 16, 64 x 8), with and without a bias, bf16 and
+# fp32.
+@pytest.mark.parametrize("H,D", [(4, 64), (16, 64), (1, 8), (32, 16), (64, 8)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_dot_stored_and_recomputed_ds_backwards_agree(H, D, dtype, with_bias):
