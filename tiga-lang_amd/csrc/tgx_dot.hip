@@ -260,6 +260,7 @@ struct DotDstArgs {
   int64_t bld;      // floats between consecutive edges' rows of bias and dbias
   const int32_t* inv_perm;  // STORED: [E] transposed position of each edge
   const float* ds_t;        // STORED: [E, H] ds in transposed order (from B3)
+  int64_t n_edges;          // STORED: E, the rows of ds_t (reads past it give 0)
 };
 
 // STORED: ds read through inv_perm (B3 ran first); otherwise recomputed.
@@ -305,7 +306,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<DT, 
           const int j = fetch_lane<EPW>(my_col, src);
           const int64_t p = fetch_lane<EPW>(my_p, src);
           kk[u] = V::load(a.k + static_cast<int64_t>(j) * a.ld + 8 * c);
-          dsv[u] = slot < n ? a.ds_t[p * H + hd] : 0.f;
+          dsv[u] = slot < n && p < a.n_edges ? a.ds_t[p * H + hd] : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -411,6 +412,7 @@ struct DotSrcArgs {
   int64_t mld;      // floats between consecutive nodes' rows of ml
   int64_t bld;      // floats between consecutive edges' rows of bias
   float* ds_t;      // STORE_DS: [E, H] out, ds at each edge's transposed position
+  int64_t n_edges;  // STORE_DS: E, the rows of ds_t (no write past it)
 };
 
 // STORE_DS: a window's ds (up to 64 edges x H) waits in LDS and leaves in
@@ -490,7 +492,7 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs<DT> 
           if (valid && c % HL == 0) {
             if constexpr (STAGE)
               stage[wave][slot * H + hd] = ds;
-            else
+            else if (base + slot < a.n_edges)
               a.ds_t[(base + slot) * H + hd] = ds;
           }
         }
@@ -506,7 +508,8 @@ __global__ __launch_bounds__(kTaskBlock) void dot_bwd_src_kernel(DotSrcArgs<DT> 
       // reads the window's ds written above; the next window's writes come
       // after these reads.
       __builtin_amdgcn_wave_barrier();
-      for (int x = lane; x < n * H; x += kWave) a.ds_t[base * H + x] = stage[wave][x];
+      const int cnt = static_cast<int>(min(static_cast<int64_t>(n), a.n_edges - base)) * H;
+      for (int x = lane; x < cnt; x += kWave) a.ds_t[base * H + x] = stage[wave][x];
       __builtin_amdgcn_wave_barrier();
     }
   }
@@ -730,7 +733,7 @@ int dot_bwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_
                   const float* bias, float scale, const void* out, float* ml, const void* dout,
                   void* dq, void* dk, void* dv, float* dbias, int64_t n_dst, int H, int D,
                   float* dst_part, float* src_part, const int32_t* inv_perm, float* ds_t,
-                  hipStream_t s) {
+                  int64_t n_edges, hipStream_t s) {
   using T = typename Vals<DT, 8>::T;
   const int64_t ld = static_cast<int64_t>(H) * D, mld = 2 * static_cast<int64_t>(H), bld = H;
   auto at = [](const void* p, int64_t off) {
@@ -748,7 +751,7 @@ int dot_bwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_
     float* dbb = dbias ? dbias + h0 : nullptr;
     float* mm = ml + 2 * h0;
     const DotSrcArgs<DT> sa{row_ptr_t, col_t, perm, plan_view(*plan_t), qq, kk, vv, bb, scale,
-                            mm, gg, dkk, dvv, src_part, ld, mld, bld, ds_t};
+                            mm, gg, dkk, dvv, src_part, ld, mld, bld, ds_t, n_edges};
     int st = TGX_UNSUPPORTED;
 #define TGX_DOT_BWD(GG, HH)                                                                   \
     if (shp.G == GG && shp.HL == HH) {                                                        \
@@ -757,14 +760,14 @@ int dot_bwd_dtype(const void* row_ptr, const void* col, int idx_bits, const tgx_
             DotDstArgs<DT, int32_t>{static_cast<const int32_t*>(row_ptr),                     \
                                     static_cast<const int32_t*>(col), plan_view(*plan), qq,   \
                                     kk, vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld,   \
-                                    bld, inv_perm, ds_t},                                     \
+                                    bld, inv_perm, ds_t, n_edges},                            \
             sa, oo, mm, n_dst, s);                                                            \
       else                                                                                    \
         st = dot_bwd_launch<DT, int64_t, GG, HH>(                                             \
             DotDstArgs<DT, int64_t>{static_cast<const int64_t*>(row_ptr),                     \
                                     static_cast<const int64_t*>(col), plan_view(*plan), qq,   \
                                     kk, vv, bb, scale, mm, gg, dqq, dbb, dst_part, ld, mld,   \
-                                    bld, inv_perm, ds_t},                                     \
+                                    bld, inv_perm, ds_t, n_edges},                            \
             sa, oo, mm, n_dst, s);                                                            \
     } else
     TGX_DOT_SHAPES(TGX_DOT_BWD)
@@ -869,17 +872,17 @@ extern "C" int tgx_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bi
       return dot_bwd_dtype<TGX_DTYPE_BF16>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
                                            plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
                                            dv, dbias, n_dst, H, D, dst_part, src_part, inv_perm,
-                                           ds_t, s);
+                                           ds_t, n_edges, s);
     case TGX_DTYPE_F16:
       return dot_bwd_dtype<TGX_DTYPE_F16>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
                                           plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
                                           dv, dbias, n_dst, H, D, dst_part, src_part, inv_perm,
-                                          ds_t, s);
+                                          ds_t, n_edges, s);
     default:
       return dot_bwd_dtype<TGX_DTYPE_F32>(row_ptr, col, idx_bits, plan, row_ptr_t, col_t, perm,
                                           plan_t, q, k, v, bias, scale, out, ml, dout, dq, dk,
                                           dv, dbias, n_dst, H, D, dst_part, src_part, inv_perm,
-                                          ds_t, s);
+                                          ds_t, n_edges, s);
   }
 }
 
