@@ -309,6 +309,20 @@ def test_no_grad_launch_matches_autograd_launch():
     assert torch.equal(plain, tracked.detach())
     tracked.sum().backward()
     assert sg.grad is not None and torch.isfinite(sg.grad).all()
+    # GAT: a forward that a backward may follow also accumulates the
+    # positive-branch rows (another instantiation of the same online
+    # softmax); its output is the no-grad launch's to fp32 rounding.
+    h = torch.randn(3000, 4, 32, device=DEV)
+    a_s, a_d = 0.1 * torch.randn(4, 32, device=DEV), 0.1 * torch.randn(4, 32, device=DEV)
+    gk = GatParams()
+    plain = gk(graph=g, src={"h": h}, dst={"h": h}, a_src=a_s, a_dst=a_d)
+    assert gk.last_variant.backend == "hip" and plain.grad_fn is None
+    hg = h.clone().requires_grad_(True)
+    tracked = GatParams()(graph=g, src={"h": hg}, dst={"h": hg}, a_src=a_s, a_dst=a_d)
+    assert tracked.grad_fn is not None
+    diff = (plain - tracked.detach()).abs().max().item() / plain.abs().max().item()
+    print(f"  GAT no-grad vs autograd forward: max diff / max {diff:.2e}", flush=True)
+    assert diff <= 1e-6
     # prepare() binds the native arguments of a no-grad sum; a strided x
     # (which the launch would copy) stays on the per-call path; both see
     # in-place updates, and a gradient requested later gets autograd.
