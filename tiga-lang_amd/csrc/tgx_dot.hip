@@ -203,7 +203,23 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
   SoftState<8> st;
   st.init();
-  for (int q = c0; q < c1; ++q) {
+  // Eight chunks' partials are requested before they are merged (a hub row
+  // has up to hundreds of chunks; the merges depend on each other, the
+  // loads do not): the C3 merge 0.115 -> 0.034 ms.
+  int q = c0;
+  for (; q + 8 <= c1; q += 8) {
+    float acc[8][8], pm[8], pl[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float* p = partial + static_cast<int64_t>(q + u) * (HD + 2 * H);
+      load8(p + 8 * c, acc[u]);
+      pm[u] = p[HD + hd];
+      pl[u] = p[HD + H + hd];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) st.merge(pm[u], pl[u], acc[u]);
+  }
+  for (; q < c1; ++q) {
     const float* p = partial + static_cast<int64_t>(q) * (HD + 2 * H);
     float acc[8];
     load8(p + 8 * c, acc);
@@ -380,7 +396,18 @@ __global__ __launch_bounds__(kTaskBlock) void dot_dq_merge_kernel(
   const int64_t row = uniform(plan.rows[plan.n_empty + plan.n_wave + k]);
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
   float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int q = c0; q < c1; ++q) {
+  // Eight chunks' partials in flight per step; summed in chunk order.
+  int q = c0;
+  for (; q + 8 <= c1; q += 8) {
+    float p[8][8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) load8(partial + static_cast<int64_t>(q + u) * HD + 8 * c, p[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) s[r] += p[u][r];
+  }
+  for (; q < c1; ++q) {
     float p[8];
     load8(partial + static_cast<int64_t>(q) * HD + 8 * c, p);
 #pragma unroll
@@ -543,7 +570,25 @@ __global__ __launch_bounds__(kTaskBlock) void dot_kv_merge_kernel(
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
   float sk[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int q = c0; q < c1; ++q) {
+  // Four chunks' dk and dv partials in flight per step; summed in chunk
+  // order.
+  int q = c0;
+  for (; q + 4 <= c1; q += 4) {
+    float pk[4][8], pv[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      load8(partial + static_cast<int64_t>(q + u) * (2 * HD) + 8 * c, pk[u]);
+      load8(partial + static_cast<int64_t>(q + u) * (2 * HD) + HD + 8 * c, pv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        sk[r] += pk[u][r];
+        sv[r] += pv[u][r];
+      }
+  }
+  for (; q < c1; ++q) {
     float pk[8], pv[8];
     load8(partial + static_cast<int64_t>(q) * (2 * HD) + 8 * c, pk);
     load8(partial + static_cast<int64_t>(q) * (2 * HD) + HD + 8 * c, pv);
