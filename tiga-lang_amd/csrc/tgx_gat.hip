@@ -248,19 +248,30 @@ __global__ __launch_bounds__(kTaskBlock) void gat_fwd_merge_kernel(
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
   SoftState<NA> st;
   st.init();
-  for (int q = c0; q < c1; ++q) {
-    const float* p = partial + static_cast<int64_t>(q) * gat_partial_floats(HD, H, POS);
-    const f32x4 acc = ld4(p + 4 * c);
-    float accs[NA];
+  // The partials of up to eight chunks are requested before they are merged
+  // in chunk order (the merges depend on each other, the loads do not).
+  constexpr int B = 8;
+  for (int q0 = c0; q0 < c1; q0 += B) {
+    float accs[B][NA], pm[B], pl[B];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) accs[k] = acc[k];
-    if constexpr (POS) {
-      const f32x4 pacc = ld4(p + HD + 2 * H + 4 * c);
+    for (int u = 0; u < B; ++u) {
+      const int q = q0 + u < c1 ? q0 + u : c1 - 1;
+      const float* p = partial + static_cast<int64_t>(q) * gat_partial_floats(HD, H, POS);
+      const f32x4 acc = ld4(p + 4 * c);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) accs[4 + k] = pacc[k];
-      accs[8] = p[2 * HD + 2 * H + hd];
+      for (int k = 0; k < 4; ++k) accs[u][k] = acc[k];
+      if constexpr (POS) {
+        const f32x4 pacc = ld4(p + HD + 2 * H + 4 * c);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) accs[u][4 + k] = pacc[k];
+        accs[u][8] = p[2 * HD + 2 * H + hd];
+      }
+      pm[u] = p[HD + hd];
+      pl[u] = p[HD + H + hd];
     }
-    st.merge(p[HD + hd], p[HD + H + hd], accs);
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (q0 + u < c1) st.merge(pm[u], pl[u], accs[u]);
   }
   store_row<V, POS>(out, pos, row * ld + 4 * c, st);
   const f32x4 hi = V::widen(V::load(hd_rows + row * ld + 4 * c));
@@ -445,10 +456,24 @@ __global__ __launch_bounds__(kTaskBlock) void gat_bwd_src_merge_kernel(
   const int c0 = plan.chunk_off[k], c1 = plan.chunk_off[k + 1];
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   float z = 0.f;
-  for (int q = c0; q < c1; ++q) {
-    const float* p = partial + static_cast<int64_t>(q) * (HD + H);
-    s += ld4(p + 4 * c);
-    z += p[HD + hd];
+  // Up to eight chunks' partials in flight, summed in chunk order.
+  constexpr int B = 8;
+  for (int q0 = c0; q0 < c1; q0 += B) {
+    f32x4 ps[B];
+    float pz[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int q = q0 + u < c1 ? q0 + u : c1 - 1;
+      const float* p = partial + static_cast<int64_t>(q) * (HD + H);
+      ps[u] = ld4(p + 4 * c);
+      pz[u] = p[HD + hd];
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (q0 + u < c1) {
+        s += ps[u];
+        z += pz[u];
+      }
   }
   if constexpr (FOLD) s = s + sdz_dst[row * H + hd] * ld4(a_dst + 4 * c);
   if (dh_acc)
