@@ -205,7 +205,8 @@ __global__ __launch_bounds__(kTaskBlock) void dot_fwd_merge_kernel(
   st.init();
   // Eight chunks' partials are requested before they are merged (a hub row
   // has up to hundreds of chunks; the merges depend on each other, the
-  // loads do not): the C3 merge 0.115 -> 0.034 ms.
+  // loads do not): 0.115 -> 0.034 ms on the R-MAT scale-21 forward
+  // (bench.py --config c3).
   int q = c0;
   for (; q + 8 <= c1; q += 8) {
     float acc[8][8], pm[8], pl[8];
@@ -281,7 +282,8 @@ struct DotDstArgs {
 
 // STORED: ds read through inv_perm (B3 ran first); otherwise recomputed.
 // (The dbias stores stay in the loop: staging them in LDS like the source
-// pass's ds measured slower here, 3.38 -> 3.60 ms on C4.)
+// pass's ds measured slower here, 3.38 -> 3.60 ms on the R-MAT scale-21
+// backward, bench.py --config c4.)
 template <int DT, typename I, int G, int HL, int U, bool STORED>
 __global__ __launch_bounds__(kTaskBlock) void dot_bwd_dst_kernel(DotDstArgs<DT, I> a) {
   using V = Vals<DT, 8>;

@@ -149,7 +149,7 @@ __device__ __forceinline__ void sum_task(const SumArgs<I, DT>& a, const Task& t)
   // A window's dw values wait in LDS and leave with one store per lane
   // after the window, not one store per edge group inside the gather loop
   // (whose following gathers would share its in-order completion count).
-  // Measured on C1: the backward unchanged (0.109 ms), the forward, which
+  // Measured on bench.py --config c1: the backward unchanged (0.109 ms), the forward, which
   // writes no dw, 0.061 -> 0.059 ms with this kernel shape.
   __shared__ float dw_stage[kWavesPerBlock][kWave];
   const int wv = threadIdx.x / kWave;

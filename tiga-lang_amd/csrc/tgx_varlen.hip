@@ -146,7 +146,7 @@ constexpr float kRescaleLog2 = 8.f;
 // MFMA clusters run at wave priority 1 (s_setprio) and the softmax work
 // between them at 0: of the two waves sharing a SIMD, the one with MFMAs
 // ready issues them back to back while the other fills the VALU (dK/dV
-// 2.32 -> 2.26 ms on C5; forward and dQ unchanged).
+// 2.32 -> 2.26 ms on bench.py --config c5; forward and dQ unchanged).
 
 // Staging of one 64-row block of two [N, H, D] tensors by 256 threads:
 // thread t holds D / 32 chunks of 16 B of each.  Rows at or past `end` are
