@@ -39,6 +39,29 @@ def test_library_exports_every_declared_symbol():
     assert lib.tgx_status_string(1) == b"invalid argument"
 
 
+def declared_arities():
+    """Parameter count of every tgx_* function declared in include/*.h."""
+    arity = {}
+    for header in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        for m in re.finditer(r"\b(tgx_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+            params = m.group(2).strip()
+            arity[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return arity
+
+
+def test_binding_signatures_match_the_header():
+    """Every ctypes signature has as many arguments as its declaration (an
+    entry point whose parameters change without the binding would pass
+    arguments in the wrong places)."""
+    arity = declared_arities()
+    assert len(arity) >= 10
+    table = {**_native._SIGNATURES, **_native._OPTIONAL}
+    for name, argtypes in table.items():
+        assert name in arity, name
+        assert len(argtypes) == arity[name], (name, len(argtypes), arity[name])
+
+
 def _native_plan(case):
     lib = _native.lib()
     hist = case["histogram"]
