@@ -82,13 +82,15 @@ int tgx_cpu_csr_edge_dot(const void* row_ptr, const void* col, int idx_bits,
 
 /* Twin of tgx_gat_fwd (eager evaluation of the additive edge function,
  * interop/torch/message_passing.py:2848-2894, reducer_oracle.py:60-137).
- * Same arguments and node_state layout [n_dst, H, 4]. */
+ * Same arguments and node_state layout [n_dst, H, 4], without the device
+ * entry's partial buffer, pos rows and stream. */
 int tgx_cpu_gat_fwd(const void* row_ptr, const void* col, int idx_bits,
                     const tgx_row_plan* plan, const void* h_src, const void* h_dst,
                     const float* a_src, const float* a_dst, float negative_slope, void* out,
                     float* node_state, int64_t n_dst, int64_t n_src, int H, int D, int dtype);
 
-/* Twin of tgx_gat_bwd; node_state slot 1 (delta) is overwritten. */
+/* Twin of tgx_gat_bwd (its per-edge destination path: no pos rows);
+ * node_state slot 1 (delta) is overwritten. */
 int tgx_cpu_gat_bwd(const void* row_ptr, const void* col, int idx_bits,
                     const tgx_row_plan* plan, const int32_t* row_ptr_t, const int32_t* col_t,
                     const int32_t* perm, const int32_t* inv_perm, const tgx_row_plan* plan_t,
@@ -105,7 +107,8 @@ int tgx_cpu_dot_attn_fwd(const void* row_ptr, const void* col, int idx_bits,
                          const void* v, const float* bias, float scale, void* out, float* ml,
                          int64_t n_dst, int64_t n_src, int H, int D, int dtype);
 
-/* Twin of tgx_dot_attn_bwd; ml slot 1 (delta) is overwritten. */
+/* Twin of tgx_dot_attn_bwd (ds recomputed in the destination pass: no
+ * inv_perm or edge count); ml slot 1 (delta) is overwritten. */
 int tgx_cpu_dot_attn_bwd(const void* row_ptr, const void* col, int idx_bits,
                          const tgx_row_plan* plan, const int32_t* row_ptr_t,
                          const int32_t* col_t, const int32_t* perm,
