@@ -135,3 +135,69 @@ def test_hip_graph_capture_of_fused_forward_and_backward():
         torch.cuda.synchronize()
         assert torch.equal(got_out, out.detach()), f"replay {replay}: output differs"
         assert torch.equal(got_dh, h.grad), f"replay {replay}: gradient differs"
+
+
+class DotBias(tg.MessagePassing):
+    reducer = tg.online_softmax()
+
+    def edge(self, src, dst, edge, scale):
+        return self.reducer((src.k * dst.q).sum(dim=-1) * scale + edge.bias, src.v)
+
+
+def test_hip_graph_capture_of_dot_attention_with_kept_score_gradients():
+    """Capture dot-product attention forward + backward (whose source pass
+    keeps each edge's score gradient for the destination pass) on an R-MAT
+    graph with hub rows split on both sides; every replay, with eager work in
+    between, equals the eager step bit for bit."""
+    from graphs import rmat_csr
+
+    print("hip graph capture dot R-MAT scale 11", flush=True)
+    rp, cl = rmat_csr(9, 11)
+    n, E, H, D = rp.size - 1, cl.size, 4, 64
+    graph = tg.Graph.from_csr(torch.as_tensor(rp, device=DEV), torch.as_tensor(cl, device=DEV),
+                              num_src=n)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    mk = lambda *shape: torch.randn(*shape, device=DEV, generator=g)
+    q, k, v = (mk(n, H, D).to(torch.bfloat16).requires_grad_(True) for _ in range(3))
+    bias = mk(E, H).requires_grad_(True)
+    dout = mk(n, H, D).to(torch.bfloat16)
+    kernel = DotBias()
+    leaves = (q, k, v, bias)
+
+    def step(tensors):
+        out = kernel(graph=graph, src={"k": tensors[1], "v": tensors[2]}, dst={"q": tensors[0]},
+                     edge={"bias": tensors[3]}, scale=0.125)
+        out.backward(dout)
+        return out
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):   # builds row plans and the transposed CSR (host syncs)
+            for t in leaves:
+                t.grad = None
+            step(leaves)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert kernel.last_variant.backend == "hip"
+
+    graph_exec = torch.cuda.CUDAGraph()
+    for t in leaves:
+        t.grad = None
+    with torch.cuda.graph(graph_exec):
+        static_out = step(leaves)
+
+    for replay in range(4):
+        fresh = [mk(*t.shape).to(t.dtype) for t in leaves]
+        with torch.no_grad():
+            for t, f in zip(leaves, fresh):
+                t.copy_(f)
+        graph_exec.replay()
+        torch.cuda.synchronize()
+        got = [static_out.clone()] + [t.grad.clone() for t in leaves]
+        eager = [f.clone().requires_grad_(True) for f in fresh]
+        out = step(eager)
+        torch.cuda.synchronize()
+        want = [out.detach()] + [t.grad for t in eager]
+        for name, a, b in zip(("out", "dq", "dk", "dv", "dbias"), got, want):
+            assert torch.equal(a, b), f"replay {replay}: {name} differs"
