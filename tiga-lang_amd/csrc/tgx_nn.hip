@@ -933,15 +933,27 @@ void launch_bwd(int L, const I* col, const int32_t* dst, int64_t E, int blocks, 
                 hipStream_t s) {
   if constexpr (!TGX_NN_MATH && !SEED) {
     // Chains whose hidden layers all use LeakyReLU (the reference's GAT
-    // score network) take the kernel built for it.
-    bool leaky = L >= 2;
-    for (int l = 0; l + 1 < L; ++l) leaky = leaky && v.act[l] == TGX_ACT_LEAKY_RELU;
+    // score network) or all ReLU take a kernel built for that activation.
+    bool leaky = L >= 2, relu = L >= 2;
+    for (int l = 0; l + 1 < L; ++l) {
+      leaky = leaky && v.act[l] == TGX_ACT_LEAKY_RELU;
+      relu = relu && v.act[l] == TGX_ACT_RELU;
+    }
     if (leaky) {
       if (L == 2)
         edge_mlp_bwd_kernel<I, W, 2, SEED, TGX_ACT_LEAKY_RELU><<<blocks, 256, 0, s>>>(
             col, dst, E, chunk, v, ds, partial, seed, hw);
       else
         edge_mlp_bwd_kernel<I, W, 3, SEED, TGX_ACT_LEAKY_RELU><<<blocks, 256, 0, s>>>(
+            col, dst, E, chunk, v, ds, partial, seed, hw);
+      return;
+    }
+    if (relu) {
+      if (L == 2)
+        edge_mlp_bwd_kernel<I, W, 2, SEED, TGX_ACT_RELU><<<blocks, 256, 0, s>>>(
+            col, dst, E, chunk, v, ds, partial, seed, hw);
+      else
+        edge_mlp_bwd_kernel<I, W, 3, SEED, TGX_ACT_RELU><<<blocks, 256, 0, s>>>(
             col, dst, E, chunk, v, ds, partial, seed, hw);
       return;
     }
